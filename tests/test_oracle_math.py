@@ -1,0 +1,297 @@
+"""Pins for the float64 oracle beyond the golden files: each check is chosen so that a plausible slip in the
+oracle (a dropped term, a swapped index, a wrong sign, a transposed operand) fails it.
+
+* local terms (plane / diagonal closed forms, series leaf) against Gauss-Legendre quadrature of their
+  defining integrals with scipy's expm (the reference's own quadrature oracle, tests/test_jordan_engine.py:240-290);
+* plane / diagonal closed forms against the series leaf at q = 24 (tests/test_engines.py:227-248);
+* Van Loan leaf: level 1 exact for any M, level 2 converging as O(1/M^2) to the exact term;
+* expm methods against scipy / their textbook formulas;
+* sequential == associative == tree Chen combine (tests/test_engines.py:198-224);
+* depth-1 prefix == the exact affine (Van Loan) recursion built with scipy.linalg.expm (tests/test_block.py:559-596);
+* A = 0: the classical signature, whose depth-2 log is the Levy area (tests/test_log_ews.py:82-96);
+* exp(log(EWS)) == EWS and the Witt dimensions (tests/test_log_ews.py:99-121);
+* autograd of the oracle against central finite differences (tests/test_log_ews.py:149-175).
+"""
+
+import math
+
+import numpy as np
+import pytest
+import scipy.linalg
+import torch
+
+from oracle import ews_oracle as O
+
+DT = torch.float64
+
+
+def _rng(seed=0):
+    return np.random.default_rng(seed)
+
+
+def _planes_A(K, rng):
+    A = np.zeros((2 * K, 2 * K))
+    for j in range(K):
+        d, w = rng.uniform(0.05, 1.5), rng.uniform(-2.0, 2.0)
+        A[2 * j : 2 * j + 2, 2 * j : 2 * j + 2] = [[d, w], [-w, d]]
+    return A
+
+
+def _quad_local(v, h, A, N, nodes=24):
+    """Levels 1..N of the interval's local term by nested Gauss-Legendre quadrature of
+    x(u) = e^{-(h-u)A} v / h over the ordered simplex of [0, h]."""
+    g, w = np.polynomial.legendre.leggauss(nodes)
+    d = len(v)
+
+    def x(u):
+        return scipy.linalg.expm(-(h - u) * A) @ v / h
+
+    def lvl1(a, b):
+        us = (b - a) / 2 * g + (a + b) / 2
+        return sum(wi * x(ui) for wi, ui in zip(w, us)) * (b - a) / 2
+
+    out = [lvl1(0.0, h)]
+    if N >= 2:
+        us = h / 2 * g + h / 2
+        s2 = np.zeros((d, d))
+        for wi, u2 in zip(w, us):
+            s2 += wi * np.outer(lvl1(0.0, u2), x(u2))
+        out.append(s2 * h / 2)
+    return out
+
+
+@pytest.mark.parametrize("h", [0.05, 0.7, 2.5])
+def test_plane_closed_form_matches_quadrature(h):
+    rng = _rng(1)
+    K = 3
+    A = _planes_A(K, rng)
+    v = rng.normal(size=2 * K)
+    got = O.plane_local_terms(torch.tensor(v[None]), O.block_planes(torch.tensor(A)), torch.tensor([h], dtype=DT), 2)
+    ref = _quad_local(v, h, A, 2)
+    for g_, r_ in zip(got, ref):
+        np.testing.assert_allclose(g_[0].numpy(), r_, rtol=0, atol=1e-11 * max(1, np.abs(r_).max()))
+
+
+@pytest.mark.parametrize("h", [1e-4, 0.3, 4.0])
+def test_diag_closed_form_matches_quadrature(h):
+    rng = _rng(2)
+    lam = rng.uniform(-0.5, 3.0, size=5)
+    v = rng.normal(size=5)
+    got = O.diag_local_terms(torch.tensor(v[None]), torch.tensor(lam), torch.tensor([h], dtype=DT), 2)
+    ref = _quad_local(v, h, np.diag(lam), 2)
+    for g_, r_ in zip(got, ref):
+        np.testing.assert_allclose(g_[0].numpy(), r_, rtol=0, atol=1e-11 * max(1, np.abs(r_).max()))
+
+
+def test_series_leaf_matches_quadrature_dense_A():
+    rng = _rng(3)
+    d, h = 4, 0.4
+    A = rng.normal(size=(d, d)) * 0.8
+    v = rng.normal(size=d)
+    got = O.series_local_terms(torch.tensor(v[None]), torch.tensor([h], dtype=DT), torch.tensor(A), 2, 24)
+    ref = _quad_local(v, h, A, 2)
+    for g_, r_ in zip(got, ref):
+        np.testing.assert_allclose(g_[0].numpy(), r_, rtol=0, atol=1e-11)
+
+
+def test_series_level3_matches_nested_quadrature():
+    rng = _rng(4)
+    d, h = 3, 0.5
+    A = rng.normal(size=(d, d)) * 0.5
+    v = rng.normal(size=d)
+    g, w = np.polynomial.legendre.leggauss(14)
+
+    def x(u):
+        return scipy.linalg.expm(-(h - u) * A) @ v / h
+
+    def S(level, b):
+        # iterated integral of x over {0 < u1 < ... < u_level < b}
+        us = b / 2 * g + b / 2
+        if level == 1:
+            return sum(wi * x(ui) for wi, ui in zip(w, us)) * b / 2
+        acc = 0
+        for wi, ui in zip(w, us):
+            acc = acc + wi * np.multiply.outer(S(level - 1, ui), x(ui))
+        return acc * b / 2
+
+    got = O.series_local_terms(torch.tensor(v[None]), torch.tensor([h], dtype=DT), torch.tensor(A), 3, 26)
+    np.testing.assert_allclose(got[2][0].numpy(), S(3, h), rtol=0, atol=1e-10)
+
+
+def test_closed_forms_match_series_q24():
+    rng = _rng(5)
+    n, K = 7, 3
+    A = _planes_A(K, rng) * 0.5
+    v = torch.tensor(rng.normal(size=(n, 2 * K)))
+    dth = torch.tensor(rng.uniform(0.05, 0.5, size=n))
+    pc = O.plane_local_terms(v, O.block_planes(torch.tensor(A)), dth, 2)
+    se = O.series_local_terms(v, dth, torch.tensor(A), 2, 24)
+    for a, b in zip(pc, se):
+        assert float((a - b).abs().max()) < 1e-10
+    lam = torch.tensor(rng.uniform(0.1, 2.0, size=6))
+    v6 = torch.tensor(rng.normal(size=(n, 6)))
+    dc = O.diag_local_terms(v6, lam, dth, 2)
+    se = O.series_local_terms(v6, dth, torch.diag(lam), 2, 24)
+    for a, b in zip(dc, se):
+        assert float((a - b).abs().max()) < 1e-10
+
+
+def test_van_loan_level1_exact_level2_second_order():
+    rng = _rng(6)
+    d, n = 3, 4
+    A = torch.tensor(rng.normal(size=(d, d)) * 0.7)
+    v = torch.tensor(rng.normal(size=(n, d)))
+    dth = torch.tensor(rng.uniform(0.3, 1.0, size=n))
+    exact = O.series_local_terms(v, dth, A, 2, 30)
+    errs = []
+    for M in (8, 16, 32):
+        vl = O.van_loan_local_terms(v, dth, A, 2, M, "exact", "displacement")
+        assert float((vl[0] - exact[0]).abs().max()) < 1e-12
+        errs.append(float((vl[1] - exact[1]).abs().max()))
+    assert 3.5 < errs[0] / errs[1] < 4.5 and 3.5 < errs[1] / errs[2] < 4.5
+
+
+def test_van_loan_uniform_equals_displacement_on_uniform_clock():
+    rng = _rng(7)
+    d, n = 4, 5
+    A = torch.tensor(rng.normal(size=(d, d)) * 0.5)
+    v = torch.tensor(rng.normal(size=(n, d)))
+    dth = torch.full((n,), 0.3, dtype=DT)
+    a = O.van_loan_local_terms(v, dth, A, 2, 5, "exact", "displacement")
+    b = O.van_loan_local_terms(v, dth, A, 2, 5, "exact", "displacement_uniform")
+    for x, y in zip(a, b):
+        assert float((x - y).abs().max()) < 1e-12
+
+
+@pytest.mark.parametrize("method", ["exact", "euler", "cayley", "pade"])
+def test_expm_methods(method):
+    rng = _rng(8)
+    X = rng.normal(size=(4, 4)) * 0.3
+    got = O.expm(torch.tensor(X), method).numpy()
+    I = np.eye(4)
+    ref = {
+        "exact": scipy.linalg.expm(X),
+        "euler": I + X,
+        "cayley": np.linalg.inv(I - X / 2) @ (I + X / 2),
+        "pade": np.linalg.inv(I - X / 2 + X @ X / 12) @ (I + X / 2 + X @ X / 12),
+    }[method]
+    np.testing.assert_allclose(got, ref, rtol=1e-12, atol=1e-13)
+
+
+@pytest.mark.parametrize("N", [1, 2, 3])
+def test_sequential_assoc_tree_agree(N):
+    rng = _rng(9)
+    d, n = 3, 11
+    A = torch.tensor(rng.normal(size=(d, d)) * 0.4)
+    v = torch.tensor(rng.normal(size=(n, d)) * 0.5)
+    dth = torch.tensor(rng.uniform(0.1, 0.6, size=n))
+    lv = O.series_local_terms(v, dth, A, N, 20)
+    M = O.flows(dth, A)
+    seq = O.chen_scan_prefix(lv, M)
+    asc = O.chen_assoc_scan_prefix(lv, M)
+    tree = O.chen_tree_final(lv, M)
+    assert float((seq - asc).abs().max()) < 1e-12
+    assert float((seq[-1] - tree).abs().max()) < 1e-12
+
+
+def test_depth1_prefix_is_the_exact_affine_recursion():
+    rng = _rng(10)
+    d, L = 4, 12
+    A = rng.normal(size=(d, d)) * 0.6
+    path = np.cumsum(rng.normal(size=(L, d)), 0)
+    clock = np.cumsum(rng.uniform(0.1, 0.5, size=L))
+    got = O.ews_single(torch.tensor(path), torch.tensor(clock), torch.tensor(A), 1, "prefix",
+                       leaf="series", series_q=30)
+    y = np.zeros(d)
+    rows = []
+    for t in range(L - 1):
+        h = clock[t + 1] - clock[t]
+        v = path[t + 1] - path[t]
+        Aug = np.zeros((d + 1, d + 1))
+        Aug[:d, :d] = -h * A
+        Aug[:d, d] = v
+        E = scipy.linalg.expm(Aug)  # [[e^{-hA}, phi(-hA) v], [0, 1]]
+        y = E[:d, :d] @ y + E[:d, d]
+        rows.append(np.concatenate([[1.0], y]))
+    np.testing.assert_allclose(got.numpy(), np.array(rows), rtol=0, atol=1e-11)
+
+
+def test_zero_drift_is_the_signature_and_log_is_levy_area():
+    rng = _rng(11)
+    d, L = 3, 9
+    path = np.cumsum(rng.normal(size=(L, d)), 0)
+    clock = np.linspace(0, 1, L)
+    A = torch.zeros((d, d), dtype=DT)
+    for leaf in ("van_loan", "series", "diag_closed"):
+        lv = O.ews_single(torch.tensor(path), torch.tensor(clock), A, 2, "terminal", leaf=leaf, M=3,
+                          series_q=5, output_format="list")
+        inc = np.diff(path, axis=0)
+        S1 = inc.sum(0)
+        # level 2 of a piecewise-linear path: sum_{s<t} D_s (x) D_t + sum_t D_t (x) D_t / 2
+        S2 = sum(np.outer(inc[s], inc[t]) for s in range(L - 1) for t in range(s + 1, L - 1))
+        S2 = S2 + sum(np.outer(x, x) for x in inc) / 2
+        np.testing.assert_allclose(lv[0][0].numpy(), S1, atol=1e-12)
+        np.testing.assert_allclose(lv[1][0].numpy(), S2, atol=1e-11)
+    logf = O.log_ews_single(torch.tensor(path), torch.tensor(clock), A, 2, "terminal", leaf="series", series_q=5)
+    inc = np.diff(path, axis=0)
+    area = sum(np.outer(inc[s], inc[t]) - np.outer(inc[t], inc[s]) for s in range(L - 1)
+               for t in range(s + 1, L - 1)) / 2
+    expect = np.concatenate([inc.sum(0), [area[i, j] for i in range(d) for j in range(i + 1, d)]])
+    np.testing.assert_allclose(logf.numpy(), expect, atol=1e-11)
+
+
+def test_exp_of_log_recovers_ews_and_witt_dims():
+    rng = _rng(12)
+    d, N, L = 3, 3, 8
+    path = torch.tensor(np.cumsum(0.3 * rng.normal(size=(L, d)), 0))
+    clock = torch.linspace(0, 1, L, dtype=DT)
+    A = torch.tensor(0.5 * rng.normal(size=(d, d)))
+    lv = O.ews_single(path, clock, A, N, "terminal", leaf="series", series_q=20, output_format="list")
+    lg = O.tensor_log(lv)
+    # exp(X) = sum X^n / n!, truncated
+    out = [x.clone() for x in lg]
+    P = lg
+    for n in range(2, N + 1):
+        P = [sum((O.outer(P[j - 1], lg[k - j - 1]) for j in range(1, k)), torch.zeros_like(lg[k - 1]))
+             for k in range(1, N + 1)]
+        out = [o + p / math.factorial(n) for o, p in zip(out, P)]
+    for a, b in zip(out, lv):
+        assert float((a - b).abs().max()) < 1e-12
+    for dd, NN, expect in [(3, 3, 14), (4, 2, 10), (2, 4, 8)]:
+        assert sum(len(w) for w in O.lyndon_words(NN, dd)) == expect
+
+
+def test_oracle_gradients_match_finite_differences():
+    rng = _rng(13)
+    K, L = 2, 7
+    A0 = _planes_A(K, rng) * 0.5
+    path = torch.tensor(np.cumsum(rng.normal(size=(L, 2 * K)) * 0.4, 0))
+    clock = torch.tensor(np.cumsum(rng.uniform(0.2, 0.6, size=L)))
+    wts = torch.tensor(rng.normal(size=(L - 1, 1 + 2 * K + 4 * K * K)))
+
+    def loss(dw, pth, clk):
+        A = torch.zeros((2 * K, 2 * K), dtype=DT)
+        for j in range(K):
+            A = A + torch.zeros_like(A).index_put_((torch.tensor([2 * j, 2 * j, 2 * j + 1, 2 * j + 1]),
+                                                   torch.tensor([2 * j, 2 * j + 1, 2 * j, 2 * j + 1])),
+                                                  torch.stack([dw[j, 0], dw[j, 1], -dw[j, 1], dw[j, 0]]))
+        out = O.ews_single(pth, clk, A, 2, "prefix", leaf="plane_closed")
+        return (out * wts).sum()
+
+    dw = O.block_planes(torch.tensor(A0)).clone().requires_grad_(True)
+    p = path.clone().requires_grad_(True)
+    c = clock.clone().requires_grad_(True)
+    gdw, gp, gc = torch.autograd.grad(loss(dw, p, c), (dw, p, c))
+    eps = 1e-6
+    base = [dw.detach(), p.detach(), c.detach()]
+    for which, grad in enumerate((gdw, gp, gc)):
+        flat = base[which].reshape(-1)
+        for idx in range(0, flat.numel(), max(1, flat.numel() // 5)):
+            e = torch.zeros_like(flat)
+            e[idx] = eps
+            args_p, args_m = list(base), list(base)
+            args_p[which] = (flat + e).reshape(base[which].shape)
+            args_m[which] = (flat - e).reshape(base[which].shape)
+            fd = (loss(*args_p) - loss(*args_m)) / (2 * eps)
+            g = grad.reshape(-1)[idx]
+            assert abs(float(fd - g)) <= 1e-6 * max(1.0, abs(float(fd))), (which, idx, float(fd), float(g))
