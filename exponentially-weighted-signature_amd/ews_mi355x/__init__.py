@@ -1,0 +1,27 @@
+"""MI355X-native EWS: the reference's EWS / LogEWS layer API over hand-written HIP kernels for gfx950."""
+
+from ._native import LIB_PATH, NativeLibraryError, load  # noqa: F401
+from .layer import (  # noqa: F401
+    COMBINE_KINDS,
+    EWS,
+    LEAF_KINDS,
+    BToSignature,
+    LogEWS,
+    log_level_sizes,
+    log_level_slices,
+    log_signature_dim,
+    lyndon_words,
+)
+from .ops import diag_scan  # noqa: F401
+from .params import (  # noqa: F401
+    AParamBlockDiag,
+    AParamBoundedRotation,
+    AParamConstant,
+    AParamDampedRotation,
+    AParamEFM,
+    AParamGeneral,
+    block_sizes_of,
+    is_rotation_planes,
+)
+
+__version__ = "0.1.0"

@@ -1,0 +1,90 @@
+"""ctypes binding of the HIP library ``libews_mi355x.so`` (C ABI in include/ews_hip.h).
+
+The library is the only compute path: if it is missing or fails to load, every call raises. There is no
+CPU fallback.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_NAME = "libews_mi355x.so"
+LIB_PATH = os.path.join(_HERE, LIB_NAME)
+
+EWS_OK = 0
+STRUCT_PLANES = 1
+STRUCT_REAL_DIAG = 2
+FLOW_PER_INTERVAL = 0
+FLOW_CACHED = 1
+FLOW_CACHED_BASEPOINT = 2
+READOUTS = {"prefix": 0, "terminal": 1, "mean": 2, "max": 3}
+DTYPE_F32 = 0
+DTYPE_BF16 = 1
+
+EXPORTED = (
+    "ews_diag_workspace_bytes",
+    "ews_diag_residual_bytes",
+    "ews_diag_forward",
+    "ews_diag_backward",
+    "ews_error_string",
+    "ews_version",
+)
+
+
+class DiagDesc(ctypes.Structure):
+    _fields_ = [
+        ("batch", ctypes.c_int32),
+        ("length", ctypes.c_int32),
+        ("dim", ctypes.c_int32),
+        ("depth", ctypes.c_int32),
+        ("structure", ctypes.c_int32),
+        ("flow_mode", ctypes.c_int32),
+        ("readout", ctypes.c_int32),
+        ("level0", ctypes.c_int32),
+        ("path_dtype", ctypes.c_int32),
+        ("chunk", ctypes.c_int32),
+    ]
+
+
+class NativeLibraryError(RuntimeError):
+    pass
+
+
+_lib = None
+
+
+def load():
+    """Load the HIP library once; raise if it is absent (no fallback)."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(LIB_PATH):
+        raise NativeLibraryError(
+            f"{LIB_PATH} is missing: build it with `python -c 'import __graft_entry__ as g; g.build()'` "
+            "(hipcc --offload-arch=gfx950)"
+        )
+    lib = ctypes.CDLL(LIB_PATH)
+    vp, sz, i32 = ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int
+    dp = ctypes.POINTER(DiagDesc)
+    lib.ews_diag_workspace_bytes.argtypes = [dp]
+    lib.ews_diag_workspace_bytes.restype = sz
+    lib.ews_diag_residual_bytes.argtypes = [dp]
+    lib.ews_diag_residual_bytes.restype = sz
+    lib.ews_diag_forward.argtypes = [dp, vp, vp, vp, vp, vp, vp, vp]
+    lib.ews_diag_forward.restype = i32
+    lib.ews_diag_backward.argtypes = [dp, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp]
+    lib.ews_diag_backward.restype = i32
+    lib.ews_error_string.argtypes = [i32]
+    lib.ews_error_string.restype = ctypes.c_char_p
+    lib.ews_version.argtypes = []
+    lib.ews_version.restype = ctypes.c_char_p
+    _lib = lib
+    return lib
+
+
+def check(rc: int, what: str):
+    if rc != EWS_OK:
+        msg = load().ews_error_string(rc).decode()
+        raise NativeLibraryError(f"{what} failed: {msg} (code {rc})")

@@ -1,0 +1,322 @@
+"""The EWS layer and its log-signature variant: the reference's layer API (ews/layer.py) over the HIP library.
+
+``EWS`` / ``LogEWS`` keep the reference's constructor arguments, field names, ``__call__`` signature, shapes,
+readouts and error behaviour (ews/layer.py:43-556). Everything between the call and the readout runs in
+``libews_mi355x.so`` on the GPU; inputs on the CPU raise instead of falling back.
+
+Engines by generator structure (the structure comes from the parametrisation's class, as in
+ews/core/kernels/combine.py:37-63):
+
+    rotation planes, leaf "plane_closed"             fused closed-form leaf + Chen scan (exact, as the reference)
+    rotation planes / real diagonal,
+        leaf "block_series" or "series"              the same fused kernel: its closed forms are the q -> infinity
+                                                     limit of the series leaves (they agree to the series' own
+                                                     truncation bound, ews/core/series_leaf.py:129-143)
+    anything else                                    NotImplementedError (dense generators)
+"""
+
+from __future__ import annotations
+
+from typing import Optional
+
+import torch
+
+from . import ops
+from .params import AParamConstant, block_sizes_of, diagonal_structure, is_rotation_planes
+
+LEAF_KINDS = ("van_loan", "series", "plane_closed", "block_series", "jordan_closed", "jordan_closed_tables")
+COMBINE_KINDS = ("assoc", "lean", "block_kernel", "dense_kernel")
+JORDAN_LEAVES = ("jordan_closed", "jordan_closed_tables")
+
+
+def _normalize_expm_method(method: str) -> str:
+    """ews/layer.py:34-40."""
+    method = method.lower()
+    if method in {"pade_lite", "pade-lite"}:
+        return "pade"
+    if method not in {"exact", "euler", "cayley", "pade"}:
+        raise ValueError("expm method must be one of 'exact', 'euler', 'cayley', 'pade'")
+    return method
+
+
+class EWS(torch.nn.Module):
+    """EWS layer (ews/layer.py:43-307): (path, clock) -> exponentially weighted signature features."""
+
+    def __init__(
+        self,
+        A,
+        N: int,
+        M: int = 20,
+        dtype: torch.dtype = torch.float32,
+        reweighting_mode: str = "displacement",
+        terminal_reduce: str = "tree",
+        van_loan_expm: str = "cayley",
+        chen_expm: str = "exact",
+        leaf: str = "van_loan",
+        series_q: Optional[int] = None,
+        combine: str = "assoc",
+        combine_chunk: int = 1024,
+        combine_tile: int = 4,
+        jordan_flows: bool = False,
+    ):
+        super().__init__()
+        if isinstance(A, torch.Tensor):
+            A_param = AParamConstant(A.to(dtype))
+        else:
+            A_param = A
+        self.A_param = A_param
+        self.d = int(A_param.dim) if hasattr(A_param, "dim") else int(A_param().shape[0])
+        self.N = N
+        self.M = M
+        self.dtype = dtype
+        self.reweighting_mode = reweighting_mode
+        if terminal_reduce not in {"tree", "assoc"}:
+            raise ValueError("terminal_reduce must be 'tree' or 'assoc'")
+        self.terminal_reduce = terminal_reduce
+        self.van_loan_expm = _normalize_expm_method(van_loan_expm)
+        self.chen_expm = _normalize_expm_method(chen_expm)
+        if leaf not in LEAF_KINDS:
+            raise ValueError(f"leaf must be one of {LEAF_KINDS}, got {leaf!r}")
+        if leaf == "series" and series_q is None:
+            raise ValueError("leaf='series' requires series_q (see ews.core.leaf.check_series_q)")
+        self.leaf = leaf
+        self.series_q = None if series_q is None else int(series_q)
+        if combine not in COMBINE_KINDS:
+            raise ValueError(f"combine must be one of {COMBINE_KINDS}, got {combine!r}")
+        self.combine = combine
+        self.combine_chunk = int(combine_chunk)
+        self.combine_tile = int(combine_tile)
+        self.block_sizes = block_sizes_of(A_param)
+        if combine == "block_kernel" and self.block_sizes is None:
+            raise ValueError(
+                "combine='block_kernel' needs a block-diagonal A parametrisation "
+                "(rotation planes, AParamUnconstrainedRotation, AParamJordanRepeated or AParamBlockDiag)"
+            )
+        self.jordan_flows = bool(jordan_flows)
+        if self.jordan_flows:
+            raise ValueError("jordan_flows needs combine='block_kernel' and a jordan_repeated A with uniform chains")
+        if leaf == "block_series" and self.block_sizes is None:
+            raise ValueError("leaf='block_series' needs a block-diagonal A parametrisation")
+        if leaf == "plane_closed" and not is_rotation_planes(A_param):
+            raise ValueError(
+                "leaf='plane_closed' needs a rotation-plane A parametrisation "
+                "(bounded/damped/relu_damped/clamped/unbounded rotation)"
+            )
+        if leaf == "block_series" and N == 2 and series_q is None:
+            raise ValueError("leaf='block_series' at depth 2 requires series_q")
+        if leaf in JORDAN_LEAVES:
+            raise ValueError(f"leaf={leaf!r} needs a jordan_repeated A with uniform chains")
+        self.structure = diagonal_structure(A_param)
+
+    # ------------------------------------------------------------------------------------------ engine
+    def _flow_mode(self, readout):
+        if self.leaf == "van_loan" and self.reweighting_mode not in (
+            "displacement", "displacement_uniform", "displacement_uniform_basepoint"
+        ):
+            raise ValueError(
+                "reweighting_mode must be 'displacement', 'displacement_uniform', or "
+                f"'displacement_uniform_basepoint', got {self.reweighting_mode}"
+            )
+        # the assoc combine's tree terminal always takes per-interval flows (ews/core/chen_scan.py:286-298)
+        if readout == "terminal" and self.combine == "assoc" and self.terminal_reduce == "tree":
+            return "per_interval"
+        if self.reweighting_mode == "displacement_uniform":
+            return "cached"
+        if self.reweighting_mode == "displacement_uniform_basepoint":
+            return "cached_basepoint"
+        return "per_interval"
+
+    def _diag_params(self, A):
+        """Kernel parameters read off the materialised A as ews/core/leaf.py:130-131 reads them."""
+        if self.structure == "planes":
+            ii = torch.arange(0, self.d, 2, device=A.device)
+            return torch.stack([A[ii, ii], A[ii, ii + 1]], -1).contiguous()
+        return torch.diagonal(A).contiguous()
+
+    def _engine_check(self):
+        if self.structure is not None and self.leaf in ("plane_closed", "block_series", "series"):
+            if self.N > 2:
+                raise NotImplementedError(
+                    f"leaf={self.leaf!r}: closed-form local terms exist for depths 1 and 2"
+                )
+            if self.structure == "planes" and self.d % 2:
+                raise ValueError("leaf='plane_closed' needs an even dimension (2x2 planes)")
+            return "diag"
+        raise NotImplementedError(
+            f"no MI355X kernel for leaf={self.leaf!r} with a dense generator in this build: use a rotation-plane or "
+            "diagonal parametrisation with leaf='plane_closed' / 'block_series' / 'series'"
+        )
+
+    def _run(self, path, clock, readout, level0, a_scale):
+        self._engine_check()
+        if self.dtype != torch.float32:
+            raise TypeError("the MI355X kernels compute in float32 (dtype=torch.float32)")
+        A = self.A_param().to(torch.float32) * torch.as_tensor(a_scale, dtype=torch.float32, device=path.device)
+        params = self._diag_params(A.to(path.device))
+        if path.dtype != torch.bfloat16:
+            path = path.to(torch.float32)
+        clock = clock.to(torch.float32)
+        return ops.diag_scan(path, clock, params, self.N, self.structure, self._flow_mode(readout), readout,
+                             level0, chunk=0)
+
+    def _levels(self, packed, lead):
+        out, s = [], 0
+        for k in range(1, self.N + 1):
+            n = self.d**k
+            out.append(packed[..., s : s + n].reshape(lead + (self.d,) * k))
+            s += n
+        return out
+
+    # ------------------------------------------------------------------------------------------ call
+    def forward(
+        self,
+        path: torch.Tensor,
+        clock: torch.Tensor,
+        return_terminal: bool = True,
+        output_format: str = "flat",
+        readout: Optional[str] = None,
+        a_scale=1.0,
+    ):
+        """path (L, d) or (B, L, d); clock (L,) or (B, L). Readouts as ews/layer.py:267-302."""
+        if readout is None:
+            readout = "terminal" if return_terminal else "prefix"
+        if readout not in {"terminal", "prefix", "mean", "max"}:
+            raise ValueError("readout must be 'terminal', 'prefix', 'mean', or 'max'")
+        if path.dim() == 2:
+            if clock.dim() != 1 or clock.shape[0] != path.shape[0]:
+                raise ValueError("clock must be 1D and aligned with path length")
+            out = self.forward(path[None], clock[None], output_format=output_format, readout=readout,
+                               a_scale=a_scale)
+            return [o[0] for o in out] if isinstance(out, list) else out[0]
+        if path.dim() != 3:
+            raise ValueError(f"Path must be 2D or 3D, got shape {tuple(path.shape)}")
+        if clock.dim() != 2:
+            raise ValueError("clock must be 2D for batched paths")
+        if clock.shape[1] != path.shape[1] or clock.shape[0] != path.shape[0]:
+            raise ValueError("clock must be 1D and aligned with path length")
+        if output_format == "list":
+            if readout in ("mean", "max"):
+                raise ValueError(f"readout='{readout}' requires output_format='flat'")
+            packed = self._run(path, clock, readout, False, a_scale)
+            return self._levels(packed, tuple(packed.shape[:-1]))
+        return self._run(path, clock, readout, True, a_scale)
+
+    @property
+    def signature_dim(self) -> int:
+        return sum(self.d**k for k in range(1, self.N + 1))
+
+
+# ---------------------------------------------------------------------------------------------- log-signature
+def lyndon_words(N, d):
+    """Lyndon words of lengths 1..N over {0..d-1}, each length in lexicographic order (Duval)."""
+    words = [[] for _ in range(N)]
+    w = [-1]
+    while w:
+        w[-1] += 1
+        words[len(w) - 1].append(tuple(w))
+        m = len(w)
+        while len(w) < N:
+            w.append(w[len(w) - m])
+        while w and w[-1] == d - 1:
+            w.pop()
+    return [sorted(ws) for ws in words]
+
+
+def log_level_sizes(d: int, N: int):
+    """[W_d(1), .., W_d(N)] (ews/layer.py:417-420)."""
+    return [len(w) for w in lyndon_words(N, d)]
+
+
+def log_signature_dim(d: int, N: int) -> int:
+    """ews/layer.py:423-425."""
+    return int(sum(log_level_sizes(d, N)))
+
+
+def log_level_slices(d: int, N: int):
+    """ews/layer.py:428-437."""
+    slices, start = [], 0
+    for size in log_level_sizes(d, N):
+        slices.append((start, start + size))
+        start += size
+    return tuple(slices)
+
+
+def _log_compress_depth_le2(levels, d):
+    """Compressed log of group-like rows: level 1 as is; level 2 = S2 - S1 (x) S1 / 2 at the Lyndon words
+    (i < j) (signax.signature_to_logsignature at depth <= 2, used at ews/layer.py:494, 502)."""
+    S1 = levels[0]
+    if len(levels) == 1:
+        return S1
+    S2 = levels[1]
+    log2 = S2 - 0.5 * S1[..., :, None] * S1[..., None, :]
+    iu = torch.triu_indices(d, d, offset=1, device=S1.device)
+    return torch.cat([S1, log2[..., iu[0], iu[1]]], -1)
+
+
+class LogEWS(torch.nn.Module):
+    """log(EWS) in the compressed Lyndon basis (ews/layer.py:440-556)."""
+
+    def __init__(self, A, N: int, M: int = 20, dtype=torch.float32, reweighting_mode="displacement",
+                 terminal_reduce="tree", van_loan_expm="cayley", chen_expm="exact", leaf="van_loan",
+                 series_q=None, combine="assoc", combine_chunk=1024, combine_tile=4, jordan_flows=False):
+        super().__init__()
+        self.ewms = EWS(A, N=N, M=M, dtype=dtype, reweighting_mode=reweighting_mode,
+                        terminal_reduce=terminal_reduce, van_loan_expm=van_loan_expm, chen_expm=chen_expm,
+                        leaf=leaf, series_q=series_q, combine=combine, combine_chunk=combine_chunk,
+                        combine_tile=combine_tile, jordan_flows=jordan_flows)
+        self.d = self.ewms.d
+        self.N = self.ewms.N
+
+    def _compress(self, levels):
+        if self.N > 2:
+            raise NotImplementedError("LogEWS on the MI355X path covers depths 1 and 2")
+        return _log_compress_depth_le2(levels, self.d)
+
+    def forward(self, path, clock, return_terminal=True, output_format="flat", readout=None):
+        if readout is None:
+            readout = "terminal" if return_terminal else "prefix"
+        if readout not in {"terminal", "prefix", "mean", "max"}:
+            raise ValueError("readout must be 'terminal', 'prefix', 'mean', or 'max'")
+        if path.dim() not in (2, 3):
+            raise ValueError(f"Path must be 2D or 3D, got shape {tuple(path.shape)}")
+        if path.dim() == 3 and clock.dim() != 2:
+            raise ValueError("clock must be 2D for batched paths")
+        if readout == "terminal":
+            lv = self.ewms(path, clock, readout="terminal", output_format="list")
+            feat = self._compress(lv)
+            if output_format == "list":
+                return self._split(feat)
+            return feat
+        lv = self.ewms(path, clock, readout="prefix", output_format="list")
+        feat = self._compress(lv)  # (..., L-1, D_log)
+        if output_format == "list":
+            if readout in ("mean", "max"):
+                raise ValueError(f"readout='{readout}' requires output_format='flat'")
+            return self._split(feat)
+        if readout == "prefix":
+            return feat
+        if readout == "mean":
+            return feat.mean(-2)
+        return feat.max(-2).values
+
+    def _split(self, feat):
+        return [feat[..., s:e] for s, e in log_level_slices(self.d, self.N)]
+
+    @property
+    def log_signature_dim(self) -> int:
+        return log_signature_dim(self.d, self.N)
+
+
+class BToSignature(torch.nn.Module):
+    """Optional lift B + EWS (ews/layer.py:310-341)."""
+
+    def __init__(self, b, ewms: EWS):
+        super().__init__()
+        self.b = b
+        self.ewms = ewms
+
+    def forward(self, path, clock, return_terminal=True, output_format="flat", readout=None):
+        if self.b is not None:
+            path = self.b(path)
+        return self.ewms(path, clock, return_terminal=return_terminal, output_format=output_format,
+                         readout=readout)

@@ -1,0 +1,95 @@
+/* C ABI of the MI355X EWS Chen-scan library (libews_mi355x.so).
+ *
+ * The entry points replace the combine/leaf stage behind the reference layer `EWS._single_path`
+ * (ews/layer.py:154-265): the leaf `local_signatures` (ews/core/leaf.py:50-198), the flows
+ * `_chen_M_per_interval` (ews/core/chen_scan.py:155-168) and the Chen combine `combine_packed`
+ * (ews/core/kernels/combine.py:193-269) / `chen_associative_scan_prefix_packed_with_M` (chen_scan.py:172-214),
+ * together with the custom VJPs of the Pallas kernels (ews/core/kernels/pallas_combine.py:1673-1801).
+ *
+ * Conventions: every pointer is device memory owned by the caller; nothing here allocates; all work is
+ * stream-ordered on `stream`; the calls are re-entrant (no global mutable state). Sign convention is the
+ * reference's: the flow over a clock step h is exp(-h A).
+ */
+#ifndef EWS_HIP_H
+#define EWS_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct ihipStream_t* ews_stream_t; /* hipStream_t */
+
+/* return codes */
+#define EWS_OK 0
+#define EWS_ERR_NULL (-1)      /* a required pointer is NULL */
+#define EWS_ERR_SHAPE (-2)     /* batch/length/dim out of range */
+#define EWS_ERR_DEPTH (-3)     /* depth not supported by this structure */
+#define EWS_ERR_OPTION (-4)    /* unknown structure / flow mode / readout / dtype */
+#define EWS_ERR_LAUNCH (-5)    /* a kernel launch failed */
+
+/* generator structure */
+#define EWS_STRUCT_PLANES 1    /* rotation planes A_j = [[d_j, w_j], [-w_j, d_j]] on channels (2j, 2j+1) */
+#define EWS_STRUCT_REAL_DIAG 2 /* A = diag(lambda) */
+
+/* flows M_t = exp(-h A) (chen_scan.py:155-168): per interval, or one shared flow (cached) */
+#define EWS_FLOW_PER_INTERVAL 0       /* reweighting_mode "displacement" */
+#define EWS_FLOW_CACHED 1             /* "displacement_uniform": every interval uses dtheta[0] */
+#define EWS_FLOW_CACHED_BASEPOINT 2   /* "displacement_uniform_basepoint": dtheta[1], interval 0 = I */
+
+/* readouts (ews/layer.py:189-265) */
+#define EWS_READOUT_PREFIX 0   /* (B, L-1, W) */
+#define EWS_READOUT_TERMINAL 1 /* (B, W) */
+#define EWS_READOUT_MEAN 2     /* (B, W) */
+#define EWS_READOUT_MAX 3      /* (B, W) */
+
+#define EWS_DTYPE_F32 0
+#define EWS_DTYPE_BF16 1
+
+typedef struct ews_diag_desc {
+  int32_t batch;      /* B >= 1 */
+  int32_t length;     /* L >= 2 knots (L-1 intervals) */
+  int32_t dim;        /* d: even for planes (d <= 64), real diagonal d <= 32 */
+  int32_t depth;      /* N in {1, 2} (closed-form local terms exist for depths 1-2) */
+  int32_t structure;  /* EWS_STRUCT_* */
+  int32_t flow_mode;  /* EWS_FLOW_* */
+  int32_t readout;    /* EWS_READOUT_* */
+  int32_t level0;     /* 1: rows carry the leading level-0 constant (the "flat" format), 0: packed */
+  int32_t path_dtype; /* EWS_DTYPE_F32 or EWS_DTYPE_BF16 */
+  int32_t chunk;      /* intervals per chunk; 0 selects the default */
+} ews_diag_desc;
+
+/* Scratch the forward/backward need between launches (chunk summaries, carries, partial reductions).
+ * Replaces the XLA-side chunk scan of pallas_combine.py:1395-1422. */
+size_t ews_diag_workspace_bytes(const ews_diag_desc* desc);
+
+/* Residual the forward leaves for the backward: float64 chunk-start states (B, C+1, D) and, for the max
+ * readout, int32 argmax (B, W). Replaces the custom-VJP residuals of pallas_combine.py:1684-1697. */
+size_t ews_diag_residual_bytes(const ews_diag_desc* desc);
+
+/* Forward: path (B, L, d) [f32 or bf16], clock (B, L) f32, params f32 [planes: (d/2, 2) rows (d_j, w_j);
+ * real diagonal: (d,)], out f32 [(B, L-1, W) for prefix, (B, W) otherwise], W = level0 + sum_k d^k.
+ * Replaces local_signatures + combine_packed + the readout of EWS._single_path (ews/layer.py:172-265). */
+int ews_diag_forward(const ews_diag_desc* desc, const void* path, const float* clock, const float* params,
+                     float* out, void* residual, void* workspace, ews_stream_t stream);
+
+/* Backward: cotangent grad_out shaped like out; writes grad_path (B, L, d) f32, grad_clock (B, L) f32 and
+ * grad_params (same shape as params). Replaces the custom VJP _cvjp_bwd (pallas_combine.py:1698-1798) and
+ * JAX autodiff through the leaf (plane_engine.py:134-152). */
+int ews_diag_backward(const ews_diag_desc* desc, const void* path, const float* clock, const float* params,
+                      const void* residual, const float* grad_out, float* grad_path, float* grad_clock,
+                      float* grad_params, void* workspace, ews_stream_t stream);
+
+/* Human-readable text of a return code. */
+const char* ews_error_string(int code);
+
+/* Library version, "major.minor.patch". */
+const char* ews_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* EWS_HIP_H */

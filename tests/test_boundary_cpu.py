@@ -1,0 +1,111 @@
+"""CPU checks of the boundary: the built library loads and exports every C-ABI symbol include/ews_hip.h
+declares (no compute call: there is no GPU here), the host layer mirrors the reference's constructor
+validation and call-shape errors (ews/layer.py:82-152, 290-302; tests/test_engines.py:170-192), and the
+C ABI rejects bad descriptors with its error codes."""
+
+import ctypes
+import os
+import re
+
+import pytest
+import torch
+
+import ews_mi355x as E
+from ews_mi355x import _native as nat
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def _declared_functions():
+    src = open(os.path.join(ROOT, "include", "ews_hip.h")).read()
+    return sorted(set(re.findall(r"^\s*(?:size_t|int|const char\*)\s+(ews_\w+)\s*\(", src, re.M)))
+
+
+def test_library_exports_every_declared_symbol():
+    lib = nat.load()
+    declared = _declared_functions()
+    assert len(declared) >= 6
+    for name in declared:
+        assert hasattr(lib, name), name
+    assert set(nat.EXPORTED) <= set(declared)
+    assert lib.ews_version().decode().count(".") == 2
+
+
+def _desc(**kw):
+    base = dict(batch=2, length=10, dim=8, depth=2, structure=1, flow_mode=0, readout=0, level0=1, path_dtype=0,
+                chunk=0)
+    base.update(kw)
+    return nat.DiagDesc(**base)
+
+
+def test_c_abi_error_codes():
+    lib = nat.load()
+    good = _desc()
+    assert lib.ews_diag_workspace_bytes(ctypes.byref(good)) > 0
+    assert lib.ews_diag_residual_bytes(ctypes.byref(good)) > 0
+    null = ctypes.c_void_p(0)
+    # NULL pointers are rejected before any launch
+    assert lib.ews_diag_forward(ctypes.byref(good), null, null, null, null, null, null, null) == -1
+    bad = {
+        "depth": (_desc(depth=3), -3),
+        "odd planes": (_desc(dim=7), -2),
+        "length": (_desc(length=1), -2),
+        "structure": (_desc(structure=9), -4),
+        "readout": (_desc(readout=7), -4),
+        "dtype": (_desc(path_dtype=5), -4),
+        "real too wide": (_desc(structure=2, dim=40), -2),
+    }
+    for name, (dsc, code) in bad.items():
+        assert lib.ews_diag_forward(ctypes.byref(dsc), null, null, null, null, null, null, null) == code, name
+        assert lib.ews_diag_workspace_bytes(ctypes.byref(dsc)) == 0, name
+    assert lib.ews_error_string(-2).decode().startswith("batch/length/dim")
+
+
+def _planes(K=2):
+    return E.AParamDampedRotation(torch.zeros(K), torch.zeros(K), 2 * K)
+
+
+def test_layer_option_validation_mirrors_reference():
+    with pytest.raises(ValueError):
+        E.EWS(E.AParamGeneral(torch.zeros(4, 4)), N=1, combine="block_kernel")
+    with pytest.raises(ValueError):
+        E.EWS(E.AParamGeneral(torch.zeros(4, 4)), N=1, leaf="plane_closed")
+    with pytest.raises(ValueError):
+        E.EWS(E.AParamBlockDiag([torch.zeros(2, 2), torch.zeros(2, 2)], [2, 2]), N=1, leaf="plane_closed")
+    with pytest.raises(ValueError):
+        E.EWS(E.AParamGeneral(torch.zeros(4, 4)), N=1, combine="nonsense")
+    with pytest.raises(ValueError):
+        E.EWS(E.AParamBlockDiag([torch.zeros(2, 2), torch.zeros(2, 2)], [2, 2]), N=2, leaf="block_series")
+    with pytest.raises(ValueError):
+        E.EWS(_planes(), N=2, leaf="series")  # series needs series_q
+    with pytest.raises(ValueError):
+        E.EWS(_planes(), N=2, terminal_reduce="sideways")
+    with pytest.raises(ValueError):
+        E.EWS(_planes(), N=2, van_loan_expm="taylor")
+    layer = E.EWS(_planes(3), N=2, leaf="plane_closed", combine="block_kernel")
+    assert layer.block_sizes == (2, 2, 2) and layer.signature_dim == 6 + 36
+    assert E.block_sizes_of(E.AParamGeneral(torch.zeros(3, 3))) is None
+
+
+def test_layer_call_shape_errors_and_no_cpu_path():
+    layer = E.EWS(_planes(2), N=2, leaf="plane_closed")
+    with pytest.raises(ValueError):
+        layer(torch.zeros(5, 4), torch.zeros(4))  # misaligned clock
+    with pytest.raises(ValueError):
+        layer(torch.zeros(2, 5, 4), torch.zeros(5))  # batched path needs a 2-D clock
+    with pytest.raises(ValueError):
+        layer(torch.zeros(5), torch.zeros(5))
+    with pytest.raises(ValueError):
+        layer(torch.zeros(5, 4), torch.zeros(5), readout="median")
+    with pytest.raises(ValueError):
+        layer(torch.zeros(5, 4), torch.zeros(5), readout="mean", output_format="list")
+    with pytest.raises(NotImplementedError):
+        E.EWS(_planes(2), N=3, leaf="plane_closed")(torch.zeros(5, 4), torch.zeros(5))
+    with pytest.raises(RuntimeError, match="HIP device"):
+        layer(torch.zeros(5, 4), torch.linspace(0, 1, 5))  # CPU tensors never fall back
+
+
+def test_log_dims_mirror_reference():
+    for d, N, expect in [(3, 3, 14), (4, 2, 10), (2, 4, 8)]:
+        assert E.log_signature_dim(d, N) == expect
+    assert E.log_level_slices(4, 2) == ((0, 4), (4, 10))
