@@ -1,0 +1,238 @@
+#!/usr/bin/env python
+"""EWS Chen-scan forward+backward throughput on one MI355X (BASELINE.json metric, config c2).
+
+Workload: B=32 Brownian paths of L=17,984 knots, 6 channels with N(0, 1/L)
+increments lifted to d=16 by W ~ N(0, 1/6); complex-diagonal A as 8 rotation planes (damping U(0.01, 1),
+frequency U(0, pi)); uniform clock theta_k = k/L (float64, then float32); depth 2, float32; prefix readout
+(B, L-1, 1 + 16 + 256) and its custom-VJP backward against a fixed synthetic cotangent. One step = the
+forward and the backward of that batch, every kernel on the GPU with inputs resident in HBM.
+
+Prints one JSON line: value = time-steps/s = B (L-1) / seconds per step; roofline of the dominant kernel
+from HIP events recorded between the library's passes on the compute stream; cpu_baseline = the C/OpenMP
+restatement (oracle/cpu_scan.c, float32) on a bounded sample of the same workload on the host cores.
+"""
+
+from __future__ import annotations
+
+import argparse
+import ctypes
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+PKG_DIR = os.path.join(ROOT, "exponentially-weighted-signature_amd")
+for _p in (ROOT, PKG_DIR):
+    if _p not in sys.path:
+        sys.path.insert(0, _p)
+
+import numpy as np  # noqa: E402
+
+HBM_PEAK_GBS = 8000.0
+FWD_PASS_NAMES = ["chunk_summary", "carry_scan", "chunk_output", "readout_reduce"]
+BWD_PASS_NAMES = ["chunk_adjoint_local", "adjoint_scan", "chunk_adjoint_full", "knot_grads", "param_grads"]
+
+
+def make_inputs(B=32, L=17984, c=6, d=16, seed_cfg=2):
+    """Synthetic c2 inputs with np.random.default_rng([cfg, stream]) streams 0=increments, 1=lift, 2=A."""
+    rng0 = np.random.default_rng([seed_cfg, 0])
+    inc = rng0.normal(0.0, np.sqrt(1.0 / L), size=(B, L - 1, c))
+    path_c = np.concatenate([np.zeros((B, 1, c)), np.cumsum(inc, 1)], 1)
+    rng1 = np.random.default_rng([seed_cfg, 1])
+    Wl = rng1.normal(0.0, np.sqrt(1.0 / c), size=(d, c))
+    path = (path_c @ Wl.T).astype(np.float32)
+    rng2 = np.random.default_rng([seed_cfg, 2])
+    K = d // 2
+    damp = rng2.uniform(0.01, 1.0, K)
+    freq = rng2.uniform(0.0, np.pi, K)
+    # BASELINE writes exp(A tau) with Re A < 0; the reference discounts with exp(-tau A_ref), A_ref = -A: plane j
+    # of A_ref is [[a_j, w_j], [-w_j, a_j]] with a_j the damping and w_j the frequency
+    dw = np.stack([damp, freq], -1).astype(np.float32)
+    clock = np.broadcast_to((np.arange(L, dtype=np.float64) / L).astype(np.float32), (B, L)).copy()
+    return path, clock, dw
+
+
+def algorithmic_bytes(B, L, d, W, s_in=4):
+    """Compulsory HBM bytes per launch of each pass (per-interval figures times B (L-1) intervals)."""
+    n = B * (L - 1)
+    D = W - 1
+    return {
+        "chunk_output": n * (s_in * (d + 1) + 4 * W),          # read path+clock, write the prefix rows
+        "chunk_adjoint_full": n * (4 * W + 2 * s_in * (d + 1)),  # read cotangent rows + inputs, write dv/dh
+        "chunk_adjoint_local": n * (4 * W + s_in * (d + 1)),   # read cotangent rows + inputs
+        "chunk_summary": n * s_in * (d + 1),
+        "knot_grads": n * 2 * 4 * (d + 1),
+        "fwd_total": n * (s_in * (d + 1) + 4 * D),             # BASELINE.md bytes_fwd
+        "bwd_total": n * (4 * D + 2 * s_in * (d + 1)),         # BASELINE.md bytes_bwd
+    }
+
+
+def cpu_baseline(path, clock, dw, g, budget_s=12.0):
+    """Time the float32 C/OpenMP restatement (fwd + bwd) on a bounded sample of samples of the workload."""
+    from oracle import cbuild
+    from oracle import cpu_scan_py as C
+
+    cbuild.build(verbose=False)
+    cores = len(os.sched_getaffinity(0))
+    omp = int(os.environ.get("OMP_NUM_THREADS", cores))
+    threads = max(1, min(cores, omp))
+    B, L, d = path.shape
+    n = 1
+    t_one = None
+    while True:
+        t0 = time.perf_counter()
+        C.planes_forward(path[:n], clock[:n], dw, kind="f32")
+        C.planes_backward(path[:n], clock[:n], dw, g[:n], kind="f32")
+        dt = time.perf_counter() - t0
+        if t_one is None:
+            t_one = dt
+        if dt >= budget_s / 3 or n >= B:
+            break
+        n = min(B, max(n * 2, int(n * budget_s / 3 / max(dt, 1e-3))))
+    return {
+        "value": n * (L - 1) / dt,
+        "unit": "time-steps/s",
+        "cores": threads,
+        "kind": "port",
+        "sample": f"{n} of {B} samples at full L={L}, fwd+bwd, float32, oracle/cpu_scan.c with OpenMP "
+                  f"({threads} threads; os.cpu_count()={os.cpu_count()}, affinity={cores}); {dt:.2f} s",
+    }
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--check", action="store_true", help="also check one forward against the C float64 checker")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU: --gpus {args.gpus} is not supported (the EWS scan here is single-GPU; "
+              "multi-GPU sharding is a design note, not a measured path)", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+
+    import ews_mi355x as E
+    from ews_mi355x import _native as nat
+    from ews_mi355x.ops import make_desc
+
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    lib = nat.load()
+    B, L, c, d, N = 32, 17984, 6, 16, 2
+    path_np, clock_np, dw_np = make_inputs(B, L, c, d)
+    W = 1 + d + d * d
+    rng = np.random.default_rng([2, 5])
+    g_np = rng.normal(size=(B, L - 1, W)).astype(np.float32) / np.sqrt(W)
+    path = torch.tensor(path_np, device=dev)
+    clock = torch.tensor(clock_np, device=dev)
+    dw = torch.tensor(dw_np, device=dev)
+    gout = torch.tensor(g_np, device=dev)
+    desc = make_desc(B, L, d, N, nat.STRUCT_PLANES, nat.FLOW_PER_INTERVAL, "prefix", True, nat.DTYPE_F32)
+    ws = torch.empty(int(lib.ews_diag_workspace_bytes(ctypes.byref(desc))), device=dev, dtype=torch.uint8)
+    resid = torch.empty(int(lib.ews_diag_residual_bytes(ctypes.byref(desc))), device=dev, dtype=torch.uint8)
+    out = torch.empty((B, L - 1, W), device=dev, dtype=torch.float32)
+    dpath = torch.empty((B, L, d), device=dev, dtype=torch.float32)
+    dclock = torch.empty((B, L), device=dev, dtype=torch.float32)
+    ddw = torch.empty_like(dw)
+    nf, nb = lib.ews_diag_num_passes(0), lib.ews_diag_num_passes(1)
+
+    def step(events=None):
+        stream = ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream)
+        for p in range(nf):
+            if events is not None:
+                events[p].record()
+            nat.check(lib.ews_diag_forward_pass(ctypes.byref(desc), p, path.data_ptr(), clock.data_ptr(),
+                                                dw.data_ptr(), out.data_ptr(), resid.data_ptr(), ws.data_ptr(),
+                                                stream), "forward pass")
+        for p in range(nb):
+            if events is not None:
+                events[nf + p].record()
+            nat.check(lib.ews_diag_backward_pass(ctypes.byref(desc), p, path.data_ptr(), clock.data_ptr(),
+                                                 dw.data_ptr(), resid.data_ptr(), gout.data_ptr(),
+                                                 dpath.data_ptr(), dclock.data_ptr(), ddw.data_ptr(),
+                                                 ws.data_ptr(), stream), "backward pass")
+        if events is not None:
+            events[nf + nb].record()
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+
+    # sanity: the layer API on the same inputs gives the same forward rows
+    A = E.AParamConstant(torch.zeros(d, d))
+    check_rows = None
+    if args.check:
+        from oracle import cbuild
+        from oracle import cpu_scan_py as C
+
+        cbuild.build(verbose=False)
+        ref = C.planes_forward(path_np[:2], clock_np[:2], dw_np, kind="f64")
+        got = out[:2].cpu().numpy().astype(np.float64)
+        check_rows = float(np.abs(got - ref).max() / np.abs(ref).max())
+    del A
+
+    per_step_events = []
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    t_wall0 = time.perf_counter()
+    start.record()
+    for _ in range(args.steps):
+        evs = [torch.cuda.Event(enable_timing=True) for _ in range(nf + nb + 1)]
+        step(evs)
+        per_step_events.append(evs)
+    end.record()
+    torch.cuda.synchronize()
+    t_wall = time.perf_counter() - t_wall0
+    total_ms = start.elapsed_time(end)
+    ms_per_step = total_ms / args.steps
+    names = FWD_PASS_NAMES[:nf] + BWD_PASS_NAMES[:nb]
+    pass_ms = {nm: 0.0 for nm in names}
+    for evs in per_step_events:
+        for i, nm in enumerate(names):
+            pass_ms[nm] += evs[i].elapsed_time(evs[i + 1])
+    pass_ms = {k: v / args.steps for k, v in pass_ms.items()}
+    dominant = max(pass_ms, key=pass_ms.get)
+    ab = algorithmic_bytes(B, L, d, W)
+    dom_bytes = ab.get(dominant)
+    roof = None
+    if dom_bytes is not None:
+        achieved = dom_bytes / (pass_ms[dominant] * 1e-3) / 1e9
+        roof = {"bound": "hbm", "kernel": dominant, "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
+                "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None}
+    steps_per_s = B * (L - 1) / (ms_per_step * 1e-3)
+    fwdbwd_bytes = ab["fwd_total"] + ab["bwd_total"]
+    result = {
+        "metric": "EWS Chen-scan fwd+bwd time-steps/sec and HBM GB/s (% peak) on 1 MI355X",
+        "value": round(steps_per_s, 1),
+        "unit": "time-steps/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic",
+        "config": {"workload": "c2: single EWS layer, B=32, L=17984, d=16 (8 rotation planes), depth 2, fp32, "
+                               "prefix readout, forward + custom-VJP backward", "global_batch": B, "seq_len": L,
+                   "parallelism": "none (1 GPU)"},
+        "hbm_gbs_effective": round(fwdbwd_bytes / (ms_per_step * 1e-3) / 1e9, 1),
+        "hbm_frac_effective": round(fwdbwd_bytes / (ms_per_step * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+        "roofline": roof,
+        "passes_ms": {k: round(v, 4) for k, v in pass_ms.items()},
+        "wall_s": round(t_wall, 3),
+    }
+    if check_rows is not None:
+        result["check_forward_relerr_vs_f64"] = check_rows
+    if not args.no_cpu_baseline:
+        result["cpu_baseline"] = cpu_baseline(path_np, clock_np, dw_np, g_np)
+    print(json.dumps(result), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -66,6 +66,7 @@ struct DiagArgs {
   int B, L, n_int, d, K;  // K: planes (complex) or channels (real)
   int N, flow_mode, readout;
   int T, C;               // chunk length, chunk count
+  int scan_cb;            // chunks per LDS-staged block in the float64 scans
   int W, off1, off2, lvl0, D, npar;
   int path_bf16;
   const void* path;
@@ -117,14 +118,39 @@ __device__ __forceinline__ float load_path(const DiagArgs& a, size_t idx) {
   return reinterpret_cast<const float*>(a.path)[idx];
 }
 
+// Global -> LDS copy with eight independent loads in flight per thread (a plain strided loop waits on each
+// load before issuing the next).
+__device__ __forceinline__ void copy_to_lds(float* dst, const float* src, int n) {
+  const int st = blockDim.x;
+  int i = threadIdx.x;
+  for (; i + 7 * st < n; i += 8 * st) {
+    float r[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) r[u] = src[i + u * st];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) dst[i + u * st] = r[u];
+  }
+  for (; i < n; i += st) dst[i] = src[i];
+}
+
 // Increments v_t = X_{t+1} - X_t and clock steps h_t = theta_{t+1} - theta_t of chunk intervals [t0, t0+Tc).
 __device__ __forceinline__ void load_chunk(const DiagArgs& a, int b, int t0, int Tc, float* s_v, float* s_h) {
   const size_t base = ((size_t)b * a.L + t0) * a.d;
-  for (int i = threadIdx.x; i < Tc * a.d; i += blockDim.x) {
-    s_v[i] = load_path(a, base + i + a.d) - load_path(a, base + i);
+  const int n = Tc * a.d, st = blockDim.x;
+  int i = threadIdx.x;
+  for (; i + 3 * st < n; i += 4 * st) {
+    float x0[4], x1[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      x0[u] = load_path(a, base + i + u * st);
+      x1[u] = load_path(a, base + i + u * st + a.d);
+    }
+#pragma unroll
+    for (int u = 0; u < 4; ++u) s_v[i + u * st] = x1[u] - x0[u];
   }
+  for (; i < n; i += st) s_v[i] = load_path(a, base + i + a.d) - load_path(a, base + i);
   const float* th = a.clock + (size_t)b * a.L + t0;
-  for (int i = threadIdx.x; i < Tc; i += blockDim.x) s_h[i] = th[i + 1] - th[i];
+  for (int k = threadIdx.x; k < Tc; k += st) s_h[k] = th[k + 1] - th[k];
 }
 
 // ------------------------------------------------------------------------------------------- coefficients
@@ -182,6 +208,13 @@ __device__ __forceinline__ void eval_coef(float h, float hf, bool per_int, T uj,
       }
     }
   }
+}
+
+// The per-step exact evaluation (irregular clocks) stays out of line so it does not inflate the register
+// budget of the uniform-clock fast path it shares a loop with.
+template <class T, bool CPLX, int N, bool DERIV>
+__device__ __noinline__ void eval_coef_step(float h, float hf, bool per_int, T uj, T uk, Coef<T>& c, CoefD<T>& q) {
+  eval_coef<T, CPLX, N, DERIV>(h, hf, per_int, uj, uk, c, q);
 }
 
 // First-order model c(h_t) = c0 + c1 (h_t - hbar) of every h-dependent coefficient.
@@ -339,7 +372,7 @@ __global__ __launch_bounds__(MAXT) void k_chunk_fwd(DiagArgs a) {
       lin_coef<T, CPLX, N>(c0, q, h - cc.hbar, cc.per_int, co);
     } else {
       CoefD<T> qq;
-      eval_coef<T, CPLX, N, false>(h, cc.href, cc.per_int, uj, uk, co, qq);
+      eval_coef_step<T, CPLX, N, false>(h, cc.href, cc.per_int, uj, uk, co, qq);
     }
     const T pj = lds_p<T>(s_v, t, a.d, m.j);
     const T pk = (N == 2) ? lds_p<T>(s_v, t, a.d, m.k) : zero<T>();
@@ -497,48 +530,64 @@ __device__ __forceinline__ void write_row_d(const DiagArgs& a, const LaneMap& m,
   }
 }
 
+// Sequential float64 Chen combine of the chunk summaries per sample: carries[c] = state before chunk c.
+// Blocks of scan_cb chunks are staged in LDS (summaries, and the chunk flows computed in parallel), so the
+// sequential loop reads no global memory.
 template <bool CPLX, int N, int MAXT>
 __global__ __launch_bounds__(MAXT) void k_carry_scan(DiagArgs a) {
   using TD = typename Types<CPLX>::TD;
+  extern __shared__ double dsm[];
+  constexpr int CW = CPLX ? 2 : 1;
+  const int K = a.K, CB = a.scan_cb, NT = blockDim.x;
+  double* s_F = dsm;                                         // CB * K
+  float* s_l = reinterpret_cast<float*>(s_F + (size_t)CB * K * CW);  // CB * D
   const int b = blockIdx.x, tid = threadIdx.x;
   const LaneMap m = lane_map(a, tid);
-  if (!m.active) return;
   TD dummy{};
-  const TD uj = load_ud(a.params, m.j, &dummy);
-  const TD uk = load_ud(a.params, m.k, &dummy);
   TD S1{}, SA{}, SB{};
-  for (int c = 0; c < a.C; ++c) {
-    double* cr = a.carries + ((size_t)b * (a.C + 1) + c) * a.D;
-    if (m.plane) stD(cr + st1<CPLX>(m.j), S1);
-    if (N == 2) {
-      double* p2 = cr + st2<CPLX>(a, m.j, m.k);
-      if (CPLX) {
-        stD(p2, SA);
-        stD(p2 + 2, SB);
-      } else {
-        stD(p2, SB);
-      }
+  for (int c0 = 0; c0 < a.C; c0 += CB) {
+    const int nb = min(CB, a.C - c0);
+    __syncthreads();
+    copy_to_lds(s_l, a.summ + ((size_t)b * a.C + c0) * a.D, nb * a.D);
+    for (int i = tid; i < nb * K; i += NT) {
+      const int cc = i / K, j = i % K, c = c0 + cc;
+      const int Tc = min(a.T, a.n_int - c * a.T);
+      stD(s_F + (size_t)i * CW, dexp(mul_s(load_ud(a.params, j, &dummy), chunk_tau(a, b, c, Tc))));
     }
-    const int Tc = min(a.T, a.n_int - c * a.T);
-    const double tau = chunk_tau(a, b, c, Tc);
-    const float* sp = a.summ + ((size_t)b * a.C + c) * a.D;
-    const TD Fj = dexp(mul_s(uj, tau));
-    const TD l1j = ldD(sp + st1<CPLX>(m.j), &dummy);
-    const TD cj = Fj * S1;
-    if (N == 2) {
-      const TD l1k = ldD(sp + st1<CPLX>(m.k), &dummy);
-      const float* p2 = sp + st2<CPLX>(a, m.j, m.k);
-      const TD lamB = dexp(mul_s(uj + uk, tau));
-      if (CPLX) {
-        const TD lamA = dexp(mul_s(uj + conj(uk), tau));
-        SA = lamA * SA + cj * conj(l1k) + ldD(p2, &dummy);
-        SB = lamB * SB + cj * l1k + ldD(p2 + 2, &dummy);
-      } else {
-        SB = lamB * SB + cj * l1k + ldD(p2, &dummy);
+    __syncthreads();
+    if (!m.active) continue;
+    for (int cc = 0; cc < nb; ++cc) {
+      const int c = c0 + cc;
+      double* cr = a.carries + ((size_t)b * (a.C + 1) + c) * a.D;
+      if (m.plane) stD(cr + st1<CPLX>(m.j), S1);
+      if (N == 2) {
+        double* p2 = cr + st2<CPLX>(a, m.j, m.k);
+        if (CPLX) {
+          stD(p2, SA);
+          stD(p2 + 2, SB);
+        } else {
+          stD(p2, SB);
+        }
       }
+      const float* sp = s_l + (size_t)cc * a.D;
+      const TD Fj = ldDD(s_F + (size_t)(cc * K + m.j) * CW, &dummy);
+      const TD l1j = ldD(sp + st1<CPLX>(m.j), &dummy);
+      const TD cj = Fj * S1;
+      if (N == 2) {
+        const TD Fk = ldDD(s_F + (size_t)(cc * K + m.k) * CW, &dummy);
+        const TD l1k = ldD(sp + st1<CPLX>(m.k), &dummy);
+        const float* p2 = sp + st2<CPLX>(a, m.j, m.k);
+        if (CPLX) {
+          SA = (Fj * conj(Fk)) * SA + cj * conj(l1k) + ldD(p2, &dummy);
+          SB = (Fj * Fk) * SB + cj * l1k + ldD(p2 + 2, &dummy);
+        } else {
+          SB = (Fj * Fk) * SB + cj * l1k + ldD(p2, &dummy);
+        }
+      }
+      S1 = cj + l1j;
     }
-    S1 = cj + l1j;
   }
+  if (!m.active) return;
   double* cr = a.carries + ((size_t)b * (a.C + 1) + a.C) * a.D;
   if (m.plane) stD(cr + st1<CPLX>(m.j), S1);
   if (N == 2) {
@@ -583,35 +632,58 @@ __global__ void k_reduce_readout(DiagArgs a) {
   }
 }
 
-// ------------------------------------------------------------------------------------------- cotangents
-// Cotangents of the lane's state at interval tg from the readout's cotangent (complex convention
-// gamma = dL/dRe + i dL/dIm). Level 2 (complex): the row layout's block (j, k) is
-// q00 = (ReSA + ReSB)/2, q01 = (ImSB - ImSA)/2, q10 = (ImSA + ImSB)/2, q11 = (ReSA - ReSB)/2.
-template <bool CPLX, int N, class T>
-__device__ __forceinline__ void gamma_at(const DiagArgs& a, const LaneMap& m, int b, int tg, T& g1, T& gA,
-                                         T& gB) {
-  g1 = zero<T>();
-  gA = zero<T>();
-  gB = zero<T>();
-  const float* row;
-  float scale = 1.0f;
-  const int* am = nullptr;
-  if (a.readout == EWS_READOUT_PREFIX) {
-    row = a.gout + ((size_t)b * a.n_int + tg) * a.W;
-  } else if (a.readout == EWS_READOUT_TERMINAL) {
-    if (tg != a.n_int - 1) return;
-    row = a.gout + (size_t)b * a.W;
-  } else if (a.readout == EWS_READOUT_MEAN) {
-    row = a.gout + (size_t)b * a.W;
-    scale = 1.0f / (float)a.n_int;
+// ------------------------------------------------------------------------------------------- backward helpers
+// Lane maps of the backward kernels. WAVE: one wavefront with lane = 8 j + k (K <= 8): row sums over k and
+// column sums over j are butterflies inside the wave, and the diagonal lane (j, j) owns plane j. Otherwise
+// lane = K j + k, the sums go through LDS, and lane (j, 0) owns plane j.
+template <bool WAVE>
+__device__ __forceinline__ LaneMap lane_map_b(const DiagArgs& a, int tid) {
+  LaneMap m;
+  const int S = WAVE ? 8 : a.K;
+  int j, k;
+  bool act;
+  if (a.N == 2) {
+    j = tid / S;
+    k = tid % S;
+    act = j < a.K && k < a.K;
   } else {
-    row = a.gout + (size_t)b * a.W;
-    am = a.argmax + (size_t)b * a.W;
+    j = tid;
+    k = 0;
+    act = tid < a.K;
   }
+  m.active = act;
+  m.j = act ? j : 0;
+  m.k = act ? k : 0;
+  m.plane = act && ((WAVE && a.N == 2) ? (j == k) : (k == 0));
+  return m;
+}
+
+template <int I, class F> __device__ __forceinline__ void static_for_rev(F&& f) {
+  if constexpr (I > 0) {
+    f(std::integral_constant<int, I - 1>{});
+    static_for_rev<I - 1>(f);
+  }
+}
+template <int I, int N, class F> __device__ __forceinline__ void static_for(F&& f) {
+  if constexpr (I < N) {
+    f(std::integral_constant<int, I>{});
+    static_for<I + 1, N>(f);
+  }
+}
+
+// Cotangents of the lane's state from one cotangent row (complex convention gamma = dL/dRe + i dL/dIm).
+// Level 2 (complex): the row layout's block (j, k) is q00 = (ReSA + ReSB)/2, q01 = (ImSB - ImSA)/2,
+// q10 = (ImSA + ImSB)/2, q11 = (ReSA - ReSB)/2. am (max readout): only elements whose argmax is tg count.
+template <bool CPLX, int N, class T>
+__device__ __forceinline__ void gamma_row(const DiagArgs& a, const LaneMap& m, const float* row, float scale,
+                                          const int* am, int tg, T& g1, T& gA, T& gB) {
   auto G = [&](int e) -> float {
     if (am && am[e] != tg) return 0.0f;
     return row[e] * scale;
   };
+  g1 = zero<T>();
+  gA = zero<T>();
+  gB = zero<T>();
   if (m.plane) {
     const int e = a.off1 + st1<CPLX>(m.j);
     if constexpr (CPLX) {
@@ -632,22 +704,147 @@ __device__ __forceinline__ void gamma_at(const DiagArgs& a, const LaneMap& m, in
   }
 }
 
+// Cotangent rows of a prefix readout are staged in LDS eight steps at a time; the next block is loaded into
+// registers while the current one is processed, so no global load sits on the sequential dependency chain.
+constexpr int kPF = 36;
+constexpr int kBLK = 8;
+__device__ __forceinline__ void pf_load(const DiagArgs& a, int b, int tg0, int n, float (&pf)[kPF]) {
+  const float* src = a.gout + ((size_t)b * a.n_int + tg0) * a.W;
+#pragma unroll
+  for (int i = 0; i < kPF; ++i) {
+    const int idx = (int)threadIdx.x + i * (int)blockDim.x;
+    pf[i] = idx < n ? src[idx] : 0.0f;
+  }
+}
+__device__ __forceinline__ void pf_store(float* dst, int n, const float (&pf)[kPF]) {
+#pragma unroll
+  for (int i = 0; i < kPF; ++i) {
+    const int idx = (int)threadIdx.x + i * (int)blockDim.x;
+    if (idx < n) dst[idx] = pf[i];
+  }
+}
+
+struct GammaSrc {
+  const float* rows;  // prefix: staged block rows (kBLK x W); else the per-sample cotangent (W)
+  const int* am;      // max readout: per-sample argmax (W)
+  float scale;
+  int kind;           // readout
+};
+
+template <bool CPLX, int N, class T>
+__device__ __forceinline__ void gamma_step(const DiagArgs& a, const LaneMap& m, const GammaSrc& gs, int r, int tg,
+                                           T& g1, T& gA, T& gB) {
+  if (!m.active) {
+    g1 = gA = gB = zero<T>();
+    return;
+  }
+  if (gs.kind == EWS_READOUT_PREFIX) {
+    gamma_row<CPLX, N>(a, m, gs.rows + r * a.W, 1.0f, nullptr, tg, g1, gA, gB);
+  } else if (gs.kind == EWS_READOUT_TERMINAL) {
+    if (tg == a.n_int - 1) {
+      gamma_row<CPLX, N>(a, m, gs.rows, 1.0f, nullptr, tg, g1, gA, gB);
+    } else {
+      g1 = gA = gB = zero<T>();
+    }
+  } else if (gs.kind == EWS_READOUT_MEAN) {
+    gamma_row<CPLX, N>(a, m, gs.rows, gs.scale, nullptr, tg, g1, gA, gB);
+  } else {
+    gamma_row<CPLX, N>(a, m, gs.rows, 1.0f, gs.am, tg, g1, gA, gB);
+  }
+}
+
+// per-sample cotangent (terminal / mean / max readouts) into LDS
+__device__ __forceinline__ void stage_vec(const DiagArgs& a, int b, float* s_gv, int* s_am) {
+  for (int e = threadIdx.x; e < a.W; e += blockDim.x) {
+    s_gv[e] = a.gout[(size_t)b * a.W + e];
+    if (a.readout == EWS_READOUT_MAX) s_am[e] = a.argmax[(size_t)b * a.W + e];
+  }
+}
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o, 64);
+  return v;
+}
+// sums over k (lanes 8j .. 8j+7) and over j (lanes k, k+8, ..)
+__device__ __forceinline__ float row_sum8(float v) {
+  v += __shfl_xor(v, 1, 64);
+  v += __shfl_xor(v, 2, 64);
+  v += __shfl_xor(v, 4, 64);
+  return v;
+}
+__device__ __forceinline__ float col_sum8(float v) {
+  v += __shfl_xor(v, 8, 64);
+  v += __shfl_xor(v, 16, 64);
+  v += __shfl_xor(v, 32, 64);
+  return v;
+}
+__device__ __forceinline__ cf row_sum8(cf v) { return cf{row_sum8(v.re), row_sum8(v.im)}; }
+__device__ __forceinline__ cf col_sum8(cf v) { return cf{col_sum8(v.re), col_sum8(v.im)}; }
+
+__device__ __forceinline__ float redot(cf a, cf b) { return a.re * b.re + a.im * b.im; }  // Re(conj(a) b)
+__device__ __forceinline__ float redot(float a, float b) { return a * b; }
+
+// parameter gradient of a node h*u with complex cotangent G (already carrying the factor h):
+// x-type u = -conj(z) = -(d - i w): (dd, dw) += (-Re G, Im G); z-type u = -z: (dd, dw) += (-Re G, -Im G)
+__device__ __forceinline__ void node_to_par(cf G, bool ztype, float& dd, float& dw) {
+  dd += -G.re;
+  dw += ztype ? -G.im : G.im;
+}
+__device__ __forceinline__ void node_to_par(float G, bool, float& dd, float&) { dd += -G; }
+
+// LDS layout shared by the host sizing and the kernels
+struct BwdLds {
+  int v, h, gb, gv, am, ck, hist, red, dh, g, total;  // offsets in floats
+};
+__host__ __device__ inline BwdLds bwd_lds_layout(int T, int d, int W, int NT, int NS, bool wave, bool full) {
+  BwdLds L;
+  int o = 0;
+  L.v = o; o += T * d;
+  L.h = o; o += T;
+  L.gb = o; o += kBLK * W;
+  L.gv = o; o += W;
+  L.am = o; o += W;
+  L.ck = o; o += full ? ((T + kBLK - 1) / kBLK) * NS * NT : 0;
+  L.hist = o; o += full ? kBLK * NS * NT : 0;
+  L.red = o; o += wave ? 0 : 8 * NT;
+  L.dh = o; o += full ? T * ((NT + 63) / 64) : 0;
+  L.g = o; o += 4 * NT;
+  L.total = o;
+  return L;
+}
+
 // ------------------------------------------------------------------------------------------- B1
 // Chunk-local adjoint with zero incoming cotangent: the cotangent mu(c) on the chunk's carry-in.
 // Level 1 uses linearity: each lane carries its pair's share of the plane cotangent, summed at the end.
-template <bool CPLX, int N, int MAXT>
+template <bool CPLX, int N, int MAXT, bool WAVE>
 __global__ __launch_bounds__(MAXT) void k_chunk_bwd_local(DiagArgs a) {
   using T = typename Types<CPLX>::T;
   extern __shared__ float smem[];
-  float* s_v = smem;
-  float* s_h = s_v + a.T * a.d;
-  float* s_red = s_h + a.T;  // MAXT * 2
+  const int NT = blockDim.x;
+  const BwdLds Lo = bwd_lds_layout(a.T, a.d, a.W, NT, 0, WAVE, false);
+  float* s_v = smem + Lo.v;
+  float* s_h = smem + Lo.h;
+  float* s_gb = smem + Lo.gb;
+  float* s_gv = smem + Lo.gv;
+  int* s_am = reinterpret_cast<int*>(smem + Lo.am);
+  float* s_red = smem + Lo.g;
   const int c = blockIdx.x, b = blockIdx.y, tid = threadIdx.x;
   const int t0 = c * a.T;
   const int Tc = min(a.T, a.n_int - t0);
+  const bool prefix = a.readout == EWS_READOUT_PREFIX;
   load_chunk(a, b, t0, Tc, s_v, s_h);
+  if (!prefix) stage_vec(a, b, s_gv, s_am);
+  const int nblk = (Tc + kBLK - 1) / kBLK;
+  float pf[kPF];
+  if (prefix) {
+    const int r0 = (nblk - 1) * kBLK;
+    const int n = (Tc - r0) * a.W;
+    pf_load(a, b, t0 + r0, n, pf);
+    pf_store(s_gb, n, pf);
+  }
   __syncthreads();
-  const LaneMap m = lane_map(a, tid);
+  const LaneMap m = lane_map_b<WAVE>(a, tid);
   const ChunkClock cc = chunk_clock<T>(a, b, Tc, s_h);
   T dummy{};
   const T uj = load_u(a.params, m.j, &dummy);
@@ -655,47 +852,64 @@ __global__ __launch_bounds__(MAXT) void k_chunk_bwd_local(DiagArgs a) {
   Coef<T> c0;
   CoefD<T> q;
   if (cc.fast) eval_coef<T, CPLX, N, true>(cc.hbar, cc.href, cc.per_int, uj, uk, c0, q);
+  GammaSrc gs{prefix ? s_gb : s_gv, s_am, 1.0f / (float)a.n_int, a.readout};
   T L1 = zero<T>(), LA = zero<T>(), LB = zero<T>();
-  if (m.active) {
-    for (int t = Tc - 1; t >= 0; --t) {
-      T g1, gA, gB;
-      gamma_at<CPLX, N>(a, m, b, t0 + t, g1, gA, gB);
-      L1 += g1;
-      LA += gA;
-      LB += gB;
-      const float h = s_h[t];
-      Coef<T> co;
-      if (cc.fast) {
-        lin_coef<T, CPLX, N>(c0, q, h - cc.hbar, cc.per_int, co);
-      } else {
-        CoefD<T> qq;
-        eval_coef<T, CPLX, N, false>(h, cc.href, cc.per_int, uj, uk, co, qq);
+  for (int blk = nblk - 1; blk >= 0; --blk) {
+    const bool more = prefix && blk > 0;
+    if (more) pf_load(a, b, t0 + (blk - 1) * kBLK, kBLK * a.W, pf);
+    if (m.active) {
+#pragma unroll 1
+      for (int s = kBLK - 1; s >= 0; --s) {
+        const int t = blk * kBLK + s;
+        if (t < Tc) {
+          T g1, gA, gB;
+          gamma_step<CPLX, N>(a, m, gs, s, t0 + t, g1, gA, gB);
+          L1 += g1;
+          LA += gA;
+          LB += gB;
+          const float h = s_h[t];
+          Coef<T> co;
+          if (cc.fast) {
+            lin_coef<T, CPLX, N>(c0, q, h - cc.hbar, cc.per_int, co);
+          } else {
+            CoefD<T> qq;
+            eval_coef_step<T, CPLX, N, false>(h, cc.href, cc.per_int, uj, uk, co, qq);
+          }
+          T toC = zero<T>();
+          if constexpr (N == 2) {
+            const T pk = lds_p<T>(s_v, t, a.d, m.k);
+            const T s1k = co.phi_k * pk;
+            toC = conjc(s1k) * LB;
+            if constexpr (CPLX) toC += s1k * LA;
+            LB = conjc(co.lamB) * LB;
+            if constexpr (CPLX) LA = conjc(co.lamA) * LA;
+          }
+          L1 = conjc(co.rho) * (L1 + toC);
+        }
       }
-      T toC = zero<T>();
-      if (N == 2) {
-        const T pk = lds_p<T>(s_v, t, a.d, m.k);
-        const T s1k = co.phi_k * pk;
-        toC = conjc(s1k) * LB;
-        if (CPLX) toC += s1k * LA;
-        LB = conjc(co.lamB) * LB;
-        if (CPLX) LA = conjc(co.lamA) * LA;
-      }
-      L1 = conjc(co.rho) * (L1 + toC);
+    }
+    if (more) {
+      __syncthreads();
+      pf_store(s_gb, kBLK * a.W, pf);
+      __syncthreads();
     }
   }
   float* mp = a.mu + ((size_t)b * a.C + c) * a.D;
-  if (N == 2) {
-    // plane cotangent = sum over the row's lanes
-    if (m.active) stT(s_red + 2 * tid, L1);
-    __syncthreads();
-    if (m.plane) {
-      T s = zero<T>();
-      for (int k = 0; k < a.K; ++k) s += ldT<CPLX, T>(s_red + 2 * (m.j * a.K + k));
-      stT(mp + st1<CPLX>(m.j), s);
+  if constexpr (N == 2) {
+    T s1 = zero<T>();
+    if constexpr (WAVE) {
+      s1 = row_sum8(L1);
+    } else {
+      if (m.active) stT(s_red + 2 * tid, L1);
+      __syncthreads();
+      if (m.plane) {
+        for (int k = 0; k < a.K; ++k) s1 += ldT<CPLX, T>(s_red + 2 * (m.j * a.K + k));
+      }
     }
+    if (m.plane) stT(mp + st1<CPLX>(m.j), s1);
     if (m.active) {
       float* p2 = mp + st2<CPLX>(a, m.j, m.k);
-      if (CPLX) {
+      if constexpr (CPLX) {
         stT(p2, LA);
         stT(p2 + 2, LB);
       } else {
@@ -708,124 +922,138 @@ __global__ __launch_bounds__(MAXT) void k_chunk_bwd_local(DiagArgs a) {
 }
 
 // ------------------------------------------------------------------------------------------- B2
-// Reverse float64 scan of chunk cotangents: X(c) = mu(c) + J_c^T X(c+1); writes mt[c-1] = X(c) (the cotangent
-// on chunk c-1's end state coming from chunks >= c) and mt[C-1] = 0.
+// Reverse float64 scan of chunk cotangents: X(c) = mu(c) + J_c^T X(c+1), J_c the Jacobian of chunk c's map on
+// its carry; writes mt[c-1] = X(c) (the cotangent on chunk c-1's end state from chunks >= c), mt[C-1] = 0.
+// Blocks of chunks are staged in LDS (mu rows, chunk flows, chunk level-1 increments) before the sequential
+// part, so the loop touches no global memory except its stores.
 template <bool CPLX, int N, int MAXT>
 __global__ __launch_bounds__(MAXT) void k_adjoint_scan(DiagArgs a) {
   using TD = typename Types<CPLX>::TD;
-  __shared__ double s_red[2 * MAXT];
+  extern __shared__ double dsm[];
+  const int K = a.K, CB = a.scan_cb, NT = blockDim.x;
+  constexpr int CW = CPLX ? 2 : 1;
+  double* s_F = dsm;                               // CB * K
+  double* s_l1 = s_F + (size_t)CB * K * CW;        // CB * K
+  double* s_red = s_l1 + (size_t)CB * K * CW;      // NT
+  float* s_mu = reinterpret_cast<float*>(s_red + (size_t)NT * CW);  // CB * D
   const int b = blockIdx.x, tid = threadIdx.x;
   const LaneMap m = lane_map(a, tid);
   TD dummy{};
   const TD uj = load_ud(a.params, m.j, &dummy);
   const TD uk = load_ud(a.params, m.k, &dummy);
   TD X1{}, XA{}, XB{};
-  // mt[C-1] = 0
   {
     float* mp = a.mt + ((size_t)b * a.C + (a.C - 1)) * a.D;
-    for (int i = tid; i < a.D; i += blockDim.x) mp[i] = 0.0f;
+    for (int i = tid; i < a.D; i += NT) mp[i] = 0.0f;
   }
-  for (int c = a.C - 1; c >= 1; --c) {
-    const int Tc = min(a.T, a.n_int - c * a.T);
-    const double tau = chunk_tau(a, b, c, Tc);
-    const TD Fj = dexp(mul_s(uj, tau));
-    TD toC{};
-    if (N == 2 && m.active) {
-      // chunk c's zero-carry level-1 increment l1_k = carry1(c+1) - F_k carry1(c)
+  for (int c1 = a.C - 1; c1 >= 1; c1 -= CB) {
+    const int cL = max(1, c1 - CB + 1);
+    const int nb = c1 - cL + 1;
+    __syncthreads();
+    copy_to_lds(s_mu, a.mu + ((size_t)b * a.C + cL) * a.D, nb * a.D);
+    for (int i = tid; i < nb * K; i += NT) {
+      const int cc = i / K, j = i % K, c = cL + cc;
+      const int Tc = min(a.T, a.n_int - c * a.T);
+      const TD u = load_ud(a.params, j, &dummy);
+      const TD F = dexp(mul_s(u, chunk_tau(a, b, c, Tc)));
+      stD(s_F + (size_t)i * CW, F);
       const double* cr0 = a.carries + ((size_t)b * (a.C + 1) + c) * a.D;
-      const double* cr1 = cr0 + a.D;
-      const TD Fk = dexp(mul_s(uk, tau));
-      const TD l1k = ldDD(cr1 + st1<CPLX>(m.k), &dummy) - Fk * ldDD(cr0 + st1<CPLX>(m.k), &dummy);
-      toC = conj(l1k) * XB;
-      if (CPLX) toC = toC + l1k * XA;
-      const TD lamB = dexp(mul_s(uj + uk, tau));
-      XB = conj(lamB) * XB;
-      if (CPLX) {
-        const TD lamA = dexp(mul_s(uj + conj(uk), tau));
-        XA = conj(lamA) * XA;
-      }
+      const TD l1 = ldDD(cr0 + a.D + st1<CPLX>(j), &dummy) - F * ldDD(cr0 + st1<CPLX>(j), &dummy);
+      stD(s_l1 + (size_t)i * CW, l1);
     }
-    if (N == 2) {
-      if (m.active) stD(s_red + 2 * tid, toC);
-      __syncthreads();
+    __syncthreads();
+    for (int c = c1; c >= cL; --c) {
+      const int cc = c - cL;
+      const TD Fj = ldDD(s_F + (size_t)(cc * K + m.j) * CW, &dummy);
+      TD toC{};
+      if (N == 2 && m.active) {
+        const TD Fk = ldDD(s_F + (size_t)(cc * K + m.k) * CW, &dummy);
+        const TD l1k = ldDD(s_l1 + (size_t)(cc * K + m.k) * CW, &dummy);
+        toC = conj(l1k) * XB;
+        if (CPLX) toC = toC + l1k * XA;
+        XB = conj(Fj * Fk) * XB;
+        if (CPLX) XA = conj(Fj * conj(Fk)) * XA;
+      }
+      if (N == 2) {
+        if (m.active) stD(s_red + (size_t)tid * CW, toC);
+        __syncthreads();
+        if (m.plane) {
+          TD s = X1;
+          for (int k = 0; k < K; ++k) s = s + ldDD(s_red + (size_t)(m.j * K + k) * CW, &dummy);
+          X1 = conj(Fj) * s;
+        }
+        __syncthreads();
+      } else if (m.plane) {
+        X1 = conj(Fj) * X1;
+      }
+      const float* mup = s_mu + (size_t)cc * a.D;
+      if (m.plane) X1 = X1 + ldD(mup + st1<CPLX>(m.j), &dummy);
+      if (N == 2 && m.active) {
+        const float* p2 = mup + st2<CPLX>(a, m.j, m.k);
+        if (CPLX) {
+          XA = XA + ldD(p2, &dummy);
+          XB = XB + ldD(p2 + 2, &dummy);
+        } else {
+          XB = XB + ldD(p2, &dummy);
+        }
+      }
+      float* mp = a.mt + ((size_t)b * a.C + (c - 1)) * a.D;
       if (m.plane) {
-        TD s = X1;
-        for (int k = 0; k < a.K; ++k) s = s + ldDD(s_red + 2 * (m.j * a.K + k), &dummy);
-        X1 = conj(Fj) * s;
+        mp[st1<CPLX>(m.j)] = (float)dre(X1);
+        if (CPLX) mp[st1<CPLX>(m.j) + 1] = (float)dim_(X1);
       }
-      __syncthreads();
-    } else if (m.plane) {
-      X1 = conj(Fj) * X1;
-    }
-    // + mu(c)
-    const float* mup = a.mu + ((size_t)b * a.C + c) * a.D;
-    if (m.plane) X1 = X1 + ldD(mup + st1<CPLX>(m.j), &dummy);
-    if (N == 2 && m.active) {
-      const float* p2 = mup + st2<CPLX>(a, m.j, m.k);
-      if (CPLX) {
-        XA = XA + ldD(p2, &dummy);
-        XB = XB + ldD(p2 + 2, &dummy);
-      } else {
-        XB = XB + ldD(p2, &dummy);
-      }
-    }
-    float* mp = a.mt + ((size_t)b * a.C + (c - 1)) * a.D;
-    if (m.plane) {
-      mp[st1<CPLX>(m.j)] = (float)dre(X1);
-      if (CPLX) mp[st1<CPLX>(m.j) + 1] = (float)dim_(X1);
-    }
-    if (N == 2 && m.active) {
-      float* p2 = mp + st2<CPLX>(a, m.j, m.k);
-      p2[0] = (float)dre(CPLX ? XA : XB);
-      if (CPLX) {
-        p2[1] = (float)dim_(XA);
-        p2[2] = (float)dre(XB);
-        p2[3] = (float)dim_(XB);
+      if (N == 2 && m.active) {
+        float* p2 = mp + st2<CPLX>(a, m.j, m.k);
+        p2[0] = (float)dre(CPLX ? XA : XB);
+        if (CPLX) {
+          p2[1] = (float)dim_(XA);
+          p2[2] = (float)dre(XB);
+          p2[3] = (float)dim_(XB);
+        }
       }
     }
   }
 }
 
 // ------------------------------------------------------------------------------------------- B3
-__device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-  for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o, 64);
-  return v;
-}
-__device__ __forceinline__ float redot(cf a, cf b) { return a.re * b.re + a.im * b.im; }  // Re(conj(a) b)
-__device__ __forceinline__ float redot(float a, float b) { return a * b; }
-
-// parameter gradient of a node h*u with complex cotangent G (already carrying the factor h):
-// x-type u = -conj(z) = -(d - i w): (dd, dw) += (-Re G, Im G); z-type u = -z: (dd, dw) += (-Re G, -Im G)
-__device__ __forceinline__ void node_to_par(cf G, bool ztype, float& dd, float& dw) {
-  dd += -G.re;
-  dw += ztype ? -G.im : G.im;
-}
-__device__ __forceinline__ void node_to_par(float G, bool, float& dd, float&) { dd += -G; }
-
-template <bool CPLX, int N, int MAXT>
+// Full adjoint of one chunk from its true end cotangent: forward states recomputed from the chunk's float64
+// carry (checkpoints every 8 steps, each block recomputed into registers), then the reverse sweep writes dv/dh
+// per interval and parameter partials per chunk.
+template <bool CPLX, int N, int MAXT, bool WAVE>
 __global__ __launch_bounds__(MAXT) void k_chunk_bwd_full(DiagArgs a) {
   using T = typename Types<CPLX>::T;
   constexpr int NS = CPLX ? 6 : 2;  // checkpoint floats per lane
-  constexpr int BLK = 8;
   extern __shared__ float smem[];
-  float* s_v = smem;
-  float* s_h = s_v + a.T * a.d;
-  const int nblk = (a.T + BLK - 1) / BLK;
   const int NT = blockDim.x, NW = (NT + 63) / 64;
-  float* s_ck = s_h + a.T;                       // nblk * NS * NT
-  float* s_rC = s_ck + nblk * NS * NT;           // 2 * NT  (sum over k -> row j)
-  float* s_rP = s_rC + 2 * NT;                   // 2 * NT  (sum over k -> row j)
-  float* s_cS = s_rP + 2 * NT;                   // 2 * NT  (sum over j -> column k)
-  float* s_cP = s_cS + 2 * NT;                   // 2 * NT  (sum over j -> column k)
-  float* s_dh = s_cP + 2 * NT;                   // T * NW
-  float* s_g = s_dh + a.T * NW;                  // NT * 4 parameter partials
+  const BwdLds Lo = bwd_lds_layout(a.T, a.d, a.W, NT, NS, WAVE, true);
+  float* s_v = smem + Lo.v;
+  float* s_h = smem + Lo.h;
+  float* s_gb = smem + Lo.gb;
+  float* s_gv = smem + Lo.gv;
+  int* s_am = reinterpret_cast<int*>(smem + Lo.am);
+  float* s_ck = smem + Lo.ck;
+  float* s_rC = smem + Lo.red;      // 2 NT each: row sums (over k) and column sums (over j)
+  float* s_rP = s_rC + 2 * NT;
+  float* s_cS = s_rP + 2 * NT;
+  float* s_cP = s_cS + 2 * NT;
+  float* s_dh = smem + Lo.dh;       // T * NW
+  float* s_g = smem + Lo.g;         // NT * 4 parameter partials
   const int c = blockIdx.x, b = blockIdx.y, tid = threadIdx.x;
   const int t0 = c * a.T;
   const int Tc = min(a.T, a.n_int - t0);
+  const bool prefix = a.readout == EWS_READOUT_PREFIX;
   load_chunk(a, b, t0, Tc, s_v, s_h);
+  if (!prefix) stage_vec(a, b, s_gv, s_am);
+  const int nblk = (Tc + kBLK - 1) / kBLK;
+  float pf[kPF];
+  if (prefix) {
+    const int r0 = (nblk - 1) * kBLK;
+    const int n = (Tc - r0) * a.W;
+    pf_load(a, b, t0 + r0, n, pf);
+    pf_store(s_gb, n, pf);
+  }
   __syncthreads();
-  const LaneMap m = lane_map(a, tid);
+  const LaneMap m = lane_map_b<WAVE>(a, tid);
   const ChunkClock cc = chunk_clock<T>(a, b, Tc, s_h);
   T dummy{};
   const T uj = load_u(a.params, m.j, &dummy);
@@ -834,34 +1062,40 @@ __global__ __launch_bounds__(MAXT) void k_chunk_bwd_full(DiagArgs a) {
   Coef<T> c0;
   CoefD<T> q0;
   if (cc.fast) eval_coef<T, CPLX, N, true>(cc.hbar, cc.href, cc.per_int, uj, uk, c0, q0);
+  GammaSrc gs{prefix ? s_gb : s_gv, s_am, 1.0f / (float)a.n_int, a.readout};
 
-  // forward pre-pass from the carry: checkpoints of the state before every BLK-th step
+  auto coef_at = [&](int t, Coef<T>& co, CoefD<T>& qq) {
+    if (cc.fast) {
+      lin_coef<T, CPLX, N>(c0, q0, s_h[t] - cc.hbar, cc.per_int, co);
+      qq = q0;
+    } else {
+      eval_coef_step<T, CPLX, N, true>(s_h[t], cc.href, cc.per_int, uj, uk, co, qq);
+    }
+  };
+  // forward pre-pass from the carry: checkpoints of the state before every kBLK-th step
   T S1 = zero<T>(), SA = zero<T>(), SB = zero<T>();
-  {
+  if (m.active) {
     const double* cr = a.carries + ((size_t)b * (a.C + 1) + c) * a.D;
-    if (m.active) {
-      S1 = ldTd<CPLX, T>(cr + st1<CPLX>(m.j));
-      if (N == 2) {
-        const double* p2 = cr + st2<CPLX>(a, m.j, m.k);
-        if (CPLX) {
-          SA = ldTd<CPLX, T>(p2);
-          SB = ldTd<CPLX, T>(p2 + 2);
-        } else {
-          SB = ldTd<CPLX, T>(p2);
-        }
+    S1 = ldTd<CPLX, T>(cr + st1<CPLX>(m.j));
+    if constexpr (N == 2) {
+      const double* p2 = cr + st2<CPLX>(a, m.j, m.k);
+      if constexpr (CPLX) {
+        SA = ldTd<CPLX, T>(p2);
+        SB = ldTd<CPLX, T>(p2 + 2);
+      } else {
+        SB = ldTd<CPLX, T>(p2);
       }
     }
   }
   auto ck_store = [&](int blk) {
     float* p = s_ck + (size_t)blk * NS * NT;
     if constexpr (CPLX) {
-      const cf s1 = S1, sa = SA, sb = SB;
-      p[0 * NT + tid] = s1.re;
-      p[1 * NT + tid] = s1.im;
-      p[2 * NT + tid] = sa.re;
-      p[3 * NT + tid] = sa.im;
-      p[4 * NT + tid] = sb.re;
-      p[5 * NT + tid] = sb.im;
+      p[0 * NT + tid] = S1.re;
+      p[1 * NT + tid] = S1.im;
+      p[2 * NT + tid] = SA.re;
+      p[3 * NT + tid] = SA.im;
+      p[4 * NT + tid] = SB.re;
+      p[5 * NT + tid] = SB.im;
     } else {
       p[0 * NT + tid] = S1;
       p[1 * NT + tid] = SB;
@@ -878,16 +1112,35 @@ __global__ __launch_bounds__(MAXT) void k_chunk_bwd_full(DiagArgs a) {
       SB = p[1 * NT + tid];
     }
   };
-  auto coef_at = [&](int t, Coef<T>& co, CoefD<T>& qq) {
-    if (cc.fast) {
-      lin_coef<T, CPLX, N>(c0, q0, s_h[t] - cc.hbar, cc.per_int, co);
-      qq = q0;
+  float* s_hist = smem + Lo.hist;
+  auto hist_store = [&](int hs) {
+    float* p = s_hist + (size_t)hs * NS * NT;
+    if constexpr (CPLX) {
+      p[0 * NT + tid] = S1.re;
+      p[1 * NT + tid] = S1.im;
+      p[2 * NT + tid] = SA.re;
+      p[3 * NT + tid] = SA.im;
+      p[4 * NT + tid] = SB.re;
+      p[5 * NT + tid] = SB.im;
     } else {
-      eval_coef<T, CPLX, N, true>(s_h[t], cc.href, cc.per_int, uj, uk, co, qq);
+      p[0 * NT + tid] = S1;
+      p[1 * NT + tid] = SB;
+    }
+  };
+  auto hist_load = [&](int hs, T& H1, T& HA, T& HB) {
+    const float* p = s_hist + (size_t)hs * NS * NT;
+    if constexpr (CPLX) {
+      H1 = cf{p[0 * NT + tid], p[1 * NT + tid]};
+      HA = cf{p[2 * NT + tid], p[3 * NT + tid]};
+      HB = cf{p[4 * NT + tid], p[5 * NT + tid]};
+    } else {
+      H1 = p[0 * NT + tid];
+      HA = 0.0f;
+      HB = p[1 * NT + tid];
     }
   };
   for (int t = 0; t < Tc; ++t) {
-    if ((t % BLK) == 0) ck_store(t / BLK);
+    if ((t % kBLK) == 0) ck_store(t / kBLK);
     Coef<T> co;
     CoefD<T> qq;
     coef_at(t, co, qq);
@@ -895,7 +1148,6 @@ __global__ __launch_bounds__(MAXT) void k_chunk_bwd_full(DiagArgs a) {
     const T pk = (N == 2) ? lds_p<T>(s_v, t, a.d, m.k) : zero<T>();
     fwd_step<T, CPLX, N>(co, pj, pk, S1, SA, SB);
   }
-  for (int i = tid; i < a.T * NW; i += NT) s_dh[i] = 0.0f;
 
   // cotangents on the chunk's end state from later chunks
   T L1 = zero<T>(), LA = zero<T>(), LB = zero<T>();
@@ -904,7 +1156,7 @@ __global__ __launch_bounds__(MAXT) void k_chunk_bwd_full(DiagArgs a) {
     if (m.plane) L1 = ldT<CPLX, T>(mp + st1<CPLX>(m.j));
     if (N == 2 && m.active) {
       const float* p2 = mp + st2<CPLX>(a, m.j, m.k);
-      if (CPLX) {
+      if constexpr (CPLX) {
         LA = ldT<CPLX, T>(p2);
         LB = ldT<CPLX, T>(p2 + 2);
       } else {
@@ -919,122 +1171,142 @@ __global__ __launch_bounds__(MAXT) void k_chunk_bwd_full(DiagArgs a) {
 
   __syncthreads();
   for (int blk = nblk - 1; blk >= 0; --blk) {
-    if (blk * BLK >= Tc) continue;
-    // recompute the block's states S(t-1)
-    T H1[BLK], HA[BLK], HB[BLK];
+    const bool more = prefix && blk > 0;
+    if (more) pf_load(a, b, t0 + (blk - 1) * kBLK, kBLK * a.W, pf);
+    // recompute the block's states S(t-1) into the LDS history (lane-private slots)
     ck_load(blk);
-#pragma unroll
-    for (int s = 0; s < BLK; ++s) {
-      const int t = blk * BLK + s;
-      H1[s] = S1;
-      HA[s] = SA;
-      HB[s] = SB;
-      if (t < Tc) {
-        Coef<T> co;
-        CoefD<T> qq;
-        coef_at(t, co, qq);
-        const T pj = lds_p<T>(s_v, t, a.d, m.j);
-        const T pk = (N == 2) ? lds_p<T>(s_v, t, a.d, m.k) : zero<T>();
-        fwd_step<T, CPLX, N>(co, pj, pk, S1, SA, SB);
-      }
-    }
-#pragma unroll
-    for (int s = BLK - 1; s >= 0; --s) {
-      const int t = blk * BLK + s;
-      if (t >= Tc) continue;
-      const int tg = t0 + t;
-      const float h = s_h[t];
-      T g1, gA, gB;
-      if (m.active) gamma_at<CPLX, N>(a, m, b, tg, g1, gA, gB);
-      else g1 = gA = gB = zero<T>();
-      L1 += g1;
-      LA += gA;
-      LB += gB;
+#pragma unroll 1
+    for (int s = 0; s < kBLK; ++s) {
+      const int t = blk * kBLK + s;
+      if (t >= Tc) break;
+      hist_store(s);
       Coef<T> co;
       CoefD<T> qq;
       coef_at(t, co, qq);
       const T pj = lds_p<T>(s_v, t, a.d, m.j);
       const T pk = (N == 2) ? lds_p<T>(s_v, t, a.d, m.k) : zero<T>();
-      const T cj = co.rho * H1[s];
-      float dhp = 0.0f;
-      if (N == 2) {
-        const T s1k = co.phi_k * pk;
-        T toC = conjc(s1k) * LB, toS = conjc(cj) * LB;
-        const T gf = conjc(co.IB) * LB;
-        T toPj = conjc(pk) * gf, toPk = conjc(pj) * gf;
-        const T gIB = conjc(pj * pk) * LB;
-        const T gLB = conjc(HB[s]) * LB;
-        Gx += h * (gIB * conjc(qq.DxB));
-        GyB += h * (gIB * conjc(qq.DyB));
-        dhp += redot(gIB, qq.IB1);
-        if (cc.per_int) {
-          GyB += h * (gLB * conjc(co.lamB));
-          dhp += redot(gLB, qq.lamB1);
-        } else {
-          SflowB += gLB;
-        }
-        if (CPLX) {
-          toC += s1k * LA;
-          toS += conjc(LA) * cj;
-          const T ge = conjc(co.IA) * LA;
-          toPj += pk * ge;
-          toPk += conjc(ge) * pj;
-          const T gIA = conjc(pj * conjc(pk)) * LA;
-          const T gLA = conjc(HA[s]) * LA;
-          Gx += h * (gIA * conjc(qq.DxA));
-          GyA += h * (gIA * conjc(qq.DyA));
-          dhp += redot(gIA, qq.IA1);
-          if (cc.per_int) {
-            GyA += h * (gLA * conjc(co.lamA));
-            dhp += redot(gLA, qq.lamA1);
-          } else {
-            SflowA += gLA;
-          }
-          LA = conjc(co.lamA) * LA;
-        }
-        LB = conjc(co.lamB) * LB;
-        if (m.active) {
-          stT(s_rC + 2 * tid, toC);
-          stT(s_rP + 2 * tid, toPj);
-          // column arrays are indexed by (k, j) so a plane lane reads a contiguous run
-          const int ct = m.k * a.K + m.j;
-          stT(s_cS + 2 * ct, toS);
-          stT(s_cP + 2 * ct, toPk);
-        }
-      }
-      __syncthreads();
-      if (m.plane) {
-        T rowC = zero<T>(), rowP = zero<T>(), colS = zero<T>(), colP = zero<T>();
-        if (N == 2) {
-          for (int kk = 0; kk < a.K; ++kk) {
-            rowC += ldT<CPLX, T>(s_rC + 2 * (m.j * a.K + kk));
-            rowP += ldT<CPLX, T>(s_rP + 2 * (m.j * a.K + kk));
-            colS += ldT<CPLX, T>(s_cS + 2 * (m.j * a.K + kk));
-            colP += ldT<CPLX, T>(s_cP + 2 * (m.j * a.K + kk));
-          }
-        }
-        const T gc = L1 + rowC;
-        const T gs1 = L1 + colS;
-        const T gp = conjc(co.phi_j) * gs1 + rowP + colP;
-        float* dvp = a.dv + ((size_t)b * a.n_int + tg) * a.d + st1<CPLX>(m.j);
-        dvp[0] = re(gp);
-        if (CPLX) dvp[1] = im(gp);
-        const T grho = conjc(H1[s]) * gc;
-        const T gphi = conjc(pj) * gs1;
-        Gxp += h * (gphi * conjc(qq.dphi_j));
-        dhp += redot(gphi, qq.phi_j1);
-        if (cc.per_int) {
-          Gxp += h * (grho * conjc(co.rho));
-          dhp += redot(grho, qq.rho1);
-        } else {
-          Sflow += grho;
-        }
-        L1 = conjc(co.rho) * gc;
-      }
-      const float ws = wave_sum(dhp);
-      if ((tid & 63) == 0) s_dh[t * NW + wid] = ws;
-      __syncthreads();
+      fwd_step<T, CPLX, N>(co, pj, pk, S1, SA, SB);
     }
+#pragma unroll 1
+    for (int s = kBLK - 1; s >= 0; --s) {
+      const int t = blk * kBLK + s;
+      if (t < Tc) {
+        T H1, HA, HB;
+        hist_load(s, H1, HA, HB);
+        const int tg = t0 + t;
+        const float h = s_h[t];
+        T g1, gA, gB;
+        gamma_step<CPLX, N>(a, m, gs, s, tg, g1, gA, gB);
+        L1 += g1;
+        LA += gA;
+        LB += gB;
+        Coef<T> co;
+        CoefD<T> qq;
+        coef_at(t, co, qq);
+        const T pj = lds_p<T>(s_v, t, a.d, m.j);
+        const T pk = (N == 2) ? lds_p<T>(s_v, t, a.d, m.k) : zero<T>();
+        const T cj = co.rho * H1;
+        float dhp = 0.0f;
+        T toC = zero<T>(), toS = zero<T>(), toPj = zero<T>(), toPk = zero<T>();
+        if constexpr (N == 2) {
+          const T s1k = co.phi_k * pk;
+          toC = conjc(s1k) * LB;
+          toS = conjc(cj) * LB;
+          const T gf = conjc(co.IB) * LB;
+          toPj = conjc(pk) * gf;
+          toPk = conjc(pj) * gf;
+          const T gIB = conjc(pj * pk) * LB;
+          const T gLB = conjc(HB) * LB;
+          Gx += h * (gIB * conjc(qq.DxB));
+          GyB += h * (gIB * conjc(qq.DyB));
+          dhp += redot(gIB, qq.IB1);
+          if (cc.per_int) {
+            GyB += h * (gLB * conjc(co.lamB));
+            dhp += redot(gLB, qq.lamB1);
+          } else {
+            SflowB += gLB;
+          }
+          if constexpr (CPLX) {
+            toC += s1k * LA;
+            toS += conjc(LA) * cj;
+            const T ge = conjc(co.IA) * LA;
+            toPj += pk * ge;
+            toPk += conjc(ge) * pj;
+            const T gIA = conjc(pj * conjc(pk)) * LA;
+            const T gLA = conjc(HA) * LA;
+            Gx += h * (gIA * conjc(qq.DxA));
+            GyA += h * (gIA * conjc(qq.DyA));
+            dhp += redot(gIA, qq.IA1);
+            if (cc.per_int) {
+              GyA += h * (gLA * conjc(co.lamA));
+              dhp += redot(gLA, qq.lamA1);
+            } else {
+              SflowA += gLA;
+            }
+            LA = conjc(co.lamA) * LA;
+          }
+          LB = conjc(co.lamB) * LB;
+        }
+        T rowC = zero<T>(), rowP = zero<T>(), colS = zero<T>(), colP = zero<T>();
+        if constexpr (N == 2) {
+          if constexpr (WAVE) {
+            rowC = row_sum8(toC);
+            rowP = row_sum8(toPj);
+            colS = col_sum8(toS);
+            colP = col_sum8(toPk);
+          } else {
+            if (m.active) {
+              stT(s_rC + 2 * tid, toC);
+              stT(s_rP + 2 * tid, toPj);
+              // column arrays are indexed by (k, j) so a plane lane reads a contiguous run
+              const int ct = m.k * a.K + m.j;
+              stT(s_cS + 2 * ct, toS);
+              stT(s_cP + 2 * ct, toPk);
+            }
+            __syncthreads();
+            if (m.plane) {
+              for (int kk = 0; kk < a.K; ++kk) {
+                rowC += ldT<CPLX, T>(s_rC + 2 * (m.j * a.K + kk));
+                rowP += ldT<CPLX, T>(s_rP + 2 * (m.j * a.K + kk));
+                colS += ldT<CPLX, T>(s_cS + 2 * (m.j * a.K + kk));
+                colP += ldT<CPLX, T>(s_cP + 2 * (m.j * a.K + kk));
+              }
+            }
+          }
+        }
+        if (m.plane) {
+          const T gc = L1 + rowC;
+          const T gs1 = L1 + colS;
+          const T gp = conjc(co.phi_j) * gs1 + rowP + colP;
+          float* dvp = a.dv + ((size_t)b * a.n_int + tg) * a.d + st1<CPLX>(m.j);
+          if constexpr (CPLX) {
+            dvp[0] = gp.re;
+            dvp[1] = gp.im;
+          } else {
+            dvp[0] = gp;
+          }
+          const T grho = conjc(H1) * gc;
+          const T gphi = conjc(pj) * gs1;
+          Gxp += h * (gphi * conjc(qq.dphi_j));
+          dhp += redot(gphi, qq.phi_j1);
+          if (cc.per_int) {
+            Gxp += h * (grho * conjc(co.rho));
+            dhp += redot(grho, qq.rho1);
+          } else {
+            Sflow += grho;
+          }
+          L1 = conjc(co.rho) * gc;
+        }
+        const float ws = wave_sum(dhp);
+        if ((tid & 63) == 0) s_dh[t * NW + wid] = ws;
+        if constexpr (!WAVE) __syncthreads();
+      }
+    }
+    if (more) {
+      __syncthreads();
+      pf_store(s_gb, kBLK * a.W, pf);
+    }
+    __syncthreads();
   }
 
   // dh of the chunk's intervals (fixed-order sum over waves)
@@ -1049,11 +1321,11 @@ __global__ __launch_bounds__(MAXT) void k_chunk_bwd_full(DiagArgs a) {
     if (!cc.per_int) {
       // cached flows: every step used the reference step href
       const float hr = cc.href;
-      if (N == 2) {
+      if constexpr (N == 2) {
         const T lamB = expv(hr * ub);
         GyB += hr * (SflowB * conjc(lamB));
         dhref += redot(SflowB, lamB * ub);
-        if (CPLX) {
+        if constexpr (CPLX) {
           const T lamA = expv(hr * ua);
           GyA += hr * (SflowA * conjc(lamA));
           dhref += redot(SflowA, lamA * ua);
@@ -1068,45 +1340,61 @@ __global__ __launch_bounds__(MAXT) void k_chunk_bwd_full(DiagArgs a) {
     node_to_par(Gx + Gxp, false, pj_d, pj_w);
     node_to_par(GyB, false, pj_d, pj_w);
     node_to_par(GyB, false, pk_d, pk_w);
-    if (CPLX) {
+    if constexpr (CPLX) {
       node_to_par(GyA, false, pj_d, pj_w);
       node_to_par(GyA, true, pk_d, pk_w);
     }
   }
-  __syncthreads();
-  s_g[4 * tid + 0] = pj_d;
-  s_g[4 * tid + 1] = pj_w;
-  s_g[4 * tid + 2] = pk_d;
-  s_g[4 * tid + 3] = pk_w;
-  const float whr = wave_sum(dhref);
-  if ((tid & 63) == 0) s_dh[wid] = whr;  // s_dh no longer needed for steps
-  __syncthreads();
-  if (tid < a.K) {
-    const int j = tid;
-    float sd = 0.0f, sw = 0.0f;
-    const int rows = (a.N == 2) ? a.K : 1;
-    for (int kk = 0; kk < rows; ++kk) {
-      const int lr = (a.N == 2) ? j * a.K + kk : j;  // lane (j, kk): row contributions
-      sd += s_g[4 * lr + 0];
-      sw += s_g[4 * lr + 1];
-      if (a.N == 2) {
-        const int lc = kk * a.K + j;  // lane (kk, j): column contributions
-        sd += s_g[4 * lc + 2];
-        sw += s_g[4 * lc + 3];
+  float* gpo = a.gp + ((size_t)b * a.C + c) * a.npar;
+  if constexpr (WAVE && N == 2) {
+    const float sd = row_sum8(pj_d) + col_sum8(pk_d);
+    const float sw = row_sum8(pj_w) + col_sum8(pk_w);
+    if (m.plane) {
+      if constexpr (CPLX) {
+        gpo[2 * m.j] = sd;
+        gpo[2 * m.j + 1] = sw;
+      } else {
+        gpo[m.j] = sd;
       }
     }
-    float* gp = a.gp + ((size_t)b * a.C + c) * a.npar;
-    if (CPLX) {
-      gp[2 * j] = sd;
-      gp[2 * j + 1] = sw;
-    } else {
-      gp[j] = sd;
+    const float whr = wave_sum(dhref);
+    if (tid == 0) a.gph[(size_t)b * a.C + c] = whr;
+  } else {
+    __syncthreads();
+    s_g[4 * tid + 0] = pj_d;
+    s_g[4 * tid + 1] = pj_w;
+    s_g[4 * tid + 2] = pk_d;
+    s_g[4 * tid + 3] = pk_w;
+    const float whr = wave_sum(dhref);
+    if ((tid & 63) == 0) s_dh[wid] = whr;  // s_dh no longer needed for steps
+    __syncthreads();
+    if (tid < a.K) {
+      const int j = tid;
+      float sd = 0.0f, sw = 0.0f;
+      const int S = (WAVE && a.N == 2) ? 8 : a.K;
+      const int rows = (a.N == 2) ? a.K : 1;
+      for (int kk = 0; kk < rows; ++kk) {
+        const int lr = (a.N == 2) ? j * S + kk : j;  // lane (j, kk): row contributions
+        sd += s_g[4 * lr + 0];
+        sw += s_g[4 * lr + 1];
+        if (a.N == 2) {
+          const int lc = kk * S + j;  // lane (kk, j): column contributions
+          sd += s_g[4 * lc + 2];
+          sw += s_g[4 * lc + 3];
+        }
+      }
+      if constexpr (CPLX) {
+        gpo[2 * j] = sd;
+        gpo[2 * j + 1] = sw;
+      } else {
+        gpo[j] = sd;
+      }
     }
-  }
-  if (tid == 0) {
-    float s = 0.0f;
-    for (int w = 0; w < NW; ++w) s += s_dh[w];
-    a.gph[(size_t)b * a.C + c] = s;
+    if (tid == 0) {
+      float s = 0.0f;
+      for (int w = 0; w < NW; ++w) s += s_dh[w];
+      a.gph[(size_t)b * a.C + c] = s;
+    }
   }
 }
 
@@ -1138,12 +1426,20 @@ __global__ void k_knot_grads(DiagArgs a) {
   }
 }
 
+// One block per parameter: fixed-order strided partial sums, then a fixed-shape tree (deterministic).
 __global__ void k_param_grads(DiagArgs a) {
-  for (int p = threadIdx.x; p < a.npar; p += blockDim.x) {
-    double s = 0.0;
-    for (int bc = 0; bc < a.B * a.C; ++bc) s += (double)a.gp[(size_t)bc * a.npar + p];
-    a.dparams[p] = (float)s;
+  __shared__ double red[256];
+  const int p = blockIdx.x;
+  const int n = a.B * a.C;
+  double s = 0.0;
+  for (int bc = threadIdx.x; bc < n; bc += blockDim.x) s += (double)a.gp[(size_t)bc * a.npar + p];
+  red[threadIdx.x] = s;
+  __syncthreads();
+  for (int o = blockDim.x / 2; o > 0; o >>= 1) {
+    if ((int)threadIdx.x < o) red[threadIdx.x] += red[threadIdx.x + o];
+    __syncthreads();
   }
+  if (threadIdx.x == 0) a.dparams[p] = (float)red[0];
 }
 
 }  // namespace ews
@@ -1157,9 +1453,18 @@ size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 
 struct Plan {
   int B, L, n_int, d, K, N, T, C, D, W, npar;
-  bool cplx;
-  int NT;
+  bool cplx, wave;
+  int NT, NTb, scan_cb;
+  size_t lds_bwd_local, lds_bwd_full, lds_carry, lds_adjoint;
 };
+
+constexpr size_t kMaxLds = 160 * 1024;  // LDS per workgroup on gfx950
+constexpr size_t kScanLds = 48 * 1024;
+
+size_t bwd_lds_bytes(const Plan& p, int T, bool full) {
+  const int NS = p.cplx ? 6 : 2;
+  return (size_t)bwd_lds_layout(T, p.d, p.W, p.NTb, NS, p.wave, full).total * 4;
+}
 
 int make_plan(const ews_diag_desc* s, Plan& p) {
   if (!s) return EWS_ERR_NULL;
@@ -1170,9 +1475,10 @@ int make_plan(const ews_diag_desc* s, Plan& p) {
   if (s->depth != 1 && s->depth != 2) return EWS_ERR_DEPTH;
   if (s->batch < 1 || s->length < 2 || s->dim < 1) return EWS_ERR_SHAPE;
   p.cplx = s->structure == EWS_STRUCT_PLANES;
-  if (p.cplx && (s->dim % 2 != 0 || s->dim > 64)) return EWS_ERR_SHAPE;
+  if (p.cplx && (s->dim % 2 != 0 || s->dim > 32)) return EWS_ERR_SHAPE;
   if (!p.cplx && s->dim > 32) return EWS_ERR_SHAPE;
   if ((s->flow_mode == EWS_FLOW_CACHED_BASEPOINT) && s->length < 3) return EWS_ERR_SHAPE;
+  if (s->chunk < 0) return EWS_ERR_SHAPE;
   p.B = s->batch;
   p.L = s->length;
   p.n_int = p.L - 1;
@@ -1184,10 +1490,25 @@ int make_plan(const ews_diag_desc* s, Plan& p) {
   p.npar = p.cplx ? 2 * p.K : p.K;
   const int P = (p.N == 2) ? p.K * p.K : p.K;
   p.NT = ((P + 63) / 64) * 64;
-  int T = s->chunk > 0 ? s->chunk : (p.NT >= 512 ? 32 : 64);
+  p.wave = p.K <= 8;  // one wavefront with lane = 8 j + k in the backward chunk kernels
+  p.NTb = p.wave ? 64 : p.NT;
+  if (kBLK * p.W > kPF * p.NTb) return EWS_ERR_SHAPE;  // cotangent block staging capacity
+  int T = s->chunk;
+  if (T == 0) {
+    T = 64;
+    while (T > 8 && bwd_lds_bytes(p, T, true) > kMaxLds) T /= 2;
+  }
   if (T > 256) T = 256;
   p.T = T;
   p.C = (p.n_int + T - 1) / T;
+  p.lds_bwd_local = bwd_lds_bytes(p, T, false);
+  p.lds_bwd_full = bwd_lds_bytes(p, T, true);
+  if (p.lds_bwd_full > kMaxLds) return EWS_ERR_SHAPE;
+  const int CW = p.cplx ? 2 : 1;
+  int cb = (int)((kScanLds - (size_t)p.NT * CW * 8) / ((size_t)p.D * 4 + (size_t)p.K * CW * 16));
+  p.scan_cb = cb < 1 ? 1 : (cb > 16 ? 16 : cb);
+  p.lds_carry = (size_t)p.scan_cb * p.K * CW * 8 + (size_t)p.scan_cb * p.D * 4;
+  p.lds_adjoint = (size_t)p.scan_cb * p.K * CW * 16 + (size_t)p.NT * CW * 8 + (size_t)p.scan_cb * p.D * 4;
   return EWS_OK;
 }
 
@@ -1216,7 +1537,7 @@ DiagArgs make_args(const ews_diag_desc* s, const Plan& p, const void* path, cons
                    const float* params, void* residual, void* workspace) {
   DiagArgs a{};
   a.B = p.B; a.L = p.L; a.n_int = p.n_int; a.d = p.d; a.K = p.K; a.N = p.N;
-  a.flow_mode = s->flow_mode; a.readout = s->readout; a.T = p.T; a.C = p.C;
+  a.flow_mode = s->flow_mode; a.readout = s->readout; a.T = p.T; a.C = p.C; a.scan_cb = p.scan_cb;
   a.W = p.W; a.lvl0 = s->level0 ? 1 : 0; a.off1 = a.lvl0; a.off2 = a.lvl0 + p.d; a.D = p.D; a.npar = p.npar;
   a.path_bf16 = s->path_dtype == EWS_DTYPE_BF16;
   a.path = path; a.clock = clock; a.params = params;
@@ -1233,61 +1554,118 @@ DiagArgs make_args(const ews_diag_desc* s, const Plan& p, const void* path, cons
 }
 
 size_t fwd_lds(const Plan& p) { return (size_t)(p.T * p.d + p.T) * 4; }
-size_t bwd_local_lds(const Plan& p) { return fwd_lds(p) + (size_t)2 * p.NT * 4; }
-size_t bwd_full_lds(const Plan& p) {
-  const int NS = p.cplx ? 6 : 2;
-  const int nblk = (p.T + 7) / 8;
-  const int NW = p.NT / 64;
-  return fwd_lds(p) + ((size_t)nblk * NS * p.NT + 8 * p.NT + (size_t)p.T * NW + 4 * p.NT) * 4;
-}
 
 #define EWS_LAUNCH_CHECK()                                  \
   do {                                                      \
     if (hipGetLastError() != hipSuccess) return EWS_ERR_LAUNCH; \
   } while (0)
 
+// Forward passes: 0 chunk summaries, 1 carry scan, 2 chunk outputs (prefix rows or mean/max partials),
+// 3 mean/max reduction. A pass that does not apply to the readout launches nothing.
 template <bool CPLX, int N, int MAXT>
-int run_forward(const ews_diag_desc* s, const Plan& p, DiagArgs a, hipStream_t st) {
+int forward_pass(const ews_diag_desc* s, const Plan& p, DiagArgs a, hipStream_t st, int pass) {
   dim3 grid(p.C, p.B), blk(p.NT);
-  hipLaunchKernelGGL((k_chunk_fwd<CPLX, N, MODE_SUMMARY, MAXT>), grid, blk, fwd_lds(p), st, a);
-  EWS_LAUNCH_CHECK();
-  hipLaunchKernelGGL((k_carry_scan<CPLX, N, MAXT>), dim3(p.B), blk, 0, st, a);
-  EWS_LAUNCH_CHECK();
-  if (s->readout == EWS_READOUT_PREFIX) {
-    hipLaunchKernelGGL((k_chunk_fwd<CPLX, N, MODE_PREFIX, MAXT>), grid, blk, fwd_lds(p), st, a);
-    EWS_LAUNCH_CHECK();
-  } else if (s->readout == EWS_READOUT_MEAN || s->readout == EWS_READOUT_MAX) {
-    hipLaunchKernelGGL((k_chunk_fwd<CPLX, N, MODE_REDUCE, MAXT>), grid, blk, fwd_lds(p), st, a);
-    EWS_LAUNCH_CHECK();
-    hipLaunchKernelGGL(k_reduce_readout, dim3(p.B), dim3(256), 0, st, a);
-    EWS_LAUNCH_CHECK();
+  switch (pass) {
+    case 0:
+      hipLaunchKernelGGL((k_chunk_fwd<CPLX, N, MODE_SUMMARY, MAXT>), grid, blk, fwd_lds(p), st, a);
+      break;
+    case 1:
+      hipLaunchKernelGGL((k_carry_scan<CPLX, N, MAXT>), dim3(p.B), blk, p.lds_carry, st, a);
+      break;
+    case 2:
+      if (s->readout == EWS_READOUT_PREFIX) {
+        hipLaunchKernelGGL((k_chunk_fwd<CPLX, N, MODE_PREFIX, MAXT>), grid, blk, fwd_lds(p), st, a);
+      } else if (s->readout == EWS_READOUT_MEAN || s->readout == EWS_READOUT_MAX) {
+        hipLaunchKernelGGL((k_chunk_fwd<CPLX, N, MODE_REDUCE, MAXT>), grid, blk, fwd_lds(p), st, a);
+      } else {
+        return EWS_OK;
+      }
+      break;
+    case 3:
+      if (s->readout == EWS_READOUT_MEAN || s->readout == EWS_READOUT_MAX) {
+        hipLaunchKernelGGL(k_reduce_readout, dim3(p.B), dim3(256), 0, st, a);
+      } else {
+        return EWS_OK;
+      }
+      break;
+    default:
+      return EWS_ERR_OPTION;
   }
+  EWS_LAUNCH_CHECK();
   return EWS_OK;
 }
 
-template <bool CPLX, int N, int MAXT>
-int run_backward(const Plan& p, DiagArgs a, hipStream_t st) {
-  dim3 grid(p.C, p.B), blk(p.NT);
-  hipLaunchKernelGGL((k_chunk_bwd_local<CPLX, N, MAXT>), grid, blk, bwd_local_lds(p), st, a);
-  EWS_LAUNCH_CHECK();
-  hipLaunchKernelGGL((k_adjoint_scan<CPLX, N, MAXT>), dim3(p.B), blk, 0, st, a);
-  EWS_LAUNCH_CHECK();
-  const size_t lds = bwd_full_lds(p);
-  if (lds > 65536) {
-    if (hipFuncSetAttribute(reinterpret_cast<const void*>(&k_chunk_bwd_full<CPLX, N, MAXT>),
-                            hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) != hipSuccess)
-      return EWS_ERR_LAUNCH;
+template <class K>
+int set_lds(K* kern, size_t lds) {
+  if (lds > 65536 &&
+      hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
+                          (int)lds) != hipSuccess)
+    return EWS_ERR_LAUNCH;
+  return EWS_OK;
+}
+
+// Backward passes: 0 chunk-local adjoints, 1 reverse adjoint scan, 2 full chunk adjoints, 3 knot gradients,
+// 4 parameter reduction.
+template <bool CPLX, int N, int MAXT, bool WAVE>
+int backward_pass(const Plan& p, DiagArgs a, hipStream_t st, int pass) {
+  dim3 grid(p.C, p.B), blkb(p.NTb);
+  switch (pass) {
+    case 0:
+      if (set_lds(&k_chunk_bwd_local<CPLX, N, MAXT, WAVE>, p.lds_bwd_local) != EWS_OK) return EWS_ERR_LAUNCH;
+      hipLaunchKernelGGL((k_chunk_bwd_local<CPLX, N, MAXT, WAVE>), grid, blkb, p.lds_bwd_local, st, a);
+      break;
+    case 1:
+      hipLaunchKernelGGL((k_adjoint_scan<CPLX, N, (MAXT < 256 ? 256 : MAXT)>), dim3(p.B), dim3(p.NT), p.lds_adjoint,
+                         st, a);
+      break;
+    case 2:
+      if (set_lds(&k_chunk_bwd_full<CPLX, N, MAXT, WAVE>, p.lds_bwd_full) != EWS_OK) return EWS_ERR_LAUNCH;
+      hipLaunchKernelGGL((k_chunk_bwd_full<CPLX, N, MAXT, WAVE>), grid, blkb, p.lds_bwd_full, st, a);
+      break;
+    case 3: {
+      const size_t total = (size_t)p.B * p.L;
+      const int nb = (int)((total + 255) / 256 < 4096 ? (total + 255) / 256 : 4096);
+      hipLaunchKernelGGL(k_knot_grads, dim3(nb), dim3(256), 0, st, a);
+      break;
+    }
+    case 4:
+      hipLaunchKernelGGL(k_param_grads, dim3(p.npar), dim3(256), 0, st, a);
+      break;
+    default:
+      return EWS_ERR_OPTION;
   }
-  hipLaunchKernelGGL((k_chunk_bwd_full<CPLX, N, MAXT>), grid, blk, lds, st, a);
-  EWS_LAUNCH_CHECK();
-  const size_t total = (size_t)p.B * p.L;
-  const int nb = (int)((total + 255) / 256 < 4096 ? (total + 255) / 256 : 4096);
-  hipLaunchKernelGGL(k_knot_grads, dim3(nb), dim3(256), 0, st, a);
-  EWS_LAUNCH_CHECK();
-  hipLaunchKernelGGL(k_param_grads, dim3(1), dim3(256), 0, st, a);
   EWS_LAUNCH_CHECK();
   return EWS_OK;
 }
+
+int dispatch_forward(const ews_diag_desc* s, const Plan& p, const DiagArgs& a, hipStream_t st, int pass) {
+  const bool big = p.NT > 256;
+  if (p.cplx) {
+    if (p.N == 2) return big ? forward_pass<true, 2, 1024>(s, p, a, st, pass) : forward_pass<true, 2, 256>(s, p, a, st, pass);
+    return forward_pass<true, 1, 256>(s, p, a, st, pass);
+  }
+  if (p.N == 2) return big ? forward_pass<false, 2, 1024>(s, p, a, st, pass) : forward_pass<false, 2, 256>(s, p, a, st, pass);
+  return forward_pass<false, 1, 256>(s, p, a, st, pass);
+}
+
+int dispatch_backward(const Plan& p, const DiagArgs& a, hipStream_t st, int pass) {
+  const bool big = p.NT > 256;
+  if (p.cplx) {
+    if (p.N == 2) {
+      if (p.wave) return backward_pass<true, 2, 64, true>(p, a, st, pass);
+      return big ? backward_pass<true, 2, 1024, false>(p, a, st, pass) : backward_pass<true, 2, 256, false>(p, a, st, pass);
+    }
+    return p.wave ? backward_pass<true, 1, 64, true>(p, a, st, pass) : backward_pass<true, 1, 256, false>(p, a, st, pass);
+  }
+  if (p.N == 2) {
+    if (p.wave) return backward_pass<false, 2, 64, true>(p, a, st, pass);
+    return big ? backward_pass<false, 2, 1024, false>(p, a, st, pass) : backward_pass<false, 2, 256, false>(p, a, st, pass);
+  }
+  return p.wave ? backward_pass<false, 1, 64, true>(p, a, st, pass) : backward_pass<false, 1, 256, false>(p, a, st, pass);
+}
+
+constexpr int kForwardPasses = 4;
+constexpr int kBackwardPasses = 5;
 
 }  // namespace
 
@@ -1305,47 +1683,57 @@ size_t ews_diag_residual_bytes(const ews_diag_desc* desc) {
   return resid_carries_bytes(p) + align256((size_t)p.B * p.W * 4);
 }
 
-int ews_diag_forward(const ews_diag_desc* desc, const void* path, const float* clock, const float* params,
-                     float* out, void* residual, void* workspace, ews_stream_t stream) {
+int ews_diag_forward_pass(const ews_diag_desc* desc, int pass, const void* path, const float* clock,
+                          const float* params, float* out, void* residual, void* workspace, ews_stream_t stream) {
   Plan p;
   const int rc = make_plan(desc, p);
   if (rc != EWS_OK) return rc;
   if (!path || !clock || !params || !out || !residual || !workspace) return EWS_ERR_NULL;
+  if (pass < 0 || pass >= kForwardPasses) return EWS_ERR_OPTION;
   DiagArgs a = make_args(desc, p, path, clock, params, residual, workspace);
   a.out = out;
-  hipStream_t st = (hipStream_t)stream;
-  const bool big = p.NT > 256;
-  if (p.cplx) {
-    if (p.N == 2) return big ? run_forward<true, 2, 1024>(desc, p, a, st) : run_forward<true, 2, 256>(desc, p, a, st);
-    return run_forward<true, 1, 256>(desc, p, a, st);
-  }
-  if (p.N == 2) return big ? run_forward<false, 2, 1024>(desc, p, a, st) : run_forward<false, 2, 256>(desc, p, a, st);
-  return run_forward<false, 1, 256>(desc, p, a, st);
+  return dispatch_forward(desc, p, a, (hipStream_t)stream, pass);
 }
 
-int ews_diag_backward(const ews_diag_desc* desc, const void* path, const float* clock, const float* params,
-                      const void* residual, const float* grad_out, float* grad_path, float* grad_clock,
-                      float* grad_params, void* workspace, ews_stream_t stream) {
+int ews_diag_forward(const ews_diag_desc* desc, const void* path, const float* clock, const float* params,
+                     float* out, void* residual, void* workspace, ews_stream_t stream) {
+  for (int pass = 0; pass < kForwardPasses; ++pass) {
+    const int rc = ews_diag_forward_pass(desc, pass, path, clock, params, out, residual, workspace, stream);
+    if (rc != EWS_OK) return rc;
+  }
+  return EWS_OK;
+}
+
+int ews_diag_backward_pass(const ews_diag_desc* desc, int pass, const void* path, const float* clock,
+                           const float* params, const void* residual, const float* grad_out, float* grad_path,
+                           float* grad_clock, float* grad_params, void* workspace, ews_stream_t stream) {
   Plan p;
   const int rc = make_plan(desc, p);
   if (rc != EWS_OK) return rc;
   if (!path || !clock || !params || !residual || !grad_out || !grad_path || !grad_clock || !grad_params ||
       !workspace)
     return EWS_ERR_NULL;
+  if (pass < 0 || pass >= kBackwardPasses) return EWS_ERR_OPTION;
   DiagArgs a = make_args(desc, p, path, clock, params, (void*)residual, workspace);
   a.gout = grad_out;
   a.dpath = grad_path;
   a.dclock = grad_clock;
   a.dparams = grad_params;
-  hipStream_t st = (hipStream_t)stream;
-  const bool big = p.NT > 256;
-  if (p.cplx) {
-    if (p.N == 2) return big ? run_backward<true, 2, 1024>(p, a, st) : run_backward<true, 2, 256>(p, a, st);
-    return run_backward<true, 1, 256>(p, a, st);
-  }
-  if (p.N == 2) return big ? run_backward<false, 2, 1024>(p, a, st) : run_backward<false, 2, 256>(p, a, st);
-  return run_backward<false, 1, 256>(p, a, st);
+  return dispatch_backward(p, a, (hipStream_t)stream, pass);
 }
+
+int ews_diag_backward(const ews_diag_desc* desc, const void* path, const float* clock, const float* params,
+                      const void* residual, const float* grad_out, float* grad_path, float* grad_clock,
+                      float* grad_params, void* workspace, ews_stream_t stream) {
+  for (int pass = 0; pass < kBackwardPasses; ++pass) {
+    const int rc = ews_diag_backward_pass(desc, pass, path, clock, params, residual, grad_out, grad_path,
+                                          grad_clock, grad_params, workspace, stream);
+    if (rc != EWS_OK) return rc;
+  }
+  return EWS_OK;
+}
+
+int ews_diag_num_passes(int direction) { return direction == 0 ? kForwardPasses : kBackwardPasses; }
 
 const char* ews_error_string(int code) {
   switch (code) {

@@ -28,6 +28,9 @@ EXPORTED = (
     "ews_diag_residual_bytes",
     "ews_diag_forward",
     "ews_diag_backward",
+    "ews_diag_forward_pass",
+    "ews_diag_backward_pass",
+    "ews_diag_num_passes",
     "ews_error_string",
     "ews_version",
 )
@@ -76,6 +79,12 @@ def load():
     lib.ews_diag_forward.restype = i32
     lib.ews_diag_backward.argtypes = [dp, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp]
     lib.ews_diag_backward.restype = i32
+    lib.ews_diag_forward_pass.argtypes = [dp, i32, vp, vp, vp, vp, vp, vp, vp]
+    lib.ews_diag_forward_pass.restype = i32
+    lib.ews_diag_backward_pass.argtypes = [dp, i32, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp]
+    lib.ews_diag_backward_pass.restype = i32
+    lib.ews_diag_num_passes.argtypes = [i32]
+    lib.ews_diag_num_passes.restype = i32
     lib.ews_error_string.argtypes = [i32]
     lib.ews_error_string.restype = ctypes.c_char_p
     lib.ews_version.argtypes = []

@@ -82,6 +82,22 @@ int ews_diag_backward(const ews_diag_desc* desc, const void* path, const float* 
                       const void* residual, const float* grad_out, float* grad_path, float* grad_clock,
                       float* grad_params, void* workspace, ews_stream_t stream);
 
+/* One pass of ews_diag_forward (pass 0 chunk summaries, 1 float64 carry scan over chunks, 2 chunk outputs,
+ * 3 mean/max reduction); running passes 0..ews_diag_num_passes(0)-1 in order is ews_diag_forward. A pass that
+ * does not apply to the readout launches nothing. For callers that place each kernel in its own custom call
+ * or time kernels separately. Replaces pass 1 / the XLA chunk scan / pass 3 of pallas_combine.py:1395-1422. */
+int ews_diag_forward_pass(const ews_diag_desc* desc, int pass, const void* path, const float* clock,
+                          const float* params, float* out, void* residual, void* workspace, ews_stream_t stream);
+
+/* One pass of ews_diag_backward (0 chunk-local adjoints, 1 float64 reverse adjoint scan, 2 full chunk adjoints,
+ * 3 knot gradients, 4 parameter reduction). Replaces B1 / B2 / B3 of pallas_combine.py:1698-1798. */
+int ews_diag_backward_pass(const ews_diag_desc* desc, int pass, const void* path, const float* clock,
+                           const float* params, const void* residual, const float* grad_out, float* grad_path,
+                           float* grad_clock, float* grad_params, void* workspace, ews_stream_t stream);
+
+/* Number of passes: direction 0 = forward, 1 = backward. */
+int ews_diag_num_passes(int direction);
+
 /* Human-readable text of a return code. */
 const char* ews_error_string(int code);
 
