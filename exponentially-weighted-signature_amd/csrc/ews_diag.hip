@@ -152,6 +152,10 @@ __device__ __forceinline__ void load_chunk(const DiagArgs& a, int b, int t0, int
   const float* th = a.clock + (size_t)b * a.L + t0;
   for (int k = threadIdx.x; k < Tc; k += st) s_h[k] = th[k + 1] - th[k];
 }
+__device__ __forceinline__ void load_clock(const DiagArgs& a, int b, int t0, int Tc, float* s_h) {
+  const float* th = a.clock + (size_t)b * a.L + t0;
+  for (int k = threadIdx.x; k < Tc; k += blockDim.x) s_h[k] = th[k + 1] - th[k];
+}
 
 // ------------------------------------------------------------------------------------------- coefficients
 template <class T> struct Coef {
@@ -210,13 +214,6 @@ __device__ __forceinline__ void eval_coef(float h, float hf, bool per_int, T uj,
   }
 }
 
-// The per-step exact evaluation (irregular clocks) stays out of line so it does not inflate the register
-// budget of the uniform-clock fast path it shares a loop with.
-template <class T, bool CPLX, int N, bool DERIV>
-__device__ __noinline__ void eval_coef_step(float h, float hf, bool per_int, T uj, T uk, Coef<T>& c, CoefD<T>& q) {
-  eval_coef<T, CPLX, N, DERIV>(h, hf, per_int, uj, uk, c, q);
-}
-
 // First-order model c(h_t) = c0 + c1 (h_t - hbar) of every h-dependent coefficient.
 template <class T, bool CPLX, int N>
 __device__ __forceinline__ void lin_coef(const Coef<T>& c0, const CoefD<T>& q, float dlt, bool per_int, Coef<T>& c) {
@@ -249,6 +246,7 @@ __device__ __forceinline__ void fwd_step(const Coef<T>& c, T pj, T pk, T& S1, T&
 struct ChunkClock {
   float hbar, href;
   bool fast, per_int;
+  bool inv_ok;  // stepping the recursion backwards amplifies errors by at most 2 over the chunk
 };
 
 template <class T>
@@ -277,6 +275,12 @@ __device__ __forceinline__ ChunkClock chunk_clock(const DiagArgs& a, int b, int 
   } else {
     cc.href = 0.0f;
   }
+  // largest contraction rate Re(-u_j) (the damping d_j of a plane, lambda_j of a real channel); a level-2
+  // element contracts at most at twice that rate, so the inverse step grows errors by e^{2 Dmax tau}
+  float Dmax = 0.0f;
+  for (int j = 0; j < a.K; ++j) Dmax = fmaxf(Dmax, -re(load_u(a.params, j, &dummy)));
+  const float tau = cc.per_int ? s : fabsf(cc.href) * (float)Tc;
+  cc.inv_ok = finite && (2.0f * Dmax * tau <= 0.69314718f);
   return cc;
 }
 
@@ -319,7 +323,7 @@ __device__ __forceinline__ void out_values(const DiagArgs& a, int j, int k, cf S
                                            float* val, int& n1, int& n2);
 
 // ------------------------------------------------------------------------------------------- F1 / F3
-template <bool CPLX, int N, int MODE, int MAXT>
+template <bool CPLX, int N, int MODE, int MAXT, bool FAST>
 __global__ __launch_bounds__(MAXT) void k_chunk_fwd(DiagArgs a) {
   using T = typename Types<CPLX>::T;
   extern __shared__ float smem[];
@@ -331,8 +335,9 @@ __global__ __launch_bounds__(MAXT) void k_chunk_fwd(DiagArgs a) {
   load_chunk(a, b, t0, Tc, s_v, s_h);
   __syncthreads();
   const LaneMap m = lane_map(a, tid);
-  if (!m.active) return;
   const ChunkClock cc = chunk_clock<T>(a, b, Tc, s_h);
+  if (cc.fast != FAST) return;  // the other instantiation owns this chunk
+  if (!m.active) return;
   T dummy{};
   const T uj = load_u(a.params, m.j, &dummy);
   const T uk = load_u(a.params, m.k, &dummy);
@@ -353,7 +358,7 @@ __global__ __launch_bounds__(MAXT) void k_chunk_fwd(DiagArgs a) {
   }
   Coef<T> c0;
   CoefD<T> q;
-  if (cc.fast) eval_coef<T, CPLX, N, true>(cc.hbar, cc.href, cc.per_int, uj, uk, c0, q);
+  if constexpr (FAST) eval_coef<T, CPLX, N, true>(cc.hbar, cc.href, cc.per_int, uj, uk, c0, q);
 
   // reduce-mode accumulators: [level-1 re, im][level-2 q00, q01, q10, q11]
   float acc[6];
@@ -368,11 +373,11 @@ __global__ __launch_bounds__(MAXT) void k_chunk_fwd(DiagArgs a) {
   for (int t = 0; t < Tc; ++t) {
     const float h = s_h[t];
     Coef<T> co;
-    if (cc.fast) {
+    if constexpr (FAST) {
       lin_coef<T, CPLX, N>(c0, q, h - cc.hbar, cc.per_int, co);
     } else {
       CoefD<T> qq;
-      eval_coef_step<T, CPLX, N, false>(h, cc.href, cc.per_int, uj, uk, co, qq);
+      eval_coef<T, CPLX, N, false>(h, cc.href, cc.per_int, uj, uk, co, qq);
     }
     const T pj = lds_p<T>(s_v, t, a.d, m.j);
     const T pk = (N == 2) ? lds_p<T>(s_v, t, a.d, m.k) : zero<T>();
@@ -706,23 +711,19 @@ __device__ __forceinline__ void gamma_row(const DiagArgs& a, const LaneMap& m, c
 
 // Cotangent rows of a prefix readout are staged in LDS eight steps at a time; the next block is loaded into
 // registers while the current one is processed, so no global load sits on the sequential dependency chain.
-constexpr int kPF = 36;
-constexpr int kBLK = 8;
-__device__ __forceinline__ void pf_load(const DiagArgs& a, int b, int tg0, int n, float (&pf)[kPF]) {
-  const float* src = a.gout + ((size_t)b * a.n_int + tg0) * a.W;
-#pragma unroll
-  for (int i = 0; i < kPF; ++i) {
-    const int idx = (int)threadIdx.x + i * (int)blockDim.x;
-    pf[i] = idx < n ? src[idx] : 0.0f;
+constexpr int kBLK = 8;   // checkpoint block and cotangent staging rows of the exact-coefficient adjoint
+constexpr int kGB = 4;    // cotangent staging rows of the local and inversion adjoints
+// Asynchronous copy of n contiguous floats into LDS (global_load_lds: each lane's dword lands at the wave's
+// LDS base + 4 * lane); completion is awaited with lds_dma_wait() before a barrier.
+typedef __attribute__((address_space(3))) void lds_void_t;
+__device__ __forceinline__ void lds_dma(float* dst, const float* src, int n) {
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, nw = (blockDim.x + 63) >> 6;
+  for (int base = w * 64; base < n; base += nw * 64) {
+    const int idx = base + lane;
+    if (idx < n) __builtin_amdgcn_global_load_lds((const void*)(src + idx), (lds_void_t*)(dst + base), 4, 0, 0);
   }
 }
-__device__ __forceinline__ void pf_store(float* dst, int n, const float (&pf)[kPF]) {
-#pragma unroll
-  for (int i = 0; i < kPF; ++i) {
-    const int idx = (int)threadIdx.x + i * (int)blockDim.x;
-    if (idx < n) dst[idx] = pf[i];
-  }
-}
+__device__ __forceinline__ void lds_dma_wait() { __builtin_amdgcn_s_waitcnt(0); }
 
 struct GammaSrc {
   const float* rows;  // prefix: staged block rows (kBLK x W); else the per-sample cotangent (W)
@@ -797,16 +798,17 @@ __device__ __forceinline__ void node_to_par(float G, bool, float& dd, float&) { 
 struct BwdLds {
   int v, h, gb, gv, am, ck, hist, red, dh, g, total;  // offsets in floats
 };
-__host__ __device__ inline BwdLds bwd_lds_layout(int T, int d, int W, int NT, int NS, bool wave, bool full) {
+__host__ __device__ inline BwdLds bwd_lds_layout(int T, int d, int W, int NT, int NS, bool wave, bool full,
+                                                int rows = kBLK) {
   BwdLds L;
   int o = 0;
   L.v = o; o += T * d;
   L.h = o; o += T;
-  L.gb = o; o += kBLK * W;
+  L.gb = o; o += 2 * rows * W;
   L.gv = o; o += W;
   L.am = o; o += W;
-  L.ck = o; o += full ? ((T + kBLK - 1) / kBLK) * NS * NT : 0;
-  L.hist = o; o += full ? kBLK * NS * NT : 0;
+  L.ck = o; o += (full && NS) ? ((T + kBLK - 1) / kBLK) * NS * NT : 0;
+  L.hist = o; o += (full && NS) ? kBLK * NS * NT : 0;
   L.red = o; o += wave ? 0 : 8 * NT;
   L.dh = o; o += full ? T * ((NT + 63) / 64) : 0;
   L.g = o; o += 4 * NT;
@@ -817,12 +819,12 @@ __host__ __device__ inline BwdLds bwd_lds_layout(int T, int d, int W, int NT, in
 // ------------------------------------------------------------------------------------------- B1
 // Chunk-local adjoint with zero incoming cotangent: the cotangent mu(c) on the chunk's carry-in.
 // Level 1 uses linearity: each lane carries its pair's share of the plane cotangent, summed at the end.
-template <bool CPLX, int N, int MAXT, bool WAVE>
+template <bool CPLX, int N, int MAXT, bool WAVE, bool FAST>
 __global__ __launch_bounds__(MAXT) void k_chunk_bwd_local(DiagArgs a) {
   using T = typename Types<CPLX>::T;
   extern __shared__ float smem[];
   const int NT = blockDim.x;
-  const BwdLds Lo = bwd_lds_layout(a.T, a.d, a.W, NT, 0, WAVE, false);
+  const BwdLds Lo = bwd_lds_layout(a.T, a.d, a.W, NT, 0, WAVE, false, kGB);
   float* s_v = smem + Lo.v;
   float* s_h = smem + Lo.h;
   float* s_gb = smem + Lo.gb;
@@ -833,34 +835,35 @@ __global__ __launch_bounds__(MAXT) void k_chunk_bwd_local(DiagArgs a) {
   const int t0 = c * a.T;
   const int Tc = min(a.T, a.n_int - t0);
   const bool prefix = a.readout == EWS_READOUT_PREFIX;
+  load_clock(a, b, t0, Tc, s_h);
+  __syncthreads();
+  const ChunkClock cc = chunk_clock<T>(a, b, Tc, s_h);
+  if (cc.fast != FAST) return;  // the other instantiation owns this chunk
   load_chunk(a, b, t0, Tc, s_v, s_h);
   if (!prefix) stage_vec(a, b, s_gv, s_am);
-  const int nblk = (Tc + kBLK - 1) / kBLK;
-  float pf[kPF];
-  if (prefix) {
-    const int r0 = (nblk - 1) * kBLK;
-    const int n = (Tc - r0) * a.W;
-    pf_load(a, b, t0 + r0, n, pf);
-    pf_store(s_gb, n, pf);
-  }
+  const int nblk = (Tc + kGB - 1) / kGB;
+  if (prefix) lds_dma(s_gb, a.gout + ((size_t)b * a.n_int + t0 + (nblk - 1) * kGB) * a.W,
+                      (Tc - (nblk - 1) * kGB) * a.W);
+  lds_dma_wait();
   __syncthreads();
   const LaneMap m = lane_map_b<WAVE>(a, tid);
-  const ChunkClock cc = chunk_clock<T>(a, b, Tc, s_h);
   T dummy{};
   const T uj = load_u(a.params, m.j, &dummy);
   const T uk = load_u(a.params, m.k, &dummy);
   Coef<T> c0;
   CoefD<T> q;
-  if (cc.fast) eval_coef<T, CPLX, N, true>(cc.hbar, cc.href, cc.per_int, uj, uk, c0, q);
-  GammaSrc gs{prefix ? s_gb : s_gv, s_am, 1.0f / (float)a.n_int, a.readout};
+  if constexpr (FAST) eval_coef<T, CPLX, N, true>(cc.hbar, cc.href, cc.per_int, uj, uk, c0, q);
   T L1 = zero<T>(), LA = zero<T>(), LB = zero<T>();
   for (int blk = nblk - 1; blk >= 0; --blk) {
+    const int buf = (nblk - 1 - blk) & 1;
     const bool more = prefix && blk > 0;
-    if (more) pf_load(a, b, t0 + (blk - 1) * kBLK, kBLK * a.W, pf);
+    if (more) lds_dma(s_gb + (buf ^ 1) * kGB * a.W, a.gout + ((size_t)b * a.n_int + t0 + (blk - 1) * kGB) * a.W,
+                      kGB * a.W);
+    const GammaSrc gs{prefix ? s_gb + buf * kGB * a.W : s_gv, s_am, 1.0f / (float)a.n_int, a.readout};
     if (m.active) {
 #pragma unroll 1
-      for (int s = kBLK - 1; s >= 0; --s) {
-        const int t = blk * kBLK + s;
+      for (int s = kGB - 1; s >= 0; --s) {
+        const int t = blk * kGB + s;
         if (t < Tc) {
           T g1, gA, gB;
           gamma_step<CPLX, N>(a, m, gs, s, t0 + t, g1, gA, gB);
@@ -869,11 +872,11 @@ __global__ __launch_bounds__(MAXT) void k_chunk_bwd_local(DiagArgs a) {
           LB += gB;
           const float h = s_h[t];
           Coef<T> co;
-          if (cc.fast) {
+          if constexpr (FAST) {
             lin_coef<T, CPLX, N>(c0, q, h - cc.hbar, cc.per_int, co);
           } else {
             CoefD<T> qq;
-            eval_coef_step<T, CPLX, N, false>(h, cc.href, cc.per_int, uj, uk, co, qq);
+            eval_coef<T, CPLX, N, false>(h, cc.href, cc.per_int, uj, uk, co, qq);
           }
           T toC = zero<T>();
           if constexpr (N == 2) {
@@ -889,8 +892,7 @@ __global__ __launch_bounds__(MAXT) void k_chunk_bwd_local(DiagArgs a) {
       }
     }
     if (more) {
-      __syncthreads();
-      pf_store(s_gb, kBLK * a.W, pf);
+      lds_dma_wait();
       __syncthreads();
     }
   }
@@ -1015,194 +1017,34 @@ __global__ __launch_bounds__(MAXT) void k_adjoint_scan(DiagArgs a) {
   }
 }
 
-// ------------------------------------------------------------------------------------------- B3
-// Full adjoint of one chunk from its true end cotangent: forward states recomputed from the chunk's float64
-// carry (checkpoints every 8 steps, each block recomputed into registers), then the reverse sweep writes dv/dh
-// per interval and parameter partials per chunk.
-template <bool CPLX, int N, int MAXT, bool WAVE>
-__global__ __launch_bounds__(MAXT) void k_chunk_bwd_full(DiagArgs a) {
-  using T = typename Types<CPLX>::T;
-  constexpr int NS = CPLX ? 6 : 2;  // checkpoint floats per lane
-  extern __shared__ float smem[];
-  const int NT = blockDim.x, NW = (NT + 63) / 64;
-  const BwdLds Lo = bwd_lds_layout(a.T, a.d, a.W, NT, NS, WAVE, true);
-  float* s_v = smem + Lo.v;
-  float* s_h = smem + Lo.h;
-  float* s_gb = smem + Lo.gb;
-  float* s_gv = smem + Lo.gv;
-  int* s_am = reinterpret_cast<int*>(smem + Lo.am);
-  float* s_ck = smem + Lo.ck;
-  float* s_rC = smem + Lo.red;      // 2 NT each: row sums (over k) and column sums (over j)
-  float* s_rP = s_rC + 2 * NT;
-  float* s_cS = s_rP + 2 * NT;
-  float* s_cP = s_cS + 2 * NT;
-  float* s_dh = smem + Lo.dh;       // T * NW
-  float* s_g = smem + Lo.g;         // NT * 4 parameter partials
-  const int c = blockIdx.x, b = blockIdx.y, tid = threadIdx.x;
-  const int t0 = c * a.T;
-  const int Tc = min(a.T, a.n_int - t0);
-  const bool prefix = a.readout == EWS_READOUT_PREFIX;
-  load_chunk(a, b, t0, Tc, s_v, s_h);
-  if (!prefix) stage_vec(a, b, s_gv, s_am);
-  const int nblk = (Tc + kBLK - 1) / kBLK;
-  float pf[kPF];
-  if (prefix) {
-    const int r0 = (nblk - 1) * kBLK;
-    const int n = (Tc - r0) * a.W;
-    pf_load(a, b, t0 + r0, n, pf);
-    pf_store(s_gb, n, pf);
-  }
-  __syncthreads();
-  const LaneMap m = lane_map_b<WAVE>(a, tid);
-  const ChunkClock cc = chunk_clock<T>(a, b, Tc, s_h);
-  T dummy{};
-  const T uj = load_u(a.params, m.j, &dummy);
-  const T uk = load_u(a.params, m.k, &dummy);
-  const T ua = uj + conjc(uk), ub = uj + uk;
-  Coef<T> c0;
-  CoefD<T> q0;
-  if (cc.fast) eval_coef<T, CPLX, N, true>(cc.hbar, cc.href, cc.per_int, uj, uk, c0, q0);
-  GammaSrc gs{prefix ? s_gb : s_gv, s_am, 1.0f / (float)a.n_int, a.readout};
+// Running cotangents and parameter accumulators of a backward chunk lane.
+template <class T> struct BwdAcc {
+  T L1, LA, LB;                    // cotangents of the state (level 1 of plane j; the pair's SA, SB)
+  T Gx, GyA, GyB, Gxp;             // node cotangents times h (per-interval coefficients)
+  T Sflow, SflowA, SflowB;         // summed flow cotangents (cached flows)
+};
+struct RedLds {
+  float *rC, *rP, *cS, *cP;        // LDS row/column sums (multi-wave workgroups)
+};
 
-  auto coef_at = [&](int t, Coef<T>& co, CoefD<T>& qq) {
-    if (cc.fast) {
-      lin_coef<T, CPLX, N>(c0, q0, s_h[t] - cc.hbar, cc.per_int, co);
-      qq = q0;
-    } else {
-      eval_coef_step<T, CPLX, N, true>(s_h[t], cc.href, cc.per_int, uj, uk, co, qq);
-    }
-  };
-  // forward pre-pass from the carry: checkpoints of the state before every kBLK-th step
-  T S1 = zero<T>(), SA = zero<T>(), SB = zero<T>();
-  if (m.active) {
-    const double* cr = a.carries + ((size_t)b * (a.C + 1) + c) * a.D;
-    S1 = ldTd<CPLX, T>(cr + st1<CPLX>(m.j));
-    if constexpr (N == 2) {
-      const double* p2 = cr + st2<CPLX>(a, m.j, m.k);
-      if constexpr (CPLX) {
-        SA = ldTd<CPLX, T>(p2);
-        SB = ldTd<CPLX, T>(p2 + 2);
-      } else {
-        SB = ldTd<CPLX, T>(p2);
-      }
-    }
-  }
-  auto ck_store = [&](int blk) {
-    float* p = s_ck + (size_t)blk * NS * NT;
-    if constexpr (CPLX) {
-      p[0 * NT + tid] = S1.re;
-      p[1 * NT + tid] = S1.im;
-      p[2 * NT + tid] = SA.re;
-      p[3 * NT + tid] = SA.im;
-      p[4 * NT + tid] = SB.re;
-      p[5 * NT + tid] = SB.im;
-    } else {
-      p[0 * NT + tid] = S1;
-      p[1 * NT + tid] = SB;
-    }
-  };
-  auto ck_load = [&](int blk) {
-    const float* p = s_ck + (size_t)blk * NS * NT;
-    if constexpr (CPLX) {
-      S1 = cf{p[0 * NT + tid], p[1 * NT + tid]};
-      SA = cf{p[2 * NT + tid], p[3 * NT + tid]};
-      SB = cf{p[4 * NT + tid], p[5 * NT + tid]};
-    } else {
-      S1 = p[0 * NT + tid];
-      SB = p[1 * NT + tid];
-    }
-  };
-  float* s_hist = smem + Lo.hist;
-  auto hist_store = [&](int hs) {
-    float* p = s_hist + (size_t)hs * NS * NT;
-    if constexpr (CPLX) {
-      p[0 * NT + tid] = S1.re;
-      p[1 * NT + tid] = S1.im;
-      p[2 * NT + tid] = SA.re;
-      p[3 * NT + tid] = SA.im;
-      p[4 * NT + tid] = SB.re;
-      p[5 * NT + tid] = SB.im;
-    } else {
-      p[0 * NT + tid] = S1;
-      p[1 * NT + tid] = SB;
-    }
-  };
-  auto hist_load = [&](int hs, T& H1, T& HA, T& HB) {
-    const float* p = s_hist + (size_t)hs * NS * NT;
-    if constexpr (CPLX) {
-      H1 = cf{p[0 * NT + tid], p[1 * NT + tid]};
-      HA = cf{p[2 * NT + tid], p[3 * NT + tid]};
-      HB = cf{p[4 * NT + tid], p[5 * NT + tid]};
-    } else {
-      H1 = p[0 * NT + tid];
-      HA = 0.0f;
-      HB = p[1 * NT + tid];
-    }
-  };
-  for (int t = 0; t < Tc; ++t) {
-    if ((t % kBLK) == 0) ck_store(t / kBLK);
-    Coef<T> co;
-    CoefD<T> qq;
-    coef_at(t, co, qq);
-    const T pj = lds_p<T>(s_v, t, a.d, m.j);
-    const T pk = (N == 2) ? lds_p<T>(s_v, t, a.d, m.k) : zero<T>();
-    fwd_step<T, CPLX, N>(co, pj, pk, S1, SA, SB);
-  }
-
-  // cotangents on the chunk's end state from later chunks
-  T L1 = zero<T>(), LA = zero<T>(), LB = zero<T>();
-  {
-    const float* mp = a.mt + ((size_t)b * a.C + c) * a.D;
-    if (m.plane) L1 = ldT<CPLX, T>(mp + st1<CPLX>(m.j));
-    if (N == 2 && m.active) {
-      const float* p2 = mp + st2<CPLX>(a, m.j, m.k);
-      if constexpr (CPLX) {
-        LA = ldT<CPLX, T>(p2);
-        LB = ldT<CPLX, T>(p2 + 2);
-      } else {
-        LB = ldT<CPLX, T>(p2);
-      }
-    }
-  }
-  // parameter-gradient accumulators (node cotangents times h)
-  T Gx = zero<T>(), GyA = zero<T>(), GyB = zero<T>(), Gxp = zero<T>();
-  T Sflow = zero<T>(), SflowA = zero<T>(), SflowB = zero<T>();  // cached flows: summed cotangents
-  const int wid = tid / 64;
-
-  __syncthreads();
-  for (int blk = nblk - 1; blk >= 0; --blk) {
-    const bool more = prefix && blk > 0;
-    if (more) pf_load(a, b, t0 + (blk - 1) * kBLK, kBLK * a.W, pf);
-    // recompute the block's states S(t-1) into the LDS history (lane-private slots)
-    ck_load(blk);
-#pragma unroll 1
-    for (int s = 0; s < kBLK; ++s) {
-      const int t = blk * kBLK + s;
-      if (t >= Tc) break;
-      hist_store(s);
-      Coef<T> co;
-      CoefD<T> qq;
-      coef_at(t, co, qq);
-      const T pj = lds_p<T>(s_v, t, a.d, m.j);
-      const T pk = (N == 2) ? lds_p<T>(s_v, t, a.d, m.k) : zero<T>();
-      fwd_step<T, CPLX, N>(co, pj, pk, S1, SA, SB);
-    }
-#pragma unroll 1
-    for (int s = kBLK - 1; s >= 0; --s) {
-      const int t = blk * kBLK + s;
-      if (t < Tc) {
-        T H1, HA, HB;
-        hist_load(s, H1, HA, HB);
-        const int tg = t0 + t;
-        const float h = s_h[t];
+// One reverse step of the adjoint at interval t (global interval tg): adds the readout cotangent, then the
+// adjoint of the Chen step with the state S(t-1) = (H1, HA, HB), writes dv[tg] for the plane lanes and the
+// step's dh partial to s_dh, and moves acc's cotangents from S(t) to S(t-1).
+template <bool CPLX, int N, bool WAVE, class T>
+__device__ __forceinline__ void bwd_step(const DiagArgs& a, const LaneMap& m, const GammaSrc& gs, int s, int t, int tg,
+                                         float h, const float* s_v, bool per_int, const Coef<T>& co,
+                                         const CoefD<T>& qq, BwdAcc<T>& acc, T H1, T HA, T HB, const RedLds& red,
+                                         float* s_dh) {
+  const int tid = threadIdx.x, NW = (blockDim.x + 63) / 64, wid = tid / 64, b = blockIdx.y;
+  float* s_rC = red.rC;
+  float* s_rP = red.rP;
+  float* s_cS = red.cS;
+  float* s_cP = red.cP;
         T g1, gA, gB;
         gamma_step<CPLX, N>(a, m, gs, s, tg, g1, gA, gB);
-        L1 += g1;
-        LA += gA;
-        LB += gB;
-        Coef<T> co;
-        CoefD<T> qq;
-        coef_at(t, co, qq);
+        acc.L1 += g1;
+        acc.LA += gA;
+        acc.LB += gB;
         const T pj = lds_p<T>(s_v, t, a.d, m.j);
         const T pk = (N == 2) ? lds_p<T>(s_v, t, a.d, m.k) : zero<T>();
         const T cj = co.rho * H1;
@@ -1210,42 +1052,42 @@ __global__ __launch_bounds__(MAXT) void k_chunk_bwd_full(DiagArgs a) {
         T toC = zero<T>(), toS = zero<T>(), toPj = zero<T>(), toPk = zero<T>();
         if constexpr (N == 2) {
           const T s1k = co.phi_k * pk;
-          toC = conjc(s1k) * LB;
-          toS = conjc(cj) * LB;
-          const T gf = conjc(co.IB) * LB;
+          toC = conjc(s1k) * acc.LB;
+          toS = conjc(cj) * acc.LB;
+          const T gf = conjc(co.IB) * acc.LB;
           toPj = conjc(pk) * gf;
           toPk = conjc(pj) * gf;
-          const T gIB = conjc(pj * pk) * LB;
-          const T gLB = conjc(HB) * LB;
-          Gx += h * (gIB * conjc(qq.DxB));
-          GyB += h * (gIB * conjc(qq.DyB));
+          const T gIB = conjc(pj * pk) * acc.LB;
+          const T gLB = conjc(HB) * acc.LB;
+          acc.Gx += h * (gIB * conjc(qq.DxB));
+          acc.GyB += h * (gIB * conjc(qq.DyB));
           dhp += redot(gIB, qq.IB1);
-          if (cc.per_int) {
-            GyB += h * (gLB * conjc(co.lamB));
+          if (per_int) {
+            acc.GyB += h * (gLB * conjc(co.lamB));
             dhp += redot(gLB, qq.lamB1);
           } else {
-            SflowB += gLB;
+            acc.SflowB += gLB;
           }
           if constexpr (CPLX) {
-            toC += s1k * LA;
-            toS += conjc(LA) * cj;
-            const T ge = conjc(co.IA) * LA;
+            toC += s1k * acc.LA;
+            toS += conjc(acc.LA) * cj;
+            const T ge = conjc(co.IA) * acc.LA;
             toPj += pk * ge;
             toPk += conjc(ge) * pj;
-            const T gIA = conjc(pj * conjc(pk)) * LA;
-            const T gLA = conjc(HA) * LA;
-            Gx += h * (gIA * conjc(qq.DxA));
-            GyA += h * (gIA * conjc(qq.DyA));
+            const T gIA = conjc(pj * conjc(pk)) * acc.LA;
+            const T gLA = conjc(HA) * acc.LA;
+            acc.Gx += h * (gIA * conjc(qq.DxA));
+            acc.GyA += h * (gIA * conjc(qq.DyA));
             dhp += redot(gIA, qq.IA1);
-            if (cc.per_int) {
-              GyA += h * (gLA * conjc(co.lamA));
+            if (per_int) {
+              acc.GyA += h * (gLA * conjc(co.lamA));
               dhp += redot(gLA, qq.lamA1);
             } else {
-              SflowA += gLA;
+              acc.SflowA += gLA;
             }
-            LA = conjc(co.lamA) * LA;
+            acc.LA = conjc(co.lamA) * acc.LA;
           }
-          LB = conjc(co.lamB) * LB;
+          acc.LB = conjc(co.lamB) * acc.LB;
         }
         T rowC = zero<T>(), rowP = zero<T>(), colS = zero<T>(), colP = zero<T>();
         if constexpr (N == 2) {
@@ -1275,8 +1117,8 @@ __global__ __launch_bounds__(MAXT) void k_chunk_bwd_full(DiagArgs a) {
           }
         }
         if (m.plane) {
-          const T gc = L1 + rowC;
-          const T gs1 = L1 + colS;
+          const T gc = acc.L1 + rowC;
+          const T gs1 = acc.L1 + colS;
           const T gp = conjc(co.phi_j) * gs1 + rowP + colP;
           float* dvp = a.dv + ((size_t)b * a.n_int + tg) * a.d + st1<CPLX>(m.j);
           if constexpr (CPLX) {
@@ -1287,35 +1129,34 @@ __global__ __launch_bounds__(MAXT) void k_chunk_bwd_full(DiagArgs a) {
           }
           const T grho = conjc(H1) * gc;
           const T gphi = conjc(pj) * gs1;
-          Gxp += h * (gphi * conjc(qq.dphi_j));
+          acc.Gxp += h * (gphi * conjc(qq.dphi_j));
           dhp += redot(gphi, qq.phi_j1);
-          if (cc.per_int) {
-            Gxp += h * (grho * conjc(co.rho));
+          if (per_int) {
+            acc.Gxp += h * (grho * conjc(co.rho));
             dhp += redot(grho, qq.rho1);
           } else {
-            Sflow += grho;
+            acc.Sflow += grho;
           }
-          L1 = conjc(co.rho) * gc;
+          acc.L1 = conjc(co.rho) * gc;
         }
         const float ws = wave_sum(dhp);
         if ((tid & 63) == 0) s_dh[t * NW + wid] = ws;
         if constexpr (!WAVE) __syncthreads();
-      }
-    }
-    if (more) {
-      __syncthreads();
-      pf_store(s_gb, kBLK * a.W, pf);
-    }
-    __syncthreads();
-  }
+}
 
-  // dh of the chunk's intervals (fixed-order sum over waves)
+// ------------------------------------------------------------------------------------------- B3
+// Chunk epilogue of the full adjoint: dh of the chunk's intervals (fixed-order sum over waves) and the chunk's
+// parameter partials (lane (j, k) contributes to plane j as a row and to plane k as a column).
+template <bool CPLX, int N, bool WAVE, class T>
+__device__ __forceinline__ void bwd_epilogue(const DiagArgs& a, const LaneMap& m, const ChunkClock& cc, BwdAcc<T>& acc,
+                                             T uj, T ua, T ub, int Tc, int t0, float* s_dh, float* s_g) {
+  const int tid = threadIdx.x, NT = blockDim.x, NW = (NT + 63) / 64, wid = tid / 64;
+  const int c = blockIdx.x, b = blockIdx.y;
   for (int t = tid; t < Tc; t += NT) {
     float s = 0.0f;
     for (int w = 0; w < NW; ++w) s += s_dh[t * NW + w];
     a.dh[(size_t)b * a.n_int + t0 + t] = s;
   }
-  // parameter partials: lane (j, k) -> plane j (row) and plane k (column) contributions, then plane sums
   float pj_d = 0.0f, pj_w = 0.0f, pk_d = 0.0f, pk_w = 0.0f, dhref = 0.0f;
   if (m.active) {
     if (!cc.per_int) {
@@ -1323,26 +1164,26 @@ __global__ __launch_bounds__(MAXT) void k_chunk_bwd_full(DiagArgs a) {
       const float hr = cc.href;
       if constexpr (N == 2) {
         const T lamB = expv(hr * ub);
-        GyB += hr * (SflowB * conjc(lamB));
-        dhref += redot(SflowB, lamB * ub);
+        acc.GyB += hr * (acc.SflowB * conjc(lamB));
+        dhref += redot(acc.SflowB, lamB * ub);
         if constexpr (CPLX) {
           const T lamA = expv(hr * ua);
-          GyA += hr * (SflowA * conjc(lamA));
-          dhref += redot(SflowA, lamA * ua);
+          acc.GyA += hr * (acc.SflowA * conjc(lamA));
+          dhref += redot(acc.SflowA, lamA * ua);
         }
       }
       if (m.plane) {
         const T rho = expv(hr * uj);
-        Gxp += hr * (Sflow * conjc(rho));
-        dhref += redot(Sflow, rho * uj);
+        acc.Gxp += hr * (acc.Sflow * conjc(rho));
+        dhref += redot(acc.Sflow, rho * uj);
       }
     }
-    node_to_par(Gx + Gxp, false, pj_d, pj_w);
-    node_to_par(GyB, false, pj_d, pj_w);
-    node_to_par(GyB, false, pk_d, pk_w);
+    node_to_par(acc.Gx + acc.Gxp, false, pj_d, pj_w);
+    node_to_par(acc.GyB, false, pj_d, pj_w);
+    node_to_par(acc.GyB, false, pk_d, pk_w);
     if constexpr (CPLX) {
-      node_to_par(GyA, false, pj_d, pj_w);
-      node_to_par(GyA, true, pk_d, pk_w);
+      node_to_par(acc.GyA, false, pj_d, pj_w);
+      node_to_par(acc.GyA, true, pk_d, pk_w);
     }
   }
   float* gpo = a.gp + ((size_t)b * a.C + c) * a.npar;
@@ -1366,7 +1207,7 @@ __global__ __launch_bounds__(MAXT) void k_chunk_bwd_full(DiagArgs a) {
     s_g[4 * tid + 2] = pk_d;
     s_g[4 * tid + 3] = pk_w;
     const float whr = wave_sum(dhref);
-    if ((tid & 63) == 0) s_dh[wid] = whr;  // s_dh no longer needed for steps
+    if ((tid & 63) == 0) s_dh[wid] = whr;  // the step partials were consumed above
     __syncthreads();
     if (tid < a.K) {
       const int j = tid;
@@ -1374,11 +1215,11 @@ __global__ __launch_bounds__(MAXT) void k_chunk_bwd_full(DiagArgs a) {
       const int S = (WAVE && a.N == 2) ? 8 : a.K;
       const int rows = (a.N == 2) ? a.K : 1;
       for (int kk = 0; kk < rows; ++kk) {
-        const int lr = (a.N == 2) ? j * S + kk : j;  // lane (j, kk): row contributions
+        const int lr = (a.N == 2) ? j * S + kk : j;
         sd += s_g[4 * lr + 0];
         sw += s_g[4 * lr + 1];
         if (a.N == 2) {
-          const int lc = kk * S + j;  // lane (kk, j): column contributions
+          const int lc = kk * S + j;
           sd += s_g[4 * lc + 2];
           sw += s_g[4 * lc + 3];
         }
@@ -1396,6 +1237,235 @@ __global__ __launch_bounds__(MAXT) void k_chunk_bwd_full(DiagArgs a) {
       a.gph[(size_t)b * a.C + c] = s;
     }
   }
+}
+
+// State loads of the lane from a float64 kernel-layout row / cotangent loads from a float32 row.
+template <bool CPLX, int N, class T>
+__device__ __forceinline__ void load_state_d(const DiagArgs& a, const LaneMap& m, const double* cr, T& S1, T& SA, T& SB) {
+  S1 = SA = SB = zero<T>();
+  if (!m.active) return;
+  S1 = ldTd<CPLX, T>(cr + st1<CPLX>(m.j));
+  if constexpr (N == 2) {
+    const double* p2 = cr + st2<CPLX>(a, m.j, m.k);
+    if constexpr (CPLX) {
+      SA = ldTd<CPLX, T>(p2);
+      SB = ldTd<CPLX, T>(p2 + 2);
+    } else {
+      SB = ldTd<CPLX, T>(p2);
+    }
+  }
+}
+template <bool CPLX, int N, class T>
+__device__ __forceinline__ void load_cot(const DiagArgs& a, const LaneMap& m, const float* mp, BwdAcc<T>& acc) {
+  acc = BwdAcc<T>{zero<T>(), zero<T>(), zero<T>(), zero<T>(), zero<T>(), zero<T>(), zero<T>(),
+                  zero<T>(), zero<T>(), zero<T>()};
+  if (m.plane) acc.L1 = ldT<CPLX, T>(mp + st1<CPLX>(m.j));
+  if (N == 2 && m.active) {
+    const float* p2 = mp + st2<CPLX>(a, m.j, m.k);
+    if constexpr (CPLX) {
+      acc.LA = ldT<CPLX, T>(p2);
+      acc.LB = ldT<CPLX, T>(p2 + 2);
+    } else {
+      acc.LB = ldT<CPLX, T>(p2);
+    }
+  }
+}
+
+// Shared prologue: clock steps, ownership test, increments, per-sample cotangent, first staged block.
+#define EWS_BWD_PROLOGUE(OWNS, ROWS)                                                                              \
+  const int c = blockIdx.x, b = blockIdx.y, tid = threadIdx.x;                                             \
+  const int t0 = c * a.T;                                                                                  \
+  const int Tc = min(a.T, a.n_int - t0);                                                                   \
+  const bool prefix = a.readout == EWS_READOUT_PREFIX;                                                     \
+  load_clock(a, b, t0, Tc, s_h);                                                                           \
+  __syncthreads();                                                                                         \
+  const ChunkClock cc = chunk_clock<T>(a, b, Tc, s_h);                                                     \
+  if (!(OWNS)) return;                                                                                     \
+  load_chunk(a, b, t0, Tc, s_v, s_h);                                                                      \
+  if (!prefix) stage_vec(a, b, s_gv, s_am);                                                                \
+  const int nblk = (Tc + (ROWS) - 1) / (ROWS);                                                             \
+  if (prefix)                                                                                              \
+    lds_dma(s_gb, a.gout + ((size_t)b * a.n_int + t0 + (nblk - 1) * (ROWS)) * a.W, (Tc - (nblk - 1) * (ROWS)) * a.W); \
+  lds_dma_wait();                                                                                          \
+  __syncthreads();                                                                                         \
+  const LaneMap m = lane_map_b<WAVE>(a, tid);                                                              \
+  T dummy{};                                                                                               \
+  const T uj = load_u(a.params, m.j, &dummy);                                                              \
+  const T uk = load_u(a.params, m.k, &dummy);                                                              \
+  const T ua = uj + conjc(uk), ub = uj + uk;
+
+// (a) Uniform-clock chunks whose decay allows it: the states S(t-1) come from inverting the steps backwards from
+// the chunk's end state (c_j = S1(t) - s1_j(t) is exact; then divide by the flows), so nothing is recomputed
+// forward and no history is kept.
+template <bool CPLX, int N, int MAXT, bool WAVE>
+__global__ __launch_bounds__(MAXT) void k_chunk_bwd_inv(DiagArgs a) {
+  using T = typename Types<CPLX>::T;
+  extern __shared__ float smem[];
+  const BwdLds Lo = bwd_lds_layout(a.T, a.d, a.W, blockDim.x, 0, WAVE, true, kGB);
+  float* s_v = smem + Lo.v;
+  float* s_h = smem + Lo.h;
+  float* s_gb = smem + Lo.gb;
+  float* s_gv = smem + Lo.gv;
+  int* s_am = reinterpret_cast<int*>(smem + Lo.am);
+  const RedLds red{smem + Lo.red, smem + Lo.red + 2 * blockDim.x, smem + Lo.red + 4 * blockDim.x,
+                   smem + Lo.red + 6 * blockDim.x};
+  float* s_dh = smem + Lo.dh;
+  float* s_g = smem + Lo.g;
+  EWS_BWD_PROLOGUE(cc.fast && cc.inv_ok, kGB)
+  Coef<T> c0;
+  CoefD<T> q0;
+  eval_coef<T, CPLX, N, true>(cc.hbar, cc.href, cc.per_int, uj, uk, c0, q0);
+  // d/dh of the inverse flows 1/rho = e^{-x}, 1/lambda = e^{-y} at hbar
+  const T irho0 = expv(-(cc.per_int ? cc.hbar : cc.href) * uj);
+  const T irho1 = cc.per_int ? -(irho0 * uj) : zero<T>();
+  T ilB0 = zero<T>(), ilB1 = zero<T>(), ilA0 = zero<T>(), ilA1 = zero<T>();
+  if constexpr (N == 2) {
+    const float hf = cc.per_int ? cc.hbar : cc.href;
+    ilB0 = expv(-hf * ub);
+    ilB1 = cc.per_int ? -(ilB0 * ub) : zero<T>();
+    if constexpr (CPLX) {
+      ilA0 = expv(-hf * ua);
+      ilA1 = cc.per_int ? -(ilA0 * ua) : zero<T>();
+    }
+  }
+  T S1, SA, SB;
+  load_state_d<CPLX, N>(a, m, a.carries + ((size_t)b * (a.C + 1) + c + 1) * a.D, S1, SA, SB);
+  BwdAcc<T> acc;
+  load_cot<CPLX, N>(a, m, a.mt + ((size_t)b * a.C + c) * a.D, acc);
+  for (int blk = nblk - 1; blk >= 0; --blk) {
+    const int buf = (nblk - 1 - blk) & 1;
+    const bool more = prefix && blk > 0;
+    if (more) lds_dma(s_gb + (buf ^ 1) * kGB * a.W, a.gout + ((size_t)b * a.n_int + t0 + (blk - 1) * kGB) * a.W,
+                      kGB * a.W);
+    const GammaSrc gs{prefix ? s_gb + buf * kGB * a.W : s_gv, s_am, 1.0f / (float)a.n_int, a.readout};
+#pragma unroll 1
+    for (int s = kGB - 1; s >= 0; --s) {
+      const int t = blk * kGB + s;
+      if (t < Tc) {
+        const float dlt = s_h[t] - cc.hbar;
+        Coef<T> co;
+        lin_coef<T, CPLX, N>(c0, q0, dlt, cc.per_int, co);
+        const T pj = lds_p<T>(s_v, t, a.d, m.j);
+        const T pk = (N == 2) ? lds_p<T>(s_v, t, a.d, m.k) : zero<T>();
+        // invert step t: S(t) -> S(t-1)
+        const T cj = S1 - co.phi_j * pj;
+        const T H1 = (irho0 + irho1 * dlt) * cj;
+        T HA = zero<T>(), HB = zero<T>();
+        if constexpr (N == 2) {
+          const T s1k = co.phi_k * pk;
+          HB = (ilB0 + ilB1 * dlt) * (SB - cj * s1k - co.IB * (pj * pk));
+          if constexpr (CPLX) HA = (ilA0 + ilA1 * dlt) * (SA - cj * conjc(s1k) - co.IA * (pj * conjc(pk)));
+        }
+        bwd_step<CPLX, N, WAVE>(a, m, gs, s, t, t0 + t, s_h[t], s_v, cc.per_int, co, q0, acc, H1, HA, HB, red,
+                                s_dh);
+        S1 = H1;
+        SA = HA;
+        SB = HB;
+      }
+    }
+    if (more) lds_dma_wait();
+    __syncthreads();
+  }
+  bwd_epilogue<CPLX, N, WAVE>(a, m, cc, acc, uj, ua, ub, Tc, t0, s_dh, s_g);
+}
+
+// (b) Every other chunk: exact per-step coefficients and forward states recomputed from the chunk's float64 carry
+// (checkpoints every kBLK steps; each block recomputed into a lane-private LDS history before its reverse sweep).
+template <bool CPLX, int N, int MAXT, bool WAVE>
+__global__ __launch_bounds__(MAXT) void k_chunk_bwd_full(DiagArgs a) {
+  using T = typename Types<CPLX>::T;
+  constexpr int NS = CPLX ? 6 : 2;  // checkpoint floats per lane
+  extern __shared__ float smem[];
+  const int NT = blockDim.x;
+  const BwdLds Lo = bwd_lds_layout(a.T, a.d, a.W, NT, NS, WAVE, true);
+  float* s_v = smem + Lo.v;
+  float* s_h = smem + Lo.h;
+  float* s_gb = smem + Lo.gb;
+  float* s_gv = smem + Lo.gv;
+  int* s_am = reinterpret_cast<int*>(smem + Lo.am);
+  float* s_ck = smem + Lo.ck;
+  float* s_hist = smem + Lo.hist;
+  const RedLds red{smem + Lo.red, smem + Lo.red + 2 * NT, smem + Lo.red + 4 * NT, smem + Lo.red + 6 * NT};
+  float* s_dh = smem + Lo.dh;
+  float* s_g = smem + Lo.g;
+  EWS_BWD_PROLOGUE(!(cc.fast && cc.inv_ok), kBLK)
+  auto coef_at = [&](int t, Coef<T>& co, CoefD<T>& qq) {
+    eval_coef<T, CPLX, N, true>(s_h[t], cc.href, cc.per_int, uj, uk, co, qq);
+  };
+  auto st_store = [&](float* p, T x1, T xa, T xb) {
+    if constexpr (CPLX) {
+      p[0 * NT + tid] = x1.re;
+      p[1 * NT + tid] = x1.im;
+      p[2 * NT + tid] = xa.re;
+      p[3 * NT + tid] = xa.im;
+      p[4 * NT + tid] = xb.re;
+      p[5 * NT + tid] = xb.im;
+    } else {
+      p[0 * NT + tid] = x1;
+      p[1 * NT + tid] = xb;
+    }
+  };
+  auto st_load = [&](const float* p, T& x1, T& xa, T& xb) {
+    if constexpr (CPLX) {
+      x1 = cf{p[0 * NT + tid], p[1 * NT + tid]};
+      xa = cf{p[2 * NT + tid], p[3 * NT + tid]};
+      xb = cf{p[4 * NT + tid], p[5 * NT + tid]};
+    } else {
+      x1 = p[0 * NT + tid];
+      xa = 0.0f;
+      xb = p[1 * NT + tid];
+    }
+  };
+  // forward pre-pass from the carry: checkpoints of the state before every kBLK-th step
+  T S1, SA, SB;
+  load_state_d<CPLX, N>(a, m, a.carries + ((size_t)b * (a.C + 1) + c) * a.D, S1, SA, SB);
+  for (int t = 0; t < Tc; ++t) {
+    if ((t % kBLK) == 0) st_store(s_ck + (size_t)(t / kBLK) * NS * NT, S1, SA, SB);
+    Coef<T> co;
+    CoefD<T> qq;
+    coef_at(t, co, qq);
+    const T pj = lds_p<T>(s_v, t, a.d, m.j);
+    const T pk = (N == 2) ? lds_p<T>(s_v, t, a.d, m.k) : zero<T>();
+    fwd_step<T, CPLX, N>(co, pj, pk, S1, SA, SB);
+  }
+  BwdAcc<T> acc;
+  load_cot<CPLX, N>(a, m, a.mt + ((size_t)b * a.C + c) * a.D, acc);
+  __syncthreads();
+  for (int blk = nblk - 1; blk >= 0; --blk) {
+    const int buf = (nblk - 1 - blk) & 1;
+    const bool more = prefix && blk > 0;
+    if (more) lds_dma(s_gb + (buf ^ 1) * kBLK * a.W, a.gout + ((size_t)b * a.n_int + t0 + (blk - 1) * kBLK) * a.W,
+                      kBLK * a.W);
+    const GammaSrc gs{prefix ? s_gb + buf * kBLK * a.W : s_gv, s_am, 1.0f / (float)a.n_int, a.readout};
+    st_load(s_ck + (size_t)blk * NS * NT, S1, SA, SB);
+#pragma unroll 1
+    for (int s = 0; s < kBLK; ++s) {
+      const int t = blk * kBLK + s;
+      if (t >= Tc) break;
+      st_store(s_hist + (size_t)s * NS * NT, S1, SA, SB);
+      Coef<T> co;
+      CoefD<T> qq;
+      coef_at(t, co, qq);
+      const T pj = lds_p<T>(s_v, t, a.d, m.j);
+      const T pk = (N == 2) ? lds_p<T>(s_v, t, a.d, m.k) : zero<T>();
+      fwd_step<T, CPLX, N>(co, pj, pk, S1, SA, SB);
+    }
+#pragma unroll 1
+    for (int s = kBLK - 1; s >= 0; --s) {
+      const int t = blk * kBLK + s;
+      if (t < Tc) {
+        T H1, HA, HB;
+        st_load(s_hist + (size_t)s * NS * NT, H1, HA, HB);
+        Coef<T> co;
+        CoefD<T> qq;
+        coef_at(t, co, qq);
+        bwd_step<CPLX, N, WAVE>(a, m, gs, s, t, t0 + t, s_h[t], s_v, cc.per_int, co, qq, acc, H1, HA, HB, red, s_dh);
+      }
+    }
+    if (more) lds_dma_wait();
+    __syncthreads();
+  }
+  bwd_epilogue<CPLX, N, WAVE>(a, m, cc, acc, uj, ua, ub, Tc, t0, s_dh, s_g);
 }
 
 // ------------------------------------------------------------------------------------------- B4
@@ -1455,7 +1525,7 @@ struct Plan {
   int B, L, n_int, d, K, N, T, C, D, W, npar;
   bool cplx, wave;
   int NT, NTb, scan_cb;
-  size_t lds_bwd_local, lds_bwd_full, lds_carry, lds_adjoint;
+  size_t lds_bwd_local, lds_bwd_full, lds_bwd_inv, lds_carry, lds_adjoint;
 };
 
 constexpr size_t kMaxLds = 160 * 1024;  // LDS per workgroup on gfx950
@@ -1492,7 +1562,6 @@ int make_plan(const ews_diag_desc* s, Plan& p) {
   p.NT = ((P + 63) / 64) * 64;
   p.wave = p.K <= 8;  // one wavefront with lane = 8 j + k in the backward chunk kernels
   p.NTb = p.wave ? 64 : p.NT;
-  if (kBLK * p.W > kPF * p.NTb) return EWS_ERR_SHAPE;  // cotangent block staging capacity
   int T = s->chunk;
   if (T == 0) {
     T = 64;
@@ -1501,8 +1570,9 @@ int make_plan(const ews_diag_desc* s, Plan& p) {
   if (T > 256) T = 256;
   p.T = T;
   p.C = (p.n_int + T - 1) / T;
-  p.lds_bwd_local = bwd_lds_bytes(p, T, false);
+  p.lds_bwd_local = (size_t)bwd_lds_layout(T, p.d, p.W, p.NTb, 0, p.wave, false, kGB).total * 4;
   p.lds_bwd_full = bwd_lds_bytes(p, T, true);
+  p.lds_bwd_inv = (size_t)bwd_lds_layout(T, p.d, p.W, p.NTb, 0, p.wave, true, kGB).total * 4;
   if (p.lds_bwd_full > kMaxLds) return EWS_ERR_SHAPE;
   const int CW = p.cplx ? 2 : 1;
   int cb = (int)((kScanLds - (size_t)p.NT * CW * 8) / ((size_t)p.D * 4 + (size_t)p.K * CW * 16));
@@ -1567,16 +1637,22 @@ int forward_pass(const ews_diag_desc* s, const Plan& p, DiagArgs a, hipStream_t 
   dim3 grid(p.C, p.B), blk(p.NT);
   switch (pass) {
     case 0:
-      hipLaunchKernelGGL((k_chunk_fwd<CPLX, N, MODE_SUMMARY, MAXT>), grid, blk, fwd_lds(p), st, a);
+      hipLaunchKernelGGL((k_chunk_fwd<CPLX, N, MODE_SUMMARY, MAXT, true>), grid, blk, fwd_lds(p), st, a);
+      EWS_LAUNCH_CHECK();
+      hipLaunchKernelGGL((k_chunk_fwd<CPLX, N, MODE_SUMMARY, MAXT, false>), grid, blk, fwd_lds(p), st, a);
       break;
     case 1:
       hipLaunchKernelGGL((k_carry_scan<CPLX, N, MAXT>), dim3(p.B), blk, p.lds_carry, st, a);
       break;
     case 2:
       if (s->readout == EWS_READOUT_PREFIX) {
-        hipLaunchKernelGGL((k_chunk_fwd<CPLX, N, MODE_PREFIX, MAXT>), grid, blk, fwd_lds(p), st, a);
+        hipLaunchKernelGGL((k_chunk_fwd<CPLX, N, MODE_PREFIX, MAXT, true>), grid, blk, fwd_lds(p), st, a);
+        EWS_LAUNCH_CHECK();
+        hipLaunchKernelGGL((k_chunk_fwd<CPLX, N, MODE_PREFIX, MAXT, false>), grid, blk, fwd_lds(p), st, a);
       } else if (s->readout == EWS_READOUT_MEAN || s->readout == EWS_READOUT_MAX) {
-        hipLaunchKernelGGL((k_chunk_fwd<CPLX, N, MODE_REDUCE, MAXT>), grid, blk, fwd_lds(p), st, a);
+        hipLaunchKernelGGL((k_chunk_fwd<CPLX, N, MODE_REDUCE, MAXT, true>), grid, blk, fwd_lds(p), st, a);
+        EWS_LAUNCH_CHECK();
+        hipLaunchKernelGGL((k_chunk_fwd<CPLX, N, MODE_REDUCE, MAXT, false>), grid, blk, fwd_lds(p), st, a);
       } else {
         return EWS_OK;
       }
@@ -1611,15 +1687,21 @@ int backward_pass(const Plan& p, DiagArgs a, hipStream_t st, int pass) {
   dim3 grid(p.C, p.B), blkb(p.NTb);
   switch (pass) {
     case 0:
-      if (set_lds(&k_chunk_bwd_local<CPLX, N, MAXT, WAVE>, p.lds_bwd_local) != EWS_OK) return EWS_ERR_LAUNCH;
-      hipLaunchKernelGGL((k_chunk_bwd_local<CPLX, N, MAXT, WAVE>), grid, blkb, p.lds_bwd_local, st, a);
+      if (set_lds(&k_chunk_bwd_local<CPLX, N, MAXT, WAVE, true>, p.lds_bwd_local) != EWS_OK) return EWS_ERR_LAUNCH;
+      if (set_lds(&k_chunk_bwd_local<CPLX, N, MAXT, WAVE, false>, p.lds_bwd_local) != EWS_OK) return EWS_ERR_LAUNCH;
+      hipLaunchKernelGGL((k_chunk_bwd_local<CPLX, N, MAXT, WAVE, true>), grid, blkb, p.lds_bwd_local, st, a);
+      EWS_LAUNCH_CHECK();
+      hipLaunchKernelGGL((k_chunk_bwd_local<CPLX, N, MAXT, WAVE, false>), grid, blkb, p.lds_bwd_local, st, a);
       break;
     case 1:
       hipLaunchKernelGGL((k_adjoint_scan<CPLX, N, (MAXT < 256 ? 256 : MAXT)>), dim3(p.B), dim3(p.NT), p.lds_adjoint,
                          st, a);
       break;
     case 2:
+      if (set_lds(&k_chunk_bwd_inv<CPLX, N, MAXT, WAVE>, p.lds_bwd_inv) != EWS_OK) return EWS_ERR_LAUNCH;
       if (set_lds(&k_chunk_bwd_full<CPLX, N, MAXT, WAVE>, p.lds_bwd_full) != EWS_OK) return EWS_ERR_LAUNCH;
+      hipLaunchKernelGGL((k_chunk_bwd_inv<CPLX, N, MAXT, WAVE>), grid, blkb, p.lds_bwd_inv, st, a);
+      EWS_LAUNCH_CHECK();
       hipLaunchKernelGGL((k_chunk_bwd_full<CPLX, N, MAXT, WAVE>), grid, blkb, p.lds_bwd_full, st, a);
       break;
     case 3: {
