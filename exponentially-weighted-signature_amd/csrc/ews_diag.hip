@@ -87,6 +87,9 @@ struct DiagArgs {
   float* dh;        // (B, n_int)
   float* gp;        // (B, C, npar)
   float* gph;       // (B, C)
+  double* gagg;     // (B, NG, D) group aggregates (forward) / group cotangent aggregates (backward)
+  double* gcar;     // (B, NG, D) state before each group (forward) / cotangent after each group (backward)
+  int NG;           // chunk groups of scan_cb chunks
   // backward outputs
   float* dpath;
   float* dclock;
@@ -535,68 +538,71 @@ __device__ __forceinline__ void write_row_d(const DiagArgs& a, const LaneMap& m,
   }
 }
 
-// Sequential float64 Chen combine of the chunk summaries per sample: carries[c] = state before chunk c.
-// Blocks of scan_cb chunks are staged in LDS (summaries, and the chunk flows computed in parallel), so the
-// sequential loop reads no global memory.
-template <bool CPLX, int N, int MAXT>
-__global__ __launch_bounds__(MAXT) void k_carry_scan(DiagArgs a) {
-  using TD = typename Types<CPLX>::TD;
-  extern __shared__ double dsm[];
-  constexpr int CW = CPLX ? 2 : 1;
-  const int K = a.K, CB = a.scan_cb, NT = blockDim.x;
-  double* s_F = dsm;                                         // CB * K
-  float* s_l = reinterpret_cast<float*>(s_F + (size_t)CB * K * CW);  // CB * D
-  const int b = blockIdx.x, tid = threadIdx.x;
-  const LaneMap m = lane_map(a, tid);
+// Float64 Chen combine of chunk summaries, in three levels so no sequential chain is longer than a group:
+//   group_agg    every group of scan_cb chunks combines its summaries from a zero state (parallel)
+//   group_scan   per sample, the group aggregates are combined in order -> the state before each group
+//   group_expand every group re-combines its chunks from its incoming state, writing carries[c]
+// Chunk and group flows are exp(u * clock span) in float64 (per-interval flows multiply to that exactly).
+__device__ __forceinline__ double span_tau(const DiagArgs& a, int b, int t_start, int t_end) {
+  const float* th = a.clock + (size_t)b * a.L;
+  if (a.flow_mode == EWS_FLOW_PER_INTERVAL) return (double)th[t_end] - (double)th[t_start];
+  if (a.flow_mode == EWS_FLOW_CACHED) return ((double)th[1] - (double)th[0]) * (t_end - t_start);
+  const double h1 = a.L > 2 ? (double)th[2] - (double)th[1] : 0.0;
+  return h1 * (t_end - t_start - (t_start == 0 ? 1 : 0));
+}
+
+// S <- (flow F applied to S) (x) l, the Chen product of a state with a summary (pair lane view)
+template <bool CPLX, int N, class TD>
+__device__ __forceinline__ void chen_fwd_lane(TD& S1, TD& SA, TD& SB, TD Fj, TD Fk, TD l1j, TD l1k, TD l2A, TD l2B) {
+  const TD cj = Fj * S1;
+  if (N == 2) {
+    if (CPLX) SA = (Fj * conj(Fk)) * SA + cj * conj(l1k) + l2A;
+    SB = (Fj * Fk) * SB + cj * l1k + l2B;
+  }
+  S1 = cj + l1j;
+}
+
+template <bool CPLX, class TD>
+__device__ __forceinline__ void lane_summary(const DiagArgs& a, const LaneMap& m, const float* sp, TD& l1j, TD& l1k,
+                                             TD& l2A, TD& l2B) {
   TD dummy{};
-  TD S1{}, SA{}, SB{};
-  for (int c0 = 0; c0 < a.C; c0 += CB) {
-    const int nb = min(CB, a.C - c0);
-    __syncthreads();
-    copy_to_lds(s_l, a.summ + ((size_t)b * a.C + c0) * a.D, nb * a.D);
-    for (int i = tid; i < nb * K; i += NT) {
-      const int cc = i / K, j = i % K, c = c0 + cc;
-      const int Tc = min(a.T, a.n_int - c * a.T);
-      stD(s_F + (size_t)i * CW, dexp(mul_s(load_ud(a.params, j, &dummy), chunk_tau(a, b, c, Tc))));
-    }
-    __syncthreads();
-    if (!m.active) continue;
-    for (int cc = 0; cc < nb; ++cc) {
-      const int c = c0 + cc;
-      double* cr = a.carries + ((size_t)b * (a.C + 1) + c) * a.D;
-      if (m.plane) stD(cr + st1<CPLX>(m.j), S1);
-      if (N == 2) {
-        double* p2 = cr + st2<CPLX>(a, m.j, m.k);
-        if (CPLX) {
-          stD(p2, SA);
-          stD(p2 + 2, SB);
-        } else {
-          stD(p2, SB);
-        }
-      }
-      const float* sp = s_l + (size_t)cc * a.D;
-      const TD Fj = ldDD(s_F + (size_t)(cc * K + m.j) * CW, &dummy);
-      const TD l1j = ldD(sp + st1<CPLX>(m.j), &dummy);
-      const TD cj = Fj * S1;
-      if (N == 2) {
-        const TD Fk = ldDD(s_F + (size_t)(cc * K + m.k) * CW, &dummy);
-        const TD l1k = ldD(sp + st1<CPLX>(m.k), &dummy);
-        const float* p2 = sp + st2<CPLX>(a, m.j, m.k);
-        if (CPLX) {
-          SA = (Fj * conj(Fk)) * SA + cj * conj(l1k) + ldD(p2, &dummy);
-          SB = (Fj * Fk) * SB + cj * l1k + ldD(p2 + 2, &dummy);
-        } else {
-          SB = (Fj * Fk) * SB + cj * l1k + ldD(p2, &dummy);
-        }
-      }
-      S1 = cj + l1j;
+  l1j = ldD(sp + st1<CPLX>(m.j), &dummy);
+  l1k = ldD(sp + st1<CPLX>(m.k), &dummy);
+  l2A = TD{};
+  l2B = TD{};
+  if (a.N == 2) {
+    const float* p2 = sp + st2<CPLX>(a, m.j, m.k);
+    if (CPLX) {
+      l2A = ldD(p2, &dummy);
+      l2B = ldD(p2 + 2, &dummy);
+    } else {
+      l2B = ldD(p2, &dummy);
     }
   }
-  if (!m.active) return;
-  double* cr = a.carries + ((size_t)b * (a.C + 1) + a.C) * a.D;
-  if (m.plane) stD(cr + st1<CPLX>(m.j), S1);
+}
+template <bool CPLX, class TD>
+__device__ __forceinline__ void lane_summary_d(const DiagArgs& a, const LaneMap& m, const double* sp, TD& l1j, TD& l1k,
+                                               TD& l2A, TD& l2B) {
+  TD dummy{};
+  l1j = ldDD(sp + st1<CPLX>(m.j), &dummy);
+  l1k = ldDD(sp + st1<CPLX>(m.k), &dummy);
+  l2A = TD{};
+  l2B = TD{};
+  if (a.N == 2) {
+    const double* p2 = sp + st2<CPLX>(a, m.j, m.k);
+    if (CPLX) {
+      l2A = ldDD(p2, &dummy);
+      l2B = ldDD(p2 + 2, &dummy);
+    } else {
+      l2B = ldDD(p2, &dummy);
+    }
+  }
+}
+template <bool CPLX, int N, class TD>
+__device__ __forceinline__ void store_lane_d(const DiagArgs& a, const LaneMap& m, double* row, TD S1, TD SA, TD SB) {
+  if (m.plane) stD(row + st1<CPLX>(m.j), S1);
   if (N == 2) {
-    double* p2 = cr + st2<CPLX>(a, m.j, m.k);
+    double* p2 = row + st2<CPLX>(a, m.j, m.k);
     if (CPLX) {
       stD(p2, SA);
       stD(p2 + 2, SB);
@@ -604,7 +610,206 @@ __global__ __launch_bounds__(MAXT) void k_carry_scan(DiagArgs a) {
       stD(p2, SB);
     }
   }
-  if (a.readout == EWS_READOUT_TERMINAL) write_row_d<CPLX, N>(a, m, a.out + (size_t)b * a.W, S1, SA, SB, tid);
+}
+
+// Stages a group's chunk summaries and chunk flows into LDS; returns the group's chunk range.
+template <bool CPLX, class TD>
+__device__ __forceinline__ int stage_group(const DiagArgs& a, int b, int g, float* s_l, double* s_F, int& c0) {
+  constexpr int CW = CPLX ? 2 : 1;
+  c0 = g * a.scan_cb;
+  const int nb = min(a.scan_cb, a.C - c0);
+  copy_to_lds(s_l, a.summ + ((size_t)b * a.C + c0) * a.D, nb * a.D);
+  TD dummy{};
+  for (int i = threadIdx.x; i < nb * a.K; i += blockDim.x) {
+    const int cc = i / a.K, j = i % a.K, c = c0 + cc;
+    const int t0 = c * a.T, t1 = min(t0 + a.T, a.n_int);
+    stD(s_F + (size_t)i * CW, dexp(mul_s(load_ud(a.params, j, &dummy), span_tau(a, b, t0, t1))));
+  }
+  __syncthreads();
+  return nb;
+}
+
+template <bool CPLX, int N, int MAXT, bool EXPAND>
+__global__ __launch_bounds__(MAXT) void k_fwd_group(DiagArgs a) {
+  using TD = typename Types<CPLX>::TD;
+  constexpr int CW = CPLX ? 2 : 1;
+  extern __shared__ double dsm[];
+  double* s_F = dsm;
+  float* s_l = reinterpret_cast<float*>(s_F + (size_t)a.scan_cb * a.K * CW);
+  const int g = blockIdx.x, b = blockIdx.y;
+  const LaneMap m = lane_map(a, threadIdx.x);
+  int c0;
+  const int nb = stage_group<CPLX, TD>(a, b, g, s_l, s_F, c0);
+  if (!m.active) return;
+  TD dummy{};
+  TD S1{}, SA{}, SB{};
+  if (EXPAND) lane_summary_d<CPLX>(a, m, a.gcar + ((size_t)b * a.NG + g) * a.D, S1, dummy, SA, SB);
+  for (int cc = 0; cc < nb; ++cc) {
+    if (EXPAND) store_lane_d<CPLX, N>(a, m, a.carries + ((size_t)b * (a.C + 1) + c0 + cc) * a.D, S1, SA, SB);
+    TD l1j, l1k, l2A, l2B;
+    lane_summary<CPLX>(a, m, s_l + (size_t)cc * a.D, l1j, l1k, l2A, l2B);
+    const TD Fj = ldDD(s_F + (size_t)(cc * a.K + m.j) * CW, &dummy);
+    const TD Fk = ldDD(s_F + (size_t)(cc * a.K + m.k) * CW, &dummy);
+    chen_fwd_lane<CPLX, N>(S1, SA, SB, Fj, Fk, l1j, l1k, l2A, l2B);
+  }
+  if (EXPAND) {
+    if (c0 + nb == a.C) {
+      store_lane_d<CPLX, N>(a, m, a.carries + ((size_t)b * (a.C + 1) + a.C) * a.D, S1, SA, SB);
+      if (a.readout == EWS_READOUT_TERMINAL) write_row_d<CPLX, N>(a, m, a.out + (size_t)b * a.W, S1, SA, SB, threadIdx.x);
+    }
+  } else {
+    store_lane_d<CPLX, N>(a, m, a.gagg + ((size_t)b * a.NG + g) * a.D, S1, SA, SB);
+  }
+}
+
+template <bool CPLX, int N, int MAXT>
+__global__ __launch_bounds__(MAXT) void k_fwd_group_scan(DiagArgs a) {
+  using TD = typename Types<CPLX>::TD;
+  const int b = blockIdx.x;
+  const LaneMap m = lane_map(a, threadIdx.x);
+  if (!m.active) return;
+  TD dummy{};
+  const TD uj = load_ud(a.params, m.j, &dummy), uk = load_ud(a.params, m.k, &dummy);
+  TD S1{}, SA{}, SB{};
+  for (int g = 0; g < a.NG; ++g) {
+    store_lane_d<CPLX, N>(a, m, a.gcar + ((size_t)b * a.NG + g) * a.D, S1, SA, SB);
+    const int t0 = g * a.scan_cb * a.T, t1 = min(t0 + a.scan_cb * a.T, a.n_int);
+    const double tau = span_tau(a, b, t0, t1);
+    TD l1j, l1k, l2A, l2B;
+    lane_summary_d<CPLX>(a, m, a.gagg + ((size_t)b * a.NG + g) * a.D, l1j, l1k, l2A, l2B);
+    chen_fwd_lane<CPLX, N>(S1, SA, SB, dexp(mul_s(uj, tau)), dexp(mul_s(uk, tau)), l1j, l1k, l2A, l2B);
+  }
+}
+
+// ---- backward: X(c) = mu(c) + J_c^T X(c+1) in the same three levels; mt[c] = X(c+1) (cotangent on chunk c's end
+// state from later chunks). J_c^T: level 2 conj(flow) X2; level 1 conj(F_j) [X1_j + sum_k (conj(l1_k) XB_jk +
+// l1_k XA_jk)], with l1 the chunk's level-1 increment carry1(c+1) - F carry1(c).
+template <bool CPLX, int N, class TD>
+__device__ __forceinline__ void adj_lane(const DiagArgs& a, const LaneMap& m, TD& X1, TD& XA, TD& XB, TD Fj, TD Fk,
+                                         TD l1k, double* s_red) {
+  constexpr int CW = CPLX ? 2 : 1;
+  TD dummy{};
+  TD toC{};
+  if (N == 2 && m.active) {
+    toC = conj(l1k) * XB;
+    if (CPLX) toC = toC + l1k * XA;
+    XB = conj(Fj * Fk) * XB;
+    if (CPLX) XA = conj(Fj * conj(Fk)) * XA;
+  }
+  if (N == 2) {
+    if (m.active) stD(s_red + (size_t)threadIdx.x * CW, toC);
+    __syncthreads();
+    if (m.plane) {
+      TD s = X1;
+      for (int k = 0; k < a.K; ++k) s = s + ldDD(s_red + (size_t)(m.j * a.K + k) * CW, &dummy);
+      X1 = conj(Fj) * s;
+    }
+    __syncthreads();
+  } else if (m.plane) {
+    X1 = conj(Fj) * X1;
+  }
+}
+template <bool CPLX, int N, class TD>
+__device__ __forceinline__ void add_mu(const DiagArgs& a, const LaneMap& m, const float* mup, TD& X1, TD& XA, TD& XB) {
+  TD dummy{};
+  if (m.plane) X1 = X1 + ldD(mup + st1<CPLX>(m.j), &dummy);
+  if (N == 2 && m.active) {
+    const float* p2 = mup + st2<CPLX>(a, m.j, m.k);
+    if (CPLX) {
+      XA = XA + ldD(p2, &dummy);
+      XB = XB + ldD(p2 + 2, &dummy);
+    } else {
+      XB = XB + ldD(p2, &dummy);
+    }
+  }
+}
+template <bool CPLX, int N, class TD>
+__device__ __forceinline__ void store_lane_f(const DiagArgs& a, const LaneMap& m, float* mp, TD X1, TD XA, TD XB) {
+  if (m.plane) {
+    mp[st1<CPLX>(m.j)] = (float)dre(X1);
+    if (CPLX) mp[st1<CPLX>(m.j) + 1] = (float)dim_(X1);
+  }
+  if (N == 2 && m.active) {
+    float* p2 = mp + st2<CPLX>(a, m.j, m.k);
+    p2[0] = (float)dre(CPLX ? XA : XB);
+    if (CPLX) {
+      p2[1] = (float)dim_(XA);
+      p2[2] = (float)dre(XB);
+      p2[3] = (float)dim_(XB);
+    }
+  }
+}
+
+template <bool CPLX, int N, int MAXT, bool EXPAND>
+__global__ __launch_bounds__(MAXT) void k_bwd_group(DiagArgs a) {
+  using TD = typename Types<CPLX>::TD;
+  constexpr int CW = CPLX ? 2 : 1;
+  extern __shared__ double dsm[];
+  const int G = a.scan_cb;
+  double* s_F = dsm;                                   // G * K
+  double* s_l1 = s_F + (size_t)G * a.K * CW;           // G * K
+  double* s_red = s_l1 + (size_t)G * a.K * CW;         // NT
+  float* s_mu = reinterpret_cast<float*>(s_red + (size_t)blockDim.x * CW);  // G * D
+  const int g = blockIdx.x, b = blockIdx.y;
+  const LaneMap m = lane_map(a, threadIdx.x);
+  const int c0 = g * G, nb = min(G, a.C - c0);
+  copy_to_lds(s_mu, a.mu + ((size_t)b * a.C + c0) * a.D, nb * a.D);
+  TD dummy{};
+  for (int i = threadIdx.x; i < nb * a.K; i += blockDim.x) {
+    const int cc = i / a.K, j = i % a.K, c = c0 + cc;
+    const int t0 = c * a.T, t1 = min(t0 + a.T, a.n_int);
+    const TD F = dexp(mul_s(load_ud(a.params, j, &dummy), span_tau(a, b, t0, t1)));
+    stD(s_F + (size_t)i * CW, F);
+    const double* cr0 = a.carries + ((size_t)b * (a.C + 1) + c) * a.D;
+    stD(s_l1 + (size_t)i * CW, ldDD(cr0 + a.D + st1<CPLX>(j), &dummy) - F * ldDD(cr0 + st1<CPLX>(j), &dummy));
+  }
+  __syncthreads();
+  TD X1{}, XA{}, XB{};
+  if (EXPAND) lane_summary_d<CPLX>(a, m, a.gcar + ((size_t)b * a.NG + g) * a.D, X1, dummy, XA, XB);
+  for (int cc = nb - 1; cc >= 0; --cc) {
+    const int c = c0 + cc;
+    if (EXPAND) store_lane_f<CPLX, N>(a, m, a.mt + ((size_t)b * a.C + c) * a.D, X1, XA, XB);
+    const TD Fj = ldDD(s_F + (size_t)(cc * a.K + m.j) * CW, &dummy);
+    const TD Fk = ldDD(s_F + (size_t)(cc * a.K + m.k) * CW, &dummy);
+    const TD l1k = ldDD(s_l1 + (size_t)(cc * a.K + m.k) * CW, &dummy);
+    adj_lane<CPLX, N>(a, m, X1, XA, XB, Fj, Fk, l1k, s_red);
+    add_mu<CPLX, N>(a, m, s_mu + (size_t)cc * a.D, X1, XA, XB);
+  }
+  if (!EXPAND && m.active) store_lane_d<CPLX, N>(a, m, a.gagg + ((size_t)b * a.NG + g) * a.D, X1, XA, XB);
+}
+
+template <bool CPLX, int N, int MAXT>
+__global__ __launch_bounds__(MAXT) void k_bwd_group_scan(DiagArgs a) {
+  using TD = typename Types<CPLX>::TD;
+  constexpr int CW = CPLX ? 2 : 1;
+  __shared__ double s_red[MAXT * CW];
+  const int b = blockIdx.x;
+  const LaneMap m = lane_map(a, threadIdx.x);
+  TD dummy{};
+  const TD uj = load_ud(a.params, m.j, &dummy), uk = load_ud(a.params, m.k, &dummy);
+  TD X1{}, XA{}, XB{};
+  for (int g = a.NG - 1; g >= 0; --g) {
+    if (m.active) store_lane_d<CPLX, N>(a, m, a.gcar + ((size_t)b * a.NG + g) * a.D, X1, XA, XB);
+    const int c0 = g * a.scan_cb, c1 = min(c0 + a.scan_cb, a.C);
+    const int t0 = c0 * a.T, t1 = min(c1 * a.T, a.n_int);
+    const double tau = span_tau(a, b, t0, t1);
+    const TD Fj = dexp(mul_s(uj, tau)), Fk = dexp(mul_s(uk, tau));
+    const double* cs = a.carries + ((size_t)b * (a.C + 1) + c0) * a.D;
+    const double* ce = a.carries + ((size_t)b * (a.C + 1) + c1) * a.D;
+    const TD l1k = ldDD(ce + st1<CPLX>(m.k), &dummy) - Fk * ldDD(cs + st1<CPLX>(m.k), &dummy);
+    adj_lane<CPLX, N>(a, m, X1, XA, XB, Fj, Fk, l1k, s_red);
+    const double* ag = a.gagg + ((size_t)b * a.NG + g) * a.D;
+    if (m.plane) X1 = X1 + ldDD(ag + st1<CPLX>(m.j), &dummy);
+    if (N == 2 && m.active) {
+      const double* p2 = ag + st2<CPLX>(a, m.j, m.k);
+      if (CPLX) {
+        XA = XA + ldDD(p2, &dummy);
+        XB = XB + ldDD(p2 + 2, &dummy);
+      } else {
+        XB = XB + ldDD(p2, &dummy);
+      }
+    }
+  }
 }
 
 // ------------------------------------------------------------------------------------------- F4
@@ -920,100 +1125,6 @@ __global__ __launch_bounds__(MAXT) void k_chunk_bwd_local(DiagArgs a) {
     }
   } else if (m.active) {
     stT(mp + st1<CPLX>(m.j), L1);
-  }
-}
-
-// ------------------------------------------------------------------------------------------- B2
-// Reverse float64 scan of chunk cotangents: X(c) = mu(c) + J_c^T X(c+1), J_c the Jacobian of chunk c's map on
-// its carry; writes mt[c-1] = X(c) (the cotangent on chunk c-1's end state from chunks >= c), mt[C-1] = 0.
-// Blocks of chunks are staged in LDS (mu rows, chunk flows, chunk level-1 increments) before the sequential
-// part, so the loop touches no global memory except its stores.
-template <bool CPLX, int N, int MAXT>
-__global__ __launch_bounds__(MAXT) void k_adjoint_scan(DiagArgs a) {
-  using TD = typename Types<CPLX>::TD;
-  extern __shared__ double dsm[];
-  const int K = a.K, CB = a.scan_cb, NT = blockDim.x;
-  constexpr int CW = CPLX ? 2 : 1;
-  double* s_F = dsm;                               // CB * K
-  double* s_l1 = s_F + (size_t)CB * K * CW;        // CB * K
-  double* s_red = s_l1 + (size_t)CB * K * CW;      // NT
-  float* s_mu = reinterpret_cast<float*>(s_red + (size_t)NT * CW);  // CB * D
-  const int b = blockIdx.x, tid = threadIdx.x;
-  const LaneMap m = lane_map(a, tid);
-  TD dummy{};
-  const TD uj = load_ud(a.params, m.j, &dummy);
-  const TD uk = load_ud(a.params, m.k, &dummy);
-  TD X1{}, XA{}, XB{};
-  {
-    float* mp = a.mt + ((size_t)b * a.C + (a.C - 1)) * a.D;
-    for (int i = tid; i < a.D; i += NT) mp[i] = 0.0f;
-  }
-  for (int c1 = a.C - 1; c1 >= 1; c1 -= CB) {
-    const int cL = max(1, c1 - CB + 1);
-    const int nb = c1 - cL + 1;
-    __syncthreads();
-    copy_to_lds(s_mu, a.mu + ((size_t)b * a.C + cL) * a.D, nb * a.D);
-    for (int i = tid; i < nb * K; i += NT) {
-      const int cc = i / K, j = i % K, c = cL + cc;
-      const int Tc = min(a.T, a.n_int - c * a.T);
-      const TD u = load_ud(a.params, j, &dummy);
-      const TD F = dexp(mul_s(u, chunk_tau(a, b, c, Tc)));
-      stD(s_F + (size_t)i * CW, F);
-      const double* cr0 = a.carries + ((size_t)b * (a.C + 1) + c) * a.D;
-      const TD l1 = ldDD(cr0 + a.D + st1<CPLX>(j), &dummy) - F * ldDD(cr0 + st1<CPLX>(j), &dummy);
-      stD(s_l1 + (size_t)i * CW, l1);
-    }
-    __syncthreads();
-    for (int c = c1; c >= cL; --c) {
-      const int cc = c - cL;
-      const TD Fj = ldDD(s_F + (size_t)(cc * K + m.j) * CW, &dummy);
-      TD toC{};
-      if (N == 2 && m.active) {
-        const TD Fk = ldDD(s_F + (size_t)(cc * K + m.k) * CW, &dummy);
-        const TD l1k = ldDD(s_l1 + (size_t)(cc * K + m.k) * CW, &dummy);
-        toC = conj(l1k) * XB;
-        if (CPLX) toC = toC + l1k * XA;
-        XB = conj(Fj * Fk) * XB;
-        if (CPLX) XA = conj(Fj * conj(Fk)) * XA;
-      }
-      if (N == 2) {
-        if (m.active) stD(s_red + (size_t)tid * CW, toC);
-        __syncthreads();
-        if (m.plane) {
-          TD s = X1;
-          for (int k = 0; k < K; ++k) s = s + ldDD(s_red + (size_t)(m.j * K + k) * CW, &dummy);
-          X1 = conj(Fj) * s;
-        }
-        __syncthreads();
-      } else if (m.plane) {
-        X1 = conj(Fj) * X1;
-      }
-      const float* mup = s_mu + (size_t)cc * a.D;
-      if (m.plane) X1 = X1 + ldD(mup + st1<CPLX>(m.j), &dummy);
-      if (N == 2 && m.active) {
-        const float* p2 = mup + st2<CPLX>(a, m.j, m.k);
-        if (CPLX) {
-          XA = XA + ldD(p2, &dummy);
-          XB = XB + ldD(p2 + 2, &dummy);
-        } else {
-          XB = XB + ldD(p2, &dummy);
-        }
-      }
-      float* mp = a.mt + ((size_t)b * a.C + (c - 1)) * a.D;
-      if (m.plane) {
-        mp[st1<CPLX>(m.j)] = (float)dre(X1);
-        if (CPLX) mp[st1<CPLX>(m.j) + 1] = (float)dim_(X1);
-      }
-      if (N == 2 && m.active) {
-        float* p2 = mp + st2<CPLX>(a, m.j, m.k);
-        p2[0] = (float)dre(CPLX ? XA : XB);
-        if (CPLX) {
-          p2[1] = (float)dim_(XA);
-          p2[2] = (float)dre(XB);
-          p2[3] = (float)dim_(XB);
-        }
-      }
-    }
   }
 }
 
@@ -1469,30 +1580,37 @@ __global__ __launch_bounds__(MAXT) void k_chunk_bwd_full(DiagArgs a) {
 }
 
 // ------------------------------------------------------------------------------------------- B4
+// Knot gradients from interval gradients: dX_t = dv_{t-1} - dv_t, dtheta_t = dh_{t-1} - dh_t (+ the shared flow
+// step's gradient for cached flows). One thread per (sample, knot, channel) element: coalesced.
 __global__ void k_knot_grads(DiagArgs a) {
-  const size_t total = (size_t)a.B * a.L;
+  const int dp1 = a.d + 1;
+  const size_t total = (size_t)a.B * a.L * dp1;
   for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += (size_t)gridDim.x * blockDim.x) {
-    const int b = (int)(i / a.L), t = (int)(i % a.L);
-    const float* dvb = a.dv + (size_t)b * a.n_int * a.d;
-    for (int ch = 0; ch < a.d; ++ch) {
+    const int ch = (int)(i % dp1);
+    const size_t bt = i / dp1;
+    const int b = (int)(bt / a.L), t = (int)(bt % a.L);
+    if (ch < a.d) {
+      const float* dvb = a.dv + (size_t)b * a.n_int * a.d;
       float g = 0.0f;
       if (t >= 1) g += dvb[(size_t)(t - 1) * a.d + ch];
       if (t < a.n_int) g -= dvb[(size_t)t * a.d + ch];
-      a.dpath[i * a.d + ch] = g;
+      a.dpath[bt * a.d + ch] = g;
+    } else {
+      const float* dhb = a.dh + (size_t)b * a.n_int;
+      float g = 0.0f;
+      if (t >= 1) g += dhb[t - 1];
+      if (t < a.n_int) g -= dhb[t];
+      if (a.flow_mode != EWS_FLOW_PER_INTERVAL) {
+        // shared flow step href = theta[r+1] - theta[r]
+        const int r = (a.flow_mode == EWS_FLOW_CACHED) ? 0 : 1;
+        if (t == r || t == r + 1) {
+          double hs = 0.0;
+          for (int c = 0; c < a.C; ++c) hs += (double)a.gph[(size_t)b * a.C + c];
+          g += (t == r + 1) ? (float)hs : -(float)hs;
+        }
+      }
+      a.dclock[bt] = g;
     }
-    const float* dhb = a.dh + (size_t)b * a.n_int;
-    float g = 0.0f;
-    if (t >= 1) g += dhb[t - 1];
-    if (t < a.n_int) g -= dhb[t];
-    if (a.flow_mode != EWS_FLOW_PER_INTERVAL) {
-      // shared flow step href = theta[r+1] - theta[r]
-      const int r = (a.flow_mode == EWS_FLOW_CACHED) ? 0 : 1;
-      double hs = 0.0;
-      for (int c = 0; c < a.C; ++c) hs += (double)a.gph[(size_t)b * a.C + c];
-      if (t == r + 1) g += (float)hs;
-      if (t == r) g -= (float)hs;
-    }
-    a.dclock[i] = g;
   }
 }
 
@@ -1524,7 +1642,7 @@ size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 struct Plan {
   int B, L, n_int, d, K, N, T, C, D, W, npar;
   bool cplx, wave;
-  int NT, NTb, scan_cb;
+  int NT, NTb, scan_cb, NG;
   size_t lds_bwd_local, lds_bwd_full, lds_bwd_inv, lds_carry, lds_adjoint;
 };
 
@@ -1577,13 +1695,14 @@ int make_plan(const ews_diag_desc* s, Plan& p) {
   const int CW = p.cplx ? 2 : 1;
   int cb = (int)((kScanLds - (size_t)p.NT * CW * 8) / ((size_t)p.D * 4 + (size_t)p.K * CW * 16));
   p.scan_cb = cb < 1 ? 1 : (cb > 16 ? 16 : cb);
+  p.NG = (p.C + p.scan_cb - 1) / p.scan_cb;
   p.lds_carry = (size_t)p.scan_cb * p.K * CW * 8 + (size_t)p.scan_cb * p.D * 4;
   p.lds_adjoint = (size_t)p.scan_cb * p.K * CW * 16 + (size_t)p.NT * CW * 8 + (size_t)p.scan_cb * p.D * 4;
   return EWS_OK;
 }
 
 struct WsLayout {
-  size_t summ, mu, mt, red, red_idx, dv, dh, gp, gph, total;
+  size_t summ, mu, mt, red, red_idx, dv, dh, gp, gph, gagg, gcar, total;
 };
 WsLayout ws_layout(const Plan& p) {
   WsLayout w;
@@ -1598,6 +1717,8 @@ WsLayout ws_layout(const Plan& p) {
   w.dh = off; off += align256((size_t)p.B * p.n_int * 4);
   w.gp = off; off += align256(BC * p.npar * 4);
   w.gph = off; off += align256(BC * 4);
+  w.gagg = off; off += align256((size_t)p.B * p.NG * p.D * 8);
+  w.gcar = off; off += align256((size_t)p.B * p.NG * p.D * 8);
   w.total = off;
   return w;
 }
@@ -1620,6 +1741,7 @@ DiagArgs make_args(const ews_diag_desc* s, const Plan& p, const void* path, cons
   a.red = (float*)(ws + w.red); a.red_idx = (int*)(ws + w.red_idx);
   a.dv = (float*)(ws + w.dv); a.dh = (float*)(ws + w.dh);
   a.gp = (float*)(ws + w.gp); a.gph = (float*)(ws + w.gph);
+  a.gagg = (double*)(ws + w.gagg); a.gcar = (double*)(ws + w.gcar); a.NG = p.NG;
   return a;
 }
 
@@ -1642,7 +1764,11 @@ int forward_pass(const ews_diag_desc* s, const Plan& p, DiagArgs a, hipStream_t 
       hipLaunchKernelGGL((k_chunk_fwd<CPLX, N, MODE_SUMMARY, MAXT, false>), grid, blk, fwd_lds(p), st, a);
       break;
     case 1:
-      hipLaunchKernelGGL((k_carry_scan<CPLX, N, MAXT>), dim3(p.B), blk, p.lds_carry, st, a);
+      hipLaunchKernelGGL((k_fwd_group<CPLX, N, MAXT, false>), dim3(p.NG, p.B), blk, p.lds_carry, st, a);
+      EWS_LAUNCH_CHECK();
+      hipLaunchKernelGGL((k_fwd_group_scan<CPLX, N, MAXT>), dim3(p.B), blk, 0, st, a);
+      EWS_LAUNCH_CHECK();
+      hipLaunchKernelGGL((k_fwd_group<CPLX, N, MAXT, true>), dim3(p.NG, p.B), blk, p.lds_carry, st, a);
       break;
     case 2:
       if (s->readout == EWS_READOUT_PREFIX) {
@@ -1694,8 +1820,13 @@ int backward_pass(const Plan& p, DiagArgs a, hipStream_t st, int pass) {
       hipLaunchKernelGGL((k_chunk_bwd_local<CPLX, N, MAXT, WAVE, false>), grid, blkb, p.lds_bwd_local, st, a);
       break;
     case 1:
-      hipLaunchKernelGGL((k_adjoint_scan<CPLX, N, (MAXT < 256 ? 256 : MAXT)>), dim3(p.B), dim3(p.NT), p.lds_adjoint,
-                         st, a);
+      hipLaunchKernelGGL((k_bwd_group<CPLX, N, (MAXT < 256 ? 256 : MAXT), false>), dim3(p.NG, p.B), dim3(p.NT),
+                         p.lds_adjoint, st, a);
+      EWS_LAUNCH_CHECK();
+      hipLaunchKernelGGL((k_bwd_group_scan<CPLX, N, (MAXT < 256 ? 256 : MAXT)>), dim3(p.B), dim3(p.NT), 0, st, a);
+      EWS_LAUNCH_CHECK();
+      hipLaunchKernelGGL((k_bwd_group<CPLX, N, (MAXT < 256 ? 256 : MAXT), true>), dim3(p.NG, p.B), dim3(p.NT),
+                         p.lds_adjoint, st, a);
       break;
     case 2:
       if (set_lds(&k_chunk_bwd_inv<CPLX, N, MAXT, WAVE>, p.lds_bwd_inv) != EWS_OK) return EWS_ERR_LAUNCH;
@@ -1705,8 +1836,8 @@ int backward_pass(const Plan& p, DiagArgs a, hipStream_t st, int pass) {
       hipLaunchKernelGGL((k_chunk_bwd_full<CPLX, N, MAXT, WAVE>), grid, blkb, p.lds_bwd_full, st, a);
       break;
     case 3: {
-      const size_t total = (size_t)p.B * p.L;
-      const int nb = (int)((total + 255) / 256 < 4096 ? (total + 255) / 256 : 4096);
+      const size_t total = (size_t)p.B * p.L * (p.d + 1);
+      const int nb = (int)((total + 255) / 256 < 8192 ? (total + 255) / 256 : 8192);
       hipLaunchKernelGGL(k_knot_grads, dim3(nb), dim3(256), 0, st, a);
       break;
     }
