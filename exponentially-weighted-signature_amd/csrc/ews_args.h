@@ -1,0 +1,49 @@
+// Argument block shared by the generic chunk kernels (ews_diag.hip) and the plane pair-group kernels
+// (ews_pairs.hip): shapes, the chunk plan and every device pointer of one forward or backward call.
+#pragma once
+
+#include <stddef.h>
+
+namespace ews {
+
+// ------------------------------------------------------------------------------------------- arguments
+struct DiagArgs {
+  int B, L, n_int, d, K;  // K: planes (complex) or channels (real)
+  int N, flow_mode, readout;
+  int T, C;               // chunk length, chunk count
+  int scan_cb;            // chunks per LDS-staged block in the float64 scans
+  int W, off1, off2, lvl0, D, npar;
+  int path_bf16;
+  const void* path;
+  const float* clock;
+  const float* params;
+  float* out;
+  const float* gout;
+  // residual
+  double* carries;  // (B, C+1, D)
+  int* argmax;      // (B, W)
+  // workspace
+  float* summ;      // (B, C, D)
+  float* mu;        // (B, C, D)
+  float* mt;        // (B, C, D)
+  float* red;       // (B, C, W)
+  int* red_idx;     // (B, C, W)
+  float* dv;        // (B, n_int, d)
+  float* dh;        // (B, n_int)
+  float* gp;        // (B, C, npar)
+  float* gph;       // (B, C)
+  double* gagg;     // (B, NG, D) group aggregates (forward) / group cotangent aggregates (backward)
+  double* gcar;     // (B, NG, D) state before each group (forward) / cotangent after each group (backward)
+  int NG;           // chunk groups of scan_cb chunks
+  // per-chunk clock classification (residual): bit 0 = uniform (the pair-group kernels own the chunk),
+  // bit 1 = the steps may be inverted backwards; and the chunk's mean clock step
+  int* cflag;       // (B, C)
+  float* chbar;     // (B, C)
+  int fast_ok;      // 1 if this configuration has pair-group kernels (flags are valid), else 0
+  // backward outputs
+  float* dpath;
+  float* dclock;
+  float* dparams;
+};
+
+}  // namespace ews

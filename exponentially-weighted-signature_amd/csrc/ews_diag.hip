@@ -25,8 +25,10 @@
 
 #include <type_traits>
 
+#include "ews_args.h"
 #include "ews_hip.h"
 #include "ews_numerics.h"
+#include "ews_pairs.h"
 
 namespace ews {
 
@@ -60,41 +62,6 @@ __device__ __forceinline__ cd to_d(cf a) { return cd{(double)a.re, (double)a.im}
 __device__ __forceinline__ double to_d(float a) { return (double)a; }
 __device__ __forceinline__ cf to_f(cd a) { return cf{(float)a.re, (float)a.im}; }
 __device__ __forceinline__ float to_f(double a) { return (float)a; }
-
-// ------------------------------------------------------------------------------------------- arguments
-struct DiagArgs {
-  int B, L, n_int, d, K;  // K: planes (complex) or channels (real)
-  int N, flow_mode, readout;
-  int T, C;               // chunk length, chunk count
-  int scan_cb;            // chunks per LDS-staged block in the float64 scans
-  int W, off1, off2, lvl0, D, npar;
-  int path_bf16;
-  const void* path;
-  const float* clock;
-  const float* params;
-  float* out;
-  const float* gout;
-  // residual
-  double* carries;  // (B, C+1, D)
-  int* argmax;      // (B, W)
-  // workspace
-  float* summ;      // (B, C, D)
-  float* mu;        // (B, C, D)
-  float* mt;        // (B, C, D)
-  float* red;       // (B, C, W)
-  int* red_idx;     // (B, C, W)
-  float* dv;        // (B, n_int, d)
-  float* dh;        // (B, n_int)
-  float* gp;        // (B, C, npar)
-  float* gph;       // (B, C)
-  double* gagg;     // (B, NG, D) group aggregates (forward) / group cotangent aggregates (backward)
-  double* gcar;     // (B, NG, D) state before each group (forward) / cotangent after each group (backward)
-  int NG;           // chunk groups of scan_cb chunks
-  // backward outputs
-  float* dpath;
-  float* dclock;
-  float* dparams;
-};
 
 enum { MODE_SUMMARY = 0, MODE_PREFIX = 1, MODE_REDUCE = 2 };
 
@@ -333,6 +300,7 @@ __global__ __launch_bounds__(MAXT) void k_chunk_fwd(DiagArgs a) {
   float* s_v = smem;
   float* s_h = s_v + a.T * a.d;
   const int c = blockIdx.x, b = blockIdx.y, tid = threadIdx.x;
+  if (a.fast_ok && (a.cflag[b * a.C + c] & 1)) return;  // a pair-group kernel owns this chunk
   const int t0 = c * a.T;
   const int Tc = min(a.T, a.n_int - t0);
   load_chunk(a, b, t0, Tc, s_v, s_h);
@@ -1037,6 +1005,7 @@ __global__ __launch_bounds__(MAXT) void k_chunk_bwd_local(DiagArgs a) {
   int* s_am = reinterpret_cast<int*>(smem + Lo.am);
   float* s_red = smem + Lo.g;
   const int c = blockIdx.x, b = blockIdx.y, tid = threadIdx.x;
+  if (a.fast_ok && (a.cflag[b * a.C + c] & 1)) return;  // a pair-group kernel owns this chunk
   const int t0 = c * a.T;
   const int Tc = min(a.T, a.n_int - t0);
   const bool prefix = a.readout == EWS_READOUT_PREFIX;
@@ -1385,12 +1354,14 @@ __device__ __forceinline__ void load_cot(const DiagArgs& a, const LaneMap& m, co
 // Shared prologue: clock steps, ownership test, increments, per-sample cotangent, first staged block.
 #define EWS_BWD_PROLOGUE(OWNS, ROWS)                                                                              \
   const int c = blockIdx.x, b = blockIdx.y, tid = threadIdx.x;                                             \
+  if (a.fast_ok && (a.cflag[b * a.C + c] & 3) == 3) return; /* a pair-group kernel owns this chunk */      \
   const int t0 = c * a.T;                                                                                  \
   const int Tc = min(a.T, a.n_int - t0);                                                                   \
   const bool prefix = a.readout == EWS_READOUT_PREFIX;                                                     \
   load_clock(a, b, t0, Tc, s_h);                                                                           \
   __syncthreads();                                                                                         \
-  const ChunkClock cc = chunk_clock<T>(a, b, Tc, s_h);                                                     \
+  ChunkClock cc = chunk_clock<T>(a, b, Tc, s_h);                                                           \
+  if (a.fast_ok) cc.inv_ok = (a.cflag[b * a.C + c] & 2) != 0; /* one invertibility test for every kernel */ \
   if (!(OWNS)) return;                                                                                     \
   load_chunk(a, b, t0, Tc, s_v, s_h);                                                                      \
   if (!prefix) stage_vec(a, b, s_gv, s_am);                                                                \
@@ -1581,22 +1552,32 @@ __global__ __launch_bounds__(MAXT) void k_chunk_bwd_full(DiagArgs a) {
 
 // ------------------------------------------------------------------------------------------- B4
 // Knot gradients from interval gradients: dX_t = dv_{t-1} - dv_t, dtheta_t = dh_{t-1} - dh_t (+ the shared flow
-// step's gradient for cached flows). One thread per (sample, knot, channel) element: coalesced.
+// step's gradient for cached flows). One workgroup per (chunk, sample): the chunk's first knot always, its interior
+// knots unless a pair-group adjoint already wrote them (it leaves dv / dh of its first and last interval for the
+// boundary knots); workgroup C handles the last knot L-1.
 __global__ void k_knot_grads(DiagArgs a) {
+  const int c = blockIdx.x, b = blockIdx.y;
   const int dp1 = a.d + 1;
-  const size_t total = (size_t)a.B * a.L * dp1;
-  for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += (size_t)gridDim.x * blockDim.x) {
-    const int ch = (int)(i % dp1);
-    const size_t bt = i / dp1;
-    const int b = (int)(bt / a.L), t = (int)(bt % a.L);
+  int k0, k1;  // knot range [k0, k1)
+  if (c == a.C) {
+    k0 = a.n_int;
+    k1 = a.L;
+  } else {
+    k0 = c * a.T;
+    const bool owned = a.fast_ok && (a.cflag[b * a.C + c] & 3) == 3;
+    k1 = owned ? k0 + 1 : min(k0 + a.T, a.n_int);
+  }
+  const float* dvb = a.dv + (size_t)b * a.n_int * a.d;
+  const float* dhb = a.dh + (size_t)b * a.n_int;
+  for (int i = threadIdx.x; i < (k1 - k0) * dp1; i += blockDim.x) {
+    const int t = k0 + i / dp1, ch = i % dp1;
+    const size_t bt = (size_t)b * a.L + t;
     if (ch < a.d) {
-      const float* dvb = a.dv + (size_t)b * a.n_int * a.d;
       float g = 0.0f;
       if (t >= 1) g += dvb[(size_t)(t - 1) * a.d + ch];
       if (t < a.n_int) g -= dvb[(size_t)t * a.d + ch];
       a.dpath[bt * a.d + ch] = g;
     } else {
-      const float* dhb = a.dh + (size_t)b * a.n_int;
       float g = 0.0f;
       if (t >= 1) g += dhb[t - 1];
       if (t < a.n_int) g -= dhb[t];
@@ -1605,7 +1586,7 @@ __global__ void k_knot_grads(DiagArgs a) {
         const int r = (a.flow_mode == EWS_FLOW_CACHED) ? 0 : 1;
         if (t == r || t == r + 1) {
           double hs = 0.0;
-          for (int c = 0; c < a.C; ++c) hs += (double)a.gph[(size_t)b * a.C + c];
+          for (int cc = 0; cc < a.C; ++cc) hs += (double)a.gph[(size_t)b * a.C + cc];
           g += (t == r + 1) ? (float)hs : -(float)hs;
         }
       }
@@ -1641,7 +1622,7 @@ size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 
 struct Plan {
   int B, L, n_int, d, K, N, T, C, D, W, npar;
-  bool cplx, wave;
+  bool cplx, wave, fast;
   int NT, NTb, scan_cb, NG;
   size_t lds_bwd_local, lds_bwd_full, lds_bwd_inv, lds_carry, lds_adjoint;
 };
@@ -1687,6 +1668,7 @@ int make_plan(const ews_diag_desc* s, Plan& p) {
   }
   if (T > 256) T = 256;
   p.T = T;
+  p.fast = pairs_eligible(s->structure, s->depth, s->dim, s->readout, s->flow_mode, T);
   p.C = (p.n_int + T - 1) / T;
   p.lds_bwd_local = (size_t)bwd_lds_layout(T, p.d, p.W, p.NTb, 0, p.wave, false, kGB).total * 4;
   p.lds_bwd_full = bwd_lds_bytes(p, T, true);
@@ -1723,6 +1705,9 @@ WsLayout ws_layout(const Plan& p) {
   return w;
 }
 size_t resid_carries_bytes(const Plan& p) { return align256((size_t)p.B * (p.C + 1) * p.D * 8); }
+size_t resid_argmax_bytes(const Plan& p) { return align256((size_t)p.B * p.W * 4); }
+size_t resid_chunk_bytes(const Plan& p) { return align256((size_t)p.B * p.C * 4); }
+size_t resid_bytes(const Plan& p) { return resid_carries_bytes(p) + resid_argmax_bytes(p) + 2 * resid_chunk_bytes(p); }
 
 DiagArgs make_args(const ews_diag_desc* s, const Plan& p, const void* path, const float* clock,
                    const float* params, void* residual, void* workspace) {
@@ -1735,6 +1720,9 @@ DiagArgs make_args(const ews_diag_desc* s, const Plan& p, const void* path, cons
   char* r = (char*)residual;
   a.carries = (double*)r;
   a.argmax = (int*)(r + resid_carries_bytes(p));
+  a.cflag = (int*)(r + resid_carries_bytes(p) + resid_argmax_bytes(p));
+  a.chbar = (float*)(r + resid_carries_bytes(p) + resid_argmax_bytes(p) + resid_chunk_bytes(p));
+  a.fast_ok = p.fast ? 1 : 0;
   const WsLayout w = ws_layout(p);
   char* ws = (char*)workspace;
   a.summ = (float*)(ws + w.summ); a.mu = (float*)(ws + w.mu); a.mt = (float*)(ws + w.mt);
@@ -1759,6 +1747,9 @@ int forward_pass(const ews_diag_desc* s, const Plan& p, DiagArgs a, hipStream_t 
   dim3 grid(p.C, p.B), blk(p.NT);
   switch (pass) {
     case 0:
+      if (p.fast) {
+        if (pairs_forward(a, st, false) != 0) return EWS_ERR_LAUNCH;
+      }
       hipLaunchKernelGGL((k_chunk_fwd<CPLX, N, MODE_SUMMARY, MAXT, true>), grid, blk, fwd_lds(p), st, a);
       EWS_LAUNCH_CHECK();
       hipLaunchKernelGGL((k_chunk_fwd<CPLX, N, MODE_SUMMARY, MAXT, false>), grid, blk, fwd_lds(p), st, a);
@@ -1772,6 +1763,7 @@ int forward_pass(const ews_diag_desc* s, const Plan& p, DiagArgs a, hipStream_t 
       break;
     case 2:
       if (s->readout == EWS_READOUT_PREFIX) {
+        if (p.fast && pairs_forward(a, st, true) != 0) return EWS_ERR_LAUNCH;
         hipLaunchKernelGGL((k_chunk_fwd<CPLX, N, MODE_PREFIX, MAXT, true>), grid, blk, fwd_lds(p), st, a);
         EWS_LAUNCH_CHECK();
         hipLaunchKernelGGL((k_chunk_fwd<CPLX, N, MODE_PREFIX, MAXT, false>), grid, blk, fwd_lds(p), st, a);
@@ -1813,6 +1805,7 @@ int backward_pass(const Plan& p, DiagArgs a, hipStream_t st, int pass) {
   dim3 grid(p.C, p.B), blkb(p.NTb);
   switch (pass) {
     case 0:
+      if (p.fast && pairs_backward(a, st, false) != 0) return EWS_ERR_LAUNCH;
       if (set_lds(&k_chunk_bwd_local<CPLX, N, MAXT, WAVE, true>, p.lds_bwd_local) != EWS_OK) return EWS_ERR_LAUNCH;
       if (set_lds(&k_chunk_bwd_local<CPLX, N, MAXT, WAVE, false>, p.lds_bwd_local) != EWS_OK) return EWS_ERR_LAUNCH;
       hipLaunchKernelGGL((k_chunk_bwd_local<CPLX, N, MAXT, WAVE, true>), grid, blkb, p.lds_bwd_local, st, a);
@@ -1829,18 +1822,16 @@ int backward_pass(const Plan& p, DiagArgs a, hipStream_t st, int pass) {
                          p.lds_adjoint, st, a);
       break;
     case 2:
+      if (p.fast && pairs_backward(a, st, true) != 0) return EWS_ERR_LAUNCH;
       if (set_lds(&k_chunk_bwd_inv<CPLX, N, MAXT, WAVE>, p.lds_bwd_inv) != EWS_OK) return EWS_ERR_LAUNCH;
       if (set_lds(&k_chunk_bwd_full<CPLX, N, MAXT, WAVE>, p.lds_bwd_full) != EWS_OK) return EWS_ERR_LAUNCH;
       hipLaunchKernelGGL((k_chunk_bwd_inv<CPLX, N, MAXT, WAVE>), grid, blkb, p.lds_bwd_inv, st, a);
       EWS_LAUNCH_CHECK();
       hipLaunchKernelGGL((k_chunk_bwd_full<CPLX, N, MAXT, WAVE>), grid, blkb, p.lds_bwd_full, st, a);
       break;
-    case 3: {
-      const size_t total = (size_t)p.B * p.L * (p.d + 1);
-      const int nb = (int)((total + 255) / 256 < 8192 ? (total + 255) / 256 : 8192);
-      hipLaunchKernelGGL(k_knot_grads, dim3(nb), dim3(256), 0, st, a);
+    case 3:
+      hipLaunchKernelGGL(k_knot_grads, dim3(p.C + 1, p.B), dim3(64), 0, st, a);
       break;
-    }
     case 4:
       hipLaunchKernelGGL(k_param_grads, dim3(p.npar), dim3(256), 0, st, a);
       break;
@@ -1893,7 +1884,7 @@ size_t ews_diag_workspace_bytes(const ews_diag_desc* desc) {
 size_t ews_diag_residual_bytes(const ews_diag_desc* desc) {
   Plan p;
   if (make_plan(desc, p) != EWS_OK) return 0;
-  return resid_carries_bytes(p) + align256((size_t)p.B * p.W * 4);
+  return resid_bytes(p);
 }
 
 int ews_diag_forward_pass(const ews_diag_desc* desc, int pass, const void* path, const float* clock,

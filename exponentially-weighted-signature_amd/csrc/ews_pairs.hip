@@ -1,0 +1,691 @@
+// Pair-group kernels of the rotation-plane EWS scan on MI355X (gfx950): d = 16 (8 planes), depth 2, per-interval
+// flows, prefix readout, on chunks whose clock steps are uniform to float32 precision. Every other chunk (and
+// every other configuration) runs in the generic kernels of ews_diag.hip.
+//
+// Math (reference sign, flow exp(-h A)): plane j acts on p_j = v_{2j} + i v_{2j+1}; with x_j = h u_j,
+// u_j = -conj(z_j), rho_j = e^{x_j}, phi_j = exp[0, x_j]:
+//     S1_j  <- rho_j S1_j + phi_j p_j
+//     SB_jk <- LB_jk SB_jk + c_j phi_k p_k       + IB_jk p_j p_k          LB = e^{h (u_j + u_k)}
+//     SA_jk <- LA_jk SA_jk + c_j conj(phi_k p_k) + IA_jk p_j conj(p_k)    LA = e^{h (u_j + conj(u_k))}
+// with c_j = rho_j S1_j (before the update), IB = exp[0, x_j, h (u_j + u_k)], IA = exp[0, x_j, h (u_j + conj u_k)]:
+// the Chen step S2 <- M S2 M^T + (M S1) s1^T + s2 (ews/core/chen_scan.py:124-152) diagonalised plane by plane,
+// with the closed-form local terms of ews/core/kernels/plane_engine.py:134-152.
+//
+// Lane layout. A chunk of T intervals belongs to a group of G = 8 * (8 / KP) lanes: lane (j, kg) = 8 kg + j owns
+// plane j's level 1 and the KP level-2 pairs (j, k), k = KP kg .. KP kg + KP - 1. A wavefront (= one workgroup) holds
+// 64 / G groups: consecutive chunks of one sample. The forward and the local adjoint use KP = 4 (16-lane groups);
+// the full adjoint, which carries four times the live values per pair, uses KP = 2 (32-lane groups). The row sums
+// over k that feed the level-1 adjoint are DPP / swizzle adds among the lanes of plane j; the column sums over j
+// (gradients of the later factor) go through LDS once per block of steps, off the sequential chain.
+//
+// Uniform chunks. When every step h_t of a chunk, and every partial sum of (h_t - hbar), is within
+// 2^-21 / max|u| of the chunk mean hbar (as with a float32 uniform clock), every coefficient is taken at hbar:
+// relative error <= 2^-21 per coefficient and <= 2^-20 on a product of flows, since the partial sums of the steps
+// telescope to clock differences. Parameter gradients, whose h-factor enters linearly, weight each step by its own
+// h_t.
+//
+// Scaling. Level-2 pair states are kept halved (SAh = SA/2, SBh = SB/2), so an output block is sums and
+// differences of them, and level-2 cotangents doubled (lA = 2 dL/dSA, lB = 2 dL/dSB); the halves fold into the
+// coefficients (phih = phi/2, IBh = IB/2, ...).
+#include <hip/hip_runtime.h>
+
+#include <type_traits>
+
+#include "ews_args.h"
+#include "ews_hip.h"
+#include "ews_numerics.h"
+#include "ews_pairs.h"
+
+namespace ews {
+namespace pairs {
+
+constexpr int K = 8;      // planes
+constexpr int DIM = 16;   // channels
+constexpr int NB = 4;     // steps per block of the full adjoint's column sums
+constexpr int VPITCH = (kMaxT + 1) * DIM;  // LDS floats per group of staged increments (one padding row)
+
+template <int KP> struct Geo {
+  static constexpr int NKG = K / KP;  // k-groups per plane row
+  static constexpr int G = K * NKG;   // lanes per chunk group
+  static constexpr int GPW = 64 / G;  // chunk groups per wavefront (workgroup)
+};
+
+typedef float f4u __attribute__((ext_vector_type(4), aligned(4)));
+typedef float f2u __attribute__((ext_vector_type(2), aligned(4)));
+typedef float f4a __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ cf cjm(cf a, cf b) { return cf{a.re * b.re + a.im * b.im, a.re * b.im - a.im * b.re}; }  // conj(a) b
+__device__ __forceinline__ float redot(cf a, cf b) { return a.re * b.re + a.im * b.im; }  // Re(conj(a) b)
+__device__ __forceinline__ cf fma_c(cf a, cf b, cf c) {  // a b + c
+  return cf{fmaf(a.re, b.re, fmaf(-a.im, b.im, c.re)), fmaf(a.re, b.im, fmaf(a.im, b.re, c.im))};
+}
+
+// cross-lane moves: DPP row_ror inside rows of 16 lanes, ds_swizzle (xor 16) inside halves of 32
+#define EWS_ROR(v, n) __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x120 + (n), 0xf, 0xf, false))
+__device__ __forceinline__ float xor16(float v) { return __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(v), 0x401F)); }
+
+// sum over the k-groups of plane j (lanes j + 8 kg of the group)
+template <int KP> __device__ __forceinline__ float kg_sum(float v) {
+  if constexpr (Geo<KP>::NKG >= 2) v += EWS_ROR(v, 8);
+  if constexpr (Geo<KP>::NKG >= 4) v += xor16(v);
+  return v;
+}
+template <int KP> __device__ __forceinline__ cf kg_sum(cf v) { return cf{kg_sum<KP>(v.re), kg_sum<KP>(v.im)}; }
+
+// Compile-time loop: the pair arrays below stay in registers only if every index is a constant.
+template <int I, int N, class F> __device__ __forceinline__ void static_for(F&& f) {
+  if constexpr (I < N) {
+    f(std::integral_constant<int, I>{});
+    static_for<I + 1, N>(f);
+  }
+}
+
+struct Lane {
+  int gi, gl, j, kg;
+};
+template <int KP> __device__ __forceinline__ Lane lane_of(int tid) {
+  Lane l;
+  l.gi = tid / Geo<KP>::G;
+  l.gl = tid % Geo<KP>::G;
+  l.j = l.gl & 7;
+  l.kg = l.gl >> 3;
+  return l;
+}
+
+__device__ __forceinline__ cf load_u(const float* params, int j) { return cf{-params[2 * j], params[2 * j + 1]}; }
+
+// Increments v_i = X_{i+1} - X_i of the workgroup's intervals into LDS, group gi's interval t at
+// s_v[gi * VPITCH + 16 t]; clock steps into s_h[gi * kMaxT + t] when s_h is given.
+template <int KP, bool BF16>
+__device__ __forceinline__ void stage(const DiagArgs& a, int b, int cb, float* s_v, float* s_h) {
+  constexpr int GPW = Geo<KP>::GPW;
+  const int i0 = cb * a.T;
+  const int n = min(GPW * a.T, a.n_int - i0);
+  const int tid = threadIdx.x;
+  if constexpr (!BF16) {
+    const float* src = reinterpret_cast<const float*>(a.path) + ((size_t)b * a.L + i0) * DIM;
+    for (int q = tid; q < n * 4; q += 64) {
+      const int i = q >> 2, c4 = q & 3;
+      const int gi = i / a.T, t = i - gi * a.T;
+      const f4a x0 = *reinterpret_cast<const f4a*>(src + (size_t)i * DIM + 4 * c4);
+      const f4a x1 = *reinterpret_cast<const f4a*>(src + (size_t)(i + 1) * DIM + 4 * c4);
+      *reinterpret_cast<f4a*>(s_v + gi * VPITCH + t * DIM + 4 * c4) = x1 - x0;
+    }
+  } else {
+    const unsigned short* src = reinterpret_cast<const unsigned short*>(a.path) + ((size_t)b * a.L + i0) * DIM;
+    for (int q = tid; q < n * DIM; q += 64) {
+      const int i = q / DIM, ch = q - i * DIM;
+      const int gi = i / a.T, t = i - gi * a.T;
+      const float x0 = __uint_as_float(((unsigned)src[(size_t)i * DIM + ch]) << 16);
+      const float x1 = __uint_as_float(((unsigned)src[(size_t)(i + 1) * DIM + ch]) << 16);
+      s_v[gi * VPITCH + t * DIM + ch] = x1 - x0;
+    }
+  }
+  if (s_h) {
+    const float* th = a.clock + (size_t)b * a.L + i0;
+    for (int i = tid; i < n; i += 64) {
+      const int gi = i / a.T, t = i - gi * a.T;
+      s_h[gi * kMaxT + t] = th[i + 1] - th[i];
+    }
+  }
+}
+
+// p_j and the lane's KP p_k of step t
+template <int KP> __device__ __forceinline__ void load_p(const float* vr, const Lane& l, cf& pj, cf* pk) {
+  const float2 a = *reinterpret_cast<const float2*>(vr + 2 * l.j);
+  pj = cf{a.x, a.y};
+  static_for<0, KP / 2>([&](auto ic) {
+    constexpr int i = ic;
+    const f4a v = *reinterpret_cast<const f4a*>(vr + 2 * KP * l.kg + 4 * i);
+    pk[2 * i] = cf{v.x, v.y};
+    pk[2 * i + 1] = cf{v.z, v.w};
+  });
+}
+
+// products p_j p_k and p_j conj(p_k)
+__device__ __forceinline__ void prods(cf pj, cf pk, cf& pi, cf& pic) {
+  const float aa = pj.re * pk.re, bb = pj.im * pk.im, cc = pj.re * pk.im, dd = pj.im * pk.re;
+  pi = cf{aa - bb, cc + dd};
+  pic = cf{aa + bb, dd - cc};
+}
+
+// Forward coefficients of the lane at the chunk's mean step.
+template <int KP> struct FwdCoef {
+  cf rho, phi;            // plane j
+  cf phk[KP];             // phi_k / 2
+  cf LB[KP], LA[KP];      // pair flows
+  cf IB[KP], IA[KP];      // IB / 2, IA / 2
+};
+template <int KP>
+__device__ __forceinline__ void fwd_coef(const DiagArgs& a, const Lane& l, float hb, FwdCoef<KP>& f) {
+  const cf uj = load_u(a.params, l.j);
+  const cf xj = hb * uj;
+  const Node1<cf> nj = node1(xj);
+  f.rho = nj.e;
+  f.phi = nj.p;
+  static_for<0, KP>([&](auto qc) {
+    constexpr int q = qc;
+    const cf uk = load_u(a.params, KP * l.kg + q);
+    const Node1<cf> nk = node1(hb * uk);
+    f.phk[q] = 0.5f * nk.p;
+    const cf ub = uj + uk, ua = uj + conj(uk);
+    f.LB[q] = expv(hb * ub);
+    f.LA[q] = expv(hb * ua);
+    f.IB[q] = 0.5f * dd3<cf, false>(xj, hb * ub).d;
+    f.IA[q] = 0.5f * dd3<cf, false>(xj, hb * ua).d;
+  });
+}
+
+// ------------------------------------------------------------------------------------------------ classification
+// Chunk c of sample b: flag bit 0 = uniform steps (coefficients at the mean step hbar), bit 1 = the steps may be
+// inverted backwards (stepping back amplifies errors by e^{2 Dmax tau} <= 2 over the chunk). Evaluated by the 16
+// lanes of the chunk's group, each over every 16th step, then combined with DPP inside the group.
+__device__ __forceinline__ float row_max16(float v) {
+  v = fmaxf(v, EWS_ROR(v, 8));
+  v = fmaxf(v, EWS_ROR(v, 4));
+  v = fmaxf(v, EWS_ROR(v, 2));
+  v = fmaxf(v, EWS_ROR(v, 1));
+  return v;
+}
+__device__ __forceinline__ int classify_chunk(const DiagArgs& a, int b, int c, int gl, float& hb) {
+  const int t0 = c * a.T, Tc = min(a.T, a.n_int - t0);
+  const float* th = a.clock + (size_t)b * a.L + t0;
+  float R = 0.0f, Dm = 0.0f;
+  for (int j = 0; j < K; ++j) {
+    R = fmaxf(R, absv(load_u(a.params, j)));
+    Dm = fmaxf(Dm, a.params[2 * j]);
+  }
+  const float th0 = th[0];
+  const float tau = th[Tc] - th0;
+  hb = tau / (float)Tc;
+  float dev = 0.0f, drift = 0.0f, bad = 0.0f;
+  for (int t = gl; t < Tc; t += 16) {
+    const float x0 = th[t], x1 = th[t + 1];
+    const float h = x1 - x0;
+    if (!isfinite(h)) bad = 1.0f;
+    dev = fmaxf(dev, fabsf(h - hb));
+    drift = fmaxf(drift, fabsf((x1 - th0) - (float)(t + 1) * hb));
+  }
+  dev = row_max16(dev);
+  drift = row_max16(drift);
+  bad = row_max16(bad);
+  const bool fin = bad == 0.0f && isfinite(tau) && isfinite(R);
+  const float lim = 4.76837158e-7f;  // 2^-21
+  const bool uni = fin && R * dev <= lim && R * drift <= lim;
+  const bool inv = fin && 2.0f * Dm * fabsf(tau) <= 0.69314718f;
+  return (uni ? 1 : 0) | (inv ? 2 : 0);
+}
+
+// ------------------------------------------------------------------------------------------------ forward
+// OUT = false: chunk summaries from a zero carry (summ), and the classification of every chunk (this launch runs
+// first); OUT = true: prefix rows from the float64 carry. 16-lane groups (KP = 4).
+template <bool OUT, bool BF16>
+__global__ __launch_bounds__(64) void k_fwd(DiagArgs a) {
+  constexpr int KP = 4, GPW = Geo<KP>::GPW;
+  __shared__ __align__(16) float s_v[GPW * VPITCH];
+  const Lane l = lane_of<KP>(threadIdx.x);
+  const int b = blockIdx.y, cb = blockIdx.x * GPW, c = cb + l.gi;
+  stage<KP, BF16>(a, b, cb, s_v, nullptr);
+  __syncthreads();
+  if (c >= a.C) return;
+  const int ci = b * a.C + c;
+  float hb;
+  if constexpr (!OUT) {
+    const int flag = classify_chunk(a, b, c, l.gl, hb);
+    if (l.gl == 0) {
+      a.cflag[ci] = flag;
+      a.chbar[ci] = hb;
+    }
+    if (!(flag & 1)) return;
+  } else {
+    if (!(a.cflag[ci] & 1)) return;
+    hb = a.chbar[ci];
+  }
+  const int t0 = c * a.T, Tc = min(a.T, a.n_int - t0);
+  FwdCoef<KP> f;
+  fwd_coef<KP>(a, l, hb, f);
+  cf S1{0.0f, 0.0f}, SA[KP], SB[KP];
+  static_for<0, KP>([&](auto qc) {
+    constexpr int q = qc;
+    SA[q] = SB[q] = cf{0.0f, 0.0f};
+  });
+  if constexpr (OUT) {
+    const double* cr = a.carries + ((size_t)b * (a.C + 1) + c) * a.D;
+    S1 = cf{(float)cr[2 * l.j], (float)cr[2 * l.j + 1]};
+    static_for<0, KP>([&](auto qc) {
+      constexpr int q = qc;
+      const double* p2 = cr + DIM + 4 * (l.j * K + KP * l.kg + q);
+      SA[q] = cf{(float)(0.5 * p2[0]), (float)(0.5 * p2[1])};
+      SB[q] = cf{(float)(0.5 * p2[2]), (float)(0.5 * p2[3])};
+    });
+  }
+  const float* vg = s_v + l.gi * VPITCH;
+  float* orow = a.out + ((size_t)b * a.n_int + t0) * a.W;
+  const int o1 = a.off1 + 2 * l.j, o2 = a.off2 + 2 * l.j * DIM + 2 * KP * l.kg;
+  for (int t = 0; t < Tc; ++t) {
+    cf pj, pk[KP];
+    load_p<KP>(vg + t * DIM, l, pj, pk);
+    const cf cj = f.rho * S1;
+    S1 = fma_c(f.phi, pj, cj);
+    static_for<0, KP>([&](auto qc) {
+      constexpr int q = qc;
+      const cf sg = f.phk[q] * pk[q];
+      cf pi, pic;
+      prods(pj, pk[q], pi, pic);
+      SB[q] = fma_c(f.LB[q], SB[q], fma_c(cj, sg, f.IB[q] * pi));
+      SA[q] = fma_c(f.LA[q], SA[q], fma_c(cj, conj(sg), f.IA[q] * pic));
+    });
+    if constexpr (OUT) {
+      float* row = orow + (size_t)t * a.W;
+      if (a.lvl0 && l.gl == 0) row[0] = 1.0f;
+      if (l.kg == 0) *reinterpret_cast<f2u*>(row + o1) = f2u{S1.re, S1.im};
+      f4u* p0 = reinterpret_cast<f4u*>(row + o2);
+      f4u* p1 = reinterpret_cast<f4u*>(row + o2 + DIM);
+      static_for<0, KP / 2>([&](auto ic) {
+        constexpr int i = ic, q0 = 2 * i, q1 = 2 * i + 1;
+        p0[i] = f4u{SA[q0].re + SB[q0].re, SB[q0].im - SA[q0].im, SA[q1].re + SB[q1].re, SB[q1].im - SA[q1].im};
+        p1[i] = f4u{SA[q0].im + SB[q0].im, SA[q0].re - SB[q0].re, SA[q1].im + SB[q1].im, SA[q1].re - SB[q1].re};
+      });
+    }
+  }
+  if constexpr (!OUT) {
+    float* sp = a.summ + ((size_t)b * a.C + c) * a.D;
+    if (l.kg == 0) *reinterpret_cast<float2*>(sp + 2 * l.j) = float2{S1.re, S1.im};
+    static_for<0, KP>([&](auto qc) {
+      constexpr int q = qc;
+      *reinterpret_cast<f4a*>(sp + DIM + 4 * (l.j * K + KP * l.kg + q)) =
+          f4a{2.0f * SA[q].re, 2.0f * SA[q].im, 2.0f * SB[q].re, 2.0f * SB[q].im};
+    });
+  }
+}
+
+// ------------------------------------------------------------------------------------------------ backward
+// Cotangent row slice of the lane: level 1 of plane j and the KP 2x2 blocks (j, k).
+template <int KP> struct GRow {
+  f4u r0[KP / 2], r1[KP / 2];
+  f2u g1;
+};
+template <int KP> __device__ __forceinline__ GRow<KP> load_g(const float* row, int o1, int o2) {
+  GRow<KP> g;
+  g.g1 = *reinterpret_cast<const f2u*>(row + o1);
+  const f4u* p0 = reinterpret_cast<const f4u*>(row + o2);
+  const f4u* p1 = reinterpret_cast<const f4u*>(row + o2 + DIM);
+  static_for<0, KP / 2>([&](auto ic) {
+    constexpr int i = ic;
+    g.r0[i] = p0[i];
+    g.r1[i] = p1[i];
+  });
+  return g;
+}
+// doubled pair cotangents (2 dL/dSA, 2 dL/dSB) of pair q from the block entries g00, g01, g10, g11
+template <int KP, int q> __device__ __forceinline__ void g_pair(const GRow<KP>& g, cf& gA, cf& gB) {
+  const f4u r0 = g.r0[q / 2], r1 = g.r1[q / 2];
+  const float g00 = (q & 1) ? r0.z : r0.x, g01 = (q & 1) ? r0.w : r0.y;
+  const float g10 = (q & 1) ? r1.z : r1.x, g11 = (q & 1) ? r1.w : r1.y;
+  gA = cf{g00 + g11, g10 - g01};
+  gB = cf{g00 - g11, g01 + g10};
+}
+
+// B1: chunk-local adjoint with zero incoming cotangent -> mu (cotangent on the chunk's carry-in state). KP = 4.
+template <bool BF16>
+__global__ __launch_bounds__(64) void k_bwd_local(DiagArgs a) {
+  constexpr int KP = 4, GPW = Geo<KP>::GPW;
+  __shared__ __align__(16) float s_v[GPW * VPITCH];
+  const Lane l = lane_of<KP>(threadIdx.x);
+  const int b = blockIdx.y, cb = blockIdx.x * GPW, c = cb + l.gi;
+  stage<KP, BF16>(a, b, cb, s_v, nullptr);
+  __syncthreads();
+  if (c >= a.C) return;
+  const int ci = b * a.C + c;
+  if (!(a.cflag[ci] & 1)) return;
+  const int t0 = c * a.T, Tc = min(a.T, a.n_int - t0);
+  FwdCoef<KP> f;
+  fwd_coef<KP>(a, l, a.chbar[ci], f);
+  const float* vg = s_v + l.gi * VPITCH;
+  const float* grow = a.gout + ((size_t)b * a.n_int + t0) * a.W;
+  const int o1 = a.off1 + 2 * l.j, o2 = a.off2 + 2 * l.j * DIM + 2 * KP * l.kg;
+  cf l1{0.0f, 0.0f}, lA[KP], lB[KP];
+  static_for<0, KP>([&](auto qc) {
+    constexpr int q = qc;
+    lA[q] = lB[q] = cf{0.0f, 0.0f};
+  });
+  GRow<KP> gn1 = load_g<KP>(grow + (size_t)(Tc - 1) * a.W, o1, o2);
+  GRow<KP> gn2 = gn1;
+  if (Tc >= 2) gn2 = load_g<KP>(grow + (size_t)(Tc - 2) * a.W, o1, o2);
+  for (int t = Tc - 1; t >= 0; --t) {
+    const GRow<KP> g = gn1;
+    gn1 = gn2;
+    if (t >= 2) gn2 = load_g<KP>(grow + (size_t)(t - 2) * a.W, o1, o2);
+    cf pj, pk[KP];
+    load_p<KP>(vg + t * DIM, l, pj, pk);
+    l1 += cf{g.g1.x, g.g1.y};
+    cf toC{0.0f, 0.0f};
+    static_for<0, KP>([&](auto qc) {
+      constexpr int q = qc;
+      cf gA, gB;
+      g_pair<KP, q>(g, gA, gB);
+      lA[q] += gA;
+      lB[q] += gB;
+      const cf sg = f.phk[q] * pk[q];
+      toC += cjm(sg, lB[q]) + sg * lA[q];
+      lB[q] = cjm(f.LB[q], lB[q]);
+      lA[q] = cjm(f.LA[q], lA[q]);
+    });
+    l1 = cjm(f.rho, l1 + kg_sum<KP>(toC));
+  }
+  float* mp = a.mu + ((size_t)b * a.C + c) * a.D;
+  if (l.kg == 0) *reinterpret_cast<float2*>(mp + 2 * l.j) = float2{l1.re, l1.im};
+  static_for<0, KP>([&](auto qc) {
+    constexpr int q = qc;
+    *reinterpret_cast<f4a*>(mp + DIM + 4 * (l.j * K + KP * l.kg + q)) =
+        f4a{0.5f * lA[q].re, 0.5f * lA[q].im, 0.5f * lB[q].re, 0.5f * lB[q].im};
+  });
+}
+
+// B3: full adjoint of a uniform chunk whose steps may be inverted: states S(t-1) by inverting each step from the
+// chunk's float64 end state; cotangents from mt (later chunks) plus the readout rows. Writes the knot gradients
+// of the chunk's interior knots directly (dpath, dclock), dv / dh of its first and last interval (the chunk
+// boundary knots are finished by k_knot_bounds), and the chunk's parameter partials. KP = 2 (32-lane groups).
+template <int KP> struct BwdCoef {
+  cf rho, rhoi, phi, rho1, phi1;        // plane j (rho1, phi1 = d/dh)
+  cf phk[KP], phi1h[KP];                // phi_k / 2, (d phi_k / dh) / 2
+  cf LB[KP], LA[KP], LBi[KP], LAi[KP];  // pair flows and their inverses
+  cf IB[KP], IA[KP], IB1[KP], IA1[KP];  // IB / 2, IA / 2, d/dh of those
+  cf LB1[KP], LA1[KP];                  // d/dh of the flows
+};
+
+template <bool BF16>
+__global__ __launch_bounds__(64) void k_bwd_full(DiagArgs a) {
+  constexpr int KP = 2, G = Geo<KP>::G, GPW = Geo<KP>::GPW;
+  __shared__ __align__(16) float s_v[GPW * VPITCH];
+  __shared__ float s_h[GPW * kMaxT];
+  __shared__ __align__(16) float s_w[GPW][NB * K * K * 2];  // column terms w[t][k][j] (complex)
+  __shared__ __align__(16) float s_dvp[GPW][NB * K * 2];    // plane part of dv[t][j] (complex)
+  __shared__ __align__(16) float s_dhp[GPW][NB * G];        // dh partials [t][lane]
+  __shared__ __align__(16) float s_dvo[GPW][(NB + 1) * DIM];  // dv of the block's steps; row NB: the step after
+  __shared__ float s_dho[GPW][NB + 1];
+  const Lane l = lane_of<KP>(threadIdx.x);
+  const int b = blockIdx.y, cb = blockIdx.x * GPW, c = cb + l.gi;
+  stage<KP, BF16>(a, b, cb, s_v, s_h);
+  __syncthreads();
+  const int ci = b * a.C + (c < a.C ? c : 0);
+  const bool active = c < a.C && (a.cflag[ci] & 3) == 3;
+  const int t0 = c * a.T, Tc = active ? min(a.T, a.n_int - t0) : 0;
+  const float hb = active ? a.chbar[ci] : 0.0f;
+  // coefficients at hbar
+  BwdCoef<KP> f;
+  const cf uj = load_u(a.params, l.j);
+  const cf xj = hb * uj;
+  {
+    const Node1<cf> nj = node1(xj);
+    f.rho = nj.e;
+    f.rhoi = expv(-xj);
+    f.phi = nj.p;
+    f.rho1 = nj.e * uj;
+    f.phi1 = nj.dp * uj;
+  }
+  static_for<0, KP>([&](auto qc) {
+    constexpr int q = qc;
+    const cf uk = load_u(a.params, KP * l.kg + q);
+    const Node1<cf> nk = node1(hb * uk);
+    f.phk[q] = 0.5f * nk.p;
+    f.phi1h[q] = 0.5f * (nk.dp * uk);
+    const cf ub = uj + uk, ua = uj + conj(uk);
+    f.LB[q] = expv(hb * ub);
+    f.LA[q] = expv(hb * ua);
+    f.LBi[q] = expv(-(hb * ub));
+    f.LAi[q] = expv(-(hb * ua));
+    f.LB1[q] = f.LB[q] * ub;
+    f.LA1[q] = f.LA[q] * ua;
+    const DD3<cf> db = dd3<cf, true>(xj, hb * ub);
+    const DD3<cf> da = dd3<cf, true>(xj, hb * ua);
+    f.IB[q] = 0.5f * db.d;
+    f.IA[q] = 0.5f * da.d;
+    f.IB1[q] = 0.5f * (db.dx * uj + db.dy * ub);
+    f.IA1[q] = 0.5f * (da.dx * uj + da.dy * ua);
+  });
+  // end state (float64 carry after the chunk) and cotangent from later chunks
+  cf S1{0.0f, 0.0f}, SA[KP], SB[KP], l1{0.0f, 0.0f}, lA[KP], lB[KP];
+  static_for<0, KP>([&](auto qc) {
+    constexpr int q = qc;
+    SA[q] = SB[q] = lA[q] = lB[q] = cf{0.0f, 0.0f};
+  });
+  if (active) {
+    const double* cr = a.carries + ((size_t)b * (a.C + 1) + c + 1) * a.D;
+    const float* mp = a.mt + ((size_t)b * a.C + c) * a.D;
+    S1 = cf{(float)cr[2 * l.j], (float)cr[2 * l.j + 1]};
+    l1 = cf{mp[2 * l.j], mp[2 * l.j + 1]};
+    static_for<0, KP>([&](auto qc) {
+      constexpr int q = qc;
+      const int e = DIM + 4 * (l.j * K + KP * l.kg + q);
+      SA[q] = cf{(float)(0.5 * cr[e]), (float)(0.5 * cr[e + 1])};
+      SB[q] = cf{(float)(0.5 * cr[e + 2]), (float)(0.5 * cr[e + 3])};
+      const f4a m = *reinterpret_cast<const f4a*>(mp + e);
+      lA[q] = cf{2.0f * m.x, 2.0f * m.y};
+      lB[q] = cf{2.0f * m.z, 2.0f * m.w};
+    });
+  }
+  // parameter-gradient accumulators (sums of h_t times coefficient cotangents)
+  cf kIB[KP], kIA[KP], kLB[KP], kLA[KP], kph[KP], krho{0.0f, 0.0f}, kphj{0.0f, 0.0f};
+  static_for<0, KP>([&](auto qc) {
+    constexpr int q = qc;
+    kIB[q] = kIA[q] = kLB[q] = kLA[q] = kph[q] = cf{0.0f, 0.0f};
+  });
+
+  const float* vg = s_v + l.gi * VPITCH;
+  const float* hg = s_h + l.gi * kMaxT;
+  float* w_g = s_w[l.gi];
+  float* dvp_g = s_dvp[l.gi];
+  float* dhp_g = s_dhp[l.gi];
+  float* dvo_g = s_dvo[l.gi];
+  float* dho_g = s_dho[l.gi];
+  const float* grow = a.gout + ((size_t)b * a.n_int + (active ? t0 : 0)) * a.W;
+  const int o1 = a.off1 + 2 * l.j, o2 = a.off2 + 2 * l.j * DIM + 2 * KP * l.kg;
+  GRow<KP> gn1{}, gn2{};
+  if (Tc >= 1) gn1 = load_g<KP>(grow + (size_t)(Tc - 1) * a.W, o1, o2);
+  if (Tc >= 2) gn2 = load_g<KP>(grow + (size_t)(Tc - 2) * a.W, o1, o2);
+  // blocks of NB steps, last block first; every group runs the same number of blocks (barriers)
+  const int nblk = (a.T + NB - 1) / NB;
+  for (int blk = nblk - 1; blk >= 0; --blk) {
+    const int tb = blk * NB;
+#pragma unroll 1
+    for (int s = NB - 1; s >= 0; --s) {
+      const int t = tb + s;
+      if (t >= Tc) continue;
+      const GRow<KP> g = gn1;
+      gn1 = gn2;
+      if (t >= 2) gn2 = load_g<KP>(grow + (size_t)(t - 2) * a.W, o1, o2);
+      const float h = hg[t];
+      cf pj, pk[KP];
+      load_p<KP>(vg + t * DIM, l, pj, pk);
+      l1 += cf{g.g1.x, g.g1.y};
+      // invert the level-1 step: c_j = rho S1(t-1) = S1(t) - phi_j p_j
+      const cf cj = S1 - f.phi * pj;
+      const cf H1 = f.rhoi * cj;
+      cf toC{0.0f, 0.0f}, toP{0.0f, 0.0f};
+      float dhp = 0.0f;
+      static_for<0, KP>([&](auto qc) {
+        constexpr int q = qc;
+        cf gA, gB;
+        g_pair<KP, q>(g, gA, gB);
+        const cf A = lA[q] + gA, Bc = lB[q] + gB;  // doubled cotangents of SA(t), SB(t)
+        const cf sg = f.phk[q] * pk[q];
+        cf pi, pic;
+        prods(pj, pk[q], pi, pic);
+        const cf XB = SB[q] - cj * sg - f.IB[q] * pi;
+        const cf XA = SA[q] - cj * conj(sg) - f.IA[q] * pic;
+        const cf HB = f.LBi[q] * XB;
+        const cf HA = f.LAi[q] * XA;
+        // row terms (plane j)
+        toC += cjm(sg, Bc) + sg * A;
+        const cf gf = cjm(f.IB[q], Bc);
+        const cf ge = cjm(f.IA[q], A);
+        toP += cjm(pk[q], gf) + pk[q] * ge;
+        // column terms (plane k): dv_k share and the phi_k cotangent share
+        const cf tS = cjm(cj, Bc) + cjm(A, cj);
+        const cf w = cjm(f.phk[q], tS) + cjm(pj, gf) + cjm(ge, pj);
+        *reinterpret_cast<float2*>(w_g + ((s * K + KP * l.kg + q) * K + l.j) * 2) = float2{w.re, w.im};
+        const cf gph = cjm(pk[q], tS);
+        dhp += redot(gph, f.phi1h[q]);
+        kph[q] = fma_c(cf{h, 0.0f}, gph, kph[q]);
+        // coefficient cotangents
+        const cf gIB = cjm(pi, Bc), gIA = cjm(pic, A), gLB = cjm(HB, Bc), gLA = cjm(HA, A);
+        dhp += redot(gIB, f.IB1[q]) + redot(gIA, f.IA1[q]) + redot(gLB, f.LB1[q]) + redot(gLA, f.LA1[q]);
+        kIB[q] = fma_c(cf{h, 0.0f}, gIB, kIB[q]);
+        kIA[q] = fma_c(cf{h, 0.0f}, gIA, kIA[q]);
+        kLB[q] = fma_c(cf{h, 0.0f}, gLB, kLB[q]);
+        kLA[q] = fma_c(cf{h, 0.0f}, gLA, kLA[q]);
+        lB[q] = cjm(f.LB[q], Bc);
+        lA[q] = cjm(f.LA[q], A);
+        SB[q] = HB;
+        SA[q] = HA;
+      });
+      toC = kg_sum<KP>(toC);
+      toP = kg_sum<KP>(toP);
+      const cf gc = l1 + toC;
+      if (l.kg == 0) {
+        const cf dvp = cjm(f.phi, l1) + toP;
+        *reinterpret_cast<float2*>(dvp_g + (s * K + l.j) * 2) = float2{dvp.re, dvp.im};
+        const cf gphL = cjm(pj, l1);
+        const cf grho = cjm(H1, gc);
+        dhp += redot(gphL, f.phi1) + redot(grho, f.rho1);
+        kphj = fma_c(cf{h, 0.0f}, gphL, kphj);
+        krho = fma_c(cf{h, 0.0f}, grho, krho);
+      }
+      dhp_g[s * G + l.gl] = dhp;
+      l1 = cjm(f.rho, gc);
+      S1 = H1;
+    }
+    __syncthreads();
+    // column sums of the block: dv[t][k] = plane part + sum_j w[t][k][j]; dh[t] = sum of the lane partials
+    for (int it = l.gl; it < NB * K; it += G) {
+      const int s = it >> 3, k = it & 7, t = tb + s;
+      if (t < Tc) {
+        const f4a* wp = reinterpret_cast<const f4a*>(w_g + (s * K + k) * K * 2);
+        const f4a acc = wp[0] + wp[1] + wp[2] + wp[3];
+        float2 dv = *reinterpret_cast<const float2*>(dvp_g + (s * K + k) * 2);
+        dv.x += acc.x + acc.z;
+        dv.y += acc.y + acc.w;
+        *reinterpret_cast<float2*>(dvo_g + s * DIM + 2 * k) = dv;
+        if (t == 0 || t == Tc - 1)  // boundary intervals: their knots are finished by k_knot_bounds
+          *reinterpret_cast<float2*>(a.dv + ((size_t)b * a.n_int + t0 + t) * DIM + 2 * k) = dv;
+      }
+    }
+    if (l.gl < NB) {
+      const int s = l.gl, t = tb + s;
+      if (t < Tc) {
+        float acc = 0.0f;
+        for (int q = 0; q < G; q += 4) {
+          const f4a v = *reinterpret_cast<const f4a*>(dhp_g + s * G + q);
+          acc += (v.x + v.y) + (v.z + v.w);
+        }
+        dho_g[s] = acc;
+        if (t == 0 || t == Tc - 1) a.dh[(size_t)b * a.n_int + t0 + t] = acc;
+      }
+    }
+    __syncthreads();
+    // interior knots tb+1 .. tb+NB of the chunk: dX = dv(t-1) - dv(t), dtheta = dh(t-1) - dh(t); row NB of the
+    // block arrays holds the step after the block (the first step of the block processed before)
+    for (int it = l.gl; it < NB * (DIM + 1); it += G) {
+      const int s = 1 + it / (DIM + 1), ch = it % (DIM + 1), t = tb + s;
+      if (t >= 1 && t <= Tc - 1) {
+        if (ch < DIM) {
+          a.dpath[((size_t)b * a.L + t0 + t) * DIM + ch] = dvo_g[(s - 1) * DIM + ch] - dvo_g[s * DIM + ch];
+        } else {
+          a.dclock[(size_t)b * a.L + t0 + t] = dho_g[s - 1] - dho_g[s];
+        }
+      }
+    }
+    __syncthreads();
+    for (int it = l.gl; it < DIM + 1; it += G) {  // keep this block's first step for the next (earlier) block
+      if (it < DIM) dvo_g[NB * DIM + it] = dvo_g[it];
+      else dho_g[NB] = dho_g[0];
+    }
+    __syncthreads();
+  }
+  // parameter partials of the chunk: node cotangents -> (d_j, w_j) per plane. A node h u contributes
+  // (-Re G, Im G) to its plane for u = -conj(z) and (-Re G, -Im G) for u = -z (the conj(u_k) of the A pairs).
+  constexpr int PS = 2 + 2 * KP;  // per-lane floats: row part, then one (d, w) per column pair
+  float* sp = s_w[l.gi];          // reuses the column-sum area
+  if (active) {
+    float rd = 0.0f, rw = 0.0f;
+    cf Gx{0.0f, 0.0f};
+    static_for<0, KP>([&](auto qc) {
+      constexpr int q = qc;
+      const cf uk = load_u(a.params, KP * l.kg + q);
+      const cf ub = uj + uk, ua = uj + conj(uk);
+      const DD3<cf> db = dd3<cf, true>(xj, hb * ub);
+      const DD3<cf> da = dd3<cf, true>(xj, hb * ua);
+      const Node1<cf> nk = node1(hb * uk);
+      Gx += 0.5f * (kIB[q] * conj(db.dx) + kIA[q] * conj(da.dx));
+      const cf GyB = 0.5f * (kIB[q] * conj(db.dy)) + kLB[q] * conj(f.LB[q]);
+      const cf GyA = 0.5f * (kIA[q] * conj(da.dy)) + kLA[q] * conj(f.LA[q]);
+      const cf Gk = 0.5f * (kph[q] * conj(nk.dp));
+      rd += -GyB.re - GyA.re;
+      rw += GyB.im + GyA.im;
+      sp[l.gl * PS + 2 + 2 * q] = -GyB.re - GyA.re - Gk.re;
+      sp[l.gl * PS + 3 + 2 * q] = GyB.im - GyA.im + Gk.im;
+    });
+    if (l.kg == 0) {
+      const Node1<cf> nj = node1(xj);
+      Gx += krho * conj(f.rho) + kphj * conj(nj.dp);
+    }
+    sp[l.gl * PS + 0] = rd - Gx.re;
+    sp[l.gl * PS + 1] = rw + Gx.im;
+  }
+  __syncthreads();
+  if (active && l.gl < K) {
+    const int p = l.gl, pkg = p / KP, pq = p % KP;
+    float sd = 0.0f, sw = 0.0f;
+    for (int kg = 0; kg < Geo<KP>::NKG; ++kg) {
+      sd += sp[(p + 8 * kg) * PS];
+      sw += sp[(p + 8 * kg) * PS + 1];
+    }
+    for (int jj = 0; jj < K; ++jj) {
+      const int src = pkg * 8 + jj;
+      sd += sp[src * PS + 2 + 2 * pq];
+      sw += sp[src * PS + 3 + 2 * pq];
+    }
+    float* gpo = a.gp + ((size_t)b * a.C + c) * a.npar;
+    gpo[2 * p] = sd;
+    gpo[2 * p + 1] = sw;
+  }
+}
+
+}  // namespace pairs
+
+// ------------------------------------------------------------------------------------------------ host side
+bool pairs_eligible(int structure, int depth, int dim, int readout, int flow_mode, int T) {
+  return structure == EWS_STRUCT_PLANES && depth == 2 && dim == pairs::DIM && readout == EWS_READOUT_PREFIX &&
+         flow_mode == EWS_FLOW_PER_INTERVAL && T <= kMaxT && T >= pairs::NB;
+}
+
+int pairs_forward(const DiagArgs& a, hipStream_t st, bool out) {
+  constexpr int GPW = pairs::Geo<4>::GPW;
+  const dim3 grid((a.C + GPW - 1) / GPW, a.B), blk(64);
+  if (out) {
+    if (a.path_bf16) hipLaunchKernelGGL((pairs::k_fwd<true, true>), grid, blk, 0, st, a);
+    else hipLaunchKernelGGL((pairs::k_fwd<true, false>), grid, blk, 0, st, a);
+  } else {
+    if (a.path_bf16) hipLaunchKernelGGL((pairs::k_fwd<false, true>), grid, blk, 0, st, a);
+    else hipLaunchKernelGGL((pairs::k_fwd<false, false>), grid, blk, 0, st, a);
+  }
+  return hipGetLastError() == hipSuccess ? 0 : -1;
+}
+
+int pairs_backward(const DiagArgs& a, hipStream_t st, bool full) {
+  if (full) {
+    constexpr int GPW = pairs::Geo<2>::GPW;
+    const dim3 grid((a.C + GPW - 1) / GPW, a.B), blk(64);
+    if (a.path_bf16) hipLaunchKernelGGL((pairs::k_bwd_full<true>), grid, blk, 0, st, a);
+    else hipLaunchKernelGGL((pairs::k_bwd_full<false>), grid, blk, 0, st, a);
+  } else {
+    constexpr int GPW = pairs::Geo<4>::GPW;
+    const dim3 grid((a.C + GPW - 1) / GPW, a.B), blk(64);
+    if (a.path_bf16) hipLaunchKernelGGL((pairs::k_bwd_local<true>), grid, blk, 0, st, a);
+    else hipLaunchKernelGGL((pairs::k_bwd_local<false>), grid, blk, 0, st, a);
+  }
+  return hipGetLastError() == hipSuccess ? 0 : -1;
+}
+
+}  // namespace ews

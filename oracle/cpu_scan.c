@@ -8,8 +8,12 @@
  *                 form of ews/core/chen_scan.py:124-152 / the lax.scan branch of plane_prefix (:188-196)
  *   flows         per interval, or one shared step (ews/core/chen_scan.py:155-168)
  *   readout       prefix rows with the level-0 constant (ews/core/output_format.py:22-30)
- * Gradients: the adjoint of the block recursion; the scalar coefficients' derivatives in (h, d, w) by central
- * differences in double precision.
+ * Gradients: the adjoint of the block recursion; the scalar coefficients' derivatives in (h, d, w) analytically,
+ * by the chain rule through the nodes x = -h conj(z_j) and delta = -h conj(z_k) (B) or -h z_k (A), with
+ *   dphi/dx = exp[0, x, x],  dD/dx = int_0^1 a^2 phi(delta a) e^{x a} da,  dD/ddelta = int_0^1 a^2 phi'(delta a) e^{x a} da
+ * (D(x, delta) = int_0^1 a phi(delta a) e^{x a} da, the simplex integral with the inner variable done in closed
+ * form), evaluated by 24-point Gauss-Legendre quadrature. No finite differences: a central difference of the
+ * direct divided-difference branch loses ~1e-13 / step to cancellation.
  */
 #include <complex.h>
 #include <math.h>
@@ -43,6 +47,46 @@ static cplx d3phi(cplx x) {
 static cplx divdiff(cplx x, cplx delta) {
   if (cabs(delta) < 4e-4) return dphi(x) + delta * (d2phi(x) / 2 + delta * d3phi(x) / 6);
   return (phi(x + delta) - phi(x)) / delta;
+}
+
+/* 24-point Gauss-Legendre nodes / weights on [0, 1] (computed once by Newton iteration on P_24) */
+#define GL_N 24
+static double gl_x[GL_N], gl_w[GL_N];
+static int gl_ready = 0;
+static void gl_init(void) {
+  if (gl_ready) return;
+  const int n = GL_N;
+  for (int i = 0; i < n; ++i) {
+    double x = cos(M_PI * (i + 0.75) / (n + 0.5)), dp = 0.0;
+    for (int it = 0; it < 100; ++it) {
+      double p0 = 1.0, p1 = x;
+      for (int k = 2; k <= n; ++k) {
+        const double p2 = ((2.0 * k - 1.0) * x * p1 - (k - 1.0) * p0) / k;
+        p0 = p1;
+        p1 = p2;
+      }
+      dp = n * (x * p1 - p0) / (x * x - 1.0);
+      const double dx = p1 / dp;
+      x -= dx;
+      if (fabs(dx) < 1e-16) break;
+    }
+    gl_x[i] = 0.5 * (1.0 - x);
+    gl_w[i] = 1.0 / ((1.0 - x * x) * dp * dp);
+  }
+  gl_ready = 1;
+}
+
+/* partial derivatives of D(x, delta) = int_0^1 a phi(delta a) e^{x a} da */
+static void divdiff_derivs(cplx x, cplx delta, cplx* Dx, cplx* Dd) {
+  cplx sx = 0, sd = 0;
+  for (int i = 0; i < GL_N; ++i) {
+    const double a = gl_x[i];
+    const cplx e = cexp(x * a) * (gl_w[i] * a * a);
+    sx += e * phi(delta * a);
+    sd += e * dphi(delta * a);
+  }
+  *Dx = sx;
+  *Dd = sd;
 }
 
 /* coefficients of one interval for planes j, k: rho_j, phi_j, IA_jk, IB_jk (complex) */
@@ -161,6 +205,7 @@ void cpu_planes_backward(int B, int L, int m, int flow_mode, const REAL* path, c
   double dw[64];
   for (int i = 0; i < 2 * K; ++i) dw[i] = dwr[i];
   double* ddw_all = calloc((size_t)B * 2 * K, sizeof(double));
+  gl_init();
 #pragma omp parallel for schedule(dynamic, 1)
   for (int b = 0; b < B; ++b) {
     const REAL* X = path + (size_t)b * L * m;
@@ -173,7 +218,6 @@ void cpu_planes_backward(int B, int L, int m, int flow_mode, const REAL* path, c
     double* dh = calloc((size_t)(L - 1), sizeof(double));
     double dhf_shared = 0.0;
     double* ddw = ddw_all + (size_t)b * 2 * K;
-    const double eps = 1e-6;
     for (int t = L - 2; t >= 0; --t) {
       const REAL* g = gout + ((size_t)b * (L - 1) + t) * W + 1;
       for (int i = 0; i < D; ++i) lam[i] += (double)g[i];
@@ -252,20 +296,22 @@ void cpu_planes_backward(int B, int L, int m, int flow_mode, const REAL* path, c
           gp[j] += p[k] * ge + conj(p[k]) * gf;
           gp[k] += conj(ge) * p[j] + conj(p[j]) * gf;
           const cplx gIA = conj(e1) * gA, gIB = conj(f1) * gB;
-          /* coefficient derivatives by central differences: d/dh, d/dd_j, d/dw_j, d/dd_k, d/dw_k */
-          const double hs = eps * fmax(fabs(h), 1e-12);
-          const double ps = eps;
+          /* coefficient derivatives: d/dh, d/dd_j, d/dw_j, d/dd_k, d/dw_k through the nodes */
+          const cplx xj = -h * zc(dj, wj), dlB = -h * zc(dk, wk), dlA = -h * (dk + I * wk);
+          cplx DxA, DdA, DxB, DdB;
+          divdiff_derivs(xj, dlA, &DxA, &DdA);
+          divdiff_derivs(xj, dlB, &DxB, &DdB);
           cplx dA[5], dB[5];
-          dA[0] = (c_IA(h + hs, dj, wj, dk, wk) - c_IA(h - hs, dj, wj, dk, wk)) / (2 * hs);
-          dB[0] = (c_IB(h + hs, dj, wj, dk, wk) - c_IB(h - hs, dj, wj, dk, wk)) / (2 * hs);
-          dA[1] = (c_IA(h, dj + ps, wj, dk, wk) - c_IA(h, dj - ps, wj, dk, wk)) / (2 * ps);
-          dB[1] = (c_IB(h, dj + ps, wj, dk, wk) - c_IB(h, dj - ps, wj, dk, wk)) / (2 * ps);
-          dA[2] = (c_IA(h, dj, wj + ps, dk, wk) - c_IA(h, dj, wj - ps, dk, wk)) / (2 * ps);
-          dB[2] = (c_IB(h, dj, wj + ps, dk, wk) - c_IB(h, dj, wj - ps, dk, wk)) / (2 * ps);
-          dA[3] = (c_IA(h, dj, wj, dk + ps, wk) - c_IA(h, dj, wj, dk - ps, wk)) / (2 * ps);
-          dB[3] = (c_IB(h, dj, wj, dk + ps, wk) - c_IB(h, dj, wj, dk - ps, wk)) / (2 * ps);
-          dA[4] = (c_IA(h, dj, wj, dk, wk + ps) - c_IA(h, dj, wj, dk, wk - ps)) / (2 * ps);
-          dB[4] = (c_IB(h, dj, wj, dk, wk + ps) - c_IB(h, dj, wj, dk, wk - ps)) / (2 * ps);
+          dA[0] = DxA * (-zc(dj, wj)) + DdA * (-(dk + I * wk));
+          dB[0] = DxB * (-zc(dj, wj)) + DdB * (-zc(dk, wk));
+          dA[1] = -h * DxA;
+          dB[1] = -h * DxB;
+          dA[2] = I * h * DxA;
+          dB[2] = I * h * DxB;
+          dA[3] = -h * DdA;
+          dB[3] = -h * DdB;
+          dA[4] = -I * h * DdA;
+          dB[4] = I * h * DdB;
           dh[t] += creal(conj(gIA) * dA[0] + conj(gIB) * dB[0]);
           ddw[2 * j] += creal(conj(gIA) * dA[1] + conj(gIB) * dB[1]);
           ddw[2 * j + 1] += creal(conj(gIA) * dA[2] + conj(gIB) * dB[2]);
@@ -285,13 +331,10 @@ void cpu_planes_backward(int B, int L, int m, int flow_mode, const REAL* path, c
         /* R from rho = a + ib: R = [[a, -b], [b, a]] */
         const cplx grho = (gR[j][0] + gR[j][3]) + I * (gR[j][2] - gR[j][1]);
         const double dj = dw[2 * j], wj = dw[2 * j + 1];
-        const double hs = eps * fmax(fabs(h), 1e-12), hfs = eps * fmax(fabs(hf), 1e-12), ps = eps;
-        const cplx dph_h = (c_phi(h + hs, dj, wj) - c_phi(h - hs, dj, wj)) / (2 * hs);
-        const cplx dph_d = (c_phi(h, dj + ps, wj) - c_phi(h, dj - ps, wj)) / (2 * ps);
-        const cplx dph_w = (c_phi(h, dj, wj + ps) - c_phi(h, dj, wj - ps)) / (2 * ps);
-        const cplx dr_h = (c_rho(hf + hfs, dj, wj) - c_rho(hf - hfs, dj, wj)) / (2 * hfs);
-        const cplx dr_d = (c_rho(hf, dj + ps, wj) - c_rho(hf, dj - ps, wj)) / (2 * ps);
-        const cplx dr_w = (c_rho(hf, dj, wj + ps) - c_rho(hf, dj, wj - ps)) / (2 * ps);
+        const cplx xj = -h * zc(dj, wj), xf = -hf * zc(dj, wj);
+        const cplx dphx = dphi(xj), erx = cexp(xf);
+        const cplx dph_h = dphx * (-zc(dj, wj)), dph_d = -h * dphx, dph_w = I * h * dphx;
+        const cplx dr_h = erx * (-zc(dj, wj)), dr_d = -hf * erx, dr_w = I * hf * erx;
         dh[t] += creal(conj(gph) * dph_h);
         if (flow_mode == 0) dh[t] += creal(conj(grho) * dr_h);
         else dhf_shared += creal(conj(grho) * dr_h);

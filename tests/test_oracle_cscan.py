@@ -48,4 +48,26 @@ def test_c_scan_matches_torch_oracle(mode, flow):
     dp, dc, dd = C.planes_backward(path, clock, dw, g, flow)
     for a, b in ((dp, pt.grad), (dc, ct.grad), (dd, wt.grad)):
         b = b.numpy()
-        assert np.abs(a - b).max() <= 1e-7 * max(1.0, np.abs(b).max())
+        assert np.abs(a - b).max() <= 1e-10 * max(1.0, np.abs(b).max())
+
+
+def test_c_scan_gradients_at_bench_shape():
+    """d = 16 planes, float32-uniform clock (the bench's c2 shape at L = 400): the checker's coefficient derivatives
+    are analytic, so its clock gradient (a difference of adjacent step gradients) stays exact to ~1e-11."""
+    rng = np.random.default_rng(11)
+    B, L = 1, 400
+    path = np.cumsum(rng.normal(0.0, np.sqrt(1.0 / L), size=(B, L, 16)), 1)
+    clock = np.broadcast_to((np.arange(L) / L).astype(np.float32).astype(np.float64), (B, L)).copy()
+    dw = np.stack([rng.uniform(0.01, 1.0, 8), rng.uniform(0.0, np.pi, 8)], -1)
+    pt = torch.tensor(path, requires_grad=True)
+    ct = torch.tensor(clock, requires_grad=True)
+    wt = torch.tensor(dw, requires_grad=True)
+    ref = O.ews(pt, ct, _dense(wt), 2, "prefix", leaf="plane_closed")
+    np.testing.assert_allclose(C.planes_forward(path, clock, dw), ref.detach().numpy(), rtol=0,
+                               atol=1e-10 * float(ref.abs().max()))
+    g = np.random.default_rng(5).normal(size=tuple(ref.shape))
+    (ref * torch.tensor(g)).sum().backward()
+    dp, dc, dd = C.planes_backward(path, clock, dw, g)
+    for a, b in ((dp, pt.grad), (dc, ct.grad), (dd, wt.grad)):
+        b = b.numpy()
+        assert np.abs(a - b).max() <= 1e-10 * np.abs(b).max()
