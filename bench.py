@@ -107,6 +107,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--check", action="store_true", help="also check one forward against the C float64 checker")
+    ap.add_argument("--chunk", type=int, default=0, help="intervals per chunk (0: the library's default)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: --gpus {args.gpus} is not supported (the EWS scan here is single-GPU; "
@@ -131,7 +132,8 @@ def main():
     clock = torch.tensor(clock_np, device=dev)
     dw = torch.tensor(dw_np, device=dev)
     gout = torch.tensor(g_np, device=dev)
-    desc = make_desc(B, L, d, N, nat.STRUCT_PLANES, nat.FLOW_PER_INTERVAL, "prefix", True, nat.DTYPE_F32)
+    desc = make_desc(B, L, d, N, nat.STRUCT_PLANES, nat.FLOW_PER_INTERVAL, "prefix", True, nat.DTYPE_F32,
+                     args.chunk)
     ws = torch.empty(int(lib.ews_diag_workspace_bytes(ctypes.byref(desc))), device=dev, dtype=torch.uint8)
     resid = torch.empty(int(lib.ews_diag_residual_bytes(ctypes.byref(desc))), device=dev, dtype=torch.uint8)
     out = torch.empty((B, L - 1, W), device=dev, dtype=torch.float32)

@@ -32,6 +32,7 @@ struct DiagArgs {
   float* dh;        // (B, n_int)
   float* gp;        // (B, C, npar)
   float* gph;       // (B, C)
+  double* gpart;    // (kParamBlocks, npar) partial parameter sums
   double* gagg;     // (B, NG, D) group aggregates (forward) / group cotangent aggregates (backward)
   double* gcar;     // (B, NG, D) state before each group (forward) / cotangent after each group (backward)
   int NG;           // chunk groups of scan_cb chunks
@@ -39,7 +40,14 @@ struct DiagArgs {
   // bit 1 = the steps may be inverted backwards; and the chunk's mean clock step
   int* cflag;       // (B, C)
   float* chbar;     // (B, C)
+  float* ctab;      // pair-group coefficient table at one reference step (residual)
   int fast_ok;      // 1 if this configuration has pair-group kernels (flags are valid), else 0
+  // quad carry scan of the pair-group path (quads of four chunks)
+  int NQ;           // quads per sample
+  float* qagg;      // (B, NQ, D) quad summaries (forward) / quad adjoint aggregates (backward)
+  double* qflow;    // (B, NQ, K, 2) quad flows exp(u tau_quad)
+  double* ql1;      // (B, NQ, K, 2) level-1 increments of the quads (backward)
+  double* cflow;    // (B, C, K, 2) chunk flows exp(u tau_chunk)
   // backward outputs
   float* dpath;
   float* dclock;

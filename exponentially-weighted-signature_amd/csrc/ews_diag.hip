@@ -1595,20 +1595,56 @@ __global__ void k_knot_grads(DiagArgs a) {
   }
 }
 
-// One block per parameter: fixed-order strided partial sums, then a fixed-shape tree (deterministic).
-__global__ void k_param_grads(DiagArgs a) {
+// Parameter gradients in two fixed-order stages (deterministic): kParamBlocks workgroups each sum a contiguous
+// range of the (B C, npar) partials in float64 (thread (r, p) takes rows r, r + R, ...: coalesced), then one
+// workgroup adds the block sums in order.
+constexpr int kParamBlocks = 128;
+__global__ __launch_bounds__(256) void k_param_partial(DiagArgs a) {
   __shared__ double red[256];
-  const int p = blockIdx.x;
-  const int n = a.B * a.C;
+  const int np = a.npar, R = 256 / np;
+  const int r = threadIdx.x / np, p = threadIdx.x % np;
+  const int n = a.B * a.C, per = (n + kParamBlocks - 1) / kParamBlocks;
+  const int r0 = blockIdx.x * per, r1 = min(n, r0 + per);
   double s = 0.0;
-  for (int bc = threadIdx.x; bc < n; bc += blockDim.x) s += (double)a.gp[(size_t)bc * a.npar + p];
+  if (r < R) {
+    int bc = r0 + r;
+    for (; bc + 3 * R < r1; bc += 4 * R) {
+      const float g0 = a.gp[(size_t)bc * np + p], g1 = a.gp[(size_t)(bc + R) * np + p];
+      const float g2 = a.gp[(size_t)(bc + 2 * R) * np + p], g3 = a.gp[(size_t)(bc + 3 * R) * np + p];
+      s += ((double)g0 + (double)g1) + ((double)g2 + (double)g3);
+    }
+    for (; bc < r1; bc += R) s += (double)a.gp[(size_t)bc * np + p];
+  }
   red[threadIdx.x] = s;
   __syncthreads();
-  for (int o = blockDim.x / 2; o > 0; o >>= 1) {
-    if ((int)threadIdx.x < o) red[threadIdx.x] += red[threadIdx.x + o];
-    __syncthreads();
+  if (threadIdx.x < np) {
+    double t = 0.0;
+    for (int rr = 0; rr < R; ++rr) t += red[rr * np + threadIdx.x];
+    a.gpart[(size_t)blockIdx.x * np + threadIdx.x] = t;
   }
-  if (threadIdx.x == 0) a.dparams[p] = (float)red[0];
+}
+__global__ __launch_bounds__(256) void k_param_grads(DiagArgs a) {
+  __shared__ double red[256];
+  const int np = a.npar, R = 256 / np;
+  const int r = threadIdx.x / np, p = threadIdx.x % np;
+  double s = 0.0;
+  if (r < R) {
+    double v[kParamBlocks / 16];
+#pragma unroll
+    for (int u = 0; u < kParamBlocks / 16; ++u) {  // loads issued together (R >= 16 for npar <= 16)
+      const int w = r + u * R;
+      v[u] = w < kParamBlocks ? a.gpart[(size_t)w * np + p] : 0.0;
+    }
+    for (int u = 0; u < kParamBlocks / 16; ++u) s += v[u];
+    for (int w = r + (kParamBlocks / 16) * R; w < kParamBlocks; w += R) s += a.gpart[(size_t)w * np + p];
+  }
+  red[threadIdx.x] = s;
+  __syncthreads();
+  if (threadIdx.x < np) {
+    double t = 0.0;
+    for (int rr = 0; rr < R; ++rr) t += red[rr * np + threadIdx.x];
+    a.dparams[threadIdx.x] = (float)t;
+  }
 }
 
 }  // namespace ews
@@ -1684,7 +1720,7 @@ int make_plan(const ews_diag_desc* s, Plan& p) {
 }
 
 struct WsLayout {
-  size_t summ, mu, mt, red, red_idx, dv, dh, gp, gph, gagg, gcar, total;
+  size_t summ, mu, mt, red, red_idx, dv, dh, gp, gph, gpart, gagg, gcar, qagg, qflow, ql1, cflow, total;
 };
 WsLayout ws_layout(const Plan& p) {
   WsLayout w;
@@ -1699,15 +1735,23 @@ WsLayout ws_layout(const Plan& p) {
   w.dh = off; off += align256((size_t)p.B * p.n_int * 4);
   w.gp = off; off += align256(BC * p.npar * 4);
   w.gph = off; off += align256(BC * 4);
+  w.gpart = off; off += align256((size_t)kParamBlocks * p.npar * 8);
   w.gagg = off; off += align256((size_t)p.B * p.NG * p.D * 8);
   w.gcar = off; off += align256((size_t)p.B * p.NG * p.D * 8);
+  const size_t NQ = (p.C + 3) / 4;
+  w.qagg = off; off += p.fast ? align256((size_t)p.B * NQ * p.D * 4) : 0;
+  w.qflow = off; off += p.fast ? align256((size_t)p.B * NQ * p.K * 16) : 0;
+  w.ql1 = off; off += p.fast ? align256((size_t)p.B * NQ * p.K * 16) : 0;
+  w.cflow = off; off += p.fast ? align256(BC * p.K * 16) : 0;
   w.total = off;
   return w;
 }
 size_t resid_carries_bytes(const Plan& p) { return align256((size_t)p.B * (p.C + 1) * p.D * 8); }
 size_t resid_argmax_bytes(const Plan& p) { return align256((size_t)p.B * p.W * 4); }
 size_t resid_chunk_bytes(const Plan& p) { return align256((size_t)p.B * p.C * 4); }
-size_t resid_bytes(const Plan& p) { return resid_carries_bytes(p) + resid_argmax_bytes(p) + 2 * resid_chunk_bytes(p); }
+size_t resid_bytes(const Plan& p) {
+  return resid_carries_bytes(p) + resid_argmax_bytes(p) + 2 * resid_chunk_bytes(p) + align256(kCoefTabFloats * 4);
+}
 
 DiagArgs make_args(const ews_diag_desc* s, const Plan& p, const void* path, const float* clock,
                    const float* params, void* residual, void* workspace) {
@@ -1722,14 +1766,18 @@ DiagArgs make_args(const ews_diag_desc* s, const Plan& p, const void* path, cons
   a.argmax = (int*)(r + resid_carries_bytes(p));
   a.cflag = (int*)(r + resid_carries_bytes(p) + resid_argmax_bytes(p));
   a.chbar = (float*)(r + resid_carries_bytes(p) + resid_argmax_bytes(p) + resid_chunk_bytes(p));
+  a.ctab = (float*)(r + resid_carries_bytes(p) + resid_argmax_bytes(p) + 2 * resid_chunk_bytes(p));
   a.fast_ok = p.fast ? 1 : 0;
   const WsLayout w = ws_layout(p);
   char* ws = (char*)workspace;
   a.summ = (float*)(ws + w.summ); a.mu = (float*)(ws + w.mu); a.mt = (float*)(ws + w.mt);
   a.red = (float*)(ws + w.red); a.red_idx = (int*)(ws + w.red_idx);
   a.dv = (float*)(ws + w.dv); a.dh = (float*)(ws + w.dh);
-  a.gp = (float*)(ws + w.gp); a.gph = (float*)(ws + w.gph);
+  a.gp = (float*)(ws + w.gp); a.gph = (float*)(ws + w.gph); a.gpart = (double*)(ws + w.gpart);
   a.gagg = (double*)(ws + w.gagg); a.gcar = (double*)(ws + w.gcar); a.NG = p.NG;
+  a.NQ = (p.C + 3) / 4;
+  a.qagg = (float*)(ws + w.qagg); a.qflow = (double*)(ws + w.qflow); a.ql1 = (double*)(ws + w.ql1);
+  a.cflow = (double*)(ws + w.cflow);
   return a;
 }
 
@@ -1755,6 +1803,10 @@ int forward_pass(const ews_diag_desc* s, const Plan& p, DiagArgs a, hipStream_t 
       hipLaunchKernelGGL((k_chunk_fwd<CPLX, N, MODE_SUMMARY, MAXT, false>), grid, blk, fwd_lds(p), st, a);
       break;
     case 1:
+      if (p.fast) {
+        if (pairs_carry_scan(a, st, false) != 0) return EWS_ERR_LAUNCH;
+        break;
+      }
       hipLaunchKernelGGL((k_fwd_group<CPLX, N, MAXT, false>), dim3(p.NG, p.B), blk, p.lds_carry, st, a);
       EWS_LAUNCH_CHECK();
       hipLaunchKernelGGL((k_fwd_group_scan<CPLX, N, MAXT>), dim3(p.B), blk, 0, st, a);
@@ -1813,6 +1865,10 @@ int backward_pass(const Plan& p, DiagArgs a, hipStream_t st, int pass) {
       hipLaunchKernelGGL((k_chunk_bwd_local<CPLX, N, MAXT, WAVE, false>), grid, blkb, p.lds_bwd_local, st, a);
       break;
     case 1:
+      if (p.fast) {
+        if (pairs_carry_scan(a, st, true) != 0) return EWS_ERR_LAUNCH;
+        break;
+      }
       hipLaunchKernelGGL((k_bwd_group<CPLX, N, (MAXT < 256 ? 256 : MAXT), false>), dim3(p.NG, p.B), dim3(p.NT),
                          p.lds_adjoint, st, a);
       EWS_LAUNCH_CHECK();
@@ -1833,7 +1889,9 @@ int backward_pass(const Plan& p, DiagArgs a, hipStream_t st, int pass) {
       hipLaunchKernelGGL(k_knot_grads, dim3(p.C + 1, p.B), dim3(64), 0, st, a);
       break;
     case 4:
-      hipLaunchKernelGGL(k_param_grads, dim3(p.npar), dim3(256), 0, st, a);
+      hipLaunchKernelGGL(k_param_partial, dim3(kParamBlocks), dim3(256), 0, st, a);
+      EWS_LAUNCH_CHECK();
+      hipLaunchKernelGGL(k_param_grads, dim3(1), dim3(256), 0, st, a);
       break;
     default:
       return EWS_ERR_OPTION;

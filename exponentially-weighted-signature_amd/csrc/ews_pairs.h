@@ -8,13 +8,19 @@
 namespace ews {
 
 constexpr int kMaxT = 64;  // longest chunk the pair-group kernels stage
+// coefficient table of the pair-group kernels: header (16 floats), 9 complex per plane, 16 complex per pair
+constexpr int kCoefTabFloats = 16 + 2 * 9 * 8 + 2 * 16 * 64;
 
 // True if the configuration has pair-group kernels (rotation planes, d = 16, depth 2, prefix readout,
 // per-interval flows, chunk length <= kMaxT).
 bool pairs_eligible(int structure, int depth, int dim, int readout, int flow_mode, int T);
-// Uniform chunks of the forward: summaries (out = false; this launch also writes every chunk's classification
-// a.cflag / a.chbar, so it runs before any other kernel of the call) or prefix rows (out = true).
+// Uniform chunks of the forward: summaries (out = false; this launch first builds the coefficient table a.ctab
+// and then writes every chunk's classification a.cflag / a.chbar, so it runs before any other kernel of the
+// call) or prefix rows (out = true).
 int pairs_forward(const DiagArgs& a, hipStream_t st, bool out);
+// Float64 carry scan over quads of four chunks: forward carries (backward = false) or the adjoint carries
+// (backward = true); the pair-group prefix / full-adjoint kernels rebuild the carries inside each quad.
+int pairs_carry_scan(const DiagArgs& a, hipStream_t st, bool backward);
 // Uniform chunks of the backward: chunk-local adjoints (full = false) or the full adjoint (full = true).
 int pairs_backward(const DiagArgs& a, hipStream_t st, bool full);
 

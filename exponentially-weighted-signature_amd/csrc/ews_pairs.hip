@@ -98,34 +98,74 @@ __device__ __forceinline__ cf load_u(const float* params, int j) { return cf{-pa
 // s_v[gi * VPITCH + 16 t]; clock steps into s_h[gi * kMaxT + t] when s_h is given.
 template <int KP, bool BF16>
 __device__ __forceinline__ void stage(const DiagArgs& a, int b, int cb, float* s_v, float* s_h) {
-  constexpr int GPW = Geo<KP>::GPW;
+  constexpr int GPW = Geo<KP>::GPW, U = 8;  // U loads per operand in flight per thread before any LDS write
   const int i0 = cb * a.T;
   const int n = min(GPW * a.T, a.n_int - i0);
   const int tid = threadIdx.x;
   if constexpr (!BF16) {
     const float* src = reinterpret_cast<const float*>(a.path) + ((size_t)b * a.L + i0) * DIM;
-    for (int q = tid; q < n * 4; q += 64) {
-      const int i = q >> 2, c4 = q & 3;
-      const int gi = i / a.T, t = i - gi * a.T;
-      const f4a x0 = *reinterpret_cast<const f4a*>(src + (size_t)i * DIM + 4 * c4);
-      const f4a x1 = *reinterpret_cast<const f4a*>(src + (size_t)(i + 1) * DIM + 4 * c4);
-      *reinterpret_cast<f4a*>(s_v + gi * VPITCH + t * DIM + 4 * c4) = x1 - x0;
+    for (int qb = tid; qb < n * 4; qb += U * 64) {
+      f4a x0[U], x1[U];
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const int q = qb + u * 64, i = q >> 2, c4 = q & 3;
+        if (q < n * 4) {
+          x0[u] = *reinterpret_cast<const f4a*>(src + (size_t)i * DIM + 4 * c4);
+          x1[u] = *reinterpret_cast<const f4a*>(src + (size_t)(i + 1) * DIM + 4 * c4);
+        }
+      }
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const int q = qb + u * 64, i = q >> 2, c4 = q & 3;
+        if (q < n * 4) {
+          const int gi = i / a.T, t = i - gi * a.T;
+          *reinterpret_cast<f4a*>(s_v + gi * VPITCH + t * DIM + 4 * c4) = x1[u] - x0[u];
+        }
+      }
     }
   } else {
     const unsigned short* src = reinterpret_cast<const unsigned short*>(a.path) + ((size_t)b * a.L + i0) * DIM;
-    for (int q = tid; q < n * DIM; q += 64) {
-      const int i = q / DIM, ch = q - i * DIM;
-      const int gi = i / a.T, t = i - gi * a.T;
-      const float x0 = __uint_as_float(((unsigned)src[(size_t)i * DIM + ch]) << 16);
-      const float x1 = __uint_as_float(((unsigned)src[(size_t)(i + 1) * DIM + ch]) << 16);
-      s_v[gi * VPITCH + t * DIM + ch] = x1 - x0;
+    for (int qb = tid; qb < n * DIM; qb += U * 64) {
+      unsigned short x0[U], x1[U];
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const int q = qb + u * 64, i = q / DIM, ch = q - i * DIM;
+        if (q < n * DIM) {
+          x0[u] = src[(size_t)i * DIM + ch];
+          x1[u] = src[(size_t)(i + 1) * DIM + ch];
+        }
+      }
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const int q = qb + u * 64, i = q / DIM, ch = q - i * DIM;
+        if (q < n * DIM) {
+          const int gi = i / a.T, t = i - gi * a.T;
+          s_v[gi * VPITCH + t * DIM + ch] =
+              __uint_as_float(((unsigned)x1[u]) << 16) - __uint_as_float(((unsigned)x0[u]) << 16);
+        }
+      }
     }
   }
   if (s_h) {
     const float* th = a.clock + (size_t)b * a.L + i0;
-    for (int i = tid; i < n; i += 64) {
-      const int gi = i / a.T, t = i - gi * a.T;
-      s_h[gi * kMaxT + t] = th[i + 1] - th[i];
+    for (int ib = tid; ib < n; ib += 4 * 64) {
+      float y0[4], y1[4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const int i = ib + u * 64;
+        if (i < n) {
+          y0[u] = th[i];
+          y1[u] = th[i + 1];
+        }
+      }
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const int i = ib + u * 64;
+        if (i < n) {
+          const int gi = i / a.T, t = i - gi * a.T;
+          s_h[gi * kMaxT + t] = y1[u] - y0[u];
+        }
+      }
     }
   }
 }
@@ -142,12 +182,112 @@ template <int KP> __device__ __forceinline__ void load_p(const float* vr, const 
   });
 }
 
+// Level-2 part of a readout row (d^2 = 256 floats from off2) moved between HBM and the lane slices through a
+// per-group LDS buffer of 256 floats, so that every global access instruction of a group covers a contiguous run
+// (G lanes x 16 bytes) instead of scattered 16-byte pieces: lane gl moves pieces gl, gl + G, ... of the row.
+// The lane slice of (j, kg) is row 2j (buffer [32 j, 32 j + 16)) and row 2j + 1 ([32 j + 16, 32 j + 32)),
+// columns 2 KP kg .. 2 KP kg + 2 KP - 1. LDS operations of one wavefront execute in program order, so a
+// compiler barrier between the write and the read of another lane's data is enough.
+template <int KP> struct Pieces {
+  static constexpr int NP = 64 / Geo<KP>::G;  // 16-byte pieces per lane
+  f4u v[NP];
+};
+template <int KP> __device__ __forceinline__ Pieces<KP> load_pieces(const float* row2, int gl) {
+  Pieces<KP> pc;
+  static_for<0, Pieces<KP>::NP>([&](auto ic) {
+    constexpr int i = ic;
+    pc.v[i] = *reinterpret_cast<const f4u*>(row2 + 4 * (gl + Geo<KP>::G * i));
+  });
+  return pc;
+}
+template <int KP> __device__ __forceinline__ void pieces_to_lds(const Pieces<KP>& pc, float* buf, int gl) {
+  static_for<0, Pieces<KP>::NP>([&](auto ic) {
+    constexpr int i = ic;
+    *reinterpret_cast<f4a*>(buf + 4 * (gl + Geo<KP>::G * i)) = f4a{pc.v[i].x, pc.v[i].y, pc.v[i].z, pc.v[i].w};
+  });
+}
+__device__ __forceinline__ void wave_order() { __builtin_amdgcn_wave_barrier(); }
+
 // products p_j p_k and p_j conj(p_k)
 __device__ __forceinline__ void prods(cf pj, cf pk, cf& pi, cf& pic) {
   const float aa = pj.re * pk.re, bb = pj.im * pk.im, cc = pj.re * pk.im, dd = pj.im * pk.re;
   pi = cf{aa - bb, cc + dd};
   pic = cf{aa + bb, dd - cc};
 }
+
+// ------------------------------------------------------------------------------------------------ coefficient table
+// Every coefficient at one reference step h0 (the mean step of chunk 0 of sample 0): chunks whose mean step hbar
+// is within 2^-22 / max|u| of h0 (every chunk of a uniform clock) take the table instead of evaluating the
+// divided differences themselves. Flows are corrected to first order, c(hbar) = c(h0) + c'(h0) (hbar - h0)
+// (their errors compound over the chunk's steps; the second-order remainder is below 2^-44); every other
+// coefficient is used at h0 (relative error <= 2^-22).
+// Layout (complex floats after a 16-float header holding h0): per plane p, entry e at 16 + 2 (9 p + e);
+// per pair 8 j + k, entry e at 16 + 2 * 72 + 2 (16 (8 j + k) + e).
+enum { TP_RHO, TP_RHO1, TP_RHOI, TP_RHOI1, TP_PHI, TP_PHI1, TP_DPHI, TP_PHIH, TP_PHI1H };
+enum { TQ_LB, TQ_LB1, TQ_LA, TQ_LA1, TQ_LBI, TQ_LBI1, TQ_LAI, TQ_LAI1, TQ_IB, TQ_IA, TQ_IB1, TQ_IA1, TQ_DXB, TQ_DYB,
+       TQ_DXA, TQ_DYA };
+__device__ __forceinline__ cf tp(const float* tab, int p, int e) {
+  const float2 v = *reinterpret_cast<const float2*>(tab + 16 + 2 * (9 * p + e));
+  return cf{v.x, v.y};
+}
+__device__ __forceinline__ cf tq(const float* tab, int j, int k, int e) {
+  const float2 v = *reinterpret_cast<const float2*>(tab + 16 + 2 * 72 + 2 * (16 * (8 * j + k) + e));
+  return cf{v.x, v.y};
+}
+__device__ __forceinline__ void stp(float* tab, int p, int e, cf v) {
+  *reinterpret_cast<float2*>(tab + 16 + 2 * (9 * p + e)) = float2{v.re, v.im};
+}
+__device__ __forceinline__ void stq(float* tab, int j, int k, int e, cf v) {
+  *reinterpret_cast<float2*>(tab + 16 + 2 * 72 + 2 * (16 * (8 * j + k) + e)) = float2{v.re, v.im};
+}
+// reference step: the mean step of chunk 0 of sample 0, in the classification's arithmetic
+__device__ __forceinline__ float ref_step(const DiagArgs& a) {
+  const int Tc = min(a.T, a.n_int);
+  return (a.clock[Tc] - a.clock[0]) / (float)Tc;
+}
+__global__ __launch_bounds__(64) void k_coef_table(DiagArgs a) {
+  const int j = threadIdx.x >> 3, k = threadIdx.x & 7;
+  float* tab = a.ctab;
+  const float h0 = ref_step(a);
+  if (threadIdx.x == 0) tab[0] = h0;
+  const cf uj = load_u(a.params, j), uk = load_u(a.params, k);
+  const cf xj = h0 * uj;
+  if (k == 0) {
+    const Node1<cf> nj = node1(xj);
+    const cf ri = expv(-xj);
+    stp(tab, j, TP_RHO, nj.e);
+    stp(tab, j, TP_RHO1, nj.e * uj);
+    stp(tab, j, TP_RHOI, ri);
+    stp(tab, j, TP_RHOI1, -(ri * uj));
+    stp(tab, j, TP_PHI, nj.p);
+    stp(tab, j, TP_PHI1, nj.dp * uj);
+    stp(tab, j, TP_DPHI, nj.dp);
+    stp(tab, j, TP_PHIH, 0.5f * nj.p);
+    stp(tab, j, TP_PHI1H, 0.5f * (nj.dp * uj));
+  }
+  const cf ub = uj + uk, ua = uj + conj(uk);
+  const cf LB = expv(h0 * ub), LA = expv(h0 * ua), LBi = expv(-(h0 * ub)), LAi = expv(-(h0 * ua));
+  stq(tab, j, k, TQ_LB, LB);
+  stq(tab, j, k, TQ_LB1, LB * ub);
+  stq(tab, j, k, TQ_LA, LA);
+  stq(tab, j, k, TQ_LA1, LA * ua);
+  stq(tab, j, k, TQ_LBI, LBi);
+  stq(tab, j, k, TQ_LBI1, -(LBi * ub));
+  stq(tab, j, k, TQ_LAI, LAi);
+  stq(tab, j, k, TQ_LAI1, -(LAi * ua));
+  const DD3<cf> db = dd3<cf, true>(xj, h0 * ub);
+  const DD3<cf> da = dd3<cf, true>(xj, h0 * ua);
+  stq(tab, j, k, TQ_IB, 0.5f * db.d);
+  stq(tab, j, k, TQ_IA, 0.5f * da.d);
+  stq(tab, j, k, TQ_IB1, 0.5f * (db.dx * uj + db.dy * ub));
+  stq(tab, j, k, TQ_IA1, 0.5f * (da.dx * uj + da.dy * ua));
+  stq(tab, j, k, TQ_DXB, db.dx);
+  stq(tab, j, k, TQ_DYB, db.dy);
+  stq(tab, j, k, TQ_DXA, da.dx);
+  stq(tab, j, k, TQ_DYA, da.dy);
+}
+// first-order flow from the table: c(h0) + c'(h0) dlt
+__device__ __forceinline__ cf tflow(cf c0, cf c1, float dlt) { return cf{fmaf(c1.re, dlt, c0.re), fmaf(c1.im, dlt, c0.im)}; }
 
 // Forward coefficients of the lane at the chunk's mean step.
 template <int KP> struct FwdCoef {
@@ -157,7 +297,23 @@ template <int KP> struct FwdCoef {
   cf IB[KP], IA[KP];      // IB / 2, IA / 2
 };
 template <int KP>
-__device__ __forceinline__ void fwd_coef(const DiagArgs& a, const Lane& l, float hb, FwdCoef<KP>& f) {
+__device__ __forceinline__ void fwd_coef(const DiagArgs& a, const Lane& l, float hb, bool use_tab, FwdCoef<KP>& f) {
+  if (use_tab) {
+    const float* tab = a.ctab;
+    const float dlt = hb - tab[0];
+    f.rho = tflow(tp(tab, l.j, TP_RHO), tp(tab, l.j, TP_RHO1), dlt);
+    f.phi = tp(tab, l.j, TP_PHI);
+    static_for<0, KP>([&](auto qc) {
+      constexpr int q = qc;
+      const int k = KP * l.kg + q;
+      f.phk[q] = tp(tab, k, TP_PHIH);
+      f.LB[q] = tflow(tq(tab, l.j, k, TQ_LB), tq(tab, l.j, k, TQ_LB1), dlt);
+      f.LA[q] = tflow(tq(tab, l.j, k, TQ_LA), tq(tab, l.j, k, TQ_LA1), dlt);
+      f.IB[q] = tq(tab, l.j, k, TQ_IB);
+      f.IA[q] = tq(tab, l.j, k, TQ_IA);
+    });
+    return;
+  }
   const cf uj = load_u(a.params, l.j);
   const cf xj = hb * uj;
   const Node1<cf> nj = node1(xj);
@@ -213,7 +369,239 @@ __device__ __forceinline__ int classify_chunk(const DiagArgs& a, int b, int c, i
   const float lim = 4.76837158e-7f;  // 2^-21
   const bool uni = fin && R * dev <= lim && R * drift <= lim;
   const bool inv = fin && 2.0f * Dm * fabsf(tau) <= 0.69314718f;
-  return (uni ? 1 : 0) | (inv ? 2 : 0);
+  const bool tab = uni && R * fabsf(hb - a.ctab[0]) <= 0.5f * lim;  // the coefficient table applies
+  return (uni ? 1 : 0) | (inv ? 2 : 0) | (tab ? 4 : 0);
+}
+
+// ------------------------------------------------------------------------------------------------ carries
+// Float64 Chen combine of the chunk summaries in quads of four chunks (the chunks of one forward workgroup):
+// every quad's summary in parallel (k_quad_fwd_agg), one sequential scan over the quads of each sample
+// (k_quad_fwd_scan), and the carries inside a quad rebuilt by the prefix-row kernel from the quad's carry
+// (at most three combines). The adjoint carries mirror it (k_quad_bwd_agg / k_quad_bwd_scan / full adjoint).
+// Lane view of these kernels: 64 lanes, lane = 8 j + k holds level 1 of plane j and the pair (j, k).
+struct dc {
+  double re, im;
+};
+__device__ __forceinline__ dc operator+(dc a, dc b) { return dc{a.re + b.re, a.im + b.im}; }
+__device__ __forceinline__ dc operator-(dc a, dc b) { return dc{a.re - b.re, a.im - b.im}; }
+__device__ __forceinline__ dc operator*(dc a, dc b) { return dc{a.re * b.re - a.im * b.im, a.re * b.im + a.im * b.re}; }
+__device__ __forceinline__ dc cjd(dc a) { return dc{a.re, -a.im}; }
+__device__ __forceinline__ dc dexpc(dc x) {
+  double sn, cs;
+  sincos(x.im, &sn, &cs);
+  const double m = exp(x.re);
+  return dc{m * cs, m * sn};
+}
+__device__ __forceinline__ dc ld_fd(const float* p) { return dc{(double)p[0], (double)p[1]}; }
+__device__ __forceinline__ dc ld_dd(const double* p) { return dc{p[0], p[1]}; }
+__device__ __forceinline__ void st_dd(double* p, dc v) {
+  p[0] = v.re;
+  p[1] = v.im;
+}
+__device__ __forceinline__ void st_fd(float* p, dc v) {
+  p[0] = (float)v.re;
+  p[1] = (float)v.im;
+}
+__device__ __forceinline__ dc rowsum8(dc v) {  // over lanes 8 j .. 8 j + 7
+#pragma unroll
+  for (int o = 1; o < 8; o <<= 1) {
+    v.re += __shfl_xor(v.re, o, 64);
+    v.im += __shfl_xor(v.im, o, 64);
+  }
+  return v;
+}
+// flow exp(u_p tau) of plane p over the clock span of chunks [c0, c1) (per-interval flows)
+__device__ __forceinline__ dc span_flow(const DiagArgs& a, int b, int c0, int c1, int p) {
+  const float* th = a.clock + (size_t)b * a.L;
+  const double tau = (double)th[min(c1 * a.T, a.n_int)] - (double)th[c0 * a.T];
+  return dexpc(dc{-(double)a.params[2 * p] * tau, (double)a.params[2 * p + 1] * tau});
+}
+
+struct PairSt {
+  dc S1, SA, SB;
+};
+__device__ __forceinline__ int poff(int j, int k) { return DIM + 4 * (8 * j + k); }
+__device__ __forceinline__ PairSt load_st_d(const double* row, int j, int k) {
+  return PairSt{ld_dd(row + 2 * j), ld_dd(row + poff(j, k)), ld_dd(row + poff(j, k) + 2)};
+}
+__device__ __forceinline__ PairSt load_st_f(const float* row, int j, int k) {
+  return PairSt{ld_fd(row + 2 * j), ld_fd(row + poff(j, k)), ld_fd(row + poff(j, k) + 2)};
+}
+__device__ __forceinline__ void store_st_d(double* row, int j, int k, const PairSt& s) {
+  if (k == 0) st_dd(row + 2 * j, s.S1);
+  st_dd(row + poff(j, k), s.SA);
+  st_dd(row + poff(j, k) + 2, s.SB);
+}
+__device__ __forceinline__ void store_st_f(float* row, int j, int k, const PairSt& s) {
+  if (k == 0) st_fd(row + 2 * j, s.S1);
+  st_fd(row + poff(j, k), s.SA);
+  st_fd(row + poff(j, k) + 2, s.SB);
+}
+// S <- (flow F applied to S) (x) Y: the Chen product with a summary Y (level 1 y1j, y1k; pair yA, yB)
+__device__ __forceinline__ void chen_d(PairSt& s, dc Fj, dc Fk, dc y1j, dc y1k, dc yA, dc yB) {
+  const dc cj = Fj * s.S1;
+  s.SA = (Fj * cjd(Fk)) * s.SA + cj * cjd(y1k) + yA;
+  s.SB = (Fj * Fk) * s.SB + cj * y1k + yB;
+  s.S1 = cj + y1j;
+}
+// X <- J^T X for the transfer of a summary with flow F and level-1 increment l1 (then add the local part)
+__device__ __forceinline__ void adj_d(PairSt& X, dc Fj, dc Fk, dc l1k) {
+  const dc toC = rowsum8(cjd(l1k) * X.SB + l1k * X.SA);
+  X.SB = cjd(Fj * Fk) * X.SB;
+  X.SA = cjd(Fj * cjd(Fk)) * X.SA;
+  X.S1 = cjd(Fj) * (X.S1 + toC);
+}
+__device__ __forceinline__ void add_st(PairSt& X, const PairSt& m) {
+  X.S1 = X.S1 + m.S1;
+  X.SA = X.SA + m.SA;
+  X.SB = X.SB + m.SB;
+}
+// level-1 increment of the span [ca, cb) of plane p: carry1(cb) - F carry1(ca)
+__device__ __forceinline__ dc l1_inc(const DiagArgs& a, int b, int ca, int cb, int p, dc F) {
+  const double* c0 = a.carries + ((size_t)b * (a.C + 1) + ca) * a.D;
+  const double* c1 = a.carries + ((size_t)b * (a.C + 1) + cb) * a.D;
+  return ld_dd(c1 + 2 * p) - F * ld_dd(c0 + 2 * p);
+}
+
+// chunk flows of the quad (LDS + cflow) and the quad flow (qflow)
+__device__ __forceinline__ void quad_flows(const DiagArgs& a, int b, int q, int c0, int nc, dc (*s_F)[K]) {
+  const int l = threadIdx.x;
+  if (l < 8 * nc) {
+    const int i = l >> 3, p = l & 7;
+    const dc F = span_flow(a, b, c0 + i, c0 + i + 1, p);
+    s_F[i][p] = F;
+    st_dd(a.cflow + (((size_t)b * a.C + c0 + i) * K + p) * 2, F);
+  } else if (l >= 32 && l < 32 + K) {
+    const int p = l - 32;
+    st_dd(a.qflow + (((size_t)b * a.NQ + q) * K + p) * 2, span_flow(a, b, c0, c0 + nc, p));
+  }
+  __syncthreads();
+}
+
+__global__ __launch_bounds__(64) void k_quad_fwd_agg(DiagArgs a) {
+  __shared__ dc s_F[4][K];
+  const int q = blockIdx.x, b = blockIdx.y, j = threadIdx.x >> 3, k = threadIdx.x & 7;
+  const int c0 = 4 * q, nc = min(4, a.C - c0);
+  quad_flows(a, b, q, c0, nc, s_F);
+  PairSt s{};
+  for (int i = 0; i < nc; ++i) {
+    const float* sp = a.summ + ((size_t)b * a.C + c0 + i) * a.D;
+    chen_d(s, s_F[i][j], s_F[i][k], ld_fd(sp + 2 * j), ld_fd(sp + 2 * k), ld_fd(sp + poff(j, k)),
+           ld_fd(sp + poff(j, k) + 2));
+  }
+  store_st_f(a.qagg + ((size_t)b * a.NQ + q) * a.D, j, k, s);
+}
+
+// Sequential scans over the quads of one sample: the quad inputs are staged into LDS a segment at a time by the
+// whole workgroup (one round trip to memory per segment), then wavefront 0 runs the chain from LDS with the next
+// step's operands loaded while the current one combines.
+constexpr int QSEG = 48;                    // quads per staged segment
+constexpr int QROW = DIM + DIM * DIM;       // floats of a quad's state
+struct QSeg {
+  float y[QSEG][QROW];                      // quad summary / adjoint aggregate (float32)
+  dc F[QSEG][K];                            // quad flows
+  dc l1[QSEG][K];                           // quad level-1 increments (adjoint scan)
+};
+__device__ __forceinline__ void stage_qseg(const DiagArgs& a, int b, int q0, int nq, bool with_l1, QSeg& sg) {
+  constexpr int U = 8, R4 = QROW / 4;
+  const float* src = a.qagg + ((size_t)b * a.NQ + q0) * a.D;
+  for (int ib = threadIdx.x; ib < nq * R4; ib += U * blockDim.x) {
+    f4a v[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int i = ib + u * blockDim.x, q = i / R4, e = i - q * R4;
+      if (i < nq * R4) v[u] = *reinterpret_cast<const f4a*>(src + (size_t)q * a.D + 4 * e);
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int i = ib + u * blockDim.x, q = i / R4, e = i - q * R4;
+      if (i < nq * R4) *reinterpret_cast<f4a*>(&sg.y[q][4 * e]) = v[u];
+    }
+  }
+  const double* fs = a.qflow + ((size_t)b * a.NQ + q0) * K * 2;
+  const double* ls = a.ql1 + ((size_t)b * a.NQ + q0) * K * 2;
+  for (int i = threadIdx.x; i < nq * K; i += blockDim.x) {  // at most two per thread
+    sg.F[i / K][i % K] = ld_dd(fs + 2 * i);
+    if (with_l1) sg.l1[i / K][i % K] = ld_dd(ls + 2 * i);
+  }
+}
+struct QOps {
+  PairSt y;
+  dc y1k, Fj, Fk, l1k;
+};
+__device__ __forceinline__ QOps q_ops(const QSeg& sg, int q, int j, int k, bool with_l1) {
+  QOps o;
+  o.y = load_st_f(sg.y[q], j, k);
+  o.y1k = ld_fd(sg.y[q] + 2 * k);
+  o.Fj = sg.F[q][j];
+  o.Fk = sg.F[q][k];
+  o.l1k = with_l1 ? sg.l1[q][k] : dc{0.0, 0.0};
+  return o;
+}
+
+__global__ __launch_bounds__(256) void k_quad_fwd_scan(DiagArgs a) {
+  __shared__ QSeg sg;
+  const int b = blockIdx.x, j = (threadIdx.x & 63) >> 3, k = threadIdx.x & 7;
+  const bool w0 = threadIdx.x < 64;
+  PairSt s{};
+  for (int q0 = 0; q0 < a.NQ; q0 += QSEG) {
+    const int nq = min(QSEG, a.NQ - q0);
+    stage_qseg(a, b, q0, nq, false, sg);
+    __syncthreads();
+    if (w0) {
+      QOps o = q_ops(sg, 0, j, k, false);
+      for (int q = 0; q < nq; ++q) {
+        store_st_d(a.carries + ((size_t)b * (a.C + 1) + 4 * (q0 + q)) * a.D, j, k, s);
+        const QOps cur = o;
+        if (q + 1 < nq) o = q_ops(sg, q + 1, j, k, false);
+        chen_d(s, cur.Fj, cur.Fk, cur.y.S1, cur.y1k, cur.y.SA, cur.y.SB);
+      }
+    }
+    __syncthreads();
+  }
+  if (w0) store_st_d(a.carries + ((size_t)b * (a.C + 1) + a.C) * a.D, j, k, s);
+}
+
+__global__ __launch_bounds__(64) void k_quad_bwd_agg(DiagArgs a) {
+  __shared__ dc s_F[4][K];
+  const int q = blockIdx.x, b = blockIdx.y, j = threadIdx.x >> 3, k = threadIdx.x & 7;
+  const int c0 = 4 * q, nc = min(4, a.C - c0);
+  quad_flows(a, b, q, c0, nc, s_F);
+  if (threadIdx.x < K) {  // the quad's level-1 increment (its flow was written by quad_flows of this lane's row)
+    const dc Fq = span_flow(a, b, c0, c0 + nc, threadIdx.x);
+    st_dd(a.ql1 + (((size_t)b * a.NQ + q) * K + threadIdx.x) * 2, l1_inc(a, b, c0, c0 + nc, threadIdx.x, Fq));
+  }
+  PairSt X = load_st_f(a.mu + ((size_t)b * a.C + c0 + nc - 1) * a.D, j, k);
+  for (int c = c0 + nc - 2; c >= c0; --c) {
+    const int i = c - c0;
+    adj_d(X, s_F[i][j], s_F[i][k], l1_inc(a, b, c, c + 1, k, s_F[i][k]));
+    add_st(X, load_st_f(a.mu + ((size_t)b * a.C + c) * a.D, j, k));
+  }
+  store_st_f(a.qagg + ((size_t)b * a.NQ + q) * a.D, j, k, X);
+}
+
+__global__ __launch_bounds__(256) void k_quad_bwd_scan(DiagArgs a) {
+  __shared__ QSeg sg;
+  const int b = blockIdx.x, j = (threadIdx.x & 63) >> 3, k = threadIdx.x & 7;
+  const bool w0 = threadIdx.x < 64;
+  PairSt X{};
+  for (int qe = a.NQ; qe > 0; qe -= QSEG) {
+    const int nq = min(QSEG, qe), q0 = qe - nq;
+    stage_qseg(a, b, q0, nq, true, sg);
+    __syncthreads();
+    if (w0) {
+      QOps o = q_ops(sg, nq - 1, j, k, true);
+      for (int q = nq - 1; q >= 0; --q) {
+        const int qq = q0 + q, c1 = min(4 * qq + 4, a.C);
+        store_st_f(a.mt + ((size_t)b * a.C + c1 - 1) * a.D, j, k, X);
+        const QOps cur = o;
+        if (q > 0) o = q_ops(sg, q - 1, j, k, true);
+        adj_d(X, cur.Fj, cur.Fk, cur.l1k);
+        add_st(X, cur.y);
+      }
+    }
+    __syncthreads();
+  }
 }
 
 // ------------------------------------------------------------------------------------------------ forward
@@ -223,45 +611,65 @@ template <bool OUT, bool BF16>
 __global__ __launch_bounds__(64) void k_fwd(DiagArgs a) {
   constexpr int KP = 4, GPW = Geo<KP>::GPW;
   __shared__ __align__(16) float s_v[GPW * VPITCH];
+  // start states of the groups (prefix rows: the carries rebuilt inside the quad), then level-2 row staging
+  __shared__ __align__(16) float s_row[GPW][DIM + DIM * DIM];
   const Lane l = lane_of<KP>(threadIdx.x);
   const int b = blockIdx.y, cb = blockIdx.x * GPW, c = cb + l.gi;
   stage<KP, BF16>(a, b, cb, s_v, nullptr);
+  if constexpr (OUT) {
+    // the workgroup's chunks are quad cb / 4: rebuild the carries inside it from the quad's carry (float64),
+    // for this kernel's groups and for every later kernel that reads carries (generic chunks, the adjoint)
+    const int jj = threadIdx.x >> 3, kk = threadIdx.x & 7, nc = min(GPW, a.C - cb);
+    PairSt st = load_st_d(a.carries + ((size_t)b * (a.C + 1) + cb) * a.D, jj, kk);
+    for (int i = 0; i < nc; ++i) {
+      store_st_f(s_row[i], jj, kk, st);
+      if (i + 1 < nc) {
+        const float* sp = a.summ + ((size_t)b * a.C + cb + i) * a.D;
+        const double* cf = a.cflow + ((size_t)b * a.C + cb + i) * K * 2;
+        chen_d(st, ld_dd(cf + 2 * jj), ld_dd(cf + 2 * kk), ld_fd(sp + 2 * jj), ld_fd(sp + 2 * kk),
+               ld_fd(sp + poff(jj, kk)), ld_fd(sp + poff(jj, kk) + 2));
+        store_st_d(a.carries + ((size_t)b * (a.C + 1) + cb + i + 1) * a.D, jj, kk, st);
+      }
+    }
+  }
   __syncthreads();
   if (c >= a.C) return;
   const int ci = b * a.C + c;
   float hb;
+  int flag;
   if constexpr (!OUT) {
-    const int flag = classify_chunk(a, b, c, l.gl, hb);
+    flag = classify_chunk(a, b, c, l.gl, hb);
     if (l.gl == 0) {
       a.cflag[ci] = flag;
       a.chbar[ci] = hb;
     }
     if (!(flag & 1)) return;
   } else {
-    if (!(a.cflag[ci] & 1)) return;
+    flag = a.cflag[ci];
+    if (!(flag & 1)) return;
     hb = a.chbar[ci];
   }
   const int t0 = c * a.T, Tc = min(a.T, a.n_int - t0);
   FwdCoef<KP> f;
-  fwd_coef<KP>(a, l, hb, f);
+  fwd_coef<KP>(a, l, hb, (flag & 4) != 0, f);
   cf S1{0.0f, 0.0f}, SA[KP], SB[KP];
   static_for<0, KP>([&](auto qc) {
     constexpr int q = qc;
     SA[q] = SB[q] = cf{0.0f, 0.0f};
   });
   if constexpr (OUT) {
-    const double* cr = a.carries + ((size_t)b * (a.C + 1) + c) * a.D;
-    S1 = cf{(float)cr[2 * l.j], (float)cr[2 * l.j + 1]};
+    const float* cr = s_row[l.gi];
+    S1 = cf{cr[2 * l.j], cr[2 * l.j + 1]};
     static_for<0, KP>([&](auto qc) {
       constexpr int q = qc;
-      const double* p2 = cr + DIM + 4 * (l.j * K + KP * l.kg + q);
-      SA[q] = cf{(float)(0.5 * p2[0]), (float)(0.5 * p2[1])};
-      SB[q] = cf{(float)(0.5 * p2[2]), (float)(0.5 * p2[3])};
+      const f4a p2 = *reinterpret_cast<const f4a*>(cr + poff(l.j, KP * l.kg + q));
+      SA[q] = cf{0.5f * p2.x, 0.5f * p2.y};
+      SB[q] = cf{0.5f * p2.z, 0.5f * p2.w};
     });
   }
   const float* vg = s_v + l.gi * VPITCH;
   float* orow = a.out + ((size_t)b * a.n_int + t0) * a.W;
-  const int o1 = a.off1 + 2 * l.j, o2 = a.off2 + 2 * l.j * DIM + 2 * KP * l.kg;
+  const int o1 = a.off1 + 2 * l.j;
   for (int t = 0; t < Tc; ++t) {
     cf pj, pk[KP];
     load_p<KP>(vg + t * DIM, l, pj, pk);
@@ -279,13 +687,23 @@ __global__ __launch_bounds__(64) void k_fwd(DiagArgs a) {
       float* row = orow + (size_t)t * a.W;
       if (a.lvl0 && l.gl == 0) row[0] = 1.0f;
       if (l.kg == 0) *reinterpret_cast<f2u*>(row + o1) = f2u{S1.re, S1.im};
-      f4u* p0 = reinterpret_cast<f4u*>(row + o2);
-      f4u* p1 = reinterpret_cast<f4u*>(row + o2 + DIM);
+      float* buf = s_row[l.gi];
+      f4a* p0 = reinterpret_cast<f4a*>(buf + 32 * l.j + 2 * KP * l.kg);
+      f4a* p1 = reinterpret_cast<f4a*>(buf + 32 * l.j + DIM + 2 * KP * l.kg);
       static_for<0, KP / 2>([&](auto ic) {
         constexpr int i = ic, q0 = 2 * i, q1 = 2 * i + 1;
-        p0[i] = f4u{SA[q0].re + SB[q0].re, SB[q0].im - SA[q0].im, SA[q1].re + SB[q1].re, SB[q1].im - SA[q1].im};
-        p1[i] = f4u{SA[q0].im + SB[q0].im, SA[q0].re - SB[q0].re, SA[q1].im + SB[q1].im, SA[q1].re - SB[q1].re};
+        p0[i] = f4a{SA[q0].re + SB[q0].re, SB[q0].im - SA[q0].im, SA[q1].re + SB[q1].re, SB[q1].im - SA[q1].im};
+        p1[i] = f4a{SA[q0].im + SB[q0].im, SA[q0].re - SB[q0].re, SA[q1].im + SB[q1].im, SA[q1].re - SB[q1].re};
       });
+      wave_order();
+      float* row2 = row + a.off2;
+      static_for<0, Pieces<KP>::NP>([&](auto ic) {
+        constexpr int i = ic;
+        const int pi = l.gl + Geo<KP>::G * i;
+        const f4a v = *reinterpret_cast<const f4a*>(buf + 4 * pi);
+        *reinterpret_cast<f4u*>(row2 + 4 * pi) = f4u{v.x, v.y, v.z, v.w};
+      });
+      wave_order();
     }
   }
   if constexpr (!OUT) {
@@ -302,24 +720,39 @@ __global__ __launch_bounds__(64) void k_fwd(DiagArgs a) {
 // ------------------------------------------------------------------------------------------------ backward
 // Cotangent row slice of the lane: level 1 of plane j and the KP 2x2 blocks (j, k).
 template <int KP> struct GRow {
-  f4u r0[KP / 2], r1[KP / 2];
+  f4a r0[KP / 2], r1[KP / 2];
+  float2 g1;
+};
+// A prefetched cotangent row: the lane's pieces of the level-2 part and its level-1 pair.
+template <int KP> struct GRaw {
+  Pieces<KP> pc;
   f2u g1;
 };
-template <int KP> __device__ __forceinline__ GRow<KP> load_g(const float* row, int o1, int o2) {
+template <int KP> __device__ __forceinline__ GRaw<KP> load_graw(const float* row, int o1, int off2, int gl) {
+  GRaw<KP> r;
+  r.g1 = *reinterpret_cast<const f2u*>(row + o1);
+  r.pc = load_pieces<KP>(row + off2, gl);
+  return r;
+}
+// raw row -> LDS -> the lane's slice
+template <int KP> __device__ __forceinline__ GRow<KP> slice_g(const GRaw<KP>& r, float* buf, const Lane& l) {
+  pieces_to_lds<KP>(r.pc, buf, l.gl);
+  wave_order();
   GRow<KP> g;
-  g.g1 = *reinterpret_cast<const f2u*>(row + o1);
-  const f4u* p0 = reinterpret_cast<const f4u*>(row + o2);
-  const f4u* p1 = reinterpret_cast<const f4u*>(row + o2 + DIM);
+  g.g1 = float2{r.g1.x, r.g1.y};
+  const f4a* p0 = reinterpret_cast<const f4a*>(buf + 32 * l.j + 2 * KP * l.kg);
+  const f4a* p1 = reinterpret_cast<const f4a*>(buf + 32 * l.j + DIM + 2 * KP * l.kg);
   static_for<0, KP / 2>([&](auto ic) {
     constexpr int i = ic;
     g.r0[i] = p0[i];
     g.r1[i] = p1[i];
   });
+  wave_order();
   return g;
 }
 // doubled pair cotangents (2 dL/dSA, 2 dL/dSB) of pair q from the block entries g00, g01, g10, g11
 template <int KP, int q> __device__ __forceinline__ void g_pair(const GRow<KP>& g, cf& gA, cf& gB) {
-  const f4u r0 = g.r0[q / 2], r1 = g.r1[q / 2];
+  const f4a r0 = g.r0[q / 2], r1 = g.r1[q / 2];
   const float g00 = (q & 1) ? r0.z : r0.x, g01 = (q & 1) ? r0.w : r0.y;
   const float g10 = (q & 1) ? r1.z : r1.x, g11 = (q & 1) ? r1.w : r1.y;
   gA = cf{g00 + g11, g10 - g01};
@@ -331,31 +764,34 @@ template <bool BF16>
 __global__ __launch_bounds__(64) void k_bwd_local(DiagArgs a) {
   constexpr int KP = 4, GPW = Geo<KP>::GPW;
   __shared__ __align__(16) float s_v[GPW * VPITCH];
+  __shared__ __align__(16) float s_row[GPW][DIM * DIM];  // cotangent row staging
   const Lane l = lane_of<KP>(threadIdx.x);
   const int b = blockIdx.y, cb = blockIdx.x * GPW, c = cb + l.gi;
   stage<KP, BF16>(a, b, cb, s_v, nullptr);
   __syncthreads();
   if (c >= a.C) return;
   const int ci = b * a.C + c;
-  if (!(a.cflag[ci] & 1)) return;
+  const int flag = a.cflag[ci];
+  if (!(flag & 1)) return;
   const int t0 = c * a.T, Tc = min(a.T, a.n_int - t0);
   FwdCoef<KP> f;
-  fwd_coef<KP>(a, l, a.chbar[ci], f);
+  fwd_coef<KP>(a, l, a.chbar[ci], (flag & 4) != 0, f);
   const float* vg = s_v + l.gi * VPITCH;
   const float* grow = a.gout + ((size_t)b * a.n_int + t0) * a.W;
-  const int o1 = a.off1 + 2 * l.j, o2 = a.off2 + 2 * l.j * DIM + 2 * KP * l.kg;
+  const int o1 = a.off1 + 2 * l.j;
+  float* gbuf = s_row[l.gi];
   cf l1{0.0f, 0.0f}, lA[KP], lB[KP];
   static_for<0, KP>([&](auto qc) {
     constexpr int q = qc;
     lA[q] = lB[q] = cf{0.0f, 0.0f};
   });
-  GRow<KP> gn1 = load_g<KP>(grow + (size_t)(Tc - 1) * a.W, o1, o2);
-  GRow<KP> gn2 = gn1;
-  if (Tc >= 2) gn2 = load_g<KP>(grow + (size_t)(Tc - 2) * a.W, o1, o2);
+  GRaw<KP> gn1 = load_graw<KP>(grow + (size_t)(Tc - 1) * a.W, o1, a.off2, l.gl);
+  GRaw<KP> gn2 = gn1;
+  if (Tc >= 2) gn2 = load_graw<KP>(grow + (size_t)(Tc - 2) * a.W, o1, a.off2, l.gl);
   for (int t = Tc - 1; t >= 0; --t) {
-    const GRow<KP> g = gn1;
+    const GRow<KP> g = slice_g<KP>(gn1, gbuf, l);
     gn1 = gn2;
-    if (t >= 2) gn2 = load_g<KP>(grow + (size_t)(t - 2) * a.W, o1, o2);
+    if (t >= 2) gn2 = load_graw<KP>(grow + (size_t)(t - 2) * a.W, o1, a.off2, l.gl);
     cf pj, pk[KP];
     load_p<KP>(vg + t * DIM, l, pj, pk);
     l1 += cf{g.g1.x, g.g1.y};
@@ -404,9 +840,29 @@ __global__ __launch_bounds__(64) void k_bwd_full(DiagArgs a) {
   __shared__ __align__(16) float s_dhp[GPW][NB * G];        // dh partials [t][lane]
   __shared__ __align__(16) float s_dvo[GPW][(NB + 1) * DIM];  // dv of the block's steps; row NB: the step after
   __shared__ float s_dho[GPW][NB + 1];
+  __shared__ __align__(16) float s_row[GPW][DIM * DIM];  // cotangent row staging
+  __shared__ __align__(16) float s_mt[GPW][DIM + DIM * DIM];  // cotangent from later chunks, per group
   const Lane l = lane_of<KP>(threadIdx.x);
   const int b = blockIdx.y, cb = blockIdx.x * GPW, c = cb + l.gi;
   stage<KP, BF16>(a, b, cb, s_v, s_h);
+  {
+    // adjoint carries inside the quad: mt[c] = mu(c+1) + J_{c+1}^T mt[c+1] down from the quad's last chunk
+    // (written by the scan); float64, written back for every later kernel that reads mt (generic chunks)
+    const int jj = threadIdx.x >> 3, kk = threadIdx.x & 7;
+    const int c_last = min(4 * (cb / 4) + 3, a.C - 1);
+    PairSt X = load_st_f(a.mt + ((size_t)b * a.C + c_last) * a.D, jj, kk);
+    if (c_last < cb + GPW) store_st_f(s_mt[c_last - cb], jj, kk, X);
+    for (int cc = c_last - 1; cc >= cb; --cc) {
+      const double* cf = a.cflow + ((size_t)b * a.C + cc + 1) * K * 2;
+      const dc Fk = ld_dd(cf + 2 * kk);
+      adj_d(X, ld_dd(cf + 2 * jj), Fk, l1_inc(a, b, cc + 1, cc + 2, kk, Fk));
+      add_st(X, load_st_f(a.mu + ((size_t)b * a.C + cc + 1) * a.D, jj, kk));
+      if (cc < cb + GPW) {
+        store_st_f(s_mt[cc - cb], jj, kk, X);
+        store_st_f(a.mt + ((size_t)b * a.C + cc) * a.D, jj, kk, X);
+      }
+    }
+  }
   __syncthreads();
   const int ci = b * a.C + (c < a.C ? c : 0);
   const bool active = c < a.C && (a.cflag[ci] & 3) == 3;
@@ -414,36 +870,61 @@ __global__ __launch_bounds__(64) void k_bwd_full(DiagArgs a) {
   const float hb = active ? a.chbar[ci] : 0.0f;
   // coefficients at hbar
   BwdCoef<KP> f;
+  const bool use_tab = active && (a.cflag[ci] & 4);
   const cf uj = load_u(a.params, l.j);
   const cf xj = hb * uj;
-  {
+  if (use_tab) {
+    const float* tab = a.ctab;
+    const float dlt = hb - tab[0];
+    f.rho = tflow(tp(tab, l.j, TP_RHO), tp(tab, l.j, TP_RHO1), dlt);
+    f.rhoi = tflow(tp(tab, l.j, TP_RHOI), tp(tab, l.j, TP_RHOI1), dlt);
+    f.phi = tp(tab, l.j, TP_PHI);
+    f.rho1 = tp(tab, l.j, TP_RHO1);
+    f.phi1 = tp(tab, l.j, TP_PHI1);
+    static_for<0, KP>([&](auto qc) {
+      constexpr int q = qc;
+      const int k = KP * l.kg + q;
+      f.phk[q] = tp(tab, k, TP_PHIH);
+      f.phi1h[q] = tp(tab, k, TP_PHI1H);
+      f.LB[q] = tflow(tq(tab, l.j, k, TQ_LB), tq(tab, l.j, k, TQ_LB1), dlt);
+      f.LA[q] = tflow(tq(tab, l.j, k, TQ_LA), tq(tab, l.j, k, TQ_LA1), dlt);
+      f.LBi[q] = tflow(tq(tab, l.j, k, TQ_LBI), tq(tab, l.j, k, TQ_LBI1), dlt);
+      f.LAi[q] = tflow(tq(tab, l.j, k, TQ_LAI), tq(tab, l.j, k, TQ_LAI1), dlt);
+      f.LB1[q] = tq(tab, l.j, k, TQ_LB1);
+      f.LA1[q] = tq(tab, l.j, k, TQ_LA1);
+      f.IB[q] = tq(tab, l.j, k, TQ_IB);
+      f.IA[q] = tq(tab, l.j, k, TQ_IA);
+      f.IB1[q] = tq(tab, l.j, k, TQ_IB1);
+      f.IA1[q] = tq(tab, l.j, k, TQ_IA1);
+    });
+  } else {
     const Node1<cf> nj = node1(xj);
     f.rho = nj.e;
     f.rhoi = expv(-xj);
     f.phi = nj.p;
     f.rho1 = nj.e * uj;
     f.phi1 = nj.dp * uj;
+    static_for<0, KP>([&](auto qc) {
+      constexpr int q = qc;
+      const cf uk = load_u(a.params, KP * l.kg + q);
+      const Node1<cf> nk = node1(hb * uk);
+      f.phk[q] = 0.5f * nk.p;
+      f.phi1h[q] = 0.5f * (nk.dp * uk);
+      const cf ub = uj + uk, ua = uj + conj(uk);
+      f.LB[q] = expv(hb * ub);
+      f.LA[q] = expv(hb * ua);
+      f.LBi[q] = expv(-(hb * ub));
+      f.LAi[q] = expv(-(hb * ua));
+      f.LB1[q] = f.LB[q] * ub;
+      f.LA1[q] = f.LA[q] * ua;
+      const DD3<cf> db = dd3<cf, true>(xj, hb * ub);
+      const DD3<cf> da = dd3<cf, true>(xj, hb * ua);
+      f.IB[q] = 0.5f * db.d;
+      f.IA[q] = 0.5f * da.d;
+      f.IB1[q] = 0.5f * (db.dx * uj + db.dy * ub);
+      f.IA1[q] = 0.5f * (da.dx * uj + da.dy * ua);
+    });
   }
-  static_for<0, KP>([&](auto qc) {
-    constexpr int q = qc;
-    const cf uk = load_u(a.params, KP * l.kg + q);
-    const Node1<cf> nk = node1(hb * uk);
-    f.phk[q] = 0.5f * nk.p;
-    f.phi1h[q] = 0.5f * (nk.dp * uk);
-    const cf ub = uj + uk, ua = uj + conj(uk);
-    f.LB[q] = expv(hb * ub);
-    f.LA[q] = expv(hb * ua);
-    f.LBi[q] = expv(-(hb * ub));
-    f.LAi[q] = expv(-(hb * ua));
-    f.LB1[q] = f.LB[q] * ub;
-    f.LA1[q] = f.LA[q] * ua;
-    const DD3<cf> db = dd3<cf, true>(xj, hb * ub);
-    const DD3<cf> da = dd3<cf, true>(xj, hb * ua);
-    f.IB[q] = 0.5f * db.d;
-    f.IA[q] = 0.5f * da.d;
-    f.IB1[q] = 0.5f * (db.dx * uj + db.dy * ub);
-    f.IA1[q] = 0.5f * (da.dx * uj + da.dy * ua);
-  });
   // end state (float64 carry after the chunk) and cotangent from later chunks
   cf S1{0.0f, 0.0f}, SA[KP], SB[KP], l1{0.0f, 0.0f}, lA[KP], lB[KP];
   static_for<0, KP>([&](auto qc) {
@@ -452,7 +933,7 @@ __global__ __launch_bounds__(64) void k_bwd_full(DiagArgs a) {
   });
   if (active) {
     const double* cr = a.carries + ((size_t)b * (a.C + 1) + c + 1) * a.D;
-    const float* mp = a.mt + ((size_t)b * a.C + c) * a.D;
+    const float* mp = s_mt[l.gi];
     S1 = cf{(float)cr[2 * l.j], (float)cr[2 * l.j + 1]};
     l1 = cf{mp[2 * l.j], mp[2 * l.j + 1]};
     static_for<0, KP>([&](auto qc) {
@@ -480,10 +961,11 @@ __global__ __launch_bounds__(64) void k_bwd_full(DiagArgs a) {
   float* dvo_g = s_dvo[l.gi];
   float* dho_g = s_dho[l.gi];
   const float* grow = a.gout + ((size_t)b * a.n_int + (active ? t0 : 0)) * a.W;
-  const int o1 = a.off1 + 2 * l.j, o2 = a.off2 + 2 * l.j * DIM + 2 * KP * l.kg;
-  GRow<KP> gn1{}, gn2{};
-  if (Tc >= 1) gn1 = load_g<KP>(grow + (size_t)(Tc - 1) * a.W, o1, o2);
-  if (Tc >= 2) gn2 = load_g<KP>(grow + (size_t)(Tc - 2) * a.W, o1, o2);
+  const int o1 = a.off1 + 2 * l.j;
+  float* gbuf = s_row[l.gi];
+  GRaw<KP> gn1{}, gn2{};
+  if (Tc >= 1) gn1 = load_graw<KP>(grow + (size_t)(Tc - 1) * a.W, o1, a.off2, l.gl);
+  if (Tc >= 2) gn2 = load_graw<KP>(grow + (size_t)(Tc - 2) * a.W, o1, a.off2, l.gl);
   // blocks of NB steps, last block first; every group runs the same number of blocks (barriers)
   const int nblk = (a.T + NB - 1) / NB;
   for (int blk = nblk - 1; blk >= 0; --blk) {
@@ -492,9 +974,9 @@ __global__ __launch_bounds__(64) void k_bwd_full(DiagArgs a) {
     for (int s = NB - 1; s >= 0; --s) {
       const int t = tb + s;
       if (t >= Tc) continue;
-      const GRow<KP> g = gn1;
+      const GRow<KP> g = slice_g<KP>(gn1, gbuf, l);
       gn1 = gn2;
-      if (t >= 2) gn2 = load_g<KP>(grow + (size_t)(t - 2) * a.W, o1, o2);
+      if (t >= 2) gn2 = load_graw<KP>(grow + (size_t)(t - 2) * a.W, o1, a.off2, l.gl);
       const float h = hg[t];
       cf pj, pk[KP];
       load_p<KP>(vg + t * DIM, l, pj, pk);
@@ -612,23 +1094,37 @@ __global__ __launch_bounds__(64) void k_bwd_full(DiagArgs a) {
     cf Gx{0.0f, 0.0f};
     static_for<0, KP>([&](auto qc) {
       constexpr int q = qc;
-      const cf uk = load_u(a.params, KP * l.kg + q);
-      const cf ub = uj + uk, ua = uj + conj(uk);
-      const DD3<cf> db = dd3<cf, true>(xj, hb * ub);
-      const DD3<cf> da = dd3<cf, true>(xj, hb * ua);
-      const Node1<cf> nk = node1(hb * uk);
-      Gx += 0.5f * (kIB[q] * conj(db.dx) + kIA[q] * conj(da.dx));
-      const cf GyB = 0.5f * (kIB[q] * conj(db.dy)) + kLB[q] * conj(f.LB[q]);
-      const cf GyA = 0.5f * (kIA[q] * conj(da.dy)) + kLA[q] * conj(f.LA[q]);
-      const cf Gk = 0.5f * (kph[q] * conj(nk.dp));
+      const int k = KP * l.kg + q;
+      cf DxB, DyB, DxA, DyA, dpk;
+      if (use_tab) {
+        DxB = tq(a.ctab, l.j, k, TQ_DXB);
+        DyB = tq(a.ctab, l.j, k, TQ_DYB);
+        DxA = tq(a.ctab, l.j, k, TQ_DXA);
+        DyA = tq(a.ctab, l.j, k, TQ_DYA);
+        dpk = tp(a.ctab, k, TP_DPHI);
+      } else {
+        const cf uk = load_u(a.params, k);
+        const cf ub = uj + uk, ua = uj + conj(uk);
+        const DD3<cf> db = dd3<cf, true>(xj, hb * ub);
+        const DD3<cf> da = dd3<cf, true>(xj, hb * ua);
+        DxB = db.dx;
+        DyB = db.dy;
+        DxA = da.dx;
+        DyA = da.dy;
+        dpk = node1(hb * uk).dp;
+      }
+      Gx += 0.5f * (kIB[q] * conj(DxB) + kIA[q] * conj(DxA));
+      const cf GyB = 0.5f * (kIB[q] * conj(DyB)) + kLB[q] * conj(f.LB[q]);
+      const cf GyA = 0.5f * (kIA[q] * conj(DyA)) + kLA[q] * conj(f.LA[q]);
+      const cf Gk = 0.5f * (kph[q] * conj(dpk));
       rd += -GyB.re - GyA.re;
       rw += GyB.im + GyA.im;
       sp[l.gl * PS + 2 + 2 * q] = -GyB.re - GyA.re - Gk.re;
       sp[l.gl * PS + 3 + 2 * q] = GyB.im - GyA.im + Gk.im;
     });
     if (l.kg == 0) {
-      const Node1<cf> nj = node1(xj);
-      Gx += krho * conj(f.rho) + kphj * conj(nj.dp);
+      const cf dpj = use_tab ? tp(a.ctab, l.j, TP_DPHI) : node1(xj).dp;
+      Gx += krho * conj(f.rho) + kphj * conj(dpj);
     }
     sp[l.gl * PS + 0] = rd - Gx.re;
     sp[l.gl * PS + 1] = rw + Gx.im;
@@ -663,12 +1159,29 @@ bool pairs_eligible(int structure, int depth, int dim, int readout, int flow_mod
 int pairs_forward(const DiagArgs& a, hipStream_t st, bool out) {
   constexpr int GPW = pairs::Geo<4>::GPW;
   const dim3 grid((a.C + GPW - 1) / GPW, a.B), blk(64);
+  if (!out) {
+    hipLaunchKernelGGL(pairs::k_coef_table, dim3(1), dim3(64), 0, st, a);
+    if (hipGetLastError() != hipSuccess) return -1;
+  }
   if (out) {
     if (a.path_bf16) hipLaunchKernelGGL((pairs::k_fwd<true, true>), grid, blk, 0, st, a);
     else hipLaunchKernelGGL((pairs::k_fwd<true, false>), grid, blk, 0, st, a);
   } else {
     if (a.path_bf16) hipLaunchKernelGGL((pairs::k_fwd<false, true>), grid, blk, 0, st, a);
     else hipLaunchKernelGGL((pairs::k_fwd<false, false>), grid, blk, 0, st, a);
+  }
+  return hipGetLastError() == hipSuccess ? 0 : -1;
+}
+
+int pairs_carry_scan(const DiagArgs& a, hipStream_t st, bool backward) {
+  if (backward) {
+    hipLaunchKernelGGL(pairs::k_quad_bwd_agg, dim3(a.NQ, a.B), dim3(64), 0, st, a);
+    if (hipGetLastError() != hipSuccess) return -1;
+    hipLaunchKernelGGL(pairs::k_quad_bwd_scan, dim3(a.B), dim3(256), 0, st, a);
+  } else {
+    hipLaunchKernelGGL(pairs::k_quad_fwd_agg, dim3(a.NQ, a.B), dim3(64), 0, st, a);
+    if (hipGetLastError() != hipSuccess) return -1;
+    hipLaunchKernelGGL(pairs::k_quad_fwd_scan, dim3(a.B), dim3(256), 0, st, a);
   }
   return hipGetLastError() == hipSuccess ? 0 : -1;
 }
