@@ -1,0 +1,734 @@
+// Dense-generator EWS on MI355X (gfx950): any d x d generator A (d <= 16), depths 1-3, the series leaf.
+//
+// Reference path (sign convention of the reference: the flow over a clock step h is M = exp(-h A)):
+//   local terms  ews/core/series_leaf.py:72-126 (letters b_0 = v, b_p = (-h/p) A b_{p-1};
+//                level k = sum_{|m|<=q} c_m b_{m1} (x) ... (x) b_{mk}, c_m = prod_j 1/(M_j + k - j + 1))
+//   flows        ews/core/chen_scan.py:155-168 (one exponential per interval, or one shared exponential)
+//   Chen combine ews/core/chen_scan.py:125-214, ews/core/kernels/pallas_combine.py:603-749 (dense kernel)
+//
+// Passes (every array is padded to 16 channels; zero channels stay exactly zero through every step):
+//   0  k_powers: table P_p = A^p / p! (float64 products, stored float32) and ||A||_1.
+//      k_local: per interval (fully parallel) the levels s_1..s_N of the series leaf and the flow M_t.
+//      Levels are built from nested degree sums instead of the coefficient tensor:
+//         g1_n = b_n / (n+1),     g2_N = 1/(N+2) sum_{p+n=N} b_p (x) g1_n,
+//         s_k  = sum_n bt^(k)_n (x) g_{k-1,n},   bt^(k)_n = sum_{p <= q-n} b_p / (p + n + k),
+//      which is the same truncated sum (|m| <= q) as the reference's coefficient tensor.
+//      Flows: Taylor polynomial of degree 12 in X = -h A / 2^s (||X||_1 <= 1), then s squarings.
+//   1  k_scan<SUMMARY>: one workgroup per (sample, chunk) scans the chunk from a zero state; writes the chunk
+//      summary and the chunk's flow product.
+//   2  k_scan<PREFIX> over the chunk summaries (one chunk per sample): the carries (state before each chunk).
+//   3  k_scan<PREFIX> from the carries: output rows (prefix), or the terminal row / mean / max.
+//
+// The Chen step in Horner form (level 3; the others are the same with fewer terms):
+//     S3' = ((S3 x_3 M + S2 (x) s1) x_2 M + S1 (x) s2) x_1 M + s3
+//     S2' = (S2 x_2 M + S1 (x) s1) x_1 M + s2,      S1' = M S1 + s1
+// where x_a M applies M along tensor axis a: S2' = M S2 M^T + (M S1) s1^T + s2 and
+// S3' = M^{(x)3} S3 + (M^{(x)2} S2) (x) s1 + (M S1) (x) s2 + s3, as in chen_scan.py:98-152.
+// Mode products are 16x16x4 float32 MFMAs. The MFMA result registers of one mode product feed the next one
+// directly: result lane l holds rows 4(l/16)+r (r = 0..3) of column l%16, and register r can be the B
+// operand of k-step r with contraction index 4(l/16)+r (or the A operand, transposed), so only the axis-1
+// product goes through LDS.
+#include <hip/hip_runtime.h>
+
+#include "ews_hip.h"
+
+namespace ews {
+namespace dense {
+
+constexpr int QMAX = 40;   // largest series order
+constexpr int PM = 12;     // Taylor degree of the flow exponential (||X||_1 <= 1: error below 1/13! ~ 1.6e-10)
+constexpr int RP = 20;     // LDS row pitch of the 16 x 16 slices (bank-conflict-free MFMA operand traffic)
+constexpr int SP = 16 * RP + 4;  // LDS slice pitch of the level-3 buffers
+
+__host__ __device__ constexpr int lw_of(int N) { return N == 1 ? 16 : (N == 2 ? 272 : 4368); }
+
+typedef float f4 __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ f4 mfma(float a, float b, f4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
+}
+
+struct Args {
+  int B, L, n_int, d, N, q, flow_mode, readout, lvl0, W, LW;
+  int T, C, npow;
+  const float* path;
+  const float* clock;
+  const float* A;
+  float* apow;  // (npow, 256) P_p = A^p / p!, then one float ||A||_1
+  float* loc;   // (B, n_int, LW) padded levels
+  float* fl;    // (B, n_int, 256) flows
+  float* summ;  // (B, C, LW)
+  float* sfl;   // (B, C, 256)
+  float* car;   // (B, C + 1, LW) state before chunk c (row C: terminal state)
+  float* pre;   // (B, n_int, W) prefix rows (mean / max readouts)
+  float* out;
+};
+
+// One scan over rows of (levels, flows): chunks of T rows, per-sample strides in floats.
+struct Seq {
+  const float* lv;
+  long lv_bs;
+  const float* fl;
+  long fl_bs;
+  int n, T;
+  const float* init;  // per-chunk initial state: init + b * init_bs + c * LW (null: zero state)
+  long init_bs;
+  // PREFIX outputs: row t of sample b at rows + b * rows_bs + t * rows_ld (+ lvl0 leading 1.0 if set)
+  float* rows;
+  long rows_bs;
+  int rows_ld, padded, lvl0, d;
+  // SUMMARY outputs: (B, C, LW) states and (B, C, 256) flow products
+  float* summ;
+  float* sfl;
+  int C;
+};
+
+// ------------------------------------------------------------------------------------------------ powers
+// P_p = A^p / p! in float64 (stored float32), p < npow, zero-padded to 16 x 16; apow[npow * 256] = ||A||_1.
+__global__ __launch_bounds__(256) void k_powers(Args a) {
+  __shared__ double P[2][256];
+  __shared__ double Ad[256];
+  const int e = threadIdx.x, i = e >> 4, j = e & 15;
+  Ad[e] = (i < a.d && j < a.d) ? (double)a.A[i * a.d + j] : 0.0;
+  P[0][e] = (i == j) ? 1.0 : 0.0;
+  a.apow[e] = (i == j) ? 1.0f : 0.0f;
+  __syncthreads();
+  for (int p = 1; p < a.npow; ++p) {
+    const double* src = P[(p - 1) & 1];
+    double acc = 0.0;
+    for (int k = 0; k < 16; ++k) acc += src[i * 16 + k] * Ad[k * 16 + j];
+    acc /= (double)p;
+    P[p & 1][e] = acc;
+    a.apow[p * 256 + e] = (float)acc;
+    __syncthreads();
+  }
+  if (e < 16) {  // column sums, then max over columns (wave 0, lanes 0..15)
+    double cs = 0.0;
+    for (int r = 0; r < 16; ++r) cs += fabs(Ad[r * 16 + e]);
+    for (int o = 8; o >= 1; o >>= 1) cs = fmax(cs, __shfl_xor(cs, o, 16));
+    if (e == 0) a.apow[a.npow * 256] = (float)cs;
+  }
+}
+
+// ------------------------------------------------------------------------------------------------ local terms
+// Clock step of interval t of sample b for the flow: per interval, or the shared step of the cached modes
+// (chen_scan.py:155-168); interval 0 of the basepoint mode has the identity flow (ident = true).
+__device__ __forceinline__ float flow_step(const Args& a, const float* th, int t, bool& ident) {
+  ident = false;
+  if (a.flow_mode == EWS_FLOW_PER_INTERVAL) return th[t + 1] - th[t];
+  if (a.flow_mode == EWS_FLOW_CACHED) return th[1] - th[0];
+  ident = t == 0;
+  return th[2] - th[1];
+}
+
+// One workgroup of 256 threads per interval (grid-stride loop). QB: compile-time bound on the series order
+// (letters p <= q <= QB stay in registers / LDS with constant indices).
+template <int N, int QB>
+__global__ __launch_bounds__(256) void k_local(Args a) {
+  __shared__ float sp[(QB > PM ? QB : PM) + 1][256];  // the powers table
+  __shared__ float lt[QB + 1][16];   // letters b_p
+  __shared__ float g1[QB + 1][16];   // b_n / (n + 1)
+  __shared__ float bt[QB + 1][16];   // bt^(N)_n (the last level's left factors)
+  __shared__ float vv[16];
+  __shared__ float mm[256];
+  const int tid = threadIdx.x, i = tid >> 4, j = tid & 15;
+  const int q = a.q;
+  for (int e = tid; e < a.npow * 256; e += 256) sp[e >> 8][e & 255] = a.apow[e];
+  const float norm1 = a.apow[a.npow * 256];
+  __syncthreads();
+  const long total = (long)a.B * a.n_int;
+  for (long it = blockIdx.x; it < total; it += gridDim.x) {
+    const int b = (int)(it / a.n_int), t = (int)(it - (long)b * a.n_int);
+    const float* th = a.clock + (size_t)b * a.L;
+    const float h = th[t + 1] - th[t];
+    if (tid < 16) {
+      const float* x = a.path + ((size_t)b * a.L + t) * a.d;
+      vv[tid] = tid < a.d ? x[a.d + tid] - x[tid] : 0.0f;
+    }
+    __syncthreads();
+    // letters b_p = (-h)^p (P_p v)
+    for (int e = tid; e < (q + 1) * 16; e += 256) {
+      const int p = e >> 4, r = e & 15;
+      float acc = 0.0f;
+#pragma unroll
+      for (int c = 0; c < 16; ++c) acc = fmaf(sp[p][r * 16 + c], vv[c], acc);
+      float pw = 1.0f;
+      for (int m = 0; m < p; ++m) pw *= -h;
+      const float bp = acc * pw;
+      lt[p][r] = bp;
+      g1[p][r] = bp / (float)(p + 1);
+    }
+    __syncthreads();
+    float* row = a.loc + ((size_t)b * a.n_int + t) * a.LW;
+    if (tid < 16) {
+      float s = 0.0f;
+      for (int p = 0; p <= q; ++p) s += g1[p][tid];
+      row[tid] = s;
+    }
+    if constexpr (N >= 2) {
+      // bt_n = sum_{p <= q - n} b_p / (p + n + N); rows q < n <= QB are zero (read by the unrolled sums below)
+      for (int e = tid; e < (QB + 1) * 16; e += 256) {
+        const int n = e >> 4, r = e & 15;
+        float s = 0.0f;
+        for (int p = 0; p + n <= q; ++p) s += lt[p][r] / (float)(p + n + N);
+        bt[n][r] = s;
+      }
+      __syncthreads();
+      if constexpr (N == 2) {
+        // s2[i][j] = sum_n bt_n[i] g1_n[j]
+        float s = 0.0f;
+        for (int n = 0; n <= q; ++n) s = fmaf(bt[n][i], g1[n][j], s);
+        row[16 + tid] = s;
+      } else {
+        // g2_M[i][j] = 1/(M+2) sum_{p+n=M} b_p[i] g1_n[j]; s2 = sum_M g2_M; s3[c][i][j] = sum_M bt_M[c] g2_M[i][j]
+        float G[QB + 1];
+        float s2 = 0.0f;
+#pragma unroll
+        for (int M = 0; M <= QB; ++M) {
+          float s = 0.0f;
+          if (M <= q) {
+#pragma unroll
+            for (int p = 0; p <= M; ++p) s = fmaf(lt[p][i], g1[M - p][j], s);
+            s /= (float)(M + 2);
+          }
+          G[M] = s;
+          s2 += s;
+        }
+        row[16 + tid] = s2;
+#pragma unroll 4
+        for (int c = 0; c < 16; ++c) {
+          float s = 0.0f;
+#pragma unroll
+          for (int M = 0; M <= QB; ++M) s = fmaf(bt[M][c], G[M], s);
+          row[272 + c * 256 + tid] = s;
+        }
+      }
+    }
+    // flow M_t = exp(-h_f A): Taylor of degree PM in X = -h_f A / 2^s, then s squarings
+    {
+      bool ident;
+      const float hf = flow_step(a, th, t, ident);
+      float* fr = a.fl + ((size_t)b * a.n_int + t) * 256;
+      if (ident) {
+        fr[tid] = (i == j) ? 1.0f : 0.0f;
+      } else {
+        int s = 0;
+        float x = fabsf(hf) * norm1;
+        while (x > 1.0f && s < 30) {
+          x *= 0.5f;
+          ++s;
+        }
+        const float y = -hf * ldexpf(1.0f, -s);
+        float acc = sp[PM][tid];
+#pragma unroll
+        for (int p = PM - 1; p >= 0; --p) acc = fmaf(acc, y, sp[p][tid]);
+        for (int r = 0; r < s; ++r) {
+          __syncthreads();
+          mm[tid] = acc;
+          __syncthreads();
+          float v = 0.0f;
+#pragma unroll
+          for (int c = 0; c < 16; ++c) v = fmaf(mm[i * 16 + c], mm[c * 16 + j], v);
+          acc = v;
+        }
+        fr[tid] = acc;
+      }
+    }
+    __syncthreads();
+  }
+}
+
+// ------------------------------------------------------------------------------------------------ Chen scan
+__device__ __forceinline__ long out_index(int N, int d, int e) {  // padded state index -> unpadded row index
+  if (e < 16) return e < d ? e : -1;
+  if (N >= 2 && e < 272) {
+    const int f = e - 16, i = f >> 4, j = f & 15;
+    return (i < d && j < d) ? d + i * d + j : -1;
+  }
+  const int f = e - 272, i = f >> 8, j = (f >> 4) & 15, k = f & 15;
+  return (i < d && j < d && k < d) ? d + d * d + (i * d + j) * d + k : -1;
+}
+__device__ __forceinline__ void put(const Seq& s, float* orow, int N, int e, float v) {
+  if (s.padded) {
+    orow[e] = v;
+  } else {
+    const long o = out_index(N, s.d, e);
+    if (o >= 0) orow[o] = v;
+  }
+}
+
+// Operands of one step: the flow as the lane's M[l%16][4g..4g+3], level-1/2 local terms, and the lane's
+// level-3 local terms of the output tiles of this wave (j = 4w + jj).
+template <int N> struct StepIn {
+  f4 M4;
+  float s1k;
+  f4 s2r;
+  f4 s3r[N >= 3 ? 4 : 1];
+};
+template <int N>
+__device__ __forceinline__ void load_step(const Seq& s, int b, int t, int w, int g, int c16, StepIn<N>& in) {
+  constexpr int LW = lw_of(N);
+  const float* lrow = s.lv + b * s.lv_bs + (long)t * LW;
+  const float* frow = s.fl + b * s.fl_bs + (long)t * 256;
+  in.M4 = *reinterpret_cast<const f4*>(frow + c16 * 16 + 4 * g);
+  in.s1k = lrow[c16];
+  if constexpr (N >= 2) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) in.s2r[r] = lrow[16 + (4 * g + r) * 16 + c16];
+  }
+  if constexpr (N >= 3) {
+#pragma unroll
+    for (int jj = 0; jj < 4; ++jj)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) in.s3r[jj][r] = lrow[272 + (4 * g + r) * 256 + (4 * w + jj) * 16 + c16];
+  }
+}
+
+template <int N, bool SUMMARY>
+__global__ __launch_bounds__(N >= 3 ? 256 : 64) void k_scan(Seq s) {
+  constexpr int LW = lw_of(N);
+  __shared__ __align__(16) float s3[N >= 3 ? 16 * SP : 4];
+  __shared__ __align__(16) float y3[N >= 3 ? 16 * SP : 4];
+  __shared__ __align__(16) float s2[16 * RP];
+  __shared__ __align__(16) float s1[16];
+  const int tid = threadIdx.x, w = tid >> 6, l = tid & 63, g = l >> 4, c16 = l & 15;
+  const int c = blockIdx.x, b = blockIdx.y;
+  const int t0 = c * s.T, Tc = min(s.T, s.n - t0);
+  const float* ini = s.init ? s.init + b * s.init_bs + (long)c * LW : nullptr;
+  if (tid < 16) s1[tid] = ini ? ini[tid] : 0.0f;
+  if constexpr (N >= 2) {
+    for (int e = tid; e < 256; e += blockDim.x) s2[(e >> 4) * RP + (e & 15)] = ini ? ini[16 + e] : 0.0f;
+  }
+  if constexpr (N >= 3) {
+    for (int e = tid; e < 4096; e += blockDim.x)
+      s3[(e >> 8) * SP + ((e >> 4) & 15) * RP + (e & 15)] = ini ? ini[272 + e] : 0.0f;
+  }
+  // chunk flow product (SUMMARY): result layout, lane holds Mc[4g + r][c16]
+  constexpr int WL1 = N >= 3 ? 1 : 0, WMC = N >= 3 ? 2 : 0;
+  f4 Mc;
+#pragma unroll
+  for (int r = 0; r < 4; ++r) Mc[r] = (4 * g + r == c16) ? 1.0f : 0.0f;
+  __syncthreads();
+  StepIn<N> cur, nxt;
+  if (Tc > 0) load_step<N>(s, b, t0, w, g, c16, cur);
+  float* orow0 = s.rows ? s.rows + b * s.rows_bs + (long)t0 * s.rows_ld : nullptr;
+  for (int t = 0; t < Tc; ++t) {
+    if (t + 1 < Tc) load_step<N>(s, b, t0 + t + 1, w, g, c16, nxt);
+    const f4 M4 = cur.M4;
+    // ---------------- phase A: modes 3 and 2 of level 3 (slices i = 4w + ii), level 2 (wave 0), level 1
+    if constexpr (N >= 3) {
+#pragma unroll
+      for (int ii = 0; ii < 4; ++ii) {
+        const int i = 4 * w + ii;
+        const f4 A4 = *reinterpret_cast<const f4*>(s3 + i * SP + c16 * RP + 4 * g);  // S3[i][c16][4g + s]
+        f4 x = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int k = 0; k < 4; ++k) x = mfma(A4[k], M4[k], x);  // X[i][4g + r][c16] = sum_k S3[i][.][k] M[c16][k]
+        const f4 S2i = *reinterpret_cast<const f4*>(s2 + i * RP + 4 * g);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) x[r] = fmaf(S2i[r], cur.s1k, x[r]);  // + S2[i][4g + r] s1[c16]
+        f4 y = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int r = 0; r < 4; ++r) y = mfma(M4[r], x[r], y);  // Y[i][4g + r][c16] = sum_j M[.][j] X[i][j][c16]
+        const float S1i = s1[i];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) y3[i * SP + (4 * g + r) * RP + c16] = fmaf(S1i, cur.s2r[r], y[r]);
+      }
+    }
+    f4 n2 = {0.0f, 0.0f, 0.0f, 0.0f};
+    if constexpr (N >= 2) {
+      if (w == 0) {
+        const f4 A4 = *reinterpret_cast<const f4*>(s2 + c16 * RP + 4 * g);  // S2[c16][4g + s]
+        f4 x = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int k = 0; k < 4; ++k) x = mfma(A4[k], M4[k], x);  // (S2 M^T)[4g + r][c16]
+        const f4 S1g = *reinterpret_cast<const f4*>(s1 + 4 * g);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) x[r] = fmaf(S1g[r], cur.s1k, x[r]);  // + S1[4g + r] s1[c16]
+#pragma unroll
+        for (int r = 0; r < 4; ++r) n2 = mfma(M4[r], x[r], n2);  // M (.) : S2'[4g + r][c16] - s2
+#pragma unroll
+        for (int r = 0; r < 4; ++r) n2[r] += cur.s2r[r];
+      }
+    }
+    float n1 = 0.0f;
+    if (w == WL1) {
+      const f4 S1g = *reinterpret_cast<const f4*>(s1 + 4 * g);
+      float part = 0.0f;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) part = fmaf(M4[r], S1g[r], part);  // sum over j = 4g + r of M[c16][j] S1[j]
+      part += __shfl_xor(part, 16, 64);
+      part += __shfl_xor(part, 32, 64);
+      n1 = part + cur.s1k;
+    }
+    if constexpr (SUMMARY) {
+      if (w == WMC) {
+        f4 m = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int r = 0; r < 4; ++r) m = mfma(M4[r], Mc[r], m);  // M_t Mc
+        Mc = m;
+      }
+    }
+    __syncthreads();
+    // ---------------- phase B: mode 1 of level 3 (tiles j = 4w + jj), write the new state
+    float* orow = (!SUMMARY && orow0) ? orow0 + (long)t * s.rows_ld : nullptr;
+    if (orow && s.lvl0 && tid == 0) orow[0] = 1.0f;
+    float* orl = orow ? orow + s.lvl0 : nullptr;
+    if constexpr (N >= 3) {
+#pragma unroll
+      for (int jj = 0; jj < 4; ++jj) {
+        const int j = 4 * w + jj;
+        f4 z = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int k = 0; k < 4; ++k) z = mfma(M4[k], y3[(4 * g + k) * SP + j * RP + c16], z);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const float v = z[r] + cur.s3r[jj][r];
+          s3[(4 * g + r) * SP + j * RP + c16] = v;
+          if (orl) put(s, orl, N, 272 + (4 * g + r) * 256 + j * 16 + c16, v);
+        }
+      }
+    }
+    if constexpr (N >= 2) {
+      if (w == 0) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          s2[(4 * g + r) * RP + c16] = n2[r];
+          if (orl) put(s, orl, N, 16 + (4 * g + r) * 16 + c16, n2[r]);
+        }
+      }
+    }
+    if (w == WL1 && l < 16) {
+      s1[c16] = n1;
+      if (orl) put(s, orl, N, c16, n1);
+    }
+    __syncthreads();
+    cur = nxt;
+  }
+  if constexpr (SUMMARY) {
+    float* so = s.summ + ((long)b * s.C + c) * LW;
+    for (int e = tid; e < LW; e += blockDim.x) {
+      float v;
+      if (e < 16) v = s1[e];
+      else if (e < 272) v = s2[((e - 16) >> 4) * RP + ((e - 16) & 15)];
+      else {
+        const int f = e - 272;
+        v = s3[(f >> 8) * SP + ((f >> 4) & 15) * RP + (f & 15)];
+      }
+      so[e] = v;
+    }
+    if (w == WMC) {
+      float* mo = s.sfl + ((long)b * s.C + c) * 256;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) mo[(4 * g + r) * 16 + c16] = Mc[r];
+    }
+  }
+}
+
+// ------------------------------------------------------------------------------------------------ readouts
+// zero state rows (carries row 0)
+__global__ void k_zero_rows(float* base, long stride, int n_rows, int width) {
+  const int r = blockIdx.y;
+  if (r >= n_rows) return;
+  for (int e = blockIdx.x * blockDim.x + threadIdx.x; e < width; e += gridDim.x * blockDim.x)
+    base[(long)r * stride + e] = 0.0f;
+}
+// terminal row: the carry after the last chunk, unpadded, with the level-0 column
+__global__ void k_terminal(Args a) {
+  const int b = blockIdx.y;
+  const float* src = a.car + ((size_t)b * (a.C + 1) + a.C) * a.LW;
+  float* o = a.out + (size_t)b * a.W;
+  if (a.lvl0 && blockIdx.x == 0 && threadIdx.x == 0) o[0] = 1.0f;
+  for (int e = blockIdx.x * blockDim.x + threadIdx.x; e < a.LW; e += gridDim.x * blockDim.x) {
+    const long oi = out_index(a.N, a.d, e);
+    if (oi >= 0) o[a.lvl0 + oi] = src[e];
+  }
+}
+// mean / max over the prefix rows (ews/layer.py:261-264), per output column
+__global__ void k_reduce(Args a) {
+  const int b = blockIdx.y;
+  const int col = blockIdx.x * blockDim.x + threadIdx.x;
+  if (col >= a.W) return;
+  const float* p = a.pre + (size_t)b * a.n_int * a.W + col;
+  float acc = a.readout == EWS_READOUT_MAX ? p[0] : 0.0f;
+  for (int t = 0; t < a.n_int; ++t) {
+    const float v = p[(size_t)t * a.W];
+    acc = a.readout == EWS_READOUT_MAX ? fmaxf(acc, v) : acc + v;
+  }
+  a.out[(size_t)b * a.W + col] = a.readout == EWS_READOUT_MAX ? acc : acc / (float)a.n_int;
+}
+// given levels (B, n, D) packed and flows (B, n, d, d) -> padded loc / fl (the combine-only entry point)
+__global__ void k_pad_inputs(Args a, const float* levels, const float* flows) {
+  const long it = blockIdx.x;
+  const int b = (int)(it / a.n_int), t = (int)(it - (long)b * a.n_int);
+  const int D = a.W - a.lvl0;
+  const float* lv = levels + ((size_t)b * a.n_int + t) * D;
+  float* lo = a.loc + ((size_t)b * a.n_int + t) * a.LW;
+  for (int e = threadIdx.x; e < a.LW; e += blockDim.x) {
+    const long oi = out_index(a.N, a.d, e);
+    lo[e] = oi >= 0 ? lv[oi] : 0.0f;
+  }
+  const float* fi = flows + ((size_t)b * a.n_int + t) * a.d * a.d;
+  float* fo = a.fl + ((size_t)b * a.n_int + t) * 256;
+  for (int e = threadIdx.x; e < 256; e += blockDim.x) {
+    const int i = e >> 4, j = e & 15;
+    fo[e] = (i < a.d && j < a.d) ? fi[i * a.d + j] : (i == j ? 1.0f : 0.0f);
+  }
+}
+// padded loc / fl -> packed levels (B, n, D) and flows (B, n, d, d) (the leaf-only entry point)
+__global__ void k_unpad_outputs(Args a, float* levels, float* flows) {
+  const long it = blockIdx.x;
+  const int b = (int)(it / a.n_int), t = (int)(it - (long)b * a.n_int);
+  const int D = a.W - a.lvl0;
+  const float* lo = a.loc + ((size_t)b * a.n_int + t) * a.LW;
+  float* lv = levels + ((size_t)b * a.n_int + t) * D;
+  for (int e = threadIdx.x; e < a.LW; e += blockDim.x) {
+    const long oi = out_index(a.N, a.d, e);
+    if (oi >= 0) lv[oi] = lo[e];
+  }
+  const float* fo = a.fl + ((size_t)b * a.n_int + t) * 256;
+  float* fi = flows + ((size_t)b * a.n_int + t) * a.d * a.d;
+  for (int e = threadIdx.x; e < 256; e += blockDim.x) {
+    const int i = e >> 4, j = e & 15;
+    if (i < a.d && j < a.d) fi[i * a.d + j] = fo[e];
+  }
+}
+
+}  // namespace dense
+}  // namespace ews
+
+// ================================================================================================= C ABI
+namespace {
+
+using namespace ews::dense;
+
+size_t al256(size_t x) { return (x + 255) & ~(size_t)255; }
+
+struct DPlan {
+  int B, L, n_int, d, N, q, QB, T, C, LW, D, W, npow;
+};
+
+int dense_plan(const ews_dense_desc* s, DPlan& p) {
+  if (!s) return EWS_ERR_NULL;
+  if (s->depth < 1 || s->depth > 3) return EWS_ERR_DEPTH;
+  if (s->flow_mode < 0 || s->flow_mode > 2) return EWS_ERR_OPTION;
+  if (s->readout < 0 || s->readout > 3) return EWS_ERR_OPTION;
+  if (s->batch < 1 || s->length < 2 || s->dim < 1 || s->dim > 16) return EWS_ERR_SHAPE;
+  if (s->series_q < 0 || s->series_q > QMAX) return EWS_ERR_OPTION;
+  if (s->flow_mode == EWS_FLOW_CACHED_BASEPOINT && s->length < 3) return EWS_ERR_SHAPE;
+  if (s->chunk < 0) return EWS_ERR_SHAPE;
+  p.B = s->batch;
+  p.L = s->length;
+  p.n_int = p.L - 1;
+  p.d = s->dim;
+  p.N = s->depth;
+  p.q = s->series_q;
+  p.QB = p.q <= 4 ? 4 : p.q <= 8 ? 8 : p.q <= 12 ? 12 : p.q <= 16 ? 16 : p.q <= 20 ? 20 : p.q <= 24 ? 24
+       : p.q <= 32 ? 32 : 40;
+  p.T = s->chunk ? s->chunk : 64;
+  p.C = (p.n_int + p.T - 1) / p.T;
+  p.LW = lw_of(p.N);
+  p.D = 0;
+  for (int k = 1, m = 1; k <= p.N; ++k) {
+    m *= p.d;
+    p.D += m;
+  }
+  p.W = p.D + (s->level0 ? 1 : 0);
+  p.npow = (p.q > PM ? p.q : PM) + 1;
+  return EWS_OK;
+}
+
+struct DWs {
+  size_t apow, loc, fl, summ, sfl, car, pre, total;
+};
+DWs dense_ws(const DPlan& p, int readout) {
+  DWs w;
+  size_t off = 0;
+  const size_t BC = (size_t)p.B * p.C, BN = (size_t)p.B * p.n_int;
+  w.apow = off; off += al256(((size_t)p.npow * 256 + 1) * 4);
+  w.loc = off; off += al256(BN * p.LW * 4);
+  w.fl = off; off += al256(BN * 256 * 4);
+  w.summ = off; off += al256(BC * p.LW * 4);
+  w.sfl = off; off += al256(BC * 256 * 4);
+  w.car = off; off += al256((size_t)p.B * (p.C + 1) * p.LW * 4);
+  w.pre = off; off += (readout == EWS_READOUT_MEAN || readout == EWS_READOUT_MAX) ? al256(BN * p.W * 4) : 0;
+  w.total = off;
+  return w;
+}
+
+Args dense_args(const ews_dense_desc* s, const DPlan& p, const float* path, const float* clock, const float* A,
+                float* out, void* workspace) {
+  Args a{};
+  a.B = p.B; a.L = p.L; a.n_int = p.n_int; a.d = p.d; a.N = p.N; a.q = p.q;
+  a.flow_mode = s->flow_mode; a.readout = s->readout; a.lvl0 = s->level0 ? 1 : 0; a.W = p.W; a.LW = p.LW;
+  a.T = p.T; a.C = p.C; a.npow = p.npow;
+  a.path = path; a.clock = clock; a.A = A; a.out = out;
+  const DWs w = dense_ws(p, s->readout);
+  char* ws = (char*)workspace;
+  a.apow = (float*)(ws + w.apow); a.loc = (float*)(ws + w.loc); a.fl = (float*)(ws + w.fl);
+  a.summ = (float*)(ws + w.summ); a.sfl = (float*)(ws + w.sfl); a.car = (float*)(ws + w.car);
+  a.pre = (float*)(ws + w.pre);
+  return a;
+}
+
+#define DENSE_CHECK()                                          \
+  do {                                                         \
+    if (hipGetLastError() != hipSuccess) return EWS_ERR_LAUNCH; \
+  } while (0)
+
+int launch_local(const DPlan& p, const Args& a, hipStream_t st) {
+  const long total = (long)p.B * p.n_int;
+  const int grid = (int)(total < 4096 ? total : 4096);
+#define EWS_LOCAL(NN, QQ) hipLaunchKernelGGL((k_local<NN, QQ>), dim3(grid), dim3(256), 0, st, a)
+#define EWS_LOCAL_Q(NN)                          \
+  switch (p.QB) {                                \
+    case 4: EWS_LOCAL(NN, 4); break;             \
+    case 8: EWS_LOCAL(NN, 8); break;             \
+    case 12: EWS_LOCAL(NN, 12); break;           \
+    case 16: EWS_LOCAL(NN, 16); break;           \
+    case 20: EWS_LOCAL(NN, 20); break;           \
+    case 24: EWS_LOCAL(NN, 24); break;           \
+    case 32: EWS_LOCAL(NN, 32); break;           \
+    default: EWS_LOCAL(NN, 40); break;           \
+  }
+  if (p.N == 1) { EWS_LOCAL_Q(1) }
+  else if (p.N == 2) { EWS_LOCAL_Q(2) }
+  else { EWS_LOCAL_Q(3) }
+#undef EWS_LOCAL_Q
+#undef EWS_LOCAL
+  DENSE_CHECK();
+  return EWS_OK;
+}
+
+template <bool SUMMARY>
+int launch_scan(int N, const Seq& s, dim3 grid, hipStream_t st) {
+  if (N == 3) hipLaunchKernelGGL((k_scan<3, SUMMARY>), grid, dim3(256), 0, st, s);
+  else if (N == 2) hipLaunchKernelGGL((k_scan<2, SUMMARY>), grid, dim3(64), 0, st, s);
+  else hipLaunchKernelGGL((k_scan<1, SUMMARY>), grid, dim3(64), 0, st, s);
+  DENSE_CHECK();
+  return EWS_OK;
+}
+
+// passes 1..3 (combine): summaries, carries, outputs
+int dense_combine_pass(const ews_dense_desc* s, const DPlan& p, const Args& a, hipStream_t st, int pass) {
+  switch (pass) {
+    case 1: {
+      Seq q{};
+      q.lv = a.loc; q.lv_bs = (long)p.n_int * p.LW; q.fl = a.fl; q.fl_bs = (long)p.n_int * 256;
+      q.n = p.n_int; q.T = p.T; q.summ = a.summ; q.sfl = a.sfl; q.C = p.C; q.d = p.d;
+      return launch_scan<true>(p.N, q, dim3(p.C, p.B), st);
+    }
+    case 2: {
+      hipLaunchKernelGGL(k_zero_rows, dim3(1, p.B), dim3(256), 0, st, a.car, (long)(p.C + 1) * p.LW, p.B, p.LW);
+      DENSE_CHECK();
+      Seq q{};
+      q.lv = a.summ; q.lv_bs = (long)p.C * p.LW; q.fl = a.sfl; q.fl_bs = (long)p.C * 256;
+      q.n = p.C; q.T = p.C; q.rows = a.car + p.LW; q.rows_bs = (long)(p.C + 1) * p.LW; q.rows_ld = p.LW;
+      q.padded = 1; q.lvl0 = 0; q.d = p.d; q.C = 1;
+      return launch_scan<false>(p.N, q, dim3(1, p.B), st);
+    }
+    case 3: {
+      if (s->readout == EWS_READOUT_TERMINAL) {
+        hipLaunchKernelGGL(k_terminal, dim3((p.LW + 255) / 256, p.B), dim3(256), 0, st, a);
+        DENSE_CHECK();
+        return EWS_OK;
+      }
+      const bool red = s->readout != EWS_READOUT_PREFIX;
+      Seq q{};
+      q.lv = a.loc; q.lv_bs = (long)p.n_int * p.LW; q.fl = a.fl; q.fl_bs = (long)p.n_int * 256;
+      q.n = p.n_int; q.T = p.T; q.init = a.car; q.init_bs = (long)(p.C + 1) * p.LW;
+      q.rows = red ? a.pre : a.out; q.rows_bs = (long)p.n_int * p.W; q.rows_ld = p.W; q.padded = 0;
+      q.lvl0 = red ? 1 : (s->level0 ? 1 : 0); q.d = p.d; q.C = p.C;
+      if (red && !s->level0) return EWS_ERR_OPTION;  // mean / max rows carry the level-0 column
+      const int rc = launch_scan<false>(p.N, q, dim3(p.C, p.B), st);
+      if (rc != EWS_OK || !red) return rc;
+      hipLaunchKernelGGL(k_reduce, dim3((p.W + 255) / 256, p.B), dim3(256), 0, st, a);
+      DENSE_CHECK();
+      return EWS_OK;
+    }
+    default:
+      return EWS_ERR_OPTION;
+  }
+}
+
+int dense_forward_pass(const ews_dense_desc* s, const DPlan& p, const Args& a, hipStream_t st, int pass) {
+  if (pass == 0) {
+    hipLaunchKernelGGL(k_powers, dim3(1), dim3(256), 0, st, a);
+    DENSE_CHECK();
+    return launch_local(p, a, st);
+  }
+  return dense_combine_pass(s, p, a, st, pass);
+}
+
+constexpr int kDenseForwardPasses = 4;
+
+}  // namespace
+
+extern "C" {
+
+size_t ews_dense_workspace_bytes(const ews_dense_desc* desc) {
+  DPlan p;
+  if (dense_plan(desc, p) != EWS_OK) return 0;
+  return dense_ws(p, desc->readout).total;
+}
+
+int ews_dense_num_passes(void) { return kDenseForwardPasses; }
+
+int ews_dense_forward_pass(const ews_dense_desc* desc, int pass, const float* path, const float* clock,
+                           const float* A, float* out, void* workspace, ews_stream_t stream) {
+  DPlan p;
+  const int rc = dense_plan(desc, p);
+  if (rc != EWS_OK) return rc;
+  if (!path || !clock || !A || !out || !workspace) return EWS_ERR_NULL;
+  if (pass < 0 || pass >= kDenseForwardPasses) return EWS_ERR_OPTION;
+  const Args a = dense_args(desc, p, path, clock, A, out, workspace);
+  return dense_forward_pass(desc, p, a, (hipStream_t)stream, pass);
+}
+
+int ews_dense_forward(const ews_dense_desc* desc, const float* path, const float* clock, const float* A,
+                      float* out, void* workspace, ews_stream_t stream) {
+  for (int pass = 0; pass < kDenseForwardPasses; ++pass) {
+    const int rc = ews_dense_forward_pass(desc, pass, path, clock, A, out, workspace, stream);
+    if (rc != EWS_OK) return rc;
+  }
+  return EWS_OK;
+}
+
+int ews_dense_local_terms(const ews_dense_desc* desc, const float* path, const float* clock, const float* A,
+                          float* levels, float* flows, void* workspace, ews_stream_t stream) {
+  DPlan p;
+  const int rc = dense_plan(desc, p);
+  if (rc != EWS_OK) return rc;
+  if (!path || !clock || !A || !levels || !flows || !workspace) return EWS_ERR_NULL;
+  ews_dense_desc s = *desc;
+  s.level0 = 0;
+  DPlan q = p;
+  q.W = p.D;
+  const Args a = dense_args(&s, q, path, clock, A, nullptr, workspace);
+  hipStream_t st = (hipStream_t)stream;
+  const int r0 = dense_forward_pass(&s, q, a, st, 0);
+  if (r0 != EWS_OK) return r0;
+  hipLaunchKernelGGL(k_unpad_outputs, dim3(p.B * p.n_int), dim3(256), 0, st, a, levels, flows);
+  DENSE_CHECK();
+  return EWS_OK;
+}
+
+int ews_dense_combine(const ews_dense_desc* desc, const float* levels, const float* flows, float* out,
+                      void* workspace, ews_stream_t stream) {
+  DPlan p;
+  const int rc = dense_plan(desc, p);
+  if (rc != EWS_OK) return rc;
+  if (!levels || !flows || !out || !workspace) return EWS_ERR_NULL;
+  Args a = dense_args(desc, p, nullptr, nullptr, nullptr, out, workspace);
+  hipStream_t st = (hipStream_t)stream;
+  // k_pad_inputs reads levels with the packed width D = W - lvl0
+  hipLaunchKernelGGL(k_pad_inputs, dim3(p.B * p.n_int), dim3(256), 0, st, a, levels, flows);
+  DENSE_CHECK();
+  for (int pass = 1; pass < kDenseForwardPasses; ++pass) {
+    const int r = dense_combine_pass(desc, p, a, st, pass);
+    if (r != EWS_OK) return r;
+  }
+  return EWS_OK;
+}
+
+}  // extern "C"

@@ -33,6 +33,12 @@ EXPORTED = (
     "ews_diag_num_passes",
     "ews_error_string",
     "ews_version",
+    "ews_dense_workspace_bytes",
+    "ews_dense_forward",
+    "ews_dense_forward_pass",
+    "ews_dense_num_passes",
+    "ews_dense_local_terms",
+    "ews_dense_combine",
 )
 
 
@@ -47,6 +53,20 @@ class DiagDesc(ctypes.Structure):
         ("readout", ctypes.c_int32),
         ("level0", ctypes.c_int32),
         ("path_dtype", ctypes.c_int32),
+        ("chunk", ctypes.c_int32),
+    ]
+
+
+class DenseDesc(ctypes.Structure):
+    _fields_ = [
+        ("batch", ctypes.c_int32),
+        ("length", ctypes.c_int32),
+        ("dim", ctypes.c_int32),
+        ("depth", ctypes.c_int32),
+        ("series_q", ctypes.c_int32),
+        ("flow_mode", ctypes.c_int32),
+        ("readout", ctypes.c_int32),
+        ("level0", ctypes.c_int32),
         ("chunk", ctypes.c_int32),
     ]
 
@@ -89,6 +109,19 @@ def load():
     lib.ews_error_string.restype = ctypes.c_char_p
     lib.ews_version.argtypes = []
     lib.ews_version.restype = ctypes.c_char_p
+    ddp = ctypes.POINTER(DenseDesc)
+    lib.ews_dense_workspace_bytes.argtypes = [ddp]
+    lib.ews_dense_workspace_bytes.restype = sz
+    lib.ews_dense_forward.argtypes = [ddp, vp, vp, vp, vp, vp, vp]
+    lib.ews_dense_forward.restype = i32
+    lib.ews_dense_forward_pass.argtypes = [ddp, i32, vp, vp, vp, vp, vp, vp]
+    lib.ews_dense_forward_pass.restype = i32
+    lib.ews_dense_num_passes.argtypes = []
+    lib.ews_dense_num_passes.restype = i32
+    lib.ews_dense_local_terms.argtypes = [ddp, vp, vp, vp, vp, vp, vp, vp]
+    lib.ews_dense_local_terms.restype = i32
+    lib.ews_dense_combine.argtypes = [ddp, vp, vp, vp, vp, vp]
+    lib.ews_dense_combine.restype = i32
     _lib = lib
     return lib
 

@@ -12,7 +12,11 @@ ews/core/kernels/combine.py:37-63):
         leaf "block_series" or "series"              the same fused kernel: its closed forms are the q -> infinity
                                                      limit of the series leaves (they agree to the series' own
                                                      truncation bound, ews/core/series_leaf.py:129-143)
-    anything else                                    NotImplementedError (dense generators)
+    any generator (dense A, d <= 16), leaf "series",
+        depths 1-3; planes / diagonals at depth 3    dense kernels: series leaf of order series_q, flows
+                                                     exp(-h A) evaluated in the kernel (chen_expm "exact"),
+                                                     MFMA Chen mode products (forward only)
+    anything else                                    NotImplementedError
 """
 
 from __future__ import annotations
@@ -134,24 +138,36 @@ class EWS(torch.nn.Module):
         return torch.diagonal(A).contiguous()
 
     def _engine_check(self):
-        if self.structure is not None and self.leaf in ("plane_closed", "block_series", "series"):
-            if self.N > 2:
-                raise NotImplementedError(
-                    f"leaf={self.leaf!r}: closed-form local terms exist for depths 1 and 2"
-                )
+        if self.structure is not None and self.leaf in ("plane_closed", "block_series", "series") and self.N <= 2:
             if self.structure == "planes" and self.d % 2:
                 raise ValueError("leaf='plane_closed' needs an even dimension (2x2 planes)")
             return "diag"
+        if self.leaf == "series":
+            if self.N > 3 or self.d > 16:
+                raise NotImplementedError("the dense-generator kernels cover depths 1-3 and d <= 16")
+            if self.chen_expm != "exact":
+                raise NotImplementedError(
+                    f"the dense-generator kernels evaluate exact flows exp(-h A) (chen_expm='exact'), "
+                    f"got chen_expm={self.chen_expm!r}"
+                )
+            return "dense"
+        if self.structure is not None and self.N > 2:
+            raise NotImplementedError(
+                f"leaf={self.leaf!r}: closed-form local terms exist for depths 1 and 2 (use leaf='series' at depth 3)"
+            )
         raise NotImplementedError(
-            f"no MI355X kernel for leaf={self.leaf!r} with a dense generator in this build: use a rotation-plane or "
-            "diagonal parametrisation with leaf='plane_closed' / 'block_series' / 'series'"
+            f"no MI355X kernel for leaf={self.leaf!r} with a dense generator in this build: use leaf='series' "
+            "(any generator, depths 1-3) or a rotation-plane / diagonal parametrisation with leaf='plane_closed'"
         )
 
     def _run(self, path, clock, readout, level0, a_scale):
-        self._engine_check()
+        engine = self._engine_check()
         if self.dtype != torch.float32:
             raise TypeError("the MI355X kernels compute in float32 (dtype=torch.float32)")
         A = self.A_param().to(torch.float32) * torch.as_tensor(a_scale, dtype=torch.float32, device=path.device)
+        if engine == "dense":
+            return ops.dense_scan(path.to(torch.float32), clock.to(torch.float32), A.to(path.device).contiguous(),
+                                  self.N, self.series_q, self._flow_mode(readout), readout, level0)
         params = self._diag_params(A.to(path.device))
         if path.dtype != torch.bfloat16:
             path = path.to(torch.float32)

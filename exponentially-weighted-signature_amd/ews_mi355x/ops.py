@@ -85,3 +85,96 @@ def diag_scan(path, clock, params, N, structure, flow_mode="per_interval", reado
           "cached_basepoint": nat.FLOW_CACHED_BASEPOINT}[flow_mode]
     st = {"planes": nat.STRUCT_PLANES, "real_diag": nat.STRUCT_REAL_DIAG}[structure]
     return DiagScan.apply(path, clock, params, int(N), st, fm, readout, bool(level0), int(chunk))
+
+
+# ---------------------------------------------------------------------------------------------- dense generators
+_FLOW_MODES = {"per_interval": nat.FLOW_PER_INTERVAL, "cached": nat.FLOW_CACHED,
+               "cached_basepoint": nat.FLOW_CACHED_BASEPOINT}
+
+
+def make_dense_desc(B, L, d, N, q, flow_mode, readout, level0, chunk=0):
+    return nat.DenseDesc(B, L, d, N, int(q), _FLOW_MODES[flow_mode], nat.READOUTS[readout], int(level0),
+                         int(chunk))
+
+
+def _check_dense(path, clock, A):
+    if not path.is_cuda:
+        raise RuntimeError("ews_mi355x runs on a HIP device only: move path/clock/A to the GPU (no CPU path)")
+    for name, x in (("path", path), ("clock", clock), ("A", A)):
+        if x.dtype != torch.float32:
+            raise TypeError(f"{name} must be float32 for the dense-generator kernels, got {x.dtype}")
+
+
+class DenseScan(torch.autograd.Function):
+    """out = EWS readout of (path, clock) under a dense generator A (series leaf of order q, exact flows).
+    Forward only: the dense-generator adjoint kernels are not part of this library yet, and a backward through
+    this op raises instead of falling back to another engine."""
+
+    @staticmethod
+    def forward(ctx, path, clock, A, N, q, flow_mode, readout, level0, chunk):
+        lib = nat.load()
+        _check_dense(path, clock, A)
+        path, clock, A = path.contiguous(), clock.contiguous(), A.contiguous()
+        B, L, d = path.shape
+        desc = make_dense_desc(B, L, d, N, q, flow_mode, readout, level0, chunk)
+        D = sum(d**k for k in range(1, N + 1))
+        W = D + (1 if level0 else 0)
+        shape = (B, L - 1, W) if readout == "prefix" else (B, W)
+        dev = path.device
+        out = torch.empty(shape, device=dev, dtype=torch.float32)
+        ws = torch.empty(int(lib.ews_dense_workspace_bytes(ctypes.byref(desc))), device=dev, dtype=torch.uint8)
+        rc = lib.ews_dense_forward(ctypes.byref(desc), path.data_ptr(), clock.data_ptr(), A.data_ptr(),
+                                   out.data_ptr(), ws.data_ptr(), _stream_handle(dev))
+        nat.check(rc, "ews_dense_forward")
+        return out
+
+    @staticmethod
+    def backward(ctx, gout):
+        raise NotImplementedError(
+            "the dense-generator EWS (leaf='series' with a general A) has no backward kernels in this build")
+
+
+def dense_scan(path, clock, A, N, q, flow_mode="per_interval", readout="prefix", level0=True, chunk=0):
+    return DenseScan.apply(path, clock, A, int(N), int(q), flow_mode, readout, bool(level0), int(chunk))
+
+
+def dense_local_terms(path, clock, A, N, q, flow_mode="per_interval"):
+    """Series-leaf levels (B, L-1, sum_k d^k) packed and flows (B, L-1, d, d) on the GPU
+    (ews/core/leaf.py:111-114 and ews/core/chen_scan.py:155-168)."""
+    lib = nat.load()
+    _check_dense(path, clock, A)
+    path, clock, A = path.contiguous(), clock.contiguous(), A.contiguous()
+    B, L, d = path.shape
+    desc = make_dense_desc(B, L, d, N, q, flow_mode, "prefix", False)
+    D = sum(d**k for k in range(1, N + 1))
+    dev = path.device
+    levels = torch.empty((B, L - 1, D), device=dev, dtype=torch.float32)
+    flows = torch.empty((B, L - 1, d, d), device=dev, dtype=torch.float32)
+    ws = torch.empty(int(lib.ews_dense_workspace_bytes(ctypes.byref(desc))), device=dev, dtype=torch.uint8)
+    rc = lib.ews_dense_local_terms(ctypes.byref(desc), path.data_ptr(), clock.data_ptr(), A.data_ptr(),
+                                   levels.data_ptr(), flows.data_ptr(), ws.data_ptr(), _stream_handle(dev))
+    nat.check(rc, "ews_dense_local_terms")
+    return levels, flows
+
+
+def dense_combine(levels, flows, N, readout="prefix", level0=True, chunk=0):
+    """Chen combine of given packed levels (B, n, sum_k d^k) and flows (B, n, d, d)
+    (ews/core/kernels/combine.py:259-269, kind "dense_kernel")."""
+    lib = nat.load()
+    if not levels.is_cuda or levels.dtype != torch.float32 or flows.dtype != torch.float32:
+        raise TypeError("levels and flows must be float32 tensors on the HIP device")
+    levels, flows = levels.contiguous(), flows.contiguous()
+    B, n, d = flows.shape[0], flows.shape[1], flows.shape[2]
+    desc = make_dense_desc(B, n + 1, d, N, 0, "per_interval", readout, level0, chunk)
+    D = sum(d**k for k in range(1, N + 1))
+    if levels.shape != (B, n, D):
+        raise ValueError(f"levels must be {(B, n, D)}, got {tuple(levels.shape)}")
+    W = D + (1 if level0 else 0)
+    shape = (B, n, W) if readout == "prefix" else (B, W)
+    out = torch.empty(shape, device=levels.device, dtype=torch.float32)
+    ws = torch.empty(int(lib.ews_dense_workspace_bytes(ctypes.byref(desc))), device=levels.device,
+                     dtype=torch.uint8)
+    rc = lib.ews_dense_combine(ctypes.byref(desc), levels.data_ptr(), flows.data_ptr(), out.data_ptr(),
+                               ws.data_ptr(), _stream_handle(levels.device))
+    nat.check(rc, "ews_dense_combine")
+    return out

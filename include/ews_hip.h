@@ -98,6 +98,51 @@ int ews_diag_backward_pass(const ews_diag_desc* desc, int pass, const void* path
 /* Number of passes: direction 0 = forward, 1 = backward. */
 int ews_diag_num_passes(int direction);
 
+/* ---------------------------------------------------------------------------------------------------------
+ * Dense generators: any d x d matrix A (d <= 16), depths 1-3, the series leaf (ews/core/series_leaf.py).
+ * Flows M_t = exp(-h_t A) are evaluated in the kernels (Taylor polynomial on a scaled argument, then
+ * squarings), replacing _chen_M_per_interval (ews/core/chen_scan.py:155-168) with chen_expm="exact".
+ * --------------------------------------------------------------------------------------------------------- */
+typedef struct ews_dense_desc {
+  int32_t batch;     /* B >= 1 */
+  int32_t length;    /* L >= 2 knots */
+  int32_t dim;       /* 1 <= d <= 16 */
+  int32_t depth;     /* N in {1, 2, 3} */
+  int32_t series_q;  /* series order q in [0, 40] (letters b_0..b_q, total order |m| <= q) */
+  int32_t flow_mode; /* EWS_FLOW_* */
+  int32_t readout;   /* EWS_READOUT_* (mean / max need level0 = 1) */
+  int32_t level0;    /* 1: rows carry the leading level-0 constant */
+  int32_t chunk;     /* intervals per chunk; 0 selects the default (64) */
+} ews_dense_desc;
+
+/* Scratch of the dense forward: powers table, padded local terms and flows (B, L-1, 16+256+4096 | 256),
+ * chunk summaries and carries. */
+size_t ews_dense_workspace_bytes(const ews_dense_desc* desc);
+
+/* Forward: path (B, L, d) f32, clock (B, L) f32, A (d, d) f32 row-major (reference sign), out f32
+ * [(B, L-1, W) for prefix, (B, W) otherwise], W = level0 + sum_k d^k. Replaces EWS._single_path with
+ * leaf="series" for a dense A: series_local_signatures (ews/core/series_leaf.py:116-126), the flows and the
+ * combine (ews/core/chen_scan.py:172-241; ews/core/kernels/pallas_combine.py:803-858 dense_kernel) and the
+ * readout (ews/layer.py:189-265). */
+int ews_dense_forward(const ews_dense_desc* desc, const float* path, const float* clock, const float* A,
+                      float* out, void* workspace, ews_stream_t stream);
+
+/* One pass of ews_dense_forward: 0 local terms + flows, 1 chunk summaries, 2 carry scan, 3 outputs. */
+int ews_dense_forward_pass(const ews_dense_desc* desc, int pass, const float* path, const float* clock,
+                           const float* A, float* out, void* workspace, ews_stream_t stream);
+int ews_dense_num_passes(void);
+
+/* The leaf alone: levels (B, L-1, sum_k d^k) packed as ews/core/chen_scan.py:33-46 and flows (B, L-1, d, d).
+ * Replaces local_signatures(kind="series") (ews/core/leaf.py:111-114) plus _chen_M_per_interval. */
+int ews_dense_local_terms(const ews_dense_desc* desc, const float* path, const float* clock, const float* A,
+                          float* levels, float* flows, void* workspace, ews_stream_t stream);
+
+/* The combine alone on given levels (B, L-1, sum_k d^k) and flows (B, L-1, d, d), with the readout of desc.
+ * Replaces combine_packed(kind="dense_kernel") (ews/core/kernels/combine.py:259-269 ->
+ * pallas_combine.py:2628 dense_general_prefix_vjp forward). */
+int ews_dense_combine(const ews_dense_desc* desc, const float* levels, const float* flows, float* out,
+                      void* workspace, ews_stream_t stream);
+
 /* Human-readable text of a return code. */
 const char* ews_error_string(int code);
 

@@ -109,3 +109,47 @@ def test_log_dims_mirror_reference():
     for d, N, expect in [(3, 3, 14), (4, 2, 10), (2, 4, 8)]:
         assert E.log_signature_dim(d, N) == expect
     assert E.log_level_slices(4, 2) == ((0, 4), (4, 10))
+
+
+def _ddesc(**kw):
+    base = dict(batch=2, length=10, dim=16, depth=3, series_q=20, flow_mode=0, readout=0, level0=1, chunk=0)
+    base.update(kw)
+    return nat.DenseDesc(**base)
+
+
+def test_dense_c_abi_error_codes():
+    lib = nat.load()
+    good = _ddesc()
+    ws = lib.ews_dense_workspace_bytes(ctypes.byref(good))
+    # powers table + padded levels/flows of 2 x 9 intervals + summaries + carries
+    assert ws >= 2 * 9 * (16 + 256 + 4096 + 256) * 4
+    assert lib.ews_dense_num_passes() == 4
+    null = ctypes.c_void_p(0)
+    assert lib.ews_dense_forward(ctypes.byref(good), null, null, null, null, null, null) == -1
+    bad = {
+        "depth": (_ddesc(depth=4), -3),
+        "too wide": (_ddesc(dim=17), -2),
+        "length": (_ddesc(length=1), -2),
+        "series order": (_ddesc(series_q=41), -4),
+        "readout": (_ddesc(readout=9), -4),
+        "flow mode": (_ddesc(flow_mode=3), -4),
+        "basepoint length": (_ddesc(flow_mode=2, length=2), -2),
+    }
+    for name, (dsc, code) in bad.items():
+        assert lib.ews_dense_forward(ctypes.byref(dsc), null, null, null, null, null, null) == code, name
+        assert lib.ews_dense_workspace_bytes(ctypes.byref(dsc)) == 0, name
+
+
+def test_dense_layer_routing_and_errors():
+    A = E.AParamGeneral(torch.zeros(4, 4))
+    assert E.EWS(A, N=3, leaf="series", series_q=8)._engine_check() == "dense"
+    assert E.EWS(_planes(2), N=3, leaf="series", series_q=8)._engine_check() == "dense"
+    assert E.EWS(_planes(2), N=2, leaf="series", series_q=8)._engine_check() == "diag"
+    with pytest.raises(NotImplementedError):
+        E.EWS(A, N=2)._engine_check()  # van_loan leaf with a dense generator
+    with pytest.raises(NotImplementedError):
+        E.EWS(A, N=3, leaf="series", series_q=8, chen_expm="cayley")._engine_check()
+    with pytest.raises(NotImplementedError):
+        E.EWS(E.AParamGeneral(torch.zeros(17, 17)), N=2, leaf="series", series_q=8)._engine_check()
+    with pytest.raises(RuntimeError, match="HIP device"):
+        E.EWS(A, N=3, leaf="series", series_q=8)(torch.zeros(5, 4), torch.linspace(0, 1, 5))
