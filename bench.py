@@ -30,6 +30,7 @@ for _p in (ROOT, PKG_DIR):
 import numpy as np  # noqa: E402
 
 HBM_PEAK_GBS = 8000.0
+MFMA_F32_PEAK_TFLOPS = 157.3
 FWD_PASS_NAMES = ["chunk_summary", "carry_scan", "chunk_output", "readout_reduce"]
 BWD_PASS_NAMES = ["chunk_adjoint_local", "adjoint_scan", "chunk_adjoint_full", "knot_grads", "param_grads"]
 
@@ -51,6 +52,117 @@ def make_inputs(B=32, L=17984, c=6, d=16, seed_cfg=2):
     dw = np.stack([damp, freq], -1).astype(np.float32)
     clock = np.broadcast_to((np.arange(L, dtype=np.float64) / L).astype(np.float32), (B, L)).copy()
     return path, clock, dw
+
+
+def _softplus(x):
+    return np.log1p(np.exp(-np.abs(x))) + np.maximum(x, 0.0)
+
+
+def c3_inputs(B=16, L=4096, c=8, d=16, seed_cfg=3):
+    """N(0,1) increments of c channels lifted to d by W ~ N(0, 1/c); generator
+    -diag(softplus(U(0,1))) + skew(N(0,0.1)) in the north star's sign, i.e. A_ref = diag(softplus(U)) - S with
+    S = (X - X^T)/sqrt(2), X ~ N(0, 0.1) (variance reading); input-dependent clock steps
+    softplus(w . dx_k + b), w, b ~ N(0, 0.1), dx_k the raw c-channel increment; theta_0 = 0."""
+    r0 = np.random.default_rng([seed_cfg, 0])
+    inc = r0.normal(0.0, 1.0, size=(B, L - 1, c))
+    raw = np.concatenate([np.zeros((B, 1, c)), np.cumsum(inc, 1)], 1)
+    Wl = np.random.default_rng([seed_cfg, 1]).normal(0.0, np.sqrt(1.0 / c), size=(d, c))
+    path = (raw @ Wl.T).astype(np.float32)
+    r2 = np.random.default_rng([seed_cfg, 2])
+    X = r2.normal(0.0, np.sqrt(0.1), size=(d, d))
+    A = (np.diag(_softplus(r2.uniform(0.0, 1.0, d))) - (X - X.T) / np.sqrt(2.0)).astype(np.float32)
+    r3 = np.random.default_rng([seed_cfg, 3])
+    w = r3.normal(0.0, np.sqrt(0.1), size=c)
+    b0 = r3.normal(0.0, np.sqrt(0.1))
+    steps = _softplus(inc @ w + b0)
+    clock = np.concatenate([np.zeros((B, 1)), np.cumsum(steps, 1)], 1).astype(np.float32)
+    return path, clock, A
+
+
+C3_CHEN_FLOPS = 427008  # per interval: 2 sum_k k d^(k+1) + 2 sum_k (k-1) d^k at d = 16, N = 3
+
+
+def bench_c3(args):
+    """Dense-generator forward at BASELINE.json configs[2]: B=16, L=4096, d=16, depth 3, series leaf (q=24),
+    input-dependent clock, prefix readout. One step = the four forward passes (leaf + flows, chunk summaries,
+    carry scan, output rows). Returns the JSON record."""
+    import torch
+
+    from ews_mi355x import _native as nat
+    from ews_mi355x.ops import make_dense_desc
+
+    dev = torch.device("cuda:0")
+    lib = nat.load()
+    B, L, d, N, q = 16, 4096, 16, 3, 24
+    path_np, clock_np, A_np = c3_inputs(B, L)
+    path = torch.tensor(path_np, device=dev)
+    clock = torch.tensor(clock_np, device=dev)
+    A = torch.tensor(A_np, device=dev)
+    D = d + d * d + d**3
+    W = D + 1
+    desc = make_dense_desc(B, L, d, N, q, "per_interval", "prefix", True, args.chunk)
+    ws = torch.empty(int(lib.ews_dense_workspace_bytes(ctypes.byref(desc))), device=dev, dtype=torch.uint8)
+    out = torch.empty((B, L - 1, W), device=dev, dtype=torch.float32)
+    npass = lib.ews_dense_num_passes()
+
+    def step(events=None):
+        stream = ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream)
+        for p in range(npass):
+            if events is not None:
+                events[p].record()
+            nat.check(lib.ews_dense_forward_pass(ctypes.byref(desc), p, path.data_ptr(), clock.data_ptr(),
+                                                 A.data_ptr(), out.data_ptr(), ws.data_ptr(), stream),
+                      "dense forward pass")
+        if events is not None:
+            events[npass].record()
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    evs_all = []
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(args.steps):
+        evs = [torch.cuda.Event(enable_timing=True) for _ in range(npass + 1)]
+        step(evs)
+        evs_all.append(evs)
+    end.record()
+    torch.cuda.synchronize()
+    ms = start.elapsed_time(end) / args.steps
+    names = ["local_terms", "chunk_summary", "carry_scan", "chunk_output"]
+    pass_ms = {nm: sum(e[i].elapsed_time(e[i + 1]) for e in evs_all) / args.steps for i, nm in enumerate(names)}
+    n = B * (L - 1)
+    flops = n * C3_CHEN_FLOPS
+    tf = flops / (pass_ms["chunk_output"] * 1e-3) / 1e12
+    rec = {
+        "metric": "EWS dense-generator forward time-steps/sec and fp32 MFMA TFLOP/s (% peak) on 1 MI355X",
+        "value": round(n / (ms * 1e-3), 1),
+        "unit": "time-steps/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic",
+        "config": {"workload": "c3: dense generator, B=16, L=4096, d=16, depth 3, series leaf q=24, "
+                               "input-dependent clock, prefix readout, forward", "global_batch": B, "seq_len": L,
+                   "parallelism": "none (1 GPU)"},
+        "roofline": {"bound": "mfma", "kernel": "chunk_output", "achieved": round(tf, 2),
+                     "peak": MFMA_F32_PEAK_TFLOPS, "unit": "TFLOP/s", "frac": round(tf / MFMA_F32_PEAK_TFLOPS, 4),
+                     "traffic": None},
+        "passes_ms": {k: round(v, 4) for k, v in pass_ms.items()},
+    }
+    if args.check:
+        from oracle import ews_oracle as O
+
+        got = out[0, :256].double().cpu()
+        ref = O.ews(torch.tensor(path_np[:1, :257]).double(), torch.tensor(clock_np[:1, :257]).double(),
+                    torch.tensor(A_np).double(), N, "prefix", leaf="series", series_q=q)[0]
+        rec["check_forward_relerr_vs_f64"] = float((got - ref).abs().max() / ref.abs().max())
+    return rec
 
 
 def algorithmic_bytes(B, L, d, W, s_in=4):
@@ -108,11 +220,19 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--check", action="store_true", help="also check one forward against the C float64 checker")
     ap.add_argument("--chunk", type=int, default=0, help="intervals per chunk (0: the library's default)")
+    ap.add_argument("--config", choices=["c2", "c3"], default="c2",
+                    help="c2 (default, the headline): planes fwd+bwd; c3: dense-generator depth-3 forward")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: --gpus {args.gpus} is not supported (the EWS scan here is single-GPU; "
               "multi-GPU sharding is a design note, not a measured path)", file=sys.stderr)
         sys.exit(2)
+    if args.config == "c3":
+        import torch
+
+        torch.cuda.set_device(0)
+        print(json.dumps(bench_c3(args)), flush=True)
+        return
 
     import torch
 

@@ -13,6 +13,7 @@ import numpy as np
 import pytest
 import torch
 
+import bench
 import ews_mi355x as E
 from ews_mi355x import ops
 from oracle import ews_oracle as O
@@ -28,29 +29,10 @@ def relerr(a, b):
     return float(np.max(np.abs(a - b)) / max(np.max(np.abs(b)), 1e-300))
 
 
-def _softplus(x):
-    return np.log1p(np.exp(-np.abs(x))) + np.maximum(x, 0.0)
-
-
-def c3_inputs(B, L, c=8, d=16, seed=3):
-    """BASELINE.json configs[2] recipe: N(0,1) increments of c channels lifted to d by W ~ N(0, 1/c); generator
-    -diag(softplus(U(0,1))) + skew(N(0,0.1)) in the north star's sign, i.e. A_ref = diag(softplus(U)) - S with
-    S = (X - X^T)/sqrt(2), X ~ N(0, 0.1) (variance); clock steps softplus(w . dx_k + b), w, b ~ N(0, 0.1)."""
-    r0 = np.random.default_rng([seed, 0])
-    inc = r0.normal(0.0, 1.0, size=(B, L - 1, c))
-    raw = np.concatenate([np.zeros((B, 1, c)), np.cumsum(inc, 1)], 1)
-    Wl = np.random.default_rng([seed, 1]).normal(0.0, np.sqrt(1.0 / c), size=(d, c))
-    path = raw @ Wl.T
-    r2 = np.random.default_rng([seed, 2])
-    X = r2.normal(0.0, np.sqrt(0.1), size=(d, d))
-    A = np.diag(_softplus(r2.uniform(0.0, 1.0, d))) - (X - X.T) / np.sqrt(2.0)
-    r3 = np.random.default_rng([seed, 3])
-    w = r3.normal(0.0, np.sqrt(0.1), size=c)
-    b0 = r3.normal(0.0, np.sqrt(0.1))
-    steps = _softplus(inc @ w + b0)
-    clock = np.concatenate([np.zeros((B, 1)), np.cumsum(steps, 1)], 1)
-    return (torch.tensor(path, dtype=torch.float32), torch.tensor(clock, dtype=torch.float32),
-            torch.tensor(A, dtype=torch.float32))
+def c3_inputs(B, L):
+    """BASELINE.json configs[2] recipe, from the bench (bench.c3_inputs), as float32 tensors."""
+    path, clock, A = bench.c3_inputs(B, L)
+    return torch.tensor(path), torch.tensor(clock), torch.tensor(A)
 
 
 def _random(B, L, d, seed, hscale=0.05, ascale=1.0):
