@@ -222,11 +222,25 @@ def main():
     ap.add_argument("--chunk", type=int, default=0, help="intervals per chunk (0: the library's default)")
     ap.add_argument("--config", choices=["c2", "c3"], default="c2",
                     help="c2 (default, the headline): planes fwd+bwd; c3: dense-generator depth-3 forward")
+    ap.add_argument("--clock-grad", action="store_true",
+                    help="also compute the clock gradient (the c2 clock is data; off by default)")
+    ap.add_argument("--copy-probe", action="store_true",
+                    help="first run a plain 1 GiB device-to-device copy (3 times): the reference kernel of known "
+                         "size that scales the FETCH_SIZE / WRITE_SIZE counters of a --pmc run")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: --gpus {args.gpus} is not supported (the EWS scan here is single-GPU; "
               "multi-GPU sharding is a design note, not a measured path)", file=sys.stderr)
         sys.exit(2)
+    if args.copy_probe:
+        import torch
+
+        src = torch.ones(1 << 28, device="cuda:0", dtype=torch.float32)
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
     if args.config == "c3":
         import torch
 
@@ -259,6 +273,9 @@ def main():
     out = torch.empty((B, L - 1, W), device=dev, dtype=torch.float32)
     dpath = torch.empty((B, L, d), device=dev, dtype=torch.float32)
     dclock = torch.empty((B, L), device=dev, dtype=torch.float32)
+    # the uniform clock is data, not a parameter: as in the reference (JAX computes no cotangent for an
+    # undifferentiated input), the backward returns the path and generator gradients; --clock-grad adds it
+    dclock_ptr = dclock.data_ptr() if args.clock_grad else None
     ddw = torch.empty_like(dw)
     nf, nb = lib.ews_diag_num_passes(0), lib.ews_diag_num_passes(1)
 
@@ -275,7 +292,7 @@ def main():
                 events[nf + p].record()
             nat.check(lib.ews_diag_backward_pass(ctypes.byref(desc), p, path.data_ptr(), clock.data_ptr(),
                                                  dw.data_ptr(), resid.data_ptr(), gout.data_ptr(),
-                                                 dpath.data_ptr(), dclock.data_ptr(), ddw.data_ptr(),
+                                                 dpath.data_ptr(), dclock_ptr, ddw.data_ptr(),
                                                  ws.data_ptr(), stream), "backward pass")
         if events is not None:
             events[nf + nb].record()
@@ -341,7 +358,8 @@ def main():
         "dtype": "f32",
         "data": "synthetic",
         "config": {"workload": "c2: single EWS layer, B=32, L=17984, d=16 (8 rotation planes), depth 2, fp32, "
-                               "prefix readout, forward + custom-VJP backward", "global_batch": B, "seq_len": L,
+                               "prefix readout, forward + custom-VJP backward (path and generator gradients"
+                               + (", clock gradient" if args.clock_grad else "") + ")", "global_batch": B, "seq_len": L,
                    "parallelism": "none (1 GPU)"},
         "hbm_gbs_effective": round(fwdbwd_bytes / (ms_per_step * 1e-3) / 1e9, 1),
         "hbm_frac_effective": round(fwdbwd_bytes / (ms_per_step * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),

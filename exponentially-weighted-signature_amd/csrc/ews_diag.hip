@@ -1577,7 +1577,7 @@ __global__ void k_knot_grads(DiagArgs a) {
       if (t >= 1) g += dvb[(size_t)(t - 1) * a.d + ch];
       if (t < a.n_int) g -= dvb[(size_t)t * a.d + ch];
       a.dpath[bt * a.d + ch] = g;
-    } else {
+    } else if (a.dclock) {  // null: the clock gradient is not requested
       float g = 0.0f;
       if (t >= 1) g += dhb[t - 1];
       if (t < a.n_int) g -= dhb[t];
@@ -1972,9 +1972,8 @@ int ews_diag_backward_pass(const ews_diag_desc* desc, int pass, const void* path
   Plan p;
   const int rc = make_plan(desc, p);
   if (rc != EWS_OK) return rc;
-  if (!path || !clock || !params || !residual || !grad_out || !grad_path || !grad_clock || !grad_params ||
-      !workspace)
-    return EWS_ERR_NULL;
+  if (!path || !clock || !params || !residual || !grad_out || !grad_path || !grad_params || !workspace)
+    return EWS_ERR_NULL;  // grad_clock may be null: the clock gradient is then not computed
   if (pass < 0 || pass >= kBackwardPasses) return EWS_ERR_OPTION;
   DiagArgs a = make_args(desc, p, path, clock, params, (void*)residual, workspace);
   a.gout = grad_out;

@@ -80,6 +80,14 @@ template <int I, int N, class F> __device__ __forceinline__ void static_for(F&& 
   }
 }
 
+// Compile-time loop I, I-1, ..., 0.
+template <int I, class F> __device__ __forceinline__ void static_down(F&& f) {
+  if constexpr (I >= 0) {
+    f(std::integral_constant<int, I>{});
+    static_down<I - 1>(f);
+  }
+}
+
 struct Lane {
   int gi, gl, j, kg;
 };
@@ -165,6 +173,64 @@ __device__ __forceinline__ void stage(const DiagArgs& a, int b, int cb, float* s
           const int gi = i / a.T, t = i - gi * a.T;
           s_h[gi * kMaxT + t] = y1[u] - y0[u];
         }
+      }
+    }
+  }
+}
+
+// Block staging of increments: SB steps of every group of the workgroup at a time, double-buffered in LDS
+// (buffer (blk & 1), group gi's step s at gi * VBLK + s * DIM). The loads of the next block are issued into
+// registers before the current block's steps and written to LDS after them, so the staging latency hides
+// behind SB steps and the LDS footprint stays at 2 x GPW x SB x 64 bytes.
+constexpr int SB = 16;           // steps per staged block
+constexpr int VBLK = SB * DIM;   // LDS floats per group and block buffer
+template <int GPW, bool BF16> struct VRaw {
+  static constexpr int IPS = BF16 ? 2 : 4;                  // 16-byte items per step
+  static constexpr int NI = (GPW * SB * IPS + 63) / 64;     // items per lane
+  f4a x0[NI], x1[NI];                                       // knots x_i, x_{i+1} (bf16: raw bits)
+};
+template <int GPW, bool BF16>
+__device__ __forceinline__ bool vblk_item(const DiagArgs& a, int cb, int blk, int item, int& gi, int& st, int& q,
+                                          int& idx) {
+  constexpr int IPS = VRaw<GPW, BF16>::IPS;
+  gi = item / (SB * IPS);
+  const int rem = item - gi * (SB * IPS);
+  st = rem / IPS;
+  q = rem - st * IPS;
+  const int c = cb + gi, t = blk * SB + st;
+  idx = c * a.T + t;
+  return item < GPW * SB * IPS && c < a.C && t < a.T && idx < a.n_int;
+}
+template <int GPW, bool BF16>
+__device__ __forceinline__ void vblk_load(const DiagArgs& a, int b, int cb, int blk, VRaw<GPW, BF16>& r) {
+#pragma unroll
+  for (int i = 0; i < VRaw<GPW, BF16>::NI; ++i) {
+    int gi, st, q, idx;
+    if (vblk_item<GPW, BF16>(a, cb, blk, (int)threadIdx.x + 64 * i, gi, st, q, idx)) {
+      const char* row = reinterpret_cast<const char*>(a.path) + ((size_t)b * a.L + idx) * DIM * (BF16 ? 2 : 4);
+      r.x0[i] = *reinterpret_cast<const f4a*>(row + 16 * q);
+      r.x1[i] = *reinterpret_cast<const f4a*>(row + DIM * (BF16 ? 2 : 4) + 16 * q);
+    }
+  }
+}
+__device__ __forceinline__ float bf_lo(float w) { return __uint_as_float(__float_as_uint(w) << 16); }
+__device__ __forceinline__ float bf_hi(float w) { return __uint_as_float(__float_as_uint(w) & 0xffff0000u); }
+template <int GPW, bool BF16>
+__device__ __forceinline__ void vblk_store(const DiagArgs& a, int cb, int blk, const VRaw<GPW, BF16>& r,
+                                           float* buf) {
+#pragma unroll
+  for (int i = 0; i < VRaw<GPW, BF16>::NI; ++i) {
+    int gi, st, q, idx;
+    if (vblk_item<GPW, BF16>(a, cb, blk, (int)threadIdx.x + 64 * i, gi, st, q, idx)) {
+      float* o = buf + gi * VBLK + st * DIM;
+      if constexpr (!BF16) {
+        *reinterpret_cast<f4a*>(o + 4 * q) = r.x1[i] - r.x0[i];
+      } else {  // 8 bf16 channels 8q .. 8q + 7, little-endian pairs
+        const f4a u = r.x0[i], w = r.x1[i];
+        *reinterpret_cast<f4a*>(o + 8 * q) =
+            f4a{bf_lo(w.x) - bf_lo(u.x), bf_hi(w.x) - bf_hi(u.x), bf_lo(w.y) - bf_lo(u.y), bf_hi(w.y) - bf_hi(u.y)};
+        *reinterpret_cast<f4a*>(o + 8 * q + 4) =
+            f4a{bf_lo(w.z) - bf_lo(u.z), bf_hi(w.z) - bf_hi(u.z), bf_lo(w.w) - bf_lo(u.w), bf_hi(w.w) - bf_hi(u.w)};
       }
     }
   }
@@ -610,12 +676,13 @@ __global__ __launch_bounds__(256) void k_quad_bwd_scan(DiagArgs a) {
 template <bool OUT, bool BF16>
 __global__ __launch_bounds__(64) void k_fwd(DiagArgs a) {
   constexpr int KP = 4, GPW = Geo<KP>::GPW;
-  __shared__ __align__(16) float s_v[GPW * VPITCH];
+  __shared__ __align__(16) float s_v[2][GPW * VBLK];
   // start states of the groups (prefix rows: the carries rebuilt inside the quad), then level-2 row staging
   __shared__ __align__(16) float s_row[GPW][DIM + DIM * DIM];
   const Lane l = lane_of<KP>(threadIdx.x);
   const int b = blockIdx.y, cb = blockIdx.x * GPW, c = cb + l.gi;
-  stage<KP, BF16>(a, b, cb, s_v, nullptr);
+  VRaw<GPW, BF16> vr;
+  vblk_load<GPW, BF16>(a, b, cb, 0, vr);
   if constexpr (OUT) {
     // the workgroup's chunks are quad cb / 4: rebuild the carries inside it from the quad's carry (float64),
     // for this kernel's groups and for every later kernel that reads carries (generic chunks, the adjoint)
@@ -632,88 +699,107 @@ __global__ __launch_bounds__(64) void k_fwd(DiagArgs a) {
       }
     }
   }
+  vblk_store<GPW, BF16>(a, cb, 0, vr, s_v[0]);
   __syncthreads();
-  if (c >= a.C) return;
-  const int ci = b * a.C + c;
-  float hb;
-  int flag;
+  // every lane stays to the end (the block staging is shared by the wave); a group whose chunk is absent or
+  // non-uniform (left to the generic kernels) only skips the arithmetic
+  bool active = c < a.C;
+  const int ci = b * a.C + (active ? c : 0);
+  float hb = 0.0f;
+  int flag = 0;
   if constexpr (!OUT) {
-    flag = classify_chunk(a, b, c, l.gl, hb);
-    if (l.gl == 0) {
-      a.cflag[ci] = flag;
-      a.chbar[ci] = hb;
+    if (active) {
+      flag = classify_chunk(a, b, c, l.gl, hb);
+      if (l.gl == 0) {
+        a.cflag[ci] = flag;
+        a.chbar[ci] = hb;
+      }
     }
-    if (!(flag & 1)) return;
   } else {
-    flag = a.cflag[ci];
-    if (!(flag & 1)) return;
-    hb = a.chbar[ci];
+    if (active) {
+      flag = a.cflag[ci];
+      hb = a.chbar[ci];
+    }
   }
-  const int t0 = c * a.T, Tc = min(a.T, a.n_int - t0);
+  active = active && (flag & 1);
+  const int t0 = active ? c * a.T : 0, Tc = active ? min(a.T, a.n_int - t0) : 0;
   FwdCoef<KP> f;
   fwd_coef<KP>(a, l, hb, (flag & 4) != 0, f);
-  cf S1{0.0f, 0.0f}, SA[KP], SB[KP];
+  cf S1{0.0f, 0.0f}, SA[KP], SB_[KP];
   static_for<0, KP>([&](auto qc) {
     constexpr int q = qc;
-    SA[q] = SB[q] = cf{0.0f, 0.0f};
+    SA[q] = SB_[q] = cf{0.0f, 0.0f};
   });
   if constexpr (OUT) {
-    const float* cr = s_row[l.gi];
-    S1 = cf{cr[2 * l.j], cr[2 * l.j + 1]};
-    static_for<0, KP>([&](auto qc) {
-      constexpr int q = qc;
-      const f4a p2 = *reinterpret_cast<const f4a*>(cr + poff(l.j, KP * l.kg + q));
-      SA[q] = cf{0.5f * p2.x, 0.5f * p2.y};
-      SB[q] = cf{0.5f * p2.z, 0.5f * p2.w};
-    });
-  }
-  const float* vg = s_v + l.gi * VPITCH;
-  float* orow = a.out + ((size_t)b * a.n_int + t0) * a.W;
-  const int o1 = a.off1 + 2 * l.j;
-  for (int t = 0; t < Tc; ++t) {
-    cf pj, pk[KP];
-    load_p<KP>(vg + t * DIM, l, pj, pk);
-    const cf cj = f.rho * S1;
-    S1 = fma_c(f.phi, pj, cj);
-    static_for<0, KP>([&](auto qc) {
-      constexpr int q = qc;
-      const cf sg = f.phk[q] * pk[q];
-      cf pi, pic;
-      prods(pj, pk[q], pi, pic);
-      SB[q] = fma_c(f.LB[q], SB[q], fma_c(cj, sg, f.IB[q] * pi));
-      SA[q] = fma_c(f.LA[q], SA[q], fma_c(cj, conj(sg), f.IA[q] * pic));
-    });
-    if constexpr (OUT) {
-      float* row = orow + (size_t)t * a.W;
-      if (a.lvl0 && l.gl == 0) row[0] = 1.0f;
-      if (l.kg == 0) *reinterpret_cast<f2u*>(row + o1) = f2u{S1.re, S1.im};
-      float* buf = s_row[l.gi];
-      f4a* p0 = reinterpret_cast<f4a*>(buf + 32 * l.j + 2 * KP * l.kg);
-      f4a* p1 = reinterpret_cast<f4a*>(buf + 32 * l.j + DIM + 2 * KP * l.kg);
-      static_for<0, KP / 2>([&](auto ic) {
-        constexpr int i = ic, q0 = 2 * i, q1 = 2 * i + 1;
-        p0[i] = f4a{SA[q0].re + SB[q0].re, SB[q0].im - SA[q0].im, SA[q1].re + SB[q1].re, SB[q1].im - SA[q1].im};
-        p1[i] = f4a{SA[q0].im + SB[q0].im, SA[q0].re - SB[q0].re, SA[q1].im + SB[q1].im, SA[q1].re - SB[q1].re};
+    if (active) {
+      const float* cr = s_row[l.gi];
+      S1 = cf{cr[2 * l.j], cr[2 * l.j + 1]};
+      static_for<0, KP>([&](auto qc) {
+        constexpr int q = qc;
+        const f4a p2 = *reinterpret_cast<const f4a*>(cr + poff(l.j, KP * l.kg + q));
+        SA[q] = cf{0.5f * p2.x, 0.5f * p2.y};
+        SB_[q] = cf{0.5f * p2.z, 0.5f * p2.w};
       });
-      wave_order();
-      float* row2 = row + a.off2;
-      static_for<0, Pieces<KP>::NP>([&](auto ic) {
-        constexpr int i = ic;
-        const int pi = l.gl + Geo<KP>::G * i;
-        const f4a v = *reinterpret_cast<const f4a*>(buf + 4 * pi);
-        *reinterpret_cast<f4u*>(row2 + 4 * pi) = f4u{v.x, v.y, v.z, v.w};
-      });
-      wave_order();
     }
   }
+  wave_order();
+  float* orow = a.out + ((size_t)b * a.n_int + t0) * a.W;
+  const int o1 = a.off1 + 2 * l.j;
+  const int nblk = (a.T + SB - 1) / SB;
+  for (int blk = 0; blk < nblk; ++blk) {
+    if (blk + 1 < nblk) vblk_load<GPW, BF16>(a, b, cb, blk + 1, vr);
+    const float* vg = s_v[blk & 1] + l.gi * VBLK;
+    for (int st = 0; st < SB; ++st) {
+      const int t = blk * SB + st;
+      if (t >= Tc) break;
+      cf pj, pk[KP];
+      load_p<KP>(vg + st * DIM, l, pj, pk);
+      const cf cj = f.rho * S1;
+      S1 = fma_c(f.phi, pj, cj);
+      static_for<0, KP>([&](auto qc) {
+        constexpr int q = qc;
+        const cf sg = f.phk[q] * pk[q];
+        cf pi, pic;
+        prods(pj, pk[q], pi, pic);
+        SB_[q] = fma_c(f.LB[q], SB_[q], fma_c(cj, sg, f.IB[q] * pi));
+        SA[q] = fma_c(f.LA[q], SA[q], fma_c(cj, conj(sg), f.IA[q] * pic));
+      });
+      if constexpr (OUT) {
+        float* row = orow + (size_t)t * a.W;
+        if (a.lvl0 && l.gl == 0) row[0] = 1.0f;
+        if (l.kg == 0) *reinterpret_cast<f2u*>(row + o1) = f2u{S1.re, S1.im};
+        float* buf = s_row[l.gi];
+        f4a* p0 = reinterpret_cast<f4a*>(buf + 32 * l.j + 2 * KP * l.kg);
+        f4a* p1 = reinterpret_cast<f4a*>(buf + 32 * l.j + DIM + 2 * KP * l.kg);
+        static_for<0, KP / 2>([&](auto ic) {
+          constexpr int i = ic, q0 = 2 * i, q1 = 2 * i + 1;
+          p0[i] = f4a{SA[q0].re + SB_[q0].re, SB_[q0].im - SA[q0].im, SA[q1].re + SB_[q1].re, SB_[q1].im - SA[q1].im};
+          p1[i] = f4a{SA[q0].im + SB_[q0].im, SA[q0].re - SB_[q0].re, SA[q1].im + SB_[q1].im, SA[q1].re - SB_[q1].re};
+        });
+        wave_order();
+        float* row2 = row + a.off2;
+        static_for<0, Pieces<KP>::NP>([&](auto ic) {
+          constexpr int i = ic;
+          const int pi = l.gl + Geo<KP>::G * i;
+          const f4a v = *reinterpret_cast<const f4a*>(buf + 4 * pi);
+          *reinterpret_cast<f4u*>(row2 + 4 * pi) = f4u{v.x, v.y, v.z, v.w};
+        });
+        wave_order();
+      }
+    }
+    if (blk + 1 < nblk) vblk_store<GPW, BF16>(a, cb, blk + 1, vr, s_v[(blk + 1) & 1]);
+    wave_order();
+  }
   if constexpr (!OUT) {
-    float* sp = a.summ + ((size_t)b * a.C + c) * a.D;
-    if (l.kg == 0) *reinterpret_cast<float2*>(sp + 2 * l.j) = float2{S1.re, S1.im};
-    static_for<0, KP>([&](auto qc) {
-      constexpr int q = qc;
-      *reinterpret_cast<f4a*>(sp + DIM + 4 * (l.j * K + KP * l.kg + q)) =
-          f4a{2.0f * SA[q].re, 2.0f * SA[q].im, 2.0f * SB[q].re, 2.0f * SB[q].im};
-    });
+    if (active) {
+      float* sp = a.summ + ((size_t)b * a.C + c) * a.D;
+      if (l.kg == 0) *reinterpret_cast<float2*>(sp + 2 * l.j) = float2{S1.re, S1.im};
+      static_for<0, KP>([&](auto qc) {
+        constexpr int q = qc;
+        *reinterpret_cast<f4a*>(sp + DIM + 4 * (l.j * K + KP * l.kg + q)) =
+            f4a{2.0f * SA[q].re, 2.0f * SA[q].im, 2.0f * SB_[q].re, 2.0f * SB_[q].im};
+      });
+    }
   }
 }
 
@@ -735,11 +821,14 @@ template <int KP> __device__ __forceinline__ GRaw<KP> load_graw(const float* row
   return r;
 }
 // raw row -> LDS -> the lane's slice
+// The level-1 pair goes through LDS too (buf[256 + 2j]), so that every register of the raw row is dead once
+// this returns and a ring slot can be reloaded in place.
 template <int KP> __device__ __forceinline__ GRow<KP> slice_g(const GRaw<KP>& r, float* buf, const Lane& l) {
   pieces_to_lds<KP>(r.pc, buf, l.gl);
+  *reinterpret_cast<float2*>(buf + DIM * DIM + 2 * l.j) = float2{r.g1.x, r.g1.y};
   wave_order();
   GRow<KP> g;
-  g.g1 = float2{r.g1.x, r.g1.y};
+  g.g1 = *reinterpret_cast<const float2*>(buf + DIM * DIM + 2 * l.j);
   const f4a* p0 = reinterpret_cast<const f4a*>(buf + 32 * l.j + 2 * KP * l.kg);
   const f4a* p1 = reinterpret_cast<const f4a*>(buf + 32 * l.j + DIM + 2 * KP * l.kg);
   static_for<0, KP / 2>([&](auto ic) {
@@ -763,20 +852,22 @@ template <int KP, int q> __device__ __forceinline__ void g_pair(const GRow<KP>& 
 template <bool BF16>
 __global__ __launch_bounds__(64) void k_bwd_local(DiagArgs a) {
   constexpr int KP = 4, GPW = Geo<KP>::GPW;
-  __shared__ __align__(16) float s_v[GPW * VPITCH];
-  __shared__ __align__(16) float s_row[GPW][DIM * DIM];  // cotangent row staging
+  __shared__ __align__(16) float s_v[2][GPW * VBLK];
+  __shared__ __align__(16) float s_row[GPW][DIM * DIM + DIM];  // cotangent row staging
   const Lane l = lane_of<KP>(threadIdx.x);
   const int b = blockIdx.y, cb = blockIdx.x * GPW, c = cb + l.gi;
-  stage<KP, BF16>(a, b, cb, s_v, nullptr);
+  const int nblk = (a.T + SB - 1) / SB;
+  VRaw<GPW, BF16> vr;
+  vblk_load<GPW, BF16>(a, b, cb, nblk - 1, vr);
+  vblk_store<GPW, BF16>(a, cb, nblk - 1, vr, s_v[(nblk - 1) & 1]);
   __syncthreads();
-  if (c >= a.C) return;
-  const int ci = b * a.C + c;
-  const int flag = a.cflag[ci];
-  if (!(flag & 1)) return;
-  const int t0 = c * a.T, Tc = min(a.T, a.n_int - t0);
+  // every lane stays to the end (shared block staging); absent or non-uniform chunks skip the arithmetic
+  const int ci = b * a.C + (c < a.C ? c : 0);
+  const int flag = c < a.C ? a.cflag[ci] : 0;
+  const bool active = (flag & 1) != 0;
+  const int t0 = active ? c * a.T : 0, Tc = active ? min(a.T, a.n_int - t0) : 0;
   FwdCoef<KP> f;
-  fwd_coef<KP>(a, l, a.chbar[ci], (flag & 4) != 0, f);
-  const float* vg = s_v + l.gi * VPITCH;
+  fwd_coef<KP>(a, l, active ? a.chbar[ci] : 0.0f, (flag & 4) != 0, f);
   const float* grow = a.gout + ((size_t)b * a.n_int + t0) * a.W;
   const int o1 = a.off1 + 2 * l.j;
   float* gbuf = s_row[l.gi];
@@ -785,30 +876,52 @@ __global__ __launch_bounds__(64) void k_bwd_local(DiagArgs a) {
     constexpr int q = qc;
     lA[q] = lB[q] = cf{0.0f, 0.0f};
   });
-  GRaw<KP> gn1 = load_graw<KP>(grow + (size_t)(Tc - 1) * a.W, o1, a.off2, l.gl);
-  GRaw<KP> gn2 = gn1;
-  if (Tc >= 2) gn2 = load_graw<KP>(grow + (size_t)(Tc - 2) * a.W, o1, a.off2, l.gl);
-  for (int t = Tc - 1; t >= 0; --t) {
-    const GRow<KP> g = slice_g<KP>(gn1, gbuf, l);
-    gn1 = gn2;
-    if (t >= 2) gn2 = load_graw<KP>(grow + (size_t)(t - 2) * a.W, o1, a.off2, l.gl);
-    cf pj, pk[KP];
-    load_p<KP>(vg + t * DIM, l, pj, pk);
-    l1 += cf{g.g1.x, g.g1.y};
-    cf toC{0.0f, 0.0f};
-    static_for<0, KP>([&](auto qc) {
-      constexpr int q = qc;
-      cf gA, gB;
-      g_pair<KP, q>(g, gA, gB);
-      lA[q] += gA;
-      lB[q] += gB;
-      const cf sg = f.phk[q] * pk[q];
-      toC += cjm(sg, lB[q]) + sg * lA[q];
-      lB[q] = cjm(f.LB[q], lB[q]);
-      lA[q] = cjm(f.LA[q], lA[q]);
-    });
-    l1 = cjm(f.rho, l1 + kg_sum<KP>(toC));
+  // Cotangent rows through a ring of RING register slots, RING steps ahead of their consumer. Every group runs
+  // the steps t = nblk SB - 1 .. 0 so that every unrolled slot index is static; slot i holds row t of the step
+  // t = tt - i. Loads and the LDS slicing are unconditional (rows clamped into the chunk), only the arithmetic
+  // of steps t >= Tc is skipped: no load sits under a branch, and the waits before each use cover only the
+  // oldest row.
+  constexpr int RING = 2;
+  static_assert(SB % RING == 0, "staged blocks hold whole ring rounds");
+  GRaw<KP> ring[RING];
+  static_for<0, RING>([&](auto ic) {
+    constexpr int i = ic;
+    ring[i] = load_graw<KP>(grow + (size_t)max(min(nblk * SB - 1 - i, Tc - 1), 0) * a.W, o1, a.off2, l.gl);
+    __builtin_amdgcn_sched_barrier(0);  // issue the slots in consumption order (oldest load consumed first)
+  });
+  for (int blk = nblk - 1; blk >= 0; --blk) {
+    if (blk > 0) vblk_load<GPW, BF16>(a, b, cb, blk - 1, vr);
+    const float* vg = s_v[blk & 1] + l.gi * VBLK - blk * SB * DIM;  // indexed by the step t of the chunk
+    for (int tt = blk * SB + SB - 1; tt >= blk * SB; tt -= RING) {
+      static_for<0, RING>([&](auto ic) {
+        constexpr int i = ic;
+        const int t = tt - i;
+        const GRow<KP> g = slice_g<KP>(ring[i], gbuf, l);
+        ring[i] = load_graw<KP>(grow + (size_t)max(min(t - RING, Tc - 1), 0) * a.W, o1, a.off2, l.gl);
+        if (t < Tc) {
+          cf pj, pk[KP];
+          load_p<KP>(vg + t * DIM, l, pj, pk);
+          l1 += cf{g.g1.x, g.g1.y};
+          cf toC{0.0f, 0.0f};
+          static_for<0, KP>([&](auto qc) {
+            constexpr int q = qc;
+            cf gA, gB;
+            g_pair<KP, q>(g, gA, gB);
+            lA[q] += gA;
+            lB[q] += gB;
+            const cf sg = f.phk[q] * pk[q];
+            toC += cjm(sg, lB[q]) + sg * lA[q];
+            lB[q] = cjm(f.LB[q], lB[q]);
+            lA[q] = cjm(f.LA[q], lA[q]);
+          });
+          l1 = cjm(f.rho, l1 + kg_sum<KP>(toC));
+        }
+      });
+    }
+    if (blk > 0) vblk_store<GPW, BF16>(a, cb, blk - 1, vr, s_v[(blk - 1) & 1]);
+    wave_order();
   }
+  if (!active) return;
   float* mp = a.mu + ((size_t)b * a.C + c) * a.D;
   if (l.kg == 0) *reinterpret_cast<float2*>(mp + 2 * l.j) = float2{l1.re, l1.im};
   static_for<0, KP>([&](auto qc) {
@@ -830,7 +943,8 @@ template <int KP> struct BwdCoef {
   cf LB1[KP], LA1[KP];                  // d/dh of the flows
 };
 
-template <bool BF16>
+// DH: the clock gradient is requested (dclock non-null); without it the step skips every dh term.
+template <bool BF16, bool DH>
 __global__ __launch_bounds__(64) void k_bwd_full(DiagArgs a) {
   constexpr int KP = 2, G = Geo<KP>::G, GPW = Geo<KP>::GPW;
   __shared__ __align__(16) float s_v[GPW * VPITCH];
@@ -840,7 +954,7 @@ __global__ __launch_bounds__(64) void k_bwd_full(DiagArgs a) {
   __shared__ __align__(16) float s_dhp[GPW][NB * G];        // dh partials [t][lane]
   __shared__ __align__(16) float s_dvo[GPW][(NB + 1) * DIM];  // dv of the block's steps; row NB: the step after
   __shared__ float s_dho[GPW][NB + 1];
-  __shared__ __align__(16) float s_row[GPW][DIM * DIM];  // cotangent row staging
+  __shared__ __align__(16) float s_row[GPW][DIM * DIM + DIM];  // cotangent row staging
   __shared__ __align__(16) float s_mt[GPW][DIM + DIM * DIM];  // cotangent from later chunks, per group
   const Lane l = lane_of<KP>(threadIdx.x);
   const int b = blockIdx.y, cb = blockIdx.x * GPW, c = cb + l.gi;
@@ -963,20 +1077,26 @@ __global__ __launch_bounds__(64) void k_bwd_full(DiagArgs a) {
   const float* grow = a.gout + ((size_t)b * a.n_int + (active ? t0 : 0)) * a.W;
   const int o1 = a.off1 + 2 * l.j;
   float* gbuf = s_row[l.gi];
-  GRaw<KP> gn1{}, gn2{};
-  if (Tc >= 1) gn1 = load_graw<KP>(grow + (size_t)(Tc - 1) * a.W, o1, a.off2, l.gl);
-  if (Tc >= 2) gn2 = load_graw<KP>(grow + (size_t)(Tc - 2) * a.W, o1, a.off2, l.gl);
-  // blocks of NB steps, last block first; every group runs the same number of blocks (barriers)
+  // cotangent rows through a ring of NB register slots: row t sits in slot t % NB (the step's static index in
+  // the unrolled block below) and is reloaded with row t - NB right after use, NB steps ahead of its consumer
+  GRaw<KP> ring[NB];
+  // (loads and slicing are unconditional, rows clamped into the chunk; only the arithmetic of steps t >= Tc is
+  // skipped, so no load sits under a branch and the waits before each use cover only the oldest row)
   const int nblk = (a.T + NB - 1) / NB;
+  static_down<NB - 1>([&](auto sc) {  // slot s holds row tb + s of the first block processed
+    constexpr int s = sc;
+    ring[s] = load_graw<KP>(grow + (size_t)max(min((nblk - 1) * NB + s, Tc - 1), 0) * a.W, o1, a.off2, l.gl);
+    __builtin_amdgcn_sched_barrier(0);  // issue the slots in consumption order (oldest load consumed first)
+  });
+  // blocks of NB steps, last block first; every group runs the same number of blocks (barriers)
   for (int blk = nblk - 1; blk >= 0; --blk) {
     const int tb = blk * NB;
-#pragma unroll 1
-    for (int s = NB - 1; s >= 0; --s) {
+    static_down<NB - 1>([&](auto sc) {
+      constexpr int s = sc;
       const int t = tb + s;
-      if (t >= Tc) continue;
-      const GRow<KP> g = slice_g<KP>(gn1, gbuf, l);
-      gn1 = gn2;
-      if (t >= 2) gn2 = load_graw<KP>(grow + (size_t)(t - 2) * a.W, o1, a.off2, l.gl);
+      const GRow<KP> g = slice_g<KP>(ring[s], gbuf, l);
+      ring[s] = load_graw<KP>(grow + (size_t)max(min(t - NB, Tc - 1), 0) * a.W, o1, a.off2, l.gl);
+      if (t >= Tc) return;
       const float h = hg[t];
       cf pj, pk[KP];
       load_p<KP>(vg + t * DIM, l, pj, pk);
@@ -1008,11 +1128,12 @@ __global__ __launch_bounds__(64) void k_bwd_full(DiagArgs a) {
         const cf w = cjm(f.phk[q], tS) + cjm(pj, gf) + cjm(ge, pj);
         *reinterpret_cast<float2*>(w_g + ((s * K + KP * l.kg + q) * K + l.j) * 2) = float2{w.re, w.im};
         const cf gph = cjm(pk[q], tS);
-        dhp += redot(gph, f.phi1h[q]);
+        if constexpr (DH) dhp += redot(gph, f.phi1h[q]);
         kph[q] = fma_c(cf{h, 0.0f}, gph, kph[q]);
         // coefficient cotangents
         const cf gIB = cjm(pi, Bc), gIA = cjm(pic, A), gLB = cjm(HB, Bc), gLA = cjm(HA, A);
-        dhp += redot(gIB, f.IB1[q]) + redot(gIA, f.IA1[q]) + redot(gLB, f.LB1[q]) + redot(gLA, f.LA1[q]);
+        if constexpr (DH)
+          dhp += redot(gIB, f.IB1[q]) + redot(gIA, f.IA1[q]) + redot(gLB, f.LB1[q]) + redot(gLA, f.LA1[q]);
         kIB[q] = fma_c(cf{h, 0.0f}, gIB, kIB[q]);
         kIA[q] = fma_c(cf{h, 0.0f}, gIA, kIA[q]);
         kLB[q] = fma_c(cf{h, 0.0f}, gLB, kLB[q]);
@@ -1030,14 +1151,14 @@ __global__ __launch_bounds__(64) void k_bwd_full(DiagArgs a) {
         *reinterpret_cast<float2*>(dvp_g + (s * K + l.j) * 2) = float2{dvp.re, dvp.im};
         const cf gphL = cjm(pj, l1);
         const cf grho = cjm(H1, gc);
-        dhp += redot(gphL, f.phi1) + redot(grho, f.rho1);
+        if constexpr (DH) dhp += redot(gphL, f.phi1) + redot(grho, f.rho1);
         kphj = fma_c(cf{h, 0.0f}, gphL, kphj);
         krho = fma_c(cf{h, 0.0f}, grho, krho);
       }
-      dhp_g[s * G + l.gl] = dhp;
+      if constexpr (DH) dhp_g[s * G + l.gl] = dhp;
       l1 = cjm(f.rho, gc);
       S1 = H1;
-    }
+    });
     __syncthreads();
     // column sums of the block: dv[t][k] = plane part + sum_j w[t][k][j]; dh[t] = sum of the lane partials
     for (int it = l.gl; it < NB * K; it += G) {
@@ -1053,7 +1174,7 @@ __global__ __launch_bounds__(64) void k_bwd_full(DiagArgs a) {
           *reinterpret_cast<float2*>(a.dv + ((size_t)b * a.n_int + t0 + t) * DIM + 2 * k) = dv;
       }
     }
-    if (l.gl < NB) {
+    if (DH && l.gl < NB) {
       const int s = l.gl, t = tb + s;
       if (t < Tc) {
         float acc = 0.0f;
@@ -1073,7 +1194,7 @@ __global__ __launch_bounds__(64) void k_bwd_full(DiagArgs a) {
       if (t >= 1 && t <= Tc - 1) {
         if (ch < DIM) {
           a.dpath[((size_t)b * a.L + t0 + t) * DIM + ch] = dvo_g[(s - 1) * DIM + ch] - dvo_g[s * DIM + ch];
-        } else {
+        } else if (DH) {
           a.dclock[(size_t)b * a.L + t0 + t] = dho_g[s - 1] - dho_g[s];
         }
       }
@@ -1190,8 +1311,13 @@ int pairs_backward(const DiagArgs& a, hipStream_t st, bool full) {
   if (full) {
     constexpr int GPW = pairs::Geo<2>::GPW;
     const dim3 grid((a.C + GPW - 1) / GPW, a.B), blk(64);
-    if (a.path_bf16) hipLaunchKernelGGL((pairs::k_bwd_full<true>), grid, blk, 0, st, a);
-    else hipLaunchKernelGGL((pairs::k_bwd_full<false>), grid, blk, 0, st, a);
+    if (a.dclock) {
+      if (a.path_bf16) hipLaunchKernelGGL((pairs::k_bwd_full<true, true>), grid, blk, 0, st, a);
+      else hipLaunchKernelGGL((pairs::k_bwd_full<false, true>), grid, blk, 0, st, a);
+    } else {
+      if (a.path_bf16) hipLaunchKernelGGL((pairs::k_bwd_full<true, false>), grid, blk, 0, st, a);
+      else hipLaunchKernelGGL((pairs::k_bwd_full<false, false>), grid, blk, 0, st, a);
+    }
   } else {
     constexpr int GPW = pairs::Geo<4>::GPW;
     const dim3 grid((a.C + GPW - 1) / GPW, a.B), blk(64);

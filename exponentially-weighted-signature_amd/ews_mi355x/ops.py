@@ -32,6 +32,11 @@ def _check_inputs(path, clock, params):
         raise TypeError("clock and A must be float32")
 
 
+def _aligned(x):
+    """The kernels read knot rows with 16-byte vector loads: copy a view whose data is not 16-byte aligned."""
+    return x if x.data_ptr() % 16 == 0 else x.clone()
+
+
 class DiagScan(torch.autograd.Function):
     """out = EWS readout of (path, clock) under a diagonal / rotation-plane generator with parameters
     ``params`` ((d/2, 2) rows (d_j, w_j) for planes, (d,) for a real diagonal)."""
@@ -40,7 +45,7 @@ class DiagScan(torch.autograd.Function):
     def forward(ctx, path, clock, params, N, structure, flow_mode, readout, level0, chunk):
         lib = nat.load()
         _check_inputs(path, clock, params)
-        path = path.contiguous()
+        path = _aligned(path.contiguous())
         clock = clock.contiguous()
         params = params.contiguous()
         B, L, d = path.shape
@@ -69,12 +74,14 @@ class DiagScan(torch.autograd.Function):
         gout = gout.contiguous().to(torch.float32)
         dev = path.device
         dpath = torch.empty((B, L, d), device=dev, dtype=torch.float32)
-        dclock = torch.empty((B, L), device=dev, dtype=torch.float32)
+        # the clock gradient is computed only when the clock requires it (a null pointer skips its terms)
+        dclock = torch.empty((B, L), device=dev, dtype=torch.float32) if ctx.needs_input_grad[1] else None
         dparams = torch.empty_like(params)
         ws = torch.empty(int(lib.ews_diag_workspace_bytes(ctypes.byref(desc))), device=dev, dtype=torch.uint8)
         rc = lib.ews_diag_backward(ctypes.byref(desc), path.data_ptr(), clock.data_ptr(), params.data_ptr(),
-                                   resid.data_ptr(), gout.data_ptr(), dpath.data_ptr(), dclock.data_ptr(),
-                                   dparams.data_ptr(), ws.data_ptr(), _stream_handle(dev))
+                                   resid.data_ptr(), gout.data_ptr(), dpath.data_ptr(),
+                                   dclock.data_ptr() if dclock is not None else None, dparams.data_ptr(),
+                                   ws.data_ptr(), _stream_handle(dev))
         nat.check(rc, "ews_diag_backward")
         return dpath.to(path.dtype), dclock, dparams, None, None, None, None, None, None
 

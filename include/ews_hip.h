@@ -76,8 +76,9 @@ int ews_diag_forward(const ews_diag_desc* desc, const void* path, const float* c
                      float* out, void* residual, void* workspace, ews_stream_t stream);
 
 /* Backward: cotangent grad_out shaped like out; writes grad_path (B, L, d) f32, grad_clock (B, L) f32 and
- * grad_params (same shape as params). Replaces the custom VJP _cvjp_bwd (pallas_combine.py:1698-1798) and
- * JAX autodiff through the leaf (plane_engine.py:134-152). */
+ * grad_params (same shape as params). grad_clock may be NULL when the clock needs no gradient (a data clock, as
+ * JAX prunes an undifferentiated input): its terms are then skipped. Replaces the custom VJP _cvjp_bwd
+ * (pallas_combine.py:1698-1798) and JAX autodiff through the leaf (plane_engine.py:134-152). */
 int ews_diag_backward(const ews_diag_desc* desc, const void* path, const float* clock, const float* params,
                       const void* residual, const float* grad_out, float* grad_path, float* grad_clock,
                       float* grad_params, void* workspace, ews_stream_t stream);

@@ -58,8 +58,9 @@ def _align(x):
     return (x + 255) // 256 * 256
 
 
-def _run(path, clock, dw, g, bf16=False):
-    """Forward + backward through the C ABI; returns out, dpath, dclock, ddw and the chunk flags."""
+def _run(path, clock, dw, g, bf16=False, clock_grad=True):
+    """Forward + backward through the C ABI; returns out, dpath, dclock, ddw and the chunk flags (clock_grad=False
+    passes a null grad_clock: the clock gradient is not requested)."""
     lib = nat.load()
     B, L, d = path.shape
     dt = nat.DTYPE_BF16 if bf16 else nat.DTYPE_F32
@@ -81,8 +82,8 @@ def _run(path, clock, dw, g, bf16=False):
     nat.check(lib.ews_diag_forward(ctypes.byref(desc), tp.data_ptr(), tc.data_ptr(), tw.data_ptr(), out.data_ptr(),
                                    rs.data_ptr(), ws.data_ptr(), st), "forward")
     nat.check(lib.ews_diag_backward(ctypes.byref(desc), tp.data_ptr(), tc.data_ptr(), tw.data_ptr(), rs.data_ptr(),
-                                    tg.data_ptr(), dpath.data_ptr(), dclock.data_ptr(), ddw.data_ptr(),
-                                    ws.data_ptr(), st), "backward")
+                                    tg.data_ptr(), dpath.data_ptr(), dclock.data_ptr() if clock_grad else None,
+                                    ddw.data_ptr(), ws.data_ptr(), st), "backward")
     torch.cuda.synchronize()
     # residual layout (ews_diag.hip): float64 carries (B, C+1, D) | argmax (B, W) int32 | chunk flags (B, C) int32
     Cn = (L - 1 + T_DEFAULT - 1) // T_DEFAULT
@@ -164,3 +165,16 @@ def test_layer_api_on_pair_kernels():
     (pp * torch.tensor(rdd)).sum().backward()
     for g_gpu, g_ref in zip([A.v.grad, A.u.grad], [Aref.v.grad, Aref.u.grad]):
         assert relerr(g_gpu.cpu().numpy(), g_ref.numpy()) < 1e-4
+
+
+def test_null_clock_gradient_leaves_the_other_gradients_unchanged():
+    """grad_clock = NULL skips the clock terms of the adjoint; path and parameter gradients are the same bits."""
+    B, L = 2, 700
+    path, clock, dw = _inputs(B, L, seed=11)
+    W = 1 + path.shape[2] + path.shape[2] ** 2
+    g = (np.random.default_rng(5).normal(size=(B, L - 1, W)) / np.sqrt(W)).astype(np.float32)
+    out1, dp1, _, dd1, _ = _run(path, clock, dw, g, clock_grad=True)
+    out2, dp2, _, dd2, _ = _run(path, clock, dw, g, clock_grad=False)
+    assert np.array_equal(out1, out2)
+    assert np.array_equal(dp1, dp2)
+    assert np.array_equal(dd1, dd2)
