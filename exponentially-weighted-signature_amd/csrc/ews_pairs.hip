@@ -251,9 +251,15 @@ template <int KP> __device__ __forceinline__ void load_p(const float* vr, const 
 // Level-2 part of a readout row (d^2 = 256 floats from off2) moved between HBM and the lane slices through a
 // per-group LDS buffer of 256 floats, so that every global access instruction of a group covers a contiguous run
 // (G lanes x 16 bytes) instead of scattered 16-byte pieces: lane gl moves pieces gl, gl + G, ... of the row.
-// The lane slice of (j, kg) is row 2j (buffer [32 j, 32 j + 16)) and row 2j + 1 ([32 j + 16, 32 j + 32)),
+// The buffer holds the 16 x 16 block row-major with 4 floats of padding after every pair of rows (row r at
+// 16 r + 4 (r >> 1)): the lanes (j = 0..7) of one LDS cycle then start their row 2j slices on distinct bank
+// quads (the unpadded pitch puts all eight on one quad), and the contiguous pieces stay conflict-free too.
+// The lane slice of (j, kg) is row 2j (buffer [36 j, 36 j + 16)) and row 2j + 1 ([36 j + 16, 36 j + 32)),
 // columns 2 KP kg .. 2 KP kg + 2 KP - 1. LDS operations of one wavefront execute in program order, so a
 // compiler barrier between the write and the read of another lane's data is enough.
+constexpr int RBUF = DIM * DIM + 2 * DIM;  // floats of the padded 16 x 16 block
+__device__ __forceinline__ int piece_at(int pi) { return 4 * pi + 4 * (pi >> 3); }  // piece pi = row pi/4, col 4(pi%4)
+__device__ __forceinline__ int row_at(int r) { return DIM * r + 4 * (r >> 1); }
 template <int KP> struct Pieces {
   static constexpr int NP = 64 / Geo<KP>::G;  // 16-byte pieces per lane
   f4u v[NP];
@@ -269,7 +275,7 @@ template <int KP> __device__ __forceinline__ Pieces<KP> load_pieces(const float*
 template <int KP> __device__ __forceinline__ void pieces_to_lds(const Pieces<KP>& pc, float* buf, int gl) {
   static_for<0, Pieces<KP>::NP>([&](auto ic) {
     constexpr int i = ic;
-    *reinterpret_cast<f4a*>(buf + 4 * (gl + Geo<KP>::G * i)) = f4a{pc.v[i].x, pc.v[i].y, pc.v[i].z, pc.v[i].w};
+    *reinterpret_cast<f4a*>(buf + piece_at(gl + Geo<KP>::G * i)) = f4a{pc.v[i].x, pc.v[i].y, pc.v[i].z, pc.v[i].w};
   });
 }
 __device__ __forceinline__ void wave_order() { __builtin_amdgcn_wave_barrier(); }
@@ -678,7 +684,7 @@ __global__ __launch_bounds__(64) void k_fwd(DiagArgs a) {
   constexpr int KP = 4, GPW = Geo<KP>::GPW;
   __shared__ __align__(16) float s_v[2][GPW * VBLK];
   // start states of the groups (prefix rows: the carries rebuilt inside the quad), then level-2 row staging
-  __shared__ __align__(16) float s_row[GPW][DIM + DIM * DIM];
+  __shared__ __align__(16) float s_row[GPW][RBUF];
   const Lane l = lane_of<KP>(threadIdx.x);
   const int b = blockIdx.y, cb = blockIdx.x * GPW, c = cb + l.gi;
   VRaw<GPW, BF16> vr;
@@ -769,8 +775,8 @@ __global__ __launch_bounds__(64) void k_fwd(DiagArgs a) {
         if (a.lvl0 && l.gl == 0) row[0] = 1.0f;
         if (l.kg == 0) *reinterpret_cast<f2u*>(row + o1) = f2u{S1.re, S1.im};
         float* buf = s_row[l.gi];
-        f4a* p0 = reinterpret_cast<f4a*>(buf + 32 * l.j + 2 * KP * l.kg);
-        f4a* p1 = reinterpret_cast<f4a*>(buf + 32 * l.j + DIM + 2 * KP * l.kg);
+        f4a* p0 = reinterpret_cast<f4a*>(buf + row_at(2 * l.j) + 2 * KP * l.kg);
+        f4a* p1 = reinterpret_cast<f4a*>(buf + row_at(2 * l.j + 1) + 2 * KP * l.kg);
         static_for<0, KP / 2>([&](auto ic) {
           constexpr int i = ic, q0 = 2 * i, q1 = 2 * i + 1;
           p0[i] = f4a{SA[q0].re + SB_[q0].re, SB_[q0].im - SA[q0].im, SA[q1].re + SB_[q1].re, SB_[q1].im - SA[q1].im};
@@ -781,7 +787,7 @@ __global__ __launch_bounds__(64) void k_fwd(DiagArgs a) {
         static_for<0, Pieces<KP>::NP>([&](auto ic) {
           constexpr int i = ic;
           const int pi = l.gl + Geo<KP>::G * i;
-          const f4a v = *reinterpret_cast<const f4a*>(buf + 4 * pi);
+          const f4a v = *reinterpret_cast<const f4a*>(buf + piece_at(pi));
           *reinterpret_cast<f4u*>(row2 + 4 * pi) = f4u{v.x, v.y, v.z, v.w};
         });
         wave_order();
@@ -821,16 +827,16 @@ template <int KP> __device__ __forceinline__ GRaw<KP> load_graw(const float* row
   return r;
 }
 // raw row -> LDS -> the lane's slice
-// The level-1 pair goes through LDS too (buf[256 + 2j]), so that every register of the raw row is dead once
+// The level-1 pair goes through LDS too (buf[RBUF + 2j]), so that every register of the raw row is dead once
 // this returns and a ring slot can be reloaded in place.
 template <int KP> __device__ __forceinline__ GRow<KP> slice_g(const GRaw<KP>& r, float* buf, const Lane& l) {
   pieces_to_lds<KP>(r.pc, buf, l.gl);
-  *reinterpret_cast<float2*>(buf + DIM * DIM + 2 * l.j) = float2{r.g1.x, r.g1.y};
+  *reinterpret_cast<float2*>(buf + RBUF + 2 * l.j) = float2{r.g1.x, r.g1.y};
   wave_order();
   GRow<KP> g;
-  g.g1 = *reinterpret_cast<const float2*>(buf + DIM * DIM + 2 * l.j);
-  const f4a* p0 = reinterpret_cast<const f4a*>(buf + 32 * l.j + 2 * KP * l.kg);
-  const f4a* p1 = reinterpret_cast<const f4a*>(buf + 32 * l.j + DIM + 2 * KP * l.kg);
+  g.g1 = *reinterpret_cast<const float2*>(buf + RBUF + 2 * l.j);
+  const f4a* p0 = reinterpret_cast<const f4a*>(buf + row_at(2 * l.j) + 2 * KP * l.kg);
+  const f4a* p1 = reinterpret_cast<const f4a*>(buf + row_at(2 * l.j + 1) + 2 * KP * l.kg);
   static_for<0, KP / 2>([&](auto ic) {
     constexpr int i = ic;
     g.r0[i] = p0[i];
@@ -853,7 +859,7 @@ template <bool BF16>
 __global__ __launch_bounds__(64) void k_bwd_local(DiagArgs a) {
   constexpr int KP = 4, GPW = Geo<KP>::GPW;
   __shared__ __align__(16) float s_v[2][GPW * VBLK];
-  __shared__ __align__(16) float s_row[GPW][DIM * DIM + DIM];  // cotangent row staging
+  __shared__ __align__(16) float s_row[GPW][RBUF + DIM];  // cotangent row staging (+ level 1)
   const Lane l = lane_of<KP>(threadIdx.x);
   const int b = blockIdx.y, cb = blockIdx.x * GPW, c = cb + l.gi;
   const int nblk = (a.T + SB - 1) / SB;
@@ -954,7 +960,7 @@ __global__ __launch_bounds__(64) void k_bwd_full(DiagArgs a) {
   __shared__ __align__(16) float s_dhp[GPW][NB * G];        // dh partials [t][lane]
   __shared__ __align__(16) float s_dvo[GPW][(NB + 1) * DIM];  // dv of the block's steps; row NB: the step after
   __shared__ float s_dho[GPW][NB + 1];
-  __shared__ __align__(16) float s_row[GPW][DIM * DIM + DIM];  // cotangent row staging
+  __shared__ __align__(16) float s_row[GPW][RBUF + DIM];  // cotangent row staging (+ level 1)
   __shared__ __align__(16) float s_mt[GPW][DIM + DIM * DIM];  // cotangent from later chunks, per group
   const Lane l = lane_of<KP>(threadIdx.x);
   const int b = blockIdx.y, cb = blockIdx.x * GPW, c = cb + l.gi;
