@@ -47,6 +47,9 @@ typedef float f4 __attribute__((ext_vector_type(4)));
 __device__ __forceinline__ f4 mfma(float a, float b, f4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
 }
+// LDS operations of one wavefront execute in program order: a compiler barrier orders a write before another
+// lane's read of it
+__device__ __forceinline__ void wave_order_d() { __builtin_amdgcn_wave_barrier(); }
 
 struct Args {
   int B, L, n_int, d, N, q, flow_mode, readout, lvl0, W, LW;
@@ -235,6 +238,158 @@ __global__ __launch_bounds__(256) void k_local(Args a) {
       }
     }
     __syncthreads();
+  }
+}
+
+// Depth-3 local terms on MFMA, one wavefront per interval (four per workgroup, grid-stride). The letters come
+// from the recursion b_p = (-h/p) A b_{p-1} (lane (c16, g) holds A[c16][4g .. 4g+3]); the degree-N blocks
+// g2_N = 1/(N+2) sum_{p <= N} b_p (x) g1_{N-p} are MFMAs with the contraction over p; four degree slices at a
+// time go through LDS and feed the level-3 contraction s3[a][i][j] = sum_N bt_N[a] g2_N[i][j] (one k-step of
+// four degrees per slice set, sixteen output tiles, tile i holding s3[.][i][.]). Rows p > q of the letter
+// buffer stay zero, so the unrolled k-steps over whole groups of four degrees add nothing beyond the order q.
+template <int QB>
+__global__ __launch_bounds__(256) void k_local3(Args a) {
+  constexpr int QB4 = (QB + 4) / 4 * 4;  // letter rows 0 .. QB4-1 (QB + 1 rounded up to whole k-steps)
+  constexpr int G2S = 16 * RP + 16;      // LDS floats per degree slice (row pitch RP; slices on offset banks)
+  constexpr int NINV = 2 * QB4 + 8;      // reciprocals 1/n, n < NINV (no divisions in the loops)
+  __shared__ __align__(16) float sp[PM + 1][256];   // P_p = A^p / p!, p <= PM (flows; P_1 = A)
+  __shared__ __align__(16) float lt[4][QB4 * 16];   // letters b_p of each wave's interval
+  __shared__ __align__(16) float gt[4][QB4 * 16];   // g1_n = b_n / (n + 1)
+  __shared__ __align__(16) float g2b[4][4 * G2S];   // four degree slices of g2 per wave
+  __shared__ __align__(16) float mmw[4][256];       // flow squarings per wave
+  __shared__ float inv[NINV];
+  const int tid = threadIdx.x, w = tid >> 6, l = tid & 63, g = l >> 4, c16 = l & 15;
+  const int q = a.q;
+  for (int e = tid; e < (PM + 1) * 256; e += 256) sp[e >> 8][e & 255] = a.apow[e];
+  for (int e = tid; e < NINV; e += 256) inv[e] = e ? 1.0f / (float)e : 0.0f;
+  const float norm1 = a.apow[a.npow * 256];
+  float* L = lt[w];
+  float* G1 = gt[w];
+  float* G2 = g2b[w];
+  for (int e = l; e < QB4 * 16; e += 64) L[e] = G1[e] = 0.0f;
+  __syncthreads();
+  const f4 a4 = *reinterpret_cast<const f4*>(&sp[1][c16 * 16 + 4 * g]);  // A[c16][4g .. 4g+3]
+  const long total = (long)a.B * a.n_int;
+  for (long it = (long)blockIdx.x * 4 + w; it < total; it += (long)gridDim.x * 4) {
+    const int b = (int)(it / a.n_int), t = (int)(it - (long)b * a.n_int);
+    const float* th = a.clock + (size_t)b * a.L;
+    const float h = th[t + 1] - th[t];
+    wave_order_d();  // the previous interval's reads of L / G1 / G2 come first
+    if (l < 16) {
+      const float* x = a.path + ((size_t)b * a.L + t) * a.d;
+      const float v = l < a.d ? x[a.d + l] - x[l] : 0.0f;
+      L[l] = v;
+      G1[l] = v;
+    }
+    wave_order_d();
+    for (int pp = 1; pp <= q; ++pp) {
+      const f4 bp = *reinterpret_cast<const f4*>(L + (pp - 1) * 16 + 4 * g);
+      float sm = fmaf(a4.x, bp.x, fmaf(a4.y, bp.y, fmaf(a4.z, bp.z, a4.w * bp.w)));
+      sm += __shfl_xor(sm, 16, 64);
+      sm += __shfl_xor(sm, 32, 64);
+      const float bv = sm * (-h * inv[pp]);
+      if (g == 0) L[pp * 16 + c16] = bv;
+      if (g == 1) G1[pp * 16 + c16] = bv * inv[pp + 1];
+      wave_order_d();
+    }
+    float* row = a.loc + ((size_t)b * a.n_int + t) * a.LW;
+    if (l < 16) {
+      float sm = 0.0f;
+      for (int n = 0; n <= q; ++n) sm += G1[n * 16 + l];
+      row[l] = sm;
+    }
+    f4 acc3[16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) acc3[i] = f4{0.0f, 0.0f, 0.0f, 0.0f};
+    f4 s2acc = {0.0f, 0.0f, 0.0f, 0.0f};
+    const int nks = (q + 4) / 4;  // k-steps that hold a degree <= q
+#pragma unroll 1
+    for (int ks = 0; ks < nks; ++ks) {
+      // A operand of this level-3 k-step: bt_N[c16] = sum_{p <= q - N} b_p[c16] / (p + N + 3), N = 4 ks + g
+      float btv = 0.0f;
+      {
+        const int N = 4 * ks + g;
+        for (int pp = 0; pp + N <= q; ++pp) btv = fmaf(L[pp * 16 + c16], inv[pp + N + 3], btv);
+      }
+      // the four degrees N = 4 ks + nn as independent accumulators: one letter column b_p (p = 4 kp + g) per
+      // k-step serves all four (g1_{N-p} is zero for p > N; degrees above q come out zero)
+      f4 dd[4];
+#pragma unroll
+      for (int nn = 0; nn < 4; ++nn) dd[nn] = f4{0.0f, 0.0f, 0.0f, 0.0f};
+      for (int kp = 0; kp <= ks; ++kp) {
+        const int pp = 4 * kp + g;
+        const float av = L[pp * 16 + c16];  // b_p[i]
+#pragma unroll
+        for (int nn = 0; nn < 4; ++nn) {
+          const int n = 4 * ks + nn - pp;
+          const float bv = (n >= 0 && 4 * ks + nn <= q) ? G1[max(n, 0) * 16 + c16] : 0.0f;  // g1_{N-p}[j]
+          dd[nn] = mfma(av, bv, dd[nn]);
+        }
+      }
+#pragma unroll
+      for (int nn = 0; nn < 4; ++nn) {
+        const float sc = inv[4 * ks + nn + 2];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) dd[nn][r] *= sc;
+        s2acc += dd[nn];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) G2[nn * G2S + (4 * g + r) * RP + c16] = dd[nn][r];
+      }
+      wave_order_d();
+      // tile i, transposed: rows j, columns a (A operand g2_N[i][j], B operand bt_N[a]), so that the lane's four
+      // result registers are s3[c16][i][4g .. 4g+3], one 16-byte store
+      const float* gs = G2 + g * G2S;
+#pragma unroll
+      for (int i = 0; i < 16; ++i) acc3[i] = mfma(gs[i * RP + c16], btv, acc3[i]);
+      wave_order_d();
+    }
+#pragma unroll
+    for (int r = 0; r < 4; ++r) row[16 + (4 * g + r) * 16 + c16] = s2acc[r];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) *reinterpret_cast<f4*>(row + 272 + c16 * 256 + i * 16 + 4 * g) = acc3[i];
+    // flow M_t = exp(-h_f A): Taylor of degree PM in X = -h_f A / 2^s (lane: entries 4l .. 4l+3), s squarings
+    {
+      bool ident;
+      const float hf = flow_step(a, th, t, ident);
+      float* fr = a.fl + ((size_t)b * a.n_int + t) * 256;
+      f4 m;
+      if (ident) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) m[r] = ((4 * l + r) >> 4) == ((4 * l + r) & 15) ? 1.0f : 0.0f;
+      } else {
+        int sq = 0;
+        float x = fabsf(hf) * norm1;
+        while (x > 1.0f && sq < 30) {
+          x *= 0.5f;
+          ++sq;
+        }
+        const float y = -hf * ldexpf(1.0f, -sq);
+        m = *reinterpret_cast<const f4*>(&sp[PM][4 * l]);
+#pragma unroll
+        for (int pp = PM - 1; pp >= 0; --pp) {
+          const f4 c = *reinterpret_cast<const f4*>(&sp[pp][4 * l]);
+#pragma unroll
+          for (int r = 0; r < 4; ++r) m[r] = fmaf(m[r], y, c[r]);
+        }
+        float* mm = mmw[w];
+        const int i = l >> 2, j0 = 4 * (l & 3);
+        for (int r2 = 0; r2 < sq; ++r2) {
+          *reinterpret_cast<f4*>(mm + 4 * l) = m;
+          wave_order_d();
+          f4 v = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+          for (int cc = 0; cc < 16; ++cc) {
+            const float mic = mm[i * 16 + cc];
+            const f4 mr = *reinterpret_cast<const f4*>(mm + cc * 16 + j0);
+#pragma unroll
+            for (int r = 0; r < 4; ++r) v[r] = fmaf(mic, mr[r], v[r]);
+          }
+          wave_order_d();
+          m = v;
+        }
+      }
+      *reinterpret_cast<f4*>(fr + 4 * l) = m;
+    }
   }
 }
 
@@ -593,7 +748,21 @@ int launch_local(const DPlan& p, const Args& a, hipStream_t st) {
   }
   if (p.N == 1) { EWS_LOCAL_Q(1) }
   else if (p.N == 2) { EWS_LOCAL_Q(2) }
-  else { EWS_LOCAL_Q(3) }
+  else {
+    const int grid3 = (int)((total + 3) / 4 < 2048 ? (total + 3) / 4 : 2048);
+#define EWS_LOCAL3(QQ) hipLaunchKernelGGL((k_local3<QQ>), dim3(grid3), dim3(256), 0, st, a)
+    switch (p.QB) {
+      case 4: EWS_LOCAL3(4); break;
+      case 8: EWS_LOCAL3(8); break;
+      case 12: EWS_LOCAL3(12); break;
+      case 16: EWS_LOCAL3(16); break;
+      case 20: EWS_LOCAL3(20); break;
+      case 24: EWS_LOCAL3(24); break;
+      case 32: EWS_LOCAL3(32); break;
+      default: EWS_LOCAL3(40); break;
+    }
+#undef EWS_LOCAL3
+  }
 #undef EWS_LOCAL_Q
 #undef EWS_LOCAL
   DENSE_CHECK();
