@@ -1112,43 +1112,102 @@ __global__ __launch_bounds__(64) void k_bwd_full(DiagArgs a) {
       const cf H1 = f.rhoi * cj;
       cf toC{0.0f, 0.0f}, toP{0.0f, 0.0f};
       float dhp = 0.0f;
-      static_for<0, KP>([&](auto qc) {
-        constexpr int q = qc;
-        cf gA, gB;
-        g_pair<KP, q>(g, gA, gB);
-        const cf A = lA[q] + gA, Bc = lB[q] + gB;  // doubled cotangents of SA(t), SB(t)
-        const cf sg = f.phk[q] * pk[q];
-        cf pi, pic;
-        prods(pj, pk[q], pi, pic);
-        const cf XB = SB[q] - cj * sg - f.IB[q] * pi;
-        const cf XA = SA[q] - cj * conj(sg) - f.IA[q] * pic;
-        const cf HB = f.LBi[q] * XB;
-        const cf HA = f.LAi[q] * XA;
-        // row terms (plane j)
-        toC += cjm(sg, Bc) + sg * A;
-        const cf gf = cjm(f.IB[q], Bc);
-        const cf ge = cjm(f.IA[q], A);
-        toP += cjm(pk[q], gf) + pk[q] * ge;
-        // column terms (plane k): dv_k share and the phi_k cotangent share
-        const cf tS = cjm(cj, Bc) + cjm(A, cj);
-        const cf w = cjm(f.phk[q], tS) + cjm(pj, gf) + cjm(ge, pj);
-        *reinterpret_cast<float2*>(w_g + ((s * K + KP * l.kg + q) * K + l.j) * 2) = float2{w.re, w.im};
-        const cf gph = cjm(pk[q], tS);
-        if constexpr (DH) dhp += redot(gph, f.phi1h[q]);
-        kph[q] = fma_c(cf{h, 0.0f}, gph, kph[q]);
-        // coefficient cotangents
-        const cf gIB = cjm(pi, Bc), gIA = cjm(pic, A), gLB = cjm(HB, Bc), gLA = cjm(HA, A);
-        if constexpr (DH)
-          dhp += redot(gIB, f.IB1[q]) + redot(gIA, f.IA1[q]) + redot(gLB, f.LB1[q]) + redot(gLA, f.LA1[q]);
-        kIB[q] = fma_c(cf{h, 0.0f}, gIB, kIB[q]);
-        kIA[q] = fma_c(cf{h, 0.0f}, gIA, kIA[q]);
-        kLB[q] = fma_c(cf{h, 0.0f}, gLB, kLB[q]);
-        kLA[q] = fma_c(cf{h, 0.0f}, gLA, kLA[q]);
-        lB[q] = cjm(f.LB[q], Bc);
-        lA[q] = cjm(f.LA[q], A);
-        SB[q] = HB;
-        SA[q] = HA;
-      });
+      if constexpr (DH) {
+        static_for<0, KP>([&](auto qc) {
+          constexpr int q = qc;
+          cf gA, gB;
+          g_pair<KP, q>(g, gA, gB);
+          const cf A = lA[q] + gA, Bc = lB[q] + gB;  // doubled cotangents of SA(t), SB(t)
+          const cf sg = f.phk[q] * pk[q];
+          cf pi, pic;
+          prods(pj, pk[q], pi, pic);
+          const cf XB = SB[q] - cj * sg - f.IB[q] * pi;
+          const cf XA = SA[q] - cj * conj(sg) - f.IA[q] * pic;
+          const cf HB = f.LBi[q] * XB;
+          const cf HA = f.LAi[q] * XA;
+          // row terms (plane j)
+          toC += cjm(sg, Bc) + sg * A;
+          const cf gf = cjm(f.IB[q], Bc);
+          const cf ge = cjm(f.IA[q], A);
+          toP += cjm(pk[q], gf) + pk[q] * ge;
+          // column terms (plane k): dv_k share and the phi_k cotangent share
+          const cf tS = cjm(cj, Bc) + cjm(A, cj);
+          const cf w = cjm(f.phk[q], tS) + cjm(pj, gf) + cjm(ge, pj);
+          *reinterpret_cast<float2*>(w_g + ((s * K + KP * l.kg + q) * K + l.j) * 2) = float2{w.re, w.im};
+          const cf gph = cjm(pk[q], tS);
+          if constexpr (DH) dhp += redot(gph, f.phi1h[q]);
+          kph[q] = fma_c(cf{h, 0.0f}, gph, kph[q]);
+          // coefficient cotangents
+          const cf gIB = cjm(pi, Bc), gIA = cjm(pic, A), gLB = cjm(HB, Bc), gLA = cjm(HA, A);
+          if constexpr (DH)
+            dhp += redot(gIB, f.IB1[q]) + redot(gIA, f.IA1[q]) + redot(gLB, f.LB1[q]) + redot(gLA, f.LA1[q]);
+          kIB[q] = fma_c(cf{h, 0.0f}, gIB, kIB[q]);
+          kIA[q] = fma_c(cf{h, 0.0f}, gIA, kIA[q]);
+          kLB[q] = fma_c(cf{h, 0.0f}, gLB, kLB[q]);
+          kLA[q] = fma_c(cf{h, 0.0f}, gLA, kLA[q]);
+          lB[q] = cjm(f.LB[q], Bc);
+          lA[q] = cjm(f.LA[q], A);
+          SB[q] = HB;
+          SA[q] = HA;
+        });
+      } else {
+        // the same step in explicit real arithmetic, shared sums P = Bc + A, Q = Bc - A and F = gf + ge,
+        // E = gf - ge; the coefficient cotangents accumulate as dot products with the h-scaled cotangents
+        static_for<0, KP>([&](auto qc) {
+          constexpr int q = qc;
+          cf gA, gB;
+          g_pair<KP, q>(g, gA, gB);
+          const float Ar = lA[q].re + gA.re, Ai = lA[q].im + gA.im;  // doubled cotangents of SA(t), SB(t)
+          const float Br = lB[q].re + gB.re, Bi = lB[q].im + gB.im;
+          const float Pr = Br + Ar, Pi = Bi + Ai, Qr = Br - Ar, Qi = Bi - Ai;
+          const cf pkq = pk[q], ph = f.phk[q];
+          const float sgr = fmaf(ph.re, pkq.re, -ph.im * pkq.im), sgi = fmaf(ph.re, pkq.im, ph.im * pkq.re);
+          const float aa = pj.re * pkq.re, bb = pj.im * pkq.im, cc = pj.re * pkq.im, dd = pj.im * pkq.re;
+          const float pir = aa - bb, pii = cc + dd, pcr = aa + bb, pci = dd - cc;  // p_j p_k, p_j conj(p_k)
+          const float rr = cj.re * sgr, ii = cj.im * sgi, ri = cj.re * sgi, ir = cj.im * sgr;
+          const cf IB = f.IB[q], IA = f.IA[q];
+          // previous states: X = S(t) - local terms, H = flow^-1 X
+          const float XBr = fmaf(IB.im, pii, fmaf(-IB.re, pir, SB[q].re - rr + ii));
+          const float XBi = fmaf(-IB.im, pir, fmaf(-IB.re, pii, SB[q].im - ri - ir));
+          const float XAr = fmaf(IA.im, pci, fmaf(-IA.re, pcr, SA[q].re - rr - ii));
+          const float XAi = fmaf(-IA.im, pcr, fmaf(-IA.re, pci, SA[q].im - ir + ri));
+          const cf LBi = f.LBi[q], LAi = f.LAi[q];
+          const float HBr = fmaf(LBi.re, XBr, -LBi.im * XBi), HBi = fmaf(LBi.re, XBi, LBi.im * XBr);
+          const float HAr = fmaf(LAi.re, XAr, -LAi.im * XAi), HAi = fmaf(LAi.re, XAi, LAi.im * XAr);
+          // row terms (plane j): toC += conj(sg) Bc + sg A; toP += conj(p_k) gf + p_k ge
+          toC.re = fmaf(sgr, Pr, fmaf(sgi, Qi, toC.re));
+          toC.im = fmaf(sgr, Pi, fmaf(-sgi, Qr, toC.im));
+          const float gfr = fmaf(IB.re, Br, IB.im * Bi), gfi = fmaf(IB.re, Bi, -IB.im * Br);  // conj(IB) Bc
+          const float ger = fmaf(IA.re, Ar, IA.im * Ai), gei = fmaf(IA.re, Ai, -IA.im * Ar);  // conj(IA) A
+          const float Fr = gfr + ger, Fi = gfi + gei, Er = gfr - ger, Ei = gfi - gei;
+          toP.re = fmaf(pkq.re, Fr, fmaf(pkq.im, Ei, toP.re));
+          toP.im = fmaf(pkq.re, Fi, fmaf(-pkq.im, Er, toP.im));
+          // column terms (plane k): tS = conj(c_j) Bc + conj(A) c_j; w = conj(phi_k/2) tS + conj(p_j) gf + conj(ge) p_j
+          const float tSr = fmaf(cj.re, Pr, cj.im * Pi), tSi = fmaf(cj.re, Qi, -cj.im * Qr);
+          const float wr = fmaf(ph.re, tSr, fmaf(ph.im, tSi, fmaf(pj.re, Fr, pj.im * Fi)));
+          const float wi = fmaf(ph.re, tSi, fmaf(-ph.im, tSr, fmaf(pj.re, Ei, -pj.im * Er)));
+          *reinterpret_cast<float2*>(w_g + ((s * K + KP * l.kg + q) * K + l.j) * 2) = float2{wr, wi};
+          // coefficient cotangents, summed with the step's h: conj(p_k) tS, conj(pi) Bc, conj(pic) A,
+          // conj(HB) Bc, conj(HA) A
+          const float tSrh = h * tSr, tSih = h * tSi, Brh = h * Br, Bih = h * Bi, Arh = h * Ar, Aih = h * Ai;
+          kph[q].re = fmaf(pkq.re, tSrh, fmaf(pkq.im, tSih, kph[q].re));
+          kph[q].im = fmaf(pkq.re, tSih, fmaf(-pkq.im, tSrh, kph[q].im));
+          kIB[q].re = fmaf(pir, Brh, fmaf(pii, Bih, kIB[q].re));
+          kIB[q].im = fmaf(pir, Bih, fmaf(-pii, Brh, kIB[q].im));
+          kIA[q].re = fmaf(pcr, Arh, fmaf(pci, Aih, kIA[q].re));
+          kIA[q].im = fmaf(pcr, Aih, fmaf(-pci, Arh, kIA[q].im));
+          kLB[q].re = fmaf(HBr, Brh, fmaf(HBi, Bih, kLB[q].re));
+          kLB[q].im = fmaf(HBr, Bih, fmaf(-HBi, Brh, kLB[q].im));
+          kLA[q].re = fmaf(HAr, Arh, fmaf(HAi, Aih, kLA[q].re));
+          kLA[q].im = fmaf(HAr, Aih, fmaf(-HAi, Arh, kLA[q].im));
+          // adjoint carried to the previous step, state stepped back
+          const cf LB = f.LB[q], LA = f.LA[q];
+          lB[q] = cf{fmaf(LB.re, Br, LB.im * Bi), fmaf(LB.re, Bi, -LB.im * Br)};
+          lA[q] = cf{fmaf(LA.re, Ar, LA.im * Ai), fmaf(LA.re, Ai, -LA.im * Ar)};
+          SB[q] = cf{HBr, HBi};
+          SA[q] = cf{HAr, HAi};
+        });
+      }
       toC = kg_sum<KP>(toC);
       toP = kg_sum<KP>(toP);
       const cf gc = l1 + toC;

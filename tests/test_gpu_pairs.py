@@ -168,7 +168,8 @@ def test_layer_api_on_pair_kernels():
 
 
 def test_null_clock_gradient_leaves_the_other_gradients_unchanged():
-    """grad_clock = NULL skips the clock terms of the adjoint; path and parameter gradients are the same bits."""
+    """grad_clock = NULL selects the adjoint without clock terms (its own arithmetic): the forward is the same bits,
+    and the path and parameter gradients meet the same bar against the float64 checker."""
     B, L = 2, 700
     path, clock, dw = _inputs(B, L, seed=11)
     W = 1 + path.shape[2] + path.shape[2] ** 2
@@ -176,5 +177,9 @@ def test_null_clock_gradient_leaves_the_other_gradients_unchanged():
     out1, dp1, _, dd1, _ = _run(path, clock, dw, g, clock_grad=True)
     out2, dp2, _, dd2, _ = _run(path, clock, dw, g, clock_grad=False)
     assert np.array_equal(out1, out2)
-    assert np.array_equal(dp1, dp2)
-    assert np.array_equal(dd1, dd2)
+    rdp, _, rdd = C.planes_backward(path.astype(np.float64), clock.astype(np.float64), dw.astype(np.float64),
+                                    g.astype(np.float64), kind="f64")
+    errs = dict(dpath=relerr(dp2, rdp), dparams=relerr(dd2, rdd), dpath_vs_clock=relerr(dp2, dp1),
+                dparams_vs_clock=relerr(dd2, dd1))
+    print(errs)
+    assert errs["dpath"] < 1e-4 and errs["dparams"] < 1e-4, errs
