@@ -235,7 +235,9 @@ __device__ __forceinline__ ChunkClock chunk_clock(const DiagArgs& a, int b, int 
   float R = 0.0f;
   T dummy{};
   for (int j = 0; j < a.K; ++j) R = fmaxf(R, absv(load_u(a.params, j, &dummy)));
-  cc.fast = finite && (dmax * 2.0f * R < 1.52587890625e-5f);  // 2^-16
+  // with the pair-group kernels active (a.fast_ok) they own every uniform chunk; the chunks left here take exact
+  // per-step coefficients, so that the FAST instantiations have no work and are not launched
+  cc.fast = finite && (dmax * 2.0f * R < 1.52587890625e-5f) && !a.fast_ok;  // 2^-16
   cc.per_int = a.flow_mode == EWS_FLOW_PER_INTERVAL;
   const float* th = a.clock + (size_t)b * a.L;
   if (a.flow_mode == EWS_FLOW_CACHED) {
@@ -1797,9 +1799,10 @@ int forward_pass(const ews_diag_desc* s, const Plan& p, DiagArgs a, hipStream_t 
     case 0:
       if (p.fast) {
         if (pairs_forward(a, st, false) != 0) return EWS_ERR_LAUNCH;
+      } else {
+        hipLaunchKernelGGL((k_chunk_fwd<CPLX, N, MODE_SUMMARY, MAXT, true>), grid, blk, fwd_lds(p), st, a);
+        EWS_LAUNCH_CHECK();
       }
-      hipLaunchKernelGGL((k_chunk_fwd<CPLX, N, MODE_SUMMARY, MAXT, true>), grid, blk, fwd_lds(p), st, a);
-      EWS_LAUNCH_CHECK();
       hipLaunchKernelGGL((k_chunk_fwd<CPLX, N, MODE_SUMMARY, MAXT, false>), grid, blk, fwd_lds(p), st, a);
       break;
     case 1:
@@ -1815,9 +1818,12 @@ int forward_pass(const ews_diag_desc* s, const Plan& p, DiagArgs a, hipStream_t 
       break;
     case 2:
       if (s->readout == EWS_READOUT_PREFIX) {
-        if (p.fast && pairs_forward(a, st, true) != 0) return EWS_ERR_LAUNCH;
-        hipLaunchKernelGGL((k_chunk_fwd<CPLX, N, MODE_PREFIX, MAXT, true>), grid, blk, fwd_lds(p), st, a);
-        EWS_LAUNCH_CHECK();
+        if (p.fast) {
+          if (pairs_forward(a, st, true) != 0) return EWS_ERR_LAUNCH;
+        } else {
+          hipLaunchKernelGGL((k_chunk_fwd<CPLX, N, MODE_PREFIX, MAXT, true>), grid, blk, fwd_lds(p), st, a);
+          EWS_LAUNCH_CHECK();
+        }
         hipLaunchKernelGGL((k_chunk_fwd<CPLX, N, MODE_PREFIX, MAXT, false>), grid, blk, fwd_lds(p), st, a);
       } else if (s->readout == EWS_READOUT_MEAN || s->readout == EWS_READOUT_MAX) {
         hipLaunchKernelGGL((k_chunk_fwd<CPLX, N, MODE_REDUCE, MAXT, true>), grid, blk, fwd_lds(p), st, a);
@@ -1860,8 +1866,10 @@ int backward_pass(const Plan& p, DiagArgs a, hipStream_t st, int pass) {
       if (p.fast && pairs_backward(a, st, false) != 0) return EWS_ERR_LAUNCH;
       if (set_lds(&k_chunk_bwd_local<CPLX, N, MAXT, WAVE, true>, p.lds_bwd_local) != EWS_OK) return EWS_ERR_LAUNCH;
       if (set_lds(&k_chunk_bwd_local<CPLX, N, MAXT, WAVE, false>, p.lds_bwd_local) != EWS_OK) return EWS_ERR_LAUNCH;
-      hipLaunchKernelGGL((k_chunk_bwd_local<CPLX, N, MAXT, WAVE, true>), grid, blkb, p.lds_bwd_local, st, a);
-      EWS_LAUNCH_CHECK();
+      if (!p.fast) {  // with the pair kernels active no chunk is left to the FAST instantiation
+        hipLaunchKernelGGL((k_chunk_bwd_local<CPLX, N, MAXT, WAVE, true>), grid, blkb, p.lds_bwd_local, st, a);
+        EWS_LAUNCH_CHECK();
+      }
       hipLaunchKernelGGL((k_chunk_bwd_local<CPLX, N, MAXT, WAVE, false>), grid, blkb, p.lds_bwd_local, st, a);
       break;
     case 1:
@@ -1881,8 +1889,10 @@ int backward_pass(const Plan& p, DiagArgs a, hipStream_t st, int pass) {
       if (p.fast && pairs_backward(a, st, true) != 0) return EWS_ERR_LAUNCH;
       if (set_lds(&k_chunk_bwd_inv<CPLX, N, MAXT, WAVE>, p.lds_bwd_inv) != EWS_OK) return EWS_ERR_LAUNCH;
       if (set_lds(&k_chunk_bwd_full<CPLX, N, MAXT, WAVE>, p.lds_bwd_full) != EWS_OK) return EWS_ERR_LAUNCH;
-      hipLaunchKernelGGL((k_chunk_bwd_inv<CPLX, N, MAXT, WAVE>), grid, blkb, p.lds_bwd_inv, st, a);
-      EWS_LAUNCH_CHECK();
+      if (!p.fast) {  // k_chunk_bwd_inv owns only FAST chunks
+        hipLaunchKernelGGL((k_chunk_bwd_inv<CPLX, N, MAXT, WAVE>), grid, blkb, p.lds_bwd_inv, st, a);
+        EWS_LAUNCH_CHECK();
+      }
       hipLaunchKernelGGL((k_chunk_bwd_full<CPLX, N, MAXT, WAVE>), grid, blkb, p.lds_bwd_full, st, a);
       break;
     case 3:
