@@ -1231,9 +1231,8 @@ __device__ __forceinline__ void bwd_step(const DiagArgs& a, const LaneMap& m, co
 // parameter partials (lane (j, k) contributes to plane j as a row and to plane k as a column).
 template <bool CPLX, int N, bool WAVE, class T>
 __device__ __forceinline__ void bwd_epilogue(const DiagArgs& a, const LaneMap& m, const ChunkClock& cc, BwdAcc<T>& acc,
-                                             T uj, T ua, T ub, int Tc, int t0, float* s_dh, float* s_g) {
+                                             T uj, T ua, T ub, int Tc, int t0, float* s_dh, float* s_g, int c, int b) {
   const int tid = threadIdx.x, NT = blockDim.x, NW = (NT + 63) / 64, wid = tid / 64;
-  const int c = blockIdx.x, b = blockIdx.y;
   for (int t = tid; t < Tc; t += NT) {
     float s = 0.0f;
     for (int w = 0; w < NW; ++w) s += s_dh[t * NW + w];
@@ -1355,7 +1354,7 @@ __device__ __forceinline__ void load_cot(const DiagArgs& a, const LaneMap& m, co
 
 // Shared prologue: clock steps, ownership test, increments, per-sample cotangent, first staged block.
 #define EWS_BWD_PROLOGUE(OWNS, ROWS)                                                                              \
-  const int c = blockIdx.x, b = blockIdx.y, tid = threadIdx.x;                                             \
+  const int tid = threadIdx.x;                                                                             \
   if (a.fast_ok && (a.cflag[b * a.C + c] & 3) == 3) return; /* a pair-group kernel owns this chunk */      \
   const int t0 = c * a.T;                                                                                  \
   const int Tc = min(a.T, a.n_int - t0);                                                                   \
@@ -1395,6 +1394,7 @@ __global__ __launch_bounds__(MAXT) void k_chunk_bwd_inv(DiagArgs a) {
                    smem + Lo.red + 6 * blockDim.x};
   float* s_dh = smem + Lo.dh;
   float* s_g = smem + Lo.g;
+  const int c = blockIdx.x, b = blockIdx.y;
   EWS_BWD_PROLOGUE(cc.fast && cc.inv_ok, kGB)
   Coef<T> c0;
   CoefD<T> q0;
@@ -1450,13 +1450,14 @@ __global__ __launch_bounds__(MAXT) void k_chunk_bwd_inv(DiagArgs a) {
     if (more) lds_dma_wait();
     __syncthreads();
   }
-  bwd_epilogue<CPLX, N, WAVE>(a, m, cc, acc, uj, ua, ub, Tc, t0, s_dh, s_g);
+  bwd_epilogue<CPLX, N, WAVE>(a, m, cc, acc, uj, ua, ub, Tc, t0, s_dh, s_g, c, b);
 }
 
 // (b) Every other chunk: exact per-step coefficients and forward states recomputed from the chunk's float64 carry
 // (checkpoints every kBLK steps; each block recomputed into a lane-private LDS history before its reverse sweep).
+// One chunk c of sample b; every early return is uniform over the workgroup.
 template <bool CPLX, int N, int MAXT, bool WAVE>
-__global__ __launch_bounds__(MAXT) void k_chunk_bwd_full(DiagArgs a) {
+__device__ __forceinline__ void chunk_bwd_full(const DiagArgs& a, const int c, const int b) {
   using T = typename Types<CPLX>::T;
   constexpr int NS = CPLX ? 6 : 2;  // checkpoint floats per lane
   extern __shared__ float smem[];
@@ -1549,7 +1550,25 @@ __global__ __launch_bounds__(MAXT) void k_chunk_bwd_full(DiagArgs a) {
     if (more) lds_dma_wait();
     __syncthreads();
   }
-  bwd_epilogue<CPLX, N, WAVE>(a, m, cc, acc, uj, ua, ub, Tc, t0, s_dh, s_g);
+  bwd_epilogue<CPLX, N, WAVE>(a, m, cc, acc, uj, ua, ub, Tc, t0, s_dh, s_g, c, b);
+}
+// Chunks blockIdx.x, blockIdx.x + gridDim.x, ... of sample blockIdx.y: with the pair kernels active the grid is
+// small (most chunks belong to them), otherwise one chunk per workgroup. The ownership flags of 64 candidate
+// chunks are read at once (one lane each) and only the chunks left to this kernel are visited.
+template <bool CPLX, int N, int MAXT, bool WAVE>
+__global__ __launch_bounds__(MAXT) void k_chunk_bwd_full(DiagArgs a) {
+  const int b = blockIdx.y, lane = threadIdx.x & 63;
+  for (int base = blockIdx.x; base < a.C; base += 64 * gridDim.x) {
+    const int cl = base + gridDim.x * lane;
+    const bool need = cl < a.C && !(a.fast_ok && (a.cflag[b * a.C + cl] & 3) == 3);
+    unsigned long long mask = __ballot(need);  // the same in every wavefront of the workgroup
+    while (mask) {
+      const int i = __ffsll((long long)mask) - 1;
+      mask &= mask - 1;
+      chunk_bwd_full<CPLX, N, MAXT, WAVE>(a, base + gridDim.x * i, b);
+      __syncthreads();
+    }
+  }
 }
 
 // ------------------------------------------------------------------------------------------- B4
@@ -1893,7 +1912,8 @@ int backward_pass(const Plan& p, DiagArgs a, hipStream_t st, int pass) {
         hipLaunchKernelGGL((k_chunk_bwd_inv<CPLX, N, MAXT, WAVE>), grid, blkb, p.lds_bwd_inv, st, a);
         EWS_LAUNCH_CHECK();
       }
-      hipLaunchKernelGGL((k_chunk_bwd_full<CPLX, N, MAXT, WAVE>), grid, blkb, p.lds_bwd_full, st, a);
+      hipLaunchKernelGGL((k_chunk_bwd_full<CPLX, N, MAXT, WAVE>), p.fast ? dim3(min(p.C, 8), p.B) : grid, blkb,
+                         p.lds_bwd_full, st, a);
       break;
     case 3:
       hipLaunchKernelGGL(k_knot_grads, dim3(p.C + 1, p.B), dim3(64), 0, st, a);
