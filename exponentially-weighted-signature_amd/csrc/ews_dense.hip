@@ -54,6 +54,7 @@ __device__ __forceinline__ void wave_order_d() { __builtin_amdgcn_wave_barrier()
 struct Args {
   int B, L, n_int, d, N, q, flow_mode, readout, lvl0, W, LW;
   int T, C, npow;
+  int leaf, vm, vl_expm, vl_mode, chen_expm;  // leaf kind; Van Loan knots M, its scheme and reweighting; flows' scheme
   const float* path;
   const float* clock;
   const float* A;
@@ -64,6 +65,7 @@ struct Args {
   float* sfl;   // (B, C, 256)
   float* car;   // (B, C + 1, LW) state before chunk c (row C: terminal state)
   float* pre;   // (B, n_int, W) prefix rows (mean / max readouts)
+  float* mats;  // (B, 3, 256) per-sample Van Loan step matrices P, V and the shared flow (uniform modes)
   float* out;
 };
 
@@ -393,6 +395,385 @@ __global__ __launch_bounds__(256) void k_local3(Args a) {
   }
 }
 
+// ------------------------------------------------------------------------------------------------ matrix functions
+// Wavefront-level functions of the zero-padded 16 x 16 generator (powers table sp: P_p = A^p / p! in LDS, so
+// sp[1] = A and sp[2] = A^2 / 2). Results are row-major 16 x 16 in per-wave LDS buffers; lane l owns entries
+// 4l .. 4l+3 (row l/4, columns 4(l%4) ..) in the elementwise parts.
+typedef float LdsTable[256];
+
+// E = exp(-c A) and, when Phi is set, Phi = phi(-c A) = sum_p (-c A)^p / (p+1)!: Taylor polynomials of degree
+// PM in X = -c A / 2^s (||X||_1 <= 1), then s doublings E <- E E, Phi <- (Phi + Phi E) / 2
+// (phi(2X) = phi(X) (I + e^X) / 2).
+__device__ __forceinline__ void wave_expm(const LdsTable* sp, float norm1, float c, float* E, float* Phi, int l) {
+  int s = 0;
+  float x = fabsf(c) * norm1;
+  while (x > 1.0f && s < 30) {
+    x *= 0.5f;
+    ++s;
+  }
+  const float y = -c * ldexpf(1.0f, -s);
+  f4 e = *reinterpret_cast<const f4*>(&sp[PM][4 * l]);
+  f4 f = e * (1.0f / (float)(PM + 1));
+#pragma unroll
+  for (int p = PM - 1; p >= 0; --p) {
+    const f4 t = *reinterpret_cast<const f4*>(&sp[p][4 * l]);
+    const float ip = 1.0f / (float)(p + 1);
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      e[r] = fmaf(e[r], y, t[r]);
+      f[r] = fmaf(f[r], y, t[r] * ip);
+    }
+  }
+  const int i = l >> 2, j0 = 4 * (l & 3);
+  for (int r2 = 0; r2 < s; ++r2) {
+    *reinterpret_cast<f4*>(E + 4 * l) = e;
+    if (Phi) *reinterpret_cast<f4*>(Phi + 4 * l) = f;
+    wave_order_d();
+    f4 ne = {0.0f, 0.0f, 0.0f, 0.0f}, nf = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int k = 0; k < 16; ++k) {
+      const f4 ek = *reinterpret_cast<const f4*>(E + k * 16 + j0);
+      const float eik = E[i * 16 + k];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) ne[r] = fmaf(eik, ek[r], ne[r]);
+      if (Phi) {
+        const float fik = Phi[i * 16 + k];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) nf[r] = fmaf(fik, ek[r], nf[r]);
+      }
+    }
+    wave_order_d();
+    e = ne;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) f[r] = 0.5f * (f[r] + nf[r]);
+  }
+  *reinterpret_cast<f4*>(E + 4 * l) = e;
+  if (Phi) *reinterpret_cast<f4*>(Phi + 4 * l) = f;
+  wave_order_d();
+}
+
+// out = (I + alpha A + beta A^2)^{-1} by Gauss-Jordan elimination on [N | I] with partial pivoting (largest
+// magnitude in the column among the rows not yet used, ties to the lower row); rows are not swapped, the
+// pivot order is undone when the result is written. Lane (r, g) holds row r, columns 8g .. 8g+7 of [N | I].
+// xch: 8 floats x 4 groups of LDS for the pivot row.
+__device__ __forceinline__ void wave_inverse(const LdsTable* sp, float alpha, float beta, float* out, float* xch, int l) {
+  const int r = l & 15, g = l >> 4;
+  float m[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    const int col = 8 * g + j;
+    if (g < 2)
+      m[j] = (r == col ? 1.0f : 0.0f) + alpha * sp[1][r * 16 + col] + 2.0f * beta * sp[2][r * 16 + col];
+    else
+      m[j] = (r == col - 16) ? 1.0f : 0.0f;
+  }
+  bool used = false;
+  int krow = 0;
+#pragma unroll
+  for (int k = 0; k < 16; ++k) {
+    const float colv = __shfl(m[k & 7], r + 16 * (k >> 3), 64);  // N'[r][k]
+    float cand = used ? -1.0f : fabsf(colv);
+    int crow = r;
+#pragma unroll
+    for (int o = 1; o < 16; o <<= 1) {
+      const float oc = __shfl_xor(cand, o, 64);
+      const int orow = __shfl_xor(crow, o, 64);
+      if (oc > cand || (oc == cand && orow < crow)) {
+        cand = oc;
+        crow = orow;
+      }
+    }
+    const int p = __builtin_amdgcn_readfirstlane(crow);
+    const float pv = __shfl(colv, p, 64);
+    if (r == p) {
+#pragma unroll
+      for (int j = 0; j < 8; ++j) m[j] = m[j] / pv;
+      used = true;
+      krow = k;
+      *reinterpret_cast<f4*>(xch + 8 * g) = f4{m[0], m[1], m[2], m[3]};
+      *reinterpret_cast<f4*>(xch + 8 * g + 4) = f4{m[4], m[5], m[6], m[7]};
+    }
+    wave_order_d();
+    const f4 lo = *reinterpret_cast<const f4*>(xch + 8 * g);
+    const f4 hi = *reinterpret_cast<const f4*>(xch + 8 * g + 4);
+    wave_order_d();
+    if (r != p) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        m[j] = fmaf(-colv, lo[j], m[j]);
+        m[j + 4] = fmaf(-colv, hi[j], m[j + 4]);
+      }
+    }
+  }
+  // the rows' right halves are the rows of the inverse in pivot order: row r holds inverse row krow
+  if (g >= 2) {
+    float* o = out + krow * 16 + 8 * (g - 2);
+    *reinterpret_cast<f4*>(o) = f4{m[0], m[1], m[2], m[3]};
+    *reinterpret_cast<f4*>(o + 4) = f4{m[4], m[5], m[6], m[7]};
+  }
+  wave_order_d();
+}
+
+// The matrix functions of one step c under a scheme of ews/core/expm_approx.py:13-41.
+//   flow = true:  P = expm_scheme(-c A):   exact exp(-cA); euler I - cA; cayley (I + cA/2)^{-1} (I - cA/2)
+//                 = 2 (I + cA/2)^{-1} - I; pade (I + cA/2 + c^2A^2/12)^{-1} (I - cA/2 + c^2A^2/12)
+//                 = I - c (I + cA/2 + c^2A^2/12)^{-1} A.
+//   flow = false: the Van Loan step of van_loan.py:31-71 with a = c A (c = dt / M): the augmented exponential
+//                 E = expm_scheme([[a, w], [0, 0]]) = [[C, u], [0, 1]]; the knot increments are
+//                 Delta_m = C^{m-1-M} u (m = 1..M), so Delta_M = C^{-1} u = V w and Delta_{m-1} = P Delta_m with
+//                 P = C^{-1}:
+//                   exact  P = exp(-a), V = phi(-a);        cayley V = (I + a/2)^{-1}, P = 2V - I;
+//                   euler  V = (I + a)^{-1}, P = V;         pade   V = (I + a/2 + a^2/12)^{-1}, P = I - V a.
+// Buffers: P and V (V only for flow = false) 256 floats, T 256 + 32 floats of scratch.
+__device__ __forceinline__ void wave_matfn(const LdsTable* sp, float norm1, int scheme, float c, bool flow, float* P, float* V,
+                           float* T, int l) {
+  if (scheme == EWS_EXPM_EXACT) {
+    wave_expm(sp, norm1, c, P, flow ? nullptr : V, l);
+    return;
+  }
+  const int i = l >> 2, j0 = 4 * (l & 3);
+  if (scheme == EWS_EXPM_EULER && flow) {
+    f4 e;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) e[r] = (i == j0 + r ? 1.0f : 0.0f) - c * sp[1][4 * l + r];
+    *reinterpret_cast<f4*>(P + 4 * l) = e;
+    wave_order_d();
+    return;
+  }
+  const float alpha = scheme == EWS_EXPM_EULER ? c : 0.5f * c;
+  const float beta = scheme == EWS_EXPM_PADE ? c * c * (1.0f / 12.0f) : 0.0f;
+  float* inv = flow ? T : V;
+  wave_inverse(sp, alpha, beta, inv, T + 256, l);
+  const f4 vi = *reinterpret_cast<const f4*>(inv + 4 * l);
+  f4 e;
+  if (scheme == EWS_EXPM_CAYLEY) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) e[r] = 2.0f * vi[r] - (i == j0 + r ? 1.0f : 0.0f);
+  } else if (scheme == EWS_EXPM_EULER) {
+    e = vi;
+  } else {  // pade: I - c inv A
+    f4 va = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int k = 0; k < 16; ++k) {
+      const float ik = inv[i * 16 + k];
+      const f4 ak = *reinterpret_cast<const f4*>(&sp[1][k * 16 + j0]);
+#pragma unroll
+      for (int r = 0; r < 4; ++r) va[r] = fmaf(ik, ak[r], va[r]);
+    }
+#pragma unroll
+    for (int r = 0; r < 4; ++r) e[r] = (i == j0 + r ? 1.0f : 0.0f) - c * va[r];
+  }
+  wave_order_d();
+  *reinterpret_cast<f4*>(P + 4 * l) = e;
+  wave_order_d();
+}
+
+__device__ __forceinline__ void wave_identity(float* P, int l) {
+  f4 e;
+#pragma unroll
+  for (int r = 0; r < 4; ++r) e[r] = ((4 * l + r) >> 4) == ((4 * l + r) & 15) ? 1.0f : 0.0f;
+  *reinterpret_cast<f4*>(P + 4 * l) = e;
+  wave_order_d();
+}
+
+// Van Loan step of the uniform reweightings (van_loan.py:91-160): dt = interval_times[0] (uniform) or
+// interval_times[1] (uniform_basepoint, whose interval 0 is the pure jump); a step dt <= 1e-12 is the jump
+// (linear knots, P = V = I).
+__device__ __forceinline__ float vl_shared_step(const Args& a, const float* th) {
+  const float dt = a.vl_mode == EWS_FLOW_CACHED ? th[1] - th[0] : th[2] - th[1];
+  return dt > 1e-12f ? dt / (float)a.vm : 0.0f;
+}
+
+// Per-sample matrices of the uniform modes, one wavefront per sample: the Van Loan P and V of the shared step
+// (mats[b][0], mats[b][1]) and the shared flow (mats[b][2]) of the cached flow modes.
+__global__ __launch_bounds__(64) void k_prep(Args a) {
+  __shared__ __align__(16) float sp[PM + 1][256];
+  __shared__ __align__(16) float P[256], V[256], T[256 + 32];
+  const int l = threadIdx.x, b = blockIdx.x;
+  for (int e = l; e < (PM + 1) * 256; e += 64) sp[e >> 8][e & 255] = a.apow[e];
+  const float norm1 = a.apow[a.npow * 256];
+  __syncthreads();
+  const float* th = a.clock + (size_t)b * a.L;
+  float* mb = a.mats + (size_t)b * 768;
+  if (a.leaf == EWS_LEAF_VAN_LOAN && a.vl_mode != EWS_FLOW_PER_INTERVAL) {
+    wave_matfn(sp, norm1, a.vl_expm, vl_shared_step(a, th), false, P, V, T, l);
+    *reinterpret_cast<f4*>(mb + 4 * l) = *reinterpret_cast<const f4*>(P + 4 * l);
+    *reinterpret_cast<f4*>(mb + 256 + 4 * l) = *reinterpret_cast<const f4*>(V + 4 * l);
+    wave_order_d();
+  }
+  if (a.flow_mode != EWS_FLOW_PER_INTERVAL) {
+    bool ident;
+    const float hf = flow_step(a, th, 1, ident);
+    wave_matfn(sp, norm1, a.chen_expm, hf, true, P, nullptr, T, l);
+    *reinterpret_cast<f4*>(mb + 512 + 4 * l) = *reinterpret_cast<const f4*>(P + 4 * l);
+  }
+}
+
+// Flows M_t = expm_scheme(-h_t A) under chen_expm (chen_scan.py:155-168), one wavefront per interval; the cached
+// modes copy the per-sample flow (identity for interval 0 of the basepoint mode).
+__global__ __launch_bounds__(256) void k_flows(Args a) {
+  __shared__ __align__(16) float sp[PM + 1][256];
+  __shared__ __align__(16) float Pw[4][256], Tw[4][256 + 32];
+  const int tid = threadIdx.x, w = tid >> 6, l = tid & 63;
+  for (int e = tid; e < (PM + 1) * 256; e += 256) sp[e >> 8][e & 255] = a.apow[e];
+  const float norm1 = a.apow[a.npow * 256];
+  __syncthreads();
+  const long total = (long)a.B * a.n_int;
+  for (long it = (long)blockIdx.x * 4 + w; it < total; it += (long)gridDim.x * 4) {
+    const int b = (int)(it / a.n_int), t = (int)(it - (long)b * a.n_int);
+    const float* th = a.clock + (size_t)b * a.L;
+    float* fr = a.fl + ((size_t)b * a.n_int + t) * 256;
+    bool ident;
+    const float hf = flow_step(a, th, t, ident);
+    f4 m;
+    if (ident) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) m[r] = ((4 * l + r) >> 4) == ((4 * l + r) & 15) ? 1.0f : 0.0f;
+    } else if (a.flow_mode != EWS_FLOW_PER_INTERVAL) {
+      m = *reinterpret_cast<const f4*>(a.mats + (size_t)b * 768 + 512 + 4 * l);
+    } else {
+      wave_matfn(sp, norm1, a.chen_expm, hf, true, Pw[w], nullptr, Tw[w], l);
+      m = *reinterpret_cast<const f4*>(Pw[w] + 4 * l);
+      wave_order_d();
+    }
+    *reinterpret_cast<f4*>(fr + 4 * l) = m;
+  }
+}
+
+// ------------------------------------------------------------------------------------------------ Van Loan leaf
+// One wavefront per interval (grid-stride). The knot increments Delta_1..Delta_M of the reweighted path
+// (van_loan.py:31-160: knots K_m = W E^m[:d, d], W = (E^M[:d, :d])^{-1}) are Delta_M = V w, Delta_{m-1} = P Delta_m
+// with w = v / M (see wave_matfn), and the levels are the signature of the piecewise-linear path through the
+// knots (signature.py:20-35): the Chen product of the segments' exponentials, which in closed form is
+//   S1 = sum_m Delta_m,   S2 = sum_m Y_m (x) Delta_m,
+//   S3 = sum_m (Y_m (x) Delta_m (x) R_m + X_m (x) Delta_m (x) Delta_m / 2)
+// with the exclusive prefix sums Pre_m = sum_{j<m} Delta_j, suffix sums R_m = sum_{j>m} Delta_j,
+// Y_m = Pre_m + Delta_m / 2 and X_m = Pre_m + Delta_m / 3 (segment m contributes Delta^{(x)2}/2 and
+// Delta^{(x)3}/6 and meets the segments before and after it). S2 and S3 are 16x16x4 float32 MFMAs contracting
+// over the segment index: S2 = Y^T Delta, and per first index a, S3[a] = G_a^T Delta with
+// G_a[m][c] = Y_m[a] R_m[c] + X_m[a] Delta_m[c] / 2.
+// LDS per wave: P (256), the vector buffer (32), then one region shared by V / scratch (while the step
+// matrices are formed) and the segment table E[m][c] = {Delta, R, Y, X} (row pitch EP floats, MP rows, the rows
+// m >= M zero).
+constexpr int EP = 68;  // row pitch of the segment table (four segments of a k-step on distinct banks)
+
+__host__ __device__ constexpr int vl_rows(int M) { return (M + 3) / 4 * 4; }
+__host__ __device__ constexpr int vl_region(int M) {
+  return 256 + 32 + (EP * vl_rows(M) > 256 + 256 + 32 ? EP * vl_rows(M) : 256 + 256 + 32);
+}
+
+template <int N>
+__global__ __launch_bounds__(256) void k_vl(Args a) {
+  extern __shared__ __align__(16) float lds[];
+  LdsTable* sp = reinterpret_cast<LdsTable*>(lds);
+  const int tid = threadIdx.x, w = tid >> 6, l = tid & 63, g = l >> 4, c16 = l & 15;
+  const int nw = blockDim.x >> 6;
+  const int Mv = a.vm, MP = vl_rows(Mv);
+  for (int e = tid; e < (PM + 1) * 256; e += blockDim.x) lds[e] = a.apow[e];
+  const float norm1 = a.apow[a.npow * 256];
+  float* P = lds + (PM + 1) * 256 + w * vl_region(Mv);
+  float* xs = P + 256;
+  float* V = xs + 32;
+  float* T = V + 256;
+  float* E = V;
+  __syncthreads();
+  const long total = (long)a.B * a.n_int;
+  for (long it = (long)blockIdx.x * nw + w; it < total; it += (long)gridDim.x * nw) {
+    const int b = (int)(it / a.n_int), t = (int)(it - (long)b * a.n_int);
+    const float* th = a.clock + (size_t)b * a.L;
+    wave_order_d();  // the previous interval's reads of the segment table come first
+    // step matrices
+    f4 vrow;  // V[c16][4g .. 4g+3]
+    if (a.vl_mode == EWS_FLOW_PER_INTERVAL) {
+      wave_matfn(sp, norm1, a.vl_expm, (th[t + 1] - th[t]) / (float)Mv, false, P, V, T, l);
+      vrow = *reinterpret_cast<const f4*>(V + c16 * 16 + 4 * g);
+    } else if (a.vl_mode == EWS_FLOW_CACHED_BASEPOINT && t == 0) {
+      wave_identity(P, l);
+#pragma unroll
+      for (int r = 0; r < 4; ++r) vrow[r] = (c16 == 4 * g + r) ? 1.0f : 0.0f;
+    } else {
+      const float* mb = a.mats + (size_t)b * 768;
+      *reinterpret_cast<f4*>(P + 4 * l) = *reinterpret_cast<const f4*>(mb + 4 * l);
+      vrow = *reinterpret_cast<const f4*>(mb + 256 + c16 * 16 + 4 * g);
+      wave_order_d();
+    }
+    const f4 prow = *reinterpret_cast<const f4*>(P + c16 * 16 + 4 * g);
+    // w = v / M
+    if (l < 16) {
+      const float* x = a.path + ((size_t)b * a.L + t) * a.d;
+      xs[l] = l < a.d ? (x[a.d + l] - x[l]) / (float)Mv : 0.0f;
+    }
+    wave_order_d();
+    f4 xv = *reinterpret_cast<const f4*>(xs + 4 * g);
+    float dl = fmaf(vrow.x, xv.x, fmaf(vrow.y, xv.y, fmaf(vrow.z, xv.z, vrow.w * xv.w)));
+    dl += __shfl_xor(dl, 16, 64);
+    dl += __shfl_xor(dl, 32, 64);
+    wave_order_d();  // V is read before the segment table overwrites it
+    // rows M .. MP-1 of the table are zero
+    for (int e = l; e < (MP - Mv) * 16; e += 64)
+      *reinterpret_cast<f4*>(E + (Mv + (e >> 4)) * EP + 4 * (e & 15)) = f4{0.0f, 0.0f, 0.0f, 0.0f};
+    // Delta_{M-1} .. Delta_0 (segments indexed from 0) and the suffix sums
+    float suf = 0.0f;
+    for (int m = Mv - 1; m >= 0; --m) {
+      if (g == 0) {
+        E[m * EP + 4 * c16] = dl;
+        E[m * EP + 4 * c16 + 1] = suf;
+      }
+      suf += dl;
+      if (m == 0) break;
+      if (g == 0) xs[c16] = dl;
+      wave_order_d();
+      xv = *reinterpret_cast<const f4*>(xs + 4 * g);
+      wave_order_d();
+      float nx = fmaf(prow.x, xv.x, fmaf(prow.y, xv.y, fmaf(prow.z, xv.z, prow.w * xv.w)));
+      nx += __shfl_xor(nx, 16, 64);
+      nx += __shfl_xor(nx, 32, 64);
+      dl = nx;
+    }
+    wave_order_d();
+    float* row = a.loc + ((size_t)b * a.n_int + t) * a.LW;
+    if (g == 0) {
+      float pre = 0.0f;
+#pragma unroll 4
+      for (int m = 0; m < Mv; ++m) {
+        const float dm = E[m * EP + 4 * c16];
+        E[m * EP + 4 * c16 + 2] = fmaf(0.5f, dm, pre);
+        E[m * EP + 4 * c16 + 3] = fmaf(1.0f / 3.0f, dm, pre);
+        pre += dm;
+      }
+      row[c16] = pre;
+    }
+    wave_order_d();
+    if constexpr (N >= 2) {
+      f4 acc2 = {0.0f, 0.0f, 0.0f, 0.0f};
+      f4 acc3[N == 3 ? 16 : 1];
+#pragma unroll
+      for (int i = 0; i < (N == 3 ? 16 : 1); ++i) acc3[i] = f4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll 1
+      for (int s = 0; s < MP / 4; ++s) {
+        const float* er = E + (4 * s + g) * EP;
+        const f4 e = *reinterpret_cast<const f4*>(er + 4 * c16);  // {Delta, R, Y, X}[c16] of segment 4s + g
+        acc2 = mfma(e.z, e.x, acc2);
+        if constexpr (N == 3) {
+          const float hv = 0.5f * e.x;
+#pragma unroll
+          for (int aa = 0; aa < 16; ++aa) {
+            const float2 yx = *reinterpret_cast<const float2*>(er + 4 * aa + 2);  // Y_m[a], X_m[a]
+            acc3[aa] = mfma(fmaf(yx.x, e.y, yx.y * hv), e.x, acc3[aa]);
+          }
+        }
+      }
+#pragma unroll
+      for (int r = 0; r < 4; ++r) row[16 + (4 * g + r) * 16 + c16] = acc2[r];
+      if constexpr (N == 3) {
+#pragma unroll
+        for (int aa = 0; aa < 16; ++aa)
+          *reinterpret_cast<f4*>(row + 272 + aa * 256 + c16 * 16 + 4 * g) = acc3[aa];
+      }
+    }
+  }
+}
+
 // ------------------------------------------------------------------------------------------------ Chen scan
 __device__ __forceinline__ long out_index(int N, int d, int e) {  // padded state index -> unpadded row index
   if (e < 16) return e < d ? e : -1;
@@ -661,6 +1042,7 @@ size_t al256(size_t x) { return (x + 255) & ~(size_t)255; }
 
 struct DPlan {
   int B, L, n_int, d, N, q, QB, T, C, LW, D, W, npow;
+  int leaf, vm, vl_expm, vl_mode, chen_expm;
 };
 
 int dense_plan(const ews_dense_desc* s, DPlan& p) {
@@ -669,15 +1051,26 @@ int dense_plan(const ews_dense_desc* s, DPlan& p) {
   if (s->flow_mode < 0 || s->flow_mode > 2) return EWS_ERR_OPTION;
   if (s->readout < 0 || s->readout > 3) return EWS_ERR_OPTION;
   if (s->batch < 1 || s->length < 2 || s->dim < 1 || s->dim > 16) return EWS_ERR_SHAPE;
-  if (s->series_q < 0 || s->series_q > QMAX) return EWS_ERR_OPTION;
+  if (s->leaf != EWS_LEAF_SERIES && s->leaf != EWS_LEAF_VAN_LOAN) return EWS_ERR_OPTION;
+  const bool vl = s->leaf == EWS_LEAF_VAN_LOAN;
+  if (!vl && (s->series_q < 0 || s->series_q > QMAX)) return EWS_ERR_OPTION;
+  if (vl && (s->vl_steps < 1 || s->vl_steps > 64)) return EWS_ERR_OPTION;
+  if (vl && (s->vl_expm < 0 || s->vl_expm > 3 || s->vl_mode < 0 || s->vl_mode > 2)) return EWS_ERR_OPTION;
+  if (s->chen_expm < 0 || s->chen_expm > 3) return EWS_ERR_OPTION;
   if (s->flow_mode == EWS_FLOW_CACHED_BASEPOINT && s->length < 3) return EWS_ERR_SHAPE;
+  if (vl && s->vl_mode == EWS_FLOW_CACHED_BASEPOINT && s->length < 3) return EWS_ERR_SHAPE;
   if (s->chunk < 0) return EWS_ERR_SHAPE;
+  p.leaf = s->leaf;
+  p.vm = vl ? s->vl_steps : 0;
+  p.vl_expm = vl ? s->vl_expm : 0;
+  p.vl_mode = vl ? s->vl_mode : 0;
+  p.chen_expm = s->chen_expm;
   p.B = s->batch;
   p.L = s->length;
   p.n_int = p.L - 1;
   p.d = s->dim;
   p.N = s->depth;
-  p.q = s->series_q;
+  p.q = vl ? 0 : s->series_q;
   p.QB = p.q <= 4 ? 4 : p.q <= 8 ? 8 : p.q <= 12 ? 12 : p.q <= 16 ? 16 : p.q <= 20 ? 20 : p.q <= 24 ? 24
        : p.q <= 32 ? 32 : 40;
   p.T = s->chunk ? s->chunk : 64;
@@ -694,7 +1087,7 @@ int dense_plan(const ews_dense_desc* s, DPlan& p) {
 }
 
 struct DWs {
-  size_t apow, loc, fl, summ, sfl, car, pre, total;
+  size_t apow, loc, fl, summ, sfl, car, pre, mats, total;
 };
 DWs dense_ws(const DPlan& p, int readout) {
   DWs w;
@@ -707,6 +1100,7 @@ DWs dense_ws(const DPlan& p, int readout) {
   w.sfl = off; off += al256(BC * 256 * 4);
   w.car = off; off += al256((size_t)p.B * (p.C + 1) * p.LW * 4);
   w.pre = off; off += (readout == EWS_READOUT_MEAN || readout == EWS_READOUT_MAX) ? al256(BN * p.W * 4) : 0;
+  w.mats = off; off += al256((size_t)p.B * 768 * 4);
   w.total = off;
   return w;
 }
@@ -717,12 +1111,13 @@ Args dense_args(const ews_dense_desc* s, const DPlan& p, const float* path, cons
   a.B = p.B; a.L = p.L; a.n_int = p.n_int; a.d = p.d; a.N = p.N; a.q = p.q;
   a.flow_mode = s->flow_mode; a.readout = s->readout; a.lvl0 = s->level0 ? 1 : 0; a.W = p.W; a.LW = p.LW;
   a.T = p.T; a.C = p.C; a.npow = p.npow;
+  a.leaf = p.leaf; a.vm = p.vm; a.vl_expm = p.vl_expm; a.vl_mode = p.vl_mode; a.chen_expm = p.chen_expm;
   a.path = path; a.clock = clock; a.A = A; a.out = out;
   const DWs w = dense_ws(p, s->readout);
   char* ws = (char*)workspace;
   a.apow = (float*)(ws + w.apow); a.loc = (float*)(ws + w.loc); a.fl = (float*)(ws + w.fl);
   a.summ = (float*)(ws + w.summ); a.sfl = (float*)(ws + w.sfl); a.car = (float*)(ws + w.car);
-  a.pre = (float*)(ws + w.pre);
+  a.pre = (float*)(ws + w.pre); a.mats = (float*)(ws + w.mats);
   return a;
 }
 
@@ -820,11 +1215,45 @@ int dense_combine_pass(const ews_dense_desc* s, const DPlan& p, const Args& a, h
   }
 }
 
+// the Van Loan leaf (levels only) and the flows of a scheme other than the series kernels' fused exact ones
+int launch_vl_and_flows(const DPlan& p, const Args& a, hipStream_t st) {
+  const bool vl = p.leaf == EWS_LEAF_VAN_LOAN;
+  const long total = (long)p.B * p.n_int;
+  const bool prep = (vl && p.vl_mode != EWS_FLOW_PER_INTERVAL) ||
+                    (a.flow_mode != EWS_FLOW_PER_INTERVAL && (vl || p.chen_expm != EWS_EXPM_EXACT));
+  if (prep) {
+    hipLaunchKernelGGL(k_prep, dim3(p.B), dim3(64), 0, st, a);
+    DENSE_CHECK();
+  }
+  if (vl) {
+    const size_t table = (size_t)(PM + 1) * 256 * 4, region = (size_t)vl_region(p.vm) * 4;
+    const int nw = table + 4 * region <= 65536 ? 4 : 2;
+    const long blocks = (total + nw - 1) / nw;
+    const int grid = (int)(blocks < 8192 ? blocks : 8192);
+    const size_t shm = table + nw * region;
+    if (p.N == 1) hipLaunchKernelGGL((k_vl<1>), dim3(grid), dim3(64 * nw), shm, st, a);
+    else if (p.N == 2) hipLaunchKernelGGL((k_vl<2>), dim3(grid), dim3(64 * nw), shm, st, a);
+    else hipLaunchKernelGGL((k_vl<3>), dim3(grid), dim3(64 * nw), shm, st, a);
+    DENSE_CHECK();
+  }
+  if (vl || p.chen_expm != EWS_EXPM_EXACT) {
+    const long blocks = (total + 3) / 4;
+    const int grid = (int)(blocks < 8192 ? blocks : 8192);
+    hipLaunchKernelGGL(k_flows, dim3(grid), dim3(256), 0, st, a);
+    DENSE_CHECK();
+  }
+  return EWS_OK;
+}
+
 int dense_forward_pass(const ews_dense_desc* s, const DPlan& p, const Args& a, hipStream_t st, int pass) {
   if (pass == 0) {
     hipLaunchKernelGGL(k_powers, dim3(1), dim3(256), 0, st, a);
     DENSE_CHECK();
-    return launch_local(p, a, st);
+    if (p.leaf == EWS_LEAF_SERIES) {
+      const int rc = launch_local(p, a, st);
+      if (rc != EWS_OK) return rc;
+    }
+    return launch_vl_and_flows(p, a, st);
   }
   return dense_combine_pass(s, p, a, st, pass);
 }

@@ -20,6 +20,9 @@ FLOW_PER_INTERVAL = 0
 FLOW_CACHED = 1
 FLOW_CACHED_BASEPOINT = 2
 READOUTS = {"prefix": 0, "terminal": 1, "mean": 2, "max": 3}
+LEAF_SERIES = 0
+LEAF_VAN_LOAN = 1
+EXPM_SCHEMES = {"exact": 0, "euler": 1, "cayley": 2, "pade": 3}
 DTYPE_F32 = 0
 DTYPE_BF16 = 1
 
@@ -68,6 +71,11 @@ class DenseDesc(ctypes.Structure):
         ("readout", ctypes.c_int32),
         ("level0", ctypes.c_int32),
         ("chunk", ctypes.c_int32),
+        ("leaf", ctypes.c_int32),
+        ("vl_steps", ctypes.c_int32),
+        ("vl_expm", ctypes.c_int32),
+        ("vl_mode", ctypes.c_int32),
+        ("chen_expm", ctypes.c_int32),
     ]
 
 

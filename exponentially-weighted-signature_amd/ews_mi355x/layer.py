@@ -11,11 +11,14 @@ ews/core/kernels/combine.py:37-63):
     rotation planes / real diagonal,
         leaf "block_series" or "series"              the same fused kernel: its closed forms are the q -> infinity
                                                      limit of the series leaves (they agree to the series' own
-                                                     truncation bound, ews/core/series_leaf.py:129-143)
-    any generator (dense A, d <= 16), leaf "series",
-        depths 1-3; planes / diagonals at depth 3    dense kernels: series leaf of order series_q, flows
-                                                     exp(-h A) evaluated in the kernel (chen_expm "exact"),
-                                                     MFMA Chen mode products (forward only)
+                                                     truncation bound, ews/core/series_leaf.py:129-143);
+                                                     exact flows (chen_expm "exact")
+    any generator (dense A, d <= 16), depths 1-3,
+        leaf "series"                                dense kernels: series leaf of order series_q
+        leaf "van_loan" (the reference default)      dense kernels: Van Loan leaf with M knots per interval under
+                                                     van_loan_expm and reweighting_mode
+        (also planes / diagonals at depth 3, or      flows M_t of chen_expm evaluated in the kernels, MFMA Chen
+        with chen_expm other than "exact")           mode products (forward only)
     anything else                                    NotImplementedError
 """
 
@@ -138,19 +141,21 @@ class EWS(torch.nn.Module):
         return torch.diagonal(A).contiguous()
 
     def _engine_check(self):
-        if self.structure is not None and self.leaf in ("plane_closed", "block_series", "series") and self.N <= 2:
+        diag_ok = self.structure is not None and self.leaf in ("plane_closed", "block_series", "series") and self.N <= 2
+        if diag_ok and self.chen_expm == "exact":
             if self.structure == "planes" and self.d % 2:
                 raise ValueError("leaf='plane_closed' needs an even dimension (2x2 planes)")
             return "diag"
-        if self.leaf == "series":
+        if self.leaf in ("series", "van_loan"):
             if self.N > 3 or self.d > 16:
-                raise NotImplementedError("the dense-generator kernels cover depths 1-3 and d <= 16")
-            if self.chen_expm != "exact":
                 raise NotImplementedError(
-                    f"the dense-generator kernels evaluate exact flows exp(-h A) (chen_expm='exact'), "
-                    f"got chen_expm={self.chen_expm!r}"
-                )
+                    f"leaf={self.leaf!r}: the dense-generator kernels cover depths 1-3 and d <= 16")
             return "dense"
+        if diag_ok:
+            raise NotImplementedError(
+                f"leaf={self.leaf!r}: the closed-form kernels take exact flows exp(-h A) (chen_expm='exact'), "
+                f"got chen_expm={self.chen_expm!r}"
+            )
         if self.structure is not None and self.N > 2:
             raise NotImplementedError(
                 f"leaf={self.leaf!r}: closed-form local terms exist for depths 1 and 2 (use leaf='series' at depth 3)"
@@ -166,8 +171,13 @@ class EWS(torch.nn.Module):
             raise TypeError("the MI355X kernels compute in float32 (dtype=torch.float32)")
         A = self.A_param().to(torch.float32) * torch.as_tensor(a_scale, dtype=torch.float32, device=path.device)
         if engine == "dense":
+            if self.leaf == "van_loan":
+                leaf = ops.DenseLeaf("van_loan", M=self.M, van_loan_expm=self.van_loan_expm,
+                                     reweighting_mode=self.reweighting_mode, chen_expm=self.chen_expm)
+            else:
+                leaf = ops.DenseLeaf("series", q=self.series_q, chen_expm=self.chen_expm)
             return ops.dense_scan(path.to(torch.float32), clock.to(torch.float32), A.to(path.device).contiguous(),
-                                  self.N, self.series_q, self._flow_mode(readout), readout, level0)
+                                  self.N, leaf.q, self._flow_mode(readout), readout, level0, leaf=leaf)
         params = self._diag_params(A.to(path.device))
         if path.dtype != torch.bfloat16:
             path = path.to(torch.float32)

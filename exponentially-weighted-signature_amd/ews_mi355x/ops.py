@@ -99,9 +99,41 @@ _FLOW_MODES = {"per_interval": nat.FLOW_PER_INTERVAL, "cached": nat.FLOW_CACHED,
                "cached_basepoint": nat.FLOW_CACHED_BASEPOINT}
 
 
-def make_dense_desc(B, L, d, N, q, flow_mode, readout, level0, chunk=0):
-    return nat.DenseDesc(B, L, d, N, int(q), _FLOW_MODES[flow_mode], nat.READOUTS[readout], int(level0),
-                         int(chunk))
+_VL_MODES = {"displacement": nat.FLOW_PER_INTERVAL, "displacement_uniform": nat.FLOW_CACHED,
+             "displacement_uniform_basepoint": nat.FLOW_CACHED_BASEPOINT}
+
+
+class DenseLeaf:
+    """Leaf options of the dense path (ews/core/leaf.py:50-198): the series leaf of order q, or the Van Loan leaf
+    with M knots per interval, its exponential scheme and its reweighting mode; chen_expm is the flows' scheme."""
+
+    def __init__(self, kind="series", q=0, M=20, van_loan_expm="cayley", reweighting_mode="displacement",
+                 chen_expm="exact"):
+        if kind not in ("series", "van_loan"):
+            raise ValueError(f"dense leaf must be 'series' or 'van_loan', got {kind!r}")
+        if reweighting_mode not in _VL_MODES:
+            raise ValueError(
+                "reweighting_mode must be 'displacement', 'displacement_uniform', or "
+                f"'displacement_uniform_basepoint', got {reweighting_mode}")
+        for name, m in (("van_loan_expm", van_loan_expm), ("chen_expm", chen_expm)):
+            if m not in nat.EXPM_SCHEMES:
+                raise ValueError(f"{name} must be one of {tuple(nat.EXPM_SCHEMES)}, got {m!r}")
+        if kind == "van_loan" and not 1 <= int(M) <= 64:
+            raise NotImplementedError(f"the Van Loan leaf kernel takes 1 <= M <= 64 knots per interval, got M={M}")
+        self.kind, self.q, self.M = kind, int(q), int(M)
+        self.van_loan_expm, self.reweighting_mode, self.chen_expm = van_loan_expm, reweighting_mode, chen_expm
+
+    def key(self):
+        return (self.kind, self.q, self.M, self.van_loan_expm, self.reweighting_mode, self.chen_expm)
+
+
+def make_dense_desc(B, L, d, N, q, flow_mode, readout, level0, chunk=0, leaf=None):
+    leaf = leaf if leaf is not None else DenseLeaf("series", q)
+    vl = leaf.kind == "van_loan"
+    return nat.DenseDesc(B, L, d, N, int(q) if not vl else 0, _FLOW_MODES[flow_mode], nat.READOUTS[readout],
+                         int(level0), int(chunk), nat.LEAF_VAN_LOAN if vl else nat.LEAF_SERIES,
+                         leaf.M if vl else 0, nat.EXPM_SCHEMES[leaf.van_loan_expm] if vl else 0,
+                         _VL_MODES[leaf.reweighting_mode] if vl else 0, nat.EXPM_SCHEMES[leaf.chen_expm])
 
 
 def _check_dense(path, clock, A):
@@ -113,17 +145,17 @@ def _check_dense(path, clock, A):
 
 
 class DenseScan(torch.autograd.Function):
-    """out = EWS readout of (path, clock) under a dense generator A (series leaf of order q, exact flows).
-    Forward only: the dense-generator adjoint kernels are not part of this library yet, and a backward through
-    this op raises instead of falling back to another engine."""
+    """out = EWS readout of (path, clock) under a dense generator A (series leaf of order q or the Van Loan leaf,
+    flows of chen_expm). Forward only: the dense-generator adjoint kernels are not part of this library yet, and a
+    backward through this op raises instead of falling back to another engine."""
 
     @staticmethod
-    def forward(ctx, path, clock, A, N, q, flow_mode, readout, level0, chunk):
+    def forward(ctx, path, clock, A, N, q, flow_mode, readout, level0, chunk, leaf):
         lib = nat.load()
         _check_dense(path, clock, A)
         path, clock, A = path.contiguous(), clock.contiguous(), A.contiguous()
         B, L, d = path.shape
-        desc = make_dense_desc(B, L, d, N, q, flow_mode, readout, level0, chunk)
+        desc = make_dense_desc(B, L, d, N, q, flow_mode, readout, level0, chunk, leaf)
         D = sum(d**k for k in range(1, N + 1))
         W = D + (1 if level0 else 0)
         shape = (B, L - 1, W) if readout == "prefix" else (B, W)
@@ -138,21 +170,23 @@ class DenseScan(torch.autograd.Function):
     @staticmethod
     def backward(ctx, gout):
         raise NotImplementedError(
-            "the dense-generator EWS (leaf='series' with a general A) has no backward kernels in this build")
+            "the dense-generator EWS (leaf='series' or 'van_loan' with a general A) has no backward kernels in "
+            "this build")
 
 
-def dense_scan(path, clock, A, N, q, flow_mode="per_interval", readout="prefix", level0=True, chunk=0):
-    return DenseScan.apply(path, clock, A, int(N), int(q), flow_mode, readout, bool(level0), int(chunk))
+def dense_scan(path, clock, A, N, q, flow_mode="per_interval", readout="prefix", level0=True, chunk=0, leaf=None):
+    leaf = leaf if leaf is not None else DenseLeaf("series", q)
+    return DenseScan.apply(path, clock, A, int(N), int(q), flow_mode, readout, bool(level0), int(chunk), leaf)
 
 
-def dense_local_terms(path, clock, A, N, q, flow_mode="per_interval"):
-    """Series-leaf levels (B, L-1, sum_k d^k) packed and flows (B, L-1, d, d) on the GPU
-    (ews/core/leaf.py:111-114 and ews/core/chen_scan.py:155-168)."""
+def dense_local_terms(path, clock, A, N, q, flow_mode="per_interval", leaf=None):
+    """Leaf levels (B, L-1, sum_k d^k) packed and flows (B, L-1, d, d) on the GPU: the series leaf of order q,
+    or the Van Loan leaf given by ``leaf`` (ews/core/leaf.py:86-114 and ews/core/chen_scan.py:155-168)."""
     lib = nat.load()
     _check_dense(path, clock, A)
     path, clock, A = path.contiguous(), clock.contiguous(), A.contiguous()
     B, L, d = path.shape
-    desc = make_dense_desc(B, L, d, N, q, flow_mode, "prefix", False)
+    desc = make_dense_desc(B, L, d, N, q, flow_mode, "prefix", False, 0, leaf)
     D = sum(d**k for k in range(1, N + 1))
     dev = path.device
     levels = torch.empty((B, L - 1, D), device=dev, dtype=torch.float32)

@@ -104,27 +104,43 @@ int ews_diag_num_passes(int direction);
  * Flows M_t = exp(-h_t A) are evaluated in the kernels (Taylor polynomial on a scaled argument, then
  * squarings), replacing _chen_M_per_interval (ews/core/chen_scan.py:155-168) with chen_expm="exact".
  * --------------------------------------------------------------------------------------------------------- */
+/* leaves of the dense path (ews/core/leaf.py:50-198) */
+#define EWS_LEAF_SERIES 0   /* series_local_signatures (ews/core/series_leaf.py:116-126) */
+#define EWS_LEAF_VAN_LOAN 1 /* reweighted_segments_van_loan + compute_reweighted_signatures (van_loan.py:163-184) */
+
+/* matrix exponential schemes (ews/core/expm_approx.py:13-41) */
+#define EWS_EXPM_EXACT 0
+#define EWS_EXPM_EULER 1
+#define EWS_EXPM_CAYLEY 2
+#define EWS_EXPM_PADE 3 /* the [2/2] Pade approximant ("pade", "pade_lite") */
+
 typedef struct ews_dense_desc {
   int32_t batch;     /* B >= 1 */
   int32_t length;    /* L >= 2 knots */
   int32_t dim;       /* 1 <= d <= 16 */
   int32_t depth;     /* N in {1, 2, 3} */
-  int32_t series_q;  /* series order q in [0, 40] (letters b_0..b_q, total order |m| <= q) */
-  int32_t flow_mode; /* EWS_FLOW_* */
+  int32_t series_q;  /* series order q in [0, 40] (letters b_0..b_q, total order |m| <= q); series leaf only */
+  int32_t flow_mode; /* EWS_FLOW_* of the Chen flows */
   int32_t readout;   /* EWS_READOUT_* (mean / max need level0 = 1) */
   int32_t level0;    /* 1: rows carry the leading level-0 constant */
   int32_t chunk;     /* intervals per chunk; 0 selects the default (64) */
+  int32_t leaf;      /* EWS_LEAF_* (0: series) */
+  int32_t vl_steps;  /* Van Loan leaf: knots per interval M, 1 <= M <= 64 (the layer's M) */
+  int32_t vl_expm;   /* Van Loan leaf: EWS_EXPM_* of the augmented exponential (the layer's van_loan_expm) */
+  int32_t vl_mode;   /* Van Loan leaf: reweighting as EWS_FLOW_* (displacement / uniform / uniform_basepoint) */
+  int32_t chen_expm; /* EWS_EXPM_* of the flows M_t (the layer's chen_expm; 0: exact) */
 } ews_dense_desc;
 
 /* Scratch of the dense forward: powers table, padded local terms and flows (B, L-1, 16+256+4096 | 256),
- * chunk summaries and carries. */
+ * chunk summaries and carries, and the per-sample step matrices of the uniform modes (B, 3, 256). */
 size_t ews_dense_workspace_bytes(const ews_dense_desc* desc);
 
 /* Forward: path (B, L, d) f32, clock (B, L) f32, A (d, d) f32 row-major (reference sign), out f32
- * [(B, L-1, W) for prefix, (B, W) otherwise], W = level0 + sum_k d^k. Replaces EWS._single_path with
- * leaf="series" for a dense A: series_local_signatures (ews/core/series_leaf.py:116-126), the flows and the
- * combine (ews/core/chen_scan.py:172-241; ews/core/kernels/pallas_combine.py:803-858 dense_kernel) and the
- * readout (ews/layer.py:189-265). */
+ * [(B, L-1, W) for prefix, (B, W) otherwise], W = level0 + sum_k d^k. Replaces EWS._single_path for a dense A
+ * with leaf="series" (series_local_signatures, ews/core/series_leaf.py:116-126) or leaf="van_loan"
+ * (reweighted_segments_van_loan, ews/core/van_loan.py:163-184, and the knot signatures of
+ * ews/core/signature.py:20-35), the flows and the combine (ews/core/chen_scan.py:155-241;
+ * ews/core/kernels/pallas_combine.py:803-858 dense_kernel) and the readout (ews/layer.py:189-265). */
 int ews_dense_forward(const ews_dense_desc* desc, const float* path, const float* clock, const float* A,
                       float* out, void* workspace, ews_stream_t stream);
 
@@ -134,7 +150,7 @@ int ews_dense_forward_pass(const ews_dense_desc* desc, int pass, const float* pa
 int ews_dense_num_passes(void);
 
 /* The leaf alone: levels (B, L-1, sum_k d^k) packed as ews/core/chen_scan.py:33-46 and flows (B, L-1, d, d).
- * Replaces local_signatures(kind="series") (ews/core/leaf.py:111-114) plus _chen_M_per_interval. */
+ * Replaces local_signatures(kind="series" | "van_loan") (ews/core/leaf.py:86-114) plus _chen_M_per_interval. */
 int ews_dense_local_terms(const ews_dense_desc* desc, const float* path, const float* clock, const float* A,
                           float* levels, float* flows, void* workspace, ews_stream_t stream);
 

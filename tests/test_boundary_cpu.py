@@ -12,6 +12,7 @@ import torch
 
 import ews_mi355x as E
 from ews_mi355x import _native as nat
+from ews_mi355x import ops
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 
@@ -112,7 +113,8 @@ def test_log_dims_mirror_reference():
 
 
 def _ddesc(**kw):
-    base = dict(batch=2, length=10, dim=16, depth=3, series_q=20, flow_mode=0, readout=0, level0=1, chunk=0)
+    base = dict(batch=2, length=10, dim=16, depth=3, series_q=20, flow_mode=0, readout=0, level0=1, chunk=0,
+                leaf=0, vl_steps=0, vl_expm=0, vl_mode=0, chen_expm=0)
     base.update(kw)
     return nat.DenseDesc(**base)
 
@@ -134,10 +136,21 @@ def test_dense_c_abi_error_codes():
         "readout": (_ddesc(readout=9), -4),
         "flow mode": (_ddesc(flow_mode=3), -4),
         "basepoint length": (_ddesc(flow_mode=2, length=2), -2),
+        "leaf": (_ddesc(leaf=2), -4),
+        "van loan knots 0": (_ddesc(leaf=1, vl_steps=0), -4),
+        "van loan knots 65": (_ddesc(leaf=1, vl_steps=65), -4),
+        "van loan scheme": (_ddesc(leaf=1, vl_steps=20, vl_expm=4), -4),
+        "van loan mode": (_ddesc(leaf=1, vl_steps=20, vl_mode=3), -4),
+        "van loan basepoint length": (_ddesc(leaf=1, vl_steps=20, vl_mode=2, length=2), -2),
+        "flow scheme": (_ddesc(chen_expm=4), -4),
     }
     for name, (dsc, code) in bad.items():
         assert lib.ews_dense_forward(ctypes.byref(dsc), null, null, null, null, null, null) == code, name
         assert lib.ews_dense_workspace_bytes(ctypes.byref(dsc)) == 0, name
+    # the Van Loan leaf ignores the series order; its options are checked instead
+    vl = _ddesc(leaf=1, vl_steps=64, vl_expm=3, vl_mode=2, series_q=99, chen_expm=2)
+    assert lib.ews_dense_workspace_bytes(ctypes.byref(vl)) > 0
+    assert lib.ews_dense_forward(ctypes.byref(vl), null, null, null, null, null, null) == -1
 
 
 def test_dense_layer_routing_and_errors():
@@ -145,11 +158,24 @@ def test_dense_layer_routing_and_errors():
     assert E.EWS(A, N=3, leaf="series", series_q=8)._engine_check() == "dense"
     assert E.EWS(_planes(2), N=3, leaf="series", series_q=8)._engine_check() == "dense"
     assert E.EWS(_planes(2), N=2, leaf="series", series_q=8)._engine_check() == "diag"
+    # the Van Loan leaf (the reference default) runs on the dense kernels for every generator structure
+    assert E.EWS(A, N=2)._engine_check() == "dense"
+    assert E.EWS(_planes(2), N=2)._engine_check() == "dense"
+    assert E.EWS(A, N=3, M=64, van_loan_expm="pade_lite")._engine_check() == "dense"
+    # flows of another scheme: the dense kernels evaluate it; the closed-form kernels take exact flows only
+    assert E.EWS(A, N=3, leaf="series", series_q=8, chen_expm="cayley")._engine_check() == "dense"
+    assert E.EWS(_planes(2), N=2, leaf="series", series_q=8, chen_expm="pade")._engine_check() == "dense"
     with pytest.raises(NotImplementedError):
-        E.EWS(A, N=2)._engine_check()  # van_loan leaf with a dense generator
+        E.EWS(_planes(2), N=2, leaf="plane_closed", chen_expm="cayley")._engine_check()
     with pytest.raises(NotImplementedError):
-        E.EWS(A, N=3, leaf="series", series_q=8, chen_expm="cayley")._engine_check()
+        E.EWS(A, N=4)._engine_check()
+    with pytest.raises(NotImplementedError):
+        E.EWS(E.AParamGeneral(torch.zeros(17, 17)), N=2)._engine_check()
     with pytest.raises(NotImplementedError):
         E.EWS(E.AParamGeneral(torch.zeros(17, 17)), N=2, leaf="series", series_q=8)._engine_check()
+    with pytest.raises(NotImplementedError):
+        ops.DenseLeaf("van_loan", M=65)
+    with pytest.raises(ValueError):
+        ops.DenseLeaf("van_loan", reweighting_mode="uniform")
     with pytest.raises(RuntimeError, match="HIP device"):
         E.EWS(A, N=3, leaf="series", series_q=8)(torch.zeros(5, 4), torch.linspace(0, 1, 5))
