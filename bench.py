@@ -89,18 +89,20 @@ def bench_c3(args):
     import torch
 
     from ews_mi355x import _native as nat
-    from ews_mi355x.ops import make_dense_desc
+    from ews_mi355x.ops import DenseLeaf, make_dense_desc
 
     dev = torch.device("cuda:0")
     lib = nat.load()
     B, L, d, N, q = 16, 4096, 16, 3, 24
+    vl = args.leaf == "van_loan"
+    leaf = DenseLeaf("van_loan", M=20, van_loan_expm="cayley") if vl else DenseLeaf("series", q)
     path_np, clock_np, A_np = c3_inputs(B, L)
     path = torch.tensor(path_np, device=dev)
     clock = torch.tensor(clock_np, device=dev)
     A = torch.tensor(A_np, device=dev)
     D = d + d * d + d**3
     W = D + 1
-    desc = make_dense_desc(B, L, d, N, q, "per_interval", "prefix", True, args.chunk)
+    desc = make_dense_desc(B, L, d, N, q, "per_interval", "prefix", True, args.chunk, leaf)
     ws = torch.empty(int(lib.ews_dense_workspace_bytes(ctypes.byref(desc))), device=dev, dtype=torch.uint8)
     out = torch.empty((B, L - 1, W), device=dev, dtype=torch.float32)
     npass = lib.ews_dense_num_passes()
@@ -147,8 +149,9 @@ def bench_c3(args):
         "vs_baseline": None,
         "dtype": "f32",
         "data": "synthetic",
-        "config": {"workload": "c3: dense generator, B=16, L=4096, d=16, depth 3, series leaf q=24, "
-                               "input-dependent clock, prefix readout, forward", "global_batch": B, "seq_len": L,
+        "config": {"workload": "c3: dense generator, B=16, L=4096, d=16, depth 3, "
+                               + ("Van Loan leaf M=20 (cayley, the reference defaults)" if vl else "series leaf q=24")
+                               + ", input-dependent clock, prefix readout, forward", "global_batch": B, "seq_len": L,
                    "parallelism": "none (1 GPU)"},
         "roofline": {"bound": "mfma", "kernel": "chunk_output", "achieved": round(tf, 2),
                      "peak": MFMA_F32_PEAK_TFLOPS, "unit": "TFLOP/s", "frac": round(tf / MFMA_F32_PEAK_TFLOPS, 4),
@@ -159,8 +162,9 @@ def bench_c3(args):
         from oracle import ews_oracle as O
 
         got = out[0, :256].double().cpu()
+        kw = dict(leaf="van_loan", M=20, van_loan_expm="cayley") if vl else dict(leaf="series", series_q=q)
         ref = O.ews(torch.tensor(path_np[:1, :257]).double(), torch.tensor(clock_np[:1, :257]).double(),
-                    torch.tensor(A_np).double(), N, "prefix", leaf="series", series_q=q)[0]
+                    torch.tensor(A_np).double(), N, "prefix", **kw)[0]
         rec["check_forward_relerr_vs_f64"] = float((got - ref).abs().max() / ref.abs().max())
     return rec
 
@@ -222,6 +226,8 @@ def main():
     ap.add_argument("--chunk", type=int, default=0, help="intervals per chunk (0: the library's default)")
     ap.add_argument("--config", choices=["c2", "c3"], default="c2",
                     help="c2 (default, the headline): planes fwd+bwd; c3: dense-generator depth-3 forward")
+    ap.add_argument("--leaf", choices=["series", "van_loan"], default="series",
+                    help="leaf of the c3 forward: series (q=24) or Van Loan (M=20, cayley)")
     ap.add_argument("--clock-grad", action="store_true",
                     help="also compute the clock gradient (the c2 clock is data; off by default)")
     ap.add_argument("--copy-probe", action="store_true",

@@ -67,6 +67,10 @@ struct Args {
   float* pre;   // (B, n_int, W) prefix rows (mean / max readouts)
   float* mats;  // (B, 3, 256) per-sample Van Loan step matrices P, V and the shared flow (uniform modes)
   float* out;
+  // backward: the adjoint scan's per-chunk local cotangents (B, C, LW), carries (B, C + 1, LW), max argmax (B, D+1)
+  float* lloc;
+  float* lam;
+  int* amax;
 };
 
 // One scan over rows of (levels, flows): chunks of T rows, per-sample strides in floats.
@@ -514,6 +518,78 @@ __device__ __forceinline__ void wave_inverse(const LdsTable* sp, float alpha, fl
   wave_order_d();
 }
 
+// Power-series form of the matrix functions below: each is analytic in a = c A at 0, sum_k b_k a^k =
+// sum_k (b_k c^k k!) P_k with the table P_k = A^k / k!, evaluated elementwise (no cross-lane traffic). Used when
+// x = |c| ||A||_1 keeps the 13-term remainder below ~1e-8 relative: exact x <= 1 (x^13 e^x / 13!); cayley
+// x <= 0.48 (poles of (1 + a/2)^{-1} at |a| = 2); euler x <= 0.24 (|a| = 1; the euler flow I - cA is a
+// polynomial); pade x <= 0.7 (poles of (1 + a/2 + a^2/12)^{-1} at |a| = sqrt 12).
+__device__ __forceinline__ bool series_fits(int scheme, float x, bool flow) {
+  switch (scheme) {
+    case EWS_EXPM_EXACT: return x <= 1.0f;
+    case EWS_EXPM_EULER: return flow || x <= 0.24f;
+    case EWS_EXPM_CAYLEY: return x <= 0.48f;
+    default: return x <= 0.7f;
+  }
+}
+
+// Coefficients b_k in a (then scaled by c^k k!), for P and V of wave_matfn:
+//   exact   P: (-1)^k / k!             V: (-1)^k / (k+1)!
+//   cayley  V: (-1/2)^k                P: 2V - I
+//   euler   V = P: (-1)^k              flow: 1, -1
+//   pade    V: b_0 = 1, b_1 = -1/2, b_k = -(b_{k-1}/2 + b_{k-2}/12)  (1 / (1 + a/2 + a^2/12))
+//           P = I - a V: 1, -b_{k-1}
+__device__ __forceinline__ void series_mats(const LdsTable* sp, int scheme, float c, bool flow, float* P, float* V,
+                                            int l) {
+  float cp[PM + 1], cv[PM + 1];
+  float fact = 1.0f, sgn = 1.0f, half = 1.0f, b1 = 0.0f, b2 = 0.0f;
+#pragma unroll
+  for (int k = 0; k <= PM; ++k) {
+    if (k) {
+      fact *= (float)k;
+      sgn = -sgn;
+      half *= -0.5f;
+    }
+    float bp, bv;
+    if (scheme == EWS_EXPM_EXACT) {
+      bv = sgn / (fact * (float)(k + 1));
+      bp = sgn / fact;
+    } else if (scheme == EWS_EXPM_CAYLEY) {
+      bv = half;
+      bp = k ? 2.0f * half : 1.0f;
+    } else if (scheme == EWS_EXPM_EULER) {
+      bv = sgn;
+      bp = flow ? (k == 0 ? 1.0f : (k == 1 ? -1.0f : 0.0f)) : sgn;
+    } else {
+      bv = k == 0 ? 1.0f : (k == 1 ? -0.5f : -(0.5f * b1 + b2 * (1.0f / 12.0f)));
+      bp = k == 0 ? 1.0f : -b1;
+      b2 = b1;
+      b1 = bv;
+    }
+    cp[k] = bp;
+    cv[k] = bv;
+  }
+  float sc = 1.0f;
+#pragma unroll
+  for (int k = 1; k <= PM; ++k) {
+    sc *= c * (float)k;
+    cp[k] *= sc;
+    cv[k] *= sc;
+  }
+  f4 ap = {0.0f, 0.0f, 0.0f, 0.0f}, av = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+  for (int k = PM; k >= 0; --k) {  // smallest terms first
+    const f4 t = *reinterpret_cast<const f4*>(&sp[k][4 * l]);
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      ap[r] = fmaf(cp[k], t[r], ap[r]);
+      av[r] = fmaf(cv[k], t[r], av[r]);
+    }
+  }
+  *reinterpret_cast<f4*>(P + 4 * l) = ap;
+  if (!flow) *reinterpret_cast<f4*>(V + 4 * l) = av;
+  wave_order_d();
+}
+
 // The matrix functions of one step c under a scheme of ews/core/expm_approx.py:13-41.
 //   flow = true:  P = expm_scheme(-c A):   exact exp(-cA); euler I - cA; cayley (I + cA/2)^{-1} (I - cA/2)
 //                 = 2 (I + cA/2)^{-1} - I; pade (I + cA/2 + c^2A^2/12)^{-1} (I - cA/2 + c^2A^2/12)
@@ -527,6 +603,10 @@ __device__ __forceinline__ void wave_inverse(const LdsTable* sp, float alpha, fl
 // Buffers: P and V (V only for flow = false) 256 floats, T 256 + 32 floats of scratch.
 __device__ __forceinline__ void wave_matfn(const LdsTable* sp, float norm1, int scheme, float c, bool flow, float* P, float* V,
                            float* T, int l) {
+  if (series_fits(scheme, fabsf(c) * norm1, flow)) {
+    series_mats(sp, scheme, c, flow, P, V, l);
+    return;
+  }
   if (scheme == EWS_EXPM_EXACT) {
     wave_expm(sp, norm1, c, P, flow ? nullptr : V, l);
     return;
@@ -609,8 +689,28 @@ __global__ __launch_bounds__(64) void k_prep(Args a) {
   }
 }
 
-// Flows M_t = expm_scheme(-h_t A) under chen_expm (chen_scan.py:155-168), one wavefront per interval; the cached
-// modes copy the per-sample flow (identity for interval 0 of the basepoint mode).
+// Flow M_t = expm_scheme(-h_t A) of interval t under chen_expm (chen_scan.py:155-168), written to its row of fl
+// by one wavefront: computed per interval, the per-sample copy of the cached modes, or the identity of interval 0
+// of the basepoint mode. P (256) and T (256 + 32) are the wave's LDS scratch.
+__device__ __forceinline__ void write_flow(const Args& a, const LdsTable* sp, float norm1, int b, int t,
+                                           const float* th, float* P, float* T, int l) {
+  bool ident;
+  const float hf = flow_step(a, th, t, ident);
+  f4 m;
+  if (ident) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) m[r] = ((4 * l + r) >> 4) == ((4 * l + r) & 15) ? 1.0f : 0.0f;
+  } else if (a.flow_mode != EWS_FLOW_PER_INTERVAL) {
+    m = *reinterpret_cast<const f4*>(a.mats + (size_t)b * 768 + 512 + 4 * l);
+  } else {
+    wave_matfn(sp, norm1, a.chen_expm, hf, true, P, nullptr, T, l);
+    m = *reinterpret_cast<const f4*>(P + 4 * l);
+    wave_order_d();
+  }
+  *reinterpret_cast<f4*>(a.fl + ((size_t)b * a.n_int + t) * 256 + 4 * l) = m;
+}
+
+// Flows of a scheme other than the series kernels' fused exact ones, one wavefront per interval.
 __global__ __launch_bounds__(256) void k_flows(Args a) {
   __shared__ __align__(16) float sp[PM + 1][256];
   __shared__ __align__(16) float Pw[4][256], Tw[4][256 + 32];
@@ -621,22 +721,7 @@ __global__ __launch_bounds__(256) void k_flows(Args a) {
   const long total = (long)a.B * a.n_int;
   for (long it = (long)blockIdx.x * 4 + w; it < total; it += (long)gridDim.x * 4) {
     const int b = (int)(it / a.n_int), t = (int)(it - (long)b * a.n_int);
-    const float* th = a.clock + (size_t)b * a.L;
-    float* fr = a.fl + ((size_t)b * a.n_int + t) * 256;
-    bool ident;
-    const float hf = flow_step(a, th, t, ident);
-    f4 m;
-    if (ident) {
-#pragma unroll
-      for (int r = 0; r < 4; ++r) m[r] = ((4 * l + r) >> 4) == ((4 * l + r) & 15) ? 1.0f : 0.0f;
-    } else if (a.flow_mode != EWS_FLOW_PER_INTERVAL) {
-      m = *reinterpret_cast<const f4*>(a.mats + (size_t)b * 768 + 512 + 4 * l);
-    } else {
-      wave_matfn(sp, norm1, a.chen_expm, hf, true, Pw[w], nullptr, Tw[w], l);
-      m = *reinterpret_cast<const f4*>(Pw[w] + 4 * l);
-      wave_order_d();
-    }
-    *reinterpret_cast<f4*>(fr + 4 * l) = m;
+    write_flow(a, sp, norm1, b, t, a.clock + (size_t)b * a.L, Pw[w], Tw[w], l);
   }
 }
 
@@ -647,19 +732,33 @@ __global__ __launch_bounds__(256) void k_flows(Args a) {
 // knots (signature.py:20-35): the Chen product of the segments' exponentials, which in closed form is
 //   S1 = sum_m Delta_m,   S2 = sum_m Y_m (x) Delta_m,
 //   S3 = sum_m (Y_m (x) Delta_m (x) R_m + X_m (x) Delta_m (x) Delta_m / 2)
-// with the exclusive prefix sums Pre_m = sum_{j<m} Delta_j, suffix sums R_m = sum_{j>m} Delta_j,
-// Y_m = Pre_m + Delta_m / 2 and X_m = Pre_m + Delta_m / 3 (segment m contributes Delta^{(x)2}/2 and
-// Delta^{(x)3}/6 and meets the segments before and after it). S2 and S3 are 16x16x4 float32 MFMAs contracting
-// over the segment index: S2 = Y^T Delta, and per first index a, S3[a] = G_a^T Delta with
+// with the exclusive prefix sums Pre_m = sum_{j<m} Delta_j (= S1 - R_m - Delta_m), suffix sums
+// R_m = sum_{j>m} Delta_j, Y_m = Pre_m + Delta_m / 2 and X_m = Pre_m + Delta_m / 3 (segment m contributes
+// Delta^{(x)2}/2 and Delta^{(x)3}/6 and meets the segments before and after it). S2 and S3 are 16x16x4 float32
+// MFMAs contracting over the segment index: S2 = Y^T Delta, and per first index a, S3[a] = G_a^T Delta with
 // G_a[m][c] = Y_m[a] R_m[c] + X_m[a] Delta_m[c] / 2.
-// LDS per wave: P (256), the vector buffer (32), then one region shared by V / scratch (while the step
-// matrices are formed) and the segment table E[m][c] = {Delta, R, Y, X} (row pitch EP floats, MP rows, the rows
-// m >= M zero).
+// The chain Delta_{m-1} = P Delta_m keeps row c16 of P in the lane's registers; every lane forms the whole dot
+// product from the vector broadcast through LDS, so no cross-lane reduction sits on the chain.
+// The wave also writes the interval's flow. LDS per wave: P (256), the vector buffer (32), then one region
+// shared by V / scratch (while the step matrices and the flow are formed) and the segment table
+// E[m][c] = {Delta, R, Y, X} (row pitch EP floats, MP rows, the rows m >= M zero).
 constexpr int EP = 68;  // row pitch of the segment table (four segments of a k-step on distinct banks)
 
 __host__ __device__ constexpr int vl_rows(int M) { return (M + 3) / 4 * 4; }
 __host__ __device__ constexpr int vl_region(int M) {
   return 256 + 32 + (EP * vl_rows(M) > 256 + 256 + 32 ? EP * vl_rows(M) : 256 + 256 + 32);
+}
+
+__device__ __forceinline__ float dot16(const f4* r, const f4* x) {
+  float s0 = r[0].x * x[0].x, s1 = r[0].y * x[0].y, s2 = r[0].z * x[0].z, s3 = r[0].w * x[0].w;
+#pragma unroll
+  for (int q = 1; q < 4; ++q) {
+    s0 = fmaf(r[q].x, x[q].x, s0);
+    s1 = fmaf(r[q].y, x[q].y, s1);
+    s2 = fmaf(r[q].z, x[q].z, s2);
+    s3 = fmaf(r[q].w, x[q].w, s3);
+  }
+  return (s0 + s1) + (s2 + s3);
 }
 
 template <int N>
@@ -682,66 +781,60 @@ __global__ __launch_bounds__(256) void k_vl(Args a) {
     const int b = (int)(it / a.n_int), t = (int)(it - (long)b * a.n_int);
     const float* th = a.clock + (size_t)b * a.L;
     wave_order_d();  // the previous interval's reads of the segment table come first
+    write_flow(a, sp, norm1, b, t, th, P, T, l);
     // step matrices
-    f4 vrow;  // V[c16][4g .. 4g+3]
     if (a.vl_mode == EWS_FLOW_PER_INTERVAL) {
       wave_matfn(sp, norm1, a.vl_expm, (th[t + 1] - th[t]) / (float)Mv, false, P, V, T, l);
-      vrow = *reinterpret_cast<const f4*>(V + c16 * 16 + 4 * g);
     } else if (a.vl_mode == EWS_FLOW_CACHED_BASEPOINT && t == 0) {
       wave_identity(P, l);
-#pragma unroll
-      for (int r = 0; r < 4; ++r) vrow[r] = (c16 == 4 * g + r) ? 1.0f : 0.0f;
+      wave_identity(V, l);
     } else {
       const float* mb = a.mats + (size_t)b * 768;
       *reinterpret_cast<f4*>(P + 4 * l) = *reinterpret_cast<const f4*>(mb + 4 * l);
-      vrow = *reinterpret_cast<const f4*>(mb + 256 + c16 * 16 + 4 * g);
+      *reinterpret_cast<f4*>(V + 4 * l) = *reinterpret_cast<const f4*>(mb + 256 + 4 * l);
       wave_order_d();
     }
-    const f4 prow = *reinterpret_cast<const f4*>(P + c16 * 16 + 4 * g);
+    f4 pr[4], vr[4], xv[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      pr[q] = *reinterpret_cast<const f4*>(P + c16 * 16 + 4 * q);
+      vr[q] = *reinterpret_cast<const f4*>(V + c16 * 16 + 4 * q);
+    }
     // w = v / M
     if (l < 16) {
       const float* x = a.path + ((size_t)b * a.L + t) * a.d;
       xs[l] = l < a.d ? (x[a.d + l] - x[l]) / (float)Mv : 0.0f;
     }
     wave_order_d();
-    f4 xv = *reinterpret_cast<const f4*>(xs + 4 * g);
-    float dl = fmaf(vrow.x, xv.x, fmaf(vrow.y, xv.y, fmaf(vrow.z, xv.z, vrow.w * xv.w)));
-    dl += __shfl_xor(dl, 16, 64);
-    dl += __shfl_xor(dl, 32, 64);
-    wave_order_d();  // V is read before the segment table overwrites it
+#pragma unroll
+    for (int q = 0; q < 4; ++q) xv[q] = *reinterpret_cast<const f4*>(xs + 4 * q);
+    float dl = dot16(vr, xv);
+    wave_order_d();  // V and the vector are read before they are overwritten
     // rows M .. MP-1 of the table are zero
     for (int e = l; e < (MP - Mv) * 16; e += 64)
       *reinterpret_cast<f4*>(E + (Mv + (e >> 4)) * EP + 4 * (e & 15)) = f4{0.0f, 0.0f, 0.0f, 0.0f};
     // Delta_{M-1} .. Delta_0 (segments indexed from 0) and the suffix sums
     float suf = 0.0f;
-    for (int m = Mv - 1; m >= 0; --m) {
-      if (g == 0) {
-        E[m * EP + 4 * c16] = dl;
-        E[m * EP + 4 * c16 + 1] = suf;
-      }
+    for (int m = Mv - 1;; --m) {
+      if (g == 0) *reinterpret_cast<float2*>(E + m * EP + 4 * c16) = float2{dl, suf};
       suf += dl;
       if (m == 0) break;
       if (g == 0) xs[c16] = dl;
       wave_order_d();
-      xv = *reinterpret_cast<const f4*>(xs + 4 * g);
+#pragma unroll
+      for (int q = 0; q < 4; ++q) xv[q] = *reinterpret_cast<const f4*>(xs + 4 * q);
       wave_order_d();
-      float nx = fmaf(prow.x, xv.x, fmaf(prow.y, xv.y, fmaf(prow.z, xv.z, prow.w * xv.w)));
-      nx += __shfl_xor(nx, 16, 64);
-      nx += __shfl_xor(nx, 32, 64);
-      dl = nx;
+      dl = dot16(pr, xv);
     }
-    wave_order_d();
     float* row = a.loc + ((size_t)b * a.n_int + t) * a.LW;
-    if (g == 0) {
-      float pre = 0.0f;
-#pragma unroll 4
-      for (int m = 0; m < Mv; ++m) {
-        const float dm = E[m * EP + 4 * c16];
-        E[m * EP + 4 * c16 + 2] = fmaf(0.5f, dm, pre);
-        E[m * EP + 4 * c16 + 3] = fmaf(1.0f / 3.0f, dm, pre);
-        pre += dm;
-      }
-      row[c16] = pre;
+    if (g == 0) row[c16] = suf;
+    wave_order_d();
+    // Y and X from Pre_m = S1 - R_m - Delta_m, segments m = g, g + 4, ...
+    for (int m = g; m < Mv; m += 4) {
+      const float2 dr = *reinterpret_cast<const float2*>(E + m * EP + 4 * c16);
+      const float pre = suf - dr.y - dr.x;
+      *reinterpret_cast<float2*>(E + m * EP + 4 * c16 + 2) =
+          float2{fmaf(0.5f, dr.x, pre), fmaf(1.0f / 3.0f, dr.x, pre)};
     }
     wave_order_d();
     if constexpr (N >= 2) {
@@ -961,6 +1054,361 @@ __global__ __launch_bounds__(N >= 3 ? 256 : 64) void k_scan(Seq s) {
   }
 }
 
+// ------------------------------------------------------------------------------------------------ adjoint scan
+// Reverse mode of the Chen scan (the chunked design of pallas_combine.py:1425-1436; the dense kernel's VJP
+// _dense_kernel_general_bwd, pallas_combine.py:2360-2565). The step S_t = R_t(S_{t-1}) = (M_t . S_{t-1}) (x) s_t is
+// affine in S, so with lambda_t the cotangent of S_t and g_t the readout's cotangent of row t
+//   lambda_{t-1} = g_{t-1} + R_t^T lambda_t,
+//   R_t^T l = (M^T rho_1, M^T rho_2 M, rho_3 x_1 M^T x_2 M^T x_3 M^T),
+//   rho_1 = l_1 + l_2 ._2 s1 + l_3 ._23 s2,   rho_2 = l_2 + l_3 ._3 s1,   rho_3 = l_3.
+// The cotangents of the step's inputs (EMIT), with y1 = M S1 and Y2 = M S2 M^T of the state before the step:
+//   ds3 = l_3,   ds2 = l_2 + y1 ._1 l_3,   ds1 = l_1 + y1 ._1 l_2 + Y2 ._12 l_3,
+//   dM = rho_1 (x) S1 + rho_2 M S2^T + rho_2^T M S2 + T1 + T2 + T3,
+// where T1 + T2 + T3 is the derivative of <l_3, M^(x)3 S3> along each tensor axis:
+//   T1 = <l_3 x_3 M^T x_2 M^T, S3>_{23},  T2 = <l_3 x_3 M^T, S3 x_1 M>_{13},  T3 = <l_3, S3 x_1 M x_2 M>_{12}
+// (<X, Y>_{jk}[p][q] contracts the two named axes of X[.., p, ..] and Y[.., q, ..]).
+// Passes: LOCAL (each chunk from lambda = 0: the chunk's own part of the cotangent of its entry state),
+// CARRY (one sample's chunks in reverse, on the chunk summaries: Lambda_c = local_c + R(chunk c)^T Lambda_{c+1}),
+// EMIT (each chunk from Lambda_{c+1}, writing ds_t over the local terms and dM_t over the flows).
+// Mode products and the T contractions are 16x16x4 float32 MFMAs (operand conventions as in k_scan).
+enum { ADJ_LOCAL = 0, ADJ_CARRY = 1, ADJ_EMIT = 2 };
+enum { G_NONE = 0, G_PREFIX = 1, G_MEAN = 2, G_MAX = 3 };
+
+struct AdjSeq {
+  const float* lv;  // local terms (padded, LW per row) or chunk summaries (CARRY)
+  long lv_bs;
+  const float* fl;  // flows (256 per row) or chunk flow products
+  long fl_bs;
+  int n, T, C, d;
+  // readout cotangent of row t: G_PREFIX rows (B, n, W) (glvl0: with the level-0 column); G_MEAN one row (B, W)
+  // scaled by gscale; G_MAX one row (B, W) applied where amax == t
+  int gmode, W, glvl0;
+  const float* g;
+  const int* amax;
+  float gscale;
+  const float* init;  // EMIT: Lambda rows (B, C + 1, LW), chunk c starts from row c + 1; CARRY: row C on entry
+  float* lam;         // LOCAL: (B, C, LW) outputs; CARRY: (B, C + 1, LW) outputs (rows 1..C)
+  const float* lloc;  // CARRY: the LOCAL outputs
+  const float* st;    // EMIT: prefix rows (B, n, Wst) with the level-0 column (the states S_t)
+  int Wst;
+  float* dlv;         // EMIT: ds_t (padded, in place of lv)
+  float* dfl;         // EMIT: dM_t (in place of fl)
+};
+
+__device__ __forceinline__ float adj_g(const AdjSeq& s, int b, int t, int e, int N) {
+  if (s.gmode == G_NONE) return 0.0f;
+  const long oi = out_index(N, s.d, e);
+  if (oi < 0) return 0.0f;
+  const long col = s.glvl0 + oi;
+  if (s.gmode == G_PREFIX) return s.g[((long)b * s.n + t) * s.W + col];
+  if (s.gmode == G_MEAN) return s.g[(long)b * s.W + col] * s.gscale;
+  return s.amax[(long)b * s.W + col] == t ? s.g[(long)b * s.W + col] : 0.0f;
+}
+
+template <int N, int MODE>
+__global__ __launch_bounds__(256) void k_adj(AdjSeq s) {
+  constexpr int LW = lw_of(N);
+  constexpr bool EMIT = MODE == ADJ_EMIT;
+  constexpr int S3N = N >= 3 ? 16 * SP : 4;
+  __shared__ __align__(16) float L3[S3N];                  // l_3 (current cotangent, level 3)
+  __shared__ __align__(16) float C3[S3N];                  // l_3 x_3 M^T, then x_2 M^T
+  __shared__ __align__(16) float A3[EMIT ? S3N : 4];       // S3 of the state before the step
+  __shared__ __align__(16) float B3[EMIT ? S3N : 4];       // S3 x_1 M, then x_2 M
+  __shared__ __align__(16) float Tw[EMIT && N >= 3 ? 4 : 1][256];  // per-wave partial T1 + T2 + T3
+  __shared__ __align__(16) float L2[16 * RP], R2[16 * RP], Ms[256], s2s[16 * RP], Zs[16 * RP];
+  __shared__ __align__(16) float S2s[16 * RP], MS2[16 * RP], MS2T[16 * RP], Y2s[16 * RP], Qs[16 * RP];
+  __shared__ float L1[16], R1[16], s1s[16], S1s[16], y1s[16];
+  const int tid = threadIdx.x, w = tid >> 6, l = tid & 63, g = l >> 4, c16 = l & 15;
+  const int ri = tid >> 4, rj = tid & 15;  // (row, column) of the 16 x 16 VALU work
+  const int b = blockIdx.y;
+  int c, t0, Tc;
+  if constexpr (MODE == ADJ_CARRY) {
+    c = 0;
+    t0 = 0;
+    Tc = s.C;
+  } else {
+    c = blockIdx.x;
+    t0 = c * s.T;
+    Tc = min(s.T, s.n - t0);
+  }
+  // initial lambda
+  {
+    const float* ini = nullptr;
+    if constexpr (MODE == ADJ_EMIT) ini = s.init + ((long)b * (s.C + 1) + c + 1) * LW;
+    if constexpr (MODE == ADJ_CARRY) ini = s.init + ((long)b * (s.C + 1) + s.C) * LW;
+    if (tid < 16) L1[tid] = ini ? ini[tid] : 0.0f;
+    if constexpr (N >= 2) L2[ri * RP + rj] = ini ? ini[16 + tid] : 0.0f;
+    if constexpr (N >= 3) {
+      for (int e = tid; e < 4096; e += 256) L3[(e >> 8) * SP + ((e >> 4) & 15) * RP + (e & 15)] = ini ? ini[272 + e] : 0.0f;
+    }
+  }
+  __syncthreads();
+  for (int k = Tc - 1; k >= 0; --k) {
+    const int t = t0 + k;  // row (interval / chunk) index
+    const float* lrow = s.lv + b * s.lv_bs + (long)t * LW;
+    const float* frow = s.fl + b * s.fl_bs + (long)t * 256;
+    if constexpr (MODE == ADJ_CARRY) {  // Lambda_{t+1} is the current lambda
+      float* o = s.lam + ((long)b * (s.C + 1) + t + 1) * LW;
+      if (t + 1 < s.C) {
+        if (tid < 16) o[tid] = L1[tid];
+        if constexpr (N >= 2) o[16 + tid] = L2[ri * RP + rj];
+        if constexpr (N >= 3) {
+          for (int e = tid; e < 4096; e += 256) o[272 + e] = L3[(e >> 8) * SP + ((e >> 4) & 15) * RP + (e & 15)];
+        }
+      }
+    }
+    // ---- inputs of the step; lambda += g_t
+    Ms[tid] = frow[tid];
+    if (tid < 16) s1s[tid] = lrow[tid];
+    if constexpr (N >= 2) s2s[ri * RP + rj] = lrow[16 + tid];
+    if constexpr (MODE != ADJ_CARRY) {
+      if (s.gmode != G_NONE) {
+        if (tid < 16) L1[tid] += adj_g(s, b, t, tid, N);
+        if constexpr (N >= 2) L2[ri * RP + rj] += adj_g(s, b, t, 16 + tid, N);
+        if constexpr (N >= 3) {
+          for (int e = tid; e < 4096; e += 256)
+            L3[(e >> 8) * SP + ((e >> 4) & 15) * RP + (e & 15)] += adj_g(s, b, t, 272 + e, N);
+        }
+      }
+    }
+    if constexpr (EMIT) {  // the state before the step: row t - 1 (zero before the first interval)
+      const float* srow = t > 0 ? s.st + ((long)b * s.n + t - 1) * s.Wst + 1 : nullptr;
+      auto sv = [&](int e) -> float {
+        if (!srow) return 0.0f;
+        const long oi = out_index(N, s.d, e);
+        return oi >= 0 ? srow[oi] : 0.0f;
+      };
+      if (tid < 16) S1s[tid] = sv(tid);
+      if constexpr (N >= 2) S2s[ri * RP + rj] = sv(16 + tid);
+      if constexpr (N >= 3) {
+        for (int e = tid; e < 4096; e += 256) A3[(e >> 8) * SP + ((e >> 4) & 15) * RP + (e & 15)] = sv(272 + e);
+      }
+    }
+    __syncthreads();
+    const f4 M4 = *reinterpret_cast<const f4*>(Ms + c16 * 16 + 4 * g);  // M[c16][4g + r]
+    f4 MT4;                                                                // M^T[c16][4g + r]
+#pragma unroll
+    for (int r = 0; r < 4; ++r) MT4[r] = Ms[(4 * g + r) * 16 + c16];
+    float* drow = EMIT ? s.dlv + b * s.lv_bs + (long)t * LW : nullptr;
+    // ---- rho_2, rho_1 (and for EMIT y1, M S2, M S2^T, ds3)
+    {
+      float r2 = 0.0f, pp = 0.0f;
+      if constexpr (N >= 3) {
+        const float* row = L3 + ri * SP + rj * RP;  // l_3[ri][rj][.]
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const f4 x = *reinterpret_cast<const f4*>(row + 4 * q);
+          const f4 a1 = *reinterpret_cast<const f4*>(s1s + 4 * q);
+          const f4 a2 = *reinterpret_cast<const f4*>(s2s + rj * RP + 4 * q);
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            r2 = fmaf(x[r], a1[r], r2);
+            pp = fmaf(x[r], a2[r], pp);
+          }
+        }
+      }
+      float v = pp;
+      if constexpr (N >= 2) {
+        const float l2 = L2[ri * RP + rj];
+        R2[ri * RP + rj] = l2 + r2;
+        v = fmaf(l2, s1s[rj], v);
+      }
+#pragma unroll
+      for (int o = 1; o < 16; o <<= 1) v += __shfl_xor(v, o, 64);
+      if (rj == 0) R1[ri] = L1[ri] + v;
+      if constexpr (EMIT) {
+        float m = Ms[ri * 16 + rj] * S1s[rj];
+#pragma unroll
+        for (int o = 1; o < 16; o <<= 1) m += __shfl_xor(m, o, 64);
+        if (rj == 0) y1s[ri] = m;
+        if constexpr (N >= 2) {
+          float a = 0.0f, bt = 0.0f;
+#pragma unroll
+          for (int k2 = 0; k2 < 16; ++k2) {
+            const float mik = Ms[ri * 16 + k2];
+            a = fmaf(mik, S2s[k2 * RP + rj], a);   // (M S2)[ri][rj]
+            bt = fmaf(mik, S2s[rj * RP + k2], bt);  // (M S2^T)[ri][rj]
+          }
+          MS2[ri * RP + rj] = a;
+          MS2T[ri * RP + rj] = bt;
+        }
+        if constexpr (N >= 3) {
+          for (int e = tid; e < 4096; e += 256) drow[272 + e] = L3[(e >> 8) * SP + ((e >> 4) & 15) * RP + (e & 15)];
+        }
+      }
+    }
+    __syncthreads();
+    // ---- EMIT: Y2 = (M S2) M^T, dM of levels 1-2, ds2
+    float dm12 = 0.0f;
+    if constexpr (EMIT) {
+      if constexpr (N >= 2) {
+        float y = 0.0f;
+#pragma unroll
+        for (int k2 = 0; k2 < 16; ++k2) y = fmaf(MS2[ri * RP + k2], Ms[rj * 16 + k2], y);
+        Y2s[ri * RP + rj] = y;
+      }
+      dm12 = R1[ri] * S1s[rj];
+      if constexpr (N >= 2) {
+#pragma unroll
+        for (int k2 = 0; k2 < 16; ++k2) {
+          dm12 = fmaf(R2[ri * RP + k2], MS2T[k2 * RP + rj], dm12);
+          dm12 = fmaf(R2[k2 * RP + ri], MS2[k2 * RP + rj], dm12);
+        }
+      }
+    }
+    __syncthreads();
+    float ds2v = 0.0f;
+    if constexpr (EMIT) {
+      if constexpr (N >= 2) {
+        // ds2[ri][rj] = l_2[ri][rj] + sum_a y1[a] l_3[a][ri][rj];  Q[ri][rj] = sum_a l_3[a][ri][rj] Y2[a][ri]
+        ds2v = L2[ri * RP + rj];
+        float qv = 0.0f;
+        if constexpr (N >= 3) {
+#pragma unroll
+          for (int a = 0; a < 16; ++a) {
+            const float x = L3[a * SP + ri * RP + rj];
+            ds2v = fmaf(y1s[a], x, ds2v);
+            qv = fmaf(Y2s[a * RP + ri], x, qv);
+          }
+        }
+        // ds1[rj] = l_1[rj] + sum_a l_2[a][rj] y1[a] + sum_ri Q[ri][rj]
+        Qs[ri * RP + rj] = qv + L2[ri * RP + rj] * y1s[ri];
+      }
+    }
+    // ---- level-3 mode products and the T contractions
+    f4 tacc = {0.0f, 0.0f, 0.0f, 0.0f};
+    if constexpr (N >= 3) {
+      f4 a23[4];
+#pragma unroll
+      for (int ii = 0; ii < 4; ++ii) {
+        const int i = 4 * w + ii;
+        const f4 A4 = *reinterpret_cast<const f4*>(L3 + i * SP + c16 * RP + 4 * g);  // l_3[i][c16][4g + k]
+        f4 x = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int k2 = 0; k2 < 4; ++k2) x = mfma(A4[k2], MT4[k2], x);  // (l_3 x_3 M^T)[i][4g + r][c16]
+#pragma unroll
+        for (int r = 0; r < 4; ++r) C3[i * SP + (4 * g + r) * RP + c16] = x[r];
+        f4 y = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int r = 0; r < 4; ++r) y = mfma(MT4[r], x[r], y);  // (.. x_2 M^T)[i][4g + r][c16]
+        a23[ii] = y;
+      }
+      if constexpr (EMIT) {
+#pragma unroll
+        for (int jj = 0; jj < 4; ++jj) {  // V1 = S3 x_1 M, tiles j
+          const int j = 4 * w + jj;
+          f4 z = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+          for (int k2 = 0; k2 < 4; ++k2) z = mfma(M4[k2], A3[(4 * g + k2) * SP + j * RP + c16], z);
+#pragma unroll
+          for (int r = 0; r < 4; ++r) B3[(4 * g + r) * SP + j * RP + c16] = z[r];
+        }
+      }
+      __syncthreads();
+      if constexpr (EMIT) {
+        // T2[p][q] = sum_{a, c} C3[a][p][c] V1[a][q][c]; this wave's k-steps 16w .. 16w + 15
+#pragma unroll 4
+        for (int ks = 16 * w; ks < 16 * w + 16; ++ks) {
+          const int a = ks >> 2, cc = 4 * (ks & 3) + g;
+          tacc = mfma(C3[a * SP + c16 * RP + cc], B3[a * SP + c16 * RP + cc], tacc);
+        }
+      }
+      __syncthreads();
+#pragma unroll
+      for (int ii = 0; ii < 4; ++ii) {
+        const int i = 4 * w + ii;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) C3[i * SP + (4 * g + r) * RP + c16] = a23[ii][r];
+        if constexpr (EMIT) {  // W3 = V1 x_2 M, slice i in place
+          f4 xv;
+#pragma unroll
+          for (int r = 0; r < 4; ++r) xv[r] = B3[i * SP + (4 * g + r) * RP + c16];
+          f4 y = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+          for (int r = 0; r < 4; ++r) y = mfma(M4[r], xv[r], y);
+#pragma unroll
+          for (int r = 0; r < 4; ++r) B3[i * SP + (4 * g + r) * RP + c16] = y[r];
+        }
+      }
+      __syncthreads();
+      if constexpr (EMIT) {
+        // T1[p][q] = sum_{j, k} C3[p][j][k] S3[q][j][k];  T3[p][q] = sum_{a, b} l_3[a][b][p] W3[a][b][q]
+#pragma unroll 4
+        for (int ks = 16 * w; ks < 16 * w + 16; ++ks) {
+          const int j = ks >> 2, kk = 4 * (ks & 3) + g;
+          tacc = mfma(C3[c16 * SP + j * RP + kk], A3[c16 * SP + j * RP + kk], tacc);
+          tacc = mfma(L3[j * SP + kk * RP + c16], B3[j * SP + kk * RP + c16], tacc);
+        }
+#pragma unroll
+        for (int r = 0; r < 4; ++r) Tw[w][(4 * g + r) * 16 + c16] = tacc[r];
+      }
+      __syncthreads();
+      // l_3 <- C3 x_1 M^T (tiles j)
+#pragma unroll
+      for (int jj = 0; jj < 4; ++jj) {
+        const int j = 4 * w + jj;
+        f4 z = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int k2 = 0; k2 < 4; ++k2) z = mfma(MT4[k2], C3[(4 * g + k2) * SP + j * RP + c16], z);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) L3[(4 * g + r) * SP + j * RP + c16] = z[r];
+      }
+    }
+    // ---- l_2 <- M^T rho_2 M (via Z = rho_2 M), l_1 <- M^T rho_1; EMIT outputs
+    if constexpr (N >= 2) {
+      float z = 0.0f;
+#pragma unroll
+      for (int k2 = 0; k2 < 16; ++k2) z = fmaf(R2[ri * RP + k2], Ms[k2 * 16 + rj], z);
+      Zs[ri * RP + rj] = z;
+    }
+    if constexpr (EMIT) {
+      float dm = dm12;
+      if constexpr (N >= 3) dm += Tw[0][tid] + Tw[1][tid] + Tw[2][tid] + Tw[3][tid];
+      s.dfl[b * s.fl_bs + (long)t * 256 + tid] = dm;
+      if constexpr (N >= 2) drow[16 + tid] = ds2v;
+    }
+    __syncthreads();
+    if constexpr (N >= 2) {
+      float v = 0.0f;
+#pragma unroll
+      for (int k2 = 0; k2 < 16; ++k2) v = fmaf(Ms[k2 * 16 + ri], Zs[k2 * RP + rj], v);
+      L2[ri * RP + rj] = v;
+    }
+    if (tid < 16) {
+      float v = 0.0f;
+#pragma unroll
+      for (int k2 = 0; k2 < 16; ++k2) v = fmaf(Ms[k2 * 16 + tid], R1[k2], v);
+      if constexpr (EMIT) {
+        float d1 = L1[tid];
+        if constexpr (N >= 2) {
+#pragma unroll
+          for (int k2 = 0; k2 < 16; ++k2) d1 += Qs[k2 * RP + tid];
+        }
+        drow[tid] = d1;
+      }
+      L1[tid] = v;
+    }
+    if constexpr (MODE == ADJ_CARRY) {  // Lambda_t = R^T Lambda_{t+1} + local_t
+      __syncthreads();
+      const float* lo = s.lloc + ((long)b * s.C + t) * LW;
+      if (tid < 16) L1[tid] += lo[tid];
+      if constexpr (N >= 2) L2[ri * RP + rj] += lo[16 + tid];
+      if constexpr (N >= 3) {
+        for (int e = tid; e < 4096; e += 256) L3[(e >> 8) * SP + ((e >> 4) & 15) * RP + (e & 15)] += lo[272 + e];
+      }
+    }
+    __syncthreads();
+  }
+  if constexpr (MODE == ADJ_LOCAL) {
+    float* o = s.lam + ((long)b * s.C + c) * LW;
+    if (tid < 16) o[tid] = L1[tid];
+    if constexpr (N >= 2) o[16 + tid] = L2[ri * RP + rj];
+    if constexpr (N >= 3) {
+      for (int e = tid; e < 4096; e += 256) o[272 + e] = L3[(e >> 8) * SP + ((e >> 4) & 15) * RP + (e & 15)];
+    }
+  }
+}
+
 // ------------------------------------------------------------------------------------------------ readouts
 // zero state rows (carries row 0)
 __global__ void k_zero_rows(float* base, long stride, int n_rows, int width) {
@@ -1030,6 +1478,33 @@ __global__ void k_unpad_outputs(Args a, float* levels, float* flows) {
   }
 }
 
+// first row index of the column maximum over the prefix rows (B, n, Wr) (the max readout's cotangent goes there)
+__global__ void k_argmax(const float* rows, int n, int Wr, int* amax) {
+  const int b = blockIdx.y;
+  const int col = blockIdx.x * blockDim.x + threadIdx.x;
+  if (col >= Wr) return;
+  const float* p = rows + (size_t)b * n * Wr + col;
+  float best = p[0];
+  int arg = 0;
+  for (int t = 1; t < n; ++t) {
+    const float v = p[(size_t)t * Wr];
+    if (v > best) {
+      best = v;
+      arg = t;
+    }
+  }
+  amax[(size_t)b * Wr + col] = arg;
+}
+// row C of the adjoint carries: the terminal readout's cotangent (padded, without the level-0 column), or zero
+__global__ void k_lam_end(Args a, const float* gterm, int glvl0) {
+  const int b = blockIdx.y;
+  float* o = a.lam + ((size_t)b * (a.C + 1) + a.C) * a.LW;
+  for (int e = blockIdx.x * blockDim.x + threadIdx.x; e < a.LW; e += gridDim.x * blockDim.x) {
+    const long oi = out_index(a.N, a.d, e);
+    o[e] = (gterm && oi >= 0) ? gterm[(size_t)b * a.W + glvl0 + oi] : 0.0f;
+  }
+}
+
 }  // namespace dense
 }  // namespace ews
 
@@ -1087,10 +1562,11 @@ int dense_plan(const ews_dense_desc* s, DPlan& p) {
 }
 
 struct DWs {
-  size_t apow, loc, fl, summ, sfl, car, pre, mats, total;
+  size_t apow, loc, fl, summ, sfl, car, pre, mats, lloc, lam, amax, total;
 };
-DWs dense_ws(const DPlan& p, int readout) {
-  DWs w;
+// bwd: the backward's layout, the forward's buffers (prefix rows always) followed by the adjoint scan's
+DWs dense_ws(const DPlan& p, int readout, bool bwd = false) {
+  DWs w{};
   size_t off = 0;
   const size_t BC = (size_t)p.B * p.C, BN = (size_t)p.B * p.n_int;
   w.apow = off; off += al256(((size_t)p.npow * 256 + 1) * 4);
@@ -1099,25 +1575,35 @@ DWs dense_ws(const DPlan& p, int readout) {
   w.summ = off; off += al256(BC * p.LW * 4);
   w.sfl = off; off += al256(BC * 256 * 4);
   w.car = off; off += al256((size_t)p.B * (p.C + 1) * p.LW * 4);
-  w.pre = off; off += (readout == EWS_READOUT_MEAN || readout == EWS_READOUT_MAX) ? al256(BN * p.W * 4) : 0;
+  w.pre = off;
+  off += bwd ? al256(BN * (p.D + 1) * 4)
+             : (readout == EWS_READOUT_MEAN || readout == EWS_READOUT_MAX) ? al256(BN * p.W * 4) : 0;
   w.mats = off; off += al256((size_t)p.B * 768 * 4);
+  if (bwd) {
+    w.lloc = off; off += al256(BC * p.LW * 4);
+    w.lam = off; off += al256((size_t)p.B * (p.C + 1) * p.LW * 4);
+    w.amax = off; off += al256((size_t)p.B * (p.D + 1) * 4);
+  }
   w.total = off;
   return w;
 }
 
 Args dense_args(const ews_dense_desc* s, const DPlan& p, const float* path, const float* clock, const float* A,
-                float* out, void* workspace) {
+                float* out, void* workspace, bool bwd = false) {
   Args a{};
   a.B = p.B; a.L = p.L; a.n_int = p.n_int; a.d = p.d; a.N = p.N; a.q = p.q;
   a.flow_mode = s->flow_mode; a.readout = s->readout; a.lvl0 = s->level0 ? 1 : 0; a.W = p.W; a.LW = p.LW;
   a.T = p.T; a.C = p.C; a.npow = p.npow;
   a.leaf = p.leaf; a.vm = p.vm; a.vl_expm = p.vl_expm; a.vl_mode = p.vl_mode; a.chen_expm = p.chen_expm;
   a.path = path; a.clock = clock; a.A = A; a.out = out;
-  const DWs w = dense_ws(p, s->readout);
+  const DWs w = dense_ws(p, s->readout, bwd);
   char* ws = (char*)workspace;
   a.apow = (float*)(ws + w.apow); a.loc = (float*)(ws + w.loc); a.fl = (float*)(ws + w.fl);
   a.summ = (float*)(ws + w.summ); a.sfl = (float*)(ws + w.sfl); a.car = (float*)(ws + w.car);
   a.pre = (float*)(ws + w.pre); a.mats = (float*)(ws + w.mats);
+  if (bwd) {
+    a.lloc = (float*)(ws + w.lloc); a.lam = (float*)(ws + w.lam); a.amax = (int*)(ws + w.amax);
+  }
   return a;
 }
 
@@ -1215,7 +1701,7 @@ int dense_combine_pass(const ews_dense_desc* s, const DPlan& p, const Args& a, h
   }
 }
 
-// the Van Loan leaf (levels only) and the flows of a scheme other than the series kernels' fused exact ones
+// the Van Loan leaf (levels and flows), or the flows of a scheme other than the series kernels' fused exact ones
 int launch_vl_and_flows(const DPlan& p, const Args& a, hipStream_t st) {
   const bool vl = p.leaf == EWS_LEAF_VAN_LOAN;
   const long total = (long)p.B * p.n_int;
@@ -1236,7 +1722,7 @@ int launch_vl_and_flows(const DPlan& p, const Args& a, hipStream_t st) {
     else hipLaunchKernelGGL((k_vl<3>), dim3(grid), dim3(64 * nw), shm, st, a);
     DENSE_CHECK();
   }
-  if (vl || p.chen_expm != EWS_EXPM_EXACT) {
+  if (!vl && p.chen_expm != EWS_EXPM_EXACT) {  // the Van Loan kernel writes its flows itself
     const long blocks = (total + 3) / 4;
     const int grid = (int)(blocks < 8192 ? blocks : 8192);
     hipLaunchKernelGGL(k_flows, dim3(grid), dim3(256), 0, st, a);
@@ -1259,6 +1745,70 @@ int dense_forward_pass(const ews_dense_desc* s, const DPlan& p, const Args& a, h
 }
 
 constexpr int kDenseForwardPasses = 4;
+
+template <int MODE>
+int launch_adj(int N, const AdjSeq& q, dim3 grid, hipStream_t st) {
+  if (N == 3) hipLaunchKernelGGL((k_adj<3, MODE>), grid, dim3(256), 0, st, q);
+  else if (N == 2) hipLaunchKernelGGL((k_adj<2, MODE>), grid, dim3(256), 0, st, q);
+  else hipLaunchKernelGGL((k_adj<1, MODE>), grid, dim3(256), 0, st, q);
+  DENSE_CHECK();
+  return EWS_OK;
+}
+
+// The adjoint of the combine and readout, given the forward's local terms / flows (loc, fl), chunk summaries and
+// carries in the workspace: recomputes the prefix rows (the states), then LOCAL, CARRY and EMIT; leaves ds_t in loc
+// and dM_t in fl.
+int dense_adjoint(const ews_dense_desc* s, const DPlan& p, const Args& a, const float* grad_out, hipStream_t st) {
+  const int Wst = p.D + 1;
+  {  // prefix rows of the forward (the states S_t), with the level-0 column
+    Seq q{};
+    q.lv = a.loc; q.lv_bs = (long)p.n_int * p.LW; q.fl = a.fl; q.fl_bs = (long)p.n_int * 256;
+    q.n = p.n_int; q.T = p.T; q.init = a.car; q.init_bs = (long)(p.C + 1) * p.LW;
+    q.rows = a.pre; q.rows_bs = (long)p.n_int * Wst; q.rows_ld = Wst; q.padded = 0; q.lvl0 = 1; q.d = p.d;
+    q.C = p.C;
+    const int rc = launch_scan<false>(p.N, q, dim3(p.C, p.B), st);
+    if (rc != EWS_OK) return rc;
+  }
+  const int ro = s->readout;
+  if ((ro == EWS_READOUT_MEAN || ro == EWS_READOUT_MAX) && !s->level0) return EWS_ERR_OPTION;
+  if (ro == EWS_READOUT_MAX) {
+    hipLaunchKernelGGL(k_argmax, dim3((Wst + 255) / 256, p.B), dim3(256), 0, st, a.pre, p.n_int, Wst, a.amax);
+    DENSE_CHECK();
+  }
+  hipLaunchKernelGGL(k_lam_end, dim3((p.LW + 255) / 256, p.B), dim3(256), 0, st, a,
+                     ro == EWS_READOUT_TERMINAL ? grad_out : nullptr, s->level0 ? 1 : 0);
+  DENSE_CHECK();
+  AdjSeq q{};
+  q.n = p.n_int; q.T = p.T; q.C = p.C; q.d = p.d;
+  q.gmode = ro == EWS_READOUT_PREFIX ? G_PREFIX : ro == EWS_READOUT_MEAN ? G_MEAN : ro == EWS_READOUT_MAX ? G_MAX
+                                                                                                     : G_NONE;
+  q.W = p.W; q.glvl0 = s->level0 ? 1 : 0; q.g = grad_out; q.amax = a.amax; q.gscale = 1.0f / (float)p.n_int;
+  q.st = a.pre; q.Wst = Wst;
+  // LOCAL (the terminal readout has no in-chunk cotangents: the local parts are zero)
+  if (q.gmode == G_NONE) {
+    hipLaunchKernelGGL(k_zero_rows, dim3((p.LW + 255) / 256, p.B * p.C), dim3(256), 0, st, a.lloc, (long)p.LW,
+                       p.B * p.C, p.LW);
+    DENSE_CHECK();
+  } else {
+    AdjSeq ql = q;
+    ql.lv = a.loc; ql.lv_bs = (long)p.n_int * p.LW; ql.fl = a.fl; ql.fl_bs = (long)p.n_int * 256;
+    ql.lam = a.lloc;
+    const int rc = launch_adj<ADJ_LOCAL>(p.N, ql, dim3(p.C, p.B), st);
+    if (rc != EWS_OK) return rc;
+  }
+  {  // CARRY over the chunk summaries
+    AdjSeq qc = q;
+    qc.gmode = G_NONE;
+    qc.lv = a.summ; qc.lv_bs = (long)p.C * p.LW; qc.fl = a.sfl; qc.fl_bs = (long)p.C * 256;
+    qc.init = a.lam; qc.lam = a.lam; qc.lloc = a.lloc;
+    const int rc = launch_adj<ADJ_CARRY>(p.N, qc, dim3(1, p.B), st);
+    if (rc != EWS_OK) return rc;
+  }
+  AdjSeq qe = q;
+  qe.lv = a.loc; qe.lv_bs = (long)p.n_int * p.LW; qe.fl = a.fl; qe.fl_bs = (long)p.n_int * 256;
+  qe.init = a.lam; qe.dlv = a.loc; qe.dfl = a.fl;
+  return launch_adj<ADJ_EMIT>(p.N, qe, dim3(p.C, p.B), st);
+}
 
 }  // namespace
 
@@ -1307,6 +1857,36 @@ int ews_dense_local_terms(const ews_dense_desc* desc, const float* path, const f
   const int r0 = dense_forward_pass(&s, q, a, st, 0);
   if (r0 != EWS_OK) return r0;
   hipLaunchKernelGGL(k_unpad_outputs, dim3(p.B * p.n_int), dim3(256), 0, st, a, levels, flows);
+  DENSE_CHECK();
+  return EWS_OK;
+}
+
+size_t ews_dense_backward_workspace_bytes(const ews_dense_desc* desc) {
+  DPlan p;
+  if (dense_plan(desc, p) != EWS_OK) return 0;
+  return dense_ws(p, desc->readout, true).total;
+}
+
+int ews_dense_combine_backward(const ews_dense_desc* desc, const float* levels, const float* flows,
+                               const float* grad_out, float* grad_levels, float* grad_flows, void* workspace,
+                               ews_stream_t stream) {
+  DPlan p;
+  const int rc = dense_plan(desc, p);
+  if (rc != EWS_OK) return rc;
+  if (!levels || !flows || !grad_out || !grad_levels || !grad_flows || !workspace) return EWS_ERR_NULL;
+  const Args a = dense_args(desc, p, nullptr, nullptr, nullptr, nullptr, workspace, true);
+  hipStream_t st = (hipStream_t)stream;
+  hipLaunchKernelGGL(k_pad_inputs, dim3(p.B * p.n_int), dim3(256), 0, st, a, levels, flows);
+  DENSE_CHECK();
+  for (int pass = 1; pass <= 2; ++pass) {
+    const int r = dense_combine_pass(desc, p, a, st, pass);
+    if (r != EWS_OK) return r;
+  }
+  const int r = dense_adjoint(desc, p, a, grad_out, st);
+  if (r != EWS_OK) return r;
+  Args u = a;
+  u.W = p.D + u.lvl0;  // k_unpad_outputs writes levels with the packed width D = W - lvl0
+  hipLaunchKernelGGL(k_unpad_outputs, dim3(p.B * p.n_int), dim3(256), 0, st, u, grad_levels, grad_flows);
   DENSE_CHECK();
   return EWS_OK;
 }

@@ -42,6 +42,8 @@ EXPORTED = (
     "ews_dense_num_passes",
     "ews_dense_local_terms",
     "ews_dense_combine",
+    "ews_dense_backward_workspace_bytes",
+    "ews_dense_combine_backward",
 )
 
 
@@ -130,6 +132,10 @@ def load():
     lib.ews_dense_local_terms.restype = i32
     lib.ews_dense_combine.argtypes = [ddp, vp, vp, vp, vp, vp]
     lib.ews_dense_combine.restype = i32
+    lib.ews_dense_backward_workspace_bytes.argtypes = [ddp]
+    lib.ews_dense_backward_workspace_bytes.restype = sz
+    lib.ews_dense_combine_backward.argtypes = [ddp, vp, vp, vp, vp, vp, vp, vp]
+    lib.ews_dense_combine_backward.restype = i32
     _lib = lib
     return lib
 

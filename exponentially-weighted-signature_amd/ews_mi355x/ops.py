@@ -219,3 +219,29 @@ def dense_combine(levels, flows, N, readout="prefix", level0=True, chunk=0):
                                ws.data_ptr(), _stream_handle(levels.device))
     nat.check(rc, "ews_dense_combine")
     return out
+
+
+def dense_combine_backward(levels, flows, grad_out, N, readout="prefix", level0=True, chunk=0):
+    """Cotangents (grad_levels, grad_flows) of dense_combine's inputs for the cotangent grad_out of its output
+    (the VJP of ews/core/kernels/pallas_combine.py:2628 dense_general_prefix_vjp)."""
+    lib = nat.load()
+    for name, x in (("levels", levels), ("flows", flows), ("grad_out", grad_out)):
+        if not x.is_cuda or x.dtype != torch.float32:
+            raise TypeError(f"{name} must be a float32 tensor on the HIP device")
+    levels, flows, grad_out = levels.contiguous(), flows.contiguous(), grad_out.contiguous()
+    B, n, d = flows.shape[0], flows.shape[1], flows.shape[2]
+    desc = make_dense_desc(B, n + 1, d, N, 0, "per_interval", readout, level0, chunk)
+    D = sum(d**k for k in range(1, N + 1))
+    W = D + (1 if level0 else 0)
+    shape = (B, n, W) if readout == "prefix" else (B, W)
+    if levels.shape != (B, n, D) or grad_out.shape != shape:
+        raise ValueError(f"levels must be {(B, n, D)} and grad_out {shape}")
+    gl = torch.empty_like(levels)
+    gf = torch.empty_like(flows)
+    ws = torch.empty(int(lib.ews_dense_backward_workspace_bytes(ctypes.byref(desc))), device=levels.device,
+                     dtype=torch.uint8)
+    rc = lib.ews_dense_combine_backward(ctypes.byref(desc), levels.data_ptr(), flows.data_ptr(),
+                                        grad_out.data_ptr(), gl.data_ptr(), gf.data_ptr(), ws.data_ptr(),
+                                        _stream_handle(levels.device))
+    nat.check(rc, "ews_dense_combine_backward")
+    return gl, gf

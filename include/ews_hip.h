@@ -160,6 +160,20 @@ int ews_dense_local_terms(const ews_dense_desc* desc, const float* path, const f
 int ews_dense_combine(const ews_dense_desc* desc, const float* levels, const float* flows, float* out,
                       void* workspace, ews_stream_t stream);
 
+/* Scratch of the dense backward entry points: the forward's buffers (with the prefix rows) and the adjoint
+ * scan's per-chunk cotangents and carries. */
+size_t ews_dense_backward_workspace_bytes(const ews_dense_desc* desc);
+
+/* Backward of ews_dense_combine: given the cotangent grad_out of out, writes grad_levels (B, L-1, sum_k d^k) and
+ * grad_flows (B, L-1, d, d). Replaces the custom VJP of dense_general_prefix_vjp (the dense kernel's
+ * _dense_kernel_general_bwd, ews/core/kernels/pallas_combine.py:2360-2565, and _cvjp_bwd :1698-1798): a local
+ * reverse scan per chunk, a reverse scan of the chunk carries over the chunk summaries, and a reverse scan per
+ * chunk from its carry that emits the cotangents (the max readout's cotangent goes to the first row attaining
+ * the maximum). */
+int ews_dense_combine_backward(const ews_dense_desc* desc, const float* levels, const float* flows,
+                               const float* grad_out, float* grad_levels, float* grad_flows, void* workspace,
+                               ews_stream_t stream);
+
 /* Human-readable text of a return code. */
 const char* ews_error_string(int code);
 
