@@ -1409,6 +1409,327 @@ __global__ __launch_bounds__(256) void k_adj(AdjSeq s) {
   }
 }
 
+// ------------------------------------------------------------------------------------------------ leaf adjoints
+// Cotangents of the leaf and the flows of one interval, given ds_t (the local terms' cotangent, padded) and dM_t,
+// one workgroup of 256 threads per interval (grid-stride); thread e owns entry e = 16 i + j of d x d matrices.
+// Outputs per interval: dv_t (the increment's cotangent) and dh_t (the clock step's); per sample: the cotangent of
+// the shared flow step (cached modes); per workgroup: dA terms.
+// dA is collected in two parts. Terms of the recursions b_p = (-h/p) A b_{p-1} go straight to a d x d sum. Terms of
+// matrix polynomials in A (the flows' Taylor polynomial T(y) = sum_p (y^p / p!) A^p) collect the cotangent H_p of
+// each power A^p; k_dA then forms sum_p sum_{j<p} (A^T)^j H_p (A^T)^{p-1-j} once.
+//
+// Series leaf (series_leaf.py:55-126 restated as nested degree sums; see k_local): with g1_n = b_n / (n+1),
+//   s1 = sum_n g1_n;  s2 = sum_n bt2_n (x) g1_n, bt2_n = sum_{p <= q-n} b_p / (p+n+2);
+//   s3 = sum_N bt3_N (x) g2_N, bt3_N = sum_{p <= q-N} b_p / (p+N+3), g2_N = 1/(N+2) sum_{p+n=N} b_p (x) g1_n
+//   (and s2 = sum_N g2_N at depth 3).
+// Flows (exact): M = T(y)^(2^s), y = -h / 2^s; the squarings' adjoint G <- G E^T + E^T G, then T's.
+constexpr int HP = PM + 1;   // powers with a collected cotangent H_p, p <= PM
+constexpr int SQMAX = 30;    // squarings the flows take at most (as in the forward)
+
+struct LeafBwd {
+  float* dv;    // (B, n, 16)
+  float* dh;    // (B, n)
+  float* dsh;   // (B, 2): cotangents of the shared flow step and of the shared Van Loan step (cached modes)
+  float* part;  // (gridDim.x, HP + 1, 256): per-workgroup H_0..H_PM and the direct dA terms
+};
+
+template <int N>
+__global__ __launch_bounds__(256) void k_leaf_bwd(Args a, LeafBwd o) {
+  constexpr int LW = lw_of(N);
+  constexpr int QN = QMAX + 1;
+  __shared__ __align__(16) float sp[HP][256];
+  __shared__ __align__(16) float Lt[QN][16], G1[QN][16], BT[QN][16], dB[QN][16], dG1[QN][16], dBT[QN][16];
+  __shared__ __align__(16) float dS3[N >= 3 ? 4096 : 4];
+  __shared__ __align__(16) float dS2[256], F[256], Gm[256], Esq[SQMAX][256];
+  __shared__ float dS1[16], yv[16], red[8];
+  const int tid = threadIdx.x, i = tid >> 4, j = tid & 15;
+  const int q = a.q;
+  for (int e = tid; e < HP * 256; e += 256) sp[e >> 8][e & 255] = a.apow[e];
+  const float norm1 = a.apow[a.npow * 256];
+  float H[HP];
+#pragma unroll
+  for (int p = 0; p < HP; ++p) H[p] = 0.0f;
+  float dAl = 0.0f;
+  const float Aij = a.apow[256 + tid];  // A[i][j] (P_1 = A)
+  __syncthreads();
+  const long total = (long)a.B * a.n_int;
+  for (long it = blockIdx.x; it < total; it += gridDim.x) {
+    const int b = (int)(it / a.n_int), t = (int)(it - (long)b * a.n_int);
+    const float* th = a.clock + (size_t)b * a.L;
+    const float h = th[t + 1] - th[t];
+    const float* drow = a.loc + ((size_t)b * a.n_int + t) * LW;  // ds_t
+    // ---- inputs
+    if (tid < 16) {
+      const float* x = a.path + ((size_t)b * a.L + t) * a.d;
+      const float v = tid < a.d ? x[a.d + tid] - x[tid] : 0.0f;
+      Lt[0][tid] = v;
+      dS1[tid] = drow[tid];
+    }
+    if constexpr (N >= 2) dS2[tid] = drow[16 + tid];
+    if constexpr (N >= 3) {
+      for (int e = tid; e < 4096; e += 256) dS3[e] = drow[272 + e];
+    }
+    Gm[tid] = a.fl[((size_t)b * a.n_int + t) * 256 + tid];  // dM_t
+    for (int e = tid; e < QN * 16; e += 256) {
+      (&dB[0][0])[e] = 0.0f;
+      (&dBT[0][0])[e] = 0.0f;
+    }
+    __syncthreads();
+    // ---- letters b_p = (-h/p) A b_{p-1}
+    for (int p = 1; p <= q; ++p) {
+      float v = Aij * Lt[p - 1][j];
+#pragma unroll
+      for (int o2 = 1; o2 < 16; o2 <<= 1) v += __shfl_xor(v, o2, 64);
+      if (j == 0) Lt[p][i] = v * (-h / (float)p);
+      __syncthreads();
+    }
+    for (int e = tid; e < (q + 1) * 16; e += 256) {
+      const int n = e >> 4, r = e & 15;
+      G1[n][r] = Lt[n][r] / (float)(n + 1);
+      dG1[n][r] = dS1[r];
+    }
+    if constexpr (N >= 2) {
+      for (int e = tid; e < (q + 1) * 16; e += 256) {
+        const int n = e >> 4, r = e & 15;
+        float sacc = 0.0f;
+        for (int p = 0; p + n <= q; ++p) sacc += Lt[p][r] / (float)(p + n + N);
+        BT[n][r] = sacc;
+      }
+    }
+    __syncthreads();
+    // ---- level adjoints
+    if constexpr (N == 2) {
+      // dbt2_n = ds2 g1_n;  dg1_n += ds2^T bt2_n
+      for (int e = tid; e < (q + 1) * 16; e += 256) {
+        const int n = e >> 4, r = e & 15;
+        float x1 = 0.0f, x2 = 0.0f;
+#pragma unroll
+        for (int k = 0; k < 16; ++k) {
+          x1 = fmaf(dS2[r * 16 + k], G1[n][k], x1);
+          x2 = fmaf(dS2[k * 16 + r], BT[n][k], x2);
+        }
+        dBT[n][r] = x1;
+        dG1[n][r] += x2;
+      }
+      __syncthreads();
+    }
+    if constexpr (N == 3) {
+      for (int NN = 0; NN <= q; ++NN) {
+        // dg2_NN = bt3_NN ._1 ds3 + ds2
+        {
+          float f = dS2[tid];
+#pragma unroll 4
+          for (int aa = 0; aa < 16; ++aa) f = fmaf(BT[NN][aa], dS3[aa * 256 + tid], f);
+          F[tid] = f;
+        }
+        __syncthreads();
+        // pairs (p, n = NN - p): db_p += dg2 g1_n / (NN+2);  dg1_n += dg2^T b_p / (NN+2)
+        const float inv2 = 1.0f / (float)(NN + 2);
+        for (int e = tid; e < (NN + 1) * 32; e += 256) {
+          const int p = e >> 5, r = e & 15, side = (e >> 4) & 1, n = NN - p;
+          float x = 0.0f;
+          if (side == 0) {
+#pragma unroll
+            for (int k = 0; k < 16; ++k) x = fmaf(F[r * 16 + k], G1[n][k], x);
+            dB[p][r] += x * inv2;
+          } else {
+#pragma unroll
+            for (int k = 0; k < 16; ++k) x = fmaf(F[k * 16 + r], Lt[p][k], x);
+            dG1[n][r] += x * inv2;
+          }
+        }
+        __syncthreads();
+      }
+      // dbt3_{p+n} += (E_n b_p) / (p+n+2), E_n = ds3 ._3 g1_n
+      for (int n = 0; n <= q; ++n) {
+        {
+          float f = 0.0f;
+#pragma unroll
+          for (int k = 0; k < 16; ++k) f = fmaf(dS3[tid * 16 + k], G1[n][k], f);
+          F[tid] = f;  // E_n[i][j]
+        }
+        __syncthreads();
+        for (int e = tid; e < (q - n + 1) * 16; e += 256) {
+          const int p = e >> 4, r = e & 15;
+          float x = 0.0f;
+#pragma unroll
+          for (int k = 0; k < 16; ++k) x = fmaf(F[r * 16 + k], Lt[p][k], x);
+          dBT[p + n][r] += x / (float)(p + n + 2);
+        }
+        __syncthreads();
+      }
+    }
+    // bt_N -> b_p; g1_n -> b_n
+    for (int e = tid; e < (q + 1) * 16; e += 256) {
+      const int p = e >> 4, r = e & 15;
+      float x = dB[p][r] + dG1[p][r] / (float)(p + 1);
+      if constexpr (N >= 2) {
+        for (int NN = 0; NN + p <= q; ++NN) x += dBT[NN][r] / (float)(p + NN + N);
+      }
+      dB[p][r] = x;
+    }
+    __syncthreads();
+    // ---- letters reverse: db_{p-1} += (-h/p) A^T db_p; dA += (-h/p) db_p (x) b_{p-1}; dh += -(1/p) <A^T db_p, b_{p-1}>
+    float dhl = 0.0f;
+    for (int p = q; p >= 1; --p) {
+      float y = sp[1][j * 16 + i] * dB[p][j];  // A[j][i] db_p[j], summed over j
+#pragma unroll
+      for (int o2 = 1; o2 < 16; o2 <<= 1) y += __shfl_xor(y, o2, 64);
+      const float c = -h / (float)p;
+      dAl = fmaf(c * dB[p][i], Lt[p - 1][j], dAl);
+      if (j == 0) {
+        dB[p - 1][i] += c * y;
+        dhl -= y * Lt[p - 1][i] / (float)p;
+      }
+      __syncthreads();
+    }
+    // ---- flow adjoint
+    float dhf = 0.0f;
+    bool ident;
+    const float hf = flow_step(a, th, t, ident);
+    if (!ident) {
+      int s = 0;
+      float x = fabsf(hf) * norm1;
+      while (x > 1.0f && s < SQMAX) {
+        x *= 0.5f;
+        ++s;
+      }
+      const float y = -hf * ldexpf(1.0f, -s);
+      float T = sp[PM][tid];
+#pragma unroll
+      for (int p = PM - 1; p >= 0; --p) T = fmaf(T, y, sp[p][tid]);
+      if (s > 0) Esq[0][tid] = T;
+      __syncthreads();
+      for (int r = 1; r < s; ++r) {
+        float e2 = 0.0f;
+#pragma unroll
+        for (int k = 0; k < 16; ++k) e2 = fmaf(Esq[r - 1][i * 16 + k], Esq[r - 1][k * 16 + j], e2);
+        Esq[r][tid] = e2;
+        __syncthreads();
+      }
+      for (int r = s - 1; r >= 0; --r) {  // G <- G E^T + E^T G
+        float g2 = 0.0f;
+#pragma unroll
+        for (int k = 0; k < 16; ++k) {
+          g2 = fmaf(Gm[i * 16 + k], Esq[r][j * 16 + k], g2);
+          g2 = fmaf(Esq[r][k * 16 + i], Gm[k * 16 + j], g2);
+        }
+        __syncthreads();
+        Gm[tid] = g2;
+        __syncthreads();
+      }
+      const float G0 = Gm[tid];
+      // H_p += (y^p / p!) G0;  dy = sum_p p y^{p-1} <G0, P_p>
+      float yp = 1.0f, fact = 1.0f;
+#pragma unroll
+      for (int p = 0; p < HP; ++p) {
+        if (p) fact *= (float)p;
+        H[p] = fmaf(yp / fact, G0, H[p]);
+        yp *= y;
+      }
+      float dy = 0.0f, ypm1 = 1.0f;  // y^{p-1}
+#pragma unroll
+      for (int p = 1; p < HP; ++p) {
+        dy = fmaf((float)p * ypm1, sp[p][tid] * G0, dy);
+        ypm1 *= y;
+      }
+#pragma unroll
+      for (int o2 = 1; o2 < 64; o2 <<= 1) dy += __shfl_xor(dy, o2, 64);
+      if ((tid & 63) == 0) red[tid >> 6] = dy;
+      __syncthreads();
+      dhf = -(red[0] + red[1] + red[2] + red[3]) * ldexpf(1.0f, -s);
+    }
+    // ---- outputs
+    if (tid < 16) o.dv[((size_t)b * a.n_int + t) * 16 + tid] = dB[0][tid];
+    {
+      float v = dhl;  // nonzero in threads j == 0
+#pragma unroll
+      for (int o2 = 16; o2 < 64; o2 <<= 1) v += __shfl_xor(v, o2, 64);
+      if ((tid & 63) == 0) red[4 + (tid >> 6)] = v;
+    }
+    __syncthreads();
+    if (tid == 0) {
+      const float dl = red[4] + red[5] + red[6] + red[7];
+      if (a.flow_mode == EWS_FLOW_PER_INTERVAL) {
+        o.dh[(size_t)b * a.n_int + t] = dl + dhf;
+      } else {
+        o.dh[(size_t)b * a.n_int + t] = dl;
+        if (!ident) atomicAdd(o.dsh + 2 * b, dhf);
+      }
+    }
+    __syncthreads();
+  }
+  float* pb = o.part + (size_t)blockIdx.x * (HP + 1) * 256;
+#pragma unroll
+  for (int p = 0; p < HP; ++p) pb[p * 256 + tid] = H[p];
+  pb[HP * 256 + tid] = dAl;
+}
+
+// sums of the workgroups' partials (float64), one workgroup per row p of (HP + 1, 256)
+__global__ __launch_bounds__(256) void k_part_reduce(const float* part, int nparts, double* hsum) {
+  const int p = blockIdx.x, tid = threadIdx.x;
+  double s0 = 0.0, s1 = 0.0, s2 = 0.0, s3 = 0.0;
+  int k = 0;
+  for (; k + 4 <= nparts; k += 4) {
+    s0 += (double)part[((size_t)k * (HP + 1) + p) * 256 + tid];
+    s1 += (double)part[((size_t)(k + 1) * (HP + 1) + p) * 256 + tid];
+    s2 += (double)part[((size_t)(k + 2) * (HP + 1) + p) * 256 + tid];
+    s3 += (double)part[((size_t)(k + 3) * (HP + 1) + p) * 256 + tid];
+  }
+  for (; k < nparts; ++k) s0 += (double)part[((size_t)k * (HP + 1) + p) * 256 + tid];
+  hsum[p * 256 + tid] = (s0 + s1) + (s2 + s3);
+}
+
+// dA = sum_p sum_{j<p} (A^T)^j H_p (A^T)^{p-1-j} + the direct terms (float64):
+// R_{P-1} = H_P, R_j = H_{j+1} + R_{j+1} A^T, dA = R_0 + A^T (R_1 + A^T (R_2 + ...)), P = PM.
+__global__ __launch_bounds__(256) void k_dA(Args a, const double* hsum, float* grad_A) {
+  __shared__ double At[256], Rs[PM][256], U[256];
+  const int tid = threadIdx.x, i = tid >> 4, j = tid & 15;
+  At[tid] = (double)a.apow[256 + j * 16 + i];  // A^T[i][j]
+  Rs[PM - 1][tid] = hsum[PM * 256 + tid];
+  __syncthreads();
+  for (int jj = PM - 2; jj >= 0; --jj) {
+    double v = hsum[(jj + 1) * 256 + tid];
+    for (int k = 0; k < 16; ++k) v += Rs[jj + 1][i * 16 + k] * At[k * 16 + j];
+    Rs[jj][tid] = v;
+    __syncthreads();
+  }
+  U[tid] = Rs[PM - 1][tid];
+  __syncthreads();
+  for (int jj = PM - 2; jj >= 0; --jj) {
+    double v = Rs[jj][tid];
+    for (int k = 0; k < 16; ++k) v += At[i * 16 + k] * U[k * 16 + j];
+    __syncthreads();
+    U[tid] = v;
+    __syncthreads();
+  }
+  if (i < a.d && j < a.d) grad_A[i * a.d + j] = (float)(U[tid] + hsum[HP * 256 + tid]);
+}
+
+// knot cotangents: dpath[k] = dv_{k-1} - dv_k, dclock[k] = dh_{k-1} - dh_k, plus the shared steps of the cached modes
+// (the flow step th[1] - th[0], or th[2] - th[1] for the basepoint mode; the Van Loan step likewise)
+__global__ void k_knots(Args a, LeafBwd o, float* grad_path, float* grad_clock) {
+  const int b = blockIdx.y;
+  const int k = blockIdx.x * blockDim.x + threadIdx.x;
+  if (k >= a.L) return;
+  const size_t base = (size_t)b * a.n_int;
+  for (int r = 0; r < a.d; ++r) {
+    const float lo = k > 0 ? o.dv[(base + k - 1) * 16 + r] : 0.0f;
+    const float hi = k < a.n_int ? o.dv[(base + k) * 16 + r] : 0.0f;
+    grad_path[((size_t)b * a.L + k) * a.d + r] = lo - hi;
+  }
+  if (grad_clock) {
+    float v = (k > 0 ? o.dh[base + k - 1] : 0.0f) - (k < a.n_int ? o.dh[base + k] : 0.0f);
+    const float sf = o.dsh[2 * b], sv = o.dsh[2 * b + 1];
+    if (a.flow_mode == EWS_FLOW_CACHED) v += (k == 1 ? sf : 0.0f) - (k == 0 ? sf : 0.0f);
+    if (a.flow_mode == EWS_FLOW_CACHED_BASEPOINT) v += (k == 2 ? sf : 0.0f) - (k == 1 ? sf : 0.0f);
+    if (a.leaf == EWS_LEAF_VAN_LOAN && a.vl_mode == EWS_FLOW_CACHED) v += (k == 1 ? sv : 0.0f) - (k == 0 ? sv : 0.0f);
+    if (a.leaf == EWS_LEAF_VAN_LOAN && a.vl_mode == EWS_FLOW_CACHED_BASEPOINT)
+      v += (k == 2 ? sv : 0.0f) - (k == 1 ? sv : 0.0f);
+    grad_clock[(size_t)b * a.L + k] = v;
+  }
+}
+
 // ------------------------------------------------------------------------------------------------ readouts
 // zero state rows (carries row 0)
 __global__ void k_zero_rows(float* base, long stride, int n_rows, int width) {
@@ -1561,8 +1882,10 @@ int dense_plan(const ews_dense_desc* s, DPlan& p) {
   return EWS_OK;
 }
 
+constexpr int kLeafBwdBlocks = 1024;  // workgroups of the leaf adjoint (one partial dA set each)
+
 struct DWs {
-  size_t apow, loc, fl, summ, sfl, car, pre, mats, lloc, lam, amax, total;
+  size_t apow, loc, fl, summ, sfl, car, pre, mats, lloc, lam, amax, dv, dh, dsh, part, hsum, total;
 };
 // bwd: the backward's layout, the forward's buffers (prefix rows always) followed by the adjoint scan's
 DWs dense_ws(const DPlan& p, int readout, bool bwd = false) {
@@ -1583,6 +1906,11 @@ DWs dense_ws(const DPlan& p, int readout, bool bwd = false) {
     w.lloc = off; off += al256(BC * p.LW * 4);
     w.lam = off; off += al256((size_t)p.B * (p.C + 1) * p.LW * 4);
     w.amax = off; off += al256((size_t)p.B * (p.D + 1) * 4);
+    w.dv = off; off += al256(BN * 16 * 4);
+    w.dh = off; off += al256(BN * 4);
+    w.dsh = off; off += al256((size_t)p.B * 2 * 4);
+    w.part = off; off += al256((size_t)kLeafBwdBlocks * (HP + 1) * 256 * 4);
+    w.hsum = off; off += al256((size_t)(HP + 1) * 256 * 8);
   }
   w.total = off;
   return w;
@@ -1887,6 +2215,44 @@ int ews_dense_combine_backward(const ews_dense_desc* desc, const float* levels, 
   Args u = a;
   u.W = p.D + u.lvl0;  // k_unpad_outputs writes levels with the packed width D = W - lvl0
   hipLaunchKernelGGL(k_unpad_outputs, dim3(p.B * p.n_int), dim3(256), 0, st, u, grad_levels, grad_flows);
+  DENSE_CHECK();
+  return EWS_OK;
+}
+
+int ews_dense_backward(const ews_dense_desc* desc, const float* path, const float* clock, const float* A,
+                       const float* grad_out, float* grad_path, float* grad_clock, float* grad_A, void* workspace,
+                       ews_stream_t stream) {
+  DPlan p;
+  const int rc = dense_plan(desc, p);
+  if (rc != EWS_OK) return rc;
+  if (!path || !clock || !A || !grad_out || !grad_path || !grad_A || !workspace) return EWS_ERR_NULL;
+  if (p.leaf != EWS_LEAF_SERIES || p.chen_expm != EWS_EXPM_EXACT) return EWS_ERR_OPTION;
+  const Args a = dense_args(desc, p, path, clock, A, nullptr, workspace, true);
+  hipStream_t st = (hipStream_t)stream;
+  for (int pass = 0; pass <= 2; ++pass) {  // the forward up to the carries
+    const int r = dense_forward_pass(desc, p, a, st, pass);
+    if (r != EWS_OK) return r;
+  }
+  const int r = dense_adjoint(desc, p, a, grad_out, st);
+  if (r != EWS_OK) return r;
+  const DWs w = dense_ws(p, desc->readout, true);
+  char* ws = (char*)workspace;
+  LeafBwd o;
+  o.dv = (float*)(ws + w.dv); o.dh = (float*)(ws + w.dh); o.dsh = (float*)(ws + w.dsh); o.part = (float*)(ws + w.part);
+  double* hsum = (double*)(ws + w.hsum);
+  hipLaunchKernelGGL(k_zero_rows, dim3(1, 1), dim3(256), 0, st, o.dsh, 0L, 1, 2 * p.B);
+  DENSE_CHECK();
+  const long total = (long)p.B * p.n_int;
+  const int grid = (int)(total < kLeafBwdBlocks ? total : kLeafBwdBlocks);
+  if (p.N == 1) hipLaunchKernelGGL((k_leaf_bwd<1>), dim3(grid), dim3(256), 0, st, a, o);
+  else if (p.N == 2) hipLaunchKernelGGL((k_leaf_bwd<2>), dim3(grid), dim3(256), 0, st, a, o);
+  else hipLaunchKernelGGL((k_leaf_bwd<3>), dim3(grid), dim3(256), 0, st, a, o);
+  DENSE_CHECK();
+  hipLaunchKernelGGL(k_part_reduce, dim3(HP + 1), dim3(256), 0, st, o.part, grid, hsum);
+  DENSE_CHECK();
+  hipLaunchKernelGGL(k_dA, dim3(1), dim3(256), 0, st, a, hsum, grad_A);
+  DENSE_CHECK();
+  hipLaunchKernelGGL(k_knots, dim3((p.L + 255) / 256, p.B), dim3(256), 0, st, a, o, grad_path, grad_clock);
   DENSE_CHECK();
   return EWS_OK;
 }

@@ -44,6 +44,7 @@ EXPORTED = (
     "ews_dense_combine",
     "ews_dense_backward_workspace_bytes",
     "ews_dense_combine_backward",
+    "ews_dense_backward",
 )
 
 
@@ -136,6 +137,8 @@ def load():
     lib.ews_dense_backward_workspace_bytes.restype = sz
     lib.ews_dense_combine_backward.argtypes = [ddp, vp, vp, vp, vp, vp, vp, vp]
     lib.ews_dense_combine_backward.restype = i32
+    lib.ews_dense_backward.argtypes = [ddp, vp, vp, vp, vp, vp, vp, vp, vp, vp]
+    lib.ews_dense_backward.restype = i32
     _lib = lib
     return lib
 

@@ -146,8 +146,9 @@ def _check_dense(path, clock, A):
 
 class DenseScan(torch.autograd.Function):
     """out = EWS readout of (path, clock) under a dense generator A (series leaf of order q or the Van Loan leaf,
-    flows of chen_expm). Forward only: the dense-generator adjoint kernels are not part of this library yet, and a
-    backward through this op raises instead of falling back to another engine."""
+    flows of chen_expm). The backward (ews_dense_backward: the combine's adjoint scans, then the leaf's and the flows'
+    adjoints) covers the series leaf with exact flows; for the other leaves and schemes it raises instead of falling
+    back to another engine."""
 
     @staticmethod
     def forward(ctx, path, clock, A, N, q, flow_mode, readout, level0, chunk, leaf):
@@ -156,6 +157,9 @@ class DenseScan(torch.autograd.Function):
         path, clock, A = path.contiguous(), clock.contiguous(), A.contiguous()
         B, L, d = path.shape
         desc = make_dense_desc(B, L, d, N, q, flow_mode, readout, level0, chunk, leaf)
+        ctx.save_for_backward(path, clock, A)
+        ctx.desc = desc
+        ctx.leaf = leaf
         D = sum(d**k for k in range(1, N + 1))
         W = D + (1 if level0 else 0)
         shape = (B, L - 1, W) if readout == "prefix" else (B, W)
@@ -169,9 +173,27 @@ class DenseScan(torch.autograd.Function):
 
     @staticmethod
     def backward(ctx, gout):
-        raise NotImplementedError(
-            "the dense-generator EWS (leaf='series' or 'van_loan' with a general A) has no backward kernels in "
-            "this build")
+        leaf = ctx.leaf
+        if leaf.kind != "series" or leaf.chen_expm != "exact":
+            raise NotImplementedError(
+                "the dense-generator backward covers the series leaf with exact flows (chen_expm='exact'); "
+                f"got leaf={leaf.kind!r}, chen_expm={leaf.chen_expm!r}")
+        lib = nat.load()
+        path, clock, A = ctx.saved_tensors
+        desc = ctx.desc
+        dev = path.device
+        gout = gout.to(torch.float32).contiguous()
+        gpath = torch.empty_like(path)
+        need_clock = ctx.needs_input_grad[1]
+        gclock = torch.empty_like(clock) if need_clock else None
+        gA = torch.empty_like(A)
+        ws = torch.empty(int(lib.ews_dense_backward_workspace_bytes(ctypes.byref(desc))), device=dev,
+                         dtype=torch.uint8)
+        rc = lib.ews_dense_backward(ctypes.byref(desc), path.data_ptr(), clock.data_ptr(), A.data_ptr(),
+                                    gout.data_ptr(), gpath.data_ptr(), gclock.data_ptr() if need_clock else None,
+                                    gA.data_ptr(), ws.data_ptr(), _stream_handle(dev))
+        nat.check(rc, "ews_dense_backward")
+        return gpath, gclock, gA, None, None, None, None, None, None, None
 
 
 def dense_scan(path, clock, A, N, q, flow_mode="per_interval", readout="prefix", level0=True, chunk=0, leaf=None):

@@ -145,10 +145,11 @@ def test_dense_c3_recipe():
     assert e < 1e-5
 
 
-def test_dense_backward_raises():
+def test_dense_backward_through_the_layer():
+    """The layer's backward runs the dense adjoint kernels (parity: tests/test_gpu_dense_bwd.py)."""
     path, clock, A = _random(1, 10, 4, seed=61)
     p = path.to(DEV).requires_grad_(True)
     layer = E.EWS(E.AParamConstant(A.to(DEV)), N=2, leaf="series", series_q=8)
     out = layer(p, clock.to(DEV), readout="prefix")
-    with pytest.raises(NotImplementedError):
-        out.sum().backward()
+    out.sum().backward()
+    assert p.grad is not None and torch.isfinite(p.grad).all()

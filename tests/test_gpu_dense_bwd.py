@@ -81,3 +81,70 @@ def test_dense_combine_backward(readout, N, d, n, chunk):
           f"flows {relerr(gfl, rfl):.2e}")
     _check_levels(glv, rlv, d, N, 1e-4, "levels")
     assert relerr(gfl, rfl) < 1e-4
+
+
+# ------------------------------------------------------------------------------------------------ full backward
+def _random(B, L, d, seed, hscale=0.05, ascale=1.0, uniform=False):
+    rng = np.random.default_rng(seed)
+    path = np.cumsum(rng.normal(size=(B, L, d)) * 0.3, 1)
+    if uniform:
+        clock = np.broadcast_to(np.arange(L) * hscale, (B, L)).copy()
+    else:
+        clock = np.cumsum(rng.uniform(0.5, 1.5, size=(B, L)) * hscale, 1)
+    A = rng.normal(size=(d, d)) * ascale / np.sqrt(d) + np.eye(d) * 0.5 * ascale
+    return torch.tensor(path), torch.tensor(clock), torch.tensor(A)
+
+
+_FLOW = {"displacement": "per_interval", "displacement_uniform": "cached",
+         "displacement_uniform_basepoint": "cached_basepoint"}
+
+
+def _grads(path, clock, A, N, q, readout, mode, level0=True, clock_grad=True, seed=3):
+    """(GPU grads, float64 autograd grads of the oracle) for (path, clock, A)."""
+    p64, c64, A64 = (x.clone().requires_grad_(True) for x in (path, clock, A))
+    ref_out = O.ews(p64, c64, A64, N, readout, leaf="series", series_q=q, reweighting_mode=mode,
+                    terminal_reduce="assoc")
+    if not level0:
+        ref_out = ref_out[..., 1:]
+    gout = torch.tensor(np.random.default_rng(seed).normal(size=ref_out.shape))
+    ref = torch.autograd.grad(ref_out, (p64, c64, A64), gout)
+    pg = path.float().to(DEV).requires_grad_(True)
+    cg = clock.float().to(DEV).requires_grad_(clock_grad)
+    Ag = A.float().to(DEV).requires_grad_(True)
+    out = ops.dense_scan(pg, cg, Ag, N, q, _FLOW[mode], readout, level0)
+    got = torch.autograd.grad(out, (pg, cg, Ag) if clock_grad else (pg, Ag), gout.float().to(DEV))
+    if not clock_grad:
+        got = (got[0], None, got[1])
+    return got, ref
+
+
+@pytest.mark.parametrize("readout", ["prefix", "terminal", "mean", "max"])
+@pytest.mark.parametrize("N,d,q,L", [(1, 16, 8, 40), (2, 16, 12, 70), (3, 16, 16, 70), (3, 5, 10, 45)])
+def test_dense_backward_series(readout, N, d, q, L):
+    path, clock, A = _random(2, L, d, seed=800 + N + d)
+    got, ref = _grads(path, clock, A, N, q, readout, "displacement", level0=readout in ("mean", "max") or N != 2)
+    errs = [relerr(g, r) for g, r in zip(got, ref)]
+    print(f"dense bwd {readout} N={N} d={d} q={q}: path {errs[0]:.2e} clock {errs[1]:.2e} A {errs[2]:.2e}")
+    assert max(errs) < 1e-4
+
+
+@pytest.mark.parametrize("mode", ["displacement_uniform", "displacement_uniform_basepoint"])
+def test_dense_backward_cached_flows(mode):
+    path, clock, A = _random(2, 60, 8, seed=820, uniform=True)
+    got, ref = _grads(path, clock, A, 3, 12, "prefix", mode)
+    errs = [relerr(g, r) for g, r in zip(got, ref)]
+    print(f"dense bwd {mode}: path {errs[0]:.2e} clock {errs[1]:.2e} A {errs[2]:.2e}")
+    assert max(errs) < 1e-4
+
+
+def test_dense_backward_large_steps_and_no_clock_grad():
+    """h ||A||_1 above 1 (flows scaled and squared, whose adjoint runs through the squarings), and a data clock
+    (no clock gradient: the kernels skip it)."""
+    path, clock, A = _random(2, 40, 16, seed=830, hscale=0.6)
+    got, ref = _grads(path, clock, A, 3, 24, "terminal", "displacement")
+    errs = [relerr(g, r) for g, r in zip(got, ref)]
+    print(f"dense bwd large steps: path {errs[0]:.2e} clock {errs[1]:.2e} A {errs[2]:.2e}")
+    assert max(errs) < 1e-4
+    got2, _ = _grads(path, clock, A, 3, 24, "terminal", "displacement", clock_grad=False)
+    assert got2[1] is None
+    assert relerr(got2[0], ref[0]) < 1e-4 and relerr(got2[2], ref[2]) < 1e-4
