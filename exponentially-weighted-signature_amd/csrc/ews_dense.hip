@@ -37,6 +37,7 @@ namespace dense {
 
 constexpr int QMAX = 40;   // largest series order
 constexpr int PM = 12;     // Taylor degree of the flow exponential (||X||_1 <= 1: error below 1/13! ~ 1.6e-10)
+constexpr int SQMAX = 20;  // squarings of a scaled exponential at most (|h| ||A||_1 <= 2^20)
 constexpr int RP = 20;     // LDS row pitch of the 16 x 16 slices (bank-conflict-free MFMA operand traffic)
 constexpr int SP = 16 * RP + 4;  // LDS slice pitch of the level-3 buffers
 
@@ -223,7 +224,7 @@ __global__ __launch_bounds__(256) void k_local(Args a) {
       } else {
         int s = 0;
         float x = fabsf(hf) * norm1;
-        while (x > 1.0f && s < 30) {
+        while (x > 1.0f && s < SQMAX) {
           x *= 0.5f;
           ++s;
         }
@@ -365,7 +366,7 @@ __global__ __launch_bounds__(256) void k_local3(Args a) {
       } else {
         int sq = 0;
         float x = fabsf(hf) * norm1;
-        while (x > 1.0f && sq < 30) {
+        while (x > 1.0f && sq < SQMAX) {
           x *= 0.5f;
           ++sq;
         }
@@ -411,7 +412,7 @@ typedef float LdsTable[256];
 __device__ __forceinline__ void wave_expm(const LdsTable* sp, float norm1, float c, float* E, float* Phi, int l) {
   int s = 0;
   float x = fabsf(c) * norm1;
-  while (x > 1.0f && s < 30) {
+  while (x > 1.0f && s < SQMAX) {
     x *= 0.5f;
     ++s;
   }
@@ -1424,7 +1425,6 @@ __global__ __launch_bounds__(256) void k_adj(AdjSeq s) {
 //   (and s2 = sum_N g2_N at depth 3).
 // Flows (exact): M = T(y)^(2^s), y = -h / 2^s; the squarings' adjoint G <- G E^T + E^T G, then T's.
 constexpr int HP = PM + 1;   // powers with a collected cotangent H_p, p <= PM
-constexpr int SQMAX = 30;    // squarings the flows take at most (as in the forward)
 
 struct LeafBwd {
   float* dv;    // (B, n, 16)
@@ -1433,6 +1433,158 @@ struct LeafBwd {
   float* part;  // (gridDim.x, HP + 1, 256): per-workgroup H_0..H_PM and the direct dA terms
 };
 
+// workgroup sum (256 threads) of one value per thread; red: 4 floats of LDS. Every thread gets the sum.
+__device__ __forceinline__ float block_sum(float v, float* red, int tid) {
+#pragma unroll
+  for (int o2 = 1; o2 < 64; o2 <<= 1) v += __shfl_xor(v, o2, 64);
+  __syncthreads();
+  if ((tid & 63) == 0) red[tid >> 6] = v;
+  __syncthreads();
+  return (red[0] + red[1]) + (red[2] + red[3]);
+}
+
+// Adjoint of E = exp(-c A) and Phi = phi(-c A) as the kernels evaluate them (wave_expm / series_mats: Taylor
+// polynomials of degree PM in y = -c / 2^s, then s doublings E <- E E, Phi <- (Phi + Phi E) / 2). GE and GPhi
+// (GPhi may be null) are the cotangents in LDS, overwritten. Adds the cotangents of the powers A^p to H (entry
+// tid) and returns the cotangent of c. Esq, Fsq: SQMAX matrices of LDS each (Fsq unused without GPhi).
+__device__ float block_exp_adjoint(const LdsTable* sp, float norm1, float c, float* GE, float* GPhi,
+                                   float (*Esq)[256], float (*Fsq)[256], float* red, float* H, int tid) {
+  const int i = tid >> 4, j = tid & 15;
+  int s = 0;
+  float x = fabsf(c) * norm1;
+  while (x > 1.0f && s < SQMAX) {
+    x *= 0.5f;
+    ++s;
+  }
+  const float y = -c * ldexpf(1.0f, -s);
+  float e = sp[PM][tid], f = e * (1.0f / (float)(PM + 1));
+#pragma unroll
+  for (int p = PM - 1; p >= 0; --p) {
+    e = fmaf(e, y, sp[p][tid]);
+    f = fmaf(f, y, sp[p][tid] * (1.0f / (float)(p + 1)));
+  }
+  if (s > 0) {
+    Esq[0][tid] = e;
+    if (GPhi) Fsq[0][tid] = f;
+  }
+  __syncthreads();
+  for (int r = 1; r < s; ++r) {
+    float e2 = 0.0f, f2 = 0.0f;
+#pragma unroll
+    for (int k = 0; k < 16; ++k) {
+      const float ekj = Esq[r - 1][k * 16 + j];
+      e2 = fmaf(Esq[r - 1][i * 16 + k], ekj, e2);
+      if (GPhi) f2 = fmaf(Fsq[r - 1][i * 16 + k], ekj, f2);
+    }
+    Esq[r][tid] = e2;
+    if (GPhi) Fsq[r][tid] = 0.5f * (Fsq[r - 1][tid] + f2);
+    __syncthreads();
+  }
+  for (int r = s - 1; r >= 0; --r) {
+    // E' = E E, Phi' = (Phi + Phi E) / 2:  GE <- GE' E^T + E^T GE' + Phi^T GPhi' / 2,  GPhi <- (GPhi' + GPhi' E^T) / 2
+    float ge = 0.0f, gf = 0.0f, gfe = 0.0f;
+#pragma unroll
+    for (int k = 0; k < 16; ++k) {
+      ge = fmaf(GE[i * 16 + k], Esq[r][j * 16 + k], ge);
+      ge = fmaf(Esq[r][k * 16 + i], GE[k * 16 + j], ge);
+      if (GPhi) {
+        gf = fmaf(Fsq[r][k * 16 + i], GPhi[k * 16 + j], gf);
+        gfe = fmaf(GPhi[i * 16 + k], Esq[r][j * 16 + k], gfe);
+      }
+    }
+    const float gp = GPhi ? GPhi[tid] : 0.0f;
+    __syncthreads();
+    GE[tid] = fmaf(0.5f, gf, ge);
+    if (GPhi) GPhi[tid] = 0.5f * (gp + gfe);
+    __syncthreads();
+  }
+  const float g0 = GE[tid], p0 = GPhi ? GPhi[tid] : 0.0f;
+  float yp = 1.0f, fact = 1.0f, dy = 0.0f, ypm1 = 1.0f;
+#pragma unroll
+  for (int p = 0; p < HP; ++p) {
+    if (p) fact *= (float)p;
+    const float gsum = g0 + p0 * (1.0f / (float)(p + 1));
+    H[p] = fmaf(yp / fact, gsum, H[p]);
+    if (p) {
+      dy = fmaf((float)p * ypm1 * sp[p][tid], gsum, dy);
+      ypm1 *= y;
+    }
+    yp *= y;
+  }
+  return -block_sum(dy, red, tid) * ldexpf(1.0f, -s);
+}
+
+// Adjoint of the rational schemes' matrices (wave_matfn): V = N^{-1}, N = I + alpha A + beta A^2, and P = 2V - I
+// (cayley), V (euler), I - c V A (pade), with (alpha, beta) = (c/2, 0), (c, 0), (c/2, c^2/12). V, GP and GV (GV may
+// be null) in LDS; dN = -V^T GV' V^T for the total cotangent GV' of V. Adds the direct dA terms to dAl (entry tid)
+// and returns the cotangent of c. W1, W2: 256 floats of LDS scratch each.
+__device__ float block_rational_adjoint(const LdsTable* sp, int scheme, float c, const float* V, const float* GP,
+                                        const float* GV, float* W1, float* W2, float* red, float& dAl, int tid) {
+  const int i = tid >> 4, j = tid & 15;
+  const float* A = sp[1];
+  float gv = GV ? GV[tid] : 0.0f, dc = 0.0f;
+  if (scheme == EWS_EXPM_CAYLEY) gv = fmaf(2.0f, GP[tid], gv);
+  else if (scheme == EWS_EXPM_EULER) gv += GP[tid];
+  else {  // pade: P = I - c V A
+    float gpa = 0.0f, vtg = 0.0f, va = 0.0f;
+#pragma unroll
+    for (int k = 0; k < 16; ++k) {
+      gpa = fmaf(GP[i * 16 + k], A[j * 16 + k], gpa);
+      vtg = fmaf(V[k * 16 + i], GP[k * 16 + j], vtg);
+      va = fmaf(V[i * 16 + k], A[k * 16 + j], va);
+    }
+    gv -= c * gpa;
+    dAl -= c * vtg;
+    dc -= GP[tid] * va;
+  }
+  W1[tid] = gv;
+  __syncthreads();
+  float xv = 0.0f;
+#pragma unroll
+  for (int k = 0; k < 16; ++k) xv = fmaf(V[k * 16 + i], W1[k * 16 + j], xv);  // V^T GV'
+  W2[tid] = xv;
+  __syncthreads();
+  float dN = 0.0f;
+#pragma unroll
+  for (int k = 0; k < 16; ++k) dN = fmaf(W2[i * 16 + k], V[j * 16 + k], dN);  // (V^T GV') V^T
+  dN = -dN;
+  const bool pade = scheme == EWS_EXPM_PADE;
+  const float alpha = scheme == EWS_EXPM_EULER ? c : 0.5f * c;
+  const float dalpha = scheme == EWS_EXPM_EULER ? 1.0f : 0.5f;
+  dAl = fmaf(alpha, dN, dAl);
+  dc = fmaf(dN, dalpha * A[tid] + (pade ? c * (1.0f / 6.0f) * 2.0f * sp[2][tid] : 0.0f), dc);
+  if (pade) {  // beta (dN A^T + A^T dN), beta = c^2 / 12
+    __syncthreads();
+    W1[tid] = dN;
+    __syncthreads();
+    float t2 = 0.0f;
+#pragma unroll
+    for (int k = 0; k < 16; ++k) {
+      t2 = fmaf(W1[i * 16 + k], A[j * 16 + k], t2);
+      t2 = fmaf(A[k * 16 + i], W1[k * 16 + j], t2);
+    }
+    dAl = fmaf(c * c * (1.0f / 12.0f), t2, dAl);
+  }
+  return block_sum(dc, red, tid);
+}
+
+// Adjoint of the interval's flow M = expm_scheme(-hf A) (chen_expm) for the workgroup, given its cotangent G in LDS
+// (overwritten); returns the cotangent of hf (zero for the identity flow). Scratch: Esq (SQMAX matrices), W1..W3
+// (256, 256, 256 + 32 floats).
+__device__ float block_flow_adjoint(const Args& a, const LdsTable* sp, float norm1, float hf, bool ident, float* G,
+                                   float (*Esq)[256], float* W1, float* W2, float* W3, float* red, float* H,
+                                   float& dAl, int tid) {
+  if (ident) return 0.0f;
+  if (a.chen_expm == EWS_EXPM_EXACT) return block_exp_adjoint(sp, norm1, hf, G, nullptr, Esq, Esq, red, H, tid);
+  if (a.chen_expm == EWS_EXPM_EULER) {  // M = I - hf A
+    dAl = fmaf(-hf, G[tid], dAl);
+    return block_sum(-G[tid] * sp[1][tid], red, tid);
+  }
+  if (tid < 64) wave_matfn(sp, norm1, a.chen_expm, hf, false, W1, W2, W3, tid);  // V (and P, unused) of the step
+  __syncthreads();
+  return block_rational_adjoint(sp, a.chen_expm, hf, W2, G, nullptr, W1, W3, red, dAl, tid);
+}
+
 template <int N>
 __global__ __launch_bounds__(256) void k_leaf_bwd(Args a, LeafBwd o) {
   constexpr int LW = lw_of(N);
@@ -1440,8 +1592,8 @@ __global__ __launch_bounds__(256) void k_leaf_bwd(Args a, LeafBwd o) {
   __shared__ __align__(16) float sp[HP][256];
   __shared__ __align__(16) float Lt[QN][16], G1[QN][16], BT[QN][16], dB[QN][16], dG1[QN][16], dBT[QN][16];
   __shared__ __align__(16) float dS3[N >= 3 ? 4096 : 4];
-  __shared__ __align__(16) float dS2[256], F[256], Gm[256], Esq[SQMAX][256];
-  __shared__ float dS1[16], yv[16], red[8];
+  __shared__ __align__(16) float dS2[256], F[256], Gm[256], Esq[SQMAX][256], W1[256], W2[256], W3[256 + 32];
+  __shared__ float dS1[16], red[8];
   const int tid = threadIdx.x, i = tid >> 4, j = tid & 15;
   const int q = a.q;
   for (int e = tid; e < HP * 256; e += 256) sp[e >> 8][e & 255] = a.apow[e];
@@ -1584,61 +1736,9 @@ __global__ __launch_bounds__(256) void k_leaf_bwd(Args a, LeafBwd o) {
       __syncthreads();
     }
     // ---- flow adjoint
-    float dhf = 0.0f;
     bool ident;
     const float hf = flow_step(a, th, t, ident);
-    if (!ident) {
-      int s = 0;
-      float x = fabsf(hf) * norm1;
-      while (x > 1.0f && s < SQMAX) {
-        x *= 0.5f;
-        ++s;
-      }
-      const float y = -hf * ldexpf(1.0f, -s);
-      float T = sp[PM][tid];
-#pragma unroll
-      for (int p = PM - 1; p >= 0; --p) T = fmaf(T, y, sp[p][tid]);
-      if (s > 0) Esq[0][tid] = T;
-      __syncthreads();
-      for (int r = 1; r < s; ++r) {
-        float e2 = 0.0f;
-#pragma unroll
-        for (int k = 0; k < 16; ++k) e2 = fmaf(Esq[r - 1][i * 16 + k], Esq[r - 1][k * 16 + j], e2);
-        Esq[r][tid] = e2;
-        __syncthreads();
-      }
-      for (int r = s - 1; r >= 0; --r) {  // G <- G E^T + E^T G
-        float g2 = 0.0f;
-#pragma unroll
-        for (int k = 0; k < 16; ++k) {
-          g2 = fmaf(Gm[i * 16 + k], Esq[r][j * 16 + k], g2);
-          g2 = fmaf(Esq[r][k * 16 + i], Gm[k * 16 + j], g2);
-        }
-        __syncthreads();
-        Gm[tid] = g2;
-        __syncthreads();
-      }
-      const float G0 = Gm[tid];
-      // H_p += (y^p / p!) G0;  dy = sum_p p y^{p-1} <G0, P_p>
-      float yp = 1.0f, fact = 1.0f;
-#pragma unroll
-      for (int p = 0; p < HP; ++p) {
-        if (p) fact *= (float)p;
-        H[p] = fmaf(yp / fact, G0, H[p]);
-        yp *= y;
-      }
-      float dy = 0.0f, ypm1 = 1.0f;  // y^{p-1}
-#pragma unroll
-      for (int p = 1; p < HP; ++p) {
-        dy = fmaf((float)p * ypm1, sp[p][tid] * G0, dy);
-        ypm1 *= y;
-      }
-#pragma unroll
-      for (int o2 = 1; o2 < 64; o2 <<= 1) dy += __shfl_xor(dy, o2, 64);
-      if ((tid & 63) == 0) red[tid >> 6] = dy;
-      __syncthreads();
-      dhf = -(red[0] + red[1] + red[2] + red[3]) * ldexpf(1.0f, -s);
-    }
+    const float dhf = block_flow_adjoint(a, sp, norm1, hf, ident, Gm, Esq, W1, W2, W3, red, H, dAl, tid);
     // ---- outputs
     if (tid < 16) o.dv[((size_t)b * a.n_int + t) * 16 + tid] = dB[0][tid];
     {
@@ -1656,6 +1756,218 @@ __global__ __launch_bounds__(256) void k_leaf_bwd(Args a, LeafBwd o) {
         o.dh[(size_t)b * a.n_int + t] = dl;
         if (!ident) atomicAdd(o.dsh + 2 * b, dhf);
       }
+    }
+    __syncthreads();
+  }
+  float* pb = o.part + (size_t)blockIdx.x * (HP + 1) * 256;
+#pragma unroll
+  for (int p = 0; p < HP; ++p) pb[p * 256 + tid] = H[p];
+  pb[HP * 256 + tid] = dAl;
+}
+
+// Van Loan leaf adjoint (one workgroup per interval, grid-stride). Recomputes the step matrices, the knot increments
+// Delta_m (Delta_{M-1} = V w, Delta_{m-1} = P Delta_m) and Pre_m, R_m, Y_m, X_m (see k_vl), then:
+//   level adjoints:  dDelta_m += dS1;  dY_m = dS2 Delta_m, dDelta_m += dS2^T Y_m;
+//     depth 3, with E = dS3 ._3 R_m, F = dS3 ._3 Delta_m, K = Y_m ._1 dS3, K' = X_m ._1 dS3:
+//     dY_m += E Delta_m, dX_m = F Delta_m / 2, dDelta_m += E^T Y_m + F^T X_m / 2 + K'^T Delta_m / 2,
+//     dR_m = K^T Delta_m;
+//   Y = Pre + Delta/2, X = Pre + Delta/3, Pre_m = sum_{j<m} Delta_j, R_m = sum_{j>m} Delta_j;
+//   chain: lambda_0 = dDelta_0, lambda_m = dDelta_m + P^T lambda_{m-1}, GP = sum_m lambda_{m-1} (x) Delta_m,
+//   GV = lambda_{M-1} (x) w, dw = V^T lambda_{M-1}, dv = dw / M;
+//   step matrices: block_exp_adjoint (exact) or block_rational_adjoint, for the step delta = h / M.
+// Then the flow's adjoint as in k_leaf_bwd.
+constexpr int VMAX = 64;  // knots per interval at most
+
+template <int N>
+__global__ __launch_bounds__(256) void k_vl_bwd(Args a, LeafBwd o) {
+  constexpr int LW = lw_of(N);
+  __shared__ __align__(16) float sp[HP][256];
+  __shared__ __align__(16) float Pm[256], Vm[256], W1[256], W2[256], W3[256 + 32], GPm[256], GVm[256], Gm[256];
+  __shared__ __align__(16) float Dl[VMAX][16], Rs[VMAX][16], Ys[VMAX][16], Xs[VMAX][16];
+  __shared__ __align__(16) float dD[VMAX][16], dP[VMAX][16], dR[VMAX][16];
+  __shared__ __align__(16) float dS3[N >= 3 ? 4096 : 4], dS2[256], EF[4][256], o5[5][16];
+  __shared__ __align__(16) float Esq[SQMAX][256], Fsq[SQMAX][256];
+  __shared__ float dS1[16], wv[16], lam[16], red[8];
+  const int tid = threadIdx.x, i = tid >> 4, j = tid & 15;
+  const int Mv = a.vm;
+  for (int e = tid; e < HP * 256; e += 256) sp[e >> 8][e & 255] = a.apow[e];
+  const float norm1 = a.apow[a.npow * 256];
+  float H[HP];
+#pragma unroll
+  for (int p = 0; p < HP; ++p) H[p] = 0.0f;
+  float dAl = 0.0f;
+  __syncthreads();
+  const long total = (long)a.B * a.n_int;
+  for (long it = blockIdx.x; it < total; it += gridDim.x) {
+    const int b = (int)(it / a.n_int), t = (int)(it - (long)b * a.n_int);
+    const float* th = a.clock + (size_t)b * a.L;
+    const float* drow = a.loc + ((size_t)b * a.n_int + t) * LW;
+    // ---- step matrices (delta = 0: the identity of the jump / basepoint interval)
+    bool fixed = false;  // P = V = I, no dependence on A or the clock
+    float delta;
+    if (a.vl_mode == EWS_FLOW_PER_INTERVAL) {
+      delta = (th[t + 1] - th[t]) / (float)Mv;
+      if (tid < 64) wave_matfn(sp, norm1, a.vl_expm, delta, false, Pm, Vm, W3, tid);
+    } else {
+      delta = vl_shared_step(a, th);
+      fixed = delta == 0.0f || (a.vl_mode == EWS_FLOW_CACHED_BASEPOINT && t == 0);
+      const float* mb = a.mats + (size_t)b * 768;
+      Pm[tid] = fixed ? (i == j ? 1.0f : 0.0f) : mb[tid];
+      Vm[tid] = fixed ? (i == j ? 1.0f : 0.0f) : mb[256 + tid];
+    }
+    if (tid < 16) {
+      const float* x = a.path + ((size_t)b * a.L + t) * a.d;
+      wv[tid] = tid < a.d ? (x[a.d + tid] - x[tid]) / (float)Mv : 0.0f;
+      dS1[tid] = drow[tid];
+    }
+    if constexpr (N >= 2) dS2[tid] = drow[16 + tid];
+    if constexpr (N >= 3) {
+      for (int e = tid; e < 4096; e += 256) dS3[e] = drow[272 + e];
+    }
+    Gm[tid] = a.fl[((size_t)b * a.n_int + t) * 256 + tid];  // dM_t
+    __syncthreads();
+    // ---- knot increments
+    {
+      float v = Vm[i * 16 + j] * wv[j];
+#pragma unroll
+      for (int o2 = 1; o2 < 16; o2 <<= 1) v += __shfl_xor(v, o2, 64);
+      if (j == 0) Dl[Mv - 1][i] = v;
+      __syncthreads();
+      for (int m = Mv - 1; m >= 1; --m) {
+        float u = Pm[i * 16 + j] * Dl[m][j];
+#pragma unroll
+        for (int o2 = 1; o2 < 16; o2 <<= 1) u += __shfl_xor(u, o2, 64);
+        if (j == 0) Dl[m - 1][i] = u;
+        __syncthreads();
+      }
+    }
+    if (tid < 16) {  // Pre, R, Y, X; level-1 cotangent; zero the other accumulators
+      float pre = 0.0f, suf = 0.0f;
+      for (int m = Mv - 1; m >= 0; --m) {
+        Rs[m][tid] = suf;
+        suf += Dl[m][tid];
+      }
+      for (int m = 0; m < Mv; ++m) {
+        const float dm = Dl[m][tid];
+        Ys[m][tid] = fmaf(0.5f, dm, pre);
+        Xs[m][tid] = fmaf(1.0f / 3.0f, dm, pre);
+        pre += dm;
+        dD[m][tid] = dS1[tid];
+        dP[m][tid] = 0.0f;
+        dR[m][tid] = 0.0f;
+      }
+    }
+    __syncthreads();
+    // ---- level adjoints
+    if constexpr (N >= 2) {
+      for (int e = tid; e < Mv * 16; e += 256) {  // dY_m = dS2 Delta_m;  dDelta_m += dS2^T Y_m
+        const int m = e >> 4, r = e & 15;
+        float y1 = 0.0f, y2 = 0.0f;
+#pragma unroll
+        for (int k = 0; k < 16; ++k) {
+          y1 = fmaf(dS2[r * 16 + k], Dl[m][k], y1);
+          y2 = fmaf(dS2[k * 16 + r], Ys[m][k], y2);
+        }
+        dP[m][r] += y1;
+        dD[m][r] += fmaf(0.5f, y1, y2);
+      }
+      __syncthreads();
+    }
+    if constexpr (N >= 3) {
+      for (int m = 0; m < Mv; ++m) {
+        {
+          float e1 = 0.0f, f1 = 0.0f, k1 = 0.0f, k2 = 0.0f;
+#pragma unroll
+          for (int k = 0; k < 16; ++k) {
+            const float s_ijk = dS3[tid * 16 + k];   // dS3[i][j][k]
+            e1 = fmaf(s_ijk, Rs[m][k], e1);
+            f1 = fmaf(s_ijk, Dl[m][k], f1);
+            const float s_kij = dS3[k * 256 + tid];  // dS3[k][i][j]
+            k1 = fmaf(Ys[m][k], s_kij, k1);
+            k2 = fmaf(Xs[m][k], s_kij, k2);
+          }
+          EF[0][tid] = e1;  // E[i][j]
+          EF[1][tid] = f1;  // F[i][j]
+          EF[2][tid] = k1;  // K[i][j]  (first index contracted with Y_m)
+          EF[3][tid] = k2;  // K'[i][j] (with X_m)
+        }
+        __syncthreads();
+        if (tid < 80) {
+          const int which = tid >> 4, r = tid & 15;
+          float v = 0.0f;
+#pragma unroll
+          for (int k = 0; k < 16; ++k) {
+            if (which == 0) v = fmaf(EF[0][r * 16 + k], Dl[m][k], v);                   // dY
+            else if (which == 1) v = fmaf(EF[1][r * 16 + k], Dl[m][k], v);              // 2 dX
+            else if (which == 2) v = fmaf(EF[0][k * 16 + r], Ys[m][k], fmaf(0.5f * EF[1][k * 16 + r], Xs[m][k], v));
+            else if (which == 3) v = fmaf(Dl[m][k], EF[2][k * 16 + r], v);              // dR
+            else v = fmaf(Dl[m][k], EF[3][k * 16 + r], v);                              // 2 x the K' term
+          }
+          o5[which][r] = v;
+        }
+        __syncthreads();
+        if (tid < 16) {
+          const float dY = o5[0][tid], dX = 0.5f * o5[1][tid];
+          dP[m][tid] += dY + dX;
+          dD[m][tid] += 0.5f * dY + dX * (1.0f / 3.0f) + o5[2][tid] + 0.5f * o5[4][tid];
+          dR[m][tid] += o5[3][tid];
+        }
+        __syncthreads();
+      }
+    }
+    // Y / X -> Pre (already folded: dP holds dPre), Pre and R -> Delta; then the chain
+    if (tid < 16) {
+      float acc = 0.0f;  // sum_{m > j} dPre_m
+      for (int m = Mv - 1; m >= 0; --m) {
+        dD[m][tid] += acc;
+        acc += dP[m][tid];
+      }
+      acc = 0.0f;  // sum_{m < j} dR_m
+      for (int m = 0; m < Mv; ++m) {
+        dD[m][tid] += acc;
+        acc += dR[m][tid];
+      }
+      lam[tid] = dD[0][tid];
+    }
+    __syncthreads();
+    float gp = 0.0f;
+    for (int m = 1; m < Mv; ++m) {
+      gp = fmaf(lam[i], Dl[m][j], gp);
+      float u = Pm[j * 16 + i] * lam[j];  // (P^T lambda)[i]
+#pragma unroll
+      for (int o2 = 1; o2 < 16; o2 <<= 1) u += __shfl_xor(u, o2, 64);
+      __syncthreads();
+      if (j == 0) lam[i] = dD[m][i] + u;
+      __syncthreads();
+    }
+    GPm[tid] = gp;
+    GVm[tid] = lam[i] * wv[j];
+    {
+      float u = Vm[j * 16 + i] * lam[j];  // (V^T lambda)[i]
+#pragma unroll
+      for (int o2 = 1; o2 < 16; o2 <<= 1) u += __shfl_xor(u, o2, 64);
+      if (j == 0) o.dv[((size_t)b * a.n_int + t) * 16 + i] = u / (float)Mv;
+    }
+    __syncthreads();
+    // ---- step matrices' adjoint
+    float ddelta = 0.0f;
+    if (!fixed) {
+      if (a.vl_expm == EWS_EXPM_EXACT)
+        ddelta = block_exp_adjoint(sp, norm1, delta, GPm, GVm, Esq, Fsq, red, H, tid);
+      else
+        ddelta = block_rational_adjoint(sp, a.vl_expm, delta, Vm, GPm, GVm, W1, W2, red, dAl, tid);
+    }
+    // ---- flow adjoint
+    bool ident;
+    const float hf = flow_step(a, th, t, ident);
+    const float dhf = block_flow_adjoint(a, sp, norm1, hf, ident, Gm, Esq, W1, W2, W3, red, H, dAl, tid);
+    if (tid == 0) {
+      float dh = 0.0f;
+      if (a.vl_mode == EWS_FLOW_PER_INTERVAL) dh += ddelta / (float)Mv;
+      else if (!fixed) atomicAdd(o.dsh + 2 * b + 1, ddelta / (float)Mv);
+      if (a.flow_mode == EWS_FLOW_PER_INTERVAL) dh += dhf;
+      else if (!ident) atomicAdd(o.dsh + 2 * b, dhf);
+      o.dh[(size_t)b * a.n_int + t] = dh;
     }
     __syncthreads();
   }
@@ -2226,7 +2538,6 @@ int ews_dense_backward(const ews_dense_desc* desc, const float* path, const floa
   const int rc = dense_plan(desc, p);
   if (rc != EWS_OK) return rc;
   if (!path || !clock || !A || !grad_out || !grad_path || !grad_A || !workspace) return EWS_ERR_NULL;
-  if (p.leaf != EWS_LEAF_SERIES || p.chen_expm != EWS_EXPM_EXACT) return EWS_ERR_OPTION;
   const Args a = dense_args(desc, p, path, clock, A, nullptr, workspace, true);
   hipStream_t st = (hipStream_t)stream;
   for (int pass = 0; pass <= 2; ++pass) {  // the forward up to the carries
@@ -2244,9 +2555,15 @@ int ews_dense_backward(const ews_dense_desc* desc, const float* path, const floa
   DENSE_CHECK();
   const long total = (long)p.B * p.n_int;
   const int grid = (int)(total < kLeafBwdBlocks ? total : kLeafBwdBlocks);
-  if (p.N == 1) hipLaunchKernelGGL((k_leaf_bwd<1>), dim3(grid), dim3(256), 0, st, a, o);
-  else if (p.N == 2) hipLaunchKernelGGL((k_leaf_bwd<2>), dim3(grid), dim3(256), 0, st, a, o);
-  else hipLaunchKernelGGL((k_leaf_bwd<3>), dim3(grid), dim3(256), 0, st, a, o);
+  if (p.leaf == EWS_LEAF_VAN_LOAN) {
+    if (p.N == 1) hipLaunchKernelGGL((k_vl_bwd<1>), dim3(grid), dim3(256), 0, st, a, o);
+    else if (p.N == 2) hipLaunchKernelGGL((k_vl_bwd<2>), dim3(grid), dim3(256), 0, st, a, o);
+    else hipLaunchKernelGGL((k_vl_bwd<3>), dim3(grid), dim3(256), 0, st, a, o);
+  } else {
+    if (p.N == 1) hipLaunchKernelGGL((k_leaf_bwd<1>), dim3(grid), dim3(256), 0, st, a, o);
+    else if (p.N == 2) hipLaunchKernelGGL((k_leaf_bwd<2>), dim3(grid), dim3(256), 0, st, a, o);
+    else hipLaunchKernelGGL((k_leaf_bwd<3>), dim3(grid), dim3(256), 0, st, a, o);
+  }
   DENSE_CHECK();
   hipLaunchKernelGGL(k_part_reduce, dim3(HP + 1), dim3(256), 0, st, o.part, grid, hsum);
   DENSE_CHECK();

@@ -146,9 +146,8 @@ def _check_dense(path, clock, A):
 
 class DenseScan(torch.autograd.Function):
     """out = EWS readout of (path, clock) under a dense generator A (series leaf of order q or the Van Loan leaf,
-    flows of chen_expm). The backward (ews_dense_backward: the combine's adjoint scans, then the leaf's and the flows'
-    adjoints) covers the series leaf with exact flows; for the other leaves and schemes it raises instead of falling
-    back to another engine."""
+    flows of chen_expm). The backward is ews_dense_backward: the combine's adjoint scans, then the leaf's and the
+    flows' adjoints per interval and one reduction for dA."""
 
     @staticmethod
     def forward(ctx, path, clock, A, N, q, flow_mode, readout, level0, chunk, leaf):
@@ -173,11 +172,6 @@ class DenseScan(torch.autograd.Function):
 
     @staticmethod
     def backward(ctx, gout):
-        leaf = ctx.leaf
-        if leaf.kind != "series" or leaf.chen_expm != "exact":
-            raise NotImplementedError(
-                "the dense-generator backward covers the series leaf with exact flows (chen_expm='exact'); "
-                f"got leaf={leaf.kind!r}, chen_expm={leaf.chen_expm!r}")
         lib = nat.load()
         path, clock, A = ctx.saved_tensors
         desc = ctx.desc

@@ -167,10 +167,10 @@ size_t ews_dense_backward_workspace_bytes(const ews_dense_desc* desc);
 /* Backward of ews_dense_forward: given the cotangent grad_out of out, writes grad_path (B, L, d), grad_clock (B, L)
  * (may be NULL) and grad_A (d, d). Recomputes the forward up to the chunk carries, runs the combine's adjoint (as
  * ews_dense_combine_backward), then the leaf's and the flows' adjoints per interval and one reduction for grad_A.
- * Replaces JAX autodiff through series_local_signatures (ews/core/series_leaf.py:72-126) and
- * _chen_M_per_interval (ews/core/chen_scan.py:155-168) around the dense kernel's custom VJP
- * (ews/core/kernels/pallas_combine.py:2360-2565). Covers the series leaf with exact flows; other leaves and flow
- * schemes return EWS_ERR_OPTION. */
+ * Replaces JAX autodiff through the leaf (series_local_signatures, ews/core/series_leaf.py:72-126, or
+ * reweighted_segments_van_loan + the knot signatures, ews/core/van_loan.py:31-160 and ews/core/signature.py:20-35)
+ * and _chen_M_per_interval (ews/core/chen_scan.py:155-168, every chen_expm scheme) around the dense kernel's custom
+ * VJP (ews/core/kernels/pallas_combine.py:2360-2565). */
 int ews_dense_backward(const ews_dense_desc* desc, const float* path, const float* clock, const float* A,
                        const float* grad_out, float* grad_path, float* grad_clock, float* grad_A, void* workspace,
                        ews_stream_t stream);

@@ -148,3 +148,68 @@ def test_dense_backward_large_steps_and_no_clock_grad():
     got2, _ = _grads(path, clock, A, 3, 24, "terminal", "displacement", clock_grad=False)
     assert got2[1] is None
     assert relerr(got2[0], ref[0]) < 1e-4 and relerr(got2[2], ref[2]) < 1e-4
+
+
+def _grads_kw(path, clock, A, N, readout, mode, leaf_kw, level0=True, seed=5):
+    """(GPU grads, float64 autograd grads of the oracle) for (path, clock, A) under the leaf options leaf_kw."""
+    p64, c64, A64 = (x.clone().requires_grad_(True) for x in (path, clock, A))
+    ref_out = O.ews(p64, c64, A64, N, readout, reweighting_mode=mode, terminal_reduce="assoc", **leaf_kw)
+    gout = torch.tensor(np.random.default_rng(seed).normal(size=ref_out.shape))
+    ref = torch.autograd.grad(ref_out, (p64, c64, A64), gout)
+    pg, cg, Ag = (x.float().to(DEV).requires_grad_(True) for x in (path, clock, A))
+    kind = leaf_kw.get("leaf", "van_loan")
+    leaf = ops.DenseLeaf(kind, q=leaf_kw.get("series_q", 0), M=leaf_kw.get("M", 20),
+                         van_loan_expm=leaf_kw.get("van_loan_expm", "cayley"), reweighting_mode=mode,
+                         chen_expm=leaf_kw.get("chen_expm", "exact"))
+    out = ops.dense_scan(pg, cg, Ag, N, leaf.q, _FLOW[mode], readout, level0, leaf=leaf)
+    got = torch.autograd.grad(out, (pg, cg, Ag), gout.float().to(DEV))
+    return got, ref
+
+
+@pytest.mark.parametrize("scheme", ["exact", "cayley", "euler", "pade"])
+@pytest.mark.parametrize("N", [1, 2, 3])
+def test_dense_backward_van_loan(scheme, N):
+    path, clock, A = _random(2, 30, 16 if N < 3 else 6, seed=900 + N)
+    got, ref = _grads_kw(path, clock, A, N, "prefix", "displacement",
+                         dict(leaf="van_loan", M=7, van_loan_expm=scheme))
+    errs = [relerr(g, r) for g, r in zip(got, ref)]
+    print(f"dense bwd van loan {scheme} N={N}: path {errs[0]:.2e} clock {errs[1]:.2e} A {errs[2]:.2e}")
+    assert max(errs) < 1e-4
+
+
+@pytest.mark.parametrize("mode", ["displacement_uniform", "displacement_uniform_basepoint"])
+@pytest.mark.parametrize("scheme", ["exact", "cayley"])
+def test_dense_backward_van_loan_uniform(mode, scheme):
+    path, clock, A = _random(2, 40, 8, seed=910, uniform=True)
+    got, ref = _grads_kw(path, clock, A, 3, "terminal", mode, dict(leaf="van_loan", M=20, van_loan_expm=scheme))
+    errs = [relerr(g, r) for g, r in zip(got, ref)]
+    print(f"dense bwd van loan {scheme} {mode}: path {errs[0]:.2e} clock {errs[1]:.2e} A {errs[2]:.2e}")
+    assert max(errs) < 1e-4
+
+
+def test_dense_backward_van_loan_large_steps():
+    """delta ||A||_1 above the series radii: Gauss-Jordan step matrices and scaled exponentials (their doublings)."""
+    path, clock, A = _random(2, 20, 8, seed=920, hscale=3.0, ascale=0.4)
+    for scheme in ("exact", "cayley", "pade", "euler"):
+        got, ref = _grads_kw(path, clock, A, 2, "terminal", "displacement",
+                             dict(leaf="van_loan", M=2, van_loan_expm=scheme))
+        errs = [relerr(g, r) for g, r in zip(got, ref)]
+        print(f"dense bwd van loan large {scheme}: path {errs[0]:.2e} clock {errs[1]:.2e} A {errs[2]:.2e}")
+        assert max(errs) < 1e-4, scheme
+
+
+@pytest.mark.parametrize("chen", ["cayley", "pade", "euler"])
+@pytest.mark.parametrize("flow_mode", ["displacement", "displacement_uniform"])
+def test_dense_backward_flow_schemes(chen, flow_mode):
+    path, clock, A = _random(2, 30, 8, seed=930, hscale=0.2, uniform=flow_mode != "displacement")
+    got, ref = _grads_kw(path, clock, A, 2, "prefix", flow_mode, dict(leaf="series", series_q=12, chen_expm=chen))
+    errs = [relerr(g, r) for g, r in zip(got, ref)]
+    print(f"dense bwd flows {chen} {flow_mode}: path {errs[0]:.2e} clock {errs[1]:.2e} A {errs[2]:.2e}")
+    assert max(errs) < 1e-4
+    # larger steps: the Gauss-Jordan inverse instead of the series
+    path, clock, A = _random(2, 12, 8, seed=931, hscale=1.5, ascale=0.5)
+    got, ref = _grads_kw(path, clock, A, 2, "terminal", "displacement",
+                         dict(leaf="series", series_q=30, chen_expm=chen))
+    errs = [relerr(g, r) for g, r in zip(got, ref)]
+    print(f"dense bwd flows large {chen}: path {errs[0]:.2e} clock {errs[1]:.2e} A {errs[2]:.2e}")
+    assert max(errs) < 1e-4
