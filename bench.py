@@ -107,6 +107,15 @@ def bench_c3(args):
     out = torch.empty((B, L - 1, W), device=dev, dtype=torch.float32)
     npass = lib.ews_dense_num_passes()
 
+    bwd = args.backward
+    if bwd:
+        gout = torch.randn((B, L - 1, W), device=dev, dtype=torch.float32)
+        gpath = torch.empty_like(path)
+        gclock = torch.empty_like(clock)
+        gA = torch.empty_like(A)
+        wsb = torch.empty(int(lib.ews_dense_backward_workspace_bytes(ctypes.byref(desc))), device=dev,
+                          dtype=torch.uint8)
+
     def step(events=None):
         stream = ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream)
         for p in range(npass):
@@ -117,6 +126,12 @@ def bench_c3(args):
                       "dense forward pass")
         if events is not None:
             events[npass].record()
+        if bwd:
+            nat.check(lib.ews_dense_backward(ctypes.byref(desc), path.data_ptr(), clock.data_ptr(), A.data_ptr(),
+                                             gout.data_ptr(), gpath.data_ptr(), gclock.data_ptr(), gA.data_ptr(),
+                                             wsb.data_ptr(), stream), "dense backward")
+            if events is not None:
+                events[npass + 1].record()
 
     for _ in range(args.warmup):
         step()
@@ -125,19 +140,22 @@ def bench_c3(args):
     start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     start.record()
     for _ in range(args.steps):
-        evs = [torch.cuda.Event(enable_timing=True) for _ in range(npass + 1)]
+        evs = [torch.cuda.Event(enable_timing=True) for _ in range(npass + 2)]
         step(evs)
         evs_all.append(evs)
     end.record()
     torch.cuda.synchronize()
     ms = start.elapsed_time(end) / args.steps
     names = ["local_terms", "chunk_summary", "carry_scan", "chunk_output"]
+    if bwd:
+        names.append("backward")
     pass_ms = {nm: sum(e[i].elapsed_time(e[i + 1]) for e in evs_all) / args.steps for i, nm in enumerate(names)}
     n = B * (L - 1)
     flops = n * C3_CHEN_FLOPS
     tf = flops / (pass_ms["chunk_output"] * 1e-3) / 1e12
     rec = {
-        "metric": "EWS dense-generator forward time-steps/sec and fp32 MFMA TFLOP/s (% peak) on 1 MI355X",
+        "metric": "EWS dense-generator " + ("forward+backward" if bwd else "forward")
+                  + " time-steps/sec and fp32 MFMA TFLOP/s (% peak) on 1 MI355X",
         "value": round(n / (ms * 1e-3), 1),
         "unit": "time-steps/s",
         "n_gpus": 1,
@@ -151,7 +169,9 @@ def bench_c3(args):
         "data": "synthetic",
         "config": {"workload": "c3: dense generator, B=16, L=4096, d=16, depth 3, "
                                + ("Van Loan leaf M=20 (cayley, the reference defaults)" if vl else "series leaf q=24")
-                               + ", input-dependent clock, prefix readout, forward", "global_batch": B, "seq_len": L,
+                               + ", input-dependent clock, prefix readout, "
+                               + ("forward + backward (gradients of path, clock and A)" if bwd else "forward"),
+                   "global_batch": B, "seq_len": L,
                    "parallelism": "none (1 GPU)"},
         "roofline": {"bound": "mfma", "kernel": "chunk_output", "achieved": round(tf, 2),
                      "peak": MFMA_F32_PEAK_TFLOPS, "unit": "TFLOP/s", "frac": round(tf / MFMA_F32_PEAK_TFLOPS, 4),
@@ -226,6 +246,7 @@ def main():
     ap.add_argument("--chunk", type=int, default=0, help="intervals per chunk (0: the library's default)")
     ap.add_argument("--config", choices=["c2", "c3"], default="c2",
                     help="c2 (default, the headline): planes fwd+bwd; c3: dense-generator depth-3 forward")
+    ap.add_argument("--backward", action="store_true", help="c3: time forward + backward (ews_dense_backward)")
     ap.add_argument("--leaf", choices=["series", "van_loan"], default="series",
                     help="leaf of the c3 forward: series (q=24) or Van Loan (M=20, cayley)")
     ap.add_argument("--clock-grad", action="store_true",
