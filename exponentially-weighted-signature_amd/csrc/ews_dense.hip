@@ -72,6 +72,7 @@ struct Args {
   float* lloc;
   float* lam;
   int* amax;
+  float* vlsave;  // backward's recompute: per interval the Van Loan P, V and knot increments (null otherwise)
 };
 
 // One scan over rows of (levels, flows): chunks of T rows, per-sample strides in floats.
@@ -801,6 +802,11 @@ __global__ __launch_bounds__(256) void k_vl(Args a) {
       pr[q] = *reinterpret_cast<const f4*>(P + c16 * 16 + 4 * q);
       vr[q] = *reinterpret_cast<const f4*>(V + c16 * 16 + 4 * q);
     }
+    float* sv = a.vlsave ? a.vlsave + ((size_t)b * a.n_int + t) * (512 + 16 * Mv) : nullptr;
+    if (sv) {
+      *reinterpret_cast<f4*>(sv + 4 * l) = *reinterpret_cast<const f4*>(P + 4 * l);
+      *reinterpret_cast<f4*>(sv + 256 + 4 * l) = *reinterpret_cast<const f4*>(V + 4 * l);
+    }
     // w = v / M
     if (l < 16) {
       const float* x = a.path + ((size_t)b * a.L + t) * a.d;
@@ -818,6 +824,7 @@ __global__ __launch_bounds__(256) void k_vl(Args a) {
     float suf = 0.0f;
     for (int m = Mv - 1;; --m) {
       if (g == 0) *reinterpret_cast<float2*>(E + m * EP + 4 * c16) = float2{dl, suf};
+      if (sv && g == 1) sv[512 + m * 16 + c16] = dl;
       suf += dl;
       if (m == 0) break;
       if (g == 0) xs[c16] = dl;
@@ -1765,15 +1772,17 @@ __global__ __launch_bounds__(256) void k_leaf_bwd(Args a, LeafBwd o) {
   pb[HP * 256 + tid] = dAl;
 }
 
-// Van Loan leaf adjoint (one workgroup per interval, grid-stride). Recomputes the step matrices, the knot increments
-// Delta_m (Delta_{M-1} = V w, Delta_{m-1} = P Delta_m) and Pre_m, R_m, Y_m, X_m (see k_vl), then:
+// Van Loan leaf adjoint (one workgroup per interval, grid-stride). The forward's recompute saved per interval the
+// step matrices P, V and the knot increments Delta_m (Delta_{M-1} = V w, Delta_{m-1} = P Delta_m); from them
+// Pre_m, R_m, Y_m, X_m (see k_vl), then:
 //   level adjoints:  dDelta_m += dS1;  dY_m = dS2 Delta_m, dDelta_m += dS2^T Y_m;
-//     depth 3, with E = dS3 ._3 R_m, F = dS3 ._3 Delta_m, K = Y_m ._1 dS3, K' = X_m ._1 dS3:
-//     dY_m += E Delta_m, dX_m = F Delta_m / 2, dDelta_m += E^T Y_m + F^T X_m / 2 + K'^T Delta_m / 2,
-//     dR_m = K^T Delta_m;
+//     depth 3 (S3 = sum_m Delta_m[b] G_m[a][c], G_m = Y_m (x) R_m + X_m (x) Delta_m / 2), with
+//     Q_m = dS3 ._2 Delta_m:  dY_m += Q_m R_m,  dX_m = Q_m Delta_m / 2,  dR_m = Q_m^T Y_m,
+//     dDelta_m += Q_m^T X_m / 2 (last index) and dDelta_m[b] += <dS3[:, b, :], G_m> (middle index);
+//     each thread keeps its column dS3[a][:][c] and its row dS3[a][b][:] in registers across the segments;
 //   Y = Pre + Delta/2, X = Pre + Delta/3, Pre_m = sum_{j<m} Delta_j, R_m = sum_{j>m} Delta_j;
-//   chain: lambda_0 = dDelta_0, lambda_m = dDelta_m + P^T lambda_{m-1}, GP = sum_m lambda_{m-1} (x) Delta_m,
-//   GV = lambda_{M-1} (x) w, dw = V^T lambda_{M-1}, dv = dw / M;
+//   chain (one wavefront): lambda_0 = dDelta_0, lambda_m = dDelta_m + P^T lambda_{m-1},
+//   GP = sum_m lambda_{m-1} (x) Delta_m, GV = lambda_{M-1} (x) w, dw = V^T lambda_{M-1}, dv = dw / M;
 //   step matrices: block_exp_adjoint (exact) or block_rational_adjoint, for the step delta = h / M.
 // Then the flow's adjoint as in k_leaf_bwd.
 constexpr int VMAX = 64;  // knots per interval at most
@@ -1785,11 +1794,11 @@ __global__ __launch_bounds__(256) void k_vl_bwd(Args a, LeafBwd o) {
   __shared__ __align__(16) float Pm[256], Vm[256], W1[256], W2[256], W3[256 + 32], GPm[256], GVm[256], Gm[256];
   __shared__ __align__(16) float Dl[VMAX][16], Rs[VMAX][16], Ys[VMAX][16], Xs[VMAX][16];
   __shared__ __align__(16) float dD[VMAX][16], dP[VMAX][16], dR[VMAX][16];
-  __shared__ __align__(16) float dS3[N >= 3 ? 4096 : 4], dS2[256], EF[4][256], o5[5][16];
+  __shared__ __align__(16) float dS3[N >= 3 ? 4096 : 4], dS2[256];
   __shared__ __align__(16) float Esq[SQMAX][256], Fsq[SQMAX][256];
-  __shared__ float dS1[16], wv[16], lam[16], red[8];
-  const int tid = threadIdx.x, i = tid >> 4, j = tid & 15;
-  const int Mv = a.vm;
+  __shared__ __align__(16) float dS1[16], wv[16], lam[16], red[8];
+  const int tid = threadIdx.x, i = tid >> 4, j = tid & 15, l = tid & 63, g = l >> 4, c16 = l & 15;
+  const int Mv = a.vm, vs = 512 + 16 * Mv;
   for (int e = tid; e < HP * 256; e += 256) sp[e >> 8][e & 255] = a.apow[e];
   const float norm1 = a.apow[a.npow * 256];
   float H[HP];
@@ -1802,19 +1811,19 @@ __global__ __launch_bounds__(256) void k_vl_bwd(Args a, LeafBwd o) {
     const int b = (int)(it / a.n_int), t = (int)(it - (long)b * a.n_int);
     const float* th = a.clock + (size_t)b * a.L;
     const float* drow = a.loc + ((size_t)b * a.n_int + t) * LW;
-    // ---- step matrices (delta = 0: the identity of the jump / basepoint interval)
+    const float* sv = a.vlsave + ((size_t)b * a.n_int + t) * vs;
+    // ---- saved step matrices and increments (delta = 0: the identity of the jump / basepoint interval)
     bool fixed = false;  // P = V = I, no dependence on A or the clock
     float delta;
     if (a.vl_mode == EWS_FLOW_PER_INTERVAL) {
       delta = (th[t + 1] - th[t]) / (float)Mv;
-      if (tid < 64) wave_matfn(sp, norm1, a.vl_expm, delta, false, Pm, Vm, W3, tid);
     } else {
       delta = vl_shared_step(a, th);
       fixed = delta == 0.0f || (a.vl_mode == EWS_FLOW_CACHED_BASEPOINT && t == 0);
-      const float* mb = a.mats + (size_t)b * 768;
-      Pm[tid] = fixed ? (i == j ? 1.0f : 0.0f) : mb[tid];
-      Vm[tid] = fixed ? (i == j ? 1.0f : 0.0f) : mb[256 + tid];
     }
+    Pm[tid] = sv[tid];
+    Vm[tid] = sv[256 + tid];
+    for (int e = tid; e < Mv * 16; e += 256) Dl[e >> 4][e & 15] = sv[512 + e];
     if (tid < 16) {
       const float* x = a.path + ((size_t)b * a.L + t) * a.d;
       wv[tid] = tid < a.d ? (x[a.d + tid] - x[tid]) / (float)Mv : 0.0f;
@@ -1826,21 +1835,6 @@ __global__ __launch_bounds__(256) void k_vl_bwd(Args a, LeafBwd o) {
     }
     Gm[tid] = a.fl[((size_t)b * a.n_int + t) * 256 + tid];  // dM_t
     __syncthreads();
-    // ---- knot increments
-    {
-      float v = Vm[i * 16 + j] * wv[j];
-#pragma unroll
-      for (int o2 = 1; o2 < 16; o2 <<= 1) v += __shfl_xor(v, o2, 64);
-      if (j == 0) Dl[Mv - 1][i] = v;
-      __syncthreads();
-      for (int m = Mv - 1; m >= 1; --m) {
-        float u = Pm[i * 16 + j] * Dl[m][j];
-#pragma unroll
-        for (int o2 = 1; o2 < 16; o2 <<= 1) u += __shfl_xor(u, o2, 64);
-        if (j == 0) Dl[m - 1][i] = u;
-        __syncthreads();
-      }
-    }
     if (tid < 16) {  // Pre, R, Y, X; level-1 cotangent; zero the other accumulators
       float pre = 0.0f, suf = 0.0f;
       for (int m = Mv - 1; m >= 0; --m) {
@@ -1874,48 +1868,48 @@ __global__ __launch_bounds__(256) void k_vl_bwd(Args a, LeafBwd o) {
       __syncthreads();
     }
     if constexpr (N >= 3) {
-      for (int m = 0; m < Mv; ++m) {
-        {
-          float e1 = 0.0f, f1 = 0.0f, k1 = 0.0f, k2 = 0.0f;
+      float colb[16], rowc[16];  // dS3[i][.][j] and dS3[i][j][.]
 #pragma unroll
-          for (int k = 0; k < 16; ++k) {
-            const float s_ijk = dS3[tid * 16 + k];   // dS3[i][j][k]
-            e1 = fmaf(s_ijk, Rs[m][k], e1);
-            f1 = fmaf(s_ijk, Dl[m][k], f1);
-            const float s_kij = dS3[k * 256 + tid];  // dS3[k][i][j]
-            k1 = fmaf(Ys[m][k], s_kij, k1);
-            k2 = fmaf(Xs[m][k], s_kij, k2);
-          }
-          EF[0][tid] = e1;  // E[i][j]
-          EF[1][tid] = f1;  // F[i][j]
-          EF[2][tid] = k1;  // K[i][j]  (first index contracted with Y_m)
-          EF[3][tid] = k2;  // K'[i][j] (with X_m)
-        }
-        __syncthreads();
-        if (tid < 80) {
-          const int which = tid >> 4, r = tid & 15;
-          float v = 0.0f;
-#pragma unroll
-          for (int k = 0; k < 16; ++k) {
-            if (which == 0) v = fmaf(EF[0][r * 16 + k], Dl[m][k], v);                   // dY
-            else if (which == 1) v = fmaf(EF[1][r * 16 + k], Dl[m][k], v);              // 2 dX
-            else if (which == 2) v = fmaf(EF[0][k * 16 + r], Ys[m][k], fmaf(0.5f * EF[1][k * 16 + r], Xs[m][k], v));
-            else if (which == 3) v = fmaf(Dl[m][k], EF[2][k * 16 + r], v);              // dR
-            else v = fmaf(Dl[m][k], EF[3][k * 16 + r], v);                              // 2 x the K' term
-          }
-          o5[which][r] = v;
-        }
-        __syncthreads();
-        if (tid < 16) {
-          const float dY = o5[0][tid], dX = 0.5f * o5[1][tid];
-          dP[m][tid] += dY + dX;
-          dD[m][tid] += 0.5f * dY + dX * (1.0f / 3.0f) + o5[2][tid] + 0.5f * o5[4][tid];
-          dR[m][tid] += o5[3][tid];
-        }
-        __syncthreads();
+      for (int k = 0; k < 16; ++k) {
+        colb[k] = dS3[i * 256 + k * 16 + j];
+        rowc[k] = dS3[i * 256 + j * 16 + ((k + j) & 15)];  // skewed: conflict-free across the 16 lanes
       }
+      for (int m = 0; m < Mv; ++m) {
+        float q = 0.0f, e1 = 0.0f, f1 = 0.0f;
+#pragma unroll
+        for (int k = 0; k < 16; ++k) {
+          q = fmaf(colb[k], Dl[m][k], q);
+          const int kk = (k + j) & 15;
+          e1 = fmaf(rowc[k], Rs[m][kk], e1);
+          f1 = fmaf(rowc[k], Dl[m][kk], f1);
+        }
+        const float yi = Ys[m][i], xi = Xs[m][i];
+        // over the last index (lanes j of a row i): dY_m[i], dX_m[i]
+        float py = q * Rs[m][j], px = 0.5f * q * Dl[m][j];
+#pragma unroll
+        for (int o2 = 1; o2 < 16; o2 <<= 1) {
+          py += __shfl_xor(py, o2, 64);
+          px += __shfl_xor(px, o2, 64);
+        }
+        // over the first index (rows i of the wave, then atomics across waves): dR_m[j], dDelta_m[j]
+        float pr2 = q * yi, pd = fmaf(0.5f * q, xi, fmaf(yi, e1, 0.5f * xi * f1));
+#pragma unroll
+        for (int o2 = 16; o2 < 64; o2 <<= 1) {
+          pr2 += __shfl_xor(pr2, o2, 64);
+          pd += __shfl_xor(pd, o2, 64);
+        }
+        if (j == 0) {
+          atomicAdd(&dP[m][i], py + px);
+          atomicAdd(&dD[m][i], fmaf(0.5f, py, px * (1.0f / 3.0f)));
+        }
+        if (l < 16) {
+          atomicAdd(&dR[m][j], pr2);
+          atomicAdd(&dD[m][j], pd);
+        }
+      }
+      __syncthreads();
     }
-    // Y / X -> Pre (already folded: dP holds dPre), Pre and R -> Delta; then the chain
+    // Pre and R -> Delta (dP holds dPre)
     if (tid < 16) {
       float acc = 0.0f;  // sum_{m > j} dPre_m
       for (int m = Mv - 1; m >= 0; --m) {
@@ -1930,17 +1924,29 @@ __global__ __launch_bounds__(256) void k_vl_bwd(Args a, LeafBwd o) {
       lam[tid] = dD[0][tid];
     }
     __syncthreads();
-    float gp = 0.0f;
-    for (int m = 1; m < Mv; ++m) {
-      gp = fmaf(lam[i], Dl[m][j], gp);
-      float u = Pm[j * 16 + i] * lam[j];  // (P^T lambda)[i]
+    // ---- the chain in reverse, one wavefront
+    if (tid < 64) {
+      f4 pc;  // P[4g + r][c16]
 #pragma unroll
-      for (int o2 = 1; o2 < 16; o2 <<= 1) u += __shfl_xor(u, o2, 64);
-      __syncthreads();
-      if (j == 0) lam[i] = dD[m][i] + u;
-      __syncthreads();
+      for (int r = 0; r < 4; ++r) pc[r] = Pm[(4 * g + r) * 16 + c16];
+      const int gi = l >> 2, gj = 4 * (l & 3);
+      f4 gp = {0.0f, 0.0f, 0.0f, 0.0f};
+      for (int m = 1; m < Mv; ++m) {
+        const f4 lv = *reinterpret_cast<const f4*>(lam + 4 * g);
+        const float li = lam[gi];
+        const f4 dm = *reinterpret_cast<const f4*>(&Dl[m][gj]);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) gp[r] = fmaf(li, dm[r], gp[r]);
+        float u = fmaf(pc.x, lv.x, fmaf(pc.y, lv.y, fmaf(pc.z, lv.z, pc.w * lv.w)));
+        u += __shfl_xor(u, 16, 64);
+        u += __shfl_xor(u, 32, 64);
+        wave_order_d();
+        if (g == 0) lam[c16] = dD[m][c16] + u;
+        wave_order_d();
+      }
+      *reinterpret_cast<f4*>(GPm + 4 * l) = gp;
     }
-    GPm[tid] = gp;
+    __syncthreads();
     GVm[tid] = lam[i] * wv[j];
     {
       float u = Vm[j * 16 + i] * lam[j];  // (V^T lambda)[i]
@@ -2197,7 +2203,7 @@ int dense_plan(const ews_dense_desc* s, DPlan& p) {
 constexpr int kLeafBwdBlocks = 1024;  // workgroups of the leaf adjoint (one partial dA set each)
 
 struct DWs {
-  size_t apow, loc, fl, summ, sfl, car, pre, mats, lloc, lam, amax, dv, dh, dsh, part, hsum, total;
+  size_t apow, loc, fl, summ, sfl, car, pre, mats, lloc, lam, amax, dv, dh, dsh, part, hsum, vlsave, total;
 };
 // bwd: the backward's layout, the forward's buffers (prefix rows always) followed by the adjoint scan's
 DWs dense_ws(const DPlan& p, int readout, bool bwd = false) {
@@ -2223,6 +2229,7 @@ DWs dense_ws(const DPlan& p, int readout, bool bwd = false) {
     w.dsh = off; off += al256((size_t)p.B * 2 * 4);
     w.part = off; off += al256((size_t)kLeafBwdBlocks * (HP + 1) * 256 * 4);
     w.hsum = off; off += al256((size_t)(HP + 1) * 256 * 8);
+    w.vlsave = off; off += p.leaf == EWS_LEAF_VAN_LOAN ? al256(BN * (512 + 16 * (size_t)p.vm) * 4) : 0;
   }
   w.total = off;
   return w;
@@ -2243,6 +2250,7 @@ Args dense_args(const ews_dense_desc* s, const DPlan& p, const float* path, cons
   a.pre = (float*)(ws + w.pre); a.mats = (float*)(ws + w.mats);
   if (bwd) {
     a.lloc = (float*)(ws + w.lloc); a.lam = (float*)(ws + w.lam); a.amax = (int*)(ws + w.amax);
+    a.vlsave = p.leaf == EWS_LEAF_VAN_LOAN ? (float*)(ws + w.vlsave) : nullptr;
   }
   return a;
 }
