@@ -1440,6 +1440,9 @@ struct LeafBwd {
   float* part;  // (gridDim.x, HP + 1, 256): per-workgroup H_0..H_PM and the direct dA terms
 };
 
+// 1/n for a small positive integer n, by the hardware reciprocal (within 1 ulp; the adjoints' rounding budget)
+__device__ __forceinline__ float frcp(int n) { return __builtin_amdgcn_rcpf((float)n); }
+
 // workgroup sum (256 threads) of one value per thread; red: 4 floats of LDS. Every thread gets the sum.
 __device__ __forceinline__ float block_sum(float v, float* red, int tid) {
 #pragma unroll
@@ -1506,12 +1509,12 @@ __device__ float block_exp_adjoint(const LdsTable* sp, float norm1, float c, flo
     __syncthreads();
   }
   const float g0 = GE[tid], p0 = GPhi ? GPhi[tid] : 0.0f;
-  float yp = 1.0f, fact = 1.0f, dy = 0.0f, ypm1 = 1.0f;
+  float yp = 1.0f, ifact = 1.0f, dy = 0.0f, ypm1 = 1.0f;  // ifact = 1/p! (compile-time constants)
 #pragma unroll
   for (int p = 0; p < HP; ++p) {
-    if (p) fact *= (float)p;
+    if (p) ifact *= 1.0f / (float)p;
     const float gsum = g0 + p0 * (1.0f / (float)(p + 1));
-    H[p] = fmaf(yp / fact, gsum, H[p]);
+    H[p] = fmaf(yp * ifact, gsum, H[p]);
     if (p) {
       dy = fmaf((float)p * ypm1 * sp[p][tid], gsum, dy);
       ypm1 *= y;
@@ -1639,19 +1642,19 @@ __global__ __launch_bounds__(256) void k_leaf_bwd(Args a, LeafBwd o) {
       float v = Aij * Lt[p - 1][j];
 #pragma unroll
       for (int o2 = 1; o2 < 16; o2 <<= 1) v += __shfl_xor(v, o2, 64);
-      if (j == 0) Lt[p][i] = v * (-h / (float)p);
+      if (j == 0) Lt[p][i] = v * (-h * frcp(p));
       __syncthreads();
     }
     for (int e = tid; e < (q + 1) * 16; e += 256) {
       const int n = e >> 4, r = e & 15;
-      G1[n][r] = Lt[n][r] / (float)(n + 1);
+      G1[n][r] = Lt[n][r] * frcp(n + 1);
       dG1[n][r] = dS1[r];
     }
     if constexpr (N >= 2) {
       for (int e = tid; e < (q + 1) * 16; e += 256) {
         const int n = e >> 4, r = e & 15;
         float sacc = 0.0f;
-        for (int p = 0; p + n <= q; ++p) sacc += Lt[p][r] / (float)(p + n + N);
+        for (int p = 0; p + n <= q; ++p) sacc = fmaf(Lt[p][r], frcp(p + n + N), sacc);
         BT[n][r] = sacc;
       }
     }
@@ -1683,7 +1686,7 @@ __global__ __launch_bounds__(256) void k_leaf_bwd(Args a, LeafBwd o) {
         }
         __syncthreads();
         // pairs (p, n = NN - p): db_p += dg2 g1_n / (NN+2);  dg1_n += dg2^T b_p / (NN+2)
-        const float inv2 = 1.0f / (float)(NN + 2);
+        const float inv2 = frcp(NN + 2);
         for (int e = tid; e < (NN + 1) * 32; e += 256) {
           const int p = e >> 5, r = e & 15, side = (e >> 4) & 1, n = NN - p;
           float x = 0.0f;
@@ -1713,7 +1716,7 @@ __global__ __launch_bounds__(256) void k_leaf_bwd(Args a, LeafBwd o) {
           float x = 0.0f;
 #pragma unroll
           for (int k = 0; k < 16; ++k) x = fmaf(F[r * 16 + k], Lt[p][k], x);
-          dBT[p + n][r] += x / (float)(p + n + 2);
+          dBT[p + n][r] += x * frcp(p + n + 2);
         }
         __syncthreads();
       }
@@ -1721,9 +1724,9 @@ __global__ __launch_bounds__(256) void k_leaf_bwd(Args a, LeafBwd o) {
     // bt_N -> b_p; g1_n -> b_n
     for (int e = tid; e < (q + 1) * 16; e += 256) {
       const int p = e >> 4, r = e & 15;
-      float x = dB[p][r] + dG1[p][r] / (float)(p + 1);
+      float x = fmaf(dG1[p][r], frcp(p + 1), dB[p][r]);
       if constexpr (N >= 2) {
-        for (int NN = 0; NN + p <= q; ++NN) x += dBT[NN][r] / (float)(p + NN + N);
+        for (int NN = 0; NN + p <= q; ++NN) x = fmaf(dBT[NN][r], frcp(p + NN + N), x);
       }
       dB[p][r] = x;
     }
@@ -1734,11 +1737,11 @@ __global__ __launch_bounds__(256) void k_leaf_bwd(Args a, LeafBwd o) {
       float y = sp[1][j * 16 + i] * dB[p][j];  // A[j][i] db_p[j], summed over j
 #pragma unroll
       for (int o2 = 1; o2 < 16; o2 <<= 1) y += __shfl_xor(y, o2, 64);
-      const float c = -h / (float)p;
+      const float c = -h * frcp(p);
       dAl = fmaf(c * dB[p][i], Lt[p - 1][j], dAl);
       if (j == 0) {
         dB[p - 1][i] += c * y;
-        dhl -= y * Lt[p - 1][i] / (float)p;
+        dhl -= y * Lt[p - 1][i] * frcp(p);
       }
       __syncthreads();
     }
