@@ -42,6 +42,7 @@ constexpr int RP = 20;     // LDS row pitch of the 16 x 16 slices (bank-conflict
 constexpr int SP = 16 * RP + 4;  // LDS slice pitch of the level-3 buffers
 
 __host__ __device__ constexpr int lw_of(int N) { return N == 1 ? 16 : (N == 2 ? 272 : 4368); }
+#define LWN(N) lw_of(N)
 
 typedef float f4 __attribute__((ext_vector_type(4)));
 
@@ -68,7 +69,7 @@ struct Args {
   float* pre;   // (B, n_int, W) prefix rows (mean / max readouts)
   float* mats;  // (B, 3, 256) per-sample Van Loan step matrices P, V and the shared flow (uniform modes)
   float* out;
-  // backward: the adjoint scan's per-chunk local cotangents (B, C, LW), carries (B, C + 1, LW), max argmax (B, D+1)
+  // backward: the adjoint scan's per-chunk local cotangents (B, C, LW), carries (B, C + 1, LW), max argmax (B, LW)
   float* lloc;
   float* lam;
   int* amax;
@@ -1074,7 +1075,8 @@ __global__ __launch_bounds__(N >= 3 ? 256 : 64) void k_scan(Seq s) {
 //   dM = rho_1 (x) S1 + rho_2 M S2^T + rho_2^T M S2 + T1 + T2 + T3,
 // where T1 + T2 + T3 is the derivative of <l_3, M^(x)3 S3> along each tensor axis:
 //   T1 = <l_3 x_3 M^T x_2 M^T, S3>_{23},  T2 = <l_3 x_3 M^T, S3 x_1 M>_{13},  T3 = <l_3, S3 x_1 M x_2 M>_{12}
-// (<X, Y>_{jk}[p][q] contracts the two named axes of X[.., p, ..] and Y[.., q, ..]).
+// (<X, Y>_{jk}[p][q] contracts the two named axes of X[.., p, ..] and Y[.., q, ..]). S3 of the state is read from
+// its row in global memory (L2-resident), which keeps the workgroup within half of the LDS.
 // Passes: LOCAL (each chunk from lambda = 0: the chunk's own part of the cotangent of its entry state),
 // CARRY (one sample's chunks in reverse, on the chunk summaries: Lambda_c = local_c + R(chunk c)^T Lambda_{c+1}),
 // EMIT (each chunk from Lambda_{c+1}, writing ds_t over the local terms and dM_t over the flows).
@@ -1097,8 +1099,7 @@ struct AdjSeq {
   const float* init;  // EMIT: Lambda rows (B, C + 1, LW), chunk c starts from row c + 1; CARRY: row C on entry
   float* lam;         // LOCAL: (B, C, LW) outputs; CARRY: (B, C + 1, LW) outputs (rows 1..C)
   const float* lloc;  // CARRY: the LOCAL outputs
-  const float* st;    // EMIT: prefix rows (B, n, Wst) with the level-0 column (the states S_t)
-  int Wst;
+  const float* st;    // EMIT: the states S_t, padded rows (B, n, LW)
   float* dlv;         // EMIT: ds_t (padded, in place of lv)
   float* dfl;         // EMIT: dM_t (in place of fl)
 };
@@ -1110,17 +1111,16 @@ __device__ __forceinline__ float adj_g(const AdjSeq& s, int b, int t, int e, int
   const long col = s.glvl0 + oi;
   if (s.gmode == G_PREFIX) return s.g[((long)b * s.n + t) * s.W + col];
   if (s.gmode == G_MEAN) return s.g[(long)b * s.W + col] * s.gscale;
-  return s.amax[(long)b * s.W + col] == t ? s.g[(long)b * s.W + col] : 0.0f;
+  return s.amax[(long)b * LWN(N) + e] == t ? s.g[(long)b * s.W + col] : 0.0f;
 }
 
 template <int N, int MODE>
-__global__ __launch_bounds__(256) void k_adj(AdjSeq s) {
+__global__ __launch_bounds__(256, 2) void k_adj(AdjSeq s) {
   constexpr int LW = lw_of(N);
   constexpr bool EMIT = MODE == ADJ_EMIT;
   constexpr int S3N = N >= 3 ? 16 * SP : 4;
   __shared__ __align__(16) float L3[S3N];                  // l_3 (current cotangent, level 3)
   __shared__ __align__(16) float C3[S3N];                  // l_3 x_3 M^T, then x_2 M^T
-  __shared__ __align__(16) float A3[EMIT ? S3N : 4];       // S3 of the state before the step
   __shared__ __align__(16) float B3[EMIT ? S3N : 4];       // S3 x_1 M, then x_2 M
   __shared__ __align__(16) float Tw[EMIT && N >= 3 ? 4 : 1][256];  // per-wave partial T1 + T2 + T3
   __shared__ __align__(16) float L2[16 * RP], R2[16 * RP], Ms[256], s2s[16 * RP], Zs[16 * RP];
@@ -1180,17 +1180,9 @@ __global__ __launch_bounds__(256) void k_adj(AdjSeq s) {
       }
     }
     if constexpr (EMIT) {  // the state before the step: row t - 1 (zero before the first interval)
-      const float* srow = t > 0 ? s.st + ((long)b * s.n + t - 1) * s.Wst + 1 : nullptr;
-      auto sv = [&](int e) -> float {
-        if (!srow) return 0.0f;
-        const long oi = out_index(N, s.d, e);
-        return oi >= 0 ? srow[oi] : 0.0f;
-      };
-      if (tid < 16) S1s[tid] = sv(tid);
-      if constexpr (N >= 2) S2s[ri * RP + rj] = sv(16 + tid);
-      if constexpr (N >= 3) {
-        for (int e = tid; e < 4096; e += 256) A3[(e >> 8) * SP + ((e >> 4) & 15) * RP + (e & 15)] = sv(272 + e);
-      }
+      const float* srow = t > 0 ? s.st + ((long)b * s.n + t - 1) * LW : nullptr;
+      if (tid < 16) S1s[tid] = srow ? srow[tid] : 0.0f;
+      if constexpr (N >= 2) S2s[ri * RP + rj] = srow ? srow[16 + tid] : 0.0f;
     }
     __syncthreads();
     const f4 M4 = *reinterpret_cast<const f4*>(Ms + c16 * 16 + 4 * g);  // M[c16][4g + r]
@@ -1302,12 +1294,16 @@ __global__ __launch_bounds__(256) void k_adj(AdjSeq s) {
         a23[ii] = y;
       }
       if constexpr (EMIT) {
+        // V1 = S3 x_1 M, tiles j, with S3 read from the state row (L2-resident; zero before the first interval)
+        const float* s3g = t > 0 ? s.st + ((long)b * s.n + t - 1) * LW + 272 : nullptr;
 #pragma unroll
-        for (int jj = 0; jj < 4; ++jj) {  // V1 = S3 x_1 M, tiles j
+        for (int jj = 0; jj < 4; ++jj) {
           const int j = 4 * w + jj;
           f4 z = {0.0f, 0.0f, 0.0f, 0.0f};
+          if (s3g) {
 #pragma unroll
-          for (int k2 = 0; k2 < 4; ++k2) z = mfma(M4[k2], A3[(4 * g + k2) * SP + j * RP + c16], z);
+            for (int k2 = 0; k2 < 4; ++k2) z = mfma(M4[k2], s3g[(4 * g + k2) * 256 + j * 16 + c16], z);
+          }
 #pragma unroll
           for (int r = 0; r < 4; ++r) B3[(4 * g + r) * SP + j * RP + c16] = z[r];
         }
@@ -1341,10 +1337,11 @@ __global__ __launch_bounds__(256) void k_adj(AdjSeq s) {
       __syncthreads();
       if constexpr (EMIT) {
         // T1[p][q] = sum_{j, k} C3[p][j][k] S3[q][j][k];  T3[p][q] = sum_{a, b} l_3[a][b][p] W3[a][b][q]
+        const float* s3g = t > 0 ? s.st + ((long)b * s.n + t - 1) * LW + 272 : nullptr;
 #pragma unroll 4
         for (int ks = 16 * w; ks < 16 * w + 16; ++ks) {
           const int j = ks >> 2, kk = 4 * (ks & 3) + g;
-          tacc = mfma(C3[c16 * SP + j * RP + kk], A3[c16 * SP + j * RP + kk], tacc);
+          if (s3g) tacc = mfma(C3[c16 * SP + j * RP + kk], s3g[c16 * 256 + j * 16 + kk], tacc);
           tacc = mfma(L3[j * SP + kk * RP + c16], B3[j * SP + kk * RP + c16], tacc);
         }
 #pragma unroll
@@ -2220,13 +2217,13 @@ DWs dense_ws(const DPlan& p, int readout, bool bwd = false) {
   w.sfl = off; off += al256(BC * 256 * 4);
   w.car = off; off += al256((size_t)p.B * (p.C + 1) * p.LW * 4);
   w.pre = off;
-  off += bwd ? al256(BN * (p.D + 1) * 4)
+  off += bwd ? al256(BN * p.LW * 4)
              : (readout == EWS_READOUT_MEAN || readout == EWS_READOUT_MAX) ? al256(BN * p.W * 4) : 0;
   w.mats = off; off += al256((size_t)p.B * 768 * 4);
   if (bwd) {
     w.lloc = off; off += al256(BC * p.LW * 4);
     w.lam = off; off += al256((size_t)p.B * (p.C + 1) * p.LW * 4);
-    w.amax = off; off += al256((size_t)p.B * (p.D + 1) * 4);
+    w.amax = off; off += al256((size_t)p.B * p.LW * 4);
     w.dv = off; off += al256(BN * 16 * 4);
     w.dh = off; off += al256(BN * 4);
     w.dsh = off; off += al256((size_t)p.B * 2 * 4);
@@ -2410,20 +2407,19 @@ int launch_adj(int N, const AdjSeq& q, dim3 grid, hipStream_t st) {
 // carries in the workspace: recomputes the prefix rows (the states), then LOCAL, CARRY and EMIT; leaves ds_t in loc
 // and dM_t in fl.
 int dense_adjoint(const ews_dense_desc* s, const DPlan& p, const Args& a, const float* grad_out, hipStream_t st) {
-  const int Wst = p.D + 1;
-  {  // prefix rows of the forward (the states S_t), with the level-0 column
+  {  // the forward's states S_t (padded rows)
     Seq q{};
     q.lv = a.loc; q.lv_bs = (long)p.n_int * p.LW; q.fl = a.fl; q.fl_bs = (long)p.n_int * 256;
     q.n = p.n_int; q.T = p.T; q.init = a.car; q.init_bs = (long)(p.C + 1) * p.LW;
-    q.rows = a.pre; q.rows_bs = (long)p.n_int * Wst; q.rows_ld = Wst; q.padded = 0; q.lvl0 = 1; q.d = p.d;
+    q.rows = a.pre; q.rows_bs = (long)p.n_int * p.LW; q.rows_ld = p.LW; q.padded = 1; q.lvl0 = 0; q.d = p.d;
     q.C = p.C;
     const int rc = launch_scan<false>(p.N, q, dim3(p.C, p.B), st);
     if (rc != EWS_OK) return rc;
   }
   const int ro = s->readout;
   if ((ro == EWS_READOUT_MEAN || ro == EWS_READOUT_MAX) && !s->level0) return EWS_ERR_OPTION;
-  if (ro == EWS_READOUT_MAX) {
-    hipLaunchKernelGGL(k_argmax, dim3((Wst + 255) / 256, p.B), dim3(256), 0, st, a.pre, p.n_int, Wst, a.amax);
+  if (ro == EWS_READOUT_MAX) {  // per padded column (the level-0 column's cotangent goes nowhere)
+    hipLaunchKernelGGL(k_argmax, dim3((p.LW + 255) / 256, p.B), dim3(256), 0, st, a.pre, p.n_int, p.LW, a.amax);
     DENSE_CHECK();
   }
   hipLaunchKernelGGL(k_lam_end, dim3((p.LW + 255) / 256, p.B), dim3(256), 0, st, a,
@@ -2434,7 +2430,7 @@ int dense_adjoint(const ews_dense_desc* s, const DPlan& p, const Args& a, const 
   q.gmode = ro == EWS_READOUT_PREFIX ? G_PREFIX : ro == EWS_READOUT_MEAN ? G_MEAN : ro == EWS_READOUT_MAX ? G_MAX
                                                                                                      : G_NONE;
   q.W = p.W; q.glvl0 = s->level0 ? 1 : 0; q.g = grad_out; q.amax = a.amax; q.gscale = 1.0f / (float)p.n_int;
-  q.st = a.pre; q.Wst = Wst;
+  q.st = a.pre;
   // LOCAL (the terminal readout has no in-chunk cotangents: the local parts are zero)
   if (q.gmode == G_NONE) {
     hipLaunchKernelGGL(k_zero_rows, dim3((p.LW + 255) / 256, p.B * p.C), dim3(256), 0, st, a.lloc, (long)p.LW,
