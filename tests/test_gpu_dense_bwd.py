@@ -213,3 +213,16 @@ def test_dense_backward_flow_schemes(chen, flow_mode):
     errs = [relerr(g, r) for g, r in zip(got, ref)]
     print(f"dense bwd flows large {chen}: path {errs[0]:.2e} clock {errs[1]:.2e} A {errs[2]:.2e}")
     assert max(errs) < 1e-4
+
+
+@pytest.mark.parametrize("B,L,d,N", [(1, 2, 1, 1), (1, 2, 3, 3), (3, 3, 2, 2), (1, 65, 4, 3), (2, 129, 16, 2)])
+def test_dense_backward_edge_shapes(B, L, d, N):
+    """One interval, width 1, the basepoint minimum length, chunk-boundary lengths (64 + 1, 128 + 1)."""
+    path, clock, A = _random(B, L, d, seed=950 + L + d)
+    for readout in ("prefix", "terminal"):
+        got, ref = _grads(path, clock, A, N, 6, readout, "displacement")
+        errs = [relerr(g, r) for g, r in zip(got, ref)]
+        print(f"dense bwd edge B={B} L={L} d={d} N={N} {readout}: {max(errs):.2e}")
+        assert max(errs) < 1e-4
+    got, ref = _grads_kw(path, clock, A, N, "mean", "displacement", dict(leaf="van_loan", M=3, van_loan_expm="cayley"))
+    assert max(relerr(g, r) for g, r in zip(got, ref)) < 1e-4
