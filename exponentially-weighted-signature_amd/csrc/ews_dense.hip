@@ -1983,31 +1983,35 @@ __global__ __launch_bounds__(256) void k_vl_bwd(Args a, LeafBwd o) {
   pb[HP * 256 + tid] = dAl;
 }
 
-// sums of the workgroups' partials (float64), one workgroup per row p of (HP + 1, 256)
+// sums of the workgroups' partials (float64): workgroup (p, c) sums row p of the partial sets c, c + PRS, ...
+constexpr int PRS = 32;  // partial-sum slices (the second level of the reduction is in k_dA)
 __global__ __launch_bounds__(256) void k_part_reduce(const float* part, int nparts, double* hsum) {
-  const int p = blockIdx.x, tid = threadIdx.x;
-  double s0 = 0.0, s1 = 0.0, s2 = 0.0, s3 = 0.0;
-  int k = 0;
-  for (; k + 4 <= nparts; k += 4) {
+  const int p = blockIdx.x, c = blockIdx.y, tid = threadIdx.x;
+  double s0 = 0.0, s1 = 0.0;
+  int k = c;
+  for (; k + PRS < nparts; k += 2 * PRS) {
     s0 += (double)part[((size_t)k * (HP + 1) + p) * 256 + tid];
-    s1 += (double)part[((size_t)(k + 1) * (HP + 1) + p) * 256 + tid];
-    s2 += (double)part[((size_t)(k + 2) * (HP + 1) + p) * 256 + tid];
-    s3 += (double)part[((size_t)(k + 3) * (HP + 1) + p) * 256 + tid];
+    s1 += (double)part[((size_t)(k + PRS) * (HP + 1) + p) * 256 + tid];
   }
-  for (; k < nparts; ++k) s0 += (double)part[((size_t)k * (HP + 1) + p) * 256 + tid];
-  hsum[p * 256 + tid] = (s0 + s1) + (s2 + s3);
+  if (k < nparts) s0 += (double)part[((size_t)k * (HP + 1) + p) * 256 + tid];
+  hsum[((size_t)c * (HP + 1) + p) * 256 + tid] = s0 + s1;
 }
 
 // dA = sum_p sum_{j<p} (A^T)^j H_p (A^T)^{p-1-j} + the direct terms (float64):
 // R_{P-1} = H_P, R_j = H_{j+1} + R_{j+1} A^T, dA = R_0 + A^T (R_1 + A^T (R_2 + ...)), P = PM.
 __global__ __launch_bounds__(256) void k_dA(Args a, const double* hsum, float* grad_A) {
-  __shared__ double At[256], Rs[PM][256], U[256];
+  __shared__ double At[256], Rs[PM][256], U[256], Hs[HP + 1][256];
   const int tid = threadIdx.x, i = tid >> 4, j = tid & 15;
+  for (int p = 0; p <= HP; ++p) {
+    double v = 0.0;
+    for (int c = 0; c < PRS; ++c) v += hsum[((size_t)c * (HP + 1) + p) * 256 + tid];
+    Hs[p][tid] = v;
+  }
   At[tid] = (double)a.apow[256 + j * 16 + i];  // A^T[i][j]
-  Rs[PM - 1][tid] = hsum[PM * 256 + tid];
+  Rs[PM - 1][tid] = Hs[PM][tid];
   __syncthreads();
   for (int jj = PM - 2; jj >= 0; --jj) {
-    double v = hsum[(jj + 1) * 256 + tid];
+    double v = Hs[jj + 1][tid];
     for (int k = 0; k < 16; ++k) v += Rs[jj + 1][i * 16 + k] * At[k * 16 + j];
     Rs[jj][tid] = v;
     __syncthreads();
@@ -2021,7 +2025,7 @@ __global__ __launch_bounds__(256) void k_dA(Args a, const double* hsum, float* g
     U[tid] = v;
     __syncthreads();
   }
-  if (i < a.d && j < a.d) grad_A[i * a.d + j] = (float)(U[tid] + hsum[HP * 256 + tid]);
+  if (i < a.d && j < a.d) grad_A[i * a.d + j] = (float)(U[tid] + Hs[HP][tid]);
 }
 
 // knot cotangents: dpath[k] = dv_{k-1} - dv_k, dclock[k] = dh_{k-1} - dh_k, plus the shared steps of the cached modes
@@ -2228,7 +2232,7 @@ DWs dense_ws(const DPlan& p, int readout, bool bwd = false) {
     w.dh = off; off += al256(BN * 4);
     w.dsh = off; off += al256((size_t)p.B * 2 * 4);
     w.part = off; off += al256((size_t)kLeafBwdBlocks * (HP + 1) * 256 * 4);
-    w.hsum = off; off += al256((size_t)(HP + 1) * 256 * 8);
+    w.hsum = off; off += al256((size_t)PRS * (HP + 1) * 256 * 8);
     w.vlsave = off; off += p.leaf == EWS_LEAF_VAN_LOAN ? al256(BN * (512 + 16 * (size_t)p.vm) * 4) : 0;
   }
   w.total = off;
@@ -2572,7 +2576,7 @@ int ews_dense_backward(const ews_dense_desc* desc, const float* path, const floa
     else hipLaunchKernelGGL((k_leaf_bwd<3>), dim3(grid), dim3(256), 0, st, a, o);
   }
   DENSE_CHECK();
-  hipLaunchKernelGGL(k_part_reduce, dim3(HP + 1), dim3(256), 0, st, o.part, grid, hsum);
+  hipLaunchKernelGGL(k_part_reduce, dim3(HP + 1, PRS), dim3(256), 0, st, o.part, grid, hsum);
   DENSE_CHECK();
   hipLaunchKernelGGL(k_dA, dim3(1), dim3(256), 0, st, a, hsum, grad_A);
   DENSE_CHECK();
