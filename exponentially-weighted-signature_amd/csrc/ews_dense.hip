@@ -1609,7 +1609,15 @@ __global__ __launch_bounds__(256) void k_leaf_bwd(Args a, LeafBwd o) {
 #pragma unroll
   for (int p = 0; p < HP; ++p) H[p] = 0.0f;
   float dAl = 0.0f;
-  const float Aij = a.apow[256 + tid];  // A[i][j] (P_1 = A)
+  const int l = tid & 63, g = l >> 4, c16 = l & 15;
+  // the letter chains run on wavefront 0: lane (c16, g) holds A[c16][4g .. 4g+3] and A[4g .. 4g+3][c16]
+  f4 Ar, Ac;
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    Ar[r] = a.apow[256 + c16 * 16 + 4 * g + r];
+    Ac[r] = a.apow[256 + (4 * g + r) * 16 + c16];
+  }
+  f4 dAl4 = {0.0f, 0.0f, 0.0f, 0.0f};  // wavefront 0: the letters' dA terms of entries 4l .. 4l+3
   __syncthreads();
   const long total = (long)a.B * a.n_int;
   for (long it = blockIdx.x; it < total; it += gridDim.x) {
@@ -1634,14 +1642,18 @@ __global__ __launch_bounds__(256) void k_leaf_bwd(Args a, LeafBwd o) {
       (&dBT[0][0])[e] = 0.0f;
     }
     __syncthreads();
-    // ---- letters b_p = (-h/p) A b_{p-1}
-    for (int p = 1; p <= q; ++p) {
-      float v = Aij * Lt[p - 1][j];
-#pragma unroll
-      for (int o2 = 1; o2 < 16; o2 <<= 1) v += __shfl_xor(v, o2, 64);
-      if (j == 0) Lt[p][i] = v * (-h * frcp(p));
-      __syncthreads();
+    // ---- letters b_p = (-h/p) A b_{p-1} (wavefront 0)
+    if (tid < 64) {
+      for (int p = 1; p <= q; ++p) {
+        const f4 bp = *reinterpret_cast<const f4*>(&Lt[p - 1][4 * g]);
+        float v = fmaf(Ar.x, bp.x, fmaf(Ar.y, bp.y, fmaf(Ar.z, bp.z, Ar.w * bp.w)));
+        v += __shfl_xor(v, 16, 64);
+        v += __shfl_xor(v, 32, 64);
+        if (g == 0) Lt[p][c16] = v * (-h * frcp(p));
+        wave_order_d();
+      }
     }
+    __syncthreads();
     for (int e = tid; e < (q + 1) * 16; e += 256) {
       const int n = e >> 4, r = e & 15;
       G1[n][r] = Lt[n][r] * frcp(n + 1);
@@ -1728,20 +1740,30 @@ __global__ __launch_bounds__(256) void k_leaf_bwd(Args a, LeafBwd o) {
       dB[p][r] = x;
     }
     __syncthreads();
-    // ---- letters reverse: db_{p-1} += (-h/p) A^T db_p; dA += (-h/p) db_p (x) b_{p-1}; dh += -(1/p) <A^T db_p, b_{p-1}>
+    // ---- letters reverse (wavefront 0): db_{p-1} += (-h/p) A^T db_p; dA += (-h/p) db_p (x) b_{p-1};
+    // dh += -(1/p) <A^T db_p, b_{p-1}>
     float dhl = 0.0f;
-    for (int p = q; p >= 1; --p) {
-      float y = sp[1][j * 16 + i] * dB[p][j];  // A[j][i] db_p[j], summed over j
+    if (tid < 64) {
+      const int gi = l >> 2, gj = 4 * (l & 3);
+      for (int p = q; p >= 1; --p) {
+        const f4 dp = *reinterpret_cast<const f4*>(&dB[p][4 * g]);
+        float y = fmaf(Ac.x, dp.x, fmaf(Ac.y, dp.y, fmaf(Ac.z, dp.z, Ac.w * dp.w)));  // (A^T db_p)[c16]
+        y += __shfl_xor(y, 16, 64);
+        y += __shfl_xor(y, 32, 64);
+        const float c = -h * frcp(p);
+        const float dpi = c * dB[p][gi];
+        const f4 bm = *reinterpret_cast<const f4*>(&Lt[p - 1][gj]);
 #pragma unroll
-      for (int o2 = 1; o2 < 16; o2 <<= 1) y += __shfl_xor(y, o2, 64);
-      const float c = -h * frcp(p);
-      dAl = fmaf(c * dB[p][i], Lt[p - 1][j], dAl);
-      if (j == 0) {
-        dB[p - 1][i] += c * y;
-        dhl -= y * Lt[p - 1][i] * frcp(p);
+        for (int r = 0; r < 4; ++r) dAl4[r] = fmaf(dpi, bm[r], dAl4[r]);
+        wave_order_d();
+        if (g == 0) {
+          dB[p - 1][c16] += c * y;
+          dhl -= y * Lt[p - 1][c16] * frcp(p);
+        }
+        wave_order_d();
       }
-      __syncthreads();
     }
+    __syncthreads();
     // ---- flow adjoint
     bool ident;
     const float hf = flow_step(a, th, t, ident);
@@ -1749,14 +1771,14 @@ __global__ __launch_bounds__(256) void k_leaf_bwd(Args a, LeafBwd o) {
     // ---- outputs
     if (tid < 16) o.dv[((size_t)b * a.n_int + t) * 16 + tid] = dB[0][tid];
     {
-      float v = dhl;  // nonzero in threads j == 0
+      float v = dhl;  // nonzero in lanes 0 .. 15 of wavefront 0
 #pragma unroll
-      for (int o2 = 16; o2 < 64; o2 <<= 1) v += __shfl_xor(v, o2, 64);
-      if ((tid & 63) == 0) red[4 + (tid >> 6)] = v;
+      for (int o2 = 1; o2 < 16; o2 <<= 1) v += __shfl_xor(v, o2, 64);
+      if (tid == 0) red[4] = v;
     }
     __syncthreads();
     if (tid == 0) {
-      const float dl = red[4] + red[5] + red[6] + red[7];
+      const float dl = red[4];
       if (a.flow_mode == EWS_FLOW_PER_INTERVAL) {
         o.dh[(size_t)b * a.n_int + t] = dl + dhf;
       } else {
@@ -1769,7 +1791,11 @@ __global__ __launch_bounds__(256) void k_leaf_bwd(Args a, LeafBwd o) {
   float* pb = o.part + (size_t)blockIdx.x * (HP + 1) * 256;
 #pragma unroll
   for (int p = 0; p < HP; ++p) pb[p * 256 + tid] = H[p];
-  pb[HP * 256 + tid] = dAl;
+  Gm[tid] = 0.0f;
+  __syncthreads();
+  if (tid < 64) *reinterpret_cast<f4*>(Gm + 4 * l) = dAl4;
+  __syncthreads();
+  pb[HP * 256 + tid] = dAl + Gm[tid];
 }
 
 // Van Loan leaf adjoint (one workgroup per interval, grid-stride). The forward's recompute saved per interval the
