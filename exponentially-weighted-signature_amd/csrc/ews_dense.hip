@@ -1599,7 +1599,7 @@ __global__ __launch_bounds__(256) void k_leaf_bwd(Args a, LeafBwd o) {
   __shared__ __align__(16) float sp[HP][256];
   __shared__ __align__(16) float Lt[QN][16], G1[QN][16], BT[QN][16], dB[QN][16], dG1[QN][16], dBT[QN][16];
   __shared__ __align__(16) float dS3[N >= 3 ? 4096 : 4];
-  __shared__ __align__(16) float dS2[256], F[256], Gm[256], Esq[SQMAX][256], W1[256], W2[256], W3[256 + 32];
+  __shared__ __align__(16) float dS2[256], F[256], F2[256], Gm[256], Esq[SQMAX][256], W1[256], W2[256], W3[256 + 32];
   __shared__ float dS1[16], red[8];
   const int tid = threadIdx.x, i = tid >> 4, j = tid & 15;
   const int q = a.q;
@@ -1685,47 +1685,42 @@ __global__ __launch_bounds__(256) void k_leaf_bwd(Args a, LeafBwd o) {
       __syncthreads();
     }
     if constexpr (N == 3) {
+      // per degree NN: dg2_NN = bt3_NN ._1 ds3 + ds2 (F) and E_NN = ds3 ._3 g1_NN (F2), then
+      //   pairs (p, n = NN - p): db_p += dg2_NN g1_n / (NN+2);  dg1_n += dg2_NN^T b_p / (NN+2)
+      //   dbt3_{p+NN} += (E_NN b_p) / (p+NN+2)
       for (int NN = 0; NN <= q; ++NN) {
-        // dg2_NN = bt3_NN ._1 ds3 + ds2
         {
-          float f = dS2[tid];
-#pragma unroll 4
-          for (int aa = 0; aa < 16; ++aa) f = fmaf(BT[NN][aa], dS3[aa * 256 + tid], f);
-          F[tid] = f;
-        }
-        __syncthreads();
-        // pairs (p, n = NN - p): db_p += dg2 g1_n / (NN+2);  dg1_n += dg2^T b_p / (NN+2)
-        const float inv2 = frcp(NN + 2);
-        for (int e = tid; e < (NN + 1) * 32; e += 256) {
-          const int p = e >> 5, r = e & 15, side = (e >> 4) & 1, n = NN - p;
-          float x = 0.0f;
-          if (side == 0) {
+          float f = dS2[tid], e2 = 0.0f;
 #pragma unroll
-            for (int k = 0; k < 16; ++k) x = fmaf(F[r * 16 + k], G1[n][k], x);
-            dB[p][r] += x * inv2;
-          } else {
-#pragma unroll
-            for (int k = 0; k < 16; ++k) x = fmaf(F[k * 16 + r], Lt[p][k], x);
-            dG1[n][r] += x * inv2;
+          for (int k = 0; k < 16; ++k) {
+            f = fmaf(BT[NN][k], dS3[k * 256 + tid], f);
+            e2 = fmaf(dS3[tid * 16 + k], G1[NN][k], e2);
           }
+          F[tid] = f;
+          F2[tid] = e2;
         }
         __syncthreads();
-      }
-      // dbt3_{p+n} += (E_n b_p) / (p+n+2), E_n = ds3 ._3 g1_n
-      for (int n = 0; n <= q; ++n) {
-        {
-          float f = 0.0f;
-#pragma unroll
-          for (int k = 0; k < 16; ++k) f = fmaf(dS3[tid * 16 + k], G1[n][k], f);
-          F[tid] = f;  // E_n[i][j]
-        }
-        __syncthreads();
-        for (int e = tid; e < (q - n + 1) * 16; e += 256) {
-          const int p = e >> 4, r = e & 15;
+        const float inv2 = frcp(NN + 2);
+        const int np = (NN + 1) * 32, ne = (q - NN + 1) * 16;
+        for (int e = tid; e < np + ne; e += 256) {
           float x = 0.0f;
+          if (e < np) {
+            const int p = e >> 5, r = e & 15, side = (e >> 4) & 1, n = NN - p;
+            if (side == 0) {
 #pragma unroll
-          for (int k = 0; k < 16; ++k) x = fmaf(F[r * 16 + k], Lt[p][k], x);
-          dBT[p + n][r] += x * frcp(p + n + 2);
+              for (int k = 0; k < 16; ++k) x = fmaf(F[r * 16 + k], G1[n][k], x);
+              dB[p][r] += x * inv2;
+            } else {
+#pragma unroll
+              for (int k = 0; k < 16; ++k) x = fmaf(F[k * 16 + r], Lt[p][k], x);
+              dG1[n][r] += x * inv2;
+            }
+          } else {
+            const int p = (e - np) >> 4, r = (e - np) & 15;
+#pragma unroll
+            for (int k = 0; k < 16; ++k) x = fmaf(F2[r * 16 + k], Lt[p][k], x);
+            dBT[p + NN][r] += x * frcp(p + NN + 2);
+          }
         }
         __syncthreads();
       }
