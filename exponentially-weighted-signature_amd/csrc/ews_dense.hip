@@ -1592,15 +1592,29 @@ __device__ float block_flow_adjoint(const Args& a, const LdsTable* sp, float nor
   return block_rational_adjoint(sp, a.chen_expm, hf, W2, G, nullptr, W1, W3, red, dAl, tid);
 }
 
-template <int N>
+template <int N, bool EXACTF>  // EXACTF: exact flows (the other schemes' code is left out)
 __global__ __launch_bounds__(256) void k_leaf_bwd(Args a, LeafBwd o) {
   constexpr int LW = lw_of(N);
-  constexpr int QN = QMAX + 1;
   __shared__ __align__(16) float sp[HP][256];
-  __shared__ __align__(16) float Lt[QN][16], G1[QN][16], BT[QN][16], dB[QN][16], dG1[QN][16], dBT[QN][16];
-  __shared__ __align__(16) float dS3[N >= 3 ? 4096 : 4];
-  __shared__ __align__(16) float dS2[256], F[256], F2[256], Gm[256], Esq[SQMAX][256], W1[256], W2[256], W3[256 + 32];
+  // ds3 of the level adjoint and, after it, the flow adjoint's squarings / scratch share one region
+  constexpr int UNF = (EXACTF ? SQMAX * 256 : 800) > (N >= 3 ? 4096 : 0) ? (EXACTF ? SQMAX * 256 : 800)
+                                                                          : (N >= 3 ? 4096 : 0);
+  __shared__ __align__(16) float UN[UNF];
+  __shared__ __align__(16) float dS2[256], F[256], F2[256], Gm[256];
   __shared__ float dS1[16], red[8];
+  extern __shared__ __align__(16) float dyn[];  // the six letter arrays, (q + 1) x 16 each
+  typedef float Row16[16];
+  const int QN = a.q + 1;
+  Row16* Lt = reinterpret_cast<Row16*>(dyn);
+  Row16* G1 = Lt + QN;
+  Row16* BT = G1 + QN;
+  Row16* dB = BT + QN;
+  Row16* dG1 = dB + QN;
+  Row16* dBT = dG1 + QN;
+  float* dS3 = UN;
+  typedef float Mat[256];
+  Mat* Esq = reinterpret_cast<Mat*>(UN);
+  float *W1 = UN, *W2 = UN + 256, *W3 = UN + 512;
   const int tid = threadIdx.x, i = tid >> 4, j = tid & 15;
   const int q = a.q;
   for (int e = tid; e < HP * 256; e += 256) sp[e >> 8][e & 255] = a.apow[e];
@@ -1762,7 +1776,8 @@ __global__ __launch_bounds__(256) void k_leaf_bwd(Args a, LeafBwd o) {
     // ---- flow adjoint
     bool ident;
     const float hf = flow_step(a, th, t, ident);
-    const float dhf = block_flow_adjoint(a, sp, norm1, hf, ident, Gm, Esq, W1, W2, W3, red, H, dAl, tid);
+    const float dhf = EXACTF ? (ident ? 0.0f : block_exp_adjoint(sp, norm1, hf, Gm, nullptr, Esq, Esq, red, H, tid))
+                             : block_flow_adjoint(a, sp, norm1, hf, ident, Gm, Esq, W1, W2, W3, red, H, dAl, tid);
     // ---- outputs
     if (tid < 16) o.dv[((size_t)b * a.n_int + t) * 16 + tid] = dB[0][tid];
     {
@@ -1808,7 +1823,7 @@ __global__ __launch_bounds__(256) void k_leaf_bwd(Args a, LeafBwd o) {
 // Then the flow's adjoint as in k_leaf_bwd.
 constexpr int VMAX = 64;  // knots per interval at most
 
-template <int N>
+template <int N, bool EXACTF>
 __global__ __launch_bounds__(256) void k_vl_bwd(Args a, LeafBwd o) {
   constexpr int LW = lw_of(N);
   __shared__ __align__(16) float sp[HP][256];
@@ -1987,7 +2002,8 @@ __global__ __launch_bounds__(256) void k_vl_bwd(Args a, LeafBwd o) {
     // ---- flow adjoint
     bool ident;
     const float hf = flow_step(a, th, t, ident);
-    const float dhf = block_flow_adjoint(a, sp, norm1, hf, ident, Gm, Esq, W1, W2, W3, red, H, dAl, tid);
+    const float dhf = EXACTF ? (ident ? 0.0f : block_exp_adjoint(sp, norm1, hf, Gm, nullptr, Esq, Esq, red, H, tid))
+                             : block_flow_adjoint(a, sp, norm1, hf, ident, Gm, Esq, W1, W2, W3, red, H, dAl, tid);
     if (tid == 0) {
       float dh = 0.0f;
       if (a.vl_mode == EWS_FLOW_PER_INTERVAL) dh += ddelta / (float)Mv;
@@ -2587,15 +2603,22 @@ int ews_dense_backward(const ews_dense_desc* desc, const float* path, const floa
   DENSE_CHECK();
   const long total = (long)p.B * p.n_int;
   const int grid = (int)(total < kLeafBwdBlocks ? total : kLeafBwdBlocks);
+  const size_t lshm = p.leaf == EWS_LEAF_VAN_LOAN ? 0 : (size_t)6 * (p.q + 1) * 16 * 4;  // k_leaf_bwd's letters
+#define EWS_LEAF_BWD(KER, NN)                                                                               \
+  do {                                                                                                      \
+    if (p.chen_expm == EWS_EXPM_EXACT) hipLaunchKernelGGL((KER<NN, true>), dim3(grid), dim3(256), lshm, st, a, o); \
+    else hipLaunchKernelGGL((KER<NN, false>), dim3(grid), dim3(256), lshm, st, a, o);                        \
+  } while (0)
   if (p.leaf == EWS_LEAF_VAN_LOAN) {
-    if (p.N == 1) hipLaunchKernelGGL((k_vl_bwd<1>), dim3(grid), dim3(256), 0, st, a, o);
-    else if (p.N == 2) hipLaunchKernelGGL((k_vl_bwd<2>), dim3(grid), dim3(256), 0, st, a, o);
-    else hipLaunchKernelGGL((k_vl_bwd<3>), dim3(grid), dim3(256), 0, st, a, o);
+    if (p.N == 1) EWS_LEAF_BWD(k_vl_bwd, 1);
+    else if (p.N == 2) EWS_LEAF_BWD(k_vl_bwd, 2);
+    else EWS_LEAF_BWD(k_vl_bwd, 3);
   } else {
-    if (p.N == 1) hipLaunchKernelGGL((k_leaf_bwd<1>), dim3(grid), dim3(256), 0, st, a, o);
-    else if (p.N == 2) hipLaunchKernelGGL((k_leaf_bwd<2>), dim3(grid), dim3(256), 0, st, a, o);
-    else hipLaunchKernelGGL((k_leaf_bwd<3>), dim3(grid), dim3(256), 0, st, a, o);
+    if (p.N == 1) EWS_LEAF_BWD(k_leaf_bwd, 1);
+    else if (p.N == 2) EWS_LEAF_BWD(k_leaf_bwd, 2);
+    else EWS_LEAF_BWD(k_leaf_bwd, 3);
   }
+#undef EWS_LEAF_BWD
   DENSE_CHECK();
   hipLaunchKernelGGL(k_part_reduce, dim3(HP + 1, PRS), dim3(256), 0, st, o.part, grid, hsum);
   DENSE_CHECK();
