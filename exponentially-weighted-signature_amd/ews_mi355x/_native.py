@@ -45,6 +45,10 @@ EXPORTED = (
     "ews_dense_backward_workspace_bytes",
     "ews_dense_combine_backward",
     "ews_dense_backward",
+    "ews_log_dim",
+    "ews_log_workspace_bytes",
+    "ews_log_forward",
+    "ews_log_backward",
 )
 
 
@@ -79,6 +83,17 @@ class DenseDesc(ctypes.Structure):
         ("vl_expm", ctypes.c_int32),
         ("vl_mode", ctypes.c_int32),
         ("chen_expm", ctypes.c_int32),
+    ]
+
+
+class LogDesc(ctypes.Structure):
+    _fields_ = [
+        ("batch", ctypes.c_int32),
+        ("rows", ctypes.c_int32),
+        ("dim", ctypes.c_int32),
+        ("depth", ctypes.c_int32),
+        ("level0", ctypes.c_int32),
+        ("readout", ctypes.c_int32),
     ]
 
 
@@ -139,6 +154,15 @@ def load():
     lib.ews_dense_combine_backward.restype = i32
     lib.ews_dense_backward.argtypes = [ddp, vp, vp, vp, vp, vp, vp, vp, vp, vp]
     lib.ews_dense_backward.restype = i32
+    ldp = ctypes.POINTER(LogDesc)
+    lib.ews_log_dim.argtypes = [i32, i32]
+    lib.ews_log_dim.restype = i32
+    lib.ews_log_workspace_bytes.argtypes = [ldp]
+    lib.ews_log_workspace_bytes.restype = sz
+    lib.ews_log_forward.argtypes = [ldp, vp, vp, vp, vp]
+    lib.ews_log_forward.restype = i32
+    lib.ews_log_backward.argtypes = [ldp, vp, vp, vp, vp, vp]
+    lib.ews_log_backward.restype = i32
     _lib = lib
     return lib
 

@@ -267,18 +267,6 @@ def log_level_slices(d: int, N: int):
     return tuple(slices)
 
 
-def _log_compress_depth_le2(levels, d):
-    """Compressed log of group-like rows: level 1 as is; level 2 = S2 - S1 (x) S1 / 2 at the Lyndon words
-    (i < j) (signax.signature_to_logsignature at depth <= 2, used at ews/layer.py:494, 502)."""
-    S1 = levels[0]
-    if len(levels) == 1:
-        return S1
-    S2 = levels[1]
-    log2 = S2 - 0.5 * S1[..., :, None] * S1[..., None, :]
-    iu = torch.triu_indices(d, d, offset=1, device=S1.device)
-    return torch.cat([S1, log2[..., iu[0], iu[1]]], -1)
-
-
 class LogEWS(torch.nn.Module):
     """log(EWS) in the compressed Lyndon basis (ews/layer.py:440-556)."""
 
@@ -293,12 +281,9 @@ class LogEWS(torch.nn.Module):
         self.d = self.ewms.d
         self.N = self.ewms.N
 
-    def _compress(self, levels):
-        if self.N > 2:
-            raise NotImplementedError("LogEWS on the MI355X path covers depths 1 and 2")
-        return _log_compress_depth_le2(levels, self.d)
-
     def forward(self, path, clock, return_terminal=True, output_format="flat", readout=None):
+        """log-then-pool (ews/layer.py:488-517): the EWS rows, then ews_log_forward (log, Lyndon coefficients,
+        readout) on the GPU."""
         if readout is None:
             readout = "terminal" if return_terminal else "prefix"
         if readout not in {"terminal", "prefix", "mean", "max"}:
@@ -307,23 +292,21 @@ class LogEWS(torch.nn.Module):
             raise ValueError(f"Path must be 2D or 3D, got shape {tuple(path.shape)}")
         if path.dim() == 3 and clock.dim() != 2:
             raise ValueError("clock must be 2D for batched paths")
+        if output_format == "list" and readout in ("mean", "max"):
+            raise ValueError(f"readout='{readout}' requires output_format='flat'")
+        single = path.dim() == 2
+        if single:
+            path, clock = path[None], clock[None]
         if readout == "terminal":
-            lv = self.ewms(path, clock, readout="terminal", output_format="list")
-            feat = self._compress(lv)
-            if output_format == "list":
-                return self._split(feat)
-            return feat
-        lv = self.ewms(path, clock, readout="prefix", output_format="list")
-        feat = self._compress(lv)  # (..., L-1, D_log)
+            rows = self.ewms(path, clock, readout="terminal", output_format="flat")[:, None, :]
+        else:
+            rows = self.ewms(path, clock, readout="prefix", output_format="flat")
+        feat = ops.log_rows(rows, self.d, self.N, True, readout)
+        if single:
+            feat = feat[0]
         if output_format == "list":
-            if readout in ("mean", "max"):
-                raise ValueError(f"readout='{readout}' requires output_format='flat'")
             return self._split(feat)
-        if readout == "prefix":
-            return feat
-        if readout == "mean":
-            return feat.mean(-2)
-        return feat.max(-2).values
+        return feat
 
     def _split(self, feat):
         return [feat[..., s:e] for s, e in log_level_slices(self.d, self.N)]

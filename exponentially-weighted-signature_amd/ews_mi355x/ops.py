@@ -261,3 +261,45 @@ def dense_combine_backward(levels, flows, grad_out, N, readout="prefix", level0=
                                         _stream_handle(levels.device))
     nat.check(rc, "ews_dense_combine_backward")
     return gl, gf
+
+
+# ---------------------------------------------------------------------------------------------- log-signature
+class LogRows(torch.autograd.Function):
+    """Compressed log of EWS state rows (B, R, level0 + D) with the LogEWS readout (ews/layer.py:488-517):
+    ews_log_forward / ews_log_backward."""
+
+    @staticmethod
+    def forward(ctx, rows, d, N, level0, readout):
+        lib = nat.load()
+        if not rows.is_cuda or rows.dtype != torch.float32:
+            raise TypeError("rows must be a float32 tensor on the HIP device")
+        rows = rows.contiguous()
+        B, R = rows.shape[0], rows.shape[1]
+        desc = nat.LogDesc(B, R, d, N, int(level0), nat.READOUTS[readout])
+        Dlog = int(lib.ews_log_dim(d, N))
+        out = torch.empty((B, R, Dlog) if readout == "prefix" else (B, Dlog), device=rows.device,
+                          dtype=torch.float32)
+        ws = torch.empty(int(lib.ews_log_workspace_bytes(ctypes.byref(desc))), device=rows.device,
+                         dtype=torch.uint8)
+        nat.check(lib.ews_log_forward(ctypes.byref(desc), rows.data_ptr(), out.data_ptr(), ws.data_ptr(),
+                                      _stream_handle(rows.device)), "ews_log_forward")
+        ctx.save_for_backward(rows)
+        ctx.desc = desc
+        return out
+
+    @staticmethod
+    def backward(ctx, gout):
+        lib = nat.load()
+        (rows,) = ctx.saved_tensors
+        desc = ctx.desc
+        gout = gout.to(torch.float32).contiguous()
+        grows = torch.empty_like(rows)
+        ws = torch.empty(int(lib.ews_log_workspace_bytes(ctypes.byref(desc))), device=rows.device,
+                         dtype=torch.uint8)
+        nat.check(lib.ews_log_backward(ctypes.byref(desc), rows.data_ptr(), gout.data_ptr(), grows.data_ptr(),
+                                       ws.data_ptr(), _stream_handle(rows.device)), "ews_log_backward")
+        return grows, None, None, None, None
+
+
+def log_rows(rows, d, N, level0=True, readout="prefix"):
+    return LogRows.apply(rows, int(d), int(N), bool(level0), readout)

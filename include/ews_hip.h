@@ -185,6 +185,32 @@ int ews_dense_combine_backward(const ews_dense_desc* desc, const float* levels, 
                                const float* grad_out, float* grad_levels, float* grad_flows, void* workspace,
                                ews_stream_t stream);
 
+/* ---------------------------------------------------------------------------------------------------------
+ * Log-signature readout of LogEWS (ews/layer.py:440-556): per state row the truncated tensor log and its
+ * coefficients at the Lyndon words (signax.signature_to_logsignature), then the readout (log-then-pool).
+ * --------------------------------------------------------------------------------------------------------- */
+typedef struct ews_log_desc {
+  int32_t batch;   /* B >= 1 */
+  int32_t rows;    /* R state rows per sample (L-1 prefix rows, or 1 for the terminal readout) */
+  int32_t dim;     /* d: 1..64 (1..16 at depth 3) */
+  int32_t depth;   /* N in {1, 2, 3} */
+  int32_t level0;  /* 1: the rows carry the leading level-0 column */
+  int32_t readout; /* EWS_READOUT_*: prefix (B, R, Dlog), terminal / mean / max (B, Dlog) */
+} ews_log_desc;
+
+/* Dlog = sum_k W_d(k), the Witt numbers (ews/layer.py:417-425). */
+int ews_log_dim(int dim, int depth);
+size_t ews_log_workspace_bytes(const ews_log_desc* desc);
+
+/* rows (B, R, level0 + sum_k d^k) of EWS states -> out. Replaces the vmapped
+ * signax.signature_to_logsignature and the pooling of LogEWS._single_path (ews/layer.py:488-517). */
+int ews_log_forward(const ews_log_desc* desc, const float* sig_rows, float* out, void* workspace,
+                    ews_stream_t stream);
+
+/* Cotangent of the rows (level-0 column zero) for the cotangent grad_out of out. */
+int ews_log_backward(const ews_log_desc* desc, const float* sig_rows, const float* grad_out, float* grad_rows,
+                     void* workspace, ews_stream_t stream);
+
 /* Human-readable text of a return code. */
 const char* ews_error_string(int code);
 

@@ -110,6 +110,24 @@ def test_log_dims_mirror_reference():
     for d, N, expect in [(3, 3, 14), (4, 2, 10), (2, 4, 8)]:
         assert E.log_signature_dim(d, N) == expect
     assert E.log_level_slices(4, 2) == ((0, 4), (4, 10))
+    lib = nat.load()
+    for d, N in [(3, 3), (4, 2), (16, 3), (32, 2), (1, 3)]:  # the library's Witt numbers (host Duval)
+        assert lib.ews_log_dim(d, N) == E.log_signature_dim(d, N)
+    assert lib.ews_log_dim(4, 4) == 0
+
+
+def test_log_c_abi_error_codes():
+    lib = nat.load()
+    null = ctypes.c_void_p(0)
+    good = nat.LogDesc(2, 5, 16, 3, 1, 0)
+    assert lib.ews_log_workspace_bytes(ctypes.byref(good)) > 0
+    assert lib.ews_log_forward(ctypes.byref(good), null, null, null, null) == -1
+    bad = {"depth": (nat.LogDesc(2, 5, 4, 4, 1, 0), -3), "wide depth 3": (nat.LogDesc(2, 5, 17, 3, 1, 0), -2),
+           "terminal rows": (nat.LogDesc(2, 5, 4, 2, 1, 1), -2), "readout": (nat.LogDesc(2, 5, 4, 2, 1, 7), -4),
+           "rows": (nat.LogDesc(2, 0, 4, 2, 1, 0), -2)}
+    for name, (dsc, code) in bad.items():
+        assert lib.ews_log_forward(ctypes.byref(dsc), null, null, null, null) == code, name
+        assert lib.ews_log_workspace_bytes(ctypes.byref(dsc)) == 0, name
 
 
 def _ddesc(**kw):
