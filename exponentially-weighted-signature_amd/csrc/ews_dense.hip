@@ -593,6 +593,59 @@ __device__ __forceinline__ void series_mats(const LdsTable* sp, int scheme, floa
   wave_order_d();
 }
 
+// Just outside a rational scheme's series radius (x = |c| ||A||_1 below 0.85 of it) the truncated series of
+// N^{-1} still has a residual E = I - N X below 1/2, and Newton-Schulz iterations X <- X (2I - N X) square it
+// (I - N X' = E^2): a few 16 x 16 products instead of a Gauss-Jordan elimination. iters: the squarings that take the
+// bound ||E|| <= x_r^13 / (1 - x_r) (1 + x), x_r = x / radius, below 1e-9.
+__device__ __forceinline__ bool ns_iters(int scheme, float x, int& iters) {
+  const float rho = scheme == EWS_EXPM_CAYLEY ? 2.0f : (scheme == EWS_EXPM_EULER ? 1.0f : 3.4641016f);
+  const float r = x / rho;
+  if (!(r < 0.85f)) return false;
+  float r13 = r;
+#pragma unroll
+  for (int k = 1; k < 13; ++k) r13 *= r;
+  float e = r13 / (1.0f - r) * (1.0f + x);
+  if (!(e < 0.5f)) return false;
+  iters = 0;
+  while (e > 1e-9f && iters < 6) {
+    e *= e;
+    ++iters;
+  }
+  return true;
+}
+
+// X <- X (2I - N X), iters times, N = I + alpha A + beta A^2 (from the table: A = P_1, A^2 = 2 P_2); X in LDS
+// (row-major 16 x 16), R: 256 floats of LDS scratch.
+__device__ __forceinline__ void wave_ns(const LdsTable* sp, float alpha, float beta, float* X, float* R, int iters,
+                                        int l) {
+  const int i = l >> 2, j0 = 4 * (l & 3);
+  for (int it = 0; it < iters; ++it) {
+    f4 y = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int k = 0; k < 16; ++k) {
+      const float nik = (i == k ? 1.0f : 0.0f) + alpha * sp[1][i * 16 + k] + 2.0f * beta * sp[2][i * 16 + k];
+      const f4 xk = *reinterpret_cast<const f4*>(X + k * 16 + j0);
+#pragma unroll
+      for (int r = 0; r < 4; ++r) y[r] = fmaf(nik, xk[r], y[r]);
+    }
+#pragma unroll
+    for (int r = 0; r < 4; ++r) y[r] = (i == j0 + r ? 2.0f : 0.0f) - y[r];
+    *reinterpret_cast<f4*>(R + 4 * l) = y;
+    wave_order_d();
+    f4 z = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int k = 0; k < 16; ++k) {
+      const float xik = X[i * 16 + k];
+      const f4 rk = *reinterpret_cast<const f4*>(R + k * 16 + j0);
+#pragma unroll
+      for (int r = 0; r < 4; ++r) z[r] = fmaf(xik, rk[r], z[r]);
+    }
+    wave_order_d();
+    *reinterpret_cast<f4*>(X + 4 * l) = z;
+    wave_order_d();
+  }
+}
+
 // The matrix functions of one step c under a scheme of ews/core/expm_approx.py:13-41.
 //   flow = true:  P = expm_scheme(-c A):   exact exp(-cA); euler I - cA; cayley (I + cA/2)^{-1} (I - cA/2)
 //                 = 2 (I + cA/2)^{-1} - I; pade (I + cA/2 + c^2A^2/12)^{-1} (I - cA/2 + c^2A^2/12)
@@ -626,7 +679,13 @@ __device__ __forceinline__ void wave_matfn(const LdsTable* sp, float norm1, int 
   const float alpha = scheme == EWS_EXPM_EULER ? c : 0.5f * c;
   const float beta = scheme == EWS_EXPM_PADE ? c * c * (1.0f / 12.0f) : 0.0f;
   float* inv = flow ? T : V;
-  wave_inverse(sp, alpha, beta, inv, T + 256, l);
+  int nsit;
+  if (ns_iters(scheme, fabsf(c) * norm1, nsit)) {
+    series_mats(sp, scheme, c, false, P, inv, l);  // the truncated series of N^{-1} (P is scratch here)
+    wave_ns(sp, alpha, beta, inv, P, nsit, l);
+  } else {
+    wave_inverse(sp, alpha, beta, inv, T + 256, l);
+  }
   const f4 vi = *reinterpret_cast<const f4*>(inv + 4 * l);
   f4 e;
   if (scheme == EWS_EXPM_CAYLEY) {
@@ -764,8 +823,8 @@ __device__ __forceinline__ float dot16(const f4* r, const f4* x) {
   return (s0 + s1) + (s2 + s3);
 }
 
-template <int N>
-__global__ __launch_bounds__(256) void k_vl(Args a) {
+template <int N, bool EXACTF>  // EXACTF: exact flows (only the scaled exponential is compiled for them)
+__global__ __launch_bounds__(256, 2) void k_vl(Args a) {
   extern __shared__ __align__(16) float lds[];
   LdsTable* sp = reinterpret_cast<LdsTable*>(lds);
   const int tid = threadIdx.x, w = tid >> 6, l = tid & 63, g = l >> 4, c16 = l & 15;
@@ -784,7 +843,24 @@ __global__ __launch_bounds__(256) void k_vl(Args a) {
     const int b = (int)(it / a.n_int), t = (int)(it - (long)b * a.n_int);
     const float* th = a.clock + (size_t)b * a.L;
     wave_order_d();  // the previous interval's reads of the segment table come first
-    write_flow(a, sp, norm1, b, t, th, P, T, l);
+    if constexpr (EXACTF) {
+      bool ident;
+      const float hf = flow_step(a, th, t, ident);
+      f4 m;
+      if (ident) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) m[r] = ((4 * l + r) >> 4) == ((4 * l + r) & 15) ? 1.0f : 0.0f;
+      } else if (a.flow_mode != EWS_FLOW_PER_INTERVAL) {
+        m = *reinterpret_cast<const f4*>(a.mats + (size_t)b * 768 + 512 + 4 * l);
+      } else {
+        wave_expm(sp, norm1, hf, P, nullptr, l);
+        m = *reinterpret_cast<const f4*>(P + 4 * l);
+        wave_order_d();
+      }
+      *reinterpret_cast<f4*>(a.fl + ((size_t)b * a.n_int + t) * 256 + 4 * l) = m;
+    } else {
+      write_flow(a, sp, norm1, b, t, th, P, T, l);
+    }
     // step matrices
     if (a.vl_mode == EWS_FLOW_PER_INTERVAL) {
       wave_matfn(sp, norm1, a.vl_expm, (th[t + 1] - th[t]) / (float)Mv, false, P, V, T, l);
@@ -2406,9 +2482,16 @@ int launch_vl_and_flows(const DPlan& p, const Args& a, hipStream_t st) {
     const long blocks = (total + nw - 1) / nw;
     const int grid = (int)(blocks < 8192 ? blocks : 8192);
     const size_t shm = table + nw * region;
-    if (p.N == 1) hipLaunchKernelGGL((k_vl<1>), dim3(grid), dim3(64 * nw), shm, st, a);
-    else if (p.N == 2) hipLaunchKernelGGL((k_vl<2>), dim3(grid), dim3(64 * nw), shm, st, a);
-    else hipLaunchKernelGGL((k_vl<3>), dim3(grid), dim3(64 * nw), shm, st, a);
+    const bool ex = p.chen_expm == EWS_EXPM_EXACT;
+#define EWS_VL(NN)                                                                                   \
+  do {                                                                                               \
+    if (ex) hipLaunchKernelGGL((k_vl<NN, true>), dim3(grid), dim3(64 * nw), shm, st, a);            \
+    else hipLaunchKernelGGL((k_vl<NN, false>), dim3(grid), dim3(64 * nw), shm, st, a);              \
+  } while (0)
+    if (p.N == 1) EWS_VL(1);
+    else if (p.N == 2) EWS_VL(2);
+    else EWS_VL(3);
+#undef EWS_VL
     DENSE_CHECK();
   }
   if (!vl && p.chen_expm != EWS_EXPM_EXACT) {  // the Van Loan kernel writes its flows itself
