@@ -257,15 +257,14 @@ __global__ __launch_bounds__(256) void k_local(Args a) {
 // four degrees per slice set, sixteen output tiles, tile i holding s3[.][i][.]). Rows p > q of the letter
 // buffer stay zero, so the unrolled k-steps over whole groups of four degrees add nothing beyond the order q.
 template <int QB>
-__global__ __launch_bounds__(256) void k_local3(Args a) {
+__global__ __launch_bounds__(256, 3) void k_local3(Args a) {
   constexpr int QB4 = (QB + 4) / 4 * 4;  // letter rows 0 .. QB4-1 (QB + 1 rounded up to whole k-steps)
   constexpr int G2S = 16 * RP + 16;      // LDS floats per degree slice (row pitch RP; slices on offset banks)
   constexpr int NINV = 2 * QB4 + 8;      // reciprocals 1/n, n < NINV (no divisions in the loops)
   __shared__ __align__(16) float sp[PM + 1][256];   // P_p = A^p / p!, p <= PM (flows; P_1 = A)
   __shared__ __align__(16) float lt[4][QB4 * 16];   // letters b_p of each wave's interval
   __shared__ __align__(16) float gt[4][QB4 * 16];   // g1_n = b_n / (n + 1)
-  __shared__ __align__(16) float g2b[4][4 * G2S];   // four degree slices of g2 per wave
-  __shared__ __align__(16) float mmw[4][256];       // flow squarings per wave
+  __shared__ __align__(16) float g2b[4][4 * G2S];   // four degree slices of g2 per wave (then the flow squarings)
   __shared__ float inv[NINV];
   const int tid = threadIdx.x, w = tid >> 6, l = tid & 63, g = l >> 4, c16 = l & 15;
   const int q = a.q;
@@ -380,7 +379,7 @@ __global__ __launch_bounds__(256) void k_local3(Args a) {
 #pragma unroll
           for (int r = 0; r < 4; ++r) m[r] = fmaf(m[r], y, c[r]);
         }
-        float* mm = mmw[w];
+        float* mm = g2b[w];  // the degree slices are done
         const int i = l >> 2, j0 = 4 * (l & 3);
         for (int r2 = 0; r2 < sq; ++r2) {
           *reinterpret_cast<f4*>(mm + 4 * l) = m;
