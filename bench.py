@@ -47,7 +47,7 @@ def make_inputs(B=32, L=17984, c=6, d=16, seed_cfg=2):
     K = d // 2
     damp = rng2.uniform(0.01, 1.0, K)
     freq = rng2.uniform(0.0, np.pi, K)
-    # BASELINE writes exp(A tau) with Re A < 0; the reference discounts with exp(-tau A_ref), A_ref = -A: plane j
+    # the benchmark writes exp(A tau) with Re A < 0; the reference discounts with exp(-tau A_ref), A_ref = -A: plane j
     # of A_ref is [[a_j, w_j], [-w_j, a_j]] with a_j the damping and w_j the frequency
     dw = np.stack([damp, freq], -1).astype(np.float32)
     clock = np.broadcast_to((np.arange(L, dtype=np.float64) / L).astype(np.float32), (B, L)).copy()
@@ -199,9 +199,37 @@ def algorithmic_bytes(B, L, d, W, s_in=4):
         "chunk_adjoint_local": n * (4 * W + s_in * (d + 1)),   # read cotangent rows + inputs
         "chunk_summary": n * s_in * (d + 1),
         "knot_grads": n * 2 * 4 * (d + 1),
-        "fwd_total": n * (s_in * (d + 1) + 4 * D),             # BASELINE.md bytes_fwd
-        "bwd_total": n * (4 * D + 2 * s_in * (d + 1)),         # BASELINE.md bytes_bwd
+        "fwd_total": n * (s_in * (d + 1) + 4 * D),             # compulsory forward bytes
+        "bwd_total": n * (4 * D + 2 * s_in * (d + 1)),         # compulsory backward bytes (recompute)
     }
+
+
+# kernel of each c2 pass whose HBM traffic the PMC summary records
+PASS_KERNELS = {
+    "chunk_summary": "pairs::k_fwd<false, false>",
+    "chunk_output": "pairs::k_fwd<true, false>",
+    "chunk_adjoint_local": "pairs::k_bwd_local<false>",
+    "chunk_adjoint_full": "pairs::k_bwd_full<false, false>",
+}
+PMC_SUMMARY = os.path.join(ROOT, "profiles", "c2_fwd_bwd_pmc_traffic.md")
+
+
+def pmc_traffic(pass_name, path=PMC_SUMMARY):
+    """HBM bytes per launch of the pass's kernel from the committed rocprofv3 PMC summary (FETCH_SIZE x2 +
+    WRITE_SIZE, calibrated on a plain copy): (bytes, source) or (None, None) when the summary or the row is
+    absent. The counters cannot be read inside a timed run, so the figure is that of the profiled build."""
+    kern = PASS_KERNELS.get(pass_name)
+    if kern is None or not os.path.exists(path):
+        return None, None
+    with open(path) as f:
+        for line in f:
+            cells = [c.strip() for c in line.strip().strip("|").split("|")]
+            if len(cells) >= 4 and kern in cells[0]:
+                try:
+                    return float(cells[3]) * 1e6, os.path.relpath(path, ROOT)
+                except ValueError:
+                    return None, None
+    return None, None
 
 
 def cpu_baseline(path, clock, dw, g, budget_s=12.0):
@@ -288,11 +316,15 @@ def main():
     path_np, clock_np, dw_np = make_inputs(B, L, c, d)
     W = 1 + d + d * d
     rng = np.random.default_rng([2, 5])
-    g_np = rng.normal(size=(B, L - 1, W)).astype(np.float32) / np.sqrt(W)
+    g_np = (rng.normal(size=(B, L - 1, W)) / np.sqrt(W)).astype(np.float32)
     path = torch.tensor(path_np, device=dev)
     clock = torch.tensor(clock_np, device=dev)
     dw = torch.tensor(dw_np, device=dev)
     gout = torch.tensor(g_np, device=dev)
+    # the C ABI reads raw float32 buffers: a wider array here would be reinterpreted, not converted
+    for nm, t in (("path", path), ("clock", clock), ("params", dw), ("grad_out", gout)):
+        if t.dtype != torch.float32 or not t.is_contiguous():
+            raise TypeError(f"bench input {nm} must be contiguous float32, got {t.dtype}")
     desc = make_desc(B, L, d, N, nat.STRUCT_PLANES, nat.FLOW_PER_INTERVAL, "prefix", True, nat.DTYPE_F32,
                      args.chunk)
     ws = torch.empty(int(lib.ews_diag_workspace_bytes(ctypes.byref(desc))), device=dev, dtype=torch.uint8)
@@ -330,7 +362,7 @@ def main():
 
     # sanity: the layer API on the same inputs gives the same forward rows
     A = E.AParamConstant(torch.zeros(d, d))
-    check_rows = None
+    check_rows = check_grad = None
     if args.check:
         from oracle import cbuild
         from oracle import cpu_scan_py as C
@@ -339,6 +371,10 @@ def main():
         ref = C.planes_forward(path_np[:2], clock_np[:2], dw_np, kind="f64")
         got = out[:2].cpu().numpy().astype(np.float64)
         check_rows = float(np.abs(got - ref).max() / np.abs(ref).max())
+        # path gradient of the first two samples (a per-sample quantity) against the float64 checker
+        ref_dp, _, _ = C.planes_backward(path_np[:2], clock_np[:2], dw_np, g_np[:2], kind="f64")
+        got_dp = dpath[:2].cpu().numpy().astype(np.float64)
+        check_grad = float(np.abs(got_dp - ref_dp).max() / np.abs(ref_dp).max())
     del A
 
     per_step_events = []
@@ -367,8 +403,12 @@ def main():
     roof = None
     if dom_bytes is not None:
         achieved = dom_bytes / (pass_ms[dominant] * 1e-3) / 1e9
+        traffic, source = pmc_traffic(dominant)
         roof = {"bound": "hbm", "kernel": dominant, "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
-                "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None}
+                "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
+                "traffic": None if traffic is None else round(traffic), "algorithmic_bytes": dom_bytes}
+        if source is not None:
+            roof["traffic_source"] = source
     steps_per_s = B * (L - 1) / (ms_per_step * 1e-3)
     fwdbwd_bytes = ab["fwd_total"] + ab["bwd_total"]
     result = {
@@ -396,6 +436,7 @@ def main():
     }
     if check_rows is not None:
         result["check_forward_relerr_vs_f64"] = check_rows
+        result["check_path_grad_relerr_vs_f64"] = check_grad
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline(path_np, clock_np, dw_np, g_np)
     print(json.dumps(result), flush=True)

@@ -256,8 +256,9 @@ __global__ __launch_bounds__(256) void k_local(Args a) {
 // time go through LDS and feed the level-3 contraction s3[a][i][j] = sum_N bt_N[a] g2_N[i][j] (one k-step of
 // four degrees per slice set, sixteen output tiles, tile i holding s3[.][i][.]). Rows p > q of the letter
 // buffer stay zero, so the unrolled k-steps over whole groups of four degrees add nothing beyond the order q.
+// Three workgroups per CU fit the LDS of the orders up to 24; the order-40 tables hold two.
 template <int QB>
-__global__ __launch_bounds__(256, 3) void k_local3(Args a) {
+__global__ __launch_bounds__(256, QB <= 24 ? 3 : 2) void k_local3(Args a) {
   constexpr int QB4 = (QB + 4) / 4 * 4;  // letter rows 0 .. QB4-1 (QB + 1 rounded up to whole k-steps)
   constexpr int G2S = 16 * RP + 16;      // LDS floats per degree slice (row pitch RP; slices on offset banks)
   constexpr int NINV = 2 * QB4 + 8;      // reciprocals 1/n, n < NINV (no divisions in the loops)
