@@ -447,7 +447,7 @@ __device__ __forceinline__ int classify_chunk(const DiagArgs& a, int b, int c, i
 
 // ------------------------------------------------------------------------------------------------ carries
 // Float64 Chen combine of the chunk summaries in quads of four chunks (the chunks of one forward workgroup):
-// every quad's summary in parallel (k_quad_fwd_agg), one sequential scan over the quads of each sample
+// every quad's summary in parallel (k_quad_fwd_agg), one blocked scan over the quads of each sample
 // (k_quad_fwd_scan), and the carries inside a quad rebuilt by the prefix-row kernel from the quad's carry
 // (at most three combines). The adjoint carries mirror it (k_quad_bwd_agg / k_quad_bwd_scan / full adjoint).
 // Lane view of these kernels: 64 lanes, lane = 8 j + k holds level 1 of plane j and the pair (j, k).
@@ -564,18 +564,30 @@ __global__ __launch_bounds__(64) void k_quad_fwd_agg(DiagArgs a) {
   store_st_f(a.qagg + ((size_t)b * a.NQ + q) * a.D, j, k, s);
 }
 
-// Sequential scans over the quads of one sample: the quad inputs are staged into LDS a segment at a time by the
-// whole workgroup (one round trip to memory per segment), then wavefront 0 runs the chain from LDS with the next
-// step's operands loaded while the current one combines.
-constexpr int QSEG = 48;                    // quads per staged segment
+// Scans over the quads of one sample, one workgroup of SW wavefronts per sample. The quad inputs are staged into
+// LDS a segment of up to SSEG quads at a time by the whole workgroup; the segment's quads are split into SW blocks
+// of consecutive quads, one per wavefront:
+//   1. every wavefront combines its block from a zero state (the block's summary and flow);
+//   2. wavefront 0 chains the SW block summaries from the segment's carry (the block carries);
+//   3. every wavefront rescans its block from its block carry and writes the carry of each quad.
+// The float64 dependency chain per segment is thus (block length) + SW + (block length) combines instead of one
+// per quad (26 instead of 71 at c2). Every wavefront reads its next operands from LDS while the current combine
+// runs. Lane view: lane = 8 j + k holds level 1 of plane j and the pair (j, k).
+constexpr int SW = 8;                       // wavefronts of a scan workgroup
+constexpr int SBQ = 9;                      // quads per wavefront block of a full segment
+constexpr int SSEG = SW * SBQ;              // quads per staged segment
 constexpr int QROW = DIM + DIM * DIM;       // floats of a quad's state
-struct QSeg {
-  float y[QSEG][QROW];                      // quad summary / adjoint aggregate (float32)
-  dc F[QSEG][K];                            // quad flows
-  dc l1[QSEG][K];                           // quad level-1 increments (adjoint scan)
+struct ScanLds {
+  float y[SSEG][QROW];                      // quad summary / adjoint aggregate (float32)
+  dc F[SSEG][K];                            // quad flows
+  dc l1[SSEG][K];                           // quad level-1 increments (adjoint scan)
+  dc bS1[SW][64], bSA[SW][64], bSB[SW][64]; // per block: summary (phase 1), then carry (phase 2), lane layout
+  dc bF[SW][K];                             // block flows
+  dc bl1[SW][K];                            // block level-1 increments (adjoint scan)
 };
-__device__ __forceinline__ void stage_qseg(const DiagArgs& a, int b, int q0, int nq, bool with_l1, QSeg& sg) {
-  constexpr int U = 8, R4 = QROW / 4;
+constexpr size_t kScanLds = sizeof(ScanLds);
+__device__ __forceinline__ void stage_seg(const DiagArgs& a, int b, int q0, int nq, bool with_l1, ScanLds& sg) {
+  constexpr int U = 4, R4 = QROW / 4;
   const float* src = a.qagg + ((size_t)b * a.NQ + q0) * a.D;
   for (int ib = threadIdx.x; ib < nq * R4; ib += U * blockDim.x) {
     f4a v[U];
@@ -601,7 +613,7 @@ struct QOps {
   PairSt y;
   dc y1k, Fj, Fk, l1k;
 };
-__device__ __forceinline__ QOps q_ops(const QSeg& sg, int q, int j, int k, bool with_l1) {
+__device__ __forceinline__ QOps q_ops(const ScanLds& sg, int q, int j, int k, bool with_l1) {
   QOps o;
   o.y = load_st_f(sg.y[q], j, k);
   o.y1k = ld_fd(sg.y[q] + 2 * k);
@@ -610,28 +622,72 @@ __device__ __forceinline__ QOps q_ops(const QSeg& sg, int q, int j, int k, bool 
   o.l1k = with_l1 ? sg.l1[q][k] : dc{0.0, 0.0};
   return o;
 }
+// block [lo, hi) of a segment of nq quads for wavefront w
+__device__ __forceinline__ void seg_block(int nq, int w, int& lo, int& hi) {
+  const int bq = (nq + SW - 1) / SW;
+  lo = min(w * bq, nq);
+  hi = min(lo + bq, nq);
+}
+__device__ __forceinline__ void put_block(ScanLds& sg, int w, int l, const PairSt& s) {
+  sg.bS1[w][l] = s.S1;
+  sg.bSA[w][l] = s.SA;
+  sg.bSB[w][l] = s.SB;
+}
+__device__ __forceinline__ PairSt get_block(const ScanLds& sg, int w, int l) {
+  return PairSt{sg.bS1[w][l], sg.bSA[w][l], sg.bSB[w][l]};
+}
 
-__global__ __launch_bounds__(256) void k_quad_fwd_scan(DiagArgs a) {
-  __shared__ QSeg sg;
-  const int b = blockIdx.x, j = (threadIdx.x & 63) >> 3, k = threadIdx.x & 7;
-  const bool w0 = threadIdx.x < 64;
-  PairSt s{};
-  for (int q0 = 0; q0 < a.NQ; q0 += QSEG) {
-    const int nq = min(QSEG, a.NQ - q0);
-    stage_qseg(a, b, q0, nq, false, sg);
+__global__ __launch_bounds__(SW * 64) void k_quad_fwd_scan(DiagArgs a) {
+  extern __shared__ __align__(16) char scan_smem[];
+  ScanLds& sg = *reinterpret_cast<ScanLds*>(scan_smem);
+  const int b = blockIdx.x, w = threadIdx.x >> 6, l = threadIdx.x & 63, j = l >> 3, k = l & 7;
+  PairSt carry{};  // segment carry, kept by wavefront 0
+  for (int q0 = 0; q0 < a.NQ; q0 += SSEG) {
+    const int nq = min(SSEG, a.NQ - q0);
+    stage_seg(a, b, q0, nq, false, sg);
     __syncthreads();
-    if (w0) {
-      QOps o = q_ops(sg, 0, j, k, false);
-      for (int q = 0; q < nq; ++q) {
-        store_st_d(a.carries + ((size_t)b * (a.C + 1) + 4 * (q0 + q)) * a.D, j, k, s);
-        const QOps cur = o;
-        if (q + 1 < nq) o = q_ops(sg, q + 1, j, k, false);
-        chen_d(s, cur.Fj, cur.Fk, cur.y.S1, cur.y1k, cur.y.SA, cur.y.SB);
+    int lo, hi;
+    seg_block(nq, w, lo, hi);
+    {  // 1. block summary and flow from a zero state
+      PairSt s{};
+      dc Fj{1.0, 0.0};
+      if (lo < hi) {
+        QOps o = q_ops(sg, lo, j, k, false);
+        for (int q = lo; q < hi; ++q) {
+          const QOps cur = o;
+          if (q + 1 < hi) o = q_ops(sg, q + 1, j, k, false);
+          chen_d(s, cur.Fj, cur.Fk, cur.y.S1, cur.y1k, cur.y.SA, cur.y.SB);
+          Fj = Fj * cur.Fj;
+        }
+      }
+      put_block(sg, w, l, s);
+      if (k == 0) sg.bF[w][j] = Fj;
+    }
+    __syncthreads();
+    if (w == 0) {  // 2. block carries
+      for (int v = 0; v < SW; ++v) {
+        const PairSt y = get_block(sg, v, l);
+        const dc y1k = sg.bS1[v][8 * k];
+        const dc Fj = sg.bF[v][j], Fk = sg.bF[v][k];
+        wave_order();  // every lane has read block v before its slot is overwritten
+        put_block(sg, v, l, carry);
+        chen_d(carry, Fj, Fk, y.S1, y1k, y.SA, y.SB);
       }
     }
     __syncthreads();
+    if (lo < hi) {  // 3. quad carries inside the block
+      PairSt s = get_block(sg, w, l);
+      QOps o = q_ops(sg, lo, j, k, false);
+      for (int q = lo; q < hi; ++q) {
+        store_st_d(a.carries + ((size_t)b * (a.C + 1) + 4 * (q0 + q)) * a.D, j, k, s);
+        const QOps cur = o;
+        if (q + 1 < hi) o = q_ops(sg, q + 1, j, k, false);
+        chen_d(s, cur.Fj, cur.Fk, cur.y.S1, cur.y1k, cur.y.SA, cur.y.SB);
+      }
+    }
+    __syncthreads();  // the segment's LDS is restaged next
   }
-  if (w0) store_st_d(a.carries + ((size_t)b * (a.C + 1) + a.C) * a.D, j, k, s);
+  if (w == 0) store_st_d(a.carries + ((size_t)b * (a.C + 1) + a.C) * a.D, j, k, carry);
 }
 
 __global__ __launch_bounds__(64) void k_quad_bwd_agg(DiagArgs a) {
@@ -652,27 +708,64 @@ __global__ __launch_bounds__(64) void k_quad_bwd_agg(DiagArgs a) {
   store_st_f(a.qagg + ((size_t)b * a.NQ + q) * a.D, j, k, X);
 }
 
-__global__ __launch_bounds__(256) void k_quad_bwd_scan(DiagArgs a) {
-  __shared__ QSeg sg;
-  const int b = blockIdx.x, j = (threadIdx.x & 63) >> 3, k = threadIdx.x & 7;
-  const bool w0 = threadIdx.x < 64;
-  PairSt X{};
-  for (int qe = a.NQ; qe > 0; qe -= QSEG) {
-    const int nq = min(QSEG, qe), q0 = qe - nq;
-    stage_qseg(a, b, q0, nq, true, sg);
+// Reverse scan of the adjoint carries, blocked as the forward scan: a block's aggregate is its cotangent at the
+// block start from a zero cotangent at its end; its transfer is adj_d over the block's span (block flow and
+// level-1 increment, carry1(end) - F carry1(start)).
+__global__ __launch_bounds__(SW * 64) void k_quad_bwd_scan(DiagArgs a) {
+  extern __shared__ __align__(16) char scan_smem[];
+  ScanLds& sg = *reinterpret_cast<ScanLds*>(scan_smem);
+  const int b = blockIdx.x, w = threadIdx.x >> 6, l = threadIdx.x & 63, j = l >> 3, k = l & 7;
+  PairSt X{};  // cotangent at the segment end, kept by wavefront 0
+  for (int qe = a.NQ; qe > 0; qe -= SSEG) {
+    const int nq = min(SSEG, qe), q0 = qe - nq;
+    stage_seg(a, b, q0, nq, true, sg);
     __syncthreads();
-    if (w0) {
-      QOps o = q_ops(sg, nq - 1, j, k, true);
-      for (int q = nq - 1; q >= 0; --q) {
-        const int qq = q0 + q, c1 = min(4 * qq + 4, a.C);
-        store_st_f(a.mt + ((size_t)b * a.C + c1 - 1) * a.D, j, k, X);
-        const QOps cur = o;
-        if (q > 0) o = q_ops(sg, q - 1, j, k, true);
-        adj_d(X, cur.Fj, cur.Fk, cur.l1k);
-        add_st(X, cur.y);
+    int lo, hi;
+    seg_block(nq, w, lo, hi);
+    {  // 1. block aggregate from a zero cotangent at the block end; block flow and level-1 increment
+      PairSt Xl{};
+      dc Fk{1.0, 0.0};
+      if (lo < hi) {
+        QOps o = q_ops(sg, hi - 1, j, k, true);
+        for (int q = hi - 1; q >= lo; --q) {
+          const QOps cur = o;
+          if (q > lo) o = q_ops(sg, q - 1, j, k, true);
+          adj_d(Xl, cur.Fj, cur.Fk, cur.l1k);
+          add_st(Xl, cur.y);
+          Fk = Fk * cur.Fk;
+        }
+      }
+      put_block(sg, w, l, Xl);
+      if (j == 0) {
+        sg.bF[w][k] = Fk;
+        const int c0 = 4 * (q0 + lo), c1 = min(4 * (q0 + hi), a.C);
+        sg.bl1[w][k] = lo < hi ? l1_inc(a, b, c0, c1, k, Fk) : dc{0.0, 0.0};
       }
     }
     __syncthreads();
+    if (w == 0) {  // 2. cotangents at the block ends, last block first
+      for (int v = SW - 1; v >= 0; --v) {
+        const PairSt y = get_block(sg, v, l);
+        const dc Fj = sg.bF[v][j], Fk = sg.bF[v][k], l1k = sg.bl1[v][k];
+        put_block(sg, v, l, X);
+        adj_d(X, Fj, Fk, l1k);
+        add_st(X, y);
+      }
+    }
+    __syncthreads();
+    if (lo < hi) {  // 3. the cotangent at the last chunk of each quad of the block
+      PairSt Xq = get_block(sg, w, l);
+      QOps o = q_ops(sg, hi - 1, j, k, true);
+      for (int q = hi - 1; q >= lo; --q) {
+        const int c1 = min(4 * (q0 + q) + 4, a.C);
+        store_st_f(a.mt + ((size_t)b * a.C + c1 - 1) * a.D, j, k, Xq);
+        const QOps cur = o;
+        if (q > lo) o = q_ops(sg, q - 1, j, k, true);
+        adj_d(Xq, cur.Fj, cur.Fk, cur.l1k);
+        add_st(Xq, cur.y);
+      }
+    }
+    __syncthreads();  // the segment's LDS is restaged next
   }
 }
 
@@ -1360,14 +1453,20 @@ int pairs_forward(const DiagArgs& a, hipStream_t st, bool out) {
 }
 
 int pairs_carry_scan(const DiagArgs& a, hipStream_t st, bool backward) {
+  // the scan workgroups stage a segment of quads in more LDS than a static allocation may hold
+  const void* scan = backward ? reinterpret_cast<const void*>(&pairs::k_quad_bwd_scan)
+                              : reinterpret_cast<const void*>(&pairs::k_quad_fwd_scan);
+  if (hipFuncSetAttribute(scan, hipFuncAttributeMaxDynamicSharedMemorySize, (int)pairs::kScanLds) != hipSuccess)
+    return -1;
+  const dim3 sgrid(a.B), sblk(pairs::SW * 64);
   if (backward) {
     hipLaunchKernelGGL(pairs::k_quad_bwd_agg, dim3(a.NQ, a.B), dim3(64), 0, st, a);
     if (hipGetLastError() != hipSuccess) return -1;
-    hipLaunchKernelGGL(pairs::k_quad_bwd_scan, dim3(a.B), dim3(256), 0, st, a);
+    hipLaunchKernelGGL(pairs::k_quad_bwd_scan, sgrid, sblk, pairs::kScanLds, st, a);
   } else {
     hipLaunchKernelGGL(pairs::k_quad_fwd_agg, dim3(a.NQ, a.B), dim3(64), 0, st, a);
     if (hipGetLastError() != hipSuccess) return -1;
-    hipLaunchKernelGGL(pairs::k_quad_fwd_scan, dim3(a.B), dim3(256), 0, st, a);
+    hipLaunchKernelGGL(pairs::k_quad_fwd_scan, sgrid, sblk, pairs::kScanLds, st, a);
   }
   return hipGetLastError() == hipSuccess ? 0 : -1;
 }

@@ -120,6 +120,15 @@ def test_uniform_chunks_run_in_pair_kernels(B, L):
         assert (flags & 3 == 3).all(), flags
 
 
+def test_multi_segment_carry_scans():
+    # the carry scans stage 72 quads (288 chunks) per segment, in 8 wavefront blocks: 145 quads make two full
+    # segments and a last one of a single quad, whose other seven blocks are empty
+    L = 1 + 64 * 4 * 144 + 37
+    path, clock, dw = _inputs(1, L, seed=11)
+    flags = _check(path, clock, dw)
+    assert (flags & 3 == 3).all(), flags
+
+
 def test_mixed_chunks():
     path, clock, dw = _inputs(2, 600, seed=3, jitter_chunks=(1, 4))
     flags = _check(path, clock, dw)
