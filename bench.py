@@ -79,6 +79,193 @@ def c3_inputs(B=16, L=4096, c=8, d=16, seed_cfg=3):
     return path, clock, A
 
 
+def c1_inputs(B=8, L=1024, d=8, seed_cfg=1):
+    """time-augmented channels [t, W1, W2] with N(0, 1/L) Brownian increments, lifted
+    to d = 8 by W ~ N(0, 1/3) with the time channel kept as lifted channel 0; real diagonal A = diag(U(0.1, 2));
+    uniform clock k/L."""
+    c = 3
+    inc = np.random.default_rng([seed_cfg, 0]).normal(0.0, np.sqrt(1.0 / L), size=(B, L - 1, c - 1))
+    t = np.broadcast_to(np.arange(L, dtype=np.float64) / L, (B, L))[..., None]
+    raw = np.concatenate([t, np.concatenate([np.zeros((B, 1, c - 1)), np.cumsum(inc, 1)], 1)], -1)
+    Wl = np.random.default_rng([seed_cfg, 1]).normal(0.0, np.sqrt(1.0 / c), size=(d, c))
+    Wl[0] = 0.0
+    Wl[0, 0] = 1.0
+    path = (raw @ Wl.T).astype(np.float32)
+    A = np.random.default_rng([seed_cfg, 2]).uniform(0.1, 2.0, d).astype(np.float32)
+    clock = np.broadcast_to((np.arange(L, dtype=np.float64) / L).astype(np.float32), (B, L)).copy()
+    return path, clock, A
+
+
+def c4_inputs(B=256, L=512, d=32, vocab=8, seed_cfg=4):
+    """BASELINE.json configs[3], one block's scan input: uniform tokens of a vocabulary of 8 embedded by an
+    N(0, std 1/sqrt(32)) table (the path, value mode); real diagonal A = diag(U(0.1, 2)); the block's default
+    clock arange(L)."""
+    tok = np.random.default_rng([seed_cfg, 4]).integers(0, vocab, size=(B, L))
+    emb = np.random.default_rng([seed_cfg, 1]).normal(0.0, 1.0 / np.sqrt(d), size=(vocab, d))
+    path = emb[tok].astype(np.float32)
+    A = np.random.default_rng([seed_cfg, 2]).uniform(0.1, 2.0, d).astype(np.float32)
+    clock = np.broadcast_to(np.arange(L, dtype=np.float32), (B, L)).copy()
+    return path, clock, A
+
+
+def c5_inputs(B=8, L=49920, c=6, d=24, seed_cfg=5):
+    """BASELINE.json configs[4], one block's scan input: c channels of 4 sinusoids (frequencies U(0.5, 3) Hz,
+    random phases) sampled at 32 Hz plus N(0, 0.05) noise, lifted to d = 24 by W ~ N(0, 1/c); 12 rotation planes
+    (damping U(0.01, 1), frequency U(0, pi)); uniform clock k/L; bfloat16 path."""
+    r0 = np.random.default_rng([seed_cfg, 0])
+    tt = np.arange(L) / 32.0
+    f = r0.uniform(0.5, 3.0, size=(B, c, 4))
+    ph = r0.uniform(0.0, 2 * np.pi, size=(B, c, 4))
+    sig = np.sin(2 * np.pi * f[..., None] * tt + ph[..., None]).sum(2)  # (B, c, L)
+    raw = sig.transpose(0, 2, 1) + r0.normal(0.0, np.sqrt(0.05), size=(B, L, c))
+    Wl = np.random.default_rng([seed_cfg, 1]).normal(0.0, np.sqrt(1.0 / c), size=(d, c))
+    path = (raw @ Wl.T).astype(np.float32)
+    r2 = np.random.default_rng([seed_cfg, 2])
+    dw = np.stack([r2.uniform(0.01, 1.0, d // 2), r2.uniform(0.0, np.pi, d // 2)], -1).astype(np.float32)
+    clock = np.broadcast_to((np.arange(L, dtype=np.float64) / L).astype(np.float32), (B, L)).copy()
+    return path, clock, dw
+
+
+def bench_diag_cfg(args):
+    """One block's hot path at BASELINE.json configs[0] (c1: real diagonal d=8, forward), configs[3] (c4: real
+    diagonal d=32, B=256, L=512, EWS scan + LogEWS compression, forward + backward) or configs[4] (c5: 12 planes,
+    d=24, B=8, L=49,920, bfloat16 path, forward + backward), through the C ABI with HIP events between passes.
+    The stacked configs repeat this block (4 and 3 times) with host-side norms between blocks. Returns the JSON
+    record."""
+    import torch
+
+    from ews_mi355x import _native as nat
+    from ews_mi355x.ops import make_desc
+
+    dev = torch.device("cuda:0")
+    lib = nat.load()
+    cfg = args.config
+    N = 2
+    if cfg == "c1":
+        path_np, clock_np, A_np = c1_inputs()
+        structure, bwd, log, bf16 = nat.STRUCT_REAL_DIAG, False, False, False
+    elif cfg == "c4":
+        path_np, clock_np, A_np = c4_inputs()
+        structure, bwd, log, bf16 = nat.STRUCT_REAL_DIAG, True, True, False
+    else:
+        path_np, clock_np, A_np = c5_inputs()
+        structure, bwd, log, bf16 = nat.STRUCT_PLANES, True, False, True
+    B, L, d = path_np.shape
+    D = d + d * d
+    W = D + 1
+    path = torch.tensor(path_np, device=dev)
+    if bf16:
+        path = path.to(torch.bfloat16)
+    clock = torch.tensor(clock_np, device=dev)
+    A = torch.tensor(A_np, device=dev)
+    desc = make_desc(B, L, d, N, structure, nat.FLOW_PER_INTERVAL, "prefix", True,
+                     nat.DTYPE_BF16 if bf16 else nat.DTYPE_F32, args.chunk)
+    ws = torch.empty(int(lib.ews_diag_workspace_bytes(ctypes.byref(desc))), device=dev, dtype=torch.uint8)
+    resid = torch.empty(int(lib.ews_diag_residual_bytes(ctypes.byref(desc))), device=dev, dtype=torch.uint8)
+    out = torch.empty((B, L - 1, W), device=dev, dtype=torch.float32)
+    nf, nb = lib.ews_diag_num_passes(0), lib.ews_diag_num_passes(1)
+    names = FWD_PASS_NAMES[:nf]
+    if log:
+        ldesc = nat.LogDesc(B, L - 1, d, N, 1, nat.READOUTS["prefix"])
+        Dlog = int(lib.ews_log_dim(d, N))
+        lout = torch.empty((B, L - 1, Dlog), device=dev, dtype=torch.float32)
+        lws = torch.empty(max(16, int(lib.ews_log_workspace_bytes(ctypes.byref(ldesc)))), device=dev,
+                          dtype=torch.uint8)
+        names = names + ["log_forward"]
+    if bwd:
+        gsrc = torch.randn((B, L - 1, Dlog if log else W), device=dev, dtype=torch.float32)
+        gout = torch.empty((B, L - 1, W), device=dev, dtype=torch.float32) if log else gsrc
+        dpath = torch.empty((B, L, d), device=dev, dtype=torch.float32)
+        dA = torch.empty_like(A)
+        names = names + (["log_backward"] if log else []) + BWD_PASS_NAMES[:nb]
+
+    def step(events):
+        st = ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream)
+        i = 0
+        for p in range(nf):
+            events[i].record()
+            i += 1
+            nat.check(lib.ews_diag_forward_pass(ctypes.byref(desc), p, path.data_ptr(), clock.data_ptr(),
+                                                A.data_ptr(), out.data_ptr(), resid.data_ptr(), ws.data_ptr(), st),
+                      "forward pass")
+        if log:
+            events[i].record()
+            i += 1
+            nat.check(lib.ews_log_forward(ctypes.byref(ldesc), out.data_ptr(), lout.data_ptr(), lws.data_ptr(), st),
+                      "log forward")
+        if bwd:
+            if log:
+                events[i].record()
+                i += 1
+                nat.check(lib.ews_log_backward(ctypes.byref(ldesc), out.data_ptr(), gsrc.data_ptr(),
+                                               gout.data_ptr(), lws.data_ptr(), st), "log backward")
+            for p in range(nb):
+                events[i].record()
+                i += 1
+                nat.check(lib.ews_diag_backward_pass(ctypes.byref(desc), p, path.data_ptr(), clock.data_ptr(),
+                                                     A.data_ptr(), resid.data_ptr(), gout.data_ptr(),
+                                                     dpath.data_ptr(), None, dA.data_ptr(), ws.data_ptr(), st),
+                          "backward pass")
+        events[i].record()
+
+    def new_events():
+        return [torch.cuda.Event(enable_timing=True) for _ in range(len(names) + 1)]
+
+    for _ in range(args.warmup):
+        step(new_events())
+    torch.cuda.synchronize()
+    evs_all = []
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(args.steps):
+        evs = new_events()
+        step(evs)
+        evs_all.append(evs)
+    end.record()
+    torch.cuda.synchronize()
+    ms = start.elapsed_time(end) / args.steps
+    pass_ms = {nm: sum(e[i].elapsed_time(e[i + 1]) for e in evs_all) / args.steps for i, nm in enumerate(names)}
+    n = B * (L - 1)
+    s_in = 2 if bf16 else 4
+    ab = algorithmic_bytes(B, L, d, W, s_in)
+    if log:
+        ab["log_forward"] = n * 4 * (W + Dlog)            # read state rows, write log rows
+        ab["log_backward"] = n * 4 * (2 * W + Dlog)       # read state rows and log cotangents, write row cotangents
+    dominant = max((k for k in pass_ms if k in ab), key=pass_ms.get)
+    achieved = ab[dominant] / (pass_ms[dominant] * 1e-3) / 1e9
+    total = ab["fwd_total"] + (ab["bwd_total"] if bwd else 0)
+    if log:
+        total += ab["log_forward"] + (ab["log_backward"] if bwd else 0)
+    what = {"c1": "c1: single EWS layer, B=8, L=1024, 3 time-augmented channels lifted to d=8, real diagonal A, "
+                  "depth 2, fp32, prefix readout, forward",
+            "c4": "c4: one of 4 stacked LogEWS blocks, B=256, L=512, 8-token vocabulary embedded to d=32, real "
+                  "diagonal A, depth 2, fp32, EWS scan + LogEWS compression (prefix), forward + backward",
+            "c5": "c5: one of 3 stacked EWS blocks, B=8, L=49920, 6 band-limited channels lifted to d=24 (12 rotation "
+                  "planes), depth 2, bf16 path / fp32 state, prefix readout, forward + backward"}[cfg]
+    return {
+        "metric": "EWS " + ("forward" if not bwd else "forward+backward") + " time-steps/sec and HBM GB/s (% peak) "
+                  "on 1 MI355X",
+        "value": round(n / (ms * 1e-3), 1),
+        "unit": "time-steps/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic",
+        "config": {"workload": what, "global_batch": B, "seq_len": L, "parallelism": "none (1 GPU)"},
+        "hbm_gbs_effective": round(total / (ms * 1e-3) / 1e9, 1),
+        "hbm_frac_effective": round(total / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+        "roofline": {"bound": "hbm", "kernel": dominant, "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
+                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                     "algorithmic_bytes": ab[dominant]},
+        "passes_ms": {k: round(v, 4) for k, v in pass_ms.items()},
+    }
+
+
 C3_CHEN_FLOPS = 427008  # per interval: 2 sum_k k d^(k+1) + 2 sum_k (k-1) d^k at d = 16, N = 3
 
 
@@ -272,8 +459,9 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--check", action="store_true", help="also check one forward against the C float64 checker")
     ap.add_argument("--chunk", type=int, default=0, help="intervals per chunk (0: the library's default)")
-    ap.add_argument("--config", choices=["c2", "c3"], default="c2",
-                    help="c2 (default, the headline): planes fwd+bwd; c3: dense-generator depth-3 forward")
+    ap.add_argument("--config", choices=["c2", "c3", "c1", "c4", "c5"], default="c2",
+                    help="c2 (default, the headline): planes fwd+bwd; c3: dense-generator depth-3 forward; c1, c4, "
+                         "c5: one block of the other BASELINE.json configs (real diagonal; LogEWS; bf16 planes)")
     ap.add_argument("--backward", action="store_true", help="c3: time forward + backward (ews_dense_backward)")
     ap.add_argument("--leaf", choices=["series", "van_loan"], default="series",
                     help="leaf of the c3 forward: series (q=24) or Van Loan (M=20, cayley)")
@@ -296,6 +484,12 @@ def main():
             dst.copy_(src)
         torch.cuda.synchronize()
         del src, dst
+    if args.config in ("c1", "c4", "c5"):
+        import torch
+
+        torch.cuda.set_device(0)
+        print(json.dumps(bench_diag_cfg(args)), flush=True)
+        return
     if args.config == "c3":
         import torch
 

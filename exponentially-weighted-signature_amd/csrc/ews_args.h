@@ -12,6 +12,7 @@ struct DiagArgs {
   int N, flow_mode, readout;
   int T, C;               // chunk length, chunk count
   int scan_cb;            // chunks per LDS-staged block in the float64 scans
+  int kb;                 // checkpoint block (steps) of the recomputing adjoint, <= kBLK
   int W, off1, off2, lvl0, D, npar;
   int path_bf16;
   const void* path;

@@ -886,7 +886,8 @@ __device__ __forceinline__ void gamma_row(const DiagArgs& a, const LaneMap& m, c
 
 // Cotangent rows of a prefix readout are staged in LDS eight steps at a time; the next block is loaded into
 // registers while the current one is processed, so no global load sits on the sequential dependency chain.
-constexpr int kBLK = 8;   // checkpoint block and cotangent staging rows of the exact-coefficient adjoint
+constexpr int kBLK = 8;   // checkpoint block and cotangent staging rows of the exact-coefficient adjoint (the
+                          // plan halves it for wide states, whose checkpoints would not fit the LDS)
 constexpr int kGB = 4;    // cotangent staging rows of the local and inversion adjoints
 // Asynchronous copy of n contiguous floats into LDS (global_load_lds: each lane's dword lands at the wave's
 // LDS base + 4 * lane); completion is awaited with lds_dma_wait() before a barrier.
@@ -901,7 +902,7 @@ __device__ __forceinline__ void lds_dma(float* dst, const float* src, int n) {
 __device__ __forceinline__ void lds_dma_wait() { __builtin_amdgcn_s_waitcnt(0); }
 
 struct GammaSrc {
-  const float* rows;  // prefix: staged block rows (kBLK x W); else the per-sample cotangent (W)
+  const float* rows;  // prefix: staged block rows (block x W); else the per-sample cotangent (W)
   const int* am;      // max readout: per-sample argmax (W)
   float scale;
   int kind;           // readout
@@ -982,8 +983,8 @@ __host__ __device__ inline BwdLds bwd_lds_layout(int T, int d, int W, int NT, in
   L.gb = o; o += 2 * rows * W;
   L.gv = o; o += W;
   L.am = o; o += W;
-  L.ck = o; o += (full && NS) ? ((T + kBLK - 1) / kBLK) * NS * NT : 0;
-  L.hist = o; o += (full && NS) ? kBLK * NS * NT : 0;
+  L.ck = o; o += (full && NS) ? ((T + rows - 1) / rows) * NS * NT : 0;
+  L.hist = o; o += (full && NS) ? rows * NS * NT : 0;
   L.red = o; o += wave ? 0 : 8 * NT;
   L.dh = o; o += full ? T * ((NT + 63) / 64) : 0;
   L.g = o; o += 4 * NT;
@@ -1454,7 +1455,7 @@ __global__ __launch_bounds__(MAXT) void k_chunk_bwd_inv(DiagArgs a) {
 }
 
 // (b) Every other chunk: exact per-step coefficients and forward states recomputed from the chunk's float64 carry
-// (checkpoints every kBLK steps; each block recomputed into a lane-private LDS history before its reverse sweep).
+// (checkpoints every kb steps; each block recomputed into a lane-private LDS history before its reverse sweep).
 // One chunk c of sample b; every early return is uniform over the workgroup.
 template <bool CPLX, int N, int MAXT, bool WAVE>
 __device__ __forceinline__ void chunk_bwd_full(const DiagArgs& a, const int c, const int b) {
@@ -1462,7 +1463,8 @@ __device__ __forceinline__ void chunk_bwd_full(const DiagArgs& a, const int c, c
   constexpr int NS = CPLX ? 6 : 2;  // checkpoint floats per lane
   extern __shared__ float smem[];
   const int NT = blockDim.x;
-  const BwdLds Lo = bwd_lds_layout(a.T, a.d, a.W, NT, NS, WAVE, true);
+  const int kb = a.kb;  // checkpoint block and cotangent staging rows
+  const BwdLds Lo = bwd_lds_layout(a.T, a.d, a.W, NT, NS, WAVE, true, kb);
   float* s_v = smem + Lo.v;
   float* s_h = smem + Lo.h;
   float* s_gb = smem + Lo.gb;
@@ -1473,7 +1475,7 @@ __device__ __forceinline__ void chunk_bwd_full(const DiagArgs& a, const int c, c
   const RedLds red{smem + Lo.red, smem + Lo.red + 2 * NT, smem + Lo.red + 4 * NT, smem + Lo.red + 6 * NT};
   float* s_dh = smem + Lo.dh;
   float* s_g = smem + Lo.g;
-  EWS_BWD_PROLOGUE(!(cc.fast && cc.inv_ok), kBLK)
+  EWS_BWD_PROLOGUE(!(cc.fast && cc.inv_ok), kb)
   auto coef_at = [&](int t, Coef<T>& co, CoefD<T>& qq) {
     eval_coef<T, CPLX, N, true>(s_h[t], cc.href, cc.per_int, uj, uk, co, qq);
   };
@@ -1501,11 +1503,11 @@ __device__ __forceinline__ void chunk_bwd_full(const DiagArgs& a, const int c, c
       xb = p[1 * NT + tid];
     }
   };
-  // forward pre-pass from the carry: checkpoints of the state before every kBLK-th step
+  // forward pre-pass from the carry: checkpoints of the state before every kb-th step
   T S1, SA, SB;
   load_state_d<CPLX, N>(a, m, a.carries + ((size_t)b * (a.C + 1) + c) * a.D, S1, SA, SB);
   for (int t = 0; t < Tc; ++t) {
-    if ((t % kBLK) == 0) st_store(s_ck + (size_t)(t / kBLK) * NS * NT, S1, SA, SB);
+    if ((t % kb) == 0) st_store(s_ck + (size_t)(t / kb) * NS * NT, S1, SA, SB);
     Coef<T> co;
     CoefD<T> qq;
     coef_at(t, co, qq);
@@ -1519,13 +1521,13 @@ __device__ __forceinline__ void chunk_bwd_full(const DiagArgs& a, const int c, c
   for (int blk = nblk - 1; blk >= 0; --blk) {
     const int buf = (nblk - 1 - blk) & 1;
     const bool more = prefix && blk > 0;
-    if (more) lds_dma(s_gb + (buf ^ 1) * kBLK * a.W, a.gout + ((size_t)b * a.n_int + t0 + (blk - 1) * kBLK) * a.W,
-                      kBLK * a.W);
-    const GammaSrc gs{prefix ? s_gb + buf * kBLK * a.W : s_gv, s_am, 1.0f / (float)a.n_int, a.readout};
+    if (more) lds_dma(s_gb + (buf ^ 1) * kb * a.W, a.gout + ((size_t)b * a.n_int + t0 + (blk - 1) * kb) * a.W,
+                      kb * a.W);
+    const GammaSrc gs{prefix ? s_gb + buf * kb * a.W : s_gv, s_am, 1.0f / (float)a.n_int, a.readout};
     st_load(s_ck + (size_t)blk * NS * NT, S1, SA, SB);
 #pragma unroll 1
-    for (int s = 0; s < kBLK; ++s) {
-      const int t = blk * kBLK + s;
+    for (int s = 0; s < kb; ++s) {
+      const int t = blk * kb + s;
       if (t >= Tc) break;
       st_store(s_hist + (size_t)s * NS * NT, S1, SA, SB);
       Coef<T> co;
@@ -1536,8 +1538,8 @@ __device__ __forceinline__ void chunk_bwd_full(const DiagArgs& a, const int c, c
       fwd_step<T, CPLX, N>(co, pj, pk, S1, SA, SB);
     }
 #pragma unroll 1
-    for (int s = kBLK - 1; s >= 0; --s) {
-      const int t = blk * kBLK + s;
+    for (int s = kb - 1; s >= 0; --s) {
+      const int t = blk * kb + s;
       if (t < Tc) {
         T H1, HA, HB;
         st_load(s_hist + (size_t)s * NS * NT, H1, HA, HB);
@@ -1678,7 +1680,7 @@ using namespace ews;
 size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 
 struct Plan {
-  int B, L, n_int, d, K, N, T, C, D, W, npar;
+  int B, L, n_int, d, K, N, T, C, D, W, npar, kb;
   bool cplx, wave, fast;
   int NT, NTb, scan_cb, NG;
   size_t lds_bwd_local, lds_bwd_full, lds_bwd_inv, lds_carry, lds_adjoint;
@@ -1687,9 +1689,9 @@ struct Plan {
 constexpr size_t kMaxLds = 160 * 1024;  // LDS per workgroup on gfx950
 constexpr size_t kScanLds = 48 * 1024;
 
-size_t bwd_lds_bytes(const Plan& p, int T, bool full) {
+size_t bwd_lds_bytes(const Plan& p, int T, bool full, int kb) {
   const int NS = p.cplx ? 6 : 2;
-  return (size_t)bwd_lds_layout(T, p.d, p.W, p.NTb, NS, p.wave, full).total * 4;
+  return (size_t)bwd_lds_layout(T, p.d, p.W, p.NTb, NS, p.wave, full, kb).total * 4;
 }
 
 int make_plan(const ews_diag_desc* s, Plan& p) {
@@ -1718,17 +1720,23 @@ int make_plan(const ews_diag_desc* s, Plan& p) {
   p.NT = ((P + 63) / 64) * 64;
   p.wave = p.K <= 8;  // one wavefront with lane = 8 j + k in the backward chunk kernels
   p.NTb = p.wave ? 64 : p.NT;
-  int T = s->chunk;
+  // chunk length and checkpoint block of the recomputing adjoint: the longest chunk (down to 16) whose LDS fits
+  // with blocks of kBLK steps, then shorter blocks (wide states: d = 32 at depth 2), then shorter chunks
+  int T = s->chunk, kb = kBLK;
+  if (T > 256) T = 256;
   if (T == 0) {
     T = 64;
-    while (T > 8 && bwd_lds_bytes(p, T, true) > kMaxLds) T /= 2;
+    while (T > 16 && bwd_lds_bytes(p, T, true, kb) > kMaxLds) T /= 2;
   }
-  if (T > 256) T = 256;
+  while (kb > 2 && bwd_lds_bytes(p, T, true, kb) > kMaxLds) kb /= 2;
+  if (s->chunk == 0)
+    while (T > 8 && bwd_lds_bytes(p, T, true, kb) > kMaxLds) T /= 2;
   p.T = T;
+  p.kb = kb;
   p.fast = pairs_eligible(s->structure, s->depth, s->dim, s->readout, s->flow_mode, T);
   p.C = (p.n_int + T - 1) / T;
   p.lds_bwd_local = (size_t)bwd_lds_layout(T, p.d, p.W, p.NTb, 0, p.wave, false, kGB).total * 4;
-  p.lds_bwd_full = bwd_lds_bytes(p, T, true);
+  p.lds_bwd_full = bwd_lds_bytes(p, T, true, kb);
   p.lds_bwd_inv = (size_t)bwd_lds_layout(T, p.d, p.W, p.NTb, 0, p.wave, true, kGB).total * 4;
   if (p.lds_bwd_full > kMaxLds) return EWS_ERR_SHAPE;
   const int CW = p.cplx ? 2 : 1;
@@ -1778,7 +1786,7 @@ DiagArgs make_args(const ews_diag_desc* s, const Plan& p, const void* path, cons
                    const float* params, void* residual, void* workspace) {
   DiagArgs a{};
   a.B = p.B; a.L = p.L; a.n_int = p.n_int; a.d = p.d; a.K = p.K; a.N = p.N;
-  a.flow_mode = s->flow_mode; a.readout = s->readout; a.T = p.T; a.C = p.C; a.scan_cb = p.scan_cb;
+  a.flow_mode = s->flow_mode; a.readout = s->readout; a.T = p.T; a.C = p.C; a.scan_cb = p.scan_cb; a.kb = p.kb;
   a.W = p.W; a.lvl0 = s->level0 ? 1 : 0; a.off1 = a.lvl0; a.off2 = a.lvl0 + p.d; a.D = p.D; a.npar = p.npar;
   a.path_bf16 = s->path_dtype == EWS_DTYPE_BF16;
   a.path = path; a.clock = clock; a.params = params;

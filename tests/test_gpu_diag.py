@@ -109,6 +109,35 @@ def test_forward_and_grads_match_oracle(case, readout):
         assert ga < 1e-4, f"A-param grad relerr {ga:.2e}"
 
 
+@pytest.mark.parametrize("structure,K,steps", [("real", 32, "unit"), ("planes", 12, "uniform"), ("planes", 12, "unit")])
+@pytest.mark.parametrize("readout", ["prefix", "mean"])
+def test_wide_states(structure, K, steps, readout):
+    """The widths of BASELINE.json configs[3] (d = 32 real diagonal) and configs[4] (d = 24, 12 planes) at depth 2.
+    Unit clock steps (the block default clock arange(L)) contract a chunk too much to invert its steps, so the
+    adjoint recomputes the states from checkpoints; at d = 32 the plan shortens the checkpoint block to fit LDS."""
+    N, B, L = 2, 2, 70
+    d = 2 * K if structure == "planes" else K
+    path, clock = _data(B, L, d, 21 + K, True)
+    if steps == "unit":
+        clock = torch.arange(L, dtype=torch.float32).expand(B, L).contiguous()
+    layer, ref_param, oleaf = _layers(structure, K, N, 9, combine="block_kernel" if structure == "planes" else "assoc")
+    p = path.to(DEV).requires_grad_(True)
+    c = clock.to(DEV).requires_grad_(True)
+    out = layer(p, c, readout=readout)
+    pr = path.double().requires_grad_(True)
+    cr = clock.double().requires_grad_(True)
+    ref = _oracle(ref_param, pr, cr, N, readout, oleaf, "displacement", "assoc")
+    e = relerr(out, ref)
+    assert e < 1e-5, f"forward relerr {e:.2e}"
+    w = torch.tensor(np.random.default_rng(8).normal(size=tuple(ref.shape)))
+    (out * w.to(DEV, torch.float32)).sum().backward()
+    (ref * w).sum().backward()
+    assert relerr(p.grad, pr.grad) < 1e-4, relerr(p.grad, pr.grad)
+    assert relerr(c.grad, cr.grad) < 1e-4, relerr(c.grad, cr.grad)
+    for g_gpu, g_ref in zip([q.grad for q in layer.A_param.parameters()], [q.grad for q in ref_param.parameters()]):
+        assert relerr(g_gpu, g_ref) < 1e-4, relerr(g_gpu, g_ref)
+
+
 @pytest.mark.parametrize("mode", ["displacement_uniform", "displacement_uniform_basepoint"])
 @pytest.mark.parametrize("readout,reduce", [("prefix", "assoc"), ("terminal", "tree"), ("terminal", "assoc"),
                                             ("mean", "tree")])
