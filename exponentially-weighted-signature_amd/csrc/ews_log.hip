@@ -23,26 +23,44 @@ struct LArgs {
   int* amax;          // (B, Dlog) first row of the maximum (max readout)
 };
 
-// Lyndon words of lengths 1..N over {0..d-1}, Duval's algorithm (one thread); off[k]: first word of length k + 1.
-__global__ void k_lyndon(int* words, int d, int N, int off1, int off2) {
-  if (threadIdx.x != 0 || blockIdx.x != 0) return;
-  int w[3] = {-1, 0, 0};
-  int len = 1;
-  int cnt[3] = {0, off1, off2};
-  while (len > 0) {
-    w[len - 1] += 1;
-    int* o = words + 4 * cnt[len - 1]++;
-    o[0] = len;
-    o[1] = w[0];
-    o[2] = len > 1 ? w[1] : 0;
-    o[3] = len > 2 ? w[2] : 0;
-    const int m = len;
-    while (len < N) {
-      w[len] = w[len - m];
-      ++len;
+// Lyndon words of lengths 1..3 over {0..d-1}, each length in lexicographic order, one thread per word. A word of
+// length 2 is Lyndon iff i < j; of length 3 iff a <= b and a < c (a rotation starting with a smaller letter, or the
+// rotation aab of aba, would be smaller otherwise). So the lexicographic rank of a word has a closed form:
+//   (i, j):    i (2d - i - 1) / 2 + (j - i - 1)
+//   (a, b, c): sum_{x < a} (d - x)(d - x - 1) + (b - a)(d - a - 1) + (c - a - 1),
+// the same table Duval's algorithm generates (sorted by length).
+__device__ __forceinline__ int widx2(int i, int j, int d) { return i * (2 * d - i - 1) / 2 + (j - i - 1); }
+__device__ __forceinline__ int widx3(int a, int b, int c, int d) {
+  const int m = d - a;  // sum_{x < a} (d - x)(d - x - 1) = ((d^3 - d) - (m^3 - m)) / 3
+  return ((d * d * d - d) - (m * m * m - m)) / 3 + (b - a) * (m - 1) + (c - a - 1);
+}
+__global__ void k_words(int* words, int d, int n1, int n2, int Dlog) {
+  const int w = blockIdx.x * blockDim.x + threadIdx.x;
+  if (w >= Dlog) return;
+  int len, i = 0, j = 0, k = 0;
+  if (w < n1) {
+    len = 1;
+    i = w;
+  } else if (w < n1 + n2) {
+    len = 2;
+    int q = w - n1;
+    while (q >= d - 1 - i) q -= d - 1 - i++;
+    j = i + 1 + q;
+  } else {
+    len = 3;
+    int q = w - n1 - n2;
+    while (q >= (d - i) * (d - i - 1)) {
+      q -= (d - i) * (d - i - 1);
+      ++i;
     }
-    while (len > 0 && w[len - 1] == d - 1) --len;
+    j = i + q / (d - i - 1);
+    k = i + 1 + q % (d - i - 1);
   }
+  int* o = words + 4 * w;
+  o[0] = len;
+  o[1] = i;
+  o[2] = j;
+  o[3] = k;
 }
 
 // log coefficient of word wd on the row (levels 1..N, no level-0 column)
@@ -90,51 +108,81 @@ __global__ void k_logpool(LArgs a) {
   }
 }
 
-// Backward, one workgroup per (row, sample): the row's cotangent gw of its log coefficients (by readout), then
-//   level 3 words (i,j,k): dS3[ijk] = g, dS1[i] -= g S2[jk]/2 - g S1[j] S1[k]/3, dS2[jk] -= g S1[i]/2,
-//                          dS2[ij] -= g S1[k]/2, dS1[k] -= g S2[ij]/2 - g S1[i] S1[j]/3, dS1[j] += g S1[i] S1[k]/3
-//   level 2 words (i,j):   dS2[ij] += g, dS1[i] -= g S1[j]/2, dS1[j] -= g S1[i]/2
-//   level 1 words (i):     dS1[i] += g
-// (LDS atomics for levels 1-2; the level-3 entries outside the words and the level-0 column are zero).
-__global__ __launch_bounds__(256) void k_logrows_bwd(LArgs a, const float* gout, float* grows) {
-  extern __shared__ float acc[];  // d + d*d
-  const int r = blockIdx.x, b = blockIdx.y, d = a.d;
+// Backward, one wavefront per (row, sample). The row's word cotangents g (by readout) and its level 1 (and level 2
+// at depth 3) are staged in LDS, then every entry of the row cotangent is gathered from the words that contain it:
+//   dS1[x] = g(x) - 1/2 sum_{y != x} g(min(x,y), max(x,y)) S1[y]
+//            + sum over words (x,b,c): g (S1[b] S1[c] / 3 - S2[bc] / 2)       (x first)
+//            + sum over words (a,x,c): g S1[a] S1[c] / 3                       (x second)
+//            + sum over words (a,b,x): g (S1[a] S1[b] / 3 - S2[ab] / 2)       (x last)
+//   dS2[xy] = g(x,y) [x < y] - 1/2 sum over words (a,x,y) of g S1[a] - 1/2 sum over words (x,y,c) of g S1[c]
+//   dS3[abc] = g(a,b,c) on the Lyndon words, 0 elsewhere; the level-0 column is 0.
+// No atomics: each entry is written once, rows stream through with coalesced stores.
+__global__ __launch_bounds__(64) void k_logrows_bwd(LArgs a, const float* gout, float* grows) {
+  extern __shared__ float sh[];  // g (Dlog) | S1 (d) | S2 (d*d, depth 3)
+  const int r = blockIdx.x, b = blockIdx.y, d = a.d, N = a.N, l = threadIdx.x;
+  float* g = sh;
+  float* s1 = g + a.Dlog;
+  float* s2 = s1 + d;
   const float* s = a.rows + ((size_t)b * a.R + r) * a.W + a.lvl0;
-  float* gr = grows + ((size_t)b * a.R + r) * a.W;
-  const int D12 = d + (a.N >= 2 ? d * d : 0);
-  for (int e = threadIdx.x; e < D12; e += blockDim.x) acc[e] = 0.0f;
-  if (a.N >= 3) {
-    for (int e = threadIdx.x; e < d * d * d; e += blockDim.x) gr[a.lvl0 + D12 + e] = 0.0f;
+  for (int w = l; w < a.Dlog; w += 64) {
+    float v;
+    if (a.readout == EWS_READOUT_PREFIX) v = gout[((size_t)b * a.R + r) * a.Dlog + w];
+    else if (a.readout == EWS_READOUT_TERMINAL) v = gout[(size_t)b * a.Dlog + w];
+    else if (a.readout == EWS_READOUT_MEAN) v = gout[(size_t)b * a.Dlog + w] / (float)a.R;
+    else v = a.amax[(size_t)b * a.Dlog + w] == r ? gout[(size_t)b * a.Dlog + w] : 0.0f;
+    g[w] = v;
   }
-  if (a.lvl0 && threadIdx.x == 0) gr[0] = 0.0f;
+  for (int e = l; e < d; e += 64) s1[e] = s[e];
+  if (N >= 3)
+    for (int e = l; e < d * d; e += 64) s2[e] = s[d + e];
   __syncthreads();
-  const float* S2 = s + d;
-  for (int w = threadIdx.x; w < a.Dlog; w += blockDim.x) {
-    float g;
-    if (a.readout == EWS_READOUT_PREFIX) g = gout[((size_t)b * a.R + r) * a.Dlog + w];
-    else if (a.readout == EWS_READOUT_TERMINAL) g = gout[(size_t)b * a.Dlog + w];
-    else if (a.readout == EWS_READOUT_MEAN) g = gout[(size_t)b * a.Dlog + w] / (float)a.R;
-    else g = a.amax[(size_t)b * a.Dlog + w] == r ? gout[(size_t)b * a.Dlog + w] : 0.0f;
-    const int* wd = a.words + 4 * w;
-    const int len = wd[0], i = wd[1], j = wd[2], k = wd[3];
-    if (len == 1) {
-      atomicAdd(&acc[i], g);
-    } else if (len == 2) {
-      atomicAdd(&acc[d + i * d + j], g);
-      atomicAdd(&acc[i], -0.5f * g * s[j]);
-      atomicAdd(&acc[j], -0.5f * g * s[i]);
-    } else {
-      gr[a.lvl0 + D12 + (i * d + j) * d + k] = g;
-      const float t3 = g * (1.0f / 3.0f);
-      atomicAdd(&acc[i], fmaf(t3, s[j] * s[k], -0.5f * g * S2[j * d + k]));
-      atomicAdd(&acc[j], t3 * s[i] * s[k]);
-      atomicAdd(&acc[k], fmaf(t3, s[i] * s[j], -0.5f * g * S2[i * d + j]));
-      atomicAdd(&acc[d + j * d + k], -0.5f * g * s[i]);
-      atomicAdd(&acc[d + i * d + j], -0.5f * g * s[k]);
+  const int n1 = d, n12 = d + (N >= 2 ? d * (d - 1) / 2 : 0);
+  float* gr = grows + ((size_t)b * a.R + r) * a.W;
+  if (a.lvl0 && l == 0) gr[0] = 0.0f;
+  gr += a.lvl0;
+  for (int x = l; x < d; x += 64) {
+    float v = g[x];
+    if (N >= 2) {
+      float t = 0.0f;
+      for (int y = 0; y < d; ++y)
+        if (y != x) t = fmaf(g[n1 + (x < y ? widx2(x, y, d) : widx2(y, x, d))], s1[y], t);
+      v = fmaf(-0.5f, t, v);
+    }
+    if (N >= 3) {
+      for (int p = 0; p < d; ++p) {
+        for (int q = 0; q < d; ++q) {
+          if (p >= x && q > x)  // (x, p, q)
+            v += g[n12 + widx3(x, p, q, d)] * fmaf((1.0f / 3.0f) * s1[p], s1[q], -0.5f * s2[p * d + q]);
+          if (p <= x && q > p)  // (p, x, q)
+            v += g[n12 + widx3(p, x, q, d)] * ((1.0f / 3.0f) * s1[p] * s1[q]);
+          if (p < x && q >= p)  // (p, q, x)
+            v += g[n12 + widx3(p, q, x, d)] * fmaf((1.0f / 3.0f) * s1[p], s1[q], -0.5f * s2[p * d + q]);
+        }
+      }
+    }
+    gr[x] = v;
+  }
+  if (N >= 2) {
+    for (int e = l; e < d * d; e += 64) {
+      const int x = e / d, y = e - x * d;
+      float v = x < y ? g[n1 + widx2(x, y, d)] : 0.0f;
+      if (N >= 3) {
+        float t = 0.0f;
+        for (int c = 0; c < d; ++c) {
+          if (c <= x && c < y) t = fmaf(g[n12 + widx3(c, x, y, d)], s1[c], t);  // (c, x, y)
+          if (x <= y && x < c) t = fmaf(g[n12 + widx3(x, y, c, d)], s1[c], t);  // (x, y, c)
+        }
+        v = fmaf(-0.5f, t, v);
+      }
+      gr[d + e] = v;
     }
   }
-  __syncthreads();
-  for (int e = threadIdx.x; e < D12; e += blockDim.x) gr[a.lvl0 + e] = acc[e];
+  if (N >= 3) {
+    for (int e = l; e < d * d * d; e += 64) {
+      const int x = e / (d * d), y = (e / d) % d, z = e % d;
+      gr[d + d * d + e] = (x <= y && x < z) ? g[n12 + widx3(x, y, z, d)] : 0.0f;
+    }
+  }
 }
 
 }  // namespace logsig
@@ -233,7 +281,7 @@ int ews_log_forward(const ews_log_desc* desc, const float* sig_rows, float* out,
   if (!sig_rows || !out || !workspace) return EWS_ERR_NULL;
   const LArgs a = log_args(p, sig_rows, out, workspace);
   hipStream_t st = (hipStream_t)stream;
-  hipLaunchKernelGGL(k_lyndon, dim3(1), dim3(1), 0, st, a.words, p.d, p.N, p.sz[0], p.sz[0] + p.sz[1]);
+  hipLaunchKernelGGL(k_words, dim3((p.Dlog + 255) / 256), dim3(256), 0, st, a.words, p.d, p.sz[0], p.sz[1], p.Dlog);
   LOG_CHECK();
   hipLaunchKernelGGL(k_logrows, dim3(p.R, p.B), dim3(256), 0, st, a);
   LOG_CHECK();
@@ -253,7 +301,7 @@ int ews_log_backward(const ews_log_desc* desc, const float* sig_rows, const floa
   const LArgs a = log_args(p, sig_rows, nullptr, workspace);
   hipStream_t st = (hipStream_t)stream;
   // the word table (and, for max, the argmax) are the forward's, recomputed here so the call stands alone
-  hipLaunchKernelGGL(k_lyndon, dim3(1), dim3(1), 0, st, a.words, p.d, p.N, p.sz[0], p.sz[0] + p.sz[1]);
+  hipLaunchKernelGGL(k_words, dim3((p.Dlog + 255) / 256), dim3(256), 0, st, a.words, p.d, p.sz[0], p.sz[1], p.Dlog);
   LOG_CHECK();
   if (p.readout == EWS_READOUT_MAX) {
     LArgs f = a;
@@ -263,8 +311,8 @@ int ews_log_backward(const ews_log_desc* desc, const float* sig_rows, const floa
     hipLaunchKernelGGL(k_logpool, dim3((p.Dlog + 255) / 256, p.B), dim3(256), 0, st, f);
     LOG_CHECK();
   }
-  const size_t shm = (size_t)(p.d + (p.N >= 2 ? p.d * p.d : 0)) * 4;
-  hipLaunchKernelGGL(k_logrows_bwd, dim3(p.R, p.B), dim3(256), shm, st, a, grad_out, grad_rows);
+  const size_t shm = (size_t)(p.Dlog + p.d + (p.N >= 3 ? p.d * p.d : 0)) * 4;
+  hipLaunchKernelGGL(k_logrows_bwd, dim3(p.R, p.B), dim3(64), shm, st, a, grad_out, grad_rows);
   LOG_CHECK();
   return EWS_OK;
 }
