@@ -1454,8 +1454,9 @@ __global__ __launch_bounds__(MAXT) void k_chunk_bwd_inv(DiagArgs a) {
   bwd_epilogue<CPLX, N, WAVE>(a, m, cc, acc, uj, ua, ub, Tc, t0, s_dh, s_g, c, b);
 }
 
-// (b) Every other chunk: exact per-step coefficients and forward states recomputed from the chunk's float64 carry
-// (checkpoints every kb steps; each block recomputed into a lane-private LDS history before its reverse sweep).
+// (b) Every other chunk: forward states recomputed from the chunk's float64 carry (checkpoints every kb steps; each
+// block recomputed into a lane-private LDS history before its reverse sweep), with exact per-step coefficients, or
+// the first-order model at the mean step for a uniform chunk.
 // One chunk c of sample b; every early return is uniform over the workgroup.
 template <bool CPLX, int N, int MAXT, bool WAVE>
 __device__ __forceinline__ void chunk_bwd_full(const DiagArgs& a, const int c, const int b) {
@@ -1476,8 +1477,18 @@ __device__ __forceinline__ void chunk_bwd_full(const DiagArgs& a, const int c, c
   float* s_dh = smem + Lo.dh;
   float* s_g = smem + Lo.g;
   EWS_BWD_PROLOGUE(!(cc.fast && cc.inv_ok), kb)
+  // uniform chunks (too contractive to invert) take the first-order model at the mean step, as every other
+  // kernel does for them; the others evaluate each step's exact coefficients
+  Coef<T> c0;
+  CoefD<T> q0;
+  if (cc.fast) eval_coef<T, CPLX, N, true>(cc.hbar, cc.href, cc.per_int, uj, uk, c0, q0);
   auto coef_at = [&](int t, Coef<T>& co, CoefD<T>& qq) {
-    eval_coef<T, CPLX, N, true>(s_h[t], cc.href, cc.per_int, uj, uk, co, qq);
+    if (cc.fast) {
+      lin_coef<T, CPLX, N>(c0, q0, s_h[t] - cc.hbar, cc.per_int, co);
+      qq = q0;
+    } else {
+      eval_coef<T, CPLX, N, true>(s_h[t], cc.href, cc.per_int, uj, uk, co, qq);
+    }
   };
   auto st_store = [&](float* p, T x1, T xa, T xb) {
     if constexpr (CPLX) {
