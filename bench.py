@@ -179,34 +179,39 @@ def bench_diag_cfg(args):
         dA = torch.empty_like(A)
         names = names + (["log_backward"] if log else []) + BWD_PASS_NAMES[:nb]
 
-    def step(events):
+    def step(events=None):
         st = ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream)
         i = 0
         for p in range(nf):
-            events[i].record()
+            if events is not None:
+                events[i].record()
             i += 1
             nat.check(lib.ews_diag_forward_pass(ctypes.byref(desc), p, path.data_ptr(), clock.data_ptr(),
                                                 A.data_ptr(), out.data_ptr(), resid.data_ptr(), ws.data_ptr(), st),
                       "forward pass")
         if log:
-            events[i].record()
+            if events is not None:
+                events[i].record()
             i += 1
             nat.check(lib.ews_log_forward(ctypes.byref(ldesc), out.data_ptr(), lout.data_ptr(), lws.data_ptr(), st),
                       "log forward")
         if bwd:
             if log:
-                events[i].record()
+                if events is not None:
+                    events[i].record()
                 i += 1
                 nat.check(lib.ews_log_backward(ctypes.byref(ldesc), out.data_ptr(), gsrc.data_ptr(),
                                                gout.data_ptr(), lws.data_ptr(), st), "log backward")
             for p in range(nb):
-                events[i].record()
+                if events is not None:
+                    events[i].record()
                 i += 1
                 nat.check(lib.ews_diag_backward_pass(ctypes.byref(desc), p, path.data_ptr(), clock.data_ptr(),
                                                      A.data_ptr(), resid.data_ptr(), gout.data_ptr(),
                                                      dpath.data_ptr(), None, dA.data_ptr(), ws.data_ptr(), st),
                           "backward pass")
-        events[i].record()
+        if events is not None:
+            events[i].record()
 
     def new_events():
         return [torch.cuda.Event(enable_timing=True) for _ in range(len(names) + 1)]
@@ -214,16 +219,20 @@ def bench_diag_cfg(args):
     for _ in range(args.warmup):
         step(new_events())
     torch.cuda.synchronize()
-    evs_all = []
+    # value from K steps with no events between the passes, per-pass times from K more steps with them
     start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     start.record()
+    for _ in range(args.steps):
+        step()
+    end.record()
+    torch.cuda.synchronize()
+    ms = start.elapsed_time(end) / args.steps
+    evs_all = []
     for _ in range(args.steps):
         evs = new_events()
         step(evs)
         evs_all.append(evs)
-    end.record()
     torch.cuda.synchronize()
-    ms = start.elapsed_time(end) / args.steps
     pass_ms = {nm: sum(e[i].elapsed_time(e[i + 1]) for e in evs_all) / args.steps for i, nm in enumerate(names)}
     n = B * (L - 1)
     s_in = 2 if bf16 else 4
@@ -323,16 +332,20 @@ def bench_c3(args):
     for _ in range(args.warmup):
         step()
     torch.cuda.synchronize()
-    evs_all = []
+    # value from K steps with no events between the passes, per-pass times from K more steps with them
     start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     start.record()
+    for _ in range(args.steps):
+        step()
+    end.record()
+    torch.cuda.synchronize()
+    ms = start.elapsed_time(end) / args.steps
+    evs_all = []
     for _ in range(args.steps):
         evs = [torch.cuda.Event(enable_timing=True) for _ in range(npass + 2)]
         step(evs)
         evs_all.append(evs)
-    end.record()
     torch.cuda.synchronize()
-    ms = start.elapsed_time(end) / args.steps
     names = ["local_terms", "chunk_summary", "carry_scan", "chunk_output"]
     if bwd:
         names.append("backward")
@@ -571,20 +584,26 @@ def main():
         check_grad = float(np.abs(got_dp - ref_dp).max() / np.abs(ref_dp).max())
     del A
 
-    per_step_events = []
+    # value: K steps with nothing between the passes (an event record between kernels costs a few microseconds
+    # of pipeline drain each); then K more steps with an event between every pass for the per-pass times and
+    # the dominant kernel's roofline
     start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
     t_wall0 = time.perf_counter()
     start.record()
     for _ in range(args.steps):
-        evs = [torch.cuda.Event(enable_timing=True) for _ in range(nf + nb + 1)]
-        step(evs)
-        per_step_events.append(evs)
+        step()
     end.record()
     torch.cuda.synchronize()
     t_wall = time.perf_counter() - t_wall0
     total_ms = start.elapsed_time(end)
     ms_per_step = total_ms / args.steps
+    per_step_events = []
+    for _ in range(args.steps):
+        evs = [torch.cuda.Event(enable_timing=True) for _ in range(nf + nb + 1)]
+        step(evs)
+        per_step_events.append(evs)
+    torch.cuda.synchronize()
     names = FWD_PASS_NAMES[:nf] + BWD_PASS_NAMES[:nb]
     pass_ms = {nm: 0.0 for nm in names}
     for evs in per_step_events:
