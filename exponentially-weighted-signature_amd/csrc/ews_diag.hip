@@ -288,6 +288,9 @@ __device__ __forceinline__ void stT(float* p, cf v) {
   p[1] = v.im;
 }
 __device__ __forceinline__ void stT(float* p, float v) { p[0] = v; }
+// value of the lane tid ^ o of the wavefront
+__device__ __forceinline__ float xor_lane(float v, int o) { return __shfl_xor(v, o, 64); }
+__device__ __forceinline__ cf xor_lane(cf v, int o) { return cf{__shfl_xor(v.re, o, 64), __shfl_xor(v.im, o, 64)}; }
 
 // Output row element indices of the lane's values (level 1 of plane j; the level-2 block (j, k)).
 template <bool CPLX>
@@ -1189,13 +1192,23 @@ __device__ __forceinline__ void bwd_step(const DiagArgs& a, const LaneMap& m, co
               stT(s_cP + 2 * ct, toPk);
             }
             __syncthreads();
-            if (m.plane) {
-              for (int kk = 0; kk < a.K; ++kk) {
+            // the first R lanes of row j (lanes j K .. j K + R - 1: one wavefront, an aligned group as R divides K)
+            // each sum every R-th entry of the plane's four runs, then combine by lane exchange; the plane lane
+            // (k = 0) ends with the totals
+            const int R = (a.K % 4 == 0) ? 4 : ((a.K % 2 == 0) ? 2 : 1);
+            if (m.active && m.k < R) {
+              for (int kk = m.k; kk < a.K; kk += R) {
                 rowC += ldT<CPLX, T>(s_rC + 2 * (m.j * a.K + kk));
                 rowP += ldT<CPLX, T>(s_rP + 2 * (m.j * a.K + kk));
                 colS += ldT<CPLX, T>(s_cS + 2 * (m.j * a.K + kk));
                 colP += ldT<CPLX, T>(s_cP + 2 * (m.j * a.K + kk));
               }
+            }
+            for (int o = 1; o < R; o <<= 1) {
+              rowC += xor_lane(rowC, o);
+              rowP += xor_lane(rowP, o);
+              colS += xor_lane(colS, o);
+              colP += xor_lane(colP, o);
             }
           }
         }
