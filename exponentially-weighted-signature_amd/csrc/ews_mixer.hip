@@ -1,0 +1,378 @@
+// Mixer epilogue of an EWS block on MI355X (gfx950), fused: the prefix rows' levels without their level-0
+// column, an optional leading zero row, the optional binomial prescale, the per-level GradedRMSNorm and the
+// c_down linear map, in one pass over the D-wide rows. Only the hidden-wide output is written.
+//
+// Reference (ews/block.py:282-306, 336-357, 405-408; ews/norms.py:47-134):
+//   levels = flat[:, 1:] (with a zero row in front unless basepoint), z_k = c(t, k) levels_k (binomial prescale,
+//   c = 1 / C(max(t_len, k), k), t_len = levels row + 1, or 1), y_k = s_k z_k with
+//     live_rms    s_k = g_k / (RMS(z_k) + eps_k)   (RMS over the level's d^k coordinates; 0 for an all-zero level)
+//     static_gain s_k = g_k
+//     dilation    s_k = lam^k,
+//   r = W y + b (eqx.nn.Linear(D, hidden)).
+// Since every scale is one number per row and level, r = b + sum_k f_k P_k with P_k = W_k x_k (W_k the level's
+// column block, x the unscaled row) and f_k = s_k c: the kernel accumulates P_k and the level's sum of squares in
+// one pass and applies f_k at the end.
+//
+// Backward (dr = dL/dr): dx_k = f_k W_k^T dr - beta_k (P_k . dr) x_k, with beta_k = g_k c^2 / ((c rho + eps)^2
+// n rho), rho = RMS(x_k), n = d^k, for live_rms (0 at rho = 0, where the reference's RMS has a zero gradient),
+// beta = 0 otherwise. The parameter gradients need only row-level quantities (host side).
+//
+// MFMA: v_mfma_f32_16x16x4f32 (lane l: A[l%16][l/16], B[l/16][l%16], result rows 4(l/16)+r of column l%16). The
+// contraction index of each 16-wide block is permuted so that a lane's four k-steps read four consecutive floats
+// of its row (slot g of step s is k0 + 4g + s), which changes nothing in the sum.
+#include <hip/hip_runtime.h>
+
+#include <cmath>
+#include <type_traits>
+
+#include "ews_hip.h"
+
+namespace ews {
+namespace mixer {
+
+typedef float f4 __attribute__((ext_vector_type(4)));
+typedef float f4u __attribute__((ext_vector_type(4), aligned(4)));
+
+constexpr int HC = 64;  // hidden columns per forward workgroup (four 16-wide tiles)
+
+struct MArgs {
+  int B, R, d, N, lvl0, W, D, hidden, variant, prepend, prescale;
+  float eps[3];
+  int st[3], n[3];  // level offsets (level-0-free) and sizes
+  const float* rows;
+  const float* weight;
+  const float* bias;
+  const float* gains;
+  float* out;
+  float* P;  // (B R, N, hidden) level products
+  float* F;  // (B R, N, 3): total scale f, beta, d f / d gain
+  const float* gout;
+  float* grows;
+  float* dots;  // (B R, N)
+};
+
+__device__ __forceinline__ f4 mfma(float a, float b, f4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
+}
+
+// p[k .. k+3] of a run ending at `end` (entries at or past end read as zero); nothing is read when !ok
+__device__ __forceinline__ f4 load4(const float* p, int k, int end, bool ok) {
+  if (!ok) return f4{0.0f, 0.0f, 0.0f, 0.0f};
+  if (k + 3 < end) {
+    const f4u v = *reinterpret_cast<const f4u*>(p + k);
+    return f4{v.x, v.y, v.z, v.w};
+  }
+  return f4{k < end ? p[k] : 0.0f, k + 1 < end ? p[k + 1] : 0.0f, k + 2 < end ? p[k + 2] : 0.0f,
+            k + 3 < end ? p[k + 3] : 0.0f};
+}
+
+template <int I, int N, class Fn> __device__ __forceinline__ void sfor(Fn&& f) {
+  if constexpr (I < N) {
+    f(std::integral_constant<int, I>{});
+    sfor<I + 1, N>(f);
+  }
+}
+
+// output row of scan row gr (sample b, row t)
+__device__ __forceinline__ size_t out_row(const MArgs& a, int gr) {
+  const int b = gr / a.R, t = gr - b * a.R;
+  return (size_t)b * (a.R + a.prepend) + t + a.prepend;
+}
+
+// Forward: a workgroup = 4 wavefronts x 16 rows, hidden columns [64 blockIdx.y, +64).
+template <int N>
+__global__ __launch_bounds__(256) void k_mix_fwd(MArgs a) {
+  __shared__ float s_f[4][3][16];
+  const int w = threadIdx.x >> 6, l = threadIdx.x & 63, i = l & 15, g = l >> 4;
+  const int M = a.B * a.R;
+  const int row0 = (blockIdx.x * 4 + w) * 16;
+  const int gr = row0 + i;
+  const bool valid = gr < M;
+  const float* xp = a.rows + (size_t)(valid ? gr : 0) * a.W + a.lvl0;
+  const int hc = blockIdx.y * HC;
+  f4 acc[N][4];
+  float ssq[N];
+  sfor<0, N>([&](auto kc) {
+    constexpr int k = kc;
+    ssq[k] = 0.0f;
+    sfor<0, 4>([&](auto hc_) { acc[k][hc_] = f4{0.0f, 0.0f, 0.0f, 0.0f}; });
+  });
+  sfor<0, N>([&](auto kc) {
+    constexpr int k = kc;
+    const int st = a.st[k], en = st + a.n[k];
+    for (int k0 = st; k0 < en; k0 += 16) {
+      const int kk = k0 + 4 * g;
+      const f4 xa = load4(xp, kk, en, valid);
+      ssq[k] = fmaf(xa.x, xa.x, fmaf(xa.y, xa.y, fmaf(xa.z, xa.z, fmaf(xa.w, xa.w, ssq[k]))));
+      sfor<0, 4>([&](auto hq) {
+        constexpr int h = hq;
+        const int hrow = hc + 16 * h + i;
+        const bool hok = hrow < a.hidden;
+        const f4 wb = load4(a.weight + (size_t)(hok ? hrow : 0) * a.D, kk, en, hok);
+        acc[k][h] = mfma(xa.x, wb.x, acc[k][h]);
+        acc[k][h] = mfma(xa.y, wb.y, acc[k][h]);
+        acc[k][h] = mfma(xa.z, wb.z, acc[k][h]);
+        acc[k][h] = mfma(xa.w, wb.w, acc[k][h]);
+      });
+    }
+  });
+  // per-row factors: the four lanes of a row hold partial sums of squares
+  sfor<0, N>([&](auto kc) {
+    constexpr int k = kc;
+    float v = ssq[k];
+    v += __shfl_xor(v, 16, 64);
+    v += __shfl_xor(v, 32, 64);
+    if (g == 0) {
+      const int t = valid ? gr % a.R : 0;
+      const int K = k + 1;
+      float c = 1.0f;
+      if (a.prescale) {
+        const double tl = fmax((double)(t + 1 + a.prepend), (double)K);
+        c = (float)exp(-(lgamma(tl + 1.0) - lgamma(tl - K + 1.0) - lgamma((double)K + 1.0)));
+      }
+      float f, beta = 0.0f, dfdg;
+      if (a.variant == EWS_GRADED_LIVE_RMS) {
+        const float gk = a.gains[k];
+        const float ms = v / (float)a.n[k];
+        const float rho = ms > 0.0f ? sqrtf(ms) : 0.0f;
+        const float den = fmaf(c, rho, a.eps[k]);
+        dfdg = c / den;
+        f = gk * dfdg;
+        if (rho > 0.0f) beta = gk * c * c / (den * den * (float)a.n[k] * rho);
+      } else if (a.variant == EWS_GRADED_STATIC_GAIN) {
+        dfdg = c;
+        f = a.gains[k] * c;
+      } else {
+        const float lam = a.gains[0];
+        const float lk1 = powf(lam, (float)(K - 1));
+        dfdg = (float)K * lk1 * c;
+        f = lk1 * lam * c;
+      }
+      s_f[w][k][i] = f;
+      if (valid && blockIdx.y == 0) {
+        float* fp = a.F + ((size_t)gr * N + k) * 3;
+        fp[0] = f;
+        fp[1] = beta;
+        fp[2] = dfdg;
+      }
+    }
+  });
+  __syncthreads();
+  sfor<0, 4>([&](auto hq) {
+    constexpr int h = hq;
+    const int col = hc + 16 * h + i;
+    if (col < a.hidden) {
+      const float bc = a.bias[col];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int row = 4 * g + r, grow = row0 + row;
+        if (grow < M) {
+          float v = bc;
+          sfor<0, N>([&](auto kc) {
+            constexpr int k = kc;
+            const float pv = r == 0 ? acc[k][h].x : (r == 1 ? acc[k][h].y : (r == 2 ? acc[k][h].z : acc[k][h].w));
+            v = fmaf(s_f[w][k][row], pv, v);
+            a.P[((size_t)grow * N + k) * a.hidden + col] = pv;
+          });
+          a.out[out_row(a, grow) * a.hidden + col] = v;
+        }
+      }
+    }
+  });
+}
+
+// the leading zero rows of the levels map to the bias alone
+__global__ void k_mix_bias_rows(MArgs a) {
+  const int b = blockIdx.x;
+  for (int col = threadIdx.x; col < a.hidden; col += blockDim.x)
+    a.out[(size_t)b * (a.R + 1) * a.hidden + col] = a.bias[col];
+}
+
+// Backward: a workgroup = 4 wavefronts x 16 rows; every column block of every level.
+template <int N>
+__global__ __launch_bounds__(256) void k_mix_bwd(MArgs a) {
+  __shared__ float s_c[4][3][2][16];
+  const int w = threadIdx.x >> 6, l = threadIdx.x & 63, i = l & 15, g = l >> 4;
+  const int M = a.B * a.R;
+  const int row0 = (blockIdx.x * 4 + w) * 16;
+  const int gr = row0 + i;
+  const bool valid = gr < M;
+  const float* drp = a.gout + (valid ? out_row(a, gr) : 0) * a.hidden;
+  // dot of each level's products with the row's cotangent (the four lanes of a row split the hidden columns)
+  sfor<0, N>([&](auto kc) {
+    constexpr int k = kc;
+    float dot = 0.0f;
+    if (valid) {
+      const float* pp = a.P + ((size_t)gr * N + k) * a.hidden;
+      for (int h = g; h < a.hidden; h += 4) dot = fmaf(pp[h], drp[h], dot);
+    }
+    dot += __shfl_xor(dot, 16, 64);
+    dot += __shfl_xor(dot, 32, 64);
+    if (g == 0) {
+      float f = 0.0f, bd = 0.0f;
+      if (valid) {
+        const float* fp = a.F + ((size_t)gr * N + k) * 3;
+        f = fp[0];
+        bd = fp[1] * dot;
+        a.dots[(size_t)gr * N + k] = dot;
+      }
+      s_c[w][k][0][i] = f;
+      s_c[w][k][1][i] = bd;
+    }
+  });
+  if (a.lvl0 && valid && g == 0) a.grows[(size_t)gr * a.W] = 0.0f;
+  __syncthreads();
+  sfor<0, N>([&](auto kc) {
+    constexpr int k = kc;
+    const int st = a.st[k], en = st + a.n[k];
+    for (int c0 = st; c0 < en; c0 += 16) {
+      const int col = c0 + i;  // this lane's column of the B operand and of the result
+      const bool cok = col < en;
+      f4 acc{0.0f, 0.0f, 0.0f, 0.0f};
+      for (int h0 = 0; h0 < a.hidden; h0 += 16) {
+        const int hh = h0 + 4 * g;
+        const f4 da = load4(drp, hh, a.hidden, valid);
+        float wv[4];
+#pragma unroll
+        for (int s = 0; s < 4; ++s)
+          wv[s] = (cok && hh + s < a.hidden) ? a.weight[(size_t)(hh + s) * a.D + col] : 0.0f;
+        acc = mfma(da.x, wv[0], acc);
+        acc = mfma(da.y, wv[1], acc);
+        acc = mfma(da.z, wv[2], acc);
+        acc = mfma(da.w, wv[3], acc);
+      }
+      if (cok) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int row = 4 * g + r, grow = row0 + row;
+          if (grow < M) {
+            const size_t e = (size_t)grow * a.W + a.lvl0 + col;
+            const float dy = r == 0 ? acc.x : (r == 1 ? acc.y : (r == 2 ? acc.z : acc.w));
+            a.grows[e] = fmaf(s_c[w][k][0][row], dy, -s_c[w][k][1][row] * a.rows[e]);
+          }
+        }
+      }
+    }
+  });
+}
+
+}  // namespace mixer
+}  // namespace ews
+
+// ================================================================================================= C ABI
+namespace {
+
+using namespace ews::mixer;
+
+size_t al256m(size_t x) { return (x + 255) & ~(size_t)255; }
+
+struct MPlan {
+  MArgs a;
+  size_t P, F, total;
+};
+
+int mixer_plan(const ews_mixer_desc* s, MPlan& p) {
+  if (!s) return EWS_ERR_NULL;
+  if (s->depth < 1 || s->depth > 3) return EWS_ERR_DEPTH;
+  if (s->variant < 0 || s->variant > 2) return EWS_ERR_OPTION;
+  if (s->batch < 1 || s->rows < 1 || s->dim < 1 || s->dim > 64 || s->hidden < 1) return EWS_ERR_SHAPE;
+  if (s->depth == 3 && s->dim > 16) return EWS_ERR_SHAPE;
+  MArgs& a = p.a;
+  a = MArgs{};
+  a.B = s->batch;
+  a.R = s->rows;
+  a.d = s->dim;
+  a.N = s->depth;
+  a.lvl0 = s->level0 ? 1 : 0;
+  a.hidden = s->hidden;
+  a.variant = s->variant;
+  a.prepend = s->prepend ? 1 : 0;
+  a.prescale = s->prescale ? 1 : 0;
+  int D = 0;
+  for (int k = 0, m = 1; k < a.N; ++k) {
+    m *= a.d;
+    a.st[k] = D;
+    a.n[k] = m;
+    a.eps[k] = s->eps[k];
+    D += m;
+  }
+  a.D = D;
+  a.W = D + a.lvl0;
+  const size_t M = (size_t)a.B * a.R;
+  size_t off = 0;
+  p.P = off;
+  off += al256m(M * a.N * a.hidden * 4);
+  p.F = off;
+  off += al256m(M * a.N * 3 * 4);
+  p.total = off;
+  return EWS_OK;
+}
+
+#define MIX_CHECK()                                            \
+  do {                                                         \
+    if (hipGetLastError() != hipSuccess) return EWS_ERR_LAUNCH; \
+  } while (0)
+
+}  // namespace
+
+extern "C" {
+
+size_t ews_mixer_residual_bytes(const ews_mixer_desc* desc) {
+  MPlan p;
+  if (mixer_plan(desc, p) != EWS_OK) return 0;
+  return p.total;
+}
+
+int ews_mixer_forward(const ews_mixer_desc* desc, const float* rows, const float* weight, const float* bias,
+                      const float* gains, float* out, void* residual, ews_stream_t stream) {
+  MPlan p;
+  const int rc = mixer_plan(desc, p);
+  if (rc != EWS_OK) return rc;
+  if (!rows || !weight || !bias || !gains || !out || !residual) return EWS_ERR_NULL;
+  MArgs a = p.a;
+  a.rows = rows;
+  a.weight = weight;
+  a.bias = bias;
+  a.gains = gains;
+  a.out = out;
+  a.P = (float*)((char*)residual + p.P);
+  a.F = (float*)((char*)residual + p.F);
+  hipStream_t st = (hipStream_t)stream;
+  const int M = a.B * a.R;
+  const dim3 grid((M + 63) / 64, (a.hidden + HC - 1) / HC), blk(256);
+  if (a.N == 1) hipLaunchKernelGGL(k_mix_fwd<1>, grid, blk, 0, st, a);
+  else if (a.N == 2) hipLaunchKernelGGL(k_mix_fwd<2>, grid, blk, 0, st, a);
+  else hipLaunchKernelGGL(k_mix_fwd<3>, grid, blk, 0, st, a);
+  MIX_CHECK();
+  if (a.prepend) {
+    hipLaunchKernelGGL(k_mix_bias_rows, dim3(a.B), dim3(64), 0, st, a);
+    MIX_CHECK();
+  }
+  return EWS_OK;
+}
+
+int ews_mixer_backward(const ews_mixer_desc* desc, const float* rows, const float* weight, const void* residual,
+                       const float* grad_out, float* grad_rows, float* row_dots, ews_stream_t stream) {
+  MPlan p;
+  const int rc = mixer_plan(desc, p);
+  if (rc != EWS_OK) return rc;
+  if (!rows || !weight || !residual || !grad_out || !grad_rows || !row_dots) return EWS_ERR_NULL;
+  MArgs a = p.a;
+  a.rows = rows;
+  a.weight = weight;
+  a.P = (float*)((char*)residual + p.P);
+  a.F = (float*)((char*)residual + p.F);
+  a.gout = grad_out;
+  a.grows = grad_rows;
+  a.dots = row_dots;
+  hipStream_t st = (hipStream_t)stream;
+  const int M = a.B * a.R;
+  const dim3 grid((M + 63) / 64), blk(256);
+  if (a.N == 1) hipLaunchKernelGGL(k_mix_bwd<1>, grid, blk, 0, st, a);
+  else if (a.N == 2) hipLaunchKernelGGL(k_mix_bwd<2>, grid, blk, 0, st, a);
+  else hipLaunchKernelGGL(k_mix_bwd<3>, grid, blk, 0, st, a);
+  MIX_CHECK();
+  return EWS_OK;
+}
+
+}  // extern "C"

@@ -12,7 +12,8 @@ from .layer import (  # noqa: F401
     log_signature_dim,
     lyndon_words,
 )
-from .ops import diag_scan  # noqa: F401
+from .mixer import GradedRMSNorm, MixerEpilogue, graded_level_slices  # noqa: F401
+from .ops import diag_scan, mixer_epilogue  # noqa: F401
 from .params import (  # noqa: F401
     AParamBlockDiag,
     AParamBoundedRotation,

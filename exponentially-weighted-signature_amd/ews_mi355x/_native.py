@@ -49,7 +49,12 @@ EXPORTED = (
     "ews_log_workspace_bytes",
     "ews_log_forward",
     "ews_log_backward",
+    "ews_mixer_residual_bytes",
+    "ews_mixer_forward",
+    "ews_mixer_backward",
 )
+
+GRADED_VARIANTS = {"live_rms": 0, "static_gain": 1, "dilation": 2}
 
 
 class DiagDesc(ctypes.Structure):
@@ -94,6 +99,21 @@ class LogDesc(ctypes.Structure):
         ("depth", ctypes.c_int32),
         ("level0", ctypes.c_int32),
         ("readout", ctypes.c_int32),
+    ]
+
+
+class MixerDesc(ctypes.Structure):
+    _fields_ = [
+        ("batch", ctypes.c_int32),
+        ("rows", ctypes.c_int32),
+        ("dim", ctypes.c_int32),
+        ("depth", ctypes.c_int32),
+        ("level0", ctypes.c_int32),
+        ("hidden", ctypes.c_int32),
+        ("variant", ctypes.c_int32),
+        ("prepend", ctypes.c_int32),
+        ("prescale", ctypes.c_int32),
+        ("eps", ctypes.c_float * 3),
     ]
 
 
@@ -163,6 +183,13 @@ def load():
     lib.ews_log_forward.restype = i32
     lib.ews_log_backward.argtypes = [ldp, vp, vp, vp, vp, vp]
     lib.ews_log_backward.restype = i32
+    mdp = ctypes.POINTER(MixerDesc)
+    lib.ews_mixer_residual_bytes.argtypes = [mdp]
+    lib.ews_mixer_residual_bytes.restype = sz
+    lib.ews_mixer_forward.argtypes = [mdp, vp, vp, vp, vp, vp, vp, vp]
+    lib.ews_mixer_forward.restype = i32
+    lib.ews_mixer_backward.argtypes = [mdp, vp, vp, vp, vp, vp, vp, vp]
+    lib.ews_mixer_backward.restype = i32
     _lib = lib
     return lib
 

@@ -303,3 +303,74 @@ class LogRows(torch.autograd.Function):
 
 def log_rows(rows, d, N, level0=True, readout="prefix"):
     return LogRows.apply(rows, int(d), int(N), bool(level0), readout)
+
+
+# ---------------------------------------------------------------------------------------------- mixer epilogue
+def _al256(x):
+    return (x + 255) // 256 * 256
+
+
+class MixerFn(torch.autograd.Function):
+    """r = c_down(graded(prescale(levels))) of EWS prefix rows (B, R, level0 + D), fused in one pass
+    (ews_mixer_forward / ews_mixer_backward; reference ews/block.py:282-306, 336-357, 405-408). The parameter
+    gradients are assembled here from the kernel's per-row quantities: grad_bias = sum of grad_out, grad_gains =
+    sum of row_dots times the gain factor, grad_weight per level = (scale_k grad_out)^T x_k (a plain GEMM)."""
+
+    @staticmethod
+    def forward(ctx, rows, weight, bias, gains, d, N, variant, eps, prepend, prescale, level0):
+        lib = nat.load()
+        for nm, t in (("rows", rows), ("weight", weight), ("bias", bias), ("gains", gains)):
+            if not t.is_cuda or t.dtype != torch.float32:
+                raise TypeError(f"{nm} must be a float32 tensor on the HIP device")
+        rows = rows.contiguous()
+        weight = weight.contiguous()
+        B, R, W = rows.shape
+        hidden = weight.shape[0]
+        eps3 = (ctypes.c_float * 3)(*[float(e) for e in (list(eps) + [0.0] * 3)[:3]])
+        desc = nat.MixerDesc(B, R, d, N, int(level0), hidden, nat.GRADED_VARIANTS[variant], int(prepend),
+                             int(prescale), eps3)
+        out = torch.empty((B, R + int(prepend), hidden), device=rows.device, dtype=torch.float32)
+        resid = torch.empty(int(lib.ews_mixer_residual_bytes(ctypes.byref(desc))), device=rows.device,
+                            dtype=torch.uint8)
+        nat.check(lib.ews_mixer_forward(ctypes.byref(desc), rows.data_ptr(), weight.data_ptr(),
+                                        bias.contiguous().data_ptr(), gains.contiguous().data_ptr(), out.data_ptr(),
+                                        resid.data_ptr(), _stream_handle(rows.device)), "ews_mixer_forward")
+        ctx.save_for_backward(rows, weight, gains, resid)
+        ctx.meta = (desc, d, N, variant, int(prepend), int(level0))
+        return out
+
+    @staticmethod
+    def backward(ctx, gout):
+        lib = nat.load()
+        rows, weight, gains, resid = ctx.saved_tensors
+        desc, d, N, variant, prepend, level0 = ctx.meta
+        gout = gout.to(torch.float32).contiguous()
+        B, R, W = rows.shape
+        hidden = weight.shape[0]
+        M = B * R
+        grows = torch.empty_like(rows)
+        dots = torch.empty((B, R, N), device=rows.device, dtype=torch.float32)
+        nat.check(lib.ews_mixer_backward(ctypes.byref(desc), rows.data_ptr(), weight.data_ptr(), resid.data_ptr(),
+                                         gout.data_ptr(), grows.data_ptr(), dots.data_ptr(),
+                                         _stream_handle(rows.device)), "ews_mixer_backward")
+        # residual: level products (M, N, hidden) then factors (M, N, 3) = (scale, beta, d scale / d gain)
+        F = resid[_al256(M * N * hidden * 4):].view(torch.float32)[: M * N * 3].view(M, N, 3)
+        dr = gout[:, prepend:, :].reshape(M, hidden)
+        gbias = gout.sum((0, 1))
+        gd = (F[:, :, 2] * dots.reshape(M, N)).sum(0)
+        ggains = gd.sum().reshape(gains.shape) if variant == "dilation" else gd
+        gweight = torch.empty_like(weight)
+        st = 0
+        for k in range(N):
+            n = d ** (k + 1)
+            xk = rows[:, :, level0 + st: level0 + st + n].reshape(M, n)
+            gweight[:, st: st + n] = (dr * F[:, k, 0:1]).t() @ xk
+            st += n
+        return grows, gweight, gbias, ggains, None, None, None, None, None, None, None
+
+
+def mixer_epilogue(rows, weight, bias, gains, d, N, variant="live_rms", eps=(1e-3,), prepend=True, prescale=False,
+                   level0=True):
+    eps = tuple(eps) if isinstance(eps, (tuple, list)) else (float(eps),) * N
+    return MixerFn.apply(rows, weight, bias, gains, int(d), int(N), variant, eps, bool(prepend), bool(prescale),
+                         bool(level0))

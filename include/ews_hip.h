@@ -211,6 +211,47 @@ int ews_log_forward(const ews_log_desc* desc, const float* sig_rows, float* out,
 int ews_log_backward(const ews_log_desc* desc, const float* sig_rows, const float* grad_out, float* grad_rows,
                      void* workspace, ews_stream_t stream);
 
+/* ---------------------------------------------------------------------------------------------------------
+ * Mixer epilogue of an EWS block (ews/block.py:282-306, 336-357, 405-408; ews/norms.py:47-134): the prefix
+ * rows' levels without the level-0 column, an optional leading zero row, the optional binomial prescale, the
+ * per-level GradedRMSNorm and the c_down linear map, fused in one pass over the rows.
+ * --------------------------------------------------------------------------------------------------------- */
+#define EWS_GRADED_LIVE_RMS 0    /* g_k x_k / (RMS_k + eps_k) */
+#define EWS_GRADED_STATIC_GAIN 1 /* g_k x_k */
+#define EWS_GRADED_DILATION 2    /* lam^k x_k */
+
+typedef struct ews_mixer_desc {
+  int32_t batch;    /* B >= 1 */
+  int32_t rows;     /* R scan rows per sample (>= 1) */
+  int32_t dim;      /* d: 1..64 (1..16 at depth 3) */
+  int32_t depth;    /* N in {1, 2, 3} */
+  int32_t level0;   /* 1: the rows carry the leading level-0 column (the flat EWS output) */
+  int32_t hidden;   /* output width of c_down (>= 1) */
+  int32_t variant;  /* EWS_GRADED_* */
+  int32_t prepend;  /* 1: the levels start with a zero row (ews/block.py:304-305): out has R + 1 rows */
+  int32_t prescale; /* 1: level k of levels row t scaled by 1 / C(max(t + 1, k), k) (graded_prescale="binomial") */
+  float eps[3];     /* live_rms floors per level */
+} ews_mixer_desc;
+
+/* Residual saved by the forward for the backward: per scan row, each level's products with its c_down block,
+ * its total scale and the two derivative factors. */
+size_t ews_mixer_residual_bytes(const ews_mixer_desc* desc);
+
+/* rows (B, R, level0 + D) -> out (B, R + prepend, hidden) = c_down(graded(prescale(levels))). weight
+ * (hidden, D) row-major and bias (hidden,) are c_down's (eqx.nn.Linear); gains are GradedRMSNorm.gains (N,) or,
+ * for the dilation variant, lam (1,). Replaces jax.vmap(self.c_down)(self.graded(levels)) of
+ * EWSBlock.mixer_levels / _forward (ews/block.py:405-406) after _mixer_levels / _prescale. */
+int ews_mixer_forward(const ews_mixer_desc* desc, const float* rows, const float* weight, const float* bias,
+                      const float* gains, float* out, void* residual, ews_stream_t stream);
+
+/* Backward: the cotangent grad_out of out -> grad_rows (B, R, level0 + D) (level-0 column zero; the input of the
+ * scan's backward) and row_dots (B, R, N), the dot product of each level's c_down products with the row's
+ * cotangent. The parameter gradients follow from these on the host: grad_bias = sum of grad_out, grad_gains =
+ * sum over rows of row_dots times the residual's gain factor, grad_weight[:, level k] = sum over rows of
+ * (scale_k grad_out) (x) level k (a plain GEMM). */
+int ews_mixer_backward(const ews_mixer_desc* desc, const float* rows, const float* weight, const void* residual,
+                       const float* grad_out, float* grad_rows, float* row_dots, ews_stream_t stream);
+
 /* Human-readable text of a return code. */
 const char* ews_error_string(int code);
 

@@ -197,3 +197,45 @@ def test_dense_layer_routing_and_errors():
         ops.DenseLeaf("van_loan", reweighting_mode="uniform")
     with pytest.raises(RuntimeError, match="HIP device"):
         E.EWS(A, N=3, leaf="series", series_q=8)(torch.zeros(5, 4), torch.linspace(0, 1, 5))
+
+
+def _mdesc(**kw):
+    base = dict(batch=2, rows=5, dim=4, depth=2, level0=1, hidden=7, variant=0, prepend=1, prescale=0)
+    base.update(kw)
+    eps = kw.pop("eps", (1e-3, 1e-3, 1e-3))
+    base.pop("eps", None)
+    return nat.MixerDesc(**base, eps=(ctypes.c_float * 3)(*eps))
+
+
+def test_mixer_c_abi_error_codes():
+    lib = nat.load()
+    null = ctypes.c_void_p(0)
+    good = _mdesc()
+    # level products (10 rows x 2 levels x 7) then factors (10 x 2 x 3), each 256-byte aligned
+    assert lib.ews_mixer_residual_bytes(ctypes.byref(good)) == 768 + 256
+    assert lib.ews_mixer_forward(ctypes.byref(good), null, null, null, null, null, null, null) == -1
+    assert lib.ews_mixer_backward(ctypes.byref(good), null, null, null, null, null, null, null) == -1
+    bad = {"depth": (_mdesc(depth=4), -3), "wide depth 3": (_mdesc(dim=17, depth=3), -2),
+           "dim": (_mdesc(dim=65), -2), "hidden": (_mdesc(hidden=0), -2), "rows": (_mdesc(rows=0), -2),
+           "variant": (_mdesc(variant=3), -4)}
+    for name, (dsc, code) in bad.items():
+        assert lib.ews_mixer_forward(ctypes.byref(dsc), null, null, null, null, null, null, null) == code, name
+        assert lib.ews_mixer_backward(ctypes.byref(dsc), null, null, null, null, null, null, null) == code, name
+        assert lib.ews_mixer_residual_bytes(ctypes.byref(dsc)) == 0, name
+
+
+def test_mixer_module_mirrors_reference_fields_and_errors():
+    m = E.MixerEpilogue(3, 2, 5, graded_variant="dilation", graded_prescale="binomial")
+    assert m.graded.level_slices == ((0, 3), (3, 12)) and m.graded.gains is None and m.graded.lam.shape == ()
+    assert tuple(m.c_down.weight.shape) == (5, 12) and tuple(m.c_down.bias.shape) == (5,)
+    assert E.graded_level_slices(2, 3) == ((0, 2), (2, 6), (6, 14))
+    with pytest.raises(ValueError, match="variant must be one of"):
+        E.GradedRMSNorm(2, 2, variant="flat")
+    with pytest.raises(ValueError, match="eps must be a scalar"):
+        E.GradedRMSNorm(2, 2, eps=[1e-3])
+    with pytest.raises(ValueError, match="last axis must be D"):
+        E.GradedRMSNorm(2, 2)(torch.zeros(5, 7))
+    with pytest.raises(ValueError, match="graded_prescale must be None or 'binomial'"):
+        E.MixerEpilogue(2, 2, 3, graded_prescale="poisson")
+    with pytest.raises(TypeError, match="HIP device"):  # no CPU path for the fused epilogue
+        m(torch.zeros(4, 13))
