@@ -150,6 +150,9 @@ def bench_diag_cfg(args):
     else:
         path_np, clock_np, A_np = c5_inputs()
         structure, bwd, log, bf16 = nat.STRUCT_PLANES, True, False, True
+    mix = bool(args.mixer) and cfg != "c1"  # the block's mixer epilogue (graded norm + c_down) after the scan
+    if mix:
+        log = False
     B, L, d = path_np.shape
     D = d + d * d
     W = D + 1
@@ -172,12 +175,24 @@ def bench_diag_cfg(args):
         lws = torch.empty(max(16, int(lib.ews_log_workspace_bytes(ctypes.byref(ldesc)))), device=dev,
                           dtype=torch.uint8)
         names = names + ["log_forward"]
+    if mix:
+        from ews_mi355x.mixer import MixerEpilogue
+        from ews_mi355x.ops import MixerFn
+
+        hidden = d
+        mixer = MixerEpilogue(d, N, hidden).to(dev)
+        with torch.no_grad():
+            mixer.c_down.weight.normal_(0.0, 1.0 / np.sqrt(D))
+        mW, mb, mg = mixer.c_down.weight, mixer.c_down.bias, mixer.graded.gains
+        names = names + ["mixer_forward"]
     if bwd:
         gsrc = torch.randn((B, L - 1, Dlog if log else W), device=dev, dtype=torch.float32)
         gout = torch.empty((B, L - 1, W), device=dev, dtype=torch.float32) if log else gsrc
+        if mix:
+            gmix = torch.randn((B, L, hidden), device=dev, dtype=torch.float32)
         dpath = torch.empty((B, L, d), device=dev, dtype=torch.float32)
         dA = torch.empty_like(A)
-        names = names + (["log_backward"] if log else []) + BWD_PASS_NAMES[:nb]
+        names = names + (["log_backward"] if log else []) + (["mixer_backward"] if mix else []) + BWD_PASS_NAMES[:nb]
 
     def step(events=None):
         st = ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream)
@@ -195,7 +210,19 @@ def bench_diag_cfg(args):
             i += 1
             nat.check(lib.ews_log_forward(ctypes.byref(ldesc), out.data_ptr(), lout.data_ptr(), lws.data_ptr(), st),
                       "log forward")
+        g_rows = gout if bwd else None
+        if mix:
+            if events is not None:
+                events[i].record()
+            i += 1
+            rows_in = out.detach().requires_grad_(bwd)
+            r = MixerFn.apply(rows_in, mW, mb, mg, d, N, "live_rms", mixer.graded.eps, True, False, True)
         if bwd:
+            if mix:
+                if events is not None:
+                    events[i].record()
+                i += 1
+                g_rows = torch.autograd.grad(r, (rows_in, mW, mb, mg), gmix)[0]
             if log:
                 if events is not None:
                     events[i].record()
@@ -207,7 +234,7 @@ def bench_diag_cfg(args):
                     events[i].record()
                 i += 1
                 nat.check(lib.ews_diag_backward_pass(ctypes.byref(desc), p, path.data_ptr(), clock.data_ptr(),
-                                                     A.data_ptr(), resid.data_ptr(), gout.data_ptr(),
+                                                     A.data_ptr(), resid.data_ptr(), g_rows.data_ptr(),
                                                      dpath.data_ptr(), None, dA.data_ptr(), ws.data_ptr(), st),
                           "backward pass")
         if events is not None:
@@ -240,17 +267,43 @@ def bench_diag_cfg(args):
     if log:
         ab["log_forward"] = n * 4 * (W + Dlog)            # read state rows, write log rows
         ab["log_backward"] = n * 4 * (2 * W + Dlog)       # read state rows and log cotangents, write row cotangents
+    torch_mix = None
+    if mix:
+        ab["mixer_forward"] = n * 4 * (W + hidden)        # read state rows, write the hidden-wide rows
+        ab["mixer_backward"] = n * 4 * (2 * W + hidden)   # read state rows and output cotangents, write row cotangents
+        # the same epilogue composed from torch ops (what a host-side block does), forward + backward, same rows
+        x_t = out.detach().requires_grad_(True)
+
+        def torch_epi():
+            lv = torch.cat([torch.zeros_like(x_t[:, :1, 1:]), x_t[:, :, 1:]], 1)
+            y = torch.nn.functional.linear(mixer.graded(lv), mW, mb)
+            torch.autograd.grad(y, (x_t, mW, mb, mg), gmix)
+
+        for _ in range(3):
+            torch_epi()
+        t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        t0.record()
+        for _ in range(args.steps):
+            torch_epi()
+        t1.record()
+        torch.cuda.synchronize()
+        torch_mix = round(t0.elapsed_time(t1) / args.steps, 4)
     dominant = max((k for k in pass_ms if k in ab), key=pass_ms.get)
     achieved = ab[dominant] / (pass_ms[dominant] * 1e-3) / 1e9
     total = ab["fwd_total"] + (ab["bwd_total"] if bwd else 0)
     if log:
         total += ab["log_forward"] + (ab["log_backward"] if bwd else 0)
+    if mix:
+        total += ab["mixer_forward"] + (ab["mixer_backward"] if bwd else 0)
     what = {"c1": "c1: single EWS layer, B=8, L=1024, 3 time-augmented channels lifted to d=8, real diagonal A, "
                   "depth 2, fp32, prefix readout, forward",
             "c4": "c4: one of 4 stacked LogEWS blocks, B=256, L=512, 8-token vocabulary embedded to d=32, real "
                   "diagonal A, depth 2, fp32, EWS scan + LogEWS compression (prefix), forward + backward",
             "c5": "c5: one of 3 stacked EWS blocks, B=8, L=49920, 6 band-limited channels lifted to d=24 (12 rotation "
                   "planes), depth 2, bf16 path / fp32 state, prefix readout, forward + backward"}[cfg]
+    if mix:
+        what = (what.replace("EWS scan + LogEWS compression (prefix)", "EWS scan")
+                + f", then the mixer epilogue (drop level 0, zero row, GradedRMSNorm live_rms, c_down to {hidden})")
     return {
         "metric": "EWS " + ("forward" if not bwd else "forward+backward") + " time-steps/sec and HBM GB/s (% peak) "
                   "on 1 MI355X",
@@ -272,6 +325,9 @@ def bench_diag_cfg(args):
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
                      "algorithmic_bytes": ab[dominant]},
         "passes_ms": {k: round(v, 4) for k, v in pass_ms.items()},
+        **({"mixer_epilogue_torch_ops_fwd_bwd_ms": torch_mix,
+            "mixer_epilogue_fused_fwd_bwd_ms": round(pass_ms["mixer_forward"] + pass_ms.get("mixer_backward", 0.0), 4)}
+           if mix else {}),
     }
 
 
@@ -478,6 +534,9 @@ def main():
     ap.add_argument("--backward", action="store_true", help="c3: time forward + backward (ews_dense_backward)")
     ap.add_argument("--leaf", choices=["series", "van_loan"], default="series",
                     help="leaf of the c3 forward: series (q=24) or Van Loan (M=20, cayley)")
+    ap.add_argument("--mixer", action="store_true",
+                    help="c4 / c5: the block's mixer epilogue (GradedRMSNorm + c_down, hidden = d) after the scan, "
+                         "in place of c4's LogEWS readout")
     ap.add_argument("--clock-grad", action="store_true",
                     help="also compute the clock gradient (the c2 clock is data; off by default)")
     ap.add_argument("--copy-probe", action="store_true",

@@ -363,10 +363,23 @@ class MixerFn(torch.autograd.Function):
         st = 0
         for k in range(N):
             n = d ** (k + 1)
-            xk = rows[:, :, level0 + st: level0 + st + n].reshape(M, n)
-            gweight[:, st: st + n] = (dr * F[:, k, 0:1]).t() @ xk
+            xk = rows[:, :, level0 + st: level0 + st + n].reshape(M, n)  # a strided view, no copy
+            gweight[:, st: st + n] = _split_k_tn(dr * F[:, k, 0:1], xk)
             st += n
         return grows, gweight, gbias, ggains, None, None, None, None, None, None, None
+
+
+def _split_k_tn(a, b, chunks=64):
+    """a^T b for tall a (M, h) and b (M, n): a GEMM whose output is small and whose reduction runs over every
+    row. A single library call tiles only the small output (a few workgroups); here the rows are cut into
+    ``chunks`` batches of one batched GEMM whose partial products are then summed."""
+    M = a.shape[0]
+    S = min(chunks, max(1, M // 256))
+    m = M // S
+    out = torch.bmm(a[: S * m].reshape(S, m, -1).transpose(1, 2), b[: S * m].reshape(S, m, -1)).sum(0)
+    if S * m < M:
+        out = out + a[S * m:].t() @ b[S * m:]
+    return out
 
 
 def mixer_epilogue(rows, weight, bias, gains, d, N, variant="live_rms", eps=(1e-3,), prepend=True, prescale=False,

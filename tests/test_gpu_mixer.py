@@ -5,6 +5,7 @@ Bars: forward max relative error <= 1e-5, gradients <
 (the reference's tests/test_engines.py:31-33). Cases cover every GradedRMSNorm variant, the binomial prescale,
 basepoint blocks (no leading zero row), depths 1-3, the widths of BASELINE.json configs[3] (d = 32) and [4]
 (d = 24), more than 64 hidden columns (two workgroup column passes), level sizes that are not multiples of 16,
+row counts above 256K (two row tiles per wavefront in the forward),
 all-zero levels (the zero-safe RMS) and the chain scan -> epilogue with gradients to the path.
 """
 
@@ -68,6 +69,9 @@ CASES = [
     (16, 3, 70, "live_rms", False, False, 1, 19),
     (5, 1, 3, "static_gain", False, False, 2, 9),
     (7, 2, 17, "live_rms", True, True, 1, 64),
+    # 256K rows and more: two row tiles per wavefront in the forward
+    (3, 2, 5, "live_rms", True, False, 2, 140000),
+    (2, 2, 40, "static_gain", False, True, 1, 270000),
 ]
 
 
