@@ -293,6 +293,111 @@ __global__ __launch_bounds__(256) void k_mix_bwd(MArgs a) {
   });
 }
 
+// Backward in two kernels, for c_down up to 128 wide. First, per row, the dot of each level's products with the
+// row's cotangent (row_dots) and the zero level-0 cotangent. Then the columns: a wavefront owns two 16-column
+// tiles, keeps their c_down blocks in registers (W[h][c], h < hidden) and walks a chunk of 16-row tiles:
+// dy = dr W (MFMA, contraction over the hidden columns), dx = f dy - beta dot x with each lane's own level (a
+// tile may straddle two levels). Each row element is read once; the chunk's output cotangents (hidden floats per
+// row) are shared through L2 by the column workgroups of the chunk, which are consecutive in the grid.
+constexpr int BW_HB = 8;    // hidden blocks of 16 held in registers: hidden <= 128 (4 up to 64)
+constexpr int BW_RC = 32;   // row tiles per workgroup chunk
+
+__global__ __launch_bounds__(256) void k_mix_bwd_dots(MArgs a) {
+  const int l = threadIdx.x & 63, i = l & 15, g = l >> 4, w = threadIdx.x >> 6;
+  const int M = a.B * a.R;
+  const int gr = (blockIdx.x * 4 + w) * 16 + i;
+  const bool valid = gr < M;
+  const float* drp = a.gout + (valid ? out_row(a, gr) : 0) * a.hidden;
+  for (int k = 0; k < a.N; ++k) {
+    float dot = 0.0f;
+    if (valid) {
+      const float* pp = a.P + ((size_t)gr * a.N + k) * a.hidden;
+      for (int h = g; h < a.hidden; h += 4) dot = fmaf(pp[h], drp[h], dot);
+    }
+    dot += __shfl_xor(dot, 16, 64);
+    dot += __shfl_xor(dot, 32, 64);
+    if (valid && g == 0) a.dots[(size_t)gr * a.N + k] = dot;
+  }
+  if (a.lvl0 && valid && g == 0) a.grows[(size_t)gr * a.W] = 0.0f;
+}
+
+// XCD-aware order: the hardware deals consecutive workgroups round-robin to the 8 XCDs (each with its own L2);
+// renumbering by (id mod 8, id / 8) gives each XCD a contiguous run of logical workgroups, so the column workgroups
+// of one row chunk share an L2 (their output-cotangent rows and the two halves of every row line)
+__device__ __forceinline__ int xcd_logical(int hw, int total) {
+  const int per = total >> 3;  // total is a multiple of 8
+  return (hw & 7) * per + (hw >> 3);
+}
+
+template <int HB>
+__global__ __launch_bounds__(256) void k_mix_bwd_cols(MArgs a, int ncolwg, int nchunks) {
+  const int w = threadIdx.x >> 6, l = threadIdx.x & 63, i = l & 15, g = l >> 4;
+  const int M = a.B * a.R;
+  const int total = gridDim.x;
+  const int lid = xcd_logical(blockIdx.x, total);
+  const int cwg = lid % ncolwg, chunk = lid / ncolwg;
+  if (chunk >= nchunks) return;  // padding of the grid to a multiple of 8 (uniform over the workgroup)
+  // two 16-column tiles per wavefront: a row's 32 columns of one wavefront are one 128-byte run
+  int col[2], lev[2];
+  bool cok[2];
+#pragma unroll
+  for (int ct = 0; ct < 2; ++ct) {
+    col[ct] = (cwg * 4 + w) * 32 + 16 * ct + i;
+    cok[ct] = col[ct] < a.D;
+    lev[ct] = 0;
+    for (int k = 1; k < a.N; ++k)
+      if (col[ct] >= a.st[k]) lev[ct] = k;
+  }
+  const int nhb = (a.hidden + 15) / 16;
+  float wr[2][HB][4];  // c_down blocks of the two tiles: W[16 hb + 4 g + s][col]
+#pragma unroll
+  for (int ct = 0; ct < 2; ++ct)
+#pragma unroll
+    for (int hb = 0; hb < HB; ++hb)
+#pragma unroll
+      for (int s = 0; s < 4; ++s) {
+        const int h = 16 * hb + 4 * g + s;
+        wr[ct][hb][s] = (hb < nhb && cok[ct] && h < a.hidden) ? a.weight[(size_t)h * a.D + col[ct]] : 0.0f;
+      }
+  const int t0 = chunk * BW_RC;
+  for (int tt = t0; tt < t0 + BW_RC; ++tt) {
+    const int row0 = tt * 16;
+    if (row0 >= M) break;  // uniform over the workgroup
+    const int ga = row0 + i;  // A-operand row of this lane
+    const float* drp = a.gout + (ga < M ? out_row(a, ga) : 0) * a.hidden;
+    f4 acc[2] = {f4{0.0f, 0.0f, 0.0f, 0.0f}, f4{0.0f, 0.0f, 0.0f, 0.0f}};
+#pragma unroll
+    for (int hb = 0; hb < HB; ++hb) {
+      if (hb < nhb) {
+        const f4 da = load4(drp, 16 * hb + 4 * g, a.hidden, ga < M);
+#pragma unroll
+        for (int ct = 0; ct < 2; ++ct) {
+          acc[ct] = mfma(da.x, wr[ct][hb][0], acc[ct]);
+          acc[ct] = mfma(da.y, wr[ct][hb][1], acc[ct]);
+          acc[ct] = mfma(da.z, wr[ct][hb][2], acc[ct]);
+          acc[ct] = mfma(da.w, wr[ct][hb][3], acc[ct]);
+        }
+      }
+    }
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int grow = row0 + 4 * g + r;
+      if (grow < M) {
+#pragma unroll
+        for (int ct = 0; ct < 2; ++ct) {
+          if (cok[ct]) {
+            const float* fp = a.F + ((size_t)grow * a.N + lev[ct]) * 3;
+            const float bd = fp[1] * a.dots[(size_t)grow * a.N + lev[ct]];
+            const size_t e = (size_t)grow * a.W + a.lvl0 + col[ct];
+            const float dy = r == 0 ? acc[ct].x : (r == 1 ? acc[ct].y : (r == 2 ? acc[ct].z : acc[ct].w));
+            a.grows[e] = fmaf(fp[0], dy, -bd * a.rows[e]);
+          }
+        }
+      }
+    }
+  }
+}
+
 }  // namespace mixer
 }  // namespace ews
 
@@ -417,12 +522,23 @@ int ews_mixer_backward(const ews_mixer_desc* desc, const float* rows, const floa
   a.dots = row_dots;
   hipStream_t st = (hipStream_t)stream;
   const int M = a.B * a.R;
-  // one row tile per wavefront: sharing c_down's loads over four tiles measured slower (fewer wavefronts to hide
-  // the row loads; 1.59 against 1.35 ms at 399K rows of 601 floats)
-  const dim3 grid((M + 63) / 64), blk(256);
-  if (a.N == 1) hipLaunchKernelGGL((k_mix_bwd<1, 1>), grid, blk, 0, st, a);
-  else if (a.N == 2) hipLaunchKernelGGL((k_mix_bwd<2, 1>), grid, blk, 0, st, a);
-  else hipLaunchKernelGGL((k_mix_bwd<3, 1>), grid, blk, 0, st, a);
+  const dim3 blk(256);
+  if (a.hidden <= 16 * BW_HB) {
+    // rows' dots, then column tiles over chunks of row tiles (column workgroups of a chunk consecutive)
+    hipLaunchKernelGGL(k_mix_bwd_dots, dim3((M + 63) / 64), blk, 0, st, a);
+    MIX_CHECK();
+    const int tiles = (M + 15) / 16;
+    const int ncolwg = (a.D + 127) / 128, nchunks = (tiles + BW_RC - 1) / BW_RC;
+    const int total = (ncolwg * nchunks + 7) / 8 * 8;  // the XCD renumbering needs a multiple of 8
+    if (a.hidden <= 64) hipLaunchKernelGGL(k_mix_bwd_cols<4>, dim3(total), blk, 0, st, a, ncolwg, nchunks);
+    else hipLaunchKernelGGL(k_mix_bwd_cols<BW_HB>, dim3(total), blk, 0, st, a, ncolwg, nchunks);
+  } else {
+    // wider c_down: a wavefront per 16 rows, every column block (c_down re-read per row tile)
+    const dim3 grid((M + 63) / 64);
+    if (a.N == 1) hipLaunchKernelGGL((k_mix_bwd<1, 1>), grid, blk, 0, st, a);
+    else if (a.N == 2) hipLaunchKernelGGL((k_mix_bwd<2, 1>), grid, blk, 0, st, a);
+    else hipLaunchKernelGGL((k_mix_bwd<3, 1>), grid, blk, 0, st, a);
+  }
   MIX_CHECK();
   return EWS_OK;
 }

@@ -72,6 +72,8 @@ CASES = [
     # 256K rows and more: two row tiles per wavefront in the forward
     (3, 2, 5, "live_rms", True, False, 2, 140000),
     (2, 2, 40, "static_gain", False, True, 1, 270000),
+    # c_down wider than 128: the backward's row-tile kernel instead of the column-tile one
+    (3, 2, 150, "live_rms", True, False, 2, 45),
 ]
 
 
