@@ -359,10 +359,27 @@ __global__ __launch_bounds__(256) void k_mix_bwd_cols(MArgs a, int ncolwg, int n
         const int h = 16 * hb + 4 * g + s;
         wr[ct][hb][s] = (hb < nhb && cok[ct] && h < a.hidden) ? a.weight[(size_t)h * a.D + col[ct]] : 0.0f;
       }
+  // per-row factors of each level (scale f, correction beta * dot) staged once per row tile for the four
+  // wavefronts, double-buffered: the barrier of tile t + 1 orders every read of tile t before slot t is rewritten
+  __shared__ float s_fb[2][16][3][2];
   const int t0 = chunk * BW_RC;
   for (int tt = t0; tt < t0 + BW_RC; ++tt) {
     const int row0 = tt * 16;
     if (row0 >= M) break;  // uniform over the workgroup
+    const int slot = tt & 1;
+    if (threadIdx.x < 16 * a.N) {
+      const int r = threadIdx.x % 16, k = threadIdx.x / 16;
+      const int grow = row0 + r;
+      float f = 0.0f, bd = 0.0f;
+      if (grow < M) {
+        const float* fp = a.F + ((size_t)grow * a.N + k) * 3;
+        f = fp[0];
+        bd = fp[1] * a.dots[(size_t)grow * a.N + k];
+      }
+      s_fb[slot][r][k][0] = f;
+      s_fb[slot][r][k][1] = bd;
+    }
+    __syncthreads();
     const int ga = row0 + i;  // A-operand row of this lane
     const float* drp = a.gout + (ga < M ? out_row(a, ga) : 0) * a.hidden;
     f4 acc[2] = {f4{0.0f, 0.0f, 0.0f, 0.0f}, f4{0.0f, 0.0f, 0.0f, 0.0f}};
@@ -381,16 +398,14 @@ __global__ __launch_bounds__(256) void k_mix_bwd_cols(MArgs a, int ncolwg, int n
     }
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
-      const int grow = row0 + 4 * g + r;
+      const int row = 4 * g + r, grow = row0 + row;
       if (grow < M) {
 #pragma unroll
         for (int ct = 0; ct < 2; ++ct) {
           if (cok[ct]) {
-            const float* fp = a.F + ((size_t)grow * a.N + lev[ct]) * 3;
-            const float bd = fp[1] * a.dots[(size_t)grow * a.N + lev[ct]];
             const size_t e = (size_t)grow * a.W + a.lvl0 + col[ct];
             const float dy = r == 0 ? acc[ct].x : (r == 1 ? acc[ct].y : (r == 2 ? acc[ct].z : acc[ct].w));
-            a.grows[e] = fmaf(fp[0], dy, -bd * a.rows[e]);
+            a.grows[e] = fmaf(s_fb[slot][row][lev[ct]][0], dy, -s_fb[slot][row][lev[ct]][1] * a.rows[e]);
           }
         }
       }
