@@ -317,46 +317,53 @@ __device__ __forceinline__ float ref_step(const DiagArgs& a) {
   const int Tc = min(a.T, a.n_int);
   return (a.clock[Tc] - a.clock[0]) / (float)Tc;
 }
-__global__ __launch_bounds__(64) void k_coef_table(DiagArgs a) {
-  const int j = threadIdx.x >> 3, k = threadIdx.x & 7;
+// Three wavefronts share the entries (a single chain of series and exponentials per lane otherwise): wavefront 0
+// the plane nodes and the pair flows, 1 the B-pair divided differences, 2 the A-pair ones.
+__global__ __launch_bounds__(192) void k_coef_table(DiagArgs a) {
+  const int role = threadIdx.x >> 6, l = threadIdx.x & 63;
+  const int j = l >> 3, k = l & 7;
   float* tab = a.ctab;
   const float h0 = ref_step(a);
-  if (threadIdx.x == 0) tab[0] = h0;
   const cf uj = load_u(a.params, j), uk = load_u(a.params, k);
   const cf xj = h0 * uj;
-  if (k == 0) {
-    const Node1<cf> nj = node1(xj);
-    const cf ri = expv(-xj);
-    stp(tab, j, TP_RHO, nj.e);
-    stp(tab, j, TP_RHO1, nj.e * uj);
-    stp(tab, j, TP_RHOI, ri);
-    stp(tab, j, TP_RHOI1, -(ri * uj));
-    stp(tab, j, TP_PHI, nj.p);
-    stp(tab, j, TP_PHI1, nj.dp * uj);
-    stp(tab, j, TP_DPHI, nj.dp);
-    stp(tab, j, TP_PHIH, 0.5f * nj.p);
-    stp(tab, j, TP_PHI1H, 0.5f * (nj.dp * uj));
-  }
   const cf ub = uj + uk, ua = uj + conj(uk);
-  const cf LB = expv(h0 * ub), LA = expv(h0 * ua), LBi = expv(-(h0 * ub)), LAi = expv(-(h0 * ua));
-  stq(tab, j, k, TQ_LB, LB);
-  stq(tab, j, k, TQ_LB1, LB * ub);
-  stq(tab, j, k, TQ_LA, LA);
-  stq(tab, j, k, TQ_LA1, LA * ua);
-  stq(tab, j, k, TQ_LBI, LBi);
-  stq(tab, j, k, TQ_LBI1, -(LBi * ub));
-  stq(tab, j, k, TQ_LAI, LAi);
-  stq(tab, j, k, TQ_LAI1, -(LAi * ua));
-  const DD3<cf> db = dd3<cf, true>(xj, h0 * ub);
-  const DD3<cf> da = dd3<cf, true>(xj, h0 * ua);
-  stq(tab, j, k, TQ_IB, 0.5f * db.d);
-  stq(tab, j, k, TQ_IA, 0.5f * da.d);
-  stq(tab, j, k, TQ_IB1, 0.5f * (db.dx * uj + db.dy * ub));
-  stq(tab, j, k, TQ_IA1, 0.5f * (da.dx * uj + da.dy * ua));
-  stq(tab, j, k, TQ_DXB, db.dx);
-  stq(tab, j, k, TQ_DYB, db.dy);
-  stq(tab, j, k, TQ_DXA, da.dx);
-  stq(tab, j, k, TQ_DYA, da.dy);
+  if (role == 0) {
+    if (l == 0) tab[0] = h0;
+    if (k == 0) {
+      const Node1<cf> nj = node1(xj);
+      const cf ri = expv(-xj);
+      stp(tab, j, TP_RHO, nj.e);
+      stp(tab, j, TP_RHO1, nj.e * uj);
+      stp(tab, j, TP_RHOI, ri);
+      stp(tab, j, TP_RHOI1, -(ri * uj));
+      stp(tab, j, TP_PHI, nj.p);
+      stp(tab, j, TP_PHI1, nj.dp * uj);
+      stp(tab, j, TP_DPHI, nj.dp);
+      stp(tab, j, TP_PHIH, 0.5f * nj.p);
+      stp(tab, j, TP_PHI1H, 0.5f * (nj.dp * uj));
+    }
+    const cf LB = expv(h0 * ub), LA = expv(h0 * ua), LBi = expv(-(h0 * ub)), LAi = expv(-(h0 * ua));
+    stq(tab, j, k, TQ_LB, LB);
+    stq(tab, j, k, TQ_LB1, LB * ub);
+    stq(tab, j, k, TQ_LA, LA);
+    stq(tab, j, k, TQ_LA1, LA * ua);
+    stq(tab, j, k, TQ_LBI, LBi);
+    stq(tab, j, k, TQ_LBI1, -(LBi * ub));
+    stq(tab, j, k, TQ_LAI, LAi);
+    stq(tab, j, k, TQ_LAI1, -(LAi * ua));
+  } else if (role == 1) {
+    const DD3<cf> db = dd3<cf, true>(xj, h0 * ub);
+    stq(tab, j, k, TQ_IB, 0.5f * db.d);
+    stq(tab, j, k, TQ_IB1, 0.5f * (db.dx * uj + db.dy * ub));
+    stq(tab, j, k, TQ_DXB, db.dx);
+    stq(tab, j, k, TQ_DYB, db.dy);
+  } else {
+    const DD3<cf> da = dd3<cf, true>(xj, h0 * ua);
+    stq(tab, j, k, TQ_IA, 0.5f * da.d);
+    stq(tab, j, k, TQ_IA1, 0.5f * (da.dx * uj + da.dy * ua));
+    stq(tab, j, k, TQ_DXA, da.dx);
+    stq(tab, j, k, TQ_DYA, da.dy);
+  }
 }
 // first-order flow from the table: c(h0) + c'(h0) dlt
 __device__ __forceinline__ cf tflow(cf c0, cf c1, float dlt) { return cf{fmaf(c1.re, dlt, c0.re), fmaf(c1.im, dlt, c0.im)}; }
@@ -1439,7 +1446,7 @@ int pairs_forward(const DiagArgs& a, hipStream_t st, bool out) {
   constexpr int GPW = pairs::Geo<4>::GPW;
   const dim3 grid((a.C + GPW - 1) / GPW, a.B), blk(64);
   if (!out) {
-    hipLaunchKernelGGL(pairs::k_coef_table, dim3(1), dim3(64), 0, st, a);
+    hipLaunchKernelGGL(pairs::k_coef_table, dim3(1), dim3(192), 0, st, a);
     if (hipGetLastError() != hipSuccess) return -1;
   }
   if (out) {
