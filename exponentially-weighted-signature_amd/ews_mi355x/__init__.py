@@ -12,6 +12,17 @@ from .layer import (  # noqa: F401
     log_signature_dim,
     lyndon_words,
 )
+from .front import (  # noqa: F401
+    B,
+    BlockFront,
+    Clock,
+    ClockSpec,
+    FixedClock,
+    GatedClock,
+    LearnableBlendedClock,
+    lift_path,
+    make_clock,
+)
 from .mixer import GradedRMSNorm, MixerEpilogue, graded_level_slices  # noqa: F401
 from .ops import diag_scan, mixer_epilogue  # noqa: F401
 from .params import (  # noqa: F401

@@ -52,7 +52,23 @@ EXPORTED = (
     "ews_mixer_residual_bytes",
     "ews_mixer_forward",
     "ews_mixer_backward",
+    "ews_clock_residual_bytes",
+    "ews_clock_workspace_bytes",
+    "ews_clock_num_params",
+    "ews_clock_forward",
+    "ews_clock_backward",
+    "ews_lift_residual_bytes",
+    "ews_lift_workspace_bytes",
+    "ews_lift_forward",
+    "ews_lift_backward",
 )
+
+CLOCK_MODES = {"time": 0, "blended_variation": 1, "blended_learn": 1, "blended_quad_variation": 2,
+               "token_gated": 3, "clamped_gate": 4}
+CLOCK_SCALINGS = {"none": 0, "[0,1]": 1, "[-1,1]": 2, "steps": 3}
+LIFT_NONE = 0
+LIFT_FULL = 1
+LIFT_PRESERVE = 2
 
 GRADED_VARIANTS = {"live_rms": 0, "static_gain": 1, "dilation": 2}
 
@@ -114,6 +130,42 @@ class MixerDesc(ctypes.Structure):
         ("prepend", ctypes.c_int32),
         ("prescale", ctypes.c_int32),
         ("eps", ctypes.c_float * 3),
+    ]
+
+
+class ClockDesc(ctypes.Structure):
+    _fields_ = [
+        ("batch", ctypes.c_int32),
+        ("length", ctypes.c_int32),
+        ("channels", ctypes.c_int32),
+        ("mode", ctypes.c_int32),
+        ("scaling", ctypes.c_int32),
+        ("normalize", ctypes.c_int32),
+        ("gates", ctypes.c_int32),
+        ("has_mask", ctypes.c_int32),
+        ("increment_driver", ctypes.c_int32),
+        ("has_time_denominator", ctypes.c_int32),
+        ("basepoint", ctypes.c_int32),
+        ("learned_alpha", ctypes.c_int32),
+        ("alpha", ctypes.c_float),
+        ("norm_constant", ctypes.c_float),
+        ("time_denominator", ctypes.c_float),
+        ("variation_eps", ctypes.c_float),
+        ("in_scale", ctypes.c_float),
+    ]
+
+
+class LiftDesc(ctypes.Structure):
+    _fields_ = [
+        ("batch", ctypes.c_int32),
+        ("length", ctypes.c_int32),
+        ("branch_dim", ctypes.c_int32),
+        ("append", ctypes.c_int32),
+        ("out_dim", ctypes.c_int32),
+        ("lift", ctypes.c_int32),
+        ("increment", ctypes.c_int32),
+        ("has_mask", ctypes.c_int32),
+        ("basepoint", ctypes.c_int32),
     ]
 
 
@@ -190,6 +242,26 @@ def load():
     lib.ews_mixer_forward.restype = i32
     lib.ews_mixer_backward.argtypes = [mdp, vp, vp, vp, vp, vp, vp, vp]
     lib.ews_mixer_backward.restype = i32
+    cdp = ctypes.POINTER(ClockDesc)
+    lib.ews_clock_residual_bytes.argtypes = [cdp]
+    lib.ews_clock_residual_bytes.restype = sz
+    lib.ews_clock_workspace_bytes.argtypes = [cdp]
+    lib.ews_clock_workspace_bytes.restype = sz
+    lib.ews_clock_num_params.argtypes = [cdp]
+    lib.ews_clock_num_params.restype = i32
+    lib.ews_clock_forward.argtypes = [cdp, vp, vp, vp, vp, vp, vp, vp]
+    lib.ews_clock_forward.restype = i32
+    lib.ews_clock_backward.argtypes = [cdp, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp]
+    lib.ews_clock_backward.restype = i32
+    ftp = ctypes.POINTER(LiftDesc)
+    lib.ews_lift_residual_bytes.argtypes = [ftp]
+    lib.ews_lift_residual_bytes.restype = sz
+    lib.ews_lift_workspace_bytes.argtypes = [ftp]
+    lib.ews_lift_workspace_bytes.restype = sz
+    lib.ews_lift_forward.argtypes = [ftp, vp, vp, vp, vp, vp, vp, vp]
+    lib.ews_lift_forward.restype = i32
+    lib.ews_lift_backward.argtypes = [ftp, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp]
+    lib.ews_lift_backward.restype = i32
     _lib = lib
     return lib
 

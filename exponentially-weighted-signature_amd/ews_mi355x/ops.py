@@ -387,3 +387,119 @@ def mixer_epilogue(rows, weight, bias, gains, d, N, variant="live_rms", eps=(1e-
     eps = tuple(eps) if isinstance(eps, (tuple, list)) else (float(eps),) * N
     return MixerFn.apply(rows, weight, bias, gains, int(d), int(N), variant, eps, bool(prepend), bool(prescale),
                          bool(level0))
+
+
+# ------------------------------------------------------------------------------------------------ block front
+def _dev_f32(name, t):
+    if not t.is_cuda or t.dtype != torch.float32:
+        raise TypeError(f"{name} must be a float32 tensor on the HIP device")
+    return t.contiguous()
+
+
+def _mask_bytes(mask, B, L, device):
+    if mask is None:
+        return None
+    m = mask.to(device=device)
+    if m.dim() == 1:
+        m = m.expand(B, L)
+    if tuple(m.shape) != (B, L):
+        raise ValueError("mask must be (seq_len,) or (batch, seq_len)")
+    return m.to(torch.uint8).contiguous()
+
+
+class ClockFn(torch.autograd.Function):
+    """theta (B, L + basepoint) of one clock over a batch (ews_clock_forward / ews_clock_backward; reference
+    ews/clocks.py:164-267 build_clock_jnp and :443-466 GatedClock.__call__). ``params`` is the flat parameter
+    vector of the clock: [alpha] (blended_learn, after its map to [0, 1]) or [w (K c), b (K)] (gated modes)."""
+
+    @staticmethod
+    def forward(ctx, driver, params, times, mask, desc):
+        lib = nat.load()
+        dev = times.device
+        B, L = desc.batch, desc.length
+        if driver is not None:
+            driver = _dev_f32("driver", driver)
+        params = _dev_f32("params", params) if params is not None and params.numel() else None
+        m = _mask_bytes(mask, B, L, dev)
+        theta = torch.empty((B, L + desc.basepoint), device=dev, dtype=torch.float32)
+        resid = torch.empty(max(1, int(lib.ews_clock_residual_bytes(ctypes.byref(desc)))), device=dev,
+                            dtype=torch.uint8)
+        nat.check(lib.ews_clock_forward(ctypes.byref(desc), times.data_ptr(),
+                                        driver.data_ptr() if driver is not None else None,
+                                        m.data_ptr() if m is not None else None,
+                                        params.data_ptr() if params is not None else None, theta.data_ptr(),
+                                        resid.data_ptr(), _stream_handle(dev)), "ews_clock_forward")
+        ctx.save_for_backward(driver, params, times, m, resid)
+        ctx.desc = desc
+        return theta
+
+    @staticmethod
+    def backward(ctx, gtheta):
+        lib = nat.load()
+        driver, params, times, m, resid = ctx.saved_tensors
+        desc = ctx.desc
+        if desc.mode == nat.CLOCK_MODES["time"]:
+            return None, None, None, None, None
+        dev = times.device
+        gtheta = gtheta.to(torch.float32).contiguous()
+        gdrv = torch.empty_like(driver) if ctx.needs_input_grad[0] else None
+        gprm = torch.empty_like(params) if params is not None else None
+        ws = torch.empty(max(1, int(lib.ews_clock_workspace_bytes(ctypes.byref(desc)))), device=dev,
+                         dtype=torch.uint8)
+        nat.check(lib.ews_clock_backward(ctypes.byref(desc), times.data_ptr(), driver.data_ptr(),
+                                         m.data_ptr() if m is not None else None,
+                                         params.data_ptr() if params is not None else None, resid.data_ptr(),
+                                         gtheta.data_ptr(), gdrv.data_ptr() if gdrv is not None else None,
+                                         gprm.data_ptr() if gprm is not None else None, ws.data_ptr(),
+                                         _stream_handle(dev)), "ews_clock_backward")
+        return gdrv, gprm, None, None, None
+
+
+class LiftFn(torch.autograd.Function):
+    """The path the block hands to its EWS layer: p (B, L + basepoint, w) from the branch (B, L, H) and the
+    appended clock channel (ews_lift_forward / ews_lift_backward; reference ews/block.py:284-301 with B.__call__,
+    ews/params.py:1181-1191, and the increment path of ews/paths.py:126-131)."""
+
+    @staticmethod
+    def forward(ctx, branch, theta_app, matrix, mask, desc):
+        lib = nat.load()
+        branch = _dev_f32("branch", branch)
+        dev = branch.device
+        if theta_app is not None:
+            theta_app = _dev_f32("theta_app", theta_app)
+        if matrix is not None:
+            matrix = _dev_f32("matrix", matrix)
+        m = _mask_bytes(mask, desc.batch, desc.length, dev)
+        path = torch.empty((desc.batch, desc.length + desc.basepoint, desc.out_dim), device=dev,
+                           dtype=torch.float32)
+        resid = torch.empty(max(1, int(lib.ews_lift_residual_bytes(ctypes.byref(desc)))), device=dev,
+                            dtype=torch.uint8)
+        nat.check(lib.ews_lift_forward(ctypes.byref(desc), branch.data_ptr(),
+                                       theta_app.data_ptr() if theta_app is not None else None,
+                                       m.data_ptr() if m is not None else None,
+                                       matrix.data_ptr() if matrix is not None else None, path.data_ptr(),
+                                       resid.data_ptr(), _stream_handle(dev)), "ews_lift_forward")
+        ctx.save_for_backward(branch, theta_app, matrix, m, resid)
+        ctx.desc = desc
+        return path
+
+    @staticmethod
+    def backward(ctx, gpath):
+        lib = nat.load()
+        branch, theta_app, matrix, m, resid = ctx.saved_tensors
+        desc = ctx.desc
+        dev = branch.device
+        gpath = gpath.to(torch.float32).contiguous()
+        gbr = torch.empty_like(branch)
+        gtha = torch.empty_like(theta_app) if theta_app is not None else None
+        gmat = torch.empty_like(matrix) if matrix is not None else None
+        ws = torch.empty(max(1, int(lib.ews_lift_workspace_bytes(ctypes.byref(desc)))), device=dev,
+                         dtype=torch.uint8)
+        nat.check(lib.ews_lift_backward(ctypes.byref(desc), branch.data_ptr(),
+                                        theta_app.data_ptr() if theta_app is not None else None,
+                                        m.data_ptr() if m is not None else None,
+                                        matrix.data_ptr() if matrix is not None else None, resid.data_ptr(),
+                                        gpath.data_ptr(), gbr.data_ptr(), gtha.data_ptr() if gtha is not None else None,
+                                        gmat.data_ptr() if gmat is not None else None, ws.data_ptr(),
+                                        _stream_handle(dev)), "ews_lift_backward")
+        return gbr, gtha, gmat, None, None

@@ -252,6 +252,91 @@ int ews_mixer_forward(const ews_mixer_desc* desc, const float* rows, const float
 int ews_mixer_backward(const ews_mixer_desc* desc, const float* rows, const float* weight, const void* residual,
                        const float* grad_out, float* grad_rows, float* row_dots, ews_stream_t stream);
 
+/* ---------------------------------------------------------------------------------------------------------
+ * Front of an EWS block: the clock theta (ews/clocks.py) and the lifted path p (ews/params.py:1165-1191,
+ * ews/block.py:284-301, ews/paths.py:126-131), computed from the block's raw inputs on the device.
+ * --------------------------------------------------------------------------------------------------------- */
+#define EWS_CLOCK_TIME 0           /* "time" */
+#define EWS_CLOCK_VARIATION 1      /* "blended_variation", "blended_learn" */
+#define EWS_CLOCK_QUAD_VARIATION 2 /* "blended_quad_variation" */
+#define EWS_CLOCK_TOKEN_GATED 3    /* "token_gated": relu(w . dx - b) */
+#define EWS_CLOCK_CLAMPED_GATE 4   /* "clamped_gate": sum_k clip(w_k . dx - b_k, 0, 1) */
+
+#define EWS_SCALING_NONE 0  /* "none" */
+#define EWS_SCALING_UNIT 1  /* "[0,1]" */
+#define EWS_SCALING_SYM 2   /* "[-1,1]" */
+#define EWS_SCALING_STEPS 3 /* "steps" (time mode only) */
+
+typedef struct ews_clock_desc {
+  int32_t batch;            /* B >= 1 */
+  int32_t length;           /* L >= 1 rows per sample */
+  int32_t channels;         /* c: driver channels, 1..64 (unused by EWS_CLOCK_TIME) */
+  int32_t mode;             /* EWS_CLOCK_* */
+  int32_t scaling;          /* EWS_SCALING_* */
+  int32_t normalize;        /* 0 "per_sample", 1 "constant" */
+  int32_t gates;            /* rows K of the gate weight: 1 (token_gated) or 1..8 (clamped_gate) */
+  int32_t has_mask;         /* 1: mask (B, L) of prefix-structured validity bytes */
+  int32_t increment_driver; /* 1: driver rows are increments; the clock's driver is their masked cumulative sum */
+  int32_t has_time_denominator;
+  int32_t basepoint;        /* 1: theta gets a leading copy of its first row (ews/block.py:298): (B, L + 1) */
+  int32_t learned_alpha;    /* 1: alpha is params[0] (blended_learn, after its clip or sigmoid) */
+  float alpha;              /* blended modes: the weight of the time component when learned_alpha == 0 */
+  float norm_constant;      /* "constant" normalisation (and the gated modes' divisor) */
+  float time_denominator;
+  float variation_eps;      /* sqrt(|dx|^2 + eps) of blended_variation */
+  float in_scale;           /* gated modes: the driver's fixed factor before the difference */
+} ews_clock_desc;
+
+/* Residual of the forward kept for the backward (per-chunk increment sums, row counts). */
+size_t ews_clock_residual_bytes(const ews_clock_desc* desc);
+/* Scratch of the backward. */
+size_t ews_clock_workspace_bytes(const ews_clock_desc* desc);
+/* Number of floats in params / grad_params: 1 (learned alpha), K c + K (gated: w row-major, then b), else 0. */
+int ews_clock_num_params(const ews_clock_desc* desc);
+
+/* times (L,) shared by the batch, driver (B, L, c), mask (B, L) -> theta (B, L + basepoint). Replaces
+ * Clock.__call__ (FixedClock / GatedClock / LearnableBlendedClock, ews/clocks.py:393-533) on every sample, i.e.
+ * build_clock_jnp (ews/clocks.py:164-267) and GatedClock.__call__ (:443-466). */
+int ews_clock_forward(const ews_clock_desc* desc, const float* times, const float* driver, const uint8_t* mask,
+                      const float* params, float* theta, void* residual, ews_stream_t stream);
+
+/* Backward: grad_theta (B, L + basepoint) -> grad_driver (B, L, c) (may be NULL) and grad_params (the layout of
+ * params; d theta / d alpha for a learned alpha). stop_gradient is the caller's: it skips this call. */
+int ews_clock_backward(const ews_clock_desc* desc, const float* times, const float* driver, const uint8_t* mask,
+                       const float* params, const void* residual, const float* grad_theta, float* grad_driver,
+                       float* grad_params, void* workspace, ews_stream_t stream);
+
+#define EWS_LIFT_NONE 0     /* no B: p = u */
+#define EWS_LIFT_FULL 1     /* p = u B^T, B (out_dim, in) */
+#define EWS_LIFT_PRESERVE 2 /* preserve_first_channel: p = [u_0, u_{1:} B^T], B (out_dim - 1, in - 1) */
+
+typedef struct ews_lift_desc {
+  int32_t batch;      /* B >= 1 */
+  int32_t length;     /* L >= 1 */
+  int32_t branch_dim; /* H: branch channels, 1..64 */
+  int32_t append;     /* 1: u = [theta_app | branch] (the appended clock channel) */
+  int32_t out_dim;    /* w: path channels, 1..64 (H + append without a lift) */
+  int32_t lift;       /* EWS_LIFT_* */
+  int32_t increment;  /* 1: path_mode "increment": the branch becomes its masked cumulative sum */
+  int32_t has_mask;   /* 1: forward fill of p past the last real row */
+  int32_t basepoint;  /* 1: a zero row in front: p (B, L + 1, w) */
+} ews_lift_desc;
+
+size_t ews_lift_residual_bytes(const ews_lift_desc* desc);
+size_t ews_lift_workspace_bytes(const ews_lift_desc* desc);
+
+/* branch (B, L, H), theta_app (B, L) (append only), mask (B, L), matrix (B's weight) -> path (B, L + basepoint, w).
+ * Replaces the path half of EWSBlock._mixer_levels (ews/block.py:284-301) with B.__call__ (ews/params.py:1181-1191)
+ * and, for path_mode "increment", to_increment_path_jnp (ews/paths.py:126-131) on the branch. */
+int ews_lift_forward(const ews_lift_desc* desc, const float* branch, const float* theta_app, const uint8_t* mask,
+                     const float* matrix, float* path, void* residual, ews_stream_t stream);
+
+/* Backward: grad_path -> grad_branch (B, L, H), grad_theta_app (B, L) (append only) and grad_matrix (the shape of
+ * matrix; lift != NONE). */
+int ews_lift_backward(const ews_lift_desc* desc, const float* branch, const float* theta_app, const uint8_t* mask,
+                      const float* matrix, const void* residual, const float* grad_path, float* grad_branch,
+                      float* grad_theta_app, float* grad_matrix, void* workspace, ews_stream_t stream);
+
 /* Human-readable text of a return code. */
 const char* ews_error_string(int code);
 

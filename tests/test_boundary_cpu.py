@@ -239,3 +239,94 @@ def test_mixer_module_mirrors_reference_fields_and_errors():
         E.MixerEpilogue(2, 2, 3, graded_prescale="poisson")
     with pytest.raises(TypeError, match="HIP device"):  # no CPU path for the fused epilogue
         m(torch.zeros(4, 13))
+
+
+def _cdesc(**kw):
+    base = dict(batch=2, length=300, channels=3, mode=1, scaling=1, normalize=0, gates=0, has_mask=0,
+                increment_driver=0, has_time_denominator=0, basepoint=0, learned_alpha=0, alpha=0.5,
+                norm_constant=1.0, time_denominator=1.0, variation_eps=1e-8, in_scale=1.0)
+    base.update(kw)
+    return nat.ClockDesc(**base)
+
+
+def test_clock_c_abi_error_codes():
+    lib = nat.load()
+    null = ctypes.c_void_p(0)
+    good = _cdesc()
+    # residual: 2 last-row ints, then 2 samples x 2 chunks of 256 rows of float64 sums (256-byte aligned)
+    assert lib.ews_clock_residual_bytes(ctypes.byref(good)) == 256 + 256
+    assert lib.ews_clock_num_params(ctypes.byref(good)) == 0
+    assert lib.ews_clock_num_params(ctypes.byref(_cdesc(mode=4, gates=3, scaling=0, normalize=1))) == 3 * 3 + 3
+    assert lib.ews_clock_num_params(ctypes.byref(_cdesc(learned_alpha=1))) == 1
+    assert lib.ews_clock_forward(ctypes.byref(good), null, null, null, null, null, null, null) == -1
+    bad = {"mode": (_cdesc(mode=5), -4), "scaling": (_cdesc(scaling=4), -4), "channels": (_cdesc(channels=65), -2),
+           "length": (_cdesc(length=0), -2), "steps blended": (_cdesc(scaling=3), -4),
+           "gate scaling": (_cdesc(mode=3, gates=1, scaling=1, normalize=1), -4),
+           "gate per-sample": (_cdesc(mode=3, gates=1, scaling=0, normalize=0), -4),
+           "token gates": (_cdesc(mode=3, gates=2, scaling=0, normalize=1), -2),
+           "clamped gates": (_cdesc(mode=4, gates=9, scaling=0, normalize=1), -2),
+           "learned time": (_cdesc(mode=0, learned_alpha=1), -4)}
+    for name, (dsc, code) in bad.items():
+        assert lib.ews_clock_forward(ctypes.byref(dsc), null, null, null, null, null, null, null) == code, name
+        assert lib.ews_clock_residual_bytes(ctypes.byref(dsc)) == 0, name
+        assert lib.ews_clock_num_params(ctypes.byref(dsc)) == -1, name
+
+
+def _ldesc(**kw):
+    base = dict(batch=2, length=300, branch_dim=6, append=0, out_dim=16, lift=1, increment=0, has_mask=0,
+                basepoint=0)
+    base.update(kw)
+    return nat.LiftDesc(**base)
+
+
+def test_lift_c_abi_error_codes():
+    lib = nat.load()
+    null = ctypes.c_void_p(0)
+    good = _ldesc(increment=1)
+    # residual: 2 last-row ints, then 2 samples x 3 chunks of 128 rows x 6 float64 channel sums
+    assert lib.ews_lift_residual_bytes(ctypes.byref(good)) == 256 + 512
+    assert lib.ews_lift_forward(ctypes.byref(good), null, null, null, null, null, null, null) == -1
+    bad = {"branch": (_ldesc(branch_dim=65), -2), "out": (_ldesc(out_dim=65), -2), "lift": (_ldesc(lift=3), -4),
+           "no lift width": (_ldesc(lift=0, out_dim=5), -2), "preserve": (_ldesc(lift=2, branch_dim=1), -2),
+           "length": (_ldesc(length=0), -2)}
+    for name, (dsc, code) in bad.items():
+        assert lib.ews_lift_forward(ctypes.byref(dsc), null, null, null, null, null, null, null) == code, name
+        assert lib.ews_lift_backward(ctypes.byref(dsc), null, null, null, null, null, null, null, null, null,
+                                     null, null) == code, name
+        assert lib.ews_lift_residual_bytes(ctypes.byref(dsc)) == 0, name
+
+
+def test_front_modules_mirror_reference_fields_and_errors():
+    """ClockSpec / make_clock / B checks and messages of ews/clocks.py:51-124, 528-537 and ews/params.py:1165-1191
+    (the cases of tests/test_clocks.py:99-124)."""
+    with pytest.raises(ValueError):
+        E.ClockSpec(mode="token_gated").validate()  # needs constant normalisation
+    with pytest.raises(ValueError):
+        E.ClockSpec(mode="nope").validate()
+    with pytest.raises(ValueError, match="needs a key"):
+        E.make_clock(E.ClockSpec(mode="token_gated", scaling="none", normalize="constant", norm_constant=1.0), 2)
+    with pytest.raises(ValueError, match="alpha = 0"):
+        E.make_clock(E.ClockSpec(mode="blended_variation", alpha=0.5, scaling="none", normalize="constant",
+                                 norm_constant=1.0), 2).per_token_increment(torch.ones(2, 2))
+    with pytest.raises(ValueError, match="unknown clock keys"):
+        E.ClockSpec.from_config({"mode": "time", "bogus": 1})
+    with pytest.raises(ValueError, match="'steps'"):
+        E.ClockSpec(mode="blended_variation", alpha=0.5, scaling="steps").validate()
+    clk = E.make_clock(E.ClockSpec(mode="clamped_gate", scaling="none", normalize="constant", norm_constant=2.0,
+                                   gate_init_bias=(-1.0, 0.0, 1.0)), dim=3, key=2)
+    assert isinstance(clk, E.GatedClock) and not clk.is_static
+    assert tuple(clk.w.shape) == (3, 3) and tuple(clk.b.tolist()) == (-1.0, 0.0, 1.0)
+    tok = E.make_clock(E.ClockSpec(mode="token_gated", scaling="none", normalize="constant", norm_constant=4.0,
+                                   gate_init_bias=-0.5), dim=5, key=1)
+    assert tuple(tok.w.shape) == (5,) and float(tok.b.detach()) == -0.5
+    lrn = E.make_clock(E.ClockSpec(mode="blended_learn", alpha=0.3, alpha_parametrisation="sigmoid"), dim=3)
+    assert isinstance(lrn, E.LearnableBlendedClock) and abs(float(lrn.alpha.detach()) - 0.3) < 1e-6
+    assert isinstance(E.make_clock(E.ClockSpec(), 3), E.FixedClock)
+    with pytest.raises(NotImplementedError):
+        lrn.per_token_increment(torch.ones(2, 3))
+    with pytest.raises(ValueError, match="at least 2 channels"):
+        E.B(torch.zeros(2, 0))(torch.zeros(4, 1))
+    with pytest.raises(TypeError, match="HIP device"):  # no CPU path for the front kernels
+        E.make_clock(E.ClockSpec(mode="blended_variation", alpha=0.5), 3)(torch.arange(6.0), torch.zeros(6, 3))
+    with pytest.raises(ValueError, match="path_mode"):
+        E.BlockFront(E.make_clock(E.ClockSpec(), 3), path_mode="delta")
