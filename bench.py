@@ -35,8 +35,9 @@ FWD_PASS_NAMES = ["chunk_summary", "carry_scan", "chunk_output", "readout_reduce
 BWD_PASS_NAMES = ["chunk_adjoint_local", "adjoint_scan", "chunk_adjoint_full", "knot_grads", "param_grads"]
 
 
-def make_inputs(B=32, L=17984, c=6, d=16, seed_cfg=2):
-    """Synthetic c2 inputs with np.random.default_rng([cfg, stream]) streams 0=increments, 1=lift, 2=A."""
+def make_inputs(B=32, L=17984, c=6, d=16, seed_cfg=2, raw=False):
+    """Synthetic c2 inputs with np.random.default_rng([cfg, stream]) streams 0=increments, 1=lift, 2=A. raw: also
+    the 6-channel path and the lift matrix it is lifted with."""
     rng0 = np.random.default_rng([seed_cfg, 0])
     inc = rng0.normal(0.0, np.sqrt(1.0 / L), size=(B, L - 1, c))
     path_c = np.concatenate([np.zeros((B, 1, c)), np.cumsum(inc, 1)], 1)
@@ -51,6 +52,8 @@ def make_inputs(B=32, L=17984, c=6, d=16, seed_cfg=2):
     # of A_ref is [[a_j, w_j], [-w_j, a_j]] with a_j the damping and w_j the frequency
     dw = np.stack([damp, freq], -1).astype(np.float32)
     clock = np.broadcast_to((np.arange(L, dtype=np.float64) / L).astype(np.float32), (B, L)).copy()
+    if raw:
+        return path, clock, dw, path_c.astype(np.float32), Wl.astype(np.float32)
     return path, clock, dw
 
 
@@ -537,6 +540,9 @@ def main():
     ap.add_argument("--mixer", action="store_true",
                     help="c4 / c5: the block's mixer epilogue (GradedRMSNorm + c_down, hidden = d) after the scan, "
                          "in place of c4's LogEWS readout")
+    ap.add_argument("--front", action="store_true",
+                    help="c2: start from the raw 6-channel path: the block front (time clock, lift B 6 -> 16) on the "
+                         "device before the scan and its backward (raw-path and B gradients) after it")
     ap.add_argument("--clock-grad", action="store_true",
                     help="also compute the clock gradient (the c2 clock is data; off by default)")
     ap.add_argument("--copy-probe", action="store_true",
@@ -579,7 +585,7 @@ def main():
     torch.cuda.set_device(dev)
     lib = nat.load()
     B, L, c, d, N = 32, 17984, 6, 16, 2
-    path_np, clock_np, dw_np = make_inputs(B, L, c, d)
+    path_np, clock_np, dw_np, pc_np, wl_np = make_inputs(B, L, c, d, raw=True)
     W = 1 + d + d * d
     rng = np.random.default_rng([2, 5])
     g_np = (rng.normal(size=(B, L - 1, W)) / np.sqrt(W)).astype(np.float32)
@@ -603,24 +609,59 @@ def main():
     dclock_ptr = dclock.data_ptr() if args.clock_grad else None
     ddw = torch.empty_like(dw)
     nf, nb = lib.ews_diag_num_passes(0), lib.ews_diag_num_passes(1)
+    nfr = 0
+    if args.front:
+        # the block front on the device: theta = the time base (mode "time", scaling "none", t = arange(L) / L: the
+        # same uniform clock) and path = path_c B^T (B the 16 x 6 lift); backward: the raw-path and B gradients
+        nfr = 1
+        cdesc = nat.ClockDesc(B, L, 0, nat.CLOCK_MODES["time"], nat.CLOCK_SCALINGS["none"], 0, 0, 0, 0, 0, 0, 0,
+                              1.0, 1.0, 1.0, 1e-8, 1.0)
+        ldesc = nat.LiftDesc(B, L, c, 0, d, nat.LIFT_FULL, 0, 0, 0)
+        times = torch.tensor((np.arange(L, dtype=np.float64) / L).astype(np.float32), device=dev)
+        pc = torch.tensor(pc_np, device=dev)
+        wl = torch.tensor(wl_np, device=dev)
+        cres = torch.empty(int(lib.ews_clock_residual_bytes(ctypes.byref(cdesc))), device=dev, dtype=torch.uint8)
+        lres = torch.empty(int(lib.ews_lift_residual_bytes(ctypes.byref(ldesc))), device=dev, dtype=torch.uint8)
+        lws = torch.empty(int(lib.ews_lift_workspace_bytes(ctypes.byref(ldesc))), device=dev, dtype=torch.uint8)
+        dpc = torch.empty_like(pc)
+        dwl = torch.empty_like(wl)
+
+    def front_fwd(stream):
+        nat.check(lib.ews_clock_forward(ctypes.byref(cdesc), times.data_ptr(), None, None, None, clock.data_ptr(),
+                                        cres.data_ptr(), stream), "clock forward")
+        nat.check(lib.ews_lift_forward(ctypes.byref(ldesc), pc.data_ptr(), None, None, wl.data_ptr(),
+                                       path.data_ptr(), lres.data_ptr(), stream), "lift forward")
+
+    def front_bwd(stream):
+        nat.check(lib.ews_lift_backward(ctypes.byref(ldesc), pc.data_ptr(), None, None, wl.data_ptr(),
+                                        lres.data_ptr(), dpath.data_ptr(), dpc.data_ptr(), None, dwl.data_ptr(),
+                                        lws.data_ptr(), stream), "lift backward")
 
     def step(events=None):
         stream = ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream)
+        if nfr:
+            if events is not None:
+                events[0].record()
+            front_fwd(stream)
         for p in range(nf):
             if events is not None:
-                events[p].record()
+                events[nfr + p].record()
             nat.check(lib.ews_diag_forward_pass(ctypes.byref(desc), p, path.data_ptr(), clock.data_ptr(),
                                                 dw.data_ptr(), out.data_ptr(), resid.data_ptr(), ws.data_ptr(),
                                                 stream), "forward pass")
         for p in range(nb):
             if events is not None:
-                events[nf + p].record()
+                events[nfr + nf + p].record()
             nat.check(lib.ews_diag_backward_pass(ctypes.byref(desc), p, path.data_ptr(), clock.data_ptr(),
                                                  dw.data_ptr(), resid.data_ptr(), gout.data_ptr(),
                                                  dpath.data_ptr(), dclock_ptr, ddw.data_ptr(),
                                                  ws.data_ptr(), stream), "backward pass")
+        if nfr:
+            if events is not None:
+                events[nfr + nf + nb].record()
+            front_bwd(stream)
         if events is not None:
-            events[nf + nb].record()
+            events[2 * nfr + nf + nb].record()
 
     for _ in range(args.warmup):
         step()
@@ -659,17 +700,45 @@ def main():
     ms_per_step = total_ms / args.steps
     per_step_events = []
     for _ in range(args.steps):
-        evs = [torch.cuda.Event(enable_timing=True) for _ in range(nf + nb + 1)]
+        evs = [torch.cuda.Event(enable_timing=True) for _ in range(2 * nfr + nf + nb + 1)]
         step(evs)
         per_step_events.append(evs)
     torch.cuda.synchronize()
-    names = FWD_PASS_NAMES[:nf] + BWD_PASS_NAMES[:nb]
+    names = (["front_forward"] if nfr else []) + FWD_PASS_NAMES[:nf] + BWD_PASS_NAMES[:nb] + \
+        (["front_backward"] if nfr else [])
     pass_ms = {nm: 0.0 for nm in names}
     for evs in per_step_events:
         for i, nm in enumerate(names):
             pass_ms[nm] += evs[i].elapsed_time(evs[i + 1])
     pass_ms = {k: v / args.steps for k, v in pass_ms.items()}
-    dominant = max(pass_ms, key=pass_ms.get)
+    front_extra = {}
+    if nfr:
+        # the same front as torch ops (matmul lift, autograd backward), for comparison
+        pcg = pc.clone().requires_grad_(True)
+        wlg = wl.clone().requires_grad_(True)
+
+        def torch_front():
+            th = times.expand(B, L).contiguous()
+            p = pcg @ wlg.t()
+            p.backward(dpath)
+            return th
+
+        for _ in range(3):
+            torch_front()
+        t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        t0.record()
+        for _ in range(args.steps):
+            torch_front()
+        t1.record()
+        torch.cuda.synchronize()
+        fb = 4 * B * L * (c + d + 1) + 4 * B * L * (d + 2 * c)  # reads and writes of the fused front fwd + bwd
+        fused = pass_ms["front_forward"] + pass_ms["front_backward"]
+        ref_path = torch.tensor(path_np, device=dev)
+        front_extra = {"front_fused_fwd_bwd_ms": round(fused, 4),
+                       "front_torch_ops_fwd_bwd_ms": round(t0.elapsed_time(t1) / args.steps, 4),
+                       "front_fused_gbs": round(fb / (fused * 1e-3) / 1e9, 1),
+                       "front_check_path_relerr": float((path - ref_path).abs().max() / ref_path.abs().max())}
+    dominant = max((k for k in pass_ms if not k.startswith("front")), key=pass_ms.get)
     ab = algorithmic_bytes(B, L, d, W)
     dom_bytes = ab.get(dominant)
     roof = None
@@ -698,7 +767,9 @@ def main():
         "data": "synthetic",
         "config": {"workload": "c2: single EWS layer, B=32, L=17984, d=16 (8 rotation planes), depth 2, fp32, "
                                "prefix readout, forward + custom-VJP backward (path and generator gradients"
-                               + (", clock gradient" if args.clock_grad else "") + ")", "global_batch": B, "seq_len": L,
+                               + (", clock gradient" if args.clock_grad else "")
+                               + ("; from the raw 6-channel path: device clock + lift, raw-path and B gradients"
+                                  if nfr else "") + ")", "global_batch": B, "seq_len": L,
                    "parallelism": "none (1 GPU)"},
         "hbm_gbs_effective": round(fwdbwd_bytes / (ms_per_step * 1e-3) / 1e9, 1),
         "hbm_frac_effective": round(fwdbwd_bytes / (ms_per_step * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
@@ -706,6 +777,7 @@ def main():
         "passes_ms": {k: round(v, 4) for k, v in pass_ms.items()},
         "wall_s": round(t_wall, 3),
     }
+    result.update(front_extra)
     if check_rows is not None:
         result["check_forward_relerr_vs_f64"] = check_rows
         result["check_path_grad_relerr_vs_f64"] = check_grad

@@ -34,7 +34,6 @@ namespace front {
 constexpr int CR = 256;  // clock rows per workgroup (a thread per row)
 constexpr int LR = 128;  // lift rows per workgroup
 constexpr int MAXK = 8;  // clamped_gate rows
-constexpr int UP = 65;   // LDS row stride of the lift tiles (odd: rows in different banks)
 
 // ------------------------------------------------------------------------------------------------ block helpers
 __device__ __forceinline__ double wave_sum(double v) {
@@ -427,19 +426,11 @@ __global__ __launch_bounds__(256) void k_clock_brows(CArgs a) {
   }
 }
 
-// grad_params = sum over (sample, chunk) partials, in a fixed order
-__global__ __launch_bounds__(256) void k_reduce_parts(const double* part, int nq, int P, float* out) {
-  const int p = blockIdx.x * 256 + threadIdx.x;
-  if (p >= P) return;
-  double acc = 0.0;
-  for (int q = 0; q < nq; ++q) acc += part[(size_t)q * P + p];
-  out[p] = (float)acc;
-}
-
 // =================================================================================================== lift
 struct LArgs {
   int B, L, H, app, Hin, w, lift, incr, has_mask, bp, nch, Hs;
-  int wl, hl;  // the matrix: (wl, hl)
+  int wl, hl;        // the matrix: (wl, hl)
+  int SU, SP, SM;    // LDS row strides (odd) of the u, dp and matrix tiles
   const float* br;
   const float* tha;
   const uint8_t* m;
@@ -452,6 +443,7 @@ struct LArgs {
   float* gtha;
   double* dsum;  // (B, nch, 2, Hin): sums of du over all rows / over rows past n
   float* part;   // (B nch, wl hl)
+  double* part2; // (S, wl hl) first-level sums of part
   float* gM;
 };
 
@@ -460,6 +452,32 @@ __device__ __forceinline__ bool lvalid(const LArgs& a, int b, int r) {
 }
 __device__ __forceinline__ int lastrow(const LArgs& a, int b) { return a.has_mask ? a.nrow[b] : a.L - 1; }
 __device__ __forceinline__ int fill_idx(int r, int n, int L) { return n >= 0 ? min(r, n) : L - 1; }
+
+// LDS carve-up (in floats; the float64 region starts at an even float offset), sized by the actual widths
+struct LLds {
+  int DP, DU, U, Ms, seg, dbl, nfloat;
+};
+__host__ __device__ inline LLds lift_lds(const LArgs& a, bool dp, bool du, bool u, bool seg) {
+  LLds l{};
+  int o = 0;
+  l.DP = o;
+  o += dp ? LR * a.SP : 0;
+  l.DU = o;
+  o += du ? LR * a.SU : 0;
+  l.U = o;
+  o += u ? LR * a.SU : 0;
+  l.Ms = o;
+  o += a.wl * a.SM;
+  l.seg = o;
+  o += seg ? 256 : 0;
+  o = (o + 1) & ~1;
+  l.dbl = o;
+  l.nfloat = o;
+  return l;
+}
+constexpr int kFwdDoubles = 64 + 256;        // carry, reduction scratch
+constexpr int kBsumDoubles = 512;            // two reductions
+constexpr int kBrowDoubles = 64 + 160 + 256; // carry, 2 x 80 sums, reduction scratch
 
 __global__ __launch_bounds__(256) void k_lift_sums(LArgs a) {
   __shared__ double red[256];
@@ -479,8 +497,9 @@ __global__ __launch_bounds__(256) void k_lift_sums(LArgs a) {
   }
 }
 
-// U tile: u rows of the chunk (forward-filled for the value path; the cumulative sum for the increment path)
-__device__ void load_u(const LArgs& a, int b, int ch, float* U, double* carry, float* segtot) {
+// U tile: u rows of the chunk (forward-filled for the value path; the cumulative sum for the increment path).
+// carry: 64 doubles, red: 256 doubles, segtot: 256 floats.
+__device__ void load_u(const LArgs& a, int b, int ch, float* U, double* carry, double* red, float* segtot) {
   const int r0 = ch * LR, n = lastrow(a, b);
   for (int e = threadIdx.x; e < LR * a.Hin; e += 256) {
     const int r = e / a.Hin, i = e - r * a.Hin, row = r0 + r;
@@ -495,7 +514,7 @@ __device__ void load_u(const LArgs& a, int b, int ch, float* U, double* carry, f
         else v = a.br[((size_t)b * a.L + src) * a.H + j];
       }
     }
-    U[r * UP + i] = v;
+    U[r * a.SU + i] = v;
   }
   if (!a.incr) {
     __syncthreads();
@@ -504,7 +523,6 @@ __device__ void load_u(const LArgs& a, int b, int ch, float* U, double* carry, f
   // float64 carry of each channel: the chunk sums before this chunk
   {
     const int j = threadIdx.x % a.Hs, part = threadIdx.x / a.Hs, np = 256 / a.Hs;
-    __shared__ double red[256];
     double c = 0.0;
     if (j < a.H)
       for (int q = part; q < ch; q += np) c += a.csum[((size_t)b * a.nch + q) * a.H + j];
@@ -517,63 +535,66 @@ __device__ void load_u(const LArgs& a, int b, int ch, float* U, double* carry, f
     }
   }
   __syncthreads();
-  // segmented inclusive scan down each channel's column
+  // segmented inclusive scan down each channel's column (nseg * Hs <= 256 segments)
   const int nseg = min(256 / a.Hs, 32), rps = LR / nseg;
   const int j = threadIdx.x % a.Hs, sg = threadIdx.x / a.Hs;
   const bool act = sg < nseg && j < a.H;
   float* col = U + a.app + j;
   if (act) {
     float t = 0.0f;
-    for (int r = sg * rps; r < (sg + 1) * rps; ++r) t += col[r * UP];
-    segtot[sg * 64 + j] = t;
+    for (int r = sg * rps; r < (sg + 1) * rps; ++r) t += col[r * a.SU];
+    segtot[sg * a.Hs + j] = t;
   }
   __syncthreads();
   if (act) {
     double off = carry[j];
-    for (int q = 0; q < sg; ++q) off += segtot[q * 64 + j];
+    for (int q = 0; q < sg; ++q) off += segtot[q * a.Hs + j];
     for (int r = sg * rps; r < (sg + 1) * rps; ++r) {
-      off += col[r * UP];
-      col[r * UP] = (float)off;
+      off += col[r * a.SU];
+      col[r * a.SU] = (float)off;
     }
   }
   __syncthreads();
 }
 
-// the matrix into LDS: Ms[o * UP + i] = M[o][i] (o < wl, i < hl)
+// the matrix into LDS: Ms[o * SM + i] = M[o][i] (o < wl, i < hl)
 __device__ void load_matrix(const LArgs& a, float* Ms) {
   if (a.lift == EWS_LIFT_NONE) return;
   for (int e = threadIdx.x; e < a.wl * a.hl; e += 256) {
     const int o = e / a.hl, i = e - o * a.hl;
-    Ms[o * UP + i] = a.M[e];
+    Ms[o * a.SM + i] = a.M[e];
   }
 }
 
 __global__ __launch_bounds__(256) void k_lift_rows(LArgs a) {
-  __shared__ float U[LR * UP];
-  __shared__ float Ms[64 * UP];
-  __shared__ float segtot[32 * 64];
-  __shared__ double carry[64];
+  extern __shared__ float lds[];
+  const LLds l = lift_lds(a, false, false, true, true);
+  float* U = lds + l.U;
+  float* Ms = lds + l.Ms;
+  float* segtot = lds + l.seg;
+  double* carry = reinterpret_cast<double*>(lds + l.dbl);
+  double* red = carry + 64;
   const int ch = blockIdx.x, b = blockIdx.y, r0 = ch * LR;
   load_matrix(a, Ms);
-  load_u(a, b, ch, U, carry, segtot);
+  load_u(a, b, ch, U, carry, red, segtot);
   float* pb = a.p + (size_t)b * (a.L + a.bp) * a.w;
   if (a.bp && ch == 0)
     for (int o = threadIdx.x; o < a.w; o += 256) pb[o] = 0.0f;
   for (int e = threadIdx.x; e < LR * a.w; e += 256) {
     const int r = e / a.w, o = e - r * a.w, row = r0 + r;
     if (row >= a.L) break;
-    const float* u = U + r * UP;
+    const float* u = U + r * a.SU;
     float v;
     if (a.lift == EWS_LIFT_NONE) {
       v = u[o];
     } else if (a.lift == EWS_LIFT_FULL) {
       v = 0.0f;
-      for (int i = 0; i < a.hl; ++i) v = fmaf(Ms[o * UP + i], u[i], v);
+      for (int i = 0; i < a.hl; ++i) v = fmaf(Ms[o * a.SM + i], u[i], v);
     } else if (o == 0) {
       v = u[0];
     } else {
       v = 0.0f;
-      for (int i = 0; i < a.hl; ++i) v = fmaf(Ms[(o - 1) * UP + i], u[i + 1], v);
+      for (int i = 0; i < a.hl; ++i) v = fmaf(Ms[(o - 1) * a.SM + i], u[i + 1], v);
     }
     pb[(size_t)(row + a.bp) * a.w + o] = v;
   }
@@ -585,49 +606,54 @@ __device__ void load_du(const LArgs& a, int b, int ch, float* DP, const float* M
   const float* gp = a.gp + (size_t)b * (a.L + a.bp) * a.w;
   for (int e = threadIdx.x; e < LR * a.w; e += 256) {
     const int r = e / a.w, o = e - r * a.w, row = r0 + r;
-    DP[r * UP + o] = row < a.L ? gp[(size_t)(row + a.bp) * a.w + o] : 0.0f;
+    DP[r * a.SP + o] = row < a.L ? gp[(size_t)(row + a.bp) * a.w + o] : 0.0f;
   }
   __syncthreads();
   for (int e = threadIdx.x; e < LR * a.Hin; e += 256) {
     const int r = e / a.Hin, i = e - r * a.Hin;
-    const float* dp = DP + r * UP;
+    const float* dp = DP + r * a.SP;
     float v;
     if (a.lift == EWS_LIFT_NONE) {
       v = dp[i];
     } else if (a.lift == EWS_LIFT_FULL) {
       v = 0.0f;
-      for (int o = 0; o < a.wl; ++o) v = fmaf(Ms[o * UP + i], dp[o], v);
+      for (int o = 0; o < a.wl; ++o) v = fmaf(Ms[o * a.SM + i], dp[o], v);
     } else if (i == 0) {
       v = dp[0];
     } else {
       v = 0.0f;
-      for (int o = 0; o < a.wl; ++o) v = fmaf(Ms[o * UP + i - 1], dp[o + 1], v);
+      for (int o = 0; o < a.wl; ++o) v = fmaf(Ms[o * a.SM + i - 1], dp[o + 1], v);
     }
-    DU[r * UP + i] = v;
+    DU[r * a.SU + i] = v;
   }
   __syncthreads();
 }
 
-// per chunk: sums of du over every row and over the rows past the last real row
+__device__ __forceinline__ int pow2_at_least8(int x) {
+  return x > 64 ? 128 : (x > 32 ? 64 : (x > 16 ? 32 : (x > 8 ? 16 : 8)));
+}
+
+// per chunk: sums of du over every row and over the rows past the last real row (increment path or mask only)
 __global__ __launch_bounds__(256) void k_lift_bsums(LArgs a) {
   extern __shared__ float lds[];
-  float* DP = lds;
-  float* DU = DP + LR * UP;
-  float* Ms = DU + LR * UP;
-  double* red = reinterpret_cast<double*>(Ms + 64 * UP);
+  const LLds l = lift_lds(a, true, true, false, false);
+  float* DP = lds + l.DP;
+  float* DU = lds + l.DU;
+  float* Ms = lds + l.Ms;
+  double* red = reinterpret_cast<double*>(lds + l.dbl);
   const int ch = blockIdx.x, b = blockIdx.y, r0 = ch * LR;
   load_matrix(a, Ms);
   __syncthreads();
   load_du(a, b, ch, DP, Ms, DU);
   const int n = lastrow(a, b);
-  const int Hs2 = a.Hin > 64 ? 128 : (a.Hin > 32 ? 64 : (a.Hin > 16 ? 32 : (a.Hin > 8 ? 16 : 8)));
+  const int Hs2 = pow2_at_least8(a.Hin);
   const int i = threadIdx.x % Hs2, part = threadIdx.x / Hs2, np = 256 / Hs2;
   double all = 0.0, tail = 0.0;
   if (i < a.Hin)
     for (int r = part; r < LR; r += np) {
       const int row = r0 + r;
       if (row >= a.L) break;
-      const double v = DU[r * UP + i];
+      const double v = DU[r * a.SU + i];
       all += v;
       if (row > n) tail += v;
     }
@@ -646,26 +672,26 @@ __global__ __launch_bounds__(256) void k_lift_bsums(LArgs a) {
   }
 }
 
-size_t lift_brows_lds() { return (size_t)(3 * LR * UP + 64 * UP + 32 * 64) * 4 + (64 + 2 * 128 + 256) * 8; }
-
 __global__ __launch_bounds__(256) void k_lift_brows(LArgs a) {
   extern __shared__ float lds[];
-  float* DP = lds;
-  float* DU = DP + LR * UP;
-  float* U = DU + LR * UP;
-  float* Ms = U + LR * UP;
-  float* segtot = Ms + 64 * UP;
-  double* carry = reinterpret_cast<double*>(segtot + 32 * 64);  // 64
-  double* acc = carry + 64;                                      // 2 x 128: reverse carry, tail
-  double* red = acc + 256;                                       // 256
+  const LLds l = lift_lds(a, true, true, true, true);
+  float* DP = lds + l.DP;
+  float* DU = lds + l.DU;
+  float* U = lds + l.U;
+  float* Ms = lds + l.Ms;
+  float* segtot = lds + l.seg;
+  double* carry = reinterpret_cast<double*>(lds + l.dbl);  // 64
+  double* acc = carry + 64;                                 // 2 x 80: sums after this chunk, sums past n
+  double* red = acc + 160;                                  // 256
   const int ch = blockIdx.x, b = blockIdx.y, r0 = ch * LR;
   load_matrix(a, Ms);
   __syncthreads();
   load_du(a, b, ch, DP, Ms, DU);
   const int n = lastrow(a, b);
+  const bool need_sums = a.incr || a.has_mask;
   // float64 sums over the other chunks: du after this chunk (increment path), du past n (the fill)
-  {
-    const int Hs2 = a.Hin > 64 ? 128 : (a.Hin > 32 ? 64 : (a.Hin > 16 ? 32 : (a.Hin > 8 ? 16 : 8)));
+  if (need_sums) {
+    const int Hs2 = pow2_at_least8(a.Hin);
     const int i = threadIdx.x % Hs2, part = threadIdx.x / Hs2, np = 256 / Hs2;
     for (int which = 0; which < 2; ++which) {
       double s = 0.0;
@@ -680,21 +706,21 @@ __global__ __launch_bounds__(256) void k_lift_brows(LArgs a) {
       if (part == 0 && i < a.Hin) {
         double t = 0.0;
         for (int q = 0; q < np; ++q) t += red[q * Hs2 + i];
-        acc[which * 128 + i] = t;
+        acc[which * 80 + i] = t;
       }
       __syncthreads();
     }
   }
   // B gradient partial: sum over the chunk's rows of dp (x) u (u forward-filled, as the forward read it)
   if (a.lift != EWS_LIFT_NONE) {
-    load_u(a, b, ch, U, carry, segtot);
+    load_u(a, b, ch, U, carry, red, segtot);
     const int nr = min(LR, a.L - r0);
     const int oo = a.lift == EWS_LIFT_PRESERVE ? 1 : 0;
     float* pp = a.part + ((size_t)b * a.nch + ch) * a.wl * a.hl;
     for (int e = threadIdx.x; e < a.wl * a.hl; e += 256) {
       const int o = e / a.hl, i = e - o * a.hl;
       float v = 0.0f;
-      for (int r = 0; r < nr; ++r) v = fmaf(DP[r * UP + o + oo], U[r * UP + i + oo], v);
+      for (int r = 0; r < nr; ++r) v = fmaf(DP[r * a.SP + o + oo], U[r * a.SU + i + oo], v);
       pp[e] = v;
     }
   }
@@ -704,8 +730,8 @@ __global__ __launch_bounds__(256) void k_lift_brows(LArgs a) {
     for (int r = threadIdx.x; r < LR; r += 256) {
       const int row = r0 + r;
       if (row >= a.L) break;
-      float v = row <= n ? DU[r * UP] : 0.0f;
-      if (row == tr && a.has_mask) v += (float)acc[128];
+      float v = row <= n ? DU[r * a.SU] : 0.0f;
+      if (row == tr && a.has_mask) v += (float)acc[80];
       a.gtha[(size_t)b * a.L + row] = v;
     }
   }
@@ -713,8 +739,8 @@ __global__ __launch_bounds__(256) void k_lift_brows(LArgs a) {
     for (int e = threadIdx.x; e < LR * a.H; e += 256) {
       const int r = e / a.H, j = e - r * a.H, row = r0 + r;
       if (row >= a.L) break;
-      float v = row <= n ? DU[r * UP + a.app + j] : 0.0f;
-      if (row == tr && a.has_mask) v += (float)acc[128 + a.app + j];
+      float v = row <= n ? DU[r * a.SU + a.app + j] : 0.0f;
+      if (row == tr && a.has_mask) v += (float)acc[80 + a.app + j];
       a.gbr[((size_t)b * a.L + row) * a.H + j] = v;
     }
     return;
@@ -727,27 +753,51 @@ __global__ __launch_bounds__(256) void k_lift_brows(LArgs a) {
   float* col = DU + a.app + j;
   if (act) {
     float t = 0.0f;
-    for (int r = sg * rps; r < (sg + 1) * rps; ++r) t += r0 + r < a.L ? col[r * UP] : 0.0f;
-    segtot[sg * 64 + j] = t;
+    for (int r = sg * rps; r < (sg + 1) * rps; ++r) t += r0 + r < a.L ? col[r * a.SU] : 0.0f;
+    segtot[sg * a.Hs + j] = t;
   }
   __syncthreads();
   if (act) {
     double off = acc[a.app + j];
-    for (int q = sg + 1; q < nseg; ++q) off += segtot[q * 64 + j];
+    for (int q = sg + 1; q < nseg; ++q) off += segtot[q * a.Hs + j];
     for (int r = (sg + 1) * rps - 1; r >= sg * rps; --r) {
       const int row = r0 + r;
       if (row >= a.L) continue;
-      off += col[r * UP];
+      off += col[r * a.SU];
       a.gbr[((size_t)b * a.L + row) * a.H + j] = lvalid(a, b, row) ? (float)off : 0.0f;
     }
   }
 }
 
-__global__ __launch_bounds__(256) void k_reduce_lift(const float* part, int nq, int P, float* out) {
+// Deterministic two-level sum of per-chunk partials part (nq, P) -> out (P): workgroup (column block of 64,
+// segment of QB partials) sums its segment with 4 wavefronts (fixed order), then one thread per column sums the
+// segments.
+constexpr int QB = 256;
+template <class T>
+__global__ __launch_bounds__(256) void k_reduce_stage1(const T* part, int nq, int P, double* out2) {
+  __shared__ double red[4][64];
+  const int l = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int p = blockIdx.x * 64 + l, sg = blockIdx.y;
+  const int q0 = sg * QB, q1 = min(nq, q0 + QB);
+  double s0 = 0.0, s1 = 0.0;
+  if (p < P) {
+    int q = q0 + w;
+    for (; q + 4 < q1; q += 8) {
+      s0 += (double)part[(size_t)q * P + p];
+      s1 += (double)part[(size_t)(q + 4) * P + p];
+    }
+    if (q < q1) s0 += (double)part[(size_t)q * P + p];
+  }
+  red[w][l] = s0 + s1;
+  __syncthreads();
+  if (w == 0 && p < P) out2[(size_t)sg * P + p] = (red[0][l] + red[1][l]) + (red[2][l] + red[3][l]);
+}
+
+__global__ __launch_bounds__(256) void k_reduce_stage2(const double* out2, int S, int P, float* out) {
   const int p = blockIdx.x * 256 + threadIdx.x;
   if (p >= P) return;
   double acc = 0.0;
-  for (int q = 0; q < nq; ++q) acc += part[(size_t)q * P + p];
+  for (int s = 0; s < S; ++s) acc += out2[(size_t)s * P + p];
   out[p] = (float)acc;
 }
 
@@ -760,6 +810,11 @@ namespace {
 using namespace ews::front;
 
 size_t al256f(size_t x) { return (x + 255) & ~(size_t)255; }
+
+// segments of the first-level partial sums
+size_t nseg(size_t nq) { return (nq + QB - 1) / QB; }
+
+size_t lds_bytes(const LLds& l, int ndouble) { return (size_t)l.nfloat * 4 + (size_t)ndouble * 8; }
 
 int clock_check(const ews_clock_desc* s) {
   if (!s) return EWS_ERR_NULL;
@@ -858,6 +913,9 @@ LArgs lift_args(const ews_lift_desc* s) {
   a.Hs = a.H > 32 ? 64 : (a.H > 16 ? 32 : (a.H > 8 ? 16 : (a.H > 4 ? 8 : (a.H > 2 ? 4 : (a.H > 1 ? 2 : 1)))));
   a.wl = a.lift == EWS_LIFT_FULL ? a.w : (a.lift == EWS_LIFT_PRESERVE ? a.w - 1 : 0);
   a.hl = a.lift == EWS_LIFT_FULL ? a.Hin : (a.lift == EWS_LIFT_PRESERVE ? a.Hin - 1 : 0);
+  a.SU = a.Hin | 1;
+  a.SP = a.w | 1;
+  a.SM = a.hl | 1;
   return a;
 }
 
@@ -881,7 +939,8 @@ size_t ews_clock_workspace_bytes(const ews_clock_desc* s) {
   if (clock_check(s) != EWS_OK) return 0;
   const CArgs a = clock_args(s);
   const size_t q = (size_t)a.B * a.nch;
-  return 2 * al256f(q * 8) + al256f(q * (size_t)(a.P > 0 ? a.P : 1) * 8);
+  const size_t P = a.P > 0 ? a.P : 1;
+  return 2 * al256f(q * 8) + al256f(q * P * 8) + al256f(nseg(q) * P * 8);
 }
 
 int ews_clock_num_params(const ews_clock_desc* s) {
@@ -935,13 +994,19 @@ int ews_clock_backward(const ews_clock_desc* s, const float* times, const float*
   a.dsum = reinterpret_cast<double*>(w);
   a.psum = reinterpret_cast<double*>(w + al256f(q * 8));
   a.part = reinterpret_cast<double*>(w + 2 * al256f(q * 8));
+  const size_t P = a.P > 0 ? a.P : 1;
+  double* part2 = reinterpret_cast<double*>(w + 2 * al256f(q * 8) + al256f(q * P * 8));
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   const dim3 grid(a.nch, a.B);
   const int cb = clock_cb(a.c);
   EWS_CB_LAUNCH(k_clock_bsums, cb, grid, st, a);
   EWS_CB_LAUNCH(k_clock_brows, cb, grid, st, a);
-  if (a.P > 0)
-    hipLaunchKernelGGL(k_reduce_parts, dim3((a.P + 255) / 256), dim3(256), 0, st, a.part, (int)q, a.P, a.gprm);
+  if (a.P > 0) {
+    const int S = (int)nseg(q);
+    hipLaunchKernelGGL(k_reduce_stage1<double>, dim3((a.P + 63) / 64, S), dim3(256), 0, st, a.part, (int)q, a.P,
+                       part2);
+    hipLaunchKernelGGL(k_reduce_stage2, dim3((a.P + 255) / 256), dim3(256), 0, st, part2, S, a.P, a.gprm);
+  }
   return launched();
 }
 
@@ -955,7 +1020,8 @@ size_t ews_lift_workspace_bytes(const ews_lift_desc* s) {
   if (lift_check(s) != EWS_OK) return 0;
   const LArgs a = lift_args(s);
   const size_t q = (size_t)a.B * a.nch;
-  return al256f(q * 2 * a.Hin * 8) + al256f(q * (size_t)(a.wl * a.hl > 0 ? a.wl * a.hl : 1) * 4);
+  const size_t P = a.wl * a.hl > 0 ? a.wl * a.hl : 1;
+  return al256f(q * 2 * a.Hin * 8) + al256f(q * P * 4) + al256f(nseg(q) * P * 8);
 }
 
 int ews_lift_forward(const ews_lift_desc* s, const float* branch, const float* theta_app, const uint8_t* mask,
@@ -976,7 +1042,10 @@ int ews_lift_forward(const ews_lift_desc* s, const float* branch, const float* t
   const dim3 grid(a.nch, a.B);
   if (a.has_mask) hipLaunchKernelGGL(k_last_row, dim3(a.B), dim3(256), 0, st, mask, a.L, a.nrow);
   if (a.incr) hipLaunchKernelGGL(k_lift_sums, grid, dim3(256), 0, st, a);
-  hipLaunchKernelGGL(k_lift_rows, grid, dim3(256), 0, st, a);
+  const size_t lf = lds_bytes(lift_lds(a, false, false, true, true), kFwdDoubles);
+  (void)hipFuncSetAttribute(reinterpret_cast<const void*>(k_lift_rows), hipFuncAttributeMaxDynamicSharedMemorySize,
+                            (int)lf);
+  hipLaunchKernelGGL(k_lift_rows, grid, dim3(256), lf, st, a);
   return launched();
 }
 
@@ -1001,20 +1070,26 @@ int ews_lift_backward(const ews_lift_desc* s, const float* branch, const float* 
   char* w = static_cast<char*>(workspace);
   const size_t q = (size_t)a.B * a.nch;
   a.dsum = reinterpret_cast<double*>(w);
+  const size_t P = a.wl * a.hl > 0 ? a.wl * a.hl : 1;
   a.part = reinterpret_cast<float*>(w + al256f(q * 2 * a.Hin * 8));
+  a.part2 = reinterpret_cast<double*>(w + al256f(q * 2 * a.Hin * 8) + al256f(q * P * 4));
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   const dim3 grid(a.nch, a.B);
-  const size_t lb = (size_t)(2 * LR * UP + 64 * UP) * 4 + 512 * 8;
-  const size_t lr = lift_brows_lds();
+  const size_t lb = lds_bytes(lift_lds(a, true, true, false, false), kBsumDoubles);
+  const size_t lr = lds_bytes(lift_lds(a, true, true, true, true), kBrowDoubles);
   (void)hipFuncSetAttribute(reinterpret_cast<const void*>(k_lift_bsums), hipFuncAttributeMaxDynamicSharedMemorySize,
-                      (int)lb);
+                            (int)lb);
   (void)hipFuncSetAttribute(reinterpret_cast<const void*>(k_lift_brows), hipFuncAttributeMaxDynamicSharedMemorySize,
-                      (int)lr);
-  hipLaunchKernelGGL(k_lift_bsums, grid, dim3(256), lb, st, a);
+                            (int)lr);
+  // the per-chunk sums serve the increment path's reverse carry and the fill's tail only
+  if (a.incr || a.has_mask) hipLaunchKernelGGL(k_lift_bsums, grid, dim3(256), lb, st, a);
   hipLaunchKernelGGL(k_lift_brows, grid, dim3(256), lr, st, a);
-  if (a.lift != EWS_LIFT_NONE)
-    hipLaunchKernelGGL(k_reduce_lift, dim3((a.wl * a.hl + 255) / 256), dim3(256), 0, st, a.part, (int)q,
-                       a.wl * a.hl, a.gM);
+  if (a.lift != EWS_LIFT_NONE) {
+    const int S = (int)nseg(q), Pm = a.wl * a.hl;
+    hipLaunchKernelGGL(k_reduce_stage1<float>, dim3((Pm + 63) / 64, S), dim3(256), 0, st, a.part, (int)q, Pm,
+                       a.part2);
+    hipLaunchKernelGGL(k_reduce_stage2, dim3((Pm + 255) / 256), dim3(256), 0, st, a.part2, S, Pm, a.gM);
+  }
   return launched();
 }
 
