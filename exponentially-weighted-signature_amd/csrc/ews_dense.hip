@@ -2234,6 +2234,69 @@ __global__ void k_unpad_outputs(Args a, float* levels, float* flows) {
   }
 }
 
+// Token cache (ews/core/token_scan.py:91-118): step (b, t) reads the cache row of its token, the packed levels
+// P_cache[g] (ews/core/chen_scan.py:33-46) and the flow D_cache[g]; a padded step is the unit signature (zero levels)
+// with the identity flow. Token ids are clamped to [0, V) (the clamping of an out-of-range JAX gather).
+__global__ void k_pad_tokens(Args a, const int* tok, const uint8_t* mask, const float* pc, const float* dc, int V,
+                             int D) {
+  const long it = blockIdx.x;
+  const bool on = mask == nullptr || mask[it] != 0;
+  const int g = min(max(tok[it], 0), V - 1);
+  const float* lv = pc + (size_t)g * D;
+  float* lo = a.loc + it * a.LW;
+  for (int e = threadIdx.x; e < a.LW; e += blockDim.x) {
+    const long oi = out_index(a.N, a.d, e);
+    lo[e] = (on && oi >= 0) ? lv[oi] : 0.0f;
+  }
+  const float* fi = dc + (size_t)g * a.d * a.d;
+  float* fo = a.fl + it * 256;
+  for (int e = threadIdx.x; e < 256; e += blockDim.x) {
+    const int i = e >> 4, j = e & 15;
+    fo[e] = (on && i < a.d && j < a.d) ? fi[i * a.d + j] : (i == j ? 1.0f : 0.0f);
+  }
+}
+
+// Cache gradients: the per-step cotangents (ds_t in loc, dM_t in fl, padded) summed by token. Stage 1: a
+// workgroup per (256 columns, chunk of kTokChunk steps, group of 16 tokens), each thread owning one column of the
+// 16 accumulators; stage 2: a thread per (token, column) sums the chunks in order and unpads. Deterministic.
+constexpr int kTokChunk = 1024;
+__global__ __launch_bounds__(256) void k_token_grads1(Args a, const int* tok, const uint8_t* mask, int V,
+                                                      float* part) {
+  __shared__ float acc[16][256];
+  const int E = a.LW + 256;
+  const int col = blockIdx.x * 256 + threadIdx.x;
+  const int ch = blockIdx.y, g0 = blockIdx.z * 16;
+  const long P = (long)a.B * a.n_int;
+  const long p0 = (long)ch * kTokChunk, p1 = min(P, p0 + kTokChunk);
+  for (int k = 0; k < 16; ++k) acc[k][threadIdx.x] = 0.0f;
+  if (col < E) {
+    for (long pos = p0; pos < p1; ++pos) {
+      if (mask != nullptr && mask[pos] == 0) continue;
+      const int g = min(max(tok[pos], 0), V - 1) - g0;
+      if (g < 0 || g >= 16) continue;
+      acc[g][threadIdx.x] += col < a.LW ? a.loc[pos * a.LW + col] : a.fl[pos * 256 + (col - a.LW)];
+    }
+    for (int k = 0; k < 16 && g0 + k < V; ++k) part[((size_t)ch * V + g0 + k) * E + col] = acc[k][threadIdx.x];
+  }
+}
+
+__global__ __launch_bounds__(256) void k_token_grads2(Args a, const float* part, int nch, int V, int D, float* gP,
+                                                      float* gD) {
+  const int E = a.LW + 256;
+  const long idx = (long)blockIdx.x * 256 + threadIdx.x;
+  if (idx >= (long)V * E) return;
+  const int g = (int)(idx / E), e = (int)(idx - (long)g * E);
+  double s = 0.0;
+  for (int c = 0; c < nch; ++c) s += part[((size_t)c * V + g) * E + e];
+  if (e < a.LW) {
+    const long oi = out_index(a.N, a.d, e);
+    if (oi >= 0) gP[(size_t)g * D + oi] = (float)s;
+  } else {
+    const int f = e - a.LW, i = f >> 4, j = f & 15;
+    if (i < a.d && j < a.d) gD[((size_t)g * a.d + i) * a.d + j] = (float)s;
+  }
+}
+
 // first row index of the column maximum over the prefix rows (B, n, Wr) (the max readout's cotangent goes there)
 __global__ void k_argmax(const float* rows, int n, int Wr, int* amax) {
   const int b = blockIdx.y;
@@ -2662,21 +2725,12 @@ int ews_dense_combine_backward(const ews_dense_desc* desc, const float* levels, 
   return EWS_OK;
 }
 
-int ews_dense_backward(const ews_dense_desc* desc, const float* path, const float* clock, const float* A,
-                       const float* grad_out, float* grad_path, float* grad_clock, float* grad_A, void* workspace,
-                       ews_stream_t stream) {
-  DPlan p;
-  const int rc = dense_plan(desc, p);
-  if (rc != EWS_OK) return rc;
-  if (!path || !clock || !A || !grad_out || !grad_path || !grad_A || !workspace) return EWS_ERR_NULL;
-  const Args a = dense_args(desc, p, path, clock, A, nullptr, workspace, true);
-  hipStream_t st = (hipStream_t)stream;
-  for (int pass = 0; pass <= 2; ++pass) {  // the forward up to the carries
-    const int r = dense_forward_pass(desc, p, a, st, pass);
-    if (r != EWS_OK) return r;
-  }
-  const int r = dense_adjoint(desc, p, a, grad_out, st);
-  if (r != EWS_OK) return r;
+}  // extern "C"
+
+namespace {
+// The leaf's and the flows' adjoints per interval, given ds_t in loc and dM_t in fl: path, clock and A gradients.
+int dense_leaf_adjoint(const ews_dense_desc* desc, const DPlan& p, const Args& a, void* workspace, float* grad_path,
+                       float* grad_clock, float* grad_A, hipStream_t st) {
   const DWs w = dense_ws(p, desc->readout, true);
   char* ws = (char*)workspace;
   LeafBwd o;
@@ -2711,6 +2765,27 @@ int ews_dense_backward(const ews_dense_desc* desc, const float* path, const floa
   DENSE_CHECK();
   return EWS_OK;
 }
+}  // namespace
+
+extern "C" {
+
+int ews_dense_backward(const ews_dense_desc* desc, const float* path, const float* clock, const float* A,
+                       const float* grad_out, float* grad_path, float* grad_clock, float* grad_A, void* workspace,
+                       ews_stream_t stream) {
+  DPlan p;
+  const int rc = dense_plan(desc, p);
+  if (rc != EWS_OK) return rc;
+  if (!path || !clock || !A || !grad_out || !grad_path || !grad_A || !workspace) return EWS_ERR_NULL;
+  const Args a = dense_args(desc, p, path, clock, A, nullptr, workspace, true);
+  hipStream_t st = (hipStream_t)stream;
+  for (int pass = 0; pass <= 2; ++pass) {  // the forward up to the carries
+    const int r = dense_forward_pass(desc, p, a, st, pass);
+    if (r != EWS_OK) return r;
+  }
+  const int r = dense_adjoint(desc, p, a, grad_out, st);
+  if (r != EWS_OK) return r;
+  return dense_leaf_adjoint(desc, p, a, workspace, grad_path, grad_clock, grad_A, st);
+}
 
 int ews_dense_combine(const ews_dense_desc* desc, const float* levels, const float* flows, float* out,
                       void* workspace, ews_stream_t stream) {
@@ -2728,6 +2803,85 @@ int ews_dense_combine(const ews_dense_desc* desc, const float* levels, const flo
     if (r != EWS_OK) return r;
   }
   return EWS_OK;
+}
+
+size_t ews_token_scan_workspace_bytes(const ews_dense_desc* desc, int vocab) {
+  DPlan p;
+  if (vocab < 1 || dense_plan(desc, p) != EWS_OK) return 0;
+  const size_t f = dense_ws(p, desc->readout, false).total, b = dense_ws(p, desc->readout, true).total;
+  const size_t nch = ((size_t)p.B * p.n_int + kTokChunk - 1) / kTokChunk;
+  const size_t part = al256(nch * (size_t)vocab * (p.LW + 256) * 4);
+  return (f > b + part ? f : b + part);
+}
+
+int ews_token_scan(const ews_dense_desc* desc, const int32_t* token_ids, const uint8_t* mask, const float* P_cache,
+                   const float* D_cache, int vocab, float* out, void* workspace, ews_stream_t stream) {
+  DPlan p;
+  const int rc = dense_plan(desc, p);
+  if (rc != EWS_OK) return rc;
+  if (vocab < 1) return EWS_ERR_SHAPE;
+  if (!token_ids || !P_cache || !D_cache || !out || !workspace) return EWS_ERR_NULL;
+  Args a = dense_args(desc, p, nullptr, nullptr, nullptr, out, workspace);
+  hipStream_t st = (hipStream_t)stream;
+  hipLaunchKernelGGL(k_pad_tokens, dim3(p.B * p.n_int), dim3(256), 0, st, a, token_ids, mask, P_cache, D_cache,
+                     vocab, p.D);
+  DENSE_CHECK();
+  for (int pass = 1; pass < kDenseForwardPasses; ++pass) {
+    const int r = dense_combine_pass(desc, p, a, st, pass);
+    if (r != EWS_OK) return r;
+  }
+  return EWS_OK;
+}
+
+int ews_token_scan_backward(const ews_dense_desc* desc, const int32_t* token_ids, const uint8_t* mask,
+                            const float* P_cache, const float* D_cache, int vocab, const float* grad_out,
+                            float* grad_P_cache, float* grad_D_cache, void* workspace, ews_stream_t stream) {
+  DPlan p;
+  const int rc = dense_plan(desc, p);
+  if (rc != EWS_OK) return rc;
+  if (vocab < 1) return EWS_ERR_SHAPE;
+  if (!token_ids || !P_cache || !D_cache || !grad_out || !grad_P_cache || !grad_D_cache || !workspace)
+    return EWS_ERR_NULL;
+  const Args a = dense_args(desc, p, nullptr, nullptr, nullptr, nullptr, workspace, true);
+  hipStream_t st = (hipStream_t)stream;
+  hipLaunchKernelGGL(k_pad_tokens, dim3(p.B * p.n_int), dim3(256), 0, st, a, token_ids, mask, P_cache, D_cache,
+                     vocab, p.D);
+  DENSE_CHECK();
+  for (int pass = 1; pass <= 2; ++pass) {
+    const int r = dense_combine_pass(desc, p, a, st, pass);
+    if (r != EWS_OK) return r;
+  }
+  const int r = dense_adjoint(desc, p, a, grad_out, st);
+  if (r != EWS_OK) return r;
+  float* part = (float*)((char*)workspace + dense_ws(p, desc->readout, true).total);
+  const int nch = (int)(((long)p.B * p.n_int + kTokChunk - 1) / kTokChunk);
+  const int E = p.LW + 256;
+  hipLaunchKernelGGL(k_token_grads1, dim3((E + 255) / 256, nch, (vocab + 15) / 16), dim3(256), 0, st, a, token_ids,
+                     mask, vocab, part);
+  DENSE_CHECK();
+  hipLaunchKernelGGL(k_token_grads2, dim3((int)(((long)vocab * E + 255) / 256)), dim3(256), 0, st, a, part, nch,
+                     vocab, p.D, grad_P_cache, grad_D_cache);
+  DENSE_CHECK();
+  return EWS_OK;
+}
+
+int ews_dense_local_terms_backward(const ews_dense_desc* desc, const float* path, const float* clock, const float* A,
+                                   const float* grad_levels, const float* grad_flows, float* grad_path,
+                                   float* grad_clock, float* grad_A, void* workspace, ews_stream_t stream) {
+  DPlan p;
+  const int rc = dense_plan(desc, p);
+  if (rc != EWS_OK) return rc;
+  if (!path || !clock || !A || !grad_levels || !grad_flows || !grad_path || !grad_A || !workspace)
+    return EWS_ERR_NULL;
+  const Args a = dense_args(desc, p, path, clock, A, nullptr, workspace, true);
+  hipStream_t st = (hipStream_t)stream;
+  const int r = dense_forward_pass(desc, p, a, st, 0);  // the leaf's recompute state (powers, Van Loan saves)
+  if (r != EWS_OK) return r;
+  Args u = a;
+  u.W = p.D + u.lvl0;  // k_pad_inputs reads levels with the packed width D = W - lvl0
+  hipLaunchKernelGGL(k_pad_inputs, dim3(p.B * p.n_int), dim3(256), 0, st, u, grad_levels, grad_flows);
+  DENSE_CHECK();
+  return dense_leaf_adjoint(desc, p, a, workspace, grad_path, grad_clock, grad_A, st);
 }
 
 }  // extern "C"

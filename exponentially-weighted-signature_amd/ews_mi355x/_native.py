@@ -61,6 +61,10 @@ EXPORTED = (
     "ews_lift_workspace_bytes",
     "ews_lift_forward",
     "ews_lift_backward",
+    "ews_dense_local_terms_backward",
+    "ews_token_scan_workspace_bytes",
+    "ews_token_scan",
+    "ews_token_scan_backward",
 )
 
 CLOCK_MODES = {"time": 0, "blended_variation": 1, "blended_learn": 1, "blended_quad_variation": 2,
@@ -242,6 +246,14 @@ def load():
     lib.ews_mixer_forward.restype = i32
     lib.ews_mixer_backward.argtypes = [mdp, vp, vp, vp, vp, vp, vp, vp]
     lib.ews_mixer_backward.restype = i32
+    lib.ews_dense_local_terms_backward.argtypes = [ddp, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp]
+    lib.ews_dense_local_terms_backward.restype = i32
+    lib.ews_token_scan_workspace_bytes.argtypes = [ddp, i32]
+    lib.ews_token_scan_workspace_bytes.restype = sz
+    lib.ews_token_scan.argtypes = [ddp, vp, vp, vp, vp, i32, vp, vp, vp]
+    lib.ews_token_scan.restype = i32
+    lib.ews_token_scan_backward.argtypes = [ddp, vp, vp, vp, vp, i32, vp, vp, vp, vp, vp]
+    lib.ews_token_scan_backward.restype = i32
     cdp = ctypes.POINTER(ClockDesc)
     lib.ews_clock_residual_bytes.argtypes = [cdp]
     lib.ews_clock_residual_bytes.restype = sz

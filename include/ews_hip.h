@@ -185,6 +185,27 @@ int ews_dense_combine_backward(const ews_dense_desc* desc, const float* levels, 
                                const float* grad_out, float* grad_levels, float* grad_flows, void* workspace,
                                ews_stream_t stream);
 
+/* Backward of ews_dense_local_terms: the cotangents grad_levels (B, L-1, sum_k d^k) and grad_flows (B, L-1, d, d)
+ * -> grad_path (B, L, d), grad_clock (B, L) (may be NULL) and grad_A (d, d). Workspace:
+ * ews_dense_backward_workspace_bytes. Replaces JAX autodiff through local_signatures + _chen_M_per_interval
+ * (ews/core/leaf.py:86-114, ews/core/chen_scan.py:155-168), as build_token_cache (ews/core/token_scan.py:44-88)
+ * needs it for the per-token segments. */
+int ews_dense_local_terms_backward(const ews_dense_desc* desc, const float* path, const float* clock, const float* A,
+                                   const float* grad_levels, const float* grad_flows, float* grad_path,
+                                   float* grad_clock, float* grad_A, void* workspace, ews_stream_t stream);
+
+/* Token-cached scan (ews/core/token_scan.py:91-118): desc as for ews_dense_combine with length = steps + 1; step t
+ * of sample b uses P_cache[g] (vocab, sum_k d^k) and D_cache[g] (vocab, d, d) for g = token_ids[b, t] (clamped to
+ * [0, vocab)); a step with mask[b, t] == 0 is the unit signature with the identity flow (mask may be NULL). */
+size_t ews_token_scan_workspace_bytes(const ews_dense_desc* desc, int vocab);
+int ews_token_scan(const ews_dense_desc* desc, const int32_t* token_ids, const uint8_t* mask, const float* P_cache,
+                   const float* D_cache, int vocab, float* out, void* workspace, ews_stream_t stream);
+/* Backward: grad_out -> grad_P_cache (vocab, sum_k d^k) and grad_D_cache (vocab, d, d), the per-step cotangents
+ * summed by token in a fixed order (deterministic). Replaces JAX autodiff through token_cached_prefix_scan. */
+int ews_token_scan_backward(const ews_dense_desc* desc, const int32_t* token_ids, const uint8_t* mask,
+                            const float* P_cache, const float* D_cache, int vocab, const float* grad_out,
+                            float* grad_P_cache, float* grad_D_cache, void* workspace, ews_stream_t stream);
+
 /* ---------------------------------------------------------------------------------------------------------
  * Log-signature readout of LogEWS (ews/layer.py:440-556): per state row the truncated tensor log and its
  * coefficients at the Lyndon words (signax.signature_to_logsignature), then the readout (log-then-pool).

@@ -330,3 +330,22 @@ def test_front_modules_mirror_reference_fields_and_errors():
         E.make_clock(E.ClockSpec(mode="blended_variation", alpha=0.5), 3)(torch.arange(6.0), torch.zeros(6, 3))
     with pytest.raises(ValueError, match="path_mode"):
         E.BlockFront(E.make_clock(E.ClockSpec(), 3), path_mode="delta")
+
+
+def test_token_scan_c_abi_error_codes():
+    lib = nat.load()
+    null = ctypes.c_void_p(0)
+    good = ops.make_dense_desc(2, 51, 4, 2, 0, "per_interval", "prefix", False)
+    assert lib.ews_token_scan_workspace_bytes(ctypes.byref(good), 5) > 0
+    assert lib.ews_token_scan_workspace_bytes(ctypes.byref(good), 0) == 0
+    assert lib.ews_token_scan(ctypes.byref(good), null, null, null, null, 5, null, null, null) == -1
+    assert lib.ews_token_scan(ctypes.byref(good), null, null, null, null, 0, null, null, null) == -2
+    assert lib.ews_token_scan_backward(ctypes.byref(good), null, null, null, null, 5, null, null, null, null,
+                                       null) == -1
+    wide = ops.make_dense_desc(2, 51, 17, 2, 0, "per_interval", "prefix", False)
+    assert lib.ews_token_scan(ctypes.byref(wide), null, null, null, null, 5, null, null, null) == -2
+    assert lib.ews_dense_local_terms_backward(ctypes.byref(good), null, null, null, null, null, null, null, null,
+                                              null, null) == -1
+    with pytest.raises(TypeError, match="HIP device"):
+        E.token_cached_prefix_scan(torch.zeros(5, dtype=torch.int64), None, torch.zeros(3, 20), torch.zeros(3, 4, 4),
+                                   4, 2)
