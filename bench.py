@@ -448,6 +448,78 @@ def bench_c3(args):
     return rec
 
 
+def bench_token(args):
+    """Token-cached scan (the reference's ews/core/token_scan.py) on a formal-language shape: B=256 sequences of
+    L=512 tokens from a vocabulary of 8, embedded to d=16 displacements (the dense path's width), depth 2, a dense
+    generator, Van Loan leaf (M=20, cayley) and exact flows. One step = the per-token cache (8 leaves and flows),
+    the cached scan forward and backward, and the cache's backward to the embeddings and A; the same prefix rows
+    from the ordinary dense scan on the expanded path are timed beside it."""
+    import torch
+
+    import ews_mi355x as E
+
+    dev = torch.device("cuda:0")
+    B, L, V, d, N = 256, 512, 8, 16, 2
+    rng = np.random.default_rng([6, 0])
+    emb = torch.tensor(rng.normal(0.0, 1.0 / np.sqrt(d), size=(V, d)), dtype=torch.float32, device=dev)
+    dth = torch.tensor(rng.uniform(0.5, 1.5, size=V) / L, dtype=torch.float32, device=dev)
+    S = rng.normal(0.0, 0.1, size=(d, d))
+    A = torch.tensor(np.diag(np.log1p(np.exp(rng.uniform(0, 1, d)))) + (S - S.T) / 2, dtype=torch.float32,
+                     device=dev)
+    ids = torch.tensor(rng.integers(0, V, size=(B, L)), device=dev)
+    g_out = torch.tensor(rng.normal(size=(B, L, d + d * d)) / np.sqrt(d + d * d), dtype=torch.float32, device=dev)
+    embg, dthg, Ag = (t.clone().requires_grad_(True) for t in (emb, dth, A))
+
+    def step():
+        P, Dc = E.build_token_cache(embg, dthg, Ag, 20, N, "cayley", "exact", "van_loan")
+        out = E.token_cached_prefix_scan(ids, None, P, Dc, d, N)
+        out.backward(g_out)
+        return out
+
+    # the ordinary route: the path of cumulated token displacements through the dense EWS kernels
+    path = torch.cat([torch.zeros(B, 1, d, device=dev), torch.cumsum(emb[ids], 1)], 1).contiguous()
+    clock = torch.cat([torch.zeros(B, 1, device=dev), torch.cumsum(dth[ids], 1)], 1).contiguous()
+    layer = E.EWS(E.AParamConstant(A), N=N, M=20, leaf="van_loan", van_loan_expm="cayley", chen_expm="exact").to(dev)
+    pg = path.clone().requires_grad_(True)
+    g_flat = torch.cat([torch.zeros(B, L, 1, device=dev), g_out], -1)
+
+    def ordinary():
+        out = layer(pg, clock, readout="prefix")
+        out.backward(g_flat)
+        return out
+
+    def timed(fn):
+        for _ in range(args.warmup):
+            fn()
+        torch.cuda.synchronize()
+        t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        t0.record()
+        for _ in range(args.steps):
+            fn()
+        t1.record()
+        torch.cuda.synchronize()
+        return t0.elapsed_time(t1) / args.steps
+
+    ms = timed(step)
+    ms_ord = timed(ordinary)
+    with torch.no_grad():
+        a = E.token_cached_prefix_scan(ids, None, *E.build_token_cache(emb, dth, A, 20, N, "cayley", "exact",
+                                                                        "van_loan"), d, N)
+        b = layer(path, clock, readout="prefix")[..., 1:]
+        agree = float((a - b).abs().max() / b.abs().max())
+    return {
+        "metric": "EWS Chen-scan fwd+bwd time-steps/sec and HBM GB/s (% peak) on 1 MI355X",
+        "value": round(B * L / (ms * 1e-3), 1), "unit": "time-steps/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(ms, 4), "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "f32", "data": "synthetic",
+        "config": {"workload": "token cache: B=256, L=512 tokens, vocab 8, d=16 dense A, depth 2, van_loan M=20, "
+                               "cache + cached scan fwd+bwd (grads to the embeddings, clock increments and A)",
+                   "global_batch": B, "seq_len": L, "parallelism": "none (1 GPU)"},
+        "ordinary_dense_scan_fwd_bwd_ms": round(ms_ord, 4),
+        "token_vs_ordinary_prefix_relerr": agree,
+    }
+
+
 def algorithmic_bytes(B, L, d, W, s_in=4):
     """Compulsory HBM bytes per launch of each pass (per-interval figures times B (L-1) intervals)."""
     n = B * (L - 1)
@@ -531,9 +603,10 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--check", action="store_true", help="also check one forward against the C float64 checker")
     ap.add_argument("--chunk", type=int, default=0, help="intervals per chunk (0: the library's default)")
-    ap.add_argument("--config", choices=["c2", "c3", "c1", "c4", "c5"], default="c2",
+    ap.add_argument("--config", choices=["c2", "c3", "c1", "c4", "c5", "tok"], default="c2",
                     help="c2 (default, the headline): planes fwd+bwd; c3: dense-generator depth-3 forward; c1, c4, "
-                         "c5: one block of the other BASELINE.json configs (real diagonal; LogEWS; bf16 planes)")
+                         "c5: one block of the other BASELINE.json configs (real diagonal; LogEWS; bf16 planes); tok: the "
+                         "token-cached scan on a formal-language shape")
     ap.add_argument("--backward", action="store_true", help="c3: time forward + backward (ews_dense_backward)")
     ap.add_argument("--leaf", choices=["series", "van_loan"], default="series",
                     help="leaf of the c3 forward: series (q=24) or Van Loan (M=20, cayley)")
@@ -573,6 +646,12 @@ def main():
 
         torch.cuda.set_device(0)
         print(json.dumps(bench_c3(args)), flush=True)
+        return
+    if args.config == "tok":
+        import torch
+
+        torch.cuda.set_device(0)
+        print(json.dumps(bench_token(args)), flush=True)
         return
 
     import torch

@@ -2258,8 +2258,9 @@ __global__ void k_pad_tokens(Args a, const int* tok, const uint8_t* mask, const 
 
 // Cache gradients: the per-step cotangents (ds_t in loc, dM_t in fl, padded) summed by token. Stage 1: a
 // workgroup per (256 columns, chunk of kTokChunk steps, group of 16 tokens), each thread owning one column of the
-// 16 accumulators; stage 2: a thread per (token, column) sums the chunks in order and unpads. Deterministic.
-constexpr int kTokChunk = 1024;
+// 16 accumulators and reading 8 steps ahead; stage 2: per (token, column) the chunks summed by 4 wavefronts and
+// combined in a fixed order, then unpadded. Deterministic.
+constexpr int kTokChunk = 512;
 __global__ __launch_bounds__(256) void k_token_grads1(Args a, const int* tok, const uint8_t* mask, int V,
                                                       float* part) {
   __shared__ float acc[16][256];
@@ -2269,25 +2270,54 @@ __global__ __launch_bounds__(256) void k_token_grads1(Args a, const int* tok, co
   const long P = (long)a.B * a.n_int;
   const long p0 = (long)ch * kTokChunk, p1 = min(P, p0 + kTokChunk);
   for (int k = 0; k < 16; ++k) acc[k][threadIdx.x] = 0.0f;
-  if (col < E) {
-    for (long pos = p0; pos < p1; ++pos) {
-      if (mask != nullptr && mask[pos] == 0) continue;
-      const int g = min(max(tok[pos], 0), V - 1) - g0;
-      if (g < 0 || g >= 16) continue;
-      acc[g][threadIdx.x] += col < a.LW ? a.loc[pos * a.LW + col] : a.fl[pos * 256 + (col - a.LW)];
+  if (col >= E) return;  // no barrier below: each thread owns its column
+  const bool isloc = col < a.LW;
+  const float* src = isloc ? a.loc + col : a.fl + (col - a.LW);
+  const long stride = isloc ? a.LW : 256;
+  long pos = p0;
+  for (; pos + 8 <= p1; pos += 8) {
+    float v[8];
+    int g[8];
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      const long pp = pos + k;
+      const bool on = mask == nullptr || mask[pp] != 0;
+      g[k] = on ? min(max(tok[pp], 0), V - 1) - g0 : -1;
+      v[k] = src[pp * stride];
     }
-    for (int k = 0; k < 16 && g0 + k < V; ++k) part[((size_t)ch * V + g0 + k) * E + col] = acc[k][threadIdx.x];
+#pragma unroll
+    for (int k = 0; k < 8; ++k)
+      if (g[k] >= 0 && g[k] < 16) acc[g[k]][threadIdx.x] += v[k];
   }
+  for (; pos < p1; ++pos) {
+    if (mask != nullptr && mask[pos] == 0) continue;
+    const int g = min(max(tok[pos], 0), V - 1) - g0;
+    if (g >= 0 && g < 16) acc[g][threadIdx.x] += src[pos * stride];
+  }
+  for (int k = 0; k < 16 && g0 + k < V; ++k) part[((size_t)ch * V + g0 + k) * E + col] = acc[k][threadIdx.x];
 }
 
 __global__ __launch_bounds__(256) void k_token_grads2(Args a, const float* part, int nch, int V, int D, float* gP,
                                                       float* gD) {
+  __shared__ double red[4][64];
   const int E = a.LW + 256;
-  const long idx = (long)blockIdx.x * 256 + threadIdx.x;
-  if (idx >= (long)V * E) return;
+  const int l = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const long idx = (long)blockIdx.x * 64 + l;
+  const bool ok = idx < (long)V * E;
+  double s0 = 0.0, s1 = 0.0;
+  if (ok) {
+    int c = w;
+    for (; c + 4 < nch; c += 8) {
+      s0 += part[(size_t)c * V * E + idx];
+      s1 += part[(size_t)(c + 4) * V * E + idx];
+    }
+    if (c < nch) s0 += part[(size_t)c * V * E + idx];
+  }
+  red[w][l] = s0 + s1;
+  __syncthreads();
+  if (w != 0 || !ok) return;
+  const double s = (red[0][l] + red[1][l]) + (red[2][l] + red[3][l]);
   const int g = (int)(idx / E), e = (int)(idx - (long)g * E);
-  double s = 0.0;
-  for (int c = 0; c < nch; ++c) s += part[((size_t)c * V + g) * E + e];
   if (e < a.LW) {
     const long oi = out_index(a.N, a.d, e);
     if (oi >= 0) gP[(size_t)g * D + oi] = (float)s;
@@ -2859,7 +2889,7 @@ int ews_token_scan_backward(const ews_dense_desc* desc, const int32_t* token_ids
   hipLaunchKernelGGL(k_token_grads1, dim3((E + 255) / 256, nch, (vocab + 15) / 16), dim3(256), 0, st, a, token_ids,
                      mask, vocab, part);
   DENSE_CHECK();
-  hipLaunchKernelGGL(k_token_grads2, dim3((int)(((long)vocab * E + 255) / 256)), dim3(256), 0, st, a, part, nch,
+  hipLaunchKernelGGL(k_token_grads2, dim3((int)(((long)vocab * E + 63) / 64)), dim3(256), 0, st, a, part, nch,
                      vocab, p.D, grad_P_cache, grad_D_cache);
   DENSE_CHECK();
   return EWS_OK;
