@@ -1182,6 +1182,25 @@ __device__ __forceinline__ void bwd_step(const DiagArgs& a, const LaneMap& m, co
             rowP = row_sum8(toPj);
             colS = col_sum8(toS);
             colP = col_sum8(toPk);
+          } else if (a.K == 16 || a.K == 32) {
+            // every lane active (K K threads) and row j on the aligned lanes j K .. j K + K - 1 of one wavefront:
+            // rows by an all-reduce over those lanes; columns transposed through LDS ((k, j) order) and then the
+            // same all-reduce, so that lane j K + k holds the sum of column j (the plane lane's share)
+            rowC = toC;
+            rowP = toPj;
+            stT(s_cS + 2 * (m.k * a.K + m.j), toS);
+            stT(s_cP + 2 * (m.k * a.K + m.j), toPk);
+            for (int o = 1; o < a.K; o <<= 1) {
+              rowC += xor_lane(rowC, o);
+              rowP += xor_lane(rowP, o);
+            }
+            __syncthreads();
+            colS = ldT<CPLX, T>(s_cS + 2 * tid);
+            colP = ldT<CPLX, T>(s_cP + 2 * tid);
+            for (int o = 1; o < a.K; o <<= 1) {
+              colS += xor_lane(colS, o);
+              colP += xor_lane(colP, o);
+            }
           } else {
             if (m.active) {
               stT(s_rC + 2 * tid, toC);

@@ -109,10 +109,13 @@ def test_forward_and_grads_match_oracle(case, readout):
         assert ga < 1e-4, f"A-param grad relerr {ga:.2e}"
 
 
-@pytest.mark.parametrize("structure,K,steps", [("real", 32, "unit"), ("planes", 12, "uniform"), ("planes", 12, "unit")])
+@pytest.mark.parametrize("structure,K,steps", [("real", 32, "unit"), ("real", 32, "uniform"), ("real", 16, "unit"),
+                                               ("planes", 16, "uniform"), ("planes", 16, "unit"),
+                                               ("planes", 12, "uniform"), ("planes", 12, "unit")])
 @pytest.mark.parametrize("readout", ["prefix", "mean"])
 def test_wide_states(structure, K, steps, readout):
-    """The widths of BASELINE.json configs[3] (d = 32 real diagonal) and configs[4] (d = 24, 12 planes) at depth 2.
+    """The widths of BASELINE.json configs[3] (d = 32 real diagonal) and configs[4] (d = 24, 12 planes) at depth 2,
+    and 16 diagonal entries or planes (the lane all-reduce of the row and column sums, K = 16 or 32).
     Unit clock steps (the block default clock arange(L)) contract a chunk too much to invert its steps, so the
     adjoint recomputes the states from checkpoints; at d = 32 the plan shortens the checkpoint block to fit LDS."""
     N, B, L = 2, 2, 70
