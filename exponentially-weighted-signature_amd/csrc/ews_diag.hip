@@ -1116,7 +1116,7 @@ struct RedLds {
 // One reverse step of the adjoint at interval t (global interval tg): adds the readout cotangent, then the
 // adjoint of the Chen step with the state S(t-1) = (H1, HA, HB), writes dv[tg] for the plane lanes and the
 // step's dh partial to s_dh, and moves acc's cotangents from S(t) to S(t-1).
-template <bool CPLX, int N, bool WAVE, class T>
+template <bool CPLX, int N, bool WAVE, bool ALLRED, class T>
 __device__ __forceinline__ void bwd_step(const DiagArgs& a, const LaneMap& m, const GammaSrc& gs, int s, int t, int tg,
                                          float h, const float* s_v, bool per_int, const Coef<T>& co,
                                          const CoefD<T>& qq, BwdAcc<T>& acc, T H1, T HA, T HB, const RedLds& red,
@@ -1182,7 +1182,8 @@ __device__ __forceinline__ void bwd_step(const DiagArgs& a, const LaneMap& m, co
             rowP = row_sum8(toPj);
             colS = col_sum8(toS);
             colP = col_sum8(toPk);
-          } else if (a.K == 16 || a.K == 32) {
+          } else if (ALLRED && a.K == 32) {
+            // (1024-lane workgroups only: compiled there, so the narrower instantiations keep their registers)
             // every lane active (K K threads) and row j on the aligned lanes j K .. j K + K - 1 of one wavefront:
             // rows by an all-reduce over those lanes; columns transposed through LDS ((k, j) order) and then the
             // same all-reduce, so that lane j K + k holds the sum of column j (the plane lane's share)
@@ -1473,7 +1474,7 @@ __global__ __launch_bounds__(MAXT) void k_chunk_bwd_inv(DiagArgs a) {
           HB = (ilB0 + ilB1 * dlt) * (SB - cj * s1k - co.IB * (pj * pk));
           if constexpr (CPLX) HA = (ilA0 + ilA1 * dlt) * (SA - cj * conjc(s1k) - co.IA * (pj * conjc(pk)));
         }
-        bwd_step<CPLX, N, WAVE>(a, m, gs, s, t, t0 + t, s_h[t], s_v, cc.per_int, co, q0, acc, H1, HA, HB, red,
+        bwd_step<CPLX, N, WAVE, MAXT == 1024>(a, m, gs, s, t, t0 + t, s_h[t], s_v, cc.per_int, co, q0, acc, H1, HA, HB, red,
                                 s_dh);
         S1 = H1;
         SA = HA;
@@ -1589,7 +1590,8 @@ __device__ __forceinline__ void chunk_bwd_full(const DiagArgs& a, const int c, c
         Coef<T> co;
         CoefD<T> qq;
         coef_at(t, co, qq);
-        bwd_step<CPLX, N, WAVE>(a, m, gs, s, t, t0 + t, s_h[t], s_v, cc.per_int, co, qq, acc, H1, HA, HB, red, s_dh);
+        bwd_step<CPLX, N, WAVE, MAXT == 1024>(a, m, gs, s, t, t0 + t, s_h[t], s_v, cc.per_int, co, qq, acc, H1, HA, HB,
+                                              red, s_dh);
       }
     }
     if (more) lds_dma_wait();

@@ -115,7 +115,8 @@ def test_forward_and_grads_match_oracle(case, readout):
 @pytest.mark.parametrize("readout", ["prefix", "mean"])
 def test_wide_states(structure, K, steps, readout):
     """The widths of BASELINE.json configs[3] (d = 32 real diagonal) and configs[4] (d = 24, 12 planes) at depth 2,
-    and 16 diagonal entries or planes (the lane all-reduce of the row and column sums, K = 16 or 32).
+    and 16 diagonal entries or planes (K = 32 runs the lane all-reduce of the row and column sums, K = 16 and 12 the
+    LDS partial sums).
     Unit clock steps (the block default clock arange(L)) contract a chunk too much to invert its steps, so the
     adjoint recomputes the states from checkpoints; at d = 32 the plan shortens the checkpoint block to fit LDS."""
     N, B, L = 2, 2, 70
