@@ -447,6 +447,25 @@ struct LArgs {
   float* gM;
 };
 
+// Walks e = tid, tid + 256, ... over a row-major tile of width X as (row r, column c), with no division per step.
+struct TileWalk {
+  int r, c, dr, dc, X;
+  __device__ explicit TileWalk(int X_) : X(X_) {
+    r = (int)threadIdx.x / X;
+    c = (int)threadIdx.x - r * X;
+    dr = 256 / X;
+    dc = 256 - dr * X;
+  }
+  __device__ void next() {
+    r += dr;
+    c += dc;
+    if (c >= X) {
+      c -= X;
+      ++r;
+    }
+  }
+};
+
 __device__ __forceinline__ bool lvalid(const LArgs& a, int b, int r) {
   return !a.has_mask || a.m[(size_t)b * a.L + r] != 0;
 }
@@ -501,8 +520,8 @@ __global__ __launch_bounds__(256) void k_lift_sums(LArgs a) {
 // carry: 64 doubles, red: 256 doubles, segtot: 256 floats.
 __device__ void load_u(const LArgs& a, int b, int ch, float* U, double* carry, double* red, float* segtot) {
   const int r0 = ch * LR, n = lastrow(a, b);
-  for (int e = threadIdx.x; e < LR * a.Hin; e += 256) {
-    const int r = e / a.Hin, i = e - r * a.Hin, row = r0 + r;
+  for (TileWalk tw(a.Hin); tw.r < LR; tw.next()) {
+    const int r = tw.r, i = tw.c, row = r0 + r;
     float v = 0.0f;
     if (row < a.L) {
       const int src = fill_idx(row, n, a.L);
@@ -560,10 +579,7 @@ __device__ void load_u(const LArgs& a, int b, int ch, float* U, double* carry, d
 // the matrix into LDS: Ms[o * SM + i] = M[o][i] (o < wl, i < hl)
 __device__ void load_matrix(const LArgs& a, float* Ms) {
   if (a.lift == EWS_LIFT_NONE) return;
-  for (int e = threadIdx.x; e < a.wl * a.hl; e += 256) {
-    const int o = e / a.hl, i = e - o * a.hl;
-    Ms[o * a.SM + i] = a.M[e];
-  }
+  for (TileWalk tw(a.hl); tw.r < a.wl; tw.next()) Ms[tw.r * a.SM + tw.c] = a.M[tw.r * a.hl + tw.c];
 }
 
 __global__ __launch_bounds__(256) void k_lift_rows(LArgs a) {
@@ -580,8 +596,8 @@ __global__ __launch_bounds__(256) void k_lift_rows(LArgs a) {
   float* pb = a.p + (size_t)b * (a.L + a.bp) * a.w;
   if (a.bp && ch == 0)
     for (int o = threadIdx.x; o < a.w; o += 256) pb[o] = 0.0f;
-  for (int e = threadIdx.x; e < LR * a.w; e += 256) {
-    const int r = e / a.w, o = e - r * a.w, row = r0 + r;
+  for (TileWalk tw(a.w); tw.r < LR; tw.next()) {
+    const int r = tw.r, o = tw.c, row = r0 + r;
     if (row >= a.L) break;
     const float* u = U + r * a.SU;
     float v;
@@ -604,13 +620,13 @@ __global__ __launch_bounds__(256) void k_lift_rows(LArgs a) {
 __device__ void load_du(const LArgs& a, int b, int ch, float* DP, const float* Ms, float* DU) {
   const int r0 = ch * LR;
   const float* gp = a.gp + (size_t)b * (a.L + a.bp) * a.w;
-  for (int e = threadIdx.x; e < LR * a.w; e += 256) {
-    const int r = e / a.w, o = e - r * a.w, row = r0 + r;
+  for (TileWalk tw(a.w); tw.r < LR; tw.next()) {
+    const int r = tw.r, o = tw.c, row = r0 + r;
     DP[r * a.SP + o] = row < a.L ? gp[(size_t)(row + a.bp) * a.w + o] : 0.0f;
   }
   __syncthreads();
-  for (int e = threadIdx.x; e < LR * a.Hin; e += 256) {
-    const int r = e / a.Hin, i = e - r * a.Hin;
+  for (TileWalk tw(a.Hin); tw.r < LR; tw.next()) {
+    const int r = tw.r, i = tw.c;
     const float* dp = DP + r * a.SP;
     float v;
     if (a.lift == EWS_LIFT_NONE) {
@@ -717,11 +733,11 @@ __global__ __launch_bounds__(256) void k_lift_brows(LArgs a) {
     const int nr = min(LR, a.L - r0);
     const int oo = a.lift == EWS_LIFT_PRESERVE ? 1 : 0;
     float* pp = a.part + ((size_t)b * a.nch + ch) * a.wl * a.hl;
-    for (int e = threadIdx.x; e < a.wl * a.hl; e += 256) {
-      const int o = e / a.hl, i = e - o * a.hl;
+    for (TileWalk tw(a.hl); tw.r < a.wl; tw.next()) {
+      const int o = tw.r, i = tw.c;
       float v = 0.0f;
       for (int r = 0; r < nr; ++r) v = fmaf(DP[r * a.SP + o + oo], U[r * a.SU + i + oo], v);
-      pp[e] = v;
+      pp[o * a.hl + i] = v;
     }
   }
   // branch and appended-clock gradients
@@ -736,8 +752,8 @@ __global__ __launch_bounds__(256) void k_lift_brows(LArgs a) {
     }
   }
   if (!a.incr) {
-    for (int e = threadIdx.x; e < LR * a.H; e += 256) {
-      const int r = e / a.H, j = e - r * a.H, row = r0 + r;
+    for (TileWalk tw(a.H); tw.r < LR; tw.next()) {
+      const int r = tw.r, j = tw.c, row = r0 + r;
       if (row >= a.L) break;
       float v = row <= n ? DU[r * a.SU + a.app + j] : 0.0f;
       if (row == tr && a.has_mask) v += (float)acc[80 + a.app + j];
