@@ -33,8 +33,10 @@ from .params import (  # noqa: F401
     AParamDampedRotation,
     AParamEFM,
     AParamGeneral,
+    AParamJordanRepeated,
     block_sizes_of,
     is_rotation_planes,
+    jordan_chains_of,
 )
 
 __version__ = "0.1.0"

@@ -29,7 +29,12 @@ from typing import Optional
 import torch
 
 from . import ops
-from .params import AParamConstant, block_sizes_of, diagonal_structure, is_rotation_planes
+from .params import AParamConstant, block_sizes_of, diagonal_structure, is_rotation_planes, jordan_chains_of
+
+# Jordan leaves: the series order that reproduces the exact chain integrals in float32, and the largest clock step
+# times ||A||_1 for which it does (truncation (x^(q+1) / (q+1)!) below 1e-10 and at most one digit of cancellation)
+JORDAN_Q = 24
+JORDAN_MAX_STEP = 4.0
 
 LEAF_KINDS = ("van_loan", "series", "plane_closed", "block_series", "jordan_closed", "jordan_closed_tables")
 COMBINE_KINDS = ("assoc", "lean", "block_kernel", "dense_kernel")
@@ -100,7 +105,7 @@ class EWS(torch.nn.Module):
                 "(rotation planes, AParamUnconstrainedRotation, AParamJordanRepeated or AParamBlockDiag)"
             )
         self.jordan_flows = bool(jordan_flows)
-        if self.jordan_flows:
+        if self.jordan_flows and (combine != "block_kernel" or jordan_chains_of(A_param) is None):
             raise ValueError("jordan_flows needs combine='block_kernel' and a jordan_repeated A with uniform chains")
         if leaf == "block_series" and self.block_sizes is None:
             raise ValueError("leaf='block_series' needs a block-diagonal A parametrisation")
@@ -111,8 +116,11 @@ class EWS(torch.nn.Module):
             )
         if leaf == "block_series" and N == 2 and series_q is None:
             raise ValueError("leaf='block_series' at depth 2 requires series_q")
-        if leaf in JORDAN_LEAVES:
-            raise ValueError(f"leaf={leaf!r} needs a jordan_repeated A with uniform chains")
+        if leaf in JORDAN_LEAVES and jordan_chains_of(A_param) is None:
+            raise ValueError(
+                f"leaf={leaf!r} needs a jordan_repeated A with uniform chains (every block the same kind and size: "
+                "real 2-4 or complex 4, 6, 8)"
+            )
         self.structure = diagonal_structure(A_param)
 
     # ------------------------------------------------------------------------------------------ engine
@@ -141,6 +149,12 @@ class EWS(torch.nn.Module):
         return torch.diagonal(A).contiguous()
 
     def _engine_check(self):
+        if self.leaf in JORDAN_LEAVES:
+            if self.N > 2:
+                raise NotImplementedError("the closed-form Jordan leaf exists for depths 1 and 2")
+            if self.d > 16:
+                raise NotImplementedError("Jordan leaves run on the dense kernels here: d <= 16")
+            return "dense"
         diag_ok = self.structure is not None and self.leaf in ("plane_closed", "block_series", "series") and self.N <= 2
         if diag_ok and self.chen_expm == "exact":
             if self.structure == "planes" and self.d % 2:
@@ -171,11 +185,25 @@ class EWS(torch.nn.Module):
             raise TypeError("the MI355X kernels compute in float32 (dtype=torch.float32)")
         A = self.A_param().to(torch.float32) * torch.as_tensor(a_scale, dtype=torch.float32, device=path.device)
         if engine == "dense":
+            chen = "exact" if self.jordan_flows else self.chen_expm  # closed-form chain flows are exact
+            if self.leaf in JORDAN_LEAVES:
+                # the Jordan closed forms are the exact local integrals; the series leaf of order JORDAN_Q equals
+                # them to float32 precision while the series argument stays small (checked here, loudly)
+                hmax = float((clock[..., 1:] - clock[..., :-1]).abs().max()) if clock.shape[-1] > 1 else 0.0
+                anorm = float(A.abs().sum(0).max())
+                if hmax * anorm > JORDAN_MAX_STEP:
+                    raise NotImplementedError(
+                        f"leaf={self.leaf!r}: clock step x ||A||_1 = {hmax * anorm:.3g} exceeds {JORDAN_MAX_STEP} "
+                        "(the large-step regime of the reference's closed-form tables is not built here)")
+                leaf = ops.DenseLeaf("series", q=JORDAN_Q, chen_expm=chen)
+                return ops.dense_scan(path.to(torch.float32), clock.to(torch.float32),
+                                      A.to(path.device).contiguous(), self.N, leaf.q, self._flow_mode(readout),
+                                      readout, level0, leaf=leaf)
             if self.leaf == "van_loan":
                 leaf = ops.DenseLeaf("van_loan", M=self.M, van_loan_expm=self.van_loan_expm,
-                                     reweighting_mode=self.reweighting_mode, chen_expm=self.chen_expm)
+                                     reweighting_mode=self.reweighting_mode, chen_expm=chen)
             else:
-                leaf = ops.DenseLeaf("series", q=self.series_q, chen_expm=self.chen_expm)
+                leaf = ops.DenseLeaf("series", q=self.series_q, chen_expm=chen)
             return ops.dense_scan(path.to(torch.float32), clock.to(torch.float32), A.to(path.device).contiguous(),
                                   self.N, leaf.q, self._flow_mode(readout), readout, level0, leaf=leaf)
         params = self._diag_params(A.to(path.device))

@@ -77,6 +77,67 @@ class AParamBlockDiag(torch.nn.Module):
         return torch.block_diag(*self.blocks)
 
 
+class AParamJordanRepeated(torch.nn.Module):
+    """Block-diagonal A of Jordan blocks (ews/params.py:412-460): a real block of size n is lambda = softplus(v) on
+    the diagonal with ones directly above (:177-187); a complex block of size 2k is R = [[a, -b], [b, a]],
+    a = softplus(v), in every diagonal slot with the 2x2 identity above (:190-204). block_params: per block a
+    tensor [v] (real) or [v, b] (complex)."""
+
+    def __init__(self, block_sizes, block_kinds, block_params):
+        super().__init__()
+        self.block_sizes = tuple(int(x) for x in block_sizes)
+        self.block_kinds = tuple(str(x) for x in block_kinds)
+        for size, kind in zip(self.block_sizes, self.block_kinds):
+            if kind not in ("real", "complex"):
+                raise ValueError(f"Unknown Jordan block kind '{kind}'")
+            if kind == "real" and size < 2:
+                raise ValueError(
+                    "a real Jordan block needs size >= 2 for the eigenvalue to repeat; "
+                    "size 1 is a plain diagonal entry"
+                )
+            if kind == "complex" and (size % 2 != 0 or size < 4):
+                raise ValueError(
+                    f"a complex Jordan block needs an even size >= 4, got {size}: a conjugate pair "
+                    "already occupies a 2x2 real block, so size 2 is one pair with nothing to chain "
+                    "to -- that is `unconstrained_rotation`, not a Jordan block"
+                )
+        self.block_params = torch.nn.ParameterList([torch.nn.Parameter(torch.as_tensor(p)) for p in block_params])
+        self.dim = int(sum(self.block_sizes))
+
+    def forward(self):
+        blocks = []
+        for size, kind, p in zip(self.block_sizes, self.block_kinds, self.block_params):
+            kw = dict(dtype=p.dtype, device=p.device)
+            if kind == "real":
+                lam = F.softplus(p[0])
+                blk = torch.diag(lam.expand(size)) + torch.diag(torch.ones(size - 1, **kw), 1)
+            else:
+                a, b = F.softplus(p[0]), p[1]
+                R = torch.stack([torch.stack([a, -b]), torch.stack([b, a])])
+                k = size // 2
+                blk = torch.kron(torch.eye(k, **kw), R) + torch.kron(torch.diag(torch.ones(k - 1, **kw), 1),
+                                                                     torch.eye(2, **kw))
+            blocks.append(blk)
+        return torch.block_diag(*blocks)
+
+
+JORDAN_REAL_SIZES, JORDAN_COMPLEX_SIZES = (2, 3, 4), (4, 6, 8)
+
+
+def jordan_chains_of(a_param):
+    """ews/core/kernels/jordan_engine.py:30-43: (kind, size) when A is AParamJordanRepeated with uniform chains of a
+    supported size (real 2-4, complex 4 / 6 / 8), else None."""
+    if not isinstance(a_param, AParamJordanRepeated) or not a_param.block_sizes:
+        return None
+    sizes, kinds = set(a_param.block_sizes), set(a_param.block_kinds)
+    if len(sizes) != 1 or len(kinds) != 1:
+        return None
+    kind, size = kinds.pop(), int(sizes.pop())
+    if size not in (JORDAN_REAL_SIZES if kind == "real" else JORDAN_COMPLEX_SIZES):
+        return None
+    return kind, size
+
+
 class AParamBoundedRotation(torch.nn.Module):
     """Planes [[0, -omega_j], [omega_j, 0]], omega_j = omega_scale * sigmoid(u_j)."""
 
@@ -134,6 +195,8 @@ def block_sizes_of(a_param):
     """Diagonal-block sizes of a parametrisation, from its class (ews/core/kernels/combine.py:37-58)."""
     if isinstance(a_param, AParamBlockDiag):
         return tuple(a_param.sizes)
+    if isinstance(a_param, AParamJordanRepeated):
+        return tuple(a_param.block_sizes)
     if type(a_param).__name__ in ROTATION_CLASSES:
         d = int(a_param.dim)
         return None if d % 2 else (2,) * (d // 2)

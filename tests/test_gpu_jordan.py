@@ -1,0 +1,89 @@
+"""GPU parity of the Jordan-chain leaves (leaf="jordan_closed" / "jordan_closed_tables") and jordan_flows against the
+float64 oracle's exact local integrals (its series leaf at order 40, pinned against quadrature in
+tests/test_oracle_*.py). The reference pins its closed forms the same way: tests/test_jordan_engine.py:66-91 holds
+them to the series leaf (q = 24 at 1e-7, q = 60 at 1e-10).
+
+Bars: forward max relative error <= 1e-5, gradients <= 1e-4 (metric max|a-b| / max|b|). Cases: real chains of 2-4
+and complex chains of 4, 6, 8 (two blocks each), depths 1 and 2, prefix / terminal / mean readouts, with and
+without jordan_flows, steps up to clock step x ||A||_1 = 3.5; and the loud error past the supported step.
+"""
+
+import numpy as np
+import pytest
+import torch
+
+import ews_mi355x as E
+from oracle import ews_oracle as O
+
+pytestmark = pytest.mark.gpu
+
+DEV = "cuda"
+DT = torch.float64
+
+
+def relerr(a, b):
+    a = a.detach().cpu().double()
+    b = b.detach().cpu().double()
+    return float((a - b).abs().max() / max(float(b.abs().max()), 1e-300))
+
+
+def _params(kind, K, seed):
+    rng = np.random.default_rng(seed)
+    return [np.array([rng.normal(-1.5, 0.7)] if kind == "real"
+                     else [rng.normal(-1.5, 0.7), rng.uniform(0.3, 1.5) * rng.choice([-1.0, 1.0])]) for _ in range(K)]
+
+
+CASES = [("real", 2), ("real", 3), ("real", 4), ("complex", 4), ("complex", 6), ("complex", 8)]
+
+
+@pytest.mark.parametrize("flows", [False, True])
+@pytest.mark.parametrize("N", [1, 2])
+@pytest.mark.parametrize("kind,size", CASES)
+def test_jordan_leaf_matches_exact_integrals(kind, size, N, flows):
+    K, B, L = 2, 2, 13
+    d = size * K
+    ps = _params(kind, K, size * 10 + N)
+    A = E.AParamJordanRepeated([size] * K, [kind] * K, [torch.tensor(p, dtype=torch.float32) for p in ps]).to(DEV)
+    Ar = E.AParamJordanRepeated([size] * K, [kind] * K, [torch.tensor(p, dtype=DT) for p in ps])
+    rng = np.random.default_rng(size + N)
+    path = torch.tensor(np.cumsum(rng.normal(size=(B, L, d)) * 0.3, 1), dtype=torch.float32)
+    clock = torch.tensor(np.cumsum(rng.uniform(0.05, 0.15, size=(B, L)), 1), dtype=torch.float32)
+    for leaf in ("jordan_closed", "jordan_closed_tables"):
+        layer = E.EWS(A, N=N, leaf=leaf, combine="block_kernel", jordan_flows=flows,
+                      chen_expm="cayley" if flows else "exact")
+        for readout in ("prefix", "terminal", "mean"):
+            p = path.to(DEV).requires_grad_(True)
+            c = clock.to(DEV).requires_grad_(True)
+            out = layer(p, c, readout=readout)
+            pr = path.double().requires_grad_(True)
+            cr = clock.double().requires_grad_(True)
+            ref = O.ews(pr, cr, Ar(), N, readout, leaf="series", series_q=40, chen_expm="exact",
+                        terminal_reduce="assoc")
+            assert relerr(out, ref) < 1e-5, (leaf, readout, relerr(out, ref))
+            w = torch.tensor(np.random.default_rng(1).normal(size=tuple(ref.shape)))
+            (out * w.to(DEV, torch.float32)).sum().backward()
+            (ref * w).sum().backward()
+            assert relerr(p.grad, pr.grad) < 1e-4, (leaf, readout, relerr(p.grad, pr.grad))
+            assert relerr(c.grad, cr.grad) < 1e-4, (leaf, readout, relerr(c.grad, cr.grad))
+            for q, qr in zip(A.parameters(), Ar.parameters()):
+                assert relerr(q.grad, qr.grad) < 1e-4, (leaf, readout, relerr(q.grad, qr.grad))
+                q.grad = None
+                qr.grad = None
+
+
+def test_jordan_leaf_at_the_largest_supported_step_and_past_it():
+    K, size, B, L = 2, 4, 1, 20
+    ps = _params("complex", K, 7)
+    A = E.AParamJordanRepeated([size] * K, ["complex"] * K, [torch.tensor(p, dtype=torch.float32) for p in ps])
+    Ad = A().detach().double()
+    norm = float(Ad.abs().sum(0).max())
+    rng = np.random.default_rng(8)
+    path = torch.tensor(np.cumsum(rng.normal(size=(B, L, size * K)), 1), dtype=torch.float32)
+    h = 3.5 / norm
+    clock = torch.tensor(np.arange(L, dtype=np.float64)[None] * h, dtype=torch.float32)
+    layer = E.EWS(A.to(DEV), N=2, leaf="jordan_closed", combine="block_kernel", jordan_flows=True)
+    out = layer(path.to(DEV), clock.to(DEV), readout="prefix")
+    ref = O.ews(path.double(), clock.double(), Ad, 2, "prefix", leaf="series", series_q=60, chen_expm="exact")
+    assert relerr(out, ref) < 1e-5, relerr(out, ref)
+    with pytest.raises(NotImplementedError, match="large-step regime"):
+        layer(path.to(DEV), (clock * 1.2).to(DEV), readout="prefix")
