@@ -31,10 +31,11 @@ import torch
 from . import ops
 from .params import AParamConstant, block_sizes_of, diagonal_structure, is_rotation_planes, jordan_chains_of
 
-# Jordan leaves: the series order that reproduces the exact chain integrals in float32, and the largest clock step
-# times ||A||_1 for which it does (truncation (x^(q+1) / (q+1)!) below 1e-10 and at most one digit of cancellation)
-JORDAN_Q = 24
-JORDAN_MAX_STEP = 4.0
+# Leaves whose terms are exact integrals (the Jordan closed forms, the block-series leaf's exact level 1): the series
+# order that reproduces them in float32, and the largest clock step times ||A||_1 for which it does (truncation
+# x^(q+1) / (q+1)! below 1e-10 and at most one digit of cancellation)
+EXACT_Q = 24
+EXACT_MAX_STEP = 4.0
 
 LEAF_KINDS = ("van_loan", "series", "plane_closed", "block_series", "jordan_closed", "jordan_closed_tables")
 COMBINE_KINDS = ("assoc", "lean", "block_kernel", "dense_kernel")
@@ -149,11 +150,11 @@ class EWS(torch.nn.Module):
         return torch.diagonal(A).contiguous()
 
     def _engine_check(self):
-        if self.leaf in JORDAN_LEAVES:
+        if self.leaf in JORDAN_LEAVES or (self.leaf == "block_series" and self.structure is None):
             if self.N > 2:
-                raise NotImplementedError("the closed-form Jordan leaf exists for depths 1 and 2")
+                raise NotImplementedError(f"leaf={self.leaf!r}: closed-form local terms exist for depths 1 and 2")
             if self.d > 16:
-                raise NotImplementedError("Jordan leaves run on the dense kernels here: d <= 16")
+                raise NotImplementedError(f"leaf={self.leaf!r} runs on the dense kernels here: d <= 16")
             return "dense"
         diag_ok = self.structure is not None and self.leaf in ("plane_closed", "block_series", "series") and self.N <= 2
         if diag_ok and self.chen_expm == "exact":
@@ -186,16 +187,18 @@ class EWS(torch.nn.Module):
         A = self.A_param().to(torch.float32) * torch.as_tensor(a_scale, dtype=torch.float32, device=path.device)
         if engine == "dense":
             chen = "exact" if self.jordan_flows else self.chen_expm  # closed-form chain flows are exact
-            if self.leaf in JORDAN_LEAVES:
-                # the Jordan closed forms are the exact local integrals; the series leaf of order JORDAN_Q equals
-                # them to float32 precision while the series argument stays small (checked here, loudly)
+            if self.leaf in JORDAN_LEAVES or self.leaf == "block_series":
+                # Jordan closed forms and the block-series leaf (exact level 1, blockwise series of order series_q
+                # at level 2) on general blocks: the series kernels at order >= EXACT_Q reproduce their exact
+                # integrals to float32 while the series argument stays small (checked here, loudly)
                 hmax = float((clock[..., 1:] - clock[..., :-1]).abs().max()) if clock.shape[-1] > 1 else 0.0
                 anorm = float(A.abs().sum(0).max())
-                if hmax * anorm > JORDAN_MAX_STEP:
+                if hmax * anorm > EXACT_MAX_STEP:
                     raise NotImplementedError(
-                        f"leaf={self.leaf!r}: clock step x ||A||_1 = {hmax * anorm:.3g} exceeds {JORDAN_MAX_STEP} "
-                        "(the large-step regime of the reference's closed-form tables is not built here)")
-                leaf = ops.DenseLeaf("series", q=JORDAN_Q, chen_expm=chen)
+                        f"leaf={self.leaf!r}: clock step x ||A||_1 = {hmax * anorm:.3g} exceeds {EXACT_MAX_STEP} "
+                        "(the large-step regime of the reference's exact forms is not built here)")
+                q = max(EXACT_Q, self.series_q or 0) if self.leaf == "block_series" else EXACT_Q
+                leaf = ops.DenseLeaf("series", q=q, chen_expm=chen)
                 return ops.dense_scan(path.to(torch.float32), clock.to(torch.float32),
                                       A.to(path.device).contiguous(), self.N, leaf.q, self._flow_mode(readout),
                                       readout, level0, leaf=leaf)

@@ -1,5 +1,5 @@
-"""GPU parity of the Jordan-chain leaves (leaf="jordan_closed" / "jordan_closed_tables") and jordan_flows against the
-float64 oracle's exact local integrals (its series leaf at order 40, pinned against quadrature in
+"""GPU parity of the exact-integral leaves, the Jordan-chain leaves (leaf="jordan_closed" / "jordan_closed_tables")
+with jordan_flows and the block-series leaf on general blocks, against the float64 oracle's exact local integrals (its series leaf at order 40, pinned against quadrature in
 tests/test_oracle_*.py). The reference pins its closed forms the same way: tests/test_jordan_engine.py:66-91 holds
 them to the series leaf (q = 24 at 1e-7, q = 60 at 1e-10).
 
@@ -87,3 +87,37 @@ def test_jordan_leaf_at_the_largest_supported_step_and_past_it():
     assert relerr(out, ref) < 1e-5, relerr(out, ref)
     with pytest.raises(NotImplementedError, match="large-step regime"):
         layer(path.to(DEV), (clock * 1.2).to(DEV), readout="prefix")
+
+
+@pytest.mark.parametrize("N", [1, 2])
+@pytest.mark.parametrize("sizes", [(2, 2, 2), (2, 3, 1), (4, 4), (3, 4)])
+def test_block_series_leaf_on_general_blocks(N, sizes):
+    """leaf="block_series" on block-diagonal generators that are neither planes nor diagonals (the cases of the
+    reference's tests/test_engines.py:240-248, which hold the leaf to the series leaf at q = 24 within 1e-7)."""
+    B, L = 2, 11
+    rng = np.random.default_rng(sum(sizes) * 10 + N)
+    blocks = []
+    for n in sizes:
+        S = rng.normal(size=(n, n)) * 0.4
+        blocks.append(np.diag(rng.uniform(0.2, 1.0, n)) + (S - S.T) / 2 + 0.1 * rng.normal(size=(n, n)))
+    A = E.AParamBlockDiag([torch.tensor(b, dtype=torch.float32) for b in blocks], sizes).to(DEV)
+    Ar = E.AParamBlockDiag([torch.tensor(b, dtype=DT) for b in blocks], sizes)
+    d = sum(sizes)
+    path = torch.tensor(np.cumsum(rng.normal(size=(B, L, d)) * 0.3, 1), dtype=torch.float32)
+    clock = torch.tensor(np.cumsum(rng.uniform(0.05, 0.2, size=(B, L)), 1), dtype=torch.float32)
+    layer = E.EWS(A, N=N, leaf="block_series", series_q=24 if N == 2 else None)
+    for readout in ("prefix", "terminal"):
+        p = path.to(DEV).requires_grad_(True)
+        out = layer(p, clock.to(DEV), readout=readout)
+        pr = path.double().requires_grad_(True)
+        ref = O.ews(pr, clock.double(), Ar(), N, readout, leaf="series", series_q=40, chen_expm="exact",
+                    terminal_reduce="assoc")
+        assert relerr(out, ref) < 1e-5, (readout, relerr(out, ref))
+        w = torch.tensor(np.random.default_rng(2).normal(size=tuple(ref.shape)))
+        (out * w.to(DEV, torch.float32)).sum().backward()
+        (ref * w).sum().backward()
+        assert relerr(p.grad, pr.grad) < 1e-4, (readout, relerr(p.grad, pr.grad))
+        for q, qr in zip(A.parameters(), Ar.parameters()):
+            assert relerr(q.grad, qr.grad) < 1e-4, (readout, relerr(q.grad, qr.grad))
+            q.grad = None
+            qr.grad = None

@@ -73,3 +73,8 @@ def test_layer_jordan_options():
         E.EWS(E.AParamConstant(torch.eye(4)), N=2, leaf="jordan_closed_tables")
     with pytest.raises(NotImplementedError, match="depths 1 and 2"):
         E.EWS(A, N=3, leaf="jordan_closed")._engine_check()
+    # block_series on general blocks: the same route (tests/test_engines.py:267-273: depth 3 fails fast)
+    blk = E.AParamBlockDiag([torch.eye(3), torch.eye(2)], [3, 2])
+    assert E.EWS(blk, N=2, leaf="block_series", series_q=12)._engine_check() == "dense"
+    with pytest.raises(NotImplementedError, match="depths 1 and 2"):
+        E.EWS(blk, N=3, leaf="block_series", series_q=12)._engine_check()
