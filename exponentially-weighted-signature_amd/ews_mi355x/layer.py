@@ -18,7 +18,10 @@ ews/core/kernels/combine.py:37-63):
         leaf "van_loan" (the reference default)      dense kernels: Van Loan leaf with M knots per interval under
                                                      van_loan_expm and reweighting_mode
         (also planes / diagonals at depth 3, or      flows M_t of chen_expm evaluated in the kernels, MFMA Chen
-        with chen_expm other than "exact")           mode products (forward only)
+        with chen_expm other than "exact")           mode products
+    Jordan chains, leaf "jordan_closed(_tables)";    dense kernels, series leaf of order >= 24: the exact local
+    block-diagonal A, leaf "block_series";           integrals to float32 while clock step x ||A||_1 <= 4 (an
+    planes, "plane_closed" with approximate flows    error past it), flows of chen_expm (exact for jordan_flows)
     anything else                                    NotImplementedError
 """
 
@@ -166,6 +169,8 @@ class EWS(torch.nn.Module):
                 raise NotImplementedError(
                     f"leaf={self.leaf!r}: the dense-generator kernels cover depths 1-3 and d <= 16")
             return "dense"
+        if diag_ok and self.d <= 16:
+            return "dense"  # closed-form leaf with approximate flows: exact integrals on the dense kernels
         if diag_ok:
             raise NotImplementedError(
                 f"leaf={self.leaf!r}: the closed-form kernels take exact flows exp(-h A) (chen_expm='exact'), "
@@ -187,7 +192,7 @@ class EWS(torch.nn.Module):
         A = self.A_param().to(torch.float32) * torch.as_tensor(a_scale, dtype=torch.float32, device=path.device)
         if engine == "dense":
             chen = "exact" if self.jordan_flows else self.chen_expm  # closed-form chain flows are exact
-            if self.leaf in JORDAN_LEAVES or self.leaf == "block_series":
+            if self.leaf in JORDAN_LEAVES or self.leaf in ("block_series", "plane_closed"):
                 # Jordan closed forms and the block-series leaf (exact level 1, blockwise series of order series_q
                 # at level 2) on general blocks: the series kernels at order >= EXACT_Q reproduce their exact
                 # integrals to float32 while the series argument stays small (checked here, loudly)
@@ -197,7 +202,7 @@ class EWS(torch.nn.Module):
                     raise NotImplementedError(
                         f"leaf={self.leaf!r}: clock step x ||A||_1 = {hmax * anorm:.3g} exceeds {EXACT_MAX_STEP} "
                         "(the large-step regime of the reference's exact forms is not built here)")
-                q = max(EXACT_Q, self.series_q or 0) if self.leaf == "block_series" else EXACT_Q
+                q = max(EXACT_Q, self.series_q or 0)
                 leaf = ops.DenseLeaf("series", q=q, chen_expm=chen)
                 return ops.dense_scan(path.to(torch.float32), clock.to(torch.float32),
                                       A.to(path.device).contiguous(), self.N, leaf.q, self._flow_mode(readout),

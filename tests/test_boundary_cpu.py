@@ -183,8 +183,10 @@ def test_dense_layer_routing_and_errors():
     # flows of another scheme: the dense kernels evaluate it; the closed-form kernels take exact flows only
     assert E.EWS(A, N=3, leaf="series", series_q=8, chen_expm="cayley")._engine_check() == "dense"
     assert E.EWS(_planes(2), N=2, leaf="series", series_q=8, chen_expm="pade")._engine_check() == "dense"
+    # closed-form leaf with approximate flows: the exact integrals on the dense kernels (d <= 16)
+    assert E.EWS(_planes(2), N=2, leaf="plane_closed", chen_expm="cayley")._engine_check() == "dense"
     with pytest.raises(NotImplementedError):
-        E.EWS(_planes(2), N=2, leaf="plane_closed", chen_expm="cayley")._engine_check()
+        E.EWS(_planes(9), N=2, leaf="plane_closed", chen_expm="cayley")._engine_check()
     with pytest.raises(NotImplementedError):
         E.EWS(A, N=4)._engine_check()
     with pytest.raises(NotImplementedError):

@@ -121,3 +121,27 @@ def test_block_series_leaf_on_general_blocks(N, sizes):
             assert relerr(q.grad, qr.grad) < 1e-4, (readout, relerr(q.grad, qr.grad))
             q.grad = None
             qr.grad = None
+
+
+@pytest.mark.parametrize("scheme", ["cayley", "euler", "pade"])
+def test_plane_closed_leaf_with_approximate_flows(scheme):
+    """leaf="plane_closed" with chen_expm other than "exact": the closed-form local terms with the scheme's flows
+    (ews/layer.py:172-265), on the dense kernels, against the oracle's plane closed forms and the same scheme."""
+    K, B, L = 4, 2, 40
+    rng = np.random.default_rng(11)
+    v = torch.tensor(rng.normal(size=K), dtype=torch.float32)
+    u = torch.tensor(rng.normal(size=K), dtype=torch.float32)
+    A = E.AParamDampedRotation(v.clone(), u.clone(), 2 * K, omega_scale=3.0).to(DEV)
+    Ar = E.AParamDampedRotation(v.double(), u.double(), 2 * K, omega_scale=3.0)
+    path = torch.tensor(np.cumsum(rng.normal(size=(B, L, 2 * K)) * 0.3, 1), dtype=torch.float32)
+    clock = torch.tensor(np.cumsum(rng.uniform(0.01, 0.05, size=(B, L)), 1), dtype=torch.float32)
+    layer = E.EWS(A, N=2, leaf="plane_closed", chen_expm=scheme)
+    p = path.to(DEV).requires_grad_(True)
+    out = layer(p, clock.to(DEV), readout="prefix")
+    pr = path.double().requires_grad_(True)
+    ref = O.ews(pr, clock.double(), Ar(), 2, "prefix", leaf="plane_closed", chen_expm=scheme)
+    assert relerr(out, ref) < 1e-5, relerr(out, ref)
+    w = torch.tensor(np.random.default_rng(3).normal(size=tuple(ref.shape)))
+    (out * w.to(DEV, torch.float32)).sum().backward()
+    (ref * w).sum().backward()
+    assert relerr(p.grad, pr.grad) < 1e-4, relerr(p.grad, pr.grad)
