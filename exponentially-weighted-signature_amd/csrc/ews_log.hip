@@ -74,13 +74,15 @@ __device__ __forceinline__ float log_coef(const float* s, const int* wd, int d) 
   return fmaf((1.0f / 3.0f) * s[i] * s[j], s[k], S3[(i * d + j) * d + k] - half);
 }
 
-// per-row logs: one workgroup per (row, sample); the prefix / terminal readouts write out, mean / max write logs
+// per-row logs: one wavefront per (row, sample), four rows per workgroup (a workgroup per row left the chip
+// scheduling tiny workgroups); the prefix / terminal readouts write out, mean / max write logs
 __global__ __launch_bounds__(256) void k_logrows(LArgs a) {
-  const int r = blockIdx.x, b = blockIdx.y;
+  const int r = blockIdx.x * 4 + (threadIdx.x >> 6), b = blockIdx.y, lane = threadIdx.x & 63;
+  if (r >= a.R) return;
   const float* s = a.rows + ((size_t)b * a.R + r) * a.W + a.lvl0;
   const bool pool = a.readout == EWS_READOUT_MEAN || a.readout == EWS_READOUT_MAX;
   float* o = (pool ? a.logs : a.out) + ((size_t)b * a.R + r) * a.Dlog;
-  for (int w = threadIdx.x; w < a.Dlog; w += blockDim.x) o[w] = log_coef(s, a.words + 4 * w, a.d);
+  for (int w = lane; w < a.Dlog; w += 64) o[w] = log_coef(s, a.words + 4 * w, a.d);
 }
 
 // mean / max over the rows, per coefficient (first row of the maximum kept for the backward)
@@ -117,10 +119,14 @@ __global__ void k_logpool(LArgs a) {
 //   dS2[xy] = g(x,y) [x < y] - 1/2 sum over words (a,x,y) of g S1[a] - 1/2 sum over words (x,y,c) of g S1[c]
 //   dS3[abc] = g(a,b,c) on the Lyndon words, 0 elsewhere; the level-0 column is 0.
 // No atomics: each entry is written once, rows stream through with coalesced stores.
-__global__ __launch_bounds__(64) void k_logrows_bwd(LArgs a, const float* gout, float* grows) {
-  extern __shared__ float sh[];  // g (Dlog) | S1 (d) | S2 (d*d, depth 3)
-  const int r = blockIdx.x, b = blockIdx.y, d = a.d, N = a.N, l = threadIdx.x;
-  float* g = sh;
+__global__ __launch_bounds__(256) void k_logrows_bwd(LArgs a, const float* gout, float* grows, int per) {
+  // one wavefront per row, four rows per workgroup; per wavefront: g (Dlog) | S1 (d) | S2 (d*d, depth 3)
+  extern __shared__ float sh[];
+  const int wv = threadIdx.x >> 6;
+  const int rw = blockIdx.x * 4 + wv, b = blockIdx.y, d = a.d, N = a.N, l = threadIdx.x & 63;
+  const bool ok = rw < a.R;
+  const int r = ok ? rw : 0;  // rows past the end read row 0, write nothing and leave after the barrier
+  float* g = sh + wv * per;
   float* s1 = g + a.Dlog;
   float* s2 = s1 + d;
   const float* s = a.rows + ((size_t)b * a.R + r) * a.W + a.lvl0;
@@ -136,6 +142,7 @@ __global__ __launch_bounds__(64) void k_logrows_bwd(LArgs a, const float* gout, 
   if (N >= 3)
     for (int e = l; e < d * d; e += 64) s2[e] = s[d + e];
   __syncthreads();
+  if (!ok) return;
   const int n1 = d, n12 = d + (N >= 2 ? d * (d - 1) / 2 : 0);
   float* gr = grows + ((size_t)b * a.R + r) * a.W;
   if (a.lvl0 && l == 0) gr[0] = 0.0f;
@@ -283,7 +290,7 @@ int ews_log_forward(const ews_log_desc* desc, const float* sig_rows, float* out,
   hipStream_t st = (hipStream_t)stream;
   hipLaunchKernelGGL(k_words, dim3((p.Dlog + 255) / 256), dim3(256), 0, st, a.words, p.d, p.sz[0], p.sz[1], p.Dlog);
   LOG_CHECK();
-  hipLaunchKernelGGL(k_logrows, dim3(p.R, p.B), dim3(256), 0, st, a);
+  hipLaunchKernelGGL(k_logrows, dim3((p.R + 3) / 4, p.B), dim3(256), 0, st, a);
   LOG_CHECK();
   if (p.readout == EWS_READOUT_MEAN || p.readout == EWS_READOUT_MAX) {
     hipLaunchKernelGGL(k_logpool, dim3((p.Dlog + 255) / 256, p.B), dim3(256), 0, st, a);
@@ -306,13 +313,16 @@ int ews_log_backward(const ews_log_desc* desc, const float* sig_rows, const floa
   if (p.readout == EWS_READOUT_MAX) {
     LArgs f = a;
     f.out = grad_rows;  // scratch for the pooled values: overwritten below
-    hipLaunchKernelGGL(k_logrows, dim3(p.R, p.B), dim3(256), 0, st, f);
+    hipLaunchKernelGGL(k_logrows, dim3((p.R + 3) / 4, p.B), dim3(256), 0, st, f);
     LOG_CHECK();
     hipLaunchKernelGGL(k_logpool, dim3((p.Dlog + 255) / 256, p.B), dim3(256), 0, st, f);
     LOG_CHECK();
   }
-  const size_t shm = (size_t)(p.Dlog + p.d + (p.N >= 3 ? p.d * p.d : 0)) * 4;
-  hipLaunchKernelGGL(k_logrows_bwd, dim3(p.R, p.B), dim3(64), shm, st, a, grad_out, grad_rows);
+  const int per = p.Dlog + p.d + (p.N >= 3 ? p.d * p.d : 0);
+  const size_t shm = (size_t)4 * per * 4;
+  (void)hipFuncSetAttribute(reinterpret_cast<const void*>(k_logrows_bwd), hipFuncAttributeMaxDynamicSharedMemorySize,
+                            (int)shm);
+  hipLaunchKernelGGL(k_logrows_bwd, dim3((p.R + 3) / 4, p.B), dim3(256), shm, st, a, grad_out, grad_rows, per);
   LOG_CHECK();
   return EWS_OK;
 }
