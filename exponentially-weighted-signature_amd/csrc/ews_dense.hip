@@ -2237,20 +2237,23 @@ __global__ void k_unpad_outputs(Args a, float* levels, float* flows) {
 // Token cache (ews/core/token_scan.py:91-118): step (b, t) reads the cache row of its token, the packed levels
 // P_cache[g] (ews/core/chen_scan.py:33-46) and the flow D_cache[g]; a padded step is the unit signature (zero levels)
 // with the identity flow. Token ids are clamped to [0, V) (the clamping of an out-of-range JAX gather).
-__global__ void k_pad_tokens(Args a, const int* tok, const uint8_t* mask, const float* pc, const float* dc, int V,
-                             int D) {
-  const long it = blockIdx.x;
+// One wavefront per step, four steps per workgroup (a workgroup per step left the chip scheduling tiny workgroups).
+__global__ __launch_bounds__(256) void k_pad_tokens(Args a, const int* tok, const uint8_t* mask, const float* pc,
+                                                    const float* dc, int V, int D) {
+  const long it = (long)blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  if (it >= (long)a.B * a.n_int) return;
   const bool on = mask == nullptr || mask[it] != 0;
   const int g = min(max(tok[it], 0), V - 1);
   const float* lv = pc + (size_t)g * D;
   float* lo = a.loc + it * a.LW;
-  for (int e = threadIdx.x; e < a.LW; e += blockDim.x) {
+  for (int e = lane; e < a.LW; e += 64) {
     const long oi = out_index(a.N, a.d, e);
     lo[e] = (on && oi >= 0) ? lv[oi] : 0.0f;
   }
   const float* fi = dc + (size_t)g * a.d * a.d;
   float* fo = a.fl + it * 256;
-  for (int e = threadIdx.x; e < 256; e += blockDim.x) {
+  for (int e = lane; e < 256; e += 64) {
     const int i = e >> 4, j = e & 15;
     fo[e] = (on && i < a.d && j < a.d) ? fi[i * a.d + j] : (i == j ? 1.0f : 0.0f);
   }
@@ -2853,7 +2856,7 @@ int ews_token_scan(const ews_dense_desc* desc, const int32_t* token_ids, const u
   if (!token_ids || !P_cache || !D_cache || !out || !workspace) return EWS_ERR_NULL;
   Args a = dense_args(desc, p, nullptr, nullptr, nullptr, out, workspace);
   hipStream_t st = (hipStream_t)stream;
-  hipLaunchKernelGGL(k_pad_tokens, dim3(p.B * p.n_int), dim3(256), 0, st, a, token_ids, mask, P_cache, D_cache,
+  hipLaunchKernelGGL(k_pad_tokens, dim3((p.B * p.n_int + 3) / 4), dim3(256), 0, st, a, token_ids, mask, P_cache, D_cache,
                      vocab, p.D);
   DENSE_CHECK();
   for (int pass = 1; pass < kDenseForwardPasses; ++pass) {
@@ -2874,7 +2877,7 @@ int ews_token_scan_backward(const ews_dense_desc* desc, const int32_t* token_ids
     return EWS_ERR_NULL;
   const Args a = dense_args(desc, p, nullptr, nullptr, nullptr, nullptr, workspace, true);
   hipStream_t st = (hipStream_t)stream;
-  hipLaunchKernelGGL(k_pad_tokens, dim3(p.B * p.n_int), dim3(256), 0, st, a, token_ids, mask, P_cache, D_cache,
+  hipLaunchKernelGGL(k_pad_tokens, dim3((p.B * p.n_int + 3) / 4), dim3(256), 0, st, a, token_ids, mask, P_cache, D_cache,
                      vocab, p.D);
   DENSE_CHECK();
   for (int pass = 1; pass <= 2; ++pass) {
