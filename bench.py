@@ -257,6 +257,28 @@ def bench_diag_cfg(args):
     end.record()
     torch.cuda.synchronize()
     ms = start.elapsed_time(end) / args.steps
+    graph_ms = None
+    if args.graph and not mix:
+        # the same step captured once as a HIP graph and replayed: the launch overhead of its kernels goes away
+        # (the library records no memset and no host synchronisation; replays are checked against eager runs in
+        # tests/test_gpu_diag.py)
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            step()
+        torch.cuda.current_stream().wait_stream(side)
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            step()
+        for _ in range(args.warmup):
+            graph.replay()
+        torch.cuda.synchronize()
+        start.record()
+        for _ in range(args.steps):
+            graph.replay()
+        end.record()
+        torch.cuda.synchronize()
+        graph_ms = start.elapsed_time(end) / args.steps
     evs_all = []
     for _ in range(args.steps):
         evs = new_events()
@@ -327,6 +349,7 @@ def bench_diag_cfg(args):
         "roofline": {"bound": "hbm", "kernel": dominant, "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
                      "algorithmic_bytes": ab[dominant]},
+        **({"graph_ms_per_step": round(graph_ms, 4)} if graph_ms is not None else {}),
         "passes_ms": {k: round(v, 4) for k, v in pass_ms.items()},
         **({"mixer_epilogue_torch_ops_fwd_bwd_ms": torch_mix,
             "mixer_epilogue_fused_fwd_bwd_ms": round(pass_ms["mixer_forward"] + pass_ms.get("mixer_backward", 0.0), 4)}
@@ -616,6 +639,8 @@ def main():
     ap.add_argument("--front", action="store_true",
                     help="c2: start from the raw 6-channel path: the block front (time clock, lift B 6 -> 16) on the "
                          "device before the scan and its backward (raw-path and B gradients) after it")
+    ap.add_argument("--graph", action="store_true",
+                    help="c1 / c4 / c5 without --mixer: also time the step captured as one HIP graph (graph_ms_per_step)")
     ap.add_argument("--clock-grad", action="store_true",
                     help="also compute the clock gradient (the c2 clock is data; off by default)")
     ap.add_argument("--copy-probe", action="store_true",
