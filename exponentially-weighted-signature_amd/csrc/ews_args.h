@@ -15,6 +15,7 @@ struct DiagArgs {
   int kb;                 // checkpoint block (steps) of the recomputing adjoint, <= kBLK
   int W, off1, off2, lvl0, D, npar;
   int path_bf16;
+  int sq1, sq2;           // series order of the level-1 / level-2 local terms (0: exact closed forms)
   const void* path;
   const float* clock;
   const float* params;

@@ -140,11 +140,13 @@ template <class T> __device__ __forceinline__ T conj_if(T x, bool) { return x; }
 __device__ __forceinline__ cf conjc(cf x) { return conj(x); }
 __device__ __forceinline__ float conjc(float x) { return x; }
 
-// Exact coefficients at clock step h (flows at hf: h per interval, the shared step when cached).
+// Coefficients at clock step h (flows at hf: h per interval, the shared step when cached). q1 / q2: series order
+// of the level-1 / level-2 local terms (0: the exact closed forms; see node1q / dd3q); flows are always exact.
 template <class T, bool CPLX, int N, bool DERIV>
-__device__ __forceinline__ void eval_coef(float h, float hf, bool per_int, T uj, T uk, Coef<T>& c, CoefD<T>& q) {
+__device__ __forceinline__ void eval_coef(int q1, int q2, float h, float hf, bool per_int, T uj, T uk, Coef<T>& c,
+                                          CoefD<T>& q) {
   const T xj = h * uj;
-  const Node1<T> nj = node1(xj);
+  const Node1<T> nj = node1q(xj, q1);
   c.phi_j = nj.p;
   hf = per_int ? h : hf;  // flows use the interval's own step unless they are cached
   c.rho = per_int ? nj.e : expv(hf * uj);
@@ -155,10 +157,10 @@ __device__ __forceinline__ void eval_coef(float h, float hf, bool per_int, T uj,
   }
   if (N == 2) {
     const T xk = h * uk;
-    const Node1<T> nk = node1(xk);
+    const Node1<T> nk = node1q(xk, q1);
     c.phi_k = nk.p;
     const T ub = uj + uk;
-    const DD3<T> db = dd3<T, DERIV>(xj, h * ub);
+    const DD3<T> db = dd3q<T, DERIV>(xj, h * ub, q2);
     c.IB = db.d;
     c.lamB = expv(hf * ub);
     if (DERIV) {
@@ -171,7 +173,7 @@ __device__ __forceinline__ void eval_coef(float h, float hf, bool per_int, T uj,
     }
     if (CPLX) {
       const T ua = uj + conjc(uk);
-      const DD3<T> da = dd3<T, DERIV>(xj, h * ua);
+      const DD3<T> da = dd3q<T, DERIV>(xj, h * ua, q2);
       c.IA = da.d;
       c.lamA = expv(hf * ua);
       if (DERIV) {
@@ -334,7 +336,7 @@ __global__ __launch_bounds__(MAXT) void k_chunk_fwd(DiagArgs a) {
   }
   Coef<T> c0;
   CoefD<T> q;
-  if constexpr (FAST) eval_coef<T, CPLX, N, true>(cc.hbar, cc.href, cc.per_int, uj, uk, c0, q);
+  if constexpr (FAST) eval_coef<T, CPLX, N, true>(a.sq1, a.sq2, cc.hbar, cc.href, cc.per_int, uj, uk, c0, q);
 
   // reduce-mode accumulators: [level-1 re, im][level-2 q00, q01, q10, q11]
   float acc[6];
@@ -353,7 +355,7 @@ __global__ __launch_bounds__(MAXT) void k_chunk_fwd(DiagArgs a) {
       lin_coef<T, CPLX, N>(c0, q, h - cc.hbar, cc.per_int, co);
     } else {
       CoefD<T> qq;
-      eval_coef<T, CPLX, N, false>(h, cc.href, cc.per_int, uj, uk, co, qq);
+      eval_coef<T, CPLX, N, false>(a.sq1, a.sq2, h, cc.href, cc.per_int, uj, uk, co, qq);
     }
     const T pj = lds_p<T>(s_v, t, a.d, m.j);
     const T pk = (N == 2) ? lds_p<T>(s_v, t, a.d, m.k) : zero<T>();
@@ -1032,7 +1034,7 @@ __global__ __launch_bounds__(MAXT) void k_chunk_bwd_local(DiagArgs a) {
   const T uk = load_u(a.params, m.k, &dummy);
   Coef<T> c0;
   CoefD<T> q;
-  if constexpr (FAST) eval_coef<T, CPLX, N, true>(cc.hbar, cc.href, cc.per_int, uj, uk, c0, q);
+  if constexpr (FAST) eval_coef<T, CPLX, N, true>(a.sq1, a.sq2, cc.hbar, cc.href, cc.per_int, uj, uk, c0, q);
   T L1 = zero<T>(), LA = zero<T>(), LB = zero<T>();
   for (int blk = nblk - 1; blk >= 0; --blk) {
     const int buf = (nblk - 1 - blk) & 1;
@@ -1056,7 +1058,7 @@ __global__ __launch_bounds__(MAXT) void k_chunk_bwd_local(DiagArgs a) {
             lin_coef<T, CPLX, N>(c0, q, h - cc.hbar, cc.per_int, co);
           } else {
             CoefD<T> qq;
-            eval_coef<T, CPLX, N, false>(h, cc.href, cc.per_int, uj, uk, co, qq);
+            eval_coef<T, CPLX, N, false>(a.sq1, a.sq2, h, cc.href, cc.per_int, uj, uk, co, qq);
           }
           T toC = zero<T>();
           if constexpr (N == 2) {
@@ -1432,7 +1434,7 @@ __global__ __launch_bounds__(MAXT) void k_chunk_bwd_inv(DiagArgs a) {
   EWS_BWD_PROLOGUE(cc.fast && cc.inv_ok, kGB)
   Coef<T> c0;
   CoefD<T> q0;
-  eval_coef<T, CPLX, N, true>(cc.hbar, cc.href, cc.per_int, uj, uk, c0, q0);
+  eval_coef<T, CPLX, N, true>(a.sq1, a.sq2, cc.hbar, cc.href, cc.per_int, uj, uk, c0, q0);
   // d/dh of the inverse flows 1/rho = e^{-x}, 1/lambda = e^{-y} at hbar
   const T irho0 = expv(-(cc.per_int ? cc.hbar : cc.href) * uj);
   const T irho1 = cc.per_int ? -(irho0 * uj) : zero<T>();
@@ -1514,13 +1516,13 @@ __device__ __forceinline__ void chunk_bwd_full(const DiagArgs& a, const int c, c
   // kernel does for them; the others evaluate each step's exact coefficients
   Coef<T> c0;
   CoefD<T> q0;
-  if (cc.fast) eval_coef<T, CPLX, N, true>(cc.hbar, cc.href, cc.per_int, uj, uk, c0, q0);
+  if (cc.fast) eval_coef<T, CPLX, N, true>(a.sq1, a.sq2, cc.hbar, cc.href, cc.per_int, uj, uk, c0, q0);
   auto coef_at = [&](int t, Coef<T>& co, CoefD<T>& qq) {
     if (cc.fast) {
       lin_coef<T, CPLX, N>(c0, q0, s_h[t] - cc.hbar, cc.per_int, co);
       qq = q0;
     } else {
-      eval_coef<T, CPLX, N, true>(s_h[t], cc.href, cc.per_int, uj, uk, co, qq);
+      eval_coef<T, CPLX, N, true>(a.sq1, a.sq2, s_h[t], cc.href, cc.per_int, uj, uk, co, qq);
     }
   };
   auto st_store = [&](float* p, T x1, T xa, T xb) {
@@ -1733,6 +1735,7 @@ struct Plan {
 
 constexpr size_t kMaxLds = 160 * 1024;  // LDS per workgroup on gfx950
 constexpr size_t kScanLds = 48 * 1024;
+constexpr int kMaxSeriesQ = 40;  // series order of the series leaves (the dense path's bound)
 
 size_t bwd_lds_bytes(const Plan& p, int T, bool full, int kb) {
   const int NS = p.cplx ? 6 : 2;
@@ -1752,6 +1755,10 @@ int make_plan(const ews_diag_desc* s, Plan& p) {
   if (!p.cplx && s->dim > 32) return EWS_ERR_SHAPE;
   if ((s->flow_mode == EWS_FLOW_CACHED_BASEPOINT) && s->length < 3) return EWS_ERR_SHAPE;
   if (s->chunk < 0) return EWS_ERR_SHAPE;
+  if (s->leaf < EWS_DIAG_LEAF_CLOSED || s->leaf > EWS_DIAG_LEAF_SERIES) return EWS_ERR_OPTION;
+  if (s->leaf != EWS_DIAG_LEAF_CLOSED && (s->series_q < 0 || s->series_q > kMaxSeriesQ)) return EWS_ERR_OPTION;
+  if (s->leaf == EWS_DIAG_LEAF_SERIES && s->series_q < 1) return EWS_ERR_OPTION;
+  if (s->leaf == EWS_DIAG_LEAF_BLOCK_SERIES && s->depth == 2 && s->series_q < 1) return EWS_ERR_OPTION;
   p.B = s->batch;
   p.L = s->length;
   p.n_int = p.L - 1;
@@ -1778,7 +1785,9 @@ int make_plan(const ews_diag_desc* s, Plan& p) {
     while (T > 8 && bwd_lds_bytes(p, T, true, kb) > kMaxLds) T /= 2;
   p.T = T;
   p.kb = kb;
-  p.fast = pairs_eligible(s->structure, s->depth, s->dim, s->readout, s->flow_mode, T);
+  // the pair-group kernels evaluate the exact closed forms only
+  p.fast = pairs_eligible(s->structure, s->depth, s->dim, s->readout, s->flow_mode, T) &&
+           s->leaf == EWS_DIAG_LEAF_CLOSED;
   p.C = (p.n_int + T - 1) / T;
   p.lds_bwd_local = (size_t)bwd_lds_layout(T, p.d, p.W, p.NTb, 0, p.wave, false, kGB).total * 4;
   p.lds_bwd_full = bwd_lds_bytes(p, T, true, kb);
@@ -1834,6 +1843,8 @@ DiagArgs make_args(const ews_diag_desc* s, const Plan& p, const void* path, cons
   a.flow_mode = s->flow_mode; a.readout = s->readout; a.T = p.T; a.C = p.C; a.scan_cb = p.scan_cb; a.kb = p.kb;
   a.W = p.W; a.lvl0 = s->level0 ? 1 : 0; a.off1 = a.lvl0; a.off2 = a.lvl0 + p.d; a.D = p.D; a.npar = p.npar;
   a.path_bf16 = s->path_dtype == EWS_DTYPE_BF16;
+  a.sq1 = s->leaf == EWS_DIAG_LEAF_SERIES ? s->series_q : 0;
+  a.sq2 = s->leaf == EWS_DIAG_LEAF_CLOSED ? 0 : s->series_q;
   a.path = path; a.clock = clock; a.params = params;
   char* r = (char*)residual;
   a.carries = (double*)r;

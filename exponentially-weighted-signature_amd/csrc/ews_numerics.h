@@ -197,4 +197,70 @@ template <class T, bool DERIV> EWS_HD DD3<T> dd3(T x, T y) {
   return o;
 }
 
+// Order-q truncations: the series leaf (ews/core/series_leaf.py:8-25) on a diagonal or plane generator. Its
+// letters are b_p = x^p / p! times the increment, so each level-k coefficient is the degree-<= q Taylor
+// polynomial of the exact divided difference in the nodes:
+//   phi_q(x)   = sum_{n <= q} x^n / (n+1)!
+//   D_q(x, y)  = sum_{m <= q} h_m(x, y) / (m+2)!        (h_m homogeneous of degree m in (x, x' = y - x))
+// Node derivatives are the derivatives of these polynomials (degree q - 1): dphi_q = sum_{n < q} (n+1) x^n/(n+2)!,
+// dD_q/dx = sum_{m < q} h_m(x, x, y)/(m+3)!, dD_q/dy = sum_{m < q} h_m(x, y, y)/(m+3)!. Each sum is accumulated
+// in increasing degree with the factorials folded into the running terms (no 1/n! table, no underflow at q = 40).
+// q <= 0 selects the exact functions above.
+template <class T> EWS_HD Node1<T> node1q(T x, int q) {
+  if (q <= 0) return node1(x);
+  Node1<T> o;
+  o.e = expv(x);
+  T t = one<T>();         // x^n / (n+1)!
+  T u = 0.5f * one<T>();  // x^n / (n+2)!
+  T p = t;
+  T dp = zero<T>();
+  if (q >= 1) dp = u;
+  for (int n = 1; n <= q; ++n) {
+    t = t * x * (1.0f / (float)(n + 1));
+    p += t;
+    if (n < q) {
+      u = u * x * (1.0f / (float)(n + 2));
+      dp += (float)(n + 1) * u;
+    }
+  }
+  o.p = p;
+  o.dp = dp;
+  return o;
+}
+
+template <class T, bool DERIV> EWS_HD DD3<T> dd3q(T x, T y, int q) {
+  if (q <= 0) return dd3<T, DERIV>(x, y);
+  DD3<T> o;
+  T a = 0.5f * one<T>();  // x^m / (m+2)!
+  T g = a;                // h_m(x, y) / (m+2)!
+  T dsum = g;
+  const float s6 = 1.0f / 6.0f;
+  T bx = s6 * one<T>(), by = s6 * one<T>();  // x^m / (m+3)!, y^m / (m+3)!
+  T gx = bx, gy = by;                        // h_m(x, x, y) / (m+3)!, h_m(x, y, y) / (m+3)!
+  T sx = zero<T>(), sy = zero<T>();
+  if (DERIV && q >= 1) {
+    sx = gx;
+    sy = gy;
+  }
+  for (int m = 1; m <= q; ++m) {
+    const float r = 1.0f / (float)(m + 2);
+    a = a * x * r;
+    g = y * g * r + a;
+    dsum += g;
+    if (DERIV && m < q) {
+      const float r3 = 1.0f / (float)(m + 3);
+      bx = bx * x * r3;
+      by = by * y * r3;
+      gx = y * gx * r3 + (float)(m + 1) * bx;
+      gy = x * gy * r3 + (float)(m + 1) * by;
+      sx += gx;
+      sy += gy;
+    }
+  }
+  o.d = dsum;
+  o.dx = sx;
+  o.dy = sy;
+  return o;
+}
+
 }  // namespace ews

@@ -22,6 +22,7 @@ FLOW_CACHED_BASEPOINT = 2
 READOUTS = {"prefix": 0, "terminal": 1, "mean": 2, "max": 3}
 LEAF_SERIES = 0
 LEAF_VAN_LOAN = 1
+DIAG_LEAVES = {"plane_closed": 0, "block_series": 1, "series": 2}
 EXPM_SCHEMES = {"exact": 0, "euler": 1, "cayley": 2, "pade": 3}
 DTYPE_F32 = 0
 DTYPE_BF16 = 1
@@ -89,6 +90,8 @@ class DiagDesc(ctypes.Structure):
         ("level0", ctypes.c_int32),
         ("path_dtype", ctypes.c_int32),
         ("chunk", ctypes.c_int32),
+        ("leaf", ctypes.c_int32),
+        ("series_q", ctypes.c_int32),
     ]
 
 

@@ -9,10 +9,10 @@ ews/core/kernels/combine.py:37-63):
 
     rotation planes, leaf "plane_closed"             fused closed-form leaf + Chen scan (exact, as the reference)
     rotation planes / real diagonal,
-        leaf "block_series" or "series"              the same fused kernel: its closed forms are the q -> infinity
-                                                     limit of the series leaves (they agree to the series' own
-                                                     truncation bound, ews/core/series_leaf.py:129-143);
-                                                     exact flows (chen_expm "exact")
+        leaf "block_series" or "series"              the same fused kernels with the leaf's order-q series: every
+                                                     coefficient is the degree-<= q Taylor polynomial of the closed
+                                                     form ("series" at every level, "block_series" at level 2 with
+                                                     an exact level 1); exact flows (chen_expm "exact")
     any generator (dense A, d <= 16), depths 1-3,
         leaf "series"                                dense kernels: series leaf of order series_q
         leaf "van_loan" (the reference default)      dense kernels: Van Loan leaf with M knots per interval under
@@ -21,12 +21,15 @@ ews/core/kernels/combine.py:37-63):
         with chen_expm other than "exact")           mode products
     Jordan chains, leaf "jordan_closed(_tables)";    dense kernels, series leaf of order >= 24: the exact local
     block-diagonal A, leaf "block_series";           integrals to float32 while clock step x ||A||_1 <= 4 (an
-    planes, "plane_closed" with approximate flows    error past it), flows of chen_expm (exact for jordan_flows)
+    planes, "plane_closed" with approximate flows    error past it), flows of chen_expm (exact for jordan_flows);
+                                                     "block_series" of an order whose truncation is visible at the
+                                                     call's largest step raises (its level 2 is the order-q series)
     anything else                                    NotImplementedError
 """
 
 from __future__ import annotations
 
+import math
 from typing import Optional
 
 import torch
@@ -39,6 +42,16 @@ from .params import AParamConstant, block_sizes_of, diagonal_structure, is_rotat
 # x^(q+1) / (q+1)! below 1e-10 and at most one digit of cancellation)
 EXACT_Q = 24
 EXACT_MAX_STEP = 4.0
+# largest truncation bound of the reference's series (ews/core/series_leaf.py:139-143) at which exact integrals stand
+# in for an order-q series: below float32 resolution
+SERIES_EXACT_TOL = 1e-7
+
+
+def series_error_bound(x: float, k: int, q: int) -> float:
+    """Per-interval relative error bound of the order-q series at level k, x = ||A|| h
+    (ews/core/series_leaf.py:139-143)."""
+    return (k * x) ** (q + 1) / math.factorial(q + 1) * math.exp(k * x)
+
 
 LEAF_KINDS = ("van_loan", "series", "plane_closed", "block_series", "jordan_closed", "jordan_closed_tables")
 COMBINE_KINDS = ("assoc", "lean", "block_kernel", "dense_kernel")
@@ -202,6 +215,15 @@ class EWS(torch.nn.Module):
                     raise NotImplementedError(
                         f"leaf={self.leaf!r}: clock step x ||A||_1 = {hmax * anorm:.3g} exceeds {EXACT_MAX_STEP} "
                         "(the large-step regime of the reference's exact forms is not built here)")
+                if self.leaf == "block_series" and self.N == 2 and (self.series_q or 0) < EXACT_Q:
+                    # the reference's level 2 is the order-q series (blockdiag_engine.py:143-154); these kernels
+                    # evaluate the exact integrals, which equal it only while its truncation is invisible
+                    xop = hmax * max(anorm, float(A.abs().sum(1).max()))  # >= ||A||_op h
+                    if series_error_bound(xop, 2, int(self.series_q)) > SERIES_EXACT_TOL:
+                        raise NotImplementedError(
+                            f"leaf='block_series' on general blocks: series_q={self.series_q} truncates visibly at "
+                            f"||A|| h = {xop:.3g}; the order-q level-2 series runs for rotation planes and real "
+                            f"diagonals (exact flows), or take series_q >= {EXACT_Q}")
                 q = max(EXACT_Q, self.series_q or 0)
                 leaf = ops.DenseLeaf("series", q=q, chen_expm=chen)
                 return ops.dense_scan(path.to(torch.float32), clock.to(torch.float32),
@@ -218,8 +240,9 @@ class EWS(torch.nn.Module):
         if path.dtype != torch.bfloat16:
             path = path.to(torch.float32)
         clock = clock.to(torch.float32)
+        leaf = self.leaf if self.leaf in ("series", "block_series") else "plane_closed"
         return ops.diag_scan(path, clock, params, self.N, self.structure, self._flow_mode(readout), readout,
-                             level0, chunk=0)
+                             level0, chunk=0, leaf=leaf, series_q=self.series_q or 0)
 
     def _levels(self, packed, lead):
         out, s = [], 0

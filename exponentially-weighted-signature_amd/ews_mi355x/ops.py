@@ -18,9 +18,11 @@ def _stream_handle(device):
     return ctypes.c_void_p(torch.cuda.current_stream(device).cuda_stream)
 
 
-def make_desc(B, L, d, N, structure, flow_mode, readout, level0, path_dtype, chunk=0):
+def make_desc(B, L, d, N, structure, flow_mode, readout, level0, path_dtype, chunk=0, leaf=0, series_q=0):
+    """leaf: 0 exact closed forms ("plane_closed"), 1 "block_series", 2 "series" (nat.DIAG_LEAVES); series_q: the
+    series order of the series leaves."""
     return nat.DiagDesc(B, L, d, N, structure, flow_mode, nat.READOUTS[readout], int(level0), path_dtype,
-                        int(chunk))
+                        int(chunk), int(leaf), int(series_q))
 
 
 def _check_inputs(path, clock, params):
@@ -42,7 +44,7 @@ class DiagScan(torch.autograd.Function):
     ``params`` ((d/2, 2) rows (d_j, w_j) for planes, (d,) for a real diagonal)."""
 
     @staticmethod
-    def forward(ctx, path, clock, params, N, structure, flow_mode, readout, level0, chunk):
+    def forward(ctx, path, clock, params, N, structure, flow_mode, readout, level0, chunk, leaf, series_q):
         lib = nat.load()
         _check_inputs(path, clock, params)
         path = _aligned(path.contiguous())
@@ -50,7 +52,7 @@ class DiagScan(torch.autograd.Function):
         params = params.contiguous()
         B, L, d = path.shape
         dt = nat.DTYPE_BF16 if path.dtype == torch.bfloat16 else nat.DTYPE_F32
-        desc = make_desc(B, L, d, N, structure, flow_mode, readout, level0, dt, chunk)
+        desc = make_desc(B, L, d, N, structure, flow_mode, readout, level0, dt, chunk, leaf, series_q)
         D = d + (d * d if N == 2 else 0)
         W = D + (1 if level0 else 0)
         shape = (B, L - 1, W) if readout == "prefix" else (B, W)
@@ -62,15 +64,15 @@ class DiagScan(torch.autograd.Function):
                                   out.data_ptr(), resid.data_ptr(), ws.data_ptr(), _stream_handle(dev))
         nat.check(rc, "ews_diag_forward")
         ctx.save_for_backward(path, clock, params, resid)
-        ctx.desc = (B, L, d, N, structure, flow_mode, readout, level0, dt, chunk)
+        ctx.desc = (B, L, d, N, structure, flow_mode, readout, level0, dt, chunk, leaf, series_q)
         return out
 
     @staticmethod
     def backward(ctx, gout):
         lib = nat.load()
         path, clock, params, resid = ctx.saved_tensors
-        B, L, d, N, structure, flow_mode, readout, level0, dt, chunk = ctx.desc
-        desc = make_desc(B, L, d, N, structure, flow_mode, readout, level0, dt, chunk)
+        B, L, d, N, structure, flow_mode, readout, level0, dt, chunk, leaf, series_q = ctx.desc
+        desc = make_desc(B, L, d, N, structure, flow_mode, readout, level0, dt, chunk, leaf, series_q)
         gout = gout.contiguous().to(torch.float32)
         dev = path.device
         dpath = torch.empty((B, L, d), device=dev, dtype=torch.float32)
@@ -83,15 +85,18 @@ class DiagScan(torch.autograd.Function):
                                    dclock.data_ptr() if dclock is not None else None, dparams.data_ptr(),
                                    ws.data_ptr(), _stream_handle(dev))
         nat.check(rc, "ews_diag_backward")
-        return dpath.to(path.dtype), dclock, dparams, None, None, None, None, None, None
+        return dpath.to(path.dtype), dclock, dparams, None, None, None, None, None, None, None, None
 
 
 def diag_scan(path, clock, params, N, structure, flow_mode="per_interval", readout="prefix", level0=True,
-              chunk=0):
+              chunk=0, leaf="plane_closed", series_q=0):
+    """leaf "plane_closed" (exact closed forms, for planes and real diagonals alike), "block_series" (exact level 1,
+    the order-series_q series at level 2) or "series" (the order-series_q series at every level)."""
     fm = {"per_interval": nat.FLOW_PER_INTERVAL, "cached": nat.FLOW_CACHED,
           "cached_basepoint": nat.FLOW_CACHED_BASEPOINT}[flow_mode]
     st = {"planes": nat.STRUCT_PLANES, "real_diag": nat.STRUCT_REAL_DIAG}[structure]
-    return DiagScan.apply(path, clock, params, int(N), st, fm, readout, bool(level0), int(chunk))
+    return DiagScan.apply(path, clock, params, int(N), st, fm, readout, bool(level0), int(chunk),
+                          nat.DIAG_LEAVES[leaf], int(series_q or 0))
 
 
 # ---------------------------------------------------------------------------------------------- dense generators

@@ -59,7 +59,15 @@ typedef struct ews_diag_desc {
   int32_t level0;     /* 1: rows carry the leading level-0 constant (the "flat" format), 0: packed */
   int32_t path_dtype; /* EWS_DTYPE_F32 or EWS_DTYPE_BF16 */
   int32_t chunk;      /* intervals per chunk; 0 selects the default */
+  int32_t leaf;       /* EWS_DIAG_LEAF_* (0: the exact closed forms) */
+  int32_t series_q;   /* series order q in [1, 40] of the series leaves (letters b_0..b_q, total order |m| <= q) */
 } ews_diag_desc;
+
+/* local terms of the plane / diagonal path (ews/core/leaf.py:99-175). The flows exp(-h A) are exact in all three. */
+#define EWS_DIAG_LEAF_CLOSED 0       /* "plane_closed" (ews/core/kernels/plane_engine.py:134-152): exact integrals */
+#define EWS_DIAG_LEAF_BLOCK_SERIES 1 /* "block_series" (blockdiag_engine.py:88-155): exact level 1, order-q series at
+                                        level 2 (series_q may be 0 at depth 1) */
+#define EWS_DIAG_LEAF_SERIES 2       /* "series" (series_leaf.py:116-126): the order-q series at every level */
 
 /* Scratch the forward/backward need between launches (chunk summaries, carries, partial reductions).
  * Replaces the XLA-side chunk scan of pallas_combine.py:1395-1422. */

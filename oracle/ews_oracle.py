@@ -270,6 +270,27 @@ def series_local_terms(v, dtheta, A, N, q):
     return levels
 
 
+def exact_level1(v, dtheta, A):
+    """Exact level-1 local term G v, G = int_0^1 e^{-h s A} ds, from the augmented exponential
+    expm([[-h A, I], [0, 0]]) = [[E, G], [0, I]] (ews/core/kernels/blockdiag_engine.py:81-112)."""
+    n, d = v.shape
+    Z = torch.zeros((n, 2 * d, 2 * d), dtype=A.dtype)
+    Z[:, :d, :d] = -dtheta[:, None, None] * A
+    Z[:, :d, d:] = torch.eye(d, dtype=A.dtype)
+    G = torch.linalg.matrix_exp(Z)[:, :d, d:]
+    return torch.einsum("nab,nb->na", G, v)
+
+
+def block_series_local_terms(v, dtheta, A, N, q):
+    """Block-series leaf (ews/core/kernels/blockdiag_engine.py:88-155, routed by ews/core/leaf.py:138-175): the
+    exact level 1 of the augmented exponential, and at depth 2 the series leaf's order-q level 2 (on a
+    block-diagonal A the blockwise letters are the letters of A)."""
+    levels = [exact_level1(v, dtheta, A)]
+    if N >= 2:
+        levels.append(series_local_terms(v, dtheta, A, 2, int(q))[1])
+    return levels
+
+
 def _van_loan_displacement(v, dtheta, A, M, method):
     """One augmented exponential per interval (ews/core/van_loan.py:31-88)."""
     n, d = v.shape
@@ -408,6 +429,8 @@ def local_signatures(path, clock, A, N, leaf="van_loan", M=20, van_loan_expm="ca
         return van_loan_local_terms(v, dtheta, A, N, M, van_loan_expm, reweighting_mode)
     if leaf == "series":
         return series_local_terms(v, dtheta, A, N, int(series_q))
+    if leaf == "block_series":
+        return block_series_local_terms(v, dtheta, A, N, series_q)
     if leaf == "plane_closed":
         return plane_local_terms(v, block_planes(A), dtheta, N)
     if leaf == "diag_closed":

@@ -56,7 +56,7 @@ def _layers(structure, K_or_d, N, seed, **kw):
         gpu = E.AParamEFM(th.clone()).to(DEV)
         ref = E.AParamEFM(th.double())
         leaf = "series"
-        oleaf = "diag_closed"
+        oleaf = "series"  # the oracle's series leaf at the same order (q = 24)
     kwg = dict(kw)
     if leaf == "series":
         kwg["series_q"] = 24
@@ -67,7 +67,7 @@ def _layers(structure, K_or_d, N, seed, **kw):
 def _oracle(ref_param, path, clock, N, readout, oleaf, mode, terminal_reduce):
     A = ref_param()
     return O.ews(path, clock, A, N, readout, leaf=oleaf, reweighting_mode=mode, terminal_reduce=terminal_reduce,
-                 chen_expm="exact")
+                 chen_expm="exact", series_q=24)
 
 
 CASES = [

@@ -96,3 +96,52 @@ def test_real_dd3_matches_opitz(shim):
         big = max(1.0, np.exp(xi), np.exp(yi))
         for g, r in zip(out[i], ref):
             assert abs(g - r) <= 5e-7 * big, (i, xi, yi, g, r)
+
+
+def _trunc(nodes, q):
+    """Degree-<= q part of exp[nodes] in the nodes: the Taylor coefficients of s -> exp[s * nodes] at s = 0
+    (50-digit Opitz, numerical Taylor expansion), summed at s = 1."""
+    mpmath.mp.dps = 50
+    f = lambda s: mpmath.mpc(_dd_exact_mp([s * a for a in nodes]))  # noqa: E731
+    return complex(sum(mpmath.taylor(f, 0, q)))
+
+
+def _dd_exact_mp(nodes):
+    n = len(nodes)
+    J = mpmath.zeros(n, n)
+    for i, a in enumerate(nodes):
+        J[i, i] = a
+        if i + 1 < n:
+            J[i, i + 1] = 1
+    return mpmath.expm(J)[0, n - 1]
+
+
+@pytest.mark.parametrize("q", [1, 4, 9])
+def test_truncated_series_coefficients(shim, q):
+    """node1q / dd3q (the series leaf's order-q coefficients on planes and diagonals) against the degree-<= q
+    Taylor polynomials of the exact divided differences, at nodes of modulus up to 3 where the truncation shows;
+    node derivatives are the degree-<= q-1 parts of exp[0,x,x], exp[0,x,x,y], exp[0,x,y,y]."""
+    rng = np.random.default_rng(40 + q)
+    n = 6
+    x = _cases(rng, n, 3.0)
+    y = (x + _cases(rng, n, 3.0)).astype(np.complex64)
+    xf = np.ascontiguousarray(np.stack([x.real, x.imag], -1).astype(np.float32))
+    yf = np.ascontiguousarray(np.stack([y.real, y.imag], -1).astype(np.float32))
+    o1 = np.zeros((n, 6), np.float32)
+    o2 = np.zeros((n, 6), np.float32)
+    shim.shim_node1q_c(n, q, _ptr(xf), _ptr(o1))
+    shim.shim_dd3q_c(n, q, _ptr(xf), _ptr(yf), _ptr(o2))
+    g1 = o1[:, 0::2] + 1j * o1[:, 1::2]
+    g2 = o2[:, 0::2] + 1j * o2[:, 1::2]
+    visible = 0.0
+    for i in range(n):
+        xi, yi = complex(xf[i, 0], xf[i, 1]), complex(yf[i, 0], yf[i, 1])
+        big = max(1.0, abs(xi), abs(yi)) ** q
+        ref1 = [np.exp(xi), _trunc([0, xi], q), _trunc([0, xi, xi], q - 1)]
+        ref2 = [_trunc([0, xi, yi], q), _trunc([0, xi, xi, yi], q - 1), _trunc([0, xi, yi, yi], q - 1)]
+        for g, r in zip(g1[i], ref1):
+            assert abs(g - r) <= 2e-6 * max(big, abs(np.exp(xi))), (q, i, xi, g, r)
+        for g, r in zip(g2[i], ref2):
+            assert abs(g - r) <= 2e-6 * big, (q, i, xi, yi, g, r)
+        visible = max(visible, abs(ref2[0] - _dd_exact([0, xi, yi])) / abs(ref2[0]))
+    assert visible > 1e-4  # the truncation shows at these nodes

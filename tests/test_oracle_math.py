@@ -295,3 +295,69 @@ def test_oracle_gradients_match_finite_differences():
             fd = (loss(*args_p) - loss(*args_m)) / (2 * eps)
             g = grad.reshape(-1)[idx]
             assert abs(float(fd - g)) <= 1e-6 * max(1.0, abs(float(fd))), (which, idx, float(fd), float(g))
+
+
+def _quad_series(v, h, A, N, q, nodes=32):
+    """The order-q series leaf by another route: the degree-<= q part in h of the defining integral of the local
+    term, i.e. x(u) = e^{-h(1-u)A} v with its exponential replaced by its Taylor polynomial of degree q in h,
+    integrated over the ordered simplex of [0, 1] by Gauss-Legendre quadrature (exact: polynomial integrands).
+    Level 2 keeps the products of total degree <= q in h, the truncation of ews/core/series_leaf.py:8-25."""
+    g, w = np.polynomial.legendre.leggauss(nodes)
+    d = len(v)
+    P = [np.linalg.matrix_power(-h * A, n) / math.factorial(n) for n in range(q + 1)]
+
+    def terms(u):  # degree-n parts of x(u), n = 0..q
+        return [P[n] @ v * (1.0 - u) ** n for n in range(q + 1)]
+
+    us, ws = g / 2 + 0.5, w / 2
+    lvl1 = sum(wi * sum(terms(ui)) for wi, ui in zip(ws, us))
+    out = [lvl1]
+    if N >= 2:
+        s2 = np.zeros((d, d))
+        for wi, u2 in zip(ws, us):
+            t2 = terms(u2)
+            # inner integral over u1 in [0, u2] of the degree-n1 parts, paired with degree n2 <= q - n1
+            inner = [np.zeros(d) for _ in range(q + 1)]
+            for wj, gj in zip(w, g):
+                u1 = u2 * (gj + 1) / 2
+                t1 = terms(u1)
+                for n1 in range(q + 1):
+                    inner[n1] += wj * u2 / 2 * t1[n1]
+            for n1 in range(q + 1):
+                for n2 in range(q + 1 - n1):
+                    s2 += wi * np.outer(inner[n1], t2[n2])
+        out.append(s2)
+    return out
+
+
+@pytest.mark.parametrize("q", [1, 3, 6, 10])
+@pytest.mark.parametrize("kind", ["planes", "diag"])
+def test_series_truncation_matches_truncated_integral(q, kind):
+    """The oracle's order-q series leaf on a plane / diagonal generator at a unit-size step, where the truncation
+    is far above float64 resolution, against the truncated defining integral."""
+    rng = _rng(11)
+    A = _planes_A(3, rng) if kind == "planes" else np.diag(rng.uniform(0.1, 2.0, size=6))
+    v = rng.normal(size=6)
+    h = 1.3
+    got = O.series_local_terms(torch.tensor(v[None]), torch.tensor([h], dtype=DT), torch.tensor(A), 2, q)
+    ref = _quad_series(v, h, A, 2, q)
+    for g_, r_ in zip(got, ref):
+        np.testing.assert_allclose(g_[0].numpy(), r_, rtol=0, atol=1e-12 * max(1, np.abs(r_).max()))
+    # and the truncation is visible: the exact closed form differs at this q
+    exact = O.local_signatures(torch.tensor(np.stack([np.zeros(6), v])), torch.tensor([0.0, h], dtype=DT),
+                               torch.tensor(A), 2, leaf="plane_closed" if kind == "planes" else "diag_closed")
+    assert (exact[1][0] - got[1][0]).abs().max() > 1e-6 * exact[1][0].abs().max()
+
+
+@pytest.mark.parametrize("q", [2, 6])
+def test_block_series_leaf_levels(q):
+    """Block-series leaf: level 1 is exact (the closed form), level 2 is the order-q series."""
+    rng = _rng(12)
+    A = torch.tensor(_planes_A(3, rng))
+    v = torch.tensor(rng.normal(size=(4, 6)))
+    h = torch.tensor([0.2, 0.9, 1.7, 3.0], dtype=DT)
+    got = O.block_series_local_terms(v, h, A, 2, q)
+    closed = O.plane_local_terms(v, O.block_planes(A), h, 2)
+    series = O.series_local_terms(v, h, A, 2, q)
+    torch.testing.assert_close(got[0], closed[0], rtol=1e-12, atol=1e-12)
+    torch.testing.assert_close(got[1], series[1], rtol=0, atol=0)
