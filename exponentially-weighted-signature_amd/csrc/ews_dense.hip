@@ -1510,6 +1510,7 @@ struct LeafBwd {
   float* dv;    // (B, n, 16)
   float* dh;    // (B, n)
   float* dsh;   // (B, 2): cotangents of the shared flow step and of the shared Van Loan step (cached modes)
+  float* dshi;  // (B, n, 2): their per-interval terms, reduced into dsh in a fixed order
   float* part;  // (gridDim.x, HP + 1, 256): per-workgroup H_0..H_PM and the direct dA terms
 };
 
@@ -1869,8 +1870,10 @@ __global__ __launch_bounds__(256) void k_leaf_bwd(Args a, LeafBwd o) {
         o.dh[(size_t)b * a.n_int + t] = dl + dhf;
       } else {
         o.dh[(size_t)b * a.n_int + t] = dl;
-        if (!ident) atomicAdd(o.dsh + 2 * b, dhf);
       }
+      // the shared step's cotangent per interval, summed in a fixed order by k_dsh_reduce
+      o.dshi[2 * ((size_t)b * a.n_int + t)] = (a.flow_mode != EWS_FLOW_PER_INTERVAL && !ident) ? dhf : 0.0f;
+      o.dshi[2 * ((size_t)b * a.n_int + t) + 1] = 0.0f;
     }
     __syncthreads();
   }
@@ -1909,7 +1912,11 @@ __global__ __launch_bounds__(256) void k_vl_bwd(Args a, LeafBwd o) {
   __shared__ __align__(16) float dS3[N >= 3 ? 4096 : 4], dS2[256];
   __shared__ __align__(16) float Esq[SQMAX][256], Fsq[SQMAX][256];
   __shared__ __align__(16) float dS1[16], wv[16], lam[16], red[8];
+  // depth 3: per-wavefront partial sums of each segment's column cotangents (double-buffered by segment parity),
+  // summed in a fixed order
+  __shared__ float wR[2][4][16], wD[2][4][16], rowD[2][16];
   const int tid = threadIdx.x, i = tid >> 4, j = tid & 15, l = tid & 63, g = l >> 4, c16 = l & 15;
+  const int wv_id = tid >> 6;
   const int Mv = a.vm, vs = 512 + 16 * Mv;
   for (int e = tid; e < HP * 256; e += 256) sp[e >> 8][e & 255] = a.apow[e];
   const float norm1 = a.apow[a.npow * 256];
@@ -2003,20 +2010,27 @@ __global__ __launch_bounds__(256) void k_vl_bwd(Args a, LeafBwd o) {
           py += __shfl_xor(py, o2, 64);
           px += __shfl_xor(px, o2, 64);
         }
-        // over the first index (rows i of the wave, then atomics across waves): dR_m[j], dDelta_m[j]
+        // over the first index (rows i of the wave, then the four wavefronts' partials in a fixed order):
+        // dR_m[j], dDelta_m[j]
         float pr2 = q * yi, pd = fmaf(0.5f * q, xi, fmaf(yi, e1, 0.5f * xi * f1));
 #pragma unroll
         for (int o2 = 16; o2 < 64; o2 <<= 1) {
           pr2 += __shfl_xor(pr2, o2, 64);
           pd += __shfl_xor(pd, o2, 64);
         }
-        if (j == 0) {
-          atomicAdd(&dP[m][i], py + px);
-          atomicAdd(&dD[m][i], fmaf(0.5f, py, px * (1.0f / 3.0f)));
+        const int sb = m & 1;
+        if (j == 0) {  // row i lives in one wavefront: a single writer
+          dP[m][i] += py + px;
+          rowD[sb][i] = fmaf(0.5f, py, px * (1.0f / 3.0f));
         }
         if (l < 16) {
-          atomicAdd(&dR[m][j], pr2);
-          atomicAdd(&dD[m][j], pd);
+          wR[sb][wv_id][j] = pr2;
+          wD[sb][wv_id][j] = pd;
+        }
+        __syncthreads();
+        if (tid < 16) {
+          dR[m][tid] += ((wR[sb][0][tid] + wR[sb][1][tid]) + wR[sb][2][tid]) + wR[sb][3][tid];
+          dD[m][tid] += rowD[sb][tid] + (((wD[sb][0][tid] + wD[sb][1][tid]) + wD[sb][2][tid]) + wD[sb][3][tid]);
         }
       }
       __syncthreads();
@@ -2081,12 +2095,14 @@ __global__ __launch_bounds__(256) void k_vl_bwd(Args a, LeafBwd o) {
     const float dhf = EXACTF ? (ident ? 0.0f : block_exp_adjoint(sp, norm1, hf, Gm, nullptr, Esq, Esq, red, H, tid))
                              : block_flow_adjoint(a, sp, norm1, hf, ident, Gm, Esq, W1, W2, W3, red, H, dAl, tid);
     if (tid == 0) {
-      float dh = 0.0f;
+      float dh = 0.0f, s_flow = 0.0f, s_vl = 0.0f;  // shared steps: summed in a fixed order by k_dsh_reduce
       if (a.vl_mode == EWS_FLOW_PER_INTERVAL) dh += ddelta / (float)Mv;
-      else if (!fixed) atomicAdd(o.dsh + 2 * b + 1, ddelta / (float)Mv);
+      else if (!fixed) s_vl = ddelta / (float)Mv;
       if (a.flow_mode == EWS_FLOW_PER_INTERVAL) dh += dhf;
-      else if (!ident) atomicAdd(o.dsh + 2 * b, dhf);
+      else if (!ident) s_flow = dhf;
       o.dh[(size_t)b * a.n_int + t] = dh;
+      o.dshi[2 * ((size_t)b * a.n_int + t)] = s_flow;
+      o.dshi[2 * ((size_t)b * a.n_int + t) + 1] = s_vl;
     }
     __syncthreads();
   }
@@ -2139,6 +2155,33 @@ __global__ __launch_bounds__(256) void k_dA(Args a, const double* hsum, float* g
     __syncthreads();
   }
   if (i < a.d && j < a.d) grad_A[i * a.d + j] = (float)(U[tid] + Hs[HP][tid]);
+}
+
+// dsh[b] = sum over the intervals of dshi[b] (both slots), a workgroup per sample: strided partials, then a fixed
+// tree, so the sum does not depend on scheduling
+__global__ __launch_bounds__(256) void k_dsh_reduce(Args a, LeafBwd o) {
+  __shared__ float r0[256], r1[256];
+  const int b = blockIdx.x, tid = threadIdx.x;
+  const float* src = o.dshi + (size_t)b * a.n_int * 2;
+  float s0 = 0.0f, s1 = 0.0f;
+  for (int t = tid; t < a.n_int; t += 256) {
+    s0 += src[2 * t];
+    s1 += src[2 * t + 1];
+  }
+  r0[tid] = s0;
+  r1[tid] = s1;
+  __syncthreads();
+  for (int w = 128; w > 0; w >>= 1) {
+    if (tid < w) {
+      r0[tid] += r0[tid + w];
+      r1[tid] += r1[tid + w];
+    }
+    __syncthreads();
+  }
+  if (tid == 0) {
+    o.dsh[2 * b] = r0[0];
+    o.dsh[2 * b + 1] = r1[0];
+  }
 }
 
 // knot cotangents: dpath[k] = dv_{k-1} - dv_k, dclock[k] = dh_{k-1} - dh_k, plus the shared steps of the cached modes
@@ -2416,7 +2459,7 @@ int dense_plan(const ews_dense_desc* s, DPlan& p) {
 constexpr int kLeafBwdBlocks = 1024;  // workgroups of the leaf adjoint (one partial dA set each)
 
 struct DWs {
-  size_t apow, loc, fl, summ, sfl, car, pre, mats, lloc, lam, amax, dv, dh, dsh, part, hsum, vlsave, total;
+  size_t apow, loc, fl, summ, sfl, car, pre, mats, lloc, lam, amax, dv, dh, dsh, dshi, part, hsum, vlsave, total;
 };
 // bwd: the backward's layout, the forward's buffers (prefix rows always) followed by the adjoint scan's
 DWs dense_ws(const DPlan& p, int readout, bool bwd = false) {
@@ -2440,6 +2483,7 @@ DWs dense_ws(const DPlan& p, int readout, bool bwd = false) {
     w.dv = off; off += al256(BN * 16 * 4);
     w.dh = off; off += al256(BN * 4);
     w.dsh = off; off += al256((size_t)p.B * 2 * 4);
+    w.dshi = off; off += al256(BN * 2 * 4);
     w.part = off; off += al256((size_t)kLeafBwdBlocks * (HP + 1) * 256 * 4);
     w.hsum = off; off += al256((size_t)PRS * (HP + 1) * 256 * 8);
     w.vlsave = off; off += p.leaf == EWS_LEAF_VAN_LOAN ? al256(BN * (512 + 16 * (size_t)p.vm) * 4) : 0;
@@ -2768,9 +2812,8 @@ int dense_leaf_adjoint(const ews_dense_desc* desc, const DPlan& p, const Args& a
   char* ws = (char*)workspace;
   LeafBwd o;
   o.dv = (float*)(ws + w.dv); o.dh = (float*)(ws + w.dh); o.dsh = (float*)(ws + w.dsh); o.part = (float*)(ws + w.part);
+  o.dshi = (float*)(ws + w.dshi);
   double* hsum = (double*)(ws + w.hsum);
-  hipLaunchKernelGGL(k_zero_rows, dim3(1, 1), dim3(256), 0, st, o.dsh, 0L, 1, 2 * p.B);
-  DENSE_CHECK();
   const long total = (long)p.B * p.n_int;
   const int grid = (int)(total < kLeafBwdBlocks ? total : kLeafBwdBlocks);
   const size_t lshm = p.leaf == EWS_LEAF_VAN_LOAN ? 0 : (size_t)6 * (p.q + 1) * 16 * 4;  // k_leaf_bwd's letters
@@ -2793,6 +2836,8 @@ int dense_leaf_adjoint(const ews_dense_desc* desc, const DPlan& p, const Args& a
   hipLaunchKernelGGL(k_part_reduce, dim3(HP + 1, PRS), dim3(256), 0, st, o.part, grid, hsum);
   DENSE_CHECK();
   hipLaunchKernelGGL(k_dA, dim3(1), dim3(256), 0, st, a, hsum, grad_A);
+  DENSE_CHECK();
+  hipLaunchKernelGGL(k_dsh_reduce, dim3(p.B), dim3(256), 0, st, a, o);
   DENSE_CHECK();
   hipLaunchKernelGGL(k_knots, dim3((p.L + 255) / 256, p.B), dim3(256), 0, st, a, o, grad_path, grad_clock);
   DENSE_CHECK();

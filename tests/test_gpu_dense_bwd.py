@@ -226,3 +226,34 @@ def test_dense_backward_edge_shapes(B, L, d, N):
         assert max(errs) < 1e-4
     got, ref = _grads_kw(path, clock, A, N, "mean", "displacement", dict(leaf="van_loan", M=3, van_loan_expm="cayley"))
     assert max(relerr(g, r) for g, r in zip(got, ref)) < 1e-4
+
+
+@pytest.mark.parametrize("leaf,N,mode", [("van_loan", 3, "displacement_uniform"), ("van_loan", 2, "displacement"),
+                                         ("series", 3, "displacement_uniform_basepoint"),
+                                         ("series", 2, "displacement_uniform")])
+def test_dense_backward_is_deterministic(leaf, N, mode):
+    """Two backward calls in one process give bit-identical gradients of A, the clock and the path: every sum in
+    the dense backward runs in a fixed order (per-wavefront partials, per-interval terms reduced by one workgroup
+    per sample), with no float atomics. The cached modes take the shared-step reduction; depth 3 of the Van Loan
+    leaf the cross-wavefront column sums."""
+    B, L, d = 3, 300, 16
+    rng = np.random.default_rng(77)
+    path = torch.tensor(np.cumsum(rng.normal(size=(B, L, d)) * 0.2, 1), dtype=torch.float32, device=DEV)
+    clock = torch.tensor(np.broadcast_to(np.arange(L) / L, (B, L)).copy(), dtype=torch.float32, device=DEV)
+    A = torch.tensor(rng.normal(size=(d, d)) / np.sqrt(d) + np.eye(d), dtype=torch.float32, device=DEV)
+    dl = ops.DenseLeaf(leaf, q=12, M=8, reweighting_mode=mode)
+    flow = {"displacement": "per_interval", "displacement_uniform": "cached",
+            "displacement_uniform_basepoint": "cached_basepoint"}[mode]
+    g = torch.tensor(rng.normal(size=(B, L - 1, 1 + sum(d**k for k in range(1, N + 1)))), dtype=torch.float32,
+                     device=DEV)
+    grads = []
+    for _ in range(2):
+        p = path.clone().requires_grad_(True)
+        c = clock.clone().requires_grad_(True)
+        a = A.clone().requires_grad_(True)
+        out = ops.dense_scan(p, c, a, N, dl.q, flow, "prefix", True, leaf=dl)
+        (out * g).sum().backward()
+        torch.cuda.synchronize()
+        grads.append((p.grad.clone(), c.grad.clone(), a.grad.clone()))
+    for name, x, y in zip(("path", "clock", "A"), grads[0], grads[1]):
+        assert torch.equal(x, y), f"{name} gradient differs between two identical calls"
