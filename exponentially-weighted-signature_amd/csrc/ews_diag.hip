@@ -23,6 +23,7 @@
 // below float32 rounding); otherwise they are evaluated exactly per step.
 #include <hip/hip_runtime.h>
 
+#include <mutex>
 #include <type_traits>
 
 #include "ews_args.h"
@@ -1727,7 +1728,7 @@ using namespace ews;
 size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 
 struct Plan {
-  int B, L, n_int, d, K, N, T, C, D, W, npar, kb;
+  int B, L, n_int, d, K, N, T, C, D, W, npar, kb, readout;
   bool cplx, wave, fast;
   int NT, NTb, scan_cb, NG;
   size_t lds_bwd_local, lds_bwd_full, lds_bwd_inv, lds_carry, lds_adjoint;
@@ -1760,6 +1761,7 @@ int make_plan(const ews_diag_desc* s, Plan& p) {
   if (s->leaf == EWS_DIAG_LEAF_SERIES && s->series_q < 1) return EWS_ERR_OPTION;
   if (s->leaf == EWS_DIAG_LEAF_BLOCK_SERIES && s->depth == 2 && s->series_q < 1) return EWS_ERR_OPTION;
   p.B = s->batch;
+  p.readout = s->readout;
   p.L = s->length;
   p.n_int = p.L - 1;
   p.d = s->dim;
@@ -1829,6 +1831,26 @@ WsLayout ws_layout(const Plan& p) {
   w.total = off;
   return w;
 }
+// The forward's buffers only (the allocation-free forward): chunk summaries, mean/max partials, group and quad
+// carries; the backward's buffers are absent.
+WsLayout ws_layout_fwd(const Plan& p) {
+  WsLayout w{};
+  size_t off = 0;
+  const size_t BC = (size_t)p.B * p.C;
+  const bool reduce = p.readout == EWS_READOUT_MEAN || p.readout == EWS_READOUT_MAX;
+  w.summ = off; off += align256(BC * p.D * 4);
+  w.red = off; off += reduce ? align256(BC * p.W * 4) : 0;
+  w.red_idx = off; off += reduce ? align256(BC * p.W * 4) : 0;
+  w.gagg = off; off += align256((size_t)p.B * p.NG * p.D * 8);
+  w.gcar = off; off += align256((size_t)p.B * p.NG * p.D * 8);
+  const size_t NQ = (p.C + 3) / 4;
+  w.qagg = off; off += p.fast ? align256((size_t)p.B * NQ * p.D * 4) : 0;
+  w.qflow = off; off += p.fast ? align256((size_t)p.B * NQ * p.K * 16) : 0;
+  w.ql1 = off; off += p.fast ? align256((size_t)p.B * NQ * p.K * 16) : 0;
+  w.cflow = off; off += p.fast ? align256(BC * p.K * 16) : 0;
+  w.total = off;
+  return w;
+}
 size_t resid_carries_bytes(const Plan& p) { return align256((size_t)p.B * (p.C + 1) * p.D * 8); }
 size_t resid_argmax_bytes(const Plan& p) { return align256((size_t)p.B * p.W * 4); }
 size_t resid_chunk_bytes(const Plan& p) { return align256((size_t)p.B * p.C * 4); }
@@ -1836,8 +1858,9 @@ size_t resid_bytes(const Plan& p) {
   return resid_carries_bytes(p) + resid_argmax_bytes(p) + 2 * resid_chunk_bytes(p) + align256(kCoefTabFloats * 4);
 }
 
+// fwd_only: the workspace has the forward's layout (ws_layout_fwd); the backward's pointers are null
 DiagArgs make_args(const ews_diag_desc* s, const Plan& p, const void* path, const float* clock,
-                   const float* params, void* residual, void* workspace) {
+                   const float* params, void* residual, void* workspace, bool fwd_only = false) {
   DiagArgs a{};
   a.B = p.B; a.L = p.L; a.n_int = p.n_int; a.d = p.d; a.K = p.K; a.N = p.N;
   a.flow_mode = s->flow_mode; a.readout = s->readout; a.T = p.T; a.C = p.C; a.scan_cb = p.scan_cb; a.kb = p.kb;
@@ -1853,12 +1876,15 @@ DiagArgs make_args(const ews_diag_desc* s, const Plan& p, const void* path, cons
   a.chbar = (float*)(r + resid_carries_bytes(p) + resid_argmax_bytes(p) + resid_chunk_bytes(p));
   a.ctab = (float*)(r + resid_carries_bytes(p) + resid_argmax_bytes(p) + 2 * resid_chunk_bytes(p));
   a.fast_ok = p.fast ? 1 : 0;
-  const WsLayout w = ws_layout(p);
+  const WsLayout w = fwd_only ? ws_layout_fwd(p) : ws_layout(p);
   char* ws = (char*)workspace;
-  a.summ = (float*)(ws + w.summ); a.mu = (float*)(ws + w.mu); a.mt = (float*)(ws + w.mt);
+  a.summ = (float*)(ws + w.summ);
   a.red = (float*)(ws + w.red); a.red_idx = (int*)(ws + w.red_idx);
-  a.dv = (float*)(ws + w.dv); a.dh = (float*)(ws + w.dh);
-  a.gp = (float*)(ws + w.gp); a.gph = (float*)(ws + w.gph); a.gpart = (double*)(ws + w.gpart);
+  if (!fwd_only) {
+    a.mu = (float*)(ws + w.mu); a.mt = (float*)(ws + w.mt);
+    a.dv = (float*)(ws + w.dv); a.dh = (float*)(ws + w.dh);
+    a.gp = (float*)(ws + w.gp); a.gph = (float*)(ws + w.gph); a.gpart = (double*)(ws + w.gpart);
+  }
   a.gagg = (double*)(ws + w.gagg); a.gcar = (double*)(ws + w.gcar); a.NG = p.NG;
   a.NQ = (p.C + 3) / 4;
   a.qagg = (float*)(ws + w.qagg); a.qflow = (double*)(ws + w.qflow); a.ql1 = (double*)(ws + w.ql1);
@@ -2023,6 +2049,31 @@ int dispatch_backward(const Plan& p, const DiagArgs& a, hipStream_t st, int pass
 constexpr int kForwardPasses = 4;
 constexpr int kBackwardPasses = 5;
 
+// ------------------------------------------------------------------------------------------- allocation-free forward
+// Scratch of ews_diag_forward_noalloc: the forward's residual and workspace in one file-scope device array, of which
+// every GPU the library runs on holds its own copy until the process ends. On the host, `scratch` names a host-side
+// stand-in, not device memory: host code uses only the per-device address hipGetSymbolAddress returns.
+constexpr size_t kNoAllocScratchBytes = size_t(64) << 20;
+__device__ __align__(256) unsigned char scratch[kNoAllocScratchBytes];
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices] = {};
+
+// the scratch address on the current device, looked up once per device with that device current
+int scratch_on_current_device(void** out) {
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return EWS_ERR_LAUNCH;
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* ptr = nullptr;
+    if (hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)) != hipSuccess || !ptr) return EWS_ERR_LAUNCH;
+    g_scratch_ptr[dev] = ptr;
+  }
+  *out = g_scratch_ptr[dev];
+  return EWS_OK;
+}
+
 }  // namespace
 
 extern "C" {
@@ -2090,6 +2141,28 @@ int ews_diag_backward(const ews_diag_desc* desc, const void* path, const float* 
 
 int ews_diag_num_passes(int direction) { return direction == 0 ? kForwardPasses : kBackwardPasses; }
 
+int ews_diag_forward_noalloc(const ews_diag_desc* desc, const void* path, const float* clock, const float* params,
+                             float* out, ews_stream_t stream) {
+  Plan p;
+  int rc = make_plan(desc, p);
+  if (rc != EWS_OK) return rc;
+  if (!path || !clock || !params || !out) return EWS_ERR_NULL;
+  const size_t rb = resid_bytes(p);
+  if (rb + ws_layout_fwd(p).total > kNoAllocScratchBytes) return EWS_ERR_SCRATCH;
+  void* base = nullptr;
+  rc = scratch_on_current_device(&base);
+  if (rc != EWS_OK) return rc;
+  // no pass reads scratch it has not written in the same call (no zeroed state is assumed), so the contents a
+  // previous call left behind are harmless
+  DiagArgs a = make_args(desc, p, path, clock, params, base, (char*)base + rb, true);
+  a.out = out;
+  for (int pass = 0; pass < kForwardPasses; ++pass) {
+    rc = dispatch_forward(desc, p, a, (hipStream_t)stream, pass);
+    if (rc != EWS_OK) return rc;
+  }
+  return EWS_OK;
+}
+
 const char* ews_error_string(int code) {
   switch (code) {
     case EWS_OK: return "ok";
@@ -2098,6 +2171,7 @@ const char* ews_error_string(int code) {
     case EWS_ERR_DEPTH: return "depth not supported by this structure";
     case EWS_ERR_OPTION: return "unknown structure, flow mode, readout or dtype";
     case EWS_ERR_LAUNCH: return "kernel launch failed";
+    case EWS_ERR_SCRATCH: return "the call needs more scratch than the allocation-free entry point holds (64 MiB)";
     default: return "unknown error";
   }
 }

@@ -29,6 +29,7 @@ typedef struct ihipStream_t* ews_stream_t; /* hipStream_t */
 #define EWS_ERR_DEPTH (-3)     /* depth not supported by this structure */
 #define EWS_ERR_OPTION (-4)    /* unknown structure / flow mode / readout / dtype */
 #define EWS_ERR_LAUNCH (-5)    /* a kernel launch failed */
+#define EWS_ERR_SCRATCH (-6)   /* ews_diag_forward_noalloc: the call needs more than its fixed scratch (64 MiB) */
 
 /* generator structure */
 #define EWS_STRUCT_PLANES 1    /* rotation planes A_j = [[d_j, w_j], [-w_j, d_j]] on channels (2j, 2j+1) */
@@ -106,6 +107,17 @@ int ews_diag_backward_pass(const ews_diag_desc* desc, int pass, const void* path
 
 /* Number of passes: direction 0 = forward, 1 = backward. */
 int ews_diag_num_passes(int direction);
+
+/* ews_diag_forward without a residual or workspace argument and without any allocation: no counterpart in the
+ * reference. For callers that cannot allocate device memory: code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc. Its scratch (the forward's float64 carries, chunk summaries and group carries)
+ * is a fixed 64 MiB device array that every GPU the library runs on holds until the process ends; calls whose
+ * scratch exceeds it return EWS_ERR_SCRATCH (c2 and c5 fit; the c4 shape at B = 256 does not). The stream must
+ * belong to the current device. Every call on one GPU shares that GPU's array: calls that overlap in time on one
+ * GPU (several streams, several host threads) race and must be serialised by the caller. The output equals
+ * ews_diag_forward's bit for bit; the residual it would leave is not kept for a backward. */
+int ews_diag_forward_noalloc(const ews_diag_desc* desc, const void* path, const float* clock, const float* params,
+                             float* out, ews_stream_t stream);
 
 /* ---------------------------------------------------------------------------------------------------------
  * Dense generators: any d x d matrix A (d <= 16), depths 1-3, the series leaf (ews/core/series_leaf.py).
