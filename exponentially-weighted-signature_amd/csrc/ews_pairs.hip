@@ -955,7 +955,8 @@ template <int KP, int q> __device__ __forceinline__ void g_pair(const GRow<KP>& 
 }
 
 // B1: chunk-local adjoint with zero incoming cotangent -> mu (cotangent on the chunk's carry-in state). KP = 4.
-template <bool BF16>
+// SKIP_INV: the chunks whose steps may be inverted are left to the full local adjoint (k_bwd_full<.., BW_LOCAL>).
+template <bool BF16, bool SKIP_INV>
 __global__ __launch_bounds__(64) void k_bwd_local(DiagArgs a) {
   constexpr int KP = 4, GPW = Geo<KP>::GPW;
   __shared__ __align__(16) float s_v[2][GPW * VBLK];
@@ -963,6 +964,14 @@ __global__ __launch_bounds__(64) void k_bwd_local(DiagArgs a) {
   const Lane l = lane_of<KP>(threadIdx.x);
   const int b = blockIdx.y, cb = blockIdx.x * GPW, c = cb + l.gi;
   const int nblk = (a.T + SB - 1) / SB;
+  if constexpr (SKIP_INV) {  // nothing to do when every chunk of the workgroup is left to the full local adjoint
+    bool any = false;
+    for (int i = 0; i < GPW && cb + i < a.C; ++i) {
+      const int fl = a.cflag[b * a.C + cb + i];
+      any = any || ((fl & 1) && (fl & 3) != 3);
+    }
+    if (!any) return;
+  }
   VRaw<GPW, BF16> vr;
   vblk_load<GPW, BF16>(a, b, cb, nblk - 1, vr);
   vblk_store<GPW, BF16>(a, cb, nblk - 1, vr, s_v[(nblk - 1) & 1]);
@@ -970,7 +979,7 @@ __global__ __launch_bounds__(64) void k_bwd_local(DiagArgs a) {
   // every lane stays to the end (shared block staging); absent or non-uniform chunks skip the arithmetic
   const int ci = b * a.C + (c < a.C ? c : 0);
   const int flag = c < a.C ? a.cflag[ci] : 0;
-  const bool active = (flag & 1) != 0;
+  const bool active = (flag & 1) != 0 && !(SKIP_INV && (flag & 3) == 3);
   const int t0 = active ? c * a.T : 0, Tc = active ? min(a.T, a.n_int - t0) : 0;
   FwdCoef<KP> f;
   fwd_coef<KP>(a, l, active ? a.chbar[ci] : 0.0f, (flag & 4) != 0, f);
@@ -1049,9 +1058,17 @@ template <int KP> struct BwdCoef {
   cf LB1[KP], LA1[KP];                  // d/dh of the flows
 };
 
-// DH: the clock gradient is requested (dclock non-null); without it the step skips every dh term.
-template <bool BF16, bool DH>
+// Modes of the invertible-chunk adjoint. BW_FULL: the adjoint from the cotangent of the later chunks (mt) plus the
+// readout rows, as described above. BW_LOCAL: the same per-step adjoint from a zero cotangent at the chunk end (the
+// chunk's own rows only): writes dv of every step (a.dv), the chunk's parameter partials and mu (the cotangent on
+// the carry-in state, for the adjoint scan); the later chunks' part is added by k_bwd_carry in closed form.
+constexpr int BW_FULL = 0, BW_LOCAL = 1;
+
+// DH: the clock gradient is requested (dclock non-null); without it the step skips every dh term (BW_LOCAL runs
+// without it only).
+template <bool BF16, bool DH, int MODE>
 __global__ __launch_bounds__(64) void k_bwd_full(DiagArgs a) {
+  static_assert(MODE == BW_FULL || !DH, "the local adjoint runs without the clock gradient");
   constexpr int KP = 2, G = Geo<KP>::G, GPW = Geo<KP>::GPW;
   __shared__ __align__(16) float s_v[GPW * VPITCH];
   __shared__ float s_h[GPW * kMaxT];
@@ -1065,7 +1082,7 @@ __global__ __launch_bounds__(64) void k_bwd_full(DiagArgs a) {
   const Lane l = lane_of<KP>(threadIdx.x);
   const int b = blockIdx.y, cb = blockIdx.x * GPW, c = cb + l.gi;
   stage<KP, BF16>(a, b, cb, s_v, s_h);
-  {
+  if constexpr (MODE == BW_FULL) {
     // adjoint carries inside the quad: mt[c] = mu(c+1) + J_{c+1}^T mt[c+1] down from the quad's last chunk
     // (written by the scan); float64, written back for every later kernel that reads mt (generic chunks)
     const int jj = threadIdx.x >> 3, kk = threadIdx.x & 7;
@@ -1155,15 +1172,17 @@ __global__ __launch_bounds__(64) void k_bwd_full(DiagArgs a) {
     const double* cr = a.carries + ((size_t)b * (a.C + 1) + c + 1) * a.D;
     const float* mp = s_mt[l.gi];
     S1 = cf{(float)cr[2 * l.j], (float)cr[2 * l.j + 1]};
-    l1 = cf{mp[2 * l.j], mp[2 * l.j + 1]};
+    if constexpr (MODE == BW_FULL) l1 = cf{mp[2 * l.j], mp[2 * l.j + 1]};
     static_for<0, KP>([&](auto qc) {
       constexpr int q = qc;
       const int e = DIM + 4 * (l.j * K + KP * l.kg + q);
       SA[q] = cf{(float)(0.5 * cr[e]), (float)(0.5 * cr[e + 1])};
       SB[q] = cf{(float)(0.5 * cr[e + 2]), (float)(0.5 * cr[e + 3])};
-      const f4a m = *reinterpret_cast<const f4a*>(mp + e);
-      lA[q] = cf{2.0f * m.x, 2.0f * m.y};
-      lB[q] = cf{2.0f * m.z, 2.0f * m.w};
+      if constexpr (MODE == BW_FULL) {
+        const f4a m = *reinterpret_cast<const f4a*>(mp + e);
+        lA[q] = cf{2.0f * m.x, 2.0f * m.y};
+        lB[q] = cf{2.0f * m.z, 2.0f * m.w};
+      }
     });
   }
   // parameter-gradient accumulators (sums of h_t times coefficient cotangents)
@@ -1335,7 +1354,8 @@ __global__ __launch_bounds__(64) void k_bwd_full(DiagArgs a) {
         dv.x += acc.x + acc.z;
         dv.y += acc.y + acc.w;
         *reinterpret_cast<float2*>(dvo_g + s * DIM + 2 * k) = dv;
-        if (t == 0 || t == Tc - 1)  // boundary intervals: their knots are finished by k_knot_bounds
+        // boundary intervals: their knots are finished by k_knot_bounds; the local adjoint keeps every step's dv
+        if (MODE == BW_LOCAL || t == 0 || t == Tc - 1)
           *reinterpret_cast<float2*>(a.dv + ((size_t)b * a.n_int + t0 + t) * DIM + 2 * k) = dv;
       }
     }
@@ -1352,6 +1372,7 @@ __global__ __launch_bounds__(64) void k_bwd_full(DiagArgs a) {
       }
     }
     __syncthreads();
+    if constexpr (MODE == BW_LOCAL) continue;  // the knots are written by k_bwd_carry
     // interior knots tb+1 .. tb+NB of the chunk: dX = dv(t-1) - dv(t), dtheta = dh(t-1) - dh(t); row NB of the
     // block arrays holds the step after the block (the first step of the block processed before)
     for (int it = l.gl; it < NB * (DIM + 1); it += G) {
@@ -1375,6 +1396,17 @@ __global__ __launch_bounds__(64) void k_bwd_full(DiagArgs a) {
   // (-Re G, Im G) to its plane for u = -conj(z) and (-Re G, -Im G) for u = -z (the conj(u_k) of the A pairs).
   constexpr int PS = 2 + 2 * KP;  // per-lane floats: row part, then one (d, w) per column pair
   float* sp = s_w[l.gi];          // reuses the column-sum area
+  if constexpr (MODE == BW_LOCAL) {  // mu: the cotangent on the chunk's carry-in state (halved pair cotangents)
+    if (active) {
+      float* mp = a.mu + ((size_t)b * a.C + c) * a.D;
+      if (l.kg == 0) *reinterpret_cast<float2*>(mp + 2 * l.j) = float2{l1.re, l1.im};
+      static_for<0, KP>([&](auto qc) {
+        constexpr int q = qc;
+        *reinterpret_cast<f4a*>(mp + DIM + 4 * (l.j * K + KP * l.kg + q)) =
+            f4a{0.5f * lA[q].re, 0.5f * lA[q].im, 0.5f * lB[q].re, 0.5f * lB[q].im};
+      });
+    }
+  }
   if (active) {
     float rd = 0.0f, rw = 0.0f;
     cf Gx{0.0f, 0.0f};
@@ -1434,6 +1466,340 @@ __global__ __launch_bounds__(64) void k_bwd_full(DiagArgs a) {
   }
 }
 
+// ------------------------------------------------------------------------------------------------ carry adjoint
+// The part of an invertible uniform chunk's adjoint that the cotangent of the later chunks (mt, the cotangent on
+// the chunk's end state) drives, in closed form; k_bwd_full<.., BW_LOCAL> has added the part of the chunk's own
+// readout rows. Linear in that cotangent, with the chunk's coefficients constant, every term is a fixed K x K
+// matrix applied to per-step vectors. Let n_t = span of the steps after t to the chunk end (clock theta_end -
+// theta_{t+1}), a_{t,j} = conj(exp(u_j n_t)) (the adjoint flow of plane j from the chunk end back to step t),
+// pi_{t,j} = p_{t,j} conj(a_{t,j}), sigma = (phi/2) pi, gamma_{t,j} = c_{t,j} conj(a_{t,j}) with c = rho S1(t-1) the
+// level-1 state; lamB, lamA (doubled) and lam1 the end cotangents, GB = conj(IB/2) lamB, GA = conj(IA/2) lamA. Then
+//   level-2 cotangents  B_t = a_j a_k lamB,  A_t = a_j conj(a_k) lamA
+//   RC_t[j] = sum_k conj(sigma_k) lamB[j,k] + sigma_k lamA[j,k],   RP_t[j] = sum_k conj(pi_k) GB + pi_k GA
+//   CS_t[k] = conj(phi_k/2) sum_j (conj(gamma_j) lamB + conj(lamA) gamma_j) + sum_j (conj(pi_j) GB + conj(GA) pi_j)
+//   level-1 cotangent   l1_t = a_j (lam1 + sum_{s>t} RC_s[j])   (the flows telescope)
+//   dv_t (plane m)      = a_m (conj(phi_m) (lam1 + sum_{s>t} RC_s) + RP_t[m]) + a_m CS_t[m]
+// and the coefficient cotangents summed with h (the parameter gradients) are outer-product sums over the steps:
+//   kIB = lamB conj(sum h pi_j pi_k), kIA = lamA conj(sum h pi_j conj(pi_k)),
+//   kph = lamB conj(sum h gamma_j pi_k) + conj(lamA) sum h gamma_j conj(pi_k),
+//   kLB = lamB conj(W_B), W_B = (C2B/2 e^{(u_j+u_k) tau} tau + (phi_k/2) sum n gamma_j pi_k + (IB/2) sum n pi_j pi_k) / LB
+//   (kLA alike with conj(u_k), conj(phi_k/2), conj(pi_k)), kphj = sum h conj(pi_j) (lam1 + sum_{s>t} RC_s),
+//   krho = sum h conj(S1(t-1)) a_j (lam1 + sum_{s>=t} RC_s);
+// C2 / 2 is the halved level-2 carry-in state and tau the chunk's clock span. One wavefront per chunk: lane = step
+// for the per-step vectors and matvecs, lane = pair (j, k) for the outer-product sums. Writes the chunk's total
+// dv (local part + this), its interior knot gradients and adds its parameter partials to the local ones.
+struct PairCoefs {
+  cf rho_j, phi_j, dphi_j, phk_k, dphi_k, IB, IA, LB, LA, DxB, DyB, DxA, DyA;
+};
+__device__ __forceinline__ PairCoefs pair_coefs(const DiagArgs& a, int j, int k, float hb, bool use_tab) {
+  PairCoefs o;
+  if (use_tab) {
+    const float* tab = a.ctab;
+    const float dlt = hb - tab[0];
+    o.rho_j = tflow(tp(tab, j, TP_RHO), tp(tab, j, TP_RHO1), dlt);
+    o.phi_j = tp(tab, j, TP_PHI);
+    o.dphi_j = tp(tab, j, TP_DPHI);
+    o.phk_k = tp(tab, k, TP_PHIH);
+    o.dphi_k = tp(tab, k, TP_DPHI);
+    o.IB = tq(tab, j, k, TQ_IB);
+    o.IA = tq(tab, j, k, TQ_IA);
+    o.LB = tflow(tq(tab, j, k, TQ_LB), tq(tab, j, k, TQ_LB1), dlt);
+    o.LA = tflow(tq(tab, j, k, TQ_LA), tq(tab, j, k, TQ_LA1), dlt);
+    o.DxB = tq(tab, j, k, TQ_DXB);
+    o.DyB = tq(tab, j, k, TQ_DYB);
+    o.DxA = tq(tab, j, k, TQ_DXA);
+    o.DyA = tq(tab, j, k, TQ_DYA);
+    return o;
+  }
+  const cf uj = load_u(a.params, j), uk = load_u(a.params, k);
+  const cf xj = hb * uj;
+  const Node1<cf> nj = node1(xj), nk = node1(hb * uk);
+  o.rho_j = nj.e;
+  o.phi_j = nj.p;
+  o.dphi_j = nj.dp;
+  o.phk_k = 0.5f * nk.p;
+  o.dphi_k = nk.dp;
+  const cf ub = uj + uk, ua = uj + conj(uk);
+  o.LB = expv(hb * ub);
+  o.LA = expv(hb * ua);
+  const DD3<cf> db = dd3<cf, true>(xj, hb * ub);
+  const DD3<cf> da = dd3<cf, true>(xj, hb * ua);
+  o.IB = 0.5f * db.d;
+  o.IA = 0.5f * da.d;
+  o.DxB = db.dx;
+  o.DyB = db.dy;
+  o.DxA = da.dx;
+  o.DyA = da.dy;
+  return o;
+}
+// sum_k conj(x_k) M1 + x_k M2 from m = (M1r + M2r, M1i - M2i, M1i + M2i, M2r - M1r)
+__device__ __forceinline__ void acc_row(cf& r, cf x, f4a m) {
+  r.re = fmaf(x.re, m.x, fmaf(x.im, m.y, r.re));
+  r.im = fmaf(x.re, m.z, fmaf(x.im, m.w, r.im));
+}
+// sum_j conj(y_j) M1 + conj(M2) y_j from m = (M1r + M2r, M1i + M2i, M1i - M2i, M2r - M1r)
+__device__ __forceinline__ void acc_col(cf& r, cf y, f4a m) { acc_row(r, y, m); }
+// the 16 channels of knot row idx of sample b
+template <bool BF16> __device__ __forceinline__ void load_knot(const DiagArgs& a, int b, int idx, float* x) {
+  if constexpr (!BF16) {
+    const f4a* r = reinterpret_cast<const f4a*>(reinterpret_cast<const float*>(a.path) + ((size_t)b * a.L + idx) * DIM);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const f4a v = r[i];
+      x[4 * i] = v.x;
+      x[4 * i + 1] = v.y;
+      x[4 * i + 2] = v.z;
+      x[4 * i + 3] = v.w;
+    }
+  } else {
+    const f4a* r = reinterpret_cast<const f4a*>(reinterpret_cast<const unsigned short*>(a.path) +
+                                                ((size_t)b * a.L + idx) * DIM);
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const f4a w = r[i];
+      const float e[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        x[8 * i + 2 * q] = bf_lo(e[q]);
+        x[8 * i + 2 * q + 1] = bf_hi(e[q]);
+      }
+    }
+  }
+}
+
+// wave-wide scans on DPP: row shifts inside rows of 16 lanes, then the row broadcasts of lanes 15 and 31
+template <int CTRL, int ROWS> __device__ __forceinline__ float dpp0(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, ROWS, 0xf, true));
+}
+__device__ __forceinline__ float wave_prefix(float v) {  // inclusive prefix sum over the 64 lanes
+  v += dpp0<0x111, 0xf>(v);  // row_shr:1
+  v += dpp0<0x112, 0xf>(v);  // row_shr:2
+  v += dpp0<0x114, 0xf>(v);  // row_shr:4
+  v += dpp0<0x118, 0xf>(v);  // row_shr:8
+  v += dpp0<0x142, 0xa>(v);  // row_bcast:15 into rows 1 and 3
+  v += dpp0<0x143, 0xc>(v);  // row_bcast:31 into rows 2 and 3
+  return v;
+}
+__device__ __forceinline__ float lane63(float v) { return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63)); }
+__device__ __forceinline__ float from_prev_lane(float v) { return dpp0<0x138, 0xf>(v); }  // wave_shr:1, lane 0 gets 0
+
+template <bool BF16>
+__global__ __launch_bounds__(64) void k_bwd_carry(DiagArgs a) {
+  __shared__ __align__(16) f4a s_mr[K][K], s_gr[K][K], s_mc[K][K], s_gc[K][K];
+  __shared__ __align__(16) float2 s_pi[kMaxT][K], s_ga[kMaxT][K], s_fl[kMaxT][K], s_wh[kMaxT];
+  __shared__ __align__(16) float2 s_pl[K][6];  // per plane: rho, phi, phi/2, lam1, e^{u tau} C1, 1/rho
+  __shared__ __align__(16) f4a s_part[64];
+  const int l = threadIdx.x, c = blockIdx.x, b = blockIdx.y;
+  const int jj = l >> 3, kk = l & 7;
+  // adjoint carry inside the quad (float64, lane = 8 j + k): the cotangent on this chunk's end state, down from the
+  // quad's last chunk (written by the adjoint scan); written back for every later kernel that reads mt
+  const int c_last = min(4 * (c / 4) + 3, a.C - 1);
+  PairSt X = load_st_f(a.mt + ((size_t)b * a.C + c_last) * a.D, jj, kk);
+  for (int cc = c_last - 1; cc >= c; --cc) {
+    const double* cfl = a.cflow + ((size_t)b * a.C + cc + 1) * K * 2;
+    const dc Fk = ld_dd(cfl + 2 * kk);
+    adj_d(X, ld_dd(cfl + 2 * jj), Fk, l1_inc(a, b, cc + 1, cc + 2, kk, Fk));
+    add_st(X, load_st_f(a.mu + ((size_t)b * a.C + cc + 1) * a.D, jj, kk));
+  }
+  if (c < c_last) store_st_f(a.mt + ((size_t)b * a.C + c) * a.D, jj, kk, X);
+  const int flag = a.cflag[b * a.C + c];
+  if ((flag & 3) != 3) return;  // the chunk is not a pair-group chunk with invertible steps (generic kernels)
+  const int t0 = c * a.T, Tc = min(a.T, a.n_int - t0);
+  const float* th = a.clock + (size_t)b * a.L + t0;
+  const float th_end = th[Tc], tau = th_end - th[0];
+  const PairCoefs pc = pair_coefs(a, jj, kk, a.chbar[b * a.C + c], (flag & 4) != 0);
+  const double* cr0 = a.carries + ((size_t)b * (a.C + 1) + c) * a.D;  // carry-in state
+  {
+    const cf lB{(float)(2.0 * X.SB.re), (float)(2.0 * X.SB.im)}, lA{(float)(2.0 * X.SA.re), (float)(2.0 * X.SA.im)};
+    const cf GB = cjm(pc.IB, lB), GA = cjm(pc.IA, lA);
+    s_mr[jj][kk] = f4a{lB.re + lA.re, lB.im - lA.im, lB.im + lA.im, lA.re - lB.re};
+    s_gr[jj][kk] = f4a{GB.re + GA.re, GB.im - GA.im, GB.im + GA.im, GA.re - GB.re};
+    s_mc[jj][kk] = f4a{lB.re + lA.re, lB.im + lA.im, lB.im - lA.im, lA.re - lB.re};
+    s_gc[jj][kk] = f4a{GB.re + GA.re, GB.im + GA.im, GB.im - GA.im, GA.re - GB.re};
+    if (kk == 0) {
+      const cf E = expv(tau * load_u(a.params, jj)) * cf{(float)cr0[2 * jj], (float)cr0[2 * jj + 1]};
+      const cf ri = cf{1.0f, 0.0f} / pc.rho_j;
+      s_pl[jj][0] = float2{pc.rho_j.re, pc.rho_j.im};
+      s_pl[jj][1] = float2{pc.phi_j.re, pc.phi_j.im};
+      s_pl[jj][3] = float2{(float)X.S1.re, (float)X.S1.im};
+      s_pl[jj][4] = float2{E.re, E.im};
+      s_pl[jj][5] = float2{ri.re, ri.im};
+    }
+    if (jj == 0) s_pl[kk][2] = float2{pc.phk_k.re, pc.phk_k.im};
+  }
+  // ---- lane = step t
+  const int t = l;
+  const bool live = t < Tc;
+  float h = 0.0f, hs = 0.0f;
+  cf pi[K], fl[K];  // fl = e^{u n_t} = conj(a_t): plane flows over the clock span after step t
+  {
+    float x0[DIM], x1[DIM];
+#pragma unroll
+    for (int i = 0; i < DIM; ++i) x0[i] = x1[i] = 0.0f;
+    if (live) {
+      h = th[t + 1] - th[t];
+      hs = th_end - th[t + 1];
+      load_knot<BF16>(a, b, t0 + t, x0);
+      load_knot<BF16>(a, b, t0 + t + 1, x1);
+    }
+#pragma unroll
+    for (int j = 0; j < K; ++j) {
+      // pi = p conj(a): p times the plane flow over the clock span after step t
+      fl[j] = live ? expv(hs * load_u(a.params, j)) : cf{0.0f, 0.0f};
+      pi[j] = cf{x1[2 * j] - x0[2 * j], x1[2 * j + 1] - x0[2 * j + 1]} * fl[j];
+    }
+  }
+  __syncthreads();
+  // gamma_t = c_t conj(a_t) = e^{u tau} C1 + phi sum_{s<t} pi_s (the flows telescope); a_t itself is recovered as
+  // conj(e^{u n_t}) where needed
+  cf ga[K];
+#pragma unroll
+  for (int j = 0; j < K; ++j) {
+    const float2 f = s_pl[j][1], e = s_pl[j][4];
+    const cf ex{wave_prefix(pi[j].re) - pi[j].re, wave_prefix(pi[j].im) - pi[j].im};
+    ga[j] = live ? fma_c(cf{f.x, f.y}, ex, cf{e.x, e.y}) : cf{0.0f, 0.0f};
+    s_pi[t][j] = float2{pi[j].re, pi[j].im};
+    s_ga[t][j] = float2{ga[j].re, ga[j].im};
+    s_fl[t][j] = float2{fl[j].re, fl[j].im};
+  }
+  s_wh[t] = float2{h, hs};
+  // per-step matvecs with the end cotangents: rows (plane j: the level-1 cotangent and the plane part of dv)
+  cf sg[K];
+#pragma unroll
+  for (int k = 0; k < K; ++k) {
+    const float2 hk = s_pl[k][2];
+    sg[k] = cf{hk.x, hk.y} * pi[k];
+  }
+  float dvt[DIM];
+  cf kphj_p{0.0f, 0.0f}, krho_p{0.0f, 0.0f};  // plane kk's sums (lanes kk < K use them)
+  // the plane loops stay rolled (their per-plane values come from LDS), so that the matrix rows are not all
+  // loaded into registers at once
+#pragma unroll 1
+  for (int j = 0; j < K; ++j) {
+    cf RC{0.0f, 0.0f}, RP{0.0f, 0.0f};
+#pragma unroll
+    for (int k = 0; k < K; ++k) {
+      acc_row(RC, sg[k], s_mr[j][k]);
+      acc_row(RP, pi[k], s_gr[j][k]);
+    }
+    // sums of RC over the steps after t (excl) and from t on (incl): the total minus the inclusive prefix
+    const float pr = wave_prefix(RC.re), pim = wave_prefix(RC.im);
+    const cf excl{lane63(pr) - pr, lane63(pim) - pim};
+    const cf incl = excl + RC;
+    const float2 f = s_pl[j][1], l1e = s_pl[j][3], ri = s_pl[j][5];
+    const float2 flj = s_fl[t][j], pij = s_pi[t][j], gaj = s_ga[t][j];
+    const cf lam1{l1e.x, l1e.y};
+    const cf ex = lam1 + excl;
+    const cf dvp = conj(cf{flj.x, flj.y}) * fma_c(conj(cf{f.x, f.y}), ex, RP);
+    s_fl[t][j] = float2{dvp.re, dvp.im};  // the lane's own slot: now the plane part of dv
+    // kphj += h conj(pi) (lam1 + excl); krho += h conj(S1(t-1)) a (lam1 + incl), S1(t-1) conj(a) = gamma / rho
+    const cf q1 = h * cjm(cf{pij.x, pij.y}, ex);
+    const cf q2 = h * cjm(cf{gaj.x, gaj.y} * cf{ri.x, ri.y}, lam1 + incl);
+    const cf s1{lane63(wave_prefix(q1.re)), lane63(wave_prefix(q1.im))};
+    const cf s2{lane63(wave_prefix(q2.re)), lane63(wave_prefix(q2.im))};
+    if (j == kk) {
+      kphj_p = s1;
+      krho_p = s2;
+    }
+  }
+  // columns (plane k: the later factor's part of dv)
+  {
+    cf CA[K], CB[K];
+#pragma unroll
+    for (int k = 0; k < K; ++k) CA[k] = CB[k] = cf{0.0f, 0.0f};
+#pragma unroll 1
+    for (int j = 0; j < K; ++j) {
+      const float2 gaj = s_ga[t][j], pij = s_pi[t][j];
+#pragma unroll
+      for (int k = 0; k < K; ++k) {
+        acc_col(CA[k], cf{gaj.x, gaj.y}, s_mc[j][k]);
+        acc_col(CB[k], cf{pij.x, pij.y}, s_gc[j][k]);
+      }
+    }
+#pragma unroll
+    for (int k = 0; k < K; ++k) {
+      const float2 hk = s_pl[k][2], dvp = s_fl[t][k];
+      const cf col = conj(fl[k]) * fma_c(conj(cf{hk.x, hk.y}), CA[k], CB[k]);
+      dvt[2 * k] = dvp.x + col.re;
+      dvt[2 * k + 1] = dvp.y + col.im;
+    }
+  }
+  if (live) {
+    float* dvr = a.dv + ((size_t)b * a.n_int + t0 + t) * DIM;
+#pragma unroll
+    for (int i = 0; i < DIM; i += 4) {
+      const f4a loc = *reinterpret_cast<const f4a*>(dvr + i);
+      dvt[i] += loc.x;
+      dvt[i + 1] += loc.y;
+      dvt[i + 2] += loc.z;
+      dvt[i + 3] += loc.w;
+      *reinterpret_cast<f4a*>(dvr + i) = f4a{dvt[i], dvt[i + 1], dvt[i + 2], dvt[i + 3]};
+    }
+  }
+  // interior knots t0 + 1 .. t0 + Tc - 1: dX_t = dv(t-1) - dv(t); the boundary knots are finished by k_knot_grads
+  {
+    float dk[DIM];
+#pragma unroll
+    for (int i = 0; i < DIM; ++i) dk[i] = from_prev_lane(dvt[i]) - dvt[i];
+    if (live && t >= 1) {
+      float* kr = a.dpath + ((size_t)b * a.L + t0 + t) * DIM;
+#pragma unroll
+      for (int i = 0; i < DIM; i += 4) *reinterpret_cast<f4a*>(kr + i) = f4a{dk[i], dk[i + 1], dk[i + 2], dk[i + 3]};
+    }
+  }
+  __syncthreads();
+  // ---- lane = pair (jj, kk): outer-product sums over the steps
+  float ph[4] = {0.0f, 0.0f, 0.0f, 0.0f}, ps[4] = {0.0f, 0.0f, 0.0f, 0.0f};  // pi_j x (h | n) pi_k
+  float gh[4] = {0.0f, 0.0f, 0.0f, 0.0f}, gs[4] = {0.0f, 0.0f, 0.0f, 0.0f};  // gamma_j x (h | n) pi_k
+#pragma unroll 4
+  for (int s = 0; s < Tc; ++s) {
+    const float2 xj = s_pi[s][jj], yk = s_pi[s][kk], gj = s_ga[s][jj], w = s_wh[s];
+    const float hyr = w.x * yk.x, hyi = w.x * yk.y, syr = w.y * yk.x, syi = w.y * yk.y;
+    ph[0] = fmaf(xj.x, hyr, ph[0]); ph[1] = fmaf(xj.y, hyi, ph[1]); ph[2] = fmaf(xj.x, hyi, ph[2]); ph[3] = fmaf(xj.y, hyr, ph[3]);
+    ps[0] = fmaf(xj.x, syr, ps[0]); ps[1] = fmaf(xj.y, syi, ps[1]); ps[2] = fmaf(xj.x, syi, ps[2]); ps[3] = fmaf(xj.y, syr, ps[3]);
+    gh[0] = fmaf(gj.x, hyr, gh[0]); gh[1] = fmaf(gj.y, hyi, gh[1]); gh[2] = fmaf(gj.x, hyi, gh[2]); gh[3] = fmaf(gj.y, hyr, gh[3]);
+    gs[0] = fmaf(gj.x, syr, gs[0]); gs[1] = fmaf(gj.y, syi, gs[1]); gs[2] = fmaf(gj.x, syi, gs[2]); gs[3] = fmaf(gj.y, syr, gs[3]);
+  }
+  // x y = (rr - ii, ri + ir), x conj(y) = (rr + ii, ir - ri)
+  const cf Psi1{ph[0] - ph[1], ph[2] + ph[3]}, Psi2{ph[0] + ph[1], ph[3] - ph[2]};
+  const cf Psi3{gh[0] - gh[1], gh[2] + gh[3]}, Psi4{gh[0] + gh[1], gh[3] - gh[2]};
+  const cf Q1{ps[0] - ps[1], ps[2] + ps[3]}, Q2{ps[0] + ps[1], ps[3] - ps[2]};
+  const cf Q3{gs[0] - gs[1], gs[2] + gs[3]}, Q4{gs[0] + gs[1], gs[3] - gs[2]};
+  const cf lB{(float)(2.0 * X.SB.re), (float)(2.0 * X.SB.im)}, lA{(float)(2.0 * X.SA.re), (float)(2.0 * X.SA.im)};
+  const cf kIB = lB * conj(Psi1), kIA = lA * conj(Psi2);
+  const cf kph = lB * conj(Psi3) + conj(lA) * Psi4;
+  const double* cr = cr0 + DIM + 4 * (8 * jj + kk);
+  const cf C2Ah{(float)(0.5 * cr[0]), (float)(0.5 * cr[1])}, C2Bh{(float)(0.5 * cr[2]), (float)(0.5 * cr[3])};
+  const cf uj = load_u(a.params, jj), uk = load_u(a.params, kk);
+  const cf WB = (tau * (C2Bh * expv(tau * (uj + uk))) + pc.phk_k * Q3 + pc.IB * Q1) / pc.LB;
+  const cf WA = (tau * (C2Ah * expv(tau * (uj + conj(uk)))) + conj(pc.phk_k) * Q4 + pc.IA * Q2) / pc.LA;
+  const cf kLB = lB * conj(WB), kLA = lA * conj(WA);
+  // coefficient cotangents -> parameter partials (d_j, w_j), as k_bwd_full: a node h u contributes (-Re G, Im G)
+  // for u = -conj(z) and (-Re G, -Im G) for u = -z (the conj(u_k) of the A pairs)
+  const cf Gx = 0.5f * (kIB * conj(pc.DxB) + kIA * conj(pc.DxA));
+  const cf GyB = 0.5f * (kIB * conj(pc.DyB)) + kLB * conj(pc.LB);
+  const cf GyA = 0.5f * (kIA * conj(pc.DyA)) + kLA * conj(pc.LA);
+  const cf Gk = 0.5f * (kph * conj(pc.dphi_k));
+  s_part[l] = f4a{-GyB.re - GyA.re - Gx.re, GyB.im + GyA.im + Gx.im, -GyB.re - GyA.re - Gk.re, GyB.im - GyA.im + Gk.im};
+  __syncthreads();
+  if (l < K) {
+    const int pl = l;  // plane: rows (pl, k) and columns (j, pl)
+    float sd = 0.0f, sw = 0.0f;
+    for (int q = 0; q < K; ++q) {
+      const f4a r = s_part[8 * pl + q], cl = s_part[8 * q + pl];
+      sd += r.x + cl.z;
+      sw += r.y + cl.w;
+    }
+    const float2 r = s_pl[pl][0];
+    const cf Gp = krho_p * conj(cf{r.x, r.y}) + kphj_p * conj(pc.dphi_k);  // lane pl: jj = 0, kk = pl
+    sd -= Gp.re;
+    sw += Gp.im;
+    float* gpo = a.gp + ((size_t)b * a.C + c) * a.npar;
+    gpo[2 * pl] += sd;
+    gpo[2 * pl + 1] += sw;
+  }
+}
+
 }  // namespace pairs
 
 // ------------------------------------------------------------------------------------------------ host side
@@ -1478,22 +1844,37 @@ int pairs_carry_scan(const DiagArgs& a, hipStream_t st, bool backward) {
   return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 
+// Without the clock gradient (dclock null) an invertible uniform chunk's adjoint is split by linearity: the full
+// per-step adjoint of its own rows (pass 0, k_bwd_full<.., BW_LOCAL>, which reads the cotangent rows once) and the
+// closed-form part of the later chunks' cotangent (pass 2, k_bwd_carry). With the clock gradient, pass 0 computes
+// mu only and pass 2 runs the full adjoint (k_bwd_full<.., BW_FULL>), reading the rows again.
 int pairs_backward(const DiagArgs& a, hipStream_t st, bool full) {
+  const bool split = a.dclock == nullptr;
   if (full) {
-    constexpr int GPW = pairs::Geo<2>::GPW;
-    const dim3 grid((a.C + GPW - 1) / GPW, a.B), blk(64);
-    if (a.dclock) {
-      if (a.path_bf16) hipLaunchKernelGGL((pairs::k_bwd_full<true, true>), grid, blk, 0, st, a);
-      else hipLaunchKernelGGL((pairs::k_bwd_full<false, true>), grid, blk, 0, st, a);
+    if (split) {
+      if (a.path_bf16) hipLaunchKernelGGL((pairs::k_bwd_carry<true>), dim3(a.C, a.B), dim3(64), 0, st, a);
+      else hipLaunchKernelGGL((pairs::k_bwd_carry<false>), dim3(a.C, a.B), dim3(64), 0, st, a);
     } else {
-      if (a.path_bf16) hipLaunchKernelGGL((pairs::k_bwd_full<true, false>), grid, blk, 0, st, a);
-      else hipLaunchKernelGGL((pairs::k_bwd_full<false, false>), grid, blk, 0, st, a);
+      constexpr int GPW = pairs::Geo<2>::GPW;
+      const dim3 grid((a.C + GPW - 1) / GPW, a.B), blk(64);
+      if (a.path_bf16) hipLaunchKernelGGL((pairs::k_bwd_full<true, true, pairs::BW_FULL>), grid, blk, 0, st, a);
+      else hipLaunchKernelGGL((pairs::k_bwd_full<false, true, pairs::BW_FULL>), grid, blk, 0, st, a);
     }
   } else {
     constexpr int GPW = pairs::Geo<4>::GPW;
     const dim3 grid((a.C + GPW - 1) / GPW, a.B), blk(64);
-    if (a.path_bf16) hipLaunchKernelGGL((pairs::k_bwd_local<true>), grid, blk, 0, st, a);
-    else hipLaunchKernelGGL((pairs::k_bwd_local<false>), grid, blk, 0, st, a);
+    if (split) {
+      if (a.path_bf16) hipLaunchKernelGGL((pairs::k_bwd_local<true, true>), grid, blk, 0, st, a);
+      else hipLaunchKernelGGL((pairs::k_bwd_local<false, true>), grid, blk, 0, st, a);
+      if (hipGetLastError() != hipSuccess) return -1;
+      constexpr int GPW2 = pairs::Geo<2>::GPW;
+      const dim3 grid2((a.C + GPW2 - 1) / GPW2, a.B);
+      if (a.path_bf16) hipLaunchKernelGGL((pairs::k_bwd_full<true, false, pairs::BW_LOCAL>), grid2, blk, 0, st, a);
+      else hipLaunchKernelGGL((pairs::k_bwd_full<false, false, pairs::BW_LOCAL>), grid2, blk, 0, st, a);
+    } else {
+      if (a.path_bf16) hipLaunchKernelGGL((pairs::k_bwd_local<true, false>), grid, blk, 0, st, a);
+      else hipLaunchKernelGGL((pairs::k_bwd_local<false, false>), grid, blk, 0, st, a);
+    }
   }
   return hipGetLastError() == hipSuccess ? 0 : -1;
 }

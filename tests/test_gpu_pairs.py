@@ -104,9 +104,13 @@ def _check(path, clock, dw, bf16=False, seed=7):
     rdp, rdc, rdd = C.planes_backward(src.astype(np.float64), clock.astype(np.float64), dw.astype(np.float64),
                                       g.astype(np.float64), kind="f64")
     errs = dict(fwd=relerr(out, ref), dpath=relerr(dp, rdp), dclock=relerr(dc, rdc), dparams=relerr(dd, rdd))
+    # without the clock gradient the invertible chunks take the split adjoint (local adjoint + closed-form carry)
+    _, dp2, _, dd2, _ = _run(path, clock, dw, g, bf16, clock_grad=False)
+    errs.update(dpath_split=relerr(dp2, rdp), dparams_split=relerr(dd2, rdd))
     print(f"B={B} L={L} bf16={bf16} flags={np.bincount(flags.ravel(), minlength=8).tolist()} errs={errs}", flush=True)
     assert errs["fwd"] < 1e-5, errs
     assert errs["dpath"] < 1e-4 and errs["dclock"] < 1e-4 and errs["dparams"] < 1e-4, errs
+    assert errs["dpath_split"] < 1e-4 and errs["dparams_split"] < 1e-4, errs
     return flags
 
 
