@@ -1583,39 +1583,127 @@ __device__ __forceinline__ float wave_prefix(float v) {  // inclusive prefix sum
 __device__ __forceinline__ float lane63(float v) { return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63)); }
 __device__ __forceinline__ float from_prev_lane(float v) { return dpp0<0x138, 0xf>(v); }  // wave_shr:1, lane 0 gets 0
 
+typedef float f4m __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ f4m mfma4(float a, float b, f4m c) { return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0); }
+// out (64 x 16) = in (64 x 16) M^T for a real 16 x 16 matrix given as its B-operand registers bm[ks] (lane l: M[l % 16]
+// [4 ks + l / 16]): four row tiles of 16 steps, four 16x16x4 MFMAs each; the result goes to LDS, row-major.
+constexpr int SP = DIM + 2;  // LDS row pitch of the per-step arrays: 16 lanes of a column hit distinct banks
+__device__ __forceinline__ void mfma_rows(const float (*in)[SP], const float* bm, float (*out)[SP], int l) {
+  const int li = l & 15, lk = l >> 4;
+#pragma unroll
+  for (int tt = 0; tt < 4; ++tt) {
+    f4m acc = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) acc = mfma4(in[16 * tt + li][4 * ks + lk], bm[ks], acc);
+#pragma unroll
+    for (int r = 0; r < 4; ++r) out[16 * tt + 4 * lk + r][li] = acc[r];
+  }
+}
+
+// the same with in = sigma = (phi_k / 2) pi_k formed while loading the operand (phk: s_pl[.][2])
+__device__ __forceinline__ void mfma_rows_sigma(const float (*pi)[SP], const float2 (*pl)[6], const float* bm,
+                                                float (*out)[SP], int l) {
+  const int li = l & 15, lk = l >> 4;
+#pragma unroll
+  for (int tt = 0; tt < 4; ++tt) {
+    f4m acc = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) {
+      const int q = 4 * ks + lk, kq = q >> 1;
+      const float2 x = *reinterpret_cast<const float2*>(&pi[16 * tt + li][2 * kq]);
+      const float2 hk = pl[kq][2];
+      const float sv = (q & 1) ? fmaf(hk.x, x.y, hk.y * x.x) : fmaf(hk.x, x.x, -hk.y * x.y);
+      acc = mfma4(sv, bm[ks], acc);
+    }
+#pragma unroll
+    for (int r = 0; r < 4; ++r) out[16 * tt + 4 * lk + r][li] = acc[r];
+  }
+}
+
+// e^x by the hardware exponential, sine and cosine while |Im x| <= 16 (their absolute error stays near 1e-6 of
+// |e^x| there), else the accurate library path
+__device__ __forceinline__ cf expv_fast(cf x) {
+  if (fabsf(x.im) > 16.0f) return expv(x);
+  const float m = __expf(x.re);
+  return cf{m * __cosf(x.im), m * __sinf(x.im)};
+}
+
 template <bool BF16>
 __global__ __launch_bounds__(64) void k_bwd_carry(DiagArgs a) {
-  __shared__ __align__(16) f4a s_mr[K][K], s_gr[K][K], s_mc[K][K], s_gc[K][K];
-  __shared__ __align__(16) float2 s_pi[kMaxT][K], s_ga[kMaxT][K], s_fl[kMaxT][K], s_wh[kMaxT];
+  __shared__ __align__(16) float s_pi[kMaxT][SP], s_ga[kMaxT][SP];  // per step: pi, gamma
+  __shared__ __align__(16) float s_o[kMaxT][SP];                    // matrices, then each MFMA result in turn
+  __shared__ __align__(16) float2 s_wh[kMaxT];
   __shared__ __align__(16) float2 s_pl[K][6];  // per plane: rho, phi, phi/2, lam1, e^{u tau} C1, 1/rho
-  __shared__ __align__(16) f4a s_part[64];
+  f4a(*s_mat)[K][K] = reinterpret_cast<f4a(*)[K][K]>(&s_o[0][0]);  // s_mr, s_gr, s_mc, s_gc: 4 KB
   const int l = threadIdx.x, c = blockIdx.x, b = blockIdx.y;
   const int jj = l >> 3, kk = l & 7;
-  // adjoint carry inside the quad (float64, lane = 8 j + k): the cotangent on this chunk's end state, down from the
-  // quad's last chunk (written by the adjoint scan); written back for every later kernel that reads mt
-  const int c_last = min(4 * (c / 4) + 3, a.C - 1);
-  PairSt X = load_st_f(a.mt + ((size_t)b * a.C + c_last) * a.D, jj, kk);
-  for (int cc = c_last - 1; cc >= c; --cc) {
-    const double* cfl = a.cflow + ((size_t)b * a.C + cc + 1) * K * 2;
-    const dc Fk = ld_dd(cfl + 2 * kk);
-    adj_d(X, ld_dd(cfl + 2 * jj), Fk, l1_inc(a, b, cc + 1, cc + 2, kk, Fk));
-    add_st(X, load_st_f(a.mu + ((size_t)b * a.C + cc + 1) * a.D, jj, kk));
-  }
-  if (c < c_last) store_st_f(a.mt + ((size_t)b * a.C + c) * a.D, jj, kk, X);
   const int flag = a.cflag[b * a.C + c];
-  if ((flag & 3) != 3) return;  // the chunk is not a pair-group chunk with invertible steps (generic kernels)
+  const bool owned = (flag & 3) == 3;  // a pair-group chunk with invertible steps (else the generic kernels)
   const int t0 = c * a.T, Tc = min(a.T, a.n_int - t0);
   const float* th = a.clock + (size_t)b * a.L + t0;
-  const float th_end = th[Tc], tau = th_end - th[0];
+  // ---- lane = step t: this step's inputs and local dv, loaded before the carry chain below
+  const int t = l;
+  const bool live = owned && t < Tc;
+  float h = 0.0f, hs = 0.0f, th_end = 0.0f, tau = 0.0f;
+  float x0[DIM], x1[DIM], dvl[DIM];
+#pragma unroll
+  for (int i = 0; i < DIM; ++i) x0[i] = x1[i] = dvl[i] = 0.0f;
+  if (owned) {
+    th_end = th[Tc];
+    tau = th_end - th[0];
+  }
+  if (live) {
+    h = th[t + 1] - th[t];
+    hs = th_end - th[t + 1];
+    load_knot<BF16>(a, b, t0 + t, x0);
+    load_knot<BF16>(a, b, t0 + t + 1, x1);
+    const f4a* dvr = reinterpret_cast<const f4a*>(a.dv + ((size_t)b * a.n_int + t0 + t) * DIM);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const f4a v = dvr[i];
+      dvl[4 * i] = v.x;
+      dvl[4 * i + 1] = v.y;
+      dvl[4 * i + 2] = v.z;
+      dvl[4 * i + 3] = v.w;
+    }
+  }
+  // adjoint carry inside the quad (float64, lane = 8 j + k): the cotangent on this chunk's end state, down from the
+  // quad's last chunk (written by the adjoint scan); written back for every later kernel that reads mt
+  // (every operand of the up to three steps is loaded before the first one: the loads do not depend on the chain)
+  const int c_last = min(4 * (c / 4) + 3, a.C - 1), nstep = c_last - c;
+  PairSt X = load_st_f(a.mt + ((size_t)b * a.C + c_last) * a.D, jj, kk);
+  dc sFj[3], sFk[3], sC0[3], sC1[3];
+  PairSt sMu[3];
+#pragma unroll
+  for (int i = 0; i < 3; ++i) {
+    if (i < nstep) {
+      const int cc = c_last - 1 - i;
+      const double* cfl = a.cflow + ((size_t)b * a.C + cc + 1) * K * 2;
+      sFj[i] = ld_dd(cfl + 2 * jj);
+      sFk[i] = ld_dd(cfl + 2 * kk);
+      sC0[i] = ld_dd(a.carries + ((size_t)b * (a.C + 1) + cc + 1) * a.D + 2 * kk);
+      sC1[i] = ld_dd(a.carries + ((size_t)b * (a.C + 1) + cc + 2) * a.D + 2 * kk);
+      sMu[i] = load_st_f(a.mu + ((size_t)b * a.C + cc + 1) * a.D, jj, kk);
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < 3; ++i) {
+    if (i < nstep) {  // uniform over the wave: the shuffles inside adj_d see every lane
+      adj_d(X, sFj[i], sFk[i], sC1[i] - sFk[i] * sC0[i]);  // level-1 increment carry1(cc+2) - F carry1(cc+1)
+      add_st(X, sMu[i]);
+    }
+  }
+  if (c < c_last) store_st_f(a.mt + ((size_t)b * a.C + c) * a.D, jj, kk, X);
+  if (!owned) return;
   const PairCoefs pc = pair_coefs(a, jj, kk, a.chbar[b * a.C + c], (flag & 4) != 0);
   const double* cr0 = a.carries + ((size_t)b * (a.C + 1) + c) * a.D;  // carry-in state
+  const cf lB{(float)(2.0 * X.SB.re), (float)(2.0 * X.SB.im)}, lA{(float)(2.0 * X.SA.re), (float)(2.0 * X.SA.im)};
   {
-    const cf lB{(float)(2.0 * X.SB.re), (float)(2.0 * X.SB.im)}, lA{(float)(2.0 * X.SA.re), (float)(2.0 * X.SA.im)};
     const cf GB = cjm(pc.IB, lB), GA = cjm(pc.IA, lA);
-    s_mr[jj][kk] = f4a{lB.re + lA.re, lB.im - lA.im, lB.im + lA.im, lA.re - lB.re};
-    s_gr[jj][kk] = f4a{GB.re + GA.re, GB.im - GA.im, GB.im + GA.im, GA.re - GB.re};
-    s_mc[jj][kk] = f4a{lB.re + lA.re, lB.im + lA.im, lB.im - lA.im, lA.re - lB.re};
-    s_gc[jj][kk] = f4a{GB.re + GA.re, GB.im + GA.im, GB.im - GA.im, GA.re - GB.re};
+    s_mat[0][jj][kk] = f4a{lB.re + lA.re, lB.im - lA.im, lB.im + lA.im, lA.re - lB.re};
+    s_mat[1][jj][kk] = f4a{GB.re + GA.re, GB.im - GA.im, GB.im + GA.im, GA.re - GB.re};
+    s_mat[2][jj][kk] = f4a{lB.re + lA.re, lB.im + lA.im, lB.im - lA.im, lA.re - lB.re};
+    s_mat[3][jj][kk] = f4a{GB.re + GA.re, GB.im + GA.im, GB.im - GA.im, GA.re - GB.re};
     if (kk == 0) {
       const cf E = expv(tau * load_u(a.params, jj)) * cf{(float)cr0[2 * jj], (float)cr0[2 * jj + 1]};
       const cf ri = cf{1.0f, 0.0f} / pc.rho_j;
@@ -1627,74 +1715,73 @@ __global__ __launch_bounds__(64) void k_bwd_carry(DiagArgs a) {
     }
     if (jj == 0) s_pl[kk][2] = float2{pc.phk_k.re, pc.phk_k.im};
   }
-  // ---- lane = step t
-  const int t = l;
-  const bool live = t < Tc;
-  float h = 0.0f, hs = 0.0f;
   cf pi[K], fl[K];  // fl = e^{u n_t} = conj(a_t): plane flows over the clock span after step t
-  {
-    float x0[DIM], x1[DIM];
 #pragma unroll
-    for (int i = 0; i < DIM; ++i) x0[i] = x1[i] = 0.0f;
-    if (live) {
-      h = th[t + 1] - th[t];
-      hs = th_end - th[t + 1];
-      load_knot<BF16>(a, b, t0 + t, x0);
-      load_knot<BF16>(a, b, t0 + t + 1, x1);
-    }
-#pragma unroll
-    for (int j = 0; j < K; ++j) {
-      // pi = p conj(a): p times the plane flow over the clock span after step t
-      fl[j] = live ? expv(hs * load_u(a.params, j)) : cf{0.0f, 0.0f};
-      pi[j] = cf{x1[2 * j] - x0[2 * j], x1[2 * j + 1] - x0[2 * j + 1]} * fl[j];
-    }
+  for (int j = 0; j < K; ++j) {
+    // pi = p conj(a): p times the plane flow over the clock span after step t
+    fl[j] = live ? expv_fast(hs * load_u(a.params, j)) : cf{0.0f, 0.0f};
+    pi[j] = cf{x1[2 * j] - x0[2 * j], x1[2 * j + 1] - x0[2 * j + 1]} * fl[j];
   }
   __syncthreads();
-  // gamma_t = c_t conj(a_t) = e^{u tau} C1 + phi sum_{s<t} pi_s (the flows telescope); a_t itself is recovered as
-  // conj(e^{u n_t}) where needed
+  // B operands of the matvec products: lane l holds M[p][q], p = l % 16, q = 4 ks + l / 16. Rows: out_j = sum_k
+  // block(j,k) in_k with block(j,k)[a][b] the (a, b) entry of s_mat[0 | 1][j][k]; columns: out_k = sum_j
+  // block(j,k) in_j with s_mat[2 | 3][j][k].
+  float bmr[4], bgr[4], bmc[4], bgc[4];
+  {
+    const int pp = l & 15;
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) {
+      const int q = 4 * ks + (l >> 4), e = 2 * (pp & 1) + (q & 1);
+      bmr[ks] = reinterpret_cast<const float*>(&s_mat[0][pp >> 1][q >> 1])[e];
+      bgr[ks] = reinterpret_cast<const float*>(&s_mat[1][pp >> 1][q >> 1])[e];
+      bmc[ks] = reinterpret_cast<const float*>(&s_mat[2][q >> 1][pp >> 1])[e];
+      bgc[ks] = reinterpret_cast<const float*>(&s_mat[3][q >> 1][pp >> 1])[e];
+    }
+  }
+  // gamma_t = c_t conj(a_t) = e^{u tau} C1 + phi sum_{s<t} pi_s (the flows telescope)
   cf ga[K];
 #pragma unroll
   for (int j = 0; j < K; ++j) {
     const float2 f = s_pl[j][1], e = s_pl[j][4];
     const cf ex{wave_prefix(pi[j].re) - pi[j].re, wave_prefix(pi[j].im) - pi[j].im};
     ga[j] = live ? fma_c(cf{f.x, f.y}, ex, cf{e.x, e.y}) : cf{0.0f, 0.0f};
-    s_pi[t][j] = float2{pi[j].re, pi[j].im};
-    s_ga[t][j] = float2{ga[j].re, ga[j].im};
-    s_fl[t][j] = float2{fl[j].re, fl[j].im};
+    *reinterpret_cast<float2*>(&s_pi[t][2 * j]) = float2{pi[j].re, pi[j].im};
+    *reinterpret_cast<float2*>(&s_ga[t][2 * j]) = float2{ga[j].re, ga[j].im};
   }
   s_wh[t] = float2{h, hs};
-  // per-step matvecs with the end cotangents: rows (plane j: the level-1 cotangent and the plane part of dv)
-  cf sg[K];
+  __syncthreads();  // the matrices are in registers; s_o is free
+  // rows: RC_t = M_R sigma_t (level-1 cotangent terms), RP_t = G_R pi_t (plane part of dv)
+  float rc[DIM], rp[DIM];
+  mfma_rows_sigma(s_pi, s_pl, bmr, s_o, l);
+  __syncthreads();
 #pragma unroll
-  for (int k = 0; k < K; ++k) {
-    const float2 hk = s_pl[k][2];
-    sg[k] = cf{hk.x, hk.y} * pi[k];
-  }
+  for (int i = 0; i < DIM; ++i) rc[i] = s_o[t][i];
+  __syncthreads();
+  mfma_rows(s_pi, bgr, s_o, l);
+  __syncthreads();
+#pragma unroll
+  for (int i = 0; i < DIM; ++i) rp[i] = s_o[t][i];
+  __syncthreads();
+  // columns: the later factor's part of dv, CA_t = M_C gamma_t, CB_t = G_C pi_t (CA waits in s_o, CB in registers)
+  mfma_rows(s_ga, bmc, s_o, l);
   float dvt[DIM];
   cf kphj_p{0.0f, 0.0f}, krho_p{0.0f, 0.0f};  // plane kk's sums (lanes kk < K use them)
-  // the plane loops stay rolled (their per-plane values come from LDS), so that the matrix rows are not all
-  // loaded into registers at once
-#pragma unroll 1
-  for (int j = 0; j < K; ++j) {
-    cf RC{0.0f, 0.0f}, RP{0.0f, 0.0f};
 #pragma unroll
-    for (int k = 0; k < K; ++k) {
-      acc_row(RC, sg[k], s_mr[j][k]);
-      acc_row(RP, pi[k], s_gr[j][k]);
-    }
+  for (int j = 0; j < K; ++j) {
+    const cf RC{rc[2 * j], rc[2 * j + 1]}, RP{rp[2 * j], rp[2 * j + 1]};
     // sums of RC over the steps after t (excl) and from t on (incl): the total minus the inclusive prefix
     const float pr = wave_prefix(RC.re), pim = wave_prefix(RC.im);
     const cf excl{lane63(pr) - pr, lane63(pim) - pim};
     const cf incl = excl + RC;
     const float2 f = s_pl[j][1], l1e = s_pl[j][3], ri = s_pl[j][5];
-    const float2 flj = s_fl[t][j], pij = s_pi[t][j], gaj = s_ga[t][j];
     const cf lam1{l1e.x, l1e.y};
     const cf ex = lam1 + excl;
-    const cf dvp = conj(cf{flj.x, flj.y}) * fma_c(conj(cf{f.x, f.y}), ex, RP);
-    s_fl[t][j] = float2{dvp.re, dvp.im};  // the lane's own slot: now the plane part of dv
+    const cf dvp = conj(fl[j]) * fma_c(conj(cf{f.x, f.y}), ex, RP);
+    dvt[2 * j] = dvp.re;
+    dvt[2 * j + 1] = dvp.im;
     // kphj += h conj(pi) (lam1 + excl); krho += h conj(S1(t-1)) a (lam1 + incl), S1(t-1) conj(a) = gamma / rho
-    const cf q1 = h * cjm(cf{pij.x, pij.y}, ex);
-    const cf q2 = h * cjm(cf{gaj.x, gaj.y} * cf{ri.x, ri.y}, lam1 + incl);
+    const cf q1 = h * cjm(pi[j], ex);
+    const cf q2 = h * cjm(ga[j] * cf{ri.x, ri.y}, lam1 + incl);
     const cf s1{lane63(wave_prefix(q1.re)), lane63(wave_prefix(q1.im))};
     const cf s2{lane63(wave_prefix(q2.re)), lane63(wave_prefix(q2.im))};
     if (j == kk) {
@@ -1702,39 +1789,24 @@ __global__ __launch_bounds__(64) void k_bwd_carry(DiagArgs a) {
       krho_p = s2;
     }
   }
-  // columns (plane k: the later factor's part of dv)
-  {
-    cf CA[K], CB[K];
+  __syncthreads();
 #pragma unroll
-    for (int k = 0; k < K; ++k) CA[k] = CB[k] = cf{0.0f, 0.0f};
-#pragma unroll 1
-    for (int j = 0; j < K; ++j) {
-      const float2 gaj = s_ga[t][j], pij = s_pi[t][j];
+  for (int i = 0; i < DIM; ++i) rc[i] = s_o[t][i];  // CA
+  __syncthreads();
+  mfma_rows(s_pi, bgc, s_o, l);
+  __syncthreads();
 #pragma unroll
-      for (int k = 0; k < K; ++k) {
-        acc_col(CA[k], cf{gaj.x, gaj.y}, s_mc[j][k]);
-        acc_col(CB[k], cf{pij.x, pij.y}, s_gc[j][k]);
-      }
-    }
-#pragma unroll
-    for (int k = 0; k < K; ++k) {
-      const float2 hk = s_pl[k][2], dvp = s_fl[t][k];
-      const cf col = conj(fl[k]) * fma_c(conj(cf{hk.x, hk.y}), CA[k], CB[k]);
-      dvt[2 * k] = dvp.x + col.re;
-      dvt[2 * k + 1] = dvp.y + col.im;
-    }
+  for (int k = 0; k < K; ++k) {
+    const float2 hk = s_pl[k][2];
+    const cf col = conj(fl[k]) * fma_c(conj(cf{hk.x, hk.y}), cf{rc[2 * k], rc[2 * k + 1]},
+                                       cf{s_o[t][2 * k], s_o[t][2 * k + 1]});
+    dvt[2 * k] += col.re + dvl[2 * k];
+    dvt[2 * k + 1] += col.im + dvl[2 * k + 1];
   }
   if (live) {
     float* dvr = a.dv + ((size_t)b * a.n_int + t0 + t) * DIM;
 #pragma unroll
-    for (int i = 0; i < DIM; i += 4) {
-      const f4a loc = *reinterpret_cast<const f4a*>(dvr + i);
-      dvt[i] += loc.x;
-      dvt[i + 1] += loc.y;
-      dvt[i + 2] += loc.z;
-      dvt[i + 3] += loc.w;
-      *reinterpret_cast<f4a*>(dvr + i) = f4a{dvt[i], dvt[i + 1], dvt[i + 2], dvt[i + 3]};
-    }
+    for (int i = 0; i < DIM; i += 4) *reinterpret_cast<f4a*>(dvr + i) = f4a{dvt[i], dvt[i + 1], dvt[i + 2], dvt[i + 3]};
   }
   // interior knots t0 + 1 .. t0 + Tc - 1: dX_t = dv(t-1) - dv(t); the boundary knots are finished by k_knot_grads
   {
@@ -1748,31 +1820,51 @@ __global__ __launch_bounds__(64) void k_bwd_carry(DiagArgs a) {
     }
   }
   __syncthreads();
-  // ---- lane = pair (jj, kk): outer-product sums over the steps
-  float ph[4] = {0.0f, 0.0f, 0.0f, 0.0f}, ps[4] = {0.0f, 0.0f, 0.0f, 0.0f};  // pi_j x (h | n) pi_k
-  float gh[4] = {0.0f, 0.0f, 0.0f, 0.0f}, gs[4] = {0.0f, 0.0f, 0.0f, 0.0f};  // gamma_j x (h | n) pi_k
+  // ---- outer-product sums over the steps on MFMA: D[m][n] = sum_t x_t[m] (w_t pi_t[n]) for x = pi, gamma and
+  // w = h, n (16 x 16 real, all four real products of each complex pair), sixteen k-steps of four steps each
+  {
+    const int li = l & 15, lk = l >> 4;
+    f4m d1 = {0.0f, 0.0f, 0.0f, 0.0f}, d2 = d1, d3 = d1, d4 = d1;
 #pragma unroll 4
-  for (int s = 0; s < Tc; ++s) {
-    const float2 xj = s_pi[s][jj], yk = s_pi[s][kk], gj = s_ga[s][jj], w = s_wh[s];
-    const float hyr = w.x * yk.x, hyi = w.x * yk.y, syr = w.y * yk.x, syi = w.y * yk.y;
-    ph[0] = fmaf(xj.x, hyr, ph[0]); ph[1] = fmaf(xj.y, hyi, ph[1]); ph[2] = fmaf(xj.x, hyi, ph[2]); ph[3] = fmaf(xj.y, hyr, ph[3]);
-    ps[0] = fmaf(xj.x, syr, ps[0]); ps[1] = fmaf(xj.y, syi, ps[1]); ps[2] = fmaf(xj.x, syi, ps[2]); ps[3] = fmaf(xj.y, syr, ps[3]);
-    gh[0] = fmaf(gj.x, hyr, gh[0]); gh[1] = fmaf(gj.y, hyi, gh[1]); gh[2] = fmaf(gj.x, hyi, gh[2]); gh[3] = fmaf(gj.y, hyr, gh[3]);
-    gs[0] = fmaf(gj.x, syr, gs[0]); gs[1] = fmaf(gj.y, syi, gs[1]); gs[2] = fmaf(gj.x, syi, gs[2]); gs[3] = fmaf(gj.y, syr, gs[3]);
+    for (int ks = 0; ks < kMaxT / 4; ++ks) {
+      const int ts = 4 * ks + lk;
+      const float xp = s_pi[ts][li], xg = s_ga[ts][li];
+      const float2 w = s_wh[ts];
+      const float yh = w.x * xp, ys = w.y * xp;
+      d1 = mfma4(xp, yh, d1);
+      d2 = mfma4(xp, ys, d2);
+      d3 = mfma4(xg, yh, d3);
+      d4 = mfma4(xg, ys, d4);
+    }
+    float(*dd)[16][17] = reinterpret_cast<float(*)[16][17]>(&s_o[0][0]);  // 4 x 16 x 17 <= 64 x SP floats
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      dd[0][4 * lk + r][li] = d1[r];
+      dd[1][4 * lk + r][li] = d2[r];
+      dd[2][4 * lk + r][li] = d3[r];
+      dd[3][4 * lk + r][li] = d4[r];
+    }
   }
-  // x y = (rr - ii, ri + ir), x conj(y) = (rr + ii, ir - ri)
-  const cf Psi1{ph[0] - ph[1], ph[2] + ph[3]}, Psi2{ph[0] + ph[1], ph[3] - ph[2]};
-  const cf Psi3{gh[0] - gh[1], gh[2] + gh[3]}, Psi4{gh[0] + gh[1], gh[3] - gh[2]};
-  const cf Q1{ps[0] - ps[1], ps[2] + ps[3]}, Q2{ps[0] + ps[1], ps[3] - ps[2]};
-  const cf Q3{gs[0] - gs[1], gs[2] + gs[3]}, Q4{gs[0] + gs[1], gs[3] - gs[2]};
-  const cf lB{(float)(2.0 * X.SB.re), (float)(2.0 * X.SB.im)}, lA{(float)(2.0 * X.SA.re), (float)(2.0 * X.SA.im)};
-  const cf kIB = lB * conj(Psi1), kIA = lA * conj(Psi2);
-  const cf kph = lB * conj(Psi3) + conj(lA) * Psi4;
+  __syncthreads();
+  // ---- lane = pair (jj, kk)
+  const float(*dd)[16][17] = reinterpret_cast<const float(*)[16][17]>(&s_o[0][0]);
+  // x y = (rr - ii, ri + ir), x conj(y) = (rr + ii, ir - ri), with rr = D[2j][2k], ii = D[2j+1][2k+1], ...
+  cf P[4], Pc[4];
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    const float rr = dd[q][2 * jj][2 * kk], ii = dd[q][2 * jj + 1][2 * kk + 1];
+    const float ri = dd[q][2 * jj][2 * kk + 1], ir = dd[q][2 * jj + 1][2 * kk];
+    P[q] = cf{rr - ii, ri + ir};
+    Pc[q] = cf{rr + ii, ir - ri};
+  }
+  // P[0] = sum h pi_j pi_k, P[1] = sum n pi_j pi_k, P[2] = sum h gamma_j pi_k, P[3] = sum n gamma_j pi_k
+  const cf kIB = lB * conj(P[0]), kIA = lA * conj(Pc[0]);
+  const cf kph = lB * conj(P[2]) + conj(lA) * Pc[2];
   const double* cr = cr0 + DIM + 4 * (8 * jj + kk);
   const cf C2Ah{(float)(0.5 * cr[0]), (float)(0.5 * cr[1])}, C2Bh{(float)(0.5 * cr[2]), (float)(0.5 * cr[3])};
   const cf uj = load_u(a.params, jj), uk = load_u(a.params, kk);
-  const cf WB = (tau * (C2Bh * expv(tau * (uj + uk))) + pc.phk_k * Q3 + pc.IB * Q1) / pc.LB;
-  const cf WA = (tau * (C2Ah * expv(tau * (uj + conj(uk)))) + conj(pc.phk_k) * Q4 + pc.IA * Q2) / pc.LA;
+  const cf WB = (tau * (C2Bh * expv(tau * (uj + uk))) + pc.phk_k * P[3] + pc.IB * P[1]) / pc.LB;
+  const cf WA = (tau * (C2Ah * expv(tau * (uj + conj(uk)))) + conj(pc.phk_k) * Pc[3] + pc.IA * Pc[1]) / pc.LA;
   const cf kLB = lB * conj(WB), kLA = lA * conj(WA);
   // coefficient cotangents -> parameter partials (d_j, w_j), as k_bwd_full: a node h u contributes (-Re G, Im G)
   // for u = -conj(z) and (-Re G, -Im G) for u = -z (the conj(u_k) of the A pairs)
@@ -1780,6 +1872,7 @@ __global__ __launch_bounds__(64) void k_bwd_carry(DiagArgs a) {
   const cf GyB = 0.5f * (kIB * conj(pc.DyB)) + kLB * conj(pc.LB);
   const cf GyA = 0.5f * (kIA * conj(pc.DyA)) + kLA * conj(pc.LA);
   const cf Gk = 0.5f * (kph * conj(pc.dphi_k));
+  f4a* s_part = reinterpret_cast<f4a*>(&s_pi[0][0]);  // pi is no longer read
   s_part[l] = f4a{-GyB.re - GyA.re - Gx.re, GyB.im + GyA.im + Gx.im, -GyB.re - GyA.re - Gk.re, GyB.im - GyA.im + Gk.im};
   __syncthreads();
   if (l < K) {
