@@ -156,6 +156,10 @@ def bench_diag_cfg(args):
     mix = bool(args.mixer) and cfg != "c1"  # the block's mixer epilogue (graded norm + c_down) after the scan
     if mix:
         log = False
+    # c4's shape (B = 256 samples of L = 512, d = 32 real diagonal): the default plan takes the per-sample sequential
+    # kernels, whose passes after the first launch nothing, and LogEWS's log rows come straight out of the scan
+    seq = cfg == "c4" and args.chunk == 0
+    fused_log = log and seq
     B, L, d = path_np.shape
     D = d + d * d
     W = D + 1
@@ -164,16 +168,17 @@ def bench_diag_cfg(args):
         path = path.to(torch.bfloat16)
     clock = torch.tensor(clock_np, device=dev)
     A = torch.tensor(A_np, device=dev)
-    desc = make_desc(B, L, d, N, structure, nat.FLOW_PER_INTERVAL, "prefix", True,
+    desc = make_desc(B, L, d, N, structure, nat.FLOW_PER_INTERVAL, "log_prefix" if fused_log else "prefix", True,
                      nat.DTYPE_BF16 if bf16 else nat.DTYPE_F32, args.chunk)
     ws = torch.empty(int(lib.ews_diag_workspace_bytes(ctypes.byref(desc))), device=dev, dtype=torch.uint8)
     resid = torch.empty(int(lib.ews_diag_residual_bytes(ctypes.byref(desc))), device=dev, dtype=torch.uint8)
-    out = torch.empty((B, L - 1, W), device=dev, dtype=torch.float32)
+    Dlog = int(lib.ews_log_dim(d, N))
+    Wout = Dlog if fused_log else W
+    out = torch.empty((B, L - 1, Wout), device=dev, dtype=torch.float32)
     nf, nb = lib.ews_diag_num_passes(0), lib.ews_diag_num_passes(1)
-    names = FWD_PASS_NAMES[:nf]
-    if log:
+    names = ["sequential_forward"] if seq else FWD_PASS_NAMES[:nf]
+    if log and not fused_log:
         ldesc = nat.LogDesc(B, L - 1, d, N, 1, nat.READOUTS["prefix"])
-        Dlog = int(lib.ews_log_dim(d, N))
         lout = torch.empty((B, L - 1, Dlog), device=dev, dtype=torch.float32)
         lws = torch.empty(max(16, int(lib.ews_log_workspace_bytes(ctypes.byref(ldesc)))), device=dev,
                           dtype=torch.uint8)
@@ -190,24 +195,26 @@ def bench_diag_cfg(args):
         names = names + ["mixer_forward"]
     if bwd:
         gsrc = torch.randn((B, L - 1, Dlog if log else W), device=dev, dtype=torch.float32)
-        gout = torch.empty((B, L - 1, W), device=dev, dtype=torch.float32) if log else gsrc
+        gout = torch.empty((B, L - 1, W), device=dev, dtype=torch.float32) if (log and not fused_log) else gsrc
         if mix:
             gmix = torch.randn((B, L, hidden), device=dev, dtype=torch.float32)
         dpath = torch.empty((B, L, d), device=dev, dtype=torch.float32)
         dA = torch.empty_like(A)
-        names = names + (["log_backward"] if log else []) + (["mixer_backward"] if mix else []) + BWD_PASS_NAMES[:nb]
+        names = (names + (["log_backward"] if log and not fused_log else []) + (["mixer_backward"] if mix else [])
+                 + (["sequential_backward"] if seq else BWD_PASS_NAMES[:nb]))
 
     def step(events=None):
         st = ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream)
         i = 0
         for p in range(nf):
-            if events is not None:
-                events[i].record()
-            i += 1
+            if p == 0 or not seq:  # the sequential plan's passes are timed as one stage
+                if events is not None:
+                    events[i].record()
+                i += 1
             nat.check(lib.ews_diag_forward_pass(ctypes.byref(desc), p, path.data_ptr(), clock.data_ptr(),
                                                 A.data_ptr(), out.data_ptr(), resid.data_ptr(), ws.data_ptr(), st),
                       "forward pass")
-        if log:
+        if log and not fused_log:
             if events is not None:
                 events[i].record()
             i += 1
@@ -226,16 +233,17 @@ def bench_diag_cfg(args):
                     events[i].record()
                 i += 1
                 g_rows = torch.autograd.grad(r, (rows_in, mW, mb, mg), gmix)[0]
-            if log:
+            if log and not fused_log:
                 if events is not None:
                     events[i].record()
                 i += 1
                 nat.check(lib.ews_log_backward(ctypes.byref(ldesc), out.data_ptr(), gsrc.data_ptr(),
                                                gout.data_ptr(), lws.data_ptr(), st), "log backward")
             for p in range(nb):
-                if events is not None:
-                    events[i].record()
-                i += 1
+                if p == 0 or not seq:
+                    if events is not None:
+                        events[i].record()
+                    i += 1
                 nat.check(lib.ews_diag_backward_pass(ctypes.byref(desc), p, path.data_ptr(), clock.data_ptr(),
                                                      A.data_ptr(), resid.data_ptr(), g_rows.data_ptr(),
                                                      dpath.data_ptr(), None, dA.data_ptr(), ws.data_ptr(), st),
@@ -289,7 +297,10 @@ def bench_diag_cfg(args):
     n = B * (L - 1)
     s_in = 2 if bf16 else 4
     ab = algorithmic_bytes(B, L, d, W, s_in)
-    if log:
+    if seq:  # the whole forward / backward in one kernel each: read the inputs, write the rows (flat or log)
+        ab["sequential_forward"] = n * (s_in * (d + 1) + 4 * Wout)
+        ab["sequential_backward"] = n * (4 * Wout + 2 * s_in * (d + 1))
+    if log and not fused_log:
         ab["log_forward"] = n * 4 * (W + Dlog)            # read state rows, write log rows
         ab["log_backward"] = n * 4 * (2 * W + Dlog)       # read state rows and log cotangents, write row cotangents
     torch_mix = None
@@ -315,8 +326,11 @@ def bench_diag_cfg(args):
         torch_mix = round(t0.elapsed_time(t1) / args.steps, 4)
     dominant = max((k for k in pass_ms if k in ab), key=pass_ms.get)
     achieved = ab[dominant] / (pass_ms[dominant] * 1e-3) / 1e9
-    total = ab["fwd_total"] + (ab["bwd_total"] if bwd else 0)
-    if log:
+    if seq:
+        total = ab["sequential_forward"] + (ab["sequential_backward"] if bwd else 0)
+    else:
+        total = ab["fwd_total"] + (ab["bwd_total"] if bwd else 0)
+    if log and not fused_log:
         total += ab["log_forward"] + (ab["log_backward"] if bwd else 0)
     if mix:
         total += ab["mixer_forward"] + (ab["mixer_backward"] if bwd else 0)
@@ -326,6 +340,8 @@ def bench_diag_cfg(args):
                   "diagonal A, depth 2, fp32, EWS scan + LogEWS compression (prefix), forward + backward",
             "c5": "c5: one of 3 stacked EWS blocks, B=8, L=49920, 6 band-limited channels lifted to d=24 (12 rotation "
                   "planes), depth 2, bf16 path / fp32 state, prefix readout, forward + backward"}[cfg]
+    if fused_log:
+        what = what.replace("LogEWS compression (prefix)", "LogEWS compression (prefix, log rows written by the scan)")
     if mix:
         what = (what.replace("EWS scan + LogEWS compression (prefix)", "EWS scan")
                 + f", then the mixer epilogue (drop level 0, zero row, GradedRMSNorm live_rms, c_down to {hidden})")

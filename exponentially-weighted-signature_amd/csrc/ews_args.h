@@ -50,6 +50,9 @@ struct DiagArgs {
   double* qflow;    // (B, NQ, K, 2) quad flows exp(u tau_quad)
   double* ql1;      // (B, NQ, K, 2) level-1 increments of the quads (backward)
   double* cflow;    // (B, C, K, 2) chunk flows exp(u tau_chunk)
+  // per-sample sequential kernels (real diagonal, ews_seq.hip)
+  float* seqck;     // (B, blocks, lanes + K) state checkpoints (residual; null: the forward keeps none)
+  float* seqgp;     // (B, K) per-sample parameter partials (backward)
   // backward outputs
   float* dpath;
   float* dclock;

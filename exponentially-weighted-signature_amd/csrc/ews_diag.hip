@@ -30,6 +30,7 @@
 #include "ews_hip.h"
 #include "ews_numerics.h"
 #include "ews_pairs.h"
+#include "ews_seq.h"
 
 namespace ews {
 
@@ -1730,6 +1731,7 @@ size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 struct Plan {
   int B, L, n_int, d, K, N, T, C, D, W, npar, kb, readout;
   bool cplx, wave, fast;
+  bool seq;  // the per-sample sequential kernels (ews_seq.hip) run the whole call
   int NT, NTb, scan_cb, NG;
   size_t lds_bwd_local, lds_bwd_full, lds_bwd_inv, lds_carry, lds_adjoint;
 };
@@ -1747,7 +1749,7 @@ int make_plan(const ews_diag_desc* s, Plan& p) {
   if (!s) return EWS_ERR_NULL;
   if (s->structure != EWS_STRUCT_PLANES && s->structure != EWS_STRUCT_REAL_DIAG) return EWS_ERR_OPTION;
   if (s->flow_mode < 0 || s->flow_mode > 2) return EWS_ERR_OPTION;
-  if (s->readout < 0 || s->readout > 3) return EWS_ERR_OPTION;
+  if (s->readout < 0 || s->readout > EWS_READOUT_LOGPREFIX) return EWS_ERR_OPTION;
   if (s->path_dtype != EWS_DTYPE_F32 && s->path_dtype != EWS_DTYPE_BF16) return EWS_ERR_OPTION;
   if (s->depth != 1 && s->depth != 2) return EWS_ERR_DEPTH;
   if (s->batch < 1 || s->length < 2 || s->dim < 1) return EWS_ERR_SHAPE;
@@ -1755,7 +1757,7 @@ int make_plan(const ews_diag_desc* s, Plan& p) {
   if (p.cplx && (s->dim % 2 != 0 || s->dim > 32)) return EWS_ERR_SHAPE;
   if (!p.cplx && s->dim > 32) return EWS_ERR_SHAPE;
   if ((s->flow_mode == EWS_FLOW_CACHED_BASEPOINT) && s->length < 3) return EWS_ERR_SHAPE;
-  if (s->chunk < 0) return EWS_ERR_SHAPE;
+  if (s->chunk < 0 && s->chunk != EWS_CHUNK_SEQUENTIAL) return EWS_ERR_SHAPE;
   if (s->leaf < EWS_DIAG_LEAF_CLOSED || s->leaf > EWS_DIAG_LEAF_SERIES) return EWS_ERR_OPTION;
   if (s->leaf != EWS_DIAG_LEAF_CLOSED && (s->series_q < 0 || s->series_q > kMaxSeriesQ)) return EWS_ERR_OPTION;
   if (s->leaf == EWS_DIAG_LEAF_SERIES && s->series_q < 1) return EWS_ERR_OPTION;
@@ -1770,6 +1772,26 @@ int make_plan(const ews_diag_desc* s, Plan& p) {
   p.D = p.d + (p.N == 2 ? p.d * p.d : 0);
   p.W = p.D + (s->level0 ? 1 : 0);
   p.npar = p.cplx ? 2 * p.K : p.K;
+  // the per-sample sequential kernels: asked for (chunk EWS_CHUNK_SEQUENTIAL, the log-prefix readout), or chosen
+  // for many samples of moderate length, where one workgroup per sample fills the chip
+  const bool seq_form = !p.cplx && p.N == 2 && p.d <= kSeqMaxK && s->flow_mode == EWS_FLOW_PER_INTERVAL &&
+                        (s->readout == EWS_READOUT_PREFIX || s->readout == EWS_READOUT_LOGPREFIX);
+  const bool seq_asked = s->chunk == EWS_CHUNK_SEQUENTIAL || s->readout == EWS_READOUT_LOGPREFIX;
+  if (seq_asked && (!seq_form || s->chunk > 0)) return EWS_ERR_OPTION;
+  p.seq = seq_form && (seq_asked || (s->chunk == 0 && p.B >= 128 && p.L <= 1025));
+  if (p.seq) {
+    if (s->readout == EWS_READOUT_LOGPREFIX) p.W = p.d + p.d * (p.d - 1) / 2;
+    p.fast = false;
+    p.wave = false;
+    p.T = p.n_int;
+    p.C = 1;
+    p.kb = 1;
+    p.NT = p.NTb = seq_threads(p.K);
+    p.scan_cb = 1;
+    p.NG = 1;
+    p.lds_bwd_local = p.lds_bwd_full = p.lds_bwd_inv = p.lds_carry = p.lds_adjoint = 0;
+    return EWS_OK;
+  }
   const int P = (p.N == 2) ? p.K * p.K : p.K;
   p.NT = ((P + 63) / 64) * 64;
   p.wave = p.K <= 8;  // one wavefront with lane = 8 j + k in the backward chunk kernels
@@ -1808,8 +1830,13 @@ struct WsLayout {
   size_t summ, mu, mt, red, red_idx, dv, dh, gp, gph, gpart, gagg, gcar, qagg, qflow, ql1, cflow, total;
 };
 WsLayout ws_layout(const Plan& p) {
-  WsLayout w;
+  WsLayout w{};
   size_t off = 0;
+  if (p.seq) {  // per-sample parameter partials of the sequential backward (in the gp slot)
+    w.gp = 0;
+    w.total = align256((size_t)p.B * p.K * 4);
+    return w;
+  }
   const size_t BC = (size_t)p.B * p.C;
   w.summ = off; off += align256(BC * p.D * 4);
   w.mu = off; off += align256(BC * p.D * 4);
@@ -1836,6 +1863,7 @@ WsLayout ws_layout(const Plan& p) {
 WsLayout ws_layout_fwd(const Plan& p) {
   WsLayout w{};
   size_t off = 0;
+  if (p.seq) return w;  // the sequential forward needs no scratch
   const size_t BC = (size_t)p.B * p.C;
   const bool reduce = p.readout == EWS_READOUT_MEAN || p.readout == EWS_READOUT_MAX;
   w.summ = off; off += align256(BC * p.D * 4);
@@ -1855,6 +1883,7 @@ size_t resid_carries_bytes(const Plan& p) { return align256((size_t)p.B * (p.C +
 size_t resid_argmax_bytes(const Plan& p) { return align256((size_t)p.B * p.W * 4); }
 size_t resid_chunk_bytes(const Plan& p) { return align256((size_t)p.B * p.C * 4); }
 size_t resid_bytes(const Plan& p) {
+  if (p.seq) return align256((size_t)p.B * seq_ckpt_floats(p.K, p.n_int) * 4);  // state checkpoints
   return resid_carries_bytes(p) + resid_argmax_bytes(p) + 2 * resid_chunk_bytes(p) + align256(kCoefTabFloats * 4);
 }
 
@@ -1869,6 +1898,14 @@ DiagArgs make_args(const ews_diag_desc* s, const Plan& p, const void* path, cons
   a.sq1 = s->leaf == EWS_DIAG_LEAF_SERIES ? s->series_q : 0;
   a.sq2 = s->leaf == EWS_DIAG_LEAF_CLOSED ? 0 : s->series_q;
   a.path = path; a.clock = clock; a.params = params;
+  if (p.seq) {
+    if (s->readout == EWS_READOUT_LOGPREFIX) {  // log rows: level 1, then the Lyndon coefficients of level 2
+      a.lvl0 = 0; a.off1 = 0; a.off2 = p.d;
+    }
+    a.seqck = fwd_only ? nullptr : (float*)residual;  // the allocation-free forward keeps no checkpoints
+    a.seqgp = fwd_only ? nullptr : (float*)workspace;
+    return a;
+  }
   char* r = (char*)residual;
   a.carries = (double*)r;
   a.argmax = (int*)(r + resid_carries_bytes(p));
@@ -2021,6 +2058,11 @@ int backward_pass(const Plan& p, DiagArgs a, hipStream_t st, int pass) {
 }
 
 int dispatch_forward(const ews_diag_desc* s, const Plan& p, const DiagArgs& a, hipStream_t st, int pass) {
+  if (p.seq) {  // one pass: the whole forward (the other pass numbers launch nothing)
+    if (pass < 0 || pass >= 4) return EWS_ERR_OPTION;
+    if (pass == 0 && seq_forward(a, st) != 0) return EWS_ERR_LAUNCH;
+    return EWS_OK;
+  }
   const bool big = p.NT > 256;
   if (p.cplx) {
     if (p.N == 2) return big ? forward_pass<true, 2, 1024>(s, p, a, st, pass) : forward_pass<true, 2, 256>(s, p, a, st, pass);
@@ -2031,6 +2073,11 @@ int dispatch_forward(const ews_diag_desc* s, const Plan& p, const DiagArgs& a, h
 }
 
 int dispatch_backward(const Plan& p, const DiagArgs& a, hipStream_t st, int pass) {
+  if (p.seq) {  // one pass: the whole backward and the parameter reduction
+    if (pass < 0 || pass >= 5) return EWS_ERR_OPTION;
+    if (pass == 0 && seq_backward(a, st) != 0) return EWS_ERR_LAUNCH;
+    return EWS_OK;
+  }
   const bool big = p.NT > 256;
   if (p.cplx) {
     if (p.N == 2) {
@@ -2147,7 +2194,7 @@ int ews_diag_forward_noalloc(const ews_diag_desc* desc, const void* path, const 
   int rc = make_plan(desc, p);
   if (rc != EWS_OK) return rc;
   if (!path || !clock || !params || !out) return EWS_ERR_NULL;
-  const size_t rb = resid_bytes(p);
+  const size_t rb = p.seq ? 0 : resid_bytes(p);  // the sequential forward keeps no checkpoints here
   if (rb + ws_layout_fwd(p).total > kNoAllocScratchBytes) return EWS_ERR_SCRATCH;
   void* base = nullptr;
   rc = scratch_on_current_device(&base);

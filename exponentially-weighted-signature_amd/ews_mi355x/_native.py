@@ -19,7 +19,8 @@ STRUCT_REAL_DIAG = 2
 FLOW_PER_INTERVAL = 0
 FLOW_CACHED = 1
 FLOW_CACHED_BASEPOINT = 2
-READOUTS = {"prefix": 0, "terminal": 1, "mean": 2, "max": 3}
+READOUTS = {"prefix": 0, "terminal": 1, "mean": 2, "max": 3, "log_prefix": 4}  # log_prefix: diag scan only
+CHUNK_SEQUENTIAL = -1  # ews_diag_desc.chunk: the per-sample sequential kernels
 LEAF_SERIES = 0
 LEAF_VAN_LOAN = 1
 DIAG_LEAVES = {"plane_closed": 0, "block_series": 1, "series": 2}

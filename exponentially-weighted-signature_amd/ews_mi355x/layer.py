@@ -244,6 +244,25 @@ class EWS(torch.nn.Module):
         return ops.diag_scan(path, clock, params, self.N, self.structure, self._flow_mode(readout), readout,
                              level0, chunk=0, leaf=leaf, series_q=self.series_q or 0)
 
+    def _log_prefix_fused(self, path, clock):
+        """LogEWS prefix rows computed inside the scan (real diagonal, depth 2, d <= 32, per-interval flows, the
+        diagonal leaves): the compressed log of every prefix row (ews/layer.py:488-517) without the flat rows ever
+        reaching memory. None when the configuration takes the rows-then-log route."""
+        if (self.structure != "real_diag" or self.N != 2 or self.d > 32 or path.dim() != 3
+                or self._flow_mode("prefix") != "per_interval"):
+            return None
+        if self._engine_check() != "diag":
+            return None
+        if self.dtype != torch.float32:
+            raise TypeError("the MI355X kernels compute in float32 (dtype=torch.float32)")
+        A = self.A_param().to(torch.float32)
+        params = self._diag_params(A.to(path.device))
+        if path.dtype != torch.bfloat16:
+            path = path.to(torch.float32)
+        leaf = self.leaf if self.leaf in ("series", "block_series") else "plane_closed"
+        return ops.diag_scan(path, clock.to(torch.float32), params, self.N, self.structure, "per_interval",
+                             "log_prefix", False, chunk=0, leaf=leaf, series_q=self.series_q or 0)
+
     def _levels(self, packed, lead):
         out, s = [], 0
         for k in range(1, self.N + 1):
@@ -273,18 +292,22 @@ class EWS(torch.nn.Module):
             out = self.forward(path[None], clock[None], output_format=output_format, readout=readout,
                                a_scale=a_scale)
             return [o[0] for o in out] if isinstance(out, list) else out[0]
-        if path.dim() != 3:
-            raise ValueError(f"Path must be 2D or 3D, got shape {tuple(path.shape)}")
-        if clock.dim() != 2:
-            raise ValueError("clock must be 2D for batched paths")
-        if clock.shape[1] != path.shape[1] or clock.shape[0] != path.shape[0]:
-            raise ValueError("clock must be 1D and aligned with path length")
+        self._check_batch(path, clock)
         if output_format == "list":
             if readout in ("mean", "max"):
                 raise ValueError(f"readout='{readout}' requires output_format='flat'")
             packed = self._run(path, clock, readout, False, a_scale)
             return self._levels(packed, tuple(packed.shape[:-1]))
         return self._run(path, clock, readout, True, a_scale)
+
+    @staticmethod
+    def _check_batch(path, clock):
+        if path.dim() != 3:
+            raise ValueError(f"Path must be 2D or 3D, got shape {tuple(path.shape)}")
+        if clock.dim() != 2:
+            raise ValueError("clock must be 2D for batched paths")
+        if clock.shape[1] != path.shape[1] or clock.shape[0] != path.shape[0]:
+            raise ValueError("clock must be 1D and aligned with path length")
 
     @property
     def signature_dim(self) -> int:
@@ -356,11 +379,16 @@ class LogEWS(torch.nn.Module):
         single = path.dim() == 2
         if single:
             path, clock = path[None], clock[None]
-        if readout == "terminal":
-            rows = self.ewms(path, clock, readout="terminal", output_format="flat")[:, None, :]
-        else:
-            rows = self.ewms(path, clock, readout="prefix", output_format="flat")
-        feat = ops.log_rows(rows, self.d, self.N, True, readout)
+        feat = None
+        if readout == "prefix":
+            self.ewms._check_batch(path, clock)
+            feat = self.ewms._log_prefix_fused(path, clock)  # the log rows written by the scan itself
+        if feat is None:
+            if readout == "terminal":
+                rows = self.ewms(path, clock, readout="terminal", output_format="flat")[:, None, :]
+            else:
+                rows = self.ewms(path, clock, readout="prefix", output_format="flat")
+            feat = ops.log_rows(rows, self.d, self.N, True, readout)
         if single:
             feat = feat[0]
         if output_format == "list":

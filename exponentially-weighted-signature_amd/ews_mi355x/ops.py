@@ -55,7 +55,9 @@ class DiagScan(torch.autograd.Function):
         desc = make_desc(B, L, d, N, structure, flow_mode, readout, level0, dt, chunk, leaf, series_q)
         D = d + (d * d if N == 2 else 0)
         W = D + (1 if level0 else 0)
-        shape = (B, L - 1, W) if readout == "prefix" else (B, W)
+        if readout == "log_prefix":  # LogEWS rows: level 1 and the Lyndon coefficients of level 2, no level 0
+            W = d + d * (d - 1) // 2
+        shape = (B, L - 1, W) if readout in ("prefix", "log_prefix") else (B, W)
         dev = path.device
         out = torch.empty(shape, device=dev, dtype=torch.float32)
         resid = torch.empty(int(lib.ews_diag_residual_bytes(ctypes.byref(desc))), device=dev, dtype=torch.uint8)
@@ -91,7 +93,9 @@ class DiagScan(torch.autograd.Function):
 def diag_scan(path, clock, params, N, structure, flow_mode="per_interval", readout="prefix", level0=True,
               chunk=0, leaf="plane_closed", series_q=0):
     """leaf "plane_closed" (exact closed forms, for planes and real diagonals alike), "block_series" (exact level 1,
-    the order-series_q series at level 2) or "series" (the order-series_q series at every level)."""
+    the order-series_q series at level 2) or "series" (the order-series_q series at every level). readout
+    "log_prefix" (real diagonal, depth 2, d <= 32, per-interval flows) returns the LogEWS prefix rows straight from
+    the scan; chunk nat.CHUNK_SEQUENTIAL asks for the per-sample sequential kernels."""
     fm = {"per_interval": nat.FLOW_PER_INTERVAL, "cached": nat.FLOW_CACHED,
           "cached_basepoint": nat.FLOW_CACHED_BASEPOINT}[flow_mode]
     st = {"planes": nat.STRUCT_PLANES, "real_diag": nat.STRUCT_REAL_DIAG}[structure]

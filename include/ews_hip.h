@@ -45,6 +45,16 @@ typedef struct ihipStream_t* ews_stream_t; /* hipStream_t */
 #define EWS_READOUT_TERMINAL 1 /* (B, W) */
 #define EWS_READOUT_MEAN 2     /* (B, W) */
 #define EWS_READOUT_MAX 3      /* (B, W) */
+/* LogEWS prefix rows (ews/layer.py:488-517 with readout "prefix"): per prefix row the compressed log
+ * signature, level 1 then S2[j,k] - S1_j S1_k / 2 at the Lyndon words j < k in lexicographic order,
+ * (B, L-1, d + d(d-1)/2), no level-0 column (level0 is ignored). Real diagonal, depth 2, d <= 32, per-interval
+ * flows only: it runs on the per-sample sequential kernels (chunk 0 or EWS_CHUNK_SEQUENTIAL). */
+#define EWS_READOUT_LOGPREFIX 4
+
+/* ews_diag_desc.chunk: 0 selects the kernels and chunk length; EWS_CHUNK_SEQUENTIAL asks for the per-sample
+ * sequential kernels (one workgroup per sample, the whole sequence in one pass; real diagonal, depth 2, d <= 32,
+ * prefix or log-prefix readout, per-interval flows), which chunk 0 also selects for B >= 128 and L <= 1025. */
+#define EWS_CHUNK_SEQUENTIAL (-1)
 
 #define EWS_DTYPE_F32 0
 #define EWS_DTYPE_BF16 1
@@ -59,7 +69,7 @@ typedef struct ews_diag_desc {
   int32_t readout;    /* EWS_READOUT_* */
   int32_t level0;     /* 1: rows carry the leading level-0 constant (the "flat" format), 0: packed */
   int32_t path_dtype; /* EWS_DTYPE_F32 or EWS_DTYPE_BF16 */
-  int32_t chunk;      /* intervals per chunk; 0 selects the default */
+  int32_t chunk;      /* intervals per chunk; 0 selects the default; EWS_CHUNK_SEQUENTIAL: one chunk per sample */
   int32_t leaf;       /* EWS_DIAG_LEAF_* (0: the exact closed forms) */
   int32_t series_q;   /* series order q in [1, 40] of the series leaves (letters b_0..b_q, total order |m| <= q) */
 } ews_diag_desc;
