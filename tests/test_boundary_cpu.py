@@ -65,7 +65,7 @@ def test_c_abi_error_codes():
 def test_sequential_plan_selection_and_log_readout():
     """The per-sample sequential kernels: asked for by chunk = EWS_CHUNK_SEQUENTIAL or the log-prefix readout (real
     diagonal, depth 2, d <= 32, per-interval flows only), chosen by chunk 0 for B >= 128 and L <= 1025. Their
-    residual is one state checkpoint per 32 steps (lanes = 32 d rounded to 64, plus the d level-1 states), their
+    residual is one state checkpoint per 16 steps (lanes = 32 d rounded to 64, plus the d level-1 states), their
     workspace the per-sample parameter partials."""
     lib = nat.load()
     null = ctypes.c_void_p(0)
@@ -77,11 +77,11 @@ def test_sequential_plan_selection_and_log_readout():
     def al(x):
         return (x + 255) // 256 * 256
 
-    # c4's block: B = 256, L = 512 -> 16 blocks of (1024 + 32) floats per sample
-    assert sizes(batch=256, length=512) == (al(256 * 16 * 1056 * 4), al(256 * 32 * 4))
+    # c4's block: B = 256, L = 512 -> 32 blocks of (1024 + 32) floats per sample
+    assert sizes(batch=256, length=512) == (al(256 * 32 * 1056 * 4), al(256 * 32 * 4))
     assert sizes(batch=256, length=512, readout=4) == sizes(batch=256, length=512)
-    assert sizes(batch=2, length=100, chunk=-1) == (al(2 * 4 * 1056 * 4), al(2 * 32 * 4))
-    assert sizes(batch=2, length=100, chunk=-1, dim=5) == (al(2 * 4 * (192 + 5) * 4), al(2 * 5 * 4))
+    assert sizes(batch=2, length=100, chunk=-1) == (al(2 * 7 * 1056 * 4), al(2 * 32 * 4))
+    assert sizes(batch=2, length=100, chunk=-1, dim=5) == (al(2 * 7 * (192 + 5) * 4), al(2 * 5 * 4))
     # not chosen: few samples, long sequences, or an explicit chunk length (the chunk kernels' larger residual)
     assert sizes(batch=2, length=100)[0] != sizes(batch=2, length=100, chunk=-1)[0]
     assert sizes(batch=256, length=2000)[0] != sizes(batch=256, length=2000, chunk=-1)[0]

@@ -3,8 +3,8 @@ LogEWS prefix rows written straight from the scan, forward and gradients (path, 
 oracle (ews/layer.py:154-265 and 488-517 restated in oracle/ews_oracle.py, pinned in tests/test_oracle_*.py).
 
 Cases cover d = 32 (1,024 lanes per sample), narrow and odd widths (idle lanes, a padded pair row), lengths with a
-partial last checkpoint block and an exact multiple of it, uniform clocks (first-order coefficient models) and
-irregular clocks (exact per-step coefficients), a bfloat16 path, the series leaf, and the c4 block at its full
+partial last checkpoint block and an exact multiple of it, the three clock modes (every step equal: one set of
+coefficients; equal to float32 rounding: first-order models; irregular: exact per-step coefficients), a bfloat16 path, the series leaf, and the c4 block at its full
 shape (B = 256, L = 512, d = 32) through the LogEWS layer, where the default plan picks these kernels. Bars: forward
 <= 1e-5, gradients <= 1e-4, metric max|a-b| / max|b|.
 """
@@ -34,8 +34,10 @@ def relerr(a, b):
 def _data(B, L, K, seed, clock):
     rng = np.random.default_rng(seed)
     path = np.cumsum(rng.normal(size=(B, L, K)) / np.sqrt(K), 1).astype(np.float32)
-    if clock == "unit":
+    if clock == "unit":  # every step exactly 1: one set of coefficients
         th = np.broadcast_to(np.arange(L, dtype=np.float32), (B, L)).copy()
+    elif clock == "frac":  # k / L in float32: steps equal to rounding, first-order coefficient models
+        th = np.broadcast_to((np.arange(L) / L).astype(np.float32), (B, L)).copy()
     else:
         th = np.cumsum(rng.uniform(0.3, 1.5, size=(B, L)), 1).astype(np.float32)
     lam = rng.uniform(0.1, 2.0, size=K).astype(np.float32)
@@ -54,7 +56,9 @@ CASES = [
     # K, L, clock, log
     (32, 100, "unit", False),
     (32, 100, "unit", True),
-    (32, 65, "irregular", True),   # 64 steps: two full checkpoint blocks
+    (32, 65, "irregular", True),   # 64 steps: whole checkpoint blocks
+    (16, 120, "frac", False),
+    (32, 90, "frac", True),
     (8, 150, "irregular", False),
     (5, 70, "unit", True),         # odd width: a padded pair row
     (7, 33, "irregular", False),
