@@ -202,13 +202,23 @@ struct FwdLds {
   float v[2][CB * MAXK], h[2][CB], red[MAXW];
 };
 
-template <bool LOG, int MODE>
+// KC: the width as a compile-time constant (32: every lane active), 0 otherwise. A log row is written by the lanes
+// j <= k, one element each: level 1 by the diagonal lanes, the Lyndon coefficient (j, k) by the others.
+template <bool LOG, int MODE, int KC>
 __device__ __forceinline__ void fwd_body(const DiagArgs& a, FwdLds& sm, const Model& md, float lj, float lk) {
-  const int b = blockIdx.x, p = threadIdx.x, j = p / RS, k = p % RS, K = a.K, n = a.n_int, NT = blockDim.x;
-  const bool act = j < K && k < K;
+  const int b = blockIdx.x, p = threadIdx.x, j = p / RS, k = p % RS, n = a.n_int, NT = blockDim.x;
+  const int K = KC ? KC : a.K;
+  const int W = (KC && LOG) ? KC + KC * (KC - 1) / 2 : a.W;
+  const bool act = KC ? true : (j < K && k < K);
+  const int jj = act ? j : 0, kk = act ? k : 0;
+  const bool wr = LOG ? (act && j <= k) : act;  // the lane writes one element of every row
+  const int off = LOG ? (j == k ? jj : K + witt2(jj, kk, K)) : a.off2 + jj * K + kk;
+  const bool wr1 = !LOG && j == 0 && act;        // flat rows: level 1 from the first pair row
   float S1j = 0.0f, S1k = 0.0f, S2 = 0.0f;
   const int nb = seq_blocks(n);
   float* ckp = a.seqck ? a.seqck + (size_t)b * seq_ckpt_floats(K, n) : nullptr;
+  Co cu{};
+  if constexpr (MODE == CK_UNIFORM) cu = md.c0;
   Stage st;
   stage_load(a, b, 0, st);
   stage_store(a, st, sm.v[0], sm.h[0]);
@@ -217,35 +227,43 @@ __device__ __forceinline__ void fwd_body(const DiagArgs& a, FwdLds& sm, const Mo
     if (ckp) {
       float* cpt = ckp + (size_t)blk * (NT + K);
       cpt[p] = S2;
-      if (j == 0 && k < K) cpt[NT + k] = S1k;
+      if (j == 0 && act) cpt[NT + k] = S1k;
     }
     if (blk + 1 < nb) stage_load(a, b, blk + 1, st);
     const float* sv = sm.v[blk & 1];
     const float* sh = sm.h[blk & 1];
     const int ns = min(CB, n - blk * CB);
-    float* row = a.out + ((size_t)b * n + (size_t)blk * CB) * a.W;
-    for (int s = 0; s < ns; ++s, row += a.W) {
+    float* row = a.out + ((size_t)b * n + (size_t)blk * CB) * W;
+    auto step = [&](int s) {
       Co c, cd;
       Nd cn;
-      coef_at<MODE>(a, md, lj, lk, sh[s], c, cd, cn);
-      const float vj = act ? sv[s * K + j] : 0.0f;
-      const float vk = act ? sv[s * K + k] : 0.0f;
+      if constexpr (MODE == CK_UNIFORM) c = cu;
+      else coef_at<MODE>(a, md, lj, lk, sh[s], c, cd, cn);
+      const float vj = act ? sv[s * K + jj] : 0.0f;
+      const float vk = act ? sv[s * K + kk] : 0.0f;
       fstep(c, vj, vk, S1j, S1k, S2);
+      float* r = row + (size_t)s * W;
       if constexpr (!LOG) {
-        if (act) row[a.off2 + j * K + k] = S2;
-        if (j == 0 && k < K) row[a.off1 + k] = S1k;
-        if (a.lvl0 && p == 0) row[0] = 1.0f;
+        if (wr) r[off] = S2;
+        if (wr1) r[a.off1 + k] = S1k;
+        if (a.lvl0 && p == 0) r[0] = 1.0f;
       } else {
-        if (j == 0 && k < K) row[k] = S1k;
-        if (act && j < k) row[K + witt2(j, k, K)] = fmaf(-0.5f * S1j, S1k, S2);
+        if (wr) r[off] = j == k ? S1k : fmaf(-0.5f * S1j, S1k, S2);
       }
+    };
+    if constexpr (LOG && KC) {  // fixed row length: the unrolled steps store at immediate offsets
+#pragma unroll
+      for (int s = 0; s < CB; ++s)
+        if (s < ns) step(s);
+    } else {
+      for (int s = 0; s < ns; ++s) step(s);
     }
     if (blk + 1 < nb) stage_store(a, st, sm.v[(blk + 1) & 1], sm.h[(blk + 1) & 1]);
     lds_sync();  // the checkpoint and row stores need no ordering here
   }
 }
 
-template <bool LOG>
+template <bool LOG, int KC>
 __global__ __launch_bounds__(1024) void k_seq_fwd(DiagArgs a) {
   __shared__ FwdLds sm;
   const int p = threadIdx.x, j = p / RS, k = p % RS;
@@ -256,20 +274,20 @@ __global__ __launch_bounds__(1024) void k_seq_fwd(DiagArgs a) {
   md.hbar = ck.hbar;
   Nd nd;
   if (ck.mode != CK_EXACT) eval_co(a, lj, lk, ck.hbar, md.c0, md.c1, nd);
-  if (ck.mode == CK_UNIFORM) fwd_body<LOG, CK_UNIFORM>(a, sm, md, lj, lk);
-  else if (ck.mode == CK_LINEAR) fwd_body<LOG, CK_LINEAR>(a, sm, md, lj, lk);
-  else fwd_body<LOG, CK_EXACT>(a, sm, md, lj, lk);
+  if (ck.mode == CK_UNIFORM) fwd_body<LOG, CK_UNIFORM, KC>(a, sm, md, lj, lk);
+  else if (ck.mode == CK_LINEAR) fwd_body<LOG, CK_LINEAR, KC>(a, sm, md, lj, lk);
+  else fwd_body<LOG, CK_EXACT, KC>(a, sm, md, lj, lk);
 }
 
 // ------------------------------------------------------------------------------------------------ backward
 struct BwdLds {
   float v[CB * MAXK], h[CB], red[MAXW];
-  float s1[CB + 1][MAXK];        // level 1 before step s of the block (row s); row ns: after the block
-  float col[Q][MAXW][RS];        // column parts of dv: per wavefront, its two rows summed
-  float rowp[Q][MAXK];           // row parts of dv
-  float dhw[Q][MAXW];            // clock-step cotangent per wavefront
-  float dv[CB][MAXK], dh[CB];    // dv / dh of the block's steps
-  float next[MAXK], nexth;       // dv / dh of the step after the block (0 after the last)
+  float s1[CB + 1][MAXK];          // level 1 before step s of the block (row s); row ns: after the block
+  float col[CB][MAXW][RS];         // column parts of dv: per wavefront, its two rows summed
+  float rowp[CB][MAXK];            // row parts of dv
+  float dhw[CB][MAXW];             // clock-step cotangent per wavefront
+  float dv[CB][MAXK], dh[CB];      // dv / dh of the block's steps
+  float next[2][MAXK], nexth[2];   // dv / dh of the step after the block (0 after the last), by block parity
   float gcol[MAXK][RS], grow[MAXK];
 };
 
@@ -304,13 +322,14 @@ __device__ __forceinline__ void bwd_body(const DiagArgs& a, BwdLds& sm, float* s
   const int jj = act ? j : 0, kk = act ? k : 0;
   const int off_g2 = LOG ? (jj == kk ? 0 : K + witt2(min(jj, kk), max(jj, kk), K)) : a.off2 + jj * K + kk;
   const int off_g1 = LOG ? jj : a.off1 + jj;
-  const float m_g = (act && (!LOG || j != k)) ? 1.0f : 0.0f;   // the lane has a level-2 cotangent
-  const float m_u = (act && (!LOG || j < k)) ? 1.0f : 0.0f;    // ... that feeds its own state (log: j < k)
+  // log rows: G' = -G/2 for the lanes j != k (the level-1 term of the log) and g2 = -2 G' for j < k
+  const float m_g = (act && (!LOG || j != k)) ? (LOG ? -0.5f : 1.0f) : 0.0f;
+  const float m_u = (act && (!LOG || j < k)) ? (LOG ? -2.0f : 1.0f) : 0.0f;
   const float m_row = rowl ? 1.0f : 0.0f;
   const float m_act = act ? 1.0f : 0.0f;
   const float m_k0 = (k == 0 && rowl) ? 1.0f : 0.0f;
-  if (p < MAXK) sm.next[p] = 0.0f;
-  if (p == 0) sm.nexth = 0.0f;
+  if (p < MAXK) sm.next[(nb - 1 + 1) & 1][p] = 0.0f;
+  if (p == 0) sm.nexth[(nb - 1 + 1) & 1] = 0.0f;
   // the level-1 rows past the last channel stay zero (read by the padded lanes of narrow widths)
   for (int e = p; e < (CB + 1) * MAXK; e += NT) (&sm.s1[0][0])[e] = 0.0f;
   // prologue: the last block's inputs, checkpoint and last cotangent group
@@ -368,7 +387,7 @@ __device__ __forceinline__ void bwd_body(const DiagArgs& a, BwdLds& sm, float* s
       }
       if (s < ns) {
         const float* grw = sg + (g & 1) * Q * W + (s - g * Q) * W;
-        const float G = grw[off_g2] * m_g;
+        const float G = grw[off_g2] * m_g;  // log rows: -G/2
         const float g2 = LOG ? G * m_u : G;
         const float g1 = grw[off_g1] * m_row;
         float h = 0.0f;
@@ -391,19 +410,17 @@ __device__ __forceinline__ void bwd_body(const DiagArgs& a, BwdLds& sm, float* s
         const float u = L2 * vk;
         const float t = u * c.pk;
         float xs = t;
-        if constexpr (LOG) xs = fmaf(-0.5f * G, sm.s1[s + 1][kk], t);
+        if constexpr (LOG) xs = fmaf(G, sm.s1[s + 1][kk], t);
         const float X = row_sum(xs);
         const float Y = row_sum(u * dm);
         const float gc = lam1 + g1 + X;
         const float colw = add_xor32(L2 * fmaf(c.pk, cj, c.D * vj));
-        const int qs = s % Q;
-        if ((p & 63) < RS) sm.col[qs][w][k] = colw;
-        if (k == 0 && rowl) sm.rowp[qs][j] = fmaf(c.pj, gc, Y);
-        if constexpr (MODE == CK_UNIFORM) {
+        if ((p & 63) < RS) sm.col[s][w][k] = colw;
+        if (k == 0 && rowl) sm.rowp[s][j] = fmaf(c.pj, gc, Y);
+        if constexpr (MODE == CK_UNIFORM) {  // sum_t t v_j = phi_k sum_t u v_j with phi_k constant: no aQ
           aL = fmaf(L2, S2p[s], aL);
           aD = fmaf(u, vj, aD);
           aP = fmaf(u, cj, aP);
-          aQ = fmaf(t, vj, aQ);
           aR = fmaf(gc, S1pj, aR);
           aG = fmaf(gc, vj, aG);
         } else if constexpr (MODE == CK_LINEAR) {
@@ -431,53 +448,51 @@ __device__ __forceinline__ void bwd_body(const DiagArgs& a, BwdLds& sm, float* s
           dh = fmaf(-t * vj, cd.pj, dh);
           dh = fmaf(m_k0 * gc, fmaf(S1pj, cd.rj, vj * cd.pj), dh);
           dh = add_xor32(row_sum(dh));
-          if ((p & 63) == 0) sm.dhw[qs][w] = dh;
+          if ((p & 63) == 0) sm.dhw[s][w] = dh;
         }
         lam1 = c.rj * gc;
         lam2 = c.L * L2;
       }
-      if (s % Q == 0) {  // group end: the next group's rows landed; reduce this group's staged partials
-        dma_sync();
-        for (int e = p; e < Q * K; e += NT) {
-          const int qq = e / K, m = e - qq * K, ss = s + qq;
-          if (ss < ns) {
-            float acc = sm.rowp[qq][m];
-            for (int ww = 0; ww < nw; ++ww) acc += sm.col[qq][ww][m];
-            sm.dv[ss][m] = acc;
-          }
-        }
-        if constexpr (DH) {
-          if (p < Q && s + p < ns) {
-            float acc = 0.0f;
-            for (int ww = 0; ww < nw; ++ww) acc += sm.dhw[p][ww];
-            sm.dh[s + p] = acc;
-          }
-        }
-        lds_sync();
+      if (s % Q == 0) dma_sync();  // group end: the next group's rows landed (and this group's partials)
+    }
+    // dv / dh of the block's steps from the staged partials
+    for (int e = p; e < ns * K; e += NT) {
+      const int ss = e / K, m = e - ss * K;
+      float acc = sm.rowp[ss][m];
+      for (int ww = 0; ww < nw; ++ww) acc += sm.col[ss][ww][m];
+      sm.dv[ss][m] = acc;
+    }
+    if constexpr (DH) {
+      for (int ss = p; ss < ns; ss += NT) {
+        float acc = 0.0f;
+        for (int ww = 0; ww < nw; ++ww) acc += sm.dhw[ss][ww];
+        sm.dh[ss] = acc;
       }
     }
+    lds_sync();
     // knots blk*CB + 1 .. blk*CB + ns: dX_t = dv_{t-1} - dv_t (and dtheta_t = dh_{t-1} - dh_t), since
     // v_t = X_{t+1} - X_t; knot 0 gets -dv_0
     const size_t kb = (size_t)b * a.L + (size_t)blk * CB;
+    const int nx = (blk + 1) & 1;  // written by the block after this one (zeros for the last)
     for (int e = p; e < ns * K; e += NT) {
       const int s = 1 + e / K, m = e - (s - 1) * K;
-      const float hi = s < ns ? sm.dv[s][m] : sm.next[m];
+      const float hi = s < ns ? sm.dv[s][m] : sm.next[nx][m];
       a.dpath[(kb + s) * a.d + m] = sm.dv[s - 1][m] - hi;
     }
     if constexpr (DH) {
-      for (int s = 1 + p; s <= ns; s += NT) a.dclock[kb + s] = sm.dh[s - 1] - (s < ns ? sm.dh[s] : sm.nexth);
+      for (int s = 1 + p; s <= ns; s += NT) a.dclock[kb + s] = sm.dh[s - 1] - (s < ns ? sm.dh[s] : sm.nexth[nx]);
     }
     if (blk == 0) {
       for (int m = p; m < K; m += NT) a.dpath[kb * a.d + m] = -sm.dv[0][m];
       if (DH && p == 0) a.dclock[kb] = -sm.dh[0];
     }
-    lds_sync();
-    if (p < K) sm.next[p] = sm.dv[0][p];
-    if (DH && p == 0) sm.nexth = sm.dh[0];
+    // for the block before this one (read after its own barriers; the other parity is read above)
+    if (p < K) sm.next[blk & 1][p] = sm.dv[0][p];
+    if (DH && p == 0) sm.nexth[blk & 1] = sm.dh[0];
   }
   // parameter partials of the sample: dlambda_m = -(sum over the coefficients of channel m of h c'(x) cot(c))
   float grow, gcol;
-  const float q = row_sum(aQ);  // the phi_j cotangent's per-lane part
+  float q = row_sum(aQ);  // the phi_j cotangent's per-lane part
   if constexpr (MODE == CK_EXACT) {
     grow = aL + aD;
     gcol = aL + aDy + aP;
@@ -487,6 +502,7 @@ __device__ __forceinline__ void bwd_body(const DiagArgs& a, BwdLds& sm, float* s
     Nd nd;
     eval_co(a, lj, lk, md.hbar, c, cd, nd);
     const float hs = MODE == CK_UNIFORM ? md.hbar : 1.0f;
+    if constexpr (MODE == CK_UNIFORM) q = row_sum(c.pk * aD);
     grow = hs * fmaf(aL, nd.L, aD * nd.Dxy);
     gcol = hs * fmaf(aL, nd.L, fmaf(aD, nd.Dy, aP * nd.pk));
     grow = fmaf(m_k0 * hs, fmaf(aR, nd.rj, (aG - q) * nd.pj), grow);
@@ -544,8 +560,14 @@ __global__ __launch_bounds__(256) void k_seq_params(DiagArgs a) {
 
 int seq_forward(const DiagArgs& a, hipStream_t st) {
   const dim3 grid(a.B), blk(seq_threads(a.K));
-  if (a.readout == EWS_READOUT_LOGPREFIX) hipLaunchKernelGGL(seq::k_seq_fwd<true>, grid, blk, 0, st, a);
-  else hipLaunchKernelGGL(seq::k_seq_fwd<false>, grid, blk, 0, st, a);
+  const bool log = a.readout == EWS_READOUT_LOGPREFIX;
+  if (a.K == 32) {
+    if (log) hipLaunchKernelGGL((seq::k_seq_fwd<true, 32>), grid, blk, 0, st, a);
+    else hipLaunchKernelGGL((seq::k_seq_fwd<false, 32>), grid, blk, 0, st, a);
+  } else {
+    if (log) hipLaunchKernelGGL((seq::k_seq_fwd<true, 0>), grid, blk, 0, st, a);
+    else hipLaunchKernelGGL((seq::k_seq_fwd<false, 0>), grid, blk, 0, st, a);
+  }
   return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 
