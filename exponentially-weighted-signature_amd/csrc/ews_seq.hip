@@ -46,11 +46,13 @@ constexpr int Q = 8;                  // steps of column partials staged before 
 constexpr int MAXW = MAXK * RS / 64;  // wavefronts per workgroup at d = 32
 static_assert(CB <= RS, "one staged increment per lane");
 
-// DPP row rotation inside rows of 16 lanes (update_dpp with a zero old value folds into the add as v_add_f32_dpp);
-// ds_swizzle xor 16 inside groups of 32 lanes
+// DPP row rotation inside rows of 16 lanes (update_dpp with a zero old value folds into the add as v_add_f32_dpp)
 #define EWS_SEQ_ROR(v, n) __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x120 + (n), 0xf, 0xf, true))
-__device__ __forceinline__ float swap16(float v) {
-  return __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(v), 0x401F));
+// value of lane l ^ 16 added to lane l's: v_permlane16_swap exchanges the odd 16-lane rows of one copy with the even
+// rows of the other, so the two results hold each lane's and its partner's value (a VALU op, no LDS round trip)
+__device__ __forceinline__ float add_xor16(float v) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
 }
 // sum over the 32 lanes of a pair row, in every lane of the row
 __device__ __forceinline__ float row_sum(float v) {
@@ -58,7 +60,7 @@ __device__ __forceinline__ float row_sum(float v) {
   v += EWS_SEQ_ROR(v, 4);
   v += EWS_SEQ_ROR(v, 2);
   v += EWS_SEQ_ROR(v, 1);
-  return v + swap16(v);
+  return add_xor16(v);
 }
 
 // Coefficients of the lane's pair (j, k) at one clock step.
