@@ -559,14 +559,24 @@ def bench_token(args):
     }
 
 
-def algorithmic_bytes(B, L, d, W, s_in=4):
-    """Compulsory HBM bytes per launch of each pass (per-interval figures times B (L-1) intervals)."""
+def algorithmic_bytes(B, L, d, W, s_in=4, split=False):
+    """Compulsory HBM bytes per launch of each pass (per-interval figures times B (L-1) intervals). split: the c2
+    backward without the clock gradient, whose pass 0 is the full per-step local adjoint (reads the cotangent rows,
+    writes every step's dv) and pass 2 the closed-form carry part (reads the inputs and the local dv, writes the
+    total dv and the interior knot gradients); otherwise pass 0 is the chunk-local summary adjoint and pass 2 the full
+    adjoint, both reading the cotangent rows."""
     n = B * (L - 1)
     D = W - 1
+    if split:
+        local = n * (4 * W + s_in * (d + 1) + 4 * d)
+        full = n * (s_in * (d + 1) + 4 * d + 8 * d)
+    else:
+        local = n * (4 * W + s_in * (d + 1))                   # read cotangent rows + inputs
+        full = n * (4 * W + 2 * s_in * (d + 1))                # read cotangent rows + inputs, write dv/dh
     return {
         "chunk_output": n * (s_in * (d + 1) + 4 * W),          # read path+clock, write the prefix rows
-        "chunk_adjoint_full": n * (4 * W + 2 * s_in * (d + 1)),  # read cotangent rows + inputs, write dv/dh
-        "chunk_adjoint_local": n * (4 * W + s_in * (d + 1)),   # read cotangent rows + inputs
+        "chunk_adjoint_full": full,
+        "chunk_adjoint_local": local,
         "chunk_summary": n * s_in * (d + 1),
         "knot_grads": n * 2 * 4 * (d + 1),
         "fwd_total": n * (s_in * (d + 1) + 4 * D),             # compulsory forward bytes
@@ -574,12 +584,13 @@ def algorithmic_bytes(B, L, d, W, s_in=4):
     }
 
 
-# kernel of each c2 pass whose HBM traffic the PMC summary records
+# kernel of each c2 pass whose HBM traffic the PMC summary records: the headline backward (no clock gradient) runs
+# the full local adjoint in pass 0 and the closed-form carry part in pass 2
 PASS_KERNELS = {
     "chunk_summary": "pairs::k_fwd<false, false>",
     "chunk_output": "pairs::k_fwd<true, false>",
-    "chunk_adjoint_local": "pairs::k_bwd_local<false>",
-    "chunk_adjoint_full": "pairs::k_bwd_full<false, false>",
+    "chunk_adjoint_local": "pairs::k_bwd_full<false, false, 1>",
+    "chunk_adjoint_full": "pairs::k_bwd_carry<false>",
 }
 PMC_SUMMARY = os.path.join(ROOT, "profiles", "c2_fwd_bwd_pmc_traffic.md")
 
@@ -859,17 +870,31 @@ def main():
                        "front_fused_gbs": round(fb / (fused * 1e-3) / 1e9, 1),
                        "front_check_path_relerr": float((path - ref_path).abs().max() / ref_path.abs().max())}
     dominant = max((k for k in pass_ms if not k.startswith("front")), key=pass_ms.get)
-    ab = algorithmic_bytes(B, L, d, W)
+    ab = algorithmic_bytes(B, L, d, W, split=not args.clock_grad)
     dom_bytes = ab.get(dominant)
     roof = None
     if dom_bytes is not None:
         achieved = dom_bytes / (pass_ms[dominant] * 1e-3) / 1e9
-        traffic, source = pmc_traffic(dominant)
+        traffic, source = pmc_traffic(dominant) if not args.clock_grad else (None, None)
         roof = {"bound": "hbm", "kernel": dominant, "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
                 "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
                 "traffic": None if traffic is None else round(traffic), "algorithmic_bytes": dom_bytes}
         if source is not None:
             roof["traffic_source"] = source
+    clock_grad_ms = None
+    if not args.clock_grad and not nfr:
+        # the same step with the clock gradient as well (a learned clock): its terms run in the backward
+        dclock_ptr = dclock.data_ptr()
+        for _ in range(2):
+            step()
+        torch.cuda.synchronize()
+        start.record()
+        for _ in range(args.steps):
+            step()
+        end.record()
+        torch.cuda.synchronize()
+        clock_grad_ms = start.elapsed_time(end) / args.steps
+        dclock_ptr = None
     steps_per_s = B * (L - 1) / (ms_per_step * 1e-3)
     fwdbwd_bytes = ab["fwd_total"] + ab["bwd_total"]
     result = {
@@ -898,6 +923,8 @@ def main():
         "wall_s": round(t_wall, 3),
     }
     result.update(front_extra)
+    if clock_grad_ms is not None:
+        result["clock_grad_ms_per_step"] = round(clock_grad_ms, 4)
     if check_rows is not None:
         result["check_forward_relerr_vs_f64"] = check_rows
         result["check_path_grad_relerr_vs_f64"] = check_grad
