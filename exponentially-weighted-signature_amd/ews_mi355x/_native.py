@@ -68,7 +68,12 @@ EXPORTED = (
     "ews_token_scan_workspace_bytes",
     "ews_token_scan",
     "ews_token_scan_backward",
+    "ews_jordan_local_terms",
+    "ews_jordan_workspace_bytes",
+    "ews_jordan_local_terms_backward",
 )
+
+JORDAN_KINDS = {"real": 0, "complex": 1}
 
 CLOCK_MODES = {"time": 0, "blended_variation": 1, "blended_learn": 1, "blended_quad_variation": 2,
                "token_gated": 3, "clamped_gate": 4}
@@ -113,6 +118,17 @@ class DenseDesc(ctypes.Structure):
         ("vl_expm", ctypes.c_int32),
         ("vl_mode", ctypes.c_int32),
         ("chen_expm", ctypes.c_int32),
+    ]
+
+
+class JordanDesc(ctypes.Structure):
+    _fields_ = [
+        ("batch", ctypes.c_int32),
+        ("length", ctypes.c_int32),
+        ("dim", ctypes.c_int32),
+        ("depth", ctypes.c_int32),
+        ("kind", ctypes.c_int32),
+        ("size", ctypes.c_int32),
     ]
 
 
@@ -281,6 +297,13 @@ def load():
     lib.ews_lift_forward.restype = i32
     lib.ews_lift_backward.argtypes = [ftp, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp]
     lib.ews_lift_backward.restype = i32
+    jdp = ctypes.POINTER(JordanDesc)
+    lib.ews_jordan_local_terms.argtypes = [jdp, vp, vp, vp, vp, vp]
+    lib.ews_jordan_local_terms.restype = i32
+    lib.ews_jordan_workspace_bytes.argtypes = [jdp]
+    lib.ews_jordan_workspace_bytes.restype = sz
+    lib.ews_jordan_local_terms_backward.argtypes = [jdp, vp, vp, vp, vp, vp, vp, vp, vp, vp]
+    lib.ews_jordan_local_terms_backward.restype = i32
     _lib = lib
     return lib
 

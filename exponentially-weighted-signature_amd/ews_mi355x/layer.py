@@ -19,11 +19,13 @@ ews/core/kernels/combine.py:37-63):
                                                      van_loan_expm and reweighting_mode
         (also planes / diagonals at depth 3, or      flows M_t of chen_expm evaluated in the kernels, MFMA Chen
         with chen_expm other than "exact")           mode products
-    Jordan chains, leaf "jordan_closed(_tables)";    dense kernels, series leaf of order >= 24: the exact local
-    block-diagonal A, leaf "block_series";           integrals to float32 while clock step x ||A||_1 <= 4 (an
-    planes, "plane_closed" with approximate flows    error past it), flows of chen_expm (exact for jordan_flows);
-                                                     "block_series" of an order whose truncation is visible at the
-                                                     call's largest step raises (its level 2 is the order-q series)
+    Jordan chains, leaf "jordan_closed(_tables)";    the chains' closed-form local terms at any step (float64
+    planes, "plane_closed" with approximate flows    tables on the device), flows of chen_expm (exact for
+                                                     jordan_flows), the dense combine (d <= 16, at most 8 chains)
+    block-diagonal A, leaf "block_series"            dense kernels, series leaf of order >= 24: the exact level 1
+                                                     to float32 while clock step x ||A||_1 <= 4 (an error past it);
+                                                     an order whose truncation is visible at the call's largest step
+                                                     raises (its level 2 is the order-q series)
     anything else                                    NotImplementedError
 """
 
@@ -205,10 +207,17 @@ class EWS(torch.nn.Module):
         A = self.A_param().to(torch.float32) * torch.as_tensor(a_scale, dtype=torch.float32, device=path.device)
         if engine == "dense":
             chen = "exact" if self.jordan_flows else self.chen_expm  # closed-form chain flows are exact
-            if self.leaf in JORDAN_LEAVES or self.leaf in ("block_series", "plane_closed"):
-                # Jordan closed forms and the block-series leaf (exact level 1, blockwise series of order series_q
-                # at level 2) on general blocks: the series kernels at order >= EXACT_Q reproduce their exact
-                # integrals to float32 while the series argument stays small (checked here, loudly)
+            if self.leaf in JORDAN_LEAVES or (self.leaf == "plane_closed" and self.structure == "planes"):
+                # the chains' closed-form local terms at any step (a rotation plane is a complex chain of one
+                # coordinate), the flows of chen_expm, the dense combine
+                kind, size = jordan_chains_of(self.A_param) if self.leaf in JORDAN_LEAVES else ("complex", 2)
+                return ops.jordan_scan(path.to(torch.float32), clock.to(torch.float32),
+                                       A.to(path.device).contiguous(), self.N, kind, size, self._flow_mode(readout),
+                                       readout, level0, chen_expm=chen)
+            if self.leaf in ("block_series", "plane_closed"):
+                # the block-series leaf (exact level 1, blockwise series of order series_q at level 2) on general
+                # blocks: the series kernels at order >= EXACT_Q reproduce its exact level 1 to float32 while the
+                # series argument stays small (checked here, loudly)
                 hmax = float((clock[..., 1:] - clock[..., :-1]).abs().max()) if clock.shape[-1] > 1 else 0.0
                 anorm = float(A.abs().sum(0).max())
                 if hmax * anorm > EXACT_MAX_STEP:

@@ -272,6 +272,82 @@ def dense_combine_backward(levels, flows, grad_out, N, readout="prefix", level0=
     return gl, gf
 
 
+# ---------------------------------------------------------------------------------------------- Jordan chains
+def _jordan_desc(B, L, d, N, kind, size):
+    return nat.JordanDesc(int(B), int(L), int(d), int(N), nat.JORDAN_KINDS[kind], int(size))
+
+
+class JordanScan(torch.autograd.Function):
+    """out = EWS readout of (path, clock) under uniform Jordan chains A (leaf jordan_closed / jordan_closed_tables,
+    ews/core/kernels/jordan_engine.py:324-353): the chains' exact local terms (ews_jordan_local_terms), the flows of
+    chen_expm under the reweighting mode (ews_dense_local_terms), the dense combine (ews_dense_combine). The
+    backward runs the combine's adjoint, then the local terms' and the flows' adjoints, and sums them."""
+
+    @staticmethod
+    def forward(ctx, path, clock, A, N, kind, size, flow_mode, readout, level0, chunk, chen_expm):
+        lib = nat.load()
+        _check_dense(path, clock, A)
+        path, clock, A = path.contiguous(), clock.contiguous(), A.contiguous()
+        B, L, d = path.shape
+        dev = path.device
+        jd = _jordan_desc(B, L, d, N, kind, size)
+        D = d + (d * d if N == 2 else 0)
+        levels = torch.empty((B, L - 1, D), device=dev, dtype=torch.float32)
+        nat.check(lib.ews_jordan_local_terms(ctypes.byref(jd), path.data_ptr(), clock.data_ptr(), A.data_ptr(),
+                                             levels.data_ptr(), _stream_handle(dev)), "ews_jordan_local_terms")
+        fleaf = DenseLeaf("series", q=0, chen_expm=chen_expm)
+        _, flows = dense_local_terms(path, clock, A, 1, 0, flow_mode, leaf=fleaf)
+        out = dense_combine(levels, flows, N, readout, level0, chunk)
+        ctx.save_for_backward(path, clock, A, levels, flows)
+        ctx.cfg = (N, kind, size, flow_mode, readout, level0, chunk, fleaf)
+        return out
+
+    @staticmethod
+    def backward(ctx, gout):
+        lib = nat.load()
+        path, clock, A, levels, flows = ctx.saved_tensors
+        N, kind, size, flow_mode, readout, level0, chunk, fleaf = ctx.cfg
+        B, L, d = path.shape
+        dev = path.device
+        gl, gf = dense_combine_backward(levels, flows, gout.to(torch.float32).contiguous(), N, readout, level0,
+                                        chunk)
+        need_clock = ctx.needs_input_grad[1]
+        jd = _jordan_desc(B, L, d, N, kind, size)
+        gpath = torch.empty_like(path)
+        gclock = torch.empty_like(clock) if need_clock else None
+        gA = torch.empty_like(A)
+        ws = torch.empty(int(lib.ews_jordan_workspace_bytes(ctypes.byref(jd))), device=dev, dtype=torch.uint8)
+        nat.check(lib.ews_jordan_local_terms_backward(ctypes.byref(jd), path.data_ptr(), clock.data_ptr(),
+                                                      A.data_ptr(), gl.data_ptr(), gpath.data_ptr(),
+                                                      gclock.data_ptr() if need_clock else None, gA.data_ptr(),
+                                                      ws.data_ptr(), _stream_handle(dev)),
+                  "ews_jordan_local_terms_backward")
+        # the flows' share: the leaf-and-flows adjoint with a zero level cotangent
+        fdesc = make_dense_desc(B, L, d, 1, 0, flow_mode, "prefix", False, 0, fleaf)
+        zl = torch.zeros((B, L - 1, d), device=dev, dtype=torch.float32)
+        fpath = torch.empty_like(path)
+        fclock = torch.empty_like(clock) if need_clock else None
+        fA = torch.empty_like(A)
+        fws = torch.empty(int(lib.ews_dense_backward_workspace_bytes(ctypes.byref(fdesc))), device=dev,
+                          dtype=torch.uint8)
+        nat.check(lib.ews_dense_local_terms_backward(ctypes.byref(fdesc), path.data_ptr(), clock.data_ptr(),
+                                                     A.data_ptr(), zl.data_ptr(), gf.contiguous().data_ptr(),
+                                                     fpath.data_ptr(), fclock.data_ptr() if need_clock else None,
+                                                     fA.data_ptr(), fws.data_ptr(), _stream_handle(dev)),
+                  "ews_dense_local_terms_backward")
+        gA += fA
+        if need_clock:
+            gclock += fclock
+        return gpath, gclock, gA, None, None, None, None, None, None, None, None
+
+
+def jordan_scan(path, clock, A, N, kind, size, flow_mode="per_interval", readout="prefix", level0=True, chunk=0,
+                chen_expm="exact"):
+    """kind "real" (chain sizes 1-4) or "complex" (sizes 2, 4, 6, 8; size 2 = rotation planes)."""
+    return JordanScan.apply(path, clock, A, int(N), kind, int(size), flow_mode, readout, bool(level0), int(chunk),
+                            chen_expm)
+
+
 # ---------------------------------------------------------------------------------------------- log-signature
 class LogRows(torch.autograd.Function):
     """Compressed log of EWS state rows (B, R, level0 + D) with the LogEWS readout (ews/layer.py:488-517):

@@ -237,6 +237,45 @@ int ews_token_scan_backward(const ews_dense_desc* desc, const int32_t* token_ids
                             float* grad_P_cache, float* grad_D_cache, void* workspace, ews_stream_t stream);
 
 /* ---------------------------------------------------------------------------------------------------------
+ * Jordan chains: the closed-form local terms of the leaves jordan_closed / jordan_closed_tables
+ * (ews/core/kernels/jordan_engine.py:324-353) for a block-diagonal A of uniform Jordan chains, exact at any clock
+ * step: a real chain of size n is lambda I + eps Nil (lambda = A[f][f], eps = A[f][f+1]); a complex chain of size 2k
+ * is c = a + ib (a = A[f][f], b = A[f+1][f]) on the coordinates v_2i + i v_2i+1 with eps = A[f][f+2] coupling them.
+ * Level 1 is sum_p (-h)^p phi^(p)(-h c) / p! (eps Nil)^p v and level 2 the pair integrals' derivatives
+ * D^(p,q) (jordan_engine.py:175-321), evaluated in float64 on the device. The flows and the combine are those of
+ * the dense family (ews_dense_local_terms / ews_dense_combine and their backward).
+ * --------------------------------------------------------------------------------------------------------- */
+#define EWS_JORDAN_REAL 0    /* chain sizes 2, 3, 4 (size 1: a real diagonal) */
+#define EWS_JORDAN_COMPLEX 1 /* chain sizes 4, 6, 8: 2, 3, 4 complex coordinates (size 2: rotation planes, the
+                                closed forms of ews/core/kernels/plane_engine.py:134-152) */
+
+typedef struct ews_jordan_desc {
+  int32_t batch;  /* B >= 1 */
+  int32_t length; /* L >= 2 knots */
+  int32_t dim;    /* d = chains x size, d <= 16, at most 8 chains */
+  int32_t depth;  /* N in {1, 2} */
+  int32_t kind;   /* EWS_JORDAN_REAL or EWS_JORDAN_COMPLEX */
+  int32_t size;   /* chain size in real coordinates */
+} ews_jordan_desc;
+
+/* Local terms: path (B, L, d) f32, clock (B, L) f32, A (d, d) f32 row-major (reference sign) -> levels
+ * (B, L-1, d [+ d*d]) f32 packed (level 1, then level 2 row-major; ews/core/chen_scan.py:33-46). Replaces
+ * jordan_engine.local_terms (ews/core/kernels/jordan_engine.py:324-353) behind ews/core/leaf.py:177-198. */
+int ews_jordan_local_terms(const ews_jordan_desc* desc, const float* path, const float* clock, const float* A,
+                           float* levels, ews_stream_t stream);
+
+/* Scratch of ews_jordan_local_terms_backward: per-interval dv, dh and chain-parameter partials. */
+size_t ews_jordan_workspace_bytes(const ews_jordan_desc* desc);
+
+/* Backward: grad_levels (B, L-1, d [+ d*d]) -> grad_path (B, L, d), grad_clock (B, L) (may be NULL) and grad_A
+ * (d, d), all written (not accumulated); grad_A is nonzero only at the entries the chains are read from. The
+ * per-interval parameter partials are summed in a fixed order (deterministic). Replaces JAX autodiff through
+ * jordan_engine.local_terms. */
+int ews_jordan_local_terms_backward(const ews_jordan_desc* desc, const float* path, const float* clock,
+                                    const float* A, const float* grad_levels, float* grad_path, float* grad_clock,
+                                    float* grad_A, void* workspace, ews_stream_t stream);
+
+/* ---------------------------------------------------------------------------------------------------------
  * Log-signature readout of LogEWS (ews/layer.py:440-556): per state row the truncated tensor log and its
  * coefficients at the Lyndon words (signax.signature_to_logsignature), then the readout (log-then-pool).
  * --------------------------------------------------------------------------------------------------------- */

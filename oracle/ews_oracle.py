@@ -291,6 +291,37 @@ def block_series_local_terms(v, dtheta, A, N, q):
     return levels
 
 
+def exact_local_terms(v, dtheta, A, N):
+    """Exact local levels 1 and 2 of each interval's linear segment under any generator A, from one augmented
+    exponential per interval. On the segment the state obeys S1' = -h A S1 + v and S2' = -h (A (+) A) S2 + S1 (x) v
+    (S1(0) = S2(0) = 0; A (+) A = A (x) I + I (x) A acts on both factors), so with
+    Z = [[-h (A (+) A), I (x) v, 0], [0, -h A, v], [0, 0, 0]] the last column of expm(Z) holds (S2(1), S1(1), 1):
+    S1 = int_0^1 e^{-(1-s) h A} v ds and S2 = int_{s<t} e^{-(1-s) h A} v (x) e^{-(1-t) h A} v, the integrals every
+    closed-form leaf evaluates (plane_engine.py:134-152, jordan_engine.py:1-15). The oracle of the Jordan leaves
+    (jordan_closed / jordan_closed_tables), by a route independent of their derivative tables."""
+    n, d = v.shape
+    if N > 2:
+        raise NotImplementedError("exact local terms are built for depths 1 and 2")
+    eye = torch.eye(d, dtype=A.dtype)
+    size = d * d + d + 1 if N == 2 else d + 1
+    Z = torch.zeros((n, size, size), dtype=A.dtype)
+    hA = dtheta[:, None, None] * A[None]
+    o1 = d * d if N == 2 else 0
+    Z[:, o1:o1 + d, o1:o1 + d] = -hA
+    Z[:, o1:o1 + d, -1] = v
+    if N == 2:
+        Z[:, :d * d, :d * d] = -(torch.einsum("nab,cd->nacbd", hA, eye) +
+                                 torch.einsum("ab,ncd->nacbd", eye, hA)).reshape(n, d * d, d * d)
+        # (I (x) v) maps S1 to S1 (x) v: row (a, b), column a carries v_b
+        Iv = torch.einsum("ac,nb->nabc", eye, v).reshape(n, d * d, d)
+        Z[:, :d * d, d * d:d * d + d] = Iv
+    E = torch.linalg.matrix_exp(Z)[:, :, -1]
+    lvl1 = E[:, o1:o1 + d]
+    if N == 1:
+        return [lvl1]
+    return [lvl1, E[:, :d * d].reshape(n, d, d)]
+
+
 def _van_loan_displacement(v, dtheta, A, M, method):
     """One augmented exponential per interval (ews/core/van_loan.py:31-88)."""
     n, d = v.shape
@@ -435,6 +466,8 @@ def local_signatures(path, clock, A, N, leaf="van_loan", M=20, van_loan_expm="ca
         return plane_local_terms(v, block_planes(A), dtheta, N)
     if leaf == "diag_closed":
         return diag_local_terms(v, torch.diagonal(A), dtheta, N)
+    if leaf in ("exact", "jordan_closed", "jordan_closed_tables"):
+        return exact_local_terms(v, dtheta, A, N)
     raise ValueError(f"oracle has no leaf {leaf!r}")
 
 

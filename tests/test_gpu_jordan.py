@@ -1,11 +1,12 @@
 """GPU parity of the exact-integral leaves, the Jordan-chain leaves (leaf="jordan_closed" / "jordan_closed_tables")
-with jordan_flows and the block-series leaf on general blocks, against the float64 oracle's exact local integrals (its series leaf at order 40, pinned against quadrature in
-tests/test_oracle_*.py). The reference pins its closed forms the same way: tests/test_jordan_engine.py:66-91 holds
-them to the series leaf (q = 24 at 1e-7, q = 60 at 1e-10).
+with jordan_flows and the block-series leaf on general blocks, against the float64 oracle's exact local integrals (its
+series leaf at order 40 at small steps, and its augmented-exponential leaf at any step, both pinned against
+quadrature in tests/test_oracle_*.py). The reference pins its closed forms the same way: tests/test_jordan_engine.py:
+66-91 holds them to the series leaf (q = 24 at 1e-7, q = 60 at 1e-10).
 
 Bars: forward max relative error <= 1e-5, gradients <= 1e-4 (metric max|a-b| / max|b|). Cases: real chains of 2-4
 and complex chains of 4, 6, 8 (two blocks each), depths 1 and 2, prefix / terminal / mean readouts, with and
-without jordan_flows, steps up to clock step x ||A||_1 = 3.5; and the loud error past the supported step.
+without jordan_flows, small steps, and steps with clock step x ||A||_1 from 5 to 60.
 """
 
 import numpy as np
@@ -71,22 +72,44 @@ def test_jordan_leaf_matches_exact_integrals(kind, size, N, flows):
                 qr.grad = None
 
 
-def test_jordan_leaf_at_the_largest_supported_step_and_past_it():
-    K, size, B, L = 2, 4, 1, 20
-    ps = _params("complex", K, 7)
-    A = E.AParamJordanRepeated([size] * K, ["complex"] * K, [torch.tensor(p, dtype=torch.float32) for p in ps])
-    Ad = A().detach().double()
-    norm = float(Ad.abs().sum(0).max())
-    rng = np.random.default_rng(8)
-    path = torch.tensor(np.cumsum(rng.normal(size=(B, L, size * K)), 1), dtype=torch.float32)
-    h = 3.5 / norm
-    clock = torch.tensor(np.arange(L, dtype=np.float64)[None] * h, dtype=torch.float32)
-    layer = E.EWS(A.to(DEV), N=2, leaf="jordan_closed", combine="block_kernel", jordan_flows=True)
-    out = layer(path.to(DEV), clock.to(DEV), readout="prefix")
-    ref = O.ews(path.double(), clock.double(), Ad, 2, "prefix", leaf="series", series_q=60, chen_expm="exact")
-    assert relerr(out, ref) < 1e-5, relerr(out, ref)
-    with pytest.raises(NotImplementedError, match="large-step regime"):
-        layer(path.to(DEV), (clock * 1.2).to(DEV), readout="prefix")
+@pytest.mark.parametrize("kind,size", CASES)
+def test_jordan_leaf_at_large_steps(kind, size):
+    """Clock steps with h ||A||_1 from 5 to 60, where a series of any practical order fails: the chains' tables are
+    exact at any argument (jordan_engine.py:175-243). Forward and gradients (path, clock, the chain parameters)
+    against the oracle's exact local terms (one augmented exponential per interval, pinned against graded
+    quadrature in tests/test_oracle_math.py); two backward calls give identical gradients."""
+    K, B, L = 2, 2, 9
+    ps = _params(kind, K, 100 + size)
+    A = E.AParamJordanRepeated([size] * K, [kind] * K, [torch.tensor(p, dtype=torch.float32) for p in ps]).to(DEV)
+    Ar = E.AParamJordanRepeated([size] * K, [kind] * K, [torch.tensor(p, dtype=DT) for p in ps])
+    norm = float(Ar().detach().abs().sum(0).max())
+    rng = np.random.default_rng(size + 50)
+    d = size * K
+    path = torch.tensor(np.cumsum(rng.normal(size=(B, L, d)), 1), dtype=torch.float32)
+    clock = torch.tensor(np.cumsum(rng.uniform(5.0, 60.0, size=(B, L)) / norm, 1), dtype=torch.float32)
+    layer = E.EWS(A, N=2, leaf="jordan_closed_tables", combine="block_kernel", jordan_flows=True)
+    grads = []
+    for rep in range(2):
+        p = path.to(DEV).requires_grad_(True)
+        c = clock.to(DEV).requires_grad_(True)
+        out = layer(p, c, readout="prefix")
+        w = torch.tensor(np.random.default_rng(4).normal(size=tuple(out.shape)))
+        (out * w.to(DEV, torch.float32)).sum().backward()
+        grads.append([p.grad.clone(), c.grad.clone()] + [q.grad.clone() for q in A.parameters()])
+        for q in A.parameters():
+            q.grad = None
+    for g0, g1 in zip(grads[0], grads[1]):
+        assert torch.equal(g0, g1)
+    pr = path.double().requires_grad_(True)
+    cr = clock.double().requires_grad_(True)
+    ref = O.ews(pr, cr, Ar(), 2, "prefix", leaf="exact", chen_expm="exact")
+    (ref * w).sum().backward()
+    e = relerr(out, ref)
+    errs = [relerr(grads[0][0], pr.grad), relerr(grads[0][1], cr.grad)]
+    errs += [relerr(q, qr.grad) for q, qr in zip(grads[0][2:], Ar.parameters())]
+    print(f"{kind} {size} at h||A|| 5-60: forward {e:.2e}, gradients {errs}", flush=True)
+    assert e < 1e-5, e
+    assert max(errs) < 1e-4, errs
 
 
 @pytest.mark.parametrize("N", [1, 2])

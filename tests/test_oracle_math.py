@@ -361,3 +361,88 @@ def test_block_series_leaf_levels(q):
     series = O.series_local_terms(v, h, A, 2, q)
     torch.testing.assert_close(got[0], closed[0], rtol=1e-12, atol=1e-12)
     torch.testing.assert_close(got[1], series[1], rtol=0, atol=0)
+
+
+def _jordan_A(kind, size, K, rng):
+    """Block-diagonal Jordan chains as AParamJordanRepeated materialises them: a real chain is lambda on the
+    diagonal with ones above; a complex chain of size 2k is R = [[a, -b], [b, a]] in every 2x2 slot with the 2x2
+    identity above."""
+    A = np.zeros((K * size, K * size))
+    for j in range(K):
+        o = j * size
+        if kind == "real":
+            lam = rng.uniform(0.2, 2.0)
+            A[o:o + size, o:o + size] = lam * np.eye(size) + np.diag(np.ones(size - 1), 1)
+        else:
+            a, b = rng.uniform(0.2, 2.0), rng.uniform(-3.0, 3.0)
+            R = np.array([[a, -b], [b, a]])
+            k = size // 2
+            A[o:o + size, o:o + size] = np.kron(np.eye(k), R) + np.kron(np.diag(np.ones(k - 1), 1), np.eye(2))
+    return A
+
+
+def _quad_local_graded(v, h, A, N, nodes=16, panels=14):
+    """_quad_local with composite Gauss-Legendre panels graded toward the interval's end (breakpoints
+    h (1 - 2^-m)), for steps where e^{-(h-u) A} is concentrated near u = h."""
+    g, w = np.polynomial.legendre.leggauss(nodes)
+    cuts = [h * (1 - 2.0 ** -m) for m in range(panels)] + [h]
+
+    def x(u):
+        return scipy.linalg.expm(-(h - u) * A) @ v / h
+
+    def rule(a, b):
+        pts, wts = [], []
+        for lo, hi in zip(cuts[:-1], cuts[1:]):
+            lo, hi = max(lo, a), min(hi, b)
+            if hi > lo:
+                pts += list((hi - lo) / 2 * g + (hi + lo) / 2)
+                wts += list(w * (hi - lo) / 2)
+        return pts, wts
+
+    def lvl1(a, b):
+        pts, wts = rule(a, b)
+        return sum(wi * x(ui) for wi, ui in zip(wts, pts))
+
+    out = [lvl1(0.0, h)]
+    if N >= 2:
+        pts, wts = rule(0.0, h)
+        out.append(sum(wi * np.outer(lvl1(0.0, u2), x(u2)) for wi, u2 in zip(wts, pts)))
+    return out
+
+
+@pytest.mark.parametrize("kind,size,h", [("real", 3, 12.0), ("real", 2, 30.0), ("complex", 4, 8.0)])
+def test_exact_leaf_matches_graded_quadrature_jordan(kind, size, h):
+    """The exact leaf (one augmented exponential per interval), the oracle of the Jordan leaves, against graded
+    quadrature of the defining integrals at steps with h ||A||_1 up to about 60."""
+    rng = _rng(7)
+    A = _jordan_A(kind, size, 2, rng)
+    v = rng.normal(size=A.shape[0])
+    ref = _quad_local_graded(v, h, A, 2)
+    got = O.exact_local_terms(torch.tensor(v[None]), torch.tensor([h]), torch.tensor(A), 2)
+    for lvl, r in zip(got, ref):
+        err = float(np.abs(lvl[0].numpy() - r).max() / np.abs(r).max())
+        assert err < 1e-9, err
+
+
+@pytest.mark.parametrize("h", [0.3, 4.0, 25.0])
+def test_exact_leaf_matches_closed_forms(h):
+    """On diagonals and rotation planes the exact leaf equals the closed forms at any step."""
+    rng = _rng(3)
+    v = torch.tensor(rng.normal(size=(3, 4)))
+    hh = torch.full((3,), h, dtype=torch.float64)
+    lam = torch.tensor(rng.uniform(0.1, 2.0, 4))
+    for a, b in zip(O.exact_local_terms(v, hh, torch.diag(lam), 2), O.diag_local_terms(v, lam, hh, 2)):
+        assert float((a - b).abs().max() / b.abs().max()) < 1e-11
+    Ap = torch.tensor(_planes_A(2, rng))
+    for a, b in zip(O.exact_local_terms(v, hh, Ap, 2), O.plane_local_terms(v, O.block_planes(Ap), hh, 2)):
+        assert float((a - b).abs().max() / b.abs().max()) < 1e-11
+
+
+def test_exact_leaf_matches_series_at_small_steps():
+    """Any generator: at h ||A|| about 0.1 the order-30 series leaf equals the exact local terms."""
+    rng = _rng(11)
+    A = torch.tensor(_jordan_A("complex", 6, 1, rng) + 0.3 * rng.normal(size=(6, 6)))
+    v = torch.tensor(rng.normal(size=(4, 6)))
+    h = torch.tensor(rng.uniform(0.005, 0.03, 4))
+    for a, b in zip(O.exact_local_terms(v, h, A, 2), O.series_local_terms(v, h, A, 2, 30)):
+        assert float((a - b).abs().max() / b.abs().max()) < 1e-12
