@@ -1,7 +1,7 @@
 """The allocation-free forward (ews_diag_forward_noalloc) through the C ABI against ews_diag_forward on the same
-inputs: bit-identical outputs on two calls in a row, the second with a smaller input (the scratch keeps the first
-call's contents, which the second must not depend on), and the size limit reported as an error code without any
-launch."""
+inputs: bit-identical outputs on calls in a row, each later one using less scratch (the scratch keeps the previous
+call's contents, which the next must not depend on), on the pair-group, generic and sequential kernels, and the size
+limit reported as an error code without any launch."""
 
 import ctypes
 
@@ -23,14 +23,14 @@ def _stream():
     return ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
 
 
-def _both(path, clock, params, structure, readout, bf16=False):
+def _both(path, clock, params, structure, readout, bf16=False, chunk=0):
     """(allocating forward, allocation-free forward) outputs for one input."""
     lib = nat.load()
     B, L, d = path.shape
     dt = nat.DTYPE_BF16 if bf16 else nat.DTYPE_F32
-    desc = make_desc(B, L, d, 2, structure, nat.FLOW_PER_INTERVAL, readout, True, dt)
-    W = 1 + d + d * d
-    shape = (B, L - 1, W) if readout == "prefix" else (B, W)
+    desc = make_desc(B, L, d, 2, structure, nat.FLOW_PER_INTERVAL, readout, True, dt, chunk=chunk)
+    W = d + d * (d - 1) // 2 if readout == "log_prefix" else 1 + d + d * d
+    shape = (B, L - 1, W) if readout in ("prefix", "log_prefix") else (B, W)
     tp = torch.tensor(path, device=DEV)
     if bf16:
         tp = tp.to(torch.bfloat16)
@@ -66,15 +66,34 @@ def test_noalloc_forward_matches_allocating_forward_twice():
     ref, got = _both(path, clock, lam, nat.STRUCT_REAL_DIAG, "mean")
     assert torch.isfinite(ref).all()
     assert torch.equal(ref, got)
+    # the per-sample sequential kernels (no checkpoints kept by the allocation-free call), LogEWS rows
+    rng = np.random.default_rng(5)
+    path = np.cumsum(rng.normal(size=(2, 300, 32)) / 8.0, 1).astype(np.float32)
+    clock = np.broadcast_to(np.arange(300, dtype=np.float32), (2, 300)).copy()
+    lam = rng.uniform(0.1, 2.0, size=32).astype(np.float32)
+    print("noalloc call 4: sequential kernels B=2 L=300 d=32 real diagonal log_prefix", flush=True)
+    ref, got = _both(path, clock, lam, nat.STRUCT_REAL_DIAG, "log_prefix", chunk=nat.CHUNK_SEQUENTIAL)
+    assert torch.isfinite(ref).all()
+    assert torch.equal(ref, got)
 
 
 def test_noalloc_forward_rejects_oversized_calls():
-    """The c4 block shape at B = 256 needs more than the 64 MiB scratch: an error code, nothing launched (the
-    pointers are never dereferenced on the host, and the check precedes every launch)."""
+    """The c4 block shape on the chunk kernels (chunk = 16: float64 chunk carries of 69 MB alone) needs more than the
+    64 MiB scratch: an error code, nothing launched. The size is checked on the host through the library's own
+    query before the call, and every buffer has the call's real size, so the call stays in bounds whatever the
+    entry point decides."""
     lib = nat.load()
-    desc = make_desc(256, 512, 32, 2, nat.STRUCT_REAL_DIAG, nat.FLOW_PER_INTERVAL, "prefix", True, nat.DTYPE_F32)
-    buf = torch.empty(16, device=DEV)
-    rc = lib.ews_diag_forward_noalloc(ctypes.byref(desc), buf.data_ptr(), buf.data_ptr(), buf.data_ptr(),
-                                      buf.data_ptr(), _stream())
+    B, L, d = 256, 512, 32
+    desc = make_desc(B, L, d, 2, nat.STRUCT_REAL_DIAG, nat.FLOW_PER_INTERVAL, "prefix", True, nat.DTYPE_F32,
+                     chunk=16)
+    need = int(lib.ews_diag_residual_bytes(ctypes.byref(desc)))
+    assert need > 64 << 20, need
+    path = torch.zeros(B, L, d, device=DEV)
+    clock = torch.arange(L, dtype=torch.float32, device=DEV).expand(B, L).contiguous()
+    lam = torch.ones(d, device=DEV)
+    out = torch.empty(B, L - 1, 1 + d + d * d, device=DEV)
+    rc = lib.ews_diag_forward_noalloc(ctypes.byref(desc), path.data_ptr(), clock.data_ptr(), lam.data_ptr(),
+                                      out.data_ptr(), _stream())
+    torch.cuda.synchronize()
     assert rc == EWS_ERR_SCRATCH
     assert b"scratch" in lib.ews_error_string(rc)
