@@ -50,6 +50,13 @@ struct DiagArgs {
   double* qflow;    // (B, NQ, K, 2) quad flows exp(u tau_quad)
   double* ql1;      // (B, NQ, K, 2) level-1 increments of the quads (backward)
   double* cflow;    // (B, C, K, 2) chunk flows exp(u tau_chunk)
+  // LogEWS rows written by the chunk kernels' output pass (log-prefix readout off the sequential kernels): the
+  // forward writes rows of Wlog = d + d (d - 1) / 2 floats (level 1, then the level-2 Lyndon coefficients) to out
+  // and level 1 of every step to s1rows; the backward turns the log cotangent into the flat-row cotangent gcot
+  // (layout W = D, no level 0) and runs on that
+  int log, Wlog;
+  float* s1rows;    // (B, n_int, d) level 1 of every step (residual)
+  float* gcot;      // (B, n_int, D) flat-row cotangent (backward workspace)
   // per-sample sequential kernels (real diagonal, ews_seq.hip)
   float* seqck;     // (B, blocks, lanes + K) state checkpoints (residual; null: the forward keeps none)
   float* seqgp;     // (B, K) per-sample parameter partials (backward)

@@ -132,10 +132,11 @@ __device__ __forceinline__ void load_clock(const DiagArgs& a, int b, int t0, int
 // ------------------------------------------------------------------------------------------- coefficients
 template <class T> struct Coef {
   T rho, phi_j, phi_k, IA, IB, lamA, lamB;
+  T rho_k;  // flow of the level-1 coordinate k (the log rows' S1_k)
 };
 template <class T> struct CoefD {
-  T rho1, phi_j1, phi_k1, IA1, IB1, lamA1, lamB1;  // d/dh
-  T dphi_j, dphi_k, DxA, DyA, DxB, DyB;           // node derivatives
+  T rho1, phi_j1, phi_k1, IA1, IB1, lamA1, lamB1, rho_k1;  // d/dh
+  T dphi_j, dphi_k, DxA, DyA, DxB, DyB;                   // node derivatives
 };
 
 template <class T> __device__ __forceinline__ T conj_if(T x, bool) { return x; }
@@ -161,6 +162,7 @@ __device__ __forceinline__ void eval_coef(int q1, int q2, float h, float hf, boo
     const T xk = h * uk;
     const Node1<T> nk = node1q(xk, q1);
     c.phi_k = nk.p;
+    c.rho_k = per_int ? nk.e : expv(hf * uk);
     const T ub = uj + uk;
     const DD3<T> db = dd3q<T, DERIV>(xj, h * ub, q2);
     c.IB = db.d;
@@ -168,6 +170,7 @@ __device__ __forceinline__ void eval_coef(int q1, int q2, float h, float hf, boo
     if (DERIV) {
       q.dphi_k = nk.dp;
       q.phi_k1 = nk.dp * uk;
+      q.rho_k1 = per_int ? c.rho_k * uk : zero<T>();
       q.DxB = db.dx;
       q.DyB = db.dy;
       q.IB1 = db.dx * uj + db.dy * ub;
@@ -195,6 +198,7 @@ __device__ __forceinline__ void lin_coef(const Coef<T>& c0, const CoefD<T>& q, f
   c.rho = per_int ? c0.rho + q.rho1 * dlt : c0.rho;
   if (N == 2) {
     c.phi_k = c0.phi_k + q.phi_k1 * dlt;
+    c.rho_k = per_int ? c0.rho_k + q.rho_k1 * dlt : c0.rho_k;
     c.IB = c0.IB + q.IB1 * dlt;
     c.lamB = per_int ? c0.lamB + q.lamB1 * dlt : c0.lamB;
     if (CPLX) {
@@ -301,6 +305,49 @@ template <bool CPLX>
 __device__ __forceinline__ void out_values(const DiagArgs& a, int j, int k, cf S1, cf SA, cf SB, int* idx,
                                            float* val, int& n1, int& n2);
 
+// One LogEWS row of step t from the lane's states after the step (ews/layer.py:488-517 at depth 2: level 1, then
+// log S at level 2 = S2 - S1 (x) S1 / 2 at the Lyndon words a < b, lexicographic; see ews_log.hip): the lane
+// (j, k) writes the words of its level-2 block, the level-1 lanes the row's level 1 and its copy in s1rows (the
+// backward's input for turning the log cotangent into a flat-row cotangent).
+__device__ __forceinline__ int lyndon2(int i, int j, int d) { return i * (2 * d - i - 1) / 2 + (j - i - 1); }
+template <bool CPLX, class T>
+__device__ __forceinline__ void write_log_row(const DiagArgs& a, const LaneMap& m, int b, int t, T S1, T S1k, T SA,
+                                              T SB) {
+  float* row = a.out + ((size_t)b * a.n_int + t) * a.Wlog;
+  const int d = a.d;
+  if constexpr (CPLX) {
+    const cf s1 = S1, s1k = S1k, sa = SA, sb = SB;
+    if (m.plane) {
+      row[2 * m.j] = s1.re;
+      row[2 * m.j + 1] = s1.im;
+      if (a.s1rows) {
+        float* q = a.s1rows + ((size_t)b * a.n_int + t) * d + 2 * m.j;
+        q[0] = s1.re;
+        q[1] = s1.im;
+      }
+    }
+    // the real 2 x 2 block (rows 2j, 2j+1; columns 2k, 2k+1) of the halved pair states, as the flat rows
+    const float q00 = 0.5f * (sa.re + sb.re), q01 = 0.5f * (sb.im - sa.im);
+    const float q10 = 0.5f * (sa.im + sb.im), q11 = 0.5f * (sa.re - sb.re);
+    const int r0 = 2 * m.j, c0 = 2 * m.k;
+    if (m.j < m.k) {
+      row[d + lyndon2(r0, c0, d)] = q00 - 0.5f * s1.re * s1k.re;
+      row[d + lyndon2(r0, c0 + 1, d)] = q01 - 0.5f * s1.re * s1k.im;
+      row[d + lyndon2(r0 + 1, c0, d)] = q10 - 0.5f * s1.im * s1k.re;
+      row[d + lyndon2(r0 + 1, c0 + 1, d)] = q11 - 0.5f * s1.im * s1k.im;
+    } else if (m.j == m.k) {
+      row[d + lyndon2(r0, r0 + 1, d)] = q01 - 0.5f * s1.re * s1.im;
+    }
+  } else {
+    const float s1 = S1, s1k = S1k, sb = SB;
+    if (m.plane) {
+      row[m.j] = s1;
+      if (a.s1rows) a.s1rows[((size_t)b * a.n_int + t) * d + m.j] = s1;
+    }
+    if (m.j < m.k) row[d + lyndon2(m.j, m.k, d)] = sb - 0.5f * s1 * s1k;
+  }
+}
+
 // ------------------------------------------------------------------------------------------- F1 / F3
 template <bool CPLX, int N, int MODE, int MAXT, bool FAST>
 __global__ __launch_bounds__(MAXT) void k_chunk_fwd(DiagArgs a) {
@@ -323,9 +370,12 @@ __global__ __launch_bounds__(MAXT) void k_chunk_fwd(DiagArgs a) {
   const T uk = load_u(a.params, m.k, &dummy);
 
   T S1 = zero<T>(), SA = zero<T>(), SB = zero<T>();
+  T S1k = zero<T>();  // level 1 of coordinate k (log rows only)
+  const bool logrows = MODE == MODE_PREFIX && N == 2 && a.log;
   if (MODE != MODE_SUMMARY) {
     const double* cr = a.carries + ((size_t)b * (a.C + 1) + c) * a.D;
     S1 = ldTd<CPLX, T>(cr + st1<CPLX>(m.j));
+    if (logrows) S1k = ldTd<CPLX, T>(cr + st1<CPLX>(m.k));
     if (N == 2) {
       const double* p2 = cr + st2<CPLX>(a, m.j, m.k);
       if (CPLX) {
@@ -363,6 +413,11 @@ __global__ __launch_bounds__(MAXT) void k_chunk_fwd(DiagArgs a) {
     const T pk = (N == 2) ? lds_p<T>(s_v, t, a.d, m.k) : zero<T>();
     fwd_step<T, CPLX, N>(co, pj, pk, S1, SA, SB);
     if (MODE == MODE_SUMMARY) continue;
+    if (logrows) {  // LogEWS row: level 1, then S2[a,b] - S1_a S1_b / 2 at the Lyndon words a < b
+      S1k = co.rho_k * S1k + co.phi_k * pk;
+      write_log_row<CPLX>(a, m, b, t0 + t, S1, S1k, SA, SB);
+      continue;
+    }
     // the lane's output values in the row layout
     float v[6];
     int n1 = 0;
@@ -1622,6 +1677,33 @@ __global__ __launch_bounds__(MAXT) void k_chunk_bwd_full(DiagArgs a) {
   }
 }
 
+// ------------------------------------------------------------------------------------------- B0 (log rows)
+// The cotangent of the log rows as a cotangent of the flat rows (level 1, then level 2 row-major, no level 0):
+// with L2[a,b] = S2[a,b] - S1_a S1_b / 2 at the Lyndon words a < b,
+//   dS2[a,b] = dL2[a,b] (a < b, else 0),  dS1_a = dL1_a - (sum_{b > a} dL2[a,b] S1_b + sum_{b < a} dL2[b,a] S1_b) / 2,
+// S1 of every step read from the forward's copy (s1rows). One wavefront per row, four rows per workgroup.
+__global__ __launch_bounds__(256) void k_log_cot(DiagArgs a, const float* __restrict__ glog) {
+  const size_t rows = (size_t)a.B * a.n_int;
+  const size_t r = (size_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (r >= rows) return;
+  const int l = threadIdx.x & 63, d = a.d;
+  const float* gl = glog + r * a.Wlog;
+  const float* x = a.s1rows + r * d;
+  float* go = a.gcot + r * a.D;
+  for (int e = l; e < d * d; e += 64) {
+    const int i = e / d, j = e - i * d;
+    go[d + e] = i < j ? gl[d + lyndon2(i, j, d)] : 0.0f;
+  }
+  for (int i = l; i < d; i += 64) {
+    float acc = 0.0f;
+    for (int j = 0; j < d; ++j) {
+      if (j > i) acc += gl[d + lyndon2(i, j, d)] * x[j];
+      else if (j < i) acc += gl[d + lyndon2(j, i, d)] * x[j];
+    }
+    go[i] = gl[i] - 0.5f * acc;
+  }
+}
+
 // ------------------------------------------------------------------------------------------- B4
 // Knot gradients from interval gradients: dX_t = dv_{t-1} - dv_t, dtheta_t = dh_{t-1} - dh_t (+ the shared flow
 // step's gradient for cached flows). One workgroup per (chunk, sample): the chunk's first knot always, its interior
@@ -1732,6 +1814,8 @@ struct Plan {
   int B, L, n_int, d, K, N, T, C, D, W, npar, kb, readout;
   bool cplx, wave, fast;
   bool seq;  // the per-sample sequential kernels (ews_seq.hip) run the whole call
+  bool log;  // log-prefix rows from the chunk kernels (W: the backward's flat-row layout, no level 0)
+  int Wlog;  // floats per log row
   int NT, NTb, scan_cb, NG;
   size_t lds_bwd_local, lds_bwd_full, lds_bwd_inv, lds_carry, lds_adjoint;
 };
@@ -1770,15 +1854,19 @@ int make_plan(const ews_diag_desc* s, Plan& p) {
   p.K = p.cplx ? p.d / 2 : p.d;
   p.N = s->depth;
   p.D = p.d + (p.N == 2 ? p.d * p.d : 0);
-  p.W = p.D + (s->level0 ? 1 : 0);
+  const bool logp = s->readout == EWS_READOUT_LOGPREFIX;
+  if (logp && p.N != 2) return EWS_ERR_DEPTH;
+  p.W = logp ? p.D : p.D + (s->level0 ? 1 : 0);
+  p.Wlog = logp ? p.d + p.d * (p.d - 1) / 2 : 0;
   p.npar = p.cplx ? 2 * p.K : p.K;
   // the per-sample sequential kernels: asked for (chunk EWS_CHUNK_SEQUENTIAL, the log-prefix readout), or chosen
   // for many samples of moderate length, where one workgroup per sample fills the chip
   const bool seq_form = !p.cplx && p.N == 2 && p.d <= kSeqMaxK && s->flow_mode == EWS_FLOW_PER_INTERVAL &&
                         (s->readout == EWS_READOUT_PREFIX || s->readout == EWS_READOUT_LOGPREFIX);
-  const bool seq_asked = s->chunk == EWS_CHUNK_SEQUENTIAL || s->readout == EWS_READOUT_LOGPREFIX;
-  if (seq_asked && (!seq_form || s->chunk > 0)) return EWS_ERR_OPTION;
-  p.seq = seq_form && (seq_asked || (s->chunk == 0 && p.B >= 128 && p.L <= 1025));
+  const bool seq_asked = s->chunk == EWS_CHUNK_SEQUENTIAL;
+  if (seq_asked && !seq_form) return EWS_ERR_OPTION;
+  p.seq = seq_form && (seq_asked || (s->chunk == 0 && (logp || (p.B >= 128 && p.L <= 1025))));
+  p.log = logp && !p.seq;
   if (p.seq) {
     if (s->readout == EWS_READOUT_LOGPREFIX) p.W = p.d + p.d * (p.d - 1) / 2;
     p.fast = false;
@@ -1827,7 +1915,7 @@ int make_plan(const ews_diag_desc* s, Plan& p) {
 }
 
 struct WsLayout {
-  size_t summ, mu, mt, red, red_idx, dv, dh, gp, gph, gpart, gagg, gcar, qagg, qflow, ql1, cflow, total;
+  size_t summ, mu, mt, red, red_idx, dv, dh, gp, gph, gpart, gagg, gcar, qagg, qflow, ql1, cflow, gcot, total;
 };
 WsLayout ws_layout(const Plan& p) {
   WsLayout w{};
@@ -1855,6 +1943,7 @@ WsLayout ws_layout(const Plan& p) {
   w.qflow = off; off += p.fast ? align256((size_t)p.B * NQ * p.K * 16) : 0;
   w.ql1 = off; off += p.fast ? align256((size_t)p.B * NQ * p.K * 16) : 0;
   w.cflow = off; off += p.fast ? align256(BC * p.K * 16) : 0;
+  w.gcot = off; off += p.log ? align256((size_t)p.B * p.n_int * p.D * 4) : 0;
   w.total = off;
   return w;
 }
@@ -1882,9 +1971,11 @@ WsLayout ws_layout_fwd(const Plan& p) {
 size_t resid_carries_bytes(const Plan& p) { return align256((size_t)p.B * (p.C + 1) * p.D * 8); }
 size_t resid_argmax_bytes(const Plan& p) { return align256((size_t)p.B * p.W * 4); }
 size_t resid_chunk_bytes(const Plan& p) { return align256((size_t)p.B * p.C * 4); }
+size_t resid_s1rows_bytes(const Plan& p) { return p.log ? align256((size_t)p.B * p.n_int * p.d * 4) : 0; }
 size_t resid_bytes(const Plan& p) {
   if (p.seq) return align256((size_t)p.B * seq_ckpt_floats(p.K, p.n_int) * 4);  // state checkpoints
-  return resid_carries_bytes(p) + resid_argmax_bytes(p) + 2 * resid_chunk_bytes(p) + align256(kCoefTabFloats * 4);
+  return resid_carries_bytes(p) + resid_argmax_bytes(p) + 2 * resid_chunk_bytes(p) + align256(kCoefTabFloats * 4) +
+         resid_s1rows_bytes(p);
 }
 
 // fwd_only: the workspace has the forward's layout (ws_layout_fwd); the backward's pointers are null
@@ -1913,6 +2004,14 @@ DiagArgs make_args(const ews_diag_desc* s, const Plan& p, const void* path, cons
   a.chbar = (float*)(r + resid_carries_bytes(p) + resid_argmax_bytes(p) + resid_chunk_bytes(p));
   a.ctab = (float*)(r + resid_carries_bytes(p) + resid_argmax_bytes(p) + 2 * resid_chunk_bytes(p));
   a.fast_ok = p.fast ? 1 : 0;
+  if (p.log) {  // log rows: written with pitch Wlog; the backward's cotangent has the flat layout without level 0
+    a.log = 1;
+    a.readout = EWS_READOUT_PREFIX;  // every kernel but the output pass sees a prefix-row call
+    a.Wlog = p.Wlog;
+    a.lvl0 = 0; a.off1 = 0; a.off2 = p.d;
+    a.s1rows = (float*)(r + resid_carries_bytes(p) + resid_argmax_bytes(p) + 2 * resid_chunk_bytes(p) +
+                        align256(kCoefTabFloats * 4));
+  }
   const WsLayout w = fwd_only ? ws_layout_fwd(p) : ws_layout(p);
   char* ws = (char*)workspace;
   a.summ = (float*)(ws + w.summ);
@@ -1926,6 +2025,7 @@ DiagArgs make_args(const ews_diag_desc* s, const Plan& p, const void* path, cons
   a.NQ = (p.C + 3) / 4;
   a.qagg = (float*)(ws + w.qagg); a.qflow = (double*)(ws + w.qflow); a.ql1 = (double*)(ws + w.ql1);
   a.cflow = (double*)(ws + w.cflow);
+  if (p.log && !fwd_only) a.gcot = (float*)(ws + w.gcot);
   return a;
 }
 
@@ -1963,7 +2063,7 @@ int forward_pass(const ews_diag_desc* s, const Plan& p, DiagArgs a, hipStream_t 
       hipLaunchKernelGGL((k_fwd_group<CPLX, N, MAXT, true>), dim3(p.NG, p.B), blk, p.lds_carry, st, a);
       break;
     case 2:
-      if (s->readout == EWS_READOUT_PREFIX) {
+      if (s->readout == EWS_READOUT_PREFIX || s->readout == EWS_READOUT_LOGPREFIX) {
         if (p.fast) {
           if (pairs_forward(a, st, true) != 0) return EWS_ERR_LAUNCH;
         } else {
@@ -2172,6 +2272,15 @@ int ews_diag_backward_pass(const ews_diag_desc* desc, int pass, const void* path
   a.dpath = grad_path;
   a.dclock = grad_clock;
   a.dparams = grad_params;
+  if (p.log) {  // the passes run on the flat-row cotangent, built from the log cotangent before pass 0
+    if (pass == 0) {
+      const size_t rows = (size_t)p.B * p.n_int;
+      hipLaunchKernelGGL(k_log_cot, dim3((unsigned)((rows + 3) / 4)), dim3(256), 0, (hipStream_t)stream, a,
+                         grad_out);
+      if (hipGetLastError() != hipSuccess) return EWS_ERR_LAUNCH;
+    }
+    a.gout = a.gcot;
+  }
   return dispatch_backward(p, a, (hipStream_t)stream, pass);
 }
 

@@ -60,14 +60,19 @@ __device__ __forceinline__ cf fma_c(cf a, cf b, cf c) {  // a b + c
   return cf{fmaf(a.re, b.re, fmaf(-a.im, b.im, c.re)), fmaf(a.re, b.im, fmaf(a.im, b.re, c.im))};
 }
 
-// cross-lane moves: DPP row_ror inside rows of 16 lanes, ds_swizzle (xor 16) inside halves of 32
-#define EWS_ROR(v, n) __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x120 + (n), 0xf, 0xf, false))
-__device__ __forceinline__ float xor16(float v) { return __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(v), 0x401F)); }
+// cross-lane moves: DPP row_ror inside rows of 16 lanes (bound_ctrl with a zero old value, so that the move folds
+// into the consuming add as its DPP source), v_permlane16_swap for lane ^ 16 (a VALU op: no LDS round trip)
+#define EWS_ROR(v, n) __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x120 + (n), 0xf, 0xf, true))
+// v[lane] + v[lane ^ 16] in every lane: the swap exchanges the odd rows of one copy with the even rows of the other
+__device__ __forceinline__ float add_xor16(float v) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
 
 // sum over the k-groups of plane j (lanes j + 8 kg of the group)
 template <int KP> __device__ __forceinline__ float kg_sum(float v) {
   if constexpr (Geo<KP>::NKG >= 2) v += EWS_ROR(v, 8);
-  if constexpr (Geo<KP>::NKG >= 4) v += xor16(v);
+  if constexpr (Geo<KP>::NKG >= 4) v = add_xor16(v);
   return v;
 }
 template <int KP> __device__ __forceinline__ cf kg_sum(cf v) { return cf{kg_sum<KP>(v.re), kg_sum<KP>(v.im)}; }

@@ -254,11 +254,11 @@ class EWS(torch.nn.Module):
                              level0, chunk=0, leaf=leaf, series_q=self.series_q or 0)
 
     def _log_prefix_fused(self, path, clock):
-        """LogEWS prefix rows computed inside the scan (real diagonal, depth 2, d <= 32, per-interval flows, the
-        diagonal leaves): the compressed log of every prefix row (ews/layer.py:488-517) without the flat rows ever
-        reaching memory. None when the configuration takes the rows-then-log route."""
-        if (self.structure != "real_diag" or self.N != 2 or self.d > 32 or path.dim() != 3
-                or self._flow_mode("prefix") != "per_interval"):
+        """LogEWS prefix rows computed inside the scan (rotation planes or a real diagonal, depth 2, the diagonal
+        leaves with exact flows): the compressed log of every prefix row (ews/layer.py:488-517), written by the
+        scan's output pass without the flat rows ever reaching memory. None when the configuration takes the
+        rows-then-log route (the dense kernels)."""
+        if self.structure is None or self.N != 2 or path.dim() != 3:
             return None
         if self._engine_check() != "diag":
             return None
@@ -269,8 +269,9 @@ class EWS(torch.nn.Module):
         if path.dtype != torch.bfloat16:
             path = path.to(torch.float32)
         leaf = self.leaf if self.leaf in ("series", "block_series") else "plane_closed"
-        return ops.diag_scan(path, clock.to(torch.float32), params, self.N, self.structure, "per_interval",
-                             "log_prefix", False, chunk=0, leaf=leaf, series_q=self.series_q or 0)
+        return ops.diag_scan(path, clock.to(torch.float32), params, self.N, self.structure,
+                             self._flow_mode("prefix"), "log_prefix", False, chunk=0, leaf=leaf,
+                             series_q=self.series_q or 0)
 
     def _levels(self, packed, lead):
         out, s = [], 0

@@ -94,8 +94,8 @@ def diag_scan(path, clock, params, N, structure, flow_mode="per_interval", reado
               chunk=0, leaf="plane_closed", series_q=0):
     """leaf "plane_closed" (exact closed forms, for planes and real diagonals alike), "block_series" (exact level 1,
     the order-series_q series at level 2) or "series" (the order-series_q series at every level). readout
-    "log_prefix" (real diagonal, depth 2, d <= 32, per-interval flows) returns the LogEWS prefix rows straight from
-    the scan; chunk nat.CHUNK_SEQUENTIAL asks for the per-sample sequential kernels."""
+    "log_prefix" (depth 2) returns the LogEWS prefix rows straight from the scan's output pass; chunk
+    nat.CHUNK_SEQUENTIAL asks for the per-sample sequential kernels (real diagonal, d <= 32, per-interval flows)."""
     fm = {"per_interval": nat.FLOW_PER_INTERVAL, "cached": nat.FLOW_CACHED,
           "cached_basepoint": nat.FLOW_CACHED_BASEPOINT}[flow_mode]
     st = {"planes": nat.STRUCT_PLANES, "real_diag": nat.STRUCT_REAL_DIAG}[structure]

@@ -63,8 +63,8 @@ def test_c_abi_error_codes():
 
 
 def test_sequential_plan_selection_and_log_readout():
-    """The per-sample sequential kernels: asked for by chunk = EWS_CHUNK_SEQUENTIAL or the log-prefix readout (real
-    diagonal, depth 2, d <= 32, per-interval flows only), chosen by chunk 0 for B >= 128 and L <= 1025. Their
+    """The per-sample sequential kernels: asked for by chunk = EWS_CHUNK_SEQUENTIAL, chosen by chunk 0 for the
+    log-prefix readout or B >= 128 and L <= 1025 (real diagonal, depth 2, d <= 32, per-interval flows). Their
     residual is one state checkpoint per 16 steps (lanes = 32 d rounded to 64, plus the d level-1 states), their
     workspace the per-sample parameter partials."""
     lib = nat.load()
@@ -86,18 +86,24 @@ def test_sequential_plan_selection_and_log_readout():
     assert sizes(batch=2, length=100)[0] != sizes(batch=2, length=100, chunk=-1)[0]
     assert sizes(batch=256, length=2000)[0] != sizes(batch=256, length=2000, chunk=-1)[0]
     assert sizes(batch=256, length=512, chunk=16)[0] != sizes(batch=256, length=512)[0]
+    # the log readout off the sequential kernels (planes, cached flows, an explicit chunk length): the chunk
+    # kernels, whose residual adds level 1 of every step and whose workspace adds one flat-row cotangent per step
+    for kw in (dict(structure=1, dim=8), dict(structure=2, dim=8, flow_mode=1), dict(structure=2, dim=8, chunk=16)):
+        B, L, d = 3, 50, 8
+        r0 = lib.ews_diag_residual_bytes(ctypes.byref(_desc(batch=B, length=L, level0=0, **kw)))
+        w0 = lib.ews_diag_workspace_bytes(ctypes.byref(_desc(batch=B, length=L, level0=0, **kw)))
+        r1 = lib.ews_diag_residual_bytes(ctypes.byref(_desc(batch=B, length=L, readout=4, **kw)))
+        w1 = lib.ews_diag_workspace_bytes(ctypes.byref(_desc(batch=B, length=L, readout=4, **kw)))
+        assert (r1, w1) == (r0 + al(B * (L - 1) * d * 4), w0 + al(B * (L - 1) * (d + d * d) * 4)), kw
     bad = {
-        "log readout on planes": _desc(readout=4),
         "log readout, depth 1": _desc(structure=2, depth=1, readout=4),
-        "log readout, cached flows": _desc(structure=2, flow_mode=1, readout=4),
-        "log readout, explicit chunk": _desc(structure=2, readout=4, chunk=16),
         "sequential planes": _desc(chunk=-1),
         "sequential terminal": _desc(structure=2, readout=1, chunk=-1),
         "chunk -2": _desc(structure=2, chunk=-2),
     }
     for name, dsc in bad.items():
         assert lib.ews_diag_workspace_bytes(ctypes.byref(dsc)) == 0, name
-        assert lib.ews_diag_forward(ctypes.byref(dsc), null, null, null, null, null, null, null) in (-2, -4), name
+        assert lib.ews_diag_forward(ctypes.byref(dsc), null, null, null, null, null, null, null) in (-2, -3, -4), name
 
 
 def _planes(K=2):
