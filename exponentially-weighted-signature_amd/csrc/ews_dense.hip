@@ -2184,6 +2184,208 @@ __global__ __launch_bounds__(256) void k_dsh_reduce(Args a, LeafBwd o) {
   }
 }
 
+// ------------------------------------------------------------------------------------------------ block-series level 1
+// Level 1 of the block-series leaf (ews/core/kernels/blockdiag_engine.py:81-136, ews/core/leaf.py:138-175): the
+// reference reads G = phi(X) = int_0^1 e^{sX} ds, X = -h A, off one augmented exponential per interval,
+// exp([[X, I], [0, 0]]) = [[e^X, phi(X)], [0, I]], and writes s1 = G v at any step; its level 2 is the series
+// leaf's (k_local at the order q, which runs first; this kernel overwrites its level 1). Here phi and e^X come from
+// the powers table (P_p = A^p / p!): on Y = X / 2^s with ||Y||_1 <= 1, phi(Y) = sum_p y^p P_p / (p + 1) and
+// e^Y = sum_p y^p P_p (degree PM, y = -h / 2^s: remainder below 1/14!), then s doublings
+// phi(2Y) = phi(Y) (e^Y + I) / 2, e^{2Y} = (e^Y)^2. One workgroup of 256 threads per interval (grid-stride), thread
+// (i, j) one entry of the 16 x 16 (padded) matrices.
+__device__ __forceinline__ float inv_int(int n) { return 1.0f / (float)n; }
+
+__global__ __launch_bounds__(256) void k_bs_level1(Args a) {
+  __shared__ float sp[PM + 1][256];
+  __shared__ float gm[256], em[256];
+  __shared__ float vv[16];
+  const int tid = threadIdx.x, i = tid >> 4, j = tid & 15;
+  for (int e = tid; e < (PM + 1) * 256; e += 256) sp[e >> 8][e & 255] = a.apow[e];
+  const float norm1 = a.apow[a.npow * 256];
+  __syncthreads();
+  const long total = (long)a.B * a.n_int;
+  for (long it = blockIdx.x; it < total; it += gridDim.x) {
+    const int b = (int)(it / a.n_int), t = (int)(it - (long)b * a.n_int);
+    const float* th = a.clock + (size_t)b * a.L;
+    const float h = th[t + 1] - th[t];
+    if (tid < 16) {
+      const float* x = a.path + ((size_t)b * a.L + t) * a.d;
+      vv[tid] = tid < a.d ? x[a.d + tid] - x[tid] : 0.0f;
+    }
+    int s = 0;
+    float xn = fabsf(h) * norm1;
+    while (xn > 1.0f && s < SQMAX) {
+      xn *= 0.5f;
+      ++s;
+    }
+    const float y = -h * ldexpf(1.0f, -s);
+    float g = sp[PM][tid] * inv_int(PM + 1), e = sp[PM][tid];
+#pragma unroll
+    for (int p = PM - 1; p >= 0; --p) {
+      g = fmaf(g, y, sp[p][tid] * inv_int(p + 1));
+      e = fmaf(e, y, sp[p][tid]);
+    }
+    for (int r = 0; r < s; ++r) {
+      gm[tid] = g;
+      em[tid] = e;
+      __syncthreads();
+      float ge = 0.0f, ee = 0.0f;
+#pragma unroll
+      for (int c = 0; c < 16; ++c) {
+        ge = fmaf(gm[i * 16 + c], em[c * 16 + j], ge);
+        ee = fmaf(em[i * 16 + c], em[c * 16 + j], ee);
+      }
+      __syncthreads();
+      g = 0.5f * (ge + g);
+      e = ee;
+    }
+    gm[tid] = g;
+    __syncthreads();
+    if (tid < 16) {
+      float acc = 0.0f;
+#pragma unroll
+      for (int c = 0; c < 16; ++c) acc = fmaf(gm[tid * 16 + c], vv[c], acc);
+      a.loc[((size_t)b * a.n_int + t) * a.LW + tid] = tid < a.d ? acc : 0.0f;
+    }
+    __syncthreads();
+  }
+}
+
+// Adjoint of s1 = phi(X) v, X = -h A, for the level-1 cotangent g of every interval (read from loc, then zeroed
+// there, so that the series leaf's adjoint that follows sees level 2 only):
+//   dv = phi(X)^T g,  dX = Gam = int_0^1 int_0^s e^{(s-r) X^T} g v^T e^{r X^T} dr ds,  dA += -h Gam,
+//   dh = -<A, Gam>.
+// Gam is the upper block of phi(Z) for the block-triangular Z = [[X^T, g v^T], [0, X^T]] (the Frechet derivative
+// of phi; its diagonal blocks are phi(X^T)), evaluated on Z / 2^s (the same s as the forward) by Horner over the
+// blocks, G_p = I / (p+1)! + Z G_{p+1} (P G_d = g (G_d^T v)^T stays a rank-one update), E = I + Z G, then s
+// doublings on the blocks: G <- G (E + I) / 2, E <- E E. Per-interval dv and dh go to dv1 / dh1 (added after the
+// series adjoint), -h Gam summed per workgroup into part (a fixed-order sum in k_bs_dA).
+__global__ __launch_bounds__(256) void k_bs_level1_bwd(Args a, float* __restrict__ dv1, float* __restrict__ dh1,
+                                                       float* __restrict__ part) {
+  __shared__ float at[256];  // A^T (padded)
+  __shared__ float yt[256], gd[256], gu[256], ed[256], eu[256];
+  __shared__ float gv[16], vv[16], w[16];
+  __shared__ float red[256];
+  const int tid = threadIdx.x, i = tid >> 4, j = tid & 15;
+  at[tid] = a.apow[256 + j * 16 + i];  // P_1 = A
+  const float norm1 = a.apow[a.npow * 256];
+  float dA = 0.0f;
+  __syncthreads();
+  const long total = (long)a.B * a.n_int;
+  for (long it = blockIdx.x; it < total; it += gridDim.x) {
+    const int b = (int)(it / a.n_int), t = (int)(it - (long)b * a.n_int);
+    const float* th = a.clock + (size_t)b * a.L;
+    const float h = th[t + 1] - th[t];
+    float* row = a.loc + ((size_t)b * a.n_int + t) * a.LW;
+    if (tid < 16) {
+      const float* x = a.path + ((size_t)b * a.L + t) * a.d;
+      vv[tid] = tid < a.d ? x[a.d + tid] - x[tid] : 0.0f;
+      gv[tid] = tid < a.d ? row[tid] : 0.0f;
+    }
+    int s = 0;
+    float xn = fabsf(h) * norm1;
+    while (xn > 1.0f && s < SQMAX) {
+      xn *= 0.5f;
+      ++s;
+    }
+    const float scl = ldexpf(1.0f, -s), y = -h * scl;
+    yt[tid] = y * at[tid];
+    if (tid < 16) row[tid] = 0.0f;  // the series adjoint sees no level-1 cotangent (gv holds it)
+    // Horner start: G_PM = I / (PM + 1)!
+    float cfac = 1.0f;
+    for (int p = 2; p <= PM + 1; ++p) cfac *= inv_int(p);
+    gd[tid] = i == j ? cfac : 0.0f;
+    gu[tid] = 0.0f;
+    __syncthreads();
+    for (int p = PM - 1; p >= -1; --p) {  // p = -1: E = I + Z G
+      if (tid < 16) {
+        float acc = 0.0f;
+#pragma unroll
+        for (int k = 0; k < 16; ++k) acc = fmaf(vv[k], gd[k * 16 + tid], acc);
+        w[tid] = acc;
+      }
+      __syncthreads();
+      float nd = 0.0f, nu = 0.0f;
+#pragma unroll
+      for (int c = 0; c < 16; ++c) {
+        nd = fmaf(yt[i * 16 + c], gd[c * 16 + j], nd);
+        nu = fmaf(yt[i * 16 + c], gu[c * 16 + j], nu);
+      }
+      nu = fmaf(scl * gv[i], w[j], nu);
+      if (p >= 0) {
+        float c = 1.0f;  // 1 / (p + 1)!
+        for (int m = 2; m <= p + 1; ++m) c *= inv_int(m);
+        nd += i == j ? c : 0.0f;
+        __syncthreads();
+        gd[tid] = nd;
+        gu[tid] = nu;
+      } else {
+        nd += i == j ? 1.0f : 0.0f;
+        __syncthreads();
+        ed[tid] = nd;
+        eu[tid] = nu;
+      }
+      __syncthreads();
+    }
+    for (int r = 0; r < s; ++r) {
+      float g_e = 0.0f, g_eu = 0.0f, u_e = 0.0f, e_e = 0.0f, e_eu = 0.0f, eu_e = 0.0f;
+#pragma unroll
+      for (int c = 0; c < 16; ++c) {
+        const float gdic = gd[i * 16 + c], guic = gu[i * 16 + c], edic = ed[i * 16 + c], euic = eu[i * 16 + c];
+        const float edcj = ed[c * 16 + j], eucj = eu[c * 16 + j];
+        g_e = fmaf(gdic, edcj, g_e);
+        g_eu = fmaf(gdic, eucj, g_eu);
+        u_e = fmaf(guic, edcj, u_e);
+        e_e = fmaf(edic, edcj, e_e);
+        e_eu = fmaf(edic, eucj, e_eu);
+        eu_e = fmaf(euic, edcj, eu_e);
+      }
+      const float ngd = 0.5f * (g_e + gd[tid]), ngu = 0.5f * (g_eu + u_e + gu[tid]);
+      __syncthreads();
+      gd[tid] = ngd;
+      gu[tid] = ngu;
+      ed[tid] = e_e;
+      eu[tid] = e_eu + eu_e;
+      __syncthreads();
+    }
+    // gd = phi(X^T), gu = Gam
+    const float gam = gu[tid];
+    dA = fmaf(-h, gam, dA);
+    red[tid] = at[j * 16 + i] * gam;  // A[i][j] Gam[i][j]
+    __syncthreads();
+    for (int o = 128; o >= 1; o >>= 1) {
+      if (tid < o) red[tid] += red[tid + o];
+      __syncthreads();
+    }
+    if (tid < 16) {
+      float acc = 0.0f;
+#pragma unroll
+      for (int k = 0; k < 16; ++k) acc = fmaf(gd[tid * 16 + k], gv[k], acc);
+      dv1[it * 16 + tid] = acc;
+    }
+    if (tid == 0) dh1[it] = -red[0];
+    __syncthreads();
+  }
+  part[(size_t)blockIdx.x * 256 + tid] = dA;
+}
+
+// the level-1 shares of dv and dh added to the series adjoint's (which wrote o.dv / o.dh)
+__global__ void k_bs_add(Args a, LeafBwd o, const float* __restrict__ dv1, const float* __restrict__ dh1) {
+  const long total = (long)a.B * a.n_int;
+  for (long e = (long)blockIdx.x * blockDim.x + threadIdx.x; e < total * 17; e += (long)gridDim.x * blockDim.x) {
+    if (e < total * 16) o.dv[e] += dv1[e];
+    else o.dh[e - total * 16] += dh1[e - total * 16];
+  }
+}
+
+// grad_A += the workgroups' -h Gam sums, in a fixed order (float64)
+__global__ __launch_bounds__(256) void k_bs_dA(Args a, const float* __restrict__ part, int nparts, float* grad_A) {
+  const int tid = threadIdx.x, i = tid >> 4, j = tid & 15;
+  double acc = 0.0;
+  for (int w = 0; w < nparts; ++w) acc += (double)part[(size_t)w * 256 + tid];
+  if (i < a.d && j < a.d) grad_A[i * a.d + j] += (float)acc;
+}
+
 // knot cotangents: dpath[k] = dv_{k-1} - dv_k, dclock[k] = dh_{k-1} - dh_k, plus the shared steps of the cached modes
 // (the flow step th[1] - th[0], or th[2] - th[1] for the basepoint mode; the Van Loan step likewise)
 __global__ void k_knots(Args a, LeafBwd o, float* grad_path, float* grad_clock) {
@@ -2421,7 +2623,9 @@ int dense_plan(const ews_dense_desc* s, DPlan& p) {
   if (s->flow_mode < 0 || s->flow_mode > 2) return EWS_ERR_OPTION;
   if (s->readout < 0 || s->readout > 3) return EWS_ERR_OPTION;
   if (s->batch < 1 || s->length < 2 || s->dim < 1 || s->dim > 16) return EWS_ERR_SHAPE;
-  if (s->leaf != EWS_LEAF_SERIES && s->leaf != EWS_LEAF_VAN_LOAN) return EWS_ERR_OPTION;
+  if (s->leaf != EWS_LEAF_SERIES && s->leaf != EWS_LEAF_VAN_LOAN && s->leaf != EWS_LEAF_BLOCK_SERIES)
+    return EWS_ERR_OPTION;
+  if (s->leaf == EWS_LEAF_BLOCK_SERIES && s->depth > 2) return EWS_ERR_DEPTH;
   const bool vl = s->leaf == EWS_LEAF_VAN_LOAN;
   if (!vl && (s->series_q < 0 || s->series_q > QMAX)) return EWS_ERR_OPTION;
   if (vl && (s->vl_steps < 1 || s->vl_steps > 64)) return EWS_ERR_OPTION;
@@ -2459,7 +2663,8 @@ int dense_plan(const ews_dense_desc* s, DPlan& p) {
 constexpr int kLeafBwdBlocks = 1024;  // workgroups of the leaf adjoint (one partial dA set each)
 
 struct DWs {
-  size_t apow, loc, fl, summ, sfl, car, pre, mats, lloc, lam, amax, dv, dh, dsh, dshi, part, hsum, vlsave, total;
+  size_t apow, loc, fl, summ, sfl, car, pre, mats, lloc, lam, amax, dv, dh, dsh, dshi, part, hsum, vlsave;
+  size_t bsdv, bsdh, bspart, total;  // block-series level 1: per-interval dv / dh and the workgroups' dA sums
 };
 // bwd: the backward's layout, the forward's buffers (prefix rows always) followed by the adjoint scan's
 DWs dense_ws(const DPlan& p, int readout, bool bwd = false) {
@@ -2487,6 +2692,10 @@ DWs dense_ws(const DPlan& p, int readout, bool bwd = false) {
     w.part = off; off += al256((size_t)kLeafBwdBlocks * (HP + 1) * 256 * 4);
     w.hsum = off; off += al256((size_t)PRS * (HP + 1) * 256 * 8);
     w.vlsave = off; off += p.leaf == EWS_LEAF_VAN_LOAN ? al256(BN * (512 + 16 * (size_t)p.vm) * 4) : 0;
+    const bool bs = p.leaf == EWS_LEAF_BLOCK_SERIES;
+    w.bsdv = off; off += bs ? al256(BN * 16 * 4) : 0;
+    w.bsdh = off; off += bs ? al256(BN * 4) : 0;
+    w.bspart = off; off += bs ? al256((size_t)kLeafBwdBlocks * 256 * 4) : 0;
   }
   w.total = off;
   return w;
@@ -2647,9 +2856,14 @@ int dense_forward_pass(const ews_dense_desc* s, const DPlan& p, const Args& a, h
   if (pass == 0) {
     hipLaunchKernelGGL(k_powers, dim3(1), dim3(256), 0, st, a);
     DENSE_CHECK();
-    if (p.leaf == EWS_LEAF_SERIES) {
+    if (p.leaf != EWS_LEAF_VAN_LOAN) {  // the series letters (block series: level 2; level 1 overwritten next)
       const int rc = launch_local(p, a, st);
       if (rc != EWS_OK) return rc;
+    }
+    if (p.leaf == EWS_LEAF_BLOCK_SERIES) {
+      const long total = (long)p.B * p.n_int;
+      hipLaunchKernelGGL(k_bs_level1, dim3((unsigned)(total < 8192 ? total : 8192)), dim3(256), 0, st, a);
+      DENSE_CHECK();
     }
     return launch_vl_and_flows(p, a, st);
   }
@@ -2817,6 +3031,14 @@ int dense_leaf_adjoint(const ews_dense_desc* desc, const DPlan& p, const Args& a
   const long total = (long)p.B * p.n_int;
   const int grid = (int)(total < kLeafBwdBlocks ? total : kLeafBwdBlocks);
   const size_t lshm = p.leaf == EWS_LEAF_VAN_LOAN ? 0 : (size_t)6 * (p.q + 1) * 16 * 4;  // k_leaf_bwd's letters
+  const bool bs = p.leaf == EWS_LEAF_BLOCK_SERIES;
+  float* bsdv = (float*)(ws + w.bsdv);
+  float* bsdh = (float*)(ws + w.bsdh);
+  float* bspart = (float*)(ws + w.bspart);
+  if (bs) {  // the exact level 1's adjoint first: it takes the level-1 cotangent out of loc
+    hipLaunchKernelGGL(k_bs_level1_bwd, dim3(grid), dim3(256), 0, st, a, bsdv, bsdh, bspart);
+    DENSE_CHECK();
+  }
 #define EWS_LEAF_BWD(KER, NN)                                                                               \
   do {                                                                                                      \
     if (p.chen_expm == EWS_EXPM_EXACT) hipLaunchKernelGGL((KER<NN, true>), dim3(grid), dim3(256), lshm, st, a, o); \
@@ -2833,10 +3055,18 @@ int dense_leaf_adjoint(const ews_dense_desc* desc, const DPlan& p, const Args& a
   }
 #undef EWS_LEAF_BWD
   DENSE_CHECK();
+  if (bs) {
+    hipLaunchKernelGGL(k_bs_add, dim3(256), dim3(256), 0, st, a, o, bsdv, bsdh);
+    DENSE_CHECK();
+  }
   hipLaunchKernelGGL(k_part_reduce, dim3(HP + 1, PRS), dim3(256), 0, st, o.part, grid, hsum);
   DENSE_CHECK();
   hipLaunchKernelGGL(k_dA, dim3(1), dim3(256), 0, st, a, hsum, grad_A);
   DENSE_CHECK();
+  if (bs) {
+    hipLaunchKernelGGL(k_bs_dA, dim3(1), dim3(256), 0, st, a, bspart, grid, grad_A);
+    DENSE_CHECK();
+  }
   hipLaunchKernelGGL(k_dsh_reduce, dim3(p.B), dim3(256), 0, st, a, o);
   DENSE_CHECK();
   hipLaunchKernelGGL(k_knots, dim3((p.L + 255) / 256, p.B), dim3(256), 0, st, a, o, grad_path, grad_clock);

@@ -23,6 +23,7 @@ READOUTS = {"prefix": 0, "terminal": 1, "mean": 2, "max": 3, "log_prefix": 4}  #
 CHUNK_SEQUENTIAL = -1  # ews_diag_desc.chunk: the per-sample sequential kernels
 LEAF_SERIES = 0
 LEAF_VAN_LOAN = 1
+LEAF_BLOCK_SERIES = 2
 DIAG_LEAVES = {"plane_closed": 0, "block_series": 1, "series": 2}
 EXPM_SCHEMES = {"exact": 0, "euler": 1, "cayley": 2, "pade": 3}
 DTYPE_F32 = 0

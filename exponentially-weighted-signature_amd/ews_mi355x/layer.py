@@ -22,38 +22,20 @@ ews/core/kernels/combine.py:37-63):
     Jordan chains, leaf "jordan_closed(_tables)";    the chains' closed-form local terms at any step (float64
     planes, "plane_closed" with approximate flows    tables on the device), flows of chen_expm (exact for
                                                      jordan_flows), the dense combine (d <= 16, at most 8 chains)
-    block-diagonal A, leaf "block_series"            dense kernels, series leaf of order >= 24: the exact level 1
-                                                     to float32 while clock step x ||A||_1 <= 4 (an error past it);
-                                                     an order whose truncation is visible at the call's largest step
-                                                     raises (its level 2 is the order-q series)
+    block-diagonal A, leaf "block_series"            dense kernels: the exact level 1 phi(-h A) v at any step
+                                                     (scaled Taylor and doublings), the order-series_q series at
+                                                     level 2, flows of chen_expm
     anything else                                    NotImplementedError
 """
 
 from __future__ import annotations
 
-import math
 from typing import Optional
 
 import torch
 
 from . import ops
 from .params import AParamConstant, block_sizes_of, diagonal_structure, is_rotation_planes, jordan_chains_of
-
-# Leaves whose terms are exact integrals (the Jordan closed forms, the block-series leaf's exact level 1): the series
-# order that reproduces them in float32, and the largest clock step times ||A||_1 for which it does (truncation
-# x^(q+1) / (q+1)! below 1e-10 and at most one digit of cancellation)
-EXACT_Q = 24
-EXACT_MAX_STEP = 4.0
-# largest truncation bound of the reference's series (ews/core/series_leaf.py:139-143) at which exact integrals stand
-# in for an order-q series: below float32 resolution
-SERIES_EXACT_TOL = 1e-7
-
-
-def series_error_bound(x: float, k: int, q: int) -> float:
-    """Per-interval relative error bound of the order-q series at level k, x = ||A|| h
-    (ews/core/series_leaf.py:139-143)."""
-    return (k * x) ** (q + 1) / math.factorial(q + 1) * math.exp(k * x)
-
 
 LEAF_KINDS = ("van_loan", "series", "plane_closed", "block_series", "jordan_closed", "jordan_closed_tables")
 COMBINE_KINDS = ("assoc", "lean", "block_kernel", "dense_kernel")
@@ -214,27 +196,11 @@ class EWS(torch.nn.Module):
                 return ops.jordan_scan(path.to(torch.float32), clock.to(torch.float32),
                                        A.to(path.device).contiguous(), self.N, kind, size, self._flow_mode(readout),
                                        readout, level0, chen_expm=chen)
-            if self.leaf in ("block_series", "plane_closed"):
-                # the block-series leaf (exact level 1, blockwise series of order series_q at level 2) on general
-                # blocks: the series kernels at order >= EXACT_Q reproduce its exact level 1 to float32 while the
-                # series argument stays small (checked here, loudly)
-                hmax = float((clock[..., 1:] - clock[..., :-1]).abs().max()) if clock.shape[-1] > 1 else 0.0
-                anorm = float(A.abs().sum(0).max())
-                if hmax * anorm > EXACT_MAX_STEP:
-                    raise NotImplementedError(
-                        f"leaf={self.leaf!r}: clock step x ||A||_1 = {hmax * anorm:.3g} exceeds {EXACT_MAX_STEP} "
-                        "(the large-step regime of the reference's exact forms is not built here)")
-                if self.leaf == "block_series" and self.N == 2 and (self.series_q or 0) < EXACT_Q:
-                    # the reference's level 2 is the order-q series (blockdiag_engine.py:143-154); these kernels
-                    # evaluate the exact integrals, which equal it only while its truncation is invisible
-                    xop = hmax * max(anorm, float(A.abs().sum(1).max()))  # >= ||A||_op h
-                    if series_error_bound(xop, 2, int(self.series_q)) > SERIES_EXACT_TOL:
-                        raise NotImplementedError(
-                            f"leaf='block_series' on general blocks: series_q={self.series_q} truncates visibly at "
-                            f"||A|| h = {xop:.3g}; the order-q level-2 series runs for rotation planes and real "
-                            f"diagonals (exact flows), or take series_q >= {EXACT_Q}")
-                q = max(EXACT_Q, self.series_q or 0)
-                leaf = ops.DenseLeaf("series", q=q, chen_expm=chen)
+            if self.leaf == "block_series":
+                # the block-series leaf (general blocks, or planes / diagonals under approximate flows): the exact
+                # level 1 G v at any step and the blockwise order-series_q series at level 2, as the reference
+                # computes them (ews/core/leaf.py:138-175, blockdiag_engine.py:88-155)
+                leaf = ops.DenseLeaf("block_series", q=self.series_q or 0, chen_expm=chen)
                 return ops.dense_scan(path.to(torch.float32), clock.to(torch.float32),
                                       A.to(path.device).contiguous(), self.N, leaf.q, self._flow_mode(readout),
                                       readout, level0, leaf=leaf)

@@ -113,13 +113,14 @@ _VL_MODES = {"displacement": nat.FLOW_PER_INTERVAL, "displacement_uniform": nat.
 
 
 class DenseLeaf:
-    """Leaf options of the dense path (ews/core/leaf.py:50-198): the series leaf of order q, or the Van Loan leaf
-    with M knots per interval, its exponential scheme and its reweighting mode; chen_expm is the flows' scheme."""
+    """Leaf options of the dense path (ews/core/leaf.py:50-198): the series leaf of order q, the block-series leaf
+    (the exact level 1 at any step and the order-q series at level 2), or the Van Loan leaf with M knots per
+    interval, its exponential scheme and its reweighting mode; chen_expm is the flows' scheme."""
 
     def __init__(self, kind="series", q=0, M=20, van_loan_expm="cayley", reweighting_mode="displacement",
                  chen_expm="exact"):
-        if kind not in ("series", "van_loan"):
-            raise ValueError(f"dense leaf must be 'series' or 'van_loan', got {kind!r}")
+        if kind not in ("series", "van_loan", "block_series"):
+            raise ValueError(f"dense leaf must be 'series', 'block_series' or 'van_loan', got {kind!r}")
         if reweighting_mode not in _VL_MODES:
             raise ValueError(
                 "reweighting_mode must be 'displacement', 'displacement_uniform', or "
@@ -139,8 +140,9 @@ class DenseLeaf:
 def make_dense_desc(B, L, d, N, q, flow_mode, readout, level0, chunk=0, leaf=None):
     leaf = leaf if leaf is not None else DenseLeaf("series", q)
     vl = leaf.kind == "van_loan"
+    kind = {"series": nat.LEAF_SERIES, "van_loan": nat.LEAF_VAN_LOAN, "block_series": nat.LEAF_BLOCK_SERIES}[leaf.kind]
     return nat.DenseDesc(B, L, d, N, int(q) if not vl else 0, _FLOW_MODES[flow_mode], nat.READOUTS[readout],
-                         int(level0), int(chunk), nat.LEAF_VAN_LOAN if vl else nat.LEAF_SERIES,
+                         int(level0), int(chunk), kind,
                          leaf.M if vl else 0, nat.EXPM_SCHEMES[leaf.van_loan_expm] if vl else 0,
                          _VL_MODES[leaf.reweighting_mode] if vl else 0, nat.EXPM_SCHEMES[leaf.chen_expm])
 

@@ -140,6 +140,10 @@ int ews_diag_forward_noalloc(const ews_diag_desc* desc, const void* path, const 
 /* leaves of the dense path (ews/core/leaf.py:50-198) */
 #define EWS_LEAF_SERIES 0   /* series_local_signatures (ews/core/series_leaf.py:116-126) */
 #define EWS_LEAF_VAN_LOAN 1 /* reweighted_segments_van_loan + compute_reweighted_signatures (van_loan.py:163-184) */
+/* block_series (ews/core/leaf.py:138-175, ews/core/kernels/blockdiag_engine.py:88-155): the exact level 1
+ * G v, G = int_0^1 exp(-s h A) ds at any step, and the series leaf's order-series_q level 2 (depths 1 and 2; on a
+ * block-diagonal A the blockwise letters are the letters of A) */
+#define EWS_LEAF_BLOCK_SERIES 2
 
 /* matrix exponential schemes (ews/core/expm_approx.py:13-41) */
 #define EWS_EXPM_EXACT 0

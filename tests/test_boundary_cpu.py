@@ -198,7 +198,8 @@ def test_dense_c_abi_error_codes():
         "readout": (_ddesc(readout=9), -4),
         "flow mode": (_ddesc(flow_mode=3), -4),
         "basepoint length": (_ddesc(flow_mode=2, length=2), -2),
-        "leaf": (_ddesc(leaf=2), -4),
+        "leaf": (_ddesc(leaf=3), -4),
+        "block series at depth 3": (_ddesc(leaf=2, depth=3), -3),
         "van loan knots 0": (_ddesc(leaf=1, vl_steps=0), -4),
         "van loan knots 65": (_ddesc(leaf=1, vl_steps=65), -4),
         "van loan scheme": (_ddesc(leaf=1, vl_steps=20, vl_expm=4), -4),
@@ -209,6 +210,12 @@ def test_dense_c_abi_error_codes():
     for name, (dsc, code) in bad.items():
         assert lib.ews_dense_forward(ctypes.byref(dsc), null, null, null, null, null, null) == code, name
         assert lib.ews_dense_workspace_bytes(ctypes.byref(dsc)) == 0, name
+    # the block-series leaf (depths 1 and 2): the series leaf's buffers plus its level-1 adjoint's
+    bsd = _ddesc(leaf=2, depth=2)
+    assert lib.ews_dense_workspace_bytes(ctypes.byref(bsd)) == lib.ews_dense_workspace_bytes(
+        ctypes.byref(_ddesc(depth=2)))
+    assert lib.ews_dense_backward_workspace_bytes(ctypes.byref(bsd)) > lib.ews_dense_backward_workspace_bytes(
+        ctypes.byref(_ddesc(depth=2)))
     # the Van Loan leaf ignores the series order; its options are checked instead
     vl = _ddesc(leaf=1, vl_steps=64, vl_expm=3, vl_mode=2, series_q=99, chen_expm=2)
     assert lib.ews_dense_workspace_bytes(ctypes.byref(vl)) > 0
