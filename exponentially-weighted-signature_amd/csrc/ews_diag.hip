@@ -1915,8 +1915,15 @@ int make_plan(const ews_diag_desc* s, Plan& p) {
 }
 
 struct WsLayout {
-  size_t summ, mu, mt, red, red_idx, dv, dh, gp, gph, gpart, gagg, gcar, qagg, qflow, ql1, cflow, gcot, total;
+  size_t summ, mu, mt, red, red_idx, dv, dh, gp, gph, gpart, gagg, gcar, qagg, qflow, ql1, cflow, gcot;
+  size_t lbflag, lbagg, total;
 };
+// the look-back forward's status words (and ticket), quad and group aggregates (groups of 8 quads)
+void lb_layout(const Plan& p, WsLayout& w, size_t& off) {
+  const size_t NQ = (p.C + 3) / 4, NG = (NQ + 7) / 8, items = (size_t)p.B * (NQ + NG);
+  w.lbflag = off; off += p.fast ? align256((items + 1) * 4) : 0;
+  w.lbagg = off; off += p.fast ? align256(items * (p.D + 2 * p.K) * 8) : 0;
+}
 WsLayout ws_layout(const Plan& p) {
   WsLayout w{};
   size_t off = 0;
@@ -1944,6 +1951,7 @@ WsLayout ws_layout(const Plan& p) {
   w.ql1 = off; off += p.fast ? align256((size_t)p.B * NQ * p.K * 16) : 0;
   w.cflow = off; off += p.fast ? align256(BC * p.K * 16) : 0;
   w.gcot = off; off += p.log ? align256((size_t)p.B * p.n_int * p.D * 4) : 0;
+  lb_layout(p, w, off);
   w.total = off;
   return w;
 }
@@ -1965,6 +1973,7 @@ WsLayout ws_layout_fwd(const Plan& p) {
   w.qflow = off; off += p.fast ? align256((size_t)p.B * NQ * p.K * 16) : 0;
   w.ql1 = off; off += p.fast ? align256((size_t)p.B * NQ * p.K * 16) : 0;
   w.cflow = off; off += p.fast ? align256(BC * p.K * 16) : 0;
+  lb_layout(p, w, off);
   w.total = off;
   return w;
 }
@@ -2025,6 +2034,7 @@ DiagArgs make_args(const ews_diag_desc* s, const Plan& p, const void* path, cons
   a.NQ = (p.C + 3) / 4;
   a.qagg = (float*)(ws + w.qagg); a.qflow = (double*)(ws + w.qflow); a.ql1 = (double*)(ws + w.ql1);
   a.cflow = (double*)(ws + w.cflow);
+  a.lbflag = (int*)(ws + w.lbflag); a.lbagg = (double*)(ws + w.lbagg);
   if (p.log && !fwd_only) a.gcot = (float*)(ws + w.gcot);
   return a;
 }
@@ -2043,19 +2053,16 @@ int forward_pass(const ews_diag_desc* s, const Plan& p, DiagArgs a, hipStream_t 
   dim3 grid(p.C, p.B), blk(p.NT);
   switch (pass) {
     case 0:
-      if (p.fast) {
+      if (p.fast) {  // the pair-group forward: the coefficient table here, everything else in pass 2
         if (pairs_forward(a, st, false) != 0) return EWS_ERR_LAUNCH;
-      } else {
-        hipLaunchKernelGGL((k_chunk_fwd<CPLX, N, MODE_SUMMARY, MAXT, true>), grid, blk, fwd_lds(p), st, a);
-        EWS_LAUNCH_CHECK();
+        return EWS_OK;
       }
+      hipLaunchKernelGGL((k_chunk_fwd<CPLX, N, MODE_SUMMARY, MAXT, true>), grid, blk, fwd_lds(p), st, a);
+      EWS_LAUNCH_CHECK();
       hipLaunchKernelGGL((k_chunk_fwd<CPLX, N, MODE_SUMMARY, MAXT, false>), grid, blk, fwd_lds(p), st, a);
       break;
     case 1:
-      if (p.fast) {
-        if (pairs_carry_scan(a, st, false) != 0) return EWS_ERR_LAUNCH;
-        break;
-      }
+      if (p.fast) return EWS_OK;
       hipLaunchKernelGGL((k_fwd_group<CPLX, N, MAXT, false>), dim3(p.NG, p.B), blk, p.lds_carry, st, a);
       EWS_LAUNCH_CHECK();
       hipLaunchKernelGGL((k_fwd_group_scan<CPLX, N, MAXT>), dim3(p.B), blk, 0, st, a);
@@ -2064,12 +2071,12 @@ int forward_pass(const ews_diag_desc* s, const Plan& p, DiagArgs a, hipStream_t 
       break;
     case 2:
       if (s->readout == EWS_READOUT_PREFIX || s->readout == EWS_READOUT_LOGPREFIX) {
-        if (p.fast) {
+        if (p.fast) {  // the look-back forward: every chunk (uniform or not), carries and rows in one launch
           if (pairs_forward(a, st, true) != 0) return EWS_ERR_LAUNCH;
-        } else {
-          hipLaunchKernelGGL((k_chunk_fwd<CPLX, N, MODE_PREFIX, MAXT, true>), grid, blk, fwd_lds(p), st, a);
-          EWS_LAUNCH_CHECK();
+          return EWS_OK;
         }
+        hipLaunchKernelGGL((k_chunk_fwd<CPLX, N, MODE_PREFIX, MAXT, true>), grid, blk, fwd_lds(p), st, a);
+        EWS_LAUNCH_CHECK();
         hipLaunchKernelGGL((k_chunk_fwd<CPLX, N, MODE_PREFIX, MAXT, false>), grid, blk, fwd_lds(p), st, a);
       } else if (s->readout == EWS_READOUT_MEAN || s->readout == EWS_READOUT_MAX) {
         hipLaunchKernelGGL((k_chunk_fwd<CPLX, N, MODE_REDUCE, MAXT, true>), grid, blk, fwd_lds(p), st, a);
@@ -2120,7 +2127,7 @@ int backward_pass(const Plan& p, DiagArgs a, hipStream_t st, int pass) {
       break;
     case 1:
       if (p.fast) {
-        if (pairs_carry_scan(a, st, true) != 0) return EWS_ERR_LAUNCH;
+        if (pairs_carry_scan(a, st) != 0) return EWS_ERR_LAUNCH;
         break;
       }
       hipLaunchKernelGGL((k_bwd_group<CPLX, N, (MAXT < 256 ? 256 : MAXT), false>), dim3(p.NG, p.B), dim3(p.NT),

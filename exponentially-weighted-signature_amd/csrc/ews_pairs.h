@@ -14,13 +14,13 @@ constexpr int kCoefTabFloats = 16 + 2 * 9 * 8 + 2 * 16 * 64;
 // True if the configuration has pair-group kernels (rotation planes, d = 16, depth 2, prefix readout,
 // per-interval flows, chunk length <= kMaxT).
 bool pairs_eligible(int structure, int depth, int dim, int readout, int flow_mode, int T);
-// Uniform chunks of the forward: summaries (out = false; this launch first builds the coefficient table a.ctab
-// and then writes every chunk's classification a.cflag / a.chbar, so it runs before any other kernel of the
-// call) or prefix rows (out = true).
+// The forward: the coefficient table a.ctab and the look-back words zeroed (out = false; runs before any other
+// kernel of the call), or the look-back forward (out = true): every chunk's classification (a.cflag / a.chbar),
+// the float64 carries (a.carries) and the prefix rows, in one launch.
 int pairs_forward(const DiagArgs& a, hipStream_t st, bool out);
-// Float64 carry scan over quads of four chunks: forward carries (backward = false) or the adjoint carries
-// (backward = true); the pair-group prefix / full-adjoint kernels rebuild the carries inside each quad.
-int pairs_carry_scan(const DiagArgs& a, hipStream_t st, bool backward);
+// Float64 adjoint carry scan over quads of four chunks; the full-adjoint kernels rebuild the carries inside each
+// quad.
+int pairs_carry_scan(const DiagArgs& a, hipStream_t st);
 // Uniform chunks of the backward: chunk-local adjoints (full = false) or the full adjoint (full = true).
 int pairs_backward(const DiagArgs& a, hipStream_t st, bool full);
 

@@ -42,6 +42,10 @@ namespace pairs {
 constexpr int K = 8;      // planes
 constexpr int DIM = 16;   // channels
 constexpr int NB = 4;     // steps per block of the full adjoint's column sums
+// look-back forward (k_fwd_lb)
+constexpr int kSpinLimit = 1 << 20;  // polls of the status words before giving up (never reached)
+constexpr int LBB = 4;               // aggregates whose loads are in flight together in the look-back
+constexpr int LBG = 8;               // quads per look-back group
 constexpr int VPITCH = (kMaxT + 1) * DIM;  // LDS floats per group of staged increments (one padding row)
 
 template <int KP> struct Geo {
@@ -325,6 +329,10 @@ __device__ __forceinline__ float ref_step(const DiagArgs& a) {
 // Three wavefronts share the entries (a single chain of series and exponentials per lane otherwise): wavefront 0
 // the plane nodes and the pair flows, 1 the B-pair divided differences, 2 the A-pair ones.
 __global__ __launch_bounds__(192) void k_coef_table(DiagArgs a) {
+  // the look-back forward's status words (quads, then groups of LBG quads) and its ticket start at zero (this
+  // launch runs first)
+  const int nwords = a.B * (a.NQ + (a.NQ + LBG - 1) / LBG) + 1;
+  for (int i = threadIdx.x; i < nwords; i += blockDim.x) a.lbflag[i] = 0;
   const int role = threadIdx.x >> 6, l = threadIdx.x & 63;
   const int j = l >> 3, k = l & 7;
   float* tab = a.ctab;
@@ -333,7 +341,16 @@ __global__ __launch_bounds__(192) void k_coef_table(DiagArgs a) {
   const cf xj = h0 * uj;
   const cf ub = uj + uk, ua = uj + conj(uk);
   if (role == 0) {
-    if (l == 0) tab[0] = h0;
+    if (l == 0) {  // header: the reference step, max |u_j| and max d_j (the chunk classification's bounds)
+      float R = 0.0f, Dm = 0.0f;
+      for (int p = 0; p < K; ++p) {
+        R = fmaxf(R, absv(load_u(a.params, p)));
+        Dm = fmaxf(Dm, a.params[2 * p]);
+      }
+      tab[0] = h0;
+      tab[1] = R;
+      tab[2] = Dm;
+    }
     if (k == 0) {
       const Node1<cf> nj = node1(xj);
       const cf ri = expv(-xj);
@@ -428,23 +445,30 @@ __device__ __forceinline__ float row_max16(float v) {
   return v;
 }
 __device__ __forceinline__ int classify_chunk(const DiagArgs& a, int b, int c, int gl, float& hb) {
+  constexpr int U = kMaxT / 16;
   const int t0 = c * a.T, Tc = min(a.T, a.n_int - t0);
   const float* th = a.clock + (size_t)b * a.L + t0;
-  float R = 0.0f, Dm = 0.0f;
-  for (int j = 0; j < K; ++j) {
-    R = fmaxf(R, absv(load_u(a.params, j)));
-    Dm = fmaxf(Dm, a.params[2 * j]);
+  const float R = a.ctab[1], Dm = a.ctab[2];  // max |u_j| and max d_j, from the coefficient table's header
+  float x0[U], x1[U];
+#pragma unroll
+  for (int u = 0; u < U; ++u) {  // every clock load in flight before the first use
+    const int t = gl + 16 * u;
+    x0[u] = t < Tc ? th[t] : 0.0f;
+    x1[u] = t < Tc ? th[t + 1] : 0.0f;
   }
   const float th0 = th[0];
   const float tau = th[Tc] - th0;
   hb = tau / (float)Tc;
   float dev = 0.0f, drift = 0.0f, bad = 0.0f;
-  for (int t = gl; t < Tc; t += 16) {
-    const float x0 = th[t], x1 = th[t + 1];
-    const float h = x1 - x0;
-    if (!isfinite(h)) bad = 1.0f;
-    dev = fmaxf(dev, fabsf(h - hb));
-    drift = fmaxf(drift, fabsf((x1 - th0) - (float)(t + 1) * hb));
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    const int t = gl + 16 * u;
+    if (t < Tc) {
+      const float h = x1[u] - x0[u];
+      if (!isfinite(h)) bad = 1.0f;
+      dev = fmaxf(dev, fabsf(h - hb));
+      drift = fmaxf(drift, fabsf((x1[u] - th0) - (float)(t + 1) * hb));
+    }
   }
   dev = row_max16(dev);
   drift = row_max16(drift);
@@ -562,20 +586,6 @@ __device__ __forceinline__ void quad_flows(const DiagArgs& a, int b, int q, int 
   __syncthreads();
 }
 
-__global__ __launch_bounds__(64) void k_quad_fwd_agg(DiagArgs a) {
-  __shared__ dc s_F[4][K];
-  const int q = blockIdx.x, b = blockIdx.y, j = threadIdx.x >> 3, k = threadIdx.x & 7;
-  const int c0 = 4 * q, nc = min(4, a.C - c0);
-  quad_flows(a, b, q, c0, nc, s_F);
-  PairSt s{};
-  for (int i = 0; i < nc; ++i) {
-    const float* sp = a.summ + ((size_t)b * a.C + c0 + i) * a.D;
-    chen_d(s, s_F[i][j], s_F[i][k], ld_fd(sp + 2 * j), ld_fd(sp + 2 * k), ld_fd(sp + poff(j, k)),
-           ld_fd(sp + poff(j, k) + 2));
-  }
-  store_st_f(a.qagg + ((size_t)b * a.NQ + q) * a.D, j, k, s);
-}
-
 // Scans over the quads of one sample, one workgroup of SW wavefronts per sample. The quad inputs are staged into
 // LDS a segment of up to SSEG quads at a time by the whole workgroup; the segment's quads are split into SW blocks
 // of consecutive quads, one per wavefront:
@@ -647,59 +657,6 @@ __device__ __forceinline__ void put_block(ScanLds& sg, int w, int l, const PairS
 }
 __device__ __forceinline__ PairSt get_block(const ScanLds& sg, int w, int l) {
   return PairSt{sg.bS1[w][l], sg.bSA[w][l], sg.bSB[w][l]};
-}
-
-__global__ __launch_bounds__(SW * 64) void k_quad_fwd_scan(DiagArgs a) {
-  extern __shared__ __align__(16) char scan_smem[];
-  ScanLds& sg = *reinterpret_cast<ScanLds*>(scan_smem);
-  const int b = blockIdx.x, w = threadIdx.x >> 6, l = threadIdx.x & 63, j = l >> 3, k = l & 7;
-  PairSt carry{};  // segment carry, kept by wavefront 0
-  for (int q0 = 0; q0 < a.NQ; q0 += SSEG) {
-    const int nq = min(SSEG, a.NQ - q0);
-    stage_seg(a, b, q0, nq, false, sg);
-    __syncthreads();
-    int lo, hi;
-    seg_block(nq, w, lo, hi);
-    {  // 1. block summary and flow from a zero state
-      PairSt s{};
-      dc Fj{1.0, 0.0};
-      if (lo < hi) {
-        QOps o = q_ops(sg, lo, j, k, false);
-        for (int q = lo; q < hi; ++q) {
-          const QOps cur = o;
-          if (q + 1 < hi) o = q_ops(sg, q + 1, j, k, false);
-          chen_d(s, cur.Fj, cur.Fk, cur.y.S1, cur.y1k, cur.y.SA, cur.y.SB);
-          Fj = Fj * cur.Fj;
-        }
-      }
-      put_block(sg, w, l, s);
-      if (k == 0) sg.bF[w][j] = Fj;
-    }
-    __syncthreads();
-    if (w == 0) {  // 2. block carries
-      for (int v = 0; v < SW; ++v) {
-        const PairSt y = get_block(sg, v, l);
-        const dc y1k = sg.bS1[v][8 * k];
-        const dc Fj = sg.bF[v][j], Fk = sg.bF[v][k];
-        wave_order();  // every lane has read block v before its slot is overwritten
-        put_block(sg, v, l, carry);
-        chen_d(carry, Fj, Fk, y.S1, y1k, y.SA, y.SB);
-      }
-    }
-    __syncthreads();
-    if (lo < hi) {  // 3. quad carries inside the block
-      PairSt s = get_block(sg, w, l);
-      QOps o = q_ops(sg, lo, j, k, false);
-      for (int q = lo; q < hi; ++q) {
-        store_st_d(a.carries + ((size_t)b * (a.C + 1) + 4 * (q0 + q)) * a.D, j, k, s);
-        const QOps cur = o;
-        if (q + 1 < hi) o = q_ops(sg, q + 1, j, k, false);
-        chen_d(s, cur.Fj, cur.Fk, cur.y.S1, cur.y1k, cur.y.SA, cur.y.SB);
-      }
-    }
-    __syncthreads();  // the segment's LDS is restaged next
-  }
-  if (w == 0) store_st_d(a.carries + ((size_t)b * (a.C + 1) + a.C) * a.D, j, k, carry);
 }
 
 __global__ __launch_bounds__(64) void k_quad_bwd_agg(DiagArgs a) {
@@ -778,139 +735,6 @@ __global__ __launch_bounds__(SW * 64) void k_quad_bwd_scan(DiagArgs a) {
       }
     }
     __syncthreads();  // the segment's LDS is restaged next
-  }
-}
-
-// ------------------------------------------------------------------------------------------------ forward
-// OUT = false: chunk summaries from a zero carry (summ), and the classification of every chunk (this launch runs
-// first); OUT = true: prefix rows from the float64 carry. 16-lane groups (KP = 4).
-template <bool OUT, bool BF16>
-__global__ __launch_bounds__(64) void k_fwd(DiagArgs a) {
-  constexpr int KP = 4, GPW = Geo<KP>::GPW;
-  __shared__ __align__(16) float s_v[2][GPW * VBLK];
-  // start states of the groups (prefix rows: the carries rebuilt inside the quad), then level-2 row staging
-  __shared__ __align__(16) float s_row[GPW][RBUF];
-  const Lane l = lane_of<KP>(threadIdx.x);
-  const int b = blockIdx.y, cb = blockIdx.x * GPW, c = cb + l.gi;
-  VRaw<GPW, BF16> vr;
-  vblk_load<GPW, BF16>(a, b, cb, 0, vr);
-  if constexpr (OUT) {
-    // the workgroup's chunks are quad cb / 4: rebuild the carries inside it from the quad's carry (float64),
-    // for this kernel's groups and for every later kernel that reads carries (generic chunks, the adjoint)
-    const int jj = threadIdx.x >> 3, kk = threadIdx.x & 7, nc = min(GPW, a.C - cb);
-    PairSt st = load_st_d(a.carries + ((size_t)b * (a.C + 1) + cb) * a.D, jj, kk);
-    for (int i = 0; i < nc; ++i) {
-      store_st_f(s_row[i], jj, kk, st);
-      if (i + 1 < nc) {
-        const float* sp = a.summ + ((size_t)b * a.C + cb + i) * a.D;
-        const double* cf = a.cflow + ((size_t)b * a.C + cb + i) * K * 2;
-        chen_d(st, ld_dd(cf + 2 * jj), ld_dd(cf + 2 * kk), ld_fd(sp + 2 * jj), ld_fd(sp + 2 * kk),
-               ld_fd(sp + poff(jj, kk)), ld_fd(sp + poff(jj, kk) + 2));
-        store_st_d(a.carries + ((size_t)b * (a.C + 1) + cb + i + 1) * a.D, jj, kk, st);
-      }
-    }
-  }
-  vblk_store<GPW, BF16>(a, cb, 0, vr, s_v[0]);
-  __syncthreads();
-  // every lane stays to the end (the block staging is shared by the wave); a group whose chunk is absent or
-  // non-uniform (left to the generic kernels) only skips the arithmetic
-  bool active = c < a.C;
-  const int ci = b * a.C + (active ? c : 0);
-  float hb = 0.0f;
-  int flag = 0;
-  if constexpr (!OUT) {
-    if (active) {
-      flag = classify_chunk(a, b, c, l.gl, hb);
-      if (l.gl == 0) {
-        a.cflag[ci] = flag;
-        a.chbar[ci] = hb;
-      }
-    }
-  } else {
-    if (active) {
-      flag = a.cflag[ci];
-      hb = a.chbar[ci];
-    }
-  }
-  active = active && (flag & 1);
-  const int t0 = active ? c * a.T : 0, Tc = active ? min(a.T, a.n_int - t0) : 0;
-  FwdCoef<KP> f;
-  fwd_coef<KP>(a, l, hb, (flag & 4) != 0, f);
-  cf S1{0.0f, 0.0f}, SA[KP], SB_[KP];
-  static_for<0, KP>([&](auto qc) {
-    constexpr int q = qc;
-    SA[q] = SB_[q] = cf{0.0f, 0.0f};
-  });
-  if constexpr (OUT) {
-    if (active) {
-      const float* cr = s_row[l.gi];
-      S1 = cf{cr[2 * l.j], cr[2 * l.j + 1]};
-      static_for<0, KP>([&](auto qc) {
-        constexpr int q = qc;
-        const f4a p2 = *reinterpret_cast<const f4a*>(cr + poff(l.j, KP * l.kg + q));
-        SA[q] = cf{0.5f * p2.x, 0.5f * p2.y};
-        SB_[q] = cf{0.5f * p2.z, 0.5f * p2.w};
-      });
-    }
-  }
-  wave_order();
-  float* orow = a.out + ((size_t)b * a.n_int + t0) * a.W;
-  const int o1 = a.off1 + 2 * l.j;
-  const int nblk = (a.T + SB - 1) / SB;
-  for (int blk = 0; blk < nblk; ++blk) {
-    if (blk + 1 < nblk) vblk_load<GPW, BF16>(a, b, cb, blk + 1, vr);
-    const float* vg = s_v[blk & 1] + l.gi * VBLK;
-    for (int st = 0; st < SB; ++st) {
-      const int t = blk * SB + st;
-      if (t >= Tc) break;
-      cf pj, pk[KP];
-      load_p<KP>(vg + st * DIM, l, pj, pk);
-      const cf cj = f.rho * S1;
-      S1 = fma_c(f.phi, pj, cj);
-      static_for<0, KP>([&](auto qc) {
-        constexpr int q = qc;
-        const cf sg = f.phk[q] * pk[q];
-        cf pi, pic;
-        prods(pj, pk[q], pi, pic);
-        SB_[q] = fma_c(f.LB[q], SB_[q], fma_c(cj, sg, f.IB[q] * pi));
-        SA[q] = fma_c(f.LA[q], SA[q], fma_c(cj, conj(sg), f.IA[q] * pic));
-      });
-      if constexpr (OUT) {
-        float* row = orow + (size_t)t * a.W;
-        if (a.lvl0 && l.gl == 0) row[0] = 1.0f;
-        if (l.kg == 0) *reinterpret_cast<f2u*>(row + o1) = f2u{S1.re, S1.im};
-        float* buf = s_row[l.gi];
-        f4a* p0 = reinterpret_cast<f4a*>(buf + row_at(2 * l.j) + 2 * KP * l.kg);
-        f4a* p1 = reinterpret_cast<f4a*>(buf + row_at(2 * l.j + 1) + 2 * KP * l.kg);
-        static_for<0, KP / 2>([&](auto ic) {
-          constexpr int i = ic, q0 = 2 * i, q1 = 2 * i + 1;
-          p0[i] = f4a{SA[q0].re + SB_[q0].re, SB_[q0].im - SA[q0].im, SA[q1].re + SB_[q1].re, SB_[q1].im - SA[q1].im};
-          p1[i] = f4a{SA[q0].im + SB_[q0].im, SA[q0].re - SB_[q0].re, SA[q1].im + SB_[q1].im, SA[q1].re - SB_[q1].re};
-        });
-        wave_order();
-        float* row2 = row + a.off2;
-        static_for<0, Pieces<KP>::NP>([&](auto ic) {
-          constexpr int i = ic;
-          const int pi = l.gl + Geo<KP>::G * i;
-          const f4a v = *reinterpret_cast<const f4a*>(buf + piece_at(pi));
-          *reinterpret_cast<f4u*>(row2 + 4 * pi) = f4u{v.x, v.y, v.z, v.w};
-        });
-        wave_order();
-      }
-    }
-    if (blk + 1 < nblk) vblk_store<GPW, BF16>(a, cb, blk + 1, vr, s_v[(blk + 1) & 1]);
-    wave_order();
-  }
-  if constexpr (!OUT) {
-    if (active) {
-      float* sp = a.summ + ((size_t)b * a.C + c) * a.D;
-      if (l.kg == 0) *reinterpret_cast<float2*>(sp + 2 * l.j) = float2{S1.re, S1.im};
-      static_for<0, KP>([&](auto qc) {
-        constexpr int q = qc;
-        *reinterpret_cast<f4a*>(sp + DIM + 4 * (l.j * K + KP * l.kg + q)) =
-            f4a{2.0f * SA[q].re, 2.0f * SA[q].im, 2.0f * SB_[q].re, 2.0f * SB_[q].im};
-      });
-    }
   }
 }
 
@@ -1898,6 +1722,447 @@ __global__ __launch_bounds__(64) void k_bwd_carry(DiagArgs a) {
   }
 }
 
+// ------------------------------------------------------------------------------------------------ look-back forward
+// The whole forward in one launch: one workgroup (one wavefront) per quad of four chunks, which takes its (sample,
+// quad) from a ticket counter, so that a quad waits only on quads whose workgroups already run:
+//   A. every chunk's classification and its summary from a zero state;
+//   B. the quad's aggregate in float64 (lane = 8 j + k), published (status 1);
+//   C. the look-back: the quad's carry is the fold of the aggregates of the earlier quads of its group of LBG quads
+//      and of the aggregates of the earlier groups; the last quad of a group publishes its group's aggregate (the
+//      fold of the group's quads) on the way. At most LBG - 1 + (quads / LBG) folds per quad, and no quad waits on
+//      another's look-back but for the group aggregates, each LBG - 1 folds after its quads' own aggregates;
+//   D. the chunk carries inside the quad (written for the backward) and the prefix rows.
+// The chunk summaries of some quads overlap other quads' row writes, and the carry scans between passes disappear.
+// Published words are agent-scope atomic stores (coherent across the XCDs' L2s without a cache write-back), ordered
+// before the status word by a wait on every outstanding memory operation; readers load them with agent-scope atomic
+// loads. The status words and the ticket are zeroed by k_coef_table, which runs first in the same stream. Uniform
+// quads run the 16-lane groups (KP = 4, coefficients at each chunk's mean step); a quad with a non-uniform chunk
+// runs one lane per pair (lane = 8 j + k) with every step's coefficients at its own clock step, chunk by chunk.
+
+__device__ __forceinline__ void pub_d(double* p, dc v) {
+  __hip_atomic_store(p, v.re, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  __hip_atomic_store(p + 1, v.im, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ dc sub_d(const double* p) {
+  return dc{__hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT),
+            __hip_atomic_load(p + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)};
+}
+__device__ __forceinline__ void pub_st(double* row, int j, int k, const PairSt& s) {
+  if (k == 0) pub_d(row + 2 * j, s.S1);
+  pub_d(row + poff(j, k), s.SA);
+  pub_d(row + poff(j, k) + 2, s.SB);
+}
+__device__ __forceinline__ PairSt sub_st(const double* row, int j, int k) {
+  return PairSt{sub_d(row + 2 * j), sub_d(row + poff(j, k)), sub_d(row + poff(j, k) + 2)};
+}
+// an aggregate (state, then its K plane flows from offset D) with status word w
+__device__ __forceinline__ void publish(double* row, int* w, int D, int j, int k, const PairSt& s, dc Fj) {
+  pub_st(row, j, k, s);
+  if (k == 0) pub_d(row + D + 2 * j, Fj);
+  __builtin_amdgcn_s_waitcnt(0);  // every published word of the wavefront has landed
+  if (threadIdx.x == 0) __hip_atomic_store(w, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ dc shfl_d(dc v, int src) { return dc{__shfl(v.re, src), __shfl(v.im, src)}; }
+
+// The look-back items of quad q, latest first: items 0 .. nq-1 the earlier quads of its group (q-1 down to its
+// group's first quad), then items nq .. nq+ng-1 the earlier groups (g-1 down to 0).
+struct LbItems {
+  const double* qrow;  // quad aggregates of the sample
+  const double* grow;  // group aggregates of the sample
+  const int* qst;      // their status words
+  const int* gst;
+  int q, g, nq, ng;
+  size_t AW;
+};
+__device__ __forceinline__ const double* item_row(const LbItems& it, int i) {
+  return i < it.nq ? it.qrow + (size_t)(it.q - 1 - i) * it.AW : it.grow + (size_t)(it.g - 1 - (i - it.nq)) * it.AW;
+}
+__device__ __forceinline__ const int* item_status(const LbItems& it, int i) {
+  return i < it.nq ? it.qst + (it.q - 1 - i) : it.gst + (it.g - 1 - (i - it.nq));
+}
+// acc <- (items i0 .. i1-1 folded, latest first) (x) acc, with the flows of the folded span in aFj, aFk; the items'
+// status words have been seen nonzero
+__device__ __forceinline__ void lb_fold(const LbItems& it, int i0, int i1, int D, int j, int k, PairSt& acc, dc& aFj,
+                                        dc& aFk) {
+  for (int b0 = i0; b0 < i1; b0 += LBB) {
+    PairSt g[LBB];
+    dc gFj[LBB], gFk[LBB];
+#pragma unroll
+    for (int u = 0; u < LBB; ++u) {
+      if (b0 + u < i1) {
+        const double* gr = item_row(it, b0 + u);
+        g[u] = sub_st(gr, j, k);
+        gFj[u] = sub_d(gr + D + 2 * j);
+        gFk[u] = sub_d(gr + D + 2 * k);
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < LBB; ++u) {
+      if (b0 + u < i1) {  // the item (earlier) followed by the folded span (later)
+        chen_d(g[u], aFj, aFk, acc.S1, shfl_d(acc.S1, 8 * k), acc.SA, acc.SB);
+        acc = g[u];
+        aFj = gFj[u] * aFj;
+        aFk = gFk[u] * aFk;
+      }
+    }
+  }
+}
+// fold items [i0, i1) as their status words turn nonzero: one load per lane reads up to 64 of them at once
+__device__ __forceinline__ bool lb_fold_ready(const LbItems& it, int i0, int i1, int D, int j, int k, PairSt& acc,
+                                             dc& aFj, dc& aFk) {
+  int polls = 0;
+  while (i0 < i1) {
+    const int i = i0 + (int)threadIdx.x;
+    const int sv = i < i1 ? __hip_atomic_load(item_status(it, i), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : 1;
+    const unsigned long long notready = __ballot(sv == 0);
+    const int nr = notready ? __ffsll((long long)notready) - 1 : 64;  // leading items already published
+    const int n = min(nr, i1 - i0);
+    lb_fold(it, i0, i0 + n, D, j, k, acc, aFj, aFk);
+    i0 += n;
+    if (n == 0) {
+      if (++polls >= kSpinLimit) return false;
+      __builtin_amdgcn_s_sleep(1);
+    }
+  }
+  return true;
+}
+
+// The steps of the group's chunk from the lane states (S1; halved pair states SA, SB) at the chunk's mean-step
+// coefficients: the summary recursion (OUT false) or the prefix rows (OUT true, row staging in buf). The staged
+// increments are shared by the wavefront: every lane runs every block, and a group whose chunk is absent only skips
+// the arithmetic.
+template <bool OUT, bool BF16>
+__device__ __forceinline__ void lb_steps(const DiagArgs& a, const Lane& l, int b, int cb, int t0, int Tc,
+                                         const FwdCoef<4>& f, cf& S1, cf* SA, cf* SB_, float (*s_v)[4 * VBLK],
+                                         float* buf) {
+  constexpr int KP = 4, GPW = 4;
+  VRaw<GPW, BF16> vr;
+  vblk_load<GPW, BF16>(a, b, cb, 0, vr);
+  vblk_store<GPW, BF16>(a, cb, 0, vr, s_v[0]);
+  wave_order();
+  float* orow = a.out + ((size_t)b * a.n_int + t0) * a.W;
+  const int o1 = a.off1 + 2 * l.j;
+  const int nblk = (a.T + SB - 1) / SB;
+  for (int blk = 0; blk < nblk; ++blk) {
+    if (blk + 1 < nblk) vblk_load<GPW, BF16>(a, b, cb, blk + 1, vr);
+    const float* vg = s_v[blk & 1] + l.gi * VBLK;
+    for (int st = 0; st < SB; ++st) {
+      const int t = blk * SB + st;
+      if (t >= Tc) break;
+      cf pj, pk[KP];
+      load_p<KP>(vg + st * DIM, l, pj, pk);
+      const cf cj = f.rho * S1;
+      S1 = fma_c(f.phi, pj, cj);
+      static_for<0, KP>([&](auto qc) {
+        constexpr int q = qc;
+        const cf sg = f.phk[q] * pk[q];
+        cf pi, pic;
+        prods(pj, pk[q], pi, pic);
+        SB_[q] = fma_c(f.LB[q], SB_[q], fma_c(cj, sg, f.IB[q] * pi));
+        SA[q] = fma_c(f.LA[q], SA[q], fma_c(cj, conj(sg), f.IA[q] * pic));
+      });
+      if constexpr (OUT) {
+        float* row = orow + (size_t)t * a.W;
+        if (a.lvl0 && l.gl == 0) row[0] = 1.0f;
+        if (l.kg == 0) *reinterpret_cast<f2u*>(row + o1) = f2u{S1.re, S1.im};
+        f4a* p0 = reinterpret_cast<f4a*>(buf + row_at(2 * l.j) + 2 * KP * l.kg);
+        f4a* p1 = reinterpret_cast<f4a*>(buf + row_at(2 * l.j + 1) + 2 * KP * l.kg);
+        static_for<0, KP / 2>([&](auto ic) {
+          constexpr int i = ic, q0 = 2 * i, q1 = 2 * i + 1;
+          p0[i] = f4a{SA[q0].re + SB_[q0].re, SB_[q0].im - SA[q0].im, SA[q1].re + SB_[q1].re, SB_[q1].im - SA[q1].im};
+          p1[i] = f4a{SA[q0].im + SB_[q0].im, SA[q0].re - SB_[q0].re, SA[q1].im + SB_[q1].im, SA[q1].re - SB_[q1].re};
+        });
+        wave_order();
+        float* row2 = row + a.off2;
+        static_for<0, Pieces<KP>::NP>([&](auto ic) {
+          constexpr int i = ic;
+          const int pi = l.gl + Geo<KP>::G * i;
+          const f4a v = *reinterpret_cast<const f4a*>(buf + piece_at(pi));
+          *reinterpret_cast<f4u*>(row2 + 4 * pi) = f4u{v.x, v.y, v.z, v.w};
+        });
+        wave_order();
+      }
+    }
+    if (blk + 1 < nblk) vblk_store<GPW, BF16>(a, cb, blk + 1, vr, s_v[(blk + 1) & 1]);
+    wave_order();
+  }
+}
+
+// The summary of a uniform chunk from a zero state in closed form, lane t = step t of the chunk. With the span
+// n_t = theta_end - theta_{t+1} after step t, pi_t = p_t e^{u n_t} (per plane) and its exclusive prefix sum
+// P_t = sum_{s<t} pi_s over the steps (the flows telescope: e^{u n_t} c_t = phi P_t for the level-1 state
+// c_t = rho S1(t-1) before step t), the chunk's full-scale summary is
+//   S1_j = phi_j sum_t pi_{t,j},
+//   SB_jk = phi_j phi_k sum_t P_{t,j} pi_{t,k} + IB_jk sum_t pi_{t,j} pi_{t,k},
+//   SA_jk = phi_j conj(phi_k) sum_t P_{t,j} conj(pi_{t,k}) + IA_jk sum_t pi_{t,j} conj(pi_{t,k}),
+// with the coefficients at the chunk's mean step. The two sums over t are real 16 x 16 outer-product sums on fp32
+// MFMA (every complex product is a combination of their four real products). Writes the summary in the layout of
+// s_row (level 1 at 2 j, pair (j, k) at poff).
+// The lane's operands of one chunk's closed form (lane t = step t): its knots and the clock span after the step.
+template <bool BF16> struct CfIn {
+  float x0[DIM], x1[DIM], n;
+};
+template <bool BF16>
+__device__ __forceinline__ void lb_cf_load(const DiagArgs& a, int b, int c, CfIn<BF16>& in) {
+  const int l = threadIdx.x, t0 = c * a.T, Tc = min(a.T, a.n_int - t0);
+  const float* th = a.clock + (size_t)b * a.L + t0;
+  if (l < Tc) {
+    load_knot<BF16>(a, b, t0 + l, in.x0);
+    load_knot<BF16>(a, b, t0 + l + 1, in.x1);
+    in.n = th[Tc] - th[l + 1];
+  }
+}
+template <bool BF16>
+__device__ __forceinline__ void lb_summary_cf(const DiagArgs& a, int b, int c, float hb, bool use_tab,
+                                              const CfIn<BF16>& in, float (*s_x)[DIM], float (*s_y)[DIM],
+                                              float* s_tot, float* sp) {
+  const int l = threadIdx.x, t0 = c * a.T, Tc = min(a.T, a.n_int - t0);
+  float pv[DIM];
+#pragma unroll
+  for (int i = 0; i < DIM; ++i) pv[i] = 0.0f;
+  if (l < Tc) {
+#pragma unroll
+    for (int j = 0; j < K; ++j) {
+      const cf v = cf{in.x1[2 * j] - in.x0[2 * j], in.x1[2 * j + 1] - in.x0[2 * j + 1]} * expv(in.n * load_u(a.params, j));
+      pv[2 * j] = v.re;
+      pv[2 * j + 1] = v.im;
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < DIM; ++i) {
+    const float inc = wave_prefix(pv[i]);
+    s_y[l][i] = pv[i];
+    s_x[l][i] = inc - pv[i];
+    if (l == Tc - 1) s_tot[i] = inc;
+  }
+  __syncthreads();
+  // dd[0] = sum_t P_t (x) pi_t, dd[1] = sum_t pi_t (x) pi_t: sixteen k-steps of four steps each; the results
+  // overwrite the start of s_x once every operand has been read (one wavefront: LDS operations in program order)
+  float(*s_dd)[16][17] = reinterpret_cast<float(*)[16][17]>(&s_x[0][0]);
+  {
+    const int li = l & 15, lk = l >> 4;
+    f4m d1 = {0.0f, 0.0f, 0.0f, 0.0f}, d2 = d1;
+#pragma unroll 4
+    for (int ks = 0; ks < kMaxT / 4; ++ks) {
+      const int ts = 4 * ks + lk;
+      const float xv = s_x[ts][li], yv = s_y[ts][li];
+      d1 = mfma4(xv, yv, d1);
+      d2 = mfma4(yv, yv, d2);
+    }
+    wave_order();
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      s_dd[0][4 * lk + r][li] = d1[r];
+      s_dd[1][4 * lk + r][li] = d2[r];
+    }
+  }
+  __syncthreads();
+  const int j = l >> 3, k = l & 7;
+  cf phj, phk, IB, IA;
+  if (use_tab) {
+    phj = tp(a.ctab, j, TP_PHI);
+    phk = tp(a.ctab, k, TP_PHI);
+    IB = 2.0f * tq(a.ctab, j, k, TQ_IB);
+    IA = 2.0f * tq(a.ctab, j, k, TQ_IA);
+  } else {
+    const cf uj = load_u(a.params, j), uk = load_u(a.params, k), xj = hb * uj;
+    phj = node1(xj).p;
+    phk = node1(hb * uk).p;
+    IB = dd3<cf, false>(xj, hb * (uj + uk)).d;
+    IA = dd3<cf, false>(xj, hb * (uj + conj(uk))).d;
+  }
+  cf X, Xc, Y, Yc;  // sum x_j y_k and sum x_j conj(y_k) of dd[0] (X) and dd[1] (Y)
+  {
+    const float rr = s_dd[0][2 * j][2 * k], ii = s_dd[0][2 * j + 1][2 * k + 1];
+    const float ri = s_dd[0][2 * j][2 * k + 1], ir = s_dd[0][2 * j + 1][2 * k];
+    X = cf{rr - ii, ri + ir};
+    Xc = cf{rr + ii, ir - ri};
+  }
+  {
+    const float rr = s_dd[1][2 * j][2 * k], ii = s_dd[1][2 * j + 1][2 * k + 1];
+    const float ri = s_dd[1][2 * j][2 * k + 1], ir = s_dd[1][2 * j + 1][2 * k];
+    Y = cf{rr - ii, ri + ir};
+    Yc = cf{rr + ii, ir - ri};
+  }
+  const cf SBv = (phj * phk) * X + IB * Y;
+  const cf SAv = (phj * conj(phk)) * Xc + IA * Yc;
+  if (k == 0) {
+    const cf S1 = phj * cf{s_tot[2 * j], s_tot[2 * j + 1]};
+    *reinterpret_cast<float2*>(sp + 2 * j) = float2{S1.re, S1.im};
+  }
+  *reinterpret_cast<f4a*>(sp + poff(j, k)) = f4a{SAv.re, SAv.im, SBv.re, SBv.im};
+  __syncthreads();  // the LDS scratch is reused by the next chunk
+}
+
+// A chunk of a quad that holds a non-uniform chunk, one lane per pair (lane = 8 j + k), every step's coefficients at
+// its own clock step; the lane's full-scale states S1 (of plane j), SA, SB (of pair (j, k)) go in and out. OUT:
+// the lane writes level 1 (k = 0) and its 2 x 2 block of every prefix row.
+template <bool OUT, bool BF16>
+__device__ __forceinline__ void lb_pairwise(const DiagArgs& a, int b, int c, int j, int k, dc& S1d, dc& SAd,
+                                            dc& SBd) {
+  const int t0 = c * a.T, Tc = min(a.T, a.n_int - t0);
+  const float* th = a.clock + (size_t)b * a.L + t0;
+  const cf uj = load_u(a.params, j), uk = load_u(a.params, k);
+  const cf ub = uj + uk, ua = uj + conj(uk);
+  cf S1{(float)S1d.re, (float)S1d.im}, SA{(float)SAd.re, (float)SAd.im}, SBv{(float)SBd.re, (float)SBd.im};
+  for (int t = 0; t < Tc; ++t) {
+    const size_t ix = (size_t)b * a.L + t0 + t;
+    cf pj, pk;
+    if constexpr (!BF16) {
+      const float* x = reinterpret_cast<const float*>(a.path) + ix * DIM;
+      pj = cf{x[DIM + 2 * j] - x[2 * j], x[DIM + 2 * j + 1] - x[2 * j + 1]};
+      pk = cf{x[DIM + 2 * k] - x[2 * k], x[DIM + 2 * k + 1] - x[2 * k + 1]};
+    } else {
+      const unsigned short* x = reinterpret_cast<const unsigned short*>(a.path) + ix * DIM;
+      auto bf = [](unsigned short v) { return __uint_as_float((unsigned)v << 16); };
+      pj = cf{bf(x[DIM + 2 * j]) - bf(x[2 * j]), bf(x[DIM + 2 * j + 1]) - bf(x[2 * j + 1])};
+      pk = cf{bf(x[DIM + 2 * k]) - bf(x[2 * k]), bf(x[DIM + 2 * k + 1]) - bf(x[2 * k + 1])};
+    }
+    const float h = th[t + 1] - th[t];
+    const cf xj = h * uj;
+    const Node1<cf> nj = node1(xj);
+    const cf s1k = node1(h * uk).p * pk;
+    const cf cj = nj.e * S1;
+    SBv = expv(h * ub) * SBv + cj * s1k + dd3<cf, false>(xj, h * ub).d * (pj * pk);
+    SA = expv(h * ua) * SA + cj * conj(s1k) + dd3<cf, false>(xj, h * ua).d * (pj * conj(pk));
+    S1 = cj + nj.p * pj;
+    if constexpr (OUT) {
+      float* row = a.out + ((size_t)b * a.n_int + t0 + t) * a.W;
+      if (a.lvl0 && j == 0 && k == 0) row[0] = 1.0f;
+      if (k == 0) *reinterpret_cast<f2u*>(row + a.off1 + 2 * j) = f2u{S1.re, S1.im};
+      float* r0 = row + a.off2 + (2 * j) * DIM + 2 * k;
+      *reinterpret_cast<f2u*>(r0) = f2u{0.5f * (SA.re + SBv.re), 0.5f * (SBv.im - SA.im)};
+      *reinterpret_cast<f2u*>(r0 + DIM) = f2u{0.5f * (SA.im + SBv.im), 0.5f * (SA.re - SBv.re)};
+    }
+  }
+  S1d = dc{(double)S1.re, (double)S1.im};
+  SAd = dc{(double)SA.re, (double)SA.im};
+  SBd = dc{(double)SBv.re, (double)SBv.im};
+}
+
+template <bool BF16>
+__global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(3))) void k_fwd_lb(DiagArgs a) {
+  constexpr int KP = 4, GPW = Geo<KP>::GPW;
+  static_assert(GPW == 4, "one quad of chunks per workgroup");
+  __shared__ __align__(16) float s_v[2][GPW * VBLK];
+  __shared__ __align__(16) float s_row[GPW][RBUF];  // chunk summaries, then chunk carries, then row staging
+  __shared__ dc s_F[GPW][K];                        // chunk flows
+  __shared__ int s_tk, s_flag[GPW];
+  __shared__ float s_hb[GPW];
+  const int tid = threadIdx.x;
+  const int NG = (a.NQ + LBG - 1) / LBG;
+  if (tid == 0) s_tk = atomicAdd(a.lbflag + (size_t)a.B * (a.NQ + NG), 1);
+  __syncthreads();
+  const int tk = s_tk, b = tk % a.B, q = tk / a.B;  // tickets run quad by quad across the samples
+  const int cb = 4 * q, nc = min(GPW, a.C - cb);
+  const Lane l = lane_of<KP>(tid);
+  const int jj = tid >> 3, kk = tid & 7;
+  const int c = cb + l.gi;
+  const bool act = c < a.C;
+  // ---- A: classification and chunk summaries from a zero state
+  int flag = 0;
+  float hb = 0.0f;
+  if (act) {
+    flag = classify_chunk(a, b, c, l.gl, hb);
+    if (l.gl == 0) {
+      a.cflag[b * a.C + c] = flag;
+      a.chbar[b * a.C + c] = hb;
+      s_flag[l.gi] = flag;
+      s_hb[l.gi] = hb;
+    }
+  }
+  const bool quad_uni = __all(!act || (flag & 1));  // wavefront-uniform: the staging is shared
+  const int t0 = act ? c * a.T : 0, Tc = act ? min(a.T, a.n_int - t0) : 0;
+  if (quad_uni) {  // the summaries in closed form, chunk by chunk (lane = step); the next chunk's loads in flight
+    __shared__ float s_tot[DIM];
+    float(*s_x)[DIM] = reinterpret_cast<float(*)[DIM]>(&s_v[0][0]);  // the staging buffers are free here
+    float(*s_y)[DIM] = reinterpret_cast<float(*)[DIM]>(&s_v[1][0]);
+    __syncthreads();  // the groups' classifications
+    CfIn<BF16> in, nx;
+    lb_cf_load<BF16>(a, b, cb, in);
+    for (int i = 0; i < nc; ++i) {
+      if (i + 1 < nc) lb_cf_load<BF16>(a, b, cb + i + 1, nx);
+      lb_summary_cf<BF16>(a, b, cb + i, s_hb[i], (s_flag[i] & 4) != 0, in, s_x, s_y, s_tot, s_row[i]);
+      in = nx;
+    }
+  } else {
+    for (int i = 0; i < nc; ++i) {
+      PairSt z{};
+      lb_pairwise<false, BF16>(a, b, cb + i, jj, kk, z.S1, z.SA, z.SB);
+      store_st_f(s_row[i], jj, kk, z);
+    }
+  }
+  if (tid < 8 * nc) s_F[tid >> 3][tid & 7] = span_flow(a, b, cb + (tid >> 3), cb + (tid >> 3) + 1, tid & 7);
+  __syncthreads();
+  // ---- B: the quad's aggregate (lane = 8 jj + kk), published
+  PairSt agg{};
+  for (int i = 0; i < nc; ++i) {
+    const float* sp = s_row[i];
+    chen_d(agg, s_F[i][jj], s_F[i][kk], ld_fd(sp + 2 * jj), ld_fd(sp + 2 * kk), ld_fd(sp + poff(jj, kk)),
+           ld_fd(sp + poff(jj, kk) + 2));
+  }
+  const dc qFj = span_flow(a, b, cb, cb + nc, jj), qFk = span_flow(a, b, cb, cb + nc, kk);
+  const size_t AW = (size_t)a.D + 2 * K;
+  LbItems it;
+  it.qrow = a.lbagg + (size_t)b * a.NQ * AW;
+  it.grow = a.lbagg + ((size_t)a.B * a.NQ + (size_t)b * NG) * AW;
+  it.qst = a.lbflag + (size_t)b * a.NQ;
+  it.gst = a.lbflag + (size_t)a.B * a.NQ + (size_t)b * NG;
+  it.q = q;
+  it.g = q / LBG;
+  it.nq = q - LBG * it.g;
+  it.ng = it.g;
+  it.AW = AW;
+  const bool last_of_group = it.nq == LBG - 1 && q + 1 < a.NQ;  // a later quad needs this group's aggregate
+  publish(const_cast<double*>(it.qrow) + (size_t)q * AW, const_cast<int*>(it.qst) + q, a.D, jj, kk, agg, qFj);
+  // ---- C: the carry: the group's earlier quads, then the earlier groups
+  PairSt acc{};
+  dc aFj{1.0, 0.0}, aFk{1.0, 0.0};
+  lb_fold_ready(it, 0, it.nq, a.D, jj, kk, acc, aFj, aFk);
+  if (last_of_group) {  // the group's aggregate: its earlier quads (folded) followed by this quad
+    PairSt ga = acc;
+    chen_d(ga, qFj, qFk, agg.S1, shfl_d(agg.S1, 8 * kk), agg.SA, agg.SB);
+    publish(const_cast<double*>(it.grow) + (size_t)it.g * AW, const_cast<int*>(it.gst) + it.g, a.D, jj, kk, ga,
+            aFj * qFj);
+  }
+  lb_fold_ready(it, it.nq, it.nq + it.ng, a.D, jj, kk, acc, aFj, aFk);
+  // ---- D: chunk carries inside the quad (for the backward), then the prefix rows
+  {
+    PairSt st = acc;  // the zero state followed by every earlier quad
+    for (int i = 0; i < nc; ++i) {
+      const float* sp = s_row[i];
+      const PairSt y = load_st_f(sp, jj, kk);
+      const dc y1k = ld_fd(sp + 2 * kk);
+      __syncthreads();  // every lane has read summary i before the carry replaces it
+      store_st_d(a.carries + ((size_t)b * (a.C + 1) + cb + i) * a.D, jj, kk, st);
+      store_st_f(s_row[i], jj, kk, st);
+      chen_d(st, s_F[i][jj], s_F[i][kk], y.S1, y1k, y.SA, y.SB);
+    }
+    if (cb + nc == a.C) store_st_d(a.carries + ((size_t)b * (a.C + 1) + a.C) * a.D, jj, kk, st);
+  }
+  __syncthreads();
+  if (quad_uni) {
+    FwdCoef<KP> f;
+    fwd_coef<KP>(a, l, hb, (flag & 4) != 0, f);
+    cf S1{0.0f, 0.0f}, SA[KP], SB_[KP];
+    const float* cr = s_row[l.gi];
+    S1 = cf{cr[2 * l.j], cr[2 * l.j + 1]};
+    static_for<0, KP>([&](auto qc) {
+      constexpr int qq = qc;
+      const f4a p2 = *reinterpret_cast<const f4a*>(cr + poff(l.j, KP * l.kg + qq));
+      SA[qq] = cf{0.5f * p2.x, 0.5f * p2.y};
+      SB_[qq] = cf{0.5f * p2.z, 0.5f * p2.w};
+    });
+    wave_order();
+    lb_steps<true, BF16>(a, l, b, cb, t0, Tc, f, S1, SA, SB_, s_v, s_row[l.gi]);
+  } else {
+    for (int i = 0; i < nc; ++i) {
+      PairSt z = load_st_f(s_row[i], jj, kk);
+      lb_pairwise<true, BF16>(a, b, cb + i, jj, kk, z.S1, z.SA, z.SB);
+    }
+  }
+}
+
 }  // namespace pairs
 
 // ------------------------------------------------------------------------------------------------ host side
@@ -1906,39 +2171,27 @@ bool pairs_eligible(int structure, int depth, int dim, int readout, int flow_mod
          flow_mode == EWS_FLOW_PER_INTERVAL && T <= kMaxT && T >= pairs::NB;
 }
 
+// out = false: the coefficient table (and the look-back words zeroed); out = true: the look-back forward (one
+// workgroup per quad, tickets in launch order)
 int pairs_forward(const DiagArgs& a, hipStream_t st, bool out) {
-  constexpr int GPW = pairs::Geo<4>::GPW;
-  const dim3 grid((a.C + GPW - 1) / GPW, a.B), blk(64);
   if (!out) {
     hipLaunchKernelGGL(pairs::k_coef_table, dim3(1), dim3(192), 0, st, a);
-    if (hipGetLastError() != hipSuccess) return -1;
-  }
-  if (out) {
-    if (a.path_bf16) hipLaunchKernelGGL((pairs::k_fwd<true, true>), grid, blk, 0, st, a);
-    else hipLaunchKernelGGL((pairs::k_fwd<true, false>), grid, blk, 0, st, a);
   } else {
-    if (a.path_bf16) hipLaunchKernelGGL((pairs::k_fwd<false, true>), grid, blk, 0, st, a);
-    else hipLaunchKernelGGL((pairs::k_fwd<false, false>), grid, blk, 0, st, a);
+    const dim3 grid(a.NQ * a.B), blk(64);
+    if (a.path_bf16) hipLaunchKernelGGL((pairs::k_fwd_lb<true>), grid, blk, 0, st, a);
+    else hipLaunchKernelGGL((pairs::k_fwd_lb<false>), grid, blk, 0, st, a);
   }
   return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 
-int pairs_carry_scan(const DiagArgs& a, hipStream_t st, bool backward) {
+int pairs_carry_scan(const DiagArgs& a, hipStream_t st) {
   // the scan workgroups stage a segment of quads in more LDS than a static allocation may hold
-  const void* scan = backward ? reinterpret_cast<const void*>(&pairs::k_quad_bwd_scan)
-                              : reinterpret_cast<const void*>(&pairs::k_quad_fwd_scan);
-  if (hipFuncSetAttribute(scan, hipFuncAttributeMaxDynamicSharedMemorySize, (int)pairs::kScanLds) != hipSuccess)
+  if (hipFuncSetAttribute(reinterpret_cast<const void*>(&pairs::k_quad_bwd_scan),
+                          hipFuncAttributeMaxDynamicSharedMemorySize, (int)pairs::kScanLds) != hipSuccess)
     return -1;
-  const dim3 sgrid(a.B), sblk(pairs::SW * 64);
-  if (backward) {
-    hipLaunchKernelGGL(pairs::k_quad_bwd_agg, dim3(a.NQ, a.B), dim3(64), 0, st, a);
-    if (hipGetLastError() != hipSuccess) return -1;
-    hipLaunchKernelGGL(pairs::k_quad_bwd_scan, sgrid, sblk, pairs::kScanLds, st, a);
-  } else {
-    hipLaunchKernelGGL(pairs::k_quad_fwd_agg, dim3(a.NQ, a.B), dim3(64), 0, st, a);
-    if (hipGetLastError() != hipSuccess) return -1;
-    hipLaunchKernelGGL(pairs::k_quad_fwd_scan, sgrid, sblk, pairs::kScanLds, st, a);
-  }
+  hipLaunchKernelGGL(pairs::k_quad_bwd_agg, dim3(a.NQ, a.B), dim3(64), 0, st, a);
+  if (hipGetLastError() != hipSuccess) return -1;
+  hipLaunchKernelGGL(pairs::k_quad_bwd_scan, dim3(a.B), dim3(pairs::SW * 64), pairs::kScanLds, st, a);
   return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 
