@@ -50,10 +50,11 @@ struct DiagArgs {
   double* qflow;    // (B, NQ, K, 2) quad flows exp(u tau_quad)
   double* ql1;      // (B, NQ, K, 2) level-1 increments of the quads (backward)
   double* cflow;    // (B, C, K, 2) chunk flows exp(u tau_chunk)
-  // look-back of the pair-group forward (one workgroup per quad, in ticket order): status words (0 nothing,
-  // 1 published) of every (sample, quad), then of every (sample, group of 8 quads), then the ticket counter; the
-  // quad aggregates, then the group aggregates (state D, then the K plane flows), float64
-  int* lbflag;      // (B NQ + B NG + 1)
+  // look-back of the pair-group forward (one workgroup per quad, a sample's quads in ticket order): status words
+  // (0 nothing, 1 published) of every (sample, quad), then of every (sample, group of 8 quads), then one ticket
+  // counter per sample (32 words apart); the quad aggregates, then the group aggregates (state D, then the K plane
+  // flows), float64
+  int* lbflag;      // (B NQ + B NG + 32 B)
   double* lbagg;    // (B NQ + B NG, D + 2K)
   // LogEWS rows written by the chunk kernels' output pass (log-prefix readout off the sequential kernels): the
   // forward writes rows of Wlog = d + d (d - 1) / 2 floats (level 1, then the level-2 Lyndon coefficients) to out

@@ -1921,7 +1921,7 @@ struct WsLayout {
 // the look-back forward's status words (and ticket), quad and group aggregates (groups of 8 quads)
 void lb_layout(const Plan& p, WsLayout& w, size_t& off) {
   const size_t NQ = (p.C + 3) / 4, NG = (NQ + 7) / 8, items = (size_t)p.B * (NQ + NG);
-  w.lbflag = off; off += p.fast ? align256((items + 1) * 4) : 0;
+  w.lbflag = off; off += p.fast ? align256((items + (size_t)p.B * 32) * 4) : 0;  // statuses, then the tickets
   w.lbagg = off; off += p.fast ? align256(items * (p.D + 2 * p.K) * 8) : 0;
 }
 WsLayout ws_layout(const Plan& p) {

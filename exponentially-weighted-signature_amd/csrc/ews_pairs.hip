@@ -46,6 +46,7 @@ constexpr int NB = 4;     // steps per block of the full adjoint's column sums
 constexpr int kSpinLimit = 1 << 20;  // polls of the status words before giving up (never reached)
 constexpr int LBB = 4;               // aggregates whose loads are in flight together in the look-back
 constexpr int LBG = 8;               // quads per look-back group
+constexpr int LBT = 32;              // words between the samples' ticket counters (one per 128-byte line)
 constexpr int VPITCH = (kMaxT + 1) * DIM;  // LDS floats per group of staged increments (one padding row)
 
 template <int KP> struct Geo {
@@ -331,7 +332,7 @@ __device__ __forceinline__ float ref_step(const DiagArgs& a) {
 __global__ __launch_bounds__(192) void k_coef_table(DiagArgs a) {
   // the look-back forward's status words (quads, then groups of LBG quads) and its ticket start at zero (this
   // launch runs first)
-  const int nwords = a.B * (a.NQ + (a.NQ + LBG - 1) / LBG) + 1;
+  const int nwords = a.B * (a.NQ + (a.NQ + LBG - 1) / LBG) + a.B * LBT;
   for (int i = threadIdx.x; i < nwords; i += blockDim.x) a.lbflag[i] = 0;
   const int role = threadIdx.x >> 6, l = threadIdx.x & 63;
   const int j = l >> 3, k = l & 7;
@@ -1723,8 +1724,9 @@ __global__ __launch_bounds__(64) void k_bwd_carry(DiagArgs a) {
 }
 
 // ------------------------------------------------------------------------------------------------ look-back forward
-// The whole forward in one launch: one workgroup (one wavefront) per quad of four chunks, which takes its (sample,
-// quad) from a ticket counter, so that a quad waits only on quads whose workgroups already run:
+// The whole forward in one launch: one workgroup (one wavefront) per quad of four chunks; its sample comes from
+// the workgroup index and its quad from the sample's ticket counter, so that a quad waits only on quads whose
+// workgroups already run (per-sample counters on separate cache lines keep the tickets from serialising):
 //   A. every chunk's classification and its summary from a zero state;
 //   B. the quad's aggregate in float64 (lane = 8 j + k), published (status 1);
 //   C. the look-back: the quad's carry is the fold of the aggregates of the earlier quads of its group of LBG quads
@@ -1912,10 +1914,18 @@ __device__ __forceinline__ void lb_cf_load(const DiagArgs& a, int b, int c, CfIn
     in.n = th[Tc] - th[l + 1];
   }
 }
+// the lane's (lane = 8 j + k) coefficients of the closed form from the coefficient table (read once per quad)
+struct CfTab {
+  cf phj, phk, IB, IA;
+};
+__device__ __forceinline__ CfTab cf_tab(const DiagArgs& a, int j, int k) {
+  return CfTab{tp(a.ctab, j, TP_PHI), tp(a.ctab, k, TP_PHI), 2.0f * tq(a.ctab, j, k, TQ_IB),
+               2.0f * tq(a.ctab, j, k, TQ_IA)};
+}
 template <bool BF16>
 __device__ __forceinline__ void lb_summary_cf(const DiagArgs& a, int b, int c, float hb, bool use_tab,
-                                              const CfIn<BF16>& in, float (*s_x)[DIM], float (*s_y)[DIM],
-                                              float* s_tot, float* sp) {
+                                              const CfTab& ct, const CfIn<BF16>& in, float (*s_x)[DIM],
+                                              float (*s_y)[DIM], float* s_tot, float* sp) {
   const int l = threadIdx.x, t0 = c * a.T, Tc = min(a.T, a.n_int - t0);
   float pv[DIM];
 #pragma unroll
@@ -1923,7 +1933,8 @@ __device__ __forceinline__ void lb_summary_cf(const DiagArgs& a, int b, int c, f
   if (l < Tc) {
 #pragma unroll
     for (int j = 0; j < K; ++j) {
-      const cf v = cf{in.x1[2 * j] - in.x0[2 * j], in.x1[2 * j + 1] - in.x0[2 * j + 1]} * expv(in.n * load_u(a.params, j));
+      const cf v =
+          cf{in.x1[2 * j] - in.x0[2 * j], in.x1[2 * j + 1] - in.x0[2 * j + 1]} * expv_fast(in.n * load_u(a.params, j));
       pv[2 * j] = v.re;
       pv[2 * j + 1] = v.im;
     }
@@ -1960,10 +1971,10 @@ __device__ __forceinline__ void lb_summary_cf(const DiagArgs& a, int b, int c, f
   const int j = l >> 3, k = l & 7;
   cf phj, phk, IB, IA;
   if (use_tab) {
-    phj = tp(a.ctab, j, TP_PHI);
-    phk = tp(a.ctab, k, TP_PHI);
-    IB = 2.0f * tq(a.ctab, j, k, TQ_IB);
-    IA = 2.0f * tq(a.ctab, j, k, TQ_IA);
+    phj = ct.phj;
+    phk = ct.phk;
+    IB = ct.IB;
+    IA = ct.IA;
   } else {
     const cf uj = load_u(a.params, j), uk = load_u(a.params, k), xj = hb * uj;
     phj = node1(xj).p;
@@ -2051,15 +2062,20 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(3))) void k_
   __shared__ float s_hb[GPW];
   const int tid = threadIdx.x;
   const int NG = (a.NQ + LBG - 1) / LBG;
-  if (tid == 0) s_tk = atomicAdd(a.lbflag + (size_t)a.B * (a.NQ + NG), 1);
+  const int b = blockIdx.x % a.B;  // consecutive workgroups take different samples
+  if (tid == 0) s_tk = atomicAdd(a.lbflag + (size_t)a.B * (a.NQ + NG) + (size_t)b * LBT, 1);
   __syncthreads();
-  const int tk = s_tk, b = tk % a.B, q = tk / a.B;  // tickets run quad by quad across the samples
+  const int q = s_tk;  // the sample's quads in the order its workgroups started
   const int cb = 4 * q, nc = min(GPW, a.C - cb);
   const Lane l = lane_of<KP>(tid);
   const int jj = tid >> 3, kk = tid & 7;
   const int c = cb + l.gi;
   const bool act = c < a.C;
-  // ---- A: classification and chunk summaries from a zero state
+  // ---- A: classification and chunk summaries from a zero state (the first chunk's operands of the closed form
+  // and the table coefficients are loaded first: they do not depend on the classification)
+  CfIn<BF16> in;
+  lb_cf_load<BF16>(a, b, cb, in);
+  const CfTab ct = cf_tab(a, jj, kk);
   int flag = 0;
   float hb = 0.0f;
   if (act) {
@@ -2078,11 +2094,10 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(3))) void k_
     float(*s_x)[DIM] = reinterpret_cast<float(*)[DIM]>(&s_v[0][0]);  // the staging buffers are free here
     float(*s_y)[DIM] = reinterpret_cast<float(*)[DIM]>(&s_v[1][0]);
     __syncthreads();  // the groups' classifications
-    CfIn<BF16> in, nx;
-    lb_cf_load<BF16>(a, b, cb, in);
+    CfIn<BF16> nx;
     for (int i = 0; i < nc; ++i) {
       if (i + 1 < nc) lb_cf_load<BF16>(a, b, cb + i + 1, nx);
-      lb_summary_cf<BF16>(a, b, cb + i, s_hb[i], (s_flag[i] & 4) != 0, in, s_x, s_y, s_tot, s_row[i]);
+      lb_summary_cf<BF16>(a, b, cb + i, s_hb[i], (s_flag[i] & 4) != 0, ct, in, s_x, s_y, s_tot, s_row[i]);
       in = nx;
     }
   } else {
