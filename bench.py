@@ -32,6 +32,9 @@ import numpy as np  # noqa: E402
 HBM_PEAK_GBS = 8000.0
 MFMA_F32_PEAK_TFLOPS = 157.3
 FWD_PASS_NAMES = ["chunk_summary", "carry_scan", "chunk_output", "readout_reduce"]
+# the pair-group forward at d = 16: pass 0 builds the per-interval coefficient table, pass 1 launches nothing and
+# pass 2 is the look-back kernel (chunk summaries, carries and prefix rows in one launch)
+PAIR_FWD_PASS_NAMES = ["coef_table", "no_launch", "chunk_output", "readout_reduce"]
 BWD_PASS_NAMES = ["chunk_adjoint_local", "adjoint_scan", "chunk_adjoint_full", "knot_grads", "param_grads"]
 
 
@@ -584,11 +587,11 @@ def algorithmic_bytes(B, L, d, W, s_in=4, split=False):
     }
 
 
-# kernel of each c2 pass whose HBM traffic the PMC summary records: the headline backward (no clock gradient) runs
-# the full local adjoint in pass 0 and the closed-form carry part in pass 2
+# kernel of each c2 pass whose HBM traffic the PMC summary records: the forward runs whole in pass 2 (the look-back
+# kernel: summaries, carries and rows; pass 0 only builds the coefficient table), the headline backward (no clock
+# gradient) runs the full local adjoint in pass 0 and the closed-form carry part in pass 2
 PASS_KERNELS = {
-    "chunk_summary": "pairs::k_fwd<false, false>",
-    "chunk_output": "pairs::k_fwd<true, false>",
+    "chunk_output": "pairs::k_fwd_lb<false>",
     "chunk_adjoint_local": "pairs::k_bwd_full<false, false, 1>",
     "chunk_adjoint_full": "pairs::k_bwd_carry<false>",
 }
@@ -835,7 +838,7 @@ def main():
         step(evs)
         per_step_events.append(evs)
     torch.cuda.synchronize()
-    names = (["front_forward"] if nfr else []) + FWD_PASS_NAMES[:nf] + BWD_PASS_NAMES[:nb] + \
+    names = (["front_forward"] if nfr else []) + PAIR_FWD_PASS_NAMES[:nf] + BWD_PASS_NAMES[:nb] + \
         (["front_backward"] if nfr else [])
     pass_ms = {nm: 0.0 for nm in names}
     for evs in per_step_events:

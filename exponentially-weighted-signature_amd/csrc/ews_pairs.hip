@@ -43,7 +43,7 @@ constexpr int K = 8;      // planes
 constexpr int DIM = 16;   // channels
 constexpr int NB = 4;     // steps per block of the full adjoint's column sums
 // look-back forward (k_fwd_lb)
-constexpr int kSpinLimit = 1 << 20;  // polls of the status words before giving up (never reached)
+constexpr int kSpinLimit = 1 << 20;  // polls of a status word before the look-back gives up (rows turn NaN)
 constexpr int LBB = 4;               // aggregates whose loads are in flight together in the look-back
 constexpr int LBG = 8;               // quads per look-back group
 constexpr int LBT = 32;              // words between the samples' ticket counters (one per 128-byte line)
@@ -2133,14 +2133,18 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(3))) void k_
   // ---- C: the carry: the group's earlier quads, then the earlier groups
   PairSt acc{};
   dc aFj{1.0, 0.0}, aFk{1.0, 0.0};
-  lb_fold_ready(it, 0, it.nq, a.D, jj, kk, acc, aFj, aFk);
+  // an aggregate still unpublished after kSpinLimit polls (a predecessor descheduled for that long) makes this
+  // quad's carry, and through the published aggregates every later quad's, NaN: the rows show the failure
+  const double qnan = __builtin_nan("");
+  const PairSt poison{{qnan, qnan}, {qnan, qnan}, {qnan, qnan}};
+  if (!lb_fold_ready(it, 0, it.nq, a.D, jj, kk, acc, aFj, aFk)) acc = poison;
   if (last_of_group) {  // the group's aggregate: its earlier quads (folded) followed by this quad
     PairSt ga = acc;
     chen_d(ga, qFj, qFk, agg.S1, shfl_d(agg.S1, 8 * kk), agg.SA, agg.SB);
     publish(const_cast<double*>(it.grow) + (size_t)it.g * AW, const_cast<int*>(it.gst) + it.g, a.D, jj, kk, ga,
             aFj * qFj);
   }
-  lb_fold_ready(it, it.nq, it.nq + it.ng, a.D, jj, kk, acc, aFj, aFk);
+  if (!lb_fold_ready(it, it.nq, it.nq + it.ng, a.D, jj, kk, acc, aFj, aFk)) acc = poison;
   // ---- D: chunk carries inside the quad (for the backward), then the prefix rows
   {
     PairSt st = acc;  // the zero state followed by every earlier quad
