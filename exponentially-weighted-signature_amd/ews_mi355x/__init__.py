@@ -24,12 +24,14 @@ from .front import (  # noqa: F401
     make_clock,
 )
 from .mixer import GradedRMSNorm, MixerEpilogue, graded_level_slices  # noqa: F401
+from .block import EWSBlock, RMSNorm, StackedEWS  # noqa: F401
 from .ops import diag_scan, mixer_epilogue  # noqa: F401
 from .token_scan import build_token_cache, token_cached_prefix_scan  # noqa: F401
 from .params import (  # noqa: F401
     AParamBlockDiag,
     AParamBoundedRotation,
     AParamConstant,
+    AParamDefinitePlusSkew,
     AParamDampedRotation,
     AParamEFM,
     AParamGeneral,

@@ -6,6 +6,7 @@ structure selects a kernel here, with the reference's class and field names so c
 reference constructs them the same way:
 
     AParamConstant / AParamGeneral    dense A                       (ews/params.py:268-277)
+    AParamDefinitePlusSkew            L L^T + eps I + (U - U^T)      (ews/params.py:372-391; EWSBlock's default)
     AParamEFM                         positive diagonal              (ews/params.py:280-301)
     AParamBlockDiag                   free diagonal blocks
     AParamBoundedRotation             planes [[0, -b], [b, 0]]       (ews/params.py:538-566)
@@ -46,6 +47,36 @@ class AParamGeneral(torch.nn.Module):
 
     def forward(self):
         return self.matrix
+
+
+class AParamDefinitePlusSkew(torch.nn.Module):
+    """A = L L^T + epsilon I + (U - U^T): ``lower`` fills the lower triangle of L (diagonal included, row-major
+    order of the lower-triangle indices), ``upper`` the strict upper triangle of U (ews/params.py:152-163,
+    372-391)."""
+
+    def __init__(self, lower: torch.Tensor, upper: torch.Tensor, dim: int, epsilon: float = 0.0):
+        super().__init__()
+        n = int(dim)
+        if lower.numel() != n * (n + 1) // 2 or upper.numel() != n * (n - 1) // 2:
+            raise ValueError(f"definite_plus_skew at dim {n} takes {n * (n + 1) // 2} lower and "
+                             f"{n * (n - 1) // 2} upper entries")
+        self.lower = torch.nn.Parameter(lower)
+        self.upper = torch.nn.Parameter(upper)
+        self.dim = n
+        self.epsilon = float(epsilon)
+
+    def forward(self):
+        n = self.dim
+        il = torch.tril_indices(n, n, 0, device=self.lower.device)
+        iu = torch.triu_indices(n, n, 1, device=self.upper.device)
+        Lm = torch.zeros((n, n), dtype=self.lower.dtype, device=self.lower.device).index_put(
+            (il[0], il[1]), self.lower)
+        Um = torch.zeros((n, n), dtype=self.upper.dtype, device=self.upper.device).index_put(
+            (iu[0], iu[1]), self.upper)
+        pd = Lm @ Lm.t()
+        if self.epsilon > 0.0:
+            pd = pd + self.epsilon * torch.eye(n, dtype=pd.dtype, device=pd.device)
+        return pd + (Um - Um.t())
 
 
 class AParamEFM(torch.nn.Module):
