@@ -1674,10 +1674,13 @@ __global__ __launch_bounds__(256) void k_leaf_bwd(Args a, LeafBwd o) {
   constexpr int LW = lw_of(N);
   __shared__ __align__(16) float sp[HP][256];
   // ds3 of the level adjoint and, after it, the flow adjoint's squarings / scratch share one region
-  constexpr int UNF = (EXACTF ? SQMAX * 256 : 800) > (N >= 3 ? 4096 : 0) ? (EXACTF ? SQMAX * 256 : 800)
-                                                                          : (N >= 3 ? 4096 : 0);
+  // 16 x 16 matrices and the rows of ds3 sit at a pitch of 17 floats (LP), so that a column read (16 lanes on
+  // consecutive rows) and a row read (lanes on consecutive columns) both hit distinct banks
+  constexpr int LP = 17;
+  constexpr int UNF = (EXACTF ? SQMAX * 256 : 800) > (N >= 3 ? 256 * LP : 0) ? (EXACTF ? SQMAX * 256 : 800)
+                                                                            : (N >= 3 ? 256 * LP : 0);
   __shared__ __align__(16) float UN[UNF];
-  __shared__ __align__(16) float dS2[256], F[256], F2[256], Gm[256];
+  __shared__ __align__(16) float dS2[16 * LP], F[16 * LP], F2[16 * LP], Gm[256];
   __shared__ float dS1[16], red[8];
   extern __shared__ __align__(16) float dyn[];  // the six letter arrays, (q + 1) x 16 each
   typedef float Row16[16];
@@ -1723,9 +1726,9 @@ __global__ __launch_bounds__(256) void k_leaf_bwd(Args a, LeafBwd o) {
       Lt[0][tid] = v;
       dS1[tid] = drow[tid];
     }
-    if constexpr (N >= 2) dS2[tid] = drow[16 + tid];
-    if constexpr (N >= 3) {
-      for (int e = tid; e < 4096; e += 256) dS3[e] = drow[272 + e];
+    if constexpr (N >= 2) dS2[i * LP + j] = drow[16 + tid];
+    if constexpr (N >= 3) {  // ds3[a][b][c] at (16 a + b) LP + c
+      for (int e = tid; e < 4096; e += 256) dS3[(e >> 4) * LP + (e & 15)] = drow[272 + e];
     }
     Gm[tid] = a.fl[((size_t)b * a.n_int + t) * 256 + tid];  // dM_t
     for (int e = tid; e < QN * 16; e += 256) {
@@ -1767,8 +1770,8 @@ __global__ __launch_bounds__(256) void k_leaf_bwd(Args a, LeafBwd o) {
         float x1 = 0.0f, x2 = 0.0f;
 #pragma unroll
         for (int k = 0; k < 16; ++k) {
-          x1 = fmaf(dS2[r * 16 + k], G1[n][k], x1);
-          x2 = fmaf(dS2[k * 16 + r], BT[n][k], x2);
+          x1 = fmaf(dS2[r * LP + k], G1[n][k], x1);
+          x2 = fmaf(dS2[k * LP + r], BT[n][k], x2);
         }
         dBT[n][r] = x1;
         dG1[n][r] += x2;
@@ -1781,14 +1784,14 @@ __global__ __launch_bounds__(256) void k_leaf_bwd(Args a, LeafBwd o) {
       //   dbt3_{p+NN} += (E_NN b_p) / (p+NN+2)
       for (int NN = 0; NN <= q; ++NN) {
         {
-          float f = dS2[tid], e2 = 0.0f;
+          float f = dS2[i * LP + j], e2 = 0.0f;
 #pragma unroll
           for (int k = 0; k < 16; ++k) {
-            f = fmaf(BT[NN][k], dS3[k * 256 + tid], f);
-            e2 = fmaf(dS3[tid * 16 + k], G1[NN][k], e2);
+            f = fmaf(BT[NN][k], dS3[(16 * k + i) * LP + j], f);  // ds3[k][i][j]
+            e2 = fmaf(dS3[tid * LP + k], G1[NN][k], e2);         // ds3[i][j][k]
           }
-          F[tid] = f;
-          F2[tid] = e2;
+          F[i * LP + j] = f;
+          F2[i * LP + j] = e2;
         }
         __syncthreads();
         const float inv2 = frcp(NN + 2);
@@ -1799,17 +1802,17 @@ __global__ __launch_bounds__(256) void k_leaf_bwd(Args a, LeafBwd o) {
             const int p = e >> 5, r = e & 15, side = (e >> 4) & 1, n = NN - p;
             if (side == 0) {
 #pragma unroll
-              for (int k = 0; k < 16; ++k) x = fmaf(F[r * 16 + k], G1[n][k], x);
+              for (int k = 0; k < 16; ++k) x = fmaf(F[r * LP + k], G1[n][k], x);
               dB[p][r] += x * inv2;
             } else {
 #pragma unroll
-              for (int k = 0; k < 16; ++k) x = fmaf(F[k * 16 + r], Lt[p][k], x);
+              for (int k = 0; k < 16; ++k) x = fmaf(F[k * LP + r], Lt[p][k], x);
               dG1[n][r] += x * inv2;
             }
           } else {
             const int p = (e - np) >> 4, r = (e - np) & 15;
 #pragma unroll
-            for (int k = 0; k < 16; ++k) x = fmaf(F2[r * 16 + k], Lt[p][k], x);
+            for (int k = 0; k < 16; ++k) x = fmaf(F2[r * LP + k], Lt[p][k], x);
             dBT[p + NN][r] += x * frcp(p + NN + 2);
           }
         }

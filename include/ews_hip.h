@@ -238,7 +238,10 @@ size_t ews_token_scan_workspace_bytes(const ews_dense_desc* desc, int vocab);
 int ews_token_scan(const ews_dense_desc* desc, const int32_t* token_ids, const uint8_t* mask, const float* P_cache,
                    const float* D_cache, int vocab, float* out, void* workspace, ews_stream_t stream);
 /* Backward: grad_out -> grad_P_cache (vocab, sum_k d^k) and grad_D_cache (vocab, d, d), the per-step cotangents
- * summed by token in a fixed order (deterministic). Replaces JAX autodiff through token_cached_prefix_scan. */
+ * summed by token in a fixed order (deterministic). Replaces JAX autodiff through token_cached_prefix_scan.
+ * The workspace holds per-512-step partial sums for every token: about ceil(B (L-1) / 512) x vocab x
+ * (sum_k d^k + 256) floats beside the scan's own (70 MB at B = 256, L = 512, d = 16, depth 2, vocab 128; 0.6 GB at
+ * depth 3), and the cotangent stream is read once per group of 16 tokens. */
 int ews_token_scan_backward(const ews_dense_desc* desc, const int32_t* token_ids, const uint8_t* mask,
                             const float* P_cache, const float* D_cache, int vocab, const float* grad_out,
                             float* grad_P_cache, float* grad_D_cache, void* workspace, ews_stream_t stream);

@@ -4,8 +4,8 @@ tests/test_oracle_token.py to the ordinary EWS scan, the reference's own claim f
 
 Bars: forward max relative error <= 1e-5, gradients <= 1e-4 (metric max|a-b| / max|b|,
 the reference's tests/test_engines.py:31-33). Cases: depths 1-3, d from 2 to 16, one and several chunks, masks
-with different lengths per sample, vocabularies of 1, 5 and 40 tokens (three groups of the gradient's token
-accumulators), more than 1024 steps (several gradient chunks), the Van Loan and series leaves of the cache, and the
+with different lengths per sample, vocabularies of 1, 5, 40 and 128 tokens (up to eight groups of the gradient's
+token accumulators; 128 is the vocabulary of the reference's set task, experiments/fl/tasks/set.py), more than 1024 steps (several gradient chunks), the Van Loan and series leaves of the cache, and the
 chain build_token_cache -> token_cached_prefix_scan against the ordinary dense EWS layer on the expanded path.
 """
 
@@ -46,6 +46,8 @@ SCANS = [
     (5, 16, 2, 2, 130, (130, 64)),
     (3, 6, 1, 2, 1500, (1500, 1100)),
     (7, 8, 3, 1, 80, None),
+    (128, 8, 2, 2, 700, (700, 333)),  # the vocabulary of the reference's set task: 8 groups of token accumulators
+    (128, 4, 3, 1, 300, None),
 ]
 
 
