@@ -1417,16 +1417,25 @@ typedef float f4m __attribute__((ext_vector_type(4)));
 __device__ __forceinline__ f4m mfma4(float a, float b, f4m c) { return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0); }
 // out (64 x 16) = in (64 x 16) M^T for a real 16 x 16 matrix given as its B-operand registers bm[ks] (lane l: M[l % 16]
 // [4 ks + l / 16]): four row tiles of 16 steps, four 16x16x4 MFMAs each; the result goes to LDS, row-major.
-constexpr int SP = DIM + 2;  // LDS row pitch of the per-step arrays: 16 lanes of a column hit distinct banks
+// The per-step arrays are 64 rows of 16 floats without padding (three of them and the rest of the kernel's LDS stay
+// under the 13 KB that lets three workgroups share a SIMD); entry (t, c) sits at column swz(t, c), an XOR of the
+// column with an even value taken from t, so that 16 consecutive rows read at one column hit 16 distinct bank pairs
+// and the complex pairs (2 j, 2 j + 1) stay adjacent.
+constexpr int SP = DIM;
+__device__ __forceinline__ int swz(int t, int c) { return c ^ (2 * ((t >> 1) & 7)); }
 __device__ __forceinline__ void mfma_rows(const float (*in)[SP], const float* bm, float (*out)[SP], int l) {
   const int li = l & 15, lk = l >> 4;
 #pragma unroll
   for (int tt = 0; tt < 4; ++tt) {
     f4m acc = {0.0f, 0.0f, 0.0f, 0.0f};
+    const int ti = 16 * tt + li;
 #pragma unroll
-    for (int ks = 0; ks < 4; ++ks) acc = mfma4(in[16 * tt + li][4 * ks + lk], bm[ks], acc);
+    for (int ks = 0; ks < 4; ++ks) acc = mfma4(in[ti][swz(ti, 4 * ks + lk)], bm[ks], acc);
 #pragma unroll
-    for (int r = 0; r < 4; ++r) out[16 * tt + 4 * lk + r][li] = acc[r];
+    for (int r = 0; r < 4; ++r) {
+      const int to = 16 * tt + 4 * lk + r;
+      out[to][swz(to, li)] = acc[r];
+    }
   }
 }
 
@@ -1439,14 +1448,17 @@ __device__ __forceinline__ void mfma_rows_sigma(const float (*pi)[SP], const flo
     f4m acc = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
     for (int ks = 0; ks < 4; ++ks) {
-      const int q = 4 * ks + lk, kq = q >> 1;
-      const float2 x = *reinterpret_cast<const float2*>(&pi[16 * tt + li][2 * kq]);
+      const int q = 4 * ks + lk, kq = q >> 1, ti = 16 * tt + li;
+      const float2 x = *reinterpret_cast<const float2*>(&pi[ti][swz(ti, 2 * kq)]);
       const float2 hk = pl[kq][2];
       const float sv = (q & 1) ? fmaf(hk.x, x.y, hk.y * x.x) : fmaf(hk.x, x.x, -hk.y * x.y);
       acc = mfma4(sv, bm[ks], acc);
     }
 #pragma unroll
-    for (int r = 0; r < 4; ++r) out[16 * tt + 4 * lk + r][li] = acc[r];
+    for (int r = 0; r < 4; ++r) {
+      const int to = 16 * tt + 4 * lk + r;
+      out[to][swz(to, li)] = acc[r];
+    }
   }
 }
 
@@ -1459,9 +1471,12 @@ __device__ __forceinline__ cf expv_fast(cf x) {
 }
 
 template <bool BF16>
-__global__ __launch_bounds__(64) void k_bwd_carry(DiagArgs a) {
-  __shared__ __align__(16) float s_pi[kMaxT][SP], s_ga[kMaxT][SP];  // per step: pi, gamma
-  __shared__ __align__(16) float s_o[kMaxT][SP];                    // matrices, then each MFMA result in turn
+__global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(3))) void k_bwd_carry(DiagArgs a) {
+  // per step: pi, gamma; then s_o: the matrices, then each MFMA result in turn (rows swizzled by swz)
+  __shared__ __align__(16) float s_buf[3][kMaxT][SP];
+  float(*s_pi)[SP] = s_buf[0];
+  float(*s_ga)[SP] = s_buf[1];
+  float(*s_o)[SP] = s_buf[2];
   __shared__ __align__(16) float2 s_wh[kMaxT];
   __shared__ __align__(16) float2 s_pl[K][6];  // per plane: rho, phi, phi/2, lam1, e^{u tau} C1, 1/rho
   f4a(*s_mat)[K][K] = reinterpret_cast<f4a(*)[K][K]>(&s_o[0][0]);  // s_mr, s_gr, s_mc, s_gc: 4 KB
@@ -1475,9 +1490,9 @@ __global__ __launch_bounds__(64) void k_bwd_carry(DiagArgs a) {
   const int t = l;
   const bool live = owned && t < Tc;
   float h = 0.0f, hs = 0.0f, th_end = 0.0f, tau = 0.0f;
-  float x0[DIM], x1[DIM], dvl[DIM];
+  float x0[DIM], x1[DIM];
 #pragma unroll
-  for (int i = 0; i < DIM; ++i) x0[i] = x1[i] = dvl[i] = 0.0f;
+  for (int i = 0; i < DIM; ++i) x0[i] = x1[i] = 0.0f;
   if (owned) {
     th_end = th[Tc];
     tau = th_end - th[0];
@@ -1487,15 +1502,6 @@ __global__ __launch_bounds__(64) void k_bwd_carry(DiagArgs a) {
     hs = th_end - th[t + 1];
     load_knot<BF16>(a, b, t0 + t, x0);
     load_knot<BF16>(a, b, t0 + t + 1, x1);
-    const f4a* dvr = reinterpret_cast<const f4a*>(a.dv + ((size_t)b * a.n_int + t0 + t) * DIM);
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const f4a v = dvr[i];
-      dvl[4 * i] = v.x;
-      dvl[4 * i + 1] = v.y;
-      dvl[4 * i + 2] = v.z;
-      dvl[4 * i + 3] = v.w;
-    }
   }
   // adjoint carry inside the quad (float64, lane = 8 j + k): the cotangent on this chunk's end state, down from the
   // quad's last chunk (written by the adjoint scan); written back for every later kernel that reads mt
@@ -1575,8 +1581,8 @@ __global__ __launch_bounds__(64) void k_bwd_carry(DiagArgs a) {
     const float2 f = s_pl[j][1], e = s_pl[j][4];
     const cf ex{wave_prefix(pi[j].re) - pi[j].re, wave_prefix(pi[j].im) - pi[j].im};
     ga[j] = live ? fma_c(cf{f.x, f.y}, ex, cf{e.x, e.y}) : cf{0.0f, 0.0f};
-    *reinterpret_cast<float2*>(&s_pi[t][2 * j]) = float2{pi[j].re, pi[j].im};
-    *reinterpret_cast<float2*>(&s_ga[t][2 * j]) = float2{ga[j].re, ga[j].im};
+    *reinterpret_cast<float2*>(&s_pi[t][swz(t, 2 * j)]) = float2{pi[j].re, pi[j].im};
+    *reinterpret_cast<float2*>(&s_ga[t][swz(t, 2 * j)]) = float2{ga[j].re, ga[j].im};
   }
   s_wh[t] = float2{h, hs};
   __syncthreads();  // the matrices are in registers; s_o is free
@@ -1585,12 +1591,12 @@ __global__ __launch_bounds__(64) void k_bwd_carry(DiagArgs a) {
   mfma_rows_sigma(s_pi, s_pl, bmr, s_o, l);
   __syncthreads();
 #pragma unroll
-  for (int i = 0; i < DIM; ++i) rc[i] = s_o[t][i];
+  for (int i = 0; i < DIM; ++i) rc[i] = s_o[t][swz(t, i)];
   __syncthreads();
   mfma_rows(s_pi, bgr, s_o, l);
   __syncthreads();
 #pragma unroll
-  for (int i = 0; i < DIM; ++i) rp[i] = s_o[t][i];
+  for (int i = 0; i < DIM; ++i) rp[i] = s_o[t][swz(t, i)];
   __syncthreads();
   // columns: the later factor's part of dv, CA_t = M_C gamma_t, CB_t = G_C pi_t (CA waits in s_o, CB in registers)
   mfma_rows(s_ga, bmc, s_o, l);
@@ -1621,15 +1627,29 @@ __global__ __launch_bounds__(64) void k_bwd_carry(DiagArgs a) {
   }
   __syncthreads();
 #pragma unroll
-  for (int i = 0; i < DIM; ++i) rc[i] = s_o[t][i];  // CA
+  for (int i = 0; i < DIM; ++i) rc[i] = s_o[t][swz(t, i)];  // CA
   __syncthreads();
+  // the step's local dv (written by the local adjoint), loaded here rather than with the inputs to keep the
+  // registers of the steps above free; this lane overwrites the same row with the total below
+  float dvl[DIM];
+  {
+    const f4a* dvr = reinterpret_cast<const f4a*>(a.dv + ((size_t)b * a.n_int + t0 + (live ? t : 0)) * DIM);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const f4a v = live ? dvr[i] : f4a{0.0f, 0.0f, 0.0f, 0.0f};
+      dvl[4 * i] = v.x;
+      dvl[4 * i + 1] = v.y;
+      dvl[4 * i + 2] = v.z;
+      dvl[4 * i + 3] = v.w;
+    }
+  }
   mfma_rows(s_pi, bgc, s_o, l);
   __syncthreads();
 #pragma unroll
   for (int k = 0; k < K; ++k) {
     const float2 hk = s_pl[k][2];
     const cf col = conj(fl[k]) * fma_c(conj(cf{hk.x, hk.y}), cf{rc[2 * k], rc[2 * k + 1]},
-                                       cf{s_o[t][2 * k], s_o[t][2 * k + 1]});
+                                       cf{s_o[t][swz(t, 2 * k)], s_o[t][swz(t, 2 * k + 1)]});
     dvt[2 * k] += col.re + dvl[2 * k];
     dvt[2 * k + 1] += col.im + dvl[2 * k + 1];
   }
@@ -1658,7 +1678,7 @@ __global__ __launch_bounds__(64) void k_bwd_carry(DiagArgs a) {
 #pragma unroll 4
     for (int ks = 0; ks < kMaxT / 4; ++ks) {
       const int ts = 4 * ks + lk;
-      const float xp = s_pi[ts][li], xg = s_ga[ts][li];
+      const float xp = s_pi[ts][swz(ts, li)], xg = s_ga[ts][swz(ts, li)];
       const float2 w = s_wh[ts];
       const float yh = w.x * xp, ys = w.y * xp;
       d1 = mfma4(xp, yh, d1);
@@ -1666,7 +1686,8 @@ __global__ __launch_bounds__(64) void k_bwd_carry(DiagArgs a) {
       d3 = mfma4(xg, yh, d3);
       d4 = mfma4(xg, ys, d4);
     }
-    float(*dd)[16][17] = reinterpret_cast<float(*)[16][17]>(&s_o[0][0]);  // 4 x 16 x 17 <= 64 x SP floats
+    __syncthreads();  // gamma and the MFMA results are no longer read
+    float(*dd)[16][17] = reinterpret_cast<float(*)[16][17]>(&s_buf[1][0][0]);  // 4 x 16 x 17 <= 2 x 64 x SP
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       dd[0][4 * lk + r][li] = d1[r];
@@ -1677,7 +1698,7 @@ __global__ __launch_bounds__(64) void k_bwd_carry(DiagArgs a) {
   }
   __syncthreads();
   // ---- lane = pair (jj, kk)
-  const float(*dd)[16][17] = reinterpret_cast<const float(*)[16][17]>(&s_o[0][0]);
+  const float(*dd)[16][17] = reinterpret_cast<const float(*)[16][17]>(&s_buf[1][0][0]);
   // x y = (rr - ii, ri + ir), x conj(y) = (rr + ii, ir - ri), with rr = D[2j][2k], ii = D[2j+1][2k+1], ...
   cf P[4], Pc[4];
 #pragma unroll
