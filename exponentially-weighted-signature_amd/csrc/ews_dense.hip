@@ -1670,7 +1670,7 @@ __device__ float block_flow_adjoint(const Args& a, const LdsTable* sp, float nor
 }
 
 template <int N, bool EXACTF>  // EXACTF: exact flows (the other schemes' code is left out)
-__global__ __launch_bounds__(256) void k_leaf_bwd(Args a, LeafBwd o) {
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(EXACTF ? 3 : 1))) void k_leaf_bwd(Args a, LeafBwd o) {
   constexpr int LW = lw_of(N);
   __shared__ __align__(16) float sp[HP][256];
   // ds3 of the level adjoint and, after it, the flow adjoint's squarings / scratch share one region
@@ -1680,7 +1680,9 @@ __global__ __launch_bounds__(256) void k_leaf_bwd(Args a, LeafBwd o) {
   constexpr int UNF = (EXACTF ? SQMAX * 256 : 800) > (N >= 3 ? 256 * LP : 0) ? (EXACTF ? SQMAX * 256 : 800)
                                                                             : (N >= 3 ? 256 * LP : 0);
   __shared__ __align__(16) float UN[UNF];
+  constexpr int TPT = QMAX + 4;  // row pitch of the transposed letters (QMAX + 1 columns)
   __shared__ __align__(16) float dS2[16 * LP], F[16 * LP], F2[16 * LP], Gm[256];
+  __shared__ __align__(16) float LtT[N >= 3 ? 16 * TPT : 1];
   __shared__ float dS1[16], red[8];
   extern __shared__ __align__(16) float dyn[];  // the six letter arrays, (q + 1) x 16 each
   typedef float Row16[16];
@@ -1782,42 +1784,83 @@ __global__ __launch_bounds__(256) void k_leaf_bwd(Args a, LeafBwd o) {
       // per degree NN: dg2_NN = bt3_NN ._1 ds3 + ds2 (F) and E_NN = ds3 ._3 g1_NN (F2), then
       //   pairs (p, n = NN - p): db_p += dg2_NN g1_n / (NN+2);  dg1_n += dg2_NN^T b_p / (NN+2)
       //   dbt3_{p+NN} += (E_NN b_p) / (p+NN+2)
-      for (int NN = 0; NN <= q; ++NN) {
-        {
-          float f = dS2[i * LP + j], e2 = 0.0f;
-#pragma unroll
-          for (int k = 0; k < 16; ++k) {
-            f = fmaf(BT[NN][k], dS3[(16 * k + i) * LP + j], f);  // ds3[k][i][j]
-            e2 = fmaf(dS3[tid * LP + k], G1[NN][k], e2);         // ds3[i][j][k]
-          }
-          F[i * LP + j] = f;
-          F2[i * LP + j] = e2;
-        }
-        __syncthreads();
-        const float inv2 = frcp(NN + 2);
-        const int np = (NN + 1) * 32, ne = (q - NN + 1) * 16;
-        for (int e = tid; e < np + ne; e += 256) {
-          float x = 0.0f;
-          if (e < np) {
-            const int p = e >> 5, r = e & 15, side = (e >> 4) & 1, n = NN - p;
-            if (side == 0) {
-#pragma unroll
-              for (int k = 0; k < 16; ++k) x = fmaf(F[r * LP + k], G1[n][k], x);
-              dB[p][r] += x * inv2;
-            } else {
-#pragma unroll
-              for (int k = 0; k < 16; ++k) x = fmaf(F[k * LP + r], Lt[p][k], x);
-              dG1[n][r] += x * inv2;
-            }
-          } else {
-            const int p = (e - np) >> 4, r = (e - np) & 15;
-#pragma unroll
-            for (int k = 0; k < 16; ++k) x = fmaf(F2[r * LP + k], Lt[p][k], x);
-            dBT[p + NN][r] += x * frcp(p + NN + 2);
-          }
-        }
-        __syncthreads();
+      // The three pair sums are products of a 16 x 16 matrix with up to QMAX + 1 letter columns, accumulated over
+      // NN on fp32 MFMA: wavefront 0 holds db (columns p), wavefront 1 dg1 (columns n), wavefront 2 dbt3 (columns
+      // s = p + NN, its 1 / (s + 2) applied at the end); the B operands read the letters transposed (LtT; g1_n =
+      // b_n / (n + 1)) so that the 16 lanes of a k-step read 16 consecutive columns.
+      for (int e = tid; e < 16 * QN; e += 256) {
+        const int n = e >> 4, r = e & 15;
+        LtT[r * TPT + n] = Lt[n][r];
       }
+      // this thread's fibres of ds3 through (i, j), read once: ds3[k][i][j] and ds3[i][j][k] over k
+      float d3c[16], d3r[16];
+#pragma unroll
+      for (int k = 0; k < 16; ++k) {
+        d3c[k] = dS3[(16 * k + i) * LP + j];
+        d3r[k] = dS3[tid * LP + k];
+      }
+      const float ds2ij = dS2[i * LP + j];
+      const int wv = tid >> 6, li = l & 15, lk = l >> 4;
+      f4 acc[3];
+#pragma unroll
+      for (int tt = 0; tt < 3; ++tt) acc[tt] = f4{0.0f, 0.0f, 0.0f, 0.0f};
+      const int ntile = (QN + 15) >> 4;  // column tiles of 16 (QN <= QMAX + 1 = 41: at most 3)
+      for (int NN = 0; NN <= q; ++NN) {
+        float* Fb = F;
+        float* F2b = F2;
+        {
+          float f = ds2ij, e2 = 0.0f;
+#pragma unroll
+          for (int k = 0; k < 16; ++k) {  // BT[NN] and G1[NN]: the same row for every lane
+            f = fmaf(BT[NN][k], d3c[k], f);
+            e2 = fmaf(d3r[k], G1[NN][k], e2);
+          }
+          Fb[i * LP + j] = f;
+          F2b[i * LP + j] = e2;
+        }
+        __syncthreads();
+        if (wv < 3) {
+          const float inv2 = wv == 2 ? 1.0f : frcp(NN + 2);
+          float av[4];
+#pragma unroll
+          for (int ks = 0; ks < 4; ++ks) {  // A[row li][k = 4 ks + lk]
+            const int k = 4 * ks + lk;
+            av[ks] = inv2 * (wv == 0 ? Fb[li * LP + k] : wv == 1 ? Fb[k * LP + li] : F2b[li * LP + k]);
+          }
+#pragma unroll
+          for (int tt = 0; tt < 3; ++tt) {
+            if (tt < ntile) {
+              const int col = 16 * tt + li;  // p (db), n (dg1) or s (dbt3)
+              // letter index of column col: NN - col (db: g1, dg1: b) or col - NN (dbt3: b), zero outside [0, q]
+              const int src = wv == 2 ? col - NN : NN - col;
+              const bool ok = src >= 0 && src <= q && col <= q;
+              const int sv = ok ? src : 0;
+              const float gs = ok ? (wv == 0 ? frcp(sv + 1) : 1.0f) : 0.0f;
+#pragma unroll
+              for (int ks = 0; ks < 4; ++ks) acc[tt] = mfma(av[ks], gs * LtT[(4 * ks + lk) * TPT + sv], acc[tt]);
+            }
+          }
+        }
+        __syncthreads();  // F and F2 are rewritten by the next degree
+      }
+      // accumulators: lane l holds rows 4 (l / 16) + r of column 16 tt + l % 16
+      if (wv < 3) {
+#pragma unroll
+        for (int tt = 0; tt < 3; ++tt) {
+          const int col = 16 * tt + li;
+          if (tt < ntile && col <= q) {
+            const float sc = wv == 2 ? frcp(col + 2) : 1.0f;
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+              const int row = 4 * lk + r;
+              if (wv == 0) dB[col][row] += acc[tt][r];
+              else if (wv == 1) dG1[col][row] += acc[tt][r];
+              else dBT[col][row] += sc * acc[tt][r];
+            }
+          }
+        }
+      }
+      __syncthreads();
     }
     // bt_N -> b_p; g1_n -> b_n
     for (int e = tid; e < (q + 1) * 16; e += 256) {
