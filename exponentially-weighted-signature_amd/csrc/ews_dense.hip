@@ -1716,23 +1716,57 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(EXACTF ? 3 
   f4 dAl4 = {0.0f, 0.0f, 0.0f, 0.0f};  // wavefront 0: the letters' dA terms of entries 4l .. 4l+3
   __syncthreads();
   const long total = (long)a.B * a.n_int;
+  // depth 3: the next interval's inputs (ds3 as four float4 per thread, ds2, dM, ds1 and the increment) are loaded
+  // into registers once the degree loop is done, so that their latency hides behind the rest of the interval
+  f4 pf3[4];
+  float pf2 = 0.0f, pfg = 0.0f, pfs1 = 0.0f, pfv = 0.0f;
+  auto prefetch = [&](long it2) {
+    const int b2 = (int)(it2 / a.n_int), t2 = (int)(it2 - (long)b2 * a.n_int);
+    const float* dr = a.loc + ((size_t)b2 * a.n_int + t2) * LW;
+#pragma unroll
+    for (int m = 0; m < 4; ++m) pf3[m] = *reinterpret_cast<const f4*>(dr + 272 + 4 * tid + 1024 * m);
+    pf2 = dr[16 + tid];
+    pfg = a.fl[((size_t)b2 * a.n_int + t2) * 256 + tid];
+    if (tid < 16) {
+      const float* x = a.path + ((size_t)b2 * a.L + t2) * a.d;
+      pfv = tid < a.d ? x[a.d + tid] - x[tid] : 0.0f;
+      pfs1 = dr[tid];
+    }
+  };
+  if constexpr (N >= 3) {
+    if (blockIdx.x < total) prefetch(blockIdx.x);
+  }
   for (long it = blockIdx.x; it < total; it += gridDim.x) {
     const int b = (int)(it / a.n_int), t = (int)(it - (long)b * a.n_int);
     const float* th = a.clock + (size_t)b * a.L;
     const float h = th[t + 1] - th[t];
     const float* drow = a.loc + ((size_t)b * a.n_int + t) * LW;  // ds_t
     // ---- inputs
-    if (tid < 16) {
-      const float* x = a.path + ((size_t)b * a.L + t) * a.d;
-      const float v = tid < a.d ? x[a.d + tid] - x[tid] : 0.0f;
-      Lt[0][tid] = v;
-      dS1[tid] = drow[tid];
+    if constexpr (N >= 3) {  // from the registers; ds3[a][b][c] at (16 a + b) LP + c
+      if (tid < 16) {
+        Lt[0][tid] = pfv;
+        dS1[tid] = pfs1;
+      }
+      dS2[i * LP + j] = pf2;
+#pragma unroll
+      for (int m = 0; m < 4; ++m) {
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+          const int e = 4 * tid + 1024 * m + c;
+          dS3[(e >> 4) * LP + (e & 15)] = pf3[m][c];
+        }
+      }
+      Gm[tid] = pfg;
+    } else {
+      if (tid < 16) {
+        const float* x = a.path + ((size_t)b * a.L + t) * a.d;
+        const float v = tid < a.d ? x[a.d + tid] - x[tid] : 0.0f;
+        Lt[0][tid] = v;
+        dS1[tid] = drow[tid];
+      }
+      if constexpr (N >= 2) dS2[i * LP + j] = drow[16 + tid];
+      Gm[tid] = a.fl[((size_t)b * a.n_int + t) * 256 + tid];  // dM_t
     }
-    if constexpr (N >= 2) dS2[i * LP + j] = drow[16 + tid];
-    if constexpr (N >= 3) {  // ds3[a][b][c] at (16 a + b) LP + c
-      for (int e = tid; e < 4096; e += 256) dS3[(e >> 4) * LP + (e & 15)] = drow[272 + e];
-    }
-    Gm[tid] = a.fl[((size_t)b * a.n_int + t) * 256 + tid];  // dM_t
     for (int e = tid; e < QN * 16; e += 256) {
       (&dB[0][0])[e] = 0.0f;
       (&dBT[0][0])[e] = 0.0f;
@@ -1860,6 +1894,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(EXACTF ? 3 
           }
         }
       }
+      if (it + gridDim.x < total) prefetch(it + gridDim.x);
       __syncthreads();
     }
     // bt_N -> b_p; g1_n -> b_n
