@@ -1246,7 +1246,15 @@ __global__ __launch_bounds__(256, 2) void k_adj(AdjSeq s) {
     if (tid < 16) s1s[tid] = lrow[tid];
     if constexpr (N >= 2) s2s[ri * RP + rj] = lrow[16 + tid];
     if constexpr (MODE != ADJ_CARRY) {
-      if (s.gmode != G_NONE) {
+      if (s.gmode == G_PREFIX && s.d == 16) {  // unpadded rows: the cotangent row is the state layout
+        const float* grow = s.g + ((long)b * s.n + t) * s.W + s.glvl0;
+        if (tid < 16) L1[tid] += grow[tid];
+        if constexpr (N >= 2) L2[ri * RP + rj] += grow[16 + tid];
+        if constexpr (N >= 3) {
+#pragma unroll 4
+          for (int e = tid; e < 4096; e += 256) L3[(e >> 8) * SP + ((e >> 4) & 15) * RP + (e & 15)] += grow[272 + e];
+        }
+      } else if (s.gmode != G_NONE) {
         if (tid < 16) L1[tid] += adj_g(s, b, t, tid, N);
         if constexpr (N >= 2) L2[ri * RP + rj] += adj_g(s, b, t, 16 + tid, N);
         if constexpr (N >= 3) {
