@@ -963,7 +963,7 @@ __device__ __forceinline__ long out_index(int N, int d, int e) {  // padded stat
   return (i < d && j < d && k < d) ? d + d * d + (i * d + j) * d + k : -1;
 }
 __device__ __forceinline__ void put(const Seq& s, float* orow, int N, int e, float v) {
-  if (s.padded) {
+  if (s.padded || s.d == 16) {  // d = 16: the unpadded row index is the padded one
     orow[e] = v;
   } else {
     const long o = out_index(N, s.d, e);
