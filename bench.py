@@ -382,7 +382,9 @@ C3_CHEN_FLOPS = 427008  # per interval: 2 sum_k k d^(k+1) + 2 sum_k (k-1) d^k at
 def bench_c3(args):
     """Dense-generator forward at BASELINE.json configs[2]: B=16, L=4096, d=16, depth 3, series leaf (q=24),
     input-dependent clock, prefix readout. One step = the four forward passes (leaf + flows, chunk summaries,
-    carry scan, output rows). Returns the JSON record."""
+    carry scan, output rows); with --backward, the training step: the forward keeping its intermediates
+    (ews_dense_forward_keep) and the backward consuming them (ews_dense_backward_kept). The per-pass times and the
+    MFMA roofline come from the forward passes timed on their own. Returns the JSON record."""
     import torch
 
     from ews_mi355x import _native as nat
@@ -413,7 +415,7 @@ def bench_c3(args):
         wsb = torch.empty(int(lib.ews_dense_backward_workspace_bytes(ctypes.byref(desc))), device=dev,
                           dtype=torch.uint8)
 
-    def step(events=None):
+    def fwd_passes(events=None):
         stream = ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream)
         for p in range(npass):
             if events is not None:
@@ -423,15 +425,27 @@ def bench_c3(args):
                       "dense forward pass")
         if events is not None:
             events[npass].record()
-        if bwd:
-            nat.check(lib.ews_dense_backward(ctypes.byref(desc), path.data_ptr(), clock.data_ptr(), A.data_ptr(),
-                                             gout.data_ptr(), gpath.data_ptr(), gclock.data_ptr(), gA.data_ptr(),
-                                             wsb.data_ptr(), stream), "dense backward")
-            if events is not None:
-                events[npass + 1].record()
 
+    def fwd_bwd(events=None):
+        # training step: the forward keeps its leaf, flows, summaries and carries, the backward consumes them
+        stream = ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream)
+        if events is not None:
+            events[0].record()
+        nat.check(lib.ews_dense_forward_keep(ctypes.byref(desc), path.data_ptr(), clock.data_ptr(), A.data_ptr(),
+                                             out.data_ptr(), wsb.data_ptr(), stream), "dense forward (kept)")
+        if events is not None:
+            events[1].record()
+        nat.check(lib.ews_dense_backward_kept(ctypes.byref(desc), path.data_ptr(), clock.data_ptr(),
+                                              A.data_ptr(), gout.data_ptr(), gpath.data_ptr(), gclock.data_ptr(),
+                                              gA.data_ptr(), wsb.data_ptr(), stream), "dense backward (kept)")
+        if events is not None:
+            events[2].record()
+
+    step = fwd_bwd if bwd else fwd_passes
     for _ in range(args.warmup):
         step()
+        if bwd:
+            fwd_passes()
     torch.cuda.synchronize()
     # value from K steps with no events between the passes, per-pass times from K more steps with them
     start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
@@ -441,16 +455,21 @@ def bench_c3(args):
     end.record()
     torch.cuda.synchronize()
     ms = start.elapsed_time(end) / args.steps
-    evs_all = []
+    evs_all, evb_all = [], []
     for _ in range(args.steps):
-        evs = [torch.cuda.Event(enable_timing=True) for _ in range(npass + 2)]
-        step(evs)
+        evs = [torch.cuda.Event(enable_timing=True) for _ in range(npass + 1)]
+        fwd_passes(evs)
         evs_all.append(evs)
+        if bwd:
+            evb = [torch.cuda.Event(enable_timing=True) for _ in range(3)]
+            fwd_bwd(evb)
+            evb_all.append(evb)
     torch.cuda.synchronize()
     names = ["local_terms", "chunk_summary", "carry_scan", "chunk_output"]
-    if bwd:
-        names.append("backward")
     pass_ms = {nm: sum(e[i].elapsed_time(e[i + 1]) for e in evs_all) / args.steps for i, nm in enumerate(names)}
+    if bwd:
+        pass_ms["forward_kept"] = sum(e[0].elapsed_time(e[1]) for e in evb_all) / args.steps
+        pass_ms["backward"] = sum(e[1].elapsed_time(e[2]) for e in evb_all) / args.steps
     n = B * (L - 1)
     flops = n * C3_CHEN_FLOPS
     tf = flops / (pass_ms["chunk_output"] * 1e-3) / 1e12

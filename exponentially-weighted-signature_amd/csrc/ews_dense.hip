@@ -3056,6 +3056,20 @@ int ews_dense_forward(const ews_dense_desc* desc, const float* path, const float
   return EWS_OK;
 }
 
+int ews_dense_forward_keep(const ews_dense_desc* desc, const float* path, const float* clock, const float* A,
+                           float* out, void* workspace, ews_stream_t stream) {
+  DPlan p;
+  const int rc = dense_plan(desc, p);
+  if (rc != EWS_OK) return rc;
+  if (!path || !clock || !A || !out || !workspace) return EWS_ERR_NULL;
+  const Args a = dense_args(desc, p, path, clock, A, out, workspace, true);  // the backward's layout
+  for (int pass = 0; pass < kDenseForwardPasses; ++pass) {
+    const int r = dense_forward_pass(desc, p, a, (hipStream_t)stream, pass);
+    if (r != EWS_OK) return r;
+  }
+  return EWS_OK;
+}
+
 int ews_dense_local_terms(const ews_dense_desc* desc, const float* path, const float* clock, const float* A,
                           float* levels, float* flows, void* workspace, ews_stream_t stream) {
   DPlan p;
@@ -3180,6 +3194,20 @@ int ews_dense_backward(const ews_dense_desc* desc, const float* path, const floa
     if (r != EWS_OK) return r;
   }
   const int r = dense_adjoint(desc, p, a, grad_out, st);
+  if (r != EWS_OK) return r;
+  return dense_leaf_adjoint(desc, p, a, workspace, grad_path, grad_clock, grad_A, st);
+}
+
+int ews_dense_backward_kept(const ews_dense_desc* desc, const float* path, const float* clock, const float* A,
+                            const float* grad_out, float* grad_path, float* grad_clock, float* grad_A,
+                            void* workspace, ews_stream_t stream) {
+  DPlan p;
+  const int rc = dense_plan(desc, p);
+  if (rc != EWS_OK) return rc;
+  if (!path || !clock || !A || !grad_out || !grad_path || !grad_A || !workspace) return EWS_ERR_NULL;
+  const Args a = dense_args(desc, p, path, clock, A, nullptr, workspace, true);
+  hipStream_t st = (hipStream_t)stream;
+  const int r = dense_adjoint(desc, p, a, grad_out, st);  // the leaf, flows, summaries and carries are kept
   if (r != EWS_OK) return r;
   return dense_leaf_adjoint(desc, p, a, workspace, grad_path, grad_clock, grad_A, st);
 }

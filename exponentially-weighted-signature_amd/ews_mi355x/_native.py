@@ -49,6 +49,8 @@ EXPORTED = (
     "ews_dense_backward_workspace_bytes",
     "ews_dense_combine_backward",
     "ews_dense_backward",
+    "ews_dense_forward_keep",
+    "ews_dense_backward_kept",
     "ews_log_dim",
     "ews_log_workspace_bytes",
     "ews_log_forward",
@@ -254,6 +256,10 @@ def load():
     lib.ews_dense_combine_backward.restype = i32
     lib.ews_dense_backward.argtypes = [ddp, vp, vp, vp, vp, vp, vp, vp, vp, vp]
     lib.ews_dense_backward.restype = i32
+    lib.ews_dense_forward_keep.argtypes = [ddp, vp, vp, vp, vp, vp, vp]
+    lib.ews_dense_forward_keep.restype = i32
+    lib.ews_dense_backward_kept.argtypes = [ddp, vp, vp, vp, vp, vp, vp, vp, vp, vp]
+    lib.ews_dense_backward_kept.restype = i32
     ldp = ctypes.POINTER(LogDesc)
     lib.ews_log_dim.argtypes = [i32, i32]
     lib.ews_log_dim.restype = i32

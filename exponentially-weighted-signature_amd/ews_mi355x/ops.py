@@ -158,7 +158,9 @@ def _check_dense(path, clock, A):
 class DenseScan(torch.autograd.Function):
     """out = EWS readout of (path, clock) under a dense generator A (series leaf of order q or the Van Loan leaf,
     flows of chen_expm). The backward is ews_dense_backward: the combine's adjoint scans, then the leaf's and the
-    flows' adjoints per interval and one reduction for dA."""
+    flows' adjoints per interval and one reduction for dA. When a gradient is needed the forward keeps its leaf,
+    flows, chunk summaries and carries (ews_dense_forward_keep) and the first backward consumes them
+    (ews_dense_backward_kept) instead of recomputing them; a second backward of the same graph recomputes."""
 
     @staticmethod
     def forward(ctx, path, clock, A, N, q, flow_mode, readout, level0, chunk, leaf):
@@ -175,10 +177,15 @@ class DenseScan(torch.autograd.Function):
         shape = (B, L - 1, W) if readout == "prefix" else (B, W)
         dev = path.device
         out = torch.empty(shape, device=dev, dtype=torch.float32)
-        ws = torch.empty(int(lib.ews_dense_workspace_bytes(ctypes.byref(desc))), device=dev, dtype=torch.uint8)
-        rc = lib.ews_dense_forward(ctypes.byref(desc), path.data_ptr(), clock.data_ptr(), A.data_ptr(),
-                                   out.data_ptr(), ws.data_ptr(), _stream_handle(dev))
+        keep = any(ctx.needs_input_grad[:3])
+        nbytes = (lib.ews_dense_backward_workspace_bytes if keep else lib.ews_dense_workspace_bytes)(
+            ctypes.byref(desc))
+        ws = torch.empty(int(nbytes), device=dev, dtype=torch.uint8)
+        fwd = lib.ews_dense_forward_keep if keep else lib.ews_dense_forward
+        rc = fwd(ctypes.byref(desc), path.data_ptr(), clock.data_ptr(), A.data_ptr(), out.data_ptr(), ws.data_ptr(),
+                 _stream_handle(dev))
         nat.check(rc, "ews_dense_forward")
+        ctx.kept = ws if keep else None
         return out
 
     @staticmethod
@@ -192,11 +199,15 @@ class DenseScan(torch.autograd.Function):
         need_clock = ctx.needs_input_grad[1]
         gclock = torch.empty_like(clock) if need_clock else None
         gA = torch.empty_like(A)
-        ws = torch.empty(int(lib.ews_dense_backward_workspace_bytes(ctypes.byref(desc))), device=dev,
-                         dtype=torch.uint8)
-        rc = lib.ews_dense_backward(ctypes.byref(desc), path.data_ptr(), clock.data_ptr(), A.data_ptr(),
-                                    gout.data_ptr(), gpath.data_ptr(), gclock.data_ptr() if need_clock else None,
-                                    gA.data_ptr(), ws.data_ptr(), _stream_handle(dev))
+        ws, kept = ctx.kept, ctx.kept is not None
+        ctx.kept = None  # the backward overwrites what the forward kept
+        if not kept:
+            ws = torch.empty(int(lib.ews_dense_backward_workspace_bytes(ctypes.byref(desc))), device=dev,
+                             dtype=torch.uint8)
+        bwd = lib.ews_dense_backward_kept if kept else lib.ews_dense_backward
+        rc = bwd(ctypes.byref(desc), path.data_ptr(), clock.data_ptr(), A.data_ptr(), gout.data_ptr(),
+                 gpath.data_ptr(), gclock.data_ptr() if need_clock else None, gA.data_ptr(), ws.data_ptr(),
+                 _stream_handle(dev))
         nat.check(rc, "ews_dense_backward")
         return gpath, gclock, gA, None, None, None, None, None, None, None
 

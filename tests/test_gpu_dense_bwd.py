@@ -257,3 +257,40 @@ def test_dense_backward_is_deterministic(leaf, N, mode):
         grads.append((p.grad.clone(), c.grad.clone(), a.grad.clone()))
     for name, x, y in zip(("path", "clock", "A"), grads[0], grads[1]):
         assert torch.equal(x, y), f"{name} gradient differs between two identical calls"
+
+
+@pytest.mark.parametrize("leaf,N,readout", [("series", 3, "prefix"), ("van_loan", 2, "max"), ("series", 2, "mean"),
+                                            ("block_series", 1, "terminal")])
+def test_kept_forward_backward_equals_recompute(leaf, N, readout):
+    """The training pair ews_dense_forward_keep / ews_dense_backward_kept (the forward's leaf, flows, summaries and
+    carries kept for the backward) gives the gradients of ews_dense_backward (which recomputes them) bit for bit:
+    both run the same kernels on the same data. A second backward of the same graph (retain_graph) finds the kept
+    data consumed and recomputes; it matches too."""
+    B, L, d = 2, 200, 16
+    rng = np.random.default_rng(91)
+    path = torch.tensor(np.cumsum(rng.normal(size=(B, L, d)) * 0.2, 1), dtype=torch.float32, device=DEV)
+    clock = torch.tensor(np.cumsum(rng.uniform(0.01, 0.05, size=(B, L)), 1), dtype=torch.float32, device=DEV)
+    A = torch.tensor(rng.normal(size=(d, d)) / np.sqrt(d) + np.eye(d), dtype=torch.float32, device=DEV)
+    dl = ops.DenseLeaf(leaf, q=10, M=6)
+    p = path.clone().requires_grad_(True)
+    c = clock.clone().requires_grad_(True)
+    a = A.clone().requires_grad_(True)
+    out = ops.dense_scan(p, c, a, N, 10, "per_interval", readout, True, leaf=dl)
+    g = torch.tensor(rng.normal(size=tuple(out.shape)), dtype=torch.float32, device=DEV)
+    kept = torch.autograd.grad(out, (p, c, a), g, retain_graph=True)
+    again = torch.autograd.grad(out, (p, c, a), g)  # the kept data is consumed: this one recomputes
+    # the recomputing entry point on its own
+    from ews_mi355x import _native as nat
+    import ctypes
+    lib = nat.load()
+    desc = ops.make_dense_desc(B, L, d, N, 10, "per_interval", readout, True, 0, dl)
+    ws = torch.empty(int(lib.ews_dense_backward_workspace_bytes(ctypes.byref(desc))), device=DEV, dtype=torch.uint8)
+    gp, gc, ga = torch.empty_like(path), torch.empty_like(clock), torch.empty_like(A)
+    st = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    nat.check(lib.ews_dense_backward(ctypes.byref(desc), path.data_ptr(), clock.data_ptr(), A.data_ptr(),
+                                     g.contiguous().data_ptr(), gp.data_ptr(), gc.data_ptr(), ga.data_ptr(),
+                                     ws.data_ptr(), st), "ews_dense_backward")
+    torch.cuda.synchronize()
+    for name, x, y, z in zip(("path", "clock", "A"), kept, again, (gp, gc, ga)):
+        assert torch.equal(x, z), f"{name}: kept backward differs from the recomputing one"
+        assert torch.equal(y, z), f"{name}: second backward differs from the recomputing one"
