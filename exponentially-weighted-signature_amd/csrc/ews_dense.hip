@@ -1677,6 +1677,17 @@ __device__ float block_flow_adjoint(const Args& a, const LdsTable* sp, float nor
   return block_rational_adjoint(sp, a.chen_expm, hf, W2, G, nullptr, W1, W3, red, dAl, tid);
 }
 
+// Coefficient of a letter from its stage's base (series-leaf adjoint): b_{a+m} = c P_m b_a with
+// c = (-h)^m / C(a + m, m) = prod_{j=1..m} (-h) j / (a + j); returns (c, dc/dh).
+__device__ __forceinline__ float2 letter_coef(float h, int a, int m) {
+  float k = 1.0f, hp = 1.0f;  // prod j / (a + j); (-h)^(m-1)
+  for (int jj = 1; jj <= m; ++jj) {
+    k *= (float)jj * frcp(a + jj);
+    if (jj < m) hp *= -h;
+  }
+  return float2{-h * hp * k, -(float)m * hp * k};
+}
+
 template <int N, bool EXACTF>  // EXACTF: exact flows (the other schemes' code is left out)
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(EXACTF ? 3 : 1))) void k_leaf_bwd(Args a, LeafBwd o) {
   constexpr int LW = lw_of(N);
@@ -1691,6 +1702,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(EXACTF ? 3 
   constexpr int TPT = QMAX + 4;  // row pitch of the transposed letters (QMAX + 1 columns)
   __shared__ __align__(16) float dS2[16 * LP], F[16 * LP], F2[16 * LP], Gm[256];
   __shared__ __align__(16) float LtT[N >= 3 ? 16 * TPT : 1];
+  __shared__ float2 s_lc[PM];  // the letter coefficients of a stage and their h-derivatives
   __shared__ float dS1[16], red[8];
   extern __shared__ __align__(16) float dyn[];  // the six letter arrays, (q + 1) x 16 each
   typedef float Row16[16];
@@ -1713,15 +1725,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(EXACTF ? 3 
 #pragma unroll
   for (int p = 0; p < HP; ++p) H[p] = 0.0f;
   float dAl = 0.0f;
-  const int l = tid & 63, g = l >> 4, c16 = l & 15;
-  // the letter chains run on wavefront 0: lane (c16, g) holds A[c16][4g .. 4g+3] and A[4g .. 4g+3][c16]
-  f4 Ar, Ac;
-#pragma unroll
-  for (int r = 0; r < 4; ++r) {
-    Ar[r] = a.apow[256 + c16 * 16 + 4 * g + r];
-    Ac[r] = a.apow[256 + (4 * g + r) * 16 + c16];
-  }
-  f4 dAl4 = {0.0f, 0.0f, 0.0f, 0.0f};  // wavefront 0: the letters' dA terms of entries 4l .. 4l+3
+  const int l = tid & 63;
   __syncthreads();
   const long total = (long)a.B * a.n_int;
   // depth 3: the next interval's inputs (ds3 as four float4 per thread, ds2, dM, ds1 and the increment) are loaded
@@ -1780,18 +1784,26 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(EXACTF ? 3 
       (&dBT[0][0])[e] = 0.0f;
     }
     __syncthreads();
-    // ---- letters b_p = (-h/p) A b_{p-1} (wavefront 0)
-    if (tid < 64) {
-      for (int p = 1; p <= q; ++p) {
-        const f4 bp = *reinterpret_cast<const f4*>(&Lt[p - 1][4 * g]);
-        float v = fmaf(Ar.x, bp.x, fmaf(Ar.y, bp.y, fmaf(Ar.z, bp.z, Ar.w * bp.w)));
-        v += __shfl_xor(v, 16, 64);
-        v += __shfl_xor(v, 32, 64);
-        if (g == 0) Lt[p][c16] = v * (-h * frcp(p));
-        wave_order_d();
+    // ---- letters b_p = (-h)^p A^p v / p!, by stages from the powers table P_m = A^m / m!: the letters a + m of
+    // the stage on base letter a (a = 0, PM, 2 PM, ...; m = 1 .. PM) are b_{a+m} = c_{a,m} P_m b_a with
+    // c_{a,m} = (-h)^m / C(a + m, m), all of a stage at once (thread: power m, row r)
+    for (int a0 = 0; a0 < q; a0 += PM) {
+      if (tid < PM) s_lc[tid] = letter_coef(h, a0, tid + 1);
+      __syncthreads();
+      for (int e = tid; e < PM * 16; e += 256) {
+        const int m = 1 + (e >> 4), r = e & 15, p = a0 + m;
+        if (p <= q) {
+          float x = 0.0f;
+#pragma unroll 4
+          for (int k = 0; k < 16; ++k) {
+            const int kk = (k + r) & 15;  // rotated so that the 16 rows of a power hit distinct banks
+            x = fmaf(sp[m][r * 16 + kk], Lt[a0][kk], x);
+          }
+          Lt[p][r] = s_lc[m - 1].x * x;
+        }
       }
+      __syncthreads();
     }
-    __syncthreads();
     for (int e = tid; e < (q + 1) * 16; e += 256) {
       const int n = e >> 4, r = e & 15;
       G1[n][r] = Lt[n][r] * frcp(n + 1);
@@ -1915,30 +1927,46 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(EXACTF ? 3 
       dB[p][r] = x;
     }
     __syncthreads();
-    // ---- letters reverse (wavefront 0): db_{p-1} += (-h/p) A^T db_p; dA += (-h/p) db_p (x) b_{p-1};
-    // dh += -(1/p) <A^T db_p, b_{p-1}>
-    float dhl = 0.0f;
-    if (tid < 64) {
-      const int gi = l >> 2, gj = 4 * (l & 3);
-      for (int p = q; p >= 1; --p) {
-        const f4 dp = *reinterpret_cast<const f4*>(&dB[p][4 * g]);
-        float y = fmaf(Ac.x, dp.x, fmaf(Ac.y, dp.y, fmaf(Ac.z, dp.z, Ac.w * dp.w)));  // (A^T db_p)[c16]
-        y += __shfl_xor(y, 16, 64);
-        y += __shfl_xor(y, 32, 64);
-        const float c = -h * frcp(p);
-        const float dpi = c * dB[p][gi];
-        const f4 bm = *reinterpret_cast<const f4*>(&Lt[p - 1][gj]);
+    // ---- the letters in reverse, stage by stage (the last first): for p = a + m, z_p = P_m^T db_p,
+    // db_a += c_{a,m} z_p, dh += (d c_{a,m} / dh) <z_p, b_a>, and the cotangent of A^m gains
+    // (c_{a,m} / m!) db_p (x) b_a (H_m, turned into dA once per launch with the flows' terms)
+    float dhl = 0.0f;  // partial dh in threads 0 .. 15
+    Row16* Zt = dBT;   // free after the degree sums
+    for (int a0 = q > 0 ? ((q - 1) / PM) * PM : -1; a0 >= 0; a0 -= PM) {
+      if (tid < PM) s_lc[tid] = letter_coef(h, a0, tid + 1);
+      for (int e = tid; e < PM * 16; e += 256) {
+        const int m = 1 + (e >> 4), jj = e & 15, p = a0 + m;
+        float z = 0.0f;
+        if (p <= q) {
 #pragma unroll
-        for (int r = 0; r < 4; ++r) dAl4[r] = fmaf(dpi, bm[r], dAl4[r]);
-        wave_order_d();
-        if (g == 0) {
-          dB[p - 1][c16] += c * y;
-          dhl -= y * Lt[p - 1][c16] * frcp(p);
+          for (int i2 = 0; i2 < 16; ++i2) z = fmaf(sp[m][i2 * 16 + jj], dB[p][i2], z);
         }
-        wave_order_d();
+        Zt[m - 1][jj] = z;
       }
+      __syncthreads();  // the stage's coefficients and z
+      {
+        const float bj = Lt[a0][j];
+        float ifact = 1.0f;
+#pragma unroll
+        for (int m = 1; m <= PM; ++m) {
+          ifact *= 1.0f / (float)m;
+          const int p = a0 + m;
+          if (p <= q) H[m] = fmaf(s_lc[m - 1].x * ifact * dB[p][i], bj, H[m]);
+        }
+      }
+      if (tid < 16) {
+        float acc = dB[a0][tid], dz = 0.0f;
+        for (int m = 1; m <= PM && a0 + m <= q; ++m) {
+          const float2 cc = s_lc[m - 1];
+          const float z = Zt[m - 1][tid];
+          acc = fmaf(cc.x, z, acc);
+          dz = fmaf(cc.y, z, dz);
+        }
+        dB[a0][tid] = acc;
+        dhl = fmaf(dz, Lt[a0][tid], dhl);
+      }
+      __syncthreads();
     }
-    __syncthreads();
     // ---- flow adjoint
     bool ident;
     const float hf = flow_step(a, th, t, ident);
@@ -1969,11 +1997,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(EXACTF ? 3 
   float* pb = o.part + (size_t)blockIdx.x * (HP + 1) * 256;
 #pragma unroll
   for (int p = 0; p < HP; ++p) pb[p * 256 + tid] = H[p];
-  Gm[tid] = 0.0f;
-  __syncthreads();
-  if (tid < 64) *reinterpret_cast<f4*>(Gm + 4 * l) = dAl4;
-  __syncthreads();
-  pb[HP * 256 + tid] = dAl + Gm[tid];
+  pb[HP * 256 + tid] = dAl;
 }
 
 // Van Loan leaf adjoint (one workgroup per interval, grid-stride). The forward's recompute saved per interval the
