@@ -1190,6 +1190,52 @@ __device__ __forceinline__ float adj_g(const AdjSeq& s, int b, int t, int e, int
   return s.amax[(long)b * LWN(N) + e] == t ? s.g[(long)b * s.W + col] : 0.0f;
 }
 
+// The inputs of one adjoint step of thread tid: the flow entry M[tid / 16][tid % 16], the local terms' level 1
+// (tid < 16) and level-2 entry tid, the row added this step (entries tid, 16 + tid, 272 + tid + 256 i: the readout
+// cotangent g_t, or for CARRY the chunk's local part), and for EMIT the state before the step (levels 1-2).
+template <int N, int MODE> struct AdjIn {
+  float M, s1, s2, r1, r2;
+  float r3[N >= 3 ? 16 : 1];
+  float S1, S2;
+};
+template <int N, int MODE>
+__device__ __forceinline__ void adj_load(const AdjSeq& s, int b, int t, int tid, AdjIn<N, MODE>& x) {
+  constexpr int LW = lw_of(N);
+  const float* lrow = s.lv + b * s.lv_bs + (long)t * LW;
+  const float* frow = s.fl + b * s.fl_bs + (long)t * 256;
+  x.M = frow[tid];
+  x.s1 = tid < 16 ? lrow[tid] : 0.0f;
+  if constexpr (N >= 2) x.s2 = lrow[16 + tid];
+  x.r1 = x.r2 = 0.0f;
+#pragma unroll
+  for (int i = 0; i < (N >= 3 ? 16 : 1); ++i) x.r3[i] = 0.0f;
+  if constexpr (MODE == ADJ_CARRY) {
+    const float* lo = s.lloc + ((long)b * s.C + t) * LW;
+    if (tid < 16) x.r1 = lo[tid];
+    if constexpr (N >= 2) x.r2 = lo[16 + tid];
+    if constexpr (N >= 3) {
+#pragma unroll
+      for (int i = 0; i < 16; ++i) x.r3[i] = lo[272 + tid + 256 * i];
+    }
+  } else if (s.gmode == G_PREFIX && s.d == 16) {  // unpadded rows: the cotangent row is the state layout
+    const float* grow = s.g + ((long)b * s.n + t) * s.W + s.glvl0;
+    if (tid < 16) x.r1 = grow[tid];
+    if constexpr (N >= 2) x.r2 = grow[16 + tid];
+    if constexpr (N >= 3) {
+#pragma unroll
+      for (int i = 0; i < 16; ++i) x.r3[i] = grow[272 + tid + 256 * i];
+    }
+  }  // the other readouts' cotangents (index mapping, mean, max) are read inside the step
+  x.S1 = x.S2 = 0.0f;
+  if constexpr (MODE == ADJ_EMIT) {
+    if (t > 0) {
+      const float* srow = s.st + ((long)b * s.n + t - 1) * LW;
+      if (tid < 16) x.S1 = srow[tid];
+      if constexpr (N >= 2) x.S2 = srow[16 + tid];
+    }
+  }
+}
+
 template <int N, int MODE>
 __global__ __launch_bounds__(256, 2) void k_adj(AdjSeq s) {
   constexpr int LW = lw_of(N);
@@ -1227,10 +1273,13 @@ __global__ __launch_bounds__(256, 2) void k_adj(AdjSeq s) {
     }
   }
   __syncthreads();
+  // The inputs of step t are loaded one step ahead into registers (cur / nxt), so that no global load sits on the
+  // step's dependency chain: the flow, the local terms' levels 1-2, the row added this step (the readout's
+  // cotangent row g_t, or CARRY's local part, added at the end of the step), and for EMIT the state before the step.
+  AdjIn<N, MODE> cur, nxt;
+  if (Tc > 0) adj_load<N, MODE>(s, b, t0 + Tc - 1, tid, cur);
   for (int k = Tc - 1; k >= 0; --k) {
     const int t = t0 + k;  // row (interval / chunk) index
-    const float* lrow = s.lv + b * s.lv_bs + (long)t * LW;
-    const float* frow = s.fl + b * s.fl_bs + (long)t * 256;
     if constexpr (MODE == ADJ_CARRY) {  // Lambda_{t+1} is the current lambda
       float* o = s.lam + ((long)b * (s.C + 1) + t + 1) * LW;
       if (t + 1 < s.C) {
@@ -1242,17 +1291,19 @@ __global__ __launch_bounds__(256, 2) void k_adj(AdjSeq s) {
       }
     }
     // ---- inputs of the step; lambda += g_t
-    Ms[tid] = frow[tid];
-    if (tid < 16) s1s[tid] = lrow[tid];
-    if constexpr (N >= 2) s2s[ri * RP + rj] = lrow[16 + tid];
+    Ms[tid] = cur.M;
+    if (tid < 16) s1s[tid] = cur.s1;
+    if constexpr (N >= 2) s2s[ri * RP + rj] = cur.s2;
     if constexpr (MODE != ADJ_CARRY) {
-      if (s.gmode == G_PREFIX && s.d == 16) {  // unpadded rows: the cotangent row is the state layout
-        const float* grow = s.g + ((long)b * s.n + t) * s.W + s.glvl0;
-        if (tid < 16) L1[tid] += grow[tid];
-        if constexpr (N >= 2) L2[ri * RP + rj] += grow[16 + tid];
+      if (s.gmode == G_PREFIX && s.d == 16) {
+        if (tid < 16) L1[tid] += cur.r1;
+        if constexpr (N >= 2) L2[ri * RP + rj] += cur.r2;
         if constexpr (N >= 3) {
-#pragma unroll 4
-          for (int e = tid; e < 4096; e += 256) L3[(e >> 8) * SP + ((e >> 4) & 15) * RP + (e & 15)] += grow[272 + e];
+#pragma unroll
+          for (int i = 0; i < 16; ++i) {
+            const int e = tid + 256 * i;
+            L3[(e >> 8) * SP + ((e >> 4) & 15) * RP + (e & 15)] += cur.r3[i];
+          }
         }
       } else if (s.gmode != G_NONE) {
         if (tid < 16) L1[tid] += adj_g(s, b, t, tid, N);
@@ -1263,11 +1314,28 @@ __global__ __launch_bounds__(256, 2) void k_adj(AdjSeq s) {
         }
       }
     }
-    if constexpr (EMIT) {  // the state before the step: row t - 1 (zero before the first interval)
-      const float* srow = t > 0 ? s.st + ((long)b * s.n + t - 1) * LW : nullptr;
-      if (tid < 16) S1s[tid] = srow ? srow[tid] : 0.0f;
-      if constexpr (N >= 2) S2s[ri * RP + rj] = srow ? srow[16 + tid] : 0.0f;
+    if constexpr (EMIT) {  // the state before the step (zero before the first interval)
+      if (tid < 16) S1s[tid] = cur.S1;
+      if constexpr (N >= 2) S2s[ri * RP + rj] = cur.S2;
     }
+    // EMIT, depth 3: the lane's operands of S3 (state before the step) for V1 = S3 x_1 M (s3v) and for T1 (s3t),
+    // issued before the next step's inputs so that their wait does not cover those
+    constexpr int NS3 = EMIT && N >= 3 ? 16 : 1;
+    float s3v[NS3], s3t[NS3];
+    if constexpr (EMIT && N >= 3) {
+      const float* s3g = t > 0 ? s.st + ((long)b * s.n + t - 1) * LW + 272 : nullptr;
+#pragma unroll
+      for (int jj = 0; jj < 4; ++jj)
+#pragma unroll
+        for (int k2 = 0; k2 < 4; ++k2) s3v[4 * jj + k2] = s3g ? s3g[(4 * g + k2) * 256 + (4 * w + jj) * 16 + c16] : 0.0f;
+#pragma unroll
+      for (int q = 0; q < 16; ++q) {
+        const int ks = 16 * w + q, j = ks >> 2, kk = 4 * (ks & 3) + g;
+        s3t[q] = s3g ? s3g[c16 * 256 + j * 16 + kk] : 0.0f;
+      }
+    }
+    // the next step's inputs (EMIT at depth 3: after the T contractions, where the S3 operands are dead)
+    if (!(EMIT && N >= 3) && k > 0) adj_load<N, MODE>(s, b, t - 1, tid, nxt);
     __syncthreads();
     const f4 M4 = *reinterpret_cast<const f4*>(Ms + c16 * 16 + 4 * g);  // M[c16][4g + r]
     f4 MT4;                                                                // M^T[c16][4g + r]
@@ -1315,9 +1383,6 @@ __global__ __launch_bounds__(256, 2) void k_adj(AdjSeq s) {
           }
           MS2[ri * RP + rj] = a;
           MS2T[ri * RP + rj] = bt;
-        }
-        if constexpr (N >= 3) {
-          for (int e = tid; e < 4096; e += 256) drow[272 + e] = L3[(e >> 8) * SP + ((e >> 4) & 15) * RP + (e & 15)];
         }
       }
     }
@@ -1379,15 +1444,12 @@ __global__ __launch_bounds__(256, 2) void k_adj(AdjSeq s) {
       }
       if constexpr (EMIT) {
         // V1 = S3 x_1 M, tiles j, with S3 read from the state row (L2-resident; zero before the first interval)
-        const float* s3g = t > 0 ? s.st + ((long)b * s.n + t - 1) * LW + 272 : nullptr;
 #pragma unroll
         for (int jj = 0; jj < 4; ++jj) {
           const int j = 4 * w + jj;
           f4 z = {0.0f, 0.0f, 0.0f, 0.0f};
-          if (s3g) {
 #pragma unroll
-            for (int k2 = 0; k2 < 4; ++k2) z = mfma(M4[k2], s3g[(4 * g + k2) * 256 + j * 16 + c16], z);
-          }
+          for (int k2 = 0; k2 < 4; ++k2) z = mfma(M4[k2], s3v[4 * jj + k2], z);
 #pragma unroll
           for (int r = 0; r < 4; ++r) B3[(4 * g + r) * SP + j * RP + c16] = z[r];
         }
@@ -1421,15 +1483,17 @@ __global__ __launch_bounds__(256, 2) void k_adj(AdjSeq s) {
       __syncthreads();
       if constexpr (EMIT) {
         // T1[p][q] = sum_{j, k} C3[p][j][k] S3[q][j][k];  T3[p][q] = sum_{a, b} l_3[a][b][p] W3[a][b][q]
-        const float* s3g = t > 0 ? s.st + ((long)b * s.n + t - 1) * LW + 272 : nullptr;
-#pragma unroll 4
-        for (int ks = 16 * w; ks < 16 * w + 16; ++ks) {
-          const int j = ks >> 2, kk = 4 * (ks & 3) + g;
-          if (s3g) tacc = mfma(C3[c16 * SP + j * RP + kk], s3g[c16 * 256 + j * 16 + kk], tacc);
+#pragma unroll
+        for (int q = 0; q < 16; ++q) {
+          const int ks = 16 * w + q, j = ks >> 2, kk = 4 * (ks & 3) + g;
+          tacc = mfma(C3[c16 * SP + j * RP + kk], s3t[q], tacc);
           tacc = mfma(L3[j * SP + kk * RP + c16], B3[j * SP + kk * RP + c16], tacc);
         }
 #pragma unroll
         for (int r = 0; r < 4; ++r) Tw[w][(4 * g + r) * 16 + c16] = tacc[r];
+        if (k > 0) adj_load<N, MODE>(s, b, t - 1, tid, nxt);
+        // ds3 = l_3 (the step's cotangent of its level-3 local term); L3 is rewritten after the next barrier
+        for (int e = tid; e < 4096; e += 256) drow[272 + e] = L3[(e >> 8) * SP + ((e >> 4) & 15) * RP + (e & 15)];
       }
       __syncthreads();
       // l_3 <- C3 x_1 M^T (tiles j)
@@ -1479,14 +1543,18 @@ __global__ __launch_bounds__(256, 2) void k_adj(AdjSeq s) {
     }
     if constexpr (MODE == ADJ_CARRY) {  // Lambda_t = R^T Lambda_{t+1} + local_t
       __syncthreads();
-      const float* lo = s.lloc + ((long)b * s.C + t) * LW;
-      if (tid < 16) L1[tid] += lo[tid];
-      if constexpr (N >= 2) L2[ri * RP + rj] += lo[16 + tid];
+      if (tid < 16) L1[tid] += cur.r1;
+      if constexpr (N >= 2) L2[ri * RP + rj] += cur.r2;
       if constexpr (N >= 3) {
-        for (int e = tid; e < 4096; e += 256) L3[(e >> 8) * SP + ((e >> 4) & 15) * RP + (e & 15)] += lo[272 + e];
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+          const int e = tid + 256 * i;
+          L3[(e >> 8) * SP + ((e >> 4) & 15) * RP + (e & 15)] += cur.r3[i];
+        }
       }
     }
     __syncthreads();
+    cur = nxt;
   }
   if constexpr (MODE == ADJ_LOCAL) {
     float* o = s.lam + ((long)b * s.C + c) * LW;
