@@ -1191,8 +1191,25 @@ __device__ __forceinline__ float adj_g(const AdjSeq& s, int b, int t, int e, int
 }
 
 // The inputs of one adjoint step of thread tid: the flow entry M[tid / 16][tid % 16], the local terms' level 1
-// (tid < 16) and level-2 entry tid, the row added this step (entries tid, 16 + tid, 272 + tid + 256 i: the readout
-// cotangent g_t, or for CARRY the chunk's local part), and for EMIT the state before the step (levels 1-2).
+// (tid < 16) and level-2 entry tid, the row added this step (entries tid, 16 + tid and the sixteen level-3 entries
+// 272 + 16 tid + i: the readout cotangent g_t, or for CARRY the chunk's local part), and for EMIT the state before
+// the step (levels 1-2).
+// x through an empty asm statement in a vector register: the compiler can neither fold it nor hoist what is
+// computed from it out of the enclosing loop
+__device__ __forceinline__ int opaque_vgpr(int x) {
+  asm volatile("" : "+v"(x));
+  return x;
+}
+// LDS row of 16 floats (16-byte aligned) += v
+__device__ __forceinline__ void add_row16(float* row, const float* v) {
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    f4 x = *reinterpret_cast<const f4*>(row + 4 * i);
+#pragma unroll
+    for (int r = 0; r < 4; ++r) x[r] += v[4 * i + r];
+    *reinterpret_cast<f4*>(row + 4 * i) = x;
+  }
+}
 template <int N, int MODE> struct AdjIn {
   float M, s1, s2, r1, r2;
   float r3[N >= 3 ? 16 : 1];
@@ -1214,16 +1231,22 @@ __device__ __forceinline__ void adj_load(const AdjSeq& s, int b, int t, int tid,
     if (tid < 16) x.r1 = lo[tid];
     if constexpr (N >= 2) x.r2 = lo[16 + tid];
     if constexpr (N >= 3) {
+      const f4* q = reinterpret_cast<const f4*>(lo + 272 + 16 * tid);  // rows of LW floats: 16-byte aligned
 #pragma unroll
-      for (int i = 0; i < 16; ++i) x.r3[i] = lo[272 + tid + 256 * i];
+      for (int i = 0; i < 4; ++i) {
+        const f4 v = q[i];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) x.r3[4 * i + r] = v[r];
+      }
     }
   } else if (s.gmode == G_PREFIX && s.d == 16) {  // unpadded rows: the cotangent row is the state layout
     const float* grow = s.g + ((long)b * s.n + t) * s.W + s.glvl0;
     if (tid < 16) x.r1 = grow[tid];
     if constexpr (N >= 2) x.r2 = grow[16 + tid];
     if constexpr (N >= 3) {
+      const float* q = grow + 272 + 16 * tid;  // any alignment (rows of W floats)
 #pragma unroll
-      for (int i = 0; i < 16; ++i) x.r3[i] = grow[272 + tid + 256 * i];
+      for (int i = 0; i < 16; ++i) x.r3[i] = q[i];
     }
   }  // the other readouts' cotangents (index mapping, mean, max) are read inside the step
   x.S1 = x.S2 = 0.0f;
@@ -1278,15 +1301,25 @@ __global__ __launch_bounds__(256, 2) void k_adj(AdjSeq s) {
   // cotangent row g_t, or CARRY's local part, added at the end of the step), and for EMIT the state before the step.
   AdjIn<N, MODE> cur, nxt;
   if (Tc > 0) adj_load<N, MODE>(s, b, t0 + Tc - 1, tid, cur);
+  const int tid_all = tid;
   for (int k = Tc - 1; k >= 0; --k) {
     const int t = t0 + k;  // row (interval / chunk) index
+    // the lane indices are re-derived every step from an opaque copy of the thread index, so that the compiler
+    // recomputes the step's LDS and global addresses (a few integer instructions) instead of keeping every one of
+    // them live across the loop
+    const int tid = opaque_vgpr(tid_all), w = tid >> 6, l = tid & 63, g = l >> 4, c16 = l & 15;
+    const int ri = tid >> 4, rj = tid & 15;
+    (void)l;
     if constexpr (MODE == ADJ_CARRY) {  // Lambda_{t+1} is the current lambda
       float* o = s.lam + ((long)b * (s.C + 1) + t + 1) * LW;
       if (t + 1 < s.C) {
         if (tid < 16) o[tid] = L1[tid];
         if constexpr (N >= 2) o[16 + tid] = L2[ri * RP + rj];
         if constexpr (N >= 3) {
-          for (int e = tid; e < 4096; e += 256) o[272 + e] = L3[(e >> 8) * SP + ((e >> 4) & 15) * RP + (e & 15)];
+          const float* src = L3 + (tid >> 4) * SP + (tid & 15) * RP;
+          f4* dst = reinterpret_cast<f4*>(o + 272 + 16 * tid);
+#pragma unroll
+          for (int i = 0; i < 4; ++i) dst[i] = *reinterpret_cast<const f4*>(src + 4 * i);
         }
       }
     }
@@ -1298,13 +1331,7 @@ __global__ __launch_bounds__(256, 2) void k_adj(AdjSeq s) {
       if (s.gmode == G_PREFIX && s.d == 16) {
         if (tid < 16) L1[tid] += cur.r1;
         if constexpr (N >= 2) L2[ri * RP + rj] += cur.r2;
-        if constexpr (N >= 3) {
-#pragma unroll
-          for (int i = 0; i < 16; ++i) {
-            const int e = tid + 256 * i;
-            L3[(e >> 8) * SP + ((e >> 4) & 15) * RP + (e & 15)] += cur.r3[i];
-          }
-        }
+        if constexpr (N >= 3) add_row16(L3 + (tid >> 4) * SP + (tid & 15) * RP, cur.r3);
       } else if (s.gmode != G_NONE) {
         if (tid < 16) L1[tid] += adj_g(s, b, t, tid, N);
         if constexpr (N >= 2) L2[ri * RP + rj] += adj_g(s, b, t, 16 + tid, N);
@@ -1324,15 +1351,15 @@ __global__ __launch_bounds__(256, 2) void k_adj(AdjSeq s) {
     float s3v[NS3], s3t[NS3];
     if constexpr (EMIT && N >= 3) {
       const float* s3g = t > 0 ? s.st + ((long)b * s.n + t - 1) * LW + 272 : nullptr;
+      // S3[4g + k2][4w + jj][c16] and S3[c16][4w + q / 4][4 (q % 4) + g]: one base each, offsets within 4 KB
+      const float* pv = s3g + (4 * g * 256 + 4 * w * 16 + c16);
+      const float* pt = s3g + (c16 * 256 + 4 * w * 16 + g);
 #pragma unroll
       for (int jj = 0; jj < 4; ++jj)
 #pragma unroll
-        for (int k2 = 0; k2 < 4; ++k2) s3v[4 * jj + k2] = s3g ? s3g[(4 * g + k2) * 256 + (4 * w + jj) * 16 + c16] : 0.0f;
+        for (int k2 = 0; k2 < 4; ++k2) s3v[4 * jj + k2] = s3g ? pv[k2 * 256 + jj * 16] : 0.0f;
 #pragma unroll
-      for (int q = 0; q < 16; ++q) {
-        const int ks = 16 * w + q, j = ks >> 2, kk = 4 * (ks & 3) + g;
-        s3t[q] = s3g ? s3g[c16 * 256 + j * 16 + kk] : 0.0f;
-      }
+      for (int q = 0; q < 16; ++q) s3t[q] = s3g ? pt[(q >> 2) * 16 + 4 * (q & 3)] : 0.0f;
     }
     // the next step's inputs (EMIT at depth 3: after the T contractions, where the S3 operands are dead)
     if (!(EMIT && N >= 3) && k > 0) adj_load<N, MODE>(s, b, t - 1, tid, nxt);
@@ -1493,7 +1520,12 @@ __global__ __launch_bounds__(256, 2) void k_adj(AdjSeq s) {
         for (int r = 0; r < 4; ++r) Tw[w][(4 * g + r) * 16 + c16] = tacc[r];
         if (k > 0) adj_load<N, MODE>(s, b, t - 1, tid, nxt);
         // ds3 = l_3 (the step's cotangent of its level-3 local term); L3 is rewritten after the next barrier
-        for (int e = tid; e < 4096; e += 256) drow[272 + e] = L3[(e >> 8) * SP + ((e >> 4) & 15) * RP + (e & 15)];
+        {
+          const float* src = L3 + (tid >> 4) * SP + (tid & 15) * RP;
+          f4* dst = reinterpret_cast<f4*>(drow + 272 + 16 * tid);  // padded rows of LW floats: 16-byte aligned
+#pragma unroll
+          for (int i = 0; i < 4; ++i) dst[i] = *reinterpret_cast<const f4*>(src + 4 * i);
+        }
       }
       __syncthreads();
       // l_3 <- C3 x_1 M^T (tiles j)
@@ -1545,13 +1577,7 @@ __global__ __launch_bounds__(256, 2) void k_adj(AdjSeq s) {
       __syncthreads();
       if (tid < 16) L1[tid] += cur.r1;
       if constexpr (N >= 2) L2[ri * RP + rj] += cur.r2;
-      if constexpr (N >= 3) {
-#pragma unroll
-        for (int i = 0; i < 16; ++i) {
-          const int e = tid + 256 * i;
-          L3[(e >> 8) * SP + ((e >> 4) & 15) * RP + (e & 15)] += cur.r3[i];
-        }
-      }
+      if constexpr (N >= 3) add_row16(L3 + (tid >> 4) * SP + (tid & 15) * RP, cur.r3);
     }
     __syncthreads();
     cur = nxt;
