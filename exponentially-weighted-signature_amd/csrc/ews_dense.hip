@@ -971,6 +971,12 @@ __device__ __forceinline__ void put(const Seq& s, float* orow, int N, int e, flo
   }
 }
 
+// x through an empty asm statement in a vector register: the compiler can neither fold it nor hoist what is
+// computed from it out of the enclosing loop
+__device__ __forceinline__ int opaque_vgpr(int x) {
+  asm volatile("" : "+v"(x));
+  return x;
+}
 // Operands of one step: the flow as the lane's M[l%16][4g..4g+3], level-1/2 local terms, and the lane's
 // level-3 local terms of the output tiles of this wave (j = 4w + jj).
 template <int N> struct StepIn {
@@ -1194,12 +1200,6 @@ __device__ __forceinline__ float adj_g(const AdjSeq& s, int b, int t, int e, int
 // (tid < 16) and level-2 entry tid, the row added this step (entries tid, 16 + tid and the sixteen level-3 entries
 // 272 + 16 tid + i: the readout cotangent g_t, or for CARRY the chunk's local part), and for EMIT the state before
 // the step (levels 1-2).
-// x through an empty asm statement in a vector register: the compiler can neither fold it nor hoist what is
-// computed from it out of the enclosing loop
-__device__ __forceinline__ int opaque_vgpr(int x) {
-  asm volatile("" : "+v"(x));
-  return x;
-}
 // LDS row of 16 floats (16-byte aligned) += v
 __device__ __forceinline__ void add_row16(float* row, const float* v) {
 #pragma unroll
@@ -1361,8 +1361,7 @@ __global__ __launch_bounds__(256, 2) void k_adj(AdjSeq s) {
 #pragma unroll
       for (int q = 0; q < 16; ++q) s3t[q] = s3g ? pt[(q >> 2) * 16 + 4 * (q & 3)] : 0.0f;
     }
-    // the next step's inputs (EMIT at depth 3: after the T contractions, where the S3 operands are dead)
-    if (!(EMIT && N >= 3) && k > 0) adj_load<N, MODE>(s, b, t - 1, tid, nxt);
+    if (k > 0) adj_load<N, MODE>(s, b, t - 1, tid, nxt);  // the next step's inputs
     __syncthreads();
     const f4 M4 = *reinterpret_cast<const f4*>(Ms + c16 * 16 + 4 * g);  // M[c16][4g + r]
     f4 MT4;                                                                // M^T[c16][4g + r]
@@ -1518,7 +1517,6 @@ __global__ __launch_bounds__(256, 2) void k_adj(AdjSeq s) {
         }
 #pragma unroll
         for (int r = 0; r < 4; ++r) Tw[w][(4 * g + r) * 16 + c16] = tacc[r];
-        if (k > 0) adj_load<N, MODE>(s, b, t - 1, tid, nxt);
         // ds3 = l_3 (the step's cotangent of its level-3 local term); L3 is rewritten after the next barrier
         {
           const float* src = L3 + (tid >> 4) * SP + (tid & 15) * RP;
