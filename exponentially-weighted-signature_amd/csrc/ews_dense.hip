@@ -1792,7 +1792,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(EXACTF ? 3 
                                                                             : (N >= 3 ? 256 * LP : 0);
   __shared__ __align__(16) float UN[UNF];
   constexpr int TPT = QMAX + 4;  // row pitch of the transposed letters (QMAX + 1 columns)
-  __shared__ __align__(16) float dS2[16 * LP], F[16 * LP], F2[16 * LP], Gm[256];
+  // F and F2 are double-buffered over the degree loop (degree NN uses half NN % 2), so that one barrier per degree
+  // orders both the writes and the MFMA reads
+  __shared__ __align__(16) float dS2[16 * LP], F[2 * 16 * LP], F2[2 * 16 * LP], Gm[256];
   __shared__ __align__(16) float LtT[N >= 3 ? 16 * TPT : 1];
   __shared__ float2 s_lc[PM];  // the letter coefficients of a stage and their h-derivatives
   __shared__ float dS1[16], red[8];
@@ -1840,7 +1842,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(EXACTF ? 3 
   if constexpr (N >= 3) {
     if (blockIdx.x < total) prefetch(blockIdx.x);
   }
+  const int tid_all = tid;
   for (long it = blockIdx.x; it < total; it += gridDim.x) {
+    // lane indices from an opaque copy of the thread index: the interval's addresses are recomputed, not held live
+    const int tid = opaque_vgpr(tid_all), i = tid >> 4, j = tid & 15, l = tid & 63;
     const int b = (int)(it / a.n_int), t = (int)(it - (long)b * a.n_int);
     const float* th = a.clock + (size_t)b * a.L;
     const float h = th[t + 1] - th[t];
