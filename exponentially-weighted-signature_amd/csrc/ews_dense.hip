@@ -2117,10 +2117,23 @@ __global__ __launch_bounds__(256) void k_vl_bwd(Args a, LeafBwd o) {
   constexpr int LW = lw_of(N);
   __shared__ __align__(16) float sp[HP][256];
   __shared__ __align__(16) float Pm[256], Vm[256], W1[256], W2[256], W3[256 + 32], GPm[256], GVm[256], Gm[256];
-  __shared__ __align__(16) float Dl[VMAX][16], Rs[VMAX][16], Ys[VMAX][16], Xs[VMAX][16];
-  __shared__ __align__(16) float dD[VMAX][16], dP[VMAX][16], dR[VMAX][16];
-  __shared__ __align__(16) float dS3[N >= 3 ? 4096 : 4], dS2[256];
-  __shared__ __align__(16) float Esq[SQMAX][256], Fsq[SQMAX][256];
+  // The knot arrays and dS3 are dead once the chain has run; the squarings of the step-matrix and flow adjoints
+  // (Esq, Fsq) then reuse their space, which keeps the workgroup at two per CU.
+  constexpr int UL = 7 * VMAX * 16 + (N >= 3 ? 4096 : 4), UE = 2 * SQMAX * 256;
+  __shared__ __align__(16) float U[UL > UE ? UL : UE];
+  __shared__ __align__(16) float dS2[256];
+  typedef float Row16[16];
+  typedef float Mat[256];
+  Row16* Dl = reinterpret_cast<Row16*>(U);
+  Row16* Rs = Dl + VMAX;
+  Row16* Ys = Rs + VMAX;
+  Row16* Xs = Ys + VMAX;
+  Row16* dD = Xs + VMAX;
+  Row16* dP = dD + VMAX;
+  Row16* dR = dP + VMAX;
+  float* dS3 = U + 7 * VMAX * 16;
+  Mat* Esq = reinterpret_cast<Mat*>(U);
+  Mat* Fsq = Esq + SQMAX;
   __shared__ __align__(16) float dS1[16], wv[16], lam[16], red[8];
   // depth 3: per-wavefront partial sums of each segment's column cotangents (double-buffered by segment parity),
   // summed in a fixed order
