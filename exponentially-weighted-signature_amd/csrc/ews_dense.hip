@@ -1792,9 +1792,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(EXACTF ? 3 
                                                                             : (N >= 3 ? 256 * LP : 0);
   __shared__ __align__(16) float UN[UNF];
   constexpr int TPT = QMAX + 4;  // row pitch of the transposed letters (QMAX + 1 columns)
-  // F and F2 are double-buffered over the degree loop (degree NN uses half NN % 2), so that one barrier per degree
-  // orders both the writes and the MFMA reads
-  __shared__ __align__(16) float dS2[16 * LP], F[2 * 16 * LP], F2[2 * 16 * LP], Gm[256];
+  __shared__ __align__(16) float dS2[16 * LP], Gm[256];
   __shared__ __align__(16) float LtT[N >= 3 ? 16 * TPT : 1];
   __shared__ float2 s_lc[PM];  // the letter coefficients of a stage and their h-derivatives
   __shared__ float dS1[16], red[8];
@@ -1943,40 +1941,38 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(EXACTF ? 3 
         const int n = e >> 4, r = e & 15;
         LtT[r * TPT + n] = Lt[n][r];
       }
-      // this thread's fibres of ds3 through (i, j), read once: ds3[k][i][j] and ds3[i][j][k] over k
-      float d3c[16], d3r[16];
-#pragma unroll
-      for (int k = 0; k < 16; ++k) {
-        d3c[k] = dS3[(16 * k + i) * LP + j];
-        d3r[k] = dS3[tid * LP + k];
-      }
-      const float ds2ij = dS2[i * LP + j];
+      __syncthreads();  // LtT
+      // Each of the three wavefronts forms the A operand of its own pair sum for every degree in registers, from
+      // the lane's 64 entries of ds3 read once (no LDS round trip and no barrier per degree):
+      //   wavefront 0: F[li][k] = ds2[li][k] + sum_c bt3_NN[c] ds3[c][li][k]   (k = 4 ks + lk)
+      //   wavefront 1: F[k][li] = ds2[k][li] + sum_c bt3_NN[c] ds3[c][k][li]
+      //   wavefront 2: E[li][k] = sum_c ds3[li][k][c] g1_NN[c]
       const int wv = tid >> 6, li = l & 15, lk = l >> 4;
       f4 acc[3];
 #pragma unroll
       for (int tt = 0; tt < 3; ++tt) acc[tt] = f4{0.0f, 0.0f, 0.0f, 0.0f};
       const int ntile = (QN + 15) >> 4;  // column tiles of 16 (QN <= QMAX + 1 = 41: at most 3)
-      for (int NN = 0; NN <= q; ++NN) {
-        float* Fb = F;
-        float* F2b = F2;
-        {
-          float f = ds2ij, e2 = 0.0f;
+      if (wv < 3) {
+        float d3[4][16], d2[4];
 #pragma unroll
-          for (int k = 0; k < 16; ++k) {  // BT[NN] and G1[NN]: the same row for every lane
-            f = fmaf(BT[NN][k], d3c[k], f);
-            e2 = fmaf(d3r[k], G1[NN][k], e2);
-          }
-          Fb[i * LP + j] = f;
-          F2b[i * LP + j] = e2;
+        for (int ks = 0; ks < 4; ++ks) {
+          const int k = 4 * ks + lk;
+#pragma unroll
+          for (int c = 0; c < 16; ++c)
+            d3[ks][c] = wv == 0 ? dS3[(16 * c + li) * LP + k] : wv == 1 ? dS3[(16 * c + k) * LP + li]
+                                                                       : dS3[(16 * li + k) * LP + c];
+          d2[ks] = wv == 0 ? dS2[li * LP + k] : wv == 1 ? dS2[k * LP + li] : 0.0f;
         }
-        __syncthreads();
-        if (wv < 3) {
+        for (int NN = 0; NN <= q; ++NN) {
+          const float* vrow = wv == 2 ? G1[NN] : BT[NN];  // the same row for every lane
           const float inv2 = wv == 2 ? 1.0f : frcp(NN + 2);
           float av[4];
 #pragma unroll
-          for (int ks = 0; ks < 4; ++ks) {  // A[row li][k = 4 ks + lk]
-            const int k = 4 * ks + lk;
-            av[ks] = inv2 * (wv == 0 ? Fb[li * LP + k] : wv == 1 ? Fb[k * LP + li] : F2b[li * LP + k]);
+          for (int ks = 0; ks < 4; ++ks) {
+            float x = d2[ks];
+#pragma unroll
+            for (int c = 0; c < 16; ++c) x = fmaf(vrow[c], d3[ks][c], x);
+            av[ks] = inv2 * x;  // A[row li][k = 4 ks + lk]
           }
 #pragma unroll
           for (int tt = 0; tt < 3; ++tt) {
@@ -1992,7 +1988,6 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(EXACTF ? 3 
             }
           }
         }
-        __syncthreads();  // F and F2 are rewritten by the next degree
       }
       // accumulators: lane l holds rows 4 (l / 16) + r of column 16 tt + l % 16
       if (wv < 3) {
