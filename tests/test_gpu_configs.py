@@ -9,7 +9,12 @@
 * c4: B = 2 of 256 at L = 512, d = 32 real diagonal at unit clock steps, EWS rows and the LogEWS
   readout, forward and gradients, against the float64 torch oracle.
 
-Inputs are the bench's own recipes (bench.py c1_inputs / c4_inputs / c5_inputs). Bars (BASELINE.json north
+* c3: the whole batch B = 16 at L = 4,096, dense d = 16 generator, depth 3, input-dependent clock,
+  forward with the series leaf (q = 24, the bench's) and with the Van Loan leaf (M = 20, cayley: the reference's
+  default) on four samples; gradients of path, clock and A (series leaf) on one sample at the full L, against the
+  float64 torch oracle and its autograd.
+
+Inputs are the bench's own recipes (bench.py c1_inputs / c3_inputs / c4_inputs / c5_inputs). Bars (BASELINE.json north
 star): forward max relative error <= 1e-5, gradients <= 1e-4, metric max|a-b| / max|b|.
 """
 
@@ -136,4 +141,36 @@ def test_c4_block_shape_with_log():
     (lref * w).sum().backward()
     errs = (relerr(p.grad, pr.grad), relerr(c.grad, cr.grad), relerr(lg.grad, lr.grad))
     print(f"c4 block shape: gradient relerrs {errs}", flush=True)
+    assert max(errs) < 1e-4, errs
+
+
+def test_c3_exact_shape():
+    path, clock, A = bench.c3_inputs()
+    B, L, d = path.shape
+    assert (B, L, d) == (16, 4096, 16)
+    tp, tc, tA = (torch.tensor(x, device=DEV) for x in (path, clock, A))
+    p64, c64, A64 = (torch.tensor(x, dtype=torch.float64) for x in (path, clock, A))
+    out = ops.dense_scan(tp, tc, tA, 3, 24)
+    ref = O.ews(p64, c64, A64, 3, "prefix", leaf="series", series_q=24)
+    e = relerr(out, ref)
+    print(f"c3 exact shape, series leaf q=24: forward relerr {e:.2e}", flush=True)
+    assert e < 1e-5, e
+    del out, ref
+    vl = ops.DenseLeaf("van_loan", 0, M=20, van_loan_expm="cayley")
+    out = ops.dense_scan(tp[:4], tc[:4], tA, 3, 0, leaf=vl)
+    ref = O.ews(p64[:4], c64[:4], A64, 3, "prefix", leaf="van_loan", M=20, van_loan_expm="cayley")
+    e = relerr(out, ref)
+    print(f"c3 exact shape, Van Loan leaf M=20: forward relerr {e:.2e}", flush=True)
+    assert e < 1e-5, e
+    del out, ref
+    # gradients of one sample at the full length (series leaf)
+    pr, cr, Ar = (x.clone().requires_grad_(True) for x in (p64[:1], c64[:1], A64))
+    r1 = O.ews(pr, cr, Ar, 3, "prefix", leaf="series", series_q=24)
+    w = torch.tensor(np.random.default_rng(3).normal(size=tuple(r1.shape)))
+    ref_g = torch.autograd.grad(r1, (pr, cr, Ar), w)
+    pg, cg, Ag = (x.clone().requires_grad_(True) for x in (tp[:1], tc[:1], tA))
+    o1 = ops.dense_scan(pg, cg, Ag, 3, 24)
+    got = torch.autograd.grad(o1, (pg, cg, Ag), w.to(DEV, torch.float32))
+    errs = tuple(relerr(g, r) for g, r in zip(got, ref_g))
+    print(f"c3 exact shape: gradient relerrs (path, clock, A) {errs}", flush=True)
     assert max(errs) < 1e-4, errs
