@@ -1976,7 +1976,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(EXACTF ? 3 
           }
 #pragma unroll
           for (int tt = 0; tt < 3; ++tt) {
-            if (tt < ntile) {
+            // a tile of columns 16 tt .. 16 tt + 15 holds a valid letter index only if 16 tt <= NN (db, dg1: NN - col
+            // >= 0) or 16 tt + 15 >= NN (dbt3: col - NN >= 0); the others add exact zeros and are skipped
+            if (tt < ntile && (wv == 2 ? 16 * tt + 15 >= NN : 16 * tt <= NN)) {
               const int col = 16 * tt + li;  // p (db), n (dg1) or s (dbt3)
               // letter index of column col: NN - col (db: g1, dg1: b) or col - NN (dbt3: b), zero outside [0, q]
               const int src = wv == 2 ? col - NN : NN - col;
