@@ -68,6 +68,10 @@ struct Args {
   float* car;   // (B, C + 1, LW) state before chunk c (row C: terminal state)
   float* pre;   // (B, n_int, W) prefix rows (mean / max readouts)
   float* mats;  // (B, 3, 256) per-sample Van Loan step matrices P, V and the shared flow (uniform modes)
+  // blocked carry scan: block summaries (B, NBc, LW), their flow products (B, NBc, 256), block carries (B, NBc + 1, LW)
+  float* bsumm;
+  float* bsfl;
+  float* bcar;
   float* out;
   // backward: the adjoint scan's per-chunk local cotangents (B, C, LW), carries (B, C + 1, LW), max argmax (B, LW)
   float* lloc;
@@ -2832,9 +2836,13 @@ using namespace ews::dense;
 
 size_t al256(size_t x) { return (x + 255) & ~(size_t)255; }
 
+// The forward's carry scan over the chunk summaries runs in blocks of kCarryBlock chunks when there are at least
+// two blocks (NBc of them): block summaries, a scan over the blocks, then each block from its carry.
+constexpr int kCarryBlock = 8;
 struct DPlan {
   int B, L, n_int, d, N, q, QB, T, C, LW, D, W, npow;
   int leaf, vm, vl_expm, vl_mode, chen_expm;
+  int NBc;  // carry-scan blocks per sample (0: one pass over the chunk summaries)
 };
 
 int dense_plan(const ews_dense_desc* s, DPlan& p) {
@@ -2869,6 +2877,7 @@ int dense_plan(const ews_dense_desc* s, DPlan& p) {
        : p.q <= 32 ? 32 : 40;
   p.T = s->chunk ? s->chunk : 64;
   p.C = (p.n_int + p.T - 1) / p.T;
+  p.NBc = p.C >= 2 * kCarryBlock ? (p.C + kCarryBlock - 1) / kCarryBlock : 0;
   p.LW = lw_of(p.N);
   p.D = 0;
   for (int k = 1, m = 1; k <= p.N; ++k) {
@@ -2883,7 +2892,8 @@ int dense_plan(const ews_dense_desc* s, DPlan& p) {
 constexpr int kLeafBwdBlocks = 1024;  // workgroups of the leaf adjoint (one partial dA set each)
 
 struct DWs {
-  size_t apow, loc, fl, summ, sfl, car, pre, mats, lloc, lam, amax, dv, dh, dsh, dshi, part, hsum, vlsave;
+  size_t apow, loc, fl, summ, sfl, car, pre, mats, bsumm, bsfl, bcar, lloc, lam, amax, dv, dh, dsh, dshi, part, hsum,
+      vlsave;
   size_t bsdv, bsdh, bspart, total;  // block-series level 1: per-interval dv / dh and the workgroups' dA sums
 };
 // bwd: the backward's layout, the forward's buffers (prefix rows always) followed by the adjoint scan's
@@ -2901,6 +2911,9 @@ DWs dense_ws(const DPlan& p, int readout, bool bwd = false) {
   off += bwd ? al256(BN * p.LW * 4)
              : (readout == EWS_READOUT_MEAN || readout == EWS_READOUT_MAX) ? al256(BN * p.W * 4) : 0;
   w.mats = off; off += al256((size_t)p.B * 768 * 4);
+  w.bsumm = off; off += al256((size_t)p.B * p.NBc * p.LW * 4);
+  w.bsfl = off; off += al256((size_t)p.B * p.NBc * 256 * 4);
+  w.bcar = off; off += p.NBc ? al256((size_t)p.B * (p.NBc + 1) * p.LW * 4) : 0;
   if (bwd) {
     w.lloc = off; off += al256(BC * p.LW * 4);
     w.lam = off; off += al256((size_t)p.B * (p.C + 1) * p.LW * 4);
@@ -2934,6 +2947,7 @@ Args dense_args(const ews_dense_desc* s, const DPlan& p, const float* path, cons
   a.apow = (float*)(ws + w.apow); a.loc = (float*)(ws + w.loc); a.fl = (float*)(ws + w.fl);
   a.summ = (float*)(ws + w.summ); a.sfl = (float*)(ws + w.sfl); a.car = (float*)(ws + w.car);
   a.pre = (float*)(ws + w.pre); a.mats = (float*)(ws + w.mats);
+  a.bsumm = (float*)(ws + w.bsumm); a.bsfl = (float*)(ws + w.bsfl); a.bcar = (float*)(ws + w.bcar);
   if (bwd) {
     a.lloc = (float*)(ws + w.lloc); a.lam = (float*)(ws + w.lam); a.amax = (int*)(ws + w.amax);
     a.vlsave = p.leaf == EWS_LEAF_VAN_LOAN ? (float*)(ws + w.vlsave) : nullptr;
@@ -3005,6 +3019,28 @@ int dense_combine_pass(const ews_dense_desc* s, const DPlan& p, const Args& a, h
     case 2: {
       hipLaunchKernelGGL(k_zero_rows, dim3(1, p.B), dim3(256), 0, st, a.car, (long)(p.C + 1) * p.LW, p.B, p.LW);
       DENSE_CHECK();
+      if (p.NBc) {  // blocks of kCarryBlock chunks: a chain of 3 kCarryBlock-ish steps instead of C
+        const int G = kCarryBlock, NB = p.NBc;
+        Seq q1{};  // block summaries: the SUMMARY scan over the chunk summaries
+        q1.lv = a.summ; q1.lv_bs = (long)p.C * p.LW; q1.fl = a.sfl; q1.fl_bs = (long)p.C * 256;
+        q1.n = p.C; q1.T = G; q1.summ = a.bsumm; q1.sfl = a.bsfl; q1.C = NB; q1.d = p.d;
+        int rc = launch_scan<true>(p.N, q1, dim3(NB, p.B), st);
+        if (rc != EWS_OK) return rc;
+        hipLaunchKernelGGL(k_zero_rows, dim3(1, p.B), dim3(256), 0, st, a.bcar, (long)(NB + 1) * p.LW, p.B, p.LW);
+        DENSE_CHECK();
+        Seq q2{};  // block carries: one pass over the block summaries of each sample
+        q2.lv = a.bsumm; q2.lv_bs = (long)NB * p.LW; q2.fl = a.bsfl; q2.fl_bs = (long)NB * 256;
+        q2.n = NB; q2.T = NB; q2.rows = a.bcar + p.LW; q2.rows_bs = (long)(NB + 1) * p.LW; q2.rows_ld = p.LW;
+        q2.padded = 1; q2.lvl0 = 0; q2.d = p.d; q2.C = 1;
+        rc = launch_scan<false>(p.N, q2, dim3(1, p.B), st);
+        if (rc != EWS_OK) return rc;
+        Seq q3{};  // chunk carries: each block from its carry
+        q3.lv = a.summ; q3.lv_bs = (long)p.C * p.LW; q3.fl = a.sfl; q3.fl_bs = (long)p.C * 256;
+        q3.n = p.C; q3.T = G; q3.init = a.bcar; q3.init_bs = (long)(NB + 1) * p.LW;
+        q3.rows = a.car + p.LW; q3.rows_bs = (long)(p.C + 1) * p.LW; q3.rows_ld = p.LW;
+        q3.padded = 1; q3.lvl0 = 0; q3.d = p.d; q3.C = NB;
+        return launch_scan<false>(p.N, q3, dim3(NB, p.B), st);
+      }
       Seq q{};
       q.lv = a.summ; q.lv_bs = (long)p.C * p.LW; q.fl = a.sfl; q.fl_bs = (long)p.C * 256;
       q.n = p.C; q.T = p.C; q.rows = a.car + p.LW; q.rows_bs = (long)(p.C + 1) * p.LW; q.rows_ld = p.LW;
