@@ -76,6 +76,8 @@ struct Args {
   // backward: the adjoint scan's per-chunk local cotangents (B, C, LW), carries (B, C + 1, LW), max argmax (B, LW)
   float* lloc;
   float* lam;
+  float* bagg;  // blocked adjoint carry scan: block local aggregates (B, NBc, LW), block-end cotangents (B, NBc + 1, LW)
+  float* bl;
   int* amax;
   float* vlsave;  // backward's recompute: per interval the Van Loan P, V and knot increments (null otherwise)
 };
@@ -1182,9 +1184,15 @@ struct AdjSeq {
   const float* g;
   const int* amax;
   float gscale;
-  const float* init;  // EMIT: Lambda rows (B, C + 1, LW), chunk c starts from row c + 1; CARRY: row C on entry
-  float* lam;         // LOCAL: (B, C, LW) outputs; CARRY: (B, C + 1, LW) outputs (rows 1..C)
-  const float* lloc;  // CARRY: the LOCAL outputs
+  const float* init;  // EMIT: Lambda rows (B, C + 1, LW), chunk c starts from row c + 1
+  float* lam;         // LOCAL: (B, C, LW) outputs
+  const float* lloc;  // CARRY: the local parts, row t at lloc + b * lloc_bs + t * LW
+  // CARRY: workgroup c takes rows [c T, min(c T + T, n)) in reverse, from the row init + b * init_bs +
+  // (c + init_off) * LW (zero when init is null); before row t it writes lambda to row t + 1 of lam (lam_bs per
+  // sample) when lam is set and t + 1 < lam_lim, and at the end the workgroup's lambda to row c of agg (agg_bs)
+  long init_bs, lloc_bs, lam_bs, agg_bs;
+  int init_off, lam_lim;
+  float* agg;
   const float* st;    // EMIT: the states S_t, padded rows (B, n, LW)
   float* dlv;         // EMIT: ds_t (padded, in place of lv)
   float* dfl;         // EMIT: dM_t (in place of fl)
@@ -1231,7 +1239,7 @@ __device__ __forceinline__ void adj_load(const AdjSeq& s, int b, int t, int tid,
 #pragma unroll
   for (int i = 0; i < (N >= 3 ? 16 : 1); ++i) x.r3[i] = 0.0f;
   if constexpr (MODE == ADJ_CARRY) {
-    const float* lo = s.lloc + ((long)b * s.C + t) * LW;
+    const float* lo = s.lloc + b * s.lloc_bs + (long)t * LW;
     if (tid < 16) x.r1 = lo[tid];
     if constexpr (N >= 2) x.r2 = lo[16 + tid];
     if constexpr (N >= 3) {
@@ -1278,21 +1286,12 @@ __global__ __launch_bounds__(256, 2) void k_adj(AdjSeq s) {
   const int tid = threadIdx.x, w = tid >> 6, l = tid & 63, g = l >> 4, c16 = l & 15;
   const int ri = tid >> 4, rj = tid & 15;  // (row, column) of the 16 x 16 VALU work
   const int b = blockIdx.y;
-  int c, t0, Tc;
-  if constexpr (MODE == ADJ_CARRY) {
-    c = 0;
-    t0 = 0;
-    Tc = s.C;
-  } else {
-    c = blockIdx.x;
-    t0 = c * s.T;
-    Tc = min(s.T, s.n - t0);
-  }
+  const int c = blockIdx.x, t0 = c * s.T, Tc = min(s.T, s.n - t0);
   // initial lambda
   {
     const float* ini = nullptr;
     if constexpr (MODE == ADJ_EMIT) ini = s.init + ((long)b * (s.C + 1) + c + 1) * LW;
-    if constexpr (MODE == ADJ_CARRY) ini = s.init + ((long)b * (s.C + 1) + s.C) * LW;
+    if constexpr (MODE == ADJ_CARRY) ini = s.init ? s.init + b * s.init_bs + (long)(c + s.init_off) * LW : nullptr;
     if (tid < 16) L1[tid] = ini ? ini[tid] : 0.0f;
     if constexpr (N >= 2) L2[ri * RP + rj] = ini ? ini[16 + tid] : 0.0f;
     if constexpr (N >= 3) {
@@ -1315,8 +1314,8 @@ __global__ __launch_bounds__(256, 2) void k_adj(AdjSeq s) {
     const int ri = tid >> 4, rj = tid & 15;
     (void)l;
     if constexpr (MODE == ADJ_CARRY) {  // Lambda_{t+1} is the current lambda
-      float* o = s.lam + ((long)b * (s.C + 1) + t + 1) * LW;
-      if (t + 1 < s.C) {
+      float* o = s.lam + b * s.lam_bs + (long)(t + 1) * LW;
+      if (s.lam && t + 1 < s.lam_lim) {
         if (tid < 16) o[tid] = L1[tid];
         if constexpr (N >= 2) o[16 + tid] = L2[ri * RP + rj];
         if constexpr (N >= 3) {
@@ -1584,8 +1583,8 @@ __global__ __launch_bounds__(256, 2) void k_adj(AdjSeq s) {
     __syncthreads();
     cur = nxt;
   }
-  if constexpr (MODE == ADJ_LOCAL) {
-    float* o = s.lam + ((long)b * s.C + c) * LW;
+  if (MODE == ADJ_LOCAL || (MODE == ADJ_CARRY && s.agg)) {
+    float* o = MODE == ADJ_LOCAL ? s.lam + ((long)b * s.C + c) * LW : s.agg + b * s.agg_bs + (long)c * LW;
     if (tid < 16) o[tid] = L1[tid];
     if constexpr (N >= 2) o[16 + tid] = L2[ri * RP + rj];
     if constexpr (N >= 3) {
@@ -2892,8 +2891,8 @@ int dense_plan(const ews_dense_desc* s, DPlan& p) {
 constexpr int kLeafBwdBlocks = 1024;  // workgroups of the leaf adjoint (one partial dA set each)
 
 struct DWs {
-  size_t apow, loc, fl, summ, sfl, car, pre, mats, bsumm, bsfl, bcar, lloc, lam, amax, dv, dh, dsh, dshi, part, hsum,
-      vlsave;
+  size_t apow, loc, fl, summ, sfl, car, pre, mats, bsumm, bsfl, bcar, lloc, lam, bagg, bl, amax, dv, dh, dsh, dshi,
+      part, hsum, vlsave;
   size_t bsdv, bsdh, bspart, total;  // block-series level 1: per-interval dv / dh and the workgroups' dA sums
 };
 // bwd: the backward's layout, the forward's buffers (prefix rows always) followed by the adjoint scan's
@@ -2917,6 +2916,8 @@ DWs dense_ws(const DPlan& p, int readout, bool bwd = false) {
   if (bwd) {
     w.lloc = off; off += al256(BC * p.LW * 4);
     w.lam = off; off += al256((size_t)p.B * (p.C + 1) * p.LW * 4);
+    w.bagg = off; off += al256((size_t)p.B * p.NBc * p.LW * 4);
+    w.bl = off; off += p.NBc ? al256((size_t)p.B * (p.NBc + 1) * p.LW * 4) : 0;
     w.amax = off; off += al256((size_t)p.B * p.LW * 4);
     w.dv = off; off += al256(BN * 16 * 4);
     w.dh = off; off += al256(BN * 4);
@@ -2950,6 +2951,7 @@ Args dense_args(const ews_dense_desc* s, const DPlan& p, const float* path, cons
   a.bsumm = (float*)(ws + w.bsumm); a.bsfl = (float*)(ws + w.bsfl); a.bcar = (float*)(ws + w.bcar);
   if (bwd) {
     a.lloc = (float*)(ws + w.lloc); a.lam = (float*)(ws + w.lam); a.amax = (int*)(ws + w.amax);
+    a.bagg = (float*)(ws + w.bagg); a.bl = (float*)(ws + w.bl);
     a.vlsave = p.leaf == EWS_LEAF_VAN_LOAN ? (float*)(ws + w.vlsave) : nullptr;
   }
   return a;
@@ -3177,13 +3179,36 @@ int dense_adjoint(const ews_dense_desc* s, const DPlan& p, const Args& a, const 
     const int rc = launch_adj<ADJ_LOCAL>(p.N, ql, dim3(p.C, p.B), st);
     if (rc != EWS_OK) return rc;
   }
-  {  // CARRY over the chunk summaries
+  {  // CARRY over the chunk summaries: Lambda_c = local_c + R(chunk c)^T Lambda_{c+1}, rows 1 .. C-1 of lam
     AdjSeq qc = q;
     qc.gmode = G_NONE;
     qc.lv = a.summ; qc.lv_bs = (long)p.C * p.LW; qc.fl = a.sfl; qc.fl_bs = (long)p.C * 256;
-    qc.init = a.lam; qc.lam = a.lam; qc.lloc = a.lloc;
-    const int rc = launch_adj<ADJ_CARRY>(p.N, qc, dim3(1, p.B), st);
-    if (rc != EWS_OK) return rc;
+    qc.lloc = a.lloc; qc.lloc_bs = (long)p.C * p.LW;
+    qc.n = p.C;
+    if (p.NBc) {  // in the forward's blocks of kCarryBlock chunks, over its block summaries
+      const int G = kCarryBlock, NB = p.NBc;
+      AdjSeq q1 = qc;  // each block's local aggregate from a zero cotangent at its end
+      q1.T = G; q1.init = nullptr; q1.lam = nullptr; q1.agg = a.bagg; q1.agg_bs = (long)NB * p.LW;
+      int rc = launch_adj<ADJ_CARRY>(p.N, q1, dim3(NB, p.B), st);
+      if (rc != EWS_OK) return rc;
+      AdjSeq q2 = qc;  // the cotangent at every block end: over the block summaries from the terminal one
+      q2.lv = a.bsumm; q2.lv_bs = (long)NB * p.LW; q2.fl = a.bsfl; q2.fl_bs = (long)NB * 256;
+      q2.lloc = a.bagg; q2.lloc_bs = (long)NB * p.LW; q2.n = NB; q2.T = NB;
+      q2.init = a.lam; q2.init_bs = (long)(p.C + 1) * p.LW; q2.init_off = p.C;
+      q2.lam = a.bl; q2.lam_bs = (long)(NB + 1) * p.LW; q2.lam_lim = NB + 1;
+      rc = launch_adj<ADJ_CARRY>(p.N, q2, dim3(1, p.B), st);
+      if (rc != EWS_OK) return rc;
+      AdjSeq q3 = qc;  // each block from the cotangent at its end: the chunk rows
+      q3.T = G; q3.init = a.bl; q3.init_bs = (long)(NB + 1) * p.LW; q3.init_off = 1;
+      q3.lam = a.lam; q3.lam_bs = (long)(p.C + 1) * p.LW; q3.lam_lim = p.C;
+      rc = launch_adj<ADJ_CARRY>(p.N, q3, dim3(NB, p.B), st);
+      if (rc != EWS_OK) return rc;
+    } else {
+      qc.T = p.C; qc.init = a.lam; qc.init_bs = (long)(p.C + 1) * p.LW; qc.init_off = p.C;
+      qc.lam = a.lam; qc.lam_bs = (long)(p.C + 1) * p.LW; qc.lam_lim = p.C;
+      const int rc = launch_adj<ADJ_CARRY>(p.N, qc, dim3(1, p.B), st);
+      if (rc != EWS_OK) return rc;
+    }
   }
   AdjSeq qe = q;
   qe.lv = a.loc; qe.lv_bs = (long)p.n_int * p.LW; qe.fl = a.fl; qe.fl_bs = (long)p.n_int * 256;
