@@ -357,12 +357,17 @@ __global__ __launch_bounds__(MAXT) void k_chunk_fwd(DiagArgs a) {
   float* s_h = s_v + a.T * a.d;
   const int c = blockIdx.x, b = blockIdx.y, tid = threadIdx.x;
   if (a.fast_ok && (a.cflag[b * a.C + c] & 1)) return;  // a pair-group kernel owns this chunk
+  // generic chunks: the first summary pass (FAST) classifies every chunk and writes its class (bit 0 uniform,
+  // bit 1 invertible); every later kernel reads it and leaves a chunk it does not own before staging anything
+  constexpr bool kClassify = MODE == MODE_SUMMARY && FAST;
+  if (!kClassify && !a.fast_ok && ((a.cflag[b * a.C + c] & 1) != 0) != FAST) return;
   const int t0 = c * a.T;
   const int Tc = min(a.T, a.n_int - t0);
   load_chunk(a, b, t0, Tc, s_v, s_h);
   __syncthreads();
   const LaneMap m = lane_map(a, tid);
   const ChunkClock cc = chunk_clock<T>(a, b, Tc, s_h);
+  if (kClassify && !a.fast_ok && tid == 0) a.cflag[b * a.C + c] = (cc.fast ? 1 : 0) | (cc.inv_ok ? 2 : 0);
   if (cc.fast != FAST) return;  // the other instantiation owns this chunk
   if (!m.active) return;
   T dummy{};
@@ -1071,6 +1076,7 @@ __global__ __launch_bounds__(MAXT) void k_chunk_bwd_local(DiagArgs a) {
   float* s_red = smem + Lo.g;
   const int c = blockIdx.x, b = blockIdx.y, tid = threadIdx.x;
   if (a.fast_ok && (a.cflag[b * a.C + c] & 1)) return;  // a pair-group kernel owns this chunk
+  if (!a.fast_ok && ((a.cflag[b * a.C + c] & 1) != 0) != FAST) return;  // the forward's chunk class
   const int t0 = c * a.T;
   const int Tc = min(a.T, a.n_int - t0);
   const bool prefix = a.readout == EWS_READOUT_PREFIX;
@@ -1449,6 +1455,13 @@ __device__ __forceinline__ void load_cot(const DiagArgs& a, const LaneMap& m, co
 #define EWS_BWD_PROLOGUE(OWNS, ROWS)                                                                              \
   const int tid = threadIdx.x;                                                                             \
   if (a.fast_ok && (a.cflag[b * a.C + c] & 3) == 3) return; /* a pair-group kernel owns this chunk */      \
+  if (!a.fast_ok) { /* the forward's chunk class: leave a chunk this kernel does not own before staging */ \
+    const int gf = a.cflag[b * a.C + c];                                                                   \
+    ChunkClock cc;                                                                                         \
+    cc.fast = (gf & 1) != 0;                                                                               \
+    cc.inv_ok = (gf & 2) != 0;                                                                             \
+    if (!(OWNS)) return;                                                                                   \
+  }                                                                                                        \
   const int t0 = c * a.T;                                                                                  \
   const int Tc = min(a.T, a.n_int - t0);                                                                   \
   const bool prefix = a.readout == EWS_READOUT_PREFIX;                                                     \
@@ -1660,13 +1673,15 @@ __device__ __forceinline__ void chunk_bwd_full(const DiagArgs& a, const int c, c
 }
 // Chunks blockIdx.x, blockIdx.x + gridDim.x, ... of sample blockIdx.y: with the pair kernels active the grid is
 // small (most chunks belong to them), otherwise one chunk per workgroup. The ownership flags of 64 candidate
-// chunks are read at once (one lane each) and only the chunks left to this kernel are visited.
+// chunks are read at once (one lane each: the pair kernels' flags, or the generic chunk class written by the first
+// summary pass) and only the chunks left to this kernel are visited.
 template <bool CPLX, int N, int MAXT, bool WAVE>
 __global__ __launch_bounds__(MAXT) void k_chunk_bwd_full(DiagArgs a) {
   const int b = blockIdx.y, lane = threadIdx.x & 63;
   for (int base = blockIdx.x; base < a.C; base += 64 * gridDim.x) {
     const int cl = base + gridDim.x * lane;
-    const bool need = cl < a.C && !(a.fast_ok && (a.cflag[b * a.C + cl] & 3) == 3);
+    // a pair-group kernel (fast_ok) or the inversion adjoint (generic class: uniform and invertible) owns the others
+    const bool need = cl < a.C && (a.cflag[b * a.C + cl] & 3) != 3;
     unsigned long long mask = __ballot(need);  // the same in every wavefront of the workgroup
     while (mask) {
       const int i = __ffsll((long long)mask) - 1;
