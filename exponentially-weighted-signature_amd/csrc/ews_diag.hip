@@ -680,7 +680,8 @@ __global__ __launch_bounds__(MAXT) void k_fwd_group(DiagArgs a) {
   if (!m.active) return;
   TD dummy{};
   TD S1{}, SA{}, SB{};
-  if (EXPAND) lane_summary_d<CPLX>(a, m, a.gcar + ((size_t)b * a.NG + g) * a.D, S1, dummy, SA, SB);
+  // the first group starts from the zero state (its carry is not read: with one group the scan is not launched)
+  if (EXPAND && g > 0) lane_summary_d<CPLX>(a, m, a.gcar + ((size_t)b * a.NG + g) * a.D, S1, dummy, SA, SB);
   for (int cc = 0; cc < nb; ++cc) {
     if (EXPAND) store_lane_d<CPLX, N>(a, m, a.carries + ((size_t)b * (a.C + 1) + c0 + cc) * a.D, S1, SA, SB);
     TD l1j, l1k, l2A, l2B;
@@ -802,7 +803,8 @@ __global__ __launch_bounds__(MAXT) void k_bwd_group(DiagArgs a) {
   }
   __syncthreads();
   TD X1{}, XA{}, XB{};
-  if (EXPAND) lane_summary_d<CPLX>(a, m, a.gcar + ((size_t)b * a.NG + g) * a.D, X1, dummy, XA, XB);
+  // the last group starts from a zero cotangent (its carry is not read: with one group the scan is not launched)
+  if (EXPAND && g < a.NG - 1) lane_summary_d<CPLX>(a, m, a.gcar + ((size_t)b * a.NG + g) * a.D, X1, dummy, XA, XB);
   for (int cc = nb - 1; cc >= 0; --cc) {
     const int c = c0 + cc;
     if (EXPAND) store_lane_f<CPLX, N>(a, m, a.mt + ((size_t)b * a.C + c) * a.D, X1, XA, XB);
@@ -2078,10 +2080,12 @@ int forward_pass(const ews_diag_desc* s, const Plan& p, DiagArgs a, hipStream_t 
       break;
     case 1:
       if (p.fast) return EWS_OK;
-      hipLaunchKernelGGL((k_fwd_group<CPLX, N, MAXT, false>), dim3(p.NG, p.B), blk, p.lds_carry, st, a);
-      EWS_LAUNCH_CHECK();
-      hipLaunchKernelGGL((k_fwd_group_scan<CPLX, N, MAXT>), dim3(p.B), blk, 0, st, a);
-      EWS_LAUNCH_CHECK();
+      if (p.NG > 1) {  // one group: its carry is the zero state, no group aggregates or group scan
+        hipLaunchKernelGGL((k_fwd_group<CPLX, N, MAXT, false>), dim3(p.NG, p.B), blk, p.lds_carry, st, a);
+        EWS_LAUNCH_CHECK();
+        hipLaunchKernelGGL((k_fwd_group_scan<CPLX, N, MAXT>), dim3(p.B), blk, 0, st, a);
+        EWS_LAUNCH_CHECK();
+      }
       hipLaunchKernelGGL((k_fwd_group<CPLX, N, MAXT, true>), dim3(p.NG, p.B), blk, p.lds_carry, st, a);
       break;
     case 2:
@@ -2145,11 +2149,13 @@ int backward_pass(const Plan& p, DiagArgs a, hipStream_t st, int pass) {
         if (pairs_carry_scan(a, st) != 0) return EWS_ERR_LAUNCH;
         break;
       }
-      hipLaunchKernelGGL((k_bwd_group<CPLX, N, (MAXT < 256 ? 256 : MAXT), false>), dim3(p.NG, p.B), dim3(p.NT),
-                         p.lds_adjoint, st, a);
-      EWS_LAUNCH_CHECK();
-      hipLaunchKernelGGL((k_bwd_group_scan<CPLX, N, (MAXT < 256 ? 256 : MAXT)>), dim3(p.B), dim3(p.NT), 0, st, a);
-      EWS_LAUNCH_CHECK();
+      if (p.NG > 1) {  // one group: its end cotangent is zero, no group aggregates or group scan
+        hipLaunchKernelGGL((k_bwd_group<CPLX, N, (MAXT < 256 ? 256 : MAXT), false>), dim3(p.NG, p.B), dim3(p.NT),
+                           p.lds_adjoint, st, a);
+        EWS_LAUNCH_CHECK();
+        hipLaunchKernelGGL((k_bwd_group_scan<CPLX, N, (MAXT < 256 ? 256 : MAXT)>), dim3(p.B), dim3(p.NT), 0, st, a);
+        EWS_LAUNCH_CHECK();
+      }
       hipLaunchKernelGGL((k_bwd_group<CPLX, N, (MAXT < 256 ? 256 : MAXT), true>), dim3(p.NG, p.B), dim3(p.NT),
                          p.lds_adjoint, st, a);
       break;
