@@ -1313,6 +1313,9 @@ __global__ __launch_bounds__(256, 2) void k_adj(AdjSeq s) {
     const int tid = opaque_vgpr(tid_all), w = tid >> 6, l = tid & 63, g = l >> 4, c16 = l & 15;
     const int ri = tid >> 4, rj = tid & 15;
     (void)l;
+    // CARRY stores a row every step: the next step's inputs are issued before it, since the memory counter is in
+    // order and a load issued after a store is waited for together with the store
+    if (MODE == ADJ_CARRY && k > 0) adj_load<N, MODE>(s, b, t - 1, tid, nxt);
     if constexpr (MODE == ADJ_CARRY) {  // Lambda_{t+1} is the current lambda
       float* o = s.lam + b * s.lam_bs + (long)(t + 1) * LW;
       if (s.lam && t + 1 < s.lam_lim) {
@@ -1364,7 +1367,7 @@ __global__ __launch_bounds__(256, 2) void k_adj(AdjSeq s) {
 #pragma unroll
       for (int q = 0; q < 16; ++q) s3t[q] = s3g ? pt[(q >> 2) * 16 + 4 * (q & 3)] : 0.0f;
     }
-    if (k > 0) adj_load<N, MODE>(s, b, t - 1, tid, nxt);  // the next step's inputs
+    if (MODE != ADJ_CARRY && k > 0) adj_load<N, MODE>(s, b, t - 1, tid, nxt);  // the next step's inputs
     __syncthreads();
     const f4 M4 = *reinterpret_cast<const f4*>(Ms + c16 * 16 + 4 * g);  // M[c16][4g + r]
     f4 MT4;                                                                // M^T[c16][4g + r]

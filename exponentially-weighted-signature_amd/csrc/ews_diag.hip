@@ -708,14 +708,26 @@ __global__ __launch_bounds__(MAXT) void k_fwd_group_scan(DiagArgs a) {
   if (!m.active) return;
   TD dummy{};
   const TD uj = load_ud(a.params, m.j, &dummy), uk = load_ud(a.params, m.k, &dummy);
-  TD S1{}, SA{}, SB{};
-  for (int g = 0; g < a.NG; ++g) {
-    store_lane_d<CPLX, N>(a, m, a.gcar + ((size_t)b * a.NG + g) * a.D, S1, SA, SB);
-    const int t0 = g * a.scan_cb * a.T, t1 = min(t0 + a.scan_cb * a.T, a.n_int);
-    const double tau = span_tau(a, b, t0, t1);
+  // group g's span and aggregate are loaded one group ahead and issued before the group's carry is stored (the
+  // memory counter is in order: a load issued after a store is waited for together with the store)
+  struct Pre {
+    double tau;
     TD l1j, l1k, l2A, l2B;
-    lane_summary_d<CPLX>(a, m, a.gagg + ((size_t)b * a.NG + g) * a.D, l1j, l1k, l2A, l2B);
-    chen_fwd_lane<CPLX, N>(S1, SA, SB, dexp(mul_s(uj, tau)), dexp(mul_s(uk, tau)), l1j, l1k, l2A, l2B);
+  };
+  auto load = [&](int g, Pre& p) {
+    const int t0 = g * a.scan_cb * a.T, t1 = min(t0 + a.scan_cb * a.T, a.n_int);
+    p.tau = span_tau(a, b, t0, t1);
+    lane_summary_d<CPLX>(a, m, a.gagg + ((size_t)b * a.NG + g) * a.D, p.l1j, p.l1k, p.l2A, p.l2B);
+  };
+  TD S1{}, SA{}, SB{};
+  Pre cur{}, nxt{};
+  if (a.NG > 0) load(0, cur);
+  for (int g = 0; g < a.NG; ++g) {
+    if (g + 1 < a.NG) load(g + 1, nxt);
+    store_lane_d<CPLX, N>(a, m, a.gcar + ((size_t)b * a.NG + g) * a.D, S1, SA, SB);
+    chen_fwd_lane<CPLX, N>(S1, SA, SB, dexp(mul_s(uj, cur.tau)), dexp(mul_s(uk, cur.tau)), cur.l1j, cur.l1k, cur.l2A,
+                           cur.l2B);
+    cur = nxt;
   }
 }
 
@@ -826,28 +838,50 @@ __global__ __launch_bounds__(MAXT) void k_bwd_group_scan(DiagArgs a) {
   const LaneMap m = lane_map(a, threadIdx.x);
   TD dummy{};
   const TD uj = load_ud(a.params, m.j, &dummy), uk = load_ud(a.params, m.k, &dummy);
-  TD X1{}, XA{}, XB{};
-  for (int g = a.NG - 1; g >= 0; --g) {
-    if (m.active) store_lane_d<CPLX, N>(a, m, a.gcar + ((size_t)b * a.NG + g) * a.D, X1, XA, XB);
+  // Group g's operands (its span, the level-1 carries at its ends, its aggregate) are loaded one group ahead and
+  // issued before the group's carry is stored: the memory counter is in order, so a load issued after a store could
+  // not be waited for without waiting for the store as well.
+  struct Pre {
+    double tau;
+    TD cek, csk, a1, aA, aB;
+  };
+  auto load = [&](int g, Pre& p) {
     const int c0 = g * a.scan_cb, c1 = min(c0 + a.scan_cb, a.C);
     const int t0 = c0 * a.T, t1 = min(c1 * a.T, a.n_int);
-    const double tau = span_tau(a, b, t0, t1);
-    const TD Fj = dexp(mul_s(uj, tau)), Fk = dexp(mul_s(uk, tau));
+    p.tau = span_tau(a, b, t0, t1);
     const double* cs = a.carries + ((size_t)b * (a.C + 1) + c0) * a.D;
     const double* ce = a.carries + ((size_t)b * (a.C + 1) + c1) * a.D;
-    const TD l1k = ldDD(ce + st1<CPLX>(m.k), &dummy) - Fk * ldDD(cs + st1<CPLX>(m.k), &dummy);
-    adj_lane<CPLX, N>(a, m, X1, XA, XB, Fj, Fk, l1k, s_red);
+    p.cek = ldDD(ce + st1<CPLX>(m.k), &dummy);
+    p.csk = ldDD(cs + st1<CPLX>(m.k), &dummy);
     const double* ag = a.gagg + ((size_t)b * a.NG + g) * a.D;
-    if (m.plane) X1 = X1 + ldDD(ag + st1<CPLX>(m.j), &dummy);
+    p.a1 = m.plane ? ldDD(ag + st1<CPLX>(m.j), &dummy) : TD{};
+    p.aA = TD{};
+    p.aB = TD{};
     if (N == 2 && m.active) {
       const double* p2 = ag + st2<CPLX>(a, m.j, m.k);
       if (CPLX) {
-        XA = XA + ldDD(p2, &dummy);
-        XB = XB + ldDD(p2 + 2, &dummy);
+        p.aA = ldDD(p2, &dummy);
+        p.aB = ldDD(p2 + 2, &dummy);
       } else {
-        XB = XB + ldDD(p2, &dummy);
+        p.aB = ldDD(p2, &dummy);
       }
     }
+  };
+  TD X1{}, XA{}, XB{};
+  Pre cur{}, nxt{};
+  if (a.NG > 0) load(a.NG - 1, cur);
+  for (int g = a.NG - 1; g >= 0; --g) {
+    if (g > 0) load(g - 1, nxt);
+    if (m.active) store_lane_d<CPLX, N>(a, m, a.gcar + ((size_t)b * a.NG + g) * a.D, X1, XA, XB);
+    const TD Fj = dexp(mul_s(uj, cur.tau)), Fk = dexp(mul_s(uk, cur.tau));
+    const TD l1k = cur.cek - Fk * cur.csk;
+    adj_lane<CPLX, N>(a, m, X1, XA, XB, Fj, Fk, l1k, s_red);
+    if (m.plane) X1 = X1 + cur.a1;
+    if (N == 2 && m.active) {
+      if (CPLX) XA = XA + cur.aA;
+      XB = XB + cur.aB;
+    }
+    cur = nxt;
   }
 }
 
