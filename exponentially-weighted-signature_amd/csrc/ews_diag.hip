@@ -2201,8 +2201,13 @@ int backward_pass(const Plan& p, DiagArgs a, hipStream_t st, int pass) {
         hipLaunchKernelGGL((k_chunk_bwd_inv<CPLX, N, MAXT, WAVE>), grid, blkb, p.lds_bwd_inv, st, a);
         EWS_LAUNCH_CHECK();
       }
-      hipLaunchKernelGGL((k_chunk_bwd_full<CPLX, N, MAXT, WAVE>), p.fast ? dim3(min(p.C, 8), p.B) : grid, blkb,
-                         p.lds_bwd_full, st, a);
+      {
+        // the recomputing adjoint's LDS leaves about one workgroup per CU, so up to eight chunks per workgroup
+        // (strided, visited only when owned) cost no parallelism while 512 or more workgroups remain, and spare
+        // the launch most of its exiting workgroups when the other kernels own the chunks
+        const int gx = p.fast ? min(p.C, 8) : min(p.C, max((p.C + 7) / 8, (512 + p.B - 1) / p.B));
+        hipLaunchKernelGGL((k_chunk_bwd_full<CPLX, N, MAXT, WAVE>), dim3(gx, p.B), blkb, p.lds_bwd_full, st, a);
+      }
       break;
     case 3:
       hipLaunchKernelGGL(k_knot_grads, dim3(p.C + 1, p.B), dim3(64), 0, st, a);
