@@ -991,7 +991,8 @@ __device__ __forceinline__ void gamma_row(const DiagArgs& a, const LaneMap& m, c
 // registers while the current one is processed, so no global load sits on the sequential dependency chain.
 constexpr int kBLK = 8;   // checkpoint block and cotangent staging rows of the exact-coefficient adjoint (the
                           // plan halves it for wide states, whose checkpoints would not fit the LDS)
-constexpr int kGB = 4;    // cotangent staging rows of the local and inversion adjoints
+constexpr int kGB = 4;    // cotangent staging rows of the inversion adjoint
+constexpr int kGBL = 2;   // and of the chunk-local adjoint (two rows suit it, four the inversion adjoint)
 // Asynchronous copy of n contiguous floats into LDS (global_load_lds: each lane's dword lands at the wave's
 // LDS base + 4 * lane); completion is awaited with lds_dma_wait() before a barrier.
 typedef __attribute__((address_space(3))) void lds_void_t;
@@ -1103,7 +1104,7 @@ __global__ __launch_bounds__(MAXT) void k_chunk_bwd_local(DiagArgs a) {
   using T = typename Types<CPLX>::T;
   extern __shared__ float smem[];
   const int NT = blockDim.x;
-  const BwdLds Lo = bwd_lds_layout(a.T, a.d, a.W, NT, 0, WAVE, false, kGB);
+  const BwdLds Lo = bwd_lds_layout(a.T, a.d, a.W, NT, 0, WAVE, false, kGBL);
   float* s_v = smem + Lo.v;
   float* s_h = smem + Lo.h;
   float* s_gb = smem + Lo.gb;
@@ -1122,9 +1123,9 @@ __global__ __launch_bounds__(MAXT) void k_chunk_bwd_local(DiagArgs a) {
   if (cc.fast != FAST) return;  // the other instantiation owns this chunk
   load_chunk(a, b, t0, Tc, s_v, s_h);
   if (!prefix) stage_vec(a, b, s_gv, s_am);
-  const int nblk = (Tc + kGB - 1) / kGB;
-  if (prefix) lds_dma(s_gb, a.gout + ((size_t)b * a.n_int + t0 + (nblk - 1) * kGB) * a.W,
-                      (Tc - (nblk - 1) * kGB) * a.W);
+  const int nblk = (Tc + kGBL - 1) / kGBL;
+  if (prefix) lds_dma(s_gb, a.gout + ((size_t)b * a.n_int + t0 + (nblk - 1) * kGBL) * a.W,
+                      (Tc - (nblk - 1) * kGBL) * a.W);
   lds_dma_wait();
   __syncthreads();
   const LaneMap m = lane_map_b<WAVE>(a, tid);
@@ -1138,13 +1139,13 @@ __global__ __launch_bounds__(MAXT) void k_chunk_bwd_local(DiagArgs a) {
   for (int blk = nblk - 1; blk >= 0; --blk) {
     const int buf = (nblk - 1 - blk) & 1;
     const bool more = prefix && blk > 0;
-    if (more) lds_dma(s_gb + (buf ^ 1) * kGB * a.W, a.gout + ((size_t)b * a.n_int + t0 + (blk - 1) * kGB) * a.W,
-                      kGB * a.W);
-    const GammaSrc gs{prefix ? s_gb + buf * kGB * a.W : s_gv, s_am, 1.0f / (float)a.n_int, a.readout};
+    if (more) lds_dma(s_gb + (buf ^ 1) * kGBL * a.W, a.gout + ((size_t)b * a.n_int + t0 + (blk - 1) * kGBL) * a.W,
+                      kGBL * a.W);
+    const GammaSrc gs{prefix ? s_gb + buf * kGBL * a.W : s_gv, s_am, 1.0f / (float)a.n_int, a.readout};
     if (m.active) {
 #pragma unroll 1
-      for (int s = kGB - 1; s >= 0; --s) {
-        const int t = blk * kGB + s;
+      for (int s = kGBL - 1; s >= 0; --s) {
+        const int t = blk * kGBL + s;
         if (t < Tc) {
           T g1, gA, gB;
           gamma_step<CPLX, N>(a, m, gs, s, t0 + t, g1, gA, gB);
@@ -1952,7 +1953,7 @@ int make_plan(const ews_diag_desc* s, Plan& p) {
   p.fast = pairs_eligible(s->structure, s->depth, s->dim, s->readout, s->flow_mode, T) &&
            s->leaf == EWS_DIAG_LEAF_CLOSED;
   p.C = (p.n_int + T - 1) / T;
-  p.lds_bwd_local = (size_t)bwd_lds_layout(T, p.d, p.W, p.NTb, 0, p.wave, false, kGB).total * 4;
+  p.lds_bwd_local = (size_t)bwd_lds_layout(T, p.d, p.W, p.NTb, 0, p.wave, false, kGBL).total * 4;
   p.lds_bwd_full = bwd_lds_bytes(p, T, true, kb);
   p.lds_bwd_inv = (size_t)bwd_lds_layout(T, p.d, p.W, p.NTb, 0, p.wave, true, kGB).total * 4;
   if (p.lds_bwd_full > kMaxLds) return EWS_ERR_SHAPE;
