@@ -436,8 +436,9 @@ def bench_c3(args):
         if events is not None:
             events[1].record()
         nat.check(lib.ews_dense_backward_kept(ctypes.byref(desc), path.data_ptr(), clock.data_ptr(),
-                                              A.data_ptr(), gout.data_ptr(), gpath.data_ptr(), gclock.data_ptr(),
-                                              gA.data_ptr(), wsb.data_ptr(), stream), "dense backward (kept)")
+                                              A.data_ptr(), out.data_ptr(), gout.data_ptr(), gpath.data_ptr(),
+                                              gclock.data_ptr(), gA.data_ptr(), wsb.data_ptr(), stream),
+                  "dense backward (kept)")
         if events is not None:
             events[2].record()
 

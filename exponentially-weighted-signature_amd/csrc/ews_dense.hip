@@ -1193,7 +1193,8 @@ struct AdjSeq {
   long init_bs, lloc_bs, lam_bs, agg_bs;
   int init_off, lam_lim;
   float* agg;
-  const float* st;    // EMIT: the states S_t, padded rows (B, n, LW)
+  const float* st;    // EMIT: the states S_t, padded rows (B, n, st_ld floats apart; st_ld >= LW)
+  long st_ld;
   float* dlv;         // EMIT: ds_t (padded, in place of lv)
   float* dfl;         // EMIT: dM_t (in place of fl)
 };
@@ -1264,7 +1265,7 @@ __device__ __forceinline__ void adj_load(const AdjSeq& s, int b, int t, int tid,
   x.S1 = x.S2 = 0.0f;
   if constexpr (MODE == ADJ_EMIT) {
     if (t > 0) {
-      const float* srow = s.st + ((long)b * s.n + t - 1) * LW;
+      const float* srow = s.st + ((long)b * s.n + t - 1) * s.st_ld;
       if (tid < 16) x.S1 = srow[tid];
       if constexpr (N >= 2) x.S2 = srow[16 + tid];
     }
@@ -1356,7 +1357,7 @@ __global__ __launch_bounds__(256, 2) void k_adj(AdjSeq s) {
     constexpr int NS3 = EMIT && N >= 3 ? 16 : 1;
     float s3v[NS3], s3t[NS3];
     if constexpr (EMIT && N >= 3) {
-      const float* s3g = t > 0 ? s.st + ((long)b * s.n + t - 1) * LW + 272 : nullptr;
+      const float* s3g = t > 0 ? s.st + ((long)b * s.n + t - 1) * s.st_ld + 272 : nullptr;
       // S3[4g + k2][4w + jj][c16] and S3[c16][4w + q / 4][4 (q % 4) + g]: one base each, offsets within 4 KB
       const float* pv = s3g + (4 * g * 256 + 4 * w * 16 + c16);
       const float* pt = s3g + (c16 * 256 + 4 * w * 16 + g);
@@ -3145,8 +3146,13 @@ int launch_adj(int N, const AdjSeq& q, dim3 grid, hipStream_t st) {
 // The adjoint of the combine and readout, given the forward's local terms / flows (loc, fl), chunk summaries and
 // carries in the workspace: recomputes the prefix rows (the states), then LOCAL, CARRY and EMIT; leaves ds_t in loc
 // and dM_t in fl.
-int dense_adjoint(const ews_dense_desc* s, const DPlan& p, const Args& a, const float* grad_out, hipStream_t st) {
-  {  // the forward's states S_t (padded rows)
+// rows: the forward's prefix rows (W floats apart, the level-0 column first when the descriptor asks for it), or
+// null. At d = 16 with the prefix readout they hold the states S_t in the padded layout, and the states pass is
+// skipped.
+int dense_adjoint(const ews_dense_desc* s, const DPlan& p, const Args& a, const float* grad_out, hipStream_t st,
+                  const float* rows = nullptr) {
+  const bool from_rows = rows && s->readout == EWS_READOUT_PREFIX && p.d == 16;
+  if (!from_rows) {  // the forward's states S_t (padded rows)
     Seq q{};
     q.lv = a.loc; q.lv_bs = (long)p.n_int * p.LW; q.fl = a.fl; q.fl_bs = (long)p.n_int * 256;
     q.n = p.n_int; q.T = p.T; q.init = a.car; q.init_bs = (long)(p.C + 1) * p.LW;
@@ -3169,7 +3175,8 @@ int dense_adjoint(const ews_dense_desc* s, const DPlan& p, const Args& a, const 
   q.gmode = ro == EWS_READOUT_PREFIX ? G_PREFIX : ro == EWS_READOUT_MEAN ? G_MEAN : ro == EWS_READOUT_MAX ? G_MAX
                                                                                                      : G_NONE;
   q.W = p.W; q.glvl0 = s->level0 ? 1 : 0; q.g = grad_out; q.amax = a.amax; q.gscale = 1.0f / (float)p.n_int;
-  q.st = a.pre;
+  q.st = from_rows ? rows + (s->level0 ? 1 : 0) : a.pre;
+  q.st_ld = from_rows ? p.W : p.LW;
   // LOCAL (the terminal readout has no in-chunk cotangents: the local parts are zero)
   if (q.gmode == G_NONE) {
     hipLaunchKernelGGL(k_zero_rows, dim3((p.LW + 255) / 256, p.B * p.C), dim3(256), 0, st, a.lloc, (long)p.LW,
@@ -3394,15 +3401,16 @@ int ews_dense_backward(const ews_dense_desc* desc, const float* path, const floa
 }
 
 int ews_dense_backward_kept(const ews_dense_desc* desc, const float* path, const float* clock, const float* A,
-                            const float* grad_out, float* grad_path, float* grad_clock, float* grad_A,
-                            void* workspace, ews_stream_t stream) {
+                            const float* out, const float* grad_out, float* grad_path, float* grad_clock,
+                            float* grad_A, void* workspace, ews_stream_t stream) {
   DPlan p;
   const int rc = dense_plan(desc, p);
   if (rc != EWS_OK) return rc;
   if (!path || !clock || !A || !grad_out || !grad_path || !grad_A || !workspace) return EWS_ERR_NULL;
   const Args a = dense_args(desc, p, path, clock, A, nullptr, workspace, true);
   hipStream_t st = (hipStream_t)stream;
-  const int r = dense_adjoint(desc, p, a, grad_out, st);  // the leaf, flows, summaries and carries are kept
+  // the leaf, flows, summaries and carries are kept; the states come from the forward's rows when given
+  const int r = dense_adjoint(desc, p, a, grad_out, st, out);
   if (r != EWS_OK) return r;
   return dense_leaf_adjoint(desc, p, a, workspace, grad_path, grad_clock, grad_A, st);
 }

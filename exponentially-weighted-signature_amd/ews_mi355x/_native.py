@@ -258,7 +258,7 @@ def load():
     lib.ews_dense_backward.restype = i32
     lib.ews_dense_forward_keep.argtypes = [ddp, vp, vp, vp, vp, vp, vp]
     lib.ews_dense_forward_keep.restype = i32
-    lib.ews_dense_backward_kept.argtypes = [ddp, vp, vp, vp, vp, vp, vp, vp, vp, vp]
+    lib.ews_dense_backward_kept.argtypes = [ddp, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp]
     lib.ews_dense_backward_kept.restype = i32
     ldp = ctypes.POINTER(LogDesc)
     lib.ews_log_dim.argtypes = [i32, i32]

@@ -169,7 +169,6 @@ class DenseScan(torch.autograd.Function):
         path, clock, A = path.contiguous(), clock.contiguous(), A.contiguous()
         B, L, d = path.shape
         desc = make_dense_desc(B, L, d, N, q, flow_mode, readout, level0, chunk, leaf)
-        ctx.save_for_backward(path, clock, A)
         ctx.desc = desc
         ctx.leaf = leaf
         D = sum(d**k for k in range(1, N + 1))
@@ -186,12 +185,18 @@ class DenseScan(torch.autograd.Function):
                  _stream_handle(dev))
         nat.check(rc, "ews_dense_forward")
         ctx.kept = ws if keep else None
+        # the kept backward reads the states from the output rows (prefix readout); autograd guards their version
+        if keep:
+            ctx.save_for_backward(path, clock, A, out)
+        else:
+            ctx.save_for_backward(path, clock, A)
         return out
 
     @staticmethod
     def backward(ctx, gout):
         lib = nat.load()
-        path, clock, A = ctx.saved_tensors
+        path, clock, A = ctx.saved_tensors[:3]
+        rows = ctx.saved_tensors[3] if len(ctx.saved_tensors) > 3 else None
         desc = ctx.desc
         dev = path.device
         gout = gout.to(torch.float32).contiguous()
@@ -204,10 +209,13 @@ class DenseScan(torch.autograd.Function):
         if not kept:
             ws = torch.empty(int(lib.ews_dense_backward_workspace_bytes(ctypes.byref(desc))), device=dev,
                              dtype=torch.uint8)
-        bwd = lib.ews_dense_backward_kept if kept else lib.ews_dense_backward
-        rc = bwd(ctypes.byref(desc), path.data_ptr(), clock.data_ptr(), A.data_ptr(), gout.data_ptr(),
-                 gpath.data_ptr(), gclock.data_ptr() if need_clock else None, gA.data_ptr(), ws.data_ptr(),
-                 _stream_handle(dev))
+        args = (gout.data_ptr(), gpath.data_ptr(), gclock.data_ptr() if need_clock else None, gA.data_ptr(),
+                ws.data_ptr(), _stream_handle(dev))
+        if kept:
+            rc = lib.ews_dense_backward_kept(ctypes.byref(desc), path.data_ptr(), clock.data_ptr(), A.data_ptr(),
+                                             rows.data_ptr() if rows is not None else None, *args)
+        else:
+            rc = lib.ews_dense_backward(ctypes.byref(desc), path.data_ptr(), clock.data_ptr(), A.data_ptr(), *args)
         nat.check(rc, "ews_dense_backward")
         return gpath, gclock, gA, None, None, None, None, None, None, None
 
