@@ -609,27 +609,40 @@ struct ScanLds {
   dc bl1[SW][K];                            // block level-1 increments (adjoint scan)
 };
 constexpr size_t kScanLds = sizeof(ScanLds);
+// Every load of the segment is in flight at once (the flows and level-1 increments first, then all of the rows:
+// at most SSEG * QROW / 4 float4 over SW * 64 threads), and only then written to LDS.
 __device__ __forceinline__ void stage_seg(const DiagArgs& a, int b, int q0, int nq, bool with_l1, ScanLds& sg) {
-  constexpr int U = 4, R4 = QROW / 4;
-  const float* src = a.qagg + ((size_t)b * a.NQ + q0) * a.D;
-  for (int ib = threadIdx.x; ib < nq * R4; ib += U * blockDim.x) {
-    f4a v[U];
-#pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const int i = ib + u * blockDim.x, q = i / R4, e = i - q * R4;
-      if (i < nq * R4) v[u] = *reinterpret_cast<const f4a*>(src + (size_t)q * a.D + 4 * e);
-    }
-#pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const int i = ib + u * blockDim.x, q = i / R4, e = i - q * R4;
-      if (i < nq * R4) *reinterpret_cast<f4a*>(&sg.y[q][4 * e]) = v[u];
-    }
-  }
+  constexpr int NT = SW * 64, R4 = QROW / 4, U = (SSEG * R4 + NT - 1) / NT, UF = (SSEG * K + NT - 1) / NT;
   const double* fs = a.qflow + ((size_t)b * a.NQ + q0) * K * 2;
   const double* ls = a.ql1 + ((size_t)b * a.NQ + q0) * K * 2;
-  for (int i = threadIdx.x; i < nq * K; i += blockDim.x) {  // at most two per thread
-    sg.F[i / K][i % K] = ld_dd(fs + 2 * i);
-    if (with_l1) sg.l1[i / K][i % K] = ld_dd(ls + 2 * i);
+  dc f[UF], g[UF];
+#pragma unroll
+  for (int u = 0; u < UF; ++u) {
+    const int i = threadIdx.x + u * NT;
+    if (i < nq * K) {
+      f[u] = ld_dd(fs + 2 * i);
+      if (with_l1) g[u] = ld_dd(ls + 2 * i);
+    }
+  }
+  const float* src = a.qagg + ((size_t)b * a.NQ + q0) * a.D;
+  f4a v[U];
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    const int i = threadIdx.x + u * NT, q = i / R4, e = i - q * R4;
+    if (i < nq * R4) v[u] = *reinterpret_cast<const f4a*>(src + (size_t)q * a.D + 4 * e);
+  }
+#pragma unroll
+  for (int u = 0; u < UF; ++u) {
+    const int i = threadIdx.x + u * NT;
+    if (i < nq * K) {
+      sg.F[i / K][i % K] = f[u];
+      if (with_l1) sg.l1[i / K][i % K] = g[u];
+    }
+  }
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    const int i = threadIdx.x + u * NT, q = i / R4, e = i - q * R4;
+    if (i < nq * R4) *reinterpret_cast<f4a*>(&sg.y[q][4 * e]) = v[u];
   }
 }
 struct QOps {
@@ -660,20 +673,37 @@ __device__ __forceinline__ PairSt get_block(const ScanLds& sg, int w, int l) {
   return PairSt{sg.bS1[w][l], sg.bSA[w][l], sg.bSB[w][l]};
 }
 
+// Every global operand of the quad's chain (its chunks' mu rows, plane k's level-1 carries at the chunk bounds, the
+// quad flow) is loaded before the first combine, so the wavefront waits for one round of loads, not one per chunk.
 __global__ __launch_bounds__(64) void k_quad_bwd_agg(DiagArgs a) {
   __shared__ dc s_F[4][K];
   const int q = blockIdx.x, b = blockIdx.y, j = threadIdx.x >> 3, k = threadIdx.x & 7;
   const int c0 = 4 * q, nc = min(4, a.C - c0);
+  PairSt m[4];
+  dc cr[5];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+    if (i < nc) m[i] = load_st_f(a.mu + ((size_t)b * a.C + c0 + i) * a.D, j, k);
+  const double* crow = a.carries + ((size_t)b * (a.C + 1) + c0) * a.D + 2 * k;
+#pragma unroll
+  for (int i = 0; i < 5; ++i)
+    if (i <= nc) cr[i] = ld_dd(crow + (size_t)i * a.D);
+  const dc Fq = threadIdx.x < K ? span_flow(a, b, c0, c0 + nc, k) : dc{1.0, 0.0};
   quad_flows(a, b, q, c0, nc, s_F);
-  if (threadIdx.x < K) {  // the quad's level-1 increment (its flow was written by quad_flows of this lane's row)
-    const dc Fq = span_flow(a, b, c0, c0 + nc, threadIdx.x);
-    st_dd(a.ql1 + (((size_t)b * a.NQ + q) * K + threadIdx.x) * 2, l1_inc(a, b, c0, c0 + nc, threadIdx.x, Fq));
+  if (threadIdx.x < K) {  // the quad's level-1 increment, carry1(c0 + nc) - Fq carry1(c0)
+    dc ce = cr[1];
+#pragma unroll
+    for (int i = 2; i < 5; ++i)
+      if (i == nc) ce = cr[i];
+    st_dd(a.ql1 + (((size_t)b * a.NQ + q) * K + k) * 2, ce - Fq * cr[0]);
   }
-  PairSt X = load_st_f(a.mu + ((size_t)b * a.C + c0 + nc - 1) * a.D, j, k);
-  for (int c = c0 + nc - 2; c >= c0; --c) {
-    const int i = c - c0;
-    adj_d(X, s_F[i][j], s_F[i][k], l1_inc(a, b, c, c + 1, k, s_F[i][k]));
-    add_st(X, load_st_f(a.mu + ((size_t)b * a.C + c) * a.D, j, k));
+  PairSt X{};
+#pragma unroll
+  for (int i = 3; i >= 0; --i) {
+    if (i < nc) {
+      if (i < nc - 1) adj_d(X, s_F[i][j], s_F[i][k], cr[i + 1] - s_F[i][k] * cr[i]);
+      add_st(X, m[i]);
+    }
   }
   store_st_f(a.qagg + ((size_t)b * a.NQ + q) * a.D, j, k, X);
 }
@@ -688,10 +718,17 @@ __global__ __launch_bounds__(SW * 64) void k_quad_bwd_scan(DiagArgs a) {
   PairSt X{};  // cotangent at the segment end, kept by wavefront 0
   for (int qe = a.NQ; qe > 0; qe -= SSEG) {
     const int nq = min(SSEG, qe), q0 = qe - nq;
-    stage_seg(a, b, q0, nq, true, sg);
-    __syncthreads();
     int lo, hi;
     seg_block(nq, w, lo, hi);
+    // plane k's level-1 carries at the block bounds (for the block's level-1 increment), loaded with the segment
+    const int bc0 = 4 * (q0 + lo), bc1 = min(4 * (q0 + hi), a.C);
+    dc cA{0.0, 0.0}, cB{0.0, 0.0};
+    if (j == 0 && lo < hi) {
+      cA = ld_dd(a.carries + ((size_t)b * (a.C + 1) + bc0) * a.D + 2 * k);
+      cB = ld_dd(a.carries + ((size_t)b * (a.C + 1) + bc1) * a.D + 2 * k);
+    }
+    stage_seg(a, b, q0, nq, true, sg);
+    __syncthreads();
     {  // 1. block aggregate from a zero cotangent at the block end; block flow and level-1 increment
       PairSt Xl{};
       dc Fk{1.0, 0.0};
@@ -708,8 +745,7 @@ __global__ __launch_bounds__(SW * 64) void k_quad_bwd_scan(DiagArgs a) {
       put_block(sg, w, l, Xl);
       if (j == 0) {
         sg.bF[w][k] = Fk;
-        const int c0 = 4 * (q0 + lo), c1 = min(4 * (q0 + hi), a.C);
-        sg.bl1[w][k] = lo < hi ? l1_inc(a, b, c0, c1, k, Fk) : dc{0.0, 0.0};
+        sg.bl1[w][k] = lo < hi ? cB - Fk * cA : dc{0.0, 0.0};  // carry1(bc1) - F carry1(bc0)
       }
     }
     __syncthreads();
