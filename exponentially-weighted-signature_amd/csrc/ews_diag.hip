@@ -2365,6 +2365,20 @@ int ews_diag_backward(const ews_diag_desc* desc, const void* path, const float* 
 
 int ews_diag_num_passes(int direction) { return direction == 0 ? kForwardPasses : kBackwardPasses; }
 
+int ews_diag_forward_status(const ews_diag_desc* desc, const void* residual, int* status, ews_stream_t stream) {
+  Plan p;
+  const int rc = make_plan(desc, p);
+  if (rc != EWS_OK) return rc;
+  if (!residual || !status) return EWS_ERR_NULL;
+  *status = 0;
+  if (!p.fast) return EWS_OK;  // only the look-back forward waits on other workgroups
+  const char* ctab = (const char*)residual + resid_carries_bytes(p) + resid_argmax_bytes(p) + 2 * resid_chunk_bytes(p);
+  if (hipMemcpyAsync(status, ctab + kCtabStatus * sizeof(int), sizeof(int), hipMemcpyDeviceToHost,
+                     (hipStream_t)stream) != hipSuccess)
+    return EWS_ERR_LAUNCH;
+  return hipStreamSynchronize((hipStream_t)stream) == hipSuccess ? EWS_OK : EWS_ERR_LAUNCH;
+}
+
 int ews_diag_forward_noalloc(const ews_diag_desc* desc, const void* path, const float* clock, const float* params,
                              float* out, ews_stream_t stream) {
   Plan p;

@@ -10,6 +10,8 @@ namespace ews {
 constexpr int kMaxT = 64;  // longest chunk the pair-group kernels stage
 // coefficient table of the pair-group kernels: header (16 floats), 9 complex per plane, 16 complex per pair
 constexpr int kCoefTabFloats = 16 + 2 * 9 * 8 + 2 * 16 * 64;
+// header word (an int) set to 1 by the look-back forward when a wait gave up (its rows are NaN), else 0
+constexpr int kCtabStatus = 3;
 
 // True if the configuration has pair-group kernels (rotation planes, d = 16, depth 2, prefix readout,
 // per-interval flows, chunk length <= kMaxT).

@@ -29,6 +29,7 @@
 // coefficients (phih = phi/2, IBh = IB/2, ...).
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <type_traits>
 
 #include "ews_args.h"
@@ -46,6 +47,9 @@ constexpr int NB = 4;     // steps per block of the full adjoint's column sums
 constexpr int kSpinLimit = 1 << 20;  // polls of a status word before the look-back gives up (rows turn NaN)
 constexpr int LBB = 4;               // aggregates whose loads are in flight together in the look-back
 constexpr int LBG = 8;               // quads per look-back group
+// a bit pattern no arithmetic here produces (a signalling NaN with a payload): a look-back aggregate word not yet
+// published
+constexpr unsigned long long kLbEmpty = 0x7FF4E3A5C0DE0000ull;
 constexpr int LBT = 32;              // words between the samples' ticket counters (one per 128-byte line)
 constexpr int VPITCH = (kMaxT + 1) * DIM;  // LDS floats per group of staged increments (one padding row)
 
@@ -330,6 +334,13 @@ __device__ __forceinline__ float ref_step(const DiagArgs& a) {
 // Three wavefronts share the entries (a single chain of series and exponentials per lane otherwise): wavefront 0
 // the plane nodes and the pair flows, 1 the B-pair divided differences, 2 the A-pair ones.
 __global__ __launch_bounds__(192) void k_coef_table(DiagArgs a) {
+  if (blockIdx.x > 0) {  // the other workgroups fill the look-back aggregates with the "not yet published" sentinel
+    const size_t n = (size_t)a.B * (a.NQ + (a.NQ + LBG - 1) / LBG) * (a.D + 2 * K);
+    unsigned long long* w = reinterpret_cast<unsigned long long*>(a.lbagg);
+    for (size_t i = (size_t)(blockIdx.x - 1) * blockDim.x + threadIdx.x; i < n; i += (size_t)(gridDim.x - 1) * blockDim.x)
+      w[i] = kLbEmpty;
+    return;
+  }
   // the look-back forward's status words (quads, then groups of LBG quads) and its ticket start at zero (this
   // launch runs first)
   const int nwords = a.B * (a.NQ + (a.NQ + LBG - 1) / LBG) + a.B * LBT;
@@ -351,6 +362,7 @@ __global__ __launch_bounds__(192) void k_coef_table(DiagArgs a) {
       tab[0] = h0;
       tab[1] = R;
       tab[2] = Dm;
+      reinterpret_cast<int*>(tab)[kCtabStatus] = 0;  // the look-back forward's error word
     }
     if (k == 0) {
       const Node1<cf> nj = node1(xj);
@@ -565,6 +577,23 @@ __device__ __forceinline__ void add_st(PairSt& X, const PairSt& m) {
   X.SA = X.SA + m.SA;
   X.SB = X.SB + m.SB;
 }
+// <m, D s> of a cotangent m and a state s (pair layout), D the derivation d/dh of the flows (level 1 of plane j
+// times u_j, pair (j, k) SB times u_j + u_k and SA times u_j + conj(u_k)): the lane's share, float64 (lanes
+// k = 0 add the level-1 term)
+__device__ __forceinline__ double flow_dot(const DiagArgs& a, const PairSt& m, const PairSt& s, int j, int k) {
+  const dc uj{-(double)a.params[2 * j], (double)a.params[2 * j + 1]};
+  const dc uk{-(double)a.params[2 * k], (double)a.params[2 * k + 1]};
+  const dc tB = cjd(m.SB) * ((uj + uk) * s.SB), tA = cjd(m.SA) * ((uj + cjd(uk)) * s.SA);
+  double r = tB.re + tA.re;
+  if (k == 0) r += (cjd(m.S1) * (uj * s.S1)).re;
+  return r;
+}
+__device__ __forceinline__ double wave_sum_d(double v) {
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) v += __shfl_xor(v, o, 64);
+  return v;
+}
+
 // level-1 increment of the span [ca, cb) of plane p: carry1(cb) - F carry1(ca)
 __device__ __forceinline__ dc l1_inc(const DiagArgs& a, int b, int ca, int cb, int p, dc F) {
   const double* c0 = a.carries + ((size_t)b * (a.C + 1) + ca) * a.D;
@@ -945,6 +974,8 @@ __global__ __launch_bounds__(64) void k_bwd_full(DiagArgs a) {
   __shared__ float s_dho[GPW][NB + 1];
   __shared__ __align__(16) float s_row[GPW][RBUF + DIM];  // cotangent row staging (+ level 1)
   __shared__ __align__(16) float s_mt[GPW][DIM + DIM * DIM];  // cotangent from later chunks, per group
+  __shared__ float s_dhr[DH ? GPW : 1][DH ? G : 1];   // the first step's dh partials without the flow terms
+  __shared__ double s_f64[GPW];                         // <mt(c - 1), D carry(c)> of each chunk (float64)
   const Lane l = lane_of<KP>(threadIdx.x);
   const int b = blockIdx.y, cb = blockIdx.x * GPW, c = cb + l.gi;
   stage<KP, BF16>(a, b, cb, s_v, s_h);
@@ -952,18 +983,34 @@ __global__ __launch_bounds__(64) void k_bwd_full(DiagArgs a) {
     // adjoint carries inside the quad: mt[c] = mu(c+1) + J_{c+1}^T mt[c+1] down from the quad's last chunk
     // (written by the scan); float64, written back for every later kernel that reads mt (generic chunks)
     const int jj = threadIdx.x >> 3, kk = threadIdx.x & 7;
-    const int c_last = min(4 * (cb / 4) + 3, a.C - 1);
+    const int q0 = 4 * (cb / 4), c_last = min(q0 + 3, a.C - 1);
     PairSt X = load_st_f(a.mt + ((size_t)b * a.C + c_last) * a.D, jj, kk);
     if (c_last < cb + GPW) store_st_f(s_mt[c_last - cb], jj, kk, X);
-    for (int cc = c_last - 1; cc >= cb; --cc) {
+    // with the clock gradient: the flow part of the chunk's first-step dh is <mt(c - 1), D carry(c)> (the
+    // carried cotangent on the state before the chunk, against the flows' derivative of that state), taken in
+    // float64 from the scanned cotangent and the float64 carry, so that the boundary knot's dh difference pairs
+    // it with the previous chunk's last step, which sees the same cotangent and state (the float32 adjoint
+    // recursion over the chunk drifts from it by more than the knot gradient's tolerance at L = 18k)
+    auto first_flow = [&](int ci, const PairSt& m) {
+      const double f = wave_sum_d(flow_dot(a, m, load_st_d(a.carries + ((size_t)b * (a.C + 1) + ci) * a.D, jj, kk),
+                                           jj, kk));
+      if (threadIdx.x == 0) s_f64[ci - cb] = f;
+    };
+    const int c_stop = DH ? max(cb - 1, q0) : cb;
+    for (int cc = c_last - 1; cc >= c_stop; --cc) {
       const double* cf = a.cflow + ((size_t)b * a.C + cc + 1) * K * 2;
       const dc Fk = ld_dd(cf + 2 * kk);
       adj_d(X, ld_dd(cf + 2 * jj), Fk, l1_inc(a, b, cc + 1, cc + 2, kk, Fk));
       add_st(X, load_st_f(a.mu + ((size_t)b * a.C + cc + 1) * a.D, jj, kk));
-      if (cc < cb + GPW) {
+      if (cc >= cb && cc < cb + GPW) {
         store_st_f(s_mt[cc - cb], jj, kk, X);
         store_st_f(a.mt + ((size_t)b * a.C + cc) * a.D, jj, kk, X);
       }
+      if (DH && cc + 1 < cb + GPW) first_flow(cc + 1, X);
+    }
+    if constexpr (DH) {
+      if (cb == q0 && cb >= 1) first_flow(cb, load_st_f(a.mt + ((size_t)b * a.C + cb - 1) * a.D, jj, kk));
+      if (cb == 0 && threadIdx.x == 0) s_f64[0] = 0.0;  // the zero state before the first chunk
     }
   }
   __syncthreads();
@@ -1096,7 +1143,7 @@ __global__ __launch_bounds__(64) void k_bwd_full(DiagArgs a) {
       const cf cj = S1 - f.phi * pj;
       const cf H1 = f.rhoi * cj;
       cf toC{0.0f, 0.0f}, toP{0.0f, 0.0f};
-      float dhp = 0.0f;
+      float dhp = 0.0f, dhf = 0.0f;  // dhf: the flow terms of dhp
       if constexpr (DH) {
         static_for<0, KP>([&](auto qc) {
           constexpr int q = qc;
@@ -1124,8 +1171,11 @@ __global__ __launch_bounds__(64) void k_bwd_full(DiagArgs a) {
           kph[q] = fma_c(cf{h, 0.0f}, gph, kph[q]);
           // coefficient cotangents
           const cf gIB = cjm(pi, Bc), gIA = cjm(pic, A), gLB = cjm(HB, Bc), gLA = cjm(HA, A);
-          if constexpr (DH)
-            dhp += redot(gIB, f.IB1[q]) + redot(gIA, f.IA1[q]) + redot(gLB, f.LB1[q]) + redot(gLA, f.LA1[q]);
+          if constexpr (DH) {
+            const float fl = redot(gLB, f.LB1[q]) + redot(gLA, f.LA1[q]);
+            dhp += redot(gIB, f.IB1[q]) + redot(gIA, f.IA1[q]) + fl;
+            dhf += fl;
+          }
           kIB[q] = fma_c(cf{h, 0.0f}, gIB, kIB[q]);
           kIA[q] = fma_c(cf{h, 0.0f}, gIA, kIA[q]);
           kLB[q] = fma_c(cf{h, 0.0f}, gLB, kLB[q]);
@@ -1201,11 +1251,18 @@ __global__ __launch_bounds__(64) void k_bwd_full(DiagArgs a) {
         *reinterpret_cast<float2*>(dvp_g + (s * K + l.j) * 2) = float2{dvp.re, dvp.im};
         const cf gphL = cjm(pj, l1);
         const cf grho = cjm(H1, gc);
-        if constexpr (DH) dhp += redot(gphL, f.phi1) + redot(grho, f.rho1);
+        if constexpr (DH) {
+          const float fl = redot(grho, f.rho1);
+          dhp += redot(gphL, f.phi1) + fl;
+          dhf += fl;
+        }
         kphj = fma_c(cf{h, 0.0f}, gphL, kphj);
         krho = fma_c(cf{h, 0.0f}, grho, krho);
       }
-      if constexpr (DH) dhp_g[s * G + l.gl] = dhp;
+      if constexpr (DH) {
+        dhp_g[s * G + l.gl] = dhp;
+        if (t == 0) s_dhr[l.gi][l.gl] = dhp - dhf;
+      }
       l1 = cjm(f.rho, gc);
       S1 = H1;
     });
@@ -1234,7 +1291,13 @@ __global__ __launch_bounds__(64) void k_bwd_full(DiagArgs a) {
           acc += (v.x + v.y) + (v.z + v.w);
         }
         dho_g[s] = acc;
-        if (t == 0 || t == Tc - 1) a.dh[(size_t)b * a.n_int + t0 + t] = acc;
+        if (t == Tc - 1) {
+          a.dh[(size_t)b * a.n_int + t0 + t] = acc;
+        } else if (t == 0) {  // the first step's dh for its boundary knot: local terms here, flows in float64
+          double r = 0.0;
+          for (int q = 0; q < G; ++q) r += (double)s_dhr[l.gi][q];
+          a.dh[(size_t)b * a.n_int + t0] = (float)(r + s_f64[l.gi]);
+        }
       }
     }
     __syncthreads();
@@ -1792,12 +1855,19 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(3))) void k_
 //      another's look-back but for the group aggregates, each LBG - 1 folds after its quads' own aggregates;
 //   D. the chunk carries inside the quad (written for the backward) and the prefix rows.
 // The chunk summaries of some quads overlap other quads' row writes, and the carry scans between passes disappear.
-// Published words are agent-scope atomic stores (coherent across the XCDs' L2s without a cache write-back), ordered
-// before the status word by a wait on every outstanding memory operation; readers load them with agent-scope atomic
-// loads. The status words and the ticket are zeroed by k_coef_table, which runs first in the same stream. Uniform
+// Publication: every aggregate word starts as the sentinel kLbEmpty (k_coef_table fills the buffer; it runs first in
+// the same stream) and is written once per call by an agent-scope relaxed atomic store (coherent across the XCDs'
+// L2s with no cache write-back); readers load each word with an agent-scope atomic load and take it only when it is
+// not the sentinel, re-reading until it is. Correctness rests on each word alone (one store per location, after the
+// fill), not on an ordering between locations, so no release/acquire pair is needed (a release at agent scope
+// writes back the XCD's dirty L2 lines: +75 us on this kernel, whose rows fill the L2). The status word is only the
+// hint of when to start reading: it is set after a wait on the wavefront's outstanding stores, so the reads
+// normally find every word already there. The status words and the ticket are zeroed by k_coef_table. Uniform
 // quads run the 16-lane groups (KP = 4, coefficients at each chunk's mean step); a quad with a non-uniform chunk
 // runs one lane per pair (lane = 8 j + k) with every step's coefficients at its own clock step, chunk by chunk.
 
+__device__ __forceinline__ bool lb_empty(double v) { return (unsigned long long)__double_as_longlong(v) == kLbEmpty; }
+__device__ __forceinline__ bool lb_empty(dc v) { return lb_empty(v.re) | lb_empty(v.im); }
 __device__ __forceinline__ void pub_d(double* p, dc v) {
   __hip_atomic_store(p, v.re, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   __hip_atomic_store(p + 1, v.im, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -1818,10 +1888,16 @@ __device__ __forceinline__ PairSt sub_st(const double* row, int j, int k) {
 __device__ __forceinline__ void publish(double* row, int* w, int D, int j, int k, const PairSt& s, dc Fj) {
   pub_st(row, j, k, s);
   if (k == 0) pub_d(row + D + 2 * j, Fj);
-  __builtin_amdgcn_s_waitcnt(0);  // every published word of the wavefront has landed
+  __builtin_amdgcn_s_waitcnt(0);  // the wavefront's published words have landed (the status is a hint only)
   if (threadIdx.x == 0) __hip_atomic_store(w, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 __device__ __forceinline__ dc shfl_d(dc v, int src) { return dc{__shfl(v.re, src), __shfl(v.im, src)}; }
+
+// a wait that reached kSpinLimit sets the coefficient table's error word (read by ews_diag_forward_status)
+__device__ __forceinline__ void lb_timeout(const DiagArgs& a) {
+  if (threadIdx.x == 0)
+    __hip_atomic_store(reinterpret_cast<int*>(a.ctab) + kCtabStatus, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
 
 // The look-back items of quad q, latest first: items 0 .. nq-1 the earlier quads of its group (q-1 down to its
 // group's first quad), then items nq .. nq+ng-1 the earlier groups (g-1 down to 0).
@@ -1840,20 +1916,28 @@ __device__ __forceinline__ const int* item_status(const LbItems& it, int i) {
   return i < it.nq ? it.qst + (it.q - 1 - i) : it.gst + (it.g - 1 - (i - it.nq));
 }
 // acc <- (items i0 .. i1-1 folded, latest first) (x) acc, with the flows of the folded span in aFj, aFk; the items'
-// status words have been seen nonzero
-__device__ __forceinline__ void lb_fold(const LbItems& it, int i0, int i1, int D, int j, int k, PairSt& acc, dc& aFj,
+// status words have been seen nonzero. A batch is re-read while any of its words is still the sentinel; false if that
+// lasts kSpinLimit reads.
+__device__ __forceinline__ bool lb_fold(const LbItems& it, int i0, int i1, int D, int j, int k, PairSt& acc, dc& aFj,
                                         dc& aFk) {
   for (int b0 = i0; b0 < i1; b0 += LBB) {
     PairSt g[LBB];
     dc gFj[LBB], gFk[LBB];
+    for (int polls = 0;; ++polls) {
+      bool empty = false;
 #pragma unroll
-    for (int u = 0; u < LBB; ++u) {
-      if (b0 + u < i1) {
-        const double* gr = item_row(it, b0 + u);
-        g[u] = sub_st(gr, j, k);
-        gFj[u] = sub_d(gr + D + 2 * j);
-        gFk[u] = sub_d(gr + D + 2 * k);
+      for (int u = 0; u < LBB; ++u) {
+        if (b0 + u < i1) {
+          const double* gr = item_row(it, b0 + u);
+          g[u] = sub_st(gr, j, k);
+          gFj[u] = sub_d(gr + D + 2 * j);
+          gFk[u] = sub_d(gr + D + 2 * k);
+          empty |= lb_empty(g[u].S1) | lb_empty(g[u].SA) | lb_empty(g[u].SB) | lb_empty(gFj[u]) | lb_empty(gFk[u]);
+        }
       }
+      if (!__any(empty)) break;
+      if (polls >= kSpinLimit) return false;
+      __builtin_amdgcn_s_sleep(1);
     }
 #pragma unroll
     for (int u = 0; u < LBB; ++u) {
@@ -1865,6 +1949,7 @@ __device__ __forceinline__ void lb_fold(const LbItems& it, int i0, int i1, int D
       }
     }
   }
+  return true;
 }
 // fold items [i0, i1) as their status words turn nonzero: one load per lane reads up to 64 of them at once
 __device__ __forceinline__ bool lb_fold_ready(const LbItems& it, int i0, int i1, int D, int j, int k, PairSt& acc,
@@ -1876,7 +1961,7 @@ __device__ __forceinline__ bool lb_fold_ready(const LbItems& it, int i0, int i1,
     const unsigned long long notready = __ballot(sv == 0);
     const int nr = notready ? __ffsll((long long)notready) - 1 : 64;  // leading items already published
     const int n = min(nr, i1 - i0);
-    lb_fold(it, i0, i0 + n, D, j, k, acc, aFj, aFk);
+    if (!lb_fold(it, i0, i0 + n, D, j, k, acc, aFj, aFk)) return false;
     i0 += n;
     if (n == 0) {
       if (++polls >= kSpinLimit) return false;
@@ -2194,14 +2279,20 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(3))) void k_
   // quad's carry, and through the published aggregates every later quad's, NaN: the rows show the failure
   const double qnan = __builtin_nan("");
   const PairSt poison{{qnan, qnan}, {qnan, qnan}, {qnan, qnan}};
-  if (!lb_fold_ready(it, 0, it.nq, a.D, jj, kk, acc, aFj, aFk)) acc = poison;
+  if (!lb_fold_ready(it, 0, it.nq, a.D, jj, kk, acc, aFj, aFk)) {
+    acc = poison;
+    lb_timeout(a);
+  }
   if (last_of_group) {  // the group's aggregate: its earlier quads (folded) followed by this quad
     PairSt ga = acc;
     chen_d(ga, qFj, qFk, agg.S1, shfl_d(agg.S1, 8 * kk), agg.SA, agg.SB);
     publish(const_cast<double*>(it.grow) + (size_t)it.g * AW, const_cast<int*>(it.gst) + it.g, a.D, jj, kk, ga,
             aFj * qFj);
   }
-  if (!lb_fold_ready(it, it.nq, it.nq + it.ng, a.D, jj, kk, acc, aFj, aFk)) acc = poison;
+  if (!lb_fold_ready(it, it.nq, it.nq + it.ng, a.D, jj, kk, acc, aFj, aFk)) {
+    acc = poison;
+    lb_timeout(a);
+  }
   // ---- D: chunk carries inside the quad (for the backward), then the prefix rows
   {
     PairSt st = acc;  // the zero state followed by every earlier quad
@@ -2251,7 +2342,10 @@ bool pairs_eligible(int structure, int depth, int dim, int readout, int flow_mod
 // workgroup per quad, tickets in launch order)
 int pairs_forward(const DiagArgs& a, hipStream_t st, bool out) {
   if (!out) {
-    hipLaunchKernelGGL(pairs::k_coef_table, dim3(1), dim3(192), 0, st, a);
+    // workgroup 0 the table, the others the aggregates' fill
+    const size_t n = (size_t)a.B * (a.NQ + (a.NQ + pairs::LBG - 1) / pairs::LBG) * (a.D + 2 * pairs::K);
+    const unsigned fill = (unsigned)std::min<size_t>(512, (n + 192 * 8 - 1) / (192 * 8));
+    hipLaunchKernelGGL(pairs::k_coef_table, dim3(1 + fill), dim3(192), 0, st, a);
   } else {
     const dim3 grid(a.NQ * a.B), blk(64);
     if (a.path_bf16) hipLaunchKernelGGL((pairs::k_fwd_lb<true>), grid, blk, 0, st, a);

@@ -38,6 +38,7 @@ EXPORTED = (
     "ews_diag_backward_pass",
     "ews_diag_num_passes",
     "ews_diag_forward_noalloc",
+    "ews_diag_forward_status",
     "ews_error_string",
     "ews_version",
     "ews_dense_workspace_bytes",
@@ -233,6 +234,8 @@ def load():
     lib.ews_diag_num_passes.restype = i32
     lib.ews_diag_forward_noalloc.argtypes = [dp, vp, vp, vp, vp, vp]
     lib.ews_diag_forward_noalloc.restype = i32
+    lib.ews_diag_forward_status.argtypes = [dp, vp, ctypes.POINTER(ctypes.c_int), vp]
+    lib.ews_diag_forward_status.restype = i32
     lib.ews_error_string.argtypes = [i32]
     lib.ews_error_string.restype = ctypes.c_char_p
     lib.ews_version.argtypes = []

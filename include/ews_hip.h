@@ -7,8 +7,9 @@
  * together with the custom VJPs of the Pallas kernels (ews/core/kernels/pallas_combine.py:1673-1801).
  *
  * Conventions: every pointer is device memory owned by the caller; nothing here allocates; all work is
- * stream-ordered on `stream`; the calls are re-entrant (no global mutable state). Sign convention is the
- * reference's: the flow over a clock step h is exp(-h A).
+ * stream-ordered on `stream`; the calls are re-entrant (no global mutable state), except
+ * `ews_diag_forward_noalloc`, whose scratch is one fixed device array per GPU: its calls that overlap on one GPU
+ * race. Sign convention is the reference's: the flow over a clock step h is exp(-h A).
  */
 #ifndef EWS_HIP_H
 #define EWS_HIP_H
@@ -120,6 +121,13 @@ int ews_diag_backward_pass(const ews_diag_desc* desc, int pass, const void* path
 
 /* Number of passes: direction 0 = forward, 1 = backward. */
 int ews_diag_num_passes(int direction);
+
+/* The forward's status word, after ews_diag_forward on `stream` (this call waits for the stream): *status is 0,
+ * or 1 when a chunk carry of the one-launch look-back forward waited on an earlier quad's aggregate past its spin
+ * limit and was set to NaN (the prefix rows of that sample from there on are NaN). Always 0 for configurations
+ * without the look-back forward. No counterpart in the reference (XLA reports no such condition); it lets a
+ * caller or a test tell a look-back timeout from a numerical NaN. */
+int ews_diag_forward_status(const ews_diag_desc* desc, const void* residual, int* status, ews_stream_t stream);
 
 /* ews_diag_forward without a residual or workspace argument and without any allocation: no counterpart in the
  * reference. For callers that cannot allocate device memory: code under HIP graph capture, tight serving loops,

@@ -163,19 +163,57 @@ def test_van_loan_uniform_equals_displacement_on_uniform_clock():
         assert float((x - y).abs().max()) < 1e-12
 
 
-@pytest.mark.parametrize("method", ["exact", "euler", "cayley", "pade"])
-def test_expm_methods(method):
-    rng = _rng(8)
-    X = rng.normal(size=(4, 4)) * 0.3
-    got = O.expm(torch.tensor(X), method).numpy()
-    I = np.eye(4)
-    ref = {
-        "exact": scipy.linalg.expm(X),
-        "euler": I + X,
-        "cayley": np.linalg.inv(I - X / 2) @ (I + X / 2),
-        "pade": np.linalg.inv(I - X / 2 + X @ X / 12) @ (I + X / 2 + X @ X / 12),
-    }[method]
-    np.testing.assert_allclose(got, ref, rtol=1e-12, atol=1e-13)
+# The approximate exponentials (ews/core/expm_approx.py:13-31) pinned by what the mathematics fixes, not by their
+# formulas: the order of agreement with the exact exponential (error ratio under halving X), the leading error term
+# (Euler X^2/2; Cayley -X^3/12; the [2/2] Pade X^5/720, the Pade error constant m! n! / ((m+n)! (m+n+1)!)),
+# orthogonality on skew-symmetric X for the two diagonal Pade schemes (r(-x) = 1/r(x)), and r(X) r(-X) = I. A
+# wrong sign, a dropped or mis-scaled term, or a solve against the wrong side fails one of these.
+_EXPM_ORDER = {"euler": (2, 0.5), "cayley": (3, -1.0 / 12.0), "pade": (5, 1.0 / 720.0)}
+_EXPM_SCALES = {"euler": (0.08, 0.04, 0.02, 0.01), "cayley": (0.08, 0.04, 0.02, 0.01), "pade": (0.2, 0.1, 0.05, 0.025)}
+
+
+def test_expm_exact_is_scipy():
+    X = _rng(8).normal(size=(4, 4)) * 0.3
+    np.testing.assert_allclose(O.expm(torch.tensor(X), "exact").numpy(), scipy.linalg.expm(X), rtol=1e-12,
+                               atol=1e-13)
+
+
+@pytest.mark.parametrize("method", ["euler", "cayley", "pade"])
+def test_expm_approx_order_and_leading_term(method):
+    p, c = _EXPM_ORDER[method]
+    rng = _rng(81)
+    X0 = rng.normal(size=(5, 5))  # a general (non-normal) matrix
+    X0 /= np.linalg.norm(X0, 2)
+    errs = []
+    for e in _EXPM_SCALES[method]:  # the [2/2] Pade error reaches float64 rounding near |X| = 0.01
+        X = e * X0
+        E = scipy.linalg.expm(X) - O.expm(torch.tensor(X), method).numpy()
+        lead = c * np.linalg.matrix_power(X, p)
+        # the leading term carries the error to relative accuracy O(|X|)
+        assert np.abs(E - lead).max() <= 2.0 * e * np.abs(lead).max(), (method, e)
+        errs.append(np.abs(E).max())
+    for a, b in zip(errs, errs[1:]):
+        assert abs(np.log2(a / b) - p) < 0.2, (method, errs)
+
+
+@pytest.mark.parametrize("method", ["cayley", "pade"])
+def test_expm_diagonal_pade_orthogonal_on_skew(method):
+    rng = _rng(82)
+    Y = rng.normal(size=(6, 6))
+    S = (Y - Y.T) * 0.7  # skew-symmetric, not small
+    Q = O.expm(torch.tensor(S), method).numpy()
+    np.testing.assert_allclose(Q.T @ Q, np.eye(6), atol=1e-12)
+    assert abs(np.linalg.det(Q) - 1.0) < 1e-12
+    Y = rng.normal(size=(6, 6)) * 0.4
+    R = O.expm(torch.tensor(Y), method).numpy() @ O.expm(torch.tensor(-Y), method).numpy()
+    np.testing.assert_allclose(R, np.eye(6), atol=1e-12)
+
+
+def test_expm_euler_is_not_symmetric():
+    # Euler is the one scheme with r(X) r(-X) = I - X^2, not I
+    Y = _rng(83).normal(size=(4, 4)) * 0.3
+    R = O.expm(torch.tensor(Y), "euler").numpy() @ O.expm(torch.tensor(-Y), "euler").numpy()
+    np.testing.assert_allclose(R, np.eye(4) - Y @ Y, atol=1e-13)
 
 
 @pytest.mark.parametrize("N", [1, 2, 3])
