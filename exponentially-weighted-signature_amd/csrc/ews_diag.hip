@@ -1911,13 +1911,14 @@ int make_plan(const ews_diag_desc* s, Plan& p) {
   p.W = logp ? p.D : p.D + (s->level0 ? 1 : 0);
   p.Wlog = logp ? p.d + p.d * (p.d - 1) / 2 : 0;
   p.npar = p.cplx ? 2 * p.K : p.K;
-  // the per-sample sequential kernels: asked for (chunk EWS_CHUNK_SEQUENTIAL, the log-prefix readout), or chosen
-  // for many samples of moderate length, where one workgroup per sample fills the chip
+  // the per-sample sequential kernels: asked for (chunk EWS_CHUNK_SEQUENTIAL), or chosen for many samples of
+  // moderate length, where one workgroup per sample fills the chip (the same rule for flat and log rows: a few long
+  // samples take the chunk kernels, whose output pass writes the log rows as well)
   const bool seq_form = !p.cplx && p.N == 2 && p.d <= kSeqMaxK && s->flow_mode == EWS_FLOW_PER_INTERVAL &&
                         (s->readout == EWS_READOUT_PREFIX || s->readout == EWS_READOUT_LOGPREFIX);
   const bool seq_asked = s->chunk == EWS_CHUNK_SEQUENTIAL;
   if (seq_asked && !seq_form) return EWS_ERR_OPTION;
-  p.seq = seq_form && (seq_asked || (s->chunk == 0 && (logp || (p.B >= 128 && p.L <= 1025))));
+  p.seq = seq_form && (seq_asked || (s->chunk == 0 && p.B >= 128 && p.L <= 1025));
   p.log = logp && !p.seq;
   if (p.seq) {
     if (s->readout == EWS_READOUT_LOGPREFIX) p.W = p.d + p.d * (p.d - 1) / 2;

@@ -30,7 +30,7 @@ import torch.nn.functional as F
 from .front import B, BlockFront, ClockSpec, make_clock
 from .layer import EWS
 from .mixer import MixerEpilogue
-from .params import AParamBoundedRotation, AParamDampedRotation, AParamDefinitePlusSkew
+from .params import AParamBoundedRotation, AParamDampedRotation, AParamDefinitePlusSkew, is_rotation_planes
 
 BOUNDED_PAD_ID = 0  # the token id the bounded-rotation scale ignores (ews/block.py:26)
 
@@ -311,7 +311,10 @@ class StackedEWS(nn.Module):
         """ews/block.py:626-677: 2 pi / dtheta_max for a rotation-plane block of a token model (dtheta_max the
         largest per-token clock increment over the embedding table, pad excluded, no gradient); 1.0 otherwise."""
         block = self.blocks[i]
-        if not (self.tokens and isinstance(block.ewms.A_param, (AParamBoundedRotation, AParamDampedRotation))):
+        # the gate keys on the class as the reference's does, by the five rotation-plane class names it lists
+        # (AParamBounded/Clamped/Damped/ReluDamped/UnboundedRotation): a parametrisation of any of them, this
+        # module's or a caller's own, gets the bounded scale, never a silent 1.0
+        if not (self.tokens and is_rotation_planes(block.ewms.A_param)):
             return 1.0
         spec = block.clock.spec
         c = spec.norm_constant or 1.0

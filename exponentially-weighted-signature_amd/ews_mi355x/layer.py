@@ -182,6 +182,11 @@ class EWS(torch.nn.Module):
             "(any generator, depths 1-3) or a rotation-plane / diagonal parametrisation with leaf='plane_closed'"
         )
 
+    def _keep_dense(self):
+        """The dense forward keeps its backward workspace only in training mode with grad mode on (and unless
+        EWS_DENSE_KEEP=0): an evaluation pass that still records a graph does not hold it."""
+        return None if self.training else False
+
     def _run(self, path, clock, readout, level0, a_scale):
         engine = self._engine_check()
         if self.dtype != torch.float32:
@@ -203,14 +208,15 @@ class EWS(torch.nn.Module):
                 leaf = ops.DenseLeaf("block_series", q=self.series_q or 0, chen_expm=chen)
                 return ops.dense_scan(path.to(torch.float32), clock.to(torch.float32),
                                       A.to(path.device).contiguous(), self.N, leaf.q, self._flow_mode(readout),
-                                      readout, level0, leaf=leaf)
+                                      readout, level0, leaf=leaf, keep=self._keep_dense())
             if self.leaf == "van_loan":
                 leaf = ops.DenseLeaf("van_loan", M=self.M, van_loan_expm=self.van_loan_expm,
                                      reweighting_mode=self.reweighting_mode, chen_expm=chen)
             else:
                 leaf = ops.DenseLeaf("series", q=self.series_q, chen_expm=chen)
             return ops.dense_scan(path.to(torch.float32), clock.to(torch.float32), A.to(path.device).contiguous(),
-                                  self.N, leaf.q, self._flow_mode(readout), readout, level0, leaf=leaf)
+                                  self.N, leaf.q, self._flow_mode(readout), readout, level0, leaf=leaf,
+                                  keep=self._keep_dense())
         params = self._diag_params(A.to(path.device))
         if path.dtype != torch.bfloat16:
             path = path.to(torch.float32)

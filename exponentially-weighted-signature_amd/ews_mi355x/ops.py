@@ -8,6 +8,7 @@ chunk-start states the library returns; the backward recomputes the rest inside 
 from __future__ import annotations
 
 import ctypes
+import os
 
 import torch
 
@@ -160,10 +161,12 @@ class DenseScan(torch.autograd.Function):
     flows of chen_expm). The backward is ews_dense_backward: the combine's adjoint scans, then the leaf's and the
     flows' adjoints per interval and one reduction for dA. When a gradient is needed the forward keeps its leaf,
     flows, chunk summaries and carries (ews_dense_forward_keep) and the first backward consumes them
-    (ews_dense_backward_kept) instead of recomputing them; a second backward of the same graph recomputes."""
+    (ews_dense_backward_kept) instead of recomputing them; a second backward of the same graph recomputes.
+    keep = False skips that (the workspace is then freed with the forward: 2.4 GB at c3's shape, per dense block of
+    a stack, until the graph is released), at the price of the recompute in the backward."""
 
     @staticmethod
-    def forward(ctx, path, clock, A, N, q, flow_mode, readout, level0, chunk, leaf):
+    def forward(ctx, path, clock, A, N, q, flow_mode, readout, level0, chunk, leaf, keep=True):
         lib = nat.load()
         _check_dense(path, clock, A)
         path, clock, A = path.contiguous(), clock.contiguous(), A.contiguous()
@@ -176,7 +179,7 @@ class DenseScan(torch.autograd.Function):
         shape = (B, L - 1, W) if readout == "prefix" else (B, W)
         dev = path.device
         out = torch.empty(shape, device=dev, dtype=torch.float32)
-        keep = any(ctx.needs_input_grad[:3])
+        keep = bool(keep) and any(ctx.needs_input_grad[:3])
         nbytes = (lib.ews_dense_backward_workspace_bytes if keep else lib.ews_dense_workspace_bytes)(
             ctypes.byref(desc))
         ws = torch.empty(int(nbytes), device=dev, dtype=torch.uint8)
@@ -217,12 +220,23 @@ class DenseScan(torch.autograd.Function):
         else:
             rc = lib.ews_dense_backward(ctypes.byref(desc), path.data_ptr(), clock.data_ptr(), A.data_ptr(), *args)
         nat.check(rc, "ews_dense_backward")
-        return gpath, gclock, gA, None, None, None, None, None, None, None
+        return gpath, gclock, gA, None, None, None, None, None, None, None, None
 
 
-def dense_scan(path, clock, A, N, q, flow_mode="per_interval", readout="prefix", level0=True, chunk=0, leaf=None):
+def dense_keep_default():
+    """Whether a dense forward keeps its backward workspace by default: yes unless EWS_DENSE_KEEP=0."""
+    return os.environ.get("EWS_DENSE_KEEP", "1") != "0"
+
+
+def dense_scan(path, clock, A, N, q, flow_mode="per_interval", readout="prefix", level0=True, chunk=0, leaf=None,
+               keep=None):
+    """keep: keep the forward's leaf, flows and carries for the backward (None: when grad mode is on, an input
+    needs a gradient and EWS_DENSE_KEEP is not 0)."""
     leaf = leaf if leaf is not None else DenseLeaf("series", q)
-    return DenseScan.apply(path, clock, A, int(N), int(q), flow_mode, readout, bool(level0), int(chunk), leaf)
+    if keep is None:
+        keep = torch.is_grad_enabled() and dense_keep_default()
+    return DenseScan.apply(path, clock, A, int(N), int(q), flow_mode, readout, bool(level0), int(chunk), leaf,
+                           bool(keep))
 
 
 def dense_local_terms(path, clock, A, N, q, flow_mode="per_interval", leaf=None):

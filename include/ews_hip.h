@@ -50,9 +50,10 @@ typedef struct ihipStream_t* ews_stream_t; /* hipStream_t */
  * signature, level 1 then S2[a,b] - S1_a S1_b / 2 at the Lyndon words a < b in lexicographic order (real
  * coordinates; a rotation plane j is coordinates 2j, 2j+1), (B, L-1, d + d(d-1)/2), no level-0 column (level0
  * is ignored). Depth 2, any structure and flow mode. The scan's output pass writes these rows; the flat rows never
- * reach memory. A real diagonal with d <= 32 and per-interval flows runs on the per-sample sequential kernels at
- * chunk 0 (or EWS_CHUNK_SEQUENTIAL); every other case, and chunk > 0, on the chunk kernels, whose residual then
- * also keeps level 1 of every step and whose backward workspace holds one flat-row cotangent per step. */
+ * reach memory. A real diagonal with d <= 32 and per-interval flows runs on the per-sample sequential kernels when
+ * chunk 0 selects them (B >= 128 and L <= 1025, as for flat rows) or EWS_CHUNK_SEQUENTIAL asks for them; every other
+ * case on the chunk kernels, whose residual then also keeps level 1 of every step and whose backward workspace
+ * holds one flat-row cotangent per step. */
 #define EWS_READOUT_LOGPREFIX 4
 
 /* ews_diag_desc.chunk: 0 selects the kernels and chunk length; EWS_CHUNK_SEQUENTIAL asks for the per-sample

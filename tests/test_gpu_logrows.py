@@ -54,6 +54,9 @@ CASES = [
     ("planes", 12, 2, 70, False, "displacement"),           # d = 24: 1,024-lane workgroups
     ("real", 8, 3, 120, False, "displacement_uniform_basepoint"),
     ("real", 5, 2, 65, True, "displacement_uniform"),
+    # a few long samples of a real diagonal with per-interval flows: the default plan takes the chunk kernels (the
+    # per-sample sequential kernels are for B >= 128 and L <= 1025), whose output pass writes the log rows
+    ("real", 8, 2, 5000, False, "displacement"),
 ]
 
 
@@ -69,7 +72,12 @@ def test_log_rows_from_chunk_kernels_match_oracle(case):
     print(f"log rows {structure} K={K} B={B} L={L} {mode}", flush=True)
     p = path.to(DEV).requires_grad_(True)
     c = clock.to(DEV).requires_grad_(True)
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(2)]
+    ev[0].record()
     out = layer(p, c, readout="prefix")
+    ev[1].record()
+    torch.cuda.synchronize()
+    print(f"  forward {ev[0].elapsed_time(ev[1]):.3f} ms (first call)", flush=True)
     pr = path.double().requires_grad_(True)
     cr = clock.double().requires_grad_(True)
     A = ref()
