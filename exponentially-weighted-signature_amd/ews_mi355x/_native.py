@@ -75,6 +75,10 @@ EXPORTED = (
     "ews_jordan_local_terms",
     "ews_jordan_workspace_bytes",
     "ews_jordan_local_terms_backward",
+    "ews_chain_residual_bytes",
+    "ews_chain_workspace_bytes",
+    "ews_chain_forward",
+    "ews_chain_backward",
 )
 
 JORDAN_KINDS = {"real": 0, "complex": 1}
@@ -133,6 +137,22 @@ class JordanDesc(ctypes.Structure):
         ("depth", ctypes.c_int32),
         ("kind", ctypes.c_int32),
         ("size", ctypes.c_int32),
+    ]
+
+
+class ChainDesc(ctypes.Structure):
+    _fields_ = [
+        ("batch", ctypes.c_int32),
+        ("length", ctypes.c_int32),
+        ("dim", ctypes.c_int32),
+        ("kind", ctypes.c_int32),
+        ("size", ctypes.c_int32),
+        ("flow_mode", ctypes.c_int32),
+        ("leaf_mode", ctypes.c_int32),
+        ("readout", ctypes.c_int32),
+        ("level0", ctypes.c_int32),
+        ("series_q", ctypes.c_int32),
+        ("chunk", ctypes.c_int32),
     ]
 
 
@@ -314,6 +334,15 @@ def load():
     lib.ews_jordan_workspace_bytes.restype = sz
     lib.ews_jordan_local_terms_backward.argtypes = [jdp, vp, vp, vp, vp, vp, vp, vp, vp, vp]
     lib.ews_jordan_local_terms_backward.restype = i32
+    chp = ctypes.POINTER(ChainDesc)
+    lib.ews_chain_residual_bytes.argtypes = [chp]
+    lib.ews_chain_residual_bytes.restype = sz
+    lib.ews_chain_workspace_bytes.argtypes = [chp]
+    lib.ews_chain_workspace_bytes.restype = sz
+    lib.ews_chain_forward.argtypes = [chp, vp, vp, vp, vp, vp, vp, vp]
+    lib.ews_chain_forward.restype = i32
+    lib.ews_chain_backward.argtypes = [chp, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp]
+    lib.ews_chain_backward.restype = i32
     _lib = lib
     return lib
 

@@ -149,7 +149,36 @@ class EWS(torch.nn.Module):
             return torch.stack([A[ii, ii], A[ii, ii + 1]], -1).contiguous()
         return torch.diagonal(A).contiguous()
 
+    def _chain_form(self):
+        """(kind, size, series_q, leaf step mode) when the depth-1 chain kernels take this layer, else None: a
+        generator of uniform Jordan chains (any number) under exact flows (jordan_flows or chen_expm "exact"),
+        and rotation planes / real diagonals wider than the dense kernels with the van_loan leaf. The leaf's level
+        1 is then phi(-hA) v exactly (jordan_closed, block_series, plane_closed, van_loan with an exact
+        van_loan_expm) or its order-q truncation (series)."""
+        if self.N != 1 or not (self.jordan_flows or self.chen_expm == "exact"):
+            return None
+        chains = jordan_chains_of(self.A_param)
+        if chains is None:
+            if self.structure is None or self.leaf != "van_loan" or self.d <= 16:
+                return None
+            chains = ("complex", 2) if self.structure == "planes" else ("real", 1)
+        if self.leaf == "van_loan":
+            if self.van_loan_expm != "exact":
+                return None
+            step = {"displacement": "per_interval", "displacement_uniform": "cached",
+                    "displacement_uniform_basepoint": "cached_basepoint"}.get(self.reweighting_mode)
+            return None if step is None else (chains[0], chains[1], 0, step)
+        if self.leaf == "series":
+            if not 1 <= int(self.series_q or 0) <= 48:
+                return None
+            return (chains[0], chains[1], int(self.series_q), "per_interval")
+        if self.leaf in JORDAN_LEAVES or self.leaf in ("block_series", "plane_closed"):
+            return (chains[0], chains[1], 0, "per_interval")
+        return None
+
     def _engine_check(self):
+        if self._chain_form() is not None:
+            return "chain"
         if self.leaf in JORDAN_LEAVES or (self.leaf == "block_series" and self.structure is None):
             if self.N > 2:
                 raise NotImplementedError(f"leaf={self.leaf!r}: closed-form local terms exist for depths 1 and 2")
@@ -192,6 +221,16 @@ class EWS(torch.nn.Module):
         if self.dtype != torch.float32:
             raise TypeError("the MI355X kernels compute in float32 (dtype=torch.float32)")
         A = self.A_param().to(torch.float32) * torch.as_tensor(a_scale, dtype=torch.float32, device=path.device)
+        if engine == "chain":
+            kind, size, q, step = self._chain_form()
+            kr = readout if readout in ("prefix", "terminal") else "prefix"
+            out = ops.chain_scan(path.to(torch.float32), clock.to(torch.float32), A.to(path.device).contiguous(),
+                                 kind, size, self._flow_mode(readout), step, kr, level0, q)
+            if readout == "mean":
+                return out.mean(1)
+            if readout == "max":
+                return out.max(1).values
+            return out
         if engine == "dense":
             chen = "exact" if self.jordan_flows else self.chen_expm  # closed-form chain flows are exact
             if self.leaf in JORDAN_LEAVES or (self.leaf == "plane_closed" and self.structure == "planes"):

@@ -383,6 +383,67 @@ def jordan_scan(path, clock, A, N, kind, size, flow_mode="per_interval", readout
                             chen_expm)
 
 
+# ---------------------------------------------------------------------------------------------- depth-1 chains
+class ChainScan(torch.autograd.Function):
+    """Depth-1 EWS of a block-diagonal A of uniform chains, any number of chains (ews_chain_forward /
+    ews_chain_backward): prefix or terminal rows; the exact level 1 phi(-hA) v (series_q 0) or the series leaf's
+    order-q truncation; exact flows in the chains' closed form. leaf_mode: the leaf's clock step (van_loan's
+    uniform modes share one step)."""
+
+    @staticmethod
+    def forward(ctx, path, clock, A, kind, size, flow_mode, leaf_mode, readout, level0, series_q, chunk):
+        lib = nat.load()
+        for nm, t in (("path", path), ("clock", clock), ("A", A)):
+            if not t.is_cuda:
+                raise RuntimeError("ews_mi355x runs on a HIP device only: move path/clock/A to the GPU (no CPU path)")
+            if t.dtype != torch.float32:
+                raise TypeError(f"{nm} must be float32 for the chain kernels, got {t.dtype}")
+        path, clock, A = path.contiguous(), clock.contiguous(), A.contiguous()
+        B, L, d = path.shape
+        desc = nat.ChainDesc(B, L, d, nat.JORDAN_KINDS[kind], int(size), _FLOW_MODES[flow_mode],
+                             _FLOW_MODES[leaf_mode], nat.READOUTS[readout], int(level0), int(series_q), int(chunk))
+        W = d + (1 if level0 else 0)
+        dev = path.device
+        out = torch.empty((B, L - 1, W) if readout == "prefix" else (B, W), device=dev, dtype=torch.float32)
+        rs = torch.empty(int(lib.ews_chain_residual_bytes(ctypes.byref(desc))), device=dev, dtype=torch.uint8)
+        ws = torch.empty(int(lib.ews_chain_workspace_bytes(ctypes.byref(desc))), device=dev, dtype=torch.uint8)
+        if rs.numel() == 0 or ws.numel() == 0:
+            raise ValueError(f"unsupported chain configuration: d={d}, kind={kind!r}, size={size}, "
+                             f"series_q={series_q}, readout={readout!r}")
+        nat.check(lib.ews_chain_forward(ctypes.byref(desc), path.data_ptr(), clock.data_ptr(), A.data_ptr(),
+                                        out.data_ptr(), rs.data_ptr(), ws.data_ptr(), _stream_handle(dev)),
+                  "ews_chain_forward")
+        ctx.save_for_backward(path, clock, A, rs)
+        ctx.desc = desc
+        return out
+
+    @staticmethod
+    def backward(ctx, gout):
+        lib = nat.load()
+        path, clock, A, rs = ctx.saved_tensors
+        desc = ctx.desc
+        dev = path.device
+        gout = gout.to(torch.float32).contiguous()
+        gpath = torch.empty_like(path)
+        need_clock = ctx.needs_input_grad[1]
+        gclock = torch.empty_like(clock) if need_clock else None
+        gA = torch.empty_like(A)
+        ws = torch.empty(int(lib.ews_chain_workspace_bytes(ctypes.byref(desc))), device=dev, dtype=torch.uint8)
+        nat.check(lib.ews_chain_backward(ctypes.byref(desc), path.data_ptr(), clock.data_ptr(), A.data_ptr(),
+                                         rs.data_ptr(), gout.data_ptr(), gpath.data_ptr(),
+                                         gclock.data_ptr() if need_clock else None, gA.data_ptr(), ws.data_ptr(),
+                                         _stream_handle(dev)), "ews_chain_backward")
+        return gpath, gclock, gA, None, None, None, None, None, None, None, None
+
+
+def chain_scan(path, clock, A, kind, size, flow_mode="per_interval", leaf_mode="per_interval", readout="prefix",
+               level0=True, series_q=0, chunk=0):
+    """kind "real" (sizes 1-4; 1 = a real diagonal) or "complex" (sizes 2, 4, 6, 8; 2 = rotation planes); readout
+    "prefix" or "terminal"."""
+    return ChainScan.apply(path, clock, A, kind, int(size), flow_mode, leaf_mode, readout, bool(level0),
+                           int(series_q), int(chunk))
+
+
 # ---------------------------------------------------------------------------------------------- log-signature
 class LogRows(torch.autograd.Function):
     """Compressed log of EWS state rows (B, R, level0 + D) with the LogEWS readout (ews/layer.py:488-517):

@@ -309,6 +309,49 @@ int ews_jordan_local_terms_backward(const ews_jordan_desc* desc, const float* pa
                                     float* grad_A, void* workspace, ews_stream_t stream);
 
 /* ---------------------------------------------------------------------------------------------------------
+ * Depth-1 scan of a block-diagonal A of uniform chains, any number of chains (chain d/size <= 64): the EWS at
+ * N = 1 (ews/layer.py:154-265 with leaf jordan_closed, series, van_loan or block_series, whose level 1 is the
+ * exact phi(-hA) v or its order-q truncation) under exact flows, which for a chain are the closed form of
+ * jordan_block_operators (ews/core/kernels/combine.py:143-190; with jordan_flows or chen_expm "exact"). Chains as
+ * in ews_jordan_desc: real chains of 1-4 coordinates (size 1: a real diagonal), complex chains of 1-4 complex
+ * coordinates (size 2: rotation planes). Everything per chain in float64; chunk carries in float64.
+ * --------------------------------------------------------------------------------------------------------- */
+typedef struct ews_chain_desc {
+  int32_t batch;     /* B >= 1 */
+  int32_t length;    /* L >= 2 knots */
+  int32_t dim;       /* d = chains x size */
+  int32_t kind;      /* EWS_JORDAN_REAL or EWS_JORDAN_COMPLEX */
+  int32_t size;      /* chain size in real coordinates: real 1-4; complex 2, 4, 6, 8 */
+  int32_t flow_mode; /* EWS_FLOW_* of the flows (chen_scan.py:155-168) */
+  int32_t leaf_mode; /* EWS_FLOW_* of the leaf's clock step: per interval, or van_loan's uniform modes
+                        (van_loan.py:147-160: one shared step; basepoint: interval 0 has none) */
+  int32_t readout;   /* EWS_READOUT_PREFIX (B, L-1, W) or EWS_READOUT_TERMINAL (B, W), W = level0 + d */
+  int32_t level0;    /* 1: the leading level-0 column of the flat format */
+  int32_t series_q;  /* 0: the exact level 1 phi(-hA) v; 1..48: the series leaf's order-q truncation */
+  int32_t chunk;     /* intervals per chunk, 0: 32; at most 64 */
+} ews_chain_desc;
+
+/* Residual the forward leaves for the backward: the float64 chunk carries (B, C+1, chains, coordinates). */
+size_t ews_chain_residual_bytes(const ews_chain_desc* desc);
+/* Scratch of both directions: chunk summaries, adjoint carries, per-interval dv and dh, parameter partials. */
+size_t ews_chain_workspace_bytes(const ews_chain_desc* desc);
+
+/* Forward: path (B, L, d) f32, clock (B, L) f32, A (d, d) f32 row-major (reference sign; the chains' parameters
+ * are read from A[f][f], A[f+1][f] and A[f][f+1] / A[f][f+2], f each chain's first row, as
+ * jordan_engine.local_terms reads them) -> out. Replaces local_signatures + combine_packed at N = 1 for these
+ * generators (ews/core/leaf.py:50-198, ews/core/kernels/combine.py:193-269). */
+int ews_chain_forward(const ews_chain_desc* desc, const void* path, const float* clock, const float* A, float* out,
+                      void* residual, void* workspace, ews_stream_t stream);
+
+/* Backward: grad_out shaped like out -> grad_path (B, L, d), grad_clock (B, L) (may be NULL) and grad_A (d, d),
+ * written; grad_A is nonzero only at the entries each chain is read from (the chain parameters' gradients, summed
+ * in a fixed order). Replaces JAX autodiff through the leaf and jordan_block_operators and the custom VJP of the
+ * block kernel (pallas_combine.py:1673-1801). */
+int ews_chain_backward(const ews_chain_desc* desc, const void* path, const float* clock, const float* A,
+                       const void* residual, const float* grad_out, float* grad_path, float* grad_clock,
+                       float* grad_A, void* workspace, ews_stream_t stream);
+
+/* ---------------------------------------------------------------------------------------------------------
  * Log-signature readout of LogEWS (ews/layer.py:440-556): per state row the truncated tensor log and its
  * coefficients at the Lyndon words (signax.signature_to_logsignature), then the readout (log-then-pool).
  * --------------------------------------------------------------------------------------------------------- */
