@@ -1,0 +1,244 @@
+// Token-cached scan at depth 1 for cached flows of any width up to 64 (ews/core/token_scan.py:91-118 with trunc 1):
+// S_t = D_{g_t} S_{t-1} + P_{g_t} from S = 0, a padded step keeping the state (D = I, P = 0). D_cache (V, d, d) is a
+// dense flow per token, P_cache (V, d) the token's level 1.
+//
+// Forward: one wavefront per sample, lane i the state coordinate i; a step reads the token's transposed flow (a
+// transposed copy made first, so that lane i reads D[g][i][j] for fixed j from consecutive addresses) against the
+// previous state broadcast through LDS. Backward: one wavefront per sample walks the steps in reverse,
+// lam_t = g_t + D_{t+1}^T lam_{t+1} (lane j reads row i of D[g] contiguously), and stores every step's cotangent;
+// then per token dP_g = sum lam_t and dD_g = sum lam_t S_{t-1}^T over the steps carrying it, from the forward's rows
+// (the states), in per-chunk partials reduced in a fixed order (deterministic).
+#include <hip/hip_runtime.h>
+
+#include "ews_hip.h"
+
+namespace ews {
+namespace tok1 {
+
+constexpr int kMaxD = 64;
+constexpr int kChunk = 2048;  // steps per partial of the token gradients
+constexpr int kStage = 16;    // steps staged in LDS at once
+
+struct TArgs {
+  int B, n, d, V;
+  const int32_t* tokens;  // (B, n)
+  const uint8_t* mask;    // (B, n) or null
+  const float* P;         // (V, d)
+  const float* D;         // (V, d, d)
+  float* Dt;              // (V, d, d) transposed copy (workspace)
+  float* out;             // (B, n, d)
+  const float* rows;      // the forward's rows (backward)
+  const float* gout;      // (B, n, d)
+  float* lam;             // (B, n, d) cotangent of every step's state (workspace)
+  float* part;            // (V, nch, d*d + d) per-chunk partials (workspace)
+  int nch;
+  float* gP;
+  float* gD;
+};
+
+__device__ __forceinline__ int tok_at(const TArgs& a, size_t e, bool& live) {
+  live = a.mask == nullptr || a.mask[e] != 0;
+  const int g = a.tokens[e];
+  return g < 0 ? 0 : (g >= a.V ? a.V - 1 : g);
+}
+
+__global__ void k_transpose(TArgs a) {
+  const size_t e = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const size_t dd = (size_t)a.d * a.d;
+  if (e >= (size_t)a.V * dd) return;
+  const size_t g = e / dd, r = e % dd, i = r / a.d, j = r % a.d;
+  a.Dt[g * dd + j * a.d + i] = a.D[e];
+}
+
+__global__ __launch_bounds__(64) void k_fwd(TArgs a) {
+  __shared__ float s_x[kMaxD];
+  const int b = blockIdx.x, i = threadIdx.x;
+  const bool on = i < a.d;
+  float S = 0.0f;
+  for (int t = 0; t < a.n; ++t) {
+    const size_t e = (size_t)b * a.n + t;
+    bool live;
+    const int g = tok_at(a, e, live);
+    if (on) s_x[i] = S;
+    __syncthreads();
+    if (live && on) {
+      const float* dt = a.Dt + (size_t)g * a.d * a.d + i;  // Dt[g][j][i] = D[g][i][j]
+      float acc = a.P[(size_t)g * a.d + i];
+      for (int j = 0; j < a.d; ++j) acc = fmaf(dt[(size_t)j * a.d], s_x[j], acc);
+      S = acc;
+    }
+    if (on) a.out[e * a.d + i] = S;
+    __syncthreads();  // s_x is rewritten by the next step
+  }
+}
+
+__global__ __launch_bounds__(64) void k_bwd_lam(TArgs a) {
+  __shared__ float s_l[kMaxD];
+  const int b = blockIdx.x, j = threadIdx.x;
+  const bool on = j < a.d;
+  float lam = 0.0f;
+  for (int t = a.n - 1; t >= 0; --t) {
+    const size_t e = (size_t)b * a.n + t;
+    if (on) {
+      lam += a.gout[e * a.d + j];
+      a.lam[e * a.d + j] = lam;
+      s_l[j] = lam;
+    }
+    __syncthreads();
+    bool live;
+    const int g = tok_at(a, e, live);
+    if (live && on) {  // lam_{t-1} carried = D_g^T lam_t: lane j takes column j (row i contiguous over lanes)
+      const float* dg = a.D + (size_t)g * a.d * a.d + j;
+      float acc = 0.0f;
+      for (int i = 0; i < a.d; ++i) acc = fmaf(dg[(size_t)i * a.d], s_l[i], acc);
+      lam = acc;
+    }
+    __syncthreads();
+  }
+}
+
+// partials of token g over steps [c * kChunk, (c + 1) * kChunk) of the flattened (sample, step) order: each thread
+// owns 16 entries of dD_g (d <= 64), threads < d also an entry of dP_g
+__global__ __launch_bounds__(256) void k_grads(TArgs a) {
+  __shared__ float s_l[kStage][kMaxD], s_s[kStage][kMaxD];
+  __shared__ int s_use[kStage];
+  const int g = blockIdx.x, c = blockIdx.y, tid = threadIdx.x;
+  const size_t tot = (size_t)a.B * a.n, e0 = (size_t)c * kChunk, e1 = min(tot, e0 + kChunk);
+  const int dd = a.d * a.d;
+  float acc[16], accp = 0.0f;
+#pragma unroll
+  for (int k = 0; k < 16; ++k) acc[k] = 0.0f;
+  for (size_t s0 = e0; s0 < e1; s0 += kStage) {
+    // stage the block's steps that carry token g: their cotangents and the states before them
+    for (int q = tid; q < kStage * kMaxD; q += 256) {
+      const int r = q / kMaxD, col = q % kMaxD;
+      const size_t e = s0 + r;
+      bool use = false;
+      if (e < e1) {
+        bool live;
+        use = tok_at(a, e, live) == g && live;
+      }
+      if (col == 0) s_use[r] = use;
+      float lv = 0.0f, sv = 0.0f;
+      if (use && col < a.d) {
+        lv = a.lam[e * a.d + col];
+        const size_t t = e % a.n;
+        sv = t > 0 ? a.rows[(e - 1) * a.d + col] : 0.0f;  // S_{t-1} (zero before the first step)
+      }
+      s_l[r][col] = lv;
+      s_s[r][col] = sv;
+    }
+    __syncthreads();
+    for (int r = 0; r < kStage; ++r) {
+      if (!s_use[r]) continue;  // uniform across the workgroup
+#pragma unroll
+      for (int k = 0; k < 16; ++k) {
+        const int q = tid + 256 * k;
+        if (q < dd) acc[k] = fmaf(s_l[r][q / a.d], s_s[r][q % a.d], acc[k]);
+      }
+      if (tid < a.d) accp += s_l[r][tid];
+    }
+    __syncthreads();
+  }
+  float* out = a.part + ((size_t)g * a.nch + c) * (dd + a.d);
+#pragma unroll
+  for (int k = 0; k < 16; ++k) {
+    const int q = tid + 256 * k;
+    if (q < dd) out[q] = acc[k];
+  }
+  if (tid < a.d) out[dd + tid] = accp;
+}
+
+// the chunks' partials summed in order, float64
+__global__ void k_reduce(TArgs a) {
+  const int dd = a.d * a.d, W = dd + a.d;
+  const size_t e = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (e >= (size_t)a.V * W) return;
+  const size_t g = e / W, q = e % W;
+  double s = 0.0;
+  for (int c = 0; c < a.nch; ++c) s += (double)a.part[((size_t)g * a.nch + c) * W + q];
+  if ((int)q < dd) a.gD[g * dd + q] = (float)s;
+  else a.gP[g * a.d + (q - dd)] = (float)s;
+}
+
+}  // namespace tok1
+
+namespace {
+int tok1_check(const ews_token1_desc* s) {
+  if (!s) return EWS_ERR_NULL;
+  if (s->batch < 1 || s->steps < 1 || s->dim < 1 || s->dim > tok1::kMaxD || s->vocab < 1) return EWS_ERR_SHAPE;
+  return EWS_OK;
+}
+size_t al256t(size_t x) { return (x + 255) & ~(size_t)255; }
+tok1::TArgs tok1_args(const ews_token1_desc* s) {
+  tok1::TArgs a{};
+  a.B = s->batch;
+  a.n = s->steps;
+  a.d = s->dim;
+  a.V = s->vocab;
+  a.nch = (int)(((size_t)a.B * a.n + tok1::kChunk - 1) / tok1::kChunk);
+  return a;
+}
+}  // namespace
+}  // namespace ews
+
+extern "C" {
+
+size_t ews_token1_workspace_bytes(const ews_token1_desc* desc) {
+  if (ews::tok1_check(desc) != EWS_OK) return 0;
+  const ews::tok1::TArgs a = ews::tok1_args(desc);
+  const size_t dd = (size_t)a.d * a.d;
+  return ews::al256t((size_t)a.V * dd * 4) + ews::al256t((size_t)a.B * a.n * a.d * 4) +
+         ews::al256t((size_t)a.V * a.nch * (dd + a.d) * 4);
+}
+
+int ews_token1_scan(const ews_token1_desc* desc, const int32_t* tokens, const uint8_t* mask, const float* P_cache,
+                    const float* D_cache, float* out, void* workspace, ews_stream_t stream) {
+  const int rc = ews::tok1_check(desc);
+  if (rc != EWS_OK) return rc;
+  if (!tokens || !P_cache || !D_cache || !out || !workspace) return EWS_ERR_NULL;
+  ews::tok1::TArgs a = ews::tok1_args(desc);
+  a.tokens = tokens;
+  a.mask = mask;
+  a.P = P_cache;
+  a.D = D_cache;
+  a.Dt = (float*)workspace;
+  a.out = out;
+  hipStream_t st = (hipStream_t)stream;
+  const size_t nd = (size_t)a.V * a.d * a.d;
+  hipLaunchKernelGGL(ews::tok1::k_transpose, dim3((unsigned)((nd + 255) / 256)), dim3(256), 0, st, a);
+  if (hipGetLastError() != hipSuccess) return EWS_ERR_LAUNCH;
+  hipLaunchKernelGGL(ews::tok1::k_fwd, dim3(a.B), dim3(64), 0, st, a);
+  return hipGetLastError() == hipSuccess ? EWS_OK : EWS_ERR_LAUNCH;
+}
+
+int ews_token1_scan_backward(const ews_token1_desc* desc, const int32_t* tokens, const uint8_t* mask,
+                             const float* P_cache, const float* D_cache, const float* out, const float* grad_out,
+                             float* grad_P, float* grad_D, void* workspace, ews_stream_t stream) {
+  const int rc = ews::tok1_check(desc);
+  if (rc != EWS_OK) return rc;
+  if (!tokens || !P_cache || !D_cache || !out || !grad_out || !grad_P || !grad_D || !workspace) return EWS_ERR_NULL;
+  ews::tok1::TArgs a = ews::tok1_args(desc);
+  a.tokens = tokens;
+  a.mask = mask;
+  a.P = P_cache;
+  a.D = D_cache;
+  a.rows = out;
+  a.gout = grad_out;
+  a.gP = grad_P;
+  a.gD = grad_D;
+  const size_t dd = (size_t)a.d * a.d;
+  char* w = (char*)workspace;
+  a.lam = (float*)(w + ews::al256t((size_t)a.V * dd * 4));
+  a.part = (float*)(w + ews::al256t((size_t)a.V * dd * 4) + ews::al256t((size_t)a.B * a.n * a.d * 4));
+  hipStream_t st = (hipStream_t)stream;
+  hipLaunchKernelGGL(ews::tok1::k_bwd_lam, dim3(a.B), dim3(64), 0, st, a);
+  if (hipGetLastError() != hipSuccess) return EWS_ERR_LAUNCH;
+  hipLaunchKernelGGL(ews::tok1::k_grads, dim3(a.V, a.nch), dim3(256), 0, st, a);
+  if (hipGetLastError() != hipSuccess) return EWS_ERR_LAUNCH;
+  const size_t W = (size_t)a.V * (dd + a.d);
+  hipLaunchKernelGGL(ews::tok1::k_reduce, dim3((unsigned)((W + 255) / 256)), dim3(256), 0, st, a);
+  return hipGetLastError() == hipSuccess ? EWS_OK : EWS_ERR_LAUNCH;
+}
+
+}  // extern "C"

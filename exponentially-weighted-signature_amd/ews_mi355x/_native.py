@@ -79,6 +79,9 @@ EXPORTED = (
     "ews_chain_workspace_bytes",
     "ews_chain_forward",
     "ews_chain_backward",
+    "ews_token1_workspace_bytes",
+    "ews_token1_scan",
+    "ews_token1_scan_backward",
 )
 
 JORDAN_KINDS = {"real": 0, "complex": 1}
@@ -153,6 +156,15 @@ class ChainDesc(ctypes.Structure):
         ("level0", ctypes.c_int32),
         ("series_q", ctypes.c_int32),
         ("chunk", ctypes.c_int32),
+    ]
+
+
+class Token1Desc(ctypes.Structure):
+    _fields_ = [
+        ("batch", ctypes.c_int32),
+        ("steps", ctypes.c_int32),
+        ("dim", ctypes.c_int32),
+        ("vocab", ctypes.c_int32),
     ]
 
 
@@ -343,6 +355,13 @@ def load():
     lib.ews_chain_forward.restype = i32
     lib.ews_chain_backward.argtypes = [chp, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp]
     lib.ews_chain_backward.restype = i32
+    t1p = ctypes.POINTER(Token1Desc)
+    lib.ews_token1_workspace_bytes.argtypes = [t1p]
+    lib.ews_token1_workspace_bytes.restype = sz
+    lib.ews_token1_scan.argtypes = [t1p, vp, vp, vp, vp, vp, vp, vp]
+    lib.ews_token1_scan.restype = i32
+    lib.ews_token1_scan_backward.argtypes = [t1p, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp]
+    lib.ews_token1_scan_backward.restype = i32
     _lib = lib
     return lib
 

@@ -352,6 +352,33 @@ int ews_chain_backward(const ews_chain_desc* desc, const void* path, const float
                        float* grad_A, void* workspace, ews_stream_t stream);
 
 /* ---------------------------------------------------------------------------------------------------------
+ * Token-cached scan at depth 1 for any width up to 64 (ews/core/token_scan.py:91-118 with trunc 1): from dense
+ * per-token caches, P_cache (V, d) the level 1 of each token's segment and D_cache (V, d, d) its flow,
+ * S_t = D_{g_t} S_{t-1} + P_{g_t} from S = 0; a padded step (mask 0) keeps the state (D = I, unit signature).
+ * --------------------------------------------------------------------------------------------------------- */
+typedef struct ews_token1_desc {
+  int32_t batch; /* B >= 1 */
+  int32_t steps; /* n >= 1 scan steps (tokens) per sample */
+  int32_t dim;   /* d: 1..64 */
+  int32_t vocab; /* V >= 1; ids are clamped to [0, V) */
+} ews_token1_desc;
+
+/* Scratch of both directions: a transposed flow cache, every step's cotangent, per-chunk token partials. */
+size_t ews_token1_workspace_bytes(const ews_token1_desc* desc);
+
+/* tokens (B, n) int32, mask (B, n) uint8 or NULL, caches f32 -> out (B, n, d) f32, the packed prefix states
+ * (no level-0 column). Replaces token_cached_prefix_scan (ews/core/token_scan.py:91-118) at trunc 1. */
+int ews_token1_scan(const ews_token1_desc* desc, const int32_t* tokens, const uint8_t* mask, const float* P_cache,
+                    const float* D_cache, float* out, void* workspace, ews_stream_t stream);
+
+/* Backward: the forward's out (its states) and grad_out (B, n, d) -> grad_P (V, d), grad_D (V, d, d), written,
+ * summed over every step carrying the token in a fixed order (deterministic). Replaces JAX autodiff through the
+ * scan's gather (token_scan.py:104-118). */
+int ews_token1_scan_backward(const ews_token1_desc* desc, const int32_t* tokens, const uint8_t* mask,
+                             const float* P_cache, const float* D_cache, const float* out, const float* grad_out,
+                             float* grad_P, float* grad_D, void* workspace, ews_stream_t stream);
+
+/* ---------------------------------------------------------------------------------------------------------
  * Log-signature readout of LogEWS (ews/layer.py:440-556): per state row the truncated tensor log and its
  * coefficients at the Lyndon words (signax.signature_to_logsignature), then the readout (log-then-pool).
  * --------------------------------------------------------------------------------------------------------- */

@@ -38,3 +38,19 @@ def token_cached_prefix_scan(token_ids, mask, P_cache, D_cache, dim, trunc):
     eye = torch.eye(dim, dtype=D_cache.dtype).expand(L, dim, dim)
     D = torch.where(on[:, None, None], D_cache[token_ids], eye)
     return O.chen_scan_prefix(O.unpack(P, dim, trunc), D)
+
+
+def token_cached_prefix_scan_depth1(token_ids, mask, P_cache, D_cache):
+    """ews/core/token_scan.py:91-118 at trunc 1, batched: token_ids (B, L), mask (B, L) or None -> (B, L, d).
+    At depth 1 mult(apply_M(S, D), P) is D S + P, so the scan is S_t = D_{g_t} S_{t-1} + P_{g_t} from zero, a padded
+    step keeping the state. Pinned to token_cached_prefix_scan (the packed Chen loop) in tests/test_oracle_token.py."""
+    B, L = token_ids.shape
+    on = torch.ones(B, L, dtype=torch.bool) if mask is None else mask.to(torch.bool).expand(B, L)
+    S = torch.zeros(B, P_cache.shape[1], dtype=P_cache.dtype)
+    rows = []
+    for t in range(L):
+        g = token_ids[:, t]
+        nxt = torch.bmm(D_cache[g], S[:, :, None])[:, :, 0] + P_cache[g]
+        S = torch.where(on[:, t, None], nxt, S)
+        rows.append(S)
+    return torch.stack(rows, 1)

@@ -13,7 +13,9 @@ Bars: forward max relative error <= 1e-5, gradients <
       weather (weather_results/config.json: m = 64, 16 complex chains of size 4, the series leaf, exact flows,
       uniform time clock; B = 16, L = 720);
       rotation planes at m = 64 with the Van Loan leaf (M = 4, exact exponentials; the formal-language blocks,
-      formal_language_results/even_pairs/config.json), every reweighting mode.
+      formal_language_results/even_pairs/config.json), every reweighting mode;
+      the formal-language token block itself: build_token_cache at m = 64 (the chain kernels) and the depth-1
+      cached scan (csrc/ews_token1.hip) against oracle/token_oracle.py, B = 256 sequences of 512 tokens.
 """
 
 import numpy as np
@@ -217,3 +219,47 @@ def test_wide_planes_van_loan(mode):
     print(f"planes m={2 * K} van_loan {mode}", flush=True)
     _layer_check(layer, gpu, ref, path, clock,
                  lambda p, c, A: CO.chain_depth1(p, c, A, "complex", 2, step, step), seed=3)
+
+
+@pytest.mark.parametrize("leaf", ["van_loan", "series"])
+def test_formal_language_token_block(leaf):
+    """formal_language_results/even_pairs/config.json: the token-cached block at depth 1, m = 64 rotation planes,
+    Van Loan M = 4 with exact exponentials (and the series leaf); B = 256 sequences of 512 tokens, vocabulary 8,
+    padded tails. build_token_cache (the chain kernels) then token_cached_prefix_scan (the depth-1 cached scan)
+    against oracle/token_oracle.py (the cache from the oracle's Van Loan / series leaf and matrix_exp flows; the
+    batched depth-1 scan pinned to the packed Chen loop): forward and the gradients of the token displacements,
+    clock increments and plane parameters."""
+    from oracle import token_oracle as TO
+
+    B, n, V, K = 256, 512, 8, 32
+    d = 2 * K
+    rng = np.random.default_rng(77)
+    v = torch.tensor(rng.normal(size=K), dtype=torch.float32)
+    u = torch.tensor(rng.normal(size=K), dtype=torch.float32)
+    gpu = E.AParamDampedRotation(v.clone(), u.clone(), d, omega_scale=2.0).to(DEV)
+    ref = E.AParamDampedRotation(v.double(), u.double(), d, omega_scale=2.0)
+    dx = torch.tensor(rng.normal(size=(V, d)) * 0.3, dtype=torch.float32)
+    dth = torch.tensor(rng.uniform(0.05, 0.4, size=V), dtype=torch.float32)
+    tok = torch.tensor(rng.integers(0, V, size=(B, n)), dtype=torch.int64)
+    lens = rng.integers(n // 4, n + 1, size=B)
+    mask = torch.tensor(np.arange(n)[None, :] < lens[:, None])
+    q = 3 if leaf == "series" else None  # an order low enough that the truncation shows at these steps
+    print(f"token block m={d} V={V} B={B} n={n} leaf={leaf}", flush=True)
+    gx = dx.to(DEV).requires_grad_(True)
+    gt = dth.to(DEV).requires_grad_(True)
+    P, Dc = E.build_token_cache(gx, gt, gpu(), 4, 1, "exact", "exact", leaf, q)
+    out = E.token_cached_prefix_scan(tok.to(DEV), mask.to(DEV), P, Dc, d, 1)
+    rx = dx.double().requires_grad_(True)
+    rt = dth.double().requires_grad_(True)
+    Pr, Dr = TO.build_token_cache(rx, rt, ref(), 4, 1, "exact", "exact", leaf, q)
+    want = TO.token_cached_prefix_scan_depth1(tok, mask, Pr, Dr)
+    errs = dict(P=relerr(P, Pr), D=relerr(Dc, Dr), fwd=relerr(out, want))
+    w = torch.tensor(rng.normal(size=tuple(want.shape)) / np.sqrt(d))
+    (out * w.to(DEV, torch.float32)).sum().backward()
+    (want * w).sum().backward()
+    errs.update(ddx=relerr(gx.grad, rx.grad), ddtheta=relerr(gt.grad, rt.grad))
+    errs.update({f"dA_{i}": relerr(g.grad, h.grad) for i, (g, h) in enumerate(zip(gpu.parameters(),
+                                                                               ref.parameters()))})
+    print("  " + ", ".join(f"{k} {x:.2e}" for k, x in errs.items()), flush=True)
+    assert max(errs["P"], errs["D"], errs["fwd"]) < 1e-5, errs
+    assert max(x for k, x in errs.items() if k not in ("P", "D", "fwd")) < 1e-4, errs

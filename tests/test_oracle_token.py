@@ -66,3 +66,22 @@ def test_one_token_stream_is_a_geometric_recursion():
     for t in range(6):
         x = D[2] @ x + P[2]
         np.testing.assert_allclose(got[t].detach().numpy(), x.detach().numpy(), rtol=1e-12)
+
+
+def test_depth1_batched_scan_equals_the_packed_chen_loop():
+    """The batched depth-1 form (D S + P) against the per-sample packed Chen loop, with masks, forward and
+    gradients."""
+    rng = np.random.default_rng(31)
+    B, L, d, V = 3, 17, 5, 4
+    P = torch.tensor(rng.normal(size=(V, d)), dtype=DT, requires_grad=True)
+    Dc = torch.tensor(rng.normal(size=(V, d, d)) * 0.4, dtype=DT, requires_grad=True)
+    tok = torch.tensor(rng.integers(0, V, size=(B, L)))
+    mask = torch.tensor(np.arange(L)[None, :] < np.array([L, 11, 5])[:, None])
+    a = TO.token_cached_prefix_scan_depth1(tok, mask, P, Dc)
+    b = torch.stack([TO.token_cached_prefix_scan(tok[i], mask[i], P, Dc, d, 1) for i in range(B)])
+    assert float((a - b).abs().max()) < 1e-13
+    w = torch.tensor(rng.normal(size=(B, L, d)), dtype=DT)
+    ga = torch.autograd.grad((a * w).sum(), [P, Dc])
+    gb = torch.autograd.grad((b * w).sum(), [P, Dc])
+    for x, y in zip(ga, gb):
+        assert float((x - y).abs().max()) < 1e-12
