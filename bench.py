@@ -186,27 +186,77 @@ def bench_diag_cfg(args):
         lws = torch.empty(max(16, int(lib.ews_log_workspace_bytes(ctypes.byref(ldesc)))), device=dev,
                           dtype=torch.uint8)
         names = names + ["log_forward"]
+    # the fused route: the scan's output pass runs the epilogue on its rows in LDS (ews_diag_mixer_forward), and the
+    # backward regenerates the rows from the float64 carries (pass 2) for the mixer's backward, as
+    # ews_mi355x.ops.ScanMixerFn does
+    fused_mix = mix and not args.mixer_composed and bool(lib.ews_diag_uses_chunk_kernels(ctypes.byref(desc)))
     if mix:
         from ews_mi355x.mixer import MixerEpilogue
-        from ews_mi355x.ops import MixerFn
+        from ews_mi355x.ops import MixerFn, _mixer_param_grads
 
         hidden = d
         mixer = MixerEpilogue(d, N, hidden).to(dev)
         with torch.no_grad():
             mixer.c_down.weight.normal_(0.0, 1.0 / np.sqrt(D))
         mW, mb, mg = mixer.c_down.weight, mixer.c_down.bias, mixer.graded.gains
-        names = names + ["mixer_forward"]
+        if fused_mix:
+            eps3 = (ctypes.c_float * 3)(*[float(x) for x in (list(mixer.graded.eps) + [0.0] * 3)[:3]])
+            mdesc = nat.MixerDesc(B, L - 1, d, N, 1, hidden, nat.GRADED_VARIANTS["live_rms"], 1, 0, eps3)
+            mres = torch.empty(int(lib.ews_mixer_residual_bytes(ctypes.byref(mdesc))), device=dev, dtype=torch.uint8)
+            mout = torch.empty((B, L, hidden), device=dev, dtype=torch.float32)
+            names = ["scan_mixer_forward"]
+        else:
+            names = names + ["mixer_forward"]
     if bwd:
         gsrc = torch.randn((B, L - 1, Dlog if log else W), device=dev, dtype=torch.float32)
         gout = torch.empty((B, L - 1, W), device=dev, dtype=torch.float32) if (log and not fused_log) else gsrc
         if mix:
             gmix = torch.randn((B, L, hidden), device=dev, dtype=torch.float32)
+        if fused_mix:
+            grows = torch.empty_like(out)
+            dots = torch.empty((B, L - 1, N), device=dev, dtype=torch.float32)
         dpath = torch.empty((B, L, d), device=dev, dtype=torch.float32)
         dA = torch.empty_like(A)
-        names = (names + (["log_backward"] if log and not fused_log else []) + (["mixer_backward"] if mix else [])
-                 + (["sequential_backward"] if seq else BWD_PASS_NAMES[:nb]))
+        names = (names + (["log_backward"] if log and not fused_log else []) + (["rows_regenerate"] if fused_mix else [])
+                 + (["mixer_backward"] if mix else []) + (["sequential_backward"] if seq else BWD_PASS_NAMES[:nb]))
+
+    def step_fused(events=None):
+        st = ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream)
+        i = 0
+
+        def mark():
+            nonlocal i
+            if events is not None:
+                events[i].record()
+            i += 1
+
+        mark()
+        nat.check(lib.ews_diag_mixer_forward(ctypes.byref(desc), ctypes.byref(mdesc), path.data_ptr(),
+                                             clock.data_ptr(), A.data_ptr(), mW.data_ptr(), mb.data_ptr(),
+                                             mg.data_ptr(), mout.data_ptr(), mres.data_ptr(), resid.data_ptr(),
+                                             ws.data_ptr(), st), "scan + mixer forward")
+        if bwd:
+            mark()
+            nat.check(lib.ews_diag_forward_pass(ctypes.byref(desc), 2, path.data_ptr(), clock.data_ptr(),
+                                                A.data_ptr(), out.data_ptr(), resid.data_ptr(), ws.data_ptr(), st),
+                      "rows regenerate")
+            mark()
+            nat.check(lib.ews_mixer_backward(ctypes.byref(mdesc), out.data_ptr(), mW.data_ptr(), mres.data_ptr(),
+                                             gmix.data_ptr(), grows.data_ptr(), dots.data_ptr(), st),
+                      "mixer backward")
+            _mixer_param_grads(gmix, out, mW, mg, mres, dots, d, N, "live_rms", 1, 1)
+            for p in range(nb):
+                mark()
+                nat.check(lib.ews_diag_backward_pass(ctypes.byref(desc), p, path.data_ptr(), clock.data_ptr(),
+                                                     A.data_ptr(), resid.data_ptr(), grows.data_ptr(),
+                                                     dpath.data_ptr(), None, dA.data_ptr(), ws.data_ptr(), st),
+                          "backward pass")
+        if events is not None:
+            events[i].record()
 
     def step(events=None):
+        if fused_mix:
+            return step_fused(events)
         st = ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream)
         i = 0
         for p in range(nf):
@@ -310,6 +360,11 @@ def bench_diag_cfg(args):
     if mix:
         ab["mixer_forward"] = n * 4 * (W + hidden)        # read state rows, write the hidden-wide rows
         ab["mixer_backward"] = n * 4 * (2 * W + hidden)   # read state rows and output cotangents, write row cotangents
+        # fused: read the path and clock, write the hidden-wide rows and the mixer's residual (N level products of
+        # hidden entries and 3 factors per level, per row); the backward first rewrites the rows (chunk_output)
+        ab["scan_mixer_forward"] = n * (s_in * (d + 1) + 4 * (hidden * (1 + N) + 3 * N))
+        ab["rows_regenerate"] = ab["chunk_output"]
+    if mix and not fused_mix:
         # the same epilogue composed from torch ops (what a host-side block does), forward + backward, same rows
         x_t = out.detach().requires_grad_(True)
 
@@ -335,7 +390,10 @@ def bench_diag_cfg(args):
         total = ab["fwd_total"] + (ab["bwd_total"] if bwd else 0)
     if log and not fused_log:
         total += ab["log_forward"] + (ab["log_backward"] if bwd else 0)
-    if mix:
+    if fused_mix:
+        total = ab["scan_mixer_forward"] + ((ab["rows_regenerate"] + ab["mixer_backward"] + ab["bwd_total"])
+                                           if bwd else 0)
+    elif mix:
         total += ab["mixer_forward"] + (ab["mixer_backward"] if bwd else 0)
     what = {"c1": "c1: single EWS layer, B=8, L=1024, 3 time-augmented channels lifted to d=8, real diagonal A, "
                   "depth 2, fp32, prefix readout, forward",
@@ -347,7 +405,9 @@ def bench_diag_cfg(args):
         what = what.replace("LogEWS compression (prefix)", "LogEWS compression (prefix, log rows written by the scan)")
     if mix:
         what = (what.replace("EWS scan + LogEWS compression (prefix)", "EWS scan")
-                + f", then the mixer epilogue (drop level 0, zero row, GradedRMSNorm live_rms, c_down to {hidden})")
+                + f", then the mixer epilogue (drop level 0, zero row, GradedRMSNorm live_rms, c_down to {hidden})"
+                + (" fused into the scan's output pass (rows regenerated for the backward)" if fused_mix else
+                   " reading the scan's rows"))
     return {
         "metric": "EWS " + ("forward" if not bwd else "forward+backward") + " time-steps/sec and HBM GB/s (% peak) "
                   "on 1 MI355X",
@@ -372,7 +432,8 @@ def bench_diag_cfg(args):
         "passes_ms": {k: round(v, 4) for k, v in pass_ms.items()},
         **({"mixer_epilogue_torch_ops_fwd_bwd_ms": torch_mix,
             "mixer_epilogue_fused_fwd_bwd_ms": round(pass_ms["mixer_forward"] + pass_ms.get("mixer_backward", 0.0), 4)}
-           if mix else {}),
+           if mix and not fused_mix else {}),
+        **({"mixer_route": "fused" if fused_mix else "composed"} if mix else {}),
     }
 
 
@@ -686,6 +747,9 @@ def main():
     ap.add_argument("--mixer", action="store_true",
                     help="c4 / c5: the block's mixer epilogue (GradedRMSNorm + c_down, hidden = d) after the scan, "
                          "in place of c4's LogEWS readout")
+    ap.add_argument("--mixer-composed", action="store_true",
+                    help="with --mixer: the scan's rows written, then the epilogue (ews_mixer_forward) reading them, "
+                         "in place of the fused route (ews_diag_mixer_forward) where the scan runs on the chunk kernels")
     ap.add_argument("--front", action="store_true",
                     help="c2: start from the raw 6-channel path: the block front (time clock, lift B 6 -> 16) on the "
                          "device before the scan and its backward (raw-path and B gradients) after it")

@@ -520,6 +520,260 @@ __global__ __launch_bounds__(MAXT) void k_chunk_fwd(DiagArgs a) {
   }
 }
 
+// ------------------------------------------------------------------------------------------- F3 + mixer
+// The output pass with the block's mixer epilogue in it (ews/block.py:282-306, 336-357, 405-408; ews/norms.py:47-134;
+// the same arithmetic as csrc/ews_mixer.hip k_mix_fwd): the chunk's prefix rows are staged in LDS kMixRB at a
+// time, without their level-0 column, and contracted there against c_down on fp32 MFMA, so that only the
+// hidden-wide rows and the mixer's residual (each level's products P_k, its scale and two derivative factors per
+// row) reach memory; the D-wide rows are never written. The wavefronts of the workgroup split each level's 16-entry
+// column blocks between them, and their partial products are summed through LDS. r = b + sum_k f_k P_k with
+// P_k = W_k x_k on the unscaled row and f_k the level's prescale times its GradedRMSNorm factor.
+constexpr int kMixRB = 16;  // rows staged per block (one MFMA row tile)
+constexpr int kMixHT = 4;   // hidden tiles of 16: c_down up to 64 wide
+constexpr int kMixNW = 4;   // wavefronts sharing the contraction (the others wait at its barriers)
+typedef float mf4 __attribute__((ext_vector_type(4)));
+typedef float mf4u __attribute__((ext_vector_type(4), aligned(4)));
+
+struct MixEpi {
+  const float* weight;  // (H, D) row-major: c_down's weight
+  const float* bias;    // (H,)
+  const float* gains;   // (N,) GradedRMSNorm gains, or (1,) lam for dilation
+  float* out;           // (B, R + prepend, H)
+  float* P;             // (B R, N, H) level products
+  float* F;             // (B R, N, 3): scale, beta, d scale / d gain
+  int H, variant, prepend, prescale;
+  float eps[2];
+};
+
+__device__ __forceinline__ mf4 mix_load4(const float* p, int k, int end, bool ok) {
+  if (!ok) return mf4{0.0f, 0.0f, 0.0f, 0.0f};
+  if (k + 3 < end) {
+    const mf4u v = *reinterpret_cast<const mf4u*>(p + k);
+    return mf4{v.x, v.y, v.z, v.w};
+  }
+  return mf4{k < end ? p[k] : 0.0f, k + 1 < end ? p[k + 1] : 0.0f, k + 2 < end ? p[k + 2] : 0.0f,
+             k + 3 < end ? p[k + 3] : 0.0f};
+}
+
+__device__ __forceinline__ int mix_pitch(int D) { return ((D + 3) & ~3) + 4; }
+
+// x[k .. k+3] of a staged row: one 16-byte LDS read when the run starts on a 16-byte boundary (al: the level
+// starts on one, as every level does when d is a multiple of 4, and the row pitch and k0 are multiples of 4); the
+// row pitch (4 mod 32 words in 16-byte units: 7 mod 8) keeps the 16 rows of a read on distinct bank groups
+__device__ __forceinline__ mf4 mix_lds4(const float* p, int k, int end, bool ok, bool al) {
+  if (ok && al && k + 3 < end) return *reinterpret_cast<const mf4*>(p + k);
+  return mix_load4(p, k, end, ok);
+}
+
+// The mixer epilogue of rows tb .. tb + nr - 1 of the chunk staged in s_rows (row pitch Dp, levels without level 0).
+template <int N, int NH>
+__device__ __forceinline__ void mix_block(const DiagArgs& a, const MixEpi& e, int b, int t0, int nr,
+                                          const float* s_rows, float* s_red, float* s_ssq, float* s_fac) {
+  const int tid = threadIdx.x, NW = min(blockDim.x >> 6, kMixNW), w = tid >> 6, l = tid & 63, i = l & 15,
+            g = l >> 4;
+  const int Dp = mix_pitch(a.D), NHT = (e.H + 15) >> 4, Hp = NHT * 16;
+  const bool rok = i < nr, wok = w < NW, al = (a.d & 3) == 0;  // wok: uniform over the wavefront
+  const float* xr = s_rows + (size_t)i * Dp;
+  mf4 acc[N][NH];
+  float ssq[N];
+#pragma unroll
+  for (int k = 0; k < N; ++k) {
+    ssq[k] = 0.0f;
+#pragma unroll
+    for (int h = 0; h < NH; ++h) acc[k][h] = mf4{0.0f, 0.0f, 0.0f, 0.0f};
+  }
+#pragma unroll
+  for (int k = 0; k < N; ++k) {
+    const int st = k == 0 ? 0 : a.d, n = k == 0 ? a.d : a.d * a.d, en = st + n;
+#pragma unroll 2
+    for (int k0 = st + 16 * w; wok && k0 < en; k0 += 16 * NW) {  // the wavefront's 16-entry blocks of the level
+      const int kk = k0 + 4 * g;
+      const mf4 xa = mix_lds4(xr, kk, en, rok, al);
+      ssq[k] = fmaf(xa.x, xa.x, fmaf(xa.y, xa.y, fmaf(xa.z, xa.z, fmaf(xa.w, xa.w, ssq[k]))));
+#pragma unroll
+      for (int h = 0; h < NH; ++h) {
+        if (h < NHT) {  // uniform
+          const int hrow = 16 * h + i;
+          const bool hok = hrow < e.H;
+          const mf4 wb = mix_load4(e.weight + (size_t)(hok ? hrow : 0) * a.D, kk, en, hok);
+          acc[k][h] = __builtin_amdgcn_mfma_f32_16x16x4f32(xa.x, wb.x, acc[k][h], 0, 0, 0);
+          acc[k][h] = __builtin_amdgcn_mfma_f32_16x16x4f32(xa.y, wb.y, acc[k][h], 0, 0, 0);
+          acc[k][h] = __builtin_amdgcn_mfma_f32_16x16x4f32(xa.z, wb.z, acc[k][h], 0, 0, 0);
+          acc[k][h] = __builtin_amdgcn_mfma_f32_16x16x4f32(xa.w, wb.w, acc[k][h], 0, 0, 0);
+        }
+      }
+    }
+  }
+  __syncthreads();  // s_red overlays the staged rows
+  // the wavefront's partial products (lane: rows 4g + r of column 16h + i) and partial sums of squares
+#pragma unroll
+  for (int k = 0; k < N && wok; ++k) {
+#pragma unroll
+    for (int h = 0; h < NH; ++h) {
+      if (h < NHT) {
+        float* rp = s_red + (((size_t)w * N + k) * 16) * Hp + 16 * h + i;
+        rp[(4 * g + 0) * Hp] = acc[k][h].x;
+        rp[(4 * g + 1) * Hp] = acc[k][h].y;
+        rp[(4 * g + 2) * Hp] = acc[k][h].z;
+        rp[(4 * g + 3) * Hp] = acc[k][h].w;
+      }
+    }
+    float v = ssq[k];
+    v += __shfl_xor(v, 16, 64);
+    v += __shfl_xor(v, 32, 64);
+    if (g == 0) s_ssq[((size_t)w * N + k) * 16 + i] = v;
+  }
+  __syncthreads();
+  // per-row factors of each level (the arithmetic of k_mix_fwd)
+#pragma unroll 1
+  for (int q = tid; q < nr * N; q += blockDim.x) {
+    const int r = q / N, k = q % N, K = k + 1;
+    float v = 0.0f;
+    for (int ww = 0; ww < NW; ++ww) v += s_ssq[((size_t)ww * N + k) * 16 + r];
+    const int t = t0 + r;  // the row within its sample
+    const size_t gr = (size_t)b * a.n_int + t;
+    float c = 1.0f;
+    if (e.prescale) {  // 1 / C(max(t + 1, K), K) with t counted from the levels' first row; K <= 2: the product
+      const double tl = fmax((double)(t + 1 + e.prepend), (double)K);
+      c = (float)(K == 1 ? 1.0 / tl : 2.0 / (tl * (tl - 1.0)));
+    }
+    const int nk = K == 1 ? a.d : a.d * a.d;
+    float f, beta = 0.0f, dfdg;
+    if (e.variant == EWS_GRADED_LIVE_RMS) {
+      const float gk = e.gains[k];
+      const float ms = v / (float)nk;
+      const float rho = ms > 0.0f ? sqrtf(ms) : 0.0f;
+      const float den = fmaf(c, rho, e.eps[k]);
+      dfdg = c / den;
+      f = gk * dfdg;
+      if (rho > 0.0f) beta = gk * c * c / (den * den * (float)nk * rho);
+    } else if (e.variant == EWS_GRADED_STATIC_GAIN) {
+      dfdg = c;
+      f = e.gains[k] * c;
+    } else {
+      const float lam = e.gains[0];
+      const float lk1 = powf(lam, (float)(K - 1));
+      dfdg = (float)K * lk1 * c;
+      f = lk1 * lam * c;
+    }
+    s_fac[r * N + k] = f;
+    float* fp = e.F + (gr * N + k) * 3;
+    fp[0] = f;
+    fp[1] = beta;
+    fp[2] = dfdg;
+  }
+  __syncthreads();
+  // output rows and the level products
+#pragma unroll 1
+  for (int q = tid; q < nr * e.H; q += blockDim.x) {
+    const int r = q / e.H, col = q % e.H, t = t0 + r;
+    const size_t gr = (size_t)b * a.n_int + t;
+    float v = e.bias[col];
+#pragma unroll
+    for (int k = 0; k < N; ++k) {
+      float pv = 0.0f;
+      for (int ww = 0; ww < NW; ++ww) pv += s_red[(((size_t)ww * N + k) * 16 + r) * Hp + col];
+      v = fmaf(s_fac[r * N + k], pv, v);
+      e.P[(gr * N + k) * e.H + col] = pv;
+    }
+    e.out[((size_t)b * (a.n_int + e.prepend) + t + e.prepend) * e.H + col] = v;
+  }
+}
+
+// LDS of k_chunk_mix: increments and steps, kMixRB staged rows (then, in the same space, the wavefronts' partial
+// products), the partial sums of squares and the rows' factors
+__host__ __device__ __forceinline__ size_t mix_rows_floats(int D, int NT, int N, int H) {
+  const size_t rows = (size_t)kMixRB * (((D + 3) & ~3) + 4);
+  const size_t red = (size_t)min((NT + 63) / 64, kMixNW) * N * 16 * (((H + 15) / 16) * 16);
+  return rows > red ? rows : red;
+}
+__host__ __device__ __forceinline__ size_t mix_lds_floats(int T, int d, int D, int NT, int N, int H) {
+  const int NW = min((NT + 63) / 64, kMixNW);
+  return (size_t)T * d + ((T + 3) & ~3) + mix_rows_floats(D, NT, N, H) + (size_t)NW * N * 16 + (size_t)kMixRB * N;
+}
+
+template <bool CPLX, int N, int MAXT, bool FAST, int NH>
+__global__ __launch_bounds__(MAXT) void k_chunk_mix(DiagArgs a, MixEpi e) {
+  using T = typename Types<CPLX>::T;
+  extern __shared__ float smem[];
+  const int NW = min((int)(blockDim.x >> 6), kMixNW), Hp = ((e.H + 15) >> 4) * 16, Dp = mix_pitch(a.D);
+  float* s_v = smem;
+  float* s_h = s_v + a.T * a.d;
+  float* s_rows = s_h + ((a.T + 3) & ~3);
+  float* s_red = s_rows;  // after the contraction
+  float* s_ssq = s_rows + mix_rows_floats(a.D, blockDim.x, N, e.H);
+  float* s_fac = s_ssq + NW * N * 16;
+  const int c = blockIdx.x, b = blockIdx.y, tid = threadIdx.x;
+  // the chunk's class (written by the summary pass): the other instantiation owns it (uniform over the workgroup)
+  if (((a.cflag[b * a.C + c] & 1) != 0) != FAST) return;
+  const int t0 = c * a.T;
+  const int Tc = min(a.T, a.n_int - t0);
+  load_chunk(a, b, t0, Tc, s_v, s_h);
+  __syncthreads();
+  const LaneMap m = lane_map(a, tid);  // lanes past the pairs join the barriers of the mixer blocks
+  const ChunkClock cc = chunk_clock<T>(a, b, Tc, s_h);
+  T dummy{};
+  const T uj = load_u(a.params, m.j, &dummy);
+  const T uk = load_u(a.params, m.k, &dummy);
+  T S1 = zero<T>(), SA = zero<T>(), SB = zero<T>();
+  {
+    const double* cr = a.carries + ((size_t)b * (a.C + 1) + c) * a.D;
+    S1 = ldTd<CPLX, T>(cr + st1<CPLX>(m.j));
+    if (N == 2) {
+      const double* p2 = cr + st2<CPLX>(a, m.j, m.k);
+      if (CPLX) {
+        SA = ldTd<CPLX, T>(p2);
+        SB = ldTd<CPLX, T>(p2 + 2);
+      } else {
+        SB = ldTd<CPLX, T>(p2);
+      }
+    }
+  }
+  Coef<T> c0;
+  CoefD<T> q;
+  if constexpr (FAST) eval_coef<T, CPLX, N, true>(a.sq1, a.sq2, cc.hbar, cc.href, cc.per_int, uj, uk, c0, q);
+  for (int tb = 0; tb < Tc; tb += kMixRB) {
+    const int nr = min(kMixRB, Tc - tb);
+#pragma unroll 1
+    for (int s = 0; s < nr; ++s) {
+      const int t = tb + s;
+      const float h = s_h[t];
+      Coef<T> co;
+      if constexpr (FAST) {
+        lin_coef<T, CPLX, N>(c0, q, h - cc.hbar, cc.per_int, co);
+      } else {
+        CoefD<T> qq;
+        eval_coef<T, CPLX, N, false>(a.sq1, a.sq2, h, cc.href, cc.per_int, uj, uk, co, qq);
+      }
+      const T pj = lds_p<T>(s_v, t, a.d, m.j);
+      const T pk = (N == 2) ? lds_p<T>(s_v, t, a.d, m.k) : zero<T>();
+      fwd_step<T, CPLX, N>(co, pj, pk, S1, SA, SB);
+      if (!m.active) continue;
+      float* row = s_rows + (size_t)s * Dp;  // levels without level 0: level 1 at 0, level 2 at d
+      if (m.plane) {
+        if constexpr (CPLX) {
+          *reinterpret_cast<float2*>(row + st1<CPLX>(m.j)) = float2{re(S1), im(S1)};
+        } else {
+          row[st1<CPLX>(m.j)] = re(S1);
+        }
+      }
+      if (N == 2) {
+        if constexpr (CPLX) {  // 8-byte stores: d is even and the row pitch a multiple of 4
+          const cf sa = SA, sb = SB;
+          float* r0 = row + a.d + (2 * m.j) * a.d + 2 * m.k;
+          *reinterpret_cast<float2*>(r0) = float2{0.5f * (sa.re + sb.re), 0.5f * (sb.im - sa.im)};
+          *reinterpret_cast<float2*>(r0 + a.d) = float2{0.5f * (sa.im + sb.im), 0.5f * (sa.re - sb.re)};
+        } else {
+          row[a.d + m.j * a.d + m.k] = re(SB);
+        }
+      }
+    }
+    __syncthreads();
+    mix_block<N, NH>(a, e, b, t0 + tb, nr, s_rows, s_red, s_ssq, s_fac);
+    __syncthreads();  // the next block restages the rows
+  }
+}
+
 // ------------------------------------------------------------------------------------------- F2
 // Exact chunk flow (float64): per-interval flows multiply to exp(u (theta_end - theta_start)).
 __device__ __forceinline__ double chunk_tau(const DiagArgs& a, int b, int c, int Tc) {
@@ -2265,6 +2519,41 @@ int dispatch_backward(const Plan& p, const DiagArgs& a, hipStream_t st, int pass
 constexpr int kForwardPasses = 4;
 constexpr int kBackwardPasses = 5;
 
+// ------------------------------------------------------------------------------------------- scan + mixer epilogue
+// the leading zero row of a sample's levels maps to c_down's bias alone
+__global__ void k_mix_bias_rows_fused(MixEpi e, int n_int) {
+  for (int col = threadIdx.x; col < e.H; col += blockDim.x)
+    e.out[(size_t)blockIdx.x * (n_int + 1) * e.H + col] = e.bias[col];
+}
+
+template <bool CPLX, int N, int MAXT, int NH>
+int mix_launch(const Plan& p, const DiagArgs& a, const MixEpi& e, hipStream_t st) {
+  const size_t lds = mix_lds_floats(p.T, p.d, p.D, p.NT, N, e.H) * 4;
+  for (auto fn : {&k_chunk_mix<CPLX, N, MAXT, true, NH>, &k_chunk_mix<CPLX, N, MAXT, false, NH>}) {
+    if (lds > 65536 && hipFuncSetAttribute(reinterpret_cast<const void*>(fn),
+                                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) != hipSuccess)
+      return EWS_ERR_LAUNCH;
+  }
+  const dim3 grid(p.C, p.B), blk(p.NT);
+  hipLaunchKernelGGL((k_chunk_mix<CPLX, N, MAXT, true, NH>), grid, blk, lds, st, a, e);
+  EWS_LAUNCH_CHECK();
+  hipLaunchKernelGGL((k_chunk_mix<CPLX, N, MAXT, false, NH>), grid, blk, lds, st, a, e);
+  EWS_LAUNCH_CHECK();
+  return EWS_OK;
+}
+
+template <bool CPLX, int N, int MAXT>
+int mix_pass(const Plan& p, const DiagArgs& a, const MixEpi& e, hipStream_t st) {
+  // hidden tiles of 16: two when c_down is at most 32 wide, else four
+  const int rc = e.H <= 32 ? mix_launch<CPLX, N, MAXT, 2>(p, a, e, st) : mix_launch<CPLX, N, MAXT, 4>(p, a, e, st);
+  if (rc != EWS_OK) return rc;
+  if (e.prepend) {
+    hipLaunchKernelGGL(k_mix_bias_rows_fused, dim3(p.B), dim3(64), 0, st, e, p.n_int);
+    EWS_LAUNCH_CHECK();
+  }
+  return EWS_OK;
+}
+
 // ------------------------------------------------------------------------------------------- allocation-free forward
 // Scratch of ews_diag_forward_noalloc: the forward's residual and workspace in one file-scope device array, of which
 // every GPU the library runs on holds its own copy until the process ends. On the host, `scratch` names a host-side
@@ -2365,6 +2654,57 @@ int ews_diag_backward(const ews_diag_desc* desc, const void* path, const float* 
 }
 
 int ews_diag_num_passes(int direction) { return direction == 0 ? kForwardPasses : kBackwardPasses; }
+
+int ews_diag_uses_chunk_kernels(const ews_diag_desc* desc) {
+  Plan p;
+  if (make_plan(desc, p) != EWS_OK) return 0;
+  return (!p.fast && !p.seq && !p.log) ? 1 : 0;
+}
+
+int ews_diag_mixer_forward(const ews_diag_desc* desc, const ews_mixer_desc* mdesc, const void* path,
+                           const float* clock, const float* params, const float* weight, const float* bias,
+                           const float* gains, float* out, void* mixer_residual, void* residual, void* workspace,
+                           ews_stream_t stream) {
+  Plan p;
+  const int rc = make_plan(desc, p);
+  if (rc != EWS_OK) return rc;
+  if (!mdesc) return EWS_ERR_NULL;
+  if (!path || !clock || !params || !weight || !bias || !gains || !out || !mixer_residual || !residual || !workspace)
+    return EWS_ERR_NULL;
+  // the chunk kernels' prefix rows only (the pair-group and per-sample kernels write their rows themselves)
+  if (p.fast || p.seq || p.log || desc->readout != EWS_READOUT_PREFIX) return EWS_ERR_OPTION;
+  if (mdesc->batch != p.B || mdesc->rows != p.n_int || mdesc->dim != p.d || mdesc->depth != p.N) return EWS_ERR_SHAPE;
+  if (mdesc->hidden < 1 || mdesc->hidden > 16 * kMixHT || mdesc->variant < 0 || mdesc->variant > 2)
+    return EWS_ERR_OPTION;
+  if (mix_lds_floats(p.T, p.d, p.D, p.NT, p.N, mdesc->hidden) * 4 > kMaxLds) return EWS_ERR_SHAPE;
+  DiagArgs a = make_args(desc, p, path, clock, params, residual, workspace);
+  hipStream_t st = (hipStream_t)stream;
+  for (int pass = 0; pass < 2; ++pass) {  // chunk summaries and the float64 carries
+    const int r = dispatch_forward(desc, p, a, st, pass);
+    if (r != EWS_OK) return r;
+  }
+  MixEpi e{};
+  e.weight = weight;
+  e.bias = bias;
+  e.gains = gains;
+  e.out = out;
+  const size_t M = (size_t)p.B * p.n_int;
+  e.P = (float*)mixer_residual;  // the layout of ews_mixer_residual_bytes: products, then factors
+  e.F = (float*)((char*)mixer_residual + align256(M * p.N * mdesc->hidden * 4));
+  e.H = mdesc->hidden;
+  e.variant = mdesc->variant;
+  e.prepend = mdesc->prepend ? 1 : 0;
+  e.prescale = mdesc->prescale ? 1 : 0;
+  e.eps[0] = mdesc->eps[0];
+  e.eps[1] = mdesc->eps[1];
+  const bool big = p.NT > 256;
+  if (p.cplx) {
+    if (p.N == 2) return big ? mix_pass<true, 2, 1024>(p, a, e, st) : mix_pass<true, 2, 256>(p, a, e, st);
+    return mix_pass<true, 1, 256>(p, a, e, st);
+  }
+  if (p.N == 2) return big ? mix_pass<false, 2, 1024>(p, a, e, st) : mix_pass<false, 2, 256>(p, a, e, st);
+  return mix_pass<false, 1, 256>(p, a, e, st);
+}
 
 int ews_diag_forward_status(const ews_diag_desc* desc, const void* residual, int* status, ews_stream_t stream) {
   Plan p;

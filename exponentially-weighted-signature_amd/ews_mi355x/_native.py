@@ -82,6 +82,8 @@ EXPORTED = (
     "ews_token1_workspace_bytes",
     "ews_token1_scan",
     "ews_token1_scan_backward",
+    "ews_diag_mixer_forward",
+    "ews_diag_uses_chunk_kernels",
 )
 
 JORDAN_KINDS = {"real": 0, "complex": 1}
@@ -355,6 +357,10 @@ def load():
     lib.ews_chain_forward.restype = i32
     lib.ews_chain_backward.argtypes = [chp, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp]
     lib.ews_chain_backward.restype = i32
+    lib.ews_diag_mixer_forward.argtypes = [dp, ctypes.POINTER(MixerDesc), vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp]
+    lib.ews_diag_mixer_forward.restype = i32
+    lib.ews_diag_uses_chunk_kernels.argtypes = [dp]
+    lib.ews_diag_uses_chunk_kernels.restype = i32
     t1p = ctypes.POINTER(Token1Desc)
     lib.ews_token1_workspace_bytes.argtypes = [t1p]
     lib.ews_token1_workspace_bytes.restype = sz

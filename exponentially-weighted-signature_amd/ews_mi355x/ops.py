@@ -534,20 +534,122 @@ class MixerFn(torch.autograd.Function):
         nat.check(lib.ews_mixer_backward(ctypes.byref(desc), rows.data_ptr(), weight.data_ptr(), resid.data_ptr(),
                                          gout.data_ptr(), grows.data_ptr(), dots.data_ptr(),
                                          _stream_handle(rows.device)), "ews_mixer_backward")
-        # residual: level products (M, N, hidden) then factors (M, N, 3) = (scale, beta, d scale / d gain)
-        F = resid[_al256(M * N * hidden * 4):].view(torch.float32)[: M * N * 3].view(M, N, 3)
-        dr = gout[:, prepend:, :].reshape(M, hidden)
-        gbias = gout.sum((0, 1))
-        gd = (F[:, :, 2] * dots.reshape(M, N)).sum(0)
-        ggains = gd.sum().reshape(gains.shape) if variant == "dilation" else gd
-        gweight = torch.empty_like(weight)
-        st = 0
-        for k in range(N):
-            n = d ** (k + 1)
-            xk = rows[:, :, level0 + st: level0 + st + n].reshape(M, n)  # a strided view, no copy
-            gweight[:, st: st + n] = _split_k_tn(dr * F[:, k, 0:1], xk)
-            st += n
+        gweight, gbias, ggains = _mixer_param_grads(gout, rows, weight, gains, resid, dots, d, N, variant, prepend,
+                                                    level0)
         return grows, gweight, gbias, ggains, None, None, None, None, None, None, None
+
+
+def _mixer_param_grads(gout, rows, weight, gains, resid, dots, d, N, variant, prepend, level0):
+    """c_down's and the gains' gradients from the per-row quantities of ews_mixer_backward: grad_bias = sum of
+    grad_out, grad_gains = sum of row_dots times the gain factor, grad_weight per level = (scale_k grad_out)^T x_k."""
+    B, R, W = rows.shape
+    hidden = weight.shape[0]
+    M = B * R
+    # residual: level products (M, N, hidden) then factors (M, N, 3) = (scale, beta, d scale / d gain)
+    F = resid[_al256(M * N * hidden * 4):].view(torch.float32)[: M * N * 3].view(M, N, 3)
+    dr = gout[:, prepend:, :].reshape(M, hidden)
+    gbias = gout.sum((0, 1))
+    gd = (F[:, :, 2] * dots.reshape(M, N)).sum(0)
+    ggains = gd.sum().reshape(gains.shape) if variant == "dilation" else gd
+    gweight = torch.empty_like(weight)
+    st = 0
+    for k in range(N):
+        n = d ** (k + 1)
+        xk = rows[:, :, level0 + st: level0 + st + n].reshape(M, n)  # a strided view, no copy
+        gweight[:, st: st + n] = _split_k_tn(dr * F[:, k, 0:1], xk)
+        st += n
+    return gweight, gbias, ggains
+
+
+class ScanMixerFn(torch.autograd.Function):
+    """The diagonal / rotation-plane scan's prefix rows straight into the block's mixer epilogue
+    (ews_diag_mixer_forward): out = c_down(graded(prescale(levels))) with the D-wide rows never written. The
+    backward regenerates the rows from the scan's float64 carries (ews_diag_forward_pass, pass 2), then runs the
+    mixer's backward (ews_mixer_backward) and the scan's (ews_diag_backward)."""
+
+    @staticmethod
+    def forward(ctx, path, clock, params, weight, bias, gains, N, structure, flow_mode, leaf, series_q, variant, eps,
+                prepend, prescale):
+        lib = nat.load()
+        _check_inputs(path, clock, params)
+        for nm, t in (("weight", weight), ("bias", bias), ("gains", gains)):
+            if not t.is_cuda or t.dtype != torch.float32:
+                raise TypeError(f"{nm} must be a float32 tensor on the HIP device")
+        path = _aligned(path.contiguous())
+        clock, params, weight = clock.contiguous(), params.contiguous(), weight.contiguous()
+        bias, gains = bias.contiguous(), gains.contiguous()
+        B, L, d = path.shape
+        hidden = weight.shape[0]
+        dt = nat.DTYPE_BF16 if path.dtype == torch.bfloat16 else nat.DTYPE_F32
+        sdesc = make_desc(B, L, d, N, structure, flow_mode, "prefix", True, dt, 0, leaf, series_q)
+        eps3 = (ctypes.c_float * 3)(*[float(x) for x in (list(eps) + [0.0] * 3)[:3]])
+        mdesc = nat.MixerDesc(B, L - 1, d, N, 1, hidden, nat.GRADED_VARIANTS[variant], int(prepend), int(prescale),
+                              eps3)
+        dev = path.device
+        out = torch.empty((B, L - 1 + int(prepend), hidden), device=dev, dtype=torch.float32)
+        mres = torch.empty(int(lib.ews_mixer_residual_bytes(ctypes.byref(mdesc))), device=dev, dtype=torch.uint8)
+        sres = torch.empty(int(lib.ews_diag_residual_bytes(ctypes.byref(sdesc))), device=dev, dtype=torch.uint8)
+        ws = torch.empty(int(lib.ews_diag_workspace_bytes(ctypes.byref(sdesc))), device=dev, dtype=torch.uint8)
+        nat.check(lib.ews_diag_mixer_forward(ctypes.byref(sdesc), ctypes.byref(mdesc), path.data_ptr(),
+                                             clock.data_ptr(), params.data_ptr(), weight.data_ptr(), bias.data_ptr(),
+                                             gains.data_ptr(), out.data_ptr(), mres.data_ptr(), sres.data_ptr(),
+                                             ws.data_ptr(), _stream_handle(dev)), "ews_diag_mixer_forward")
+        ctx.save_for_backward(path, clock, params, weight, gains, sres, mres)
+        ctx.meta = (sdesc, mdesc, d, N, variant, int(prepend))
+        return out
+
+    @staticmethod
+    def backward(ctx, gout):
+        lib = nat.load()
+        path, clock, params, weight, gains, sres, mres = ctx.saved_tensors
+        sdesc, mdesc, d, N, variant, prepend = ctx.meta
+        gout = gout.to(torch.float32).contiguous()
+        B, L, _ = path.shape
+        dev = path.device
+        st = _stream_handle(dev)
+        ws = torch.empty(int(lib.ews_diag_workspace_bytes(ctypes.byref(sdesc))), device=dev, dtype=torch.uint8)
+        # the prefix rows again, from the forward's carries (the chunk output pass)
+        rows = torch.empty((B, L - 1, 1 + d + (d * d if N == 2 else 0)), device=dev, dtype=torch.float32)
+        nat.check(lib.ews_diag_forward_pass(ctypes.byref(sdesc), 2, path.data_ptr(), clock.data_ptr(),
+                                            params.data_ptr(), rows.data_ptr(), sres.data_ptr(), ws.data_ptr(), st),
+                  "ews_diag_forward_pass")
+        grows = torch.empty_like(rows)
+        dots = torch.empty((B, L - 1, N), device=dev, dtype=torch.float32)
+        nat.check(lib.ews_mixer_backward(ctypes.byref(mdesc), rows.data_ptr(), weight.data_ptr(), mres.data_ptr(),
+                                         gout.data_ptr(), grows.data_ptr(), dots.data_ptr(), st),
+                  "ews_mixer_backward")
+        gweight, gbias, ggains = _mixer_param_grads(gout, rows, weight, gains, mres, dots, d, N, variant, prepend, 1)
+        del rows
+        dpath = torch.empty((B, L, d), device=dev, dtype=torch.float32)
+        dclock = torch.empty((B, L), device=dev, dtype=torch.float32) if ctx.needs_input_grad[1] else None
+        dparams = torch.empty_like(params)
+        nat.check(lib.ews_diag_backward(ctypes.byref(sdesc), path.data_ptr(), clock.data_ptr(), params.data_ptr(),
+                                        sres.data_ptr(), grows.data_ptr(), dpath.data_ptr(),
+                                        dclock.data_ptr() if dclock is not None else None, dparams.data_ptr(),
+                                        ws.data_ptr(), st), "ews_diag_backward")
+        return (dpath.to(path.dtype), dclock, dparams, gweight, gbias, ggains, None, None, None, None, None, None,
+                None, None, None)
+
+
+def scan_mixer(path, clock, params, weight, bias, gains, N, structure, flow_mode="per_interval",
+               leaf="plane_closed", series_q=0, variant="live_rms", eps=(1e-3,), prepend=True, prescale=False):
+    """The EWS scan's prefix rows (diagonal or rotation-plane generator) through the block's mixer epilogue, fused
+    (ews_diag_mixer_forward) where the scan runs on the chunk kernels; None where it does not (the d = 16
+    pair-group planes, the per-sample sequential kernels): the caller composes diag_scan and mixer_epilogue."""
+    lib = nat.load()
+    fm = {"per_interval": nat.FLOW_PER_INTERVAL, "cached": nat.FLOW_CACHED,
+          "cached_basepoint": nat.FLOW_CACHED_BASEPOINT}[flow_mode]
+    st = {"planes": nat.STRUCT_PLANES, "real_diag": nat.STRUCT_REAL_DIAG}[structure]
+    B, L, d = path.shape
+    if weight.shape[0] > 64 or N not in (1, 2):
+        return None
+    dt = nat.DTYPE_BF16 if path.dtype == torch.bfloat16 else nat.DTYPE_F32
+    probe = make_desc(B, L, d, N, st, fm, "prefix", True, dt, 0, nat.DIAG_LEAVES[leaf], int(series_q or 0))
+    if not lib.ews_diag_uses_chunk_kernels(ctypes.byref(probe)):
+        return None
+    eps = tuple(eps) if isinstance(eps, (tuple, list)) else (float(eps),) * N
+    return ScanMixerFn.apply(path, clock, params, weight, bias, gains, int(N), st, fm, nat.DIAG_LEAVES[leaf],
+                             int(series_q or 0), variant, eps, bool(prepend), bool(prescale))
 
 
 def _split_k_tn(a, b, chunks=64):
