@@ -192,7 +192,7 @@ def bench_diag_cfg(args):
     fused_mix = mix and not args.mixer_composed and bool(lib.ews_diag_uses_chunk_kernels(ctypes.byref(desc)))
     if mix:
         from ews_mi355x.mixer import MixerEpilogue
-        from ews_mi355x.ops import MixerFn, _mixer_param_grads
+        from ews_mi355x.ops import MixerFn, _mixer_backward
 
         hidden = d
         mixer = MixerEpilogue(d, N, hidden).to(dev)
@@ -241,10 +241,7 @@ def bench_diag_cfg(args):
                                                 A.data_ptr(), out.data_ptr(), resid.data_ptr(), ws.data_ptr(), st),
                       "rows regenerate")
             mark()
-            nat.check(lib.ews_mixer_backward(ctypes.byref(mdesc), out.data_ptr(), mW.data_ptr(), mres.data_ptr(),
-                                             gmix.data_ptr(), grows.data_ptr(), dots.data_ptr(), st),
-                      "mixer backward")
-            _mixer_param_grads(gmix, out, mW, mg, mres, dots, d, N, "live_rms", 1, 1)
+            _mixer_backward(lib, mdesc, gmix, out, mW, mg, mres, grows, dots, d, N, "live_rms", 1, 1, st)
             for p in range(nb):
                 mark()
                 nat.check(lib.ews_diag_backward_pass(ctypes.byref(desc), p, path.data_ptr(), clock.data_ptr(),

@@ -47,6 +47,7 @@ struct MArgs {
   const float* gout;
   float* grows;
   float* dots;  // (B R, N)
+  float* dwpart;  // (row chunks, hidden, D) partial c_down weight gradients of the column kernel
 };
 
 __device__ __forceinline__ f4 mfma(float a, float b, f4 c) {
@@ -302,23 +303,21 @@ __global__ __launch_bounds__(256) void k_mix_bwd(MArgs a) {
 constexpr int BW_HB = 8;    // hidden blocks of 16 held in registers: hidden <= 128 (4 up to 64)
 constexpr int BW_RC = 32;   // row tiles per workgroup chunk
 
+// a lane per row and level: the dot of the level's products with the row's cotangent, in 16-byte runs
 __global__ __launch_bounds__(256) void k_mix_bwd_dots(MArgs a) {
-  const int l = threadIdx.x & 63, i = l & 15, g = l >> 4, w = threadIdx.x >> 6;
   const int M = a.B * a.R;
-  const int gr = (blockIdx.x * 4 + w) * 16 + i;
-  const bool valid = gr < M;
-  const float* drp = a.gout + (valid ? out_row(a, gr) : 0) * a.hidden;
-  for (int k = 0; k < a.N; ++k) {
-    float dot = 0.0f;
-    if (valid) {
-      const float* pp = a.P + ((size_t)gr * a.N + k) * a.hidden;
-      for (int h = g; h < a.hidden; h += 4) dot = fmaf(pp[h], drp[h], dot);
-    }
-    dot += __shfl_xor(dot, 16, 64);
-    dot += __shfl_xor(dot, 32, 64);
-    if (valid && g == 0) a.dots[(size_t)gr * a.N + k] = dot;
+  const int q = blockIdx.x * blockDim.x + threadIdx.x;
+  if (q >= M * a.N) return;
+  const int gr = q / a.N, k = q - gr * a.N;
+  const float* drp = a.gout + out_row(a, gr) * a.hidden;
+  const float* pp = a.P + ((size_t)gr * a.N + k) * a.hidden;
+  float dot = 0.0f;
+  for (int h = 0; h < a.hidden; h += 4) {
+    const f4 p = load4(pp, h, a.hidden, true), r = load4(drp, h, a.hidden, true);
+    dot = fmaf(p.x, r.x, fmaf(p.y, r.y, fmaf(p.z, r.z, fmaf(p.w, r.w, dot))));
   }
-  if (a.lvl0 && valid && g == 0) a.grows[(size_t)gr * a.W] = 0.0f;
+  a.dots[(size_t)gr * a.N + k] = dot;
+  if (a.lvl0 && k == 0) a.grows[(size_t)gr * a.W] = 0.0f;
 }
 
 // XCD-aware order: the hardware deals consecutive workgroups round-robin to the 8 XCDs (each with its own L2);
@@ -329,7 +328,35 @@ __device__ __forceinline__ int xcd_logical(int hw, int total) {
   return (hw & 7) * per + (hw >> 3);
 }
 
-template <int HB>
+// Row access: each wavefront moves its 16 x 32 block of a row tile between memory and a private LDS tile with
+// 16-byte row-segment loads and stores (8 lanes per row: one 128-byte run), and reads it there in the MFMA layout;
+// the next tile's block is loaded into registers while the current one is worked on. A wavefront's LDS tile is its
+// own, so the hand-offs need no workgroup barrier (a wavefront's LDS operations complete in program order).
+// DW: the same pass also accumulates c_down's weight gradient over the chunk, dW[h][c] = sum_rows dr[h] f x[c]
+// (MFMA with the rows as the contraction: A = the output cotangent of rows 4 g + s at hidden column 16 hb + i,
+// B = f x of the lane's own row elements), and writes the chunk's partial; k_mix_dw_reduce sums the partials.
+constexpr int BW_XP = 36;  // LDS row pitch of a wavefront's 16 x 32 tile (16-byte rows, 2-way bank spread)
+
+// orders a wavefront's LDS accesses across lanes: no access moves across it (the hardware keeps a wavefront's LDS
+// operations in program order)
+__device__ __forceinline__ void wave_lds_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+__device__ __forceinline__ f4 ld_row4(const float* p, int c, int nc, bool ok) {
+  // p[c .. c+3] of a row segment whose valid columns end at nc (dword-aligned; unaligned 16-byte loads are fine)
+  if (!ok) return f4{0.0f, 0.0f, 0.0f, 0.0f};
+  if (c + 3 < nc) {
+    const f4u v = *reinterpret_cast<const f4u*>(p + c);
+    return f4{v.x, v.y, v.z, v.w};
+  }
+  return f4{c < nc ? p[c] : 0.0f, c + 1 < nc ? p[c + 1] : 0.0f, c + 2 < nc ? p[c + 2] : 0.0f,
+            c + 3 < nc ? p[c + 3] : 0.0f};
+}
+
+template <int HB, bool DW>
 __global__ __launch_bounds__(256) void k_mix_bwd_cols(MArgs a, int ncolwg, int nchunks) {
   const int w = threadIdx.x >> 6, l = threadIdx.x & 63, i = l & 15, g = l >> 4;
   const int M = a.B * a.R;
@@ -338,11 +365,12 @@ __global__ __launch_bounds__(256) void k_mix_bwd_cols(MArgs a, int ncolwg, int n
   const int cwg = lid % ncolwg, chunk = lid / ncolwg;
   if (chunk >= nchunks) return;  // padding of the grid to a multiple of 8 (uniform over the workgroup)
   // two 16-column tiles per wavefront: a row's 32 columns of one wavefront are one 128-byte run
+  const int cbase = (cwg * 4 + w) * 32;
   int col[2], lev[2];
   bool cok[2];
 #pragma unroll
   for (int ct = 0; ct < 2; ++ct) {
-    col[ct] = (cwg * 4 + w) * 32 + 16 * ct + i;
+    col[ct] = cbase + 16 * ct + i;
     cok[ct] = col[ct] < a.D;
     lev[ct] = 0;
     for (int k = 1; k < a.N; ++k)
@@ -359,27 +387,51 @@ __global__ __launch_bounds__(256) void k_mix_bwd_cols(MArgs a, int ncolwg, int n
         const int h = 16 * hb + 4 * g + s;
         wr[ct][hb][s] = (hb < nhb && cok[ct] && h < a.hidden) ? a.weight[(size_t)h * a.D + col[ct]] : 0.0f;
       }
-  // per-row factors of each level (scale f, correction beta * dot) staged once per row tile for the four
-  // wavefronts, double-buffered: the barrier of tile t + 1 orders every read of tile t before slot t is rewritten
-  __shared__ float s_fb[2][16][3][2];
-  const int t0 = chunk * BW_RC;
-  for (int tt = t0; tt < t0 + BW_RC; ++tt) {
-    const int row0 = tt * 16;
-    if (row0 >= M) break;  // uniform over the workgroup
-    const int slot = tt & 1;
-    if (threadIdx.x < 16 * a.N) {
-      const int r = threadIdx.x % 16, k = threadIdx.x / 16;
-      const int grow = row0 + r;
-      float f = 0.0f, bd = 0.0f;
-      if (grow < M) {
-        const float* fp = a.F + ((size_t)grow * a.N + k) * 3;
-        f = fp[0];
-        bd = fp[1] * a.dots[(size_t)grow * a.N + k];
-      }
-      s_fb[slot][r][k][0] = f;
-      s_fb[slot][r][k][1] = bd;
+  // per-row factors of each level (scale f, correction beta * dot) of the chunk's rows, staged once
+  __shared__ float s_fb[BW_RC * 16][3][2];
+  __shared__ __align__(16) float s_x[4][16][BW_XP];  // each wavefront's row tile: x, then its cotangent
+  __shared__ __align__(16) float s_gt[DW ? 4 : 1][16][DW ? 16 * HB + 4 : 1];  // DW: the tile's output cotangents
+  const int t0 = chunk * BW_RC, tiles = (M + 15) / 16, t1 = min(t0 + BW_RC, tiles);
+  for (int q = threadIdx.x; q < BW_RC * 16 * a.N; q += blockDim.x) {
+    const int r = q / a.N, k = q - r * a.N, grow = t0 * 16 + r;
+    float f = 0.0f, bd = 0.0f;
+    if (grow < M) {
+      const float* fp = a.F + ((size_t)grow * a.N + k) * 3;
+      f = fp[0];
+      bd = fp[1] * a.dots[(size_t)grow * a.N + k];
     }
-    __syncthreads();
+    s_fb[r][k][0] = f;
+    s_fb[r][k][1] = bd;
+  }
+  __syncthreads();
+  float(*sx)[BW_XP] = s_x[w];
+  // row-segment lanes: rows l / 8 and 8 + l / 8 of the tile, columns 4 (l % 8) .. + 3 of the wavefront's block
+  const int sr = l >> 3, sc = 4 * (l & 7);
+  const int nc = a.D - cbase;  // valid columns of the block (<= 0: none)
+  f4 xn[2];
+#pragma unroll
+  for (int q = 0; q < 2; ++q) {
+    const int grow = t0 * 16 + sr + 8 * q;
+    xn[q] = ld_row4(a.rows + (size_t)(grow < M ? grow : 0) * a.W + a.lvl0 + cbase, sc, nc, grow < M && nc > 0);
+  }
+  f4 dacc[DW ? 2 : 1][DW ? HB : 1];
+#pragma unroll
+  for (int ct = 0; ct < (DW ? 2 : 1); ++ct)
+#pragma unroll
+    for (int hb = 0; hb < (DW ? HB : 1); ++hb) dacc[ct][hb] = f4{0.0f, 0.0f, 0.0f, 0.0f};
+  for (int tt = t0; tt < t1; ++tt) {
+    const int row0 = tt * 16, lr0 = row0 - t0 * 16;
+    wave_lds_sync();  // the previous tile's reads of the LDS tile are done
+#pragma unroll
+    for (int q = 0; q < 2; ++q) *reinterpret_cast<f4*>(&sx[sr + 8 * q][sc]) = xn[q];
+    wave_lds_sync();
+    if (tt + 1 < t1) {  // the next tile's block, in flight while this one is worked on
+#pragma unroll
+      for (int q = 0; q < 2; ++q) {
+        const int grow = row0 + 16 + sr + 8 * q;
+        xn[q] = ld_row4(a.rows + (size_t)(grow < M ? grow : 0) * a.W + a.lvl0 + cbase, sc, nc, grow < M && nc > 0);
+      }
+    }
     const int ga = row0 + i;  // A-operand row of this lane
     const float* drp = a.gout + (ga < M ? out_row(a, ga) : 0) * a.hidden;
     f4 acc[2] = {f4{0.0f, 0.0f, 0.0f, 0.0f}, f4{0.0f, 0.0f, 0.0f, 0.0f}};
@@ -387,6 +439,7 @@ __global__ __launch_bounds__(256) void k_mix_bwd_cols(MArgs a, int ncolwg, int n
     for (int hb = 0; hb < HB; ++hb) {
       if (hb < nhb) {
         const f4 da = load4(drp, 16 * hb + 4 * g, a.hidden, ga < M);
+        if constexpr (DW) *reinterpret_cast<f4*>(&s_gt[w][i][16 * hb + 4 * g]) = da;
 #pragma unroll
         for (int ct = 0; ct < 2; ++ct) {
           acc[ct] = mfma(da.x, wr[ct][hb][0], acc[ct]);
@@ -396,20 +449,90 @@ __global__ __launch_bounds__(256) void k_mix_bwd_cols(MArgs a, int ncolwg, int n
         }
       }
     }
+    float fx[2][4];  // f x of the lane's row elements: rows 4 g + r of its two columns (zero past the rows)
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
-      const int row = 4 * g + r, grow = row0 + row;
-      if (grow < M) {
+      const int row = 4 * g + r;
 #pragma unroll
-        for (int ct = 0; ct < 2; ++ct) {
-          if (cok[ct]) {
-            const size_t e = (size_t)grow * a.W + a.lvl0 + col[ct];
-            const float dy = r == 0 ? acc[ct].x : (r == 1 ? acc[ct].y : (r == 2 ? acc[ct].z : acc[ct].w));
-            a.grows[e] = fmaf(s_fb[slot][row][lev[ct]][0], dy, -s_fb[slot][row][lev[ct]][1] * a.rows[e]);
+      for (int ct = 0; ct < 2; ++ct) {
+        float* px = &sx[row][16 * ct + i];
+        const float x = *px;
+        const float f = s_fb[lr0 + row][lev[ct]][0];
+        const float dy = r == 0 ? acc[ct].x : (r == 1 ? acc[ct].y : (r == 2 ? acc[ct].z : acc[ct].w));
+        fx[ct][r] = f * x;
+        *px = fmaf(f, dy, -s_fb[lr0 + row][lev[ct]][1] * x);
+      }
+    }
+    wave_lds_sync();
+#pragma unroll
+    for (int q = 0; q < 2; ++q) {
+      const int grow = row0 + sr + 8 * q;
+      if (grow < M && nc > 0) {
+        const f4 v = *reinterpret_cast<const f4*>(&sx[sr + 8 * q][sc]);
+        float* op = a.grows + (size_t)grow * a.W + a.lvl0 + cbase;
+        if (sc + 3 < nc) {
+          *reinterpret_cast<f4u*>(op + sc) = f4u{v.x, v.y, v.z, v.w};
+        } else {
+          if (sc < nc) op[sc] = v.x;
+          if (sc + 1 < nc) op[sc + 1] = v.y;
+          if (sc + 2 < nc) op[sc + 2] = v.z;
+        }
+      }
+    }
+    if constexpr (DW) {  // A: the cotangent of rows 4 g + s at hidden column 16 hb + i; B: f x
+#pragma unroll
+      for (int hb = 0; hb < HB; ++hb) {
+        if (hb < nhb) {  // uniform
+#pragma unroll
+          for (int s = 0; s < 4; ++s) {
+            const float gt = s_gt[w][4 * g + s][16 * hb + i];  // zero past the rows and the hidden columns
+#pragma unroll
+            for (int ct = 0; ct < 2; ++ct) dacc[ct][hb] = mfma(gt, fx[ct][s], dacc[ct][hb]);
           }
         }
       }
     }
+  }
+  if constexpr (DW) {  // lane: dW rows 16 hb + 4 g + r of its columns
+#pragma unroll
+    for (int ct = 0; ct < 2; ++ct) {
+      if (!cok[ct]) continue;
+#pragma unroll
+      for (int hb = 0; hb < HB; ++hb) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int h = 16 * hb + 4 * g + r;
+          if (hb < nhb && h < a.hidden) {
+            const float v = r == 0 ? dacc[ct][hb].x : (r == 1 ? dacc[ct][hb].y : (r == 2 ? dacc[ct][hb].z : dacc[ct][hb].w));
+            a.dwpart[((size_t)chunk * a.hidden + h) * a.D + col[ct]] = v;
+          }
+        }
+      }
+    }
+  }
+}
+
+// c_down's weight gradient: the chunks' partials summed in float64 in a fixed order (deterministic). A
+// workgroup owns 64 entries; wavefront w sums the w-th sixteenth of the chunks, then the sixteen sums are added in
+// order.
+constexpr int DW_RW = 16;  // wavefronts per reduction workgroup
+__global__ __launch_bounds__(64 * DW_RW) void k_mix_dw_reduce(MArgs a, int nchunks, float* gw) {
+  __shared__ double s_part[DW_RW][64];
+  const int w = threadIdx.x >> 6, l = threadIdx.x & 63;
+  const size_t HD = (size_t)a.hidden * a.D;
+  const size_t e = (size_t)blockIdx.x * 64 + l;
+  const int per = (nchunks + DW_RW - 1) / DW_RW, c0 = w * per, c1 = min(nchunks, c0 + per);
+  double s = 0.0;
+  if (e < HD) {
+#pragma unroll 4
+    for (int c = c0; c < c1; ++c) s += (double)a.dwpart[(size_t)c * HD + e];
+  }
+  s_part[w][l] = s;
+  __syncthreads();
+  if (w == 0 && e < HD) {
+    double t = 0.0;
+    for (int k = 0; k < DW_RW; ++k) t += s_part[k][l];
+    gw[e] = (float)t;
   }
 }
 
@@ -521,6 +644,50 @@ int ews_mixer_forward(const ews_mixer_desc* desc, const float* rows, const float
   return EWS_OK;
 }
 
+size_t ews_mixer_backward_workspace_bytes(const ews_mixer_desc* desc) {
+  MPlan p;
+  if (mixer_plan(desc, p) != EWS_OK || p.a.hidden > 16 * BW_HB) return 0;
+  const int tiles = (p.a.B * p.a.R + 15) / 16, nchunks = (tiles + BW_RC - 1) / BW_RC;
+  return al256m((size_t)nchunks * p.a.hidden * p.a.D * 4);
+}
+
+int ews_mixer_backward_weight(const ews_mixer_desc* desc, const float* rows, const float* weight,
+                              const void* residual, const float* grad_out, float* grad_rows, float* row_dots,
+                              float* grad_weight, void* workspace, ews_stream_t stream) {
+  MPlan p;
+  const int rc = mixer_plan(desc, p);
+  if (rc != EWS_OK) return rc;
+  if (p.a.hidden > 16 * BW_HB) return EWS_ERR_SHAPE;
+  if (!rows || !weight || !residual || !grad_out || !grad_rows || !row_dots || !grad_weight || !workspace)
+    return EWS_ERR_NULL;
+  MArgs a = p.a;
+  a.rows = rows;
+  a.weight = weight;
+  a.P = (float*)((char*)residual + p.P);
+  a.F = (float*)((char*)residual + p.F);
+  a.gout = grad_out;
+  a.grows = grad_rows;
+  a.dots = row_dots;
+  a.dwpart = (float*)workspace;
+  hipStream_t st = (hipStream_t)stream;
+  const int M = a.B * a.R;
+  const dim3 blk(256);
+  hipLaunchKernelGGL(k_mix_bwd_dots, dim3((M * a.N + 255) / 256), blk, 0, st, a);
+  MIX_CHECK();
+  const int tiles = (M + 15) / 16;
+  const int ncolwg = (a.D + 127) / 128, nchunks = (tiles + BW_RC - 1) / BW_RC;
+  const int total = (ncolwg * nchunks + 7) / 8 * 8;
+  if (a.hidden <= 32) hipLaunchKernelGGL((k_mix_bwd_cols<2, true>), dim3(total), blk, 0, st, a, ncolwg, nchunks);
+  else if (a.hidden <= 64) hipLaunchKernelGGL((k_mix_bwd_cols<4, true>), dim3(total), blk, 0, st, a, ncolwg, nchunks);
+  else hipLaunchKernelGGL((k_mix_bwd_cols<BW_HB, true>), dim3(total), blk, 0, st, a, ncolwg, nchunks);
+  MIX_CHECK();
+  const size_t HD = (size_t)a.hidden * a.D;
+  hipLaunchKernelGGL(k_mix_dw_reduce, dim3((unsigned)((HD + 63) / 64)), dim3(64 * DW_RW), 0, st, a, nchunks,
+                     grad_weight);
+  MIX_CHECK();
+  return EWS_OK;
+}
+
 int ews_mixer_backward(const ews_mixer_desc* desc, const float* rows, const float* weight, const void* residual,
                        const float* grad_out, float* grad_rows, float* row_dots, ews_stream_t stream) {
   MPlan p;
@@ -540,13 +707,13 @@ int ews_mixer_backward(const ews_mixer_desc* desc, const float* rows, const floa
   const dim3 blk(256);
   if (a.hidden <= 16 * BW_HB) {
     // rows' dots, then column tiles over chunks of row tiles (column workgroups of a chunk consecutive)
-    hipLaunchKernelGGL(k_mix_bwd_dots, dim3((M + 63) / 64), blk, 0, st, a);
+    hipLaunchKernelGGL(k_mix_bwd_dots, dim3((M * a.N + 255) / 256), blk, 0, st, a);
     MIX_CHECK();
     const int tiles = (M + 15) / 16;
     const int ncolwg = (a.D + 127) / 128, nchunks = (tiles + BW_RC - 1) / BW_RC;
     const int total = (ncolwg * nchunks + 7) / 8 * 8;  // the XCD renumbering needs a multiple of 8
-    if (a.hidden <= 64) hipLaunchKernelGGL(k_mix_bwd_cols<4>, dim3(total), blk, 0, st, a, ncolwg, nchunks);
-    else hipLaunchKernelGGL(k_mix_bwd_cols<BW_HB>, dim3(total), blk, 0, st, a, ncolwg, nchunks);
+    if (a.hidden <= 64) hipLaunchKernelGGL((k_mix_bwd_cols<4, false>), dim3(total), blk, 0, st, a, ncolwg, nchunks);
+    else hipLaunchKernelGGL((k_mix_bwd_cols<BW_HB, false>), dim3(total), blk, 0, st, a, ncolwg, nchunks);
   } else {
     // wider c_down: a wavefront per 16 rows, every column block (c_down re-read per row tile)
     const dim3 grid((M + 63) / 64);

@@ -59,6 +59,8 @@ EXPORTED = (
     "ews_mixer_residual_bytes",
     "ews_mixer_forward",
     "ews_mixer_backward",
+    "ews_mixer_backward_workspace_bytes",
+    "ews_mixer_backward_weight",
     "ews_clock_residual_bytes",
     "ews_clock_workspace_bytes",
     "ews_clock_num_params",
@@ -313,6 +315,10 @@ def load():
     lib.ews_mixer_forward.restype = i32
     lib.ews_mixer_backward.argtypes = [mdp, vp, vp, vp, vp, vp, vp, vp]
     lib.ews_mixer_backward.restype = i32
+    lib.ews_mixer_backward_workspace_bytes.argtypes = [mdp]
+    lib.ews_mixer_backward_workspace_bytes.restype = ctypes.c_size_t
+    lib.ews_mixer_backward_weight.argtypes = [mdp, vp, vp, vp, vp, vp, vp, vp, vp, vp]
+    lib.ews_mixer_backward_weight.restype = i32
     lib.ews_dense_local_terms_backward.argtypes = [ddp, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp]
     lib.ews_dense_local_terms_backward.restype = i32
     lib.ews_token_scan_workspace_bytes.argtypes = [ddp, i32]

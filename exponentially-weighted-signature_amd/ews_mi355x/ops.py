@@ -531,12 +531,38 @@ class MixerFn(torch.autograd.Function):
         M = B * R
         grows = torch.empty_like(rows)
         dots = torch.empty((B, R, N), device=rows.device, dtype=torch.float32)
-        nat.check(lib.ews_mixer_backward(ctypes.byref(desc), rows.data_ptr(), weight.data_ptr(), resid.data_ptr(),
-                                         gout.data_ptr(), grows.data_ptr(), dots.data_ptr(),
-                                         _stream_handle(rows.device)), "ews_mixer_backward")
-        gweight, gbias, ggains = _mixer_param_grads(gout, rows, weight, gains, resid, dots, d, N, variant, prepend,
-                                                    level0)
+        gweight, gbias, ggains = _mixer_backward(lib, desc, gout, rows, weight, gains, resid, grows, dots, d, N,
+                                                 variant, prepend, level0, _stream_handle(rows.device))
         return grows, gweight, gbias, ggains, None, None, None, None, None, None, None
+
+
+def _mixer_backward(lib, desc, gout, rows, weight, gains, resid, grows, dots, d, N, variant, prepend, level0, st):
+    """The mixer's backward: grad_rows and row_dots, and c_down's weight gradient in the same pass over the rows
+    (ews_mixer_backward_weight, hidden <= 128) or from the rows by a GEMM (wider c_down); grad_bias and grad_gains
+    from grad_out and row_dots. Returns (grad_weight, grad_bias, grad_gains)."""
+    nws = int(lib.ews_mixer_backward_workspace_bytes(ctypes.byref(desc)))
+    if nws == 0:
+        nat.check(lib.ews_mixer_backward(ctypes.byref(desc), rows.data_ptr(), weight.data_ptr(), resid.data_ptr(),
+                                         gout.data_ptr(), grows.data_ptr(), dots.data_ptr(), st),
+                  "ews_mixer_backward")
+        return _mixer_param_grads(gout, rows, weight, gains, resid, dots, d, N, variant, prepend, level0)
+    ws = torch.empty(nws, device=rows.device, dtype=torch.uint8)
+    gweight = torch.empty_like(weight)
+    nat.check(lib.ews_mixer_backward_weight(ctypes.byref(desc), rows.data_ptr(), weight.data_ptr(),
+                                            resid.data_ptr(), gout.data_ptr(), grows.data_ptr(), dots.data_ptr(),
+                                            gweight.data_ptr(), ws.data_ptr(), st), "ews_mixer_backward_weight")
+    gbias, ggains = _mixer_bias_gain_grads(gout, gains, resid, dots, N, variant, weight.shape[0])
+    return gweight, gbias, ggains
+
+
+def _mixer_bias_gain_grads(gout, gains, resid, dots, N, variant, hidden):
+    """grad_bias = sum of grad_out; grad_gains = sum over rows of row_dots times the residual's d scale / d gain."""
+    M = dots.numel() // N
+    F = resid[_al256(M * N * hidden * 4):].view(torch.float32)[: M * N * 3].view(M, N, 3)
+    gbias = gout.sum((0, 1))
+    gd = (F[:, :, 2] * dots.reshape(M, N)).sum(0)
+    ggains = gd.sum().reshape(gains.shape) if variant == "dilation" else gd
+    return gbias, ggains
 
 
 def _mixer_param_grads(gout, rows, weight, gains, resid, dots, d, N, variant, prepend, level0):
@@ -615,10 +641,8 @@ class ScanMixerFn(torch.autograd.Function):
                   "ews_diag_forward_pass")
         grows = torch.empty_like(rows)
         dots = torch.empty((B, L - 1, N), device=dev, dtype=torch.float32)
-        nat.check(lib.ews_mixer_backward(ctypes.byref(mdesc), rows.data_ptr(), weight.data_ptr(), mres.data_ptr(),
-                                         gout.data_ptr(), grows.data_ptr(), dots.data_ptr(), st),
-                  "ews_mixer_backward")
-        gweight, gbias, ggains = _mixer_param_grads(gout, rows, weight, gains, mres, dots, d, N, variant, prepend, 1)
+        gweight, gbias, ggains = _mixer_backward(lib, mdesc, gout, rows, weight, gains, mres, grows, dots, d, N,
+                                                 variant, prepend, 1, st)
         del rows
         dpath = torch.empty((B, L, d), device=dev, dtype=torch.float32)
         dclock = torch.empty((B, L), device=dev, dtype=torch.float32) if ctx.needs_input_grad[1] else None

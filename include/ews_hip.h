@@ -445,6 +445,22 @@ int ews_mixer_forward(const ews_mixer_desc* desc, const float* rows, const float
 int ews_mixer_backward(const ews_mixer_desc* desc, const float* rows, const float* weight, const void* residual,
                        const float* grad_out, float* grad_rows, float* row_dots, ews_stream_t stream);
 
+/* ews_mixer_backward that also forms c_down's weight gradient in the same pass over the rows: grad_weight (hidden,
+ * D) = sum over rows of (scale_k grad_out) (x) level k, accumulated per chunk of 512 rows on MFMA into the
+ * workspace and summed in chunk order (float64, deterministic). hidden <= 128 (EWS_ERR_SHAPE above);
+ * workspace of ews_mixer_backward_workspace_bytes (0 for an invalid descriptor or hidden > 128). grad_bias and
+ * grad_gains follow from grad_out and row_dots on the host as above. Replaces the same backward as
+ * ews_mixer_backward together with c_down's weight cotangent (eqx.nn.Linear's, ews/block.py:405-406). */
+size_t ews_mixer_backward_workspace_bytes(const ews_mixer_desc* desc);
+int ews_mixer_backward_weight(const ews_mixer_desc* desc, const float* rows, const float* weight,
+                              const void* residual, const float* grad_out, float* grad_rows, float* row_dots,
+                              float* grad_weight, void* workspace, ews_stream_t stream);
+
+/* 1 when ews_diag_forward runs this configuration on the chunk kernels (where ews_diag_mixer_forward applies), 0
+ * otherwise (the pair-group planes, the per-sample sequential kernels, an invalid descriptor). No counterpart in
+ * the reference: it tells a caller which route of the block's epilogue to take. */
+int ews_diag_uses_chunk_kernels(const ews_diag_desc* desc);
+
 /* The scan of ews_diag_forward (prefix readout) with the mixer epilogue in its output pass: the levels of each
  * prefix row go straight from the scan into GradedRMSNorm and c_down, so that out (B, L-1 + prepend, hidden) and the
  * mixer's residual (as ews_mixer_forward's, ews_mixer_residual_bytes of mdesc) are written and the D-wide prefix
@@ -452,13 +468,8 @@ int ews_mixer_backward(const ews_mixer_desc* desc, const float* rows, const floa
  * are ews_diag_forward's. Runs where the scan runs on the chunk kernels (the configurations that are neither the
  * d = 16 pair-group planes nor the per-sample sequential kernels); elsewhere it returns EWS_ERR_OPTION and the
  * caller composes ews_diag_forward and ews_mixer_forward. hidden <= 64. The backward: the prefix rows regenerated
- * by ews_diag_forward_pass (pass 2) from the same residual, then ews_mixer_backward and ews_diag_backward.
+ * by ews_diag_forward_pass (pass 2) from the same residual, then ews_mixer_backward_weight and ews_diag_backward.
  * Replaces EWSBlock._mixer_levels followed by c_down(graded(...)) (ews/block.py:282-306, 405-408). */
-/* 1 when ews_diag_forward runs this configuration on the chunk kernels (where ews_diag_mixer_forward applies), 0
- * otherwise (the pair-group planes, the per-sample sequential kernels, an invalid descriptor). No counterpart in
- * the reference: it tells a caller which route of the block's epilogue to take. */
-int ews_diag_uses_chunk_kernels(const ews_diag_desc* desc);
-
 int ews_diag_mixer_forward(const ews_diag_desc* desc, const ews_mixer_desc* mdesc, const void* path,
                            const float* clock, const float* params, const float* weight, const float* bias,
                            const float* gains, float* out, void* mixer_residual, void* residual, void* workspace,
