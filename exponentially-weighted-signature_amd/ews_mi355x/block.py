@@ -151,6 +151,9 @@ class EWSBlock(nn.Module):
             self.mixer.c_down.weight.copy_(mixer_c.weight)
             self.mixer.c_down.bias.copy_(mixer_c.bias)
         self.gate = _linear(H, H, gen, dtype) if self.output_gate else None
+        # calls that record no graph run the epilogue inside the scan's output pass where the scan allows it
+        # (EWS.mixed_prefix); False keeps the scan -> epilogue composition for every call
+        self.fused_epilogue = True
         if norm_placement == "pre":
             self.norm1 = RMSNorm(H, norm_eps, dtype)
             self.norm2 = RMSNorm(H, norm_eps, dtype) if self.second_norm else None
@@ -232,8 +235,14 @@ class EWSBlock(nn.Module):
         driver = self._resolve_driver(x, clock_driver)
         branch_in = self.norm1(x) if self.norm_placement == "pre" else x
         path, theta = self.front(branch_in, driver, t=t, mask=mask)
-        rows = self.ewms(path, theta, readout="prefix", output_format="flat", a_scale=a_scale)
-        r = self.mixer(rows)
+        r = None
+        if self.fused_epilogue and not (torch.is_grad_enabled() and _needs_grad(path, theta, self)):
+            # no graph recorded: the scan's output pass runs the epilogue itself (no D-wide rows in memory); a
+            # training step composes the scan and the epilogue, whose backward does not regenerate the rows
+            r = self.ewms.mixed_prefix(path, theta, self.mixer, a_scale=a_scale)
+        if r is None:
+            rows = self.ewms(path, theta, readout="prefix", output_format="flat", a_scale=a_scale)
+            r = self.mixer(rows)
         if self.gate is not None:
             g_in = increment_path(branch_in, mask) if self.path_mode == "increment" else branch_in
             r = r * torch.sigmoid(self.gate(g_in))
@@ -244,6 +253,10 @@ class EWSBlock(nn.Module):
         x = x + self._drop(r, inference)
         xhat = self.norm2(x) if (self.norm_placement == "pre" and self.norm2 is not None) else x
         return x + self._drop(self._channel(xhat), inference)
+
+
+def _needs_grad(path, theta, module):
+    return path.requires_grad or theta.requires_grad or any(p.requires_grad for p in module.parameters())
 
 
 class StackedEWS(nn.Module):

@@ -284,6 +284,26 @@ class EWS(torch.nn.Module):
                              self._flow_mode("prefix"), "log_prefix", False, chunk=0, leaf=leaf,
                              series_q=self.series_q or 0)
 
+    def mixed_prefix(self, path, clock, mixer, a_scale=1.0):
+        """The prefix rows (level 0 included) straight into ``mixer`` (a MixerEpilogue over this layer's width and
+        depth) inside the scan's output pass (ops.scan_mixer): the D-wide rows never reach memory. Applies to rotation
+        planes / real diagonals with exact flows that run on the chunk kernels, depth 1-2 and c_down at most 64 wide;
+        None elsewhere (the caller composes the scan and the mixer)."""
+        if self.structure is None or self.N not in (1, 2) or path.dim() != 3 or self.dtype != torch.float32:
+            return None
+        if mixer.d != self.d or mixer.N != self.N or mixer.hidden_dim > 64 or self._engine_check() != "diag":
+            return None
+        self._check_batch(path, clock)
+        A = self.A_param().to(torch.float32) * torch.as_tensor(a_scale, dtype=torch.float32, device=path.device)
+        params = self._diag_params(A.to(path.device))
+        if path.dtype != torch.bfloat16:
+            path = path.to(torch.float32)
+        leaf = self.leaf if self.leaf in ("series", "block_series") else "plane_closed"
+        return ops.scan_mixer(path, clock.to(torch.float32), params, mixer.c_down.weight, mixer.c_down.bias,
+                              mixer.graded.gain_tensor(), self.N, self.structure, self._flow_mode("prefix"), leaf,
+                              self.series_q or 0, mixer.graded.variant, mixer.graded.eps, not mixer.basepoint,
+                              mixer.graded_prescale == "binomial")
+
     def _levels(self, packed, lead):
         out, s = [], 0
         for k in range(1, self.N + 1):

@@ -57,6 +57,12 @@ def _compare(model, X, bcfgs, scfg, t=None, mask=None, x_grad=False, seed=0, a_s
     Xr = X.double().clone().requires_grad_(True) if x_grad else X
     ref = BO.stack(Xr, P, scfg, bcfgs, fns, t=None if t is None else t.double(), mask=mask, a_scales=a_scales)
     e = relerr(out, ref)
+    # with no graph recorded, blocks whose scan allows it run the epilogue inside the scan's output pass
+    with torch.no_grad():
+        out_ng = model(Xd.detach(), t=None if t is None else t.to(DEV), mask=md, inference=True)
+    e_ng = relerr(out_ng, ref)
+    print(f"  no-grad route: logits {e_ng:.2e}", flush=True)
+    assert e_ng < 1e-5, e_ng
     w = torch.tensor(np.random.default_rng(seed).normal(size=tuple(ref.shape)))
     (out * w.to(DEV, torch.float32)).sum().backward()
     (ref * w).sum().backward()
