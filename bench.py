@@ -640,6 +640,98 @@ def bench_token(args):
     }
 
 
+def _timed(fn, args):
+    import torch
+
+    for _ in range(args.warmup):
+        fn()
+    torch.cuda.synchronize()
+    t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0.record()
+    for _ in range(args.steps):
+        fn()
+    t1.record()
+    torch.cuda.synchronize()
+    return t0.elapsed_time(t1) / args.steps
+
+
+def bench_banked(args):
+    """The reference's banked depth-1 blocks at their widths (survey row f4), through the EWS layer:
+    ppg: ppg_results/config.json's block, B=8 sequences of L=49,920, m=64 as 16 complex Jordan chains of size 4,
+    leaf jordan_closed with jordan_flows, a clamped-gate clock, prefix rows, forward + backward (gradients to the
+    path, the clock and the chain parameters) on the depth-1 chain kernels (csrc/ews_chain.hip);
+    fl: formal_language_results/even_pairs's token block, B=256 sequences of 512 tokens, vocabulary 8, m=64 as 32
+    rotation planes, Van Loan M=4 with exact exponentials: the token cache (chain kernels on 8 one-interval samples)
+    and the depth-1 cached scan (csrc/ews_token1.hip), forward + backward to the token displacements, clock increments
+    and plane parameters."""
+    import torch
+
+    import ews_mi355x as E
+
+    dev = torch.device("cuda:0")
+    rng = np.random.default_rng([7, 0])
+    if args.config == "ppg":
+        B, L, K = 8, 49920, 16
+        ps = [torch.tensor([np.log(np.expm1(rng.uniform(0.005, 0.5))), rng.uniform(-15, 15)], dtype=torch.float32)
+              for _ in range(K)]
+        param = E.AParamJordanRepeated([4] * K, ["complex"] * K, ps).to(dev)
+        path = torch.tensor(np.cumsum(rng.normal(size=(B, L, 4 * K)) / np.sqrt(L), 1), dtype=torch.float32,
+                            device=dev).requires_grad_(True)
+        inc = np.clip(rng.normal(0.5, 0.6, size=(B, L)), 0.0, 1.0) * (2.0 / L)
+        clock = torch.tensor(np.cumsum(inc, 1), dtype=torch.float32, device=dev).requires_grad_(True)
+        layer = E.EWS(param, N=1, leaf="jordan_closed", combine="block_kernel", jordan_flows=True)
+        g = torch.tensor(rng.normal(size=(B, L - 1, 1 + 4 * K)), dtype=torch.float32, device=dev)
+
+        def step():
+            out = layer(path, clock, readout="prefix")
+            out.backward(g)
+
+        n, d = B * (L - 1), 4 * K
+        # read path + clock, write the rows; backward: read the row cotangents, write dpath + dclock
+        traffic = n * (4 * (d + 1) + 4 * (d + 1)) * 2
+        what = ("ppg: B=8, L=49920, m=64 as 16 complex Jordan chains of size 4, depth 1, jordan_closed + "
+                "jordan_flows, clamped-gate clock, prefix rows, forward + backward (path, clock and chain-parameter "
+                "gradients) on the depth-1 chain kernels")
+        steps_per = n
+    else:
+        B, n_tok, V, K = 256, 512, 8, 32
+        d = 2 * K
+        v = torch.tensor(rng.normal(size=K), dtype=torch.float32)
+        u = torch.tensor(rng.normal(size=K), dtype=torch.float32)
+        param = E.AParamDampedRotation(v, u, d, omega_scale=2.0).to(dev)
+        dx = torch.tensor(rng.normal(size=(V, d)) * 0.3, dtype=torch.float32, device=dev).requires_grad_(True)
+        dth = torch.tensor(rng.uniform(0.05, 0.4, size=V), dtype=torch.float32, device=dev).requires_grad_(True)
+        tok = torch.tensor(rng.integers(0, V, size=(B, n_tok)), dtype=torch.int64, device=dev)
+        lens = rng.integers(n_tok // 4, n_tok + 1, size=B)
+        mask = torch.tensor(np.arange(n_tok)[None, :] < lens[:, None], device=dev)
+        g = torch.tensor(rng.normal(size=(B, n_tok, d)) / np.sqrt(d), dtype=torch.float32, device=dev)
+
+        def step():
+            P, Dc = E.build_token_cache(dx, dth, param(), 4, 1, "exact", "exact", "van_loan")
+            out = E.token_cached_prefix_scan(tok, mask, P, Dc, d, 1)
+            out.backward(g)
+
+        # the cached scan's rows and their cotangents, and the backward's per-step cotangents (written, read)
+        traffic = B * n_tok * 4 * d * 4
+        what = ("fl: token block, B=256 x 512 tokens, vocab 8, m=64 as 32 rotation planes, depth 1, van_loan M=4 "
+                "exact, token cache (chain kernels) + depth-1 cached scan, forward + backward (token displacements, "
+                "clock increments, plane parameters)")
+        steps_per = B * n_tok
+    ms = _timed(step, args)
+    gbs = traffic / (ms * 1e-3) / 1e9
+    return {
+        "metric": "EWS forward+backward time-steps/sec and HBM GB/s (% peak) on 1 MI355X",
+        "value": round(steps_per / (ms * 1e-3), 1), "unit": "time-steps/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(ms, 4), "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "f32", "data": "synthetic",
+        "config": {"workload": what, "global_batch": B, "seq_len": L if args.config == "ppg" else n_tok,
+                   "parallelism": "none (1 GPU)"},
+        "roofline": {"bound": "hbm", "kernel": "step", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS,
+                     "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None,
+                     "algorithmic_bytes": traffic},
+    }
+
+
 def algorithmic_bytes(B, L, d, W, s_in=4, split=False):
     """Compulsory HBM bytes per launch of each pass (per-interval figures times B (L-1) intervals). split: the c2
     backward without the clock gradient, whose pass 0 is the full per-step local adjoint (reads the cotangent rows,
@@ -734,10 +826,11 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--check", action="store_true", help="also check one forward against the C float64 checker")
     ap.add_argument("--chunk", type=int, default=0, help="intervals per chunk (0: the library's default)")
-    ap.add_argument("--config", choices=["c2", "c3", "c1", "c4", "c5", "tok"], default="c2",
+    ap.add_argument("--config", choices=["c2", "c3", "c1", "c4", "c5", "tok", "ppg", "fl"], default="c2",
                     help="c2 (default, the headline): planes fwd+bwd; c3: dense-generator depth-3 forward; c1, c4, "
                          "c5: one block of the other BASELINE.json configs (real diagonal; LogEWS; bf16 planes); tok: the "
-                         "token-cached scan on a formal-language shape")
+                         "token-cached scan on a formal-language shape; ppg, fl: the banked depth-1 blocks at m=64 "
+                         "(PPG Jordan chains; the formal-language token block)")
     ap.add_argument("--backward", action="store_true", help="c3: time forward + backward (ews_dense_backward)")
     ap.add_argument("--leaf", choices=["series", "van_loan"], default="series",
                     help="leaf of the c3 forward: series (q=24) or Van Loan (M=20, cayley)")
@@ -782,6 +875,12 @@ def main():
 
         torch.cuda.set_device(0)
         print(json.dumps(bench_c3(args)), flush=True)
+        return
+    if args.config in ("ppg", "fl"):
+        import torch
+
+        torch.cuda.set_device(0)
+        print(json.dumps(bench_banked(args)), flush=True)
         return
     if args.config == "tok":
         import torch

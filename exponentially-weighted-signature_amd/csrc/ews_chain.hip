@@ -16,14 +16,15 @@
 // u_r for the exact leaf: the entire series sum_j x^j / ((j + r + 1) j!) / r! below |x| = 2, else the recurrence
 // phi^(r) = (e^x - r phi^(r-1)) / x from (e^x - 1) / x, in float64.
 //
-// Passes: chunk summaries from a zero state; a float64 carry scan over chunks per (sample, chain), the chunk's flow
-// taken in closed form over its clock span (the chain's flows commute); the rows from the carries. Adjoint: each
-// chunk's own rows from a zero cotangent (its cotangent on the carry-in state), a float64 reverse scan over chunks,
-// then each chunk from the cotangent at its end with the states recomputed from its carry into LDS: dv, dh and the
-// chain-parameter partials (c, eps), summed in a fixed order (deterministic). Gradients of A land on the entries the
-// chain is read from (A[f, f], A[f+1, f] and the coupling A[f, f+1] or A[f, f+2], f the chain's first row), as the
-// reference's closed-form leaf and jordan_flows read them; a parametrisation of uniform chains gets its exact
-// parameter gradient from them.
+// Passes: chunk summaries from a zero state; a float64 carry scan over chunks per (sample, chain) (a workgroup each:
+// runs of chunks composed in parallel, then chained), the chunk's flow taken in closed form over its clock span (the
+// chain's flows commute); the rows from the carries. Adjoint: each chunk's own rows from a zero cotangent (its
+// cotangent on the carry-in state), a float64 reverse scan over chunks (the same parallel scan), then each chunk
+// from the cotangent at its end with the states recomputed from its carry into LDS: dv, dh and the chain-parameter
+// partials (c, eps), summed in a fixed order (deterministic). Gradients of A land on the entries the chain is read
+// from (A[f, f], A[f+1, f] and the coupling A[f, f+1] or A[f, f+2], f the chain's first row), as the reference's
+// closed-form leaf and jordan_flows read them; a parametrisation of uniform chains gets its exact parameter gradient
+// from them.
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
@@ -319,32 +320,128 @@ __global__ __launch_bounds__(64) void k_rows(CArgs a) {
   fwd_body<M, CPLX, true>(a);
 }
 
-// float64 carries over the chunks, one thread per (sample, chain)
-template <int M, bool CPLX>
-__global__ void k_carry(CArgs a) {
-  const int e = blockIdx.x * blockDim.x + threadIdx.x;
-  if (e >= a.B * a.K) return;
-  const int b = e / a.K, j = e % a.K;
+// ---- carry scans over the chunks: a workgroup per (sample, chain), its 256 threads each owning a run of
+// consecutive chunks. A chunk acts on the chain's state as S -> F S + z (F its flow over the chunk's clock span, a
+// polynomial in Nil; z its summary) and, in the adjoint, on the cotangent as X -> F^H X + m with the chunks taken
+// from the last. Each thread composes its run into one such map, thread 0 chains the 256 maps from the initial
+// state in order (float64, fixed order), and each thread re-walks its run from its start state writing the carries
+// (cotangents). The maps compose as (F2, z2) o (F1, z1) = (F2 F1, F2 z1 + z2) (adjoint: F2^H z1 + z2), the flows
+// being polynomials in Nil that commute.
+constexpr int kCarryThreads = 256;
+
+template <int M>
+__device__ __forceinline__ void nil_apply(const zd* F, const zd* S, zd* o) {  // (F S)_i = sum_p F[p] S_{i+p}
+#pragma unroll
+  for (int i = 0; i < M; ++i) {
+    zd acc = Z(0.0);
+#pragma unroll
+    for (int p = 0; p + i < M; ++p) acc += F[p] * S[i + p];
+    o[i] = acc;
+  }
+}
+template <int M>
+__device__ __forceinline__ void nil_apply_h(const zd* F, const zd* X, zd* o) {  // (F^H X)_k = sum_p conj(F[p]) X_{k-p}
+#pragma unroll
+  for (int k = 0; k < M; ++k) {
+    zd acc = Z(0.0);
+#pragma unroll
+    for (int p = 0; p <= k; ++p) acc += cjm(F[p], X[k - p]);
+    o[k] = acc;
+  }
+}
+template <int M>
+__device__ __forceinline__ void nil_mul(const zd* F2, const zd* F1, zd* o) {  // product of polynomials in Nil
+#pragma unroll
+  for (int r = 0; r < M; ++r) {
+    zd acc = Z(0.0);
+#pragma unroll
+    for (int p = 0; p <= r; ++p) acc += F2[p] * F1[r - p];
+    o[r] = acc;
+  }
+}
+// the map of chunk cc (application order: ascending chunks forward, descending in the adjoint)
+template <int M, bool BWD>
+__device__ __forceinline__ void chunk_map(const CArgs& a, int b, int j, zd c, double eps, const float* th, int cc,
+                                          zd* F, zd* z) {
+  span_flow<M>(c, eps, chunk_span(a, th, cc), F);
+  if (!BWD) {
+    ld_state<M>(a.summ + ch_off(a, b, cc, j), z);
+  } else if (a.readout != EWS_READOUT_TERMINAL) {
+    ld_state<M>(a.mu + ch_off(a, b, cc, j), z);
+  } else {
+#pragma unroll
+    for (int i = 0; i < M; ++i) z[i] = Z(0.0);
+  }
+}
+template <int M, bool BWD>
+__device__ __forceinline__ void map_apply(const zd* F, const zd* z, zd* S) {
+  zd o[M];
+  if (BWD) nil_apply_h<M>(F, S, o);
+  else nil_apply<M>(F, S, o);
+#pragma unroll
+  for (int i = 0; i < M; ++i) S[i] = o[i] + z[i];
+}
+template <int M, bool CPLX, bool BWD>
+__device__ __forceinline__ void carry_scan(const CArgs& a) {
+  __shared__ double s_map[kCarryThreads][4 * M];  // each thread's composed map: F, then z (complex)
+  __shared__ double s_in[kCarryThreads][2 * M];   // each thread's start state
+  const int b = blockIdx.x / a.K, j = blockIdx.x % a.K, tid = threadIdx.x;
   zd c;
   double eps;
   chain_params(a, j, c, eps);
   const float* th = a.clock + (size_t)b * a.L;
-  zd S[M], F[M], z[M];
+  const int nth = blockDim.x, per = (a.C + nth - 1) / nth, nrun = (a.C + per - 1) / per;
+  const int q0 = tid * per, q1 = min(a.C, q0 + per);  // the thread's run, in application order
+  zd AF[M], Az[M], F[M], z[M], t[M];
 #pragma unroll
-  for (int i = 0; i < M; ++i) S[i] = Z(0.0);
-  st_state<M>(a.carries + st_off(a, b, 0, j), S);
-  for (int cc = 0; cc < a.C; ++cc) {
-    ld_state<M>(a.summ + ch_off(a, b, cc, j), z);
-    span_flow<M>(c, eps, chunk_span(a, th, cc), F);
-#pragma unroll
-    for (int i = 0; i < M; ++i) {
-      zd acc = z[i];
-#pragma unroll
-      for (int p = 0; p + i < M; ++p) acc += F[p] * S[i + p];
-      S[i] = acc;
-    }
-    st_state<M>(a.carries + st_off(a, b, cc + 1, j), S);
+  for (int i = 0; i < M; ++i) {
+    AF[i] = Z(i == 0 ? 1.0 : 0.0);
+    Az[i] = Z(0.0);
   }
+  for (int q = q0; q < q1; ++q) {
+    const int cc = BWD ? a.C - 1 - q : q;
+    chunk_map<M, BWD>(a, b, j, c, eps, th, cc, F, z);
+    nil_mul<M>(F, AF, t);  // the chunk after the run so far
+#pragma unroll
+    for (int i = 0; i < M; ++i) AF[i] = t[i];
+    map_apply<M, BWD>(F, z, Az);
+  }
+  st_state<M>(&s_map[tid][0], AF);
+  st_state<M>(&s_map[tid][2 * M], Az);
+  __syncthreads();
+  if (tid == 0) {
+    zd S[M];
+    if (BWD && a.readout == EWS_READOUT_TERMINAL) {
+      const float* r = a.gout + (size_t)b * a.W + a.lvl0 + (size_t)j * a.size;
+#pragma unroll
+      for (int i = 0; i < M; ++i) S[i] = CPLX ? Z((double)r[2 * i], (double)r[2 * i + 1]) : Z((double)r[i]);
+    } else {
+#pragma unroll
+      for (int i = 0; i < M; ++i) S[i] = Z(0.0);
+    }
+    for (int u = 0; u < nrun; ++u) {  // the threads past nrun own no chunk
+      st_state<M>(&s_in[u][0], S);
+      ld_state<M>(&s_map[u][0], F);
+      ld_state<M>(&s_map[u][2 * M], z);
+      map_apply<M, BWD>(F, z, S);
+    }
+  }
+  __syncthreads();
+  if (tid >= nrun) return;
+  zd S[M];
+  ld_state<M>(&s_in[tid][0], S);
+  for (int q = q0; q < q1; ++q) {
+    const int cc = BWD ? a.C - 1 - q : q;
+    if (BWD) st_state<M>(a.mt + ch_off(a, b, cc, j), S);  // the cotangent at the chunk's end
+    else st_state<M>(a.carries + st_off(a, b, cc, j), S);  // the state before the chunk
+    chunk_map<M, BWD>(a, b, j, c, eps, th, cc, F, z);
+    map_apply<M, BWD>(F, z, S);
+    if (!BWD && cc == a.C - 1) st_state<M>(a.carries + st_off(a, b, a.C, j), S);
+  }
+}
+template <int M, bool CPLX>
+__global__ __launch_bounds__(kCarryThreads) void k_carry(CArgs a) {
+  carry_scan<M, CPLX, false>(a);
 }
 
 // the terminal row: the state after the last chunk
@@ -411,33 +508,8 @@ __global__ __launch_bounds__(64) void k_local(CArgs a) {
 // the reverse carry scan: mt[c] = the cotangent at chunk c's end from the later chunks (the terminal row's at the
 // last chunk); mt[c-1] = F_c^H mt[c] + mu[c]
 template <int M, bool CPLX>
-__global__ void k_carry_bwd(CArgs a) {
-  const int e = blockIdx.x * blockDim.x + threadIdx.x;
-  if (e >= a.B * a.K) return;
-  const int b = e / a.K, j = e % a.K;
-  zd c;
-  double eps;
-  chain_params(a, j, c, eps);
-  const float* th = a.clock + (size_t)b * a.L;
-  zd X[M], F[M], m[M];
-  if (a.readout == EWS_READOUT_TERMINAL) {
-    const float* r = a.gout + (size_t)b * a.W + a.lvl0 + (size_t)j * a.size;
-#pragma unroll
-    for (int i = 0; i < M; ++i) X[i] = CPLX ? Z((double)r[2 * i], (double)r[2 * i + 1]) : Z((double)r[i]);
-  } else {
-#pragma unroll
-    for (int i = 0; i < M; ++i) X[i] = Z(0.0);
-  }
-  for (int cc = a.C - 1; cc >= 0; --cc) {
-    st_state<M>(a.mt + ch_off(a, b, cc, j), X);
-    span_flow<M>(c, eps, chunk_span(a, th, cc), F);
-    adj_flow<M>(F, X);
-    if (a.readout != EWS_READOUT_TERMINAL) {
-      ld_state<M>(a.mu + ch_off(a, b, cc, j), m);
-#pragma unroll
-      for (int i = 0; i < M; ++i) X[i] += m[i];
-    }
-  }
+__global__ __launch_bounds__(kCarryThreads) void k_carry_bwd(CArgs a) {
+  carry_scan<M, CPLX, true>(a);
 }
 
 // each chunk from the cotangent at its end: states from the carry into LDS, then the steps in reverse with dv, dh
@@ -716,6 +788,9 @@ WsOff ws_off(const CArgs& a) {
   return w;
 }
 
+// threads of a carry-scan workgroup: one per chunk up to 256, in whole wavefronts
+int carry_threads(int C) { return std::min(chain::kCarryThreads, std::max(64, (C + 63) / 64 * 64)); }
+
 #define EWS_CHAIN_LAUNCH(KERNEL, GRID, BLK, LDS, ST, A)                                                       \
   do {                                                                                                        \
     const bool cp = (A).cplx != 0;                                                                            \
@@ -791,8 +866,8 @@ int ews_chain_forward(const ews_chain_desc* desc, const void* path, const float*
   hipStream_t st = (hipStream_t)stream;
   const dim3 grid((a.C + a.CPW - 1) / a.CPW, a.B), blk(64);
   EWS_CHAIN_LAUNCH(ews::chain::k_summary, grid, blk, 0, st, a);
-  const dim3 gs((a.B * a.K + 63) / 64);
-  EWS_CHAIN_LAUNCH(ews::chain::k_carry, gs, blk, 0, st, a);
+  const dim3 ct(ews::carry_threads(a.C));
+  EWS_CHAIN_LAUNCH(ews::chain::k_carry, dim3(a.B * a.K), ct, 0, st, a);
   if (a.readout == EWS_READOUT_PREFIX) {
     EWS_CHAIN_LAUNCH(ews::chain::k_rows, grid, blk, 0, st, a);
   } else {
@@ -828,8 +903,7 @@ int ews_chain_backward(const ews_chain_desc* desc, const void* path, const float
   hipStream_t st = (hipStream_t)stream;
   const dim3 grid((a.C + a.CPW - 1) / a.CPW, a.B), blk(64);
   if (a.readout == EWS_READOUT_PREFIX) EWS_CHAIN_LAUNCH(ews::chain::k_local, grid, blk, 0, st, a);
-  const dim3 gs((a.B * a.K + 63) / 64);
-  EWS_CHAIN_LAUNCH(ews::chain::k_carry_bwd, gs, blk, 0, st, a);
+  EWS_CHAIN_LAUNCH(ews::chain::k_carry_bwd, dim3(a.B * a.K), dim3(ews::carry_threads(a.C)), 0, st, a);
   const size_t lds = (size_t)64 * a.T * a.M * sizeof(float2);
   if (lds > 65536 && ews::allow_full_lds(a, lds) != EWS_OK) return EWS_ERR_LAUNCH;
   EWS_CHAIN_LAUNCH(ews::chain::k_full, grid, blk, lds, st, a);

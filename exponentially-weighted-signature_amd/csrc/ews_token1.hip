@@ -161,13 +161,176 @@ __global__ void k_reduce(TArgs a) {
   else a.gP[g * a.d + (q - dd)] = (float)s;
 }
 
+// ---- block-diagonal caches (desc->block = BS): the flow of every token is block-diagonal with blocks of BS
+// consecutive coordinates (the chain-structured caches: rotation planes BS = 2, Jordan chains BS = their size, a
+// real diagonal BS = 1). Lane i then needs only row i of its block: S_i = P_g[i] + sum_r D_g[i][base + r] S_{base+r}
+// (base = BS floor(i / BS)), with the block partners' states by lane shuffles: no LDS broadcast, no barrier. The
+// caches' block entries are staged in LDS when they fit (row i of token g's block at (g d + i) BS), the step's token
+// and mask bit come from a register holding the next 64 steps. The backward walks the steps in reverse with the
+// cotangent lam_{t-1} = D_g^T lam_t (+ the row cotangent), and accumulates the token gradients per lane in LDS
+// (lane i owns dP_g[i] and row i of dD_g's block): per-sample partials, then a fixed-order sum over the samples.
+// Entries of D outside the blocks are taken as zero and their gradients are written as zero.
+constexpr int kStageFloats = 12288;  // caches staged in LDS up to 48 KB
+
+__device__ __forceinline__ float blk_d(const TArgs& a, const float* sD, bool staged, int BS, int g, int row,
+                                       int r) {
+  if (staged) return sD[((size_t)g * a.d + row) * BS + r];
+  return a.D[((size_t)g * a.d + row) * a.d + (row / BS) * BS + r];
+}
+
+template <int BS>
+__global__ __launch_bounds__(64) void k_fwd_blk(TArgs a) {
+  extern __shared__ float s_c[];
+  const int b = blockIdx.x, i = threadIdx.x;
+  const bool on = i < a.d;
+  const int base = (i / BS) * BS;
+  const bool staged = (size_t)a.V * a.d * (BS + 1) <= (size_t)kStageFloats;
+  float* sP = s_c;
+  float* sD = s_c + (size_t)a.V * a.d;
+  if (staged) {
+    for (int q = i; q < a.V * a.d; q += 64) sP[q] = a.P[q];
+    for (int q = i; q < a.V * a.d * BS; q += 64) {
+      const int gr = q / BS, r = q - gr * BS, g = gr / a.d, row = gr - g * a.d;
+      sD[q] = a.D[((size_t)g * a.d + row) * a.d + (row / BS) * BS + r];
+    }
+    __syncthreads();
+  }
+  float S = 0.0f;
+  for (int t0 = 0; t0 < a.n; t0 += 64) {
+    int tokv = 0, livev = 0;
+    if (t0 + i < a.n) {
+      bool live;
+      tokv = tok_at(a, (size_t)b * a.n + t0 + i, live);
+      livev = live ? 1 : 0;
+    }
+    const int cnt = min(64, a.n - t0);
+    for (int s = 0; s < cnt; ++s) {
+      const int g = __shfl(tokv, s), live = __shfl(livev, s);  // uniform over the wavefront
+      if (live) {
+        float acc = on ? (staged ? sP[g * a.d + i] : a.P[(size_t)g * a.d + i]) : 0.0f;
+#pragma unroll
+        for (int r = 0; r < BS; ++r) {
+          const float sr = __shfl(S, base + r);
+          if (on) acc = fmaf(blk_d(a, sD, staged, BS, g, i, r), sr, acc);
+        }
+        S = acc;
+      }
+      if (on) a.out[((size_t)b * a.n + t0 + s) * a.d + i] = S;
+    }
+  }
+}
+
+template <int BS>
+__global__ __launch_bounds__(64) void k_bwd_blk(TArgs a) {
+  extern __shared__ float s_c[];
+  const int b = blockIdx.x, i = threadIdx.x;
+  const bool on = i < a.d;
+  const int base = (i / BS) * BS;
+  const bool staged = (size_t)a.V * a.d * (BS + 1) <= (size_t)kStageFloats;
+  float* sD = s_c + (size_t)a.V * a.d;  // the same layout as the forward's (P's slot unused)
+  float* sAcc = staged ? sD + (size_t)a.V * a.d * BS : s_c;  // (V, BS + 1, 64): lane i's column
+  if (staged) {
+    for (int q = i; q < a.V * a.d * BS; q += 64) {
+      const int gr = q / BS, r = q - gr * BS, g = gr / a.d, row = gr - g * a.d;
+      sD[q] = a.D[((size_t)g * a.d + row) * a.d + (row / BS) * BS + r];
+    }
+  }
+  for (int q = 0; q < a.V * (BS + 1); ++q) sAcc[q * 64 + i] = 0.0f;
+  __syncthreads();
+  float lam = 0.0f;
+  for (int t1 = a.n; t1 > 0; t1 -= 64) {
+    const int t0 = max(0, t1 - 64);
+    int tokv = 0, livev = 0;
+    if (t0 + i < t1) {
+      bool live;
+      tokv = tok_at(a, (size_t)b * a.n + t0 + i, live);
+      livev = live ? 1 : 0;
+    }
+    for (int t = t1 - 1; t >= t0; --t) {
+      const int g = __shfl(tokv, t - t0), live = __shfl(livev, t - t0);  // uniform over the wavefront
+      if (on) lam += a.gout[((size_t)b * a.n + t) * a.d + i];
+      if (live) {
+        const float sp = (on && t > 0) ? a.rows[((size_t)b * a.n + t - 1) * a.d + i] : 0.0f;  // S_{t-1}
+        float* acc = sAcc + (size_t)g * (BS + 1) * 64 + i;
+        float ln = 0.0f;
+#pragma unroll
+        for (int r = 0; r < BS; ++r) {
+          const float s_r = __shfl(sp, base + r), l_r = __shfl(lam, base + r);
+          if (on) {
+            acc[r * 64] += lam * s_r;                                         // dD_g[i][base + r]
+            ln = fmaf(blk_d(a, sD, staged, BS, g, base + r, i - base), l_r, ln);  // (D_g^T lam)_i
+          }
+        }
+        if (on) acc[BS * 64] += lam;  // dP_g[i]
+        lam = ln;
+      }
+    }
+  }
+  if (on) {
+    for (int q = 0; q < a.V * (BS + 1); ++q)
+      a.part[(((size_t)b * a.V * (BS + 1)) + q) * a.d + i] = sAcc[q * 64 + i];
+  }
+}
+
+// gP and gD from the per-sample partials (samples in order, float64); gD's entries outside the blocks are zero
+__global__ void k_reduce_blk(TArgs a, int BS) {
+  const size_t e = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const size_t dd = (size_t)a.d * a.d, tot = (size_t)a.V * (dd + a.d);
+  if (e >= tot) return;
+  int g, i, r;
+  bool isP;
+  if (e < (size_t)a.V * dd) {
+    g = (int)(e / dd);
+    const int rc = (int)(e - (size_t)g * dd);
+    i = rc / a.d;
+    const int col = rc - i * a.d;
+    r = col - (i / BS) * BS;
+    isP = false;
+    if (r < 0 || r >= BS) {
+      a.gD[e] = 0.0f;
+      return;
+    }
+  } else {
+    const size_t q = e - (size_t)a.V * dd;
+    g = (int)(q / a.d);
+    i = (int)(q - (size_t)g * a.d);
+    r = BS;
+    isP = true;
+  }
+  double s = 0.0;
+  for (int b = 0; b < a.B; ++b) s += (double)a.part[(((size_t)b * a.V + g) * (BS + 1) + r) * a.d + i];
+  if (isP) a.gP[(size_t)g * a.d + i] = (float)s;
+  else a.gD[e] = (float)s;
+}
+
 }  // namespace tok1
 
 namespace {
 int tok1_check(const ews_token1_desc* s) {
   if (!s) return EWS_ERR_NULL;
   if (s->batch < 1 || s->steps < 1 || s->dim < 1 || s->dim > tok1::kMaxD || s->vocab < 1) return EWS_ERR_SHAPE;
+  const int bs = s->block;
+  if (bs < 0 || bs > 8 || bs == 5 || bs == 7 || (bs > 0 && s->dim % bs != 0)) return EWS_ERR_OPTION;
+  // the backward's per-lane accumulators (16 KB at most) sit in LDS beside the staged caches (48 KB at most)
+  if (bs > 0 && (size_t)s->vocab * (bs + 1) > 64) return EWS_ERR_SHAPE;
   return EWS_OK;
+}
+// launch of a block-diagonal kernel for the descriptor's block size
+#define EWS_TOK1_BLK(KERNEL, BS, GRID, LDS, ST, A)                                                    \
+  do {                                                                                               \
+    switch (BS) {                                                                                    \
+      case 1: hipLaunchKernelGGL((KERNEL<1>), GRID, dim3(64), LDS, ST, A); break;                  \
+      case 2: hipLaunchKernelGGL((KERNEL<2>), GRID, dim3(64), LDS, ST, A); break;                  \
+      case 3: hipLaunchKernelGGL((KERNEL<3>), GRID, dim3(64), LDS, ST, A); break;                  \
+      case 4: hipLaunchKernelGGL((KERNEL<4>), GRID, dim3(64), LDS, ST, A); break;                  \
+      case 6: hipLaunchKernelGGL((KERNEL<6>), GRID, dim3(64), LDS, ST, A); break;                  \
+      default: hipLaunchKernelGGL((KERNEL<8>), GRID, dim3(64), LDS, ST, A); break;                 \
+    }                                                                                                \
+  } while (0)
+size_t blk_lds_bytes(const ews_token1_desc* s, bool bwd) {
+  const size_t stage = (size_t)s->vocab * s->dim * (s->block + 1);
+  const size_t staged = stage <= (size_t)tok1::kStageFloats ? stage : 0;
+  return (staged + (bwd ? (size_t)s->vocab * (s->block + 1) * 64 : 0)) * 4;
 }
 size_t al256t(size_t x) { return (x + 255) & ~(size_t)255; }
 tok1::TArgs tok1_args(const ews_token1_desc* s) {
@@ -187,6 +350,7 @@ extern "C" {
 size_t ews_token1_workspace_bytes(const ews_token1_desc* desc) {
   if (ews::tok1_check(desc) != EWS_OK) return 0;
   const ews::tok1::TArgs a = ews::tok1_args(desc);
+  if (desc->block > 0) return ews::al256t((size_t)a.B * a.V * (desc->block + 1) * a.d * 4);  // per-sample partials
   const size_t dd = (size_t)a.d * a.d;
   return ews::al256t((size_t)a.V * dd * 4) + ews::al256t((size_t)a.B * a.n * a.d * 4) +
          ews::al256t((size_t)a.V * a.nch * (dd + a.d) * 4);
@@ -205,6 +369,10 @@ int ews_token1_scan(const ews_token1_desc* desc, const int32_t* tokens, const ui
   a.Dt = (float*)workspace;
   a.out = out;
   hipStream_t st = (hipStream_t)stream;
+  if (desc->block > 0) {
+    EWS_TOK1_BLK(ews::tok1::k_fwd_blk, desc->block, dim3(a.B), ews::blk_lds_bytes(desc, false), st, a);
+    return hipGetLastError() == hipSuccess ? EWS_OK : EWS_ERR_LAUNCH;
+  }
   const size_t nd = (size_t)a.V * a.d * a.d;
   hipLaunchKernelGGL(ews::tok1::k_transpose, dim3((unsigned)((nd + 255) / 256)), dim3(256), 0, st, a);
   if (hipGetLastError() != hipSuccess) return EWS_ERR_LAUNCH;
@@ -228,10 +396,19 @@ int ews_token1_scan_backward(const ews_token1_desc* desc, const int32_t* tokens,
   a.gP = grad_P;
   a.gD = grad_D;
   const size_t dd = (size_t)a.d * a.d;
+  hipStream_t st = (hipStream_t)stream;
+  if (desc->block > 0) {
+    a.part = (float*)workspace;
+    EWS_TOK1_BLK(ews::tok1::k_bwd_blk, desc->block, dim3(a.B), ews::blk_lds_bytes(desc, true), st, a);
+    if (hipGetLastError() != hipSuccess) return EWS_ERR_LAUNCH;
+    const size_t tot = (size_t)a.V * (dd + a.d);
+    hipLaunchKernelGGL(ews::tok1::k_reduce_blk, dim3((unsigned)((tot + 255) / 256)), dim3(256), 0, st, a,
+                       desc->block);
+    return hipGetLastError() == hipSuccess ? EWS_OK : EWS_ERR_LAUNCH;
+  }
   char* w = (char*)workspace;
   a.lam = (float*)(w + ews::al256t((size_t)a.V * dd * 4));
   a.part = (float*)(w + ews::al256t((size_t)a.V * dd * 4) + ews::al256t((size_t)a.B * a.n * a.d * 4));
-  hipStream_t st = (hipStream_t)stream;
   hipLaunchKernelGGL(ews::tok1::k_bwd_lam, dim3(a.B), dim3(64), 0, st, a);
   if (hipGetLastError() != hipSuccess) return EWS_ERR_LAUNCH;
   hipLaunchKernelGGL(ews::tok1::k_grads, dim3(a.V, a.nch), dim3(256), 0, st, a);

@@ -169,6 +169,7 @@ class Token1Desc(ctypes.Structure):
         ("steps", ctypes.c_int32),
         ("dim", ctypes.c_int32),
         ("vocab", ctypes.c_int32),
+        ("block", ctypes.c_int32),
     ]
 
 

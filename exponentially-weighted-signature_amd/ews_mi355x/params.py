@@ -134,8 +134,62 @@ class AParamJordanRepeated(torch.nn.Module):
                 )
         self.block_params = torch.nn.ParameterList([torch.nn.Parameter(torch.as_tensor(p)) for p in block_params])
         self.dim = int(sum(self.block_sizes))
+        self._index = {}  # uniform chains: entry indices of A by device
+
+    def _uniform_index(self, device):
+        """Index tensors of A's entries for uniform chains (every block the same kind and size): the eigenvalue
+        slots, the -b / +b slots of complex blocks, and the constant couplings (ones)."""
+        key = str(device)
+        if key not in self._index:
+            kind, size = self.block_kinds[0], self.block_sizes[0]
+            lam_r, lam_c, nb_r, nb_c, pb_r, pb_c, one_r, one_c = [], [], [], [], [], [], [], []
+            for j in range(len(self.block_sizes)):
+                f = j * size
+                if kind == "real":
+                    lam_r += [f + i for i in range(size)]
+                    lam_c += [f + i for i in range(size)]
+                    one_r += [f + i for i in range(size - 1)]
+                    one_c += [f + i + 1 for i in range(size - 1)]
+                else:
+                    for m in range(size // 2):
+                        r = f + 2 * m
+                        lam_r += [r, r + 1]
+                        lam_c += [r, r + 1]
+                        nb_r.append(r)
+                        nb_c.append(r + 1)
+                        pb_r.append(r + 1)
+                        pb_c.append(r)
+                        if m + 1 < size // 2:
+                            one_r += [r, r + 1]
+                            one_c += [r + 2, r + 3]
+            mk = lambda x: torch.tensor(x, dtype=torch.long, device=device)  # noqa: E731
+            self._index[key] = tuple(mk(x) for x in (lam_r, lam_c, nb_r, nb_c, pb_r, pb_c, one_r, one_c))
+        return self._index[key]
+
+    def _forward_uniform(self):
+        """The same A for uniform chains from a handful of batched operations (one stack of the block parameters,
+        one softplus, one scatter), instead of a few per block."""
+        kind, size = self.block_kinds[0], self.block_sizes[0]
+        P = torch.stack(list(self.block_params))
+        lam_r, lam_c, nb_r, nb_c, pb_r, pb_c, one_r, one_c = self._uniform_index(P.device)
+        a = F.softplus(P[:, 0]).repeat_interleave(size)  # eigenvalue slots per block (2 per complex coordinate)
+        rows, cols, vals = [lam_r], [lam_c], [a]
+        if kind == "complex":
+            b = P[:, 1].repeat_interleave(size // 2)
+            rows += [nb_r, pb_r]
+            cols += [nb_c, pb_c]
+            vals += [-b, b]
+        if one_r.numel():
+            rows.append(one_r)
+            cols.append(one_c)
+            vals.append(torch.ones(one_r.numel(), dtype=P.dtype, device=P.device))
+        A = torch.zeros(self.dim, self.dim, dtype=P.dtype, device=P.device)
+        return A.index_put((torch.cat(rows), torch.cat(cols)), torch.cat(vals))
 
     def forward(self):
+        if len(set(self.block_sizes)) == 1 and len(set(self.block_kinds)) == 1 and all(
+                p.shape == self.block_params[0].shape for p in self.block_params):
+            return self._forward_uniform()
         blocks = []
         for size, kind, p in zip(self.block_sizes, self.block_kinds, self.block_params):
             kw = dict(dtype=p.dtype, device=p.device)

@@ -116,6 +116,7 @@ def _wide_cache(vocab_dx, vocab_dtheta, A, N, expm_method, chen_method, leaf, se
     kc = torch.stack([torch.zeros_like(th), torch.zeros_like(th), th], 1)
     cols = ops.chain_scan(kp, kc, A, kind, size, readout="prefix", level0=False, series_q=q)[:, 1]  # (V d, d)
     D = cols.reshape(V, d, d).transpose(1, 2).contiguous()  # column i of token g's flow
+    D._ews_block = int(size)  # block-diagonal with blocks of `size` coordinates: the cached scan's sparse route
     return P, D
 
 
@@ -201,7 +202,7 @@ class _Token1ScanFn(torch.autograd.Function):
     """Depth-1 cached scan for caches of any width up to 64 (ews_token1_scan / ews_token1_scan_backward)."""
 
     @staticmethod
-    def forward(ctx, P_cache, D_cache, token_ids, mask):
+    def forward(ctx, P_cache, D_cache, token_ids, mask, block):
         lib = nat.load()
         for nm, t in (("P_cache", P_cache), ("D_cache", D_cache)):
             if not t.is_cuda or t.dtype != torch.float32:
@@ -214,7 +215,9 @@ class _Token1ScanFn(torch.autograd.Function):
         dev = P_cache.device
         tok = token_ids.to(device=dev, dtype=torch.int32).contiguous()
         m = None if mask is None else mask.to(device=dev).expand(B, n).to(torch.uint8).contiguous()
-        desc = nat.Token1Desc(B, n, d, V)
+        if block and (d % block or V * (block + 1) > 64 or block not in (1, 2, 3, 4, 6, 8)):
+            block = 0  # the dense route
+        desc = nat.Token1Desc(B, n, d, V, int(block))
         out = torch.empty((B, n, d), device=dev, dtype=torch.float32)
         ws = torch.empty(int(lib.ews_token1_workspace_bytes(ctypes.byref(desc))), device=dev, dtype=torch.uint8)
         nat.check(lib.ews_token1_scan(ctypes.byref(desc), tok.data_ptr(), m.data_ptr() if m is not None else None,
@@ -239,13 +242,15 @@ class _Token1ScanFn(torch.autograd.Function):
                                                D_cache.data_ptr(), out.data_ptr(), gout.data_ptr(), gP.data_ptr(),
                                                gD.data_ptr(), ws.data_ptr(), _stream_handle(dev)),
                   "ews_token1_scan_backward")
-        return gP, gD, None, None
+        return gP, gD, None, None, None
 
 
-def token_cached_prefix_scan(token_ids, mask, P_cache, D_cache, dim, trunc, chunk=0):
+def token_cached_prefix_scan(token_ids, mask, P_cache, D_cache, dim, trunc, chunk=0, block=None):
     """ews/core/token_scan.py:91-118, batched: token_ids (B, L) or (L,) ints, mask (B, L) / (L,) bool or None ->
     the packed prefix signatures (B, L, sum_k d^k) (no level-0 column, the layout of pack_signatures).
-    S_t = mult(apply_M(S_{t-1}, D_t), P_t) from the unit; a padded step applies D = I and the unit signature."""
+    S_t = mult(apply_M(S_{t-1}, D_t), P_t) from the unit; a padded step applies D = I and the unit signature.
+    Above 16 coordinates, block (default: the value build_token_cache records on a chain-structured D_cache) says
+    that every flow is block-diagonal with blocks of that many coordinates, which the scan then exploits."""
     single = token_ids.dim() == 1
     if single:
         token_ids = token_ids[None]
@@ -255,7 +260,8 @@ def token_cached_prefix_scan(token_ids, mask, P_cache, D_cache, dim, trunc, chun
     if int(dim) > 16:
         if int(trunc) != 1:
             raise NotImplementedError("the token-cached scan above 16 coordinates runs at depth 1")
-        out = _Token1ScanFn.apply(P_cache, D_cache, token_ids, mask)
+        bs = getattr(D_cache, "_ews_block", 0) if block is None else int(block)
+        out = _Token1ScanFn.apply(P_cache, D_cache, token_ids, mask, bs)
         return out[0] if single else out
     out = _TokenScanFn.apply(P_cache, D_cache, token_ids, mask, int(trunc), int(chunk))
     return out[0] if single else out

@@ -361,9 +361,13 @@ typedef struct ews_token1_desc {
   int32_t steps; /* n >= 1 scan steps (tokens) per sample */
   int32_t dim;   /* d: 1..64 */
   int32_t vocab; /* V >= 1; ids are clamped to [0, V) */
+  int32_t block; /* 0: dense flows; BS in {1, 2, 3, 4, 6, 8} (d % BS == 0, V (BS + 1) <= 64): every flow is
+                    block-diagonal with blocks of BS consecutive coordinates (the chain-structured caches); entries
+                    outside the blocks are taken as zero and their gradients written as zero */
 } ews_token1_desc;
 
-/* Scratch of both directions: a transposed flow cache, every step's cotangent, per-chunk token partials. */
+/* Scratch of both directions: dense flows, a transposed flow cache, every step's cotangent and per-chunk token
+ * partials; block-diagonal flows, the per-sample token partials. */
 size_t ews_token1_workspace_bytes(const ews_token1_desc* desc);
 
 /* tokens (B, n) int32, mask (B, n) uint8 or NULL, caches f32 -> out (B, n, d) f32, the packed prefix states

@@ -263,3 +263,14 @@ def test_formal_language_token_block(leaf):
     print("  " + ", ".join(f"{k} {x:.2e}" for k, x in errs.items()), flush=True)
     assert max(errs["P"], errs["D"], errs["fwd"]) < 1e-5, errs
     assert max(x for k, x in errs.items() if k not in ("P", "D", "fwd")) < 1e-4, errs
+    # the cache is block-diagonal (planes: blocks of 2), which the scan above exploited; the dense route on the same
+    # caches (block=0: every flow entry read, the full dense token gradients) gives the same rows and gradients
+    gx2 = dx.to(DEV).requires_grad_(True)
+    gt2 = dth.to(DEV).requires_grad_(True)
+    P2, D2 = E.build_token_cache(gx2, gt2, gpu(), 4, 1, "exact", "exact", leaf, q)
+    assert getattr(D2, "_ews_block", 0) == 2
+    out2 = E.token_cached_prefix_scan(tok.to(DEV), mask.to(DEV), P2, D2, d, 1, block=0)
+    (out2 * w.to(DEV, torch.float32)).sum().backward()
+    e2 = [relerr(out2, want), relerr(gx2.grad, rx.grad), relerr(gt2.grad, rt.grad)]
+    print(f"  dense route: forward {e2[0]:.2e}, ddx {e2[1]:.2e}, ddtheta {e2[2]:.2e}", flush=True)
+    assert e2[0] < 1e-5 and max(e2[1:]) < 1e-4, e2
