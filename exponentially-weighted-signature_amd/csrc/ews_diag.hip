@@ -1472,7 +1472,8 @@ struct RedLds {
 // One reverse step of the adjoint at interval t (global interval tg): adds the readout cotangent, then the
 // adjoint of the Chen step with the state S(t-1) = (H1, HA, HB), writes dv[tg] for the plane lanes and the
 // step's dh partial to s_dh, and moves acc's cotangents from S(t) to S(t-1).
-template <bool CPLX, int N, bool WAVE, bool ALLRED, class T>
+// DH: the clock gradient is requested; without it the step's dh terms are not formed.
+template <bool CPLX, int N, bool WAVE, bool ALLRED, bool DH, class T>
 __device__ __forceinline__ void bwd_step(const DiagArgs& a, const LaneMap& m, const GammaSrc& gs, int s, int t, int tg,
                                          float h, const float* s_v, bool per_int, const Coef<T>& co,
                                          const CoefD<T>& qq, BwdAcc<T>& acc, T H1, T HA, T HB, const RedLds& red,
@@ -1503,10 +1504,10 @@ __device__ __forceinline__ void bwd_step(const DiagArgs& a, const LaneMap& m, co
           const T gLB = conjc(HB) * acc.LB;
           acc.Gx += h * (gIB * conjc(qq.DxB));
           acc.GyB += h * (gIB * conjc(qq.DyB));
-          dhp += redot(gIB, qq.IB1);
+          if constexpr (DH) dhp += redot(gIB, qq.IB1);
           if (per_int) {
             acc.GyB += h * (gLB * conjc(co.lamB));
-            dhp += redot(gLB, qq.lamB1);
+            if constexpr (DH) dhp += redot(gLB, qq.lamB1);
           } else {
             acc.SflowB += gLB;
           }
@@ -1520,10 +1521,10 @@ __device__ __forceinline__ void bwd_step(const DiagArgs& a, const LaneMap& m, co
             const T gLA = conjc(HA) * acc.LA;
             acc.Gx += h * (gIA * conjc(qq.DxA));
             acc.GyA += h * (gIA * conjc(qq.DyA));
-            dhp += redot(gIA, qq.IA1);
+            if constexpr (DH) dhp += redot(gIA, qq.IA1);
             if (per_int) {
               acc.GyA += h * (gLA * conjc(co.lamA));
-              dhp += redot(gLA, qq.lamA1);
+              if constexpr (DH) dhp += redot(gLA, qq.lamA1);
             } else {
               acc.SflowA += gLA;
             }
@@ -1602,31 +1603,35 @@ __device__ __forceinline__ void bwd_step(const DiagArgs& a, const LaneMap& m, co
           const T grho = conjc(H1) * gc;
           const T gphi = conjc(pj) * gs1;
           acc.Gxp += h * (gphi * conjc(qq.dphi_j));
-          dhp += redot(gphi, qq.phi_j1);
+          if constexpr (DH) dhp += redot(gphi, qq.phi_j1);
           if (per_int) {
             acc.Gxp += h * (grho * conjc(co.rho));
-            dhp += redot(grho, qq.rho1);
+            if constexpr (DH) dhp += redot(grho, qq.rho1);
           } else {
             acc.Sflow += grho;
           }
           acc.L1 = conjc(co.rho) * gc;
         }
-        const float ws = wave_sum(dhp);
-        if ((tid & 63) == 0) s_dh[t * NW + wid] = ws;
+        if constexpr (DH) {
+          const float ws = wave_sum(dhp);
+          if ((tid & 63) == 0) s_dh[t * NW + wid] = ws;
+        }
         if constexpr (!WAVE) __syncthreads();
 }
 
 // ------------------------------------------------------------------------------------------- B3
 // Chunk epilogue of the full adjoint: dh of the chunk's intervals (fixed-order sum over waves) and the chunk's
 // parameter partials (lane (j, k) contributes to plane j as a row and to plane k as a column).
-template <bool CPLX, int N, bool WAVE, class T>
+template <bool CPLX, int N, bool WAVE, bool DH, class T>
 __device__ __forceinline__ void bwd_epilogue(const DiagArgs& a, const LaneMap& m, const ChunkClock& cc, BwdAcc<T>& acc,
                                              T uj, T ua, T ub, int Tc, int t0, float* s_dh, float* s_g, int c, int b) {
   const int tid = threadIdx.x, NT = blockDim.x, NW = (NT + 63) / 64, wid = tid / 64;
-  for (int t = tid; t < Tc; t += NT) {
-    float s = 0.0f;
-    for (int w = 0; w < NW; ++w) s += s_dh[t * NW + w];
-    a.dh[(size_t)b * a.n_int + t0 + t] = s;
+  if constexpr (DH) {
+    for (int t = tid; t < Tc; t += NT) {
+      float s = 0.0f;
+      for (int w = 0; w < NW; ++w) s += s_dh[t * NW + w];
+      a.dh[(size_t)b * a.n_int + t0 + t] = s;
+    }
   }
   float pj_d = 0.0f, pj_w = 0.0f, pk_d = 0.0f, pk_w = 0.0f, dhref = 0.0f;
   if (m.active) {
@@ -1669,16 +1674,20 @@ __device__ __forceinline__ void bwd_epilogue(const DiagArgs& a, const LaneMap& m
         gpo[m.j] = sd;
       }
     }
-    const float whr = wave_sum(dhref);
-    if (tid == 0) a.gph[(size_t)b * a.C + c] = whr;
+    if constexpr (DH) {
+      const float whr = wave_sum(dhref);
+      if (tid == 0) a.gph[(size_t)b * a.C + c] = whr;
+    }
   } else {
     __syncthreads();
     s_g[4 * tid + 0] = pj_d;
     s_g[4 * tid + 1] = pj_w;
     s_g[4 * tid + 2] = pk_d;
     s_g[4 * tid + 3] = pk_w;
-    const float whr = wave_sum(dhref);
-    if ((tid & 63) == 0) s_dh[wid] = whr;  // the step partials were consumed above
+    if constexpr (DH) {
+      const float whr = wave_sum(dhref);
+      if ((tid & 63) == 0) s_dh[wid] = whr;  // the step partials were consumed above
+    }
     __syncthreads();
     if (tid < a.K) {
       const int j = tid;
@@ -1702,7 +1711,7 @@ __device__ __forceinline__ void bwd_epilogue(const DiagArgs& a, const LaneMap& m
         gpo[j] = sd;
       }
     }
-    if (tid == 0) {
+    if (DH && tid == 0) {
       float s = 0.0f;
       for (int w = 0; w < NW; ++w) s += s_dh[w];
       a.gph[(size_t)b * a.C + c] = s;
@@ -1777,7 +1786,7 @@ __device__ __forceinline__ void load_cot(const DiagArgs& a, const LaneMap& m, co
 // (a) Uniform-clock chunks whose decay allows it: the states S(t-1) come from inverting the steps backwards from
 // the chunk's end state (c_j = S1(t) - s1_j(t) is exact; then divide by the flows), so nothing is recomputed
 // forward and no history is kept.
-template <bool CPLX, int N, int MAXT, bool WAVE>
+template <bool CPLX, int N, int MAXT, bool WAVE, bool DH>
 __global__ __launch_bounds__(MAXT) void k_chunk_bwd_inv(DiagArgs a) {
   using T = typename Types<CPLX>::T;
   extern __shared__ float smem[];
@@ -1837,7 +1846,8 @@ __global__ __launch_bounds__(MAXT) void k_chunk_bwd_inv(DiagArgs a) {
           HB = (ilB0 + ilB1 * dlt) * (SB - cj * s1k - co.IB * (pj * pk));
           if constexpr (CPLX) HA = (ilA0 + ilA1 * dlt) * (SA - cj * conjc(s1k) - co.IA * (pj * conjc(pk)));
         }
-        bwd_step<CPLX, N, WAVE, MAXT == 1024>(a, m, gs, s, t, t0 + t, s_h[t], s_v, cc.per_int, co, q0, acc, H1, HA, HB, red,
+        bwd_step<CPLX, N, WAVE, MAXT == 1024, DH>(a, m, gs, s, t, t0 + t, s_h[t], s_v, cc.per_int, co, q0, acc, H1, HA,
+                                                  HB, red,
                                 s_dh);
         S1 = H1;
         SA = HA;
@@ -1847,14 +1857,14 @@ __global__ __launch_bounds__(MAXT) void k_chunk_bwd_inv(DiagArgs a) {
     if (more) lds_dma_wait();
     __syncthreads();
   }
-  bwd_epilogue<CPLX, N, WAVE>(a, m, cc, acc, uj, ua, ub, Tc, t0, s_dh, s_g, c, b);
+  bwd_epilogue<CPLX, N, WAVE, DH>(a, m, cc, acc, uj, ua, ub, Tc, t0, s_dh, s_g, c, b);
 }
 
 // (b) Every other chunk: forward states recomputed from the chunk's float64 carry (checkpoints every kb steps; each
 // block recomputed into a lane-private LDS history before its reverse sweep), with exact per-step coefficients, or
 // the first-order model at the mean step for a uniform chunk.
 // One chunk c of sample b; every early return is uniform over the workgroup.
-template <bool CPLX, int N, int MAXT, bool WAVE>
+template <bool CPLX, int N, int MAXT, bool WAVE, bool DH>
 __device__ __forceinline__ void chunk_bwd_full(const DiagArgs& a, const int c, const int b) {
   using T = typename Types<CPLX>::T;
   constexpr int NS = CPLX ? 6 : 2;  // checkpoint floats per lane
@@ -1953,20 +1963,20 @@ __device__ __forceinline__ void chunk_bwd_full(const DiagArgs& a, const int c, c
         Coef<T> co;
         CoefD<T> qq;
         coef_at(t, co, qq);
-        bwd_step<CPLX, N, WAVE, MAXT == 1024>(a, m, gs, s, t, t0 + t, s_h[t], s_v, cc.per_int, co, qq, acc, H1, HA, HB,
+        bwd_step<CPLX, N, WAVE, MAXT == 1024, DH>(a, m, gs, s, t, t0 + t, s_h[t], s_v, cc.per_int, co, qq, acc, H1, HA, HB,
                                               red, s_dh);
       }
     }
     if (more) lds_dma_wait();
     __syncthreads();
   }
-  bwd_epilogue<CPLX, N, WAVE>(a, m, cc, acc, uj, ua, ub, Tc, t0, s_dh, s_g, c, b);
+  bwd_epilogue<CPLX, N, WAVE, DH>(a, m, cc, acc, uj, ua, ub, Tc, t0, s_dh, s_g, c, b);
 }
 // Chunks blockIdx.x, blockIdx.x + gridDim.x, ... of sample blockIdx.y: with the pair kernels active the grid is
 // small (most chunks belong to them), otherwise one chunk per workgroup. The ownership flags of 64 candidate
 // chunks are read at once (one lane each: the pair kernels' flags, or the generic chunk class written by the first
 // summary pass) and only the chunks left to this kernel are visited.
-template <bool CPLX, int N, int MAXT, bool WAVE>
+template <bool CPLX, int N, int MAXT, bool WAVE, bool DH>
 __global__ __launch_bounds__(MAXT) void k_chunk_bwd_full(DiagArgs a) {
   const int b = blockIdx.y, lane = threadIdx.x & 63;
   for (int base = blockIdx.x; base < a.C; base += 64 * gridDim.x) {
@@ -1977,7 +1987,7 @@ __global__ __launch_bounds__(MAXT) void k_chunk_bwd_full(DiagArgs a) {
     while (mask) {
       const int i = __ffsll((long long)mask) - 1;
       mask &= mask - 1;
-      chunk_bwd_full<CPLX, N, MAXT, WAVE>(a, base + gridDim.x * i, b);
+      chunk_bwd_full<CPLX, N, MAXT, WAVE, DH>(a, base + gridDim.x * i, b);
       __syncthreads();
     }
   }
@@ -2418,6 +2428,25 @@ int set_lds(K* kern, size_t lds) {
   return EWS_OK;
 }
 
+// pass 2's generic kernels: the inverting full adjoint (FAST invertible chunks) and the recomputing one (the rest)
+template <bool CPLX, int N, int MAXT, bool WAVE, bool DH>
+int full_adjoints(const Plan& p, const DiagArgs& a, hipStream_t st) {
+  dim3 grid(p.C, p.B), blkb(p.NTb);
+  if (set_lds(&k_chunk_bwd_inv<CPLX, N, MAXT, WAVE, DH>, p.lds_bwd_inv) != EWS_OK) return EWS_ERR_LAUNCH;
+  if (set_lds(&k_chunk_bwd_full<CPLX, N, MAXT, WAVE, DH>, p.lds_bwd_full) != EWS_OK) return EWS_ERR_LAUNCH;
+  if (!p.fast) {  // k_chunk_bwd_inv owns only FAST chunks
+    hipLaunchKernelGGL((k_chunk_bwd_inv<CPLX, N, MAXT, WAVE, DH>), grid, blkb, p.lds_bwd_inv, st, a);
+    EWS_LAUNCH_CHECK();
+  }
+  // the recomputing adjoint's LDS leaves about one workgroup per CU, so up to eight chunks per workgroup (strided,
+  // visited only when owned) cost no parallelism while 512 or more workgroups remain, and spare the launch most of
+  // its exiting workgroups when the other kernels own the chunks
+  const int gx = p.fast ? min(p.C, 8) : min(p.C, max((p.C + 7) / 8, (512 + p.B - 1) / p.B));
+  hipLaunchKernelGGL((k_chunk_bwd_full<CPLX, N, MAXT, WAVE, DH>), dim3(gx, p.B), blkb, p.lds_bwd_full, st, a);
+  EWS_LAUNCH_CHECK();
+  return EWS_OK;
+}
+
 // Backward passes: 0 chunk-local adjoints, 1 reverse adjoint scan, 2 full chunk adjoints, 3 knot gradients,
 // 4 parameter reduction.
 template <bool CPLX, int N, int MAXT, bool WAVE>
@@ -2451,20 +2480,9 @@ int backward_pass(const Plan& p, DiagArgs a, hipStream_t st, int pass) {
       break;
     case 2:
       if (p.fast && pairs_backward(a, st, true) != 0) return EWS_ERR_LAUNCH;
-      if (set_lds(&k_chunk_bwd_inv<CPLX, N, MAXT, WAVE>, p.lds_bwd_inv) != EWS_OK) return EWS_ERR_LAUNCH;
-      if (set_lds(&k_chunk_bwd_full<CPLX, N, MAXT, WAVE>, p.lds_bwd_full) != EWS_OK) return EWS_ERR_LAUNCH;
-      if (!p.fast) {  // k_chunk_bwd_inv owns only FAST chunks
-        hipLaunchKernelGGL((k_chunk_bwd_inv<CPLX, N, MAXT, WAVE>), grid, blkb, p.lds_bwd_inv, st, a);
-        EWS_LAUNCH_CHECK();
-      }
-      {
-        // the recomputing adjoint's LDS leaves about one workgroup per CU, so up to eight chunks per workgroup
-        // (strided, visited only when owned) cost no parallelism while 512 or more workgroups remain, and spare
-        // the launch most of its exiting workgroups when the other kernels own the chunks
-        const int gx = p.fast ? min(p.C, 8) : min(p.C, max((p.C + 7) / 8, (512 + p.B - 1) / p.B));
-        hipLaunchKernelGGL((k_chunk_bwd_full<CPLX, N, MAXT, WAVE>), dim3(gx, p.B), blkb, p.lds_bwd_full, st, a);
-      }
-      break;
+      // the clock gradient's dh terms only when it is requested (grad_clock non-null)
+      if (a.dclock) return full_adjoints<CPLX, N, MAXT, WAVE, true>(p, a, st);
+      return full_adjoints<CPLX, N, MAXT, WAVE, false>(p, a, st);
     case 3:
       hipLaunchKernelGGL(k_knot_grads, dim3(p.C + 1, p.B), dim3(64), 0, st, a);
       break;
