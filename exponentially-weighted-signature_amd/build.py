@@ -13,7 +13,7 @@ from concurrent.futures import ThreadPoolExecutor
 HERE = os.path.dirname(os.path.abspath(__file__))
 ROOT = os.path.dirname(HERE)
 CSRC = os.path.join(HERE, "csrc")
-SOURCES = ["ews_diag.hip", "ews_pairs.hip", "ews_seq.hip", "ews_jordan.hip", "ews_chain.hip", "ews_token1.hip", "ews_dense.hip", "ews_log.hip", "ews_mixer.hip", "ews_front.hip"]
+SOURCES = ["ews_diag.hip", "ews_pairs.hip", "ews_seq.hip", "ews_jordan.hip", "ews_chain.hip", "ews_token1.hip", "ews_dense.hip", "ews_wide.hip", "ews_log.hip", "ews_mixer.hip", "ews_front.hip"]
 OUT = os.path.join(HERE, "ews_mi355x", "libews_mi355x.so")
 OBJ_DIR = os.path.join(HERE, "_build")
 

@@ -31,6 +31,7 @@
 #include <hip/hip_runtime.h>
 
 #include "ews_hip.h"
+#include "ews_wide.h"
 
 namespace ews {
 namespace dense {
@@ -3231,6 +3232,7 @@ int dense_adjoint(const ews_dense_desc* s, const DPlan& p, const Args& a, const 
 extern "C" {
 
 size_t ews_dense_workspace_bytes(const ews_dense_desc* desc) {
+  if (ews::wide::eligible(desc)) return ews::wide::workspace_bytes(desc, false);
   DPlan p;
   if (dense_plan(desc, p) != EWS_OK) return 0;
   return dense_ws(p, desc->readout).total;
@@ -3251,6 +3253,8 @@ int ews_dense_forward_pass(const ews_dense_desc* desc, int pass, const float* pa
 
 int ews_dense_forward(const ews_dense_desc* desc, const float* path, const float* clock, const float* A,
                       float* out, void* workspace, ews_stream_t stream) {
+  if (ews::wide::eligible(desc))
+    return ews::wide::forward(desc, path, clock, A, out, workspace, false, (hipStream_t)stream);
   for (int pass = 0; pass < kDenseForwardPasses; ++pass) {
     const int rc = ews_dense_forward_pass(desc, pass, path, clock, A, out, workspace, stream);
     if (rc != EWS_OK) return rc;
@@ -3260,6 +3264,9 @@ int ews_dense_forward(const ews_dense_desc* desc, const float* path, const float
 
 int ews_dense_forward_keep(const ews_dense_desc* desc, const float* path, const float* clock, const float* A,
                            float* out, void* workspace, ews_stream_t stream) {
+  // d > 16: nothing is kept (the backward recomputes), the forward runs in the backward's workspace
+  if (ews::wide::eligible(desc))
+    return ews::wide::forward(desc, path, clock, A, out, workspace, true, (hipStream_t)stream);
   DPlan p;
   const int rc = dense_plan(desc, p);
   if (rc != EWS_OK) return rc;
@@ -3292,6 +3299,7 @@ int ews_dense_local_terms(const ews_dense_desc* desc, const float* path, const f
 }
 
 size_t ews_dense_backward_workspace_bytes(const ews_dense_desc* desc) {
+  if (ews::wide::eligible(desc)) return ews::wide::workspace_bytes(desc, true);
   DPlan p;
   if (dense_plan(desc, p) != EWS_OK) return 0;
   return dense_ws(p, desc->readout, true).total;
@@ -3385,6 +3393,9 @@ extern "C" {
 int ews_dense_backward(const ews_dense_desc* desc, const float* path, const float* clock, const float* A,
                        const float* grad_out, float* grad_path, float* grad_clock, float* grad_A, void* workspace,
                        ews_stream_t stream) {
+  if (ews::wide::eligible(desc))
+    return ews::wide::backward(desc, path, clock, A, grad_out, grad_path, grad_clock, grad_A, workspace,
+                          (hipStream_t)stream);
   DPlan p;
   const int rc = dense_plan(desc, p);
   if (rc != EWS_OK) return rc;
@@ -3403,6 +3414,9 @@ int ews_dense_backward(const ews_dense_desc* desc, const float* path, const floa
 int ews_dense_backward_kept(const ews_dense_desc* desc, const float* path, const float* clock, const float* A,
                             const float* out, const float* grad_out, float* grad_path, float* grad_clock,
                             float* grad_A, void* workspace, ews_stream_t stream) {
+  if (ews::wide::eligible(desc))
+    return ews::wide::backward(desc, path, clock, A, grad_out, grad_path, grad_clock, grad_A, workspace,
+                          (hipStream_t)stream);
   DPlan p;
   const int rc = dense_plan(desc, p);
   if (rc != EWS_OK) return rc;

@@ -1,0 +1,53 @@
+// Dense generators with 16 < d <= 32 at depths 1-2 (csrc/ews_wide.hip): arguments of the kernels and the host
+// entry points that ews_dense_* calls for such a descriptor.
+#pragma once
+
+#include <stddef.h>
+#include <stdint.h>
+
+#include "ews_hip.h"
+
+namespace ews {
+namespace wide {
+
+struct WArgs {
+  int B, L, n, d, N, T, C, W, lvl0, readout;
+  int flow_mode, chen, leaf, q, vm, vl_expm, vl_mode;
+  const float* path;
+  const float* clock;
+  const float* A;
+  float* out;
+  // forward workspace (padded 32 x 32 matrices, rows of 32 + 32 x 32 floats)
+  float* fl;    // flows: per interval (B, n) or per sample (B)
+  float* vlm;   // Van Loan (P, V): per interval or per sample
+  float* loc;   // local terms (B, n)
+  float* summ;  // chunk summaries (B, C)
+  float* sfl;   // chunk flow products (B, C)
+  float* car;   // carries (B, C + 1): the state before each chunk, then the final state
+  float* rows;  // padded prefix states (B, n), when kept
+  int* amax;    // max readout: row of the maximum per (sample, column)
+  // backward workspace
+  float* grow;   // row cotangents (B, n)
+  float* mu;     // each chunk's own cotangent on its carry-in state (B, C)
+  float* lend;   // cotangent on each chunk's end state from the later chunks (B, C)
+  float* dloc;   // local-term cotangents (B, n)
+  float* dfl;    // per-interval flow cotangents (B, n)
+  float* cpart;  // per-chunk sums of the shared flow's and Van Loan pair's cotangents (B, C, 3)
+  float* dvlm;   // per-interval Van Loan pair cotangents (B, n, 2)
+  float* apart;  // dA partials of the workgroups
+  float* dv;     // increment cotangents (B, n, 32)
+  float* dhl;    // series leaf's clock-step cotangents (B, n)
+  float* dhm;    // per-interval matrix functions' clock-step cotangents (B, n)
+  float* dsh;    // shared steps' cotangents (B, 2): flow, Van Loan
+};
+
+// The descriptor takes this path: 16 < d <= 32, depth 1 or 2, leaf series or van_loan.
+bool eligible(const ews_dense_desc* s);
+size_t workspace_bytes(const ews_dense_desc* s, bool backward);
+int forward(const ews_dense_desc* s, const float* path, const float* clock, const float* A, float* out,
+            void* workspace, bool backward_layout, hipStream_t st);
+int backward(const ews_dense_desc* s, const float* path, const float* clock, const float* A, const float* grad_out,
+             float* grad_path, float* grad_clock, float* grad_A, void* workspace, hipStream_t st);
+
+}  // namespace wide
+}  // namespace ews

@@ -1,0 +1,1626 @@
+// Dense generators wider than 16 channels (16 < d <= 32), depths 1 and 2, on MI355X (gfx950): the series leaf and
+// the Van Loan leaf with their flows, the Chen scan and the custom-VJP backward, behind the ews_dense_* entry points.
+//
+// Reference path (sign convention of the reference: the flow over a clock step h is M = expm_scheme(-h A)):
+//   series leaf   ews/core/series_leaf.py:72-126 (letters b_0 = v, b_p = (-h/p) A b_{p-1}; level 1
+//                 sum_p b_p / (p + 1), level 2 sum_{p+r<=q} b_p (x) b_r / ((p + r + 2)(r + 1)))
+//   Van Loan leaf ews/core/van_loan.py:31-184 (knots of the augmented exponential, reweighted by W = C^{-M}) and
+//                 the knot signature of ews/core/signature.py:20-35
+//   schemes       ews/core/expm_approx.py:13-41 (exact, euler, cayley, [2/2] pade)
+//   flows         ews/core/chen_scan.py:155-168 (per interval, or one shared step)
+//   Chen combine  ews/core/chen_scan.py:98-214 and the dense kernel ews/core/kernels/pallas_combine.py:803-858
+//   adjoints      the custom VJP of the dense kernel (pallas_combine.py:2360-2565) and JAX autodiff through the
+//                 leaf and the scheme of each matrix function
+//
+// Every matrix is padded to 32 x 32 and every vector to 32 entries with zeros (the padded block of a flow is the
+// identity, which maps the zero padding of the states to zero). A workgroup of 256 threads works on one 32 x 32
+// matrix at a time in LDS (row pitch 36, so the 8 rows a wavefront touches sit on distinct banks): thread t owns
+// row t / 8, columns 4 (t % 8) .. +3 of every product; matrix-vector products reduce over the 8 lanes of a row.
+//
+// Passes of the forward (per sample b, intervals t = 0 .. n-1, chunks of T intervals):
+//   k_wmat    the step matrices: the flow F = scheme(-c A) and the Van Loan pair (P, V) of a = c A, per interval or
+//             once per sample (uniform modes). exp / phi: Taylor polynomial of degree 12 on X / 2^s (||.||_1 <= 1),
+//             then s doublings (e^{2Y} = (e^Y)^2, phi(2Y) = phi(Y)(I + e^Y)/2); rational schemes: Gauss-Jordan
+//             elimination with partial pivoting.
+//   k_wleaf   the local terms (s1, s2) of each interval.
+//   k_wscan   SUMMARY: each chunk from the zero state, its summary and flow product; ROWS: each chunk from its
+//             carry, the rows.
+//   k_wcarry  one workgroup per sample: the carries (state before each chunk) from the summaries.
+// The Chen step (chen_scan.py:98-152): S1' = F S1 + s1, S2' = F S2 F^T + (F S1) s1^T + s2.
+//
+// Backward: the row cotangents g_t (readout adjoint), then with lambda the cotangent of the state after a step
+//   lambda_{t-1} = g_{t-1} + R_t^T lambda_t:  lambda1 <- F^T (lambda1 + lambda2 s1),  lambda2 <- F^T lambda2 F,
+//   ds1 = lambda1 + lambda2^T (F S1),  ds2 = lambda2,
+//   dF = (lambda1 + lambda2 s1) S1^T + lambda2 F S2^T + lambda2^T F S2   (S: the state before the step),
+// chunk-parallel: each chunk's own part from a zero cotangent at its end (k_wadj LOCAL), a reverse scan of the
+// chunks' transposed Chen maps (k_wadj_carry), then each chunk from its end cotangent (k_wadj FULL). Then the
+// leaf adjoints (k_wleaf_bwd) and the matrix functions' adjoints (k_wmat_bwd): for the rational schemes through
+// d(N^{-1}) = -N^{-1} dN N^{-1}; for exact exp and phi through the block identity
+//   f([[Z^T, G], [0, Z^T]]) = [[f(Z^T), L_f(Z^T)[G]], [0, f(Z^T)]],  L_f(Z)^*[G] = L_f(Z^T)[G],
+// on a 64 x 64 block matrix (G scaled to the norm of Z, the result scaled back). dA is summed over workgroup
+// partials in float64 in a fixed order.
+#include <hip/hip_runtime.h>
+
+#include <math.h>
+
+#include <algorithm>
+#include <type_traits>
+
+#include "ews_hip.h"
+#include "ews_wide.h"
+
+namespace ews {
+namespace wide {
+
+constexpr int DP = 32;            // padded channels
+constexpr int MM = DP * DP;       // floats of a padded matrix in global memory (row-major, pitch 32)
+constexpr int RW = DP + MM;       // floats of a padded state / local-term row (level 1, then level 2)
+constexpr int NT = 256;           // threads of every workgroup
+constexpr int VMAXK = 64;         // Van Loan knots per interval at most
+constexpr int QMAXW = 40;         // series order at most
+
+template <int NM>
+struct Geo {
+  static constexpr int P = NM + 4;         // LDS row pitch
+  static constexpr int SZ = NM * P;        // floats of one LDS matrix
+  static constexpr int TPR = NT / NM;      // threads per row
+  static constexpr int CPT = NM / TPR;     // columns per thread
+};
+constexpr int P32 = Geo<32>::P, S32 = Geo<32>::SZ;
+
+template <int NM>
+__device__ __forceinline__ int trow() { return (int)threadIdx.x / Geo<NM>::TPR; }
+template <int NM>
+__device__ __forceinline__ int tcol() { return ((int)threadIdx.x % Geo<NM>::TPR) * Geo<NM>::CPT; }
+
+// acc[c] = sum_k X(i, k) Y(k, j0 + c) for the thread's row i and columns j0 ..; X(i, k) = X[k][i] when TX, and
+// Y(k, j) = Y[j][k] when TY (S: float or double)
+template <int NM, bool TX, bool TY, typename S>
+__device__ __forceinline__ void mm(const S* X, const S* Y, S* acc) {
+  constexpr int P = Geo<NM>::P, CPT = Geo<NM>::CPT;
+  const int i = trow<NM>(), j0 = tcol<NM>();
+#pragma unroll
+  for (int c = 0; c < CPT; ++c) acc[c] = S(0);
+#pragma unroll 4
+  for (int k = 0; k < NM; ++k) {
+    const S x = TX ? X[k * P + i] : X[i * P + k];
+    if constexpr (!TY && std::is_same<S, float>::value) {
+#pragma unroll
+      for (int c = 0; c < CPT; c += 4) {
+        const float4 y = *reinterpret_cast<const float4*>(Y + k * P + j0 + c);
+        acc[c] = fmaf(x, y.x, acc[c]);
+        acc[c + 1] = fmaf(x, y.y, acc[c + 1]);
+        acc[c + 2] = fmaf(x, y.z, acc[c + 2]);
+        acc[c + 3] = fmaf(x, y.w, acc[c + 3]);
+      }
+    } else {
+#pragma unroll
+      for (int c = 0; c < CPT; ++c) acc[c] = fma(x, TY ? Y[(j0 + c) * P + k] : Y[k * P + j0 + c], acc[c]);
+    }
+  }
+}
+
+template <int NM, typename S>
+__device__ __forceinline__ void st(S* Z, const S* acc) {
+  constexpr int P = Geo<NM>::P, CPT = Geo<NM>::CPT;
+  const int i = trow<NM>(), j0 = tcol<NM>();
+#pragma unroll
+  for (int c = 0; c < CPT; ++c) Z[i * P + j0 + c] = acc[c];
+}
+
+template <int NM, typename S>
+__device__ __forceinline__ void ld(const S* Z, S* acc) {
+  constexpr int P = Geo<NM>::P, CPT = Geo<NM>::CPT;
+  const int i = trow<NM>(), j0 = tcol<NM>();
+#pragma unroll
+  for (int c = 0; c < CPT; ++c) acc[c] = Z[i * P + j0 + c];
+}
+
+// the thread's four entries of a padded 32 x 32 matrix in global memory (pitch 32)
+__device__ __forceinline__ float4 gld4(const float* g) {
+  return *reinterpret_cast<const float4*>(g + trow<32>() * DP + tcol<32>());
+}
+__device__ __forceinline__ void gst4(float* g, float4 v) {
+  *reinterpret_cast<float4*>(g + trow<32>() * DP + tcol<32>()) = v;
+}
+__device__ __forceinline__ void sld4(float* Z, float4 v) {
+  *reinterpret_cast<float4*>(Z + trow<32>() * P32 + tcol<32>()) = v;
+}
+__device__ __forceinline__ float4 lds4(const float* Z) {
+  return *reinterpret_cast<const float4*>(Z + trow<32>() * P32 + tcol<32>());
+}
+__device__ __forceinline__ float4 f4add(float4 a, float4 b) {
+  return float4{a.x + b.x, a.y + b.y, a.z + b.z, a.w + b.w};
+}
+__device__ __forceinline__ float4 acc4(const float* a) { return float4{a[0], a[1], a[2], a[3]}; }
+
+// y[i] = sum_k M(i, k) x[k] (M(i, k) = M[k][i] when TM), 32 x 32 in LDS: the 8 lanes of row i each take four k and
+// sum by lane exchanges; every lane of the row returns y[i]
+template <bool TM>
+__device__ __forceinline__ float mv(const float* M, const float* x) {
+  const int i = (int)threadIdx.x >> 3, p = ((int)threadIdx.x & 7) * 4;
+  float s = 0.0f;
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const int k = p + r;
+    s = fmaf(TM ? M[k * P32 + i] : M[i * P32 + k], x[k], s);
+  }
+  s += __shfl_xor(s, 1, 64);
+  s += __shfl_xor(s, 2, 64);
+  s += __shfl_xor(s, 4, 64);
+  return s;
+}
+__device__ __forceinline__ bool row_lead() { return (threadIdx.x & 7) == 0; }
+
+// sum over the workgroup (every thread returns it); red: NT / 64 floats of LDS
+__device__ __forceinline__ float block_sum(float v, float* red) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+  __syncthreads();
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+  __syncthreads();
+  float s = 0.0f;
+#pragma unroll
+  for (int w = 0; w < NT / 64; ++w) s += red[w];
+  return s;
+}
+
+// ------------------------------------------------------------------------------------------------ matrix functions
+// The forward's step matrices are formed in float64 (S = double; each is reused at every step of its sample, so its
+// rounding would add up along the scan) and stored in float32; the adjoints run in float32 (S = float).
+
+// ||X||_1 (largest column sum of magnitudes), NM x NM in LDS; every thread returns it. red: NM entries.
+template <int NM, typename S>
+__device__ S norm1(const S* X, S* red) {
+  constexpr int P = Geo<NM>::P;
+  __syncthreads();
+  if ((int)threadIdx.x < NM) {
+    S s = S(0);
+    for (int r = 0; r < NM; ++r) s += fabs(X[r * P + threadIdx.x]);
+    red[threadIdx.x] = s;
+  }
+  __syncthreads();
+  S m = S(0);
+  for (int c = 0; c < NM; ++c) m = fmax(m, red[c]);
+  __syncthreads();
+  return m;
+}
+
+// E = exp(X), Ph = phi(X) = sum_k X^k / (k + 1)! (NM x NM in LDS; X is overwritten with X / 2^s). Taylor polynomial of
+// degree 12 of phi in Y = X / 2^s with ||Y||_1 <= 1 (remainder below 1/13!), E = I + Y phi(Y), then s doublings
+// phi(2Y) = phi(Y)(I + e^Y)/2, e^{2Y} = e^Y e^Y. T1, T2: scratch matrices; red: NM entries.
+template <int NM, typename S>
+__device__ void exp_phi(S* X, S* E, S* Ph, S* T1, S* T2, S* red) {
+  constexpr int CPT = Geo<NM>::CPT;
+  const int i = trow<NM>(), j0 = tcol<NM>();
+  const S nrm = norm1<NM>(X, red);
+  int s = 0;
+  S sc = S(1);
+  while (nrm * sc > S(1) && s < 64) {
+    sc *= S(0.5);
+    ++s;
+  }
+  S acc[CPT];
+  ld<NM>(X, acc);
+#pragma unroll
+  for (int c = 0; c < CPT; ++c) acc[c] *= sc;
+  __syncthreads();
+  st<NM>(X, acc);
+  // Horner: R = c_12 I, R <- c_k I + Y R (k = 11 .. 0), c_k = 1 / (k + 1)!
+  S ck = S(1);
+  for (int k = 1; k <= 13; ++k) ck /= S(k);  // 1 / 13!
+#pragma unroll
+  for (int c = 0; c < CPT; ++c) acc[c] = (i == j0 + c) ? ck : S(0);
+  st<NM>(T1, acc);
+  __syncthreads();
+  S* R = T1;
+  S* Rn = T2;
+  for (int k = 11; k >= 0; --k) {
+    ck *= S(k + 2);  // 1 / (k + 1)!
+    mm<NM, false, false>(X, R, acc);
+#pragma unroll
+    for (int c = 0; c < CPT; ++c) acc[c] += (i == j0 + c) ? ck : S(0);
+    st<NM>(Rn, acc);
+    __syncthreads();
+    S* tmp = R;
+    R = Rn;
+    Rn = tmp;
+  }
+  mm<NM, false, false>(X, R, acc);
+#pragma unroll
+  for (int c = 0; c < CPT; ++c) acc[c] += (i == j0 + c) ? S(1) : S(0);
+  st<NM>(E, acc);
+  S ph[CPT];
+  ld<NM>(R, ph);
+  st<NM>(Ph, ph);
+  __syncthreads();
+  for (int r = 0; r < s; ++r) {
+    S pe[CPT];
+    mm<NM, false, false>(Ph, E, pe);
+    mm<NM, false, false>(E, E, acc);
+    __syncthreads();
+#pragma unroll
+    for (int c = 0; c < CPT; ++c) ph[c] = S(0.5) * (ph[c] + pe[c]);
+    st<NM>(Ph, ph);
+    st<NM>(E, acc);
+    __syncthreads();
+  }
+}
+
+// Y = N^{-1} (32 x 32 in LDS) by Gauss-Jordan elimination on [N | I] with partial pivoting (largest magnitude in the
+// column among the rows not yet reduced, ties to the lower row; rows are swapped). Aug: 32 x 68 entries of LDS;
+// sh: 64 entries of LDS.
+template <typename S>
+__device__ void inv32(const S* Nm, S* Y, S* Aug, S* sh) {
+  constexpr int AP = 68;
+  const int tid = threadIdx.x;
+  for (int e = tid; e < 32 * 64; e += NT) {
+    const int r = e >> 6, c = e & 63;
+    Aug[r * AP + c] = c < 32 ? Nm[r * P32 + c] : (c - 32 == r ? S(1) : S(0));
+  }
+  __syncthreads();
+  for (int k = 0; k < 32; ++k) {
+    if (tid < 64) {  // wavefront 0: the pivot row
+      S v = (tid < 32 && tid >= k) ? fabs(Aug[tid * AP + k]) : S(-1);
+      int r = tid;
+#pragma unroll
+      for (int o = 32; o > 0; o >>= 1) {
+        const S v2 = __shfl_xor(v, o, 64);
+        const int r2 = __shfl_xor(r, o, 64);
+        if (v2 > v || (v2 == v && r2 < r)) {
+          v = v2;
+          r = r2;
+        }
+      }
+      if (tid == 0) sh[32] = S(r);
+    }
+    __syncthreads();
+    const int pr = (int)sh[32];
+    if (pr != k && tid < 64) {
+      const S a = Aug[k * AP + tid], b = Aug[pr * AP + tid];
+      Aug[k * AP + tid] = b;
+      Aug[pr * AP + tid] = a;
+    }
+    __syncthreads();
+    if (tid < 32) sh[tid] = Aug[tid * AP + k];  // the elimination factors (column k)
+    __syncthreads();
+    const S inv = S(1) / sh[k];
+    if (tid < 64) Aug[k * AP + tid] *= inv;
+    __syncthreads();
+    for (int e = tid; e < 32 * 64; e += NT) {
+      const int r = e >> 6, c = e & 63;
+      if (r != k) Aug[r * AP + c] = fma(-sh[r], Aug[k * AP + c], Aug[r * AP + c]);
+    }
+    __syncthreads();
+  }
+  for (int e = tid; e < 32 * 32; e += NT) {
+    const int r = e >> 5, c = e & 31;
+    Y[r * P32 + c] = Aug[r * AP + 32 + c];
+  }
+  __syncthreads();
+}
+
+// LDS layout of the matrix-function workgroups (entries of S): A, X, Y, T, U, N (32 x 36 each), Aug (32 x 68), small;
+// then the exact scheme's block area: five 32 x 36 matrices in the forward, five 64 x 68 in the adjoint.
+constexpr int MF_A = 0, MF_X = S32, MF_Y = 2 * S32, MF_T = 3 * S32, MF_U = 4 * S32, MF_N = 5 * S32;
+constexpr int MF_AUG = 6 * S32, MF_SH = MF_AUG + 32 * 68, MF_RED = MF_SH + 64, MF_BLK = MF_RED + 64;
+constexpr int S64 = Geo<64>::SZ;
+constexpr int MF_ENT_FWD = MF_BLK + 5 * S32, MF_ENT_BWD = MF_BLK, MF_ENT_BWD_EXACT = MF_BLK + 5 * S64;
+
+template <typename S>
+__device__ __forceinline__ void set_ident32(S* Z, S diag) {
+  const int i = trow<32>(), j0 = tcol<32>();
+  S a[4];
+#pragma unroll
+  for (int c = 0; c < 4; ++c) a[c] = (i == j0 + c) ? diag : S(0);
+  st<32>(Z, a);
+}
+
+// N = I + alpha X + beta X^2 into U (X in LDS)
+template <typename S>
+__device__ void form_n(const S* X, S* U, S alpha, S beta) {
+  const int i = trow<32>(), j0 = tcol<32>();
+  S x2[4] = {S(0), S(0), S(0), S(0)}, x[4];
+  if (beta != S(0)) mm<32, false, false>(X, X, x2);
+  ld<32>(X, x);
+  S n[4];
+#pragma unroll
+  for (int c = 0; c < 4; ++c) n[c] = ((i == j0 + c) ? S(1) : S(0)) + alpha * x[c] + beta * x2[c];
+  st<32>(U, n);
+  __syncthreads();
+}
+
+__device__ __forceinline__ void scheme_ab(int scheme, bool flow, double& alpha, double& beta) {
+  // N = I + alpha X + beta X^2 of the rational schemes (the flow's cayley / pade, the Van Loan V)
+  alpha = 0.5;
+  beta = 0.0;
+  if (scheme == EWS_EXPM_PADE) beta = 1.0 / 12.0;
+  if (scheme == EWS_EXPM_EULER && !flow) alpha = 1.0;
+}
+
+template <typename S>
+__device__ __forceinline__ void load_A(int d, const float* Ag, S* A) {
+  for (int e = threadIdx.x; e < MM; e += NT) {
+    const int r = e >> 5, c = e & 31;
+    A[r * P32 + c] = (r < d && c < d) ? S(Ag[r * d + c]) : S(0);
+  }
+}
+
+// Forward matrix functions of X = c A in float64 (A, X in the LDS layout above): flow F = scheme(-X) into out0, or
+// the Van Loan pair P into out0, V into out1 (global float32, pitch 32).
+__device__ void matfn_fwd(double* sm, int scheme, bool flow, double c, float* out0, float* out1) {
+  double* A = sm + MF_A;
+  double* X = sm + MF_X;
+  double* Y = sm + MF_Y;
+  double* U = sm + MF_U;
+  const int i = trow<32>(), j0 = tcol<32>();
+  double a[4];
+  ld<32>(A, a);
+#pragma unroll
+  for (int k = 0; k < 4; ++k) a[k] *= c;
+  st<32>(X, a);
+  __syncthreads();
+  double r0[4], r1[4];
+  if (scheme == EWS_EXPM_EXACT) {
+    double* B = sm + MF_BLK;  // Z = -X, E = exp(Z), Ph = phi(Z)
+    double* Z = B;
+    double* E = B + S32;
+    double* Ph = B + 2 * S32;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) a[k] = -a[k];
+    st<32>(Z, a);
+    __syncthreads();
+    exp_phi<32>(Z, E, Ph, B + 3 * S32, B + 4 * S32, sm + MF_RED);
+    ld<32>(E, r0);
+    ld<32>(Ph, r1);
+  } else if (flow && scheme == EWS_EXPM_EULER) {
+#pragma unroll
+    for (int k = 0; k < 4; ++k) r0[k] = ((i == j0 + k) ? 1.0 : 0.0) - a[k];
+  } else {
+    double alpha, beta;
+    scheme_ab(scheme, flow, alpha, beta);
+    form_n(X, U, alpha, beta);
+    inv32(U, Y, sm + MF_AUG, sm + MF_SH);
+    double y[4];
+    ld<32>(Y, y);
+    if (scheme == EWS_EXPM_PADE) {  // F = I - Y X (flow), P = I - V X (Van Loan, V = Y)
+      double yx[4];
+      mm<32, false, false>(Y, X, yx);
+#pragma unroll
+      for (int k = 0; k < 4; ++k) r0[k] = ((i == j0 + k) ? 1.0 : 0.0) - yx[k];
+    } else if (scheme == EWS_EXPM_CAYLEY) {  // F = P = 2Y - I
+#pragma unroll
+      for (int k = 0; k < 4; ++k) r0[k] = 2.0 * y[k] - ((i == j0 + k) ? 1.0 : 0.0);
+    } else {  // Van Loan euler: P = V = Y
+#pragma unroll
+      for (int k = 0; k < 4; ++k) r0[k] = y[k];
+    }
+#pragma unroll
+    for (int k = 0; k < 4; ++k) r1[k] = y[k];
+  }
+  gst4(out0, float4{(float)r0[0], (float)r0[1], (float)r0[2], (float)r0[3]});
+  if (!flow) gst4(out1, float4{(float)r1[0], (float)r1[1], (float)r1[2], (float)r1[3]});
+  __syncthreads();
+}
+
+// Adjoint of matfn_fwd (float32): given the cotangents G0 (of F, or of P) and G1 (of V; unused for a flow) in LDS
+// (T, U), returns in xb the thread's four entries of the cotangent of X = c A.
+__device__ void matfn_bwd(float* sm, int scheme, bool flow, float c, float* xb) {
+  float* A = sm + MF_A;
+  float* X = sm + MF_X;
+  float* Y = sm + MF_Y;
+  float* G0 = sm + MF_T;
+  float* G1 = sm + MF_U;
+  const int i = trow<32>(), j0 = tcol<32>();
+  float a[4];
+  ld<32>(A, a);
+#pragma unroll
+  for (int k = 0; k < 4; ++k) a[k] *= c;
+  st<32>(X, a);
+  __syncthreads();
+  if (scheme == EWS_EXPM_EXACT) {
+    // Z = -X; dZ = L_exp(Z^T)[G0] (+ L_phi(Z^T)[G1]); each from the 64 x 64 block [[Z^T, G/tau], [0, Z^T]]
+    float* B = sm + MF_BLK;
+    constexpr int P = Geo<64>::P;
+    const float zn = fmaxf(norm1<32>(X, sm + MF_RED), 1.0f);  // G is scaled to at most max(||Z||_1, 1)
+    float dz[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    for (int pass = 0; pass < (flow ? 1 : 2); ++pass) {
+      const float* Gs = pass == 0 ? G0 : G1;
+      const float gn = norm1<32>(Gs, sm + MF_RED);
+      if (gn == 0.0f) continue;  // uniform over the workgroup
+      const float tau = gn / zn;
+      for (int e = threadIdx.x; e < 64 * 64; e += NT) {
+        const int r = e >> 6, q = e & 63;
+        float v = 0.0f;
+        if (r < 32 && q < 32) v = -X[q * P32 + r];                   // Z^T
+        else if (r >= 32 && q >= 32) v = -X[(q - 32) * P32 + (r - 32)];
+        else if (r < 32 && q >= 32) v = Gs[r * P32 + (q - 32)] / tau;
+        B[r * P + q] = v;
+      }
+      __syncthreads();
+      exp_phi<64>(B, B + S64, B + 2 * S64, B + 3 * S64, B + 4 * S64, sm + MF_RED);
+      const float* R = pass == 0 ? B + S64 : B + 2 * S64;  // exp for P (or F), phi for V
+#pragma unroll
+      for (int k = 0; k < 4; ++k) dz[k] = fmaf(tau, R[i * P + 32 + j0 + k], dz[k]);
+      __syncthreads();
+    }
+#pragma unroll
+    for (int k = 0; k < 4; ++k) xb[k] = -dz[k];
+    return;
+  }
+  float g0[4];
+  ld<32>(G0, g0);
+  if (flow && scheme == EWS_EXPM_EULER) {  // F = I - X
+#pragma unroll
+    for (int k = 0; k < 4; ++k) xb[k] = -g0[k];
+    return;
+  }
+  double alpha_d, beta_d;
+  scheme_ab(scheme, flow, alpha_d, beta_d);
+  const float alpha = (float)alpha_d, beta = (float)beta_d;
+  form_n(X, sm + MF_N, alpha, beta);
+  inv32(sm + MF_N, Y, sm + MF_AUG, sm + MF_SH);
+  // Yb: the cotangent of Y; direct: the part of dX not through Y
+  float yb[4], direct[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+  if (scheme == EWS_EXPM_PADE) {
+    float t[4];
+    mm<32, false, true>(G0, X, t);       // G0 X^T
+    mm<32, true, false>(Y, G0, direct);  // Y^T G0
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      yb[k] = -t[k];
+      direct[k] = -direct[k];
+    }
+  } else if (scheme == EWS_EXPM_CAYLEY) {
+#pragma unroll
+    for (int k = 0; k < 4; ++k) yb[k] = 2.0f * g0[k];
+  } else {  // Van Loan euler: P = V = Y
+#pragma unroll
+    for (int k = 0; k < 4; ++k) yb[k] = g0[k];
+  }
+  if (!flow) {
+    float g1[4];
+    ld<32>(G1, g1);
+#pragma unroll
+    for (int k = 0; k < 4; ++k) yb[k] += g1[k];
+  }
+  // Nb = -Y^T Yb Y^T;  dX = direct + alpha Nb + beta (Nb X^T + X^T Nb)
+  float* W1 = sm + MF_AUG;  // free after the inverse (32 x 68 >= 32 x 36)
+  __syncthreads();
+  st<32>(W1, yb);
+  __syncthreads();
+  float t1[4];
+  mm<32, false, true>(W1, Y, t1);  // Yb Y^T
+  __syncthreads();
+  st<32>(W1, t1);
+  __syncthreads();
+  float nb[4];
+  mm<32, true, false>(Y, W1, nb);  // Y^T (Yb Y^T)
+#pragma unroll
+  for (int k = 0; k < 4; ++k) nb[k] = -nb[k];
+  __syncthreads();
+  st<32>(W1, nb);
+  __syncthreads();
+#pragma unroll
+  for (int k = 0; k < 4; ++k) xb[k] = direct[k] + alpha * nb[k];
+  if (beta != 0.0f) {
+    float p1[4], p2[4];
+    mm<32, false, true>(W1, X, p1);  // Nb X^T
+    mm<32, true, false>(X, W1, p2);  // X^T Nb
+#pragma unroll
+    for (int k = 0; k < 4; ++k) xb[k] = fmaf(beta, p1[k] + p2[k], xb[k]);
+  }
+  __syncthreads();
+}
+
+// ------------------------------------------------------------------------------------------------ steps
+// Clock step of the flow of interval t (chen_scan.py:155-168): per interval, or the shared step; interval 0 of the
+// basepoint mode has the identity flow.
+__device__ __forceinline__ float flow_step(const WArgs& a, const float* th, int t, bool& ident) {
+  ident = false;
+  if (a.flow_mode == EWS_FLOW_PER_INTERVAL) return th[t + 1] - th[t];
+  if (a.flow_mode == EWS_FLOW_CACHED) return th[1] - th[0];
+  ident = t == 0;
+  return th[2] - th[1];
+}
+// Van Loan step dt / M of interval t (van_loan.py:31-160): per interval; the uniform modes share dt = th[1] - th[0]
+// (or th[2] - th[1] with the pure jump at interval 0 of the basepoint mode); a shared dt <= 1e-12 is the jump
+// (linear knots: P = V = I, fixed = true).
+__device__ __forceinline__ float vl_step(const WArgs& a, const float* th, int t, bool& fixed) {
+  fixed = false;
+  if (a.vl_mode == EWS_FLOW_PER_INTERVAL) return (th[t + 1] - th[t]) / (float)a.vm;
+  const float dt = a.vl_mode == EWS_FLOW_CACHED ? th[1] - th[0] : th[2] - th[1];
+  fixed = !(dt > 1e-12f) || (a.vl_mode == EWS_FLOW_CACHED_BASEPOINT && t == 0);
+  return fixed ? 0.0f : dt / (float)a.vm;
+}
+
+// Step matrices: item = interval (per-interval modes) or sample (shared modes); the flow and the Van Loan pair are
+// each formed when their mode matches the item kind.
+__global__ __launch_bounds__(NT) void k_wmat(WArgs a, int per_interval) {
+  extern __shared__ __align__(16) double smd[];
+  load_A(a.d, a.A, smd + MF_A);
+  __syncthreads();
+  const long items = per_interval ? (long)a.B * a.n : a.B;
+  const bool do_flow = (a.flow_mode == EWS_FLOW_PER_INTERVAL) == (per_interval != 0);
+  const bool do_vl = a.leaf == EWS_LEAF_VAN_LOAN && (a.vl_mode == EWS_FLOW_PER_INTERVAL) == (per_interval != 0);
+  for (long it = blockIdx.x; it < items; it += gridDim.x) {
+    const int b = per_interval ? (int)(it / a.n) : (int)it;
+    const int t = per_interval ? (int)(it - (long)b * a.n) : 1;
+    const float* th = a.clock + (size_t)b * a.L;
+    if (do_flow) {
+      bool ident;
+      const float h = flow_step(a, th, t, ident);
+      matfn_fwd(smd, a.chen, true, (double)h, a.fl + it * MM, nullptr);
+    }
+    if (do_vl) {
+      bool fixed;
+      const float c = vl_step(a, th, t, fixed);
+      matfn_fwd(smd, fixed ? EWS_EXPM_EULER : a.vl_expm, false, fixed ? 0.0 : (double)c, a.vlm + it * 2 * MM,
+                a.vlm + it * 2 * MM + MM);
+    }
+  }
+}
+
+// The flow of interval t of sample b into F (and its transpose into Ft), LDS
+__device__ __forceinline__ void load_flow(const WArgs& a, int b, int t, float* F, float* Ft) {
+  const float* th = a.clock + (size_t)b * a.L;
+  bool ident;
+  flow_step(a, th, t, ident);
+  float4 v;
+  if (ident) {
+    const int i = trow<32>(), j0 = tcol<32>();
+    v = float4{i == j0 ? 1.0f : 0.0f, i == j0 + 1 ? 1.0f : 0.0f, i == j0 + 2 ? 1.0f : 0.0f, i == j0 + 3 ? 1.0f : 0.0f};
+  } else {
+    const size_t item = a.flow_mode == EWS_FLOW_PER_INTERVAL ? (size_t)b * a.n + t : (size_t)b;
+    v = gld4(a.fl + item * MM);
+  }
+  sld4(F, v);
+  const int i = trow<32>(), j0 = tcol<32>();
+  Ft[(j0 + 0) * P32 + i] = v.x;
+  Ft[(j0 + 1) * P32 + i] = v.y;
+  Ft[(j0 + 2) * P32 + i] = v.z;
+  Ft[(j0 + 3) * P32 + i] = v.w;
+}
+
+// ------------------------------------------------------------------------------------------------ local terms
+// LDS of the leaf kernels (floats): A, P, V (32 x 36 each), vectors, the knot / letter table and its cotangents.
+constexpr int LF_A = 0, LF_P = S32, LF_V = 2 * S32, LF_S2 = 3 * S32, LF_VEC = 4 * S32;  // vectors: 8 x 32
+constexpr int LF_TAB = LF_VEC + 8 * 32;        // up to 65 rows of 32: knots Delta_m (or letters b_p)
+constexpr int LF_TAB2 = LF_TAB + 65 * 32;      // Y_m (or u_p)
+constexpr int LF_TAB3 = LF_TAB2 + 65 * 32;     // R_m, Pre_m (or w_p, A b_{p-1})
+constexpr int LF_TAB4 = LF_TAB3 + 65 * 32;     // cotangents
+constexpr int LF_RED = LF_TAB4 + 65 * 32;
+constexpr int LF_FLOATS = LF_RED + 64;
+
+__device__ __forceinline__ float inv_f(int n) { return 1.0f / (float)n; }
+__device__ __forceinline__ float c2coef(int p, int r) { return 1.0f / ((float)(p + r + 2) * (float)(r + 1)); }
+
+// the step matrices of the interval's Van Loan leaf into P, V (LDS)
+__device__ __forceinline__ void load_vl(const WArgs& a, int b, int t, float* P, float* V) {
+  bool fixed;
+  vl_step(a, a.clock + (size_t)b * a.L, t, fixed);
+  if (fixed && a.vl_mode != EWS_FLOW_PER_INTERVAL) {
+    set_ident32(P, 1.0f);
+    set_ident32(V, 1.0f);
+    return;
+  }
+  const size_t item = a.vl_mode == EWS_FLOW_PER_INTERVAL ? (size_t)b * a.n + t : (size_t)b;
+  sld4(P, gld4(a.vlm + item * 2 * MM));
+  sld4(V, gld4(a.vlm + item * 2 * MM + MM));
+}
+
+// knots of the interval: Delta_M = V w, Delta_{m-1} = P Delta_m (rows 0 .. M-1 of D hold Delta_1 .. Delta_M),
+// w = v / M in wv
+__device__ void vl_knots(const WArgs& a, const float* P, const float* V, const float* wv, float* D) {
+  const int M = a.vm, i = (int)threadIdx.x >> 3;
+  float y = mv<false>(V, wv);
+  if (threadIdx.x < 256 && row_lead()) D[(M - 1) * 32 + i] = y;
+  __syncthreads();
+  for (int m = M - 1; m >= 1; --m) {
+    y = mv<false>(P, D + m * 32);
+    if (row_lead()) D[(m - 1) * 32 + i] = y;
+    __syncthreads();
+  }
+}
+
+// interval's local terms (s1 into s1v, s2 into the thread's registers)
+template <int N>
+__device__ void leaf_fwd(const WArgs& a, float* sm, int b, int t, float* s1v, float* s2r) {
+  float* A = sm + LF_A;
+  float* vec = sm + LF_VEC;
+  float* T1 = sm + LF_TAB;
+  float* T2 = sm + LF_TAB2;
+  const int tid = threadIdx.x, i = tid >> 3, j0 = (tid & 7) * 4;
+  const float* x = a.path + ((size_t)b * a.L + t) * a.d;
+  const float* th = a.clock + (size_t)b * a.L;
+  if (a.leaf == EWS_LEAF_VAN_LOAN) {
+    float* P = sm + LF_P;
+    float* V = sm + LF_V;
+    load_vl(a, b, t, P, V);
+    if (tid < 32) vec[tid] = tid < a.d ? (x[a.d + tid] - x[tid]) / (float)a.vm : 0.0f;
+    __syncthreads();
+    vl_knots(a, P, V, vec, T1);
+    const int M = a.vm;
+    if (tid < 32) {  // s1 and Y_m = Pre_m + Delta_m / 2
+      float pre = 0.0f;
+      for (int m = 0; m < M; ++m) {
+        const float dm = T1[m * 32 + tid];
+        T2[m * 32 + tid] = fmaf(0.5f, dm, pre);
+        pre += dm;
+      }
+      s1v[tid] = pre;
+    }
+    __syncthreads();
+    if constexpr (N >= 2) {  // s2 = sum_m Y_m Delta_m^T
+#pragma unroll
+      for (int c = 0; c < 4; ++c) s2r[c] = 0.0f;
+      for (int m = 0; m < M; ++m) {
+        const float y = T2[m * 32 + i];
+        const float4 dl = *reinterpret_cast<const float4*>(T1 + m * 32 + j0);
+        s2r[0] = fmaf(y, dl.x, s2r[0]);
+        s2r[1] = fmaf(y, dl.y, s2r[1]);
+        s2r[2] = fmaf(y, dl.z, s2r[2]);
+        s2r[3] = fmaf(y, dl.w, s2r[3]);
+      }
+    }
+  } else {
+    // letters b_p (rows of T1), u_p = sum_{r <= q-p} C2[p][r] b_r (rows of T2)
+    const int q = a.q;
+    const float h = th[t + 1] - th[t];
+    if (tid < 32) T1[tid] = tid < a.d ? x[a.d + tid] - x[tid] : 0.0f;
+    __syncthreads();
+    for (int p = 1; p <= q; ++p) {
+      const float y = mv<false>(A, T1 + (p - 1) * 32);
+      if (row_lead()) T1[p * 32 + i] = (-h / (float)p) * y;
+      __syncthreads();
+    }
+    if (tid < 32) {
+      float s = 0.0f;
+      for (int p = 0; p <= q; ++p) s = fmaf(inv_f(p + 1), T1[p * 32 + tid], s);
+      s1v[tid] = s;
+    }
+    if constexpr (N >= 2) {
+      for (int e = tid; e < (q + 1) * 32; e += NT) {
+        const int p = e >> 5, k = e & 31;
+        float s = 0.0f;
+        for (int r = 0; r <= q - p; ++r) s = fmaf(c2coef(p, r), T1[r * 32 + k], s);
+        T2[p * 32 + k] = s;
+      }
+      __syncthreads();
+#pragma unroll
+      for (int c = 0; c < 4; ++c) s2r[c] = 0.0f;
+      for (int p = 0; p <= q; ++p) {  // s2 = sum_p b_p u_p^T
+        const float y = T1[p * 32 + i];
+        const float4 u = *reinterpret_cast<const float4*>(T2 + p * 32 + j0);
+        s2r[0] = fmaf(y, u.x, s2r[0]);
+        s2r[1] = fmaf(y, u.y, s2r[1]);
+        s2r[2] = fmaf(y, u.z, s2r[2]);
+        s2r[3] = fmaf(y, u.w, s2r[3]);
+      }
+    }
+  }
+  __syncthreads();
+}
+
+template <int N>
+__global__ __launch_bounds__(NT) void k_wleaf(WArgs a) {
+  __shared__ __align__(16) float sm[LF_FLOATS];
+  float* s1v = sm + LF_VEC + 32;
+  load_A(a.d, a.A, sm + LF_A);
+  __syncthreads();
+  const long items = (long)a.B * a.n;
+  for (long it = blockIdx.x; it < items; it += gridDim.x) {
+    const int b = (int)(it / a.n), t = (int)(it - (long)b * a.n);
+    float s2r[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    leaf_fwd<N>(a, sm, b, t, s1v, s2r);
+    float* row = a.loc + it * RW;
+    if (threadIdx.x < 32) row[threadIdx.x] = s1v[threadIdx.x];
+    if constexpr (N >= 2) gst4(row + DP, acc4(s2r));
+    __syncthreads();
+  }
+}
+
+// ------------------------------------------------------------------------------------------------ Chen scan
+constexpr int SC_F = 0, SC_FT = S32, SC_S2 = 2 * S32, SC_T = 3 * S32, SC_PH = 4 * S32, SC_PN = 5 * S32;
+constexpr int SC_VEC = 6 * S32;  // S1, y1, s1 (32 each)
+constexpr int SC_FLOATS = SC_VEC + 3 * 32;
+
+// one Chen step of the state (S1, S2) in LDS by (F, Ft, s1 in LDS; s2 the thread's entries); with PHI the flow
+// product Ph <- F Ph as well (Pn scratch; the pointers swap)
+template <int N, bool PHI>
+__device__ __forceinline__ void chen_step(float* sm, const float4 s2, float*& Ph, float*& Pn) {
+  float* F = sm + SC_F;
+  float* Ft = sm + SC_FT;
+  float* S2 = sm + SC_S2;
+  float* T = sm + SC_T;
+  float* S1 = sm + SC_VEC;
+  float* y1 = S1 + 32;
+  float* s1 = S1 + 64;
+  const int i = (int)threadIdx.x >> 3, j0 = ((int)threadIdx.x & 7) * 4;
+  const float y = mv<false>(F, S1);
+  float acc[4];
+  if constexpr (N >= 2) {
+    mm<32, false, false>(F, S2, acc);
+    st<32>(T, acc);
+  }
+  if constexpr (PHI) {
+    float pa[4];
+    mm<32, false, false>(F, Ph, pa);
+    st<32>(Pn, pa);
+  }
+  if (row_lead()) y1[i] = y;
+  __syncthreads();
+  if constexpr (N >= 2) {
+    mm<32, false, false>(T, Ft, acc);  // F S2 F^T
+    const float4 sv = *reinterpret_cast<const float4*>(s1 + j0);
+    acc[0] += fmaf(y, sv.x, s2.x);
+    acc[1] += fmaf(y, sv.y, s2.y);
+    acc[2] += fmaf(y, sv.z, s2.z);
+    acc[3] += fmaf(y, sv.w, s2.w);
+    st<32>(S2, acc);
+  }
+  if (row_lead()) S1[i] = y + s1[i];
+  if constexpr (PHI) {
+    float* tmp = Ph;
+    Ph = Pn;
+    Pn = tmp;
+  }
+  __syncthreads();
+}
+
+__device__ __forceinline__ void load_state(const float* g, float* S1, float* S2) {
+  if (threadIdx.x < 32) S1[threadIdx.x] = g[threadIdx.x];
+  sld4(S2, gld4(g + DP));
+}
+__device__ __forceinline__ void store_state(float* g, const float* S1, const float* S2) {
+  if (threadIdx.x < 32) g[threadIdx.x] = S1[threadIdx.x];
+  gst4(g + DP, lds4(S2));
+}
+
+// the packed output row (level 0, S1[:d], S2[:d, :d]) of the state in LDS
+template <int N>
+__device__ __forceinline__ void store_packed(const WArgs& a, float* o, const float* S1, const float* S2) {
+  const int d = a.d;
+  if (a.lvl0 && threadIdx.x == 0) o[0] = 1.0f;
+  o += a.lvl0;
+  if ((int)threadIdx.x < d) o[threadIdx.x] = S1[threadIdx.x];
+  if constexpr (N >= 2) {
+    for (int e = threadIdx.x; e < d * d; e += NT) {
+      const int r = e / d, c = e - r * d;
+      o[d + e] = S2[r * P32 + c];
+    }
+  }
+}
+
+constexpr int SCAN_SUMMARY = 0, SCAN_ROWS = 1;
+
+template <int N, int MODE>
+__global__ __launch_bounds__(NT) void k_wscan(WArgs a) {
+  __shared__ __align__(16) float sm[SC_FLOATS];
+  const int c = blockIdx.x, b = blockIdx.y;
+  const int t0 = c * a.T, t1 = min(a.n, t0 + a.T);
+  float* S1 = sm + SC_VEC;
+  float* S2 = sm + SC_S2;
+  float* s1 = S1 + 64;
+  float* Ph = sm + SC_PH;
+  float* Pn = sm + SC_PN;
+  if (MODE == SCAN_SUMMARY) {
+    if (threadIdx.x < 32) S1[threadIdx.x] = 0.0f;
+    sld4(S2, float4{0.0f, 0.0f, 0.0f, 0.0f});
+    set_ident32(Ph, 1.0f);
+  } else {
+    load_state(a.car + ((size_t)b * (a.C + 1) + c) * RW, S1, S2);
+  }
+  const bool cached = a.flow_mode != EWS_FLOW_PER_INTERVAL;
+  for (int t = t0; t < t1; ++t) {
+    if (!cached || t == t0 || (a.flow_mode == EWS_FLOW_CACHED_BASEPOINT && t <= 1))
+      load_flow(a, b, t, sm + SC_F, sm + SC_FT);
+    const float* lrow = a.loc + ((size_t)b * a.n + t) * RW;
+    if (threadIdx.x < 32) s1[threadIdx.x] = lrow[threadIdx.x];
+    const float4 s2 = N >= 2 ? gld4(lrow + DP) : float4{0.0f, 0.0f, 0.0f, 0.0f};
+    __syncthreads();
+    chen_step<N, MODE == SCAN_SUMMARY>(sm, s2, Ph, Pn);
+    if constexpr (MODE == SCAN_ROWS) {
+      const size_t r = (size_t)b * a.n + t;
+      if (a.rows) store_state(a.rows + r * RW, S1, S2);
+      if (a.readout == EWS_READOUT_PREFIX) store_packed<N>(a, a.out + r * a.W, S1, S2);
+    }
+  }
+  if (MODE == SCAN_SUMMARY) {
+    store_state(a.summ + ((size_t)b * a.C + c) * RW, S1, S2);
+    gst4(a.sfl + ((size_t)b * a.C + c) * MM, lds4(Ph));
+  }
+}
+
+// carries: car[b][0] = 0, car[b][c + 1] = the chunk-c Chen map of car[b][c] (flow product and summary)
+template <int N>
+__global__ __launch_bounds__(NT) void k_wcarry(WArgs a) {
+  __shared__ __align__(16) float sm[SC_FLOATS];
+  const int b = blockIdx.x;
+  float* S1 = sm + SC_VEC;
+  float* S2 = sm + SC_S2;
+  float* s1 = S1 + 64;
+  float* F = sm + SC_F;
+  float* Ft = sm + SC_FT;
+  if (threadIdx.x < 32) S1[threadIdx.x] = 0.0f;
+  sld4(S2, float4{0.0f, 0.0f, 0.0f, 0.0f});
+  __syncthreads();
+  float* car = a.car + (size_t)b * (a.C + 1) * RW;
+  store_state(car, S1, S2);
+  float* dummy0 = nullptr;
+  float* dummy1 = nullptr;
+  for (int c = 0; c < a.C; ++c) {
+    const float4 v = gld4(a.sfl + ((size_t)b * a.C + c) * MM);
+    sld4(F, v);
+    const int i = trow<32>(), j0 = tcol<32>();
+    Ft[(j0 + 0) * P32 + i] = v.x;
+    Ft[(j0 + 1) * P32 + i] = v.y;
+    Ft[(j0 + 2) * P32 + i] = v.z;
+    Ft[(j0 + 3) * P32 + i] = v.w;
+    const float* sr = a.summ + ((size_t)b * a.C + c) * RW;
+    if (threadIdx.x < 32) s1[threadIdx.x] = sr[threadIdx.x];
+    const float4 s2 = N >= 2 ? gld4(sr + DP) : float4{0.0f, 0.0f, 0.0f, 0.0f};
+    __syncthreads();
+    chen_step<N, false>(sm, s2, dummy0, dummy1);
+    store_state(car + (size_t)(c + 1) * RW, S1, S2);
+  }
+}
+
+// terminal / mean / max readouts: per sample and packed column
+__global__ __launch_bounds__(NT) void k_wreadout(WArgs a) {
+  const int b = blockIdx.y, col = blockIdx.x * NT + threadIdx.x;
+  if (col >= a.W) return;
+  float* o = a.out + (size_t)b * a.W;
+  if (a.lvl0 && col == 0) {
+    o[0] = 1.0f;
+    return;
+  }
+  const int e = col - a.lvl0, d = a.d;
+  const int pe = e < d ? e : DP + ((e - d) / d) * DP + (e - d) % d;  // padded index
+  if (a.readout == EWS_READOUT_TERMINAL) {
+    o[col] = a.car[((size_t)b * (a.C + 1) + a.C) * RW + pe];
+    return;
+  }
+  const float* r = a.rows + (size_t)b * a.n * RW + pe;
+  if (a.readout == EWS_READOUT_MEAN) {
+    float s = 0.0f;
+    for (int t = 0; t < a.n; ++t) s += r[(size_t)t * RW];
+    o[col] = s / (float)a.n;
+  } else {
+    float best = r[0];
+    int arg = 0;
+    for (int t = 1; t < a.n; ++t) {
+      const float v = r[(size_t)t * RW];
+      if (v > best) {
+        best = v;
+        arg = t;
+      }
+    }
+    o[col] = best;
+    if (a.amax) a.amax[(size_t)b * a.W + col] = arg;
+  }
+}
+
+// ------------------------------------------------------------------------------------------------ backward
+// row cotangents g (B, n, RW) padded from the readout's cotangent
+__global__ __launch_bounds__(NT) void k_wgrows(WArgs a, const float* gout) {
+  const long total = (long)a.B * a.n * RW;
+  for (long e = (long)blockIdx.x * NT + threadIdx.x; e < total; e += (long)gridDim.x * NT) {
+    const int pe = (int)(e % RW);
+    const long r = e / RW;
+    const int b = (int)(r / a.n), t = (int)(r - (long)b * a.n);
+    const int d = a.d;
+    int col = -1;  // packed column of the padded entry
+    if (pe < DP) {
+      if (pe < d) col = pe;
+    } else {
+      const int q = pe - DP, ri = q >> 5, ci = q & 31;
+      if (a.N >= 2 && ri < d && ci < d) col = d + ri * d + ci;
+    }
+    float g = 0.0f;
+    if (col >= 0) {
+      col += a.lvl0;
+      if (a.readout == EWS_READOUT_PREFIX) g = gout[r * a.W + col];
+      else if (a.readout == EWS_READOUT_TERMINAL) g = t == a.n - 1 ? gout[(size_t)b * a.W + col] : 0.0f;
+      else if (a.readout == EWS_READOUT_MEAN) g = gout[(size_t)b * a.W + col] / (float)a.n;
+      else g = a.amax[(size_t)b * a.W + col] == t ? gout[(size_t)b * a.W + col] : 0.0f;
+    }
+    a.grow[e] = g;
+  }
+}
+
+// adjoint scan LDS (floats): F, Ft, lambda2, S2 (state before the step), H, G1, G2 (32 x 36 each); vectors
+constexpr int AD_F = 0, AD_FT = S32, AD_L2 = 2 * S32, AD_S2 = 3 * S32, AD_H = 4 * S32, AD_G1 = 5 * S32,
+              AD_G2 = 6 * S32, AD_VEC = 7 * S32;  // lambda1, S1, s1, y1, rho1 (32 each)
+constexpr int AD_FLOATS = AD_VEC + 5 * 32;
+constexpr int ADJ_LOCAL = 0, ADJ_FULL = 1;
+
+// one reverse step: (lambda1, lambda2) of the state after the step (row cotangent included) to the state before it;
+// FULL: also ds1, ds2 (into dl) and dF (returned in df) from the state before the step (S1, S2 in LDS)
+template <int N, int MODE>
+__device__ __forceinline__ void adj_step(float* sm, float* dl, float* df) {
+  float* F = sm + AD_F;
+  float* Ft = sm + AD_FT;
+  float* L2 = sm + AD_L2;
+  float* S2 = sm + AD_S2;
+  float* H = sm + AD_H;
+  float* G1 = sm + AD_G1;
+  float* G2 = sm + AD_G2;
+  float* l1 = sm + AD_VEC;
+  float* S1 = l1 + 32;
+  float* s1 = l1 + 64;
+  float* y1 = l1 + 96;
+  float* rho = l1 + 128;
+  const int i = (int)threadIdx.x >> 3, j0 = ((int)threadIdx.x & 7) * 4;
+  float acc[4];
+  float r = 0.0f, y = 0.0f;
+  if constexpr (N >= 2) {
+    r = mv<false>(L2, s1);      // (lambda2 s1)[i]
+    mm<32, false, false>(L2, F, acc);  // H = lambda2 F
+    st<32>(H, acc);
+    if constexpr (MODE == ADJ_FULL) {
+      y = mv<false>(F, S1);     // y1 = F S1
+      float g[4];
+      mm<32, false, false>(F, S2, g);  // G1 = F S2
+      st<32>(G1, g);
+      mm<32, false, true>(F, S2, g);   // G2 = F S2^T
+      st<32>(G2, g);
+    }
+  } else if constexpr (MODE == ADJ_FULL) {
+    y = mv<false>(F, S1);
+  }
+  if (row_lead()) {
+    rho[i] = l1[i] + r;
+    y1[i] = y;
+  }
+  __syncthreads();
+  float ln[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+  if constexpr (N >= 2) mm<32, false, false>(Ft, H, ln);  // F^T H (Ft holds F^T row-major)
+  const float l1n = mv<true>(F, rho);  // (F^T rho)[i]
+  if constexpr (MODE == ADJ_FULL) {
+    float ds1 = l1[i];
+    if constexpr (N >= 2) ds1 += mv<true>(L2, y1);  // lambda2^T y1
+    if (row_lead()) dl[i] = ds1;
+    // dF = rho S1^T + lambda2 G2 + lambda2^T G1
+    const float4 sv = *reinterpret_cast<const float4*>(S1 + j0);
+    const float rr = rho[i];
+    df[0] = rr * sv.x;
+    df[1] = rr * sv.y;
+    df[2] = rr * sv.z;
+    df[3] = rr * sv.w;
+    if constexpr (N >= 2) {
+      float p1[4], p2[4];
+      mm<32, false, false>(L2, G2, p1);
+      mm<32, true, false>(L2, G1, p2);
+#pragma unroll
+      for (int k = 0; k < 4; ++k) df[k] += p1[k] + p2[k];
+      gst4(dl + DP, lds4(L2));  // ds2 = lambda2 (of the state after the step)
+    }
+  }
+  __syncthreads();
+  if constexpr (N >= 2) st<32>(L2, ln);
+  if (row_lead()) l1[i] = l1n;
+  __syncthreads();
+}
+
+template <int N, int MODE>
+__global__ __launch_bounds__(NT) void k_wadj(WArgs a) {
+  __shared__ __align__(16) float sm[AD_FLOATS];
+  const int c = blockIdx.x, b = blockIdx.y;
+  const int t0 = c * a.T, t1 = min(a.n, t0 + a.T);
+  float* L2 = sm + AD_L2;
+  float* l1 = sm + AD_VEC;
+  float* S1 = l1 + 32;
+  float* s1 = l1 + 64;
+  float* S2 = sm + AD_S2;
+  if (MODE == ADJ_LOCAL) {
+    if (threadIdx.x < 32) l1[threadIdx.x] = 0.0f;
+    sld4(L2, float4{0.0f, 0.0f, 0.0f, 0.0f});
+  } else {
+    load_state(a.lend + ((size_t)b * a.C + c) * RW, l1, L2);
+  }
+  const bool cached = a.flow_mode != EWS_FLOW_PER_INTERVAL;
+  float dfs[4] = {0.0f, 0.0f, 0.0f, 0.0f};  // shared-flow cotangent summed over the chunk's steps
+  for (int t = t1 - 1; t >= t0; --t) {
+    const size_t r = (size_t)b * a.n + t;
+    // row cotangent of the step's output, the flow, s1, and (FULL) the state before the step
+    const float* gr = a.grow + r * RW;
+    if (threadIdx.x < 32) {
+      l1[threadIdx.x] += gr[threadIdx.x];
+      s1[threadIdx.x] = a.loc[r * RW + threadIdx.x];
+    }
+    if constexpr (N >= 2) sld4(L2, f4add(lds4(L2), gld4(gr + DP)));
+    load_flow(a, b, t, sm + AD_F, sm + AD_FT);
+    if constexpr (MODE == ADJ_FULL) {
+      const float* sp = t > t0 ? a.rows + (r - 1) * RW : a.car + ((size_t)b * (a.C + 1) + c) * RW;
+      load_state(sp, S1, S2);
+    }
+    __syncthreads();
+    float df[4];
+    adj_step<N, MODE>(sm, MODE == ADJ_FULL ? a.dloc + r * RW : nullptr, df);
+    if constexpr (MODE == ADJ_FULL) {
+      bool ident;
+      flow_step(a, a.clock + (size_t)b * a.L, t, ident);
+      if (!cached) {
+        gst4(a.dfl + r * MM, acc4(df));
+      } else if (!ident) {
+#pragma unroll
+        for (int k = 0; k < 4; ++k) dfs[k] += df[k];
+      }
+    }
+  }
+  if (MODE == ADJ_LOCAL) {
+    store_state(a.mu + ((size_t)b * a.C + c) * RW, l1, L2);
+  } else if (cached) {
+    gst4(a.cpart + ((size_t)b * a.C + c) * 3 * MM, acc4(dfs));
+  }
+}
+
+// end cotangents of the chunks: lend[b][C-1] = 0, lend[b][c-1] = J_c^T lend[b][c] + mu[b][c] (J_c: chunk c's map)
+template <int N>
+__global__ __launch_bounds__(NT) void k_wadj_carry(WArgs a) {
+  __shared__ __align__(16) float sm[AD_FLOATS];
+  const int b = blockIdx.x;
+  float* L2 = sm + AD_L2;
+  float* l1 = sm + AD_VEC;
+  float* s1 = l1 + 64;
+  float* F = sm + AD_F;
+  float* Ft = sm + AD_FT;
+  if (threadIdx.x < 32) l1[threadIdx.x] = 0.0f;
+  sld4(L2, float4{0.0f, 0.0f, 0.0f, 0.0f});
+  __syncthreads();
+  store_state(a.lend + ((size_t)b * a.C + a.C - 1) * RW, l1, L2);
+  for (int c = a.C - 1; c >= 1; --c) {
+    const float4 v = gld4(a.sfl + ((size_t)b * a.C + c) * MM);
+    sld4(F, v);
+    const int i = trow<32>(), j0 = tcol<32>();
+    Ft[(j0 + 0) * P32 + i] = v.x;
+    Ft[(j0 + 1) * P32 + i] = v.y;
+    Ft[(j0 + 2) * P32 + i] = v.z;
+    Ft[(j0 + 3) * P32 + i] = v.w;
+    if (threadIdx.x < 32) s1[threadIdx.x] = a.summ[((size_t)b * a.C + c) * RW + threadIdx.x];
+    __syncthreads();
+    float df[4];
+    adj_step<N, ADJ_LOCAL>(sm, nullptr, df);
+    const float* m = a.mu + ((size_t)b * a.C + c) * RW;
+    if (threadIdx.x < 32) l1[threadIdx.x] += m[threadIdx.x];
+    if constexpr (N >= 2) sld4(L2, f4add(lds4(L2), gld4(m + DP)));
+    __syncthreads();
+    store_state(a.lend + ((size_t)b * a.C + c - 1) * RW, l1, L2);
+  }
+}
+
+// Leaf adjoints, a workgroup per (chunk, sample): dv per interval, the series leaf's dh and dA (workgroup partial),
+// the Van Loan leaf's (dP, dV) per interval (per-interval mode) or summed over the chunk (shared modes).
+template <int N>
+__global__ __launch_bounds__(NT) void k_wleaf_bwd(WArgs a) {
+  __shared__ __align__(16) float sm[LF_FLOATS];
+  float* A = sm + LF_A;
+  float* S2b = sm + LF_S2;  // ds2
+  float* vec = sm + LF_VEC;
+  float* ds1 = vec;
+  float* wv = vec + 32;
+  float* T1 = sm + LF_TAB;
+  float* T2 = sm + LF_TAB2;
+  float* T3 = sm + LF_TAB3;
+  float* T4 = sm + LF_TAB4;
+  const int c = blockIdx.x, b = blockIdx.y;
+  const int t0 = c * a.T, t1 = min(a.n, t0 + a.T);
+  const int tid = threadIdx.x, i = tid >> 3, j0 = (tid & 7) * 4;
+  load_A(a.d, a.A, A);
+  float dA[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+  float sP[4] = {0.0f, 0.0f, 0.0f, 0.0f}, sV[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+  const float* th = a.clock + (size_t)b * a.L;
+  __syncthreads();
+  for (int t = t0; t < t1; ++t) {
+    const size_t r = (size_t)b * a.n + t;
+    const float* x = a.path + ((size_t)b * a.L + t) * a.d;
+    if (tid < 32) ds1[tid] = a.dloc[r * RW + tid];
+    if constexpr (N >= 2) sld4(S2b, gld4(a.dloc + r * RW + DP));
+    float dvi = 0.0f, dh = 0.0f;
+    if (a.leaf == EWS_LEAF_VAN_LOAN) {
+      float* P = sm + LF_P;
+      float* V = sm + LF_V;
+      load_vl(a, b, t, P, V);
+      const int M = a.vm;
+      if (tid < 32) wv[tid] = tid < a.d ? (x[a.d + tid] - x[tid]) / (float)M : 0.0f;
+      __syncthreads();
+      vl_knots(a, P, V, wv, T1);  // Delta_m in rows 0 .. M-1
+      if (tid < 32) {  // Z_m = R_m + Delta_m / 2 (T2), Y_m = Pre_m + Delta_m / 2 (T3)
+        float suf = 0.0f;
+        for (int m = M - 1; m >= 0; --m) {
+          const float dm = T1[m * 32 + tid];
+          T2[m * 32 + tid] = fmaf(0.5f, dm, suf);
+          suf += dm;
+        }
+        float pre = 0.0f;
+        for (int m = 0; m < M; ++m) {
+          const float dm = T1[m * 32 + tid];
+          T3[m * 32 + tid] = fmaf(0.5f, dm, pre);
+          pre += dm;
+        }
+      }
+      __syncthreads();
+      // dDelta_m = ds1 + ds2 Z_m + ds2^T Y_m (rows of T4)
+      for (int m = 0; m < M; ++m) {
+        float v = 0.0f;
+        if constexpr (N >= 2) v = mv<false>(S2b, T2 + m * 32) + mv<true>(S2b, T3 + m * 32);
+        if (row_lead()) T4[m * 32 + i] = ds1[i] + v;
+      }
+      __syncthreads();
+      // chain: lam_1 = dDelta_1, lam_m = dDelta_m + P^T lam_{m-1} (in place in T4)
+      for (int m = 1; m < M; ++m) {
+        const float v = mv<true>(P, T4 + (m - 1) * 32);
+        __syncthreads();
+        if (row_lead()) T4[m * 32 + i] += v;
+        __syncthreads();
+      }
+      // dP = sum_{m >= 1} lam_{m-1} Delta_m^T, dV = lam_M w^T, dv = V^T lam_M / M
+      float gp[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+      for (int m = 1; m < M; ++m) {
+        const float l = T4[(m - 1) * 32 + i];
+        const float4 dm = *reinterpret_cast<const float4*>(T1 + m * 32 + j0);
+        gp[0] = fmaf(l, dm.x, gp[0]);
+        gp[1] = fmaf(l, dm.y, gp[1]);
+        gp[2] = fmaf(l, dm.z, gp[2]);
+        gp[3] = fmaf(l, dm.w, gp[3]);
+      }
+      const float lM = T4[(M - 1) * 32 + i];
+      const float4 w4 = *reinterpret_cast<const float4*>(wv + j0);
+      const float gv[4] = {lM * w4.x, lM * w4.y, lM * w4.z, lM * w4.w};
+      dvi = mv<true>(V, T4 + (M - 1) * 32) / (float)M;
+      bool fixed;
+      vl_step(a, th, t, fixed);
+      if (a.vl_mode == EWS_FLOW_PER_INTERVAL) {
+        gst4(a.dvlm + r * 2 * MM, acc4(gp));
+        gst4(a.dvlm + r * 2 * MM + MM, acc4(gv));
+      } else if (!fixed) {
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+          sP[k] += gp[k];
+          sV[k] += gv[k];
+        }
+      }
+    } else {
+      const int q = a.q;
+      const float h = th[t + 1] - th[t];
+      if (tid < 32) T1[tid] = tid < a.d ? x[a.d + tid] - x[tid] : 0.0f;
+      __syncthreads();
+      for (int p = 1; p <= q; ++p) {  // letters b_p (T1) and A b_{p-1} (T3)
+        const float y = mv<false>(A, T1 + (p - 1) * 32);
+        if (row_lead()) {
+          T3[p * 32 + i] = y;
+          T1[p * 32 + i] = (-h / (float)p) * y;
+        }
+        __syncthreads();
+      }
+      if constexpr (N >= 2) {  // u_p (T2) and w_p = sum_r C2[r][p] b_r (T4 for now)
+        for (int e = tid; e < (q + 1) * 32; e += NT) {
+          const int p = e >> 5, k = e & 31;
+          float su = 0.0f, sw = 0.0f;
+          for (int rr = 0; rr <= q - p; ++rr) {
+            su = fmaf(c2coef(p, rr), T1[rr * 32 + k], su);
+            sw = fmaf(c2coef(rr, p), T1[rr * 32 + k], sw);
+          }
+          T2[p * 32 + k] = su;
+          T4[p * 32 + k] = sw;
+        }
+        __syncthreads();
+      }
+      // db_p = ds1 / (p + 1) + ds2 u_p + ds2^T w_p, kept by the row leads in registers: lane (i) of each p
+      // goes through LDS: T4 row p is replaced by db_p
+      for (int p = 0; p <= q; ++p) {
+        float v = 0.0f;
+        if constexpr (N >= 2) v = mv<false>(S2b, T2 + p * 32) + mv<true>(S2b, T4 + p * 32);
+        __syncthreads();
+        if (row_lead()) T4[p * 32 + i] = fmaf(inv_f(p + 1), ds1[i], v);
+        __syncthreads();
+      }
+      // reverse recursion: for p = q .. 1: dh += -(1/p) <db_p, A b_{p-1}>, dA += (-h/p) db_p b_{p-1}^T,
+      // db_{p-1} += (-h/p) A^T db_p
+      for (int p = q; p >= 1; --p) {
+        const float cpf = -h / (float)p;
+        const float dbi = T4[p * 32 + i];
+        const float4 bp = *reinterpret_cast<const float4*>(T1 + (p - 1) * 32 + j0);
+        dA[0] = fmaf(cpf * dbi, bp.x, dA[0]);
+        dA[1] = fmaf(cpf * dbi, bp.y, dA[1]);
+        dA[2] = fmaf(cpf * dbi, bp.z, dA[2]);
+        dA[3] = fmaf(cpf * dbi, bp.w, dA[3]);
+        if (tid < 32) dh = fmaf(-inv_f(p) * T4[p * 32 + tid], T3[p * 32 + tid], dh);
+        const float v = mv<true>(A, T4 + p * 32);
+        __syncthreads();
+        if (row_lead()) T4[(p - 1) * 32 + i] = fmaf(cpf, v, T4[(p - 1) * 32 + i]);
+        __syncthreads();
+      }
+      dvi = T4[i];
+    }
+    if (row_lead() && i < a.d) a.dv[r * DP + i] = dvi;
+    if (a.leaf != EWS_LEAF_VAN_LOAN) {
+      // dh: the 32 partials of threads 0..31 (wavefront 0)
+      float s = tid < 32 ? dh : 0.0f;
+      if (tid < 64) {
+#pragma unroll
+        for (int o = 16; o > 0; o >>= 1) s += __shfl_xor(s, o, 64);
+        if (tid == 0) a.dhl[r] = s;
+      }
+    }
+    __syncthreads();
+  }
+  if (a.leaf == EWS_LEAF_VAN_LOAN && a.vl_mode != EWS_FLOW_PER_INTERVAL) {
+    float* cp = a.cpart + ((size_t)b * a.C + c) * 3 * MM;
+    gst4(cp + MM, acc4(sP));
+    gst4(cp + 2 * MM, acc4(sV));
+  }
+  gst4(a.apart + ((size_t)b * a.C + c) * MM, acc4(dA));  // zero for the Van Loan leaf
+}
+
+// Matrix-function adjoints. per_interval: one item per interval, the flow's (dfl) and the Van Loan pair's (dvlm)
+// cotangents of the per-interval modes, dh into dhm; else one item per sample, the chunk partials of the shared
+// flow and pair summed in chunk order, the shared steps' gradients into dsh[b][0..1]. dA: workgroup partials at
+// apart + slot0.
+__global__ __launch_bounds__(NT) void k_wmat_bwd(WArgs a, int per_interval, long slot0) {
+  extern __shared__ __align__(16) float sm[];
+  float* A = sm + MF_A;
+  load_A(a.d, a.A, A);
+  __syncthreads();
+  float dA[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+  const long items = per_interval ? (long)a.B * a.n : a.B;
+  const bool do_flow = (a.flow_mode == EWS_FLOW_PER_INTERVAL) == (per_interval != 0);
+  const bool do_vl = a.leaf == EWS_LEAF_VAN_LOAN && (a.vl_mode == EWS_FLOW_PER_INTERVAL) == (per_interval != 0);
+  float* G0 = sm + MF_T;
+  float* G1 = sm + MF_U;
+  for (long it = blockIdx.x; it < items; it += gridDim.x) {
+    const int b = per_interval ? (int)(it / a.n) : (int)it;
+    const int t = per_interval ? (int)(it - (long)b * a.n) : 1;
+    const float* th = a.clock + (size_t)b * a.L;
+    float dh_f = 0.0f, dh_v = 0.0f;
+    if (do_flow) {
+      bool ident;
+      const float h = flow_step(a, th, t, ident);
+      float g[4];
+      if (per_interval) {
+        const float4 v = gld4(a.dfl + it * MM);
+        g[0] = v.x; g[1] = v.y; g[2] = v.z; g[3] = v.w;
+      } else {
+        g[0] = g[1] = g[2] = g[3] = 0.0f;
+        for (int c = 0; c < a.C; ++c) {
+          const float4 v = gld4(a.cpart + ((size_t)b * a.C + c) * 3 * MM);
+          g[0] += v.x; g[1] += v.y; g[2] += v.z; g[3] += v.w;
+        }
+      }
+      __syncthreads();
+      st<32>(G0, g);
+      __syncthreads();
+      float xb[4];
+      matfn_bwd(sm, a.chen, true, h, xb);
+      const float4 av = lds4(A);
+      const float dot = xb[0] * av.x + xb[1] * av.y + xb[2] * av.z + xb[3] * av.w;
+#pragma unroll
+      for (int k = 0; k < 4; ++k) dA[k] = fmaf(h, xb[k], dA[k]);
+      dh_f = block_sum(dot, sm + MF_RED);
+    }
+    if (do_vl) {
+      bool fixed;
+      const float cst = vl_step(a, th, t, fixed);
+      if (!fixed) {
+        float g0[4], g1[4];
+        if (per_interval) {
+          const float4 p = gld4(a.dvlm + it * 2 * MM), v = gld4(a.dvlm + it * 2 * MM + MM);
+          g0[0] = p.x; g0[1] = p.y; g0[2] = p.z; g0[3] = p.w;
+          g1[0] = v.x; g1[1] = v.y; g1[2] = v.z; g1[3] = v.w;
+        } else {
+#pragma unroll
+          for (int k = 0; k < 4; ++k) g0[k] = g1[k] = 0.0f;
+          for (int c = 0; c < a.C; ++c) {
+            const float* cp = a.cpart + ((size_t)b * a.C + c) * 3 * MM;
+            const float4 p = gld4(cp + MM), v = gld4(cp + 2 * MM);
+            g0[0] += p.x; g0[1] += p.y; g0[2] += p.z; g0[3] += p.w;
+            g1[0] += v.x; g1[1] += v.y; g1[2] += v.z; g1[3] += v.w;
+          }
+        }
+        __syncthreads();
+        st<32>(G0, g0);
+        st<32>(G1, g1);
+        __syncthreads();
+        float xb[4];
+        matfn_bwd(sm, a.vl_expm, false, cst, xb);
+        const float4 av = lds4(A);
+        const float dot = xb[0] * av.x + xb[1] * av.y + xb[2] * av.z + xb[3] * av.w;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) dA[k] = fmaf(cst, xb[k], dA[k]);
+        dh_v = block_sum(dot, sm + MF_RED) / (float)a.vm;  // c = dt / M
+      }
+    }
+    if (threadIdx.x == 0) {
+      if (per_interval) {
+        a.dhm[it] = dh_f + dh_v;
+      } else {
+        a.dsh[2 * b] = dh_f;
+        a.dsh[2 * b + 1] = dh_v;
+      }
+    }
+    __syncthreads();
+  }
+  gst4(a.apart + (slot0 + blockIdx.x) * MM, acc4(dA));
+}
+
+// grad_A = sum of the partials (float64, in slot order), entries i, j < d
+__global__ __launch_bounds__(NT) void k_wfinal_A(WArgs a, long nparts, float* grad_A) {
+  const int e = blockIdx.x * NT + threadIdx.x;
+  if (e >= MM) return;
+  const int r = e >> 5, c = e & 31;
+  if (r >= a.d || c >= a.d) return;
+  double s = 0.0;
+  for (long k = 0; k < nparts; ++k) s += (double)a.apart[k * MM + e];
+  grad_A[r * a.d + c] = (float)s;
+}
+
+// grad_path[b][k] = dv[k-1] - dv[k]; grad_clock[b][k] = dh[k-1] - dh[k] plus the shared steps' gradients
+__global__ __launch_bounds__(NT) void k_wknots(WArgs a, float* grad_path, float* grad_clock) {
+  const int b = blockIdx.y;
+  const int k = blockIdx.x * NT + threadIdx.x;
+  if (k >= a.L) return;
+  const size_t base = (size_t)b * a.n;
+  for (int ch = 0; ch < a.d; ++ch) {
+    const float lo = k >= 1 ? a.dv[(base + k - 1) * DP + ch] : 0.0f;
+    const float hi = k < a.n ? a.dv[(base + k) * DP + ch] : 0.0f;
+    grad_path[((size_t)b * a.L + k) * a.d + ch] = lo - hi;
+  }
+  if (!grad_clock) return;
+  auto dh = [&](int t) -> float {
+    float s = 0.0f;
+    if (a.leaf != EWS_LEAF_VAN_LOAN) s += a.dhl[base + t];
+    if (a.flow_mode == EWS_FLOW_PER_INTERVAL || (a.leaf == EWS_LEAF_VAN_LOAN && a.vl_mode == EWS_FLOW_PER_INTERVAL))
+      s += a.dhm[base + t];
+    return s;
+  };
+  float g = (k >= 1 ? dh(k - 1) : 0.0f) - (k < a.n ? dh(k) : 0.0f);
+  // shared steps: th[1] - th[0] (uniform) or th[2] - th[1] (basepoint)
+  if (a.flow_mode != EWS_FLOW_PER_INTERVAL) {
+    const int k0 = a.flow_mode == EWS_FLOW_CACHED ? 0 : 1;
+    if (k == k0) g -= a.dsh[2 * b];
+    if (k == k0 + 1) g += a.dsh[2 * b];
+  }
+  if (a.leaf == EWS_LEAF_VAN_LOAN && a.vl_mode != EWS_FLOW_PER_INTERVAL) {
+    const int k0 = a.vl_mode == EWS_FLOW_CACHED ? 0 : 1;
+    if (k == k0) g -= a.dsh[2 * b + 1];
+    if (k == k0 + 1) g += a.dsh[2 * b + 1];
+  }
+  grad_clock[(size_t)b * a.L + k] = g;
+}
+
+}  // namespace wide
+}  // namespace ews
+
+// ------------------------------------------------------------------------------------------------ host side
+namespace ews {
+namespace wide {
+namespace {
+
+size_t al256(size_t x) { return (x + 255) & ~(size_t)255; }
+
+struct WPlan {
+  int B, L, n, d, N, T, C, W;
+  bool fl_int, vl, vl_int, exact_int, exact_smp, mats_int, mats_smp;
+  long g_int, g_smp;  // workgroups of the matrix-function adjoints
+};
+
+int plan(const ews_dense_desc* s, WPlan& p) {
+  if (!s) return EWS_ERR_NULL;
+  if (s->depth < 1 || s->depth > 2) return EWS_ERR_DEPTH;
+  if (s->batch < 1 || s->length < 2 || s->dim <= 16 || s->dim > DP) return EWS_ERR_SHAPE;
+  if (s->flow_mode < 0 || s->flow_mode > 2 || s->readout < 0 || s->readout > 3) return EWS_ERR_OPTION;
+  if (s->leaf != EWS_LEAF_SERIES && s->leaf != EWS_LEAF_VAN_LOAN) return EWS_ERR_OPTION;
+  const bool vl = s->leaf == EWS_LEAF_VAN_LOAN;
+  if (!vl && (s->series_q < 0 || s->series_q > QMAXW)) return EWS_ERR_OPTION;
+  if (vl && (s->vl_steps < 1 || s->vl_steps > VMAXK)) return EWS_ERR_OPTION;
+  if (vl && (s->vl_expm < 0 || s->vl_expm > 3 || s->vl_mode < 0 || s->vl_mode > 2)) return EWS_ERR_OPTION;
+  if (s->chen_expm < 0 || s->chen_expm > 3) return EWS_ERR_OPTION;
+  if (s->flow_mode == EWS_FLOW_CACHED_BASEPOINT && s->length < 3) return EWS_ERR_SHAPE;
+  if (vl && s->vl_mode == EWS_FLOW_CACHED_BASEPOINT && s->length < 3) return EWS_ERR_SHAPE;
+  if (s->chunk < 0) return EWS_ERR_SHAPE;
+  p.B = s->batch;
+  p.L = s->length;
+  p.n = p.L - 1;
+  p.d = s->dim;
+  p.N = s->depth;
+  p.T = s->chunk ? s->chunk : 64;
+  p.C = (p.n + p.T - 1) / p.T;
+  p.W = p.d + (p.N >= 2 ? p.d * p.d : 0) + (s->level0 ? 1 : 0);
+  p.fl_int = s->flow_mode == EWS_FLOW_PER_INTERVAL;
+  p.vl = vl;
+  p.vl_int = vl && s->vl_mode == EWS_FLOW_PER_INTERVAL;
+  p.mats_int = p.fl_int || p.vl_int;
+  p.mats_smp = !p.fl_int || (vl && !p.vl_int);
+  p.exact_int = (p.fl_int && s->chen_expm == EWS_EXPM_EXACT) || (p.vl_int && s->vl_expm == EWS_EXPM_EXACT);
+  p.exact_smp = (!p.fl_int && s->chen_expm == EWS_EXPM_EXACT) || (vl && !p.vl_int && s->vl_expm == EWS_EXPM_EXACT);
+  p.g_int = p.mats_int ? std::min<long>((long)p.B * p.n, 2048) : 0;
+  p.g_smp = p.mats_smp ? p.B : 0;
+  return EWS_OK;
+}
+
+struct WLay {
+  size_t fl, vlm, loc, summ, sfl, car, rows, amax, outs, grow, mu, lend, dloc, dfl, cpart, dvlm, apart, dv, dhl,
+      dhm, dsh, total;
+};
+
+WLay layout(const ews_dense_desc* s, const WPlan& p, bool bwd) {
+  WLay w{};
+  size_t off = 0;
+  const size_t BN = (size_t)p.B * p.n, BC = (size_t)p.B * p.C;
+  auto take = [&](size_t& f, size_t bytes) {
+    f = off;
+    off += al256(bytes);
+  };
+  take(w.fl, (p.fl_int ? BN : (size_t)p.B) * MM * 4);
+  take(w.vlm, p.vl ? (p.vl_int ? BN : (size_t)p.B) * 2 * MM * 4 : 0);
+  take(w.loc, BN * RW * 4);
+  take(w.summ, BC * RW * 4);
+  take(w.sfl, BC * MM * 4);
+  take(w.car, (size_t)p.B * (p.C + 1) * RW * 4);
+  const bool mm_ro = s->readout == EWS_READOUT_MEAN || s->readout == EWS_READOUT_MAX;
+  take(w.rows, (bwd || mm_ro) ? BN * RW * 4 : 0);
+  take(w.amax, s->readout == EWS_READOUT_MAX ? (size_t)p.B * p.W * 4 : 0);
+  if (bwd) {
+    take(w.outs, s->readout == EWS_READOUT_MAX ? (size_t)p.B * p.W * 4 : 0);
+    take(w.grow, BN * RW * 4);
+    take(w.mu, BC * RW * 4);
+    take(w.lend, BC * RW * 4);
+    take(w.dloc, BN * RW * 4);
+    take(w.dfl, p.fl_int ? BN * MM * 4 : 0);
+    take(w.cpart, BC * 3 * MM * 4);
+    take(w.dvlm, p.vl_int ? BN * 2 * MM * 4 : 0);
+    take(w.apart, (BC + p.g_int + p.g_smp) * MM * 4);
+    take(w.dv, BN * DP * 4);
+    take(w.dhl, BN * 4);
+    take(w.dhm, BN * 4);
+    take(w.dsh, (size_t)p.B * 2 * 4);
+  }
+  w.total = off;
+  return w;
+}
+
+WArgs make_args(const ews_dense_desc* s, const WPlan& p, const float* path, const float* clock, const float* A,
+                float* out, void* workspace, bool bwd) {
+  WArgs a{};
+  a.B = p.B; a.L = p.L; a.n = p.n; a.d = p.d; a.N = p.N; a.T = p.T; a.C = p.C; a.W = p.W;
+  a.lvl0 = s->level0 ? 1 : 0; a.readout = s->readout;
+  a.flow_mode = s->flow_mode; a.chen = s->chen_expm; a.leaf = s->leaf;
+  a.q = p.vl ? 0 : s->series_q; a.vm = p.vl ? s->vl_steps : 0;
+  a.vl_expm = p.vl ? s->vl_expm : 0; a.vl_mode = p.vl ? s->vl_mode : 0;
+  a.path = path; a.clock = clock; a.A = A; a.out = out;
+  const WLay w = layout(s, p, bwd);
+  char* ws = (char*)workspace;
+  auto f = [&](size_t o) { return (float*)(ws + o); };
+  a.fl = f(w.fl); a.vlm = p.vl ? f(w.vlm) : nullptr; a.loc = f(w.loc); a.summ = f(w.summ); a.sfl = f(w.sfl);
+  a.car = f(w.car);
+  const bool mm_ro = s->readout == EWS_READOUT_MEAN || s->readout == EWS_READOUT_MAX;
+  a.rows = (bwd || mm_ro) ? f(w.rows) : nullptr;
+  a.amax = s->readout == EWS_READOUT_MAX ? (int*)(ws + w.amax) : nullptr;
+  if (bwd) {
+    a.grow = f(w.grow); a.mu = f(w.mu); a.lend = f(w.lend); a.dloc = f(w.dloc);
+    a.dfl = p.fl_int ? f(w.dfl) : nullptr; a.cpart = f(w.cpart); a.dvlm = p.vl_int ? f(w.dvlm) : nullptr;
+    a.apart = f(w.apart); a.dv = f(w.dv); a.dhl = f(w.dhl); a.dhm = f(w.dhm); a.dsh = f(w.dsh);
+  }
+  return a;
+}
+
+#define WIDE_CHECK()                                            \
+  do {                                                          \
+    if (hipGetLastError() != hipSuccess) return EWS_ERR_LAUNCH; \
+  } while (0)
+
+int set_lds(const void* fn, size_t bytes) {
+  return hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)bytes) == hipSuccess
+             ? EWS_OK : EWS_ERR_LAUNCH;
+}
+
+// forward passes: step matrices, local terms, chunk summaries, carries, rows (and the readout)
+int run_forward(const WPlan& p, const WArgs& a, hipStream_t st) {
+  const size_t lds = MF_ENT_FWD * sizeof(double);
+  if (set_lds(reinterpret_cast<const void*>(&k_wmat), lds) != EWS_OK) return EWS_ERR_LAUNCH;
+  if (p.mats_int) {
+    hipLaunchKernelGGL(k_wmat, dim3((unsigned)std::min<long>((long)p.B * p.n, 4096)), dim3(NT), lds, st, a, 1);
+    WIDE_CHECK();
+  }
+  if (p.mats_smp) {
+    hipLaunchKernelGGL(k_wmat, dim3(p.B), dim3(NT), lds, st, a, 0);
+    WIDE_CHECK();
+  }
+  const dim3 gl((unsigned)std::min<long>((long)p.B * p.n, 4096)), gc(p.C, p.B);
+  if (p.N == 1) {
+    hipLaunchKernelGGL(k_wleaf<1>, gl, dim3(NT), 0, st, a);
+    hipLaunchKernelGGL((k_wscan<1, SCAN_SUMMARY>), gc, dim3(NT), 0, st, a);
+    hipLaunchKernelGGL(k_wcarry<1>, dim3(p.B), dim3(NT), 0, st, a);
+    hipLaunchKernelGGL((k_wscan<1, SCAN_ROWS>), gc, dim3(NT), 0, st, a);
+  } else {
+    hipLaunchKernelGGL(k_wleaf<2>, gl, dim3(NT), 0, st, a);
+    hipLaunchKernelGGL((k_wscan<2, SCAN_SUMMARY>), gc, dim3(NT), 0, st, a);
+    hipLaunchKernelGGL(k_wcarry<2>, dim3(p.B), dim3(NT), 0, st, a);
+    hipLaunchKernelGGL((k_wscan<2, SCAN_ROWS>), gc, dim3(NT), 0, st, a);
+  }
+  WIDE_CHECK();
+  if (a.readout == EWS_READOUT_TERMINAL || a.readout == EWS_READOUT_MEAN || a.readout == EWS_READOUT_MAX) {
+    hipLaunchKernelGGL(k_wreadout, dim3((p.W + NT - 1) / NT, p.B), dim3(NT), 0, st, a);
+    WIDE_CHECK();
+  }
+  return EWS_OK;
+}
+
+}  // namespace
+
+bool eligible(const ews_dense_desc* s) {
+  return s && s->dim > 16 && s->dim <= DP && s->depth >= 1 && s->depth <= 2 &&
+         (s->leaf == EWS_LEAF_SERIES || s->leaf == EWS_LEAF_VAN_LOAN);
+}
+
+size_t workspace_bytes(const ews_dense_desc* s, bool backward) {
+  WPlan p;
+  if (plan(s, p) != EWS_OK) return 0;
+  return layout(s, p, backward).total;
+}
+
+int forward(const ews_dense_desc* s, const float* path, const float* clock, const float* A, float* out,
+            void* workspace, bool backward_layout, hipStream_t st) {
+  WPlan p;
+  const int rc = plan(s, p);
+  if (rc != EWS_OK) return rc;
+  if (!path || !clock || !A || !out || !workspace) return EWS_ERR_NULL;
+  WArgs a = make_args(s, p, path, clock, A, out, workspace, backward_layout);
+  return run_forward(p, a, st);
+}
+
+int backward(const ews_dense_desc* s, const float* path, const float* clock, const float* A, const float* grad_out,
+             float* grad_path, float* grad_clock, float* grad_A, void* workspace, hipStream_t st) {
+  WPlan p;
+  const int rc = plan(s, p);
+  if (rc != EWS_OK) return rc;
+  if (!path || !clock || !A || !grad_out || !grad_path || !grad_A || !workspace) return EWS_ERR_NULL;
+  const WLay w = layout(s, p, true);
+  WArgs a = make_args(s, p, path, clock, A, nullptr, workspace, true);
+  {  // the forward again, with the padded prefix states kept (and the rows of the maxima of the max readout)
+    WArgs f = a;
+    if (s->readout == EWS_READOUT_MAX) f.out = (float*)((char*)workspace + w.outs);
+    else f.readout = -1;  // no output: the states go to the workspace only
+    const int r = run_forward(p, f, st);
+    if (r != EWS_OK) return r;
+  }
+  hipLaunchKernelGGL(k_wgrows, dim3((unsigned)std::min<long>(((long)p.B * p.n * RW + NT - 1) / NT, 8192)),
+                     dim3(NT), 0, st, a, grad_out);
+  WIDE_CHECK();
+  const dim3 gc(p.C, p.B);
+  if (p.N == 1) {
+    hipLaunchKernelGGL((k_wadj<1, ADJ_LOCAL>), gc, dim3(NT), 0, st, a);
+    hipLaunchKernelGGL(k_wadj_carry<1>, dim3(p.B), dim3(NT), 0, st, a);
+    hipLaunchKernelGGL((k_wadj<1, ADJ_FULL>), gc, dim3(NT), 0, st, a);
+    hipLaunchKernelGGL(k_wleaf_bwd<1>, gc, dim3(NT), 0, st, a);
+  } else {
+    hipLaunchKernelGGL((k_wadj<2, ADJ_LOCAL>), gc, dim3(NT), 0, st, a);
+    hipLaunchKernelGGL(k_wadj_carry<2>, dim3(p.B), dim3(NT), 0, st, a);
+    hipLaunchKernelGGL((k_wadj<2, ADJ_FULL>), gc, dim3(NT), 0, st, a);
+    hipLaunchKernelGGL(k_wleaf_bwd<2>, gc, dim3(NT), 0, st, a);
+  }
+  WIDE_CHECK();
+  const long base = (long)p.B * p.C;
+  if (p.mats_int) {
+    const size_t lds = (p.exact_int ? MF_ENT_BWD_EXACT : MF_ENT_BWD) * 4;
+    if (set_lds(reinterpret_cast<const void*>(&k_wmat_bwd), MF_ENT_BWD_EXACT * 4) != EWS_OK)
+      return EWS_ERR_LAUNCH;
+    hipLaunchKernelGGL(k_wmat_bwd, dim3((unsigned)p.g_int), dim3(NT), lds, st, a, 1, base);
+    WIDE_CHECK();
+  }
+  if (p.mats_smp) {
+    const size_t lds = (p.exact_smp ? MF_ENT_BWD_EXACT : MF_ENT_BWD) * 4;
+    if (set_lds(reinterpret_cast<const void*>(&k_wmat_bwd), MF_ENT_BWD_EXACT * 4) != EWS_OK)
+      return EWS_ERR_LAUNCH;
+    hipLaunchKernelGGL(k_wmat_bwd, dim3((unsigned)p.g_smp), dim3(NT), lds, st, a, 0, base + p.g_int);
+    WIDE_CHECK();
+  }
+  hipLaunchKernelGGL(k_wfinal_A, dim3(MM / NT), dim3(NT), 0, st, a, base + p.g_int + p.g_smp, grad_A);
+  hipLaunchKernelGGL(k_wknots, dim3((p.L + NT - 1) / NT, p.B), dim3(NT), 0, st, a, grad_path, grad_clock);
+  WIDE_CHECK();
+  return EWS_OK;
+}
+
+}  // namespace wide
+}  // namespace ews

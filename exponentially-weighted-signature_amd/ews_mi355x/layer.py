@@ -13,7 +13,8 @@ ews/core/kernels/combine.py:37-63):
                                                      coefficient is the degree-<= q Taylor polynomial of the closed
                                                      form ("series" at every level, "block_series" at level 2 with
                                                      an exact level 1); exact flows (chen_expm "exact")
-    any generator (dense A, d <= 16), depths 1-3,
+    any generator (dense A: d <= 16 at depths    dense kernels (d <= 32: padded 32 x 32 step matrices and
+    1-3, 16 < d <= 32 at depths 1-2)              states, matrix functions per interval or per sample)
         leaf "series"                                dense kernels: series leaf of order series_q
         leaf "van_loan" (the reference default)      dense kernels: Van Loan leaf with M knots per interval under
                                                      van_loan_expm and reweighting_mode
@@ -191,9 +192,10 @@ class EWS(torch.nn.Module):
                 raise ValueError("leaf='plane_closed' needs an even dimension (2x2 planes)")
             return "diag"
         if self.leaf in ("series", "van_loan"):
-            if self.N > 3 or self.d > 16:
+            if self.N > 3 or self.d > 32 or (self.d > 16 and self.N > 2):
                 raise NotImplementedError(
-                    f"leaf={self.leaf!r}: the dense-generator kernels cover depths 1-3 and d <= 16")
+                    f"leaf={self.leaf!r}: the dense-generator kernels cover depths 1-3 at d <= 16 and depths 1-2 at "
+                    "d <= 32")
             return "dense"
         if diag_ok and self.d <= 16:
             return "dense"  # closed-form leaf with approximate flows: exact integrals on the dense kernels

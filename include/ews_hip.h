@@ -163,7 +163,8 @@ int ews_diag_forward_noalloc(const ews_diag_desc* desc, const void* path, const 
 typedef struct ews_dense_desc {
   int32_t batch;     /* B >= 1 */
   int32_t length;    /* L >= 2 knots */
-  int32_t dim;       /* 1 <= d <= 16 */
+  int32_t dim;       /* 1 <= d <= 16; or 16 < d <= 32 at depths 1-2 with the series or Van Loan leaf (ews_dense_forward,
+                      * ews_dense_backward and their _keep / _kept forms; the other dense entry points take d <= 16) */
   int32_t depth;     /* N in {1, 2, 3} */
   int32_t series_q;  /* series order q in [0, 40] (letters b_0..b_q, total order |m| <= q); series leaf only */
   int32_t flow_mode; /* EWS_FLOW_* of the Chen flows */
@@ -178,7 +179,9 @@ typedef struct ews_dense_desc {
 } ews_dense_desc;
 
 /* Scratch of the dense forward: powers table, padded local terms and flows (B, L-1, 16+256+4096 | 256),
- * chunk summaries and carries, and the per-sample step matrices of the uniform modes (B, 3, 256). */
+ * chunk summaries and carries, and the per-sample step matrices of the uniform modes (B, 3, 256). For d > 16:
+ * the step matrices padded to 32 x 32 (per interval or per sample), local terms (B, L-1, 32 + 1024), chunk
+ * summaries, flow products and carries. */
 size_t ews_dense_workspace_bytes(const ews_dense_desc* desc);
 
 /* Forward: path (B, L, d) f32, clock (B, L) f32, A (d, d) f32 row-major (reference sign), out f32
@@ -222,8 +225,10 @@ int ews_dense_backward(const ews_dense_desc* desc, const float* path, const floa
                        ews_stream_t stream);
 
 /* The same forward and backward with the forward's intermediates kept for the backward instead of recomputed
- * (the residuals a custom VJP keeps between its two halves, pallas_combine.py:2360-2565; here the leaf, the flows,
- * the chunk summaries and carries: about B (L-1) (sum_k d^k + 256) floats, 1.2 GB at c3's shape).
+ * (for d > 16 nothing is kept: the _keep forward is the plain one on the backward's workspace and the _kept
+ * backward recomputes); the residuals a custom VJP keeps between its two halves (pallas_combine.py:2360-2565) are
+ * here the leaf, the flows, the chunk summaries and carries: about B (L-1) (sum_k d^k + 256) floats, 1.2 GB at
+ * c3's shape.
  * ews_dense_forward_keep is ews_dense_forward on a workspace of ews_dense_backward_workspace_bytes(desc) bytes;
  * ews_dense_backward_kept is ews_dense_backward on that workspace, unchanged since, with the same desc and inputs:
  * it skips the recompute (at c3, 1.3 ms of the backward) and overwrites the kept data (one backward per forward).

@@ -192,7 +192,9 @@ def test_dense_c_abi_error_codes():
     assert lib.ews_dense_forward(ctypes.byref(good), null, null, null, null, null, null) == -1
     bad = {
         "depth": (_ddesc(depth=4), -3),
-        "too wide": (_ddesc(dim=17), -2),
+        "too wide": (_ddesc(dim=33), -2),
+        "wide at depth 3": (_ddesc(dim=17, depth=3), -2),
+        "wide block series": (_ddesc(dim=17, leaf=2, depth=2), -2),
         "length": (_ddesc(length=1), -2),
         "series order": (_ddesc(series_q=41), -4),
         "readout": (_ddesc(readout=9), -4),
@@ -210,6 +212,13 @@ def test_dense_c_abi_error_codes():
     for name, (dsc, code) in bad.items():
         assert lib.ews_dense_forward(ctypes.byref(dsc), null, null, null, null, null, null) == code, name
         assert lib.ews_dense_workspace_bytes(ctypes.byref(dsc)) == 0, name
+    # 16 < d <= 32 at depths 1-2 (series and Van Loan leaves): padded 32 x 32 step matrices and states
+    for leaf, kw in ((0, {}), (1, {"vl_steps": 4})):
+        wd = _ddesc(dim=24, depth=2, leaf=leaf, **kw)
+        wsz = lib.ews_dense_workspace_bytes(ctypes.byref(wd))
+        assert wsz >= 2 * 9 * (32 + 1024) * 4, leaf
+        assert lib.ews_dense_backward_workspace_bytes(ctypes.byref(wd)) > wsz
+        assert lib.ews_dense_forward(ctypes.byref(wd), null, null, null, null, null, null) == -1
     # the block-series leaf (depths 1 and 2): the series leaf's buffers plus its level-1 adjoint's
     bsd = _ddesc(leaf=2, depth=2)
     assert lib.ews_dense_workspace_bytes(ctypes.byref(bsd)) == lib.ews_dense_workspace_bytes(
@@ -240,10 +249,14 @@ def test_dense_layer_routing_and_errors():
         E.EWS(_planes(9), N=2, leaf="plane_closed", chen_expm="cayley")._engine_check()
     with pytest.raises(NotImplementedError):
         E.EWS(A, N=4)._engine_check()
+    # 16 < d <= 32: the wide dense kernels at depths 1-2 (series and Van Loan leaves)
+    assert E.EWS(E.AParamGeneral(torch.zeros(17, 17)), N=2)._engine_check() == "dense"
+    assert E.EWS(E.AParamGeneral(torch.zeros(32, 32)), N=1, leaf="series", series_q=8)._engine_check() == "dense"
+    assert E.EWS(_planes(12), N=2, van_loan_expm="cayley")._engine_check() == "dense"
     with pytest.raises(NotImplementedError):
-        E.EWS(E.AParamGeneral(torch.zeros(17, 17)), N=2)._engine_check()
+        E.EWS(E.AParamGeneral(torch.zeros(17, 17)), N=3)._engine_check()
     with pytest.raises(NotImplementedError):
-        E.EWS(E.AParamGeneral(torch.zeros(17, 17)), N=2, leaf="series", series_q=8)._engine_check()
+        E.EWS(E.AParamGeneral(torch.zeros(33, 33)), N=2, leaf="series", series_q=8)._engine_check()
     with pytest.raises(NotImplementedError):
         ops.DenseLeaf("van_loan", M=65)
     with pytest.raises(ValueError):
