@@ -656,14 +656,16 @@ def _timed(fn, args):
 
 
 def bench_banked(args):
-    """The reference's banked depth-1 blocks at their widths (survey row f4), through the EWS layer:
+    """The reference's banked blocks at their widths (survey rows f4 and a3), through the EWS layer:
     ppg: ppg_results/config.json's block, B=8 sequences of L=49,920, m=64 as 16 complex Jordan chains of size 4,
     leaf jordan_closed with jordan_flows, a clamped-gate clock, prefix rows, forward + backward (gradients to the
     path, the clock and the chain parameters) on the depth-1 chain kernels (csrc/ews_chain.hip);
     fl: formal_language_results/even_pairs's token block, B=256 sequences of 512 tokens, vocabulary 8, m=64 as 32
     rotation planes, Van Loan M=4 with exact exponentials: the token cache (chain kernels on 8 one-interval samples)
     and the depth-1 cached scan (csrc/ews_token1.hip), forward + backward to the token displacements, clock increments
-    and plane parameters."""
+    and plane parameters;
+    scp1: uea_results/scp1's block, B=32 x 896 steps, a dense d=17 generator at depth 2 (Van Loan M=4 euler, cayley
+    flows, uniform reweighting, mean readout), forward + backward on the d > 16 dense kernels (csrc/ews_wide.hip)."""
     import torch
 
     import ews_mi355x as E
@@ -692,6 +694,30 @@ def bench_banked(args):
         what = ("ppg: B=8, L=49920, m=64 as 16 complex Jordan chains of size 4, depth 1, jordan_closed + "
                 "jordan_flows, clamped-gate clock, prefix rows, forward + backward (path, clock and chain-parameter "
                 "gradients) on the depth-1 chain kernels")
+        steps_per = n
+    elif args.config == "scp1":
+        # uea_results/scp1/config.json: B=32, 896 samples of SelfRegulationSCP1 lifted to d=17, skew-symmetric A,
+        # depth 2, van_loan M=4 euler, chen_expm cayley, displacement_uniform, mean readout
+        B, L, d = 32, 896, 17
+        G = rng.normal(size=(d, d)) * np.sqrt(0.010095)
+        param = E.AParamGeneral(torch.tensor(G - G.T, dtype=torch.float32)).to(dev)
+        path = torch.tensor(np.cumsum(rng.normal(size=(B, L, d)) / np.sqrt(L), 1), dtype=torch.float32,
+                            device=dev).requires_grad_(True)
+        clock = torch.tensor(np.broadcast_to(np.linspace(-1.0, 1.0, L), (B, L)).copy(), dtype=torch.float32,
+                             device=dev)
+        layer = E.EWS(param, N=2, leaf="van_loan", M=4, van_loan_expm="euler", chen_expm="cayley",
+                      reweighting_mode="displacement_uniform")
+        g = torch.tensor(rng.normal(size=(B, 1 + d + d * d)), dtype=torch.float32, device=dev)
+
+        def step():
+            out = layer(path, clock, readout="mean")
+            out.backward(g)
+
+        n = B * (L - 1)
+        traffic = n * 4 * (d + 1) * 2  # read path and clock, write the path gradient
+        what = ("scp1: uea_results/scp1 block, B=32, L=896, dense d=17 (skew-symmetric A), depth 2, van_loan M=4 "
+                "euler, chen_expm cayley, displacement_uniform, mean readout, forward + backward (path and A "
+                "gradients) on the d > 16 dense kernels")
         steps_per = n
     else:
         B, n_tok, V, K = 256, 512, 8, 32
@@ -724,7 +750,7 @@ def bench_banked(args):
         "value": round(steps_per / (ms * 1e-3), 1), "unit": "time-steps/s", "n_gpus": 1, "steps": args.steps,
         "warmup": args.warmup, "ms_per_step": round(ms, 4), "higher_is_better": True, "scaling": "weak",
         "vs_baseline": None, "dtype": "f32", "data": "synthetic",
-        "config": {"workload": what, "global_batch": B, "seq_len": L if args.config == "ppg" else n_tok,
+        "config": {"workload": what, "global_batch": B, "seq_len": n_tok if args.config == "fl" else L,
                    "parallelism": "none (1 GPU)"},
         "roofline": {"bound": "hbm", "kernel": "step", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None,
@@ -826,11 +852,12 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--check", action="store_true", help="also check one forward against the C float64 checker")
     ap.add_argument("--chunk", type=int, default=0, help="intervals per chunk (0: the library's default)")
-    ap.add_argument("--config", choices=["c2", "c3", "c1", "c4", "c5", "tok", "ppg", "fl"], default="c2",
+    ap.add_argument("--config", choices=["c2", "c3", "c1", "c4", "c5", "tok", "ppg", "fl", "scp1"], default="c2",
                     help="c2 (default, the headline): planes fwd+bwd; c3: dense-generator depth-3 forward; c1, c4, "
                          "c5: one block of the other BASELINE.json configs (real diagonal; LogEWS; bf16 planes); tok: the "
                          "token-cached scan on a formal-language shape; ppg, fl: the banked depth-1 blocks at m=64 "
-                         "(PPG Jordan chains; the formal-language token block)")
+                         "(PPG Jordan chains; the formal-language token block); scp1: the banked SCP1 block (dense "
+                         "d=17 generator, depth 2)")
     ap.add_argument("--backward", action="store_true", help="c3: time forward + backward (ews_dense_backward)")
     ap.add_argument("--leaf", choices=["series", "van_loan"], default="series",
                     help="leaf of the c3 forward: series (q=24) or Van Loan (M=20, cayley)")
@@ -876,7 +903,7 @@ def main():
         torch.cuda.set_device(0)
         print(json.dumps(bench_c3(args)), flush=True)
         return
-    if args.config in ("ppg", "fl"):
+    if args.config in ("ppg", "fl", "scp1"):
         import torch
 
         torch.cuda.set_device(0)

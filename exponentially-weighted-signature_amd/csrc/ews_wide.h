@@ -12,6 +12,7 @@ namespace wide {
 
 struct WArgs {
   int B, L, n, d, N, T, C, W, lvl0, readout;
+  int TL, NSL, CP;  // leaf adjoint: intervals per slice, slices per sample; CP = max(C, NSL)
   int flow_mode, chen, leaf, q, vm, vl_expm, vl_mode;
   const float* path;
   const float* clock;
@@ -32,12 +33,12 @@ struct WArgs {
   float* lend;   // cotangent on each chunk's end state from the later chunks (B, C)
   float* dloc;   // local-term cotangents (B, n)
   float* dfl;    // per-interval flow cotangents (B, n)
-  float* cpart;  // per-chunk sums of the shared flow's and Van Loan pair's cotangents (B, C, 3)
+  float* cpart;  // per-chunk sums of the shared flow's cotangent and per-slice sums of the Van Loan pair's (B, CP, 3)
   float* dvlm;   // per-interval Van Loan pair cotangents (B, n, 2)
   float* apart;  // dA partials of the workgroups
   float* dv;     // increment cotangents (B, n, 32)
   float* dhl;    // series leaf's clock-step cotangents (B, n)
-  float* dhm;    // per-interval matrix functions' clock-step cotangents (B, n)
+  float* dhm;    // per-interval matrix functions' clock-step cotangents (B, n, 2): flow, Van Loan
   float* dsh;    // shared steps' cotangents (B, 2): flow, Van Loan
 };
 

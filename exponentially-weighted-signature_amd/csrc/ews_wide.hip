@@ -541,8 +541,11 @@ __global__ __launch_bounds__(NT) void k_wmat(WArgs a, int per_interval) {
   load_A(a.d, a.A, smd + MF_A);
   __syncthreads();
   const long items = per_interval ? (long)a.B * a.n : a.B;
-  const bool do_flow = (a.flow_mode == EWS_FLOW_PER_INTERVAL) == (per_interval != 0);
-  const bool do_vl = a.leaf == EWS_LEAF_VAN_LOAN && (a.vl_mode == EWS_FLOW_PER_INTERVAL) == (per_interval != 0);
+  // with two grid rows, row 0 forms the flows and row 1 the Van Loan pairs
+  const bool do_flow = (a.flow_mode == EWS_FLOW_PER_INTERVAL) == (per_interval != 0) &&
+                       (gridDim.y == 1 || blockIdx.y == 0);
+  const bool do_vl = a.leaf == EWS_LEAF_VAN_LOAN && (a.vl_mode == EWS_FLOW_PER_INTERVAL) == (per_interval != 0) &&
+                     (gridDim.y == 1 || blockIdx.y == 1);
   for (long it = blockIdx.x; it < items; it += gridDim.x) {
     const int b = per_interval ? (int)(it / a.n) : (int)it;
     const int t = per_interval ? (int)(it - (long)b * a.n) : 1;
@@ -561,19 +564,20 @@ __global__ __launch_bounds__(NT) void k_wmat(WArgs a, int per_interval) {
   }
 }
 
-// The flow of interval t of sample b into F (and its transpose into Ft), LDS
-__device__ __forceinline__ void load_flow(const WArgs& a, int b, int t, float* F, float* Ft) {
-  const float* th = a.clock + (size_t)b * a.L;
+// The thread's four entries of the flow of interval t of sample b (registers), and their store into F and, transposed,
+// Ft (LDS): the scans load a step's operands into registers during the step before it.
+__device__ __forceinline__ float4 flow_regs(const WArgs& a, int b, int t) {
   bool ident;
-  flow_step(a, th, t, ident);
-  float4 v;
+  flow_step(a, a.clock + (size_t)b * a.L, t, ident);
   if (ident) {
     const int i = trow<32>(), j0 = tcol<32>();
-    v = float4{i == j0 ? 1.0f : 0.0f, i == j0 + 1 ? 1.0f : 0.0f, i == j0 + 2 ? 1.0f : 0.0f, i == j0 + 3 ? 1.0f : 0.0f};
-  } else {
-    const size_t item = a.flow_mode == EWS_FLOW_PER_INTERVAL ? (size_t)b * a.n + t : (size_t)b;
-    v = gld4(a.fl + item * MM);
+    return float4{i == j0 ? 1.0f : 0.0f, i == j0 + 1 ? 1.0f : 0.0f, i == j0 + 2 ? 1.0f : 0.0f,
+                  i == j0 + 3 ? 1.0f : 0.0f};
   }
+  const size_t item = a.flow_mode == EWS_FLOW_PER_INTERVAL ? (size_t)b * a.n + t : (size_t)b;
+  return gld4(a.fl + item * MM);
+}
+__device__ __forceinline__ void commit_mat(float4 v, float* F, float* Ft) {
   sld4(F, v);
   const int i = trow<32>(), j0 = tcol<32>();
   Ft[(j0 + 0) * P32 + i] = v.x;
@@ -811,14 +815,24 @@ __global__ __launch_bounds__(NT) void k_wscan(WArgs a) {
   } else {
     load_state(a.car + ((size_t)b * (a.C + 1) + c) * RW, S1, S2);
   }
-  const bool cached = a.flow_mode != EWS_FLOW_PER_INTERVAL;
-  for (int t = t0; t < t1; ++t) {
-    if (!cached || t == t0 || (a.flow_mode == EWS_FLOW_CACHED_BASEPOINT && t <= 1))
-      load_flow(a, b, t, sm + SC_F, sm + SC_FT);
+  // the step's flow, s1 and s2 in registers, loaded during the step before
+  float4 nF = flow_regs(a, b, t0), ns2 = float4{0.0f, 0.0f, 0.0f, 0.0f};
+  float ns1 = 0.0f;
+  auto fetch = [&](int t) {
     const float* lrow = a.loc + ((size_t)b * a.n + t) * RW;
-    if (threadIdx.x < 32) s1[threadIdx.x] = lrow[threadIdx.x];
-    const float4 s2 = N >= 2 ? gld4(lrow + DP) : float4{0.0f, 0.0f, 0.0f, 0.0f};
+    if (threadIdx.x < 32) ns1 = lrow[threadIdx.x];
+    if (N >= 2) ns2 = gld4(lrow + DP);
+  };
+  fetch(t0);
+  for (int t = t0; t < t1; ++t) {
+    commit_mat(nF, sm + SC_F, sm + SC_FT);
+    if (threadIdx.x < 32) s1[threadIdx.x] = ns1;
+    const float4 s2 = ns2;
     __syncthreads();
+    if (t + 1 < t1) {
+      nF = flow_regs(a, b, t + 1);
+      fetch(t + 1);
+    }
     chen_step<N, MODE == SCAN_SUMMARY>(sm, s2, Ph, Pn);
     if constexpr (MODE == SCAN_ROWS) {
       const size_t r = (size_t)b * a.n + t;
@@ -850,13 +864,7 @@ __global__ __launch_bounds__(NT) void k_wcarry(WArgs a) {
   float* dummy0 = nullptr;
   float* dummy1 = nullptr;
   for (int c = 0; c < a.C; ++c) {
-    const float4 v = gld4(a.sfl + ((size_t)b * a.C + c) * MM);
-    sld4(F, v);
-    const int i = trow<32>(), j0 = tcol<32>();
-    Ft[(j0 + 0) * P32 + i] = v.x;
-    Ft[(j0 + 1) * P32 + i] = v.y;
-    Ft[(j0 + 2) * P32 + i] = v.z;
-    Ft[(j0 + 3) * P32 + i] = v.w;
+    commit_mat(gld4(a.sfl + ((size_t)b * a.C + c) * MM), F, Ft);
     const float* sr = a.summ + ((size_t)b * a.C + c) * RW;
     if (threadIdx.x < 32) s1[threadIdx.x] = sr[threadIdx.x];
     const float4 s2 = N >= 2 ? gld4(sr + DP) : float4{0.0f, 0.0f, 0.0f, 0.0f};
@@ -866,38 +874,61 @@ __global__ __launch_bounds__(NT) void k_wcarry(WArgs a) {
   }
 }
 
-// terminal / mean / max readouts: per sample and packed column
+// terminal / mean / max readouts: a workgroup per (sample, 32 packed columns); the mean and max run over the rows in
+// 8 interleaved groups combined in a fixed order (the max keeps the first row attaining it)
+constexpr int RO_COLS = 32, RO_GROUPS = NT / RO_COLS;
 __global__ __launch_bounds__(NT) void k_wreadout(WArgs a) {
-  const int b = blockIdx.y, col = blockIdx.x * NT + threadIdx.x;
-  if (col >= a.W) return;
+  __shared__ float s_v[RO_GROUPS][RO_COLS];
+  __shared__ int s_i[RO_GROUPS][RO_COLS];
+  const int b = blockIdx.y, cl = threadIdx.x % RO_COLS, grp = threadIdx.x / RO_COLS;
+  const int col = blockIdx.x * RO_COLS + cl;
+  const bool ok = col < a.W;
   float* o = a.out + (size_t)b * a.W;
-  if (a.lvl0 && col == 0) {
-    o[0] = 1.0f;
-    return;
-  }
   const int e = col - a.lvl0, d = a.d;
-  const int pe = e < d ? e : DP + ((e - d) / d) * DP + (e - d) % d;  // padded index
+  const int pe = !ok || e < 0 ? 0 : (e < d ? e : DP + ((e - d) / d) * DP + (e - d) % d);  // padded index
   if (a.readout == EWS_READOUT_TERMINAL) {
-    o[col] = a.car[((size_t)b * (a.C + 1) + a.C) * RW + pe];
+    if (ok && grp == 0) o[col] = e < 0 ? 1.0f : a.car[((size_t)b * (a.C + 1) + a.C) * RW + pe];
     return;
   }
   const float* r = a.rows + (size_t)b * a.n * RW + pe;
+  float acc = a.readout == EWS_READOUT_MEAN ? 0.0f : -INFINITY;
+  int arg = -1;
+  for (int t = grp; t < a.n; t += RO_GROUPS) {
+    const float v = ok ? r[(size_t)t * RW] : 0.0f;
+    if (a.readout == EWS_READOUT_MEAN) {
+      acc += v;
+    } else if (arg < 0 || v > acc) {
+      acc = v;
+      arg = t;
+    }
+  }
+  s_v[grp][cl] = acc;
+  s_i[grp][cl] = arg;
+  __syncthreads();
+  if (grp != 0 || !ok) return;
+  if (e < 0) {
+    o[col] = 1.0f;
+    if (a.amax) a.amax[(size_t)b * a.W + col] = 0;
+    return;
+  }
   if (a.readout == EWS_READOUT_MEAN) {
-    float s = 0.0f;
-    for (int t = 0; t < a.n; ++t) s += r[(size_t)t * RW];
-    o[col] = s / (float)a.n;
+    float sum = 0.0f;
+    for (int g2 = 0; g2 < RO_GROUPS; ++g2) sum += s_v[g2][cl];
+    o[col] = sum / (float)a.n;
   } else {
-    float best = r[0];
-    int arg = 0;
-    for (int t = 1; t < a.n; ++t) {
-      const float v = r[(size_t)t * RW];
-      if (v > best) {
+    float best = s_v[0][cl];
+    int bi = s_i[0][cl];
+    for (int g2 = 1; g2 < RO_GROUPS; ++g2) {
+      const int ti = s_i[g2][cl];
+      if (ti < 0) continue;
+      const float v = s_v[g2][cl];
+      if (bi < 0 || v > best || (v == best && ti < bi)) {
         best = v;
-        arg = t;
+        bi = ti;
       }
     }
     o[col] = best;
-    if (a.amax) a.amax[(size_t)b * a.W + col] = arg;
+    if (a.amax) a.amax[(size_t)b * a.W + col] = bi;
   }
 }
 
@@ -1021,21 +1052,39 @@ __global__ __launch_bounds__(NT) void k_wadj(WArgs a) {
   }
   const bool cached = a.flow_mode != EWS_FLOW_PER_INTERVAL;
   float dfs[4] = {0.0f, 0.0f, 0.0f, 0.0f};  // shared-flow cotangent summed over the chunk's steps
-  for (int t = t1 - 1; t >= t0; --t) {
+  // the step's row cotangent, flow, s1 and (FULL) the state before it in registers, loaded during the step after
+  float4 nF, ng2 = float4{0.0f, 0.0f, 0.0f, 0.0f}, nS2 = float4{0.0f, 0.0f, 0.0f, 0.0f};
+  float ng1 = 0.0f, ns1 = 0.0f, nS1 = 0.0f;
+  auto fetch = [&](int t) {
     const size_t r = (size_t)b * a.n + t;
-    // row cotangent of the step's output, the flow, s1, and (FULL) the state before the step
     const float* gr = a.grow + r * RW;
     if (threadIdx.x < 32) {
-      l1[threadIdx.x] += gr[threadIdx.x];
-      s1[threadIdx.x] = a.loc[r * RW + threadIdx.x];
+      ng1 = gr[threadIdx.x];
+      ns1 = a.loc[r * RW + threadIdx.x];
     }
-    if constexpr (N >= 2) sld4(L2, f4add(lds4(L2), gld4(gr + DP)));
-    load_flow(a, b, t, sm + AD_F, sm + AD_FT);
-    if constexpr (MODE == ADJ_FULL) {
+    if (N >= 2) ng2 = gld4(gr + DP);
+    nF = flow_regs(a, b, t);
+    if (MODE == ADJ_FULL) {
       const float* sp = t > t0 ? a.rows + (r - 1) * RW : a.car + ((size_t)b * (a.C + 1) + c) * RW;
-      load_state(sp, S1, S2);
+      if (threadIdx.x < 32) nS1 = sp[threadIdx.x];
+      if (N >= 2) nS2 = gld4(sp + DP);
     }
+  };
+  fetch(t1 - 1);
+  for (int t = t1 - 1; t >= t0; --t) {
+    const size_t r = (size_t)b * a.n + t;
+    if (threadIdx.x < 32) {
+      l1[threadIdx.x] += ng1;
+      s1[threadIdx.x] = ns1;
+      if (MODE == ADJ_FULL) S1[threadIdx.x] = nS1;
+    }
+    if constexpr (N >= 2) {
+      sld4(L2, f4add(lds4(L2), ng2));
+      if (MODE == ADJ_FULL) sld4(S2, nS2);
+    }
+    commit_mat(nF, sm + AD_F, sm + AD_FT);
     __syncthreads();
+    if (t > t0) fetch(t - 1);
     float df[4];
     adj_step<N, MODE>(sm, MODE == ADJ_FULL ? a.dloc + r * RW : nullptr, df);
     if constexpr (MODE == ADJ_FULL) {
@@ -1052,7 +1101,7 @@ __global__ __launch_bounds__(NT) void k_wadj(WArgs a) {
   if (MODE == ADJ_LOCAL) {
     store_state(a.mu + ((size_t)b * a.C + c) * RW, l1, L2);
   } else if (cached) {
-    gst4(a.cpart + ((size_t)b * a.C + c) * 3 * MM, acc4(dfs));
+    gst4(a.cpart + ((size_t)b * a.CP + c) * 3 * MM, acc4(dfs));
   }
 }
 
@@ -1071,13 +1120,7 @@ __global__ __launch_bounds__(NT) void k_wadj_carry(WArgs a) {
   __syncthreads();
   store_state(a.lend + ((size_t)b * a.C + a.C - 1) * RW, l1, L2);
   for (int c = a.C - 1; c >= 1; --c) {
-    const float4 v = gld4(a.sfl + ((size_t)b * a.C + c) * MM);
-    sld4(F, v);
-    const int i = trow<32>(), j0 = tcol<32>();
-    Ft[(j0 + 0) * P32 + i] = v.x;
-    Ft[(j0 + 1) * P32 + i] = v.y;
-    Ft[(j0 + 2) * P32 + i] = v.z;
-    Ft[(j0 + 3) * P32 + i] = v.w;
+    commit_mat(gld4(a.sfl + ((size_t)b * a.C + c) * MM), F, Ft);
     if (threadIdx.x < 32) s1[threadIdx.x] = a.summ[((size_t)b * a.C + c) * RW + threadIdx.x];
     __syncthreads();
     float df[4];
@@ -1090,8 +1133,9 @@ __global__ __launch_bounds__(NT) void k_wadj_carry(WArgs a) {
   }
 }
 
-// Leaf adjoints, a workgroup per (chunk, sample): dv per interval, the series leaf's dh and dA (workgroup partial),
-// the Van Loan leaf's (dP, dV) per interval (per-interval mode) or summed over the chunk (shared modes).
+// Leaf adjoints, a workgroup per (slice of TL intervals, sample): dv per interval, the series leaf's dh and dA
+// (workgroup partial), the Van Loan leaf's (dP, dV) per interval (per-interval mode) or summed over the slice (shared
+// modes).
 template <int N>
 __global__ __launch_bounds__(NT) void k_wleaf_bwd(WArgs a) {
   __shared__ __align__(16) float sm[LF_FLOATS];
@@ -1104,27 +1148,54 @@ __global__ __launch_bounds__(NT) void k_wleaf_bwd(WArgs a) {
   float* T2 = sm + LF_TAB2;
   float* T3 = sm + LF_TAB3;
   float* T4 = sm + LF_TAB4;
-  const int c = blockIdx.x, b = blockIdx.y;
-  const int t0 = c * a.T, t1 = min(a.n, t0 + a.T);
+  const int sl = blockIdx.x, b = blockIdx.y;
+  const int t0 = sl * a.TL, t1 = min(a.n, t0 + a.TL);
   const int tid = threadIdx.x, i = tid >> 3, j0 = (tid & 7) * 4;
   load_A(a.d, a.A, A);
   float dA[4] = {0.0f, 0.0f, 0.0f, 0.0f};
   float sP[4] = {0.0f, 0.0f, 0.0f, 0.0f}, sV[4] = {0.0f, 0.0f, 0.0f, 0.0f};
   const float* th = a.clock + (size_t)b * a.L;
+  const bool vl = a.leaf == EWS_LEAF_VAN_LOAN;
+  const bool vl_shared = vl && a.vl_mode != EWS_FLOW_PER_INTERVAL;
+  // the interval's cotangents, increment and (per-interval Van Loan) step matrices in registers, loaded during the
+  // interval before
+  float nd1 = 0.0f, nv = 0.0f;
+  float4 nd2 = float4{0.0f, 0.0f, 0.0f, 0.0f}, nP = nd2, nV = nd2;
+  auto fetch = [&](int t) {
+    const size_t r = (size_t)b * a.n + t;
+    const float* x = a.path + ((size_t)b * a.L + t) * a.d;
+    if (tid < 32) {
+      nd1 = a.dloc[r * RW + tid];
+      nv = tid < a.d ? x[a.d + tid] - x[tid] : 0.0f;
+    }
+    if (N >= 2) nd2 = gld4(a.dloc + r * RW + DP);
+    if (vl && !vl_shared) {
+      nP = gld4(a.vlm + r * 2 * MM);
+      nV = gld4(a.vlm + r * 2 * MM + MM);
+    }
+  };
+  if (t0 < t1) fetch(t0);
   __syncthreads();
   for (int t = t0; t < t1; ++t) {
     const size_t r = (size_t)b * a.n + t;
-    const float* x = a.path + ((size_t)b * a.L + t) * a.d;
-    if (tid < 32) ds1[tid] = a.dloc[r * RW + tid];
-    if constexpr (N >= 2) sld4(S2b, gld4(a.dloc + r * RW + DP));
+    if (tid < 32) {
+      ds1[tid] = nd1;
+      wv[tid] = vl ? nv / (float)a.vm : nv;
+    }
+    if constexpr (N >= 2) sld4(S2b, nd2);
     float dvi = 0.0f, dh = 0.0f;
-    if (a.leaf == EWS_LEAF_VAN_LOAN) {
+    if (vl) {
       float* P = sm + LF_P;
       float* V = sm + LF_V;
-      load_vl(a, b, t, P, V);
+      if (vl_shared) {
+        load_vl(a, b, t, P, V);
+      } else {
+        sld4(P, nP);
+        sld4(V, nV);
+      }
       const int M = a.vm;
-      if (tid < 32) wv[tid] = tid < a.d ? (x[a.d + tid] - x[tid]) / (float)M : 0.0f;
       __syncthreads();
+      if (t + 1 < t1) fetch(t + 1);
       vl_knots(a, P, V, wv, T1);  // Delta_m in rows 0 .. M-1
       if (tid < 32) {  // Z_m = R_m + Delta_m / 2 (T2), Y_m = Pre_m + Delta_m / 2 (T3)
         float suf = 0.0f;
@@ -1184,8 +1255,9 @@ __global__ __launch_bounds__(NT) void k_wleaf_bwd(WArgs a) {
     } else {
       const int q = a.q;
       const float h = th[t + 1] - th[t];
-      if (tid < 32) T1[tid] = tid < a.d ? x[a.d + tid] - x[tid] : 0.0f;
+      if (tid < 32) T1[tid] = wv[tid];
       __syncthreads();
+      if (t + 1 < t1) fetch(t + 1);
       for (int p = 1; p <= q; ++p) {  // letters b_p (T1) and A b_{p-1} (T3)
         const float y = mv<false>(A, T1 + (p - 1) * 32);
         if (row_lead()) {
@@ -1246,18 +1318,18 @@ __global__ __launch_bounds__(NT) void k_wleaf_bwd(WArgs a) {
     }
     __syncthreads();
   }
-  if (a.leaf == EWS_LEAF_VAN_LOAN && a.vl_mode != EWS_FLOW_PER_INTERVAL) {
-    float* cp = a.cpart + ((size_t)b * a.C + c) * 3 * MM;
+  if (vl_shared) {
+    float* cp = a.cpart + ((size_t)b * a.CP + sl) * 3 * MM;
     gst4(cp + MM, acc4(sP));
     gst4(cp + 2 * MM, acc4(sV));
   }
-  gst4(a.apart + ((size_t)b * a.C + c) * MM, acc4(dA));  // zero for the Van Loan leaf
+  gst4(a.apart + ((size_t)b * a.NSL + sl) * MM, acc4(dA));  // zero for the Van Loan leaf
 }
 
 // Matrix-function adjoints. per_interval: one item per interval, the flow's (dfl) and the Van Loan pair's (dvlm)
-// cotangents of the per-interval modes, dh into dhm; else one item per sample, the chunk partials of the shared
-// flow and pair summed in chunk order, the shared steps' gradients into dsh[b][0..1]. dA: workgroup partials at
-// apart + slot0.
+// cotangents of the per-interval modes, dh into dhm (flow, Van Loan); else one item per sample, the partials of the
+// shared flow (per chunk) and pair (per leaf slice) summed in order, the shared steps' gradients into dsh[b][0..1].
+// dA: workgroup partials at apart + slot0 (grid row by row).
 __global__ __launch_bounds__(NT) void k_wmat_bwd(WArgs a, int per_interval, long slot0) {
   extern __shared__ __align__(16) float sm[];
   float* A = sm + MF_A;
@@ -1265,8 +1337,11 @@ __global__ __launch_bounds__(NT) void k_wmat_bwd(WArgs a, int per_interval, long
   __syncthreads();
   float dA[4] = {0.0f, 0.0f, 0.0f, 0.0f};
   const long items = per_interval ? (long)a.B * a.n : a.B;
-  const bool do_flow = (a.flow_mode == EWS_FLOW_PER_INTERVAL) == (per_interval != 0);
-  const bool do_vl = a.leaf == EWS_LEAF_VAN_LOAN && (a.vl_mode == EWS_FLOW_PER_INTERVAL) == (per_interval != 0);
+  // with two grid rows, row 0 takes the flows and row 1 the Van Loan pairs
+  const bool do_flow = (a.flow_mode == EWS_FLOW_PER_INTERVAL) == (per_interval != 0) &&
+                       (gridDim.y == 1 || blockIdx.y == 0);
+  const bool do_vl = a.leaf == EWS_LEAF_VAN_LOAN && (a.vl_mode == EWS_FLOW_PER_INTERVAL) == (per_interval != 0) &&
+                     (gridDim.y == 1 || blockIdx.y == 1);
   float* G0 = sm + MF_T;
   float* G1 = sm + MF_U;
   for (long it = blockIdx.x; it < items; it += gridDim.x) {
@@ -1284,7 +1359,7 @@ __global__ __launch_bounds__(NT) void k_wmat_bwd(WArgs a, int per_interval, long
       } else {
         g[0] = g[1] = g[2] = g[3] = 0.0f;
         for (int c = 0; c < a.C; ++c) {
-          const float4 v = gld4(a.cpart + ((size_t)b * a.C + c) * 3 * MM);
+          const float4 v = gld4(a.cpart + ((size_t)b * a.CP + c) * 3 * MM);
           g[0] += v.x; g[1] += v.y; g[2] += v.z; g[3] += v.w;
         }
       }
@@ -1311,8 +1386,8 @@ __global__ __launch_bounds__(NT) void k_wmat_bwd(WArgs a, int per_interval, long
         } else {
 #pragma unroll
           for (int k = 0; k < 4; ++k) g0[k] = g1[k] = 0.0f;
-          for (int c = 0; c < a.C; ++c) {
-            const float* cp = a.cpart + ((size_t)b * a.C + c) * 3 * MM;
+          for (int c = 0; c < a.NSL; ++c) {
+            const float* cp = a.cpart + ((size_t)b * a.CP + c) * 3 * MM;
             const float4 p = gld4(cp + MM), v = gld4(cp + 2 * MM);
             g0[0] += p.x; g0[1] += p.y; g0[2] += p.z; g0[3] += p.w;
             g1[0] += v.x; g1[1] += v.y; g1[2] += v.z; g1[3] += v.w;
@@ -1331,28 +1406,31 @@ __global__ __launch_bounds__(NT) void k_wmat_bwd(WArgs a, int per_interval, long
         dh_v = block_sum(dot, sm + MF_RED) / (float)a.vm;  // c = dt / M
       }
     }
-    if (threadIdx.x == 0) {
-      if (per_interval) {
-        a.dhm[it] = dh_f + dh_v;
-      } else {
-        a.dsh[2 * b] = dh_f;
-        a.dsh[2 * b + 1] = dh_v;
-      }
+    if (threadIdx.x == 0) {  // [flow, Van Loan] per interval or per sample
+      float* dst = per_interval ? a.dhm + 2 * it : a.dsh + 2 * b;
+      if (do_flow) dst[0] = dh_f;
+      if (do_vl) dst[1] = dh_v;
     }
     __syncthreads();
   }
-  gst4(a.apart + (slot0 + blockIdx.x) * MM, acc4(dA));
+  gst4(a.apart + (slot0 + (long)blockIdx.y * gridDim.x + blockIdx.x) * MM, acc4(dA));
 }
 
-// grad_A = sum of the partials (float64, in slot order), entries i, j < d
+// grad_A = sum of the partials (float64): a workgroup per 16 entries, 16 interleaved groups of slots combined in a
+// fixed order; entries i, j < d
 __global__ __launch_bounds__(NT) void k_wfinal_A(WArgs a, long nparts, float* grad_A) {
-  const int e = blockIdx.x * NT + threadIdx.x;
-  if (e >= MM) return;
-  const int r = e >> 5, c = e & 31;
-  if (r >= a.d || c >= a.d) return;
+  __shared__ double s_p[16][16];
+  const int el = threadIdx.x & 15, grp = threadIdx.x >> 4;
+  const int e = blockIdx.x * 16 + el;
   double s = 0.0;
-  for (long k = 0; k < nparts; ++k) s += (double)a.apart[k * MM + e];
-  grad_A[r * a.d + c] = (float)s;
+  for (long k = grp; k < nparts; k += 16) s += (double)a.apart[k * MM + e];
+  s_p[grp][el] = s;
+  __syncthreads();
+  if (grp != 0) return;
+  double tot = 0.0;
+  for (int g2 = 0; g2 < 16; ++g2) tot += s_p[g2][el];
+  const int r = e >> 5, c = e & 31;
+  if (r < a.d && c < a.d) grad_A[r * a.d + c] = (float)tot;
 }
 
 // grad_path[b][k] = dv[k-1] - dv[k]; grad_clock[b][k] = dh[k-1] - dh[k] plus the shared steps' gradients
@@ -1370,8 +1448,8 @@ __global__ __launch_bounds__(NT) void k_wknots(WArgs a, float* grad_path, float*
   auto dh = [&](int t) -> float {
     float s = 0.0f;
     if (a.leaf != EWS_LEAF_VAN_LOAN) s += a.dhl[base + t];
-    if (a.flow_mode == EWS_FLOW_PER_INTERVAL || (a.leaf == EWS_LEAF_VAN_LOAN && a.vl_mode == EWS_FLOW_PER_INTERVAL))
-      s += a.dhm[base + t];
+    if (a.flow_mode == EWS_FLOW_PER_INTERVAL) s += a.dhm[2 * (base + t)];
+    if (a.leaf == EWS_LEAF_VAN_LOAN && a.vl_mode == EWS_FLOW_PER_INTERVAL) s += a.dhm[2 * (base + t) + 1];
     return s;
   };
   float g = (k >= 1 ? dh(k - 1) : 0.0f) - (k < a.n ? dh(k) : 0.0f);
@@ -1399,10 +1477,13 @@ namespace {
 
 size_t al256(size_t x) { return (x + 255) & ~(size_t)255; }
 
+constexpr int kLeafSlice = 16;  // intervals per workgroup of the leaf adjoint
+
 struct WPlan {
-  int B, L, n, d, N, T, C, W;
+  int B, L, n, d, N, T, C, W, TL, NSL, CP;
   bool fl_int, vl, vl_int, exact_int, exact_smp, mats_int, mats_smp;
-  long g_int, g_smp;  // workgroups of the matrix-function adjoints
+  long g_int, g_smp;   // workgroups of the matrix-function adjoints (per grid row)
+  int gy_int, gy_smp;  // grid rows: 2 when both the flows and the Van Loan pairs are of that kind
 };
 
 int plan(const ews_dense_desc* s, WPlan& p) {
@@ -1426,6 +1507,9 @@ int plan(const ews_dense_desc* s, WPlan& p) {
   p.N = s->depth;
   p.T = s->chunk ? s->chunk : 64;
   p.C = (p.n + p.T - 1) / p.T;
+  p.TL = kLeafSlice;
+  p.NSL = (p.n + p.TL - 1) / p.TL;
+  p.CP = std::max(p.C, p.NSL);
   p.W = p.d + (p.N >= 2 ? p.d * p.d : 0) + (s->level0 ? 1 : 0);
   p.fl_int = s->flow_mode == EWS_FLOW_PER_INTERVAL;
   p.vl = vl;
@@ -1436,6 +1520,8 @@ int plan(const ews_dense_desc* s, WPlan& p) {
   p.exact_smp = (!p.fl_int && s->chen_expm == EWS_EXPM_EXACT) || (vl && !p.vl_int && s->vl_expm == EWS_EXPM_EXACT);
   p.g_int = p.mats_int ? std::min<long>((long)p.B * p.n, 2048) : 0;
   p.g_smp = p.mats_smp ? p.B : 0;
+  p.gy_int = p.fl_int && p.vl_int ? 2 : 1;
+  p.gy_smp = !p.fl_int && vl && !p.vl_int ? 2 : 1;
   return EWS_OK;
 }
 
@@ -1468,12 +1554,12 @@ WLay layout(const ews_dense_desc* s, const WPlan& p, bool bwd) {
     take(w.lend, BC * RW * 4);
     take(w.dloc, BN * RW * 4);
     take(w.dfl, p.fl_int ? BN * MM * 4 : 0);
-    take(w.cpart, BC * 3 * MM * 4);
+    take(w.cpart, (size_t)p.B * p.CP * 3 * MM * 4);
     take(w.dvlm, p.vl_int ? BN * 2 * MM * 4 : 0);
-    take(w.apart, (BC + p.g_int + p.g_smp) * MM * 4);
+    take(w.apart, ((size_t)p.B * p.NSL + p.g_int * p.gy_int + p.g_smp * p.gy_smp) * MM * 4);
     take(w.dv, BN * DP * 4);
     take(w.dhl, BN * 4);
-    take(w.dhm, BN * 4);
+    take(w.dhm, BN * 2 * 4);
     take(w.dsh, (size_t)p.B * 2 * 4);
   }
   w.total = off;
@@ -1484,6 +1570,7 @@ WArgs make_args(const ews_dense_desc* s, const WPlan& p, const float* path, cons
                 float* out, void* workspace, bool bwd) {
   WArgs a{};
   a.B = p.B; a.L = p.L; a.n = p.n; a.d = p.d; a.N = p.N; a.T = p.T; a.C = p.C; a.W = p.W;
+  a.TL = p.TL; a.NSL = p.NSL; a.CP = p.CP;
   a.lvl0 = s->level0 ? 1 : 0; a.readout = s->readout;
   a.flow_mode = s->flow_mode; a.chen = s->chen_expm; a.leaf = s->leaf;
   a.q = p.vl ? 0 : s->series_q; a.vm = p.vl ? s->vl_steps : 0;
@@ -1520,11 +1607,12 @@ int run_forward(const WPlan& p, const WArgs& a, hipStream_t st) {
   const size_t lds = MF_ENT_FWD * sizeof(double);
   if (set_lds(reinterpret_cast<const void*>(&k_wmat), lds) != EWS_OK) return EWS_ERR_LAUNCH;
   if (p.mats_int) {
-    hipLaunchKernelGGL(k_wmat, dim3((unsigned)std::min<long>((long)p.B * p.n, 4096)), dim3(NT), lds, st, a, 1);
+    hipLaunchKernelGGL(k_wmat, dim3((unsigned)std::min<long>((long)p.B * p.n, 4096), p.gy_int), dim3(NT), lds, st, a,
+                       1);
     WIDE_CHECK();
   }
   if (p.mats_smp) {
-    hipLaunchKernelGGL(k_wmat, dim3(p.B), dim3(NT), lds, st, a, 0);
+    hipLaunchKernelGGL(k_wmat, dim3(p.B, p.gy_smp), dim3(NT), lds, st, a, 0);
     WIDE_CHECK();
   }
   const dim3 gl((unsigned)std::min<long>((long)p.B * p.n, 4096)), gc(p.C, p.B);
@@ -1541,7 +1629,7 @@ int run_forward(const WPlan& p, const WArgs& a, hipStream_t st) {
   }
   WIDE_CHECK();
   if (a.readout == EWS_READOUT_TERMINAL || a.readout == EWS_READOUT_MEAN || a.readout == EWS_READOUT_MAX) {
-    hipLaunchKernelGGL(k_wreadout, dim3((p.W + NT - 1) / NT, p.B), dim3(NT), 0, st, a);
+    hipLaunchKernelGGL(k_wreadout, dim3((p.W + RO_COLS - 1) / RO_COLS, p.B), dim3(NT), 0, st, a);
     WIDE_CHECK();
   }
   return EWS_OK;
@@ -1593,30 +1681,32 @@ int backward(const ews_dense_desc* s, const float* path, const float* clock, con
     hipLaunchKernelGGL((k_wadj<1, ADJ_LOCAL>), gc, dim3(NT), 0, st, a);
     hipLaunchKernelGGL(k_wadj_carry<1>, dim3(p.B), dim3(NT), 0, st, a);
     hipLaunchKernelGGL((k_wadj<1, ADJ_FULL>), gc, dim3(NT), 0, st, a);
-    hipLaunchKernelGGL(k_wleaf_bwd<1>, gc, dim3(NT), 0, st, a);
+    hipLaunchKernelGGL(k_wleaf_bwd<1>, dim3(p.NSL, p.B), dim3(NT), 0, st, a);
   } else {
     hipLaunchKernelGGL((k_wadj<2, ADJ_LOCAL>), gc, dim3(NT), 0, st, a);
     hipLaunchKernelGGL(k_wadj_carry<2>, dim3(p.B), dim3(NT), 0, st, a);
     hipLaunchKernelGGL((k_wadj<2, ADJ_FULL>), gc, dim3(NT), 0, st, a);
-    hipLaunchKernelGGL(k_wleaf_bwd<2>, gc, dim3(NT), 0, st, a);
+    hipLaunchKernelGGL(k_wleaf_bwd<2>, dim3(p.NSL, p.B), dim3(NT), 0, st, a);
   }
   WIDE_CHECK();
-  const long base = (long)p.B * p.C;
+  const long base = (long)p.B * p.NSL;
   if (p.mats_int) {
     const size_t lds = (p.exact_int ? MF_ENT_BWD_EXACT : MF_ENT_BWD) * 4;
     if (set_lds(reinterpret_cast<const void*>(&k_wmat_bwd), MF_ENT_BWD_EXACT * 4) != EWS_OK)
       return EWS_ERR_LAUNCH;
-    hipLaunchKernelGGL(k_wmat_bwd, dim3((unsigned)p.g_int), dim3(NT), lds, st, a, 1, base);
+    hipLaunchKernelGGL(k_wmat_bwd, dim3((unsigned)p.g_int, p.gy_int), dim3(NT), lds, st, a, 1, base);
     WIDE_CHECK();
   }
   if (p.mats_smp) {
     const size_t lds = (p.exact_smp ? MF_ENT_BWD_EXACT : MF_ENT_BWD) * 4;
     if (set_lds(reinterpret_cast<const void*>(&k_wmat_bwd), MF_ENT_BWD_EXACT * 4) != EWS_OK)
       return EWS_ERR_LAUNCH;
-    hipLaunchKernelGGL(k_wmat_bwd, dim3((unsigned)p.g_smp), dim3(NT), lds, st, a, 0, base + p.g_int);
+    hipLaunchKernelGGL(k_wmat_bwd, dim3((unsigned)p.g_smp, p.gy_smp), dim3(NT), lds, st, a, 0,
+                       base + p.g_int * p.gy_int);
     WIDE_CHECK();
   }
-  hipLaunchKernelGGL(k_wfinal_A, dim3(MM / NT), dim3(NT), 0, st, a, base + p.g_int + p.g_smp, grad_A);
+  hipLaunchKernelGGL(k_wfinal_A, dim3(MM / 16), dim3(NT), 0, st, a, base + p.g_int * p.gy_int + p.g_smp * p.gy_smp,
+                     grad_A);
   hipLaunchKernelGGL(k_wknots, dim3((p.L + NT - 1) / NT, p.B), dim3(NT), 0, st, a, grad_path, grad_clock);
   WIDE_CHECK();
   return EWS_OK;
