@@ -152,6 +152,45 @@ __device__ __forceinline__ float mv(const float* M, const float* x) {
 }
 __device__ __forceinline__ bool row_lead() { return (threadIdx.x & 7) == 0; }
 
+// 32 x 32 products of the scans on fp32 MFMA (mfma_f32_16x16x4f32): wavefront w computes the 16 x 16 tile
+// (rows m0 = 16 (w / 2), columns n0 = 16 (w % 2)) of Z = X Y (X(m, k) = X[k][m] when TX, Y(k, n) = Y[n][k] when TY),
+// LDS operands at pitch 36; lane (i, g) gives A[m0 + i][k] and B[k][n0 + i] for k = 4u + g and holds the result rows
+// m0 + 4g + r (r = 0..3) of column n0 + i.
+typedef float v4f __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ int tile_m0() { return 16 * ((int)threadIdx.x >> 7); }
+__device__ __forceinline__ int tile_n0() { return 16 * (((int)threadIdx.x >> 6) & 1); }
+__device__ __forceinline__ int tile_i() { return (int)threadIdx.x & 15; }
+__device__ __forceinline__ int tile_g() { return ((int)threadIdx.x >> 4) & 3; }
+
+template <bool TX, bool TY>
+__device__ __forceinline__ v4f mm_tile(const float* X, const float* Y, v4f acc) {
+  const int m0 = tile_m0(), n0 = tile_n0(), i = tile_i(), g = tile_g();
+#pragma unroll
+  for (int u = 0; u < 8; ++u) {
+    const int k = 4 * u + g;
+    const float xa = TX ? X[k * P32 + m0 + i] : X[(m0 + i) * P32 + k];
+    const float yb = TY ? Y[(n0 + i) * P32 + k] : Y[k * P32 + n0 + i];
+    acc = __builtin_amdgcn_mfma_f32_16x16x4f32(xa, yb, acc, 0, 0, 0);
+  }
+  return acc;
+}
+__device__ __forceinline__ v4f zero4() { return v4f{0.0f, 0.0f, 0.0f, 0.0f}; }
+// the lane's tile entries of a 32 x 32 matrix: LDS (pitch 36) or global (pitch 32)
+__device__ __forceinline__ void st_tile(float* Z, v4f v) {
+  const int m = tile_m0() + 4 * tile_g(), n = tile_n0() + tile_i();
+#pragma unroll
+  for (int r = 0; r < 4; ++r) Z[(m + r) * P32 + n] = v[r];
+}
+__device__ __forceinline__ v4f gld_tile(const float* g) {
+  const int m = tile_m0() + 4 * tile_g(), n = tile_n0() + tile_i();
+  return v4f{g[m * DP + n], g[(m + 1) * DP + n], g[(m + 2) * DP + n], g[(m + 3) * DP + n]};
+}
+__device__ __forceinline__ void gst_tile(float* g, v4f v) {
+  const int m = tile_m0() + 4 * tile_g(), n = tile_n0() + tile_i();
+#pragma unroll
+  for (int r = 0; r < 4; ++r) g[(m + r) * DP + n] = v[r];
+}
+
 // sum over the workgroup (every thread returns it); red: NT / 64 floats of LDS
 __device__ __forceinline__ float block_sum(float v, float* red) {
 #pragma unroll
@@ -729,10 +768,10 @@ constexpr int SC_F = 0, SC_FT = S32, SC_S2 = 2 * S32, SC_T = 3 * S32, SC_PH = 4 
 constexpr int SC_VEC = 6 * S32;  // S1, y1, s1 (32 each)
 constexpr int SC_FLOATS = SC_VEC + 3 * 32;
 
-// one Chen step of the state (S1, S2) in LDS by (F, Ft, s1 in LDS; s2 the thread's entries); with PHI the flow
-// product Ph <- F Ph as well (Pn scratch; the pointers swap)
+// one Chen step of the state (S1, S2) in LDS by (F, Ft, s1 in LDS; s2 the lane's tile entries); with PHI the flow
+// product Ph <- F Ph as well (Pn scratch; the pointers swap). The three products run on MFMA.
 template <int N, bool PHI>
-__device__ __forceinline__ void chen_step(float* sm, const float4 s2, float*& Ph, float*& Pn) {
+__device__ __forceinline__ void chen_step(float* sm, const v4f s2, float*& Ph, float*& Pn) {
   float* F = sm + SC_F;
   float* Ft = sm + SC_FT;
   float* S2 = sm + SC_S2;
@@ -740,28 +779,19 @@ __device__ __forceinline__ void chen_step(float* sm, const float4 s2, float*& Ph
   float* S1 = sm + SC_VEC;
   float* y1 = S1 + 32;
   float* s1 = S1 + 64;
-  const int i = (int)threadIdx.x >> 3, j0 = ((int)threadIdx.x & 7) * 4;
+  const int i = (int)threadIdx.x >> 3;
   const float y = mv<false>(F, S1);
-  float acc[4];
-  if constexpr (N >= 2) {
-    mm<32, false, false>(F, S2, acc);
-    st<32>(T, acc);
-  }
-  if constexpr (PHI) {
-    float pa[4];
-    mm<32, false, false>(F, Ph, pa);
-    st<32>(Pn, pa);
-  }
+  if constexpr (N >= 2) st_tile(T, mm_tile<false, false>(F, S2, zero4()));
+  if constexpr (PHI) st_tile(Pn, mm_tile<false, false>(F, Ph, zero4()));
   if (row_lead()) y1[i] = y;
   __syncthreads();
-  if constexpr (N >= 2) {
-    mm<32, false, false>(T, Ft, acc);  // F S2 F^T
-    const float4 sv = *reinterpret_cast<const float4*>(s1 + j0);
-    acc[0] += fmaf(y, sv.x, s2.x);
-    acc[1] += fmaf(y, sv.y, s2.y);
-    acc[2] += fmaf(y, sv.z, s2.z);
-    acc[3] += fmaf(y, sv.w, s2.w);
-    st<32>(S2, acc);
+  if constexpr (N >= 2) {  // S2 <- F S2 F^T + y1 s1^T + s2 (S2 is not read in this phase)
+    v4f acc = mm_tile<false, false>(T, Ft, s2);
+    const int m = tile_m0() + 4 * tile_g(), n = tile_n0() + tile_i();
+    const float sn = s1[n];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) acc[r] = fmaf(y1[m + r], sn, acc[r]);
+    st_tile(S2, acc);
   }
   if (row_lead()) S1[i] = y + s1[i];
   if constexpr (PHI) {
@@ -816,18 +846,19 @@ __global__ __launch_bounds__(NT) void k_wscan(WArgs a) {
     load_state(a.car + ((size_t)b * (a.C + 1) + c) * RW, S1, S2);
   }
   // the step's flow, s1 and s2 in registers, loaded during the step before
-  float4 nF = flow_regs(a, b, t0), ns2 = float4{0.0f, 0.0f, 0.0f, 0.0f};
+  float4 nF = flow_regs(a, b, t0);
+  v4f ns2 = zero4();
   float ns1 = 0.0f;
   auto fetch = [&](int t) {
     const float* lrow = a.loc + ((size_t)b * a.n + t) * RW;
     if (threadIdx.x < 32) ns1 = lrow[threadIdx.x];
-    if (N >= 2) ns2 = gld4(lrow + DP);
+    if (N >= 2) ns2 = gld_tile(lrow + DP);
   };
   fetch(t0);
   for (int t = t0; t < t1; ++t) {
     commit_mat(nF, sm + SC_F, sm + SC_FT);
     if (threadIdx.x < 32) s1[threadIdx.x] = ns1;
-    const float4 s2 = ns2;
+    const v4f s2 = ns2;
     __syncthreads();
     if (t + 1 < t1) {
       nF = flow_regs(a, b, t + 1);
@@ -867,7 +898,7 @@ __global__ __launch_bounds__(NT) void k_wcarry(WArgs a) {
     commit_mat(gld4(a.sfl + ((size_t)b * a.C + c) * MM), F, Ft);
     const float* sr = a.summ + ((size_t)b * a.C + c) * RW;
     if (threadIdx.x < 32) s1[threadIdx.x] = sr[threadIdx.x];
-    const float4 s2 = N >= 2 ? gld4(sr + DP) : float4{0.0f, 0.0f, 0.0f, 0.0f};
+    const v4f s2 = N >= 2 ? gld_tile(sr + DP) : zero4();
     __syncthreads();
     chen_step<N, false>(sm, s2, dummy0, dummy1);
     store_state(car + (size_t)(c + 1) * RW, S1, S2);
@@ -967,9 +998,10 @@ constexpr int AD_FLOATS = AD_VEC + 5 * 32;
 constexpr int ADJ_LOCAL = 0, ADJ_FULL = 1;
 
 // one reverse step: (lambda1, lambda2) of the state after the step (row cotangent included) to the state before it;
-// FULL: also ds1, ds2 (into dl) and dF (returned in df) from the state before the step (S1, S2 in LDS)
+// FULL: also ds1, ds2 (into dl) and dF (returned in the lane's tile entries) from the state before the step (S1, S2
+// in LDS). The products run on MFMA.
 template <int N, int MODE>
-__device__ __forceinline__ void adj_step(float* sm, float* dl, float* df) {
+__device__ __forceinline__ v4f adj_step(float* sm, float* dl) {
   float* F = sm + AD_F;
   float* Ft = sm + AD_FT;
   float* L2 = sm + AD_L2;
@@ -982,20 +1014,15 @@ __device__ __forceinline__ void adj_step(float* sm, float* dl, float* df) {
   float* s1 = l1 + 64;
   float* y1 = l1 + 96;
   float* rho = l1 + 128;
-  const int i = (int)threadIdx.x >> 3, j0 = ((int)threadIdx.x & 7) * 4;
-  float acc[4];
+  const int i = (int)threadIdx.x >> 3;
   float r = 0.0f, y = 0.0f;
   if constexpr (N >= 2) {
-    r = mv<false>(L2, s1);      // (lambda2 s1)[i]
-    mm<32, false, false>(L2, F, acc);  // H = lambda2 F
-    st<32>(H, acc);
+    r = mv<false>(L2, s1);                                      // (lambda2 s1)[i]
+    st_tile(H, mm_tile<false, false>(L2, F, zero4()));          // H = lambda2 F
     if constexpr (MODE == ADJ_FULL) {
-      y = mv<false>(F, S1);     // y1 = F S1
-      float g[4];
-      mm<32, false, false>(F, S2, g);  // G1 = F S2
-      st<32>(G1, g);
-      mm<32, false, true>(F, S2, g);   // G2 = F S2^T
-      st<32>(G2, g);
+      y = mv<false>(F, S1);                                     // y1 = F S1
+      st_tile(G1, mm_tile<false, false>(F, S2, zero4()));       // G1 = F S2
+      st_tile(G2, mm_tile<false, true>(F, S2, zero4()));        // G2 = F S2^T
     }
   } else if constexpr (MODE == ADJ_FULL) {
     y = mv<false>(F, S1);
@@ -1005,33 +1032,29 @@ __device__ __forceinline__ void adj_step(float* sm, float* dl, float* df) {
     y1[i] = y;
   }
   __syncthreads();
-  float ln[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-  if constexpr (N >= 2) mm<32, false, false>(Ft, H, ln);  // F^T H (Ft holds F^T row-major)
-  const float l1n = mv<true>(F, rho);  // (F^T rho)[i]
+  v4f ln = zero4(), df = zero4();
+  if constexpr (N >= 2) ln = mm_tile<false, false>(Ft, H, zero4());  // F^T H (Ft holds F^T row-major)
+  const float l1n = mv<true>(F, rho);                                // (F^T rho)[i]
   if constexpr (MODE == ADJ_FULL) {
     float ds1 = l1[i];
     if constexpr (N >= 2) ds1 += mv<true>(L2, y1);  // lambda2^T y1
     if (row_lead()) dl[i] = ds1;
     // dF = rho S1^T + lambda2 G2 + lambda2^T G1
-    const float4 sv = *reinterpret_cast<const float4*>(S1 + j0);
-    const float rr = rho[i];
-    df[0] = rr * sv.x;
-    df[1] = rr * sv.y;
-    df[2] = rr * sv.z;
-    df[3] = rr * sv.w;
     if constexpr (N >= 2) {
-      float p1[4], p2[4];
-      mm<32, false, false>(L2, G2, p1);
-      mm<32, true, false>(L2, G1, p2);
-#pragma unroll
-      for (int k = 0; k < 4; ++k) df[k] += p1[k] + p2[k];
+      df = mm_tile<false, false>(L2, G2, df);
+      df = mm_tile<true, false>(L2, G1, df);
       gst4(dl + DP, lds4(L2));  // ds2 = lambda2 (of the state after the step)
     }
+    const int m = tile_m0() + 4 * tile_g(), n = tile_n0() + tile_i();
+    const float sn = S1[n];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) df[k] = fmaf(rho[m + k], sn, df[k]);
   }
   __syncthreads();
-  if constexpr (N >= 2) st<32>(L2, ln);
+  if constexpr (N >= 2) st_tile(L2, ln);
   if (row_lead()) l1[i] = l1n;
   __syncthreads();
+  return df;
 }
 
 template <int N, int MODE>
@@ -1051,7 +1074,7 @@ __global__ __launch_bounds__(NT) void k_wadj(WArgs a) {
     load_state(a.lend + ((size_t)b * a.C + c) * RW, l1, L2);
   }
   const bool cached = a.flow_mode != EWS_FLOW_PER_INTERVAL;
-  float dfs[4] = {0.0f, 0.0f, 0.0f, 0.0f};  // shared-flow cotangent summed over the chunk's steps
+  v4f dfs = zero4();  // shared-flow cotangent summed over the chunk's steps (the lane's tile entries)
   // the step's row cotangent, flow, s1 and (FULL) the state before it in registers, loaded during the step after
   float4 nF, ng2 = float4{0.0f, 0.0f, 0.0f, 0.0f}, nS2 = float4{0.0f, 0.0f, 0.0f, 0.0f};
   float ng1 = 0.0f, ns1 = 0.0f, nS1 = 0.0f;
@@ -1085,23 +1108,21 @@ __global__ __launch_bounds__(NT) void k_wadj(WArgs a) {
     commit_mat(nF, sm + AD_F, sm + AD_FT);
     __syncthreads();
     if (t > t0) fetch(t - 1);
-    float df[4];
-    adj_step<N, MODE>(sm, MODE == ADJ_FULL ? a.dloc + r * RW : nullptr, df);
+    const v4f df = adj_step<N, MODE>(sm, MODE == ADJ_FULL ? a.dloc + r * RW : nullptr);
     if constexpr (MODE == ADJ_FULL) {
       bool ident;
       flow_step(a, a.clock + (size_t)b * a.L, t, ident);
       if (!cached) {
-        gst4(a.dfl + r * MM, acc4(df));
+        gst_tile(a.dfl + r * MM, df);
       } else if (!ident) {
-#pragma unroll
-        for (int k = 0; k < 4; ++k) dfs[k] += df[k];
+        dfs += df;
       }
     }
   }
   if (MODE == ADJ_LOCAL) {
     store_state(a.mu + ((size_t)b * a.C + c) * RW, l1, L2);
   } else if (cached) {
-    gst4(a.cpart + ((size_t)b * a.CP + c) * 3 * MM, acc4(dfs));
+    gst_tile(a.cpart + ((size_t)b * a.CP + c) * 3 * MM, dfs);
   }
 }
 
@@ -1123,8 +1144,7 @@ __global__ __launch_bounds__(NT) void k_wadj_carry(WArgs a) {
     commit_mat(gld4(a.sfl + ((size_t)b * a.C + c) * MM), F, Ft);
     if (threadIdx.x < 32) s1[threadIdx.x] = a.summ[((size_t)b * a.C + c) * RW + threadIdx.x];
     __syncthreads();
-    float df[4];
-    adj_step<N, ADJ_LOCAL>(sm, nullptr, df);
+    adj_step<N, ADJ_LOCAL>(sm, nullptr);
     const float* m = a.mu + ((size_t)b * a.C + c) * RW;
     if (threadIdx.x < 32) l1[threadIdx.x] += m[threadIdx.x];
     if constexpr (N >= 2) sld4(L2, f4add(lds4(L2), gld4(m + DP)));
