@@ -162,3 +162,27 @@ def test_wide_backward_is_deterministic():
         grads.append((p.grad.clone(), c.grad.clone(), a.grad.clone()))
     for name, x, y in zip(("path", "clock", "A"), grads[0], grads[1]):
         assert torch.equal(x, y), f"{name} gradient differs between two identical calls"
+
+
+@pytest.mark.parametrize("readout", ["prefix", "mean"])
+def test_wide_logews(readout):
+    """LogEWS over a dense d = 20 generator at depth 2: the wide kernels' rows, then the log and Lyndon compression
+    (csrc/ews_log.hip), against the oracle's log_ews_single (ews/layer.py:488-517), forward and gradients."""
+    path, clock, A = _inputs(2, 30, 20, seed=44)
+    layer = E.LogEWS(E.AParamGeneral(A.float()), N=2, M=4, van_loan_expm="pade", chen_expm="cayley",
+                     reweighting_mode="displacement").to(DEV)
+    pg = path.float().to(DEV).requires_grad_(True)
+    out = layer(pg, clock.float().to(DEV), readout=readout)
+    p64 = path.clone().requires_grad_(True)
+    ref = torch.stack([O.log_ews_single(p64[b], clock[b], A, 2, readout, leaf="van_loan", M=4,
+                                        van_loan_expm="pade", chen_expm="cayley", reweighting_mode="displacement")
+                       for b in range(2)])
+    e = relerr(out, ref)
+    print(f"logews {readout}: forward {e:.2e}")
+    assert e < 1e-5
+    gout = torch.tensor(np.random.default_rng(3).normal(size=ref.shape))
+    (rg,) = torch.autograd.grad(ref, (p64,), gout)
+    out.backward(gout.float().to(DEV))
+    eg = relerr(pg.grad, rg)
+    print(f"logews {readout}: path grad {eg:.2e}")
+    assert eg < 1e-4
