@@ -695,6 +695,28 @@ def bench_banked(args):
                 "jordan_flows, clamped-gate clock, prefix rows, forward + backward (path, clock and chain-parameter "
                 "gradients) on the depth-1 chain kernels")
         steps_per = n
+    elif args.config == "dense24":
+        # EWS's defaults (van_loan M=20 cayley, exact flows, displacement: every interval its own step matrices) on
+        # a dense d=24 generator at depth 2, B=32 x 896 steps of an irregular clock, terminal readout
+        B, L, d = 32, 896, 24
+        param = E.AParamGeneral(torch.tensor(rng.normal(size=(d, d)) * 0.3, dtype=torch.float32)).to(dev)
+        path = torch.tensor(np.cumsum(rng.normal(size=(B, L, d)) / np.sqrt(L), 1), dtype=torch.float32,
+                            device=dev).requires_grad_(True)
+        clock = torch.tensor(np.cumsum(rng.uniform(0.5, 1.5, size=(B, L)) / L, 1), dtype=torch.float32,
+                             device=dev).requires_grad_(True)
+        layer = E.EWS(param, N=2)
+        g = torch.tensor(rng.normal(size=(B, 1 + d + d * d)), dtype=torch.float32, device=dev)
+
+        def step():
+            out = layer(path, clock, readout="terminal")
+            out.backward(g)
+
+        n = B * (L - 1)
+        traffic = n * 4 * (d + 1) * 2
+        what = ("dense24: EWS defaults (van_loan M=20 cayley, chen_expm exact, displacement) on a dense d=24 generator, "
+                "depth 2, B=32, L=896, irregular clock, terminal readout, forward + backward (path, clock and A "
+                "gradients) on the d > 16 dense kernels")
+        steps_per = n
     elif args.config == "scp1":
         # uea_results/scp1/config.json: B=32, 896 samples of SelfRegulationSCP1 lifted to d=17, skew-symmetric A,
         # depth 2, van_loan M=4 euler, chen_expm cayley, displacement_uniform, mean readout
@@ -852,12 +874,13 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--check", action="store_true", help="also check one forward against the C float64 checker")
     ap.add_argument("--chunk", type=int, default=0, help="intervals per chunk (0: the library's default)")
-    ap.add_argument("--config", choices=["c2", "c3", "c1", "c4", "c5", "tok", "ppg", "fl", "scp1"], default="c2",
+    ap.add_argument("--config", choices=["c2", "c3", "c1", "c4", "c5", "tok", "ppg", "fl", "scp1", "dense24"],
+                    default="c2",
                     help="c2 (default, the headline): planes fwd+bwd; c3: dense-generator depth-3 forward; c1, c4, "
                          "c5: one block of the other BASELINE.json configs (real diagonal; LogEWS; bf16 planes); tok: the "
                          "token-cached scan on a formal-language shape; ppg, fl: the banked depth-1 blocks at m=64 "
                          "(PPG Jordan chains; the formal-language token block); scp1: the banked SCP1 block (dense "
-                         "d=17 generator, depth 2)")
+                         "d=17 generator, depth 2); dense24: the layer's defaults on a dense d=24 generator")
     ap.add_argument("--backward", action="store_true", help="c3: time forward + backward (ews_dense_backward)")
     ap.add_argument("--leaf", choices=["series", "van_loan"], default="series",
                     help="leaf of the c3 forward: series (q=24) or Van Loan (M=20, cayley)")
@@ -903,7 +926,7 @@ def main():
         torch.cuda.set_device(0)
         print(json.dumps(bench_c3(args)), flush=True)
         return
-    if args.config in ("ppg", "fl", "scp1"):
+    if args.config in ("ppg", "fl", "scp1", "dense24"):
         import torch
 
         torch.cuda.set_device(0)

@@ -40,6 +40,11 @@ struct WArgs {
   float* dhl;    // series leaf's clock-step cotangents (B, n)
   float* dhm;    // per-interval matrix functions' clock-step cotangents (B, n, 2): flow, Van Loan
   float* dsh;    // shared steps' cotangents (B, 2): flow, Van Loan
+  // power series of the per-interval matrix functions
+  float* apow;   // A^0 .. A^PW (padded, float) and ||A||_1
+  int* mflag;    // per interval: bit 0 the flow, bit 1 the Van Loan pair outside the series radius
+  float* hpart;  // the adjoint's sums H_k = sum gamma_k c^k dOut per workgroup
+  double* hsum;  // H_k summed over the workgroups
 };
 
 // The descriptor takes this path: 16 < d <= 32, depth 1 or 2, leaf series or van_loan.

@@ -44,6 +44,7 @@
 #include <math.h>
 
 #include <algorithm>
+#include <climits>
 #include <type_traits>
 
 #include "ews_hip.h"
@@ -573,34 +574,326 @@ __device__ __forceinline__ float vl_step(const WArgs& a, const float* th, int t,
   return fixed ? 0.0f : dt / (float)a.vm;
 }
 
+// The items of a matrix-function workgroup: modes 0 and 1 every gridDim-th item from blockIdx.x; mode 2 (the
+// matrices outside the series radius) the flagged items of the workgroup's blocks of NT consecutive intervals
+// (blocks blockIdx.x, blockIdx.x + gridDim.x, ...), found by one flag load per thread and a workgroup vote, in
+// increasing order. next_item(.., prev) returns the item after prev (prev = -1: the first), or item_end when none
+// is left; uniform over the workgroup.
+__device__ __forceinline__ long item_end(int mode, long items) { return mode == 2 ? LONG_MAX : items; }
+__device__ long next_item(const WArgs& a, int mode, int need, long prev, long items) {
+  if (mode != 2) return prev < 0 ? (long)blockIdx.x : prev + gridDim.x;
+  __shared__ int s_first;
+  long blk = prev < 0 ? (long)blockIdx.x : prev / NT;
+  long from = prev < 0 ? blk * NT : prev + 1;
+  for (; blk * NT < items; blk += gridDim.x, from = blk * NT) {
+    const long it = blk * NT + threadIdx.x;
+    const bool f = it >= from && it < items && (a.mflag[it] & need);
+    if (threadIdx.x == 0) s_first = NT;
+    __syncthreads();
+    if (f) atomicMin(&s_first, (int)threadIdx.x);
+    __syncthreads();
+    const int first = s_first;
+    __syncthreads();
+    if (first < NT) return blk * NT + first;
+  }
+  return LONG_MAX;
+}
+
 // Step matrices: item = interval (per-interval modes) or sample (shared modes); the flow and the Van Loan pair are
 // each formed when their mode matches the item kind.
-__global__ __launch_bounds__(NT) void k_wmat(WArgs a, int per_interval) {
+// mode: 0 per sample, 1 per interval, 2 per interval, only the matrices flagged outside the series radius
+__global__ __launch_bounds__(NT) void k_wmat(WArgs a, int mode) {
   extern __shared__ __align__(16) double smd[];
   load_A(a.d, a.A, smd + MF_A);
   __syncthreads();
+  const int per_interval = mode != 0;
   const long items = per_interval ? (long)a.B * a.n : a.B;
   // with two grid rows, row 0 forms the flows and row 1 the Van Loan pairs
   const bool do_flow = (a.flow_mode == EWS_FLOW_PER_INTERVAL) == (per_interval != 0) &&
                        (gridDim.y == 1 || blockIdx.y == 0);
   const bool do_vl = a.leaf == EWS_LEAF_VAN_LOAN && (a.vl_mode == EWS_FLOW_PER_INTERVAL) == (per_interval != 0) &&
                      (gridDim.y == 1 || blockIdx.y == 1);
-  for (long it = blockIdx.x; it < items; it += gridDim.x) {
+  const int need = (do_flow ? 1 : 0) | (do_vl ? 2 : 0);
+  for (long it = next_item(a, mode, need, -1, items), it_end = item_end(mode, items); it < it_end;
+       it = next_item(a, mode, need, it, items)) {
     const int b = per_interval ? (int)(it / a.n) : (int)it;
     const int t = per_interval ? (int)(it - (long)b * a.n) : 1;
     const float* th = a.clock + (size_t)b * a.L;
-    if (do_flow) {
+    const int flag = mode == 2 ? a.mflag[it] : 3;
+    if (do_flow && (flag & 1)) {
       bool ident;
       const float h = flow_step(a, th, t, ident);
       matfn_fwd(smd, a.chen, true, (double)h, a.fl + it * MM, nullptr);
     }
-    if (do_vl) {
+    if (do_vl && (flag & 2)) {
       bool fixed;
       const float c = vl_step(a, th, t, fixed);
       matfn_fwd(smd, fixed ? EWS_EXPM_EULER : a.vl_expm, false, fixed ? 0.0 : (double)c, a.vlm + it * 2 * MM,
                 a.vlm + it * 2 * MM + MM);
     }
   }
+}
+
+// ------------------------------------------------------------------------------------------------ series path
+// Per-interval matrix functions as power series in X = c A over a table of powers A^0 .. A^PW formed once per call:
+// out = sum_k gamma_k c^k A^k, entry by entry (each thread keeps its four entries of every power in registers),
+// wherever |c| ||A||_1 is inside the scheme's radius (series remainder below about 1e-11); a matrix outside it is
+// flagged and formed by k_wmat (mode 2). The adjoint accumulates H_k = sum_items gamma_k c^k dOut and turns it
+// into dA once: dA = sum_k sum_{i<k} (A^T)^i H_k (A^T)^{k-1-i}; the step's cotangent is <dOut, d out / dc>.
+// gamma_k (kind 0 the flow scheme(-X); kind 1 the Van Loan P, kind 2 its V):
+//   exact   F, P: (-1)^k / k!          V: (-1)^k / (k+1)!
+//   cayley  F, P: 1, then 2 (-1/2)^k   V: (-1/2)^k                          ((I + X/2)^{-1})
+//   euler   F: 1, -1                   P = V: (-1)^k                         ((I + X)^{-1})
+//   pade    F, P: 1, then -b_{k-1}     V: b_k, b_0 = 1, b_1 = -1/2, b_k = -(b_{k-1}/2 + b_{k-2}/12)
+constexpr int PW = 18;
+
+__device__ void series_gamma(int scheme, int kind, float* g) {
+  double b[PW + 1];
+  b[0] = 1.0;
+  for (int k = 1; k <= PW; ++k) {
+    if (scheme == EWS_EXPM_EXACT) b[k] = -b[k - 1] / (double)(kind == 2 ? k + 1 : k);
+    else if (scheme == EWS_EXPM_CAYLEY) b[k] = -0.5 * b[k - 1];
+    else if (scheme == EWS_EXPM_EULER) b[k] = -b[k - 1];
+    else b[k] = -(0.5 * b[k - 1] + (k >= 2 ? b[k - 2] / 12.0 : 0.0));
+  }
+  for (int k = 0; k <= PW; ++k) g[k] = 0.0f;
+  if (scheme == EWS_EXPM_EULER && kind == 0) {
+    g[0] = 1.0f;
+    g[1] = -1.0f;
+  } else if (kind == 2 || scheme == EWS_EXPM_EXACT || (scheme == EWS_EXPM_EULER && kind == 1)) {
+    for (int k = 0; k <= PW; ++k) g[k] = (float)b[k];
+  } else if (scheme == EWS_EXPM_CAYLEY) {  // F, P = 2V - I
+    g[0] = 1.0f;
+    for (int k = 1; k <= PW; ++k) g[k] = (float)(2.0 * b[k]);
+  } else {  // pade F, P = I - V X
+    g[0] = 1.0f;
+    for (int k = 1; k <= PW; ++k) g[k] = (float)(-b[k - 1]);
+  }
+}
+__device__ __forceinline__ float series_radius(int scheme, int kind) {
+  if (scheme == EWS_EXPM_EXACT) return 1.0f;
+  if (scheme == EWS_EXPM_CAYLEY) return 0.5f;
+  if (scheme == EWS_EXPM_EULER) return kind == 0 ? 3.0e38f : 0.25f;
+  return 0.7f;
+}
+
+// the table: A^k (k = 0 .. PW) in float64, stored float, and ||A||_1 at apow[(PW + 1) MM]
+__global__ __launch_bounds__(NT) void k_wpowers(WArgs a) {
+  __shared__ __align__(16) double sd[3 * S32 + 64];
+  double* A = sd;
+  double* T = sd + S32;
+  double* Tn = sd + 2 * S32;
+  load_A(a.d, a.A, A);
+  set_ident32(T, 1.0);
+  __syncthreads();
+  const int i = trow<32>(), j0 = tcol<32>();
+  gst4(a.apow, float4{i == j0 ? 1.0f : 0.0f, i == j0 + 1 ? 1.0f : 0.0f, i == j0 + 2 ? 1.0f : 0.0f,
+                      i == j0 + 3 ? 1.0f : 0.0f});
+  for (int k = 1; k <= PW; ++k) {
+    double acc[4];
+    mm<32, false, false>(T, A, acc);
+    st<32>(Tn, acc);
+    gst4(a.apow + (size_t)k * MM, float4{(float)acc[0], (float)acc[1], (float)acc[2], (float)acc[3]});
+    __syncthreads();
+    double* tmp = T;
+    T = Tn;
+    Tn = tmp;
+  }
+  const double nrm = norm1<32>(A, sd + 3 * S32);
+  if (threadIdx.x == 0) a.apow[(size_t)(PW + 1) * MM] = (float)nrm;
+}
+
+// the thread's four entries of every power
+__device__ __forceinline__ void load_powers(const WArgs& a, float4* T) {
+#pragma unroll
+  for (int k = 0; k <= PW; ++k) T[k] = gld4(a.apow + (size_t)k * MM);
+}
+__device__ __forceinline__ float4 series_eval(const float4* T, const float* g, float c) {
+  float4 r = float4{0.0f, 0.0f, 0.0f, 0.0f};
+  float ck = 1.0f;
+#pragma unroll
+  for (int k = 0; k <= PW; ++k) {
+    const float w = g[k] * ck;
+    r.x = fmaf(w, T[k].x, r.x);
+    r.y = fmaf(w, T[k].y, r.y);
+    r.z = fmaf(w, T[k].z, r.z);
+    r.w = fmaf(w, T[k].w, r.w);
+    ck *= c;
+  }
+  return r;
+}
+
+// per-interval flows and Van Loan pairs on the series path; flags the others
+__global__ __launch_bounds__(NT) void k_wmat_series(WArgs a) {
+  __shared__ float s_g[3][PW + 1];
+  if (threadIdx.x == 0) {
+    series_gamma(a.chen, 0, s_g[0]);
+    if (a.leaf == EWS_LEAF_VAN_LOAN) {
+      series_gamma(a.vl_expm, 1, s_g[1]);
+      series_gamma(a.vl_expm, 2, s_g[2]);
+    }
+  }
+  __syncthreads();
+  float4 T[PW + 1];
+  load_powers(a, T);
+  const float nrm = a.apow[(size_t)(PW + 1) * MM];
+  const bool do_flow = a.flow_mode == EWS_FLOW_PER_INTERVAL;
+  const bool do_vl = a.leaf == EWS_LEAF_VAN_LOAN && a.vl_mode == EWS_FLOW_PER_INTERVAL;
+  const float rf = series_radius(a.chen, 0), rv = series_radius(a.vl_expm, 1);
+  const long items = (long)a.B * a.n;
+  for (long it = blockIdx.x; it < items; it += gridDim.x) {
+    const int b = (int)(it / a.n), t = (int)(it - (long)b * a.n);
+    const float h = a.clock[(size_t)b * a.L + t + 1] - a.clock[(size_t)b * a.L + t];
+    int flag = 0;
+    if (do_flow) {
+      if (fabsf(h) * nrm <= rf) gst4(a.fl + it * MM, series_eval(T, s_g[0], h));
+      else flag |= 1;
+    }
+    if (do_vl) {
+      const float c = h / (float)a.vm;
+      if (fabsf(c) * nrm <= rv) {
+        gst4(a.vlm + it * 2 * MM, series_eval(T, s_g[1], c));
+        gst4(a.vlm + it * 2 * MM + MM, series_eval(T, s_g[2], c));
+      } else {
+        flag |= 2;
+      }
+    }
+    if (threadIdx.x == 0) a.mflag[it] = flag;
+  }
+}
+
+// sum over the workgroup of two values (every thread returns both); red: 2 NT / 64 floats
+__device__ __forceinline__ float2 block_sum2(float u, float v, float* red) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) {
+    u += __shfl_xor(u, o, 64);
+    v += __shfl_xor(v, o, 64);
+  }
+  __syncthreads();
+  if ((threadIdx.x & 63) == 0) {
+    red[threadIdx.x >> 6] = u;
+    red[NT / 64 + (threadIdx.x >> 6)] = v;
+  }
+  __syncthreads();
+  float su = 0.0f, sv = 0.0f;
+#pragma unroll
+  for (int w = 0; w < NT / 64; ++w) {
+    su += red[w];
+    sv += red[NT / 64 + w];
+  }
+  return float2{su, sv};
+}
+
+// Adjoint of the series path: H_k partials of the workgroup (hpart) and the steps' cotangents (dhm) of every
+// per-interval matrix not flagged; the flagged ones are k_wmat_bwd's (mode 2)
+__global__ __launch_bounds__(NT) void k_wmat_bwd_series(WArgs a) {
+  __shared__ float s_g[3][PW + 1];
+  __shared__ float red[2 * NT / 64];
+  if (threadIdx.x == 0) {
+    series_gamma(a.chen, 0, s_g[0]);
+    if (a.leaf == EWS_LEAF_VAN_LOAN) {
+      series_gamma(a.vl_expm, 1, s_g[1]);
+      series_gamma(a.vl_expm, 2, s_g[2]);
+    }
+  }
+  __syncthreads();
+  float4 T[PW + 1], H[PW + 1];
+  load_powers(a, T);
+#pragma unroll
+  for (int k = 0; k <= PW; ++k) H[k] = float4{0.0f, 0.0f, 0.0f, 0.0f};
+  const bool do_flow = a.flow_mode == EWS_FLOW_PER_INTERVAL;
+  const bool do_vl = a.leaf == EWS_LEAF_VAN_LOAN && a.vl_mode == EWS_FLOW_PER_INTERVAL;
+  const long items = (long)a.B * a.n;
+  for (long it = blockIdx.x; it < items; it += gridDim.x) {
+    const int b = (int)(it / a.n), t = (int)(it - (long)b * a.n);
+    const float h = a.clock[(size_t)b * a.L + t + 1] - a.clock[(size_t)b * a.L + t];
+    const int flag = a.mflag[it];
+    const bool sf = do_flow && !(flag & 1), sv = do_vl && !(flag & 2);
+    float df = 0.0f, dv = 0.0f;
+    if (sf) {  // H_k += gamma_k h^k G; dh = <G, sum_k k gamma_k h^(k-1) A^k>
+      const float4 G = gld4(a.dfl + it * MM);
+      float ck = 1.0f, dk = 0.0f;  // h^k, k h^(k-1)
+#pragma unroll
+      for (int k = 0; k <= PW; ++k) {
+        const float w = s_g[0][k] * ck, wd = s_g[0][k] * dk;
+        H[k].x = fmaf(w, G.x, H[k].x);
+        H[k].y = fmaf(w, G.y, H[k].y);
+        H[k].z = fmaf(w, G.z, H[k].z);
+        H[k].w = fmaf(w, G.w, H[k].w);
+        // the weight first: with large cotangents, <G, A^k> alone can overflow where the weight is zero or tiny
+        df += (wd * G.x) * T[k].x + (wd * G.y) * T[k].y + (wd * G.z) * T[k].z + (wd * G.w) * T[k].w;
+        dk = fmaf(dk, h, ck);
+        ck *= h;
+      }
+    }
+    if (sv) {
+      const float c = h / (float)a.vm;
+      const float4 GP = gld4(a.dvlm + it * 2 * MM), GV = gld4(a.dvlm + it * 2 * MM + MM);
+      float ck = 1.0f, dk = 0.0f;
+#pragma unroll
+      for (int k = 0; k <= PW; ++k) {
+        const float wp = s_g[1][k], wv = s_g[2][k];
+        const float4 G = float4{wp * GP.x + wv * GV.x, wp * GP.y + wv * GV.y, wp * GP.z + wv * GV.z,
+                                wp * GP.w + wv * GV.w};
+        H[k].x = fmaf(ck, G.x, H[k].x);
+        H[k].y = fmaf(ck, G.y, H[k].y);
+        H[k].z = fmaf(ck, G.z, H[k].z);
+        H[k].w = fmaf(ck, G.w, H[k].w);
+        dv += (dk * G.x) * T[k].x + (dk * G.y) * T[k].y + (dk * G.z) * T[k].z + (dk * G.w) * T[k].w;
+        dk = fmaf(dk, c, ck);
+        ck *= c;
+      }
+    }
+    if (sf || sv) {  // uniform over the workgroup
+      const float2 s2 = block_sum2(df, dv, red);
+      if (threadIdx.x == 0) {
+        if (sf) a.dhm[2 * it] = s2.x;
+        if (sv) a.dhm[2 * it + 1] = s2.y / (float)a.vm;  // c = h / M
+      }
+    }
+  }
+#pragma unroll
+  for (int k = 0; k <= PW; ++k) gst4(a.hpart + ((size_t)blockIdx.x * (PW + 1) + k) * MM, H[k]);
+}
+
+// H_k summed over the workgroups' partials (float64, in order): a workgroup per (k, quarter of the entries)
+__global__ __launch_bounds__(NT) void k_whsum(WArgs a, int nparts) {
+  const int k = blockIdx.x, e = blockIdx.y * NT + threadIdx.x;
+  double s = 0.0;
+  for (int g = 0; g < nparts; ++g) s += (double)a.hpart[((size_t)g * (PW + 1) + k) * MM + e];
+  a.hsum[(size_t)k * MM + e] = s;
+}
+
+// dA of the series path (float64): R_{PW-1} = H_PW, R_i = H_{i+1} + R_{i+1} A^T, U_i = R_i + A^T U_{i+1},
+// dA = U_0; into apart slot `slot`
+__global__ __launch_bounds__(NT) void k_wseries_dA(WArgs a, long slot) {
+  __shared__ __align__(16) double sd[3 * S32];
+  double* A = sd;
+  double* R = sd + S32;
+  double* U = sd + 2 * S32;
+  load_A(a.d, a.A, A);
+  const int i = trow<32>(), j0 = tcol<32>();
+  double z[4] = {0.0, 0.0, 0.0, 0.0};
+  st<32>(R, z);
+  st<32>(U, z);
+  __syncthreads();
+  for (int ii = PW - 1; ii >= 0; --ii) {
+    double r[4], u[4];
+    mm<32, false, true>(R, A, r);  // R A^T
+    mm<32, true, false>(A, U, u);  // A^T U
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      r[c] += a.hsum[(size_t)(ii + 1) * MM + i * DP + j0 + c];
+      u[c] += r[c];
+    }
+    __syncthreads();
+    st<32>(U, u);
+    st<32>(R, r);
+    __syncthreads();
+  }
+  double u[4];
+  ld<32>(U, u);
+  gst4(a.apart + slot * MM, float4{(float)u[0], (float)u[1], (float)u[2], (float)u[3]});
 }
 
 // The thread's four entries of the flow of interval t of sample b (registers), and their store into F and, transposed,
@@ -1350,12 +1643,13 @@ __global__ __launch_bounds__(NT) void k_wleaf_bwd(WArgs a) {
 // cotangents of the per-interval modes, dh into dhm (flow, Van Loan); else one item per sample, the partials of the
 // shared flow (per chunk) and pair (per leaf slice) summed in order, the shared steps' gradients into dsh[b][0..1].
 // dA: workgroup partials at apart + slot0 (grid row by row).
-__global__ __launch_bounds__(NT) void k_wmat_bwd(WArgs a, int per_interval, long slot0) {
+__global__ __launch_bounds__(NT) void k_wmat_bwd(WArgs a, int mode, long slot0) {
   extern __shared__ __align__(16) float sm[];
   float* A = sm + MF_A;
   load_A(a.d, a.A, A);
   __syncthreads();
   float dA[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+  const int per_interval = mode != 0;
   const long items = per_interval ? (long)a.B * a.n : a.B;
   // with two grid rows, row 0 takes the flows and row 1 the Van Loan pairs
   const bool do_flow = (a.flow_mode == EWS_FLOW_PER_INTERVAL) == (per_interval != 0) &&
@@ -1364,12 +1658,16 @@ __global__ __launch_bounds__(NT) void k_wmat_bwd(WArgs a, int per_interval, long
                      (gridDim.y == 1 || blockIdx.y == 1);
   float* G0 = sm + MF_T;
   float* G1 = sm + MF_U;
-  for (long it = blockIdx.x; it < items; it += gridDim.x) {
+  const int need = (do_flow ? 1 : 0) | (do_vl ? 2 : 0);
+  for (long it = next_item(a, mode, need, -1, items), it_end = item_end(mode, items); it < it_end;
+       it = next_item(a, mode, need, it, items)) {
     const int b = per_interval ? (int)(it / a.n) : (int)it;
     const int t = per_interval ? (int)(it - (long)b * a.n) : 1;
     const float* th = a.clock + (size_t)b * a.L;
     float dh_f = 0.0f, dh_v = 0.0f;
-    if (do_flow) {
+    const int flag = mode == 2 ? a.mflag[it] : 3;
+    const bool run_f = do_flow && (flag & 1), run_v = do_vl && (flag & 2);
+    if (run_f) {
       bool ident;
       const float h = flow_step(a, th, t, ident);
       float g[4];
@@ -1394,7 +1692,7 @@ __global__ __launch_bounds__(NT) void k_wmat_bwd(WArgs a, int per_interval, long
       for (int k = 0; k < 4; ++k) dA[k] = fmaf(h, xb[k], dA[k]);
       dh_f = block_sum(dot, sm + MF_RED);
     }
-    if (do_vl) {
+    if (run_v) {
       bool fixed;
       const float cst = vl_step(a, th, t, fixed);
       if (!fixed) {
@@ -1428,8 +1726,8 @@ __global__ __launch_bounds__(NT) void k_wmat_bwd(WArgs a, int per_interval, long
     }
     if (threadIdx.x == 0) {  // [flow, Van Loan] per interval or per sample
       float* dst = per_interval ? a.dhm + 2 * it : a.dsh + 2 * b;
-      if (do_flow) dst[0] = dh_f;
-      if (do_vl) dst[1] = dh_v;
+      if (run_f) dst[0] = dh_f;
+      if (run_v) dst[1] = dh_v;
     }
     __syncthreads();
   }
@@ -1502,7 +1800,8 @@ constexpr int kLeafSlice = 16;  // intervals per workgroup of the leaf adjoint
 struct WPlan {
   int B, L, n, d, N, T, C, W, TL, NSL, CP;
   bool fl_int, vl, vl_int, exact_int, exact_smp, mats_int, mats_smp;
-  long g_int, g_smp;   // workgroups of the matrix-function adjoints (per grid row)
+  long g_int, g_smp;   // workgroups of the matrix-function adjoints (per grid row; per interval: the flagged ones)
+  long g_ser;          // workgroups of the series path's adjoint
   int gy_int, gy_smp;  // grid rows: 2 when both the flows and the Van Loan pairs are of that kind
 };
 
@@ -1538,7 +1837,8 @@ int plan(const ews_dense_desc* s, WPlan& p) {
   p.mats_smp = !p.fl_int || (vl && !p.vl_int);
   p.exact_int = (p.fl_int && s->chen_expm == EWS_EXPM_EXACT) || (p.vl_int && s->vl_expm == EWS_EXPM_EXACT);
   p.exact_smp = (!p.fl_int && s->chen_expm == EWS_EXPM_EXACT) || (vl && !p.vl_int && s->vl_expm == EWS_EXPM_EXACT);
-  p.g_int = p.mats_int ? std::min<long>((long)p.B * p.n, 2048) : 0;
+  p.g_int = p.mats_int ? std::min<long>((long)p.B * p.n, 256) : 0;
+  p.g_ser = p.mats_int ? std::min<long>((long)p.B * p.n, 256) : 0;
   p.g_smp = p.mats_smp ? p.B : 0;
   p.gy_int = p.fl_int && p.vl_int ? 2 : 1;
   p.gy_smp = !p.fl_int && vl && !p.vl_int ? 2 : 1;
@@ -1546,8 +1846,8 @@ int plan(const ews_dense_desc* s, WPlan& p) {
 }
 
 struct WLay {
-  size_t fl, vlm, loc, summ, sfl, car, rows, amax, outs, grow, mu, lend, dloc, dfl, cpart, dvlm, apart, dv, dhl,
-      dhm, dsh, total;
+  size_t fl, vlm, loc, summ, sfl, car, rows, amax, apow, mflag, outs, grow, mu, lend, dloc, dfl, cpart, dvlm, apart,
+      dv, dhl, dhm, dsh, hpart, hsum, total;
 };
 
 WLay layout(const ews_dense_desc* s, const WPlan& p, bool bwd) {
@@ -1567,6 +1867,8 @@ WLay layout(const ews_dense_desc* s, const WPlan& p, bool bwd) {
   const bool mm_ro = s->readout == EWS_READOUT_MEAN || s->readout == EWS_READOUT_MAX;
   take(w.rows, (bwd || mm_ro) ? BN * RW * 4 : 0);
   take(w.amax, s->readout == EWS_READOUT_MAX ? (size_t)p.B * p.W * 4 : 0);
+  take(w.apow, p.mats_int ? ((size_t)(PW + 1) * MM + 64) * 4 : 0);
+  take(w.mflag, p.mats_int ? BN * 4 : 0);
   if (bwd) {
     take(w.outs, s->readout == EWS_READOUT_MAX ? (size_t)p.B * p.W * 4 : 0);
     take(w.grow, BN * RW * 4);
@@ -1576,11 +1878,13 @@ WLay layout(const ews_dense_desc* s, const WPlan& p, bool bwd) {
     take(w.dfl, p.fl_int ? BN * MM * 4 : 0);
     take(w.cpart, (size_t)p.B * p.CP * 3 * MM * 4);
     take(w.dvlm, p.vl_int ? BN * 2 * MM * 4 : 0);
-    take(w.apart, ((size_t)p.B * p.NSL + p.g_int * p.gy_int + p.g_smp * p.gy_smp) * MM * 4);
+    take(w.apart, ((size_t)p.B * p.NSL + p.g_int * p.gy_int + p.g_smp * p.gy_smp + 1) * MM * 4);
     take(w.dv, BN * DP * 4);
     take(w.dhl, BN * 4);
     take(w.dhm, BN * 2 * 4);
     take(w.dsh, (size_t)p.B * 2 * 4);
+    take(w.hpart, (size_t)p.g_ser * (PW + 1) * MM * 4);
+    take(w.hsum, p.mats_int ? (size_t)(PW + 1) * MM * 8 : 0);
   }
   w.total = off;
   return w;
@@ -1604,10 +1908,13 @@ WArgs make_args(const ews_dense_desc* s, const WPlan& p, const float* path, cons
   const bool mm_ro = s->readout == EWS_READOUT_MEAN || s->readout == EWS_READOUT_MAX;
   a.rows = (bwd || mm_ro) ? f(w.rows) : nullptr;
   a.amax = s->readout == EWS_READOUT_MAX ? (int*)(ws + w.amax) : nullptr;
+  a.apow = p.mats_int ? f(w.apow) : nullptr;
+  a.mflag = p.mats_int ? (int*)(ws + w.mflag) : nullptr;
   if (bwd) {
     a.grow = f(w.grow); a.mu = f(w.mu); a.lend = f(w.lend); a.dloc = f(w.dloc);
     a.dfl = p.fl_int ? f(w.dfl) : nullptr; a.cpart = f(w.cpart); a.dvlm = p.vl_int ? f(w.dvlm) : nullptr;
     a.apart = f(w.apart); a.dv = f(w.dv); a.dhl = f(w.dhl); a.dhm = f(w.dhm); a.dsh = f(w.dsh);
+    a.hpart = f(w.hpart); a.hsum = p.mats_int ? (double*)(ws + w.hsum) : nullptr;
   }
   return a;
 }
@@ -1626,9 +1933,10 @@ int set_lds(const void* fn, size_t bytes) {
 int run_forward(const WPlan& p, const WArgs& a, hipStream_t st) {
   const size_t lds = MF_ENT_FWD * sizeof(double);
   if (set_lds(reinterpret_cast<const void*>(&k_wmat), lds) != EWS_OK) return EWS_ERR_LAUNCH;
-  if (p.mats_int) {
-    hipLaunchKernelGGL(k_wmat, dim3((unsigned)std::min<long>((long)p.B * p.n, 4096), p.gy_int), dim3(NT), lds, st, a,
-                       1);
+  if (p.mats_int) {  // the powers table, the series path, then the matrices outside its radius
+    hipLaunchKernelGGL(k_wpowers, dim3(1), dim3(NT), 0, st, a);
+    hipLaunchKernelGGL(k_wmat_series, dim3((unsigned)std::min<long>((long)p.B * p.n, 1024)), dim3(NT), 0, st, a);
+    hipLaunchKernelGGL(k_wmat, dim3((unsigned)p.g_int, p.gy_int), dim3(NT), lds, st, a, 2);
     WIDE_CHECK();
   }
   if (p.mats_smp) {
@@ -1714,7 +2022,11 @@ int backward(const ews_dense_desc* s, const float* path, const float* clock, con
     const size_t lds = (p.exact_int ? MF_ENT_BWD_EXACT : MF_ENT_BWD) * 4;
     if (set_lds(reinterpret_cast<const void*>(&k_wmat_bwd), MF_ENT_BWD_EXACT * 4) != EWS_OK)
       return EWS_ERR_LAUNCH;
-    hipLaunchKernelGGL(k_wmat_bwd, dim3((unsigned)p.g_int, p.gy_int), dim3(NT), lds, st, a, 1, base);
+    hipLaunchKernelGGL(k_wmat_bwd_series, dim3((unsigned)p.g_ser), dim3(NT), 0, st, a);
+    hipLaunchKernelGGL(k_wmat_bwd, dim3((unsigned)p.g_int, p.gy_int), dim3(NT), lds, st, a, 2, base);
+    hipLaunchKernelGGL(k_whsum, dim3(PW + 1, MM / NT), dim3(NT), 0, st, a, (int)p.g_ser);
+    hipLaunchKernelGGL(k_wseries_dA, dim3(1), dim3(NT), 0, st, a,
+                       base + p.g_int * p.gy_int + p.g_smp * p.gy_smp);
     WIDE_CHECK();
   }
   if (p.mats_smp) {
@@ -1725,8 +2037,8 @@ int backward(const ews_dense_desc* s, const float* path, const float* clock, con
                        base + p.g_int * p.gy_int);
     WIDE_CHECK();
   }
-  hipLaunchKernelGGL(k_wfinal_A, dim3(MM / 16), dim3(NT), 0, st, a, base + p.g_int * p.gy_int + p.g_smp * p.gy_smp,
-                     grad_A);
+  hipLaunchKernelGGL(k_wfinal_A, dim3(MM / 16), dim3(NT), 0, st, a,
+                     base + p.g_int * p.gy_int + p.g_smp * p.gy_smp + (p.mats_int ? 1 : 0), grad_A);
   hipLaunchKernelGGL(k_wknots, dim3((p.L + NT - 1) / NT, p.B), dim3(NT), 0, st, a, grad_path, grad_clock);
   WIDE_CHECK();
   return EWS_OK;

@@ -186,3 +186,21 @@ def test_wide_logews(readout):
     eg = relerr(pg.grad, rg)
     print(f"logews {readout}: path grad {eg:.2e}")
     assert eg < 1e-4
+
+
+@pytest.mark.parametrize("scheme", ["exact", "cayley", "pade"])
+def test_wide_series_and_fallback_in_one_call(scheme):
+    """Per-interval steps on both sides of the series radius in one call (|h| ||A||_1 from about 0.3 to 2.5): the
+    matrices inside it come from the powers table, the others from the scaled / inverted forms (k_wmat mode 2), and
+    the adjoint splits the same way."""
+    rng = np.random.default_rng(17)
+    d, L = 20, 50
+    path = torch.tensor(np.cumsum(rng.normal(size=(2, L, d)) * 0.3, 1))
+    clock = torch.tensor(np.cumsum(rng.uniform(0.05, 0.45, size=(2, L)), 1))
+    G = rng.normal(size=(d, d))
+    A = torch.tensor((G - G.T) * (0.5 / np.sqrt(d)) + np.eye(d))
+    out, ref, gg, rg = _run(path, clock, A, 2, "prefix", "displacement",
+                            dict(van_loan_expm=scheme, chen_expm=scheme, M=1), chunk=16)
+    tag = f"mixed radius {scheme}"
+    _check_levels(out, ref, d, 2, 1e-5, tag)
+    _check_grads(gg, rg, tag)
