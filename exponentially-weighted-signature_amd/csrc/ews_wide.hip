@@ -920,13 +920,11 @@ __device__ __forceinline__ void commit_mat(float4 v, float* F, float* Ft) {
 
 // ------------------------------------------------------------------------------------------------ local terms
 // LDS of the leaf kernels (floats): A, P, V (32 x 36 each), vectors, the knot / letter table and its cotangents.
+// The four tables hold `rows` rows of 32 (the knots M or the letters q + 1), in dynamic LDS sized to them:
+// knots Delta_m (or letters b_p); Y_m (or u_p); R_m, Pre_m (or w_p, A b_{p-1}); cotangents.
 constexpr int LF_A = 0, LF_P = S32, LF_V = 2 * S32, LF_S2 = 3 * S32, LF_VEC = 4 * S32;  // vectors: 8 x 32
-constexpr int LF_TAB = LF_VEC + 8 * 32;        // up to 65 rows of 32: knots Delta_m (or letters b_p)
-constexpr int LF_TAB2 = LF_TAB + 65 * 32;      // Y_m (or u_p)
-constexpr int LF_TAB3 = LF_TAB2 + 65 * 32;     // R_m, Pre_m (or w_p, A b_{p-1})
-constexpr int LF_TAB4 = LF_TAB3 + 65 * 32;     // cotangents
-constexpr int LF_RED = LF_TAB4 + 65 * 32;
-constexpr int LF_FLOATS = LF_RED + 64;
+constexpr int LF_TAB = LF_VEC + 8 * 32;
+__host__ __device__ constexpr int lf_floats(int rows, int ntab) { return LF_TAB + ntab * rows * 32 + 64; }
 
 __device__ __forceinline__ float inv_f(int n) { return 1.0f / (float)n; }
 __device__ __forceinline__ float c2coef(int p, int r) { return 1.0f / ((float)(p + r + 2) * (float)(r + 1)); }
@@ -965,7 +963,7 @@ __device__ void leaf_fwd(const WArgs& a, float* sm, int b, int t, float* s1v, fl
   float* A = sm + LF_A;
   float* vec = sm + LF_VEC;
   float* T1 = sm + LF_TAB;
-  float* T2 = sm + LF_TAB2;
+  float* T2 = T1 + (a.leaf == EWS_LEAF_VAN_LOAN ? a.vm : a.q + 1) * 32;
   const int tid = threadIdx.x, i = tid >> 3, j0 = (tid & 7) * 4;
   const float* x = a.path + ((size_t)b * a.L + t) * a.d;
   const float* th = a.clock + (size_t)b * a.L;
@@ -1040,7 +1038,7 @@ __device__ void leaf_fwd(const WArgs& a, float* sm, int b, int t, float* s1v, fl
 
 template <int N>
 __global__ __launch_bounds__(NT) void k_wleaf(WArgs a) {
-  __shared__ __align__(16) float sm[LF_FLOATS];
+  extern __shared__ __align__(16) float sm[];  // lf_floats(rows, 2)
   float* s1v = sm + LF_VEC + 32;
   load_A(a.d, a.A, sm + LF_A);
   __syncthreads();
@@ -1451,16 +1449,17 @@ __global__ __launch_bounds__(NT) void k_wadj_carry(WArgs a) {
 // modes).
 template <int N>
 __global__ __launch_bounds__(NT) void k_wleaf_bwd(WArgs a) {
-  __shared__ __align__(16) float sm[LF_FLOATS];
+  extern __shared__ __align__(16) float sm[];  // lf_floats(rows, 4)
   float* A = sm + LF_A;
   float* S2b = sm + LF_S2;  // ds2
   float* vec = sm + LF_VEC;
   float* ds1 = vec;
   float* wv = vec + 32;
+  const int rows = a.leaf == EWS_LEAF_VAN_LOAN ? a.vm : a.q + 1;
   float* T1 = sm + LF_TAB;
-  float* T2 = sm + LF_TAB2;
-  float* T3 = sm + LF_TAB3;
-  float* T4 = sm + LF_TAB4;
+  float* T2 = T1 + rows * 32;
+  float* T3 = T2 + rows * 32;
+  float* T4 = T3 + rows * 32;
   const int sl = blockIdx.x, b = blockIdx.y;
   const int t0 = sl * a.TL, t1 = min(a.n, t0 + a.TL);
   const int tid = threadIdx.x, i = tid >> 3, j0 = (tid & 7) * 4;
@@ -1798,7 +1797,7 @@ size_t al256(size_t x) { return (x + 255) & ~(size_t)255; }
 constexpr int kLeafSlice = 16;  // intervals per workgroup of the leaf adjoint
 
 struct WPlan {
-  int B, L, n, d, N, T, C, W, TL, NSL, CP;
+  int B, L, n, d, N, T, C, W, TL, NSL, CP, rows;  // rows: knots M or letters q + 1 of the leaf tables
   bool fl_int, vl, vl_int, exact_int, exact_smp, mats_int, mats_smp;
   long g_int, g_smp;   // workgroups of the matrix-function adjoints (per grid row; per interval: the flagged ones)
   long g_ser;          // workgroups of the series path's adjoint
@@ -1832,6 +1831,7 @@ int plan(const ews_dense_desc* s, WPlan& p) {
   p.W = p.d + (p.N >= 2 ? p.d * p.d : 0) + (s->level0 ? 1 : 0);
   p.fl_int = s->flow_mode == EWS_FLOW_PER_INTERVAL;
   p.vl = vl;
+  p.rows = vl ? s->vl_steps : s->series_q + 1;
   p.vl_int = vl && s->vl_mode == EWS_FLOW_PER_INTERVAL;
   p.mats_int = p.fl_int || p.vl_int;
   p.mats_smp = !p.fl_int || (vl && !p.vl_int);
@@ -1944,13 +1944,14 @@ int run_forward(const WPlan& p, const WArgs& a, hipStream_t st) {
     WIDE_CHECK();
   }
   const dim3 gl((unsigned)std::min<long>((long)p.B * p.n, 4096)), gc(p.C, p.B);
+  const size_t lds_leaf = (size_t)lf_floats(p.rows, 2) * 4;
   if (p.N == 1) {
-    hipLaunchKernelGGL(k_wleaf<1>, gl, dim3(NT), 0, st, a);
+    hipLaunchKernelGGL(k_wleaf<1>, gl, dim3(NT), lds_leaf, st, a);
     hipLaunchKernelGGL((k_wscan<1, SCAN_SUMMARY>), gc, dim3(NT), 0, st, a);
     hipLaunchKernelGGL(k_wcarry<1>, dim3(p.B), dim3(NT), 0, st, a);
     hipLaunchKernelGGL((k_wscan<1, SCAN_ROWS>), gc, dim3(NT), 0, st, a);
   } else {
-    hipLaunchKernelGGL(k_wleaf<2>, gl, dim3(NT), 0, st, a);
+    hipLaunchKernelGGL(k_wleaf<2>, gl, dim3(NT), lds_leaf, st, a);
     hipLaunchKernelGGL((k_wscan<2, SCAN_SUMMARY>), gc, dim3(NT), 0, st, a);
     hipLaunchKernelGGL(k_wcarry<2>, dim3(p.B), dim3(NT), 0, st, a);
     hipLaunchKernelGGL((k_wscan<2, SCAN_ROWS>), gc, dim3(NT), 0, st, a);
@@ -2005,16 +2006,17 @@ int backward(const ews_dense_desc* s, const float* path, const float* clock, con
                      dim3(NT), 0, st, a, grad_out);
   WIDE_CHECK();
   const dim3 gc(p.C, p.B);
+  const size_t lds_lb = (size_t)lf_floats(p.rows, 4) * 4;
   if (p.N == 1) {
     hipLaunchKernelGGL((k_wadj<1, ADJ_LOCAL>), gc, dim3(NT), 0, st, a);
     hipLaunchKernelGGL(k_wadj_carry<1>, dim3(p.B), dim3(NT), 0, st, a);
     hipLaunchKernelGGL((k_wadj<1, ADJ_FULL>), gc, dim3(NT), 0, st, a);
-    hipLaunchKernelGGL(k_wleaf_bwd<1>, dim3(p.NSL, p.B), dim3(NT), 0, st, a);
+    hipLaunchKernelGGL(k_wleaf_bwd<1>, dim3(p.NSL, p.B), dim3(NT), lds_lb, st, a);
   } else {
     hipLaunchKernelGGL((k_wadj<2, ADJ_LOCAL>), gc, dim3(NT), 0, st, a);
     hipLaunchKernelGGL(k_wadj_carry<2>, dim3(p.B), dim3(NT), 0, st, a);
     hipLaunchKernelGGL((k_wadj<2, ADJ_FULL>), gc, dim3(NT), 0, st, a);
-    hipLaunchKernelGGL(k_wleaf_bwd<2>, dim3(p.NSL, p.B), dim3(NT), 0, st, a);
+    hipLaunchKernelGGL(k_wleaf_bwd<2>, dim3(p.NSL, p.B), dim3(NT), lds_lb, st, a);
   }
   WIDE_CHECK();
   const long base = (long)p.B * p.NSL;
