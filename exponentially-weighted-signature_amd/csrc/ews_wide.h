@@ -41,10 +41,13 @@ struct WArgs {
   float* dhm;    // per-interval matrix functions' clock-step cotangents (B, n, 2): flow, Van Loan
   float* dsh;    // shared steps' cotangents (B, 2): flow, Van Loan
   // power series of the per-interval matrix functions
-  float* apow;   // A^0 .. A^PW (padded, float) and ||A||_1
-  int* mflag;    // per interval: bit 0 the flow, bit 1 the Van Loan pair outside the series radius
+  float* apow;   // A^0 .. A^PW (padded, float), ||A||_1 and the Van Loan knots' coefficients phi[m][k]
+  int* mflag;    // per interval: bit 0 the flow, bit 1 the Van Loan pair outside the series radius, bit 2 the
+                 // Van Loan knots by the M-step chain (M |c| ||A||_1 outside the radius)
   float* hpart;  // the adjoint's sums H_k = sum gamma_k c^k dOut per workgroup
   double* hsum;  // H_k summed over the workgroups
+  float* ubuf;   // series-path knots: u_k = A^k w per interval (B, n, PW + 1, 32)
+  float* ebuf;   // their cotangents e_k = sum_m phi[m][k] dDelta_m (B, n, PW + 1, 32)
 };
 
 // The descriptor takes this path: 16 < d <= 32, depth 1 or 2, leaf series or van_loan.

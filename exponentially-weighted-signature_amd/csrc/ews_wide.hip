@@ -677,7 +677,15 @@ __device__ __forceinline__ float series_radius(int scheme, int kind) {
   return 0.7f;
 }
 
-// the table: A^k (k = 0 .. PW) in float64, stored float, and ||A||_1 at apow[(PW + 1) MM]
+// Van Loan knots on the series path: knot r (Delta_{r+1}, r = 0 .. M-1) is f_r(X) w with f_{M-1} = V and
+// f_{r-1} = P f_r, analytic in X = c A (P and V commute), so Delta_{r+1} = sum_k phi[r][k] c^k (A^k w); the
+// coefficients phi are the products of the schemes' scalar series, truncated at order PW, formed once per call.
+// The series holds where M |c| ||A||_1 is inside the scheme's radius.
+constexpr int PHI_OFF = (PW + 1) * MM + 64;  // offset of phi in apow (M rows of PW + 1)
+constexpr int APOW_FLOATS = PHI_OFF + 64 * (PW + 1);
+
+// the table: A^k (k = 0 .. PW) in float64, stored float, ||A||_1 at apow[(PW + 1) MM]; with a per-interval Van Loan
+// leaf the knots' coefficients phi at apow[PHI_OFF]
 __global__ __launch_bounds__(NT) void k_wpowers(WArgs a) {
   __shared__ __align__(16) double sd[3 * S32 + 64];
   double* A = sd;
@@ -701,6 +709,23 @@ __global__ __launch_bounds__(NT) void k_wpowers(WArgs a) {
   }
   const double nrm = norm1<32>(A, sd + 3 * S32);
   if (threadIdx.x == 0) a.apow[(size_t)(PW + 1) * MM] = (float)nrm;
+  if (threadIdx.x == 0 && a.leaf == EWS_LEAF_VAN_LOAN && a.vl_mode == EWS_FLOW_PER_INTERVAL) {
+    float gp[PW + 1], gv[PW + 1];
+    series_gamma(a.vl_expm, 1, gp);
+    series_gamma(a.vl_expm, 2, gv);
+    double f[PW + 1], g[PW + 1];
+    for (int k = 0; k <= PW; ++k) f[k] = gv[k];
+    float* phi = a.apow + PHI_OFF;
+    for (int r = a.vm - 1; r >= 0; --r) {
+      for (int k = 0; k <= PW; ++k) phi[r * (PW + 1) + k] = (float)f[k];
+      for (int k = 0; k <= PW; ++k) {  // f <- P f, truncated
+        double x = 0.0;
+        for (int j = 0; j <= k; ++j) x += (double)gp[j] * f[k - j];
+        g[k] = x;
+      }
+      for (int k = 0; k <= PW; ++k) f[k] = g[k];
+    }
+  }
 }
 
 // the thread's four entries of every power
@@ -723,7 +748,8 @@ __device__ __forceinline__ float4 series_eval(const float4* T, const float* g, f
   return r;
 }
 
-// per-interval flows and Van Loan pairs on the series path; flags the others
+// per-interval flows and Van Loan pairs on the series path; flags the others (bit 0: the flow, bit 1: the Van Loan
+// pair outside the series radius; bit 2: the Van Loan knots by the chain, not by their series)
 __global__ __launch_bounds__(NT) void k_wmat_series(WArgs a) {
   __shared__ float s_g[3][PW + 1];
   if (threadIdx.x == 0) {
@@ -749,31 +775,55 @@ __global__ __launch_bounds__(NT) void k_wmat_series(WArgs a) {
       if (fabsf(h) * nrm <= rf) gst4(a.fl + it * MM, series_eval(T, s_g[0], h));
       else flag |= 1;
     }
-    if (do_vl) {
-      const float c = h / (float)a.vm;
-      if (fabsf(c) * nrm <= rv) {
-        gst4(a.vlm + it * 2 * MM, series_eval(T, s_g[1], c));
-        gst4(a.vlm + it * 2 * MM + MM, series_eval(T, s_g[2], c));
-      } else {
-        flag |= 2;
+    if (do_vl) {  // the knots on the series path (u_k, no P, V); or P, V on it with the knot chain; or neither
+      const float c = h / (float)a.vm, x = fabsf(c) * nrm;
+      if ((float)a.vm * x > rv) {
+        flag |= 4;
+        if (x <= rv) {
+          gst4(a.vlm + it * 2 * MM, series_eval(T, s_g[1], c));
+          gst4(a.vlm + it * 2 * MM + MM, series_eval(T, s_g[2], c));
+        } else {
+          flag |= 2;
+        }
+      } else {  // u_k = A^k w, w = v / M: the thread's four columns of row i, summed over the row's 8 lanes
+        const int i = trow<32>(), j0 = tcol<32>();
+        const float* xp = a.path + ((size_t)b * a.L + t) * a.d;
+        float w[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) w[u] = j0 + u < a.d ? (xp[a.d + j0 + u] - xp[j0 + u]) / (float)a.vm : 0.0f;
+        float* ub = a.ubuf + it * (PW + 1) * 32;
+#pragma unroll
+        for (int k = 0; k <= PW; ++k) {
+          float pk = T[k].x * w[0] + T[k].y * w[1] + T[k].z * w[2] + T[k].w * w[3];
+          pk += __shfl_xor(pk, 1, 64);
+          pk += __shfl_xor(pk, 2, 64);
+          pk += __shfl_xor(pk, 4, 64);
+          if (row_lead()) ub[k * 32 + i] = pk;
+        }
       }
     }
     if (threadIdx.x == 0) a.mflag[it] = flag;
   }
 }
 
-// sum over the workgroup of two values (every thread returns both); red: 2 NT / 64 floats
-__device__ __forceinline__ float2 block_sum2(float u, float v, float* red) {
+// sum over the workgroup of two values (every thread returns both; red: 2 NT / 64 floats); when cols, also each
+// wavefront's column sums (lanes 0 .. 7, four columns each) into redw[wavefront][32] between the two barriers: they
+// are read after the call returns and rewritten only after the next call's first barrier
+__device__ __forceinline__ float2 block_sum2_cols(float u, float v, const float* dw, bool cols, float* red,
+                                                  float* redw) {
 #pragma unroll
   for (int o = 32; o > 0; o >>= 1) {
     u += __shfl_xor(u, o, 64);
     v += __shfl_xor(v, o, 64);
   }
   __syncthreads();
-  if ((threadIdx.x & 63) == 0) {
-    red[threadIdx.x >> 6] = u;
-    red[NT / 64 + (threadIdx.x >> 6)] = v;
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  if (lane == 0) {
+    red[wv] = u;
+    red[NT / 64 + wv] = v;
   }
+  if (cols && lane < 8)
+    *reinterpret_cast<float4*>(redw + wv * 32 + lane * 4) = float4{dw[0], dw[1], dw[2], dw[3]};
   __syncthreads();
   float su = 0.0f, sv = 0.0f;
 #pragma unroll
@@ -789,6 +839,7 @@ __device__ __forceinline__ float2 block_sum2(float u, float v, float* red) {
 __global__ __launch_bounds__(NT) void k_wmat_bwd_series(WArgs a) {
   __shared__ float s_g[3][PW + 1];
   __shared__ float red[2 * NT / 64];
+  __shared__ __align__(16) float redw[NT / 64][32];  // the series-path knots' dw, per wavefront
   if (threadIdx.x == 0) {
     series_gamma(a.chen, 0, s_g[0]);
     if (a.leaf == EWS_LEAF_VAN_LOAN) {
@@ -808,7 +859,9 @@ __global__ __launch_bounds__(NT) void k_wmat_bwd_series(WArgs a) {
     const int b = (int)(it / a.n), t = (int)(it - (long)b * a.n);
     const float h = a.clock[(size_t)b * a.L + t + 1] - a.clock[(size_t)b * a.L + t];
     const int flag = a.mflag[it];
-    const bool sf = do_flow && !(flag & 1), sv = do_vl && !(flag & 2);
+    // sv: the Van Loan pair on the series path (its knots by the chain); sk: the knots themselves on it (their
+    // clock-step cotangent is the leaf adjoint's)
+    const bool sf = do_flow && !(flag & 1), sv = do_vl && (flag & 4) && !(flag & 2), sk = do_vl && !(flag & 4);
     float df = 0.0f, dv = 0.0f;
     if (sf) {  // H_k += gamma_k h^k G; dh = <G, sum_k k gamma_k h^(k-1) A^k>
       const float4 G = gld4(a.dfl + it * MM);
@@ -844,11 +897,50 @@ __global__ __launch_bounds__(NT) void k_wmat_bwd_series(WArgs a) {
         ck *= c;
       }
     }
-    if (sf || sv) {  // uniform over the workgroup
-      const float2 s2 = block_sum2(df, dv, red);
+    float dw[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    if (sk) {
+      // knots sum_k phi[m][k] c^k A^k w with e_k their cotangents: H_k += c^k e_k w^T, dw = sum_k c^k (A^k)^T e_k
+      // (the thread's row-i part of its four columns), dc = sum_k k c^(k-1) <e_k, A^k w> (into dv); w = v / M
+      const float c = h / (float)a.vm;
+      const int i = trow<32>(), j0 = tcol<32>();
+      const float* x = a.path + ((size_t)b * a.L + t) * a.d;
+      float w[4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) w[u] = j0 + u < a.d ? (x[a.d + j0 + u] - x[j0 + u]) / (float)a.vm : 0.0f;
+      const float* e = a.ebuf + (size_t)it * (PW + 1) * 32 + i;
+      float ck = 1.0f, dk = 0.0f;  // c^k, k c^(k-1)
+#pragma unroll
+      for (int k = 0; k <= PW; ++k) {
+        const float ek = e[k * 32], cek = ck * ek;
+        H[k].x = fmaf(cek, w[0], H[k].x);
+        H[k].y = fmaf(cek, w[1], H[k].y);
+        H[k].z = fmaf(cek, w[2], H[k].z);
+        H[k].w = fmaf(cek, w[3], H[k].w);
+        dw[0] = fmaf(cek, T[k].x, dw[0]);
+        dw[1] = fmaf(cek, T[k].y, dw[1]);
+        dw[2] = fmaf(cek, T[k].z, dw[2]);
+        dw[3] = fmaf(cek, T[k].w, dw[3]);
+        dv = fmaf(dk * ek, T[k].x * w[0] + T[k].y * w[1] + T[k].z * w[2] + T[k].w * w[3], dv);
+        dk = fmaf(dk, c, ck);
+        ck *= c;
+      }
+      // over the wavefront's 8 rows (lanes 8 apart hold the same columns): lanes 0 .. 7 keep the sums
+#pragma unroll
+      for (int o = 8; o < 64; o <<= 1)
+#pragma unroll
+        for (int u = 0; u < 4; ++u) dw[u] += __shfl_xor(dw[u], o, 64);
+    }
+    if (sf || sv || sk) {  // uniform over the workgroup
+      const float2 s2 = block_sum2_cols(df, dv, dw, sk, red, &redw[0][0]);
       if (threadIdx.x == 0) {
         if (sf) a.dhm[2 * it] = s2.x;
-        if (sv) a.dhm[2 * it + 1] = s2.y / (float)a.vm;  // c = h / M
+        if (sv || sk) a.dhm[2 * it + 1] = s2.y / (float)a.vm;  // c = h / M
+      }
+      if (sk && threadIdx.x < a.d) {  // the wavefronts' column sums, in order: dv = dw / M
+        float sw = 0.0f;
+#pragma unroll
+        for (int wv = 0; wv < NT / 64; ++wv) sw += redw[wv][threadIdx.x];
+        a.dv[(size_t)it * DP + threadIdx.x] = sw / (float)a.vm;
       }
     }
   }
@@ -925,6 +1017,58 @@ __device__ __forceinline__ void commit_mat(float4 v, float* F, float* Ft) {
 constexpr int LF_A = 0, LF_P = S32, LF_V = 2 * S32, LF_S2 = 3 * S32, LF_VEC = 4 * S32;  // vectors: 8 x 32
 constexpr int LF_TAB = LF_VEC + 8 * 32;
 __host__ __device__ constexpr int lf_floats(int rows, int ntab) { return LF_TAB + ntab * rows * 32 + 64; }
+// with a per-interval Van Loan leaf: phi (M rows of PW + 1) and u_k = A^k w (PW + 1 rows of 32)
+constexpr int LX_PHI = 64 * (PW + 1), LX_U = (PW + 1) * 32;
+constexpr int LF_EXTRA = LX_PHI + LX_U;
+
+// knots Delta_1 .. Delta_M into D (rows 0 .. M-1) on the series path: Delta_{r+1} = sum_k phi[r][k] c^k u_k from
+// u_k = A^k w (rows of U, formed per interval by k_wmat_series)
+__device__ void series_knots(int M, const float* phi, const float* U, float* D, float c) {
+  const int tid = threadIdx.x;
+  for (int e = tid; e < M * 32; e += NT) {
+    const int r = e >> 5, row = e & 31;
+    float x = 0.0f, ck = 1.0f;
+#pragma unroll 4
+    for (int k = 0; k <= PW; ++k) {
+      x = fmaf(phi[r * (PW + 1) + k] * ck, U[k * 32 + row], x);
+      ck *= c;
+    }
+    D[e] = x;
+  }
+  __syncthreads();
+}
+
+// the knots' partial sums, 8 lanes per channel (a segment of ceil(M / 8) knots each, scanned across the 8 lanes):
+// Y_m = Pre_m + Delta_m / 2 (Pre_m the knots before m), Z_m = R_m + Delta_m / 2 (R_m the knots after m, when Z is
+// given) and s1 = sum_m Delta_m (into s1 when given); D, Y, Z hold rows m of 32
+__device__ void knot_sums(int M, const float* D, float* Y, float* Z, float* s1) {
+  const int tid = threadIdx.x, col = tid >> 3, seg = tid & 7;
+  const int S = (M + 7) >> 3, m0 = min(M, seg * S), m1 = min(M, m0 + S);
+  float own = 0.0f;
+  for (int m = m0; m < m1; ++m) own += D[m * 32 + col];
+  float inc = own;
+#pragma unroll
+  for (int o = 1; o < 8; o <<= 1) {
+    const float v = __shfl_up(inc, o, 8);
+    if (seg >= o) inc += v;
+  }
+  const float total = __shfl(inc, 7, 8);
+  float pre = inc - own;
+  for (int m = m0; m < m1; ++m) {
+    const float dm = D[m * 32 + col];
+    Y[m * 32 + col] = fmaf(0.5f, dm, pre);
+    pre += dm;
+  }
+  if (Z) {
+    float suf = total - inc;
+    for (int m = m1 - 1; m >= m0; --m) {
+      const float dm = D[m * 32 + col];
+      Z[m * 32 + col] = fmaf(0.5f, dm, suf);
+      suf += dm;
+    }
+  }
+  if (s1 && seg == 0) s1[col] = total;
+}
 
 __device__ __forceinline__ float inv_f(int n) { return 1.0f / (float)n; }
 __device__ __forceinline__ float c2coef(int p, int r) { return 1.0f / ((float)(p + r + 2) * (float)(r + 1)); }
@@ -959,7 +1103,7 @@ __device__ void vl_knots(const WArgs& a, const float* P, const float* V, const f
 
 // interval's local terms (s1 into s1v, s2 into the thread's registers)
 template <int N>
-__device__ void leaf_fwd(const WArgs& a, float* sm, int b, int t, float* s1v, float* s2r) {
+__device__ void leaf_fwd(const WArgs& a, float* sm, int b, int t, float* s1v, float* s2r, bool ser) {
   float* A = sm + LF_A;
   float* vec = sm + LF_VEC;
   float* T1 = sm + LF_TAB;
@@ -970,20 +1114,19 @@ __device__ void leaf_fwd(const WArgs& a, float* sm, int b, int t, float* s1v, fl
   if (a.leaf == EWS_LEAF_VAN_LOAN) {
     float* P = sm + LF_P;
     float* V = sm + LF_V;
-    load_vl(a, b, t, P, V);
-    if (tid < 32) vec[tid] = tid < a.d ? (x[a.d + tid] - x[tid]) / (float)a.vm : 0.0f;
-    __syncthreads();
-    vl_knots(a, P, V, vec, T1);
-    const int M = a.vm;
-    if (tid < 32) {  // s1 and Y_m = Pre_m + Delta_m / 2
-      float pre = 0.0f;
-      for (int m = 0; m < M; ++m) {
-        const float dm = T1[m * 32 + tid];
-        T2[m * 32 + tid] = fmaf(0.5f, dm, pre);
-        pre += dm;
-      }
-      s1v[tid] = pre;
+    float* phi = sm + lf_floats(a.vm, 2);
+    if (ser) {
+      const float* u = a.ubuf + ((size_t)b * a.n + t) * (PW + 1) * 32;
+      for (int e = tid; e < (PW + 1) * 32; e += NT) phi[LX_PHI + e] = u[e];
+    } else {
+      load_vl(a, b, t, P, V);
+      if (tid < 32) vec[tid] = tid < a.d ? (x[a.d + tid] - x[tid]) / (float)a.vm : 0.0f;
     }
+    __syncthreads();
+    if (ser) series_knots(a.vm, phi, phi + LX_PHI, T1, (th[t + 1] - th[t]) / (float)a.vm);
+    else vl_knots(a, P, V, vec, T1);
+    const int M = a.vm;
+    knot_sums(M, T1, T2, nullptr, s1v);  // s1 and Y_m = Pre_m + Delta_m / 2
     __syncthreads();
     if constexpr (N >= 2) {  // s2 = sum_m Y_m Delta_m^T
 #pragma unroll
@@ -1036,17 +1179,23 @@ __device__ void leaf_fwd(const WArgs& a, float* sm, int b, int t, float* s1v, fl
   __syncthreads();
 }
 
-template <int N>
+// SER: the per-interval Van Loan leaf, whose knots may take the series path (a separate instantiation keeps the
+// other leaves' register count low)
+template <int N, bool SER>
 __global__ __launch_bounds__(NT) void k_wleaf(WArgs a) {
-  extern __shared__ __align__(16) float sm[];  // lf_floats(rows, 2)
+  extern __shared__ __align__(16) float sm[];  // lf_floats(rows, 2) (+ LF_EXTRA, per-interval Van Loan)
   float* s1v = sm + LF_VEC + 32;
   load_A(a.d, a.A, sm + LF_A);
+  if (SER) {  // the knots' coefficients of the series path
+    float* phi = sm + lf_floats(a.vm, 2);
+    for (int e = threadIdx.x; e < a.vm * (PW + 1); e += NT) phi[e] = a.apow[PHI_OFF + e];
+  }
   __syncthreads();
   const long items = (long)a.B * a.n;
   for (long it = blockIdx.x; it < items; it += gridDim.x) {
     const int b = (int)(it / a.n), t = (int)(it - (long)b * a.n);
     float s2r[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-    leaf_fwd<N>(a, sm, b, t, s1v, s2r);
+    leaf_fwd<N>(a, sm, b, t, s1v, s2r, SER && !(a.mflag[it] & 4));
     float* row = a.loc + it * RW;
     if (threadIdx.x < 32) row[threadIdx.x] = s1v[threadIdx.x];
     if constexpr (N >= 2) gst4(row + DP, acc4(s2r));
@@ -1447,9 +1596,9 @@ __global__ __launch_bounds__(NT) void k_wadj_carry(WArgs a) {
 // Leaf adjoints, a workgroup per (slice of TL intervals, sample): dv per interval, the series leaf's dh and dA
 // (workgroup partial), the Van Loan leaf's (dP, dV) per interval (per-interval mode) or summed over the slice (shared
 // modes).
-template <int N>
-__global__ __launch_bounds__(NT) void k_wleaf_bwd(WArgs a) {
-  extern __shared__ __align__(16) float sm[];  // lf_floats(rows, 4)
+template <int N, bool SER>
+__global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(4))) void k_wleaf_bwd(WArgs a) {
+  extern __shared__ __align__(16) float sm[];  // lf_floats(rows, 4) (+ LF_EXTRA, per-interval Van Loan)
   float* A = sm + LF_A;
   float* S2b = sm + LF_S2;  // ds2
   float* vec = sm + LF_VEC;
@@ -1469,10 +1618,17 @@ __global__ __launch_bounds__(NT) void k_wleaf_bwd(WArgs a) {
   const float* th = a.clock + (size_t)b * a.L;
   const bool vl = a.leaf == EWS_LEAF_VAN_LOAN;
   const bool vl_shared = vl && a.vl_mode != EWS_FLOW_PER_INTERVAL;
+  const bool vl_int = SER;
+  float* phi = sm + lf_floats(rows, 4);
+  float* U = phi + LX_PHI;
+  if (vl_int) {
+    for (int e = tid; e < a.vm * (PW + 1); e += NT) phi[e] = a.apow[PHI_OFF + e];
+  }
   // the interval's cotangents, increment and (per-interval Van Loan) step matrices in registers, loaded during the
   // interval before
   float nd1 = 0.0f, nv = 0.0f;
   float4 nd2 = float4{0.0f, 0.0f, 0.0f, 0.0f}, nP = nd2, nV = nd2;
+  float nU[3] = {0.0f, 0.0f, 0.0f};  // (PW + 1) * 32 <= 3 NT
   auto fetch = [&](int t) {
     const size_t r = (size_t)b * a.n + t;
     const float* x = a.path + ((size_t)b * a.L + t) * a.d;
@@ -1481,7 +1637,12 @@ __global__ __launch_bounds__(NT) void k_wleaf_bwd(WArgs a) {
       nv = tid < a.d ? x[a.d + tid] - x[tid] : 0.0f;
     }
     if (N >= 2) nd2 = gld4(a.dloc + r * RW + DP);
-    if (vl && !vl_shared) {
+    if (vl_int && !(a.mflag[r] & 4)) {  // the series path: u_k, no (P, V)
+      for (int k = 0; k < 3; ++k) {
+        const int e = tid + k * NT;
+        nU[k] = e < (PW + 1) * 32 ? a.ubuf[r * (PW + 1) * 32 + e] : 0.0f;
+      }
+    } else if (vl_int) {
       nP = gld4(a.vlm + r * 2 * MM);
       nV = gld4(a.vlm + r * 2 * MM + MM);
     }
@@ -1496,41 +1657,67 @@ __global__ __launch_bounds__(NT) void k_wleaf_bwd(WArgs a) {
     }
     if constexpr (N >= 2) sld4(S2b, nd2);
     float dvi = 0.0f, dh = 0.0f;
+    bool dv_done = false;  // dv of a series-path interval is k_wmat_bwd_series's
     if (vl) {
       float* P = sm + LF_P;
       float* V = sm + LF_V;
+      const bool ser = vl_int && !(a.mflag[r] & 4);
       if (vl_shared) {
         load_vl(a, b, t, P, V);
-      } else {
+      } else if (!ser) {
         sld4(P, nP);
         sld4(V, nV);
+      } else {
+        for (int k = 0; k < 3; ++k) {
+          const int e = tid + k * NT;
+          if (e < (PW + 1) * 32) U[e] = nU[k];
+        }
       }
       const int M = a.vm;
+      const float c = (th[t + 1] - th[t]) / (float)M;
       __syncthreads();
       if (t + 1 < t1) fetch(t + 1);
-      vl_knots(a, P, V, wv, T1);  // Delta_m in rows 0 .. M-1
-      if (tid < 32) {  // Z_m = R_m + Delta_m / 2 (T2), Y_m = Pre_m + Delta_m / 2 (T3)
-        float suf = 0.0f;
-        for (int m = M - 1; m >= 0; --m) {
-          const float dm = T1[m * 32 + tid];
-          T2[m * 32 + tid] = fmaf(0.5f, dm, suf);
-          suf += dm;
+      if (ser) series_knots(M, phi, U, T1, c);  // Delta_m in rows 0 .. M-1
+      else vl_knots(a, P, V, wv, T1);
+      knot_sums(M, T1, T3, T2, nullptr);  // Z_m = R_m + Delta_m / 2 (T2), Y_m = Pre_m + Delta_m / 2 (T3)
+      __syncthreads();
+      // dDelta_m = ds1 + ds2 Z_m + ds2^T Y_m (rows of T4), a thread per entry
+      for (int e = tid; e < M * 32; e += NT) {
+        const int m = e >> 5, ii = e & 31;
+        float v = ds1[ii];
+        if constexpr (N >= 2) {
+          const float* z = T2 + m * 32;
+          const float* y = T3 + m * 32;
+          const float* srow = S2b + ii * P32;
+#pragma unroll 2
+          for (int j = 0; j < 32; j += 4) {
+            const float4 zz = *reinterpret_cast<const float4*>(z + j);
+            const float4 yy = *reinterpret_cast<const float4*>(y + j);
+            const float4 sr = *reinterpret_cast<const float4*>(srow + j);
+            v = fmaf(sr.x, zz.x, v);
+            v = fmaf(sr.y, zz.y, v);
+            v = fmaf(sr.z, zz.z, v);
+            v = fmaf(sr.w, zz.w, v);
+            v = fmaf(S2b[j * P32 + ii], yy.x, v);
+            v = fmaf(S2b[(j + 1) * P32 + ii], yy.y, v);
+            v = fmaf(S2b[(j + 2) * P32 + ii], yy.z, v);
+            v = fmaf(S2b[(j + 3) * P32 + ii], yy.w, v);
+          }
         }
-        float pre = 0.0f;
-        for (int m = 0; m < M; ++m) {
-          const float dm = T1[m * 32 + tid];
-          T3[m * 32 + tid] = fmaf(0.5f, dm, pre);
-          pre += dm;
-        }
+        T4[e] = v;
       }
       __syncthreads();
-      // dDelta_m = ds1 + ds2 Z_m + ds2^T Y_m (rows of T4)
-      for (int m = 0; m < M; ++m) {
-        float v = 0.0f;
-        if constexpr (N >= 2) v = mv<false>(S2b, T2 + m * 32) + mv<true>(S2b, T3 + m * 32);
-        if (row_lead()) T4[m * 32 + i] = ds1[i] + v;
-      }
-      __syncthreads();
+      if (ser) {
+        // e_k = sum_r phi[r][k] dDelta_r, to ebuf: the powers' cotangent c^k e_k w^T, dw = sum_k c^k (A^k)^T e_k
+        // and dc = sum_k k c^(k-1) <e_k, u_k> are k_wmat_bwd_series's (it holds the powers)
+        for (int e = tid; e < (PW + 1) * 32; e += NT) {
+          const int k = e >> 5, row = e & 31;
+          float x = 0.0f;
+          for (int m = 0; m < M; ++m) x = fmaf(phi[m * (PW + 1) + k], T4[m * 32 + row], x);
+          a.ebuf[r * (PW + 1) * 32 + e] = x;
+        }
+        dv_done = true;
+      } else {
       // chain: lam_1 = dDelta_1, lam_m = dDelta_m + P^T lam_{m-1} (in place in T4)
       for (int m = 1; m < M; ++m) {
         const float v = mv<true>(P, T4 + (m - 1) * 32);
@@ -1563,6 +1750,7 @@ __global__ __launch_bounds__(NT) void k_wleaf_bwd(WArgs a) {
           sP[k] += gp[k];
           sV[k] += gv[k];
         }
+      }
       }
     } else {
       const int q = a.q;
@@ -1618,7 +1806,7 @@ __global__ __launch_bounds__(NT) void k_wleaf_bwd(WArgs a) {
       }
       dvi = T4[i];
     }
-    if (row_lead() && i < a.d) a.dv[r * DP + i] = dvi;
+    if (!dv_done && row_lead() && i < a.d) a.dv[r * DP + i] = dvi;
     if (a.leaf != EWS_LEAF_VAN_LOAN) {
       // dh: the 32 partials of threads 0..31 (wavefront 0)
       float s = tid < 32 ? dh : 0.0f;
@@ -1847,7 +2035,7 @@ int plan(const ews_dense_desc* s, WPlan& p) {
 
 struct WLay {
   size_t fl, vlm, loc, summ, sfl, car, rows, amax, apow, mflag, outs, grow, mu, lend, dloc, dfl, cpart, dvlm, apart,
-      dv, dhl, dhm, dsh, hpart, hsum, total;
+      dv, dhl, dhm, dsh, hpart, hsum, ubuf, ebuf, total;
 };
 
 WLay layout(const ews_dense_desc* s, const WPlan& p, bool bwd) {
@@ -1867,8 +2055,9 @@ WLay layout(const ews_dense_desc* s, const WPlan& p, bool bwd) {
   const bool mm_ro = s->readout == EWS_READOUT_MEAN || s->readout == EWS_READOUT_MAX;
   take(w.rows, (bwd || mm_ro) ? BN * RW * 4 : 0);
   take(w.amax, s->readout == EWS_READOUT_MAX ? (size_t)p.B * p.W * 4 : 0);
-  take(w.apow, p.mats_int ? ((size_t)(PW + 1) * MM + 64) * 4 : 0);
+  take(w.apow, p.mats_int ? (size_t)APOW_FLOATS * 4 : 0);
   take(w.mflag, p.mats_int ? BN * 4 : 0);
+  take(w.ubuf, p.vl_int ? BN * (PW + 1) * 32 * 4 : 0);
   if (bwd) {
     take(w.outs, s->readout == EWS_READOUT_MAX ? (size_t)p.B * p.W * 4 : 0);
     take(w.grow, BN * RW * 4);
@@ -1885,6 +2074,7 @@ WLay layout(const ews_dense_desc* s, const WPlan& p, bool bwd) {
     take(w.dsh, (size_t)p.B * 2 * 4);
     take(w.hpart, (size_t)p.g_ser * (PW + 1) * MM * 4);
     take(w.hsum, p.mats_int ? (size_t)(PW + 1) * MM * 8 : 0);
+    take(w.ebuf, p.vl_int ? BN * (PW + 1) * 32 * 4 : 0);
   }
   w.total = off;
   return w;
@@ -1910,11 +2100,13 @@ WArgs make_args(const ews_dense_desc* s, const WPlan& p, const float* path, cons
   a.amax = s->readout == EWS_READOUT_MAX ? (int*)(ws + w.amax) : nullptr;
   a.apow = p.mats_int ? f(w.apow) : nullptr;
   a.mflag = p.mats_int ? (int*)(ws + w.mflag) : nullptr;
+  a.ubuf = p.vl_int ? f(w.ubuf) : nullptr;
   if (bwd) {
     a.grow = f(w.grow); a.mu = f(w.mu); a.lend = f(w.lend); a.dloc = f(w.dloc);
     a.dfl = p.fl_int ? f(w.dfl) : nullptr; a.cpart = f(w.cpart); a.dvlm = p.vl_int ? f(w.dvlm) : nullptr;
     a.apart = f(w.apart); a.dv = f(w.dv); a.dhl = f(w.dhl); a.dhm = f(w.dhm); a.dsh = f(w.dsh);
     a.hpart = f(w.hpart); a.hsum = p.mats_int ? (double*)(ws + w.hsum) : nullptr;
+    a.ebuf = p.vl_int ? f(w.ebuf) : nullptr;
   }
   return a;
 }
@@ -1944,14 +2136,21 @@ int run_forward(const WPlan& p, const WArgs& a, hipStream_t st) {
     WIDE_CHECK();
   }
   const dim3 gl((unsigned)std::min<long>((long)p.B * p.n, 4096)), gc(p.C, p.B);
-  const size_t lds_leaf = (size_t)lf_floats(p.rows, 2) * 4;
+  const size_t lds_leaf = (size_t)(lf_floats(p.rows, 2) + (p.vl_int ? LF_EXTRA : 0)) * 4;
+  const void* kl = p.N == 1 ? (p.vl_int ? reinterpret_cast<const void*>(&k_wleaf<1, true>)
+                                          : reinterpret_cast<const void*>(&k_wleaf<1, false>))
+                            : (p.vl_int ? reinterpret_cast<const void*>(&k_wleaf<2, true>)
+                                        : reinterpret_cast<const void*>(&k_wleaf<2, false>));
+  if (set_lds(kl, lds_leaf) != EWS_OK) return EWS_ERR_LAUNCH;
   if (p.N == 1) {
-    hipLaunchKernelGGL(k_wleaf<1>, gl, dim3(NT), lds_leaf, st, a);
+    if (p.vl_int) hipLaunchKernelGGL((k_wleaf<1, true>), gl, dim3(NT), lds_leaf, st, a);
+    else hipLaunchKernelGGL((k_wleaf<1, false>), gl, dim3(NT), lds_leaf, st, a);
     hipLaunchKernelGGL((k_wscan<1, SCAN_SUMMARY>), gc, dim3(NT), 0, st, a);
     hipLaunchKernelGGL(k_wcarry<1>, dim3(p.B), dim3(NT), 0, st, a);
     hipLaunchKernelGGL((k_wscan<1, SCAN_ROWS>), gc, dim3(NT), 0, st, a);
   } else {
-    hipLaunchKernelGGL(k_wleaf<2>, gl, dim3(NT), lds_leaf, st, a);
+    if (p.vl_int) hipLaunchKernelGGL((k_wleaf<2, true>), gl, dim3(NT), lds_leaf, st, a);
+    else hipLaunchKernelGGL((k_wleaf<2, false>), gl, dim3(NT), lds_leaf, st, a);
     hipLaunchKernelGGL((k_wscan<2, SCAN_SUMMARY>), gc, dim3(NT), 0, st, a);
     hipLaunchKernelGGL(k_wcarry<2>, dim3(p.B), dim3(NT), 0, st, a);
     hipLaunchKernelGGL((k_wscan<2, SCAN_ROWS>), gc, dim3(NT), 0, st, a);
@@ -2006,17 +2205,24 @@ int backward(const ews_dense_desc* s, const float* path, const float* clock, con
                      dim3(NT), 0, st, a, grad_out);
   WIDE_CHECK();
   const dim3 gc(p.C, p.B);
-  const size_t lds_lb = (size_t)lf_floats(p.rows, 4) * 4;
+  const size_t lds_lb = (size_t)(lf_floats(p.rows, 4) + (p.vl_int ? LF_EXTRA : 0)) * 4;
+  const void* kb = p.N == 1 ? (p.vl_int ? reinterpret_cast<const void*>(&k_wleaf_bwd<1, true>)
+                                          : reinterpret_cast<const void*>(&k_wleaf_bwd<1, false>))
+                            : (p.vl_int ? reinterpret_cast<const void*>(&k_wleaf_bwd<2, true>)
+                                        : reinterpret_cast<const void*>(&k_wleaf_bwd<2, false>));
+  if (set_lds(kb, lds_lb) != EWS_OK) return EWS_ERR_LAUNCH;
   if (p.N == 1) {
     hipLaunchKernelGGL((k_wadj<1, ADJ_LOCAL>), gc, dim3(NT), 0, st, a);
     hipLaunchKernelGGL(k_wadj_carry<1>, dim3(p.B), dim3(NT), 0, st, a);
     hipLaunchKernelGGL((k_wadj<1, ADJ_FULL>), gc, dim3(NT), 0, st, a);
-    hipLaunchKernelGGL(k_wleaf_bwd<1>, dim3(p.NSL, p.B), dim3(NT), lds_lb, st, a);
+    if (p.vl_int) hipLaunchKernelGGL((k_wleaf_bwd<1, true>), dim3(p.NSL, p.B), dim3(NT), lds_lb, st, a);
+    else hipLaunchKernelGGL((k_wleaf_bwd<1, false>), dim3(p.NSL, p.B), dim3(NT), lds_lb, st, a);
   } else {
     hipLaunchKernelGGL((k_wadj<2, ADJ_LOCAL>), gc, dim3(NT), 0, st, a);
     hipLaunchKernelGGL(k_wadj_carry<2>, dim3(p.B), dim3(NT), 0, st, a);
     hipLaunchKernelGGL((k_wadj<2, ADJ_FULL>), gc, dim3(NT), 0, st, a);
-    hipLaunchKernelGGL(k_wleaf_bwd<2>, dim3(p.NSL, p.B), dim3(NT), lds_lb, st, a);
+    if (p.vl_int) hipLaunchKernelGGL((k_wleaf_bwd<2, true>), dim3(p.NSL, p.B), dim3(NT), lds_lb, st, a);
+    else hipLaunchKernelGGL((k_wleaf_bwd<2, false>), dim3(p.NSL, p.B), dim3(NT), lds_lb, st, a);
   }
   WIDE_CHECK();
   const long base = (long)p.B * p.NSL;

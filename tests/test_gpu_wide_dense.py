@@ -204,3 +204,25 @@ def test_wide_series_and_fallback_in_one_call(scheme):
     tag = f"mixed radius {scheme}"
     _check_levels(out, ref, d, 2, 1e-5, tag)
     _check_grads(gg, rg, tag)
+
+
+@pytest.mark.parametrize("scheme", ["exact", "cayley", "euler", "pade"])
+def test_wide_van_loan_knots_three_ways(scheme):
+    """Per-interval Van Loan leaf at M = 20 with |h| ||A||_1 from 0.05 to about 14, so that one call holds the
+    three forms of the knots: their own power series (M |c| ||A||_1 inside the scheme's radius, c = h / M), the
+    M-step chain over (P, V) from the powers table (|c| ||A||_1 inside it), and the chain over (P, V) from the
+    scaled / inverted forms (outside it); the adjoint takes the same three routes."""
+    rng = np.random.default_rng(23)
+    d, L, M = 20, 48, 20
+    G = rng.normal(size=(d, d))
+    A = (G - G.T) * (0.5 / np.sqrt(d)) + np.eye(d)
+    nrm = np.abs(A).sum(0).max()
+    steps = np.exp(rng.uniform(np.log(0.05), np.log(14.0), size=(2, L))) / nrm
+    steps[:, 0] = 0.0
+    path = torch.tensor(np.cumsum(rng.normal(size=(2, L, d)) * 0.3, 1))
+    clock = torch.tensor(np.cumsum(steps, 1))
+    out, ref, gg, rg = _run(path, clock, torch.tensor(A), 2, "prefix", "displacement",
+                            dict(van_loan_expm=scheme, chen_expm=scheme, M=M), chunk=16)
+    tag = f"knots three ways {scheme}"
+    _check_levels(out, ref, d, 2, 1e-5, tag)
+    _check_grads(gg, rg, tag)
