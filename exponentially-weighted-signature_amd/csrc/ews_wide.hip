@@ -135,8 +135,18 @@ __device__ __forceinline__ float4 f4add(float4 a, float4 b) {
 }
 __device__ __forceinline__ float4 acc4(const float* a) { return float4{a[0], a[1], a[2], a[3]}; }
 
+// sum over each aligned group of 8 lanes, every lane returning it: DPP quad permutations [1,0,3,2] and [2,3,0,1]
+// give each lane its quad's sum, then the half-row mirror (lane l of 8 reads lane 7 - l, in the other quad) adds
+// the other quad's; all on the VALU, no LDS round trip
+__device__ __forceinline__ float sum8(float v) {
+  v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0xB1, 0xf, 0xf, false));
+  v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x4E, 0xf, 0xf, false));
+  v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x141, 0xf, 0xf, false));
+  return v;
+}
+
 // y[i] = sum_k M(i, k) x[k] (M(i, k) = M[k][i] when TM), 32 x 32 in LDS: the 8 lanes of row i each take four k and
-// sum by lane exchanges; every lane of the row returns y[i]
+// sum them (sum8); every lane of the row returns y[i]
 template <bool TM>
 __device__ __forceinline__ float mv(const float* M, const float* x) {
   const int i = (int)threadIdx.x >> 3, p = ((int)threadIdx.x & 7) * 4;
@@ -146,10 +156,7 @@ __device__ __forceinline__ float mv(const float* M, const float* x) {
     const int k = p + r;
     s = fmaf(TM ? M[k * P32 + i] : M[i * P32 + k], x[k], s);
   }
-  s += __shfl_xor(s, 1, 64);
-  s += __shfl_xor(s, 2, 64);
-  s += __shfl_xor(s, 4, 64);
-  return s;
+  return sum8(s);
 }
 __device__ __forceinline__ bool row_lead() { return (threadIdx.x & 7) == 0; }
 
@@ -767,9 +774,28 @@ __global__ __launch_bounds__(NT) void k_wmat_series(WArgs a) {
   const bool do_vl = a.leaf == EWS_LEAF_VAN_LOAN && a.vl_mode == EWS_FLOW_PER_INTERVAL;
   const float rf = series_radius(a.chen, 0), rv = series_radius(a.vl_expm, 1);
   const long items = (long)a.B * a.n;
-  for (long it = blockIdx.x; it < items; it += gridDim.x) {
+  const int i = trow<32>(), j0 = tcol<32>(), s8 = threadIdx.x & 7;
+  // the item's clock step and (series-path knots) increment w = v / M, loaded during the item before
+  float nh = 0.0f, nw[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+  auto fetch = [&](long it) {
     const int b = (int)(it / a.n), t = (int)(it - (long)b * a.n);
-    const float h = a.clock[(size_t)b * a.L + t + 1] - a.clock[(size_t)b * a.L + t];
+    nh = a.clock[(size_t)b * a.L + t + 1] - a.clock[(size_t)b * a.L + t];
+    if (do_vl) {
+      const float* xp = a.path + ((size_t)b * a.L + t) * a.d;
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const int j = min(j0 + u, a.d - 1);  // in bounds; the padded columns are zeroed below
+        nw[u] = xp[a.d + j] - xp[j];
+      }
+    }
+  };
+  if ((long)blockIdx.x < items) fetch(blockIdx.x);
+  for (long it = blockIdx.x; it < items; it += gridDim.x) {
+    const float h = nh;
+    float w[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) w[u] = j0 + u < a.d ? nw[u] / (float)a.vm : 0.0f;
+    if (it + gridDim.x < items) fetch(it + gridDim.x);
     int flag = 0;
     if (do_flow) {
       if (fabsf(h) * nrm <= rf) gst4(a.fl + it * MM, series_eval(T, s_g[0], h));
@@ -785,21 +811,26 @@ __global__ __launch_bounds__(NT) void k_wmat_series(WArgs a) {
         } else {
           flag |= 2;
         }
-      } else {  // u_k = A^k w, w = v / M: the thread's four columns of row i, summed over the row's 8 lanes
-        const int i = trow<32>(), j0 = tcol<32>();
-        const float* xp = a.path + ((size_t)b * a.L + t) * a.d;
-        float w[4];
+      } else {
+        // u_k = A^k w: the thread's four columns of row i, summed over the row's 8 lanes (every lane gets each
+        // sum); lane s of the 8 stores u_s, u_{s+8}, u_{s+16} of row i
+        float pk[PW + 1];
 #pragma unroll
-        for (int u = 0; u < 4; ++u) w[u] = j0 + u < a.d ? (xp[a.d + j0 + u] - xp[j0 + u]) / (float)a.vm : 0.0f;
-        float* ub = a.ubuf + it * (PW + 1) * 32;
+        for (int k = 0; k <= PW; ++k)
+          pk[k] = sum8(T[k].x * w[0] + T[k].y * w[1] + T[k].z * w[2] + T[k].w * w[3]);
+        float o0 = pk[0], o1 = pk[8], o2 = pk[16];
 #pragma unroll
-        for (int k = 0; k <= PW; ++k) {
-          float pk = T[k].x * w[0] + T[k].y * w[1] + T[k].z * w[2] + T[k].w * w[3];
-          pk += __shfl_xor(pk, 1, 64);
-          pk += __shfl_xor(pk, 2, 64);
-          pk += __shfl_xor(pk, 4, 64);
-          if (row_lead()) ub[k * 32 + i] = pk;
+        for (int q = 1; q < 8; ++q) {
+          if (s8 == q) {
+            o0 = pk[q];
+            o1 = pk[8 + q];
+            o2 = 16 + q <= PW ? pk[16 + q] : 0.0f;
+          }
         }
+        float* ub = a.ubuf + it * (PW + 1) * 32 + i;
+        ub[s8 * 32] = o0;
+        ub[(8 + s8) * 32] = o1;
+        if (16 + s8 <= PW) ub[(16 + s8) * 32] = o2;
       }
     }
     if (threadIdx.x == 0) a.mflag[it] = flag;
@@ -855,16 +886,45 @@ __global__ __launch_bounds__(NT) void k_wmat_bwd_series(WArgs a) {
   const bool do_flow = a.flow_mode == EWS_FLOW_PER_INTERVAL;
   const bool do_vl = a.leaf == EWS_LEAF_VAN_LOAN && a.vl_mode == EWS_FLOW_PER_INTERVAL;
   const long items = (long)a.B * a.n;
+  const int i = trow<32>(), j0 = tcol<32>();
+  // the next item's clock step and flags, loaded during the item before
+  float nh = 0.0f;
+  int nflag = 0;
+  auto fetch = [&](long it) {
+    const int b = (int)(it / a.n), t = (int)(it - (long)b * a.n);
+    nh = a.clock[(size_t)b * a.L + t + 1] - a.clock[(size_t)b * a.L + t];
+    nflag = a.mflag[it];
+  };
+  if ((long)blockIdx.x < items) fetch(blockIdx.x);
   for (long it = blockIdx.x; it < items; it += gridDim.x) {
     const int b = (int)(it / a.n), t = (int)(it - (long)b * a.n);
-    const float h = a.clock[(size_t)b * a.L + t + 1] - a.clock[(size_t)b * a.L + t];
-    const int flag = a.mflag[it];
+    const float h = nh;
+    const int flag = nflag;
     // sv: the Van Loan pair on the series path (its knots by the chain); sk: the knots themselves on it (their
     // clock-step cotangent is the leaf adjoint's)
     const bool sf = do_flow && !(flag & 1), sv = do_vl && (flag & 4) && !(flag & 2), sk = do_vl && !(flag & 4);
+    // every load of the item issued before its first use
+    float4 G = float4{0.0f, 0.0f, 0.0f, 0.0f}, GP = G, GV = G;
+    float ek[PW + 1], xv[4];
+    if (sf) G = gld4(a.dfl + it * MM);
+    if (sv) {
+      GP = gld4(a.dvlm + it * 2 * MM);
+      GV = gld4(a.dvlm + it * 2 * MM + MM);
+    }
+    if (sk) {
+      const float* e = a.ebuf + (size_t)it * (PW + 1) * 32 + i;
+#pragma unroll
+      for (int k = 0; k <= PW; ++k) ek[k] = e[k * 32];
+      const float* x = a.path + ((size_t)b * a.L + t) * a.d;
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const int j = min(j0 + u, a.d - 1);  // in bounds; the padded columns are zeroed below
+        xv[u] = x[a.d + j] - x[j];
+      }
+    }
+    if (it + gridDim.x < items) fetch(it + gridDim.x);
     float df = 0.0f, dv = 0.0f;
     if (sf) {  // H_k += gamma_k h^k G; dh = <G, sum_k k gamma_k h^(k-1) A^k>
-      const float4 G = gld4(a.dfl + it * MM);
       float ck = 1.0f, dk = 0.0f;  // h^k, k h^(k-1)
 #pragma unroll
       for (int k = 0; k <= PW; ++k) {
@@ -881,7 +941,6 @@ __global__ __launch_bounds__(NT) void k_wmat_bwd_series(WArgs a) {
     }
     if (sv) {
       const float c = h / (float)a.vm;
-      const float4 GP = gld4(a.dvlm + it * 2 * MM), GV = gld4(a.dvlm + it * 2 * MM + MM);
       float ck = 1.0f, dk = 0.0f;
 #pragma unroll
       for (int k = 0; k <= PW; ++k) {
@@ -902,16 +961,13 @@ __global__ __launch_bounds__(NT) void k_wmat_bwd_series(WArgs a) {
       // knots sum_k phi[m][k] c^k A^k w with e_k their cotangents: H_k += c^k e_k w^T, dw = sum_k c^k (A^k)^T e_k
       // (the thread's row-i part of its four columns), dc = sum_k k c^(k-1) <e_k, A^k w> (into dv); w = v / M
       const float c = h / (float)a.vm;
-      const int i = trow<32>(), j0 = tcol<32>();
-      const float* x = a.path + ((size_t)b * a.L + t) * a.d;
       float w[4];
 #pragma unroll
-      for (int u = 0; u < 4; ++u) w[u] = j0 + u < a.d ? (x[a.d + j0 + u] - x[j0 + u]) / (float)a.vm : 0.0f;
-      const float* e = a.ebuf + (size_t)it * (PW + 1) * 32 + i;
+      for (int u = 0; u < 4; ++u) w[u] = j0 + u < a.d ? xv[u] / (float)a.vm : 0.0f;
       float ck = 1.0f, dk = 0.0f;  // c^k, k c^(k-1)
 #pragma unroll
       for (int k = 0; k <= PW; ++k) {
-        const float ek = e[k * 32], cek = ck * ek;
+        const float cek = ck * ek[k];
         H[k].x = fmaf(cek, w[0], H[k].x);
         H[k].y = fmaf(cek, w[1], H[k].y);
         H[k].z = fmaf(cek, w[2], H[k].z);
@@ -920,15 +976,18 @@ __global__ __launch_bounds__(NT) void k_wmat_bwd_series(WArgs a) {
         dw[1] = fmaf(cek, T[k].y, dw[1]);
         dw[2] = fmaf(cek, T[k].z, dw[2]);
         dw[3] = fmaf(cek, T[k].w, dw[3]);
-        dv = fmaf(dk * ek, T[k].x * w[0] + T[k].y * w[1] + T[k].z * w[2] + T[k].w * w[3], dv);
+        dv = fmaf(dk * ek[k], T[k].x * w[0] + T[k].y * w[1] + T[k].z * w[2] + T[k].w * w[3], dv);
         dk = fmaf(dk, c, ck);
         ck *= c;
       }
-      // over the wavefront's 8 rows (lanes 8 apart hold the same columns): lanes 0 .. 7 keep the sums
+      // over the wavefront's 8 rows (lanes 8 apart hold the same columns): lanes 0 .. 7 keep the sums; lanes 8
+      // apart by a DPP rotation of each row of 16 lanes by 8, then 16 and 32 apart by lane exchanges
 #pragma unroll
-      for (int o = 8; o < 64; o <<= 1)
-#pragma unroll
-        for (int u = 0; u < 4; ++u) dw[u] += __shfl_xor(dw[u], o, 64);
+      for (int u = 0; u < 4; ++u) {
+        dw[u] += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(dw[u]), 0x128, 0xf, 0xf, false));
+        dw[u] += __shfl_xor(dw[u], 16, 64);
+        dw[u] += __shfl_xor(dw[u], 32, 64);
+      }
     }
     if (sf || sv || sk) {  // uniform over the workgroup
       const float2 s2 = block_sum2_cols(df, dv, dw, sk, red, &redw[0][0]);
@@ -948,12 +1007,30 @@ __global__ __launch_bounds__(NT) void k_wmat_bwd_series(WArgs a) {
   for (int k = 0; k <= PW; ++k) gst4(a.hpart + ((size_t)blockIdx.x * (PW + 1) + k) * MM, H[k]);
 }
 
-// H_k summed over the workgroups' partials (float64, in order): a workgroup per (k, quarter of the entries)
+// H_k summed over the workgroups' partials (float64, a fixed order): a workgroup per (k, 64 entries); its four
+// wavefronts take the partials g = 4 q + w (two running sums each, even and odd q), then wavefront 0 adds the
+// eight sums in order
 __global__ __launch_bounds__(NT) void k_whsum(WArgs a, int nparts) {
-  const int k = blockIdx.x, e = blockIdx.y * NT + threadIdx.x;
-  double s = 0.0;
-  for (int g = 0; g < nparts; ++g) s += (double)a.hpart[((size_t)g * (PW + 1) + k) * MM + e];
-  a.hsum[(size_t)k * MM + e] = s;
+  __shared__ double red[NT / 64][2][64];
+  const int k = blockIdx.x, lane = threadIdx.x & 63, w = threadIdx.x >> 6, e = blockIdx.y * 64 + lane;
+  const float* src = a.hpart + (size_t)k * MM + e;
+  const size_t stride = (size_t)(PW + 1) * MM;
+  double s0 = 0.0, s1 = 0.0;
+  int g = w;
+  for (; g + 4 < nparts; g += 8) {
+    s0 += (double)src[(size_t)g * stride];
+    s1 += (double)src[(size_t)(g + 4) * stride];
+  }
+  if (g < nparts) s0 += (double)src[(size_t)g * stride];
+  red[w][0][lane] = s0;
+  red[w][1][lane] = s1;
+  __syncthreads();
+  if (w == 0) {
+    double s = 0.0;
+#pragma unroll
+    for (int q = 0; q < NT / 64; ++q) s += red[q][0][lane] + red[q][1][lane];
+    a.hsum[(size_t)k * MM + e] = s;
+  }
 }
 
 // dA of the series path (float64): R_{PW-1} = H_PW, R_i = H_{i+1} + R_{i+1} A^T, U_i = R_i + A^T U_{i+1},
@@ -1596,8 +1673,11 @@ __global__ __launch_bounds__(NT) void k_wadj_carry(WArgs a) {
 // Leaf adjoints, a workgroup per (slice of TL intervals, sample): dv per interval, the series leaf's dh and dA
 // (workgroup partial), the Van Loan leaf's (dP, dV) per interval (per-interval mode) or summed over the slice (shared
 // modes).
-template <int N, bool SER>
-__global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(4))) void k_wleaf_bwd(WArgs a) {
+// LK: the leaf (LK_SERIES, LK_VL_SHARED, LK_VL_INT: the Van Loan leaf with shared or per-interval step matrices),
+// one instantiation each so that each carries only its own registers
+constexpr int LK_SERIES = 0, LK_VL_SHARED = 1, LK_VL_INT = 2;
+template <int N, int LK>
+__global__ __launch_bounds__(NT) void k_wleaf_bwd(WArgs a) {
   extern __shared__ __align__(16) float sm[];  // lf_floats(rows, 4) (+ LF_EXTRA, per-interval Van Loan)
   float* A = sm + LF_A;
   float* S2b = sm + LF_S2;  // ds2
@@ -1616,9 +1696,7 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(4))) void k_
   float dA[4] = {0.0f, 0.0f, 0.0f, 0.0f};
   float sP[4] = {0.0f, 0.0f, 0.0f, 0.0f}, sV[4] = {0.0f, 0.0f, 0.0f, 0.0f};
   const float* th = a.clock + (size_t)b * a.L;
-  const bool vl = a.leaf == EWS_LEAF_VAN_LOAN;
-  const bool vl_shared = vl && a.vl_mode != EWS_FLOW_PER_INTERVAL;
-  const bool vl_int = SER;
+  constexpr bool vl = LK != LK_SERIES, vl_shared = LK == LK_VL_SHARED, vl_int = LK == LK_VL_INT;
   float* phi = sm + lf_floats(rows, 4);
   float* U = phi + LX_PHI;
   if (vl_int) {
@@ -1658,7 +1736,7 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(4))) void k_
     if constexpr (N >= 2) sld4(S2b, nd2);
     float dvi = 0.0f, dh = 0.0f;
     bool dv_done = false;  // dv of a series-path interval is k_wmat_bwd_series's
-    if (vl) {
+    if constexpr (vl) {
       float* P = sm + LF_P;
       float* V = sm + LF_V;
       const bool ser = vl_int && !(a.mflag[r] & 4);
@@ -1807,7 +1885,7 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(4))) void k_
       dvi = T4[i];
     }
     if (!dv_done && row_lead() && i < a.d) a.dv[r * DP + i] = dvi;
-    if (a.leaf != EWS_LEAF_VAN_LOAN) {
+    if constexpr (!vl) {
       // dh: the 32 partials of threads 0..31 (wavefront 0)
       float s = tid < 32 ? dh : 0.0f;
       if (tid < 64) {
@@ -2026,7 +2104,7 @@ int plan(const ews_dense_desc* s, WPlan& p) {
   p.exact_int = (p.fl_int && s->chen_expm == EWS_EXPM_EXACT) || (p.vl_int && s->vl_expm == EWS_EXPM_EXACT);
   p.exact_smp = (!p.fl_int && s->chen_expm == EWS_EXPM_EXACT) || (vl && !p.vl_int && s->vl_expm == EWS_EXPM_EXACT);
   p.g_int = p.mats_int ? std::min<long>((long)p.B * p.n, 256) : 0;
-  p.g_ser = p.mats_int ? std::min<long>((long)p.B * p.n, 256) : 0;
+  p.g_ser = p.mats_int ? std::min<long>((long)p.B * p.n, 512) : 0;  // two workgroups per CU
   p.g_smp = p.mats_smp ? p.B : 0;
   p.gy_int = p.fl_int && p.vl_int ? 2 : 1;
   p.gy_smp = !p.fl_int && vl && !p.vl_int ? 2 : 1;
@@ -2206,23 +2284,30 @@ int backward(const ews_dense_desc* s, const float* path, const float* clock, con
   WIDE_CHECK();
   const dim3 gc(p.C, p.B);
   const size_t lds_lb = (size_t)(lf_floats(p.rows, 4) + (p.vl_int ? LF_EXTRA : 0)) * 4;
-  const void* kb = p.N == 1 ? (p.vl_int ? reinterpret_cast<const void*>(&k_wleaf_bwd<1, true>)
-                                          : reinterpret_cast<const void*>(&k_wleaf_bwd<1, false>))
-                            : (p.vl_int ? reinterpret_cast<const void*>(&k_wleaf_bwd<2, true>)
-                                        : reinterpret_cast<const void*>(&k_wleaf_bwd<2, false>));
-  if (set_lds(kb, lds_lb) != EWS_OK) return EWS_ERR_LAUNCH;
+  const int lk = !p.vl ? LK_SERIES : p.vl_int ? LK_VL_INT : LK_VL_SHARED;
+  const void* kbs[2][3] = {{reinterpret_cast<const void*>(&k_wleaf_bwd<1, LK_SERIES>),
+                            reinterpret_cast<const void*>(&k_wleaf_bwd<1, LK_VL_SHARED>),
+                            reinterpret_cast<const void*>(&k_wleaf_bwd<1, LK_VL_INT>)},
+                           {reinterpret_cast<const void*>(&k_wleaf_bwd<2, LK_SERIES>),
+                            reinterpret_cast<const void*>(&k_wleaf_bwd<2, LK_VL_SHARED>),
+                            reinterpret_cast<const void*>(&k_wleaf_bwd<2, LK_VL_INT>)}};
+  if (set_lds(kbs[p.N - 1][lk], lds_lb) != EWS_OK) return EWS_ERR_LAUNCH;
   if (p.N == 1) {
     hipLaunchKernelGGL((k_wadj<1, ADJ_LOCAL>), gc, dim3(NT), 0, st, a);
     hipLaunchKernelGGL(k_wadj_carry<1>, dim3(p.B), dim3(NT), 0, st, a);
     hipLaunchKernelGGL((k_wadj<1, ADJ_FULL>), gc, dim3(NT), 0, st, a);
-    if (p.vl_int) hipLaunchKernelGGL((k_wleaf_bwd<1, true>), dim3(p.NSL, p.B), dim3(NT), lds_lb, st, a);
-    else hipLaunchKernelGGL((k_wleaf_bwd<1, false>), dim3(p.NSL, p.B), dim3(NT), lds_lb, st, a);
+    if (lk == LK_SERIES) hipLaunchKernelGGL((k_wleaf_bwd<1, LK_SERIES>), dim3(p.NSL, p.B), dim3(NT), lds_lb, st, a);
+    else if (lk == LK_VL_SHARED)
+      hipLaunchKernelGGL((k_wleaf_bwd<1, LK_VL_SHARED>), dim3(p.NSL, p.B), dim3(NT), lds_lb, st, a);
+    else hipLaunchKernelGGL((k_wleaf_bwd<1, LK_VL_INT>), dim3(p.NSL, p.B), dim3(NT), lds_lb, st, a);
   } else {
     hipLaunchKernelGGL((k_wadj<2, ADJ_LOCAL>), gc, dim3(NT), 0, st, a);
     hipLaunchKernelGGL(k_wadj_carry<2>, dim3(p.B), dim3(NT), 0, st, a);
     hipLaunchKernelGGL((k_wadj<2, ADJ_FULL>), gc, dim3(NT), 0, st, a);
-    if (p.vl_int) hipLaunchKernelGGL((k_wleaf_bwd<2, true>), dim3(p.NSL, p.B), dim3(NT), lds_lb, st, a);
-    else hipLaunchKernelGGL((k_wleaf_bwd<2, false>), dim3(p.NSL, p.B), dim3(NT), lds_lb, st, a);
+    if (lk == LK_SERIES) hipLaunchKernelGGL((k_wleaf_bwd<2, LK_SERIES>), dim3(p.NSL, p.B), dim3(NT), lds_lb, st, a);
+    else if (lk == LK_VL_SHARED)
+      hipLaunchKernelGGL((k_wleaf_bwd<2, LK_VL_SHARED>), dim3(p.NSL, p.B), dim3(NT), lds_lb, st, a);
+    else hipLaunchKernelGGL((k_wleaf_bwd<2, LK_VL_INT>), dim3(p.NSL, p.B), dim3(NT), lds_lb, st, a);
   }
   WIDE_CHECK();
   const long base = (long)p.B * p.NSL;
@@ -2232,7 +2317,7 @@ int backward(const ews_dense_desc* s, const float* path, const float* clock, con
       return EWS_ERR_LAUNCH;
     hipLaunchKernelGGL(k_wmat_bwd_series, dim3((unsigned)p.g_ser), dim3(NT), 0, st, a);
     hipLaunchKernelGGL(k_wmat_bwd, dim3((unsigned)p.g_int, p.gy_int), dim3(NT), lds, st, a, 2, base);
-    hipLaunchKernelGGL(k_whsum, dim3(PW + 1, MM / NT), dim3(NT), 0, st, a, (int)p.g_ser);
+    hipLaunchKernelGGL(k_whsum, dim3(PW + 1, MM / 64), dim3(NT), 0, st, a, (int)p.g_ser);
     hipLaunchKernelGGL(k_wseries_dA, dim3(1), dim3(NT), 0, st, a,
                        base + p.g_int * p.gy_int + p.g_smp * p.gy_smp);
     WIDE_CHECK();
