@@ -3264,7 +3264,7 @@ int ews_dense_forward(const ews_dense_desc* desc, const float* path, const float
 
 int ews_dense_forward_keep(const ews_dense_desc* desc, const float* path, const float* clock, const float* A,
                            float* out, void* workspace, ews_stream_t stream) {
-  // d > 16: nothing is kept (the backward recomputes), the forward runs in the backward's workspace
+  // d > 16: the forward runs in the backward's workspace, and ews_dense_backward_kept starts from what it left
   if (ews::wide::eligible(desc))
     return ews::wide::forward(desc, path, clock, A, out, workspace, true, (hipStream_t)stream);
   DPlan p;
@@ -3394,8 +3394,8 @@ int ews_dense_backward(const ews_dense_desc* desc, const float* path, const floa
                        const float* grad_out, float* grad_path, float* grad_clock, float* grad_A, void* workspace,
                        ews_stream_t stream) {
   if (ews::wide::eligible(desc))
-    return ews::wide::backward(desc, path, clock, A, grad_out, grad_path, grad_clock, grad_A, workspace,
-                          (hipStream_t)stream);
+    return ews::wide::backward(desc, path, clock, A, grad_out, grad_path, grad_clock, grad_A, workspace, false,
+                               (hipStream_t)stream);
   DPlan p;
   const int rc = dense_plan(desc, p);
   if (rc != EWS_OK) return rc;
@@ -3415,8 +3415,8 @@ int ews_dense_backward_kept(const ews_dense_desc* desc, const float* path, const
                             const float* out, const float* grad_out, float* grad_path, float* grad_clock,
                             float* grad_A, void* workspace, ews_stream_t stream) {
   if (ews::wide::eligible(desc))
-    return ews::wide::backward(desc, path, clock, A, grad_out, grad_path, grad_clock, grad_A, workspace,
-                          (hipStream_t)stream);
+    return ews::wide::backward(desc, path, clock, A, grad_out, grad_path, grad_clock, grad_A, workspace, true,
+                               (hipStream_t)stream);
   DPlan p;
   const int rc = dense_plan(desc, p);
   if (rc != EWS_OK) return rc;

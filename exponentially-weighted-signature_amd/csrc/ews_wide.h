@@ -55,8 +55,11 @@ bool eligible(const ews_dense_desc* s);
 size_t workspace_bytes(const ews_dense_desc* s, bool backward);
 int forward(const ews_dense_desc* s, const float* path, const float* clock, const float* A, float* out,
             void* workspace, bool backward_layout, hipStream_t st);
+// kept: the workspace holds what forward(.., backward_layout = true, ..) wrote for the same inputs (the step
+// matrices, local terms, chunk summaries and carries, padded prefix states and the maxima's rows); else the backward
+// runs that forward first
 int backward(const ews_dense_desc* s, const float* path, const float* clock, const float* A, const float* grad_out,
-             float* grad_path, float* grad_clock, float* grad_A, void* workspace, hipStream_t st);
+             float* grad_path, float* grad_clock, float* grad_A, void* workspace, bool kept, hipStream_t st);
 
 }  // namespace wide
 }  // namespace ews

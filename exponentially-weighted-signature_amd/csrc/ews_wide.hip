@@ -1150,20 +1150,6 @@ __device__ void knot_sums(int M, const float* D, float* Y, float* Z, float* s1) 
 __device__ __forceinline__ float inv_f(int n) { return 1.0f / (float)n; }
 __device__ __forceinline__ float c2coef(int p, int r) { return 1.0f / ((float)(p + r + 2) * (float)(r + 1)); }
 
-// the step matrices of the interval's Van Loan leaf into P, V (LDS)
-__device__ __forceinline__ void load_vl(const WArgs& a, int b, int t, float* P, float* V) {
-  bool fixed;
-  vl_step(a, a.clock + (size_t)b * a.L, t, fixed);
-  if (fixed && a.vl_mode != EWS_FLOW_PER_INTERVAL) {
-    set_ident32(P, 1.0f);
-    set_ident32(V, 1.0f);
-    return;
-  }
-  const size_t item = a.vl_mode == EWS_FLOW_PER_INTERVAL ? (size_t)b * a.n + t : (size_t)b;
-  sld4(P, gld4(a.vlm + item * 2 * MM));
-  sld4(V, gld4(a.vlm + item * 2 * MM + MM));
-}
-
 // knots of the interval: Delta_M = V w, Delta_{m-1} = P Delta_m (rows 0 .. M-1 of D hold Delta_1 .. Delta_M),
 // w = v / M in wv
 __device__ void vl_knots(const WArgs& a, const float* P, const float* V, const float* wv, float* D) {
@@ -1178,30 +1164,21 @@ __device__ void vl_knots(const WArgs& a, const float* P, const float* V, const f
   }
 }
 
-// interval's local terms (s1 into s1v, s2 into the thread's registers)
+// interval's local terms (s1 into s1v, s2 into the thread's registers) from its inputs staged in LDS: the increment
+// (divided by M for the Van Loan leaf) in vec; P, V (the Van Loan leaf off the series path) or u_k (on it, ser)
 template <int N>
-__device__ void leaf_fwd(const WArgs& a, float* sm, int b, int t, float* s1v, float* s2r, bool ser) {
-  float* A = sm + LF_A;
+__device__ void leaf_fwd(const WArgs& a, float* sm, float h, float* s1v, float* s2r, bool ser) {
   float* vec = sm + LF_VEC;
   float* T1 = sm + LF_TAB;
   float* T2 = T1 + (a.leaf == EWS_LEAF_VAN_LOAN ? a.vm : a.q + 1) * 32;
   const int tid = threadIdx.x, i = tid >> 3, j0 = (tid & 7) * 4;
-  const float* x = a.path + ((size_t)b * a.L + t) * a.d;
-  const float* th = a.clock + (size_t)b * a.L;
   if (a.leaf == EWS_LEAF_VAN_LOAN) {
-    float* P = sm + LF_P;
-    float* V = sm + LF_V;
-    float* phi = sm + lf_floats(a.vm, 2);
     if (ser) {
-      const float* u = a.ubuf + ((size_t)b * a.n + t) * (PW + 1) * 32;
-      for (int e = tid; e < (PW + 1) * 32; e += NT) phi[LX_PHI + e] = u[e];
+      float* phi = sm + lf_floats(a.vm, 2);
+      series_knots(a.vm, phi, phi + LX_PHI, T1, h / (float)a.vm);
     } else {
-      load_vl(a, b, t, P, V);
-      if (tid < 32) vec[tid] = tid < a.d ? (x[a.d + tid] - x[tid]) / (float)a.vm : 0.0f;
+      vl_knots(a, sm + LF_P, sm + LF_V, vec, T1);
     }
-    __syncthreads();
-    if (ser) series_knots(a.vm, phi, phi + LX_PHI, T1, (th[t + 1] - th[t]) / (float)a.vm);
-    else vl_knots(a, P, V, vec, T1);
     const int M = a.vm;
     knot_sums(M, T1, T2, nullptr, s1v);  // s1 and Y_m = Pre_m + Delta_m / 2
     __syncthreads();
@@ -1220,8 +1197,8 @@ __device__ void leaf_fwd(const WArgs& a, float* sm, int b, int t, float* s1v, fl
   } else {
     // letters b_p (rows of T1), u_p = sum_{r <= q-p} C2[p][r] b_r (rows of T2)
     const int q = a.q;
-    const float h = th[t + 1] - th[t];
-    if (tid < 32) T1[tid] = tid < a.d ? x[a.d + tid] - x[tid] : 0.0f;
+    float* A = sm + LF_A;
+    if (tid < 32) T1[tid] = vec[tid];
     __syncthreads();
     for (int p = 1; p <= q; ++p) {
       const float y = mv<false>(A, T1 + (p - 1) * 32);
@@ -1257,24 +1234,79 @@ __device__ void leaf_fwd(const WArgs& a, float* sm, int b, int t, float* s1v, fl
 }
 
 // SER: the per-interval Van Loan leaf, whose knots may take the series path (a separate instantiation keeps the
-// other leaves' register count low)
+// other leaves' register count low). Each interval's inputs are loaded into registers during the interval before.
 template <int N, bool SER>
 __global__ __launch_bounds__(NT) void k_wleaf(WArgs a) {
   extern __shared__ __align__(16) float sm[];  // lf_floats(rows, 2) (+ LF_EXTRA, per-interval Van Loan)
+  float* vec = sm + LF_VEC;
   float* s1v = sm + LF_VEC + 32;
+  float* P = sm + LF_P;
+  float* V = sm + LF_V;
+  float* Ub = sm + lf_floats(a.vm, 2) + LX_PHI;  // u_k (SER)
+  const int tid = threadIdx.x;
   load_A(a.d, a.A, sm + LF_A);
   if (SER) {  // the knots' coefficients of the series path
     float* phi = sm + lf_floats(a.vm, 2);
-    for (int e = threadIdx.x; e < a.vm * (PW + 1); e += NT) phi[e] = a.apow[PHI_OFF + e];
+    for (int e = tid; e < a.vm * (PW + 1); e += NT) phi[e] = a.apow[PHI_OFF + e];
   }
-  __syncthreads();
+  const bool vl = a.leaf == EWS_LEAF_VAN_LOAN;
+  const bool vl_int = vl && a.vl_mode == EWS_FLOW_PER_INTERVAL;
   const long items = (long)a.B * a.n;
-  for (long it = blockIdx.x; it < items; it += gridDim.x) {
+  float nv = 0.0f, nh = 0.0f, nU[3] = {0.0f, 0.0f, 0.0f};  // (PW + 1) * 32 <= 3 NT
+  float4 nP = float4{0.0f, 0.0f, 0.0f, 0.0f}, nV = nP;
+  bool nser = false, nfixed = false;
+  auto fetch = [&](long it) {
     const int b = (int)(it / a.n), t = (int)(it - (long)b * a.n);
+    const float* x = a.path + ((size_t)b * a.L + t) * a.d;
+    const float* th = a.clock + (size_t)b * a.L;
+    if (tid < 32) nv = tid < a.d ? x[a.d + tid] - x[tid] : 0.0f;
+    nh = th[t + 1] - th[t];
+    if (vl) {
+      nser = SER && !(a.mflag[it] & 4);
+      if (nser) {
+#pragma unroll
+        for (int k = 0; k < 3; ++k) {
+          const int e = tid + k * NT;
+          nU[k] = e < (PW + 1) * 32 ? a.ubuf[it * (PW + 1) * 32 + e] : 0.0f;
+        }
+      } else {
+        bool fixed;
+        vl_step(a, th, t, fixed);
+        nfixed = fixed && !vl_int;
+        if (!nfixed) {
+          const size_t item = vl_int ? (size_t)it : (size_t)b;
+          nP = gld4(a.vlm + item * 2 * MM);
+          nV = gld4(a.vlm + item * 2 * MM + MM);
+        }
+      }
+    }
+  };
+  if ((long)blockIdx.x < items) fetch(blockIdx.x);
+  for (long it = blockIdx.x; it < items; it += gridDim.x) {
+    const bool ser = nser;
+    const float h = nh;
+    if (tid < 32) vec[tid] = vl ? nv / (float)a.vm : nv;
+    if (vl) {
+      if (ser) {
+#pragma unroll
+        for (int k = 0; k < 3; ++k) {
+          const int e = tid + k * NT;
+          if (e < (PW + 1) * 32) Ub[e] = nU[k];
+        }
+      } else if (nfixed) {
+        set_ident32(P, 1.0f);
+        set_ident32(V, 1.0f);
+      } else {
+        sld4(P, nP);
+        sld4(V, nV);
+      }
+    }
+    __syncthreads();
+    if (it + gridDim.x < items) fetch(it + gridDim.x);
     float s2r[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-    leaf_fwd<N>(a, sm, b, t, s1v, s2r, SER && !(a.mflag[it] & 4));
+    leaf_fwd<N>(a, sm, h, s1v, s2r, ser);
     float* row = a.loc + it * RW;
-    if (threadIdx.x < 32) row[threadIdx.x] = s1v[threadIdx.x];
+    if (tid < 32) row[tid] = s1v[tid];
     if constexpr (N >= 2) gst4(row + DP, acc4(s2r));
     __syncthreads();
   }
@@ -1707,6 +1739,7 @@ __global__ __launch_bounds__(NT) void k_wleaf_bwd(WArgs a) {
   float nd1 = 0.0f, nv = 0.0f;
   float4 nd2 = float4{0.0f, 0.0f, 0.0f, 0.0f}, nP = nd2, nV = nd2;
   float nU[3] = {0.0f, 0.0f, 0.0f};  // (PW + 1) * 32 <= 3 NT
+  bool nfixed = false;
   auto fetch = [&](int t) {
     const size_t r = (size_t)b * a.n + t;
     const float* x = a.path + ((size_t)b * a.L + t) * a.d;
@@ -1723,6 +1756,12 @@ __global__ __launch_bounds__(NT) void k_wleaf_bwd(WArgs a) {
     } else if (vl_int) {
       nP = gld4(a.vlm + r * 2 * MM);
       nV = gld4(a.vlm + r * 2 * MM + MM);
+    } else if (vl_shared) {
+      vl_step(a, th, t, nfixed);
+      if (!nfixed) {
+        nP = gld4(a.vlm + (size_t)b * 2 * MM);
+        nV = gld4(a.vlm + (size_t)b * 2 * MM + MM);
+      }
     }
   };
   if (t0 < t1) fetch(t0);
@@ -1740,8 +1779,9 @@ __global__ __launch_bounds__(NT) void k_wleaf_bwd(WArgs a) {
       float* P = sm + LF_P;
       float* V = sm + LF_V;
       const bool ser = vl_int && !(a.mflag[r] & 4);
-      if (vl_shared) {
-        load_vl(a, b, t, P, V);
+      if (vl_shared && nfixed) {
+        set_ident32(P, 1.0f);
+        set_ident32(V, 1.0f);
       } else if (!ser) {
         sld4(P, nP);
         sld4(V, nV);
@@ -2265,14 +2305,14 @@ int forward(const ews_dense_desc* s, const float* path, const float* clock, cons
 }
 
 int backward(const ews_dense_desc* s, const float* path, const float* clock, const float* A, const float* grad_out,
-             float* grad_path, float* grad_clock, float* grad_A, void* workspace, hipStream_t st) {
+             float* grad_path, float* grad_clock, float* grad_A, void* workspace, bool kept, hipStream_t st) {
   WPlan p;
   const int rc = plan(s, p);
   if (rc != EWS_OK) return rc;
   if (!path || !clock || !A || !grad_out || !grad_path || !grad_A || !workspace) return EWS_ERR_NULL;
   const WLay w = layout(s, p, true);
   WArgs a = make_args(s, p, path, clock, A, nullptr, workspace, true);
-  {  // the forward again, with the padded prefix states kept (and the rows of the maxima of the max readout)
+  if (!kept) {  // the forward again, with the padded prefix states kept (and the rows of the maxima of the max readout)
     WArgs f = a;
     if (s->readout == EWS_READOUT_MAX) f.out = (float*)((char*)workspace + w.outs);
     else f.readout = -1;  // no output: the states go to the workspace only

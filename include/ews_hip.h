@@ -224,11 +224,10 @@ int ews_dense_backward(const ews_dense_desc* desc, const float* path, const floa
                        const float* grad_out, float* grad_path, float* grad_clock, float* grad_A, void* workspace,
                        ews_stream_t stream);
 
-/* The same forward and backward with the forward's intermediates kept for the backward instead of recomputed
- * (for d > 16 nothing is kept: the _keep forward is the plain one on the backward's workspace and the _kept
- * backward recomputes); the residuals a custom VJP keeps between its two halves (pallas_combine.py:2360-2565) are
- * here the leaf, the flows, the chunk summaries and carries: about B (L-1) (sum_k d^k + 256) floats, 1.2 GB at
- * c3's shape.
+/* The same forward and backward with the forward's intermediates kept for the backward instead of recomputed;
+ * the residuals a custom VJP keeps between its two halves (pallas_combine.py:2360-2565) are here the leaf, the
+ * flows, the chunk summaries and carries: about B (L-1) (sum_k d^k + 256) floats, 1.2 GB at c3's shape (for
+ * 16 < d <= 32 also the padded prefix states, 32 x 33 floats per interval, and the per-interval step matrices).
  * ews_dense_forward_keep is ews_dense_forward on a workspace of ews_dense_backward_workspace_bytes(desc) bytes;
  * ews_dense_backward_kept is ews_dense_backward on that workspace, unchanged since, with the same desc and inputs:
  * it skips the recompute (at c3, 1.3 ms of the backward) and overwrites the kept data (one backward per forward).

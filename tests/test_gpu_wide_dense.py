@@ -164,6 +164,38 @@ def test_wide_backward_is_deterministic():
         assert torch.equal(x, y), f"{name} gradient differs between two identical calls"
 
 
+KEPT_CASES = [
+    # d, readout, mode, leaf kw
+    (24, "max", "displacement", dict(van_loan_expm="cayley", M=6)),
+    (17, "terminal", "displacement_uniform", dict(van_loan_expm="euler", chen_expm="cayley")),
+    (20, "mean", "displacement_uniform_basepoint", dict(leaf="series", series_q=5, chen_expm="pade")),
+]
+
+
+@pytest.mark.parametrize("case", KEPT_CASES, ids=[f"d{c[0]}-{c[1]}-{c[2]}" for c in KEPT_CASES])
+def test_wide_kept_backward_equals_recomputing(case):
+    """ews_dense_backward_kept starts from what ews_dense_forward_keep left in the workspace (step matrices, local
+    terms, chunk summaries and carries, prefix states, the maxima's rows); ews_dense_backward recomputes them. The
+    same kernels on the same data: the gradients agree bit for bit, and the kept forward's output with the plain
+    forward's."""
+    d, readout, mode, kw = case
+    path, clock, A = _inputs(2, 50, d, seed=d + 3)
+    leaf = _leaf(kw, mode)
+    gout = None
+    res = []
+    for keep in (True, False):
+        p = path.float().to(DEV).requires_grad_(True)
+        c = clock.float().to(DEV).requires_grad_(True)
+        a = A.float().to(DEV).requires_grad_(True)
+        out = ops.dense_scan(p, c, a, 2, leaf.q, _FLOW[mode], readout, True, chunk=8, leaf=leaf, keep=keep)
+        if gout is None:
+            gout = torch.randn(out.shape, generator=torch.Generator().manual_seed(5)).to(DEV)
+        out.backward(gout)
+        res.append((out.detach().clone(), p.grad.clone(), c.grad.clone(), a.grad.clone()))
+    for name, x, y in zip(("out", "path", "clock", "A"), res[0], res[1]):
+        assert torch.equal(x, y), f"{name}: kept and recomputing backward differ"
+
+
 @pytest.mark.parametrize("readout", ["prefix", "mean"])
 def test_wide_logews(readout):
     """LogEWS over a dense d = 20 generator at depth 2: the wide kernels' rows, then the log and Lyndon compression
