@@ -31,6 +31,7 @@
 #include <hip/hip_runtime.h>
 
 #include "ews_hip.h"
+#include "ews_lanes.h"
 #include "ews_wide.h"
 
 namespace ews {
@@ -1399,13 +1400,11 @@ __global__ __launch_bounds__(256, 2) void k_adj(AdjSeq s) {
         R2[ri * RP + rj] = l2 + r2;
         v = fmaf(l2, s1s[rj], v);
       }
-#pragma unroll
-      for (int o = 1; o < 16; o <<= 1) v += __shfl_xor(v, o, 64);
+      v = lanes::sum16(v);
       if (rj == 0) R1[ri] = L1[ri] + v;
       if constexpr (EMIT) {
         float m = Ms[ri * 16 + rj] * S1s[rj];
-#pragma unroll
-        for (int o = 1; o < 16; o <<= 1) m += __shfl_xor(m, o, 64);
+        m = lanes::sum16(m);
         if (rj == 0) y1s[ri] = m;
         if constexpr (N >= 2) {
           float a = 0.0f, bt = 0.0f;
@@ -2078,8 +2077,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(EXACTF ? 3 
     if (tid < 16) o.dv[((size_t)b * a.n_int + t) * 16 + tid] = dB[0][tid];
     {
       float v = dhl;  // nonzero in lanes 0 .. 15 of wavefront 0
-#pragma unroll
-      for (int o2 = 1; o2 < 16; o2 <<= 1) v += __shfl_xor(v, o2, 64);
+      v = lanes::sum16(v);
       if (tid == 0) red[4] = v;
     }
     __syncthreads();
@@ -2233,11 +2231,8 @@ __global__ __launch_bounds__(256) void k_vl_bwd(Args a, LeafBwd o) {
         const float yi = Ys[m][i], xi = Xs[m][i];
         // over the last index (lanes j of a row i): dY_m[i], dX_m[i]
         float py = q * Rs[m][j], px = 0.5f * q * Dl[m][j];
-#pragma unroll
-        for (int o2 = 1; o2 < 16; o2 <<= 1) {
-          py += __shfl_xor(py, o2, 64);
-          px += __shfl_xor(px, o2, 64);
-        }
+        py = lanes::sum16(py);
+        px = lanes::sum16(px);
         // over the first index (rows i of the wave, then the four wavefronts' partials in a fixed order):
         // dR_m[j], dDelta_m[j]
         float pr2 = q * yi, pd = fmaf(0.5f * q, xi, fmaf(yi, e1, 0.5f * xi * f1));
@@ -2304,8 +2299,7 @@ __global__ __launch_bounds__(256) void k_vl_bwd(Args a, LeafBwd o) {
     GVm[tid] = lam[i] * wv[j];
     {
       float u = Vm[j * 16 + i] * lam[j];  // (V^T lambda)[i]
-#pragma unroll
-      for (int o2 = 1; o2 < 16; o2 <<= 1) u += __shfl_xor(u, o2, 64);
+      u = lanes::sum16(u);
       if (j == 0) o.dv[((size_t)b * a.n_int + t) * 16 + i] = u / (float)Mv;
     }
     __syncthreads();

@@ -28,6 +28,7 @@
 
 #include "ews_args.h"
 #include "ews_hip.h"
+#include "ews_lanes.h"
 #include "ews_numerics.h"
 #include "ews_pairs.h"
 #include "ews_seq.h"
@@ -297,8 +298,6 @@ __device__ __forceinline__ void stT(float* p, cf v) {
 }
 __device__ __forceinline__ void stT(float* p, float v) { p[0] = v; }
 // value of the lane tid ^ o of the wavefront
-__device__ __forceinline__ float xor_lane(float v, int o) { return __shfl_xor(v, o, 64); }
-__device__ __forceinline__ cf xor_lane(cf v, int o) { return cf{__shfl_xor(v.re, o, 64), __shfl_xor(v.im, o, 64)}; }
 
 // Output row element indices of the lane's values (level 1 of plane j; the level-2 block (j, k)).
 template <bool CPLX>
@@ -1301,19 +1300,12 @@ __device__ __forceinline__ float wave_sum(float v) {
   for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o, 64);
   return v;
 }
-// sums over k (lanes 8j .. 8j+7) and over j (lanes k, k+8, ..)
-__device__ __forceinline__ float row_sum8(float v) {
-  v += __shfl_xor(v, 1, 64);
-  v += __shfl_xor(v, 2, 64);
-  v += __shfl_xor(v, 4, 64);
-  return v;
-}
-__device__ __forceinline__ float col_sum8(float v) {
-  v += __shfl_xor(v, 8, 64);
-  v += __shfl_xor(v, 16, 64);
-  v += __shfl_xor(v, 32, 64);
-  return v;
-}
+// sums over k (lanes 8j .. 8j+7) and over j (lanes k, k+8, ..), by DPP where the lanes share a row of 16
+__device__ __forceinline__ float row_sum8(float v) { return lanes::sum8(v); }
+__device__ __forceinline__ float col_sum8(float v) { return lanes::colsum8(v); }
+// sum over each aligned group of n lanes (n a power of two up to 64)
+__device__ __forceinline__ float group_sum(float v, int n) { return lanes::sum_n(v, n); }
+__device__ __forceinline__ cf group_sum(cf v, int n) { return cf{lanes::sum_n(v.re, n), lanes::sum_n(v.im, n)}; }
 __device__ __forceinline__ cf row_sum8(cf v) { return cf{row_sum8(v.re), row_sum8(v.im)}; }
 __device__ __forceinline__ cf col_sum8(cf v) { return cf{col_sum8(v.re), col_sum8(v.im)}; }
 
@@ -1548,17 +1540,13 @@ __device__ __forceinline__ void bwd_step(const DiagArgs& a, const LaneMap& m, co
             rowP = toPj;
             stT(s_cS + 2 * (m.k * a.K + m.j), toS);
             stT(s_cP + 2 * (m.k * a.K + m.j), toPk);
-            for (int o = 1; o < a.K; o <<= 1) {
-              rowC += xor_lane(rowC, o);
-              rowP += xor_lane(rowP, o);
-            }
+            rowC = group_sum(rowC, a.K);
+            rowP = group_sum(rowP, a.K);
             __syncthreads();
             colS = ldT<CPLX, T>(s_cS + 2 * tid);
             colP = ldT<CPLX, T>(s_cP + 2 * tid);
-            for (int o = 1; o < a.K; o <<= 1) {
-              colS += xor_lane(colS, o);
-              colP += xor_lane(colP, o);
-            }
+            colS = group_sum(colS, a.K);
+            colP = group_sum(colP, a.K);
           } else {
             if (m.active) {
               stT(s_rC + 2 * tid, toC);
@@ -1581,12 +1569,10 @@ __device__ __forceinline__ void bwd_step(const DiagArgs& a, const LaneMap& m, co
                 colP += ldT<CPLX, T>(s_cP + 2 * (m.j * a.K + kk));
               }
             }
-            for (int o = 1; o < R; o <<= 1) {
-              rowC += xor_lane(rowC, o);
-              rowP += xor_lane(rowP, o);
-              colS += xor_lane(colS, o);
-              colP += xor_lane(colP, o);
-            }
+            rowC = group_sum(rowC, R);
+            rowP = group_sum(rowP, R);
+            colS = group_sum(colS, R);
+            colP = group_sum(colP, R);
           }
         }
         if (m.plane) {

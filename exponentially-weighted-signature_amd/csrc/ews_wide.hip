@@ -48,10 +48,13 @@
 #include <type_traits>
 
 #include "ews_hip.h"
+#include "ews_lanes.h"
 #include "ews_wide.h"
 
 namespace ews {
 namespace wide {
+using lanes::colsum8;
+using lanes::sum8;
 
 constexpr int DP = 32;            // padded channels
 constexpr int MM = DP * DP;       // floats of a padded matrix in global memory (row-major, pitch 32)
@@ -135,18 +138,8 @@ __device__ __forceinline__ float4 f4add(float4 a, float4 b) {
 }
 __device__ __forceinline__ float4 acc4(const float* a) { return float4{a[0], a[1], a[2], a[3]}; }
 
-// sum over each aligned group of 8 lanes, every lane returning it: DPP quad permutations [1,0,3,2] and [2,3,0,1]
-// give each lane its quad's sum, then the half-row mirror (lane l of 8 reads lane 7 - l, in the other quad) adds
-// the other quad's; all on the VALU, no LDS round trip
-__device__ __forceinline__ float sum8(float v) {
-  v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0xB1, 0xf, 0xf, false));
-  v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x4E, 0xf, 0xf, false));
-  v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x141, 0xf, 0xf, false));
-  return v;
-}
-
 // y[i] = sum_k M(i, k) x[k] (M(i, k) = M[k][i] when TM), 32 x 32 in LDS: the 8 lanes of row i each take four k and
-// sum them (sum8); every lane of the row returns y[i]
+// sum them (a DPP sum over the 8 lanes); every lane of the row returns y[i]
 template <bool TM>
 __device__ __forceinline__ float mv(const float* M, const float* x) {
   const int i = (int)threadIdx.x >> 3, p = ((int)threadIdx.x & 7) * 4;
@@ -980,14 +973,9 @@ __global__ __launch_bounds__(NT) void k_wmat_bwd_series(WArgs a) {
         dk = fmaf(dk, c, ck);
         ck *= c;
       }
-      // over the wavefront's 8 rows (lanes 8 apart hold the same columns): lanes 0 .. 7 keep the sums; lanes 8
-      // apart by a DPP rotation of each row of 16 lanes by 8, then 16 and 32 apart by lane exchanges
+      // over the wavefront's 8 rows (lanes 8 apart hold the same columns): lanes 0 .. 7 keep the sums
 #pragma unroll
-      for (int u = 0; u < 4; ++u) {
-        dw[u] += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(dw[u]), 0x128, 0xf, 0xf, false));
-        dw[u] += __shfl_xor(dw[u], 16, 64);
-        dw[u] += __shfl_xor(dw[u], 32, 64);
-      }
+      for (int u = 0; u < 4; ++u) dw[u] = colsum8(dw[u]);
     }
     if (sf || sv || sk) {  // uniform over the workgroup
       const float2 s2 = block_sum2_cols(df, dv, dw, sk, red, &redw[0][0]);
