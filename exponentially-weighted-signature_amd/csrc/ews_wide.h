@@ -28,7 +28,7 @@ struct WArgs {
   float* rows;  // padded prefix states (B, n), when kept
   int* amax;    // max readout: row of the maximum per (sample, column)
   // backward workspace
-  float* grow;   // row cotangents (B, n)
+  const float* gout;  // the readout's cotangent (packed rows of W)
   float* mu;     // each chunk's own cotangent on its carry-in state (B, C)
   float* lend;   // cotangent on each chunk's end state from the later chunks (B, C)
   float* dloc;   // local-term cotangents (B, n)

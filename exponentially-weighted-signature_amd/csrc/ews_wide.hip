@@ -1501,33 +1501,6 @@ __global__ __launch_bounds__(NT) void k_wreadout(WArgs a) {
 }
 
 // ------------------------------------------------------------------------------------------------ backward
-// row cotangents g (B, n, RW) padded from the readout's cotangent
-__global__ __launch_bounds__(NT) void k_wgrows(WArgs a, const float* gout) {
-  const long total = (long)a.B * a.n * RW;
-  for (long e = (long)blockIdx.x * NT + threadIdx.x; e < total; e += (long)gridDim.x * NT) {
-    const int pe = (int)(e % RW);
-    const long r = e / RW;
-    const int b = (int)(r / a.n), t = (int)(r - (long)b * a.n);
-    const int d = a.d;
-    int col = -1;  // packed column of the padded entry
-    if (pe < DP) {
-      if (pe < d) col = pe;
-    } else {
-      const int q = pe - DP, ri = q >> 5, ci = q & 31;
-      if (a.N >= 2 && ri < d && ci < d) col = d + ri * d + ci;
-    }
-    float g = 0.0f;
-    if (col >= 0) {
-      col += a.lvl0;
-      if (a.readout == EWS_READOUT_PREFIX) g = gout[r * a.W + col];
-      else if (a.readout == EWS_READOUT_TERMINAL) g = t == a.n - 1 ? gout[(size_t)b * a.W + col] : 0.0f;
-      else if (a.readout == EWS_READOUT_MEAN) g = gout[(size_t)b * a.W + col] / (float)a.n;
-      else g = a.amax[(size_t)b * a.W + col] == t ? gout[(size_t)b * a.W + col] : 0.0f;
-    }
-    a.grow[e] = g;
-  }
-}
-
 // adjoint scan LDS (floats): F, Ft, lambda2, S2 (state before the step), H, G1, G2 (32 x 36 each); vectors
 constexpr int AD_F = 0, AD_FT = S32, AD_L2 = 2 * S32, AD_S2 = 3 * S32, AD_H = 4 * S32, AD_G1 = 5 * S32,
               AD_G2 = 6 * S32, AD_VEC = 7 * S32;  // lambda1, S1, s1, y1, rho1 (32 each)
@@ -1612,17 +1585,62 @@ __global__ __launch_bounds__(NT) void k_wadj(WArgs a) {
   }
   const bool cached = a.flow_mode != EWS_FLOW_PER_INTERVAL;
   v4f dfs = zero4();  // shared-flow cotangent summed over the chunk's steps (the lane's tile entries)
+  // The row cotangents come from the readout's cotangent (packed rows of W): the thread's level-1 entry (threads
+  // below d) and its four level-2 entries (row i, columns j0 .. j0 + 3), zero in the padding. Prefix: row t of
+  // gout; mean: gout / n at every step; terminal: gout at the last step; max: gout where the maximum's row is t.
+  const int ri = trow<32>(), rj0 = tcol<32>(), d = a.d;
+  const bool ok1 = (int)threadIdx.x < d;
+  const int col1 = a.lvl0 + (int)threadIdx.x;
+  bool ok2[4];
+  int col2[4];
+#pragma unroll
+  for (int u = 0; u < 4; ++u) {
+    ok2[u] = N >= 2 && ri < d && rj0 + u < d;
+    col2[u] = a.lvl0 + d + ri * d + rj0 + u;
+  }
+  float k1 = 0.0f, k2[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+  int am1 = -1, am2[4] = {-1, -1, -1, -1};
+  if (a.readout != EWS_READOUT_PREFIX) {  // one cotangent row per sample
+    const float* g = a.gout + (size_t)b * a.W;
+    if (ok1) k1 = a.readout == EWS_READOUT_MEAN ? g[col1] / (float)a.n : g[col1];
+#pragma unroll
+    for (int u = 0; u < 4; ++u)
+      if (ok2[u]) k2[u] = a.readout == EWS_READOUT_MEAN ? g[col2[u]] / (float)a.n : g[col2[u]];
+    if (a.readout == EWS_READOUT_MAX) {
+      const int* am = a.amax + (size_t)b * a.W;
+      if (ok1) am1 = am[col1];
+#pragma unroll
+      for (int u = 0; u < 4; ++u)
+        if (ok2[u]) am2[u] = am[col2[u]];
+    }
+  }
   // the step's row cotangent, flow, s1 and (FULL) the state before it in registers, loaded during the step after
   float4 nF, ng2 = float4{0.0f, 0.0f, 0.0f, 0.0f}, nS2 = float4{0.0f, 0.0f, 0.0f, 0.0f};
   float ng1 = 0.0f, ns1 = 0.0f, nS1 = 0.0f;
   auto fetch = [&](int t) {
     const size_t r = (size_t)b * a.n + t;
-    const float* gr = a.grow + r * RW;
-    if (threadIdx.x < 32) {
-      ng1 = gr[threadIdx.x];
-      ns1 = a.loc[r * RW + threadIdx.x];
+    float c2[4];
+    if (a.readout == EWS_READOUT_PREFIX) {
+      const float* g = a.gout + r * a.W;
+      ng1 = ok1 ? g[col1] : 0.0f;
+#pragma unroll
+      for (int u = 0; u < 4; ++u) c2[u] = ok2[u] ? g[col2[u]] : 0.0f;
+    } else if (a.readout == EWS_READOUT_MEAN) {
+      ng1 = k1;
+#pragma unroll
+      for (int u = 0; u < 4; ++u) c2[u] = k2[u];
+    } else if (a.readout == EWS_READOUT_TERMINAL) {
+      const bool last = t == a.n - 1;
+      ng1 = last ? k1 : 0.0f;
+#pragma unroll
+      for (int u = 0; u < 4; ++u) c2[u] = last ? k2[u] : 0.0f;
+    } else {
+      ng1 = am1 == t ? k1 : 0.0f;
+#pragma unroll
+      for (int u = 0; u < 4; ++u) c2[u] = am2[u] == t ? k2[u] : 0.0f;
     }
-    if (N >= 2) ng2 = gld4(gr + DP);
+    ng2 = float4{c2[0], c2[1], c2[2], c2[3]};
+    if (threadIdx.x < 32) ns1 = a.loc[r * RW + threadIdx.x];
     nF = flow_regs(a, b, t);
     if (MODE == ADJ_FULL) {
       const float* sp = t > t0 ? a.rows + (r - 1) * RW : a.car + ((size_t)b * (a.C + 1) + c) * RW;
@@ -2117,7 +2135,9 @@ int plan(const ews_dense_desc* s, WPlan& p) {
   p.n = p.L - 1;
   p.d = s->dim;
   p.N = s->depth;
-  p.T = s->chunk ? s->chunk : 64;
+  // default chunk: 64 intervals, or 32 when that leaves fewer than two chunk workgroups per CU (measured at
+  // B = 32, L = 896: 32 takes 3-4% less time than 64, 16 and 48 none)
+  p.T = s->chunk ? s->chunk : ((long)s->batch * ((s->length - 1 + 63) / 64) < 512 ? 32 : 64);
   p.C = (p.n + p.T - 1) / p.T;
   p.TL = kLeafSlice;
   p.NSL = (p.n + p.TL - 1) / p.TL;
@@ -2140,7 +2160,7 @@ int plan(const ews_dense_desc* s, WPlan& p) {
 }
 
 struct WLay {
-  size_t fl, vlm, loc, summ, sfl, car, rows, amax, apow, mflag, outs, grow, mu, lend, dloc, dfl, cpart, dvlm, apart,
+  size_t fl, vlm, loc, summ, sfl, car, rows, amax, apow, mflag, outs, mu, lend, dloc, dfl, cpart, dvlm, apart,
       dv, dhl, dhm, dsh, hpart, hsum, ubuf, ebuf, total;
 };
 
@@ -2166,7 +2186,6 @@ WLay layout(const ews_dense_desc* s, const WPlan& p, bool bwd) {
   take(w.ubuf, p.vl_int ? BN * (PW + 1) * 32 * 4 : 0);
   if (bwd) {
     take(w.outs, s->readout == EWS_READOUT_MAX ? (size_t)p.B * p.W * 4 : 0);
-    take(w.grow, BN * RW * 4);
     take(w.mu, BC * RW * 4);
     take(w.lend, BC * RW * 4);
     take(w.dloc, BN * RW * 4);
@@ -2208,7 +2227,7 @@ WArgs make_args(const ews_dense_desc* s, const WPlan& p, const float* path, cons
   a.mflag = p.mats_int ? (int*)(ws + w.mflag) : nullptr;
   a.ubuf = p.vl_int ? f(w.ubuf) : nullptr;
   if (bwd) {
-    a.grow = f(w.grow); a.mu = f(w.mu); a.lend = f(w.lend); a.dloc = f(w.dloc);
+    a.mu = f(w.mu); a.lend = f(w.lend); a.dloc = f(w.dloc);
     a.dfl = p.fl_int ? f(w.dfl) : nullptr; a.cpart = f(w.cpart); a.dvlm = p.vl_int ? f(w.dvlm) : nullptr;
     a.apart = f(w.apart); a.dv = f(w.dv); a.dhl = f(w.dhl); a.dhm = f(w.dhm); a.dsh = f(w.dsh);
     a.hpart = f(w.hpart); a.hsum = p.mats_int ? (double*)(ws + w.hsum) : nullptr;
@@ -2300,6 +2319,7 @@ int backward(const ews_dense_desc* s, const float* path, const float* clock, con
   if (!path || !clock || !A || !grad_out || !grad_path || !grad_A || !workspace) return EWS_ERR_NULL;
   const WLay w = layout(s, p, true);
   WArgs a = make_args(s, p, path, clock, A, nullptr, workspace, true);
+  a.gout = grad_out;
   if (!kept) {  // the forward again, with the padded prefix states kept (and the rows of the maxima of the max readout)
     WArgs f = a;
     if (s->readout == EWS_READOUT_MAX) f.out = (float*)((char*)workspace + w.outs);
@@ -2307,9 +2327,6 @@ int backward(const ews_dense_desc* s, const float* path, const float* clock, con
     const int r = run_forward(p, f, st);
     if (r != EWS_OK) return r;
   }
-  hipLaunchKernelGGL(k_wgrows, dim3((unsigned)std::min<long>(((long)p.B * p.n * RW + NT - 1) / NT, 8192)),
-                     dim3(NT), 0, st, a, grad_out);
-  WIDE_CHECK();
   const dim3 gc(p.C, p.B);
   const size_t lds_lb = (size_t)(lf_floats(p.rows, 4) + (p.vl_int ? LF_EXTRA : 0)) * 4;
   const int lk = !p.vl ? LK_SERIES : p.vl_int ? LK_VL_INT : LK_VL_SHARED;
