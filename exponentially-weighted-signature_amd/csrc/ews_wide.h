@@ -25,7 +25,9 @@ struct WArgs {
   float* summ;  // chunk summaries (B, C)
   float* sfl;   // chunk flow products (B, C)
   float* car;   // carries (B, C + 1): the state before each chunk, then the final state
-  float* rows;  // padded prefix states (B, n), when kept
+  float* rows;  // padded prefix states (B, n), for the backward
+  float* rpart;  // mean / max readout: each chunk's sum or maximum of its padded rows (B, C)
+  int* ridx;     // max readout: the first row attaining each chunk's maximum (B, C)
   int* amax;    // max readout: row of the maximum per (sample, column)
   // backward workspace
   const float* gout;  // the readout's cotangent (packed rows of W)

@@ -1392,6 +1392,11 @@ __global__ __launch_bounds__(NT) void k_wscan(WArgs a) {
     if (N >= 2) ns2 = gld_tile(lrow + DP);
   };
   fetch(t0);
+  // mean / max readout: the chunk's sum, or its maximum and the first row attaining it, of the thread's padded
+  // entries (level 1: threads below 32; level 2: row i, columns j0 .. j0 + 3)
+  const bool mean = a.readout == EWS_READOUT_MEAN, mx = a.readout == EWS_READOUT_MAX;
+  float p1 = mean ? 0.0f : -INFINITY, p2[4] = {p1, p1, p1, p1};
+  int i1 = -1, i2[4] = {-1, -1, -1, -1};
   for (int t = t0; t < t1; ++t) {
     commit_mat(nF, sm + SC_F, sm + SC_FT);
     if (threadIdx.x < 32) s1[threadIdx.x] = ns1;
@@ -1406,6 +1411,43 @@ __global__ __launch_bounds__(NT) void k_wscan(WArgs a) {
       const size_t r = (size_t)b * a.n + t;
       if (a.rows) store_state(a.rows + r * RW, S1, S2);
       if (a.readout == EWS_READOUT_PREFIX) store_packed<N>(a, a.out + r * a.W, S1, S2);
+      if (mean || mx) {
+        const float v1 = threadIdx.x < 32 ? S1[threadIdx.x] : 0.0f;
+        const float4 v2 = N >= 2 ? lds4(S2) : float4{0.0f, 0.0f, 0.0f, 0.0f};
+        const float v[4] = {v2.x, v2.y, v2.z, v2.w};
+        if (mean) {
+          p1 += v1;
+#pragma unroll
+          for (int u = 0; u < 4; ++u) p2[u] += v[u];
+        } else {
+          if (i1 < 0 || v1 > p1) {
+            p1 = v1;
+            i1 = t;
+          }
+#pragma unroll
+          for (int u = 0; u < 4; ++u) {
+            if (i2[u] < 0 || v[u] > p2[u]) {
+              p2[u] = v[u];
+              i2[u] = t;
+            }
+          }
+        }
+      }
+    }
+  }
+  if constexpr (MODE == SCAN_ROWS) {
+    if (mean || mx) {
+      const size_t slot = ((size_t)b * a.C + c) * RW;
+      if (threadIdx.x < 32) a.rpart[slot + threadIdx.x] = p1;
+      if constexpr (N >= 2) gst4(a.rpart + slot + DP, float4{p2[0], p2[1], p2[2], p2[3]});
+      if (mx) {
+        if (threadIdx.x < 32) a.ridx[slot + threadIdx.x] = i1;
+        if constexpr (N >= 2) {
+          int* q = a.ridx + slot + DP + trow<32>() * DP + tcol<32>();
+#pragma unroll
+          for (int u = 0; u < 4; ++u) q[u] = i2[u];
+        }
+      }
     }
   }
   if (MODE == SCAN_SUMMARY) {
@@ -1458,16 +1500,18 @@ __global__ __launch_bounds__(NT) void k_wreadout(WArgs a) {
     if (ok && grp == 0) o[col] = e < 0 ? 1.0f : a.car[((size_t)b * (a.C + 1) + a.C) * RW + pe];
     return;
   }
-  const float* r = a.rows + (size_t)b * a.n * RW + pe;
+  // the chunks' partials (k_wscan rows pass) in 8 interleaved groups of chunks
+  const float* r = a.rpart + (size_t)b * a.C * RW + pe;
+  const int* ri = a.ridx ? a.ridx + (size_t)b * a.C * RW + pe : nullptr;
   float acc = a.readout == EWS_READOUT_MEAN ? 0.0f : -INFINITY;
   int arg = -1;
-  for (int t = grp; t < a.n; t += RO_GROUPS) {
-    const float v = ok ? r[(size_t)t * RW] : 0.0f;
+  for (int c = grp; c < a.C; c += RO_GROUPS) {
+    const float v = ok ? r[(size_t)c * RW] : 0.0f;
     if (a.readout == EWS_READOUT_MEAN) {
       acc += v;
-    } else if (arg < 0 || v > acc) {
+    } else if (arg < 0 || v > acc) {  // chunks in order: the first row attaining the maximum is kept
       acc = v;
-      arg = t;
+      arg = ok ? ri[(size_t)c * RW] : 0;
     }
   }
   s_v[grp][cl] = acc;
@@ -1947,7 +1991,7 @@ __global__ __launch_bounds__(NT) void k_wleaf_bwd(WArgs a) {
     gst4(cp + MM, acc4(sP));
     gst4(cp + 2 * MM, acc4(sV));
   }
-  gst4(a.apart + ((size_t)b * a.NSL + sl) * MM, acc4(dA));  // zero for the Van Loan leaf
+  if constexpr (!vl) gst4(a.apart + ((size_t)b * a.NSL + sl) * MM, acc4(dA));  // (the Van Loan leaf has none)
 }
 
 // Matrix-function adjoints. per_interval: one item per interval, the flow's (dfl) and the Van Loan pair's (dvlm)
@@ -2045,14 +2089,14 @@ __global__ __launch_bounds__(NT) void k_wmat_bwd(WArgs a, int mode, long slot0) 
   gst4(a.apart + (slot0 + (long)blockIdx.y * gridDim.x + blockIdx.x) * MM, acc4(dA));
 }
 
-// grad_A = sum of the partials (float64): a workgroup per 16 entries, 16 interleaved groups of slots combined in a
-// fixed order; entries i, j < d
-__global__ __launch_bounds__(NT) void k_wfinal_A(WArgs a, long nparts, float* grad_A) {
+// grad_A = sum of the partials first .. nparts - 1 (float64; the Van Loan leaf's adjoint writes none, so its slots
+// are skipped): a workgroup per 16 entries, 16 interleaved groups of slots combined in a fixed order; entries i, j < d
+__global__ __launch_bounds__(NT) void k_wfinal_A(WArgs a, long first, long nparts, float* grad_A) {
   __shared__ double s_p[16][16];
   const int el = threadIdx.x & 15, grp = threadIdx.x >> 4;
   const int e = blockIdx.x * 16 + el;
   double s = 0.0;
-  for (long k = grp; k < nparts; k += 16) s += (double)a.apart[k * MM + e];
+  for (long k = first + grp; k < nparts; k += 16) s += (double)a.apart[k * MM + e];
   s_p[grp][el] = s;
   __syncthreads();
   if (grp != 0) return;
@@ -2160,7 +2204,7 @@ int plan(const ews_dense_desc* s, WPlan& p) {
 }
 
 struct WLay {
-  size_t fl, vlm, loc, summ, sfl, car, rows, amax, apow, mflag, outs, mu, lend, dloc, dfl, cpart, dvlm, apart,
+  size_t fl, vlm, loc, summ, sfl, car, rows, rpart, ridx, amax, apow, mflag, outs, mu, lend, dloc, dfl, cpart, dvlm, apart,
       dv, dhl, dhm, dsh, hpart, hsum, ubuf, ebuf, total;
 };
 
@@ -2179,7 +2223,9 @@ WLay layout(const ews_dense_desc* s, const WPlan& p, bool bwd) {
   take(w.sfl, BC * MM * 4);
   take(w.car, (size_t)p.B * (p.C + 1) * RW * 4);
   const bool mm_ro = s->readout == EWS_READOUT_MEAN || s->readout == EWS_READOUT_MAX;
-  take(w.rows, (bwd || mm_ro) ? BN * RW * 4 : 0);
+  take(w.rows, bwd ? BN * RW * 4 : 0);
+  take(w.rpart, mm_ro ? BC * RW * 4 : 0);
+  take(w.ridx, s->readout == EWS_READOUT_MAX ? BC * RW * 4 : 0);
   take(w.amax, s->readout == EWS_READOUT_MAX ? (size_t)p.B * p.W * 4 : 0);
   take(w.apow, p.mats_int ? (size_t)APOW_FLOATS * 4 : 0);
   take(w.mflag, p.mats_int ? BN * 4 : 0);
@@ -2221,7 +2267,9 @@ WArgs make_args(const ews_dense_desc* s, const WPlan& p, const float* path, cons
   a.fl = f(w.fl); a.vlm = p.vl ? f(w.vlm) : nullptr; a.loc = f(w.loc); a.summ = f(w.summ); a.sfl = f(w.sfl);
   a.car = f(w.car);
   const bool mm_ro = s->readout == EWS_READOUT_MEAN || s->readout == EWS_READOUT_MAX;
-  a.rows = (bwd || mm_ro) ? f(w.rows) : nullptr;
+  a.rows = bwd ? f(w.rows) : nullptr;
+  a.rpart = mm_ro ? f(w.rpart) : nullptr;
+  a.ridx = s->readout == EWS_READOUT_MAX ? (int*)(ws + w.ridx) : nullptr;
   a.amax = s->readout == EWS_READOUT_MAX ? (int*)(ws + w.amax) : nullptr;
   a.apow = p.mats_int ? f(w.apow) : nullptr;
   a.mflag = p.mats_int ? (int*)(ws + w.mflag) : nullptr;
@@ -2375,7 +2423,7 @@ int backward(const ews_dense_desc* s, const float* path, const float* clock, con
                        base + p.g_int * p.gy_int);
     WIDE_CHECK();
   }
-  hipLaunchKernelGGL(k_wfinal_A, dim3(MM / 16), dim3(NT), 0, st, a,
+  hipLaunchKernelGGL(k_wfinal_A, dim3(MM / 16), dim3(NT), 0, st, a, p.vl ? base : 0L,
                      base + p.g_int * p.gy_int + p.g_smp * p.gy_smp + (p.mats_int ? 1 : 0), grad_A);
   hipLaunchKernelGGL(k_wknots, dim3((p.L + NT - 1) / NT, p.B), dim3(NT), 0, st, a, grad_path, grad_clock);
   WIDE_CHECK();

@@ -177,7 +177,8 @@ def test_wide_kept_backward_equals_recomputing(case):
     """ews_dense_backward_kept starts from what ews_dense_forward_keep left in the workspace (step matrices, local
     terms, chunk summaries and carries, prefix states, the maxima's rows); ews_dense_backward recomputes them. The
     same kernels on the same data: the gradients agree bit for bit, and the kept forward's output with the plain
-    forward's."""
+    forward's and with the forward alone (no gradient: its own workspace, the mean / max from the chunks'
+    partials without the prefix states)."""
     d, readout, mode, kw = case
     path, clock, A = _inputs(2, 50, d, seed=d + 3)
     leaf = _leaf(kw, mode)
@@ -194,6 +195,10 @@ def test_wide_kept_backward_equals_recomputing(case):
         res.append((out.detach().clone(), p.grad.clone(), c.grad.clone(), a.grad.clone()))
     for name, x, y in zip(("out", "path", "clock", "A"), res[0], res[1]):
         assert torch.equal(x, y), f"{name}: kept and recomputing backward differ"
+    with torch.no_grad():  # the forward alone (its own workspace layout, no prefix states kept)
+        out0 = ops.dense_scan(path.float().to(DEV), clock.float().to(DEV), A.float().to(DEV), 2, leaf.q,
+                              _FLOW[mode], readout, True, chunk=8, leaf=leaf, keep=False)
+    assert torch.equal(out0, res[0][0]), "forward alone and kept forward differ"
 
 
 @pytest.mark.parametrize("readout", ["prefix", "mean"])
