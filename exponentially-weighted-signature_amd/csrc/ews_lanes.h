@@ -33,6 +33,27 @@ __device__ __forceinline__ float sum16(float v) {
   v = sum8(v);
   return v + dpp<kMirror>(v);
 }
+// float64: the two 32-bit halves moved by the same DPP control
+template <int CTRL>
+__device__ __forceinline__ double dpp(double v) {
+  const unsigned long long x = (unsigned long long)__double_as_longlong(v);
+  const unsigned lo = (unsigned)__builtin_amdgcn_update_dpp(0, (int)(unsigned)x, CTRL, 0xf, 0xf, false);
+  const unsigned hi = (unsigned)__builtin_amdgcn_update_dpp(0, (int)(unsigned)(x >> 32), CTRL, 0xf, 0xf, false);
+  return __longlong_as_double((long long)(((unsigned long long)hi << 32) | lo));
+}
+__device__ __forceinline__ double sum8(double v) {
+  v += dpp<kXor1>(v);
+  v += dpp<kXor2>(v);
+  return v + dpp<kHalfMirror>(v);
+}
+// sum over the 64 lanes (every lane returns it)
+__device__ __forceinline__ double sum64(double v) {
+  v = sum8(v);
+  v += dpp<kMirror>(v);
+  v += __shfl_xor(v, 16, 64);
+  return v + __shfl_xor(v, 32, 64);
+}
+
 // sum over lanes l, l ^ 8, l ^ 16, l ^ 32 (the same lane of each group of 8)
 __device__ __forceinline__ float colsum8(float v) {
   v += dpp<kXor8>(v);

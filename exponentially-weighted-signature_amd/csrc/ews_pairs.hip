@@ -34,6 +34,7 @@
 
 #include "ews_args.h"
 #include "ews_hip.h"
+#include "ews_lanes.h"
 #include "ews_numerics.h"
 #include "ews_pairs.h"
 
@@ -523,13 +524,8 @@ __device__ __forceinline__ void st_fd(float* p, dc v) {
   p[0] = (float)v.re;
   p[1] = (float)v.im;
 }
-__device__ __forceinline__ dc rowsum8(dc v) {  // over lanes 8 j .. 8 j + 7
-#pragma unroll
-  for (int o = 1; o < 8; o <<= 1) {
-    v.re += __shfl_xor(v.re, o, 64);
-    v.im += __shfl_xor(v.im, o, 64);
-  }
-  return v;
+__device__ __forceinline__ dc rowsum8(dc v) {  // over lanes 8 j .. 8 j + 7 (DPP)
+  return dc{lanes::sum8(v.re), lanes::sum8(v.im)};
 }
 // flow exp(u_p tau) of plane p over the clock span of chunks [c0, c1) (per-interval flows)
 __device__ __forceinline__ dc span_flow(const DiagArgs& a, int b, int c0, int c1, int p) {
@@ -588,11 +584,7 @@ __device__ __forceinline__ double flow_dot(const DiagArgs& a, const PairSt& m, c
   if (k == 0) r += (cjd(m.S1) * (uj * s.S1)).re;
   return r;
 }
-__device__ __forceinline__ double wave_sum_d(double v) {
-#pragma unroll
-  for (int o = 1; o < 64; o <<= 1) v += __shfl_xor(v, o, 64);
-  return v;
-}
+__device__ __forceinline__ double wave_sum_d(double v) { return lanes::sum64(v); }
 
 // level-1 increment of the span [ca, cb) of plane p: carry1(cb) - F carry1(ca)
 __device__ __forceinline__ dc l1_inc(const DiagArgs& a, int b, int ca, int cb, int p, dc F) {
