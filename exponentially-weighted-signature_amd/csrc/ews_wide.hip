@@ -164,14 +164,16 @@ __device__ __forceinline__ int tile_i() { return (int)threadIdx.x & 15; }
 __device__ __forceinline__ int tile_g() { return ((int)threadIdx.x >> 4) & 3; }
 
 template <bool TX, bool TY>
-__device__ __forceinline__ v4f mm_tile(const float* X, const float* Y, v4f acc) {
+__device__ __forceinline__ v4f mm_tile(const float* X, const float* Y, v4f acc, int ku = 8) {
   const int m0 = tile_m0(), n0 = tile_n0(), i = tile_i(), g = tile_g();
 #pragma unroll
   for (int u = 0; u < 8; ++u) {
-    const int k = 4 * u + g;
-    const float xa = TX ? X[k * P32 + m0 + i] : X[(m0 + i) * P32 + k];
-    const float yb = TY ? Y[(n0 + i) * P32 + k] : Y[k * P32 + n0 + i];
-    acc = __builtin_amdgcn_mfma_f32_16x16x4f32(xa, yb, acc, 0, 0, 0);
+    if (u < ku) {  // (uniform) the k-steps past ku read only zero padding of one factor
+      const int k = 4 * u + g;
+      const float xa = TX ? X[k * P32 + m0 + i] : X[(m0 + i) * P32 + k];
+      const float yb = TY ? Y[(n0 + i) * P32 + k] : Y[k * P32 + n0 + i];
+      acc = __builtin_amdgcn_mfma_f32_16x16x4f32(xa, yb, acc, 0, 0, 0);
+    }
   }
   return acc;
 }
@@ -1306,9 +1308,10 @@ constexpr int SC_VEC = 6 * S32;  // S1, y1, s1 (32 each)
 constexpr int SC_FLOATS = SC_VEC + 3 * 32;
 
 // one Chen step of the state (S1, S2) in LDS by (F, Ft, s1 in LDS; s2 the lane's tile entries); with PHI the flow
-// product Ph <- F Ph as well (Pn scratch; the pointers swap). The three products run on MFMA.
+// product Ph <- F Ph as well (Pn scratch; the pointers swap). The three products run on MFMA, over the first ku
+// k-steps where a factor is a state (zero past d).
 template <int N, bool PHI>
-__device__ __forceinline__ void chen_step(float* sm, const v4f s2, float*& Ph, float*& Pn) {
+__device__ __forceinline__ void chen_step(float* sm, const v4f s2, float*& Ph, float*& Pn, int ku) {
   float* F = sm + SC_F;
   float* Ft = sm + SC_FT;
   float* S2 = sm + SC_S2;
@@ -1318,12 +1321,12 @@ __device__ __forceinline__ void chen_step(float* sm, const v4f s2, float*& Ph, f
   float* s1 = S1 + 64;
   const int i = (int)threadIdx.x >> 3;
   const float y = mv<false>(F, S1);
-  if constexpr (N >= 2) st_tile(T, mm_tile<false, false>(F, S2, zero4()));
-  if constexpr (PHI) st_tile(Pn, mm_tile<false, false>(F, Ph, zero4()));
+  if constexpr (N >= 2) st_tile(T, mm_tile<false, false>(F, S2, zero4(), ku));
+  if constexpr (PHI) st_tile(Pn, mm_tile<false, false>(F, Ph, zero4()));  // (all of K: Ph's padding is I)
   if (row_lead()) y1[i] = y;
   __syncthreads();
   if constexpr (N >= 2) {  // S2 <- F S2 F^T + y1 s1^T + s2 (S2 is not read in this phase)
-    v4f acc = mm_tile<false, false>(T, Ft, s2);
+    v4f acc = mm_tile<false, false>(T, Ft, s2, ku);
     const int m = tile_m0() + 4 * tile_g(), n = tile_n0() + tile_i();
     const float sn = s1[n];
 #pragma unroll
@@ -1367,6 +1370,7 @@ constexpr int SCAN_SUMMARY = 0, SCAN_ROWS = 1;
 
 template <int N, int MODE>
 __global__ __launch_bounds__(NT) void k_wscan(WArgs a) {
+  const int ku = (a.d + 3) >> 2;  // MFMA k-steps that reach a nonzero entry (d <= 4 ku)
   __shared__ __align__(16) float sm[SC_FLOATS];
   const int c = blockIdx.x, b = blockIdx.y;
   const int t0 = c * a.T, t1 = min(a.n, t0 + a.T);
@@ -1406,7 +1410,7 @@ __global__ __launch_bounds__(NT) void k_wscan(WArgs a) {
       nF = flow_regs(a, b, t + 1);
       fetch(t + 1);
     }
-    chen_step<N, MODE == SCAN_SUMMARY>(sm, s2, Ph, Pn);
+    chen_step<N, MODE == SCAN_SUMMARY>(sm, s2, Ph, Pn, ku);
     if constexpr (MODE == SCAN_ROWS) {
       const size_t r = (size_t)b * a.n + t;
       if (a.rows) store_state(a.rows + r * RW, S1, S2);
@@ -1459,6 +1463,7 @@ __global__ __launch_bounds__(NT) void k_wscan(WArgs a) {
 // carries: car[b][0] = 0, car[b][c + 1] = the chunk-c Chen map of car[b][c] (flow product and summary)
 template <int N>
 __global__ __launch_bounds__(NT) void k_wcarry(WArgs a) {
+  const int ku = (a.d + 3) >> 2;  // MFMA k-steps that reach a nonzero entry (d <= 4 ku)
   __shared__ __align__(16) float sm[SC_FLOATS];
   const int b = blockIdx.x;
   float* S1 = sm + SC_VEC;
@@ -1479,7 +1484,7 @@ __global__ __launch_bounds__(NT) void k_wcarry(WArgs a) {
     if (threadIdx.x < 32) s1[threadIdx.x] = sr[threadIdx.x];
     const v4f s2 = N >= 2 ? gld_tile(sr + DP) : zero4();
     __syncthreads();
-    chen_step<N, false>(sm, s2, dummy0, dummy1);
+    chen_step<N, false>(sm, s2, dummy0, dummy1, ku);
     store_state(car + (size_t)(c + 1) * RW, S1, S2);
   }
 }
@@ -1553,9 +1558,10 @@ constexpr int ADJ_LOCAL = 0, ADJ_FULL = 1;
 
 // one reverse step: (lambda1, lambda2) of the state after the step (row cotangent included) to the state before it;
 // FULL: also ds1, ds2 (into dl) and dF (returned in the lane's tile entries) from the state before the step (S1, S2
-// in LDS). The products run on MFMA.
+// in LDS). The products run on MFMA over the first ku k-steps (every product has a factor that is zero past d in
+// the summed index: a state, a cotangent or a product of one).
 template <int N, int MODE>
-__device__ __forceinline__ v4f adj_step(float* sm, float* dl) {
+__device__ __forceinline__ v4f adj_step(float* sm, float* dl, int ku) {
   float* F = sm + AD_F;
   float* Ft = sm + AD_FT;
   float* L2 = sm + AD_L2;
@@ -1572,11 +1578,11 @@ __device__ __forceinline__ v4f adj_step(float* sm, float* dl) {
   float r = 0.0f, y = 0.0f;
   if constexpr (N >= 2) {
     r = mv<false>(L2, s1);                                      // (lambda2 s1)[i]
-    st_tile(H, mm_tile<false, false>(L2, F, zero4()));          // H = lambda2 F
+    st_tile(H, mm_tile<false, false>(L2, F, zero4(), ku));      // H = lambda2 F
     if constexpr (MODE == ADJ_FULL) {
       y = mv<false>(F, S1);                                     // y1 = F S1
-      st_tile(G1, mm_tile<false, false>(F, S2, zero4()));       // G1 = F S2
-      st_tile(G2, mm_tile<false, true>(F, S2, zero4()));        // G2 = F S2^T
+      st_tile(G1, mm_tile<false, false>(F, S2, zero4(), ku));   // G1 = F S2
+      st_tile(G2, mm_tile<false, true>(F, S2, zero4(), ku));    // G2 = F S2^T
     }
   } else if constexpr (MODE == ADJ_FULL) {
     y = mv<false>(F, S1);
@@ -1587,7 +1593,7 @@ __device__ __forceinline__ v4f adj_step(float* sm, float* dl) {
   }
   __syncthreads();
   v4f ln = zero4(), df = zero4();
-  if constexpr (N >= 2) ln = mm_tile<false, false>(Ft, H, zero4());  // F^T H (Ft holds F^T row-major)
+  if constexpr (N >= 2) ln = mm_tile<false, false>(Ft, H, zero4(), ku);  // F^T H (Ft holds F^T row-major)
   const float l1n = mv<true>(F, rho);                                // (F^T rho)[i]
   if constexpr (MODE == ADJ_FULL) {
     float ds1 = l1[i];
@@ -1595,8 +1601,8 @@ __device__ __forceinline__ v4f adj_step(float* sm, float* dl) {
     if (row_lead()) dl[i] = ds1;
     // dF = rho S1^T + lambda2 G2 + lambda2^T G1
     if constexpr (N >= 2) {
-      df = mm_tile<false, false>(L2, G2, df);
-      df = mm_tile<true, false>(L2, G1, df);
+      df = mm_tile<false, false>(L2, G2, df, ku);
+      df = mm_tile<true, false>(L2, G1, df, ku);
       gst4(dl + DP, lds4(L2));  // ds2 = lambda2 (of the state after the step)
     }
     const int m = tile_m0() + 4 * tile_g(), n = tile_n0() + tile_i();
@@ -1613,6 +1619,7 @@ __device__ __forceinline__ v4f adj_step(float* sm, float* dl) {
 
 template <int N, int MODE>
 __global__ __launch_bounds__(NT) void k_wadj(WArgs a) {
+  const int ku = (a.d + 3) >> 2;  // MFMA k-steps that reach a nonzero entry (d <= 4 ku)
   __shared__ __align__(16) float sm[AD_FLOATS];
   const int c = blockIdx.x, b = blockIdx.y;
   const int t0 = c * a.T, t1 = min(a.n, t0 + a.T);
@@ -1707,7 +1714,7 @@ __global__ __launch_bounds__(NT) void k_wadj(WArgs a) {
     commit_mat(nF, sm + AD_F, sm + AD_FT);
     __syncthreads();
     if (t > t0) fetch(t - 1);
-    const v4f df = adj_step<N, MODE>(sm, MODE == ADJ_FULL ? a.dloc + r * RW : nullptr);
+    const v4f df = adj_step<N, MODE>(sm, MODE == ADJ_FULL ? a.dloc + r * RW : nullptr, ku);
     if constexpr (MODE == ADJ_FULL) {
       bool ident;
       flow_step(a, a.clock + (size_t)b * a.L, t, ident);
@@ -1728,6 +1735,7 @@ __global__ __launch_bounds__(NT) void k_wadj(WArgs a) {
 // end cotangents of the chunks: lend[b][C-1] = 0, lend[b][c-1] = J_c^T lend[b][c] + mu[b][c] (J_c: chunk c's map)
 template <int N>
 __global__ __launch_bounds__(NT) void k_wadj_carry(WArgs a) {
+  const int ku = (a.d + 3) >> 2;  // MFMA k-steps that reach a nonzero entry (d <= 4 ku)
   __shared__ __align__(16) float sm[AD_FLOATS];
   const int b = blockIdx.x;
   float* L2 = sm + AD_L2;
@@ -1743,7 +1751,7 @@ __global__ __launch_bounds__(NT) void k_wadj_carry(WArgs a) {
     commit_mat(gld4(a.sfl + ((size_t)b * a.C + c) * MM), F, Ft);
     if (threadIdx.x < 32) s1[threadIdx.x] = a.summ[((size_t)b * a.C + c) * RW + threadIdx.x];
     __syncthreads();
-    adj_step<N, ADJ_LOCAL>(sm, nullptr);
+    adj_step<N, ADJ_LOCAL>(sm, nullptr, ku);
     const float* m = a.mu + ((size_t)b * a.C + c) * RW;
     if (threadIdx.x < 32) l1[threadIdx.x] += m[threadIdx.x];
     if constexpr (N >= 2) sld4(L2, f4add(lds4(L2), gld4(m + DP)));
