@@ -46,6 +46,7 @@ struct WArgs {
   float* apow;   // A^0 .. A^PW (padded, float), ||A||_1 and the Van Loan knots' coefficients phi[m][k]
   int* mflag;    // per interval: bit 0 the flow, bit 1 the Van Loan pair outside the series radius, bit 2 the
                  // Van Loan knots by the M-step chain (M |c| ||A||_1 outside the radius)
+  int* sflag;    // per sample (uniform modes): bit 0 the shared flow, bit 1 the shared pair outside the series radius
   float* hpart;  // the adjoint's sums H_k = sum gamma_k c^k dOut per workgroup
   double* hsum;  // H_k summed over the workgroups
   float* ubuf;   // series-path knots: u_k = A^k w per interval (B, n, PW + 1, 32)

@@ -178,6 +178,29 @@ __device__ __forceinline__ v4f mm_tile(const float* X, const float* Y, v4f acc, 
   return acc;
 }
 __device__ __forceinline__ v4f zero4() { return v4f{0.0f, 0.0f, 0.0f, 0.0f}; }
+// float64 products on MFMA (mfma_f64_16x16x4f64): the wavefront's 16 x 16 tile of Z = X Y (X(m, k) = X[k][m] when
+// TX, Y(k, n) = Y[n][k] when TY), LDS at pitch 36. The operands are laid out as for mfma_f32_16x16x4f32 (lane
+// (i, g): X(m0 + i, 4 u + g), Y(4 u + g, n0 + i)), but the result rows are interleaved: lane (i, g) holds rows
+// m0 + g + 4 r (r = 0..3) of column n0 + i (a probe with one-hot operands showed it)
+typedef double v4d __attribute__((ext_vector_type(4)));
+template <bool TX, bool TY>
+__device__ __forceinline__ v4d mm_tile_d(const double* X, const double* Y, v4d acc) {
+  const int m0 = tile_m0(), n0 = tile_n0(), i = tile_i(), g = tile_g();
+#pragma unroll
+  for (int u = 0; u < 8; ++u) {
+    const int k = 4 * u + g;
+    const double xa = TX ? X[k * P32 + m0 + i] : X[(m0 + i) * P32 + k];
+    const double yb = TY ? Y[(n0 + i) * P32 + k] : Y[k * P32 + n0 + i];
+    acc = __builtin_amdgcn_mfma_f64_16x16x4f64(xa, yb, acc, 0, 0, 0);
+  }
+  return acc;
+}
+__device__ __forceinline__ int tile_row_d(int r) { return tile_m0() + tile_g() + 4 * r; }  // result row of item r
+__device__ __forceinline__ void st_tile_d(double* Z, v4d v) {
+  const int n = tile_n0() + tile_i();
+#pragma unroll
+  for (int r = 0; r < 4; ++r) Z[tile_row_d(r) * P32 + n] = v[r];
+}
 // the lane's tile entries of a 32 x 32 matrix: LDS (pitch 36) or global (pitch 32)
 __device__ __forceinline__ void st_tile(float* Z, v4f v) {
   const int m = tile_m0() + 4 * tile_g(), n = tile_n0() + tile_i();
@@ -621,7 +644,7 @@ __global__ __launch_bounds__(NT) void k_wmat(WArgs a, int mode) {
     const int b = per_interval ? (int)(it / a.n) : (int)it;
     const int t = per_interval ? (int)(it - (long)b * a.n) : 1;
     const float* th = a.clock + (size_t)b * a.L;
-    const int flag = mode == 2 ? a.mflag[it] : 3;
+    const int flag = mode == 2 ? a.mflag[it] : a.sflag[it];  // the matrices outside the series radius
     if (do_flow && (flag & 1)) {
       bool ident;
       const float h = flow_step(a, th, t, ident);
@@ -686,9 +709,40 @@ __device__ __forceinline__ float series_radius(int scheme, int kind) {
 constexpr int PHI_OFF = (PW + 1) * MM + 64;  // offset of phi in apow (M rows of PW + 1)
 constexpr int APOW_FLOATS = PHI_OFF + 64 * (PW + 1);
 
-// the table: A^k (k = 0 .. PW) in float64, stored float, ||A||_1 at apow[(PW + 1) MM]; with a per-interval Van Loan
-// leaf the knots' coefficients phi at apow[PHI_OFF]
+// the knots' coefficients phi[r][k] of the series path: f_{M-1} = V, f_{r-1} = P f_r as truncated series (float64),
+// thread k < PW + 1 forming coefficient k of each
+__device__ void wpowers_phi(const WArgs& a) {
+  __shared__ float s_gp[PW + 1], s_gv[PW + 1];
+  __shared__ double s_f[2][PW + 1];
+  if (threadIdx.x == 0) {
+    series_gamma(a.vl_expm, 1, s_gp);
+    series_gamma(a.vl_expm, 2, s_gv);
+  }
+  __syncthreads();
+  const int k = threadIdx.x;
+  if (k <= PW) s_f[0][k] = s_gv[k];
+  __syncthreads();
+  float* phi = a.apow + PHI_OFF;
+  int cur = 0;
+  for (int r = a.vm - 1; r >= 0; --r) {
+    if (k <= PW) {
+      phi[r * (PW + 1) + k] = (float)s_f[cur][k];
+      double x = 0.0;
+      for (int j = 0; j <= k; ++j) x += (double)s_gp[j] * s_f[cur][k - j];
+      s_f[cur ^ 1][k] = x;
+    }
+    __syncthreads();
+    cur ^= 1;
+  }
+}
+
+// the table: A^k (k = 0 .. PW) in float64, stored float, ||A||_1 at apow[(PW + 1) MM] (workgroup 0); with a
+// per-interval Van Loan leaf the knots' coefficients phi at apow[PHI_OFF] (workgroup 1)
 __global__ __launch_bounds__(NT) void k_wpowers(WArgs a) {
+  if (blockIdx.x == 1) {  // a second workgroup (per-interval Van Loan leaf): the knots' coefficients
+    wpowers_phi(a);
+    return;
+  }
   __shared__ __align__(16) double sd[3 * S32 + 64];
   double* A = sd;
   double* T = sd + S32;
@@ -699,11 +753,12 @@ __global__ __launch_bounds__(NT) void k_wpowers(WArgs a) {
   const int i = trow<32>(), j0 = tcol<32>();
   gst4(a.apow, float4{i == j0 ? 1.0f : 0.0f, i == j0 + 1 ? 1.0f : 0.0f, i == j0 + 2 ? 1.0f : 0.0f,
                       i == j0 + 3 ? 1.0f : 0.0f});
+  const int tn = tile_n0() + tile_i();  // the lane's tile entries: rows tile_row_d(r) of column tn
   for (int k = 1; k <= PW; ++k) {
-    double acc[4];
-    mm<32, false, false>(T, A, acc);
-    st<32>(Tn, acc);
-    gst4(a.apow + (size_t)k * MM, float4{(float)acc[0], (float)acc[1], (float)acc[2], (float)acc[3]});
+    const v4d acc = mm_tile_d<false, false>(T, A, v4d{0.0, 0.0, 0.0, 0.0});
+    st_tile_d(Tn, acc);
+#pragma unroll
+    for (int r = 0; r < 4; ++r) a.apow[(size_t)k * MM + tile_row_d(r) * DP + tn] = (float)acc[r];
     __syncthreads();
     double* tmp = T;
     T = Tn;
@@ -711,23 +766,6 @@ __global__ __launch_bounds__(NT) void k_wpowers(WArgs a) {
   }
   const double nrm = norm1<32>(A, sd + 3 * S32);
   if (threadIdx.x == 0) a.apow[(size_t)(PW + 1) * MM] = (float)nrm;
-  if (threadIdx.x == 0 && a.leaf == EWS_LEAF_VAN_LOAN && a.vl_mode == EWS_FLOW_PER_INTERVAL) {
-    float gp[PW + 1], gv[PW + 1];
-    series_gamma(a.vl_expm, 1, gp);
-    series_gamma(a.vl_expm, 2, gv);
-    double f[PW + 1], g[PW + 1];
-    for (int k = 0; k <= PW; ++k) f[k] = gv[k];
-    float* phi = a.apow + PHI_OFF;
-    for (int r = a.vm - 1; r >= 0; --r) {
-      for (int k = 0; k <= PW; ++k) phi[r * (PW + 1) + k] = (float)f[k];
-      for (int k = 0; k <= PW; ++k) {  // f <- P f, truncated
-        double x = 0.0;
-        for (int j = 0; j <= k; ++j) x += (double)gp[j] * f[k - j];
-        g[k] = x;
-      }
-      for (int k = 0; k <= PW; ++k) f[k] = g[k];
-    }
-  }
 }
 
 // the thread's four entries of every power
@@ -830,6 +868,51 @@ __global__ __launch_bounds__(NT) void k_wmat_series(WArgs a) {
     }
     if (threadIdx.x == 0) a.mflag[it] = flag;
   }
+}
+
+// per-sample step matrices (uniform reweighting modes) on the series path, a workgroup per sample: the shared flow
+// (flow_mode cached / cached_basepoint) and the shared Van Loan pair; sflag[b] bit 0 (flow) / 1 (pair) flags a
+// matrix outside the series radius, formed by k_wmat (mode 0) instead. An identity step (a zero or basepoint step)
+// is never read and is not formed.
+__global__ __launch_bounds__(NT) void k_wmat_series_smp(WArgs a) {
+  __shared__ float s_g[3][PW + 1];
+  if (threadIdx.x == 0) {
+    series_gamma(a.chen, 0, s_g[0]);
+    if (a.leaf == EWS_LEAF_VAN_LOAN) {
+      series_gamma(a.vl_expm, 1, s_g[1]);
+      series_gamma(a.vl_expm, 2, s_g[2]);
+    }
+  }
+  __syncthreads();
+  const int b = blockIdx.x;
+  const float* th = a.clock + (size_t)b * a.L;
+  const bool do_flow = a.flow_mode != EWS_FLOW_PER_INTERVAL;
+  const bool do_vl = a.leaf == EWS_LEAF_VAN_LOAN && a.vl_mode != EWS_FLOW_PER_INTERVAL;
+  float4 T[PW + 1];
+  load_powers(a, T);
+  const float nrm = a.apow[(size_t)(PW + 1) * MM];
+  int flag = 0;
+  if (do_flow) {
+    bool ident;
+    const float h = flow_step(a, th, 1, ident);
+    if (!ident) {
+      if (fabsf(h) * nrm <= series_radius(a.chen, 0)) gst4(a.fl + (size_t)b * MM, series_eval(T, s_g[0], h));
+      else flag |= 1;
+    }
+  }
+  if (do_vl) {
+    bool fixed;
+    const float c = vl_step(a, th, 1, fixed);
+    if (!fixed) {
+      if (fabsf(c) * nrm <= series_radius(a.vl_expm, 1)) {
+        gst4(a.vlm + (size_t)b * 2 * MM, series_eval(T, s_g[1], c));
+        gst4(a.vlm + (size_t)b * 2 * MM + MM, series_eval(T, s_g[2], c));
+      } else {
+        flag |= 2;
+      }
+    }
+  }
+  if (threadIdx.x == 0) a.sflag[b] = flag;
 }
 
 // sum over the workgroup of two values (every thread returns both; red: 2 NT / 64 floats); when cols, also each
@@ -997,6 +1080,89 @@ __global__ __launch_bounds__(NT) void k_wmat_bwd_series(WArgs a) {
   for (int k = 0; k <= PW; ++k) gst4(a.hpart + ((size_t)blockIdx.x * (PW + 1) + k) * MM, H[k]);
 }
 
+// Adjoint of the per-sample series path, a workgroup per sample: the shared flow's cotangent (its chunks' partials)
+// and the shared pair's (its leaf slices' partials), summed in order as k_wmat_bwd does, into the sample's H_k slot
+// (hpart slot hslot0 + b) and the shared steps' cotangents dsh[b]; flagged matrices are k_wmat_bwd's (mode 0)
+__global__ __launch_bounds__(NT) void k_wmat_bwd_series_smp(WArgs a, int hslot0) {
+  __shared__ float s_g[3][PW + 1];
+  __shared__ float red[2 * NT / 64];
+  if (threadIdx.x == 0) {
+    series_gamma(a.chen, 0, s_g[0]);
+    if (a.leaf == EWS_LEAF_VAN_LOAN) {
+      series_gamma(a.vl_expm, 1, s_g[1]);
+      series_gamma(a.vl_expm, 2, s_g[2]);
+    }
+  }
+  __syncthreads();
+  const int b = blockIdx.x;
+  const float* th = a.clock + (size_t)b * a.L;
+  const int flag = a.sflag[b];
+  const bool do_flow = a.flow_mode != EWS_FLOW_PER_INTERVAL && !(flag & 1);
+  const bool do_vl = a.leaf == EWS_LEAF_VAN_LOAN && a.vl_mode != EWS_FLOW_PER_INTERVAL && !(flag & 2);
+  float4 T[PW + 1], H[PW + 1];
+  load_powers(a, T);
+#pragma unroll
+  for (int k = 0; k <= PW; ++k) H[k] = float4{0.0f, 0.0f, 0.0f, 0.0f};
+  float df = 0.0f, dv = 0.0f;
+  bool sf = false, sv = false;
+  if (do_flow) {
+    bool ident;
+    const float h = flow_step(a, th, 1, ident);
+    sf = true;
+    float4 G = float4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll 8
+    for (int c = 0; c < a.C; ++c) G = f4add(G, gld4(a.cpart + ((size_t)b * a.CP + c) * 3 * MM));
+    float ck = 1.0f, dk = 0.0f;  // h^k, k h^(k-1)
+#pragma unroll
+    for (int k = 0; k <= PW; ++k) {
+      const float w = s_g[0][k] * ck, wd = s_g[0][k] * dk;
+      H[k].x = fmaf(w, G.x, H[k].x);
+      H[k].y = fmaf(w, G.y, H[k].y);
+      H[k].z = fmaf(w, G.z, H[k].z);
+      H[k].w = fmaf(w, G.w, H[k].w);
+      df += (wd * G.x) * T[k].x + (wd * G.y) * T[k].y + (wd * G.z) * T[k].z + (wd * G.w) * T[k].w;
+      dk = fmaf(dk, h, ck);
+      ck *= h;
+    }
+  }
+  if (do_vl) {
+    bool fixed;
+    const float c = vl_step(a, th, 1, fixed);
+    if (!fixed) {
+      sv = true;
+      float4 GP = float4{0.0f, 0.0f, 0.0f, 0.0f}, GV = GP;
+#pragma unroll 8
+      for (int s2 = 0; s2 < a.NSL; ++s2) {
+        const float* cp = a.cpart + ((size_t)b * a.CP + s2) * 3 * MM;
+        GP = f4add(GP, gld4(cp + MM));
+        GV = f4add(GV, gld4(cp + 2 * MM));
+      }
+      float ck = 1.0f, dk = 0.0f;
+#pragma unroll
+      for (int k = 0; k <= PW; ++k) {
+        const float wp = s_g[1][k], wv = s_g[2][k];
+        const float4 G = float4{wp * GP.x + wv * GV.x, wp * GP.y + wv * GV.y, wp * GP.z + wv * GV.z,
+                                wp * GP.w + wv * GV.w};
+        H[k].x = fmaf(ck, G.x, H[k].x);
+        H[k].y = fmaf(ck, G.y, H[k].y);
+        H[k].z = fmaf(ck, G.z, H[k].z);
+        H[k].w = fmaf(ck, G.w, H[k].w);
+        dv += (dk * G.x) * T[k].x + (dk * G.y) * T[k].y + (dk * G.z) * T[k].z + (dk * G.w) * T[k].w;
+        dk = fmaf(dk, c, ck);
+        ck *= c;
+      }
+    }
+  }
+  const float dw0[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+  const float2 s2 = block_sum2_cols(df, dv, dw0, false, red, nullptr);
+  if (threadIdx.x == 0) {
+    if (sf) a.dsh[2 * b] = s2.x;
+    if (sv) a.dsh[2 * b + 1] = s2.y / (float)a.vm;  // c = dt / M
+  }
+#pragma unroll
+  for (int k = 0; k <= PW; ++k) gst4(a.hpart + ((size_t)(hslot0 + b) * (PW + 1) + k) * MM, H[k]);
+}
+
 // H_k summed over the workgroups' partials (float64, a fixed order): a workgroup per (k, 64 entries); its four
 // wavefronts take the partials g = 4 q + w (two running sums each, even and odd q), then wavefront 0 adds the
 // eight sums in order
@@ -1031,28 +1197,27 @@ __global__ __launch_bounds__(NT) void k_wseries_dA(WArgs a, long slot) {
   double* R = sd + S32;
   double* U = sd + 2 * S32;
   load_A(a.d, a.A, A);
-  const int i = trow<32>(), j0 = tcol<32>();
-  double z[4] = {0.0, 0.0, 0.0, 0.0};
-  st<32>(R, z);
-  st<32>(U, z);
+  const v4d z = v4d{0.0, 0.0, 0.0, 0.0};
+  st_tile_d(R, z);
+  st_tile_d(U, z);
   __syncthreads();
+  const int tn = tile_n0() + tile_i();  // the lane's tile entries: rows tile_row_d(r) of column tn
+  v4d u = z;
   for (int ii = PW - 1; ii >= 0; --ii) {
-    double r[4], u[4];
-    mm<32, false, true>(R, A, r);  // R A^T
-    mm<32, true, false>(A, U, u);  // A^T U
+    v4d r = mm_tile_d<false, true>(R, A, z);  // R A^T
+    u = mm_tile_d<true, false>(A, U, z);      // A^T U
 #pragma unroll
     for (int c = 0; c < 4; ++c) {
-      r[c] += a.hsum[(size_t)(ii + 1) * MM + i * DP + j0 + c];
+      r[c] += a.hsum[(size_t)(ii + 1) * MM + tile_row_d(c) * DP + tn];
       u[c] += r[c];
     }
     __syncthreads();
-    st<32>(U, u);
-    st<32>(R, r);
+    st_tile_d(U, u);
+    st_tile_d(R, r);
     __syncthreads();
   }
-  double u[4];
-  ld<32>(U, u);
-  gst4(a.apart + slot * MM, float4{(float)u[0], (float)u[1], (float)u[2], (float)u[3]});
+#pragma unroll
+  for (int c = 0; c < 4; ++c) a.apart[slot * MM + tile_row_d(c) * DP + tn] = (float)u[c];
 }
 
 // The thread's four entries of the flow of interval t of sample b (registers), and their store into F and, transposed,
@@ -2028,7 +2193,7 @@ __global__ __launch_bounds__(NT) void k_wmat_bwd(WArgs a, int mode, long slot0) 
     const int t = per_interval ? (int)(it - (long)b * a.n) : 1;
     const float* th = a.clock + (size_t)b * a.L;
     float dh_f = 0.0f, dh_v = 0.0f;
-    const int flag = mode == 2 ? a.mflag[it] : 3;
+    const int flag = mode == 2 ? a.mflag[it] : a.sflag[it];  // the matrices outside the series radius
     const bool run_f = do_flow && (flag & 1), run_v = do_vl && (flag & 2);
     if (run_f) {
       bool ident;
@@ -2212,8 +2377,8 @@ int plan(const ews_dense_desc* s, WPlan& p) {
 }
 
 struct WLay {
-  size_t fl, vlm, loc, summ, sfl, car, rows, rpart, ridx, amax, apow, mflag, outs, mu, lend, dloc, dfl, cpart, dvlm, apart,
-      dv, dhl, dhm, dsh, hpart, hsum, ubuf, ebuf, total;
+  size_t fl, vlm, loc, summ, sfl, car, rows, rpart, ridx, amax, apow, mflag, sflag, outs, mu, lend, dloc, dfl, cpart,
+      dvlm, apart, dv, dhl, dhm, dsh, hpart, hsum, ubuf, ebuf, total;
 };
 
 WLay layout(const ews_dense_desc* s, const WPlan& p, bool bwd) {
@@ -2235,8 +2400,9 @@ WLay layout(const ews_dense_desc* s, const WPlan& p, bool bwd) {
   take(w.rpart, mm_ro ? BC * RW * 4 : 0);
   take(w.ridx, s->readout == EWS_READOUT_MAX ? BC * RW * 4 : 0);
   take(w.amax, s->readout == EWS_READOUT_MAX ? (size_t)p.B * p.W * 4 : 0);
-  take(w.apow, p.mats_int ? (size_t)APOW_FLOATS * 4 : 0);
+  take(w.apow, (size_t)APOW_FLOATS * 4);  // the series path serves both per-interval and per-sample matrices
   take(w.mflag, p.mats_int ? BN * 4 : 0);
+  take(w.sflag, p.mats_smp ? (size_t)p.B * 4 : 0);
   take(w.ubuf, p.vl_int ? BN * (PW + 1) * 32 * 4 : 0);
   if (bwd) {
     take(w.outs, s->readout == EWS_READOUT_MAX ? (size_t)p.B * p.W * 4 : 0);
@@ -2251,8 +2417,8 @@ WLay layout(const ews_dense_desc* s, const WPlan& p, bool bwd) {
     take(w.dhl, BN * 4);
     take(w.dhm, BN * 2 * 4);
     take(w.dsh, (size_t)p.B * 2 * 4);
-    take(w.hpart, (size_t)p.g_ser * (PW + 1) * MM * 4);
-    take(w.hsum, p.mats_int ? (size_t)(PW + 1) * MM * 8 : 0);
+    take(w.hpart, (size_t)(p.g_ser + (p.mats_smp ? p.B : 0)) * (PW + 1) * MM * 4);
+    take(w.hsum, (size_t)(PW + 1) * MM * 8);
     take(w.ebuf, p.vl_int ? BN * (PW + 1) * 32 * 4 : 0);
   }
   w.total = off;
@@ -2279,14 +2445,15 @@ WArgs make_args(const ews_dense_desc* s, const WPlan& p, const float* path, cons
   a.rpart = mm_ro ? f(w.rpart) : nullptr;
   a.ridx = s->readout == EWS_READOUT_MAX ? (int*)(ws + w.ridx) : nullptr;
   a.amax = s->readout == EWS_READOUT_MAX ? (int*)(ws + w.amax) : nullptr;
-  a.apow = p.mats_int ? f(w.apow) : nullptr;
+  a.apow = f(w.apow);
   a.mflag = p.mats_int ? (int*)(ws + w.mflag) : nullptr;
+  a.sflag = p.mats_smp ? (int*)(ws + w.sflag) : nullptr;
   a.ubuf = p.vl_int ? f(w.ubuf) : nullptr;
   if (bwd) {
     a.mu = f(w.mu); a.lend = f(w.lend); a.dloc = f(w.dloc);
     a.dfl = p.fl_int ? f(w.dfl) : nullptr; a.cpart = f(w.cpart); a.dvlm = p.vl_int ? f(w.dvlm) : nullptr;
     a.apart = f(w.apart); a.dv = f(w.dv); a.dhl = f(w.dhl); a.dhm = f(w.dhm); a.dsh = f(w.dsh);
-    a.hpart = f(w.hpart); a.hsum = p.mats_int ? (double*)(ws + w.hsum) : nullptr;
+    a.hpart = f(w.hpart); a.hsum = (double*)(ws + w.hsum);
     a.ebuf = p.vl_int ? f(w.ebuf) : nullptr;
   }
   return a;
@@ -2306,13 +2473,15 @@ int set_lds(const void* fn, size_t bytes) {
 int run_forward(const WPlan& p, const WArgs& a, hipStream_t st) {
   const size_t lds = MF_ENT_FWD * sizeof(double);
   if (set_lds(reinterpret_cast<const void*>(&k_wmat), lds) != EWS_OK) return EWS_ERR_LAUNCH;
-  if (p.mats_int) {  // the powers table, the series path, then the matrices outside its radius
-    hipLaunchKernelGGL(k_wpowers, dim3(1), dim3(NT), 0, st, a);
+  // the powers table, the series path, then the matrices outside its radius (LDS forms)
+  hipLaunchKernelGGL(k_wpowers, dim3(p.vl_int ? 2 : 1), dim3(NT), 0, st, a);
+  if (p.mats_int) {
     hipLaunchKernelGGL(k_wmat_series, dim3((unsigned)std::min<long>((long)p.B * p.n, 1024)), dim3(NT), 0, st, a);
     hipLaunchKernelGGL(k_wmat, dim3((unsigned)p.g_int, p.gy_int), dim3(NT), lds, st, a, 2);
     WIDE_CHECK();
   }
   if (p.mats_smp) {
+    hipLaunchKernelGGL(k_wmat_series_smp, dim3(p.B), dim3(NT), 0, st, a);
     hipLaunchKernelGGL(k_wmat, dim3(p.B, p.gy_smp), dim3(NT), lds, st, a, 0);
     WIDE_CHECK();
   }
@@ -2412,27 +2581,25 @@ int backward(const ews_dense_desc* s, const float* path, const float* clock, con
   }
   WIDE_CHECK();
   const long base = (long)p.B * p.NSL;
+  if (set_lds(reinterpret_cast<const void*>(&k_wmat_bwd), MF_ENT_BWD_EXACT * 4) != EWS_OK) return EWS_ERR_LAUNCH;
   if (p.mats_int) {
     const size_t lds = (p.exact_int ? MF_ENT_BWD_EXACT : MF_ENT_BWD) * 4;
-    if (set_lds(reinterpret_cast<const void*>(&k_wmat_bwd), MF_ENT_BWD_EXACT * 4) != EWS_OK)
-      return EWS_ERR_LAUNCH;
     hipLaunchKernelGGL(k_wmat_bwd_series, dim3((unsigned)p.g_ser), dim3(NT), 0, st, a);
     hipLaunchKernelGGL(k_wmat_bwd, dim3((unsigned)p.g_int, p.gy_int), dim3(NT), lds, st, a, 2, base);
-    hipLaunchKernelGGL(k_whsum, dim3(PW + 1, MM / 64), dim3(NT), 0, st, a, (int)p.g_ser);
-    hipLaunchKernelGGL(k_wseries_dA, dim3(1), dim3(NT), 0, st, a,
-                       base + p.g_int * p.gy_int + p.g_smp * p.gy_smp);
     WIDE_CHECK();
   }
   if (p.mats_smp) {
     const size_t lds = (p.exact_smp ? MF_ENT_BWD_EXACT : MF_ENT_BWD) * 4;
-    if (set_lds(reinterpret_cast<const void*>(&k_wmat_bwd), MF_ENT_BWD_EXACT * 4) != EWS_OK)
-      return EWS_ERR_LAUNCH;
+    hipLaunchKernelGGL(k_wmat_bwd_series_smp, dim3(p.B), dim3(NT), 0, st, a, (int)p.g_ser);
     hipLaunchKernelGGL(k_wmat_bwd, dim3((unsigned)p.g_smp, p.gy_smp), dim3(NT), lds, st, a, 0,
                        base + p.g_int * p.gy_int);
     WIDE_CHECK();
   }
+  // the series path's H_k: the per-interval workgroups' partials, then one per sample; one contraction into dA
+  hipLaunchKernelGGL(k_whsum, dim3(PW + 1, MM / 64), dim3(NT), 0, st, a, (int)(p.g_ser + (p.mats_smp ? p.B : 0)));
+  hipLaunchKernelGGL(k_wseries_dA, dim3(1), dim3(NT), 0, st, a, base + p.g_int * p.gy_int + p.g_smp * p.gy_smp);
   hipLaunchKernelGGL(k_wfinal_A, dim3(MM / 16), dim3(NT), 0, st, a, p.vl ? base : 0L,
-                     base + p.g_int * p.gy_int + p.g_smp * p.gy_smp + (p.mats_int ? 1 : 0), grad_A);
+                     base + p.g_int * p.gy_int + p.g_smp * p.gy_smp + 1, grad_A);
   hipLaunchKernelGGL(k_wknots, dim3((p.L + NT - 1) / NT, p.B), dim3(NT), 0, st, a, grad_path, grad_clock);
   WIDE_CHECK();
   return EWS_OK;

@@ -263,3 +263,24 @@ def test_wide_van_loan_knots_three_ways(scheme):
     tag = f"knots three ways {scheme}"
     _check_levels(out, ref, d, 2, 1e-5, tag)
     _check_grads(gg, rg, tag)
+
+
+@pytest.mark.parametrize("scheme", ["exact", "cayley", "euler", "pade"])
+@pytest.mark.parametrize("mode", ["displacement_uniform", "displacement_uniform_basepoint"])
+def test_wide_shared_steps_both_sides_of_the_radius(scheme, mode):
+    """Uniform reweighting modes: each sample's shared flow and Van Loan pair come from the powers table when
+    |dt| ||A||_1 is inside the series radius (sample 0) and from the scaled / inverted forms otherwise (sample 1,
+    flagged per sample), in one call; the adjoint splits the same way."""
+    rng = np.random.default_rng(29)
+    d, L = 20, 40
+    path = torch.tensor(np.cumsum(rng.normal(size=(2, L, d)) * 0.3, 1))
+    G = rng.normal(size=(d, d))
+    A = (G - G.T) * (0.5 / np.sqrt(d)) + np.eye(d)
+    nrm = np.abs(A).sum(0).max()
+    steps = np.array([0.05, 2.5]) / nrm  # |dt| ||A||_1: 0.05 and 2.5
+    clock = torch.tensor(np.arange(L)[None, :] * steps[:, None])
+    out, ref, gg, rg = _run(path, clock, torch.tensor(A), 2, "prefix", mode,
+                            dict(van_loan_expm=scheme, chen_expm=scheme, M=3), chunk=8)
+    tag = f"shared steps {scheme} {mode}"
+    _check_levels(out, ref, d, 2, 1e-5, tag)
+    _check_grads(gg, rg, tag)
