@@ -2167,6 +2167,237 @@ __global__ __launch_bounds__(NT) void k_wleaf_bwd(WArgs a) {
   if constexpr (!vl) gst4(a.apart + ((size_t)b * a.NSL + sl) * MM, acc4(dA));  // (the Van Loan leaf has none)
 }
 
+// ------------------------------------------------------------------------------------------------ slice leaf
+// The Van Loan leaf with the shared pair (uniform reweighting modes) and M <= VLS_M knots, a workgroup per slice of
+// VLS_T consecutive intervals of one sample: (P, V) is the same for every interval of the sample, so the knots of
+// the whole slice are products of 32 x 32 matrices with 32 x VLS_T blocks (one column per interval), the knots'
+// adjoint chain likewise, and the pair's cotangent sums over the slice are products over its intervals: a barrier
+// per product for the slice instead of one per matrix-vector product per interval. A step the mode fixes to the
+// identity (the basepoint interval) takes P = V = I: its column is patched after each product.
+constexpr int VLS_M = 4, VLS_T = 16, VLS_B = 32 * VLS_T;  // knots at most, intervals per slice, floats per block
+// LDS (floats) of the forward: P, V, W (the slice's w = v / M), knots D (VLS_M blocks), Y (VLS_M blocks)
+constexpr int VF_P = 0, VF_V = S32, VF_W = 2 * S32, VF_D = VF_W + VLS_B, VF_Y = VF_D + VLS_M * VLS_B,
+              VF_FLOATS = VF_Y + VLS_M * VLS_B;
+// of the backward: the same, then DD (the knots' cotangents), the cotangent staging of two intervals (ds2), the
+// slice's ds1 and s1 (S, the knots' sums); Y becomes the chain's lambda once DD is formed
+constexpr int VB_DD = VF_FLOATS, VB_G2 = VB_DD + VLS_M * VLS_B, VB_G1 = VB_G2 + 2 * S32, VB_S = VB_G1 + VLS_B,
+              VB_MASK = VB_S + VLS_B, VB_FLOATS = VB_MASK + VLS_T;
+
+// Z[r][t] = sum_k Mx(r, k) X[k][t] for the thread's row r = tid / 8 and columns t, t + 1 (t = 2 (tid % 8));
+// Mx(r, k) = Mx[k][r] when TM; Mx at pitch 36, X and Z blocks of 32 x VLS_T
+template <bool TM>
+__device__ __forceinline__ float2 mcols(const float* Mx, const float* X) {
+  const int r = (int)threadIdx.x >> 3, t = ((int)threadIdx.x & 7) * 2;
+  float2 acc = float2{0.0f, 0.0f};
+#pragma unroll 8
+  for (int k = 0; k < 32; ++k) {
+    const float m = TM ? Mx[k * P32 + r] : Mx[r * P32 + k];
+    const float2 x = *reinterpret_cast<const float2*>(X + k * VLS_T + t);
+    acc.x = fmaf(m, x.x, acc.x);
+    acc.y = fmaf(m, x.y, acc.y);
+  }
+  return acc;
+}
+
+// the slice's P, V (identity when the mode fixes every step), W and the fixed-column mask; returns the slice's
+// interval count
+__device__ int vls_stage(const WArgs& a, float* sm, int b, int t0, int t1, float* mask) {
+  const float* th = a.clock + (size_t)b * a.L;
+  bool all_fixed;
+  vl_step(a, th, 1, all_fixed);  // a zero shared step: every interval's pair is the identity
+  float* P = sm + VF_P;
+  float* V = sm + VF_V;
+  if (all_fixed) {
+    set_ident32(P, 1.0f);
+    set_ident32(V, 1.0f);
+  } else {
+    sld4(P, gld4(a.vlm + (size_t)b * 2 * MM));
+    sld4(V, gld4(a.vlm + (size_t)b * 2 * MM + MM));
+  }
+  const int nt = t1 - t0;
+  for (int e = threadIdx.x; e < VLS_B; e += NT) {  // W[k][t]
+    const int k = e / VLS_T, t = e - k * VLS_T;
+    float w = 0.0f;
+    if (t < nt && k < a.d) {
+      const float* x = a.path + ((size_t)b * a.L + t0 + t) * a.d;
+      w = (x[a.d + k] - x[k]) / (float)a.vm;
+    }
+    sm[VF_W + e] = w;
+  }
+  if (mask && threadIdx.x < VLS_T) {  // 1: the pair's cotangent gets this interval's terms
+    bool fixed = true;
+    if ((int)threadIdx.x < nt) vl_step(a, th, t0 + threadIdx.x, fixed);
+    mask[threadIdx.x] = fixed ? 0.0f : 1.0f;
+  }
+  return nt;
+}
+
+// knots of the slice: D_{M-1} = V W, D_{m-1} = P D_m (block m - 1 holds Delta_m); a fixed column keeps w
+__device__ void vls_knots(const WArgs& a, float* sm, int t0) {
+  const int M = a.vm, r = (int)threadIdx.x >> 3, t = ((int)threadIdx.x & 7) * 2;
+  const bool fix0 = a.vl_mode == EWS_FLOW_CACHED_BASEPOINT && t0 == 0;  // the basepoint interval: P = V = I
+  float* D = sm + VF_D;
+  const float* W = sm + VF_W;
+  __syncthreads();
+  float2 y = mcols<false>(sm + VF_V, W);
+  if (fix0 && t == 0) y.x = W[r * VLS_T];
+  *reinterpret_cast<float2*>(D + (M - 1) * VLS_B + r * VLS_T + t) = y;
+  __syncthreads();
+  for (int m = M - 1; m >= 1; --m) {
+    y = mcols<false>(sm + VF_P, D + m * VLS_B);
+    if (fix0 && t == 0) y.x = D[m * VLS_B + r * VLS_T];
+    *reinterpret_cast<float2*>(D + (m - 1) * VLS_B + r * VLS_T + t) = y;
+    __syncthreads();
+  }
+}
+
+// Y_m = Pre_m + Delta_m / 2 per (row, column) (thread: row tid / 8, columns 2 (tid % 8) .. + 1); returns the
+// columns' sums s1
+__device__ float2 vls_sums(int M, float* sm) {
+  const int r = (int)threadIdx.x >> 3, t = ((int)threadIdx.x & 7) * 2;
+  const float* D = sm + VF_D;
+  float* Y = sm + VF_Y;
+  float2 pre = float2{0.0f, 0.0f};
+  for (int m = 0; m < M; ++m) {
+    const float2 dm = *reinterpret_cast<const float2*>(D + m * VLS_B + r * VLS_T + t);
+    *reinterpret_cast<float2*>(Y + m * VLS_B + r * VLS_T + t) =
+        float2{fmaf(0.5f, dm.x, pre.x), fmaf(0.5f, dm.y, pre.y)};
+    pre.x += dm.x;
+    pre.y += dm.y;
+  }
+  return pre;
+}
+
+template <int N>
+__global__ __launch_bounds__(NT) void k_wleaf_vls(WArgs a) {
+  extern __shared__ __align__(16) float sm[];  // VF_FLOATS
+  const int sl = blockIdx.x, b = blockIdx.y, t0 = sl * VLS_T, t1 = min(a.n, t0 + VLS_T), M = a.vm;
+  const int nt = vls_stage(a, sm, b, t0, t1, nullptr);
+  vls_knots(a, sm, t0);
+  const float2 s1 = vls_sums(M, sm);
+  const int r = (int)threadIdx.x >> 3, tc = ((int)threadIdx.x & 7) * 2;
+  if (tc < nt) a.loc[((size_t)b * a.n + t0 + tc) * RW + r] = s1.x;
+  if (tc + 1 < nt) a.loc[((size_t)b * a.n + t0 + tc + 1) * RW + r] = s1.y;
+  if constexpr (N >= 2) {  // s2_t = sum_m Y_m Delta_m^T per interval: one MFMA tile per wavefront, K = the knots
+    __syncthreads();
+    const float* D = sm + VF_D;
+    const float* Y = sm + VF_Y;
+    const int m0 = tile_m0(), n0 = tile_n0(), ti = tile_i(), g = tile_g();  // g: the knot (K index)
+    for (int t = 0; t < nt; ++t) {
+      const float ya = g < M ? Y[g * VLS_B + (m0 + ti) * VLS_T + t] : 0.0f;
+      const float db = g < M ? D[g * VLS_B + (n0 + ti) * VLS_T + t] : 0.0f;
+      const v4f s2 = __builtin_amdgcn_mfma_f32_16x16x4f32(ya, db, zero4(), 0, 0, 0);
+      gst_tile(a.loc + ((size_t)b * a.n + t0 + t) * RW + DP, s2);
+    }
+  }
+}
+
+// Adjoint of the slice leaf: dDelta_m = ds1 + ds2 (S - Y_m) + ds2^T Y_m per interval (two intervals at a time:
+// Z_m = S - Y_m, S the interval's s1), then the chain lambda_0 = dD_0, lambda_m = dD_m + P^T lambda_{m-1} for the
+// slice, dP = sum_{m >= 1} lambda_{m-1} D_m^T and dV = lambda_{M-1} W^T over its non-fixed intervals (into cpart),
+// dv = V^T lambda_{M-1} / M
+template <int N>
+__global__ __launch_bounds__(NT) void k_wleaf_bwd_vls(WArgs a) {
+  extern __shared__ __align__(16) float sm[];  // VB_FLOATS
+  const int sl = blockIdx.x, b = blockIdx.y, t0 = sl * VLS_T, t1 = min(a.n, t0 + VLS_T), M = a.vm;
+  const int tid = threadIdx.x;
+  float* mask = sm + VB_MASK;
+  float* DD = sm + VB_DD;
+  float* G2 = sm + VB_G2;
+  float* G1 = sm + VB_G1;  // ds1 of the slice, G1[t][k]
+  // the slice's ds1 and the first two intervals' ds2, loaded ahead of the knots
+  const int nt = vls_stage(a, sm, b, t0, t1, mask);
+  for (int e = tid; e < VLS_B; e += NT) {
+    const int t = e >> 5, k = e & 31;
+    G1[e] = t < nt ? a.dloc[((size_t)b * a.n + t0 + t) * RW + k] : 0.0f;
+  }
+  float4 nd2[2] = {float4{0.0f, 0.0f, 0.0f, 0.0f}, float4{0.0f, 0.0f, 0.0f, 0.0f}};
+  auto fetch = [&](int tp) {
+#pragma unroll
+    for (int u = 0; u < 2; ++u)
+      if (N >= 2 && tp + u < nt) nd2[u] = gld4(a.dloc + ((size_t)b * a.n + t0 + tp + u) * RW + DP);
+  };
+  fetch(0);
+  for (int e = tid; e < VLS_M * VLS_B; e += NT) DD[e] = 0.0f;  // the columns past the slice's end stay zero
+  vls_knots(a, sm, t0);
+  {
+    const float2 s1 = vls_sums(M, sm);
+    *reinterpret_cast<float2*>(sm + VB_S + (tid >> 3) * VLS_T + (tid & 7) * 2) = s1;
+  }
+  // dD for two intervals at a time: thread (u = tid / 128, m = (tid / 32) % 4, row = tid % 32)
+  const int u = tid >> 7, mm = (tid >> 5) & 3, row = tid & 31;
+  const float* Y = sm + VF_Y;
+  const float* D = sm + VF_D;
+  for (int tp = 0; tp < nt; tp += 2) {
+    if constexpr (N >= 2) {
+      sld4(G2, nd2[0]);
+      sld4(G2 + S32, nd2[1]);
+    }
+    __syncthreads();
+    if (tp + 2 < nt) fetch(tp + 2);
+    const int t = tp + u;
+    if (mm < M && t < nt) {
+      float v = G1[t * 32 + row];
+      if constexpr (N >= 2) {
+        const float* g2 = G2 + u * S32;
+        const float* y = Y + mm * VLS_B + t;
+        const float* sv = sm + VB_S + t;
+        float sz = 0.0f, sy = 0.0f;  // (ds2 Z_m)[row], (ds2^T Y_m)[row]
+#pragma unroll 8
+        for (int k = 0; k < 32; ++k) {
+          const float yk = y[k * VLS_T];
+          sz = fmaf(g2[row * P32 + k], sv[k * VLS_T] - yk, sz);
+          sy = fmaf(g2[k * P32 + row], yk, sy);
+        }
+        v += sz + sy;
+      }
+      DD[mm * VLS_B + row * VLS_T + t] = v;
+    }
+    __syncthreads();
+  }
+  // the chain over the slice (Y's blocks become lambda): L_0 = DD_0, L_m = DD_m + P^T L_{m-1}; a fixed column
+  // (P = I) adds L_{m-1} itself
+  float* L = sm + VF_Y;
+  const int r = tid >> 3, tc = (tid & 7) * 2;
+  const bool fix0 = a.vl_mode == EWS_FLOW_CACHED_BASEPOINT && t0 == 0;
+  *reinterpret_cast<float2*>(L + r * VLS_T + tc) = *reinterpret_cast<const float2*>(DD + r * VLS_T + tc);
+  __syncthreads();
+  for (int m = 1; m < M; ++m) {
+    float2 y2 = mcols<true>(sm + VF_P, L + (m - 1) * VLS_B);
+    if (fix0 && tc == 0) y2.x = L[(m - 1) * VLS_B + r * VLS_T];
+    const float2 dd = *reinterpret_cast<const float2*>(DD + m * VLS_B + r * VLS_T + tc);
+    *reinterpret_cast<float2*>(L + m * VLS_B + r * VLS_T + tc) = float2{dd.x + y2.x, dd.y + y2.y};
+    __syncthreads();
+  }
+  // dv = V^T L_{M-1} / M (a fixed column: L_{M-1} / M)
+  {
+    float2 y2 = mcols<true>(sm + VF_V, L + (M - 1) * VLS_B);
+    if (fix0 && tc == 0) y2.x = L[(M - 1) * VLS_B + r * VLS_T];
+    if (r < a.d) {
+      if (tc < nt) a.dv[((size_t)b * a.n + t0 + tc) * DP + r] = y2.x / (float)M;
+      if (tc + 1 < nt) a.dv[((size_t)b * a.n + t0 + tc + 1) * DP + r] = y2.y / (float)M;
+    }
+  }
+  // dP = sum_{m >= 1} L_{m-1} D_m^T, dV = L_{M-1} W^T over the non-fixed intervals: products over the slice's
+  // columns (K = VLS_T, four k-steps) on MFMA, the wavefront's tile of each
+  const float* W = sm + VF_W;
+  const int m0 = tile_m0(), n0 = tile_n0(), ti = tile_i(), g = tile_g();
+  v4f gp = zero4(), gv = zero4();
+#pragma unroll
+  for (int uu = 0; uu < VLS_T / 4; ++uu) {
+    const int t = 4 * uu + g;
+    const float mk = mask[t];
+    for (int m = 1; m < M; ++m)
+      gp = __builtin_amdgcn_mfma_f32_16x16x4f32(mk * L[(m - 1) * VLS_B + (m0 + ti) * VLS_T + t],
+                                               D[m * VLS_B + (n0 + ti) * VLS_T + t], gp, 0, 0, 0);
+    gv = __builtin_amdgcn_mfma_f32_16x16x4f32(mk * L[(M - 1) * VLS_B + (m0 + ti) * VLS_T + t],
+                                             W[(n0 + ti) * VLS_T + t], gv, 0, 0, 0);
+  }
+  float* cp = a.cpart + ((size_t)b * a.CP + sl) * 3 * MM;
+  gst_tile(cp + MM, gp);
+  gst_tile(cp + 2 * MM, gv);
+}
+
 // Matrix-function adjoints. per_interval: one item per interval, the flow's (dfl) and the Van Loan pair's (dvlm)
 // cotangents of the per-interval modes, dh into dhm (flow, Van Loan); else one item per sample, the partials of the
 // shared flow (per chunk) and pair (per leaf slice) summed in order, the shared steps' gradients into dsh[b][0..1].
@@ -2327,7 +2558,7 @@ constexpr int kLeafSlice = 16;  // intervals per workgroup of the leaf adjoint
 
 struct WPlan {
   int B, L, n, d, N, T, C, W, TL, NSL, CP, rows;  // rows: knots M or letters q + 1 of the leaf tables
-  bool fl_int, vl, vl_int, exact_int, exact_smp, mats_int, mats_smp;
+  bool fl_int, vl, vl_int, vls, exact_int, exact_smp, mats_int, mats_smp;
   long g_int, g_smp;   // workgroups of the matrix-function adjoints (per grid row; per interval: the flagged ones)
   long g_ser;          // workgroups of the series path's adjoint
   int gy_int, gy_smp;  // grid rows: 2 when both the flows and the Van Loan pairs are of that kind
@@ -2364,6 +2595,8 @@ int plan(const ews_dense_desc* s, WPlan& p) {
   p.vl = vl;
   p.rows = vl ? s->vl_steps : s->series_q + 1;
   p.vl_int = vl && s->vl_mode == EWS_FLOW_PER_INTERVAL;
+  static_assert(kLeafSlice == VLS_T, "the slice leaf kernels take the leaf adjoint's slices");
+  p.vls = vl && !p.vl_int && s->vl_steps <= VLS_M;  // the shared pair with few knots: slice leaf kernels
   p.mats_int = p.fl_int || p.vl_int;
   p.mats_smp = !p.fl_int || (vl && !p.vl_int);
   p.exact_int = (p.fl_int && s->chen_expm == EWS_EXPM_EXACT) || (p.vl_int && s->vl_expm == EWS_EXPM_EXACT);
@@ -2492,14 +2725,18 @@ int run_forward(const WPlan& p, const WArgs& a, hipStream_t st) {
                             : (p.vl_int ? reinterpret_cast<const void*>(&k_wleaf<2, true>)
                                         : reinterpret_cast<const void*>(&k_wleaf<2, false>));
   if (set_lds(kl, lds_leaf) != EWS_OK) return EWS_ERR_LAUNCH;
+  const dim3 gs(p.NSL, p.B);
+  const size_t lds_vls = (size_t)VF_FLOATS * 4;
   if (p.N == 1) {
-    if (p.vl_int) hipLaunchKernelGGL((k_wleaf<1, true>), gl, dim3(NT), lds_leaf, st, a);
+    if (p.vls) hipLaunchKernelGGL(k_wleaf_vls<1>, gs, dim3(NT), lds_vls, st, a);
+    else if (p.vl_int) hipLaunchKernelGGL((k_wleaf<1, true>), gl, dim3(NT), lds_leaf, st, a);
     else hipLaunchKernelGGL((k_wleaf<1, false>), gl, dim3(NT), lds_leaf, st, a);
     hipLaunchKernelGGL((k_wscan<1, SCAN_SUMMARY>), gc, dim3(NT), 0, st, a);
     hipLaunchKernelGGL(k_wcarry<1>, dim3(p.B), dim3(NT), 0, st, a);
     hipLaunchKernelGGL((k_wscan<1, SCAN_ROWS>), gc, dim3(NT), 0, st, a);
   } else {
-    if (p.vl_int) hipLaunchKernelGGL((k_wleaf<2, true>), gl, dim3(NT), lds_leaf, st, a);
+    if (p.vls) hipLaunchKernelGGL(k_wleaf_vls<2>, gs, dim3(NT), lds_vls, st, a);
+    else if (p.vl_int) hipLaunchKernelGGL((k_wleaf<2, true>), gl, dim3(NT), lds_leaf, st, a);
     else hipLaunchKernelGGL((k_wleaf<2, false>), gl, dim3(NT), lds_leaf, st, a);
     hipLaunchKernelGGL((k_wscan<2, SCAN_SUMMARY>), gc, dim3(NT), 0, st, a);
     hipLaunchKernelGGL(k_wcarry<2>, dim3(p.B), dim3(NT), 0, st, a);
@@ -2566,7 +2803,9 @@ int backward(const ews_dense_desc* s, const float* path, const float* clock, con
     hipLaunchKernelGGL((k_wadj<1, ADJ_LOCAL>), gc, dim3(NT), 0, st, a);
     hipLaunchKernelGGL(k_wadj_carry<1>, dim3(p.B), dim3(NT), 0, st, a);
     hipLaunchKernelGGL((k_wadj<1, ADJ_FULL>), gc, dim3(NT), 0, st, a);
-    if (lk == LK_SERIES) hipLaunchKernelGGL((k_wleaf_bwd<1, LK_SERIES>), dim3(p.NSL, p.B), dim3(NT), lds_lb, st, a);
+    if (p.vls) hipLaunchKernelGGL(k_wleaf_bwd_vls<1>, dim3(p.NSL, p.B), dim3(NT), (size_t)VB_FLOATS * 4, st, a);
+    else if (lk == LK_SERIES)
+      hipLaunchKernelGGL((k_wleaf_bwd<1, LK_SERIES>), dim3(p.NSL, p.B), dim3(NT), lds_lb, st, a);
     else if (lk == LK_VL_SHARED)
       hipLaunchKernelGGL((k_wleaf_bwd<1, LK_VL_SHARED>), dim3(p.NSL, p.B), dim3(NT), lds_lb, st, a);
     else hipLaunchKernelGGL((k_wleaf_bwd<1, LK_VL_INT>), dim3(p.NSL, p.B), dim3(NT), lds_lb, st, a);
@@ -2574,7 +2813,9 @@ int backward(const ews_dense_desc* s, const float* path, const float* clock, con
     hipLaunchKernelGGL((k_wadj<2, ADJ_LOCAL>), gc, dim3(NT), 0, st, a);
     hipLaunchKernelGGL(k_wadj_carry<2>, dim3(p.B), dim3(NT), 0, st, a);
     hipLaunchKernelGGL((k_wadj<2, ADJ_FULL>), gc, dim3(NT), 0, st, a);
-    if (lk == LK_SERIES) hipLaunchKernelGGL((k_wleaf_bwd<2, LK_SERIES>), dim3(p.NSL, p.B), dim3(NT), lds_lb, st, a);
+    if (p.vls) hipLaunchKernelGGL(k_wleaf_bwd_vls<2>, dim3(p.NSL, p.B), dim3(NT), (size_t)VB_FLOATS * 4, st, a);
+    else if (lk == LK_SERIES)
+      hipLaunchKernelGGL((k_wleaf_bwd<2, LK_SERIES>), dim3(p.NSL, p.B), dim3(NT), lds_lb, st, a);
     else if (lk == LK_VL_SHARED)
       hipLaunchKernelGGL((k_wleaf_bwd<2, LK_VL_SHARED>), dim3(p.NSL, p.B), dim3(NT), lds_lb, st, a);
     else hipLaunchKernelGGL((k_wleaf_bwd<2, LK_VL_INT>), dim3(p.NSL, p.B), dim3(NT), lds_lb, st, a);
