@@ -2138,9 +2138,10 @@ __global__ __launch_bounds__(256) void k_vl_bwd(Args a, LeafBwd o) {
   Mat* Esq = reinterpret_cast<Mat*>(U);
   Mat* Fsq = Esq + SQMAX;
   __shared__ __align__(16) float dS1[16], wv[16], lam[16], red[8];
-  // depth 3: per-wavefront partial sums of each segment's column cotangents (double-buffered by segment parity),
-  // summed in a fixed order
-  __shared__ float wR[2][4][16], wD[2][4][16], rowD[2][16];
+  // depth 3: per-wavefront partial sums of the column cotangents of a block of VB knots, summed in a fixed order
+  // once per block
+  constexpr int VB = 8;
+  __shared__ float wR[VB][4][16], wD[VB][4][16], rowD[VB][16];
   const int tid = threadIdx.x, i = tid >> 4, j = tid & 15, l = tid & 63, g = l >> 4, c16 = l & 15;
   const int wv_id = tid >> 6;
   const int Mv = a.vm, vs = 512 + 16 * Mv;
@@ -2180,20 +2181,31 @@ __global__ __launch_bounds__(256) void k_vl_bwd(Args a, LeafBwd o) {
     }
     Gm[tid] = a.fl[((size_t)b * a.n_int + t) * 256 + tid];  // dM_t
     __syncthreads();
-    if (tid < 16) {  // Pre, R, Y, X; level-1 cotangent; zero the other accumulators
-      float pre = 0.0f, suf = 0.0f;
-      for (int m = Mv - 1; m >= 0; --m) {
-        Rs[m][tid] = suf;
-        suf += Dl[m][tid];
+    {  // Pre, R, Y, X; level-1 cotangent; zero the other accumulators. 16 lanes per column, a segment of
+       // ceil(M / 16) knots each: the segments' sums scanned across the lanes, then each lane walks its segment
+      const int col = tid >> 4, seg = tid & 15, S = (Mv + 15) >> 4, m0 = min(Mv, seg * S), m1 = min(Mv, m0 + S);
+      float own = 0.0f;
+      for (int m = m0; m < m1; ++m) own += Dl[m][col];
+      float inc = own;
+#pragma unroll
+      for (int o = 1; o < 16; o <<= 1) {
+        const float v = __shfl_up(inc, o, 16);
+        if (seg >= o) inc += v;
       }
-      for (int m = 0; m < Mv; ++m) {
-        const float dm = Dl[m][tid];
-        Ys[m][tid] = fmaf(0.5f, dm, pre);
-        Xs[m][tid] = fmaf(1.0f / 3.0f, dm, pre);
+      const float total = __shfl(inc, 15, 16);
+      float pre = inc - own, suf = total - inc;
+      for (int m = m0; m < m1; ++m) {
+        const float dm = Dl[m][col];
+        Ys[m][col] = fmaf(0.5f, dm, pre);
+        Xs[m][col] = fmaf(1.0f / 3.0f, dm, pre);
         pre += dm;
-        dD[m][tid] = dS1[tid];
-        dP[m][tid] = 0.0f;
-        dR[m][tid] = 0.0f;
+        dD[m][col] = dS1[col];
+        dP[m][col] = 0.0f;
+        dR[m][col] = 0.0f;
+      }
+      for (int m = m1 - 1; m >= m0; --m) {  // R_m: the knots after m
+        Rs[m][col] = suf;
+        suf += Dl[m][col];
       }
     }
     __syncthreads();
@@ -2219,7 +2231,9 @@ __global__ __launch_bounds__(256) void k_vl_bwd(Args a, LeafBwd o) {
         colb[k] = dS3[i * 256 + k * 16 + j];
         rowc[k] = dS3[i * 256 + j * 16 + ((k + j) & 15)];  // skewed: conflict-free across the 16 lanes
       }
-      for (int m = 0; m < Mv; ++m) {
+      for (int mb = 0; mb < Mv; mb += VB) {
+      const int me = min(Mv, mb + VB);
+      for (int m = mb; m < me; ++m) {
         float q = 0.0f, e1 = 0.0f, f1 = 0.0f;
 #pragma unroll
         for (int k = 0; k < 16; ++k) {
@@ -2241,7 +2255,7 @@ __global__ __launch_bounds__(256) void k_vl_bwd(Args a, LeafBwd o) {
           pr2 += __shfl_xor(pr2, o2, 64);
           pd += __shfl_xor(pd, o2, 64);
         }
-        const int sb = m & 1;
+        const int sb = m - mb;
         if (j == 0) {  // row i lives in one wavefront: a single writer
           dP[m][i] += py + px;
           rowD[sb][i] = fmaf(0.5f, py, px * (1.0f / 3.0f));
@@ -2250,27 +2264,46 @@ __global__ __launch_bounds__(256) void k_vl_bwd(Args a, LeafBwd o) {
           wR[sb][wv_id][j] = pr2;
           wD[sb][wv_id][j] = pd;
         }
-        __syncthreads();
-        if (tid < 16) {
-          dR[m][tid] += ((wR[sb][0][tid] + wR[sb][1][tid]) + wR[sb][2][tid]) + wR[sb][3][tid];
-          dD[m][tid] += rowD[sb][tid] + (((wD[sb][0][tid] + wD[sb][1][tid]) + wD[sb][2][tid]) + wD[sb][3][tid]);
-        }
       }
       __syncthreads();
+      {  // the block's partials: thread (knot mb + tid / 16, column tid % 16)
+        const int sb = tid >> 4, c = tid & 15;
+        if (sb < me - mb) {
+          const int m = mb + sb;
+          dR[m][c] += ((wR[sb][0][c] + wR[sb][1][c]) + wR[sb][2][c]) + wR[sb][3][c];
+          dD[m][c] += rowD[sb][c] + (((wD[sb][0][c] + wD[sb][1][c]) + wD[sb][2][c]) + wD[sb][3][c]);
+        }
+      }
+      __syncthreads();  // before the next block's partials
+      }
     }
-    // Pre and R -> Delta (dP holds dPre)
-    if (tid < 16) {
-      float acc = 0.0f;  // sum_{m > j} dPre_m
-      for (int m = Mv - 1; m >= 0; --m) {
-        dD[m][tid] += acc;
-        acc += dP[m][tid];
+    // Pre and R -> Delta (dP holds dPre): dDelta_m += sum_{m' > m} dPre_m' + sum_{m' < m} dR_m', segments as above
+    {
+      const int col = tid >> 4, seg = tid & 15, S = (Mv + 15) >> 4, m0 = min(Mv, seg * S), m1 = min(Mv, m0 + S);
+      float ownP = 0.0f, ownR = 0.0f;
+      for (int m = m0; m < m1; ++m) {
+        ownP += dP[m][col];
+        ownR += dR[m][col];
       }
-      acc = 0.0f;  // sum_{m < j} dR_m
-      for (int m = 0; m < Mv; ++m) {
-        dD[m][tid] += acc;
-        acc += dR[m][tid];
+      float incP = ownP, incR = ownR;
+#pragma unroll
+      for (int o = 1; o < 16; o <<= 1) {
+        const float vp = __shfl_up(incP, o, 16), vr = __shfl_up(incR, o, 16);
+        if (seg >= o) {
+          incP += vp;
+          incR += vr;
+        }
       }
-      lam[tid] = dD[0][tid];
+      float accP = __shfl(incP, 15, 16) - incP, accR = incR - ownR;
+      for (int m = m1 - 1; m >= m0; --m) {
+        dD[m][col] += accP;
+        accP += dP[m][col];
+      }
+      for (int m = m0; m < m1; ++m) {
+        dD[m][col] += accR;
+        accR += dR[m][col];
+      }
+      if (seg == 0) lam[col] = dD[0][col];
     }
     __syncthreads();
     // ---- the chain in reverse, one wavefront
