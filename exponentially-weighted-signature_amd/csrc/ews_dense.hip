@@ -302,8 +302,7 @@ __global__ __launch_bounds__(256, QB <= 24 ? 3 : 2) void k_local3(Args a) {
     for (int pp = 1; pp <= q; ++pp) {
       const f4 bp = *reinterpret_cast<const f4*>(L + (pp - 1) * 16 + 4 * g);
       float sm = fmaf(a4.x, bp.x, fmaf(a4.y, bp.y, fmaf(a4.z, bp.z, a4.w * bp.w)));
-      sm += __shfl_xor(sm, 16, 64);
-      sm += __shfl_xor(sm, 32, 64);
+      sm = lanes::add_xor32(lanes::add_xor16(sm));
       const float bv = sm * (-h * inv[pp]);
       if (g == 0) L[pp * 16 + c16] = bv;
       if (g == 1) G1[pp * 16 + c16] = bv * inv[pp + 1];
@@ -1085,8 +1084,7 @@ __global__ __launch_bounds__(N >= 3 ? 256 : 64) void k_scan(Seq s) {
       float part = 0.0f;
 #pragma unroll
       for (int r = 0; r < 4; ++r) part = fmaf(M4[r], S1g[r], part);  // sum over j = 4g + r of M[c16][j] S1[j]
-      part += __shfl_xor(part, 16, 64);
-      part += __shfl_xor(part, 32, 64);
+      part = lanes::add_xor32(lanes::add_xor16(part));
       n1 = part + cur.s1k;
     }
     if constexpr (SUMMARY) {
@@ -1626,8 +1624,7 @@ __device__ __forceinline__ float frcp(int n) { return __builtin_amdgcn_rcpf((flo
 
 // workgroup sum (256 threads) of one value per thread; red: 4 floats of LDS. Every thread gets the sum.
 __device__ __forceinline__ float block_sum(float v, float* red, int tid) {
-#pragma unroll
-  for (int o2 = 1; o2 < 64; o2 <<= 1) v += __shfl_xor(v, o2, 64);
+  v = lanes::sum64(v);
   __syncthreads();
   if ((tid & 63) == 0) red[tid >> 6] = v;
   __syncthreads();
@@ -2250,11 +2247,8 @@ __global__ __launch_bounds__(256) void k_vl_bwd(Args a, LeafBwd o) {
         // over the first index (rows i of the wave, then the four wavefronts' partials in a fixed order):
         // dR_m[j], dDelta_m[j]
         float pr2 = q * yi, pd = fmaf(0.5f * q, xi, fmaf(yi, e1, 0.5f * xi * f1));
-#pragma unroll
-        for (int o2 = 16; o2 < 64; o2 <<= 1) {
-          pr2 += __shfl_xor(pr2, o2, 64);
-          pd += __shfl_xor(pd, o2, 64);
-        }
+        pr2 = lanes::add_xor32(lanes::add_xor16(pr2));
+        pd = lanes::add_xor32(lanes::add_xor16(pd));
         const int sb = m - mb;
         if (j == 0) {  // row i lives in one wavefront: a single writer
           dP[m][i] += py + px;
@@ -2320,8 +2314,7 @@ __global__ __launch_bounds__(256) void k_vl_bwd(Args a, LeafBwd o) {
 #pragma unroll
         for (int r = 0; r < 4; ++r) gp[r] = fmaf(li, dm[r], gp[r]);
         float u = fmaf(pc.x, lv.x, fmaf(pc.y, lv.y, fmaf(pc.z, lv.z, pc.w * lv.w)));
-        u += __shfl_xor(u, 16, 64);
-        u += __shfl_xor(u, 32, 64);
+        u = lanes::add_xor32(lanes::add_xor16(u));
         wave_order_d();
         if (g == 0) lam[c16] = dD[m][c16] + u;
         wave_order_d();

@@ -618,8 +618,7 @@ __device__ __forceinline__ void mix_block(const DiagArgs& a, const MixEpi& e, in
       }
     }
     float v = ssq[k];
-    v += __shfl_xor(v, 16, 64);
-    v += __shfl_xor(v, 32, 64);
+    v = lanes::add_xor32(lanes::add_xor16(v));
     if (g == 0) s_ssq[((size_t)w * N + k) * 16 + i] = v;
   }
   __syncthreads();
@@ -1296,8 +1295,7 @@ __device__ __forceinline__ void stage_vec(const DiagArgs& a, int b, float* s_gv,
 }
 
 __device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-  for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o, 64);
+  v = lanes::sum64(v);
   return v;
 }
 // sums over k (lanes 8j .. 8j+7) and over j (lanes k, k+8, ..), by DPP where the lanes share a row of 16

@@ -27,6 +27,7 @@
 #include <cstdint>
 
 #include "ews_hip.h"
+#include "ews_lanes.h"
 
 namespace ews {
 namespace front {
@@ -36,14 +37,8 @@ constexpr int LR = 128;  // lift rows per workgroup
 constexpr int MAXK = 8;  // clamped_gate rows
 
 // ------------------------------------------------------------------------------------------------ block helpers
-__device__ __forceinline__ double wave_sum(double v) {
-  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
-  return v;
-}
-__device__ __forceinline__ float wave_sumf(float v) {
-  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
-  return v;
-}
+__device__ __forceinline__ double wave_sum(double v) { return lanes::sum64(v); }
+__device__ __forceinline__ float wave_sumf(float v) { return lanes::sum64(v); }
 
 // sum over the 256 threads, returned to all (sh: 4 doubles of LDS)
 __device__ double block_sum(double v, double* sh) {

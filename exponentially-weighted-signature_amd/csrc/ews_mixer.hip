@@ -26,6 +26,7 @@
 #include <type_traits>
 
 #include "ews_hip.h"
+#include "ews_lanes.h"
 
 namespace ews {
 namespace mixer {
@@ -147,8 +148,7 @@ __global__ __launch_bounds__(256) void k_mix_fwd(MArgs a) {
 #pragma unroll
     for (int rt = 0; rt < RT; ++rt) {
       float v = ssq[k][rt];
-      v += __shfl_xor(v, 16, 64);
-      v += __shfl_xor(v, 32, 64);
+      v = lanes::add_xor32(lanes::add_xor16(v));
       if (g == 0) {
         const int gr = row0 + 16 * rt + i;
         const int t = valid[rt] ? gr % a.R : 0;
@@ -316,8 +316,7 @@ __global__ __launch_bounds__(256) void k_mix_fwd_s(MArgs a) {
     sfor<0, N>([&](auto kc) {
       constexpr int kx = kc;
       float v = ssq[kx][rt];
-      v += __shfl_xor(v, 16, 64);
-      v += __shfl_xor(v, 32, 64);
+      v = lanes::add_xor32(lanes::add_xor16(v));
       const int t = vi ? gi % a.R : 0;
       const int K = kx + 1;
       float c = 1.0f;
@@ -405,8 +404,7 @@ __global__ __launch_bounds__(256) void k_mix_bwd(MArgs a) {
         const float* pp = a.P + ((size_t)gr * N + k) * a.hidden;
         for (int h = g; h < a.hidden; h += 4) dot = fmaf(pp[h], drp[rt][h], dot);
       }
-      dot += __shfl_xor(dot, 16, 64);
-      dot += __shfl_xor(dot, 32, 64);
+      dot = lanes::add_xor32(lanes::add_xor16(dot));
       if (g == 0) {
         float f = 0.0f, bd = 0.0f;
         if (valid) {

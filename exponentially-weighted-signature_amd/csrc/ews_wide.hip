@@ -54,6 +54,7 @@
 namespace ews {
 namespace wide {
 using lanes::colsum8;
+using lanes::sum64;
 using lanes::sum8;
 
 constexpr int DP = 32;            // padded channels
@@ -219,8 +220,7 @@ __device__ __forceinline__ void gst_tile(float* g, v4f v) {
 
 // sum over the workgroup (every thread returns it); red: NT / 64 floats of LDS
 __device__ __forceinline__ float block_sum(float v, float* red) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+  v = sum64(v);
   __syncthreads();
   if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
   __syncthreads();
@@ -920,11 +920,8 @@ __global__ __launch_bounds__(NT) void k_wmat_series_smp(WArgs a) {
 // are read after the call returns and rewritten only after the next call's first barrier
 __device__ __forceinline__ float2 block_sum2_cols(float u, float v, const float* dw, bool cols, float* red,
                                                   float* redw) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) {
-    u += __shfl_xor(u, o, 64);
-    v += __shfl_xor(v, o, 64);
-  }
+  u = sum64(u);
+  v = sum64(v);
   __syncthreads();
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
   if (lane == 0) {
@@ -2152,8 +2149,7 @@ __global__ __launch_bounds__(NT) void k_wleaf_bwd(WArgs a) {
       // dh: the 32 partials of threads 0..31 (wavefront 0)
       float s = tid < 32 ? dh : 0.0f;
       if (tid < 64) {
-#pragma unroll
-        for (int o = 16; o > 0; o >>= 1) s += __shfl_xor(s, o, 64);
+        s = lanes::sum_n(s, 32);
         if (tid == 0) a.dhl[r] = s;
       }
     }
