@@ -2142,7 +2142,8 @@ __global__ __launch_bounds__(256) void k_vl_bwd(Args a, LeafBwd o) {
   const int tid = threadIdx.x, i = tid >> 4, j = tid & 15, l = tid & 63, g = l >> 4, c16 = l & 15;
   const int wv_id = tid >> 6;
   const int Mv = a.vm, vs = 512 + 16 * Mv;
-  for (int e = tid; e < HP * 256; e += 256) sp[e >> 8][e & 255] = a.apow[e];
+#pragma unroll
+  for (int p = 0; p < HP; ++p) sp[p][tid] = a.apow[p * 256 + tid];
   const float norm1 = a.apow[a.npow * 256];
   float H[HP];
 #pragma unroll
@@ -2155,8 +2156,27 @@ __global__ __launch_bounds__(256) void k_vl_bwd(Args a, LeafBwd o) {
     const float* th = a.clock + (size_t)b * a.L;
     const float* drow = a.loc + ((size_t)b * a.n_int + t) * LW;
     const float* sv = a.vlsave + ((size_t)b * a.n_int + t) * vs;
-    // ---- saved step matrices and increments (delta = 0: the identity of the jump / basepoint interval)
-    bool fixed = false;  // P = V = I, no dependence on A or the clock
+    // ---- saved step matrices and increments: every input of the interval is loaded into registers before the
+    // first store to LDS, so that the loads' latencies overlap (the knots as one float4 per thread: M <= 64; dS3 as
+    // four); the clock's loads after them, since the step's first use waits for every load before it
+    const float in_p = sv[tid], in_v = sv[256 + tid];
+    const float in_g = a.fl[((size_t)b * a.n_int + t) * 256 + tid];  // dM_t
+    const bool dl_own = tid < Mv * 4;
+    f4 in_d = {0.0f, 0.0f, 0.0f, 0.0f};
+    if (dl_own) in_d = reinterpret_cast<const f4*>(sv + 512)[tid];
+    float in_s2 = 0.0f, in_w = 0.0f, in_s1 = 0.0f;
+    if constexpr (N >= 2) in_s2 = drow[16 + tid];
+    f4 in_s3[N >= 3 ? 4 : 1];
+    if constexpr (N >= 3) {
+#pragma unroll
+      for (int m = 0; m < 4; ++m) in_s3[m] = reinterpret_cast<const f4*>(drow + 272)[tid + 256 * m];
+    }
+    if (tid < 16) {
+      const float* x = a.path + ((size_t)b * a.L + t) * a.d;
+      in_w = tid < a.d ? (x[a.d + tid] - x[tid]) / (float)Mv : 0.0f;
+      in_s1 = drow[tid];
+    }
+    bool fixed = false;  // delta = 0: P = V = I (the jump / basepoint interval), no dependence on A or the clock
     float delta;
     if (a.vl_mode == EWS_FLOW_PER_INTERVAL) {
       delta = (th[t + 1] - th[t]) / (float)Mv;
@@ -2164,19 +2184,19 @@ __global__ __launch_bounds__(256) void k_vl_bwd(Args a, LeafBwd o) {
       delta = vl_shared_step(a, th);
       fixed = delta == 0.0f || (a.vl_mode == EWS_FLOW_CACHED_BASEPOINT && t == 0);
     }
-    Pm[tid] = sv[tid];
-    Vm[tid] = sv[256 + tid];
-    for (int e = tid; e < Mv * 16; e += 256) Dl[e >> 4][e & 15] = sv[512 + e];
+    Pm[tid] = in_p;
+    Vm[tid] = in_v;
+    if (dl_own) reinterpret_cast<f4*>(U)[tid] = in_d;  // Dl[m][c] at U[16 m + c]
     if (tid < 16) {
-      const float* x = a.path + ((size_t)b * a.L + t) * a.d;
-      wv[tid] = tid < a.d ? (x[a.d + tid] - x[tid]) / (float)Mv : 0.0f;
-      dS1[tid] = drow[tid];
+      wv[tid] = in_w;
+      dS1[tid] = in_s1;
     }
-    if constexpr (N >= 2) dS2[tid] = drow[16 + tid];
+    if constexpr (N >= 2) dS2[tid] = in_s2;
     if constexpr (N >= 3) {
-      for (int e = tid; e < 4096; e += 256) dS3[e] = drow[272 + e];
+#pragma unroll
+      for (int m = 0; m < 4; ++m) reinterpret_cast<f4*>(dS3)[tid + 256 * m] = in_s3[m];
     }
-    Gm[tid] = a.fl[((size_t)b * a.n_int + t) * 256 + tid];  // dM_t
+    Gm[tid] = in_g;
     __syncthreads();
     {  // Pre, R, Y, X; level-1 cotangent; zero the other accumulators. 16 lanes per column, a segment of
        // ceil(M / 16) knots each: the segments' sums scanned across the lanes, then each lane walks its segment
@@ -2222,22 +2242,27 @@ __global__ __launch_bounds__(256) void k_vl_bwd(Args a, LeafBwd o) {
       __syncthreads();
     }
     if constexpr (N >= 3) {
-      float colb[16], rowc[16];  // dS3[i][.][j] and dS3[i][j][.]
+      float colb[16];  // dS3[i][.][j]
+      f4 rowc[4];      // dS3[i][j][.]
 #pragma unroll
-      for (int k = 0; k < 16; ++k) {
-        colb[k] = dS3[i * 256 + k * 16 + j];
-        rowc[k] = dS3[i * 256 + j * 16 + ((k + j) & 15)];  // skewed: conflict-free across the 16 lanes
-      }
+      for (int k = 0; k < 16; ++k) colb[k] = dS3[i * 256 + k * 16 + j];
+#pragma unroll
+      for (int k = 0; k < 4; ++k) rowc[k] = *reinterpret_cast<const f4*>(dS3 + i * 256 + j * 16 + 4 * k);
       for (int mb = 0; mb < Mv; mb += VB) {
       const int me = min(Mv, mb + VB);
       for (int m = mb; m < me; ++m) {
+        // the knot's Delta_m and R_m: the same 16 floats in every lane (broadcast float4 reads)
         float q = 0.0f, e1 = 0.0f, f1 = 0.0f;
 #pragma unroll
-        for (int k = 0; k < 16; ++k) {
-          q = fmaf(colb[k], Dl[m][k], q);
-          const int kk = (k + j) & 15;
-          e1 = fmaf(rowc[k], Rs[m][kk], e1);
-          f1 = fmaf(rowc[k], Dl[m][kk], f1);
+        for (int k4 = 0; k4 < 4; ++k4) {
+          const f4 dk = *reinterpret_cast<const f4*>(&Dl[m][4 * k4]);
+          const f4 rk = *reinterpret_cast<const f4*>(&Rs[m][4 * k4]);
+#pragma unroll
+          for (int c = 0; c < 4; ++c) {
+            q = fmaf(colb[4 * k4 + c], dk[c], q);
+            e1 = fmaf(rowc[k4][c], rk[c], e1);
+            f1 = fmaf(rowc[k4][c], dk[c], f1);
+          }
         }
         const float yi = Ys[m][i], xi = Xs[m][i];
         // over the last index (lanes j of a row i): dY_m[i], dX_m[i]
