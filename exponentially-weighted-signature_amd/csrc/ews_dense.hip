@@ -51,6 +51,23 @@ typedef float f4 __attribute__((ext_vector_type(4)));
 __device__ __forceinline__ f4 mfma(float a, float b, f4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
 }
+// n floats from global memory into LDS by nt threads, eight loads in flight per thread before their stores (a
+// loop of load-then-store waits out one memory latency per element)
+__device__ __forceinline__ void stage_lds(float* dst, const float* src, int n, int tid, int nt) {
+  for (int e0 = tid; e0 < n; e0 += 8 * nt) {
+    float v[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const int e = e0 + u * nt;
+      v[u] = e < n ? src[e] : 0.0f;
+    }
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const int e = e0 + u * nt;
+      if (e < n) dst[e] = v[u];
+    }
+  }
+}
 // LDS operations of one wavefront execute in program order: a compiler barrier orders a write before another
 // lane's read of it
 __device__ __forceinline__ void wave_order_d() { __builtin_amdgcn_wave_barrier(); }
@@ -153,7 +170,7 @@ __global__ __launch_bounds__(256) void k_local(Args a) {
   __shared__ float mm[256];
   const int tid = threadIdx.x, i = tid >> 4, j = tid & 15;
   const int q = a.q;
-  for (int e = tid; e < a.npow * 256; e += 256) sp[e >> 8][e & 255] = a.apow[e];
+  stage_lds(&sp[0][0], a.apow, a.npow * 256, tid, 256);
   const float norm1 = a.apow[a.npow * 256];
   __syncthreads();
   const long total = (long)a.B * a.n_int;
@@ -277,7 +294,7 @@ __global__ __launch_bounds__(256, QB <= 24 ? 3 : 2) void k_local3(Args a) {
   __shared__ float inv[NINV];
   const int tid = threadIdx.x, w = tid >> 6, l = tid & 63, g = l >> 4, c16 = l & 15;
   const int q = a.q;
-  for (int e = tid; e < (PM + 1) * 256; e += 256) sp[e >> 8][e & 255] = a.apow[e];
+  stage_lds(&sp[0][0], a.apow, (PM + 1) * 256, tid, 256);
   for (int e = tid; e < NINV; e += 256) inv[e] = e ? 1.0f / (float)e : 0.0f;
   const float norm1 = a.apow[a.npow * 256];
   float* L = lt[w];
@@ -739,7 +756,7 @@ __global__ __launch_bounds__(64) void k_prep(Args a) {
   __shared__ __align__(16) float sp[PM + 1][256];
   __shared__ __align__(16) float P[256], V[256], T[256 + 32];
   const int l = threadIdx.x, b = blockIdx.x;
-  for (int e = l; e < (PM + 1) * 256; e += 64) sp[e >> 8][e & 255] = a.apow[e];
+  stage_lds(&sp[0][0], a.apow, (PM + 1) * 256, l, 64);
   const float norm1 = a.apow[a.npow * 256];
   __syncthreads();
   const float* th = a.clock + (size_t)b * a.L;
@@ -784,7 +801,7 @@ __global__ __launch_bounds__(256) void k_flows(Args a) {
   __shared__ __align__(16) float sp[PM + 1][256];
   __shared__ __align__(16) float Pw[4][256], Tw[4][256 + 32];
   const int tid = threadIdx.x, w = tid >> 6, l = tid & 63;
-  for (int e = tid; e < (PM + 1) * 256; e += 256) sp[e >> 8][e & 255] = a.apow[e];
+  stage_lds(&sp[0][0], a.apow, (PM + 1) * 256, tid, 256);
   const float norm1 = a.apow[a.npow * 256];
   __syncthreads();
   const long total = (long)a.B * a.n_int;
@@ -837,7 +854,7 @@ __global__ __launch_bounds__(256, 2) void k_vl(Args a) {
   const int tid = threadIdx.x, w = tid >> 6, l = tid & 63, g = l >> 4, c16 = l & 15;
   const int nw = blockDim.x >> 6;
   const int Mv = a.vm, MP = vl_rows(Mv);
-  for (int e = tid; e < (PM + 1) * 256; e += blockDim.x) lds[e] = a.apow[e];
+  stage_lds(lds, a.apow, (PM + 1) * 256, tid, blockDim.x);
   const float norm1 = a.apow[a.npow * 256];
   float* P = lds + (PM + 1) * 256 + w * vl_region(Mv);
   float* xs = P + 256;
@@ -1815,7 +1832,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(EXACTF ? 3 
   float *W1 = UN, *W2 = UN + 256, *W3 = UN + 512;
   const int tid = threadIdx.x, i = tid >> 4, j = tid & 15;
   const int q = a.q;
-  for (int e = tid; e < HP * 256; e += 256) sp[e >> 8][e & 255] = a.apow[e];
+  stage_lds(&sp[0][0], a.apow, HP * 256, tid, 256);
   const float norm1 = a.apow[a.npow * 256];
   float H[HP];
 #pragma unroll
@@ -2473,7 +2490,7 @@ __global__ __launch_bounds__(256) void k_bs_level1(Args a) {
   __shared__ float gm[256], em[256];
   __shared__ float vv[16];
   const int tid = threadIdx.x, i = tid >> 4, j = tid & 15;
-  for (int e = tid; e < (PM + 1) * 256; e += 256) sp[e >> 8][e & 255] = a.apow[e];
+  stage_lds(&sp[0][0], a.apow, (PM + 1) * 256, tid, 256);
   const float norm1 = a.apow[a.npow * 256];
   __syncthreads();
   const long total = (long)a.B * a.n_int;

@@ -11,6 +11,7 @@
 #include <hip/hip_runtime.h>
 
 #include "ews_hip.h"
+#include "ews_lanes.h"
 
 namespace ews {
 namespace tok1 {
@@ -172,29 +173,70 @@ __global__ void k_reduce(TArgs a) {
 // Entries of D outside the blocks are taken as zero and their gradients are written as zero.
 constexpr int kStageFloats = 12288;  // caches staged in LDS up to 48 KB
 
-__device__ __forceinline__ float blk_d(const TArgs& a, const float* sD, bool staged, int BS, int g, int row,
-                                       int r) {
-  if (staged) return sD[((size_t)g * a.d + row) * BS + r];
+template <bool STAGED>
+__device__ __forceinline__ float blk_d(const TArgs& a, const float* sD, int BS, int g, int row, int r) {
+  if constexpr (STAGED) return sD[((size_t)g * a.d + row) * BS + r];
   return a.D[((size_t)g * a.d + row) * a.d + (row / BS) * BS + r];
 }
 
+// v of lane base + r, the r-th lane of this lane's block (base = BS floor(lane / BS)); every lane of the wavefront
+// takes part. Blocks of 2 and 4 lie inside a quad of lanes: one DPP quad permutation (a VALU operand, no memory
+// round trip); blocks of 3, 6 and 8 go through an LDS permute.
 template <int BS>
-__global__ __launch_bounds__(64) void k_fwd_blk(TArgs a) {
-  extern __shared__ float s_c[];
-  const int b = blockIdx.x, i = threadIdx.x;
+__device__ __forceinline__ float blk_lane(float v, int base, int r) {
+  if constexpr (BS == 1) {
+    return v;
+  } else if constexpr (BS == 2) {
+    return r == 0 ? lanes::dpp<0xA0>(v) : lanes::dpp<0xF5>(v);  // quad_perm [0, 0, 2, 2], [1, 1, 3, 3]
+  } else if constexpr (BS == 4) {
+    switch (r) {  // quad_perm [r, r, r, r]
+      case 0: return lanes::dpp<0x00>(v);
+      case 1: return lanes::dpp<0x55>(v);
+      case 2: return lanes::dpp<0xAA>(v);
+      default: return lanes::dpp<0xFF>(v);
+    }
+  } else {
+    return __shfl(v, base + r);
+  }
+}
+
+// the block caches into LDS (row i of token g's block at (g d + i) BS, then P), eight loads in flight per lane
+template <int BS>
+__device__ __forceinline__ void stage_blk(const TArgs& a, float* sP, float* sD, bool with_p, int i) {
+  const int nd = a.V * a.d * BS;
+  for (int q0 = i; q0 < nd; q0 += 8 * 64) {
+    float v[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const int q = min(q0 + 64 * u, nd - 1);  // clamped: every load unconditional
+      const int gr = q / BS, r = q - gr * BS, g = gr / a.d, row = gr - g * a.d;
+      v[u] = a.D[((size_t)g * a.d + row) * a.d + (row / BS) * BS + r];
+    }
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      if (q0 + 64 * u < nd) sD[q0 + 64 * u] = v[u];
+    }
+  }
+  if (with_p) {
+    const int np = a.V * a.d;
+    for (int q0 = i; q0 < np; q0 += 8 * 64) {
+      float v[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) v[u] = a.P[min(q0 + 64 * u, np - 1)];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        if (q0 + 64 * u < np) sP[q0 + 64 * u] = v[u];
+      }
+    }
+  }
+}
+
+// The step loops take the caches from LDS (STAGED) or from global memory, a compile-time choice: one load kind each
+template <int BS, bool STAGED>
+__device__ __forceinline__ void fwd_blk_steps(const TArgs& a, const float* sP, const float* sD, int b, int i) {
   const bool on = i < a.d;
   const int base = (i / BS) * BS;
-  const bool staged = (size_t)a.V * a.d * (BS + 1) <= (size_t)kStageFloats;
-  float* sP = s_c;
-  float* sD = s_c + (size_t)a.V * a.d;
-  if (staged) {
-    for (int q = i; q < a.V * a.d; q += 64) sP[q] = a.P[q];
-    for (int q = i; q < a.V * a.d * BS; q += 64) {
-      const int gr = q / BS, r = q - gr * BS, g = gr / a.d, row = gr - g * a.d;
-      sD[q] = a.D[((size_t)g * a.d + row) * a.d + (row / BS) * BS + r];
-    }
-    __syncthreads();
-  }
+  const int row = on ? i : 0;  // lanes past d read row 0 and keep S = 0
   float S = 0.0f;
   for (int t0 = 0; t0 < a.n; t0 += 64) {
     int tokv = 0, livev = 0;
@@ -204,39 +246,55 @@ __global__ __launch_bounds__(64) void k_fwd_blk(TArgs a) {
       livev = live ? 1 : 0;
     }
     const int cnt = min(64, a.n - t0);
-    for (int s = 0; s < cnt; ++s) {
-      const int g = __shfl(tokv, s), live = __shfl(livev, s);  // uniform over the wavefront
-      if (live) {
-        float acc = on ? (staged ? sP[g * a.d + i] : a.P[(size_t)g * a.d + i]) : 0.0f;
+    // groups of eight steps without a branch (the lane reads are convergent, so only a constant trip count is
+    // unrolled; the states are stored after the group), so that the group's cache reads are issued ahead of the
+    // state chain; steps past n carry token 0 and no mask bit
+    for (int s0 = 0; s0 < 64; s0 += 8) {
+      float Sv[8];
 #pragma unroll
-        for (int r = 0; r < BS; ++r) {
-          const float sr = __shfl(S, base + r);
-          if (on) acc = fmaf(blk_d(a, sD, staged, BS, g, i, r), sr, acc);
-        }
-        S = acc;
+      for (int u = 0; u < 8; ++u) {
+        const int g = __builtin_amdgcn_readlane(tokv, s0 + u), live = __builtin_amdgcn_readlane(livev, s0 + u);
+        float acc = STAGED ? sP[g * a.d + row] : a.P[(size_t)g * a.d + row];
+        float dr[BS];
+#pragma unroll
+        for (int r = 0; r < BS; ++r) dr[r] = blk_d<STAGED>(a, sD, BS, g, row, r);
+#pragma unroll
+        for (int r = 0; r < BS; ++r) acc = fmaf(dr[r], blk_lane<BS>(S, base, r), acc);
+        if (live && on) S = acc;
+        Sv[u] = S;
       }
-      if (on) a.out[((size_t)b * a.n + t0 + s) * a.d + i] = S;
+      if (on) {
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+          if (s0 + u < cnt) a.out[((size_t)b * a.n + t0 + s0 + u) * a.d + i] = Sv[u];
+        }
+      }
     }
   }
 }
 
 template <int BS>
-__global__ __launch_bounds__(64) void k_bwd_blk(TArgs a) {
+__global__ __launch_bounds__(64) void k_fwd_blk(TArgs a) {
   extern __shared__ float s_c[];
   const int b = blockIdx.x, i = threadIdx.x;
+  float* sP = s_c;
+  float* sD = s_c + (size_t)a.V * a.d;
+  if ((size_t)a.V * a.d * (BS + 1) <= (size_t)kStageFloats) {
+    stage_blk<BS>(a, sP, sD, true, i);
+    __syncthreads();
+    fwd_blk_steps<BS, true>(a, sP, sD, b, i);
+  } else {
+    fwd_blk_steps<BS, false>(a, sP, sD, b, i);
+  }
+}
+
+template <int BS, bool STAGED>
+__device__ __forceinline__ void bwd_blk_steps(const TArgs& a, const float* sD, float* sAcc, float* sG, float* sR,
+                                              int b, int i) {
   const bool on = i < a.d;
   const int base = (i / BS) * BS;
-  const bool staged = (size_t)a.V * a.d * (BS + 1) <= (size_t)kStageFloats;
-  float* sD = s_c + (size_t)a.V * a.d;  // the same layout as the forward's (P's slot unused)
-  float* sAcc = staged ? sD + (size_t)a.V * a.d * BS : s_c;  // (V, BS + 1, 64): lane i's column
-  if (staged) {
-    for (int q = i; q < a.V * a.d * BS; q += 64) {
-      const int gr = q / BS, r = q - gr * BS, g = gr / a.d, row = gr - g * a.d;
-      sD[q] = a.D[((size_t)g * a.d + row) * a.d + (row / BS) * BS + r];
-    }
-  }
-  for (int q = 0; q < a.V * (BS + 1); ++q) sAcc[q * 64 + i] = 0.0f;
-  __syncthreads();
+  // lanes past d read block row 0 (their products are dropped); their lam, state and accumulators stay zero
+  const int rowb = on ? base : 0, col = on ? i - base : 0, ic = on ? i : 0;
   float lam = 0.0f;
   for (int t1 = a.n; t1 > 0; t1 -= 64) {
     const int t0 = max(0, t1 - 64);
@@ -246,26 +304,66 @@ __global__ __launch_bounds__(64) void k_bwd_blk(TArgs a) {
       tokv = tok_at(a, (size_t)b * a.n + t0 + i, live);
       livev = live ? 1 : 0;
     }
-    for (int t = t1 - 1; t >= t0; --t) {
-      const int g = __shfl(tokv, t - t0), live = __shfl(livev, t - t0);  // uniform over the wavefront
-      if (on) lam += a.gout[((size_t)b * a.n + t) * a.d + i];
-      if (live) {
-        const float sp = (on && t > 0) ? a.rows[((size_t)b * a.n + t - 1) * a.d + i] : 0.0f;  // S_{t-1}
+    for (int u1 = t1; u1 > t0; u1 -= kStage) {
+      const int u0 = max(t0, u1 - kStage);
+      {  // the stage's inputs: unconditional loads from clamped (valid) addresses, all issued before the first
+         // store, zeroed afterwards
+        float gv[kStage], rv[kStage];
+#pragma unroll
+        for (int k = 0; k < kStage; ++k) {
+          const int t = min(u0 + k, u1 - 1), tp = max(t - 1, 0);
+          gv[k] = a.gout[((size_t)b * a.n + t) * a.d + ic];
+          rv[k] = a.rows[((size_t)b * a.n + tp) * a.d + ic];  // S_{t-1}
+        }
+#pragma unroll
+        for (int k = 0; k < kStage; ++k) {
+          const int t = u0 + k;
+          sG[k * 64 + i] = (on && t < u1) ? gv[k] : 0.0f;
+          sR[k * 64 + i] = (on && t < u1 && t > 0) ? rv[k] : 0.0f;
+        }
+      }
+      // steps u1 - 1 down to u0, unrolled and without a branch (see the forward): a step past u1 or without its
+      // mask bit adds zero to the accumulators (exact: they start at +0 and never become -0) and keeps lam
+#pragma unroll
+      for (int k = kStage - 1; k >= 0; --k) {
+        const int t = u0 + k;  // t - t0 < 64
+        // uniform over the wavefront: the step's token and mask bit from lane t - t0
+        const int g = __builtin_amdgcn_readlane(tokv, t - t0);
+        const bool live = __builtin_amdgcn_readlane(livev, t - t0) && t < u1;
+        lam += sG[k * 64 + i];
+        const float sp = sR[k * 64 + i];
+        const float lw = live ? lam : 0.0f;
         float* acc = sAcc + (size_t)g * (BS + 1) * 64 + i;
         float ln = 0.0f;
 #pragma unroll
         for (int r = 0; r < BS; ++r) {
-          const float s_r = __shfl(sp, base + r), l_r = __shfl(lam, base + r);
-          if (on) {
-            acc[r * 64] += lam * s_r;                                         // dD_g[i][base + r]
-            ln = fmaf(blk_d(a, sD, staged, BS, g, base + r, i - base), l_r, ln);  // (D_g^T lam)_i
-          }
+          const float s_r = blk_lane<BS>(sp, base, r), l_r = blk_lane<BS>(lam, base, r);
+          acc[r * 64] += lw * s_r;                                              // dD_g[i][base + r]
+          ln = fmaf(blk_d<STAGED>(a, sD, BS, g, rowb + r, col), l_r, ln);       // (D_g^T lam)_i
         }
-        if (on) acc[BS * 64] += lam;  // dP_g[i]
-        lam = ln;
+        acc[BS * 64] += lw;  // dP_g[i]
+        lam = live ? (on ? ln : 0.0f) : lam;
       }
     }
   }
+}
+
+template <int BS>
+__global__ __launch_bounds__(64) void k_bwd_blk(TArgs a) {
+  extern __shared__ float s_c[];
+  const int b = blockIdx.x, i = threadIdx.x;
+  const bool on = i < a.d;
+  const bool staged = (size_t)a.V * a.d * (BS + 1) <= (size_t)kStageFloats;
+  float* sD = s_c + (size_t)a.V * a.d;  // the same layout as the forward's (P's slot unused)
+  float* sAcc = staged ? sD + (size_t)a.V * a.d * BS : s_c;  // (V, BS + 1, 64): lane i's column
+  // kStage steps' row cotangents and previous states, lane i's column of each (only lane i reads it: no barrier)
+  float* sG = sAcc + (size_t)a.V * (BS + 1) * 64;
+  float* sR = sG + kStage * 64;
+  if (staged) stage_blk<BS>(a, nullptr, sD, false, i);
+  for (int q = 0; q < a.V * (BS + 1); ++q) sAcc[q * 64 + i] = 0.0f;
+  __syncthreads();
+  if (staged) bwd_blk_steps<BS, true>(a, sD, sAcc, sG, sR, b, i);
+  else bwd_blk_steps<BS, false>(a, sD, sAcc, sG, sR, b, i);
   if (on) {
     for (int q = 0; q < a.V * (BS + 1); ++q)
       a.part[(((size_t)b * a.V * (BS + 1)) + q) * a.d + i] = sAcc[q * 64 + i];
@@ -297,8 +395,18 @@ __global__ void k_reduce_blk(TArgs a, int BS) {
     r = BS;
     isP = true;
   }
+  // the samples in order; eight loads in flight before their adds (the same order of additions)
+  const size_t off = ((size_t)g * (BS + 1) + r) * a.d + i, stride = (size_t)a.V * (BS + 1) * a.d;
   double s = 0.0;
-  for (int b = 0; b < a.B; ++b) s += (double)a.part[(((size_t)b * a.V + g) * (BS + 1) + r) * a.d + i];
+  int b = 0;
+  for (; b + 8 <= a.B; b += 8) {
+    float v[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) v[u] = a.part[(size_t)(b + u) * stride + off];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) s += (double)v[u];
+  }
+  for (; b < a.B; ++b) s += (double)a.part[(size_t)b * stride + off];
   if (isP) a.gP[(size_t)g * a.d + i] = (float)s;
   else a.gD[e] = (float)s;
 }
@@ -311,7 +419,8 @@ int tok1_check(const ews_token1_desc* s) {
   if (s->batch < 1 || s->steps < 1 || s->dim < 1 || s->dim > tok1::kMaxD || s->vocab < 1) return EWS_ERR_SHAPE;
   const int bs = s->block;
   if (bs < 0 || bs > 8 || bs == 5 || bs == 7 || (bs > 0 && s->dim % bs != 0)) return EWS_ERR_OPTION;
-  // the backward's per-lane accumulators (16 KB at most) sit in LDS beside the staged caches (48 KB at most)
+  // the backward's per-lane accumulators (16 KB at most) and its staged steps (8 KB) sit in LDS beside the staged
+  // caches (48 KB at most)
   if (bs > 0 && (size_t)s->vocab * (bs + 1) > 64) return EWS_ERR_SHAPE;
   return EWS_OK;
 }
@@ -330,7 +439,7 @@ int tok1_check(const ews_token1_desc* s) {
 size_t blk_lds_bytes(const ews_token1_desc* s, bool bwd) {
   const size_t stage = (size_t)s->vocab * s->dim * (s->block + 1);
   const size_t staged = stage <= (size_t)tok1::kStageFloats ? stage : 0;
-  return (staged + (bwd ? (size_t)s->vocab * (s->block + 1) * 64 : 0)) * 4;
+  return (staged + (bwd ? (size_t)s->vocab * (s->block + 1) * 64 + 2 * tok1::kStage * 64 : 0)) * 4;
 }
 size_t al256t(size_t x) { return (x + 255) & ~(size_t)255; }
 tok1::TArgs tok1_args(const ews_token1_desc* s) {
