@@ -664,6 +664,20 @@ __global__ __launch_bounds__(64) void k_full(CArgs a) {
 
 // knot gradients: dX_t = dv_{t-1} - dv_t; dtheta_t = dh_{t-1} - dh_t, plus the reference steps' shares (summed over
 // the sample's chunks and chains in order)
+__device__ __forceinline__ void knot_clock(const CArgs& a, size_t b, size_t t) {
+  double g = (t > 0 ? (double)a.dh[b * a.n + t - 1] : 0.0) - (t < (size_t)a.n ? (double)a.dh[b * a.n + t] : 0.0);
+  if (t <= 2 && (a.flow_mode != EWS_FLOW_PER_INTERVAL || a.leaf_mode != EWS_FLOW_PER_INTERVAL)) {
+    double r0 = 0.0, r1 = 0.0;
+    for (size_t i = 0; i < (size_t)a.C * a.K; ++i) {
+      r0 += a.pp[(b * a.C * a.K + i) * 5 + 3];
+      r1 += a.pp[(b * a.C * a.K + i) * 5 + 4];
+    }
+    if (t == 1) g += r0 - r1;
+    else if (t == 0) g -= r0;
+    else g += r1;
+  }
+  a.gclock[b * a.L + t] = (float)g;
+}
 __global__ void k_knots(CArgs a) {
   const size_t e = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
   const size_t per = (size_t)a.L * (a.d + 1);
@@ -674,18 +688,25 @@ __global__ void k_knots(CArgs a) {
     const float hi = t < (size_t)a.n ? a.dv[(b * a.n + t) * a.d + ch] : 0.0f;
     a.gpath[(b * a.L + t) * a.d + ch] = lo - hi;
   } else if (a.gclock) {
-    double g = (t > 0 ? (double)a.dh[b * a.n + t - 1] : 0.0) - (t < (size_t)a.n ? (double)a.dh[b * a.n + t] : 0.0);
-    if (t <= 2 && (a.flow_mode != EWS_FLOW_PER_INTERVAL || a.leaf_mode != EWS_FLOW_PER_INTERVAL)) {
-      double r0 = 0.0, r1 = 0.0;
-      for (size_t i = 0; i < (size_t)a.C * a.K; ++i) {
-        r0 += a.pp[(b * a.C * a.K + i) * 5 + 3];
-        r1 += a.pp[(b * a.C * a.K + i) * 5 + 4];
-      }
-      if (t == 1) g += r0 - r1;
-      else if (t == 0) g -= r0;
-      else g += r1;
-    }
-    a.gclock[b * a.L + t] = (float)g;
+    knot_clock(a, b, t);
+  }
+}
+// the same for d % 4 == 0 and 16-byte aligned rows: the path columns four at a time (a thread per sample, knot and
+// float4), then the clock column, a thread per (sample, knot), in threads B L d / 4 ..
+__global__ void k_knots4(CArgs a) {
+  const size_t e = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const size_t d4 = (size_t)a.d / 4, np = (size_t)a.B * a.L * d4;
+  if (e < np) {
+    const size_t b = e / ((size_t)a.L * d4), r = e % ((size_t)a.L * d4), t = r / d4, q = r % d4;
+    const float4* dv4 = reinterpret_cast<const float4*>(a.dv);
+    const float4 z = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    const float4 lo = t > 0 ? dv4[(b * a.n + t - 1) * d4 + q] : z;
+    const float4 hi = t < (size_t)a.n ? dv4[(b * a.n + t) * d4 + q] : z;
+    reinterpret_cast<float4*>(a.gpath)[(b * a.L + t) * d4 + q] =
+        make_float4(lo.x - hi.x, lo.y - hi.y, lo.z - hi.z, lo.w - hi.w);
+  } else if (a.gclock && e < np + (size_t)a.B * a.L) {
+    const size_t k = e - np;
+    knot_clock(a, k / a.L, k % a.L);
   }
 }
 
@@ -907,8 +928,13 @@ int ews_chain_backward(const ews_chain_desc* desc, const void* path, const float
   const size_t lds = (size_t)64 * a.T * a.M * sizeof(float2);
   if (lds > 65536 && ews::allow_full_lds(a, lds) != EWS_OK) return EWS_ERR_LAUNCH;
   EWS_CHAIN_LAUNCH(ews::chain::k_full, grid, blk, lds, st, a);
-  const size_t kt = (size_t)a.B * a.L * (a.d + 1);
-  hipLaunchKernelGGL(ews::chain::k_knots, dim3((unsigned)((kt + 255) / 256)), dim3(256), 0, st, a);
+  if (a.d % 4 == 0 && ((uintptr_t)grad_path & 15) == 0) {  // dv rows sit at 256-byte aligned offsets
+    const size_t kt = (size_t)a.B * a.L * (a.d / 4 + 1);
+    hipLaunchKernelGGL(ews::chain::k_knots4, dim3((unsigned)((kt + 255) / 256)), dim3(256), 0, st, a);
+  } else {
+    const size_t kt = (size_t)a.B * a.L * (a.d + 1);
+    hipLaunchKernelGGL(ews::chain::k_knots, dim3((unsigned)((kt + 255) / 256)), dim3(256), 0, st, a);
+  }
   if (hipGetLastError() != hipSuccess) return EWS_ERR_LAUNCH;
   hipLaunchKernelGGL(ews::chain::k_zero_a, dim3((a.d * a.d + 255) / 256), dim3(256), 0, st, a);
   if (hipGetLastError() != hipSuccess) return EWS_ERR_LAUNCH;
