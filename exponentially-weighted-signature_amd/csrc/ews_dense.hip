@@ -304,14 +304,31 @@ __global__ __launch_bounds__(256, QB <= 24 ? 3 : 2) void k_local3(Args a) {
   __syncthreads();
   const f4 a4 = *reinterpret_cast<const f4*>(&sp[1][c16 * 16 + 4 * g]);  // A[c16][4g .. 4g+3]
   const long total = (long)a.B * a.n_int;
-  for (long it = (long)blockIdx.x * 4 + w; it < total; it += (long)gridDim.x * 4) {
+  // the interval's clock values and increment coordinates are loaded one interval ahead into registers, so that no
+  // memory round trip sits at the top of an interval
+  const long first = (long)blockIdx.x * 4 + w, stride = (long)gridDim.x * 4;
+  float nth0 = 0.0f, nth1 = 0.0f, nx0 = 0.0f, nx1 = 0.0f;
+  const bool xl = l < 16 && l < a.d;
+  auto prefetch = [&](long i2) {
+    const int b2 = (int)(i2 / a.n_int), t2 = (int)(i2 - (long)b2 * a.n_int);
+    const float* th2 = a.clock + (size_t)b2 * a.L + t2;
+    nth0 = th2[0];
+    nth1 = th2[1];
+    if (xl) {
+      const float* x = a.path + ((size_t)b2 * a.L + t2) * a.d;
+      nx0 = x[l];
+      nx1 = x[a.d + l];
+    }
+  };
+  if (first < total) prefetch(first);
+  for (long it = first; it < total; it += stride) {
     const int b = (int)(it / a.n_int), t = (int)(it - (long)b * a.n_int);
     const float* th = a.clock + (size_t)b * a.L;
-    const float h = th[t + 1] - th[t];
+    const float h = nth1 - nth0;
+    const float v = xl ? nx1 - nx0 : 0.0f;
+    if (it + stride < total) prefetch(it + stride);
     wave_order_d();  // the previous interval's reads of L / G1 / G2 come first
     if (l < 16) {
-      const float* x = a.path + ((size_t)b * a.L + t) * a.d;
-      const float v = l < a.d ? x[a.d + l] - x[l] : 0.0f;
       L[l] = v;
       G1[l] = v;
     }
@@ -382,8 +399,8 @@ __global__ __launch_bounds__(256, QB <= 24 ? 3 : 2) void k_local3(Args a) {
     for (int i = 0; i < 16; ++i) *reinterpret_cast<f4*>(row + 272 + c16 * 256 + i * 16 + 4 * g) = acc3[i];
     // flow M_t = exp(-h_f A): Taylor of degree PM in X = -h_f A / 2^s (lane: entries 4l .. 4l+3), s squarings
     {
-      bool ident;
-      const float hf = flow_step(a, th, t, ident);
+      bool ident = false;
+      const float hf = a.flow_mode == EWS_FLOW_PER_INTERVAL ? h : flow_step(a, th, t, ident);
       float* fr = a.fl + ((size_t)b * a.n_int + t) * 256;
       f4 m;
       if (ident) {
