@@ -880,13 +880,32 @@ __global__ __launch_bounds__(256, 2) void k_vl(Args a) {
   float* E = V;
   __syncthreads();
   const long total = (long)a.B * a.n_int;
-  for (long it = (long)blockIdx.x * nw + w; it < total; it += (long)gridDim.x * nw) {
+  // the interval's clock values and increment coordinates are loaded one interval ahead into registers, so that no
+  // memory round trip sits at the top of an interval
+  const long first = (long)blockIdx.x * nw + w, stride = (long)gridDim.x * nw;
+  float nth0 = 0.0f, nth1 = 0.0f, nx0 = 0.0f, nx1 = 0.0f;
+  const bool xl = l < 16 && l < a.d;
+  auto prefetch = [&](long i2) {
+    const int b2 = (int)(i2 / a.n_int), t2 = (int)(i2 - (long)b2 * a.n_int);
+    const float* th2 = a.clock + (size_t)b2 * a.L + t2;
+    nth0 = th2[0];
+    nth1 = th2[1];
+    if (xl) {
+      const float* x = a.path + ((size_t)b2 * a.L + t2) * a.d;
+      nx0 = x[l];
+      nx1 = x[a.d + l];
+    }
+  };
+  if (first < total) prefetch(first);
+  for (long it = first; it < total; it += stride) {
     const int b = (int)(it / a.n_int), t = (int)(it - (long)b * a.n_int);
     const float* th = a.clock + (size_t)b * a.L;
+    const float hi = nth1 - nth0, x0 = nx0, x1 = nx1;  // th[t + 1] - th[t]; path[t][l], path[t + 1][l]
+    if (it + stride < total) prefetch(it + stride);
     wave_order_d();  // the previous interval's reads of the segment table come first
     if constexpr (EXACTF) {
-      bool ident;
-      const float hf = flow_step(a, th, t, ident);
+      bool ident = false;
+      const float hf = a.flow_mode == EWS_FLOW_PER_INTERVAL ? hi : flow_step(a, th, t, ident);
       f4 m;
       if (ident) {
 #pragma unroll
@@ -904,7 +923,7 @@ __global__ __launch_bounds__(256, 2) void k_vl(Args a) {
     }
     // step matrices
     if (a.vl_mode == EWS_FLOW_PER_INTERVAL) {
-      wave_matfn(sp, norm1, a.vl_expm, (th[t + 1] - th[t]) / (float)Mv, false, P, V, T, l);
+      wave_matfn(sp, norm1, a.vl_expm, hi / (float)Mv, false, P, V, T, l);
     } else if (a.vl_mode == EWS_FLOW_CACHED_BASEPOINT && t == 0) {
       wave_identity(P, l);
       wave_identity(V, l);
@@ -926,10 +945,7 @@ __global__ __launch_bounds__(256, 2) void k_vl(Args a) {
       *reinterpret_cast<f4*>(sv + 256 + 4 * l) = *reinterpret_cast<const f4*>(V + 4 * l);
     }
     // w = v / M
-    if (l < 16) {
-      const float* x = a.path + ((size_t)b * a.L + t) * a.d;
-      xs[l] = l < a.d ? (x[a.d + l] - x[l]) / (float)Mv : 0.0f;
-    }
+    if (l < 16) xs[l] = xl ? (x1 - x0) / (float)Mv : 0.0f;
     wave_order_d();
 #pragma unroll
     for (int q = 0; q < 4; ++q) xv[q] = *reinterpret_cast<const f4*>(xs + 4 * q);
