@@ -2201,31 +2201,41 @@ __global__ __launch_bounds__(256) void k_vl_bwd(Args a, LeafBwd o) {
   float dAl = 0.0f;
   __syncthreads();
   const long total = (long)a.B * a.n_int;
+  // ---- saved step matrices and increments, loaded into registers during the interval before (issued once the
+  // depth-3 sums are done): P, V, the knots (one float4 per thread: M <= 64), ds1, ds2, ds3 (four float4), dM and the
+  // increment's coordinates; all of them before the first store to LDS
+  const bool dl_own = tid < Mv * 4;
+  float in_p = 0.0f, in_v = 0.0f, in_g = 0.0f, in_s2 = 0.0f, in_s1 = 0.0f, in_x0 = 0.0f, in_x1 = 0.0f;
+  f4 in_d = {0.0f, 0.0f, 0.0f, 0.0f};
+  f4 in_s3[N >= 3 ? 4 : 1];
+  auto prefetch = [&](long i2) {
+    const size_t r2 = (size_t)i2;  // = b2 n_int + t2
+    const int b2 = (int)(i2 / a.n_int), t2 = (int)(i2 - (long)b2 * a.n_int);
+    const float* sv2 = a.vlsave + r2 * vs;
+    const float* dr2 = a.loc + r2 * LW;
+    in_p = sv2[tid];
+    in_v = sv2[256 + tid];
+    in_g = a.fl[r2 * 256 + tid];  // dM_t
+    if (dl_own) in_d = reinterpret_cast<const f4*>(sv2 + 512)[tid];
+    if constexpr (N >= 2) in_s2 = dr2[16 + tid];
+    if constexpr (N >= 3) {
+#pragma unroll
+      for (int m = 0; m < 4; ++m) in_s3[m] = reinterpret_cast<const f4*>(dr2 + 272)[tid + 256 * m];
+    }
+    if (tid < 16) {
+      in_s1 = dr2[tid];
+      if (tid < a.d) {
+        const float* x = a.path + ((size_t)b2 * a.L + t2) * a.d;
+        in_x0 = x[tid];
+        in_x1 = x[a.d + tid];
+      }
+    }
+  };
+  if (blockIdx.x < total) prefetch(blockIdx.x);
   for (long it = blockIdx.x; it < total; it += gridDim.x) {
     const int b = (int)(it / a.n_int), t = (int)(it - (long)b * a.n_int);
     const float* th = a.clock + (size_t)b * a.L;
-    const float* drow = a.loc + ((size_t)b * a.n_int + t) * LW;
-    const float* sv = a.vlsave + ((size_t)b * a.n_int + t) * vs;
-    // ---- saved step matrices and increments: every input of the interval is loaded into registers before the
-    // first store to LDS, so that the loads' latencies overlap (the knots as one float4 per thread: M <= 64; dS3 as
-    // four); the clock's loads after them, since the step's first use waits for every load before it
-    const float in_p = sv[tid], in_v = sv[256 + tid];
-    const float in_g = a.fl[((size_t)b * a.n_int + t) * 256 + tid];  // dM_t
-    const bool dl_own = tid < Mv * 4;
-    f4 in_d = {0.0f, 0.0f, 0.0f, 0.0f};
-    if (dl_own) in_d = reinterpret_cast<const f4*>(sv + 512)[tid];
-    float in_s2 = 0.0f, in_w = 0.0f, in_s1 = 0.0f;
-    if constexpr (N >= 2) in_s2 = drow[16 + tid];
-    f4 in_s3[N >= 3 ? 4 : 1];
-    if constexpr (N >= 3) {
-#pragma unroll
-      for (int m = 0; m < 4; ++m) in_s3[m] = reinterpret_cast<const f4*>(drow + 272)[tid + 256 * m];
-    }
-    if (tid < 16) {
-      const float* x = a.path + ((size_t)b * a.L + t) * a.d;
-      in_w = tid < a.d ? (x[a.d + tid] - x[tid]) / (float)Mv : 0.0f;
-      in_s1 = drow[tid];
-    }
+    const float in_w = (tid < 16 && tid < a.d) ? (in_x1 - in_x0) / (float)Mv : 0.0f;
     bool fixed = false;  // delta = 0: P = V = I (the jump / basepoint interval), no dependence on A or the clock
     float delta;
     if (a.vl_mode == EWS_FLOW_PER_INTERVAL) {
@@ -2346,6 +2356,7 @@ __global__ __launch_bounds__(256) void k_vl_bwd(Args a, LeafBwd o) {
       __syncthreads();  // before the next block's partials
       }
     }
+    if (it + gridDim.x < total) prefetch(it + gridDim.x);  // the next interval's inputs
     // Pre and R -> Delta (dP holds dPre): dDelta_m += sum_{m' > m} dPre_m' + sum_{m' < m} dR_m', segments as above
     {
       const int col = tid >> 4, seg = tid & 15, S = (Mv + 15) >> 4, m0 = min(Mv, seg * S), m1 = min(Mv, m0 + S);
