@@ -1877,10 +1877,13 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(EXACTF ? 3 
   // depth 3: the next interval's inputs (ds3 as four float4 per thread, ds2, dM, ds1 and the increment) are loaded
   // into registers once the degree loop is done, so that their latency hides behind the rest of the interval
   f4 pf3[4];
-  float pf2 = 0.0f, pfg = 0.0f, pfs1 = 0.0f, pfv = 0.0f;
+  float pf2 = 0.0f, pfg = 0.0f, pfs1 = 0.0f, pfv = 0.0f, pft0 = 0.0f, pft1 = 0.0f;
   auto prefetch = [&](long it2) {
     const int b2 = (int)(it2 / a.n_int), t2 = (int)(it2 - (long)b2 * a.n_int);
     const float* dr = a.loc + ((size_t)b2 * a.n_int + t2) * LW;
+    const float* th2 = a.clock + (size_t)b2 * a.L + t2;  // the clock values around the interval
+    pft0 = th2[0];
+    pft1 = th2[1];
 #pragma unroll
     for (int m = 0; m < 4; ++m) pf3[m] = *reinterpret_cast<const f4*>(dr + 272 + 4 * tid + 1024 * m);
     pf2 = dr[16 + tid];
@@ -1900,7 +1903,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(EXACTF ? 3 
     const int tid = opaque_vgpr(tid_all), i = tid >> 4, j = tid & 15, l = tid & 63;
     const int b = (int)(it / a.n_int), t = (int)(it - (long)b * a.n_int);
     const float* th = a.clock + (size_t)b * a.L;
-    const float h = th[t + 1] - th[t];
+    const float h = N >= 3 ? pft1 - pft0 : th[t + 1] - th[t];  // depth 3: from the registers
     const float* drow = a.loc + ((size_t)b * a.n_int + t) * LW;  // ds_t
     // ---- inputs
     if constexpr (N >= 3) {  // from the registers; ds3[a][b][c] at (16 a + b) LP + c
@@ -2116,8 +2119,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(EXACTF ? 3 
       __syncthreads();
     }
     // ---- flow adjoint
-    bool ident;
-    const float hf = flow_step(a, th, t, ident);
+    bool ident = false;
+    const float hf = a.flow_mode == EWS_FLOW_PER_INTERVAL ? h : flow_step(a, th, t, ident);
     const float dhf = EXACTF ? (ident ? 0.0f : block_exp_adjoint(sp, norm1, hf, Gm, nullptr, Esq, Esq, red, H, tid))
                              : block_flow_adjoint(a, sp, norm1, hf, ident, Gm, Esq, W1, W2, W3, red, H, dAl, tid);
     // ---- outputs
