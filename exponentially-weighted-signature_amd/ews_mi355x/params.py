@@ -94,7 +94,9 @@ class AParamEFM(torch.nn.Module):
         return self.theta**2 if self.positivity == "square" else F.softplus(self.theta)
 
     def forward(self):
-        return torch.diag(self.diagonal())
+        A = torch.diag(self.diagonal())
+        A._ews_chain = ("real", 1)  # the structure by construction (read without a device-to-host copy)
+        return A
 
 
 class AParamBlockDiag(torch.nn.Module):
@@ -273,6 +275,7 @@ def _planes_to_dense(dw):
     A = A.index_put((2 * i + 1, 2 * i + 1), dw[:, 0])
     A = A.index_put((2 * i, 2 * i + 1), dw[:, 1])
     A = A.index_put((2 * i + 1, 2 * i), -dw[:, 1])
+    A._ews_chain = ("complex", 2)  # rotation planes by construction (read without a device-to-host copy)
     return A
 
 

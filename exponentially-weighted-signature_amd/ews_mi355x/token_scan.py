@@ -97,7 +97,9 @@ def _wide_cache(vocab_dx, vocab_dtheta, A, N, expm_method, chen_method, leaf, se
     if chen_method != "exact" or (leaf == "van_loan" and expm_method != "exact"):
         raise NotImplementedError("token caches wider than 16 coordinates take exact exponentials")
     if chain is None:
-        chain = _chain_structure(A)
+        # the structure the parametrisation tagged its output with, else read off A's values (a copy to the host,
+        # which waits for the device's queued work)
+        chain = getattr(A, "_ews_chain", None) or _chain_structure(A)
     if chain is None:
         raise NotImplementedError("token caches wider than 16 coordinates need rotation planes, a real diagonal or "
                                   "uniform Jordan chains (pass chain=(kind, size))")
